@@ -1,0 +1,221 @@
+/* C ABI of the MI355X (gfx950) MoE-layer hot path of Lewi Surge.
+ *
+ * Every entry point is stateless and stream-ordered: it enqueues HIP kernels on `stream` and returns
+ * without a host synchronisation.  All pointers are caller-owned device buffers; the library never
+ * allocates device memory.  Scratch space is passed in as `workspace` of at least the size the matching
+ * `*_workspace_bytes` function reports.  Return value: 0 on success, a negative LSURGE_ERR_* code
+ * otherwise; `lsurge_last_error()` then holds a message (thread-local).
+ *
+ * Reference interfaces replaced (paths in prostos2162-maker/lewi-surge):
+ *   modal/moe_permute.py   gather_rows / gather_reduce / gather_dot / sort_indices / dispatch /
+ *                          combine / permute_rows (the Pallas-TPU kernels and XLA refs)
+ *   modal/padded_gmm.py    padded_ragged_dot (the jax.lax.ragged_dot replacement)
+ *   MaxText RoutedMoE      router top-k, SwiGLU experts and shared expert (third-party, not vendored)
+ * Each function below cites the reference line it stands in for.  The reference binds its kernels with
+ * `pl.pallas_call` inside jit (modal/moe_permute.py:150-158, 203-211); the binding a JAX user adds for
+ * these is an XLA FFI custom call per entry point.
+ */
+#ifndef LEWI_SURGE_H_
+#define LEWI_SURGE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* lsurge_stream_t; /* == hipStream_t */
+
+/* element types of row arrays (modal/moe_permute.py:53-54 accepts 32- and 16-bit floats) */
+enum { LSURGE_F32 = 0, LSURGE_BF16 = 1, LSURGE_F16 = 2 };
+
+enum {
+  LSURGE_OK = 0,
+  LSURGE_ERR_INVALID = -1,     /* bad shape / null pointer / out-of-range argument */
+  LSURGE_ERR_DTYPE = -2,       /* unsupported element type */
+  LSURGE_ERR_LAUNCH = -3,      /* HIP launch failure */
+  LSURGE_ERR_WORKSPACE = -4    /* workspace too small */
+};
+
+#define LSURGE_ABI_VERSION 1
+#define LSURGE_BLOCK_ROWS 128 /* rows per padded expert block */
+
+int lsurge_abi_version(void);
+const char* lsurge_last_error(void);
+
+/* ------------------------------------------------------------------------------------------------
+ * Row movement (memory-bound).
+ * ------------------------------------------------------------------------------------------------ */
+
+/* out[i] = x[idx[i]], or dtype(f32(x[idx[i]]) * scale[i]) when scale != NULL.
+ * x: [n, d] of `dtype`; idx: [m] int32 in [0, n); scale: [m] f32 or NULL; out: [m, d] of `dtype`.
+ * Replaces moe_permute.gather_rows (modal/moe_permute.py:116-158). */
+int lsurge_gather_rows(const void* x, int64_t n, int64_t d, int dtype, const int32_t* idx, int64_t m,
+                       const float* scale, void* out, lsurge_stream_t stream);
+
+/* out[t] = sum_{j<k} w[t,j] * y[pos[t,j]] accumulated in f32, j ascending; w == NULL means w = 1.
+ * y: [m, d] of y_dtype; pos: [n, k] int32 in [0, m); out: [n, d] of out_dtype.
+ * Replaces moe_permute.gather_reduce (modal/moe_permute.py:161-225, dot=False). */
+int lsurge_gather_reduce(const void* y, int64_t m, int64_t d, int y_dtype, const int32_t* pos, int64_t n,
+                         int64_t k, const float* w, void* out, int out_dtype, lsurge_stream_t stream);
+
+/* out[t,j] = <g[t], y[pos[t,j]]> in f32.  y: [m, d]; pos: [n, k]; g: [n, d]; out: [n, k] f32.
+ * Replaces moe_permute.gather_dot (modal/moe_permute.py:228-234, _reduce_like dot=True). */
+int lsurge_gather_dot(const void* y, int64_t m, int64_t d, int y_dtype, const int32_t* pos, int64_t n,
+                      int64_t k, const void* g, int g_dtype, float* out, lsurge_stream_t stream);
+
+/* Fused combine backward in one pass over g:  dy[order[p]] ... i.e. for every token t and j<k:
+ *   dy[pos[t,j]] = y_dtype(w[t,j] * f32(g[t]))      (moe_permute.py:306-307)
+ *   dw[t,j]      = <f32(g[t]), f32(y[pos[t,j]])>    (moe_permute.py:308)
+ * y, dy: [n*k, d] of y_dtype; g: [n, d] of g_dtype (rounded to y_dtype first, as g.astype(y.dtype));
+ * pos: [n*k] int32 (a permutation); w: [n, k] f32; dw: [n, k] f32.
+ * Replaces the two-kernel moe_permute._combine_bwd (modal/moe_permute.py:303-309). */
+int lsurge_combine_bwd(const void* y, int y_dtype, const int32_t* pos, const float* w, int64_t n, int64_t k,
+                       int64_t d, const void* g, int g_dtype, void* dy, float* dw, lsurge_stream_t stream);
+
+/* inv[idx[i]] = i for a permutation idx of [0, m).  Replaces jnp.argsort(idx) in
+ * moe_permute._permute_rows_bwd (modal/moe_permute.py:325-326). */
+int lsurge_invert_permutation(const int32_t* idx, int64_t m, int32_t* inv, lsurge_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Routing indices (integer, bit-exact).
+ * ------------------------------------------------------------------------------------------------ */
+
+/* Stable sort of the m flat slot experts: order[p] = slot at sorted position p, pos = order^-1;
+ * group_sizes (optional, [num_experts]) = bincount.  flat values must lie in [0, num_experts).
+ * Replaces moe_permute.sort_indices (modal/moe_permute.py:240-264). */
+size_t lsurge_sort_indices_workspace_bytes(int64_t m, int64_t num_experts);
+int lsurge_sort_indices(const int32_t* flat, int64_t m, int64_t num_experts, int32_t* order, int32_t* pos,
+                        int32_t* group_sizes, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
+/* Router: logits = x @ w_r (+ bias) in f32, summed sequentially over d; sel = top-k with ties broken
+ * toward the lower expert index; weights = softmax over the k selected logits.
+ * x: [t, d] bf16; w_r: [d, e] bf16; bias: [e] f32 or NULL; logits: [t, e] f32 (may be NULL);
+ * sel: [t, k] int32; weights: [t, k] f32.  1 <= k <= e <= 256.
+ * Replaces MaxText RoutedMoE gate + top-k (third-party; configs/stage1.yml:34-37). */
+int lsurge_router_topk(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d, int64_t e,
+                       int64_t k, float* logits, int32_t* sel, float* weights, lsurge_stream_t stream);
+
+/* Padded block layout of the flat slots (m = t*k): stable expert sort (as lsurge_sort_indices) plus
+ *   offsets[e]   = exclusive scan of group_sizes,
+ *   block_off[e] = exclusive scan of ceil(group_sizes/128),
+ *   slot[i]      = 128*block_off[flat[i]] + (pos[i] - offsets[flat[i]])  (padded row of slot i),
+ *   row_src[r]   = flat slot stored at padded row r, -1 for padding rows,
+ *   blk_expert / blk_rows [max_blocks] = expert and valid rows of block b (-1 / 0 past the end),
+ *   num_blocks[0] = sum_e ceil(group_sizes[e]/128).
+ * max_blocks must be lsurge_max_blocks(m, e); row_src has 128*max_blocks entries.
+ * Replaces sort_indices (modal/moe_permute.py:240-264) + padded_gmm's row<->slot maps
+ * (modal/padded_gmm.py:51-64), dropless. */
+int64_t lsurge_max_blocks(int64_t m, int64_t num_experts);
+size_t lsurge_layout_workspace_bytes(int64_t m, int64_t num_experts);
+int lsurge_build_layout(const int32_t* flat, int64_t m, int64_t num_experts, int32_t* group_sizes,
+                        int32_t* offsets, int32_t* block_off, int32_t* order, int32_t* pos, int32_t* slot,
+                        int32_t* row_src, int32_t* blk_expert, int32_t* blk_rows, int32_t* num_blocks,
+                        void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Grouped GEMM (bf16 MFMA, f32 accumulation).
+ * ------------------------------------------------------------------------------------------------ */
+
+/* Dropless ragged_dot: out[r] = lhs[r] @ rhs[e(r)] for r < sum(group_sizes), 0 for the rows after.
+ * lhs: [m, kdim] bf16 rows sorted by group; rhs: [e, kdim, n] bf16; group_sizes: [e] int32 (device);
+ * out: [m, n] of out_dtype (LSURGE_BF16, or LSURGE_F32 for preferred_element_type=float32).
+ * kdim % 8 == 0, n % 8 == 0.
+ * Replaces padded_gmm.padded_ragged_dot (modal/padded_gmm.py:45-69) / jax.lax.ragged_dot. */
+size_t lsurge_ragged_dot_workspace_bytes(int64_t m, int64_t e);
+int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_sizes, int64_t m, int64_t kdim,
+                      int64_t n, int64_t e, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
+                      lsurge_stream_t stream);
+
+/* Backward of lsurge_ragged_dot for upstream g [m, n] bf16: dlhs [m, kdim] bf16 (rows past the groups
+ * = 0) and drhs [e, kdim, n] f32.  Replaces the VJP of padded_gmm.padded_ragged_dot
+ * (modal/padded_gmm.py:35-39 + XLA autodiff of the einsum at 67-68). */
+int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group_sizes, const void* g,
+                          int64_t m, int64_t kdim, int64_t n, int64_t e, void* dlhs, float* drhs,
+                          void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Whole MoE layer: router -> layout -> dispatch -> gate/up GEMM (+SiLU*mul) -> down GEMM -> combine
+ * (+ shared expert), and its gather-only backward.
+ * Weights follow MaxText's layout: w_gate/w_up = wi_0/wi_1 [e, d, f], w_down = wo [e, f, d]
+ * (modal/stage2.py:338-345); shared expert ws_gate/ws_up [d, fs], ws_down [fs, d]; router w_r [d, e].
+ * ------------------------------------------------------------------------------------------------ */
+typedef struct {
+  int64_t t;  /* tokens */
+  int64_t d;  /* d_model */
+  int64_t e;  /* routed experts */
+  int64_t k;  /* experts per token */
+  int64_t f;  /* routed expert FFN dim */
+  int64_t fs; /* shared expert FFN dim, 0 = no shared expert */
+} lsurge_moe_shape;
+
+typedef struct {
+  const void* x;       /* [t, d] bf16 */
+  const void* w_r;     /* [d, e] bf16 */
+  const float* bias;   /* [e] f32 router logit bias or NULL */
+  const void* w_gate;  /* [e, d, f] bf16 */
+  const void* w_up;    /* [e, d, f] bf16 */
+  const void* w_down;  /* [e, f, d] bf16 */
+  const void* ws_gate; /* [d, fs] bf16 or NULL */
+  const void* ws_up;   /* [d, fs] bf16 or NULL */
+  const void* ws_down; /* [fs, d] bf16 or NULL */
+} lsurge_moe_params;
+
+typedef struct {
+  void* dx;        /* [t, d] bf16 */
+  float* dw_r;     /* [d, e] f32 */
+  float* dw_gate;  /* [e, d, f] f32 */
+  float* dw_up;    /* [e, d, f] f32 */
+  float* dw_down;  /* [e, f, d] f32 */
+  float* dws_gate; /* [d, fs] f32 or NULL */
+  float* dws_up;   /* [d, fs] f32 or NULL */
+  float* dws_down; /* [fs, d] f32 or NULL */
+  float* dweights; /* [t, k] f32 gradient of the routing weights (may be NULL) */
+} lsurge_moe_grads;
+
+/* Bytes of the `saved` buffer the forward fills and the backward reads (activations + layout). */
+size_t lsurge_moe_saved_bytes(const lsurge_moe_shape* s);
+/* Scratch bytes for forward and backward (not kept between calls). */
+size_t lsurge_moe_fwd_workspace_bytes(const lsurge_moe_shape* s);
+size_t lsurge_moe_bwd_workspace_bytes(const lsurge_moe_shape* s);
+
+/* out: [t, d] bf16 = sum_j w[t,j] * expert_{sel[t,j]}(x[t]) + shared(x[t]) (f32 sum, one rounding). */
+int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* out, void* saved,
+                   size_t saved_bytes, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+/* dy: [t, d] bf16 upstream gradient.  `saved` must come from lsurge_moe_fwd with the same s and p. */
+int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* dy, const void* saved,
+                   const lsurge_moe_grads* g, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
+/* Views into `saved` (device pointers), for tests and the Python surface. */
+typedef struct {
+  float* logits;       /* [t, e] */
+  int32_t* sel;        /* [t, k] */
+  float* weights;      /* [t, k] */
+  int32_t* group_sizes, *offsets, *block_off; /* [e] */
+  int32_t* order, *pos, *slot;                /* [t*k] */
+  int32_t* row_src;    /* [128*max_blocks] */
+  int32_t* blk_expert, *blk_rows;             /* [max_blocks] */
+  int32_t* num_blocks; /* [1] */
+  void* x_pad;         /* [128*max_blocks, d] bf16 dispatched rows */
+  void* h_gate;        /* [128*max_blocks, f] bf16 x.W_gate */
+  void* h_up;          /* [128*max_blocks, f] bf16 x.W_up */
+  void* h;             /* [128*max_blocks, f] bf16 silu(gate)*up */
+  void* y_pad;         /* [128*max_blocks, d] bf16 expert outputs */
+} lsurge_moe_saved_views;
+int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_saved_views* v);
+
+/* ------------------------------------------------------------------------------------------------
+ * Live per-kernel timing with HIP events on the launch stream (used by the benchmark).
+ * ------------------------------------------------------------------------------------------------ */
+int lsurge_prof_enable(int on);            /* on=1: create events, start recording; 0: stop */
+int lsurge_prof_collect(void);             /* after a device sync: fold recorded pairs into totals */
+int lsurge_prof_kernel_count(void);
+const char* lsurge_prof_kernel_name(int id);
+int lsurge_prof_read(int id, double* total_ms, int64_t* launches);
+void lsurge_prof_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LEWI_SURGE_H_ */

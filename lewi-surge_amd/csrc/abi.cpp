@@ -1,0 +1,131 @@
+// Status reporting and the live event profiler of the C ABI.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <vector>
+
+#include "common.h"
+
+namespace lsurge {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(LSURGE_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return LSURGE_OK;
+}
+
+// ------------------------------------------------------------------------------ live profiler
+// Brackets selected kernels with a pair of HIP events recorded on the launch stream.  Only kernels whose
+// bit is set in the mask are bracketed, so the timed layer carries one event pair per step at most.
+
+namespace {
+struct Pair {
+  int kid;
+  hipEvent_t a, b;
+};
+std::mutex g_mu;
+bool g_on = false;
+uint64_t g_mask = 0;
+std::vector<Pair> g_pool;
+size_t g_used = 0;
+int g_open[KID_COUNT];
+double g_total_ms[KID_COUNT];
+int64_t g_count[KID_COUNT];
+const char* g_names[KID_COUNT] = {
+    "router_topk",      "layout_hist",       "layout_scan",       "layout_rank",      "dispatch",
+    "gemm_gu_fwd",      "gemm_down_fwd",     "combine_fwd",       "combine_bwd",      "gemm_down_dgrad",
+    "gemm_down_wgrad",  "gemm_gu_dgrad",     "gemm_gu_wgrad",     "dispatch_bwd",     "router_wgrad",
+    "shared_gu_fwd",    "shared_down_fwd",   "shared_down_dgrad", "shared_down_wgrad", "shared_gu_dgrad",
+    "shared_gu_wgrad",  "splitk_reduce",     "misc"};
+constexpr size_t kPool = 8192;
+}  // namespace
+
+hipError_t prof_mark_begin(int kid, hipStream_t s) {
+  if (!g_on || !((g_mask >> kid) & 1)) return hipSuccess;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_used >= g_pool.size()) return hipSuccess;  // pool exhausted: skip (collect() reports counts)
+  g_pool[g_used].kid = kid;
+  g_open[kid] = (int)g_used;
+  return hipEventRecord(g_pool[g_used++].a, s);
+}
+
+hipError_t prof_mark_end(int kid, hipStream_t s) {
+  if (!g_on || !((g_mask >> kid) & 1)) return hipSuccess;
+  std::lock_guard<std::mutex> lk(g_mu);
+  int i = g_open[kid];
+  if (i < 0) return hipSuccess;
+  g_open[kid] = -1;
+  return hipEventRecord(g_pool[i].b, s);
+}
+
+}  // namespace lsurge
+
+using namespace lsurge;
+
+extern "C" {
+
+int lsurge_abi_version(void) { return LSURGE_ABI_VERSION; }
+const char* lsurge_last_error(void) { return g_err; }
+
+int lsurge_prof_kernel_count(void) { return KID_COUNT; }
+const char* lsurge_prof_kernel_name(int id) { return (id >= 0 && id < KID_COUNT) ? g_names[id] : ""; }
+
+void lsurge_prof_reset(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (int i = 0; i < KID_COUNT; ++i) {
+    g_total_ms[i] = 0;
+    g_count[i] = 0;
+    g_open[i] = -1;
+  }
+  g_used = 0;
+}
+
+// on: 0 = off, otherwise a bit mask of kernel ids to bracket (all ones = every kernel).
+int lsurge_prof_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (on && g_pool.empty()) {
+    g_pool.resize(kPool);
+    for (auto& p : g_pool) {
+      if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess)
+        return set_error(LSURGE_ERR_LAUNCH, "hipEventCreate failed");
+    }
+  }
+  g_on = on != 0;
+  g_mask = (on == -1) ? ~0ull : (uint64_t)(uint32_t)on;
+  for (int i = 0; i < KID_COUNT; ++i) g_open[i] = -1;
+  return LSURGE_OK;
+}
+
+int lsurge_prof_collect(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  for (size_t i = 0; i < g_used; ++i) {
+    float ms = 0;
+    hipError_t e = hipEventElapsedTime(&ms, g_pool[i].a, g_pool[i].b);
+    if (e != hipSuccess) return set_error(LSURGE_ERR_LAUNCH, "hipEventElapsedTime: %s", hipGetErrorString(e));
+    g_total_ms[g_pool[i].kid] += ms;
+    g_count[g_pool[i].kid] += 1;
+  }
+  g_used = 0;
+  return LSURGE_OK;
+}
+
+int lsurge_prof_read(int id, double* total_ms, int64_t* launches) {
+  if (id < 0 || id >= KID_COUNT) return set_error(LSURGE_ERR_INVALID, "bad kernel id %d", id);
+  *total_ms = g_total_ms[id];
+  *launches = g_count[id];
+  return LSURGE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+// Shared device/host helpers for the MI355X (gfx950) MoE hot-path kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lewi_surge.h"
+
+typedef uint16_t bf16_t;  // bf16 storage (bit pattern)
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
+
+// ------------------------------------------------------------------------------------ scalar conversions
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {  // round to nearest even, NaN kept quiet
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// element load/store by runtime dtype tag (LSURGE_F32 / LSURGE_BF16 / LSURGE_F16)
+template <int DT> struct Elem;
+template <> struct Elem<LSURGE_F32> {
+  typedef float T;
+  static __device__ __forceinline__ float ld(const T* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = v; }
+};
+template <> struct Elem<LSURGE_BF16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float ld(const T* p, int64_t i) { return bf16_to_f32(p[i]); }
+  static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+};
+template <> struct Elem<LSURGE_F16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float ld(const T* p, int64_t i) { return f16_to_f32(p[i]); }
+  static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = f32_to_f16(v); }
+};
+
+// ------------------------------------------------------------------------------------ wave helpers
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ------------------------------------------------------------------------------------ host-side status
+
+namespace lsurge {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+hipError_t prof_mark_begin(int kernel_id, hipStream_t s);
+hipError_t prof_mark_end(int kernel_id, hipStream_t s);
+}  // namespace lsurge
+
+#define LSURGE_REQUIRE(cond, ...)                                         \
+  do {                                                                    \
+    if (!(cond)) return lsurge::set_error(LSURGE_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+// Kernel ids for the live profiler (lsurge_prof_*); names in abi.cpp.
+enum {
+  KID_ROUTER = 0,
+  KID_LAYOUT_HIST,
+  KID_LAYOUT_SCAN,
+  KID_LAYOUT_RANK,
+  KID_DISPATCH,
+  KID_GEMM_GU_FWD,
+  KID_GEMM_DOWN_FWD,
+  KID_COMBINE_FWD,
+  KID_COMBINE_BWD,
+  KID_GEMM_DOWN_DGRAD,
+  KID_GEMM_DOWN_WGRAD,
+  KID_GEMM_GU_DGRAD,
+  KID_GEMM_GU_WGRAD,
+  KID_DISPATCH_BWD,
+  KID_ROUTER_WGRAD,
+  KID_SHARED_GU_FWD,
+  KID_SHARED_DOWN_FWD,
+  KID_SHARED_DOWN_DGRAD,
+  KID_SHARED_DOWN_WGRAD,
+  KID_SHARED_GU_DGRAD,
+  KID_SHARED_GU_WGRAD,
+  KID_SPLITK_REDUCE,
+  KID_MISC,
+  KID_COUNT
+};
+
+// RAII-free launch bracket used by the layer entry points.
+#define LSURGE_LAUNCH(kid, stream, ...)             \
+  do {                                              \
+    (void)lsurge::prof_mark_begin((kid), (stream)); \
+    __VA_ARGS__;                                    \
+    (void)lsurge::prof_mark_end((kid), (stream));   \
+    int _rc = lsurge::check_launch(#kid);           \
+    if (_rc) return _rc;                            \
+  } while (0)

@@ -1,0 +1,640 @@
+// Grouped GEMMs of the MoE layer on CDNA4 matrix cores: bf16 inputs, f32 accumulation,
+// v_mfma_f32_32x32x16_bf16, 128x128 workgroup tiles (4 waves, 64x64 each), K staged through LDS in
+// 64-wide double-buffered chunks.
+//
+// Replaces the padded batched einsum of modal/padded_gmm.py:66-69 (cuBLAS on the reference's GPU path) and
+// its autodiff.  Two kernel families:
+//
+//  gemm_rows   row-blocked: C[block rows, n-tile] = A[block rows, :] @ B[expert(block)], one 128-row expert
+//              block per workgroup row.  Blocks past the device-side block count exit at once, so padding
+//              tiles cost nothing; rows past a block's valid count are loaded as zeros.
+//              B either K-major ([N, K], read with ds_read_b128) or N-major ([K, N], read with the gfx950
+//              LDS transpose read ds_read_b64_tr_b16).  Epilogues: plain bf16 store, SwiGLU forward
+//              (gate and up tiles side by side in one accumulator set -> h = silu(g) * u, plus g and u
+//              for the backward), SwiGLU backward (dH -> dG, dU from the saved g, u).
+//  gemm_wgrad  per-expert weight gradient: C_e = A_e^T @ B_e with the reduction over the expert's rows
+//              (ragged K); both operands N-major in LDS, transpose-read.  Optional split of the rows into
+//              S slices with f32 partials summed afterwards in a fixed order (deterministic, no atomics).
+#include "common.h"
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int GT = 256;           // threads per workgroup
+constexpr int KPAD = 8;           // K-major LDS row padding (elements)
+constexpr int NPAD = 8;           // N-major LDS row padding (elements)
+constexpr int KM_PITCH = BK + KPAD;   // K-major tile pitch: [rows][KM_PITCH]
+constexpr int NM_PITCH = BN + NPAD;   // N-major tile pitch: [BK][NM_PITCH]
+
+enum { B_NK = 0, B_KN = 1 };                        // B operand storage
+enum { EPI_STORE = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
+
+struct RowsArgs {
+  const bf16_t* A;  // rows with K contiguous
+  int64_t lda;
+  const bf16_t* B;   // expert 0 of the first B matrix
+  const bf16_t* B2;  // second B (SwiGLU up weights / dgrad up weights), same strides
+  int64_t ldb;       // row pitch of B as stored
+  int64_t b_estride; // elements between experts
+  int64_t K, N;      // reduction dim, output columns (EPI_SWIGLU_FWD: N = f, tile covers 64 outputs)
+  int64_t k_split;   // B_NK with B2: k < k_split from B, else B2 at k - k_split (0 = unused)
+  bf16_t* C;         // output [rows, ldc]
+  float* Cf;         // EPI_STORE: f32 output instead of C when set
+  int64_t ldc;
+  bf16_t* G;         // SwiGLU saved gate pre-activation [rows, ldg] (fwd: written, bwd: read)
+  bf16_t* U;         // SwiGLU saved up projection
+  int64_t ldg;
+  const int32_t* blk_expert;  // nullptr: dense (expert 0, rows = min(128, dense_rows - 128 b))
+  const int32_t* blk_rows;
+  const int32_t* blk_row0;    // first row of block b (nullptr: 128 b)
+  const int32_t* num_blocks;
+  int64_t dense_rows;
+  int n_tiles;
+  int max_blocks;
+};
+
+struct WgradArgs {
+  const bf16_t* A;   // [rows, lda], the reduction runs over rows; C's rows are A's columns
+  int64_t lda;
+  const bf16_t* B;   // [rows, ldb]
+  int64_t ldb;
+  int64_t I, N;      // output [I, N] per expert
+  float* C;          // expert e at C + e * c_estride, row pitch ldc
+  float* C2;         // columns n >= n_split go to C2 at column n - n_split (nullptr: unused)
+  int64_t n_split;
+  int64_t ldc, c_estride;
+  float* part;       // split partials [S][E][I][N] when S > 1
+  const int32_t* e_row0;  // first row of expert e, in units of row0_mult rows (nullptr: dense)
+  const int32_t* e_rows;  // rows of expert e
+  int row0_mult;
+  int64_t dense_rows;
+  int E, S, i_tiles, n_tiles;
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// K-major fragment: 8 consecutive k of one row -> one 16-byte LDS read
+__device__ __forceinline__ bf16x8 frag_kmajor(const bf16_t* tile, int row, int k) {
+  return as_bf16x8(*reinterpret_cast<const u32x4*>(tile + row * KM_PITCH + k));
+}
+
+// N-major fragment for the 32x32x16 operand layout: lane l needs rows (k) 8(l/32)+0..7 of column l%32.
+// ds_read_b64_tr_b16 in a 16-lane group g: lane i receives D[4j + i/4][i%4], j = 0..3, where D[s] are the four
+// 16-bit values at source lane s's address.  With source lane s pointing at (k = kb + s/4, n = nb + 4(s%4)),
+// lane i receives column nb + i, rows kb..kb+3.  Two reads give the 8 k values.
+__device__ __forceinline__ bf16x8 frag_nmajor(const bf16_t* tile, int kbase, int nbase, int lane) {
+  const int g = lane >> 4, s = lane & 15;
+  const int n = nbase + 16 * (g & 1) + 4 * (s & 3);
+  const int k0 = kbase + 8 * (g >> 1) + (s >> 2);
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, tile + k0 * NM_PITCH + n));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, tile + (k0 + 4) * NM_PITCH + n));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ u32x4 ld16(const bf16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(bf16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.f + __expf(-g)); }
+
+// XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so consecutive logical
+// tiles (same expert block, neighbouring N tiles and experts) are sent to the same XCD's L2.
+__device__ __forceinline__ int64_t xcd_logical(int64_t id, int64_t total) {
+  const int64_t per = total / 8;
+  return (id % 8) * per + id / 8;
+}
+
+// =====================================================================================================
+template <int BMODE, int EPI>
+__global__ __launch_bounds__(GT, 2) void gemm_rows_kernel(RowsArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * KM_PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BMODE == B_NK ? BN * KM_PITCH : BK * NM_PITCH];
+
+  const int64_t total = (int64_t)gridDim.x;
+  const int64_t logical = xcd_logical(blockIdx.x, total);
+  const int nt = (int)(logical % a.n_tiles);
+  const int b = (int)(logical / a.n_tiles);
+  if (b >= a.max_blocks) return;
+  int expert, rows;
+  int64_t row0;
+  if (a.blk_expert) {
+    if (b >= a.num_blocks[0]) return;
+    expert = a.blk_expert[b];
+    rows = a.blk_rows[b];
+    row0 = a.blk_row0 ? (int64_t)a.blk_row0[b] : (int64_t)b * BM;
+  } else {
+    expert = 0;
+    row0 = (int64_t)b * BM;
+    rows = (int)min((int64_t)BM, a.dense_rows - row0);
+    if (rows <= 0) return;
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  // output column origin of this tile
+  const int64_t n0 = (EPI == EPI_SWIGLU_FWD) ? (int64_t)nt * 64 : (int64_t)nt * BN;
+  const bf16_t* Bbase = a.B + (int64_t)expert * a.b_estride;
+  const bf16_t* B2base = a.B2 ? a.B2 + (int64_t)expert * a.b_estride : nullptr;
+  const int64_t K = a.K;
+  const int nk = (int)((K + BK - 1) / BK);
+
+  // ---- global -> register staging (4 x 16 B per thread for each operand)
+  u32x4 ra[4], rb[4];
+  auto load_tiles = [&](int kt) {
+    const int64_t k0 = (int64_t)kt * BK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = tid + GT * i;
+      const int r = v >> 3, kv = (v & 7) * 8;
+      const bool ok = r < rows && k0 + kv < K;
+      ra[i] = ok ? ld16(a.A + (row0 + r) * a.lda + k0 + kv) : u32x4{0, 0, 0, 0};
+    }
+    if (BMODE == B_NK) {
+      const bf16_t* src = Bbase;
+      int64_t kk0 = k0;
+      if (a.k_split && k0 >= a.k_split) {
+        src = B2base;
+        kk0 = k0 - a.k_split;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int v = tid + GT * i;
+        const int n = v >> 3, kv = (v & 7) * 8;
+        const int64_t gn = n0 + n;
+        const bool ok = gn < a.N && k0 + kv < K;
+        rb[i] = ok ? ld16(src + gn * a.ldb + kk0 + kv) : u32x4{0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int v = tid + GT * i;
+        const int kr = v >> 4, nv = (v & 15) * 8;
+        const int64_t gk = k0 + kr;
+        const bf16_t* src;
+        int64_t gn;
+        if (EPI == EPI_SWIGLU_FWD) {
+          src = nv < 64 ? Bbase : B2base;
+          gn = n0 + (nv & 63);
+        } else {
+          src = Bbase;
+          gn = n0 + nv;
+        }
+        const bool ok = gk < K && gn < a.N;
+        rb[i] = ok ? ld16(src + gk * a.ldb + gn) : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto store_tiles = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = tid + GT * i;
+      st16(&As[buf][(v >> 3) * KM_PITCH + (v & 7) * 8], ra[i]);
+      if (BMODE == B_NK) st16(&Bs[buf][(v >> 3) * KM_PITCH + (v & 7) * 8], rb[i]);
+      else st16(&Bs[buf][(v >> 4) * NM_PITCH + (v & 15) * 8], rb[i]);
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  // column origin (inside the tile) of this wave's two 32-wide fragments
+  auto ncol = [&](int j) { return EPI == EPI_SWIGLU_FWD ? j * 64 + 32 * wn : wn * 64 + 32 * j; };
+
+  load_tiles(0);
+  store_tiles(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load_tiles(kt + 1);
+    const bf16_t* at = As[buf];
+    const bf16_t* bt = Bs[buf];
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) fa[i] = frag_kmajor(at, wm * 64 + 32 * i + (lane & 31), kk + 8 * (lane >> 5));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (BMODE == B_NK) fb[j] = frag_kmajor(bt, ncol(j) + (lane & 31), kk + 8 * (lane >> 5));
+        else fb[j] = frag_nmajor(bt, kk, ncol(j), lane);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) store_tiles(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue.  acc[i][j][r]: row wm*64 + 32 i + 8 (r/4) + 4 (lane/32) + r%4, column ncol(j) + lane%32
+  const int lc = lane & 31, lr = 4 * (lane >> 5);
+  if (EPI == EPI_SWIGLU_FWD) {
+    const int64_t col = n0 + 32 * wn + lc;
+    if (col < a.N) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = wm * 64 + 32 * i + 8 * (r >> 2) + lr + (r & 3);
+          if (row < rows) {
+            const float g = acc[i][0][r], u = acc[i][1][r];
+            const int64_t gr = row0 + row;
+            a.C[gr * a.ldc + col] = f32_to_bf16(silu_f(g) * u);
+            if (a.G) a.G[gr * a.ldg + col] = f32_to_bf16(g);
+            if (a.U) a.U[gr * a.ldg + col] = f32_to_bf16(u);
+          }
+        }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + ncol(j) + lc;
+      if (col >= a.N) continue;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = wm * 64 + 32 * i + 8 * (r >> 2) + lr + (r & 3);
+          if (row >= rows) continue;
+          const int64_t gr = row0 + row;
+          const float v = acc[i][j][r];
+          if (EPI == EPI_STORE) {
+            if (a.Cf) a.Cf[gr * a.ldc + col] = v;
+            else a.C[gr * a.ldc + col] = f32_to_bf16(v);
+          } else {  // EPI_SWIGLU_BWD: v = dH; dgu row = [dG (N cols) | dU (N cols)]
+            const float g = bf16_to_f32(a.G[gr * a.ldg + col]);
+            const float u = bf16_to_f32(a.U[gr * a.ldg + col]);
+            const float sg = 1.f / (1.f + __expf(-g));
+            const float dg = v * u * sg * (1.f + g * (1.f - sg));
+            const float du = v * g * sg;
+            a.C[gr * a.ldc + col] = f32_to_bf16(dg);
+            a.C[gr * a.ldc + a.N + col] = f32_to_bf16(du);
+          }
+        }
+    }
+  }
+}
+
+// =====================================================================================================
+__global__ __launch_bounds__(GT, 2) void gemm_wgrad_kernel(WgradArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16_t As[2][BK * NM_PITCH];
+  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BK * NM_PITCH];
+  const int64_t total = (int64_t)gridDim.x;
+  int64_t logical = xcd_logical(blockIdx.x, total);
+  const int64_t tiles_per_e = (int64_t)a.S * a.i_tiles * a.n_tiles;
+  const int e = (int)(logical / tiles_per_e);
+  if (e >= a.E) return;
+  int64_t rem = logical % tiles_per_e;
+  const int s = (int)(rem / ((int64_t)a.i_tiles * a.n_tiles));
+  rem %= (int64_t)a.i_tiles * a.n_tiles;
+  const int it = (int)(rem / a.n_tiles), nt = (int)(rem % a.n_tiles);
+  int64_t r0, nrows;
+  if (a.e_rows) {
+    r0 = (int64_t)a.e_row0[e] * a.row0_mult;
+    nrows = a.e_rows[e];
+  } else {
+    r0 = 0;
+    nrows = a.dense_rows;
+  }
+  // rows of split s
+  const int64_t chunk = ((nrows + a.S - 1) / a.S + BK - 1) / BK * BK;
+  const int64_t rs = (int64_t)s * chunk;
+  const int64_t re = min(nrows, rs + chunk);
+  const int64_t i0 = (int64_t)it * BM, n0 = (int64_t)nt * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  const int nk = re > rs ? (int)((re - rs + BK - 1) / BK) : 0;
+  u32x4 ra[4], rb[4];
+  auto load_tiles = [&](int kt) {
+    const int64_t rbase = rs + (int64_t)kt * BK;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int v = tid + GT * q;
+      const int rr = v >> 4, cv = (v & 15) * 8;
+      const int64_t row = rbase + rr;
+      const bool rok = row < re;
+      ra[q] = (rok && i0 + cv < a.I) ? ld16(a.A + (r0 + row) * a.lda + i0 + cv) : u32x4{0, 0, 0, 0};
+      rb[q] = (rok && n0 + cv < a.N) ? ld16(a.B + (r0 + row) * a.ldb + n0 + cv) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_tiles = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int v = tid + GT * q;
+      st16(&As[buf][(v >> 4) * NM_PITCH + (v & 15) * 8], ra[q]);
+      st16(&Bs[buf][(v >> 4) * NM_PITCH + (v & 15) * 8], rb[q]);
+    }
+  };
+  if (nk > 0) {
+    load_tiles(0);
+    store_tiles(0);
+    __syncthreads();
+  }
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load_tiles(kt + 1);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) fa[i] = frag_nmajor(As[buf], kk, wm * 64 + 32 * i, lane);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[j] = frag_nmajor(Bs[buf], kk, wn * 64 + 32 * j, lane);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) store_tiles(buf ^ 1);
+    __syncthreads();
+  }
+  // epilogue (f32)
+  const int lc = lane & 31, lr = 4 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t col = n0 + wn * 64 + 32 * j + lc;
+    if (col >= a.N) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = i0 + wm * 64 + 32 * i + 8 * (r >> 2) + lr + (r & 3);
+        if (row >= a.I) continue;
+        const float v = acc[i][j][r];
+        if (a.S > 1) {
+          a.part[(((int64_t)s * a.E + e) * a.I + row) * a.N + col] = v;
+        } else if (a.C2 && col >= a.n_split) {
+          a.C2[(int64_t)e * a.c_estride + row * a.ldc + (col - a.n_split)] = v;
+        } else {
+          a.C[(int64_t)e * a.c_estride + row * a.ldc + col] = v;
+        }
+      }
+  }
+}
+
+// sum of the S split partials in split order -> C (and C2 for n >= n_split)
+__global__ void splitk_reduce_kernel(const float* __restrict__ part, int S, int E, int64_t I, int64_t N,
+                                     float* __restrict__ C, float* __restrict__ C2, int64_t n_split, int64_t ldc,
+                                     int64_t c_estride) {
+  const int64_t total = (int64_t)E * I * N;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < total; x += (int64_t)gridDim.x * blockDim.x) {
+    float v = 0.f;
+    for (int s = 0; s < S; ++s) v += part[(int64_t)s * total + x];
+    const int64_t e = x / (I * N), rem = x % (I * N);
+    const int64_t row = rem / N, col = rem % N;
+    if (C2 && col >= n_split) C2[e * c_estride + row * ldc + (col - n_split)] = v;
+    else C[e * c_estride + row * ldc + col] = v;
+  }
+}
+
+// block table of an unpadded ragged layout (rows of group e start at sum_{e'<e} gs[e'])
+__global__ void ragged_blocks_kernel(const int32_t* __restrict__ gs, int E, int max_blocks, int32_t* __restrict__ blk_row0,
+                                     int32_t* __restrict__ blk_rows, int32_t* __restrict__ blk_expert,
+                                     int32_t* __restrict__ num_blocks, int32_t* __restrict__ total_rows,
+                                     int32_t* __restrict__ e_row0) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int b = 0, run = 0;
+  for (int e = 0; e < E; ++e) {
+    const int g = gs[e];
+    e_row0[e] = run;
+    for (int j = 0; j * BM < g; ++j, ++b) {
+      if (b < max_blocks) {
+        blk_row0[b] = run + j * BM;
+        blk_rows[b] = min(BM, g - j * BM);
+        blk_expert[b] = e;
+      }
+    }
+    run += g;
+  }
+  num_blocks[0] = min(b, max_blocks);
+  total_rows[0] = run;
+  for (int i = b; i < max_blocks; ++i) {
+    blk_rows[i] = 0;
+    blk_expert[i] = -1;
+  }
+}
+
+// zero the rows [from[0], m) of an [m, n] matrix with esize-byte elements (rows past the groups)
+__global__ void zero_rows_from_kernel(void* __restrict__ out, int64_t m, int64_t n, int esize,
+                                      const int32_t* __restrict__ from) {
+  const int64_t r0 = from[0];
+  const int64_t total = (m - r0) * n;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < total; x += (int64_t)gridDim.x * blockDim.x) {
+    if (esize == 4) ((float*)out)[r0 * n + x] = 0.f;
+    else ((bf16_t*)out)[r0 * n + x] = 0;
+  }
+}
+
+inline unsigned pad8(int64_t g) { return (unsigned)((g + 7) / 8 * 8); }
+
+}  // namespace
+
+// ------------------------------------------------------------------------------ internal launchers
+namespace lsurge {
+
+struct GemmBlocks {
+  const int32_t* blk_expert;
+  const int32_t* blk_rows;
+  const int32_t* blk_row0;
+  const int32_t* num_blocks;
+  int max_blocks;
+  int64_t dense_rows;  // used when blk_expert == nullptr
+};
+
+static int check_gemm_shape(int64_t K, int64_t N, const char* what) {
+  LSURGE_REQUIRE(K > 0 && N > 0 && K % 8 == 0 && N % 8 == 0, "%s: K=%lld N=%lld must be positive multiples of 8", what,
+                 (long long)K, (long long)N);
+  return LSURGE_OK;
+}
+
+static int max_blocks_of(const GemmBlocks& g) {
+  return g.blk_expert ? g.max_blocks : (int)((g.dense_rows + BM - 1) / BM);
+}
+
+// C[rows, N] = A[rows, K] @ B_e where B_e is [K, N] (n-major) -- forward projections
+int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, int64_t ldb,
+                 int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32) {
+  if (int rc = check_gemm_shape(K, N, "gemm_rows_kn")) return rc;
+  RowsArgs a{};
+  a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.b_estride = b_estride;
+  a.K = K; a.N = N; a.ldc = ldc;
+  if (out_f32) a.Cf = (float*)C;
+  else a.C = (bf16_t*)C;
+  a.blk_expert = g.blk_expert; a.blk_rows = g.blk_rows; a.blk_row0 = g.blk_row0; a.num_blocks = g.num_blocks;
+  a.dense_rows = g.dense_rows; a.max_blocks = max_blocks_of(g);
+  a.n_tiles = (int)((N + BN - 1) / BN);
+  if (a.max_blocks == 0) return LSURGE_OK;
+  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<B_KN, EPI_STORE>),
+                                           dim3(pad8((int64_t)a.n_tiles * a.max_blocks)), dim3(GT), 0, s, a));
+  return LSURGE_OK;
+}
+
+// h = silu(A @ Bg) * (A @ Bu); also stores g, u.  Bg, Bu: [K, N] per expert.
+int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* Bg, const void* Bu,
+                         int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* H, void* Gs, void* Us,
+                         int64_t ldh, hipStream_t s) {
+  if (int rc = check_gemm_shape(K, N, "gemm_rows_swiglu_fwd")) return rc;
+  RowsArgs a{};
+  a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)Bg; a.B2 = (const bf16_t*)Bu; a.ldb = ldb;
+  a.b_estride = b_estride; a.K = K; a.N = N; a.C = (bf16_t*)H; a.ldc = ldh; a.G = (bf16_t*)Gs; a.U = (bf16_t*)Us;
+  a.ldg = ldh;
+  a.blk_expert = g.blk_expert; a.blk_rows = g.blk_rows; a.blk_row0 = g.blk_row0; a.num_blocks = g.num_blocks;
+  a.dense_rows = g.dense_rows; a.max_blocks = max_blocks_of(g);
+  a.n_tiles = (int)((N + 63) / 64);
+  if (a.max_blocks == 0) return LSURGE_OK;
+  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<B_KN, EPI_SWIGLU_FWD>),
+                                           dim3(pad8((int64_t)a.n_tiles * a.max_blocks)), dim3(GT), 0, s, a));
+  return LSURGE_OK;
+}
+
+// C[rows, N] = A[rows, K] @ B_e^T where B_e is stored [N, K] (k-major); with B2 and k_split the K range
+// [k_split, K) reads B2 (gate/up dgrad: A = [dG | dU], B = W_gate, B2 = W_up, k_split = f).
+// swiglu_bwd: C = [dG | dU] from dH = A @ B^T and the saved G, U (ldg pitch).
+int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
+                 int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
+                 bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32) {
+  if (int rc = check_gemm_shape(K, N, "gemm_rows_nk")) return rc;
+  LSURGE_REQUIRE(!B2 || (k_split > 0 && k_split % BK == 0), "gemm_rows_nk: k_split must be a multiple of %d", BK);
+  RowsArgs a{};
+  a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.B2 = (const bf16_t*)B2; a.k_split = B2 ? k_split : 0;
+  a.ldb = ldb; a.b_estride = b_estride; a.K = K; a.N = N; a.ldc = ldc;
+  if (out_f32 && !swiglu_bwd) a.Cf = (float*)C;
+  else a.C = (bf16_t*)C;
+  a.G = (bf16_t*)Gs; a.U = (bf16_t*)Us; a.ldg = ldg;
+  a.blk_expert = g.blk_expert; a.blk_rows = g.blk_rows; a.blk_row0 = g.blk_row0; a.num_blocks = g.num_blocks;
+  a.dense_rows = g.dense_rows; a.max_blocks = max_blocks_of(g);
+  a.n_tiles = (int)((N + BN - 1) / BN);
+  if (a.max_blocks == 0) return LSURGE_OK;
+  const dim3 grid(pad8((int64_t)a.n_tiles * a.max_blocks));
+  if (swiglu_bwd)
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<B_NK, EPI_SWIGLU_BWD>), grid, dim3(GT), 0, s, a));
+  else
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<B_NK, EPI_STORE>), grid, dim3(GT), 0, s, a));
+  return LSURGE_OK;
+}
+
+size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S) {
+  return S > 1 ? sizeof(float) * (size_t)S * E * I * N : 0;
+}
+
+// C_e[I, N] = A_e^T @ B_e over the rows of expert e; columns >= n_split go to C2 (if given).
+int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows, const void* A,
+               int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
+               int64_t ldc, int64_t c_estride, int S, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (int rc = check_gemm_shape(I, N, "gemm_wgrad")) return rc;
+  LSURGE_REQUIRE(S >= 1 && E >= 1, "gemm_wgrad: bad S/E");
+  WgradArgs a{};
+  a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.I = I; a.N = N; a.C = C; a.C2 = C2;
+  a.n_split = n_split; a.ldc = ldc; a.c_estride = c_estride; a.e_row0 = e_row0; a.e_rows = e_rows;
+  a.row0_mult = row0_mult;
+  a.dense_rows = dense_rows; a.E = E; a.S = S;
+  a.i_tiles = (int)((I + BM - 1) / BM);
+  a.n_tiles = (int)((N + BN - 1) / BN);
+  if (S > 1) {
+    const size_t need = wgrad_workspace_bytes(E, I, N, S);
+    LSURGE_REQUIRE(ws && ws_bytes >= need, "gemm_wgrad: workspace %zu < %zu", ws_bytes, need);
+    a.part = (float*)ws;
+  }
+  const int64_t tiles = (int64_t)E * S * a.i_tiles * a.n_tiles;
+  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel, dim3(pad8(tiles)), dim3(GT), 0, s, a));
+  if (S > 1) {
+    const int64_t total = (int64_t)E * I * N;
+    const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+    LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
+                  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(256), 0, s, (const float*)ws, S, E, I, N, C,
+                                     C2, n_split, ldc, c_estride));
+  }
+  return LSURGE_OK;
+}
+
+}  // namespace lsurge
+
+// ------------------------------------------------------------------------------ C ABI: ragged_dot
+// workspace: blk_row0, blk_rows, blk_expert [max_blocks] | num_blocks, total_rows | e_row0 [e]
+extern "C" {
+
+size_t lsurge_ragged_dot_workspace_bytes(int64_t m, int64_t e) {
+  const int64_t mb = lsurge_max_blocks(m, e);
+  return sizeof(int32_t) * (size_t)(3 * mb + 4 + e);
+}
+
+static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_t ws_bytes, hipStream_t s,
+                        lsurge::GemmBlocks* g, int32_t** total_rows, int32_t** e_row0) {
+  const size_t need = lsurge_ragged_dot_workspace_bytes(m, e);
+  LSURGE_REQUIRE(ws && ws_bytes >= need, "ragged_dot: workspace %zu < %zu bytes", ws_bytes, need);
+  const int64_t mb = lsurge_max_blocks(m, e);
+  int32_t* p = (int32_t*)ws;
+  int32_t* blk_row0 = p;
+  int32_t* blk_rows = p + mb;
+  int32_t* blk_expert = p + 2 * mb;
+  int32_t* nb = p + 3 * mb;
+  *total_rows = nb + 1;
+  *e_row0 = nb + 4;
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(ragged_blocks_kernel, dim3(1), dim3(64), 0, s, gs, (int)e, (int)mb, blk_row0, blk_rows,
+                                   blk_expert, nb, *total_rows, *e_row0));
+  g->blk_expert = blk_expert;
+  g->blk_rows = blk_rows;
+  g->blk_row0 = blk_row0;
+  g->num_blocks = nb;
+  g->max_blocks = (int)mb;
+  g->dense_rows = 0;
+  return LSURGE_OK;
+}
+
+int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_sizes, int64_t m, int64_t kdim, int64_t n,
+                      int64_t e, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
+                      lsurge_stream_t stream) {
+  LSURGE_REQUIRE(m >= 0 && e >= 1 && m < (1ll << 31), "ragged_dot: bad m/e");
+  LSURGE_REQUIRE(out_dtype == LSURGE_BF16 || out_dtype == LSURGE_F32, "ragged_dot: out_dtype must be bf16 or f32");
+  if (m == 0) return LSURGE_OK;
+  LSURGE_REQUIRE(lhs && rhs && group_sizes && out, "ragged_dot: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  lsurge::GemmBlocks g;
+  int32_t *total, *e_row0;
+  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0)) return rc;
+  const bool f32 = out_dtype == LSURGE_F32;
+  if (int rc = lsurge::gemm_rows_kn(KID_MISC, g, lhs, kdim, rhs, n, kdim * n, kdim, n, out, n, s, f32)) return rc;
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, out, m, n, f32 ? 4 : 2, total));
+  return LSURGE_OK;
+}
+
+int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group_sizes, const void* g, int64_t m,
+                          int64_t kdim, int64_t n, int64_t e, void* dlhs, float* drhs, void* workspace,
+                          size_t workspace_bytes, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(m >= 0 && e >= 1 && m < (1ll << 31), "ragged_dot_bwd: bad m/e");
+  LSURGE_REQUIRE(lhs && rhs && group_sizes && g && dlhs && drhs, "ragged_dot_bwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  lsurge::GemmBlocks gb;
+  int32_t *total, *e_row0;
+  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &gb, &total, &e_row0)) return rc;
+  // dlhs[r] = g[r] @ rhs[e]^T : rhs[e] is [K, N] = k-major storage of the [N -> K] operand
+  if (m > 0) {
+    if (int rc = lsurge::gemm_rows_nk(KID_MISC, gb, g, n, rhs, nullptr, 0, n, kdim * n, n, kdim, dlhs, kdim, false,
+                                      nullptr, nullptr, 0, s, false))
+      return rc;
+    LSURGE_LAUNCH(KID_MISC, s,
+                  hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, dlhs, m, kdim, 2, total));
+  }
+  // drhs[e] = lhs_e^T @ g_e
+  return lsurge::gemm_wgrad(KID_MISC, (int)e, e_row0, 1, group_sizes, 0, lhs, kdim, g, n, kdim, n, drhs, nullptr, 0, n,
+                            kdim * n, 1, nullptr, 0, s);
+}
+
+}  // extern "C"

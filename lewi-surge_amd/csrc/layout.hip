@@ -1,0 +1,280 @@
+// Routing layout: stable counting sort of the flat (token, choice) slots by expert, without atomics on
+// global memory, plus the padded 128-row block table.
+//
+// Replaces moe_permute.sort_indices (modal/moe_permute.py:240-264: one-hot chunk cumsum -> offsets ->
+// pos = offsets[e] + rank) and padded_gmm's row<->slot maps (modal/padded_gmm.py:51-64).
+//
+// Three kernels:
+//   hist  one workgroup per chunk of LT_CHUNK slots; per-wave LDS histograms -> hist[chunk][E]
+//   scan  one workgroup: per expert, exclusive scan over chunks (chunk_base), group sizes, expert
+//         offsets, block offsets, block table and padding markers in row_src
+//   rank  one workgroup per chunk again; each wave walks its slots 64 at a time in ascending slot order:
+//         lanes with the same expert are found with 8 ballots over the expert-id bits, the rank inside
+//         the wave is popcount(peers below me), and a per-wave LDS counter advances by popcount(peers).
+#include "common.h"
+
+namespace {
+
+constexpr int LT_THREADS = 256;
+constexpr int LT_WAVES = LT_THREADS / 64;
+constexpr int LT_PER_WAVE = 512;                       // slots per wave per chunk
+constexpr int LT_CHUNK = LT_WAVES * LT_PER_WAVE;       // 2048 slots per workgroup
+constexpr int LT_EMAX = 1024;
+constexpr int BLK = LSURGE_BLOCK_ROWS;
+
+__global__ __launch_bounds__(LT_THREADS) void layout_hist_kernel(const int32_t* __restrict__ flat, int64_t M,
+                                                                 int E, int32_t* __restrict__ hist) {
+  extern __shared__ int32_t h[];  // [LT_WAVES][E]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  for (int i = tid; i < LT_WAVES * E; i += LT_THREADS) h[i] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * LT_CHUNK + (int64_t)wv * LT_PER_WAVE;
+  for (int r = 0; r < LT_PER_WAVE; r += 64) {
+    const int64_t i = base + r + lane;
+    if (i < M) {
+      const int e = flat[i];
+      if (e >= 0 && e < E) atomicAdd(&h[wv * E + e], 1);  // LDS counter: order-independent result
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += LT_THREADS) {
+    int c = 0;
+    for (int w = 0; w < LT_WAVES; ++w) c += h[w * E + e];
+    hist[(int64_t)blockIdx.x * E + e] = c;
+  }
+}
+
+// One workgroup.  hist [nchunk][E] is overwritten with the exclusive per-expert chunk base.
+__global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__ hist, int nchunk, int E,
+                                                           int32_t* __restrict__ group_sizes,
+                                                           int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ block_off,
+                                                           int32_t* __restrict__ row_src,
+                                                           int32_t* __restrict__ blk_expert,
+                                                           int32_t* __restrict__ blk_rows,
+                                                           int32_t* __restrict__ num_blocks, int max_blocks) {
+  __shared__ int32_t gs_s[LT_EMAX], off_s[LT_EMAX], boff_s[LT_EMAX + 1];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += blockDim.x) {
+    int run = 0;
+    for (int c = 0; c < nchunk; ++c) {
+      const int v = hist[(int64_t)c * E + e];
+      hist[(int64_t)c * E + e] = run;
+      run += v;
+    }
+    gs_s[e] = run;
+  }
+  __syncthreads();
+  if (tid == 0) {  // E <= 1024: a serial scan is a few microseconds at most
+    int run = 0, brun = 0;
+    for (int e = 0; e < E; ++e) {
+      off_s[e] = run;
+      boff_s[e] = brun;
+      run += gs_s[e];
+      brun += (gs_s[e] + BLK - 1) / BLK;
+    }
+    boff_s[E] = brun;
+    num_blocks[0] = brun;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += blockDim.x) {
+    if (group_sizes) group_sizes[e] = gs_s[e];
+    if (offsets) offsets[e] = off_s[e];
+    if (block_off) block_off[e] = boff_s[e];
+  }
+  if (!blk_expert) return;
+  // block table; padding rows of the last block of each expert get row_src = -1
+  const int nb = boff_s[E];
+  for (int b = tid; b < max_blocks; b += blockDim.x) {
+    if (b >= nb) {
+      blk_expert[b] = -1;
+      blk_rows[b] = 0;
+      continue;
+    }
+    int lo = 0, hi = E - 1;  // expert e with boff[e] <= b < boff[e+1] (skips empty experts)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (boff_s[mid] <= b) lo = mid;
+      else hi = mid - 1;
+    }
+    const int e = lo;
+    const int j = b - boff_s[e];
+    const int rows = min(BLK, gs_s[e] - j * BLK);
+    blk_expert[b] = e;
+    blk_rows[b] = rows;
+    for (int r = rows; r < BLK; ++r) row_src[(int64_t)b * BLK + r] = -1;
+  }
+}
+
+__device__ __forceinline__ uint64_t peers_of(int key, int nbits) {
+  uint64_t m = ~0ull;
+  for (int b = 0; b < nbits; ++b) {
+    const uint64_t bal = __ballot((key >> b) & 1);
+    m &= ((key >> b) & 1) ? bal : ~bal;
+  }
+  return m;
+}
+
+__global__ __launch_bounds__(LT_THREADS) void layout_rank_kernel(
+    const int32_t* __restrict__ flat, int64_t M, int E, const int32_t* __restrict__ chunk_base,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ block_off, int nbits,
+    int32_t* __restrict__ order, int32_t* __restrict__ pos, int32_t* __restrict__ slot,
+    int32_t* __restrict__ row_src) {
+  extern __shared__ int32_t sh[];  // cnt[LT_WAVES][E] (per-wave running rank base inside the expert)
+  int32_t* cnt = sh;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t cbase = (int64_t)blockIdx.x * LT_CHUNK;
+  for (int i = tid; i < LT_WAVES * E; i += LT_THREADS) cnt[i] = 0;
+  __syncthreads();
+  // per-wave histograms of this chunk
+  for (int r = 0; r < LT_PER_WAVE; r += 64) {
+    const int64_t i = cbase + (int64_t)wv * LT_PER_WAVE + r + lane;
+    if (i < M) {
+      const int e = flat[i];
+      if (e >= 0 && e < E) atomicAdd(&cnt[wv * E + e], 1);
+    }
+  }
+  __syncthreads();
+  // exclusive scan over waves, seeded with the chunk base (rank of the first slot of this chunk in e)
+  for (int e = tid; e < E; e += LT_THREADS) {
+    int run = chunk_base[(int64_t)blockIdx.x * E + e];
+    for (int w = 0; w < LT_WAVES; ++w) {
+      const int v = cnt[w * E + e];
+      cnt[w * E + e] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  int32_t* my = cnt + wv * E;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int r = 0; r < LT_PER_WAVE; r += 64) {
+    const int64_t i = cbase + (int64_t)wv * LT_PER_WAVE + r + lane;
+    const int fe = i < M ? flat[i] : -1;
+    const bool valid = fe >= 0 && fe < E;  // ids outside [0, E) are skipped (documented as invalid input)
+    const int e = valid ? fe : -1;
+    // invalid lanes use key with all bits set above E's range; they never match a valid expert
+    const int key = valid ? e : ((1 << nbits) - 1);
+    uint64_t peers = peers_of(key, nbits) & __ballot(valid);
+    if (!valid) peers = 0;
+    const int rank_in = __popcll(peers & below);
+    int rank = 0;
+    if (valid) rank = my[e] + rank_in;
+    // the highest peer lane advances the counter after everyone has read it
+    __builtin_amdgcn_wave_barrier();
+    if (valid && (peers >> lane) == 1ull) my[e] = rank + 1;
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      const int p = offsets[e] + rank;
+      if (pos) pos[i] = p;
+      if (order) order[p] = (int32_t)i;
+      if (slot) {
+        const int sl = BLK * block_off[e] + rank;
+        slot[i] = sl;
+        if (row_src) row_src[sl] = (int32_t)i;
+      }
+    }
+  }
+}
+
+__global__ void invert_perm_kernel(const int32_t* __restrict__ idx, int64_t m, int32_t* __restrict__ inv) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < m) inv[idx[i]] = (int32_t)i;
+}
+
+int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
+                  int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
+                  int32_t* blk_rows, int32_t* num_blocks, int64_t max_blocks, void* ws, size_t ws_bytes,
+                  hipStream_t s) {
+  const int64_t nchunk = (M + LT_CHUNK - 1) / LT_CHUNK;
+  // workspace: hist [nchunk][E] | offsets [E] | block_off [E] | num_blocks (when caller gives none)
+  const size_t need = sizeof(int32_t) * (size_t)(nchunk * E + 2 * E + 4);
+  LSURGE_REQUIRE(ws && ws_bytes >= need, "layout: workspace %zu < %zu bytes", ws_bytes, need);
+  int32_t* hist = (int32_t*)ws;
+  int32_t* off_ws = hist + nchunk * E;
+  int32_t* boff_ws = off_ws + E;
+  int32_t* nb_ws = boff_ws + E;
+  if (!offsets) offsets = off_ws;
+  if (!block_off) block_off = boff_ws;
+  if (!num_blocks) num_blocks = nb_ws;
+  int nbits = 1;
+  while ((1ll << nbits) <= E) ++nbits;  // keys 0..E-1 valid, (1<<nbits)-1 >= E reserved for idle lanes
+  if (M == 0) {
+    LSURGE_LAUNCH(KID_LAYOUT_SCAN, s,
+                  hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(1024), 0, s, hist, 0, (int)E, gs, offsets,
+                                     block_off, row_src, blk_expert, blk_rows, num_blocks, (int)max_blocks));
+    return LSURGE_OK;
+  }
+  const size_t lds = sizeof(int32_t) * LT_WAVES * (size_t)E;
+  LSURGE_LAUNCH(KID_LAYOUT_HIST, s,
+                hipLaunchKernelGGL(layout_hist_kernel, dim3((unsigned)nchunk), dim3(LT_THREADS), lds, s, flat, M,
+                                   (int)E, hist));
+  LSURGE_LAUNCH(KID_LAYOUT_SCAN, s,
+                hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nchunk, (int)E, gs,
+                                   offsets, block_off, row_src, blk_expert, blk_rows, num_blocks,
+                                   (int)max_blocks));
+  LSURGE_LAUNCH(KID_LAYOUT_RANK, s,
+                hipLaunchKernelGGL(layout_rank_kernel, dim3((unsigned)nchunk), dim3(LT_THREADS), lds, s, flat, M,
+                                   (int)E, hist, offsets, block_off, nbits, order, pos, slot, row_src));
+  return LSURGE_OK;
+}
+
+}  // namespace
+
+namespace lsurge {
+int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
+                      int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
+                      int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s) {
+  return layout_common(flat, M, E, gs, offsets, block_off, order, pos, slot, row_src, blk_expert, blk_rows,
+                       num_blocks, lsurge_max_blocks(M, E), ws, ws_bytes, s);
+}
+}  // namespace lsurge
+
+extern "C" {
+
+int64_t lsurge_max_blocks(int64_t m, int64_t num_experts) { return (m + BLK - 1) / BLK + num_experts; }
+
+size_t lsurge_layout_workspace_bytes(int64_t m, int64_t num_experts) {
+  const int64_t nchunk = (m + LT_CHUNK - 1) / LT_CHUNK;
+  return sizeof(int32_t) * (size_t)(nchunk * num_experts + 2 * num_experts + 4);
+}
+
+size_t lsurge_sort_indices_workspace_bytes(int64_t m, int64_t num_experts) {
+  return lsurge_layout_workspace_bytes(m, num_experts);
+}
+
+int lsurge_sort_indices(const int32_t* flat, int64_t m, int64_t num_experts, int32_t* order, int32_t* pos,
+                        int32_t* group_sizes, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(m >= 0 && m < (1ll << 31), "sort_indices: bad m=%lld", (long long)m);
+  LSURGE_REQUIRE(num_experts >= 1 && num_experts <= LT_EMAX, "sort_indices: num_experts=%lld not in [1, %d]",
+                 (long long)num_experts, LT_EMAX);
+  LSURGE_REQUIRE(m == 0 || (flat && order && pos), "sort_indices: null pointer");
+  return layout_common(flat, m, num_experts, group_sizes, nullptr, nullptr, order, pos, nullptr, nullptr, nullptr,
+                       nullptr, nullptr, 0, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int lsurge_build_layout(const int32_t* flat, int64_t m, int64_t num_experts, int32_t* group_sizes, int32_t* offsets,
+                        int32_t* block_off, int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src,
+                        int32_t* blk_expert, int32_t* blk_rows, int32_t* num_blocks, void* workspace,
+                        size_t workspace_bytes, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(m >= 0 && m < (1ll << 31), "build_layout: bad m=%lld", (long long)m);
+  LSURGE_REQUIRE(num_experts >= 1 && num_experts <= LT_EMAX, "build_layout: num_experts=%lld not in [1, %d]",
+                 (long long)num_experts, LT_EMAX);
+  LSURGE_REQUIRE(m == 0 || (flat && order && pos && slot && row_src), "build_layout: null pointer");
+  LSURGE_REQUIRE(blk_expert && blk_rows && num_blocks, "build_layout: null block table");
+  return lsurge::build_layout_impl(flat, m, num_experts, group_sizes, offsets, block_off, order, pos, slot, row_src,
+                                   blk_expert, blk_rows, num_blocks, workspace, workspace_bytes,
+                                   (hipStream_t)stream);
+}
+
+int lsurge_invert_permutation(const int32_t* idx, int64_t m, int32_t* inv, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(m >= 0 && m < (1ll << 31), "invert_permutation: bad m");
+  if (m == 0) return LSURGE_OK;
+  LSURGE_REQUIRE(idx && inv, "invert_permutation: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(invert_perm_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, idx, m,
+                                   inv));
+  return LSURGE_OK;
+}
+
+}  // extern "C"

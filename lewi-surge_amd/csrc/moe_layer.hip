@@ -1,0 +1,315 @@
+// Whole MoE layer, forward and gather-only backward, as one stream-ordered sequence of the hot-path kernels.
+//
+// Forward:  router top-k -> routing layout -> dispatch into 128-row expert blocks -> gate/up grouped GEMM with
+//           the SiLU*mul epilogue -> down grouped GEMM -> weighted combine (+ shared expert, the dense E = 1 case
+//           of the same GEMMs).
+// Backward: fused combine backward (dY rows, d(routing weights), d(router logits)) -> down dgrad with the
+//           SwiGLU backward epilogue -> down wgrad -> gate/up dgrad -> gate/up wgrad -> shared expert ->
+//           router wgrad -> dispatch backward (gather-reduce, plus the router and shared-expert dx terms).
+// No scatter-add anywhere: every row written by a kernel has exactly one writer.
+//
+// The reference composes these from MaxText RoutedMoE (third-party) with the patches of modal/moe_permute.py
+// (dispatch/combine, 270-312) and modal/padded_gmm.py (ragged_dot, 45-69); the call order mirrors
+// moe_permute.moe_block (modal/moe_permute.py:348-353) with a SwiGLU expert_fn.
+#include <cstring>
+
+#include "common.h"
+
+namespace lsurge {
+int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
+                      int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
+                      int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s);
+int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src, const int32_t* num_blocks,
+                        int64_t max_rows, void* xp, hipStream_t s);
+int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, const float* w, int64_t n,
+                       const void* add, void* out, int out_dtype, hipStream_t s);
+int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
+                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s);
+int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* slot, int64_t n, const float* dl,
+                            const int32_t* sel, const void* w_rT, const void* add, void* dx, hipStream_t s);
+int launch_transpose_bf16(const void* a, int R, int C, void* at, hipStream_t s);
+int launch_scatter_dlogits(const float* dl, const int32_t* sel, int64_t T, int E, int k, void* dlog, hipStream_t s);
+
+struct GemmBlocks {
+  const int32_t* blk_expert;
+  const int32_t* blk_rows;
+  const int32_t* blk_row0;
+  const int32_t* num_blocks;
+  int max_blocks;
+  int64_t dense_rows;
+};
+int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, int64_t ldb,
+                 int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32 = false);
+int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* Bg, const void* Bu,
+                         int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* H, void* Gs, void* Us,
+                         int64_t ldh, hipStream_t s);
+int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
+                 int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
+                 bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false);
+size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S);
+int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
+               const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2,
+               int64_t n_split, int64_t ldc, int64_t c_estride, int S, void* ws, size_t ws_bytes, hipStream_t s);
+}  // namespace lsurge
+
+namespace {
+
+constexpr int BLK = LSURGE_BLOCK_ROWS;
+
+// Bump allocator over a caller buffer, 256-byte aligned pieces.
+struct Carve {
+  char* base;
+  size_t off = 0;
+  explicit Carve(void* b) : base((char*)b) {}
+  template <class T> T* take(size_t count) {
+    off = (off + 255) & ~(size_t)255;
+    T* p = base ? (T*)(base + off) : nullptr;
+    off += sizeof(T) * count;
+    return p;
+  }
+};
+
+struct Dims {
+  int64_t T, d, E, k, f, fs, M, MB, P;
+};
+
+Dims dims_of(const lsurge_moe_shape* s) {
+  Dims q;
+  q.T = s->t; q.d = s->d; q.E = s->e; q.k = s->k; q.f = s->f; q.fs = s->fs;
+  q.M = q.T * q.k;
+  q.MB = lsurge_max_blocks(q.M, q.E);
+  q.P = q.MB * BLK;
+  return q;
+}
+
+struct Saved {
+  float* logits;
+  int32_t *sel;
+  float* weights;
+  int32_t *gs, *offsets, *block_off, *order, *pos, *slot, *row_src, *blk_expert, *blk_rows, *num_blocks;
+  bf16_t *x_pad, *g, *u, *h, *y_pad;
+  bf16_t *sg, *su, *sh, *sy;  // shared expert: gate, up, h, output
+};
+
+size_t carve_saved(const Dims& q, void* base, Saved* sv) {
+  Carve c(base);
+  sv->logits = c.take<float>(q.T * q.E);
+  sv->sel = c.take<int32_t>(q.M);
+  sv->weights = c.take<float>(q.M);
+  sv->gs = c.take<int32_t>(q.E);
+  sv->offsets = c.take<int32_t>(q.E);
+  sv->block_off = c.take<int32_t>(q.E);
+  sv->order = c.take<int32_t>(q.M);
+  sv->pos = c.take<int32_t>(q.M);
+  sv->slot = c.take<int32_t>(q.M);
+  sv->row_src = c.take<int32_t>(q.P);
+  sv->blk_expert = c.take<int32_t>(q.MB);
+  sv->blk_rows = c.take<int32_t>(q.MB);
+  sv->num_blocks = c.take<int32_t>(4);
+  sv->x_pad = c.take<bf16_t>(q.P * q.d);
+  sv->g = c.take<bf16_t>(q.P * q.f);
+  sv->u = c.take<bf16_t>(q.P * q.f);
+  sv->h = c.take<bf16_t>(q.P * q.f);
+  sv->y_pad = c.take<bf16_t>(q.P * q.d);
+  sv->sg = c.take<bf16_t>(q.T * q.fs);
+  sv->su = c.take<bf16_t>(q.T * q.fs);
+  sv->sh = c.take<bf16_t>(q.T * q.fs);
+  sv->sy = c.take<bf16_t>(q.fs ? q.T * q.d : 0);
+  return c.off + 256;
+}
+
+// split count for a dense (one-expert) weight gradient: enough workgroups to fill 256 CUs
+int dense_splits(int64_t rows, int64_t I, int64_t N) {
+  const int64_t tiles = ((I + 127) / 128) * ((N + 127) / 128);
+  int64_t S = (512 + tiles - 1) / tiles;
+  S = std::min<int64_t>(S, 16);
+  S = std::min<int64_t>(S, std::max<int64_t>(1, rows / 256));
+  return (int)std::max<int64_t>(1, S);
+}
+
+struct BwdWs {
+  bf16_t *dy_pad, *dgu, *dx_pad, *sdgu, *sdx, *dlog, *w_rT;
+  float* dl;
+  float* dweights;
+  void* part;
+  size_t part_bytes;
+};
+
+size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
+  Carve c(base);
+  w->dy_pad = c.take<bf16_t>(q.P * q.d);
+  w->dgu = c.take<bf16_t>(q.P * 2 * q.f);
+  w->dx_pad = c.take<bf16_t>(q.P * q.d);
+  w->sdgu = c.take<bf16_t>(q.T * 2 * q.fs);
+  w->sdx = c.take<bf16_t>(q.fs ? q.T * q.d : 0);
+  w->dlog = c.take<bf16_t>(q.T * q.E);
+  w->w_rT = c.take<bf16_t>(q.E * q.d);
+  w->dl = c.take<float>(q.M);
+  w->dweights = c.take<float>(q.M);
+  size_t part = 0;
+  if (q.fs) {
+    part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, 2 * q.fs, dense_splits(q.T, q.d, 2 * q.fs)));
+    part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.fs, q.d, dense_splits(q.T, q.fs, q.d)));
+  }
+  part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, q.E, dense_splits(q.T, q.d, q.E)));
+  w->part_bytes = part;
+  w->part = c.take<char>(part);
+  return c.off + 256;
+}
+
+int check_shape(const lsurge_moe_shape* s) {
+  LSURGE_REQUIRE(s, "moe: null shape");
+  LSURGE_REQUIRE(s->t >= 1 && s->d >= 8 && s->e >= 1 && s->e <= 256 && s->k >= 1 && s->k <= s->e && s->k <= 16 &&
+                     s->f >= 64 && s->fs >= 0,
+                 "moe: bad shape t=%lld d=%lld e=%lld k=%lld f=%lld fs=%lld", (long long)s->t, (long long)s->d,
+                 (long long)s->e, (long long)s->k, (long long)s->f, (long long)s->fs);
+  LSURGE_REQUIRE(s->e % 8 == 0, "moe: e=%lld must be a multiple of 8", (long long)s->e);
+  LSURGE_REQUIRE(s->d % 64 == 0 && s->f % 64 == 0 && s->fs % 64 == 0,
+                 "moe: d, f and fs must be multiples of 64 (d=%lld f=%lld fs=%lld)", (long long)s->d, (long long)s->f,
+                 (long long)s->fs);
+  LSURGE_REQUIRE(s->t * s->k < (1ll << 31) && lsurge_max_blocks(s->t * s->k, s->e) * BLK < (1ll << 31),
+                 "moe: too many routed rows");
+  return LSURGE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t lsurge_moe_saved_bytes(const lsurge_moe_shape* s) {
+  if (check_shape(s)) return 0;
+  Saved sv;
+  return carve_saved(dims_of(s), nullptr, &sv);
+}
+
+size_t lsurge_moe_fwd_workspace_bytes(const lsurge_moe_shape* s) {
+  if (check_shape(s)) return 0;
+  return lsurge_layout_workspace_bytes(s->t * s->k, s->e) + 256;
+}
+
+size_t lsurge_moe_bwd_workspace_bytes(const lsurge_moe_shape* s) {
+  if (check_shape(s)) return 0;
+  BwdWs w;
+  return carve_bwd(dims_of(s), nullptr, &w);
+}
+
+int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_saved_views* v) {
+  if (int rc = check_shape(s)) return rc;
+  LSURGE_REQUIRE(saved && v, "moe_saved_layout: null pointer");
+  Saved sv;
+  carve_saved(dims_of(s), saved, &sv);
+  v->logits = sv.logits; v->sel = sv.sel; v->weights = sv.weights; v->group_sizes = sv.gs; v->offsets = sv.offsets;
+  v->block_off = sv.block_off; v->order = sv.order; v->pos = sv.pos; v->slot = sv.slot; v->row_src = sv.row_src;
+  v->blk_expert = sv.blk_expert; v->blk_rows = sv.blk_rows; v->num_blocks = sv.num_blocks; v->x_pad = sv.x_pad;
+  v->h_gate = sv.g; v->h_up = sv.u; v->h = sv.h; v->y_pad = sv.y_pad;
+  return LSURGE_OK;
+}
+
+int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* out, void* saved, size_t saved_bytes,
+                   void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+  if (int rc = check_shape(s)) return rc;
+  LSURGE_REQUIRE(p && p->x && p->w_r && p->w_gate && p->w_up && p->w_down && out && saved, "moe_fwd: null pointer");
+  LSURGE_REQUIRE(!s->fs || (p->ws_gate && p->ws_up && p->ws_down), "moe_fwd: shared expert weights missing");
+  const Dims q = dims_of(s);
+  Saved sv;
+  const size_t need = carve_saved(q, nullptr, &sv);
+  LSURGE_REQUIRE(saved_bytes >= need, "moe_fwd: saved buffer %zu < %zu bytes", saved_bytes, need);
+  carve_saved(q, saved, &sv);
+  hipStream_t st = (hipStream_t)stream;
+
+  if (int rc = lsurge_router_topk(p->x, p->w_r, p->bias, q.T, q.d, q.E, q.k, sv.logits, sv.sel, sv.weights, stream))
+    return rc;
+  if (int rc = lsurge::build_layout_impl(sv.sel, q.M, q.E, sv.gs, sv.offsets, sv.block_off, sv.order, sv.pos, sv.slot,
+                                         sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks, workspace,
+                                         workspace_bytes, st))
+    return rc;
+  if (int rc = lsurge::launch_dispatch_pad(p->x, q.d, (int)q.k, sv.row_src, sv.num_blocks, q.P, sv.x_pad, st)) return rc;
+  const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+  if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_GEMM_GU_FWD, blocks, sv.x_pad, q.d, p->w_gate, p->w_up, q.f, q.d * q.f,
+                                            q.d, q.f, sv.h, sv.g, sv.u, q.f, st))
+    return rc;
+  if (int rc = lsurge::gemm_rows_kn(KID_GEMM_DOWN_FWD, blocks, sv.h, q.f, p->w_down, q.d, q.f * q.d, q.f, q.d, sv.y_pad,
+                                    q.d, st))
+    return rc;
+  if (q.fs) {
+    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
+    if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
+                                              q.fs, sv.sh, sv.sg, sv.su, q.fs, st))
+      return rc;
+    if (int rc = lsurge::gemm_rows_kn(KID_SHARED_DOWN_FWD, dense, sv.sh, q.fs, p->ws_down, q.d, 0, q.fs, q.d, sv.sy, q.d,
+                                      st))
+      return rc;
+  }
+  return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sv.sy : nullptr, out,
+                                    LSURGE_BF16, st);
+}
+
+int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* dy, const void* saved,
+                   const lsurge_moe_grads* g, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+  if (int rc = check_shape(s)) return rc;
+  LSURGE_REQUIRE(p && p->x && p->w_r && p->w_gate && p->w_up && p->w_down && dy && saved && g, "moe_bwd: null pointer");
+  LSURGE_REQUIRE(g->dx && g->dw_r && g->dw_gate && g->dw_up && g->dw_down, "moe_bwd: null gradient pointer");
+  LSURGE_REQUIRE(!s->fs || (p->ws_gate && p->ws_up && p->ws_down && g->dws_gate && g->dws_up && g->dws_down),
+                 "moe_bwd: shared expert pointers missing");
+  const Dims q = dims_of(s);
+  Saved sv;
+  carve_saved(q, (void*)saved, &sv);
+  BwdWs w;
+  const size_t need = carve_bwd(q, nullptr, &w);
+  LSURGE_REQUIRE(workspace && workspace_bytes >= need, "moe_bwd: workspace %zu < %zu bytes", workspace_bytes, need);
+  carve_bwd(q, workspace, &w);
+  hipStream_t st = (hipStream_t)stream;
+  float* dweights = g->dweights ? g->dweights : w.dweights;
+  const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+
+  // combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel)
+  if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, q.P, sv.slot, sv.weights, q.T, (int)q.k, q.d, dy, w.dy_pad, dweights,
+                                              w.dl, st))
+    return rc;
+  // down dgrad + SwiGLU backward: dH = dY W_down^T -> [dG | dU]
+  if (int rc = lsurge::gemm_rows_nk(KID_GEMM_DOWN_DGRAD, blocks, w.dy_pad, q.d, p->w_down, nullptr, 0, q.d, q.f * q.d,
+                                    q.d, q.f, w.dgu, 2 * q.f, true, sv.g, sv.u, q.f, st))
+    return rc;
+  // down wgrad: dW_down[e] = h_e^T dY_e
+  if (int rc = lsurge::gemm_wgrad(KID_GEMM_DOWN_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, sv.h, q.f, w.dy_pad, q.d,
+                                  q.f, q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, 1, nullptr, 0, st))
+    return rc;
+  // gate/up dgrad: dX_pad = dG W_gate^T + dU W_up^T
+  if (int rc = lsurge::gemm_rows_nk(KID_GEMM_GU_DGRAD, blocks, w.dgu, 2 * q.f, p->w_gate, p->w_up, q.f, q.f, q.d * q.f,
+                                    2 * q.f, q.d, w.dx_pad, q.d, false, nullptr, nullptr, 0, st))
+    return rc;
+  // gate/up wgrad: [dW_gate | dW_up][e] = x_e^T [dG | dU]_e
+  if (int rc = lsurge::gemm_wgrad(KID_GEMM_GU_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, sv.x_pad, q.d, w.dgu,
+                                  2 * q.f, q.d, 2 * q.f, g->dw_gate, g->dw_up, q.f, q.f, q.d * q.f, 1, nullptr, 0, st))
+    return rc;
+  if (q.fs) {
+    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
+    if (int rc = lsurge::gemm_rows_nk(KID_SHARED_DOWN_DGRAD, dense, dy, q.d, p->ws_down, nullptr, 0, q.d, 0, q.d, q.fs,
+                                      w.sdgu, 2 * q.fs, true, sv.sg, sv.su, q.fs, st))
+      return rc;
+    int S = dense_splits(q.T, q.fs, q.d);
+    if (int rc = lsurge::gemm_wgrad(KID_SHARED_DOWN_WGRAD, 1, nullptr, 1, nullptr, q.T, sv.sh, q.fs, dy, q.d, q.fs, q.d,
+                                    g->dws_down, nullptr, 0, q.d, 0, S, w.part, w.part_bytes, st))
+      return rc;
+    if (int rc = lsurge::gemm_rows_nk(KID_SHARED_GU_DGRAD, dense, w.sdgu, 2 * q.fs, p->ws_gate, p->ws_up, q.fs, q.fs, 0,
+                                      2 * q.fs, q.d, w.sdx, q.d, false, nullptr, nullptr, 0, st))
+      return rc;
+    S = dense_splits(q.T, q.d, 2 * q.fs);
+    if (int rc = lsurge::gemm_wgrad(KID_SHARED_GU_WGRAD, 1, nullptr, 1, nullptr, q.T, p->x, q.d, w.sdgu, 2 * q.fs, q.d,
+                                    2 * q.fs, g->dws_gate, g->dws_up, q.fs, q.fs, 0, S, w.part, w.part_bytes, st))
+      return rc;
+  }
+  // router: dW_r = x^T dlogits (bf16 MFMA over the dense [T, E] dlogits), dx += dlogits W_r^T in dispatch bwd
+  if (int rc = lsurge::launch_scatter_dlogits(w.dl, sv.sel, q.T, (int)q.E, (int)q.k, w.dlog, st)) return rc;
+  {
+    const int S = dense_splits(q.T, q.d, q.E);
+    if (int rc = lsurge::gemm_wgrad(KID_ROUTER_WGRAD, 1, nullptr, 1, nullptr, q.T, p->x, q.d, w.dlog, q.E, q.d, q.E,
+                                    g->dw_r, nullptr, 0, q.E, 0, S, w.part, w.part_bytes, st))
+      return rc;
+  }
+  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, st)) return rc;
+  return lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT,
+                                         q.fs ? w.sdx : nullptr, g->dx, st);
+}
+
+}  // extern "C"

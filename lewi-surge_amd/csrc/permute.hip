@@ -1,0 +1,536 @@
+// Memory-bound row movement: gather_rows, gather_reduce, gather_dot, fused combine backward, and the
+// padded-layout dispatch / combine / dispatch-backward used by the fused layer.
+//
+// Replaces the Pallas-TPU row-DMA kernels of modal/moe_permute.py:116-234 (gather_rows, _reduce_like).
+// On CDNA a row is moved by one wave with 16-byte vector accesses (coalesced 1 KiB per instruction); there
+// is no need for the TPU's bf16 u32 packing (moe_permute.py:68-84).  All reductions run in f32 with the
+// choice index j ascending, the order of moe_permute.py:189-200.
+#include "common.h"
+
+namespace {
+
+constexpr int PM_THREADS = 256;
+constexpr int PM_WAVES = PM_THREADS / 64;
+
+// 8 consecutive elements <-> 8 floats
+template <int DT> struct V8;
+template <> struct V8<LSURGE_BF16> {
+  static __device__ __forceinline__ void ld(const void* p, float* v) {
+    const u32x4 u = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(u[i] << 16);
+      v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ void st(void* p, const float* v) {
+    u32x4 u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+    *reinterpret_cast<u32x4*>(p) = u;
+  }
+};
+template <> struct V8<LSURGE_F16> {
+  static __device__ __forceinline__ void ld(const void* p, float* v) {
+    const u32x4 u = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = f16_to_f32((uint16_t)(u[i] & 0xffffu));
+      v[2 * i + 1] = f16_to_f32((uint16_t)(u[i] >> 16));
+    }
+  }
+  static __device__ __forceinline__ void st(void* p, const float* v) {
+    u32x4 u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = (uint32_t)f32_to_f16(v[2 * i]) | ((uint32_t)f32_to_f16(v[2 * i + 1]) << 16);
+    *reinterpret_cast<u32x4*>(p) = u;
+  }
+};
+template <> struct V8<LSURGE_F32> {
+  static __device__ __forceinline__ void ld(const void* p, float* v) {
+    const f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
+    const f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = a[i];
+      v[4 + i] = b[i];
+    }
+  }
+  static __device__ __forceinline__ void st(void* p, const float* v) {
+    f32x4 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = v[i];
+      b[i] = v[4 + i];
+    }
+    reinterpret_cast<f32x4*>(p)[0] = a;
+    reinterpret_cast<f32x4*>(p)[1] = b;
+  }
+};
+
+template <int DT> constexpr int esize() { return DT == LSURGE_F32 ? 4 : 2; }
+
+// value after a round trip through element type DT
+template <int DT> __device__ __forceinline__ float round_to(float v) {
+  if (DT == LSURGE_BF16) return bf16_to_f32(f32_to_bf16(v));
+  if (DT == LSURGE_F16) return f16_to_f32(f32_to_f16(v));
+  return v;
+}
+
+// ------------------------------------------------------------------------------ gather_rows
+// out[i] = x[idx[i]] (byte copy), or round(f32(x[idx[i]]) * scale[i]).  An index outside [0, n) gives a zero
+// row (padded_gmm's zero-row sentinel, modal/padded_gmm.py:26-28).
+template <int DT, bool VEC>
+__global__ __launch_bounds__(PM_THREADS) void gather_rows_kernel(const void* __restrict__ x, int64_t n, int64_t d,
+                                                                 const int32_t* __restrict__ idx, int64_t m,
+                                                                 const float* __restrict__ scale,
+                                                                 void* __restrict__ out) {
+  constexpr int ES = esize<DT>();
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  for (int64_t i = wave; i < m; i += nwaves) {
+    const int64_t src = idx[i];
+    const char* xr = (const char*)x + src * d * ES;
+    char* orow = (char*)out + i * d * ES;
+    if (src < 0 || src >= n) {
+      if (VEC) {
+        for (int64_t c = lane * 8; c < d; c += 64 * 8)
+          for (int h = 0; h < ES * 8 / 16; ++h) reinterpret_cast<u32x4*>(orow + c * ES)[h] = u32x4{0, 0, 0, 0};
+      } else {
+        typedef typename Elem<DT>::T T;
+        for (int64_t c = lane; c < d; c += 64) ((T*)orow)[c] = (T)0;
+      }
+      continue;
+    }
+    if (VEC) {
+      if (!scale) {
+        for (int64_t c = lane * 8; c < d; c += 64 * 8)
+          for (int h = 0; h < ES * 8 / 16; ++h)
+            reinterpret_cast<u32x4*>(orow + c * ES)[h] = reinterpret_cast<const u32x4*>(xr + c * ES)[h];
+      } else {
+        const float sc = scale[i];
+        for (int64_t c = lane * 8; c < d; c += 64 * 8) {
+          float v[8];
+          V8<DT>::ld(xr + c * ES, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] *= sc;
+          V8<DT>::st(orow + c * ES, v);
+        }
+      }
+    } else {
+      typedef typename Elem<DT>::T T;
+      const T* xs = (const T*)xr;
+      T* os = (T*)orow;
+      if (!scale) {
+        for (int64_t c = lane; c < d; c += 64) os[c] = xs[c];
+      } else {
+        const float sc = scale[i];
+        for (int64_t c = lane; c < d; c += 64) Elem<DT>::st(os, c, Elem<DT>::ld(xs, c) * sc);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------ gather_reduce / dot
+template <int DT, int OT, bool VEC>
+__global__ __launch_bounds__(PM_THREADS) void gather_reduce_kernel(const void* __restrict__ y, int64_t m, int64_t d,
+                                                                   const int32_t* __restrict__ pos, int64_t n, int k,
+                                                                   const float* __restrict__ w,
+                                                                   void* __restrict__ out) {
+  constexpr int ES = esize<DT>(), OS = esize<OT>();
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  for (int64_t t = wave; t < n; t += nwaves) {
+    if (VEC) {
+      for (int64_t c = lane * 8; c < d; c += 64 * 8) {
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int j = 0; j < k; ++j) {
+          const int64_t r = pos[t * k + j];
+          if (r < 0 || r >= m) continue;  // out-of-range position contributes nothing
+          const float wj = w ? w[t * k + j] : 1.f;
+          float v[8];
+          V8<DT>::ld((const char*)y + (r * d + c) * ES, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] = w ? acc[e] + wj * v[e] : acc[e] + v[e];
+        }
+        V8<OT>::st((char*)out + (t * d + c) * OS, acc);
+      }
+    } else {
+      typedef typename Elem<DT>::T T;
+      typedef typename Elem<OT>::T O;
+      for (int64_t c = lane; c < d; c += 64) {
+        float acc = 0.f;
+        for (int j = 0; j < k; ++j) {
+          const int64_t r = pos[t * k + j];
+          if (r < 0 || r >= m) continue;
+          const float v = Elem<DT>::ld((const T*)y, r * d + c);
+          acc = w ? acc + w[t * k + j] * v : acc + v;
+        }
+        Elem<OT>::st((O*)out, t * d + c, acc);
+      }
+    }
+  }
+}
+
+template <int DT, int GT, bool VEC>
+__global__ __launch_bounds__(PM_THREADS) void gather_dot_kernel(const void* __restrict__ y, int64_t m, int64_t d,
+                                                                const int32_t* __restrict__ pos, int64_t n, int k,
+                                                                const void* __restrict__ g,
+                                                                float* __restrict__ out) {
+  constexpr int ES = esize<DT>(), GS = esize<GT>();
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  for (int64_t t = wave; t < n; t += nwaves) {
+    for (int j = 0; j < k; ++j) {
+      const int64_t r = pos[t * k + j];
+      float acc = 0.f;
+      if (r < 0 || r >= m) {
+        // out-of-range position: dot product 0
+      } else if (VEC) {
+        for (int64_t c = lane * 8; c < d; c += 64 * 8) {
+          float v[8], gv[8];
+          V8<DT>::ld((const char*)y + (r * d + c) * ES, v);
+          V8<GT>::ld((const char*)g + (t * d + c) * GS, gv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc += v[e] * gv[e];
+        }
+      } else {
+        typedef typename Elem<DT>::T T;
+        typedef typename Elem<GT>::T G;
+        for (int64_t c = lane; c < d; c += 64)
+          acc += Elem<DT>::ld((const T*)y, r * d + c) * Elem<GT>::ld((const G*)g, t * d + c);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) out[t * k + j] = acc;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------ fused combine backward
+// One wave per token: g[t] is read once; for every j the expert row y[pos] is read, dy[pos] written and
+// the dot <g, y[pos]> reduced.  Optionally also the router backward dl[t,j] = w_j (dw_j - sum_i w_i dw_i).
+template <int DT, int GT, bool VEC>
+__global__ __launch_bounds__(PM_THREADS) void combine_bwd_kernel(const void* __restrict__ y, int64_t m,
+                                                                 const int32_t* __restrict__ pos,
+                                                                 const float* __restrict__ w, int64_t n, int k,
+                                                                 int64_t d, const void* __restrict__ g,
+                                                                 void* __restrict__ dy, float* __restrict__ dw,
+                                                                 float* __restrict__ dl) {
+  constexpr int ES = esize<DT>(), GS = esize<GT>();
+  typedef typename Elem<DT>::T T;
+  typedef typename Elem<GT>::T G;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  for (int64_t t = wave; t < n; t += nwaves) {
+    float dwv[16];
+    for (int j = 0; j < k; ++j) {
+      const int64_t r = pos[t * k + j];
+      const float wj = w[t * k + j];
+      float acc = 0.f;
+      if (r < 0 || r >= m) {
+        // out-of-range position: nothing written, dw = 0
+      } else if (VEC) {
+        for (int64_t c = lane * 8; c < d; c += 64 * 8) {
+          float v[8], gv[8], o[8];
+          V8<DT>::ld((const char*)y + (r * d + c) * ES, v);
+          V8<GT>::ld((const char*)g + (t * d + c) * GS, gv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            if (GT != DT) gv[e] = round_to<DT>(gv[e]);  // g.astype(y.dtype) first (moe_permute.py:307)
+            acc += v[e] * gv[e];
+            o[e] = wj * gv[e];
+          }
+          V8<DT>::st((char*)dy + (r * d + c) * ES, o);
+        }
+      } else {
+        for (int64_t c = lane; c < d; c += 64) {
+          float gv = Elem<GT>::ld((const G*)g, t * d + c);
+          if (GT != DT) gv = round_to<DT>(gv);
+          acc += Elem<DT>::ld((const T*)y, r * d + c) * gv;
+          Elem<DT>::st((T*)dy, r * d + c, wj * gv);
+        }
+      }
+      acc = wave_sum(acc);
+      if (j < 16) dwv[j] = acc;
+      if (lane == 0 && dw) dw[t * k + j] = acc;
+    }
+    if (dl && lane == 0) {
+      float s = 0.f;
+      for (int j = 0; j < k; ++j) s += w[t * k + j] * dwv[j];
+      for (int j = 0; j < k; ++j) dl[t * k + j] = w[t * k + j] * (dwv[j] - s);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------ padded-layout layer kernels
+// dispatch: x_pad[r] = x[row_src[r] / k] for valid padded rows of the used blocks (padding rows untouched;
+// the GEMMs mask them by blk_rows).
+__global__ __launch_bounds__(PM_THREADS) void dispatch_pad_kernel(const bf16_t* __restrict__ x, int64_t d, int k,
+                                                                  const int32_t* __restrict__ row_src,
+                                                                  const int32_t* __restrict__ num_blocks,
+                                                                  int64_t max_rows, bf16_t* __restrict__ xp) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  const int64_t rows = min((int64_t)num_blocks[0] * LSURGE_BLOCK_ROWS, max_rows);
+  for (int64_t r = wave; r < rows; r += nwaves) {
+    const int32_t src = row_src[r];
+    if (src < 0) continue;
+    const bf16_t* xr = x + (int64_t)(src / k) * d;
+    bf16_t* o = xp + r * d;
+    for (int64_t c = lane * 8; c < d; c += 64 * 8)
+      *reinterpret_cast<u32x4*>(o + c) = *reinterpret_cast<const u32x4*>(xr + c);
+  }
+}
+
+// combine: out[t] = sum_j w[t,j] * y_pad[slot[t,j]] (+ add[t]), f32 accumulate, j ascending, one rounding.
+template <int OT>
+__global__ __launch_bounds__(PM_THREADS) void combine_pad_kernel(const bf16_t* __restrict__ yp, int64_t d, int k,
+                                                                 const int32_t* __restrict__ slot,
+                                                                 const float* __restrict__ w, int64_t n,
+                                                                 const bf16_t* __restrict__ add,
+                                                                 void* __restrict__ out) {
+  constexpr int OS = esize<OT>();
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  for (int64_t t = wave; t < n; t += nwaves) {
+    for (int64_t c = lane * 8; c < d; c += 64 * 8) {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int j = 0; j < k; ++j) {
+        const int64_t r = slot[t * k + j];
+        const float wj = w[t * k + j];
+        float v[8];
+        V8<LSURGE_BF16>::ld(yp + r * d + c, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += wj * v[e];
+      }
+      if (add) {
+        float v[8];
+        V8<LSURGE_BF16>::ld(add + t * d + c, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += v[e];
+      }
+      V8<OT>::st((char*)out + (t * d + c) * OS, acc);
+    }
+  }
+}
+
+// dispatch backward + router dx + shared-expert dx, one rounding:
+//   dx[t] = sum_j dxp[slot[t,j]] + sum_j dl[t,j] * w_rT[sel[t,j]] + add[t]
+__global__ __launch_bounds__(PM_THREADS) void dispatch_bwd_pad_kernel(
+    const bf16_t* __restrict__ dxp, int64_t d, int k, const int32_t* __restrict__ slot, int64_t n,
+    const float* __restrict__ dl, const int32_t* __restrict__ sel, const bf16_t* __restrict__ w_rT,
+    const bf16_t* __restrict__ add, bf16_t* __restrict__ dx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  for (int64_t t = wave; t < n; t += nwaves) {
+    for (int64_t c = lane * 8; c < d; c += 64 * 8) {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int j = 0; j < k; ++j) {
+        float v[8];
+        V8<LSURGE_BF16>::ld(dxp + (int64_t)slot[t * k + j] * d + c, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += v[e];
+      }
+      if (dl) {
+        for (int j = 0; j < k; ++j) {
+          const float lj = dl[t * k + j];
+          float v[8];
+          V8<LSURGE_BF16>::ld(w_rT + (int64_t)sel[t * k + j] * d + c, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += lj * v[e];
+        }
+      }
+      if (add) {
+        float v[8];
+        V8<LSURGE_BF16>::ld(add + t * d + c, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += v[e];
+      }
+      V8<LSURGE_BF16>::st(dx + t * d + c, acc);
+    }
+  }
+}
+
+// Transpose a small [R, C] bf16 matrix into [C, R] (router weight for the dx term).
+__global__ void transpose_bf16_kernel(const bf16_t* __restrict__ a, int R, int C, bf16_t* __restrict__ at) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < (int64_t)R * C) {
+    const int r = (int)(i / C), c = (int)(i % C);
+    at[(int64_t)c * R + r] = a[i];
+  }
+}
+
+// dense dlogits [T, E] bf16 from the k selected gradients (zeros elsewhere)
+__global__ void scatter_dlogits_kernel(const float* __restrict__ dl, const int32_t* __restrict__ sel, int64_t T,
+                                       int E, int k, bf16_t* __restrict__ dlog) {
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= T) return;
+  for (int e = lane; e < E; e += 64) {
+    float v = 0.f;
+    for (int j = 0; j < k; ++j)
+      if (sel[t * k + j] == e) v = dl[t * k + j];
+    dlog[t * E + e] = f32_to_bf16(v);
+  }
+}
+
+inline unsigned grid_for_rows(int64_t rows) {
+  const int64_t g = (rows + PM_WAVES - 1) / PM_WAVES;
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(g, 256 * 16));
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+// ------------------------------------------------------------------------------ internal launchers
+namespace lsurge {
+
+int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src, const int32_t* num_blocks,
+                        int64_t max_rows, void* xp, hipStream_t s) {
+  LSURGE_LAUNCH(KID_DISPATCH, s,
+                hipLaunchKernelGGL(dispatch_pad_kernel, dim3(grid_for_rows(max_rows)), dim3(PM_THREADS), 0, s,
+                                   (const bf16_t*)x, d, k, row_src, num_blocks, max_rows, (bf16_t*)xp));
+  return LSURGE_OK;
+}
+
+int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, const float* w, int64_t n,
+                       const void* add, void* out, int out_dtype, hipStream_t s) {
+  if (out_dtype == LSURGE_BF16)
+    LSURGE_LAUNCH(KID_COMBINE_FWD, s,
+                  hipLaunchKernelGGL(combine_pad_kernel<LSURGE_BF16>, dim3(grid_for_rows(n)), dim3(PM_THREADS), 0, s,
+                                     (const bf16_t*)yp, d, k, slot, w, n, (const bf16_t*)add, out));
+  else
+    LSURGE_LAUNCH(KID_COMBINE_FWD, s,
+                  hipLaunchKernelGGL(combine_pad_kernel<LSURGE_F32>, dim3(grid_for_rows(n)), dim3(PM_THREADS), 0, s,
+                                     (const bf16_t*)yp, d, k, slot, w, n, (const bf16_t*)add, out));
+  return LSURGE_OK;
+}
+
+int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
+                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s) {
+  LSURGE_LAUNCH(KID_COMBINE_BWD, s,
+                hipLaunchKernelGGL((combine_bwd_kernel<LSURGE_BF16, LSURGE_BF16, true>), dim3(grid_for_rows(n)),
+                                   dim3(PM_THREADS), 0, s, yp, rows, slot, w, n, k, d, g, dyp, dw, dl));
+  return LSURGE_OK;
+}
+
+int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* slot, int64_t n, const float* dl,
+                            const int32_t* sel, const void* w_rT, const void* add, void* dx, hipStream_t s) {
+  LSURGE_LAUNCH(KID_DISPATCH_BWD, s,
+                hipLaunchKernelGGL(dispatch_bwd_pad_kernel, dim3(grid_for_rows(n)), dim3(PM_THREADS), 0, s,
+                                   (const bf16_t*)dxp, d, k, slot, n, dl, sel, (const bf16_t*)w_rT,
+                                   (const bf16_t*)add, (bf16_t*)dx));
+  return LSURGE_OK;
+}
+
+int launch_transpose_bf16(const void* a, int R, int C, void* at, hipStream_t s) {
+  const int64_t n = (int64_t)R * C;
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                                   (const bf16_t*)a, R, C, (bf16_t*)at));
+  return LSURGE_OK;
+}
+
+int launch_scatter_dlogits(const float* dl, const int32_t* sel, int64_t T, int E, int k, void* dlog, hipStream_t s) {
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(scatter_dlogits_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, s, dl, sel, T,
+                                   E, k, (bf16_t*)dlog));
+  return LSURGE_OK;
+}
+
+}  // namespace lsurge
+
+// ------------------------------------------------------------------------------ C ABI
+#define DT_SWITCH(dt, DT, ...)                                                \
+  switch (dt) {                                                               \
+    case LSURGE_F32: { constexpr int DT = LSURGE_F32; __VA_ARGS__; } break;   \
+    case LSURGE_BF16: { constexpr int DT = LSURGE_BF16; __VA_ARGS__; } break; \
+    case LSURGE_F16: { constexpr int DT = LSURGE_F16; __VA_ARGS__; } break;   \
+    default: return lsurge::set_error(LSURGE_ERR_DTYPE, "unsupported dtype %d", (int)(dt)); \
+  }
+
+extern "C" {
+
+int lsurge_gather_rows(const void* x, int64_t n, int64_t d, int dtype, const int32_t* idx, int64_t m,
+                       const float* scale, void* out, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(n >= 0 && d >= 0 && m >= 0, "gather_rows: negative shape");
+  if (m == 0 || d == 0) return LSURGE_OK;
+  LSURGE_REQUIRE(x && idx && out && n > 0, "gather_rows: null pointer or empty source");
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = (d % 8 == 0) && aligned16(x) && aligned16(out);
+  DT_SWITCH(dtype, DT, {
+    if (vec)
+      LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL((gather_rows_kernel<DT, true>), dim3(grid_for_rows(m)),
+                                                    dim3(PM_THREADS), 0, s, x, n, d, idx, m, scale, out));
+    else
+      LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL((gather_rows_kernel<DT, false>), dim3(grid_for_rows(m)),
+                                                    dim3(PM_THREADS), 0, s, x, n, d, idx, m, scale, out));
+  });
+  return LSURGE_OK;
+}
+
+int lsurge_gather_reduce(const void* y, int64_t m, int64_t d, int y_dtype, const int32_t* pos, int64_t n, int64_t k,
+                         const float* w, void* out, int out_dtype, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(m >= 0 && d >= 0 && n >= 0 && k >= 0, "gather_reduce: negative shape");
+  if (n == 0 || d == 0) return LSURGE_OK;
+  LSURGE_REQUIRE(out && (k == 0 || (y && pos)), "gather_reduce: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = (d % 8 == 0) && aligned16(y) && aligned16(out);
+  DT_SWITCH(y_dtype, DT, DT_SWITCH(out_dtype, OT, {
+    if (vec)
+      LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL((gather_reduce_kernel<DT, OT, true>), dim3(grid_for_rows(n)),
+                                                    dim3(PM_THREADS), 0, s, y, m, d, pos, n, (int)k, w, out));
+    else
+      LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL((gather_reduce_kernel<DT, OT, false>), dim3(grid_for_rows(n)),
+                                                    dim3(PM_THREADS), 0, s, y, m, d, pos, n, (int)k, w, out));
+  }));
+  return LSURGE_OK;
+}
+
+int lsurge_gather_dot(const void* y, int64_t m, int64_t d, int y_dtype, const int32_t* pos, int64_t n, int64_t k,
+                      const void* g, int g_dtype, float* out, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(m >= 0 && d >= 0 && n >= 0 && k >= 0, "gather_dot: negative shape");
+  if (n == 0 || k == 0) return LSURGE_OK;
+  LSURGE_REQUIRE(y && pos && g && out, "gather_dot: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = (d % 8 == 0) && aligned16(y) && aligned16(g);
+  DT_SWITCH(y_dtype, DT, DT_SWITCH(g_dtype, GT, {
+    if (vec)
+      LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL((gather_dot_kernel<DT, GT, true>), dim3(grid_for_rows(n)),
+                                                    dim3(PM_THREADS), 0, s, y, m, d, pos, n, (int)k, g, out));
+    else
+      LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL((gather_dot_kernel<DT, GT, false>), dim3(grid_for_rows(n)),
+                                                    dim3(PM_THREADS), 0, s, y, m, d, pos, n, (int)k, g, out));
+  }));
+  return LSURGE_OK;
+}
+
+int lsurge_combine_bwd(const void* y, int y_dtype, const int32_t* pos, const float* w, int64_t n, int64_t k, int64_t d,
+                       const void* g, int g_dtype, void* dy, float* dw, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(n >= 0 && k >= 0 && d >= 0 && k <= 16, "combine_bwd: bad shape (k <= 16)");
+  if (n == 0 || k == 0) return LSURGE_OK;
+  LSURGE_REQUIRE(y && pos && w && g && dy && dw, "combine_bwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = (d % 8 == 0) && aligned16(y) && aligned16(g) && aligned16(dy);
+  DT_SWITCH(y_dtype, DT, DT_SWITCH(g_dtype, GT, {
+    if (vec)
+      LSURGE_LAUNCH(KID_COMBINE_BWD, s,
+                    hipLaunchKernelGGL((combine_bwd_kernel<DT, GT, true>), dim3(grid_for_rows(n)), dim3(PM_THREADS), 0,
+                                       s, y, n * k, pos, w, n, (int)k, d, g, dy, dw, (float*)nullptr));
+    else
+      LSURGE_LAUNCH(KID_COMBINE_BWD, s,
+                    hipLaunchKernelGGL((combine_bwd_kernel<DT, GT, false>), dim3(grid_for_rows(n)), dim3(PM_THREADS),
+                                       0, s, y, n * k, pos, w, n, (int)k, d, g, dy, dw, (float*)nullptr));
+  }));
+  return LSURGE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,472 @@
+"""CPU oracle for the Lewi Surge MoE-layer hot path (numpy restatement).
+
+TEST INFRASTRUCTURE ONLY.  Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
+`bench.py` may import this module, and only as the checker or the timed CPU baseline.  The product
+path (the HIP library and the Python surface in `lewi-surge_amd/`) never calls it.
+
+What it restates (reference paths are relative to the reference repository root):
+
+* `modal/moe_permute.py` -- gather_rows (116-158), gather_reduce / gather_dot (161-234),
+  sort_indices (240-264), dispatch / combine / permute_rows and their VJPs (270-329),
+  ref_dispatch / ref_combine / moe_block (335-353).
+* `modal/padded_gmm.py` -- _perm_gather and its gather-only VJP (24-42), padded_ragged_dot with
+  the capacity layout (45-69); plus the dropless `jax.lax.ragged_dot` semantics it stands in for.
+* The MoE layer around them, whose code is MaxText 0.2.5 (`maxtext.layers.moe.RoutedMoE`, a
+  third-party package that is not in the reference tree): router logits, top-k with ties broken
+  toward the lower expert index, softmax over the selected logits (`norm_topk_prob: True`,
+  configs/stage1.yml:37), SwiGLU experts `silu(x Wg) * (x Wu) -> Wd` (weights `wi_0, wi_1, wo`,
+  modal/stage2.py:338), one ungated shared expert (configs/stage1.yml:35), and the backward of all
+  of it.  No reference test pins these at the MaxText boundary; they are pinned here by closed
+  forms, brute force and finite differences (tests/test_oracle.py).
+
+Numerics contract shared with the HIP path:
+
+* bf16 values are held in float32 arrays whose values are exactly bf16-representable
+  (round-to-nearest-even, `round_bf16`).
+* Router logits are float32: logits[t, e] = (((0 + x[t,0] w[0,e]) + x[t,1] w[1,e]) + ...) summed
+  sequentially over d in float32, then `+ bias[e]` in float32.  Products of two bf16 values are exact
+  in float32, so fused and unfused multiply-add give the same bits; this fixed order is what makes
+  the routing indices bit-exact between CPU and GPU.
+* Everything that is tolerance-checked (weights, layer outputs, gradients) is computed here in
+  float64 with no intermediate rounding.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+BLOCK = 128  # rows per padded expert block
+
+# --------------------------------------------------------------------------------------------- bf16
+
+
+def bf16_bits(a):
+    """float32 -> bf16 bit pattern (uint16), round to nearest even; NaN -> canonical quiet NaN."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    u = a.view(np.uint32)
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    r[np.isnan(a)] = np.uint16(0x7FC0)
+    return r
+
+
+def bf16_to_f32(b):
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def round_bf16(a):
+    return bf16_to_f32(bf16_bits(a))
+
+
+# --------------------------------------------------------------------------------------------- inputs
+
+CONFIGS = {
+    # name: T, d, E, k, f, f_s, seed, zipf, mode
+    "C1": dict(T=4096, d=1024, E=64, k=6, f=512, fs=512, seed=0, zipf=False, bwd=False),
+    "C2": dict(T=16384, d=1024, E=64, k=6, f=512, fs=512, seed=0, zipf=False, bwd=True),
+    "C3": dict(T=16384, d=1024, E=128, k=6, f=512, fs=512, seed=1, zipf=False, bwd=True),
+    "C4": dict(T=32768, d=1024, E=128, k=6, f=512, fs=512, seed=1, zipf=True, bwd=True),
+    "C5": dict(T=65536, d=2048, E=256, k=8, f=512, fs=2048, seed=0, zipf=False, bwd=True),
+}
+
+
+def zipf_bias(E):
+    """Load-imbalance router bias b_e = 1.5 * log(1 / rank_e) with rank_e = e + 1 (expert 0 hottest)."""
+    return (1.5 * np.log(1.0 / np.arange(1, E + 1, dtype=np.float64))).astype(np.float32)
+
+
+def make_inputs(T, d, E, k, f, fs, seed=0, zipf=False, **_):
+    """Seeded synthetic layer inputs (numpy PCG64 float32 normals rounded to bf16).
+
+    Draw order: x, w_r, w_gate, w_up, w_down, ws_gate, ws_up, ws_down, dy.
+    """
+    rng = np.random.default_rng(seed)
+
+    def nrm(shape, std):
+        return round_bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+
+    p = dict(
+        x=nrm((T, d), 1.0),
+        w_r=nrm((d, E), 0.02),
+        w_gate=nrm((E, d, f), 0.02),
+        w_up=nrm((E, d, f), 0.02),
+        w_down=nrm((E, f, d), 0.02),
+        ws_gate=nrm((d, fs), 0.02) if fs else None,
+        ws_up=nrm((d, fs), 0.02) if fs else None,
+        ws_down=nrm((fs, d), 0.02) if fs else None,
+    )
+    p["dy"] = nrm((T, d), 1.0)
+    p["bias"] = zipf_bias(E) if zipf else None
+    p["k"] = k
+    return p
+
+
+# --------------------------------------------------------------------------------------------- router (A1)
+
+
+def router_logits(x, w_r, bias=None):
+    """float32 logits, summed sequentially over d (see the numerics contract in the module docstring)."""
+    x = np.asarray(x, np.float32)
+    w_r = np.asarray(w_r, np.float32)
+    T, d = x.shape
+    acc = np.zeros((T, w_r.shape[1]), np.float32)
+    for i in range(d):
+        acc += x[:, i:i + 1] * w_r[i][None, :]  # float32 product (exact for bf16 inputs) + float32 add
+    if bias is not None:
+        acc += np.asarray(bias, np.float32)[None, :]
+    return acc
+
+
+def topk_lower_index(logits, k):
+    """Indices of the k largest logits per row, descending; equal logits -> lower expert index first.
+
+    Same as `argsort(-logits)[:, :k]` with a stable sort (modal/test_moe_permute.py:23-26 routes this way).
+    """
+    return np.argsort(-np.asarray(logits), axis=1, kind="stable")[:, :k].astype(np.int32)
+
+
+def topk_softmax(logits, sel):
+    """Routing weights: softmax over the selected logits (norm_topk_prob=True), float64."""
+    l = np.take_along_axis(np.asarray(logits, np.float64), sel.astype(np.int64), axis=1)
+    z = np.exp(l - l.max(axis=1, keepdims=True))
+    return z / z.sum(axis=1, keepdims=True)
+
+
+def router(x, w_r, k, bias=None):
+    logits = router_logits(x, w_r, bias)
+    sel = topk_lower_index(logits, k)
+    return logits, sel, topk_softmax(logits, sel)
+
+
+# --------------------------------------------------------------------------------------------- layout (A2, A3)
+
+
+def sort_indices(flat_experts, num_experts=None):
+    """(order, pos): order = stable argsort of the flat slot experts, pos = its inverse.
+
+    modal/moe_permute.py:240-264 (both the argsort and the counting method give this).
+    """
+    flat = np.asarray(flat_experts, np.int64).reshape(-1)
+    order = np.argsort(flat, kind="stable").astype(np.int32)
+    pos = np.empty_like(order)
+    pos[order] = np.arange(flat.shape[0], dtype=np.int32)
+    return order, pos
+
+
+def build_layout(sel, E, block=BLOCK):
+    """Routing layout for the padded per-expert block format.
+
+    Returns dict with group_sizes [E], offsets [E] (exclusive scan), block_off [E] (exclusive scan of
+    ceil(gs/block)), num_blocks, order [M], pos [M], slot [M] (padded row of flat slot i) and
+    block_expert [num_blocks].
+    """
+    flat = np.asarray(sel, np.int64).reshape(-1)
+    order, pos = sort_indices(flat, E)
+    gs = np.bincount(flat, minlength=E).astype(np.int32)
+    offsets = (np.cumsum(gs) - gs).astype(np.int32)
+    nblk = (gs + block - 1) // block
+    block_off = (np.cumsum(nblk) - nblk).astype(np.int32)
+    slot = (block * block_off[flat] + (pos - offsets[flat])).astype(np.int32)
+    block_expert = np.repeat(np.arange(E, dtype=np.int32), nblk)
+    return dict(group_sizes=gs, offsets=offsets, block_off=block_off, num_blocks=int(nblk.sum()),
+                order=order, pos=pos, slot=slot, block_expert=block_expert)
+
+
+def max_blocks(M, E, block=BLOCK):
+    """Static upper bound on the number of padded blocks: sum_e ceil(gs_e/block) <= ceil(M/block) + E."""
+    return (M + block - 1) // block + E
+
+
+# --------------------------------------------------------------------------------------------- row movement (A7-A12)
+
+
+def gather_rows(x, idx, scale=None, dtype="bf16"):
+    """out[i] = x[idx[i]] (* scale[i], then rounded to x's dtype).  modal/moe_permute.py:116-121."""
+    out = np.asarray(x)[np.asarray(idx, np.int64)]
+    if scale is None:
+        return out
+    v = out.astype(np.float32) * np.asarray(scale, np.float32)[:, None]
+    return _cast(v, dtype)
+
+
+def gather_reduce(y, pos, w=None):
+    """out[t] = sum_j w[t,j] * y[pos[t,j]] (float64 here).  modal/moe_permute.py:214-225."""
+    rows = np.asarray(y, np.float64)[np.asarray(pos, np.int64)]  # [N, k, D]
+    if w is not None:
+        rows = rows * np.asarray(w, np.float64)[:, :, None]
+    return rows.sum(axis=1)
+
+
+def gather_dot(y, pos, g):
+    """out[t,j] = <g[t], y[pos[t,j]]> (float64 here).  modal/moe_permute.py:228-234."""
+    rows = np.asarray(y, np.float64)[np.asarray(pos, np.int64)]
+    return np.einsum("nkd,nd->nk", rows, np.asarray(g, np.float64))
+
+
+def dispatch(x, order, pos):
+    """x[order // k]: tokens to rows grouped by expert.  modal/moe_permute.py:270-275."""
+    k = order.shape[0] // x.shape[0]
+    return np.asarray(x)[np.asarray(order, np.int64) // k]
+
+
+def dispatch_bwd(g, pos, n):
+    """dx[t] = sum_j g[pos[t,j]].  modal/moe_permute.py:282-286."""
+    k = pos.shape[0] // n
+    return gather_reduce(g, np.asarray(pos).reshape(n, k))
+
+
+def combine(y, pos, w):
+    """sum_j w[t,j] y[pos[t,j]] in float.  modal/moe_permute.py:292-296."""
+    n, k = w.shape
+    return gather_reduce(y, np.asarray(pos).reshape(n, k), w)
+
+
+def combine_bwd(y, order, pos, w, g, dtype="bf16"):
+    """(dy, dw): dy[p] = w_sorted[p] * g[order[p]//k] rounded to y's dtype; dw = gather_dot(y, pos, g).
+
+    modal/moe_permute.py:303-309.
+    """
+    n, k = w.shape
+    w_sorted = np.asarray(w, np.float32).reshape(-1)[np.asarray(order, np.int64)]
+    dy = gather_rows(_cast(np.asarray(g, np.float32), dtype), np.asarray(order) // k, w_sorted, dtype)
+    dw = gather_dot(y, np.asarray(pos).reshape(n, k), g)
+    return dy, dw
+
+
+def permute_rows(x, idx):
+    """x[idx]; its VJP is gather_rows(g, argsort(idx)).  modal/moe_permute.py:315-326."""
+    return np.asarray(x)[np.asarray(idx, np.int64)]
+
+
+def permute_rows_bwd(g, idx):
+    inv = np.argsort(np.asarray(idx), kind="stable")
+    return np.asarray(g)[inv]
+
+
+def ref_dispatch(x, flat_experts):
+    """modal/moe_permute.py:335-338."""
+    k = flat_experts.shape[0] // x.shape[0]
+    order = np.argsort(flat_experts, kind="stable")
+    return np.asarray(x)[order // k]
+
+
+def ref_combine(y, flat_experts, w):
+    """modal/moe_permute.py:341-345 (float64 here)."""
+    n, k = w.shape
+    pos = np.argsort(np.argsort(flat_experts, kind="stable"), kind="stable")
+    rows = np.asarray(y, np.float64)[pos].reshape(n, k, -1)
+    return np.einsum("nkd,nk->nd", rows, np.asarray(w, np.float64))
+
+
+def _cast(v, dtype):
+    if dtype == "bf16":
+        return round_bf16(v)
+    if dtype == "f16":
+        return np.asarray(v, np.float32).astype(np.float16).astype(np.float32)
+    return np.asarray(v, np.float32)
+
+
+# --------------------------------------------------------------------------------------------- grouped GEMM (A4, A5)
+
+
+def ragged_dot(lhs, rhs, group_sizes):
+    """Dropless `jax.lax.ragged_dot`: out[r] = lhs[r] @ rhs[e(r)] for r < sum(gs), else 0 (float64)."""
+    lhs = np.asarray(lhs, np.float64)
+    rhs = np.asarray(rhs, np.float64)
+    gs = np.asarray(group_sizes, np.int64)
+    out = np.zeros((lhs.shape[0], rhs.shape[2]), np.float64)
+    start = 0
+    for e, g in enumerate(gs):
+        out[start:start + g] = lhs[start:start + g] @ rhs[e]
+        start += g
+    return out
+
+
+def padded_capacity(m, e, factor):
+    """C = max(8, roundup8(ceil(m / e * factor))).  modal/padded_gmm.py:51-52."""
+    c = int(math.ceil(m / e * factor))
+    return max(8, (c + 7) // 8 * 8)
+
+
+def padded_maps(group_sizes, m, factor):
+    """(slot, src, C) of padded_gmm's capacity layout.  modal/padded_gmm.py:53-64."""
+    gs = np.asarray(group_sizes, np.int64)
+    e = gs.shape[0]
+    c = padded_capacity(m, e, factor)
+    starts = np.cumsum(gs) - gs
+    rows = np.arange(m)
+    expert = np.minimum(np.searchsorted(np.cumsum(gs), rows, side="right"), e - 1)
+    p = rows - starts[expert]
+    valid = (rows < gs.sum()) & (p < c)
+    slot = np.where(valid, expert * c + p, e * c)
+    se = np.arange(e * c) // c
+    sc = np.arange(e * c) % c
+    src = np.where(sc < np.minimum(gs[se], c), starts[se] + sc, m)
+    return slot.astype(np.int32), src.astype(np.int32), c
+
+
+def padded_ragged_dot_capacity(lhs, rhs, group_sizes, factor):
+    """padded_gmm's capacity semantics (rows past C in an expert give 0).  modal/padded_gmm.py:45-69."""
+    lhs = np.asarray(lhs, np.float64)
+    m, k = lhs.shape
+    e, _, n = rhs.shape
+    slot, src, c = padded_maps(group_sizes, m, factor)
+    lhs_ext = np.concatenate([lhs, np.zeros((1, k))])
+    buf = lhs_ext[src].reshape(e, c, k)
+    out = np.einsum("eck,ekn->ecn", buf, np.asarray(rhs, np.float64)).reshape(e * c, n)
+    out_ext = np.concatenate([out, np.zeros((1, n))])
+    return out_ext[slot]
+
+
+def ragged_dot_bwd(lhs, rhs, group_sizes, g):
+    """(dlhs, drhs) of the dropless ragged_dot for upstream g [M, N] (rows past sum(gs) get 0)."""
+    lhs = np.asarray(lhs, np.float64)
+    rhs = np.asarray(rhs, np.float64)
+    g = np.asarray(g, np.float64)
+    gs = np.asarray(group_sizes, np.int64)
+    dl = np.zeros_like(lhs)
+    dr = np.zeros_like(rhs)
+    start = 0
+    for e, n in enumerate(gs):
+        dl[start:start + n] = g[start:start + n] @ rhs[e].T
+        dr[e] = lhs[start:start + n].T @ g[start:start + n]
+        start += n
+    return dl, dr
+
+
+# --------------------------------------------------------------------------------------------- SwiGLU layer (A6, A13-A16)
+
+
+def silu(z):
+    return z / (1.0 + np.exp(-z))
+
+
+def dsilu(z):
+    s = 1.0 / (1.0 + np.exp(-z))
+    return s * (1.0 + z * (1.0 - s))
+
+
+def swiglu(x, wg, wu, wd):
+    g = x @ wg
+    u = x @ wu
+    h = silu(g) * u
+    return h @ wd, (g, u, h)
+
+
+def swiglu_bwd(x, wg, wu, wd, cache, dy):
+    g, u, h = cache
+    dh = dy @ wd.T
+    dg = dh * u * dsilu(g)
+    du = dh * silu(g)
+    dx = dg @ wg.T + du @ wu.T
+    return dx, x.T @ dg, x.T @ du, h.T @ dy
+
+
+def moe_layer_fwd(p, dtype=np.float64, route=None):
+    """Full MoE layer forward.  Returns (out [T,d], cache).  Routing is integer (bit-exact contract).
+
+    route: optional precomputed (logits, sel) of the same contract (e.g. from the C restatement, for speed).
+    """
+    x = np.asarray(p["x"], dtype)
+    k = p["k"]
+    # selection: the bit-exact f32 contract logits; weights: softmax of the same logits computed in `dtype`
+    # (the differentiable quantity; it differs from the f32 logits only by f32 rounding)
+    if route is None:
+        logits, sel, _ = router(p["x"], p["w_r"], k, p.get("bias"))
+    else:
+        logits, sel = route
+    lw = x @ np.asarray(p["w_r"], dtype)
+    if p.get("bias") is not None:
+        lw = lw + np.asarray(p["bias"], dtype)
+    w = topk_softmax(lw, sel)
+    E = p["w_gate"].shape[0]
+    lay = build_layout(sel, E)
+    T, d = x.shape
+    flat = sel.reshape(-1)
+    order = lay["order"]
+    xs = x[order // k]  # dispatched rows, grouped by expert
+    gs = lay["group_sizes"]
+    wg, wu, wd = (np.asarray(p[n], dtype) for n in ("w_gate", "w_up", "w_down"))
+    f = wg.shape[2]
+    ys = np.zeros((xs.shape[0], d), dtype)
+    gg = np.zeros((xs.shape[0], f), dtype)
+    uu = np.zeros_like(gg)
+    hh = np.zeros_like(gg)
+    start = 0
+    for e in range(E):
+        n = int(gs[e])
+        if n:
+            ys[start:start + n], (gg[start:start + n], uu[start:start + n], hh[start:start + n]) = swiglu(
+                xs[start:start + n], wg[e], wu[e], wd[e])
+        start += n
+    w = w.astype(dtype)
+    routed = (ys[lay["pos"]].reshape(T, k, d) * w[:, :, None]).sum(axis=1)
+    out = routed
+    shared = None
+    if p.get("ws_gate") is not None:
+        ysh, shared = swiglu(x, *(np.asarray(p[n], dtype) for n in ("ws_gate", "ws_up", "ws_down")))
+        out = out + ysh
+    cache = dict(logits=logits, sel=sel, w=w, lay=lay, xs=xs, ys=ys, g=gg, u=uu, h=hh, shared=shared, flat=flat)
+    return out, cache
+
+
+def moe_layer_bwd(p, cache, dy, dtype=np.float64):
+    """Backward of `moe_layer_fwd` for upstream dy [T,d].
+
+    Returns dict dx, dw_r, dw_gate, dw_up, dw_down, dws_gate, dws_up, dws_down, dw (routing weights
+    gradient [T,k]) and dlogits [T,E].
+    """
+    x = np.asarray(p["x"], dtype)
+    dy = np.asarray(dy, dtype)
+    T, d = x.shape
+    k = p["k"]
+    lay, w, sel = cache["lay"], cache["w"], cache["sel"]
+    order, pos, gs = lay["order"], lay["pos"], lay["group_sizes"]
+    E = p["w_gate"].shape[0]
+    wg, wu, wd = (np.asarray(p[n], dtype) for n in ("w_gate", "w_up", "w_down"))
+    # combine backward: dy_sorted[p] = w_flat[order[p]] * dy[order[p] // k]; dw[t,j] = <dy[t], y[pos[t,j]]>
+    w_flat = w.reshape(-1)
+    dys = dy[order // k] * w_flat[order][:, None]
+    dw = np.einsum("tkd,td->tk", cache["ys"][pos].reshape(T, k, d), dy)
+    dxs = np.zeros_like(cache["xs"])
+    dwg = np.zeros_like(wg)
+    dwu = np.zeros_like(wu)
+    dwd = np.zeros_like(wd)
+    start = 0
+    for e in range(E):
+        n = int(gs[e])
+        if n:
+            sl = slice(start, start + n)
+            dxs[sl], dwg[e], dwu[e], dwd[e] = swiglu_bwd(
+                cache["xs"][sl], wg[e], wu[e], wd[e], (cache["g"][sl], cache["u"][sl], cache["h"][sl]), dys[sl])
+        start += n
+    # dispatch backward (gather-only): dx[t] = sum_j dxs[pos[t,j]]
+    dx = dxs[pos].reshape(T, k, d).sum(axis=1)
+    # router backward: softmax over the selected logits
+    dl_sel = w * (dw - (w * dw).sum(axis=1, keepdims=True))
+    dlogits = np.zeros((T, E), dtype)
+    np.put_along_axis(dlogits, sel.astype(np.int64), dl_sel, axis=1)
+    w_r = np.asarray(p["w_r"], dtype)
+    dx = dx + dlogits @ w_r.T
+    out = dict(dx=dx, dw_r=x.T @ dlogits, dw_gate=dwg, dw_up=dwu, dw_down=dwd, dw=dw, dlogits=dlogits)
+    if cache["shared"] is not None:
+        ws = [np.asarray(p[n], dtype) for n in ("ws_gate", "ws_up", "ws_down")]
+        dxs_, out["dws_gate"], out["dws_up"], out["dws_down"] = swiglu_bwd(x, *ws, cache["shared"], dy)
+        out["dx"] = out["dx"] + dxs_
+    return out
+
+
+# --------------------------------------------------------------------------------------------- metrics
+
+
+def rel_l2(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / (np.linalg.norm(want) + 1e-30))
+
+
+def rel_max(got, want):
+    """max|got - want| / (max|want| + 1e-6): modal/test_moe_permute.py:29-34."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.abs(got - want).max() / (np.abs(want).max() + 1e-6)) if want.size else 0.0

@@ -1,0 +1,89 @@
+"""Grouped GEMM (padded_gmm.padded_ragged_dot surface) on the GPU against the oracle's dropless ragged_dot.
+
+The reference's known-answer case is modal/te_run.py:72-79: gs=[5,0,9,3,7,1,6,4], M = sum(gs)+3 (tail rows past
+the groups), K=64, N=48, bf16, forward + dlhs + drhs.  Tolerance: 2e-2 relative L2 against the fp64 oracle
+(north-star tolerance); in practice bf16 inputs with f32 accumulation land near 1e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+import padded_gmm as pg
+from oracle import moe_oracle as mo
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _bf(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev).to(torch.bfloat16)
+
+
+def run_case(gs, M, K, N, dev, seed=0, out_dtype=None):
+    rng = np.random.default_rng(seed)
+    E = len(gs)
+    a = mo.round_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    b = mo.round_bf16(rng.standard_normal((E, K, N)).astype(np.float32))
+    g = mo.round_bf16(rng.standard_normal((M, N)).astype(np.float32))
+    at = _bf(a, dev).requires_grad_(True)
+    bt = _bf(b, dev).requires_grad_(True)
+    gst = torch.tensor(gs, dtype=torch.int32, device=dev)
+    out = pg.padded_ragged_dot(at, bt, gst, preferred_element_type=out_dtype)
+    out.backward(_bf(g, dev).to(out.dtype))
+    want = mo.ragged_dot(a, b, gs)
+    S = int(np.sum(gs))
+    got = out.detach().float().cpu().numpy()
+    assert np.all(got[S:] == 0)
+    assert mo.rel_l2(got, want) < TOL
+    dl, dr = mo.ragged_dot_bwd(a, b, gs, g)
+    gl = at.grad.float().cpu().numpy()
+    assert np.all(gl[S:] == 0)
+    assert mo.rel_l2(gl, dl) < TOL
+    gr = bt.grad.float().cpu().numpy()
+    for e in range(E):
+        if gs[e] == 0:
+            assert np.all(gr[e] == 0)
+    assert mo.rel_l2(gr, dr) < TOL
+    return mo.rel_l2(got, want)
+
+
+def test_te_known_answer_case(dev):
+    gs = [5, 0, 9, 3, 7, 1, 6, 4]
+    err = run_case(gs, sum(gs) + 3, 64, 48, dev)
+    assert err < 5e-3
+
+
+def test_f32_output(dev):
+    gs = [5, 0, 9, 3, 7, 1, 6, 4]
+    run_case(gs, sum(gs) + 3, 64, 48, dev, out_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("E,M,K,N", [(8, 1000, 256, 192), (4, 777, 128, 1024), (64, 6000, 1024, 512),
+                                     (3, 129, 520, 136)])
+def test_random_groups(E, M, K, N, dev):
+    rng = np.random.default_rng(M)
+    cuts = np.sort(rng.integers(0, M - 5, E - 1))
+    gs = np.diff(np.concatenate([[0], cuts, [M - 5]])).astype(int).tolist()  # 5 tail rows, some empty groups
+    run_case(gs, M, K, N, dev, seed=E)
+
+
+def test_all_rows_one_group_and_capacity_semantics(dev):
+    """One hot group past padded_gmm's capacity: the reference would drop rows, the kernel is dropless."""
+    gs = [0, 700, 0, 20]
+    M = 720
+    c = pg.capacity(M, 4, 1.5)
+    assert c < 700
+    run_case(gs, M, 128, 64, dev, seed=3)
+
+
+def test_perm_gather_sentinel(dev):
+    """_perm_gather: y[i] = x_ext[idx[i]] with a zero row at index len(x); backward is the inverse gather."""
+    x = torch.randn(6, 16, device=dev).to(torch.bfloat16).requires_grad_(True)
+    idx = torch.tensor([3, 6, 0, 6, 5, 1, 2, 4], dtype=torch.int32, device=dev)
+    inv = torch.tensor([2, 5, 6, 0, 7, 4], dtype=torch.int32, device=dev)
+    y = pg._perm_gather(x, idx, inv)
+    xe = torch.cat([x.detach(), torch.zeros(1, 16, device=dev, dtype=x.dtype)])
+    assert torch.equal(y.detach(), xe[idx.long()])
+    g = torch.randn(8, 16, device=dev).to(torch.bfloat16)
+    y.backward(g)
+    assert torch.equal(x.grad, g[inv.long()])

@@ -1,0 +1,132 @@
+"""Whole MoE layer (lsurge_moe_fwd / lsurge_moe_bwd) on the GPU against the oracle.
+
+Bar (north star): routing indices / expert offsets / permutation bit-exact; outputs and gradients within 2e-2
+relative L2 of the oracle (float64 on small shapes, float32 on the BASELINE shapes for speed -- either is far
+more precise than the bf16 path it checks).  At C5 the oracle runs on a token subset: out[t], dx[t] and
+d(weights)[t] depend on token t and the weights only.
+"""
+import numpy as np
+import pytest
+import torch
+
+from moe_layer import MoELayer, MoEShape, moe_layer
+from oracle import c_oracle as co
+from oracle import moe_oracle as mo
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def to_dev(p, dev):
+    out = {}
+    for n in ("x", "w_r", "w_gate", "w_up", "w_down", "ws_gate", "ws_up", "ws_down"):
+        if p.get(n) is not None:
+            out[n] = torch.from_numpy(np.ascontiguousarray(p[n])).to(dev).to(torch.bfloat16)
+    out["bias"] = None if p.get("bias") is None else torch.from_numpy(p["bias"]).to(dev)
+    return out
+
+
+def run_gpu(p, shape, dev, bwd=True):
+    layer = MoELayer(shape, dev)
+    tp = to_dev(p, dev)
+    out = layer.forward(tp).float().cpu().numpy()
+    views = {k: v.cpu().numpy() for k, v in layer.views().items()
+             if k in ("sel", "group_sizes", "offsets", "block_off", "order", "pos", "slot", "num_blocks")}
+    grads = None
+    if bwd:
+        dy = torch.from_numpy(np.ascontiguousarray(p["dy"])).to(dev).to(torch.bfloat16)
+        g = layer.backward(tp, dy)
+        grads = {k: v.float().cpu().numpy() for k, v in g.items()}
+    return out, views, grads
+
+
+def check_layer(p, shape, dev, bwd=True, odt=np.float64, fast_route=False):
+    route = None
+    if fast_route:
+        logits, sel, _ = co.router(p["x"], p["w_r"], p["k"], p.get("bias"))
+        route = (logits, sel)
+    out, views, grads = run_gpu(p, shape, dev, bwd)
+    want, cache = mo.moe_layer_fwd(p, odt, route=route)
+    lay = cache["lay"]
+    assert np.array_equal(views["sel"], cache["sel"])
+    for n in ("group_sizes", "offsets", "block_off", "order", "pos", "slot"):
+        assert np.array_equal(views[n], lay[n]), n
+    errs = {"out": mo.rel_l2(out, want)}
+    if bwd:
+        g = mo.moe_layer_bwd(p, cache, p["dy"], odt)
+        pairs = [("dx", "dx"), ("dw_r", "dw_r"), ("dw_gate", "dw_gate"), ("dw_up", "dw_up"), ("dw_down", "dw_down"),
+                 ("dweights", "dw")]
+        if shape.fs:
+            pairs += [("dws_gate", "dws_gate"), ("dws_up", "dws_up"), ("dws_down", "dws_down")]
+        for gn, on in pairs:
+            errs[gn] = mo.rel_l2(grads[gn], g[on])
+    print({k: f"{v:.2e}" for k, v in errs.items()})
+    bad = {k: v for k, v in errs.items() if not v < TOL}
+    assert not bad, bad
+    return errs
+
+
+@pytest.mark.parametrize("T,d,E,k,f,fs", [(256, 128, 8, 2, 64, 64), (300, 256, 16, 6, 128, 0),
+                                          (1000, 512, 64, 6, 256, 128), (77, 64, 8, 8, 64, 64)])
+def test_small_layers_fp64(T, d, E, k, f, fs, dev):
+    p = mo.make_inputs(T=T, d=d, E=E, k=k, f=f, fs=fs, seed=T)
+    check_layer(p, MoEShape(T, d, E, k, f, fs), dev)
+
+
+def test_small_layer_zipf_bias(dev):
+    p = mo.make_inputs(T=2048, d=256, E=32, k=4, f=128, fs=128, seed=2, zipf=True)
+    check_layer(p, MoEShape(2048, 256, 32, 4, 128, 128), dev)
+
+
+@pytest.mark.parametrize("name", ["C1", "C2", "C4"])
+def test_baseline_configs(name, dev):
+    c = mo.CONFIGS[name]
+    p = mo.make_inputs(**c)
+    shape = MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"])
+    check_layer(p, shape, dev, bwd=c["bwd"], odt=np.float32, fast_route=True)
+
+
+def test_c5_token_subset(dev):
+    c = mo.CONFIGS["C5"]
+    p = mo.make_inputs(**c)
+    shape = MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"])
+    out, views, grads = run_gpu(p, shape, dev, bwd=True)
+    toks = np.random.default_rng(0).choice(c["T"], 192, replace=False)
+    sub = dict(p)
+    sub["x"], sub["dy"] = p["x"][toks], p["dy"][toks]
+    logits, sel, _ = co.router(sub["x"], p["w_r"], c["k"])
+    assert np.array_equal(views["sel"][toks], sel)
+    want, cache = mo.moe_layer_fwd(sub, np.float32, route=(logits, sel))
+    g = mo.moe_layer_bwd(sub, cache, sub["dy"], np.float32)
+    errs = {"out": mo.rel_l2(out[toks], want), "dx": mo.rel_l2(grads["dx"][toks], g["dx"]),
+            "dweights": mo.rel_l2(grads["dweights"][toks], g["dw"])}
+    print(errs)
+    assert all(v < TOL for v in errs.values()), errs
+    assert all(np.isfinite(v).all() for v in grads.values())
+
+
+def test_deterministic_bitwise(dev):
+    """No atomics: two runs give identical bits for the output and every gradient."""
+    c = mo.CONFIGS["C2"]
+    p = mo.make_inputs(**c)
+    shape = MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"])
+    a = run_gpu(p, shape, dev)
+    b = run_gpu(p, shape, dev)
+    assert np.array_equal(a[0], b[0])
+    for k in a[2]:
+        assert np.array_equal(a[2][k], b[2][k]), k
+
+
+def test_autograd_function(dev):
+    T, d, E, k, f, fs = 256, 128, 8, 2, 64, 64
+    p = mo.make_inputs(T=T, d=d, E=E, k=k, f=f, fs=fs, seed=1)
+    tp = {n: v.requires_grad_(True) if v is not None else None for n, v in to_dev(p, dev).items()}
+    out = moe_layer(tp["x"], tp["w_r"], tp["w_gate"], tp["w_up"], tp["w_down"], tp["ws_gate"], tp["ws_up"],
+                    tp["ws_down"], k=k)
+    dy = torch.from_numpy(p["dy"]).to(dev).to(torch.bfloat16)
+    out.backward(dy)
+    want, cache = mo.moe_layer_fwd(p)
+    g = mo.moe_layer_bwd(p, cache, p["dy"])
+    assert mo.rel_l2(out.detach().float().cpu().numpy(), want) < TOL
+    assert mo.rel_l2(tp["w_gate"].grad.float().cpu().numpy(), g["dw_gate"]) < TOL
+    assert mo.rel_l2(tp["x"].grad.float().cpu().numpy(), g["dx"]) < TOL
