@@ -402,15 +402,19 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, int S, int 
   }
 }
 
-// block table of an unpadded ragged layout (rows of group e start at sum_{e'<e} gs[e'])
-__global__ void ragged_blocks_kernel(const int32_t* __restrict__ gs, int E, int max_blocks, int32_t* __restrict__ blk_row0,
-                                     int32_t* __restrict__ blk_rows, int32_t* __restrict__ blk_expert,
-                                     int32_t* __restrict__ num_blocks, int32_t* __restrict__ total_rows,
-                                     int32_t* __restrict__ e_row0) {
+// block table of an unpadded ragged layout (rows of group e start at sum_{e'<e} gs[e']).  Group sizes are
+// clamped so that no group reaches past row m: negative sizes count as 0 and a sum above m is cut at m, so a
+// bad group_sizes array can never send the GEMMs outside lhs/out.
+__global__ void ragged_blocks_kernel(const int32_t* __restrict__ gs, int E, int64_t m, int max_blocks,
+                                     int32_t* __restrict__ blk_row0, int32_t* __restrict__ blk_rows,
+                                     int32_t* __restrict__ blk_expert, int32_t* __restrict__ num_blocks,
+                                     int32_t* __restrict__ total_rows, int32_t* __restrict__ e_row0,
+                                     int32_t* __restrict__ e_rows) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
   int b = 0, run = 0;
   for (int e = 0; e < E; ++e) {
-    const int g = gs[e];
+    const int g = (int)min((int64_t)max(gs[e], 0), m - run);
+    e_rows[e] = g;
     e_row0[e] = run;
     for (int j = 0; j * BM < g; ++j, ++b) {
       if (b < max_blocks) {
@@ -570,11 +574,11 @@ extern "C" {
 
 size_t lsurge_ragged_dot_workspace_bytes(int64_t m, int64_t e) {
   const int64_t mb = lsurge_max_blocks(m, e);
-  return sizeof(int32_t) * (size_t)(3 * mb + 4 + e);
+  return sizeof(int32_t) * (size_t)(3 * mb + 4 + 2 * e);
 }
 
 static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_t ws_bytes, hipStream_t s,
-                        lsurge::GemmBlocks* g, int32_t** total_rows, int32_t** e_row0) {
+                        lsurge::GemmBlocks* g, int32_t** total_rows, int32_t** e_row0, int32_t** e_rows) {
   const size_t need = lsurge_ragged_dot_workspace_bytes(m, e);
   LSURGE_REQUIRE(ws && ws_bytes >= need, "ragged_dot: workspace %zu < %zu bytes", ws_bytes, need);
   const int64_t mb = lsurge_max_blocks(m, e);
@@ -585,9 +589,10 @@ static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_
   int32_t* nb = p + 3 * mb;
   *total_rows = nb + 1;
   *e_row0 = nb + 4;
+  *e_rows = nb + 4 + e;
   LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(ragged_blocks_kernel, dim3(1), dim3(64), 0, s, gs, (int)e, (int)mb, blk_row0, blk_rows,
-                                   blk_expert, nb, *total_rows, *e_row0));
+                hipLaunchKernelGGL(ragged_blocks_kernel, dim3(1), dim3(64), 0, s, gs, (int)e, m, (int)mb, blk_row0,
+                                   blk_rows, blk_expert, nb, *total_rows, *e_row0, *e_rows));
   g->blk_expert = blk_expert;
   g->blk_rows = blk_rows;
   g->blk_row0 = blk_row0;
@@ -606,8 +611,8 @@ int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_siz
   LSURGE_REQUIRE(lhs && rhs && group_sizes && out, "ragged_dot: null pointer");
   hipStream_t s = (hipStream_t)stream;
   lsurge::GemmBlocks g;
-  int32_t *total, *e_row0;
-  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0)) return rc;
+  int32_t *total, *e_row0, *e_rows;
+  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0, &e_rows)) return rc;
   const bool f32 = out_dtype == LSURGE_F32;
   if (int rc = lsurge::gemm_rows_kn(KID_MISC, g, lhs, kdim, rhs, n, kdim * n, kdim, n, out, n, s, f32)) return rc;
   LSURGE_LAUNCH(KID_MISC, s,
@@ -622,8 +627,8 @@ int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group
   LSURGE_REQUIRE(lhs && rhs && group_sizes && g && dlhs && drhs, "ragged_dot_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   lsurge::GemmBlocks gb;
-  int32_t *total, *e_row0;
-  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &gb, &total, &e_row0)) return rc;
+  int32_t *total, *e_row0, *e_rows;
+  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &gb, &total, &e_row0, &e_rows)) return rc;
   // dlhs[r] = g[r] @ rhs[e]^T : rhs[e] is [K, N] = k-major storage of the [N -> K] operand
   if (m > 0) {
     if (int rc = lsurge::gemm_rows_nk(KID_MISC, gb, g, n, rhs, nullptr, 0, n, kdim * n, n, kdim, dlhs, kdim, false,
@@ -633,7 +638,7 @@ int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group
                   hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, dlhs, m, kdim, 2, total));
   }
   // drhs[e] = lhs_e^T @ g_e
-  return lsurge::gemm_wgrad(KID_MISC, (int)e, e_row0, 1, group_sizes, 0, lhs, kdim, g, n, kdim, n, drhs, nullptr, 0, n,
+  return lsurge::gemm_wgrad(KID_MISC, (int)e, e_row0, 1, e_rows, 0, lhs, kdim, g, n, kdim, n, drhs, nullptr, 0, n,
                             kdim * n, 1, nullptr, 0, s);
 }
 
