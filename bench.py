@@ -149,6 +149,9 @@ def main():
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB three times (calibrates rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE against a known byte count) and exit")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py: this build measures one GPU only (the MoE layer at one GPU's share); "
@@ -156,6 +159,16 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if a.copy_probe:
+        n = a.copy_probe << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "launches": 3}), flush=True)
+        return
 
     import _lib
     from moe_layer import MoELayer, MoEShape
