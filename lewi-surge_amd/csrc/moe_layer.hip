@@ -48,7 +48,7 @@ int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
                  bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false);
 size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S);
 int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
-               const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2,
+               int64_t max_rows, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2,
                int64_t n_split, int64_t ldc, int64_t c_estride, int S, void* ws, size_t ws_bytes, hipStream_t s);
 }  // namespace lsurge
 
@@ -271,7 +271,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                     q.d, q.f, w.dgu, 2 * q.f, true, sv.g, sv.u, q.f, st))
     return rc;
   // down wgrad: dW_down[e] = h_e^T dY_e
-  if (int rc = lsurge::gemm_wgrad(KID_GEMM_DOWN_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, sv.h, q.f, w.dy_pad, q.d,
+  if (int rc = lsurge::gemm_wgrad(KID_GEMM_DOWN_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, sv.h, q.f, w.dy_pad, q.d,
                                   q.f, q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, 1, nullptr, 0, st))
     return rc;
   // gate/up dgrad: dX_pad = dG W_gate^T + dU W_up^T
@@ -279,7 +279,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                     2 * q.f, q.d, w.dx_pad, q.d, false, nullptr, nullptr, 0, st))
     return rc;
   // gate/up wgrad: [dW_gate | dW_up][e] = x_e^T [dG | dU]_e
-  if (int rc = lsurge::gemm_wgrad(KID_GEMM_GU_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, sv.x_pad, q.d, w.dgu,
+  if (int rc = lsurge::gemm_wgrad(KID_GEMM_GU_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, sv.x_pad, q.d, w.dgu,
                                   2 * q.f, q.d, 2 * q.f, g->dw_gate, g->dw_up, q.f, q.f, q.d * q.f, 1, nullptr, 0, st))
     return rc;
   if (q.fs) {
@@ -288,14 +288,14 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                       w.sdgu, 2 * q.fs, true, sv.sg, sv.su, q.fs, st))
       return rc;
     int S = dense_splits(q.T, q.fs, q.d);
-    if (int rc = lsurge::gemm_wgrad(KID_SHARED_DOWN_WGRAD, 1, nullptr, 1, nullptr, q.T, sv.sh, q.fs, dy, q.d, q.fs, q.d,
+    if (int rc = lsurge::gemm_wgrad(KID_SHARED_DOWN_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, sv.sh, q.fs, dy, q.d, q.fs, q.d,
                                     g->dws_down, nullptr, 0, q.d, 0, S, w.part, w.part_bytes, st))
       return rc;
     if (int rc = lsurge::gemm_rows_nk(KID_SHARED_GU_DGRAD, dense, w.sdgu, 2 * q.fs, p->ws_gate, p->ws_up, q.fs, q.fs, 0,
                                       2 * q.fs, q.d, w.sdx, q.d, false, nullptr, nullptr, 0, st))
       return rc;
     S = dense_splits(q.T, q.d, 2 * q.fs);
-    if (int rc = lsurge::gemm_wgrad(KID_SHARED_GU_WGRAD, 1, nullptr, 1, nullptr, q.T, p->x, q.d, w.sdgu, 2 * q.fs, q.d,
+    if (int rc = lsurge::gemm_wgrad(KID_SHARED_GU_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.sdgu, 2 * q.fs, q.d,
                                     2 * q.fs, g->dws_gate, g->dws_up, q.fs, q.fs, 0, S, w.part, w.part_bytes, st))
       return rc;
   }
@@ -303,7 +303,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   if (int rc = lsurge::launch_scatter_dlogits(w.dl, sv.sel, q.T, (int)q.E, (int)q.k, w.dlog, st)) return rc;
   {
     const int S = dense_splits(q.T, q.d, q.E);
-    if (int rc = lsurge::gemm_wgrad(KID_ROUTER_WGRAD, 1, nullptr, 1, nullptr, q.T, p->x, q.d, w.dlog, q.E, q.d, q.E,
+    if (int rc = lsurge::gemm_wgrad(KID_ROUTER_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.dlog, q.E, q.d, q.E,
                                     g->dw_r, nullptr, 0, q.E, 0, S, w.part, w.part_bytes, st))
       return rc;
   }

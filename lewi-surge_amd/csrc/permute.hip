@@ -26,7 +26,7 @@ template <> struct V8<LSURGE_BF16> {
   static __device__ __forceinline__ void st(void* p, const float* v) {
     u32x4 u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) u[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+    for (int i = 0; i < 4; ++i) u[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
     *reinterpret_cast<u32x4*>(p) = u;
   }
 };
