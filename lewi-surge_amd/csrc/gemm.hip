@@ -1,7 +1,6 @@
 // Grouped GEMMs of the MoE layer on CDNA4 matrix cores: bf16 inputs, f32 accumulation,
-// v_mfma_f32_32x32x16_bf16, 128 x 256 workgroup tiles (4 waves, 64 x 128 each), K staged through LDS in
-// BK-wide double-buffered chunks fed from two register sets (global loads run two chunks ahead); two
-// workgroups share a CU.
+// v_mfma_f32_32x32x16_bf16, 128 x 256 workgroup tiles (4 waves, 64 x 128 each), K in 32-wide stages that the
+// buffer unit copies straight into a 3-deep LDS ring (buffer_load_dwordx4 ... lds), two workgroups per CU.
 //
 // Replaces the padded batched einsum of modal/padded_gmm.py:66-69 (cuBLAS on the reference's GPU path) and
 // its autodiff.  Two kernel families:
@@ -23,14 +22,13 @@
 namespace {
 
 // Workgroup tile: BM rows (one 128-row expert block) x BN columns, 4 waves in a 2 x 2 grid of 64 x 128 wave
-// tiles; K is staged through LDS BK at a time (54-57 KB of LDS, so two workgroups fit in a CU's 160 KB).  Per wave and 16-wide k step: 2 activation fragments + 4 weight
-// fragments (6 x 1 KiB of LDS reads) feed 8 MFMAs, which keeps LDS traffic at 3/4 of what 64 x 64 wave tiles
-// need.  Global loads run two K stages ahead through two register sets.
+// tiles.  Per wave and 16-wide k step: 2 activation fragments + 4 weight fragments (6 x 1 KiB of LDS reads)
+// feed 8 MFMAs.  K runs in BK = 32 stages; a stage is 8 KiB of activations + 16 KiB of weights, the ring holds
+// 3 stages (72 KiB), so two workgroups share a CU's 160 KiB and one's prologue/epilogue overlaps the other's
+// MFMAs.
 constexpr int BM = 128, BN = 256, BK = 32;
 constexpr int GT = 256;            // threads per workgroup
-constexpr int OCC = 2;             // workgroups per CU: one's prologue/epilogue overlaps the other's MFMAs
-constexpr int NPB = BN + 32;       // N-major B tile pitch: 576 B, rows k..k+3 fall on distinct 64 B bank groups
-constexpr int NPA = BM + 32;       // N-major A tile pitch (wgrad): 320 B, same property
+constexpr int OCC = 2;             // workgroups per CU
 
 enum { B_NK = 0, B_KN = 1 };                        // B operand storage
 enum { EPI_STORE = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
@@ -87,11 +85,18 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 p, bf16x8 q, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
 }
 
-// K-major tiles hold BK = 32 k per row (4 chunks of 16 B, 64 B rows, no padding).  Chunk c of row r sits at
-// slot c ^ ((r >> 2) & 3): a 16-lane group storing 4 whole rows covers 256 contiguous bytes, and a 16-lane
-// group reading one chunk of 16 consecutive rows hits 16 distinct 16-byte slots of a 256-byte bank window, so
-// neither direction has bank conflicts.
+// ---------------------------------------------------------------------------------------------- LDS tiles
+// K-major tile: rows of BK = 32 k (4 chunks of 16 B, 64 B rows, no padding).  Chunk c of row r sits at slot
+// c ^ ((r >> 2) & 3): the 16 lanes that fill 4 whole rows cover 256 contiguous bytes, and the 16 lanes that
+// read one chunk of 16 consecutive rows hit 16 distinct 16-byte slots of a 256-byte bank window, so neither
+// direction has bank conflicts.  One 1 KiB copy instruction fills 16 rows.
 __device__ __forceinline__ int km_off(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 2) & 3)) << 3); }
+
+// N-major sub-tile: BK k-rows x 128 columns (16 chunks of 16 B, 256 B rows).  Chunk c of row k sits at slot
+// c ^ ((k & 3) << 2), which moves the 64-byte column group of 4 consecutive rows to 4 different 64-byte bank
+// groups: a transpose read (4 rows x 64 B per 32 lanes) is conflict-free.  One copy instruction fills 4 rows.
+constexpr int NS = 128;  // columns per N-major sub-tile
+__device__ __forceinline__ int nm_off(int k, int n) { return k * NS + ((((n >> 3) ^ ((k & 3) << 2))) << 3) + (n & 7); }
 
 // K-major fragment: 8 consecutive k (chunk kc) of one row -> one 16-byte LDS read
 __device__ __forceinline__ bf16x8 frag_k(const bf16_t* tile, int row, int kc) {
@@ -102,41 +107,62 @@ __device__ __forceinline__ bf16x8 frag_k(const bf16_t* tile, int row, int kc) {
 // ds_read_b64_tr_b16 in a 16-lane group g: lane i receives D[4j + i/4][i%4], j = 0..3, where D[s] are the four
 // 16-bit values at source lane s's address.  With source lane s pointing at (k = kb + s/4, n = nb + 4(s%4)),
 // lane i receives column nb + i, rows kb..kb+3.  Two reads give the 8 k values.
-__device__ __forceinline__ bf16x8 frag_n(const bf16_t* tile, int pitch, int kbase, int nbase, int lane) {
+__device__ __forceinline__ bf16x8 frag_n(const bf16_t* sub, int kbase, int nbase, int lane) {
   const int g = lane >> 4, s = lane & 15;
   const int n = nbase + 16 * (g & 1) + 4 * (s & 3);
   const int k0 = kbase + 8 * (g >> 1) + (s >> 2);
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, tile + k0 * pitch + n));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, tile + (k0 + 4) * pitch + n));
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, sub + nm_off(k0, n)));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, sub + nm_off(k0 + 4, n)));
   typedef short s16x8 __attribute__((ext_vector_type(8)));
   const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return __builtin_bit_cast(bf16x8, v);
 }
 
-__device__ __forceinline__ void st16(bf16_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
-
-// Operand tiles are fetched with raw buffer loads: one descriptor per operand covers exactly the bytes the tile
-// may read (a block's valid rows, an expert's weight matrix), and a lane whose element lies outside the tile
-// (rows past the block, K or N tails) passes an offset past the end, for which the buffer unit returns zeros.
-// That keeps the load path free of branches and the zero padding exact.
+// ---------------------------------------------------------------------------------------------- global -> LDS
+// Operand tiles are copied by the buffer unit straight into LDS (buffer_load_dwordx4 ... lds): lane p of a copy
+// instruction writes its 16 bytes at (M0 + 16 p), so the LDS layouts above are produced by choosing which global
+// chunk each lane fetches.  One descriptor per operand covers exactly the bytes the tile may read (a block's
+// valid rows, an expert's weight matrix), and a lane whose element lies outside (rows past the block, K or N
+// tails) passes an offset past the end, for which the buffer unit writes zeros.  No VGPR staging, no LDS store
+// instructions.
+//
+// The copy is issued from inline asm so that the compiler does not see an LDS write: it would otherwise guard
+// LDS reads with waits for every copy in flight (it cannot tell the ring slots apart through the transpose
+// reads), draining the prefetch ring.  Completion is tracked by hand instead: stage_barrier<N> waits until at
+// most N copies of this wave are outstanding before the workgroup barrier.
 constexpr uint32_t OOB = 0x80000000u;  // every descriptor covers < 2^31 bytes (checked on the host)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, int64_t bytes) {
+  const uint64_t b = (uint64_t)base;
+  // base (48 bits), stride 0, num_records = bytes, dword3 = 32-bit data format, no swizzle
+  return u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xffffu, (uint32_t)bytes, 0x00020000u};
 }
-__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
+__device__ __forceinline__ void copy16(u32x4 rsrc, uint32_t byte_off, bf16_t* lds_1k) {
+  // descriptor and LDS base are wave-uniform; readfirstlane pins them to scalar registers for the asm
+  const u32x4 r = {(uint32_t)__builtin_amdgcn_readfirstlane(rsrc[0]), (uint32_t)__builtin_amdgcn_readfirstlane(rsrc[1]),
+                   (uint32_t)__builtin_amdgcn_readfirstlane(rsrc[2]), (uint32_t)__builtin_amdgcn_readfirstlane(rsrc[3])};
+  const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(size_t)LDS_PTR(void, lds_1k));
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(r), "s"(m0)
+               : "memory");
+}
+
+// Per wave and stage: A tile 8 KiB = 2 copies, B tile 16 KiB = 4 copies.
+constexpr int CP_STAGE = 6;
+static_assert(BM * BK * 2 / 1024 == 2 * 4 && BN * BK * 2 / 1024 == 4 * 4, "copy counts assume 4 waves");
+
+// Wait until at most N copies of this wave are in flight and its LDS reads are done, then barrier: after it
+// every wave's copies of the stage in question have landed and nobody still reads the buffer about to be
+// refilled.  The barrier is an asm statement with a memory clobber so the compiler keeps LDS accesses on
+// their side of it without adding a wait for all copies (which would drain the prefetch ring).
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));  // vmcnt(N) lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
 }
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void st_bf16x4(bf16_t* p, float a, float b, float c, float d) {
   *reinterpret_cast<u32x2*>(p) = u32x2{pack_bf16x2(a, b), pack_bf16x2(c, d)};
-}
-__device__ __forceinline__ void ld_bf16x4(const bf16_t* p, float* o) {
-  const u32x2 v = *reinterpret_cast<const u32x2*>(p);
-  o[0] = __uint_as_float(v[0] << 16);
-  o[1] = __uint_as_float(v[0] & 0xffff0000u);
-  o[2] = __uint_as_float(v[1] << 16);
-  o[3] = __uint_as_float(v[1] & 0xffff0000u);
 }
 
 // 1 / (1 + e^-g) with the hardware reciprocal (about 1 ulp): plenty for bf16 outputs, and it keeps the
@@ -151,29 +177,37 @@ __device__ __forceinline__ int64_t xcd_logical(int64_t id, int64_t total) {
   return (id % 8) * per + id / 8;
 }
 
-constexpr int KC = BK / 8;          // 16-byte chunks per K-major tile row
-static_assert(KC == 4, "km_off swizzles 4 chunks per row");
-constexpr int SA = BM * BK / 8 / GT;  // 16-byte loads per thread: activation tile (or wgrad A tile)
-constexpr int SB = BN * BK / 8 / GT;  // weight tile (or wgrad B tile)
-struct Stage {
-  u32x4 a[SA];
-  u32x4 b[SB];
-};
-
-// N-major B tile (BK k-rows x BN columns): 16-byte chunk i of thread tid -> (k row, first column).  Loads
-// i < SB/2 cover columns [0, BN/2) and the rest [BN/2, BN), so in the SwiGLU forward (gate columns, then up
-// columns) every load instruction reads from one weight matrix and its descriptor stays wave-uniform.
-__device__ __forceinline__ int2 kn_chunk(int tid, int i) {
-  constexpr int HALF_CHUNKS = BN / 2 / 8;                     // 16 chunks per half row
-  const int v = tid + GT * (i % (SB / 2));                    // 0 .. BK * 16 - 1
-  return int2{v / HALF_CHUNKS, (i < SB / 2 ? 0 : BN / 2) + (v % HALF_CHUNKS) * 8};
+// Run the K loop: stage kt lives in ring slot kt % 3.  Each step waits for its own stage, barriers, refills the
+// slot read one step earlier with stage kt + 2, and multiplies.  Stages past the end copy zeros (out-of-range
+// offsets), so every step has the same shape.  issue(slot, kt) enqueues the copies, compute(slot) the MFMAs.
+template <class Issue, class Compute>
+__device__ __forceinline__ void k_loop(int nk, Issue&& issue, Compute&& compute) {
+  issue(0, 0);
+  issue(1, 1);
+  for (int kt = 0;; kt += 3) {
+    stage_barrier<CP_STAGE>();
+    issue(2, kt + 2);
+    compute(0);
+    if (kt + 1 >= nk) break;
+    stage_barrier<CP_STAGE>();
+    issue(0, kt + 3);
+    compute(1);
+    if (kt + 2 >= nk) break;
+    stage_barrier<CP_STAGE>();
+    issue(1, kt + 4);
+    compute(2);
+    if (kt + 3 >= nk) break;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the copies of the zero stages past the end land before the epilogue
 }
 
 // =====================================================================================================
 template <int BMODE, int EPI>
 __global__ __launch_bounds__(GT, OCC) void gemm_rows_kernel(RowsArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BMODE == B_NK ? BN * BK : BK * NPB];
+  // LDS ring: 3 stages of A (K-major 128 x 32) and B (K-major 256 x 32, or two N-major 32 x 128 sub-tiles);
+  // separate arrays per slot let the compiler track the copies into each slot separately
+  __shared__ __attribute__((aligned(1024))) bf16_t A0[BM * BK], A1[BM * BK], A2[BM * BK];
+  __shared__ __attribute__((aligned(1024))) bf16_t B0[BN * BK], B1[BN * BK], B2[BN * BK];
 
   const int64_t total = (int64_t)gridDim.x;
   const int64_t logical = xcd_logical(blockIdx.x, total);
@@ -193,79 +227,84 @@ __global__ __launch_bounds__(GT, OCC) void gemm_rows_kernel(RowsArgs a) {
     rows = (int)min((int64_t)BM, a.dense_rows - row0);
     if (rows <= 0) return;
   }
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index is uniform: keeping it in a scalar register keeps the copy destinations (M0) and the choice
+  // of weight descriptor scalar as well
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   // column origin of this tile: weight columns for B, output columns for C (SwiGLU: gate and up halves)
   const int64_t n0 = (int64_t)nt * (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN);
   const bf16_t* Bbase = a.B + (int64_t)expert * a.b_estride;
-  const bf16_t* B2base = a.B2 ? a.B2 + (int64_t)expert * a.b_estride : nullptr;
+  const bf16_t* B2base = a.B2 ? a.B2 + (int64_t)expert * a.b_estride : Bbase;
   const int64_t K = a.K, N = a.N;
   const int nk = (int)((K + BK - 1) / BK);
 
   // descriptors: this block's rows of A; the expert's B (and B2) matrix
-  const __amdgpu_buffer_rsrc_t rsA = make_rsrc(a.A + row0 * a.lda, (int64_t)rows * a.lda * 2);
+  const u32x4 rsA = make_rsrc(a.A + row0 * a.lda, (int64_t)rows * a.lda * 2);
   const int64_t b_bytes = (BMODE == B_NK ? N : K) * a.ldb * 2;
-  const __amdgpu_buffer_rsrc_t rsB = make_rsrc(Bbase, b_bytes);
-  const __amdgpu_buffer_rsrc_t rsB2 = make_rsrc(B2base ? B2base : Bbase, b_bytes);
+  const u32x4 rsB = make_rsrc(Bbase, b_bytes);
+  const u32x4 rsB2 = make_rsrc(B2base, b_bytes);
 
-  auto load = [&](Stage& st, int kt) {
+  // ---- per-lane copy geometry (fixed over k): which global row / column chunk this lane fetches
+  // A: copies q = 2 wave + c (c = 0, 1), 16 rows each; lane -> row 16 q + lane / 4, slot lane % 4
+  int a_row[2], a_kc[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int r = 16 * (2 * wave + c) + (lane >> 2);
+    a_row[c] = r;
+    a_kc[c] = (lane & 3) ^ ((r >> 2) & 3);
+  }
+  // B K-major: copies q = 4 wave + c, 16 rows (n) each.  B N-major: sub-tile wave / 2, copies (wave & 1) * 4 + c
+  // of 4 k-rows each; lane -> k row 4 q' + lane / 16, slot lane % 16.
+  int b_r[4], b_c[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    if (BMODE == B_NK) {
+      const int n = 16 * (4 * wave + c) + (lane >> 2);
+      b_r[c] = n;
+      b_c[c] = (lane & 3) ^ ((n >> 2) & 3);
+    } else {
+      const int k = 4 * ((wave & 1) * 4 + c) + (lane >> 4);
+      b_r[c] = k;
+      b_c[c] = (lane & 15) ^ ((k & 3) << 2);
+    }
+  }
+  const bool b_sub1 = (wave >> 1) != 0;  // N-major: this wave fills sub-tile 1 (columns 128..255)
+
+  auto issue = [&](int slot, int kt) {
+    bf16_t* At = slot == 0 ? A0 : slot == 1 ? A1 : A2;
+    bf16_t* Bt = slot == 0 ? B0 : slot == 1 ? B1 : B2;
     const int k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < SA; ++i) {
-      const int v = tid + GT * i;
-      const int r = v / KC, kc = (v % KC) * 8;
-      const bool ok = r < rows && k0 + kc < K;
-      st.a[i] = bload16(rsA, ok ? (uint32_t)((r * a.lda + k0 + kc) * 2) : OOB);
+    for (int c = 0; c < 2; ++c) {
+      const int r = a_row[c], kk = k0 + 8 * a_kc[c];
+      const bool ok = r < rows && kk < K;
+      copy16(rsA, ok ? (uint32_t)((r * a.lda + kk) * 2) : OOB, At + 512 * (2 * wave + c));
     }
     if (BMODE == B_NK) {
-      const bool second = a.k_split && k0 >= a.k_split;
-      const int kk0 = second ? k0 - (int)a.k_split : k0;
+      const bool second = a.k_split && k0 >= a.k_split;  // k range of B2 (gate/up dgrad)
+      const int kb = second ? k0 - (int)a.k_split : k0;
 #pragma unroll
-      for (int i = 0; i < SB; ++i) {
-        const int v = tid + GT * i;
-        const int n = v / KC, kc = (v % KC) * 8;
-        const int64_t gn = n0 + n;
-        const bool ok = gn < N && k0 + kc < K;
-        const uint32_t off = ok ? (uint32_t)((gn * a.ldb + kk0 + kc) * 2) : OOB;
-        st.b[i] = second ? bload16(rsB2, off) : bload16(rsB, off);
+      for (int c = 0; c < 4; ++c) {
+        const int64_t gn = n0 + b_r[c];
+        const int kk = kb + 8 * b_c[c];
+        const uint32_t off = (gn < N && k0 + 8 * b_c[c] < K) ? (uint32_t)((gn * a.ldb + kk) * 2) : OOB;
+        if (second) copy16(rsB2, off, Bt + 512 * (4 * wave + c));
+        else copy16(rsB, off, Bt + 512 * (4 * wave + c));
       }
     } else {
+      bf16_t* sub = Bt + (b_sub1 ? BK * NS : 0);
 #pragma unroll
-      for (int i = 0; i < SB; ++i) {
-        const int2 kn = kn_chunk(tid, i);
-        const int64_t gk = k0 + kn.x;
-        if (EPI == EPI_SWIGLU_FWD) {  // tile columns [0, 128) gate, [128, 256) up, same output columns
-          const int64_t gn = n0 + (kn.y & (BN / 2 - 1));
-          const uint32_t off = (gk < K && gn < N) ? (uint32_t)((gk * a.ldb + gn) * 2) : OOB;
-          st.b[i] = i < SB / 2 ? bload16(rsB, off) : bload16(rsB2, off);  // uniform choice of descriptor
-        } else {
-          const int64_t gn = n0 + kn.y;
-          st.b[i] = bload16(rsB, (gk < K && gn < N) ? (uint32_t)((gk * a.ldb + gn) * 2) : OOB);
-        }
+      for (int c = 0; c < 4; ++c) {
+        const int64_t gk = k0 + b_r[c];
+        int64_t gn;
+        if (EPI == EPI_SWIGLU_FWD) gn = n0 + 8 * b_c[c];                      // sub-tile 0 gate, 1 up
+        else gn = n0 + (b_sub1 ? NS : 0) + 8 * b_c[c];
+        const uint32_t off = (gk < K && gn < N) ? (uint32_t)((gk * a.ldb + gn) * 2) : OOB;
+        bf16_t* dst = sub + 512 * ((wave & 1) * 4 + c);
+        if (EPI == EPI_SWIGLU_FWD && b_sub1) copy16(rsB2, off, dst);
+        else copy16(rsB, off, dst);
       }
     }
-  };
-  auto store = [&](const Stage& st, int buf) {
-#pragma unroll
-    for (int i = 0; i < SA; ++i) {
-      const int v = tid + GT * i;
-      st16(&As[buf][km_off(v / KC, v % KC)], st.a[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < SB; ++i) {
-      const int v = tid + GT * i;
-      if (BMODE == B_NK) {
-        st16(&Bs[buf][km_off(v / KC, v % KC)], st.b[i]);
-      } else {
-        const int2 kn = kn_chunk(tid, i);
-        st16(&Bs[buf][kn.x * NPB + kn.y], st.b[i]);
-      }
-    }
-  };
-  // tile column of this wave's weight fragment j
-  auto bcol = [&](int j) {
-    if (EPI == EPI_SWIGLU_FWD) return (j < 2 ? 0 : BN / 2) + wn * 64 + 32 * (j & 1);
-    return wn * 128 + 32 * j;
   };
 
   f32x16 acc[2][4];
@@ -274,10 +313,15 @@ __global__ __launch_bounds__(GT, OCC) void gemm_rows_kernel(RowsArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  auto compute = [&](int buf) {
+  // tile column of this wave's weight fragment j (SwiGLU: j < 2 gate, j >= 2 up, same output columns)
+  auto bcol = [&](int j) {
+    if (EPI == EPI_SWIGLU_FWD) return (j < 2 ? 0 : BN / 2) + wn * 64 + 32 * (j & 1);
+    return wn * 128 + 32 * j;
+  };
+  auto compute = [&](int slot) {
     __builtin_amdgcn_iglp_opt(0);  // interleave the fragment reads with the MFMAs
-    const bf16_t* at = As[buf];
-    const bf16_t* bt = Bs[buf];
+    const bf16_t* at = slot == 0 ? A0 : slot == 1 ? A1 : A2;
+    const bf16_t* bt = slot == 0 ? B0 : slot == 1 ? B1 : B2;
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
       bf16x8 xf[2], wf[4];
@@ -285,8 +329,9 @@ __global__ __launch_bounds__(GT, OCC) void gemm_rows_kernel(RowsArgs a) {
       for (int i = 0; i < 2; ++i) xf[i] = frag_k(at, wm * 64 + 32 * i + (lane & 31), kk / 8 + (lane >> 5));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (BMODE == B_NK) wf[j] = frag_k(bt, bcol(j) + (lane & 31), kk / 8 + (lane >> 5));
-        else wf[j] = frag_n(bt, NPB, kk, bcol(j), lane);
+        const int col = bcol(j);
+        if (BMODE == B_NK) wf[j] = frag_k(bt, col + (lane & 31), kk / 8 + (lane >> 5));
+        else wf[j] = frag_n(bt + (col >= NS ? BK * NS : 0), kk, col & (NS - 1), lane);
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -295,26 +340,7 @@ __global__ __launch_bounds__(GT, OCC) void gemm_rows_kernel(RowsArgs a) {
     }
   };
 
-  // Software pipeline: LDS buffers 0/1, register sets ra/rb; the loads of stage kt+2 are issued while stage kt
-  // is multiplied, so global latency has two compute phases to hide behind.  One barrier per stage.  The loop
-  // body is branch-free: stages past the end load as zeros (out-of-range offsets), so the wait counts are the
-  // same on every trip and an odd stage count just multiplies one zero stage.
-  Stage ra, rb;
-  load(ra, 0);
-  load(rb, 1);
-  store(ra, 0);
-  load(ra, 2);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt += 2) {
-    store(rb, 1);
-    load(rb, kt + 3);
-    compute(0);
-    __syncthreads();
-    store(ra, 0);
-    load(ra, kt + 4);
-    compute(1);
-    __syncthreads();
-  }
+  k_loop(nk, issue, compute);
 
   // ---- epilogue.  acc[i][j][4q + t]: activation row wm*64 + 32 i + lane%32, tile column bcol(j) + 8 q +
   // 4 (lane/32) + t.
@@ -407,8 +433,9 @@ __global__ __launch_bounds__(GT, OCC) void gemm_rows_kernel(RowsArgs a) {
 // Weight gradient C_e[I, N] = A_e^T B_e, reduced over the rows of expert e: both operands are row-major
 // [rows, .] (the reduction dim is the slow one), so both are staged N-major and read with the transpose read.
 __global__ __launch_bounds__(GT, OCC) void gemm_wgrad_kernel(WgradArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t As[2][BK * NPA];
-  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BK * NPB];
+  // ring: A 32 rows x 128 columns (one N-major sub-tile), B 32 rows x 256 columns (two sub-tiles)
+  __shared__ __attribute__((aligned(1024))) bf16_t A0[BK * NS], A1[BK * NS], A2[BK * NS];
+  __shared__ __attribute__((aligned(1024))) bf16_t B0[BK * BN], B1[BK * BN], B2[BK * BN];
   const int64_t total = (int64_t)gridDim.x;
   int64_t logical = xcd_logical(blockIdx.x, total);
   const int64_t tiles_per_e = (int64_t)a.S * a.i_tiles * a.n_tiles;
@@ -431,7 +458,7 @@ __global__ __launch_bounds__(GT, OCC) void gemm_wgrad_kernel(WgradArgs a) {
   const int64_t rs = (int64_t)s * chunk;
   const int64_t re = min(nrows, rs + chunk);
   const int64_t i0 = (int64_t)it * BM, n0 = (int64_t)nt * BN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t I = a.I, N = a.N;
 
@@ -444,69 +471,59 @@ __global__ __launch_bounds__(GT, OCC) void gemm_wgrad_kernel(WgradArgs a) {
   const int nk = re > rs ? (int)((re - rs + BK - 1) / BK) : 0;
   // descriptors over rows [rs, re) of this expert (empty when the split has no rows)
   const int64_t span = re > rs ? re - rs : 0;
-  const __amdgpu_buffer_rsrc_t rsA = make_rsrc(a.A + (r0 + rs) * a.lda, span * a.lda * 2);
-  const __amdgpu_buffer_rsrc_t rsB = make_rsrc(a.B + (r0 + rs) * a.ldb, span * a.ldb * 2);
-  auto load = [&](Stage& st, int kt) {
-    const int rbase = kt * BK;
+  const u32x4 rsA = make_rsrc(a.A + (r0 + rs) * a.lda, span * a.lda * 2);
+  const u32x4 rsB = make_rsrc(a.B + (r0 + rs) * a.ldb, span * a.ldb * 2);
+  // copies: A sub-tile 8 copies of 4 rows (wave w: 2 w, 2 w + 1); B 16 copies (wave w: sub-tile w / 2,
+  // copies (w & 1) * 4 + c)
+  int a_k[2], a_c[2], b_k[4], b_c[4];
 #pragma unroll
-    for (int q = 0; q < SA; ++q) {
-      const int v = tid + GT * q;
-      const int rr = rbase + (v >> 4), ic = (v & 15) * 8;
-      const bool ok = rr < span && i0 + ic < I;
-      st.a[q] = bload16(rsA, ok ? (uint32_t)((rr * a.lda + i0 + ic) * 2) : OOB);
+  for (int c = 0; c < 2; ++c) {
+    a_k[c] = 4 * (2 * wave + c) + (lane >> 4);
+    a_c[c] = (lane & 15) ^ ((a_k[c] & 3) << 2);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    b_k[c] = 4 * ((wave & 1) * 4 + c) + (lane >> 4);
+    b_c[c] = (lane & 15) ^ ((b_k[c] & 3) << 2);
+  }
+  const int b_sub = wave >> 1;
+  auto issue = [&](int slot, int kt) {
+    bf16_t* At = slot == 0 ? A0 : slot == 1 ? A1 : A2;
+    bf16_t* Bt = slot == 0 ? B0 : slot == 1 ? B1 : B2;
+    const int rb = kt * BK;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int rr = rb + a_k[c];
+      const int64_t ic = i0 + 8 * a_c[c];
+      copy16(rsA, (rr < span && ic < I) ? (uint32_t)((rr * a.lda + ic) * 2) : OOB, At + 512 * (2 * wave + c));
     }
 #pragma unroll
-    for (int q = 0; q < SB; ++q) {
-      const int v = tid + GT * q;
-      const int rr = rbase + (v >> 5), nc = (v & 31) * 8;
-      const bool ok = rr < span && n0 + nc < N;
-      st.b[q] = bload16(rsB, ok ? (uint32_t)((rr * a.ldb + n0 + nc) * 2) : OOB);
+    for (int c = 0; c < 4; ++c) {
+      const int rr = rb + b_k[c];
+      const int64_t nc = n0 + NS * b_sub + 8 * b_c[c];
+      copy16(rsB, (rr < span && nc < N) ? (uint32_t)((rr * a.ldb + nc) * 2) : OOB,
+             Bt + BK * NS * b_sub + 512 * ((wave & 1) * 4 + c));
     }
   };
-  auto store = [&](const Stage& st, int buf) {
-#pragma unroll
-    for (int q = 0; q < SA; ++q) {
-      const int v = tid + GT * q;
-      st16(&As[buf][(v >> 4) * NPA + (v & 15) * 8], st.a[q]);
-    }
-#pragma unroll
-    for (int q = 0; q < SB; ++q) {
-      const int v = tid + GT * q;
-      st16(&Bs[buf][(v >> 5) * NPB + (v & 31) * 8], st.b[q]);
-    }
-  };
-  auto compute = [&](int buf) {
+  auto compute = [&](int slot) {
     __builtin_amdgcn_iglp_opt(0);
+    const bf16_t* at = slot == 0 ? A0 : slot == 1 ? A1 : A2;
+    const bf16_t* bt = slot == 0 ? B0 : slot == 1 ? B1 : B2;
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
       bf16x8 af[2], bfr[4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = frag_n(As[buf], NPA, kk, wm * 64 + 32 * i, lane);
+      for (int i = 0; i < 2; ++i) af[i] = frag_n(at, kk, wm * 64 + 32 * i, lane);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bfr[j] = frag_n(Bs[buf], NPB, kk, wn * 128 + 32 * j, lane);
+      for (int j = 0; j < 4; ++j) bfr[j] = frag_n(bt + BK * NS * wn, kk, 32 * j, lane);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(bfr[j], af[i], acc[i][j]);
     }
   };
-  // same branch-free pipeline as gemm_rows_kernel (rows past the split load as zeros)
-  Stage ra, rb;
-  load(ra, 0);
-  load(rb, 1);
-  store(ra, 0);
-  load(ra, 2);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt += 2) {
-    store(rb, 1);
-    load(rb, kt + 3);
-    compute(0);
-    __syncthreads();
-    store(ra, 0);
-    load(ra, kt + 4);
-    compute(1);
-    __syncthreads();
-  }
+  k_loop(nk, issue, compute);
+
   // epilogue (f32): acc[i][j][4q + t] = C[i0 + wm*64 + 32 i + lane%32][n0 + wn*128 + 32 j + 8 q + 4 (lane/32) + t]
   const int lm = lane & 31, lh = lane >> 5;
 #pragma unroll
