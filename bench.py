@@ -48,7 +48,8 @@ def kernel_work(c):
         "gemm_gu_dgrad": ("mfma", 2 * M * 2 * f * d),
         "gemm_gu_wgrad": ("mfma", 2 * M * d * 2 * f),
         "router_wgrad": ("mfma", 2 * T * d * E),
-        "router_topk": ("hbm", T * d * 2 + d * E * 2 + T * E * 4 + 8 * T * k),
+        "router_topk": ("hbm", T * d * 2 + d * E * 2 + T * E * 4),
+        "router_select": ("hbm", T * E * 4 + 8 * T * k),
         "dispatch": ("hbm", 2 * M * d * 2 + 4 * M),
         "combine_fwd": ("hbm", M * d * 2 + T * d * 2 * (2 if fs else 1) + 8 * T * k),
         "combine_bwd": ("hbm", 2 * M * d * 2 + T * d * 2 + 16 * T * k),

@@ -48,7 +48,7 @@ const char* g_names[KID_COUNT] = {
     "gemm_gu_fwd",      "gemm_down_fwd",     "combine_fwd",       "combine_bwd",      "gemm_down_dgrad",
     "gemm_down_wgrad",  "gemm_gu_dgrad",     "gemm_gu_wgrad",     "dispatch_bwd",     "router_wgrad",
     "shared_gu_fwd",    "shared_down_fwd",   "shared_down_dgrad", "shared_down_wgrad", "shared_gu_dgrad",
-    "shared_gu_wgrad",  "splitk_reduce",     "misc"};
+    "shared_gu_wgrad",  "splitk_reduce",     "misc",             "router_select"};
 constexpr size_t kPool = 8192;
 }  // namespace
 

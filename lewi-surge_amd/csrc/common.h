@@ -96,6 +96,7 @@ enum {
   KID_SHARED_GU_WGRAD,
   KID_SPLITK_REDUCE,
   KID_MISC,
+  KID_ROUTER_SELECT,
   KID_COUNT
 };
 

@@ -267,28 +267,45 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_kernel(const void* __r
 }
 
 // ------------------------------------------------------------------------------ padded-layout layer kernels
+// One wave per token (or padded row).  A row of d elements is NC chunks of 8 per lane (d == 512 NC) and the
+// loop over the k choices is unrolled KK times when NC and KK are compile-time constants (d = 1024 / 2048,
+// k = 6 / 8 at the BASELINE configs), so every row load of a token is in flight at once; NC = 0 or KK = 0
+// select the run-time loops for other shapes.  The wave's token index is made scalar so the routing
+// indices come through the scalar cache.
+__device__ __forceinline__ int64_t wave_id() {
+  return (int64_t)blockIdx.x * PM_WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
 // dispatch: x_pad[r] = x[row_src[r] / k] for valid padded rows of the used blocks (padding rows untouched;
 // the GEMMs mask them by blk_rows).
+template <int NC>
 __global__ __launch_bounds__(PM_THREADS) void dispatch_pad_kernel(const bf16_t* __restrict__ x, int64_t d, int k,
                                                                   const int32_t* __restrict__ row_src,
                                                                   const int32_t* __restrict__ num_blocks,
                                                                   int64_t max_rows, bf16_t* __restrict__ xp) {
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
   const int64_t rows = min((int64_t)num_blocks[0] * LSURGE_BLOCK_ROWS, max_rows);
-  for (int64_t r = wave; r < rows; r += nwaves) {
+  for (int64_t r = wave_id(); r < rows; r += nwaves) {
     const int32_t src = row_src[r];
     if (src < 0) continue;
     const bf16_t* xr = x + (int64_t)(src / k) * d;
     bf16_t* o = xp + r * d;
-    for (int64_t c = lane * 8; c < d; c += 64 * 8)
-      *reinterpret_cast<u32x4*>(o + c) = *reinterpret_cast<const u32x4*>(xr + c);
+    if (NC) {
+      u32x4 v[NC > 0 ? NC : 1];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) v[c] = *reinterpret_cast<const u32x4*>(xr + (c * 64 + lane) * 8);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) *reinterpret_cast<u32x4*>(o + (c * 64 + lane) * 8) = v[c];
+    } else {
+      for (int64_t c = lane * 8; c < d; c += 64 * 8)
+        *reinterpret_cast<u32x4*>(o + c) = *reinterpret_cast<const u32x4*>(xr + c);
+    }
   }
 }
 
 // combine: out[t] = sum_j w[t,j] * y_pad[slot[t,j]] (+ add[t]), f32 accumulate, j ascending, one rounding.
-template <int OT>
+template <int NC, int KK, int OT>
 __global__ __launch_bounds__(PM_THREADS) void combine_pad_kernel(const bf16_t* __restrict__ yp, int64_t d, int k,
                                                                  const int32_t* __restrict__ slot,
                                                                  const float* __restrict__ w, int64_t n,
@@ -296,64 +313,198 @@ __global__ __launch_bounds__(PM_THREADS) void combine_pad_kernel(const bf16_t* _
                                                                  void* __restrict__ out) {
   constexpr int OS = esize<OT>();
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
-  for (int64_t t = wave; t < n; t += nwaves) {
-    for (int64_t c = lane * 8; c < d; c += 64 * 8) {
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int j = 0; j < k; ++j) {
-        const int64_t r = slot[t * k + j];
-        const float wj = w[t * k + j];
-        float v[8];
-        V8<LSURGE_BF16>::ld(yp + r * d + c, v);
+  const int kk = KK ? KK : k;
+  for (int64_t t = wave_id(); t < n; t += nwaves) {
+    if (NC) {
+      float acc[NC > 0 ? NC : 1][8] = {};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += wj * v[e];
+      for (int j = 0; j < (KK ? KK : 1); ++j) {
+        if (!KK) break;
+        const int64_t r = slot[t * kk + j];
+        const float wj = w[t * kk + j];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          float v[8];
+          V8<LSURGE_BF16>::ld(yp + r * d + (c * 64 + lane) * 8, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[c][e] += wj * v[e];
+        }
+      }
+      if (!KK) {
+        for (int j = 0; j < kk; ++j) {
+          const int64_t r = slot[t * kk + j];
+          const float wj = w[t * kk + j];
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            float v[8];
+            V8<LSURGE_BF16>::ld(yp + r * d + (c * 64 + lane) * 8, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[c][e] += wj * v[e];
+          }
+        }
       }
       if (add) {
-        float v[8];
-        V8<LSURGE_BF16>::ld(add + t * d + c, v);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += v[e];
+        for (int c = 0; c < NC; ++c) {
+          float v[8];
+          V8<LSURGE_BF16>::ld(add + t * d + (c * 64 + lane) * 8, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[c][e] += v[e];
+        }
       }
-      V8<OT>::st((char*)out + (t * d + c) * OS, acc);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) V8<OT>::st((char*)out + (t * d + (c * 64 + lane) * 8) * OS, acc[c]);
+    } else {
+      for (int64_t c = lane * 8; c < d; c += 64 * 8) {
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int j = 0; j < kk; ++j) {
+          const int64_t r = slot[t * kk + j];
+          const float wj = w[t * kk + j];
+          float v[8];
+          V8<LSURGE_BF16>::ld(yp + r * d + c, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += wj * v[e];
+        }
+        if (add) {
+          float v[8];
+          V8<LSURGE_BF16>::ld(add + t * d + c, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += v[e];
+        }
+        V8<OT>::st((char*)out + (t * d + c) * OS, acc);
+      }
+    }
+  }
+}
+
+// Fused combine backward of the layer (bf16 rows): per token, g is read once; for every choice j the expert
+// row y_pad[slot] is read once, dy_pad[slot] = bf16(w_j g) written once and <g, y> reduced; then the router
+// term dl[t,j] = w_j (dw_j - sum_i w_i dw_i).  moe_permute.py:303-309 does this in two passes over g and y.
+template <int NC, int KK>
+__global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_t* __restrict__ yp,
+                                                                     const int32_t* __restrict__ slot,
+                                                                     const float* __restrict__ w, int64_t n,
+                                                                     int64_t d, const bf16_t* __restrict__ g,
+                                                                     bf16_t* __restrict__ dyp, float* __restrict__ dw,
+                                                                     float* __restrict__ dl) {
+  static_assert(NC > 0 && KK > 0, "fixed-shape kernel");
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  for (int64_t t = wave_id(); t < n; t += nwaves) {
+    float gv[NC][8];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) V8<LSURGE_BF16>::ld(g + t * d + (c * 64 + lane) * 8, gv[c]);
+    float dot[KK];
+#pragma unroll
+    for (int j = 0; j < KK; ++j) {
+      const int64_t r = slot[t * KK + j];
+      const float wj = w[t * KK + j];
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        float v[8], o[8];
+        V8<LSURGE_BF16>::ld(yp + r * d + (c * 64 + lane) * 8, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc += v[e] * gv[c][e];
+          o[e] = wj * gv[c][e];
+        }
+        V8<LSURGE_BF16>::st(dyp + r * d + (c * 64 + lane) * 8, o);
+      }
+      dot[j] = acc;
+    }
+#pragma unroll
+    for (int j = 0; j < KK; ++j) dot[j] = wave_sum(dot[j]);
+    if (lane == 0) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < KK; ++j) {
+        if (dw) dw[t * KK + j] = dot[j];
+        s += w[t * KK + j] * dot[j];
+      }
+      if (dl) {
+#pragma unroll
+        for (int j = 0; j < KK; ++j) dl[t * KK + j] = w[t * KK + j] * (dot[j] - s);
+      }
     }
   }
 }
 
 // dispatch backward + router dx + shared-expert dx, one rounding:
 //   dx[t] = sum_j dxp[slot[t,j]] + sum_j dl[t,j] * w_rT[sel[t,j]] + add[t]
+template <int NC, int KK>
 __global__ __launch_bounds__(PM_THREADS) void dispatch_bwd_pad_kernel(
     const bf16_t* __restrict__ dxp, int64_t d, int k, const int32_t* __restrict__ slot, int64_t n,
     const float* __restrict__ dl, const int32_t* __restrict__ sel, const bf16_t* __restrict__ w_rT,
     const bf16_t* __restrict__ add, bf16_t* __restrict__ dx) {
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * PM_WAVES + (threadIdx.x >> 6);
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
-  for (int64_t t = wave; t < n; t += nwaves) {
-    for (int64_t c = lane * 8; c < d; c += 64 * 8) {
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int j = 0; j < k; ++j) {
-        float v[8];
-        V8<LSURGE_BF16>::ld(dxp + (int64_t)slot[t * k + j] * d + c, v);
+  for (int64_t t = wave_id(); t < n; t += nwaves) {
+    if (NC && KK) {
+      float acc[NC > 0 ? NC : 1][8] = {};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += v[e];
+      for (int j = 0; j < KK; ++j) {
+        const int64_t r = slot[t * KK + j];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          float v[8];
+          V8<LSURGE_BF16>::ld(dxp + r * d + (c * 64 + lane) * 8, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[c][e] += v[e];
+        }
       }
       if (dl) {
-        for (int j = 0; j < k; ++j) {
-          const float lj = dl[t * k + j];
-          float v[8];
-          V8<LSURGE_BF16>::ld(w_rT + (int64_t)sel[t * k + j] * d + c, v);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[e] += lj * v[e];
+        for (int j = 0; j < KK; ++j) {
+          const float lj = dl[t * KK + j];
+          const int64_t e_ = sel[t * KK + j];
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            float v[8];
+            V8<LSURGE_BF16>::ld(w_rT + e_ * d + (c * 64 + lane) * 8, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[c][e] += lj * v[e];
+          }
         }
       }
       if (add) {
-        float v[8];
-        V8<LSURGE_BF16>::ld(add + t * d + c, v);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += v[e];
+        for (int c = 0; c < NC; ++c) {
+          float v[8];
+          V8<LSURGE_BF16>::ld(add + t * d + (c * 64 + lane) * 8, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[c][e] += v[e];
+        }
       }
-      V8<LSURGE_BF16>::st(dx + t * d + c, acc);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) V8<LSURGE_BF16>::st(dx + t * d + (c * 64 + lane) * 8, acc[c]);
+    } else {
+      for (int64_t c = lane * 8; c < d; c += 64 * 8) {
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int j = 0; j < k; ++j) {
+          float v[8];
+          V8<LSURGE_BF16>::ld(dxp + (int64_t)slot[t * k + j] * d + c, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += v[e];
+        }
+        if (dl) {
+          for (int j = 0; j < k; ++j) {
+            const float lj = dl[t * k + j];
+            float v[8];
+            V8<LSURGE_BF16>::ld(w_rT + (int64_t)sel[t * k + j] * d + c, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] += lj * v[e];
+          }
+        }
+        if (add) {
+          float v[8];
+          V8<LSURGE_BF16>::ld(add + t * d + c, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += v[e];
+        }
+        V8<LSURGE_BF16>::st(dx + t * d + c, acc);
+      }
     }
   }
 }
@@ -393,41 +544,77 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // ------------------------------------------------------------------------------ internal launchers
 namespace lsurge {
 
+// Fixed chunk counts for the row kernels: NC = d / 512 for d in {512, 1024, 2048, 4096}, else 0 (run-time loop).
+static int row_chunks(int64_t d) {
+  return (d == 512 || d == 1024 || d == 2048 || d == 4096) ? (int)(d / 512) : 0;
+}
+#define LS_NC_SWITCH(nc, NCV, ...)                          \
+  switch (nc) {                                             \
+    case 1: { constexpr int NCV = 1; __VA_ARGS__; } break;  \
+    case 2: { constexpr int NCV = 2; __VA_ARGS__; } break;  \
+    case 4: { constexpr int NCV = 4; __VA_ARGS__; } break;  \
+    case 8: { constexpr int NCV = 8; __VA_ARGS__; } break;  \
+    default: { constexpr int NCV = 0; __VA_ARGS__; } break; \
+  }
+#define LS_KK_SWITCH(k, KKV, ...)                           \
+  switch (k) {                                              \
+    case 6: { constexpr int KKV = 6; __VA_ARGS__; } break;  \
+    case 8: { constexpr int KKV = 8; __VA_ARGS__; } break;  \
+    default: { constexpr int KKV = 0; __VA_ARGS__; } break; \
+  }
+
 int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src, const int32_t* num_blocks,
                         int64_t max_rows, void* xp, hipStream_t s) {
-  LSURGE_LAUNCH(KID_DISPATCH, s,
-                hipLaunchKernelGGL(dispatch_pad_kernel, dim3(grid_for_rows(max_rows)), dim3(PM_THREADS), 0, s,
-                                   (const bf16_t*)x, d, k, row_src, num_blocks, max_rows, (bf16_t*)xp));
+  LS_NC_SWITCH(row_chunks(d), NC,
+               LSURGE_LAUNCH(KID_DISPATCH, s,
+                             hipLaunchKernelGGL(dispatch_pad_kernel<NC>, dim3(grid_for_rows(max_rows)),
+                                                dim3(PM_THREADS), 0, s, (const bf16_t*)x, d, k, row_src, num_blocks,
+                                                max_rows, (bf16_t*)xp)));
   return LSURGE_OK;
 }
 
 int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, const float* w, int64_t n,
                        const void* add, void* out, int out_dtype, hipStream_t s) {
-  if (out_dtype == LSURGE_BF16)
-    LSURGE_LAUNCH(KID_COMBINE_FWD, s,
-                  hipLaunchKernelGGL(combine_pad_kernel<LSURGE_BF16>, dim3(grid_for_rows(n)), dim3(PM_THREADS), 0, s,
-                                     (const bf16_t*)yp, d, k, slot, w, n, (const bf16_t*)add, out));
-  else
-    LSURGE_LAUNCH(KID_COMBINE_FWD, s,
-                  hipLaunchKernelGGL(combine_pad_kernel<LSURGE_F32>, dim3(grid_for_rows(n)), dim3(PM_THREADS), 0, s,
-                                     (const bf16_t*)yp, d, k, slot, w, n, (const bf16_t*)add, out));
+  const dim3 grid(grid_for_rows(n));
+  LS_NC_SWITCH(row_chunks(d), NC, LS_KK_SWITCH(k, KK, {
+    if (out_dtype == LSURGE_BF16)
+      LSURGE_LAUNCH(KID_COMBINE_FWD, s,
+                    hipLaunchKernelGGL((combine_pad_kernel<NC, KK, LSURGE_BF16>), grid, dim3(PM_THREADS), 0, s,
+                                       (const bf16_t*)yp, d, k, slot, w, n, (const bf16_t*)add, out));
+    else
+      LSURGE_LAUNCH(KID_COMBINE_FWD, s,
+                    hipLaunchKernelGGL((combine_pad_kernel<NC, KK, LSURGE_F32>), grid, dim3(PM_THREADS), 0, s,
+                                       (const bf16_t*)yp, d, k, slot, w, n, (const bf16_t*)add, out));
+  }));
   return LSURGE_OK;
 }
 
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
                            int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s) {
+  const dim3 grid(grid_for_rows(n));
+  const int nc = row_chunks(d);
+  if (nc && (k == 6 || k == 8)) {
+    LS_NC_SWITCH(nc, NC, LS_KK_SWITCH(k, KK, {
+      if (NC && KK)
+        LSURGE_LAUNCH(KID_COMBINE_BWD, s,
+                      hipLaunchKernelGGL((combine_bwd_pad_kernel<NC ? NC : 1, KK ? KK : 1>), grid, dim3(PM_THREADS), 0,
+                                         s, (const bf16_t*)yp, slot, w, n, d, (const bf16_t*)g, (bf16_t*)dyp, dw, dl));
+    }));
+    return LSURGE_OK;
+  }
   LSURGE_LAUNCH(KID_COMBINE_BWD, s,
-                hipLaunchKernelGGL((combine_bwd_kernel<LSURGE_BF16, LSURGE_BF16, true>), dim3(grid_for_rows(n)),
-                                   dim3(PM_THREADS), 0, s, yp, rows, slot, w, n, k, d, g, dyp, dw, dl));
+                hipLaunchKernelGGL((combine_bwd_kernel<LSURGE_BF16, LSURGE_BF16, true>), grid, dim3(PM_THREADS), 0, s,
+                                   yp, rows, slot, w, n, k, d, g, dyp, dw, dl));
   return LSURGE_OK;
 }
 
 int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* slot, int64_t n, const float* dl,
                             const int32_t* sel, const void* w_rT, const void* add, void* dx, hipStream_t s) {
-  LSURGE_LAUNCH(KID_DISPATCH_BWD, s,
-                hipLaunchKernelGGL(dispatch_bwd_pad_kernel, dim3(grid_for_rows(n)), dim3(PM_THREADS), 0, s,
-                                   (const bf16_t*)dxp, d, k, slot, n, dl, sel, (const bf16_t*)w_rT,
-                                   (const bf16_t*)add, (bf16_t*)dx));
+  LS_NC_SWITCH(row_chunks(d), NC, LS_KK_SWITCH(k, KK,
+               LSURGE_LAUNCH(KID_DISPATCH_BWD, s,
+                             hipLaunchKernelGGL((dispatch_bwd_pad_kernel<NC, KK>), dim3(grid_for_rows(n)),
+                                                dim3(PM_THREADS), 0, s, (const bf16_t*)dxp, d, k, slot, n, dl, sel,
+                                                (const bf16_t*)w_rT, (const bf16_t*)add, (bf16_t*)dx))));
   return LSURGE_OK;
 }
 

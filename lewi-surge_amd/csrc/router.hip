@@ -2,18 +2,26 @@
 //
 // Stands in for MaxText RoutedMoE's gate + top-k (third-party; configured by configs/stage1.yml:34-37 of the
 // reference).  Logit order contract: logits[t,e] = (((x[t,0]w[0,e]) + x[t,1]w[1,e]) + ...) in f32, then
-// + bias[e].  bf16 x bf16 products are exact in f32, so this is reproducible bit for bit on the CPU.
+// + bias[e].  bf16 x bf16 products are exact in f32, so fused multiply-add and the CPU's separate multiply and
+// add give the same bits: the result is reproducible bit for bit on the CPU whatever the thread mapping.
+//
+// Two paths.  With a logits buffer: a logits kernel over (token block, expert block) tiles and a selection
+// kernel with one wave per token (below).  Without one, the fused kernel: one workgroup of 128 threads owns 64
+// tokens and all experts.  Thread (tq, eq) accumulates 4 tokens x EPT
+// experts in registers; per d it reads one f32x4 of x (4 tokens) and EPT/4 f32x4 of w from LDS, so the loop is
+// FMA-bound (32 FMAs per 3 LDS reads at E = 64).  The selection then runs one wave per token over the logits
+// left in LDS.
 #include "common.h"
 
 namespace {
 
-constexpr int RT_TOK = 32;      // tokens per workgroup
-constexpr int RT_DC = 64;       // d chunk staged in LDS
-constexpr int RT_THREADS = 256;
+constexpr int RT_TOK = 64;       // tokens per workgroup
+constexpr int RT_DC = 32;        // d chunk staged in LDS
+constexpr int RT_THREADS = 128;  // 16 token quads x 8 expert groups
 constexpr int RT_EMAX = 256;
 
-// LDS: x chunk transposed [RT_DC][RT_TOK] f32 (8 KB) + w chunk [RT_DC][EP] f32 (<= 64 KB).
-// After the d loop the w region is reused for the [RT_TOK][EP] logits.
+// LDS: x chunk transposed [RT_DC][RT_TOK] f32 (8 KB) + w chunk [RT_DC][EP] f32 (<= 32 KB).  After the d loop
+// the w region holds the [RT_TOK][EP] logits (<= 64 KB, sized for that).
 template <int EP>  // experts padded to a multiple of 32
 __global__ __launch_bounds__(RT_THREADS) void router_topk_kernel(const bf16_t* __restrict__ x,
                                                                  const bf16_t* __restrict__ w,
@@ -21,56 +29,69 @@ __global__ __launch_bounds__(RT_THREADS) void router_topk_kernel(const bf16_t* _
                                                                  int E, int k, float* __restrict__ logits,
                                                                  int32_t* __restrict__ sel,
                                                                  float* __restrict__ weights) {
-  constexpr int EJ = EP / 32;  // experts per thread
-  __shared__ float xs[RT_DC][RT_TOK];
-  __shared__ float ws[RT_DC * EP > RT_TOK * EP ? RT_DC * EP : RT_TOK * EP];
+  constexpr int EPT = EP / 8;  // experts per thread (contiguous)
+  __shared__ __attribute__((aligned(16))) float xs[RT_DC][RT_TOK];
+  __shared__ __attribute__((aligned(16))) float ws[RT_TOK * EP > RT_DC * EP ? RT_TOK * EP : RT_DC * EP];
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * RT_TOK;
-  const int q = tid & 7;    // token quad: tokens 4q..4q+3
-  const int s = tid >> 3;   // expert slice: experts s + 32 j
-  float acc[4][EJ];
+  const int eq = tid & 7;   // expert group: experts eq*EPT .. eq*EPT + EPT - 1
+  const int tq = tid >> 3;  // token quad: tokens 4tq .. 4tq+3
+  float acc[4][EPT];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int j = 0; j < EJ; ++j) acc[a][j] = 0.f;
+    for (int j = 0; j < EPT; ++j) acc[a][j] = 0.f;
 
   for (int d0 = 0; d0 < d; d0 += RT_DC) {
     const int dc = min(RT_DC, d - d0);
-    // stage x[t0 .. t0+32, d0 .. d0+dc) transposed, as f32 (zeros past T / d)
-    for (int i = tid; i < RT_TOK * RT_DC; i += RT_THREADS) {
-      const int tt = i / RT_DC, dd = i % RT_DC;
+    // x[t0 .. t0+64, d0 .. d0+32): 8-element chunks (16 B), stored transposed as f32 (zeros past T / d)
+    for (int c = tid; c < RT_TOK * RT_DC / 8; c += RT_THREADS) {
+      const int tt = c / (RT_DC / 8), dd0 = (c % (RT_DC / 8)) * 8;
       const int t = t0 + tt;
-      xs[dd][tt] = (t < T && dd < dc) ? bf16_to_f32(x[(int64_t)t * d + d0 + dd]) : 0.f;
+      float v[8];
+      if (t < T && dd0 + 8 <= dc && (d & 7) == 0) {
+        const u32x4 u = *reinterpret_cast<const u32x4*>(x + (int64_t)t * d + d0 + dd0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = __uint_as_float(u[i] << 16);
+          v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[i] = (t < T && dd0 + i < dc) ? bf16_to_f32(x[(int64_t)t * d + d0 + dd0 + i]) : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xs[dd0 + i][tt] = v[i];
     }
-    // stage w[d0 .. d0+dc, 0 .. E) as f32, experts padded with zeros
+    // w[d0 .. d0+32, 0 .. E) as f32, experts padded with zeros
     for (int i = tid; i < RT_DC * EP; i += RT_THREADS) {
       const int dd = i / EP, e = i % EP;
       ws[i] = (dd < dc && e < E) ? bf16_to_f32(w[(int64_t)(d0 + dd) * E + e]) : 0.f;
     }
     __syncthreads();
     for (int dd = 0; dd < dc; ++dd) {
-      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[dd][4 * q]);
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[dd][4 * tq]);
 #pragma unroll
-      for (int j = 0; j < EJ; ++j) {
-        const float wv = ws[dd * EP + s + 32 * j];
-        // exact products; one f32 rounding per add, ascending d
-        acc[0][j] = acc[0][j] + xv[0] * wv;
-        acc[1][j] = acc[1][j] + xv[1] * wv;
-        acc[2][j] = acc[2][j] + xv[2] * wv;
-        acc[3][j] = acc[3][j] + xv[3] * wv;
+      for (int c = 0; c < EPT / 4; ++c) {
+        const f32x4 wv = *reinterpret_cast<const f32x4*>(&ws[dd * EP + eq * EPT + 4 * c]);
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[a][4 * c + i] = __builtin_fmaf(xv[a], wv[i], acc[a][4 * c + i]);
       }
     }
     __syncthreads();
   }
-  // logits -> LDS [RT_TOK][EP] and global
+  // logits (+ bias) -> LDS [RT_TOK][EP] and global
   float* ls = ws;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
-    const int tt = 4 * q + a;
+    const int tt = 4 * tq + a;
     const int t = t0 + tt;
 #pragma unroll
-    for (int j = 0; j < EJ; ++j) {
-      const int e = s + 32 * j;
+    for (int j = 0; j < EPT; ++j) {
+      const int e = eq * EPT + j;
       float v = acc[a][j];
       if (e < E && bias) v = v + bias[e];
       ls[tt * EP + e] = (e < E) ? v : -INFINITY;
@@ -78,7 +99,7 @@ __global__ __launch_bounds__(RT_THREADS) void router_topk_kernel(const bf16_t* _
     }
   }
   __syncthreads();
-  // top-k: one wave per token, 8 tokens per wave
+  // top-k: one wave per token
   const int lane = tid & 63, wv = tid >> 6;
   for (int tt = wv; tt < RT_TOK; tt += RT_THREADS / 64) {
     const int t = t0 + tt;
@@ -93,8 +114,6 @@ __global__ __launch_bounds__(RT_THREADS) void router_topk_kernel(const bf16_t* _
       taken[c] = !(e < E);
     }
     float top0 = 0.f, denom = 0.f;
-    float selv[8];
-    int seli[8];
     for (int j = 0; j < k; ++j) {
       // lane-local best (lowest index wins ties: c ascending, strict >)
       float bv = -INFINITY;
@@ -120,10 +139,6 @@ __global__ __launch_bounds__(RT_THREADS) void router_topk_kernel(const bf16_t* _
 #pragma unroll
       for (int c = 0; c < EC; ++c)
         if (lane + 64 * c == bi) taken[c] = true;
-      if (j < 8) {
-        selv[j] = bv;
-        seli[j] = bi;
-      }
       if (j == 0) top0 = bv;
       const float z = __expf(bv - top0);
       denom += z;
@@ -136,9 +151,141 @@ __global__ __launch_bounds__(RT_THREADS) void router_topk_kernel(const bf16_t* _
       const float inv = 1.f / denom;
       for (int j = 0; j < k; ++j) weights[(int64_t)t * k + j] *= inv;
     }
-    (void)selv;
-    (void)seli;
   }
+}
+
+// ---------------------------------------------------------------------------------------------- split path
+// Logits kernel: workgroup = 64 tokens x 32 experts (256 threads, 4 tokens x 2 experts each), grid over token
+// blocks x expert blocks, so there are enough waves to fill every SIMD; the d loop is the same sequential
+// f32 sum as above.  The top-k then runs as its own kernel, one wave per token, over the logits in HBM.
+constexpr int RL_TOK = 64, RL_EXP = 32, RL_DC = 64, RL_THREADS = 256;
+
+__global__ __launch_bounds__(RL_THREADS) void router_logits_kernel(const bf16_t* __restrict__ x,
+                                                                   const bf16_t* __restrict__ w,
+                                                                   const float* __restrict__ bias, int T, int d,
+                                                                   int E, float* __restrict__ logits) {
+  __shared__ __attribute__((aligned(16))) float xs[RL_DC][RL_TOK];
+  __shared__ __attribute__((aligned(16))) float ws[RL_DC][RL_EXP];
+  const int tid = threadIdx.x;
+  const int t0 = blockIdx.x * RL_TOK, e0 = blockIdx.y * RL_EXP;
+  const int ep = tid & 15;   // experts e0 + 2 ep, e0 + 2 ep + 1
+  const int tq = tid >> 4;   // tokens t0 + 4 tq .. + 3
+  float acc[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+  const bool vec = (d & 7) == 0 && (E & 7) == 0;
+  for (int d0 = 0; d0 < d; d0 += RL_DC) {
+    const int dc = min(RL_DC, d - d0);
+    // x: 64 tokens x 64 d as 16-byte chunks (2 per thread), stored transposed as f32
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int c = tid + RL_THREADS * r;
+      const int tt = c >> 3, dd0 = (c & 7) * 8;
+      const int t = t0 + tt;
+      float v[8];
+      if (vec && t < T && dd0 + 8 <= dc) {
+        const u32x4 u = *reinterpret_cast<const u32x4*>(x + (int64_t)t * d + d0 + dd0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = __uint_as_float(u[i] << 16);
+          v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[i] = (t < T && dd0 + i < dc) ? bf16_to_f32(x[(int64_t)t * d + d0 + dd0 + i]) : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xs[dd0 + i][tt] = v[i];
+    }
+    // w: 64 d x 32 experts as 16-byte chunks (8 experts, 1 per thread)
+    {
+      const int dd = tid >> 2, ec = (tid & 3) * 8;
+      float v[8];
+      if (vec && dd < dc && e0 + ec + 8 <= E) {
+        const u32x4 u = *reinterpret_cast<const u32x4*>(w + (int64_t)(d0 + dd) * E + e0 + ec);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[2 * i] = __uint_as_float(u[i] << 16);
+          v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[i] = (dd < dc && e0 + ec + i < E) ? bf16_to_f32(w[(int64_t)(d0 + dd) * E + e0 + ec + i]) : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ws[dd][ec + i] = v[i];
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int dd = 0; dd < dc; ++dd) {
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[dd][4 * tq]);
+      const float w0 = ws[dd][2 * ep], w1 = ws[dd][2 * ep + 1];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        acc[a][0] = __builtin_fmaf(xv[a], w0, acc[a][0]);
+        acc[a][1] = __builtin_fmaf(xv[a], w1, acc[a][1]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int t = t0 + 4 * tq + a;
+    if (t >= T) continue;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = e0 + 2 * ep + j;
+      if (e < E) logits[(int64_t)t * E + e] = bias ? acc[a][j] + bias[e] : acc[a][j];
+    }
+  }
+}
+
+// one wave per token: top-k (larger logit first, ties to the lower expert index), softmax over the k
+template <int EC>  // logits per lane: E <= 64 EC
+__global__ __launch_bounds__(256) void router_select_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                            int32_t* __restrict__ sel, float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float v[EC];
+  bool taken[EC];
+#pragma unroll
+  for (int c = 0; c < EC; ++c) {
+    const int e = lane + 64 * c;
+    v[c] = (e < E) ? logits[(int64_t)t * E + e] : -INFINITY;
+    taken[c] = !(e < E);
+  }
+  float top0 = 0.f, denom = 0.f, mine = 0.f;
+  for (int j = 0; j < k; ++j) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int c = 0; c < EC; ++c) {
+      const int e = lane + 64 * c;
+      if (!taken[c] && (bi == 0x7fffffff || v[c] > bv)) {
+        bv = v[c];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < EC; ++c)
+      if (lane + 64 * c == bi) taken[c] = true;
+    if (j == 0) top0 = bv;
+    const float z = __expf(bv - top0);
+    denom += z;
+    if (lane == j) mine = z;
+    if (lane == 0) sel[(int64_t)t * k + j] = bi;
+  }
+  if (lane < k) weights[(int64_t)t * k + lane] = mine / denom;
 }
 
 }  // namespace
@@ -151,8 +298,24 @@ extern "C" int lsurge_router_topk(const void* x, const void* w_r, const float* b
                  (long long)t, (long long)d, (long long)e, (long long)k);
   LSURGE_REQUIRE(t < (1ll << 31) && t * d < (1ll << 40), "router_topk: too large");
   if (t == 0) return LSURGE_OK;
-  dim3 grid((unsigned)((t + RT_TOK - 1) / RT_TOK)), block(RT_THREADS);
   hipStream_t s = (hipStream_t)stream;
+  if (logits && k <= 64) {  // split path: logits kernel over (token, expert) blocks, then one wave per token
+    const dim3 lg((unsigned)((t + RL_TOK - 1) / RL_TOK), (unsigned)((e + RL_EXP - 1) / RL_EXP));
+    LSURGE_LAUNCH(KID_ROUTER, s,
+                  hipLaunchKernelGGL(router_logits_kernel, lg, dim3(RL_THREADS), 0, s, (const bf16_t*)x,
+                                     (const bf16_t*)w_r, bias, (int)t, (int)d, (int)e, logits));
+    const dim3 sg((unsigned)((t + 3) / 4));
+#define RS_CASE(EC)                                                                                        \
+  LSURGE_LAUNCH(KID_ROUTER_SELECT, s,                                                                      \
+                hipLaunchKernelGGL(router_select_kernel<EC>, sg, dim3(256), 0, s, logits, (int)t, (int)e, (int)k, sel, \
+                                   weights))
+    if (e <= 64) RS_CASE(1);
+    else if (e <= 128) RS_CASE(2);
+    else RS_CASE(4);
+#undef RS_CASE
+    return LSURGE_OK;
+  }
+  dim3 grid((unsigned)((t + RT_TOK - 1) / RT_TOK)), block(RT_THREADS);
   const bf16_t* xb = (const bf16_t*)x;
   const bf16_t* wb = (const bf16_t*)w_r;
 #define RT_CASE(EP)                                                                                       \
