@@ -7,9 +7,11 @@ expert blocks, gate/up GEMM + SiLU*mul, down GEMM, combine + shared expert; back
 dW_r) over T tokens of synthetic bf16 input already resident in HBM.  Prints one JSON line.
 
 roofline: the dominant kernel (largest share of the step, found with HIP events on the launch stream in a short
-profiled pass) is bracketed by a pair of HIP events in every timed step; achieved = algorithmic flops (or bytes)
-per launch / its mean event-timed duration.  cpu_baseline: the numpy CPU oracle's float32 layer forward +
-backward on a bounded token sample of the same layer, timed on this host.
+profiled pass that runs every kernel on one stream) is bracketed by a pair of HIP events in every timed step;
+achieved = algorithmic flops (or bytes) per launch / its mean event-timed duration.  The timed region runs the
+layer's independent chains on helper streams (--concurrency 1, the default; lsurge_set_concurrency).
+cpu_baseline: the numpy CPU oracle's float32 layer forward + backward on a bounded token sample of the same
+layer, timed on this host.
 """
 from __future__ import annotations
 
@@ -150,6 +152,9 @@ def main():
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")
+    ap.add_argument("--concurrency", type=int, default=1,
+                    help="timed region: 1 runs the layer's independent chains on helper streams "
+                         "(lsurge_set_concurrency), 0 everything on one stream")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against a known byte count) and exit")
@@ -177,6 +182,7 @@ def main():
     c = CONFIGS[a.config]
     dev = torch.device("cuda", 0)
     lib = _lib.lib()
+    lib.lsurge_set_concurrency(0)
     p, dy = make_params(c, dev)
     layer = MoELayer(MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"]), dev)
     grads = layer.alloc_grads() if c["bwd"] else None
@@ -190,7 +196,8 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    # profiled pass: every kernel bracketed, to find the dominant one
+    # profiled pass (one stream, so every kernel's time is its own): every kernel bracketed, to find the
+    # dominant one and fill the per-kernel table
     lib.lsurge_prof_reset()
     lib.lsurge_prof_enable(-1)
     nprof = 3
@@ -205,6 +212,9 @@ def main():
     names = [lib.lsurge_prof_kernel_name(i).decode() for i in range(lib.lsurge_prof_kernel_count())]
 
     # timed region: K steps, only the dominant kernel bracketed by events on its launch stream
+    lib.lsurge_set_concurrency(a.concurrency)
+    for _ in range(2):  # settle the helper streams
+        step()
     lib.lsurge_prof_reset()
     lib.lsurge_prof_enable(1 << names.index(dom))
     torch.cuda.synchronize()
@@ -225,8 +235,9 @@ def main():
 
     ms = el / a.steps * 1e3
     tokens_s = c["T"] * a.steps / el
-    kern = {n: dict(ms=round(v[0], 4), share=round(v[2] / ms, 4)) for n, v in sorted(table.items(),
-                                                                                     key=lambda kv: -kv[1][2])}
+    serial_ms = sum(v[2] for v in table.values())
+    kern = {n: dict(ms=round(v[0], 4), share=round(v[2] / serial_ms, 4)) for n, v in sorted(table.items(),
+                                                                                          key=lambda kv: -kv[1][2])}
     for n, v in kern.items():
         if n in work:
             b, amt = work[n]
@@ -252,12 +263,15 @@ def main():
         "config": {"workload": f"{a.config}: MoE layer {'fwd+bwd' if c['bwd'] else 'fwd'} T={c['T']} d={c['d']} "
                                f"E={c['E']}x{c['f']} top-{c['k']} shared={c['fs']}" + (" zipf-bias" if c["zipf"] else ""),
                    "T": c["T"], "d_model": c["d"], "experts": c["E"], "top_k": c["k"], "expert_ffn": c["f"],
-                   "shared_ffn": c["fs"], "block_rows": 128, "parallelism": "single GPU"},
+                   "shared_ffn": c["fs"], "block_rows": 128, "parallelism": "single GPU",
+                   "concurrent_streams": bool(a.concurrency)},
         "layer_tflops": round(layer_flops(c) / (ms * 1e-3) / 1e12, 1),
         "mfu": round(layer_flops(c) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4), "traffic": None, "launch_ms": round(dom_ms, 4)},
         "kernels": kern,
+        "kernels_note": "per-kernel ms from a profiled pass on one stream (share of that pass's kernel time); "
+                        "the timed region runs with concurrent_streams",
     }
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(c)

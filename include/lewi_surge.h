@@ -44,6 +44,14 @@ enum {
 int lsurge_abi_version(void);
 const char* lsurge_last_error(void);
 
+/* Run the independent chains of lsurge_moe_fwd / lsurge_moe_bwd (shared expert, weight gradients, router
+ * backward) on helper streams of the current device that fork from and join back into the caller's stream
+ * (on = 1), or everything on the caller's stream (on = 0, the default).  Either way a call is stream-ordered
+ * on its stream and never synchronises the host.  Process-wide setting.  No reference counterpart: the
+ * reference's XLA program is scheduled by XLA. */
+int lsurge_set_concurrency(int on);
+int lsurge_get_concurrency(void);
+
 /* ------------------------------------------------------------------------------------------------
  * Row movement (memory-bound).
  * ------------------------------------------------------------------------------------------------ */

@@ -3,6 +3,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -70,6 +71,71 @@ hipError_t prof_mark_end(int kid, hipStream_t s) {
   return hipEventRecord(g_pool[i].b, s);
 }
 
+// ------------------------------------------------------------------------------ helper streams
+// The layer entry points run independent kernel chains (shared expert, weight gradients, router backward) on
+// helper streams that fork from and join back into the caller's stream through events, so each call stays
+// stream-ordered with respect to that stream and never synchronises the host.  One set per device, created
+// on first use (default priority); calls that overlap on one device serialise their enqueueing on its mutex.
+namespace {
+struct DeviceFork {
+  std::mutex mu;
+  bool ready = false;
+  hipStream_t side[kForkStreams];
+  hipEvent_t ev[kForkEvents];
+};
+constexpr int kMaxDevices = 64;
+DeviceFork g_fork[kMaxDevices];
+}  // namespace
+
+static std::atomic<int> g_concurrency{0};
+
+int fork_acquire(ForkSet* f, hipStream_t main) {
+  if (!g_concurrency.load(std::memory_order_relaxed)) {  // serial: every chain on the caller's stream
+    for (int i = 0; i < kForkStreams; ++i) f->side[i] = main;
+    f->dev = -1;
+    return LSURGE_OK;
+  }
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(LSURGE_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(LSURGE_ERR_INVALID, "device %d out of range", dev);
+  DeviceFork& d = g_fork[dev];
+  d.mu.lock();
+  if (!d.ready) {
+    for (int i = 0; i < kForkStreams; ++i) {
+      e = hipStreamCreateWithFlags(&d.side[i], hipStreamNonBlocking);
+      if (e != hipSuccess) {
+        d.mu.unlock();
+        return set_error(LSURGE_ERR_LAUNCH, "hipStreamCreateWithFlags: %s", hipGetErrorString(e));
+      }
+    }
+    for (int i = 0; i < kForkEvents; ++i) {
+      e = hipEventCreateWithFlags(&d.ev[i], hipEventDisableTiming);
+      if (e != hipSuccess) {
+        d.mu.unlock();
+        return set_error(LSURGE_ERR_LAUNCH, "hipEventCreateWithFlags: %s", hipGetErrorString(e));
+      }
+    }
+    d.ready = true;
+  }
+  for (int i = 0; i < kForkStreams; ++i) f->side[i] = d.side[i];
+  for (int i = 0; i < kForkEvents; ++i) f->ev[i] = d.ev[i];
+  f->dev = dev;
+  return LSURGE_OK;
+}
+
+void fork_release(ForkSet* f) {
+  if (f->dev >= 0) g_fork[f->dev].mu.unlock();
+}
+
+int stream_after(hipStream_t waiter, hipStream_t producer, hipEvent_t ev) {
+  if (waiter == producer) return LSURGE_OK;
+  hipError_t e = hipEventRecord(ev, producer);
+  if (e == hipSuccess) e = hipStreamWaitEvent(waiter, ev, 0);
+  if (e != hipSuccess) return set_error(LSURGE_ERR_LAUNCH, "stream join: %s", hipGetErrorString(e));
+  return LSURGE_OK;
+}
+
 }  // namespace lsurge
 
 using namespace lsurge;
@@ -77,6 +143,12 @@ using namespace lsurge;
 extern "C" {
 
 int lsurge_abi_version(void) { return LSURGE_ABI_VERSION; }
+
+int lsurge_set_concurrency(int on) {
+  g_concurrency.store(on ? 1 : 0);
+  return LSURGE_OK;
+}
+int lsurge_get_concurrency(void) { return g_concurrency.load(); }
 const char* lsurge_last_error(void) { return g_err; }
 
 int lsurge_prof_kernel_count(void) { return KID_COUNT; }

@@ -62,6 +62,19 @@ __device__ __forceinline__ float wave_sum(float v) {
 namespace lsurge {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+
+// helper streams of the current device (see abi.cpp); fork_acquire locks the device's set until fork_release.
+// With concurrency off (the default) every helper is the caller's stream and nothing is locked.
+constexpr int kForkStreams = 3, kForkEvents = 12;
+struct ForkSet {
+  hipStream_t side[kForkStreams];
+  hipEvent_t ev[kForkEvents];
+  int dev;
+};
+int fork_acquire(ForkSet* f, hipStream_t main);
+void fork_release(ForkSet* f);
+// enqueue on `waiter` a wait for everything enqueued so far on `producer`
+int stream_after(hipStream_t waiter, hipStream_t producer, hipEvent_t ev);
 hipError_t prof_mark_begin(int kernel_id, hipStream_t s);
 hipError_t prof_mark_end(int kernel_id, hipStream_t s);
 }  // namespace lsurge

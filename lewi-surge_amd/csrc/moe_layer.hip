@@ -131,8 +131,10 @@ struct BwdWs {
   bf16_t *dy_pad, *dgu, *dx_pad, *sdgu, *sdx, *dlog, *w_rT;
   float* dl;
   float* dweights;
-  void* part;
+  void* part;         // split-K partials of the shared-expert weight gradients (their own stream)
   size_t part_bytes;
+  void* part_r;       // split-K partials of the router weight gradient (another stream)
+  size_t part_r_bytes;
 };
 
 size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
@@ -151,9 +153,10 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
     part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, 2 * q.fs, dense_splits(q.T, q.d, 2 * q.fs)));
     part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.fs, q.d, dense_splits(q.T, q.fs, q.d)));
   }
-  part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, q.E, dense_splits(q.T, q.d, q.E)));
   w->part_bytes = part;
   w->part = c.take<char>(part);
+  w->part_r_bytes = lsurge::wgrad_workspace_bytes(1, q.d, q.E, dense_splits(q.T, q.d, q.E));
+  w->part_r = c.take<char>(w->part_r_bytes);
   return c.off + 256;
 }
 
@@ -205,6 +208,28 @@ int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_s
   return LSURGE_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// holds a device's helper streams for the duration of one layer call
+struct ForkGuard {
+  lsurge::ForkSet f;
+  bool held = false;
+  int acquire(hipStream_t main) {
+    const int rc = lsurge::fork_acquire(&f, main);
+    held = rc == LSURGE_OK;
+    return rc;
+  }
+  ~ForkGuard() {
+    if (held) lsurge::fork_release(&f);
+  }
+};
+}  // namespace
+
+extern "C" {
+
+// Forward.  Stream plan: the shared expert (dense, depends on x only) runs on a helper stream while the routed
+// chain (router -> layout -> dispatch -> gate/up -> down) runs on the caller's stream; the combine joins both.
 int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* out, void* saved, size_t saved_bytes,
                    void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
   if (int rc = check_shape(s)) return rc;
@@ -216,7 +241,20 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   LSURGE_REQUIRE(saved_bytes >= need, "moe_fwd: saved buffer %zu < %zu bytes", saved_bytes, need);
   carve_saved(q, saved, &sv);
   hipStream_t st = (hipStream_t)stream;
+  ForkGuard fg;
+  if (int rc = fg.acquire(st)) return rc;
+  hipStream_t s0 = fg.f.side[0];
 
+  if (q.fs) {
+    if (int rc = lsurge::stream_after(s0, st, fg.f.ev[0])) return rc;
+    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
+    if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
+                                              q.fs, sv.sh, sv.sg, sv.su, q.fs, s0))
+      return rc;
+    if (int rc = lsurge::gemm_rows_kn(KID_SHARED_DOWN_FWD, dense, sv.sh, q.fs, p->ws_down, q.d, 0, q.fs, q.d, sv.sy, q.d,
+                                      s0))
+      return rc;
+  }
   if (int rc = lsurge_router_topk(p->x, p->w_r, p->bias, q.T, q.d, q.E, q.k, sv.logits, sv.sel, sv.weights, stream))
     return rc;
   if (int rc = lsurge::build_layout_impl(sv.sel, q.M, q.E, sv.gs, sv.offsets, sv.block_off, sv.order, sv.pos, sv.slot,
@@ -231,19 +269,17 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   if (int rc = lsurge::gemm_rows_kn(KID_GEMM_DOWN_FWD, blocks, sv.h, q.f, p->w_down, q.d, q.f * q.d, q.f, q.d, sv.y_pad,
                                     q.d, st))
     return rc;
-  if (q.fs) {
-    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
-    if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
-                                              q.fs, sv.sh, sv.sg, sv.su, q.fs, st))
-      return rc;
-    if (int rc = lsurge::gemm_rows_kn(KID_SHARED_DOWN_FWD, dense, sv.sh, q.fs, p->ws_down, q.d, 0, q.fs, q.d, sv.sy, q.d,
-                                      st))
-      return rc;
-  }
+  if (q.fs)
+    if (int rc = lsurge::stream_after(st, s0, fg.f.ev[1])) return rc;
   return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sv.sy : nullptr, out,
                                     LSURGE_BF16, st);
 }
 
+// Backward.  Stream plan (caller's stream = critical path):
+//   main:  combine bwd -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd
+//   s0:    shared expert: down dgrad, down wgrad, gate/up dgrad, gate/up wgrad   (needs dy only)
+//   s1:    W_r transpose; after combine bwd: down wgrad, d(logits) scatter, router wgrad
+//   s2:    after down dgrad: gate/up wgrad
 int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* dy, const void* saved,
                    const lsurge_moe_grads* g, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
   if (int rc = check_shape(s)) return rc;
@@ -261,53 +297,69 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   hipStream_t st = (hipStream_t)stream;
   float* dweights = g->dweights ? g->dweights : w.dweights;
   const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+  ForkGuard fg;
+  if (int rc = fg.acquire(st)) return rc;
+  hipStream_t s0 = fg.f.side[0], s1 = fg.f.side[1], s2 = fg.f.side[2];
+  hipEvent_t* ev = fg.f.ev;
 
-  // combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel)
-  if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, q.P, sv.slot, sv.weights, q.T, (int)q.k, q.d, dy, w.dy_pad, dweights,
-                                              w.dl, st))
-    return rc;
-  // down dgrad + SwiGLU backward: dH = dY W_down^T -> [dG | dU]
-  if (int rc = lsurge::gemm_rows_nk(KID_GEMM_DOWN_DGRAD, blocks, w.dy_pad, q.d, p->w_down, nullptr, 0, q.d, q.f * q.d,
-                                    q.d, q.f, w.dgu, 2 * q.f, true, sv.g, sv.u, q.f, st))
-    return rc;
-  // down wgrad: dW_down[e] = h_e^T dY_e
-  if (int rc = lsurge::gemm_wgrad(KID_GEMM_DOWN_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, sv.h, q.f, w.dy_pad, q.d,
-                                  q.f, q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, 1, nullptr, 0, st))
-    return rc;
-  // gate/up dgrad: dX_pad = dG W_gate^T + dU W_up^T
-  if (int rc = lsurge::gemm_rows_nk(KID_GEMM_GU_DGRAD, blocks, w.dgu, 2 * q.f, p->w_gate, p->w_up, q.f, q.f, q.d * q.f,
-                                    2 * q.f, q.d, w.dx_pad, q.d, false, nullptr, nullptr, 0, st))
-    return rc;
-  // gate/up wgrad: [dW_gate | dW_up][e] = x_e^T [dG | dU]_e
-  if (int rc = lsurge::gemm_wgrad(KID_GEMM_GU_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, sv.x_pad, q.d, w.dgu,
-                                  2 * q.f, q.d, 2 * q.f, g->dw_gate, g->dw_up, q.f, q.f, q.d * q.f, 1, nullptr, 0, st))
-    return rc;
+  // fork: the helper streams start after everything the caller enqueued before this call
+  if (int rc = lsurge::stream_after(s0, st, ev[0])) return rc;
+  if (int rc = lsurge::stream_after(s1, st, ev[1])) return rc;
+
+  // s0: shared expert backward
   if (q.fs) {
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
     if (int rc = lsurge::gemm_rows_nk(KID_SHARED_DOWN_DGRAD, dense, dy, q.d, p->ws_down, nullptr, 0, q.d, 0, q.d, q.fs,
-                                      w.sdgu, 2 * q.fs, true, sv.sg, sv.su, q.fs, st))
+                                      w.sdgu, 2 * q.fs, true, sv.sg, sv.su, q.fs, s0))
       return rc;
     int S = dense_splits(q.T, q.fs, q.d);
-    if (int rc = lsurge::gemm_wgrad(KID_SHARED_DOWN_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, sv.sh, q.fs, dy, q.d, q.fs, q.d,
-                                    g->dws_down, nullptr, 0, q.d, 0, S, w.part, w.part_bytes, st))
+    if (int rc = lsurge::gemm_wgrad(KID_SHARED_DOWN_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, sv.sh, q.fs, dy, q.d, q.fs,
+                                    q.d, g->dws_down, nullptr, 0, q.d, 0, S, w.part, w.part_bytes, s0))
       return rc;
     if (int rc = lsurge::gemm_rows_nk(KID_SHARED_GU_DGRAD, dense, w.sdgu, 2 * q.fs, p->ws_gate, p->ws_up, q.fs, q.fs, 0,
-                                      2 * q.fs, q.d, w.sdx, q.d, false, nullptr, nullptr, 0, st))
+                                      2 * q.fs, q.d, w.sdx, q.d, false, nullptr, nullptr, 0, s0))
       return rc;
     S = dense_splits(q.T, q.d, 2 * q.fs);
-    if (int rc = lsurge::gemm_wgrad(KID_SHARED_GU_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.sdgu, 2 * q.fs, q.d,
-                                    2 * q.fs, g->dws_gate, g->dws_up, q.fs, q.fs, 0, S, w.part, w.part_bytes, st))
+    if (int rc = lsurge::gemm_wgrad(KID_SHARED_GU_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.sdgu, 2 * q.fs,
+                                    q.d, 2 * q.fs, g->dws_gate, g->dws_up, q.fs, q.fs, 0, S, w.part, w.part_bytes, s0))
       return rc;
   }
-  // router: dW_r = x^T dlogits (bf16 MFMA over the dense [T, E] dlogits), dx += dlogits W_r^T in dispatch bwd
-  if (int rc = lsurge::launch_scatter_dlogits(w.dl, sv.sel, q.T, (int)q.E, (int)q.k, w.dlog, st)) return rc;
+  // s1: W_r^T for the router's dx term (independent of everything else)
+  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, s1)) return rc;
+
+  // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel)
+  if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, q.P, sv.slot, sv.weights, q.T, (int)q.k, q.d, dy, w.dy_pad,
+                                              dweights, w.dl, st))
+    return rc;
+  if (int rc = lsurge::stream_after(s1, st, ev[2])) return rc;
+  // s1: down wgrad dW_down[e] = h_e^T dY_e; router: dW_r = x^T dlogits (bf16 MFMA over the dense [T, E] dlogits)
+  if (int rc = lsurge::gemm_wgrad(KID_GEMM_DOWN_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, sv.h, q.f, w.dy_pad,
+                                  q.d, q.f, q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, 1, nullptr, 0, s1))
+    return rc;
+  if (int rc = lsurge::launch_scatter_dlogits(w.dl, sv.sel, q.T, (int)q.E, (int)q.k, w.dlog, s1)) return rc;
   {
     const int S = dense_splits(q.T, q.d, q.E);
-    if (int rc = lsurge::gemm_wgrad(KID_ROUTER_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.dlog, q.E, q.d, q.E,
-                                    g->dw_r, nullptr, 0, q.E, 0, S, w.part, w.part_bytes, st))
+    if (int rc = lsurge::gemm_wgrad(KID_ROUTER_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.dlog, q.E, q.d,
+                                    q.E, g->dw_r, nullptr, 0, q.E, 0, S, w.part_r, w.part_r_bytes, s1))
       return rc;
   }
-  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, st)) return rc;
+  // main: down dgrad + SwiGLU backward: dH = dY W_down^T -> [dG | dU]
+  if (int rc = lsurge::gemm_rows_nk(KID_GEMM_DOWN_DGRAD, blocks, w.dy_pad, q.d, p->w_down, nullptr, 0, q.d, q.f * q.d,
+                                    q.d, q.f, w.dgu, 2 * q.f, true, sv.g, sv.u, q.f, st))
+    return rc;
+  if (int rc = lsurge::stream_after(s2, st, ev[3])) return rc;
+  // s2: gate/up wgrad: [dW_gate | dW_up][e] = x_e^T [dG | dU]_e
+  if (int rc = lsurge::gemm_wgrad(KID_GEMM_GU_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, sv.x_pad, q.d, w.dgu,
+                                  2 * q.f, q.d, 2 * q.f, g->dw_gate, g->dw_up, q.f, q.f, q.d * q.f, 1, nullptr, 0, s2))
+    return rc;
+  // main: gate/up dgrad: dX_pad = dG W_gate^T + dU W_up^T
+  if (int rc = lsurge::gemm_rows_nk(KID_GEMM_GU_DGRAD, blocks, w.dgu, 2 * q.f, p->w_gate, p->w_up, q.f, q.f, q.d * q.f,
+                                    2 * q.f, q.d, w.dx_pad, q.d, false, nullptr, nullptr, 0, st))
+    return rc;
+  // join all helpers, then dx = gather-reduce of dX_pad + router dx term + shared-expert dx, one rounding
+  if (int rc = lsurge::stream_after(st, s0, ev[4])) return rc;
+  if (int rc = lsurge::stream_after(st, s1, ev[5])) return rc;
+  if (int rc = lsurge::stream_after(st, s2, ev[6])) return rc;
   return lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT,
                                          q.fs ? w.sdx : nullptr, g->dx, st);
 }

@@ -117,6 +117,26 @@ def test_deterministic_bitwise(dev):
         assert np.array_equal(a[2][k], b[2][k]), k
 
 
+def test_concurrent_streams_bitwise(dev):
+    """lsurge_set_concurrency(1) runs the independent chains on helper streams: same bits as the serial run."""
+    import _lib as L
+    c = dict(mo.CONFIGS["C2"], T=4096)
+    p = mo.make_inputs(**c)
+    shape = MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"])
+    lib = L.lib()
+    assert lib.lsurge_get_concurrency() == 0
+    a = run_gpu(p, shape, dev)
+    lib.lsurge_set_concurrency(1)
+    try:
+        b = run_gpu(p, shape, dev)
+        b2 = run_gpu(p, shape, dev)
+    finally:
+        lib.lsurge_set_concurrency(0)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(b[0], b2[0])
+    for k in a[2]:
+        assert np.array_equal(a[2][k], b[2][k]), k
+
+
 def test_autograd_function(dev):
     T, d, E, k, f, fs = 256, 128, 8, 2, 64, 64
     p = mo.make_inputs(T=T, d=d, E=E, k=k, f=f, fs=fs, seed=1)
