@@ -96,6 +96,21 @@ def make_params(c, dev, seed=0):
     return p, dy
 
 
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (lines
+    `bench-traffic <kernel> <bytes>` in profiles/moe_layer_<config>_fwd_bwd.md), or None."""
+    path = os.path.join(ROOT, "profiles", f"moe_layer_{config.lower()}_fwd_bwd.md")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                f = line.split()
+                if len(f) == 3 and f[0] == "bench-traffic" and f[1] == kernel:
+                    return float(f[2])
+    except OSError:
+        return None
+    return None
+
+
 def prof_table(lib, steps):
     import ctypes
     out = {}
@@ -268,7 +283,8 @@ def main():
         "layer_tflops": round(layer_flops(c) / (ms * 1e-3) / 1e12, 1),
         "mfu": round(layer_flops(c) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": None, "launch_ms": round(dom_ms, 4)},
+                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(a.config, dom),
+                     "launch_ms": round(dom_ms, 4)},
         "kernels": kern,
         "kernels_note": "per-kernel ms from a profiled pass on one stream (share of that pass's kernel time); "
                         "the timed region runs with concurrent_streams",
