@@ -78,7 +78,7 @@ def test_small_layer_zipf_bias(dev):
     check_layer(p, MoEShape(2048, 256, 32, 4, 128, 128), dev)
 
 
-@pytest.mark.parametrize("name", ["C1", "C2", "C4"])
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4"])
 def test_baseline_configs(name, dev):
     c = mo.CONFIGS[name]
     p = mo.make_inputs(**c)
