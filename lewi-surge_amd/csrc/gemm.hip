@@ -16,7 +16,8 @@
 //              (ragged K); both operands N-major in LDS, transpose-read.  Optional split of the rows into
 //              S slices with f32 partials summed afterwards in a fixed order (deterministic, no atomics).
 // The MFMA operands are passed weight-first, so each lane's accumulators hold four consecutive output
-// columns of one row and every epilogue store is an 8-byte (bf16) or 16-byte (f32) vector.
+// columns of one row.  Epilogues park the accumulators in the idle LDS ring and read them back
+// row-contiguous, so every global epilogue access is a 16-byte vector and 16 lanes cover a whole row.
 #include "common.h"
 
 namespace {
@@ -164,6 +165,16 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void st_bf16x4(bf16_t* p, float a, float b, float c, float d) {
   *reinterpret_cast<u32x2*>(p) = u32x2{pack_bf16x2(a, b), pack_bf16x2(c, d)};
 }
+__device__ __forceinline__ void st_bf16x8(bf16_t* p, const float* v) {
+  *reinterpret_cast<u32x4*>(p) =
+      u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+}
+
+// Epilogue staging: a wave parks 32 rows x 128 f32 columns in LDS with a row pitch of SP floats.  The 4-float
+// pad shifts consecutive rows by 4 banks, so the 16-byte accumulator writes (one column group of 32 rows)
+// spread over all banks.  4 waves x 32 x SP x 4 B = 66 KiB fits in the 72 KiB ring.
+constexpr int SP = 132;
+static_assert(4 * 32 * SP * 4 <= 3 * (BM + BN) * BK * 2, "epilogue staging must fit in the LDS ring");
 
 // 1 / (1 + e^-g) with the hardware reciprocal (about 1 ulp): plenty for bf16 outputs, and it keeps the
 // epilogue short
@@ -204,10 +215,15 @@ __device__ __forceinline__ void k_loop(int nk, Issue&& issue, Compute&& compute)
 // =====================================================================================================
 template <int BMODE, int EPI>
 __global__ __launch_bounds__(GT, OCC) void gemm_rows_kernel(RowsArgs a) {
-  // LDS ring: 3 stages of A (K-major 128 x 32) and B (K-major 256 x 32, or two N-major 32 x 128 sub-tiles);
-  // separate arrays per slot let the compiler track the copies into each slot separately
-  __shared__ __attribute__((aligned(1024))) bf16_t A0[BM * BK], A1[BM * BK], A2[BM * BK];
-  __shared__ __attribute__((aligned(1024))) bf16_t B0[BN * BK], B1[BN * BK], B2[BN * BK];
+  // LDS ring: 3 stages of A (K-major 128 x 32) and B (K-major 256 x 32, or two N-major 32 x 128 sub-tiles).
+  // After the K loop the same memory stages the epilogue.
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[3 * (BM + BN) * BK];
+  bf16_t* const A0 = smem;
+  bf16_t* const A1 = smem + BM * BK;
+  bf16_t* const A2 = smem + 2 * BM * BK;
+  bf16_t* const B0 = smem + 3 * BM * BK;
+  bf16_t* const B1 = B0 + BN * BK;
+  bf16_t* const B2 = B1 + BN * BK;
 
   const int64_t total = (int64_t)gridDim.x;
   const int64_t logical = xcd_logical(blockIdx.x, total);
@@ -342,89 +358,90 @@ __global__ __launch_bounds__(GT, OCC) void gemm_rows_kernel(RowsArgs a) {
 
   k_loop(nk, issue, compute);
 
-  // ---- epilogue.  acc[i][j][4q + t]: activation row wm*64 + 32 i + lane%32, tile column bcol(j) + 8 q +
-  // 4 (lane/32) + t.
+  // ---- epilogue, staged through LDS.  acc[i][j][4q + t] holds activation row wm*64 + 32 i + lane%32 and
+  // wave column 32 j + 8 q + 4 (lane/32) + t (SwiGLU: j < 2 gate, j >= 2 up).  Written straight out, one
+  // store instruction would cover 16 bytes of 32 different rows.  Instead each wave parks one 32-row half
+  // of its accumulators in the (now idle) ring as f32 rows, then reads them back row-contiguous: 16 lanes x
+  // 16 bytes cover a row's 128 columns, so every global load and store spans whole 128-byte lines.
+  __syncthreads();  // all waves are done with the ring
+  float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * SP);
   const int lm = lane & 31, lh = lane >> 5;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int mloc = wm * 64 + 32 * i + lm;
-    if (mloc >= rows) continue;
-    const int64_t gr = row0 + mloc;
+    const int mbase = wm * 64 + 32 * i;  // first tile row of this half
+    // SwiGLU backward: fetch the saved g, u of this half before parking the accumulators, so the loads'
+    // latency overlaps the LDS round trip.  Lane -> row 4 it + lane/16, 8 columns at 8 (lane % 16).
+    u32x4 gq[8], uq[8];
+    if (EPI == EPI_SWIGLU_BWD) {
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int r = 4 * it + (lane >> 4);
+        const int64_t col = n0 + wn * 128 + 8 * (lane & 15);
+        const bool ok = mbase + r < rows && col < N;
+        const int64_t off = ok ? (row0 + mbase + r) * a.ldg + col : row0 * a.ldg;
+        gq[it] = *reinterpret_cast<const u32x4*>(a.G + off);
+        uq[it] = *reinterpret_cast<const u32x4*>(a.U + off);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4*>(stg + lm * SP + 32 * j + 8 * q + 4 * lh) =
+            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
     if (EPI == EPI_SWIGLU_FWD) {
+      // 64 gate + 64 up columns per row: lane -> row 8 it + lane/8, 8 output columns at 8 (lane % 8)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int it = 0; it < 4; ++it) {
+        const int r = 8 * it + (lane >> 3), c = 8 * (lane & 7);
+        const int64_t col = n0 + wn * 64 + c;
+        if (mbase + r >= rows || col >= N) continue;
+        const float* src = stg + r * SP + c;
+        const f32x4 g0 = *reinterpret_cast<const f32x4*>(src), g1 = *reinterpret_cast<const f32x4*>(src + 4);
+        const f32x4 u0 = *reinterpret_cast<const f32x4*>(src + 64), u1 = *reinterpret_cast<const f32x4*>(src + 68);
+        const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+        const float u[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+        float h[8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t col = n0 + wn * 64 + 32 * j + 8 * q + 4 * lh;
-          if (col >= N) continue;
-          float h[4], g[4], u[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            g[t] = acc[i][j][4 * q + t];
-            u[t] = acc[i][j + 2][4 * q + t];
-            h[t] = silu_f(g[t]) * u[t];
-          }
-          st_bf16x4(a.C + gr * a.ldc + col, h[0], h[1], h[2], h[3]);
-          if (a.G) st_bf16x4(a.G + gr * a.ldg + col, g[0], g[1], g[2], g[3]);
-          if (a.U) st_bf16x4(a.U + gr * a.ldg + col, u[0], u[1], u[2], u[3]);
-        }
+        for (int t = 0; t < 8; ++t) h[t] = silu_f(g[t]) * u[t];
+        const int64_t gr = row0 + mbase + r;
+        st_bf16x8(a.C + gr * a.ldc + col, h);
+        if (a.G) st_bf16x8(a.G + gr * a.ldg + col, g);
+        if (a.U) st_bf16x8(a.U + gr * a.ldg + col, u);
+      }
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t col = n0 + wn * 128 + 32 * j + 8 * q + 4 * lh;
-          if (col >= N) continue;
-          const float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-          if (EPI == EPI_STORE) {
-            if (a.Cf) {
-              *reinterpret_cast<f32x4*>(a.Cf + gr * a.ldc + col) = f32x4{v[0], v[1], v[2], v[3]};
-            } else {
-              st_bf16x4(a.C + gr * a.ldc + col, v[0], v[1], v[2], v[3]);
-            }
+      for (int it = 0; it < 8; ++it) {
+        const int r = 4 * it + (lane >> 4), c = 8 * (lane & 15);
+        const int64_t col = n0 + wn * 128 + c;
+        if (mbase + r >= rows || col >= N) continue;
+        const float* src = stg + r * SP + c;
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(src), v1 = *reinterpret_cast<const f32x4*>(src + 4);
+        const int64_t gr = row0 + mbase + r;
+        if (EPI == EPI_STORE) {
+          if (a.Cf) {
+            *reinterpret_cast<f32x4*>(a.Cf + gr * a.ldc + col) = v0;
+            *reinterpret_cast<f32x4*>(a.Cf + gr * a.ldc + col + 4) = v1;
+          } else {
+            const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            st_bf16x8(a.C + gr * a.ldc + col, v);
           }
-        }
-    }
-  }
-  if (EPI == EPI_SWIGLU_BWD) {
-    // v = dH; C row = [dG (N cols) | dU (N cols)].  The saved g, u of one 32-row half are fetched in one batch
-    // (32 loads in flight per lane) before any output is written, so their latency is paid twice per tile
-    // rather than once per 4-column group.
+        } else {  // EPI_SWIGLU_BWD: v = dH; C row = [dG (N cols) | dU (N cols)]
+          const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          float dg[8], du[8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int mloc = wm * 64 + 32 * i + lm;
-      if (mloc >= rows) continue;
-      const int64_t gr = row0 + mloc;
-      u32x2 gq[4][4], uq[4][4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t col = n0 + wn * 128 + 32 * j + 8 * q + 4 * lh;
-          const int64_t c = col < N ? col : 0;
-          gq[j][q] = *reinterpret_cast<const u32x2*>(a.G + gr * a.ldg + c);
-          uq[j][q] = *reinterpret_cast<const u32x2*>(a.U + gr * a.ldg + c);
-        }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t col = n0 + wn * 128 + 32 * j + 8 * q + 4 * lh;
-          if (col >= N) continue;
-          float dg[4], du[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const uint32_t gw = gq[j][q][t >> 1], uw = uq[j][q][t >> 1];
+          for (int t = 0; t < 8; ++t) {
+            const uint32_t gw = gq[it][t >> 1], uw = uq[it][t >> 1];
             const float g = __uint_as_float((t & 1) ? (gw & 0xffff0000u) : (gw << 16));
             const float u = __uint_as_float((t & 1) ? (uw & 0xffff0000u) : (uw << 16));
-            const float v = acc[i][j][4 * q + t];
             const float sg = sigmoid_f(g);
-            dg[t] = v * u * sg * (1.f + g * (1.f - sg));
-            du[t] = v * g * sg;
+            dg[t] = v[t] * u * sg * (1.f + g * (1.f - sg));
+            du[t] = v[t] * g * sg;
           }
-          st_bf16x4(a.C + gr * a.ldc + col, dg[0], dg[1], dg[2], dg[3]);
-          st_bf16x4(a.C + gr * a.ldc + N + col, du[0], du[1], du[2], du[3]);
+          st_bf16x8(a.C + gr * a.ldc + col, dg);
+          st_bf16x8(a.C + gr * a.ldc + N + col, du);
         }
+      }
     }
   }
 }
@@ -433,9 +450,15 @@ __global__ __launch_bounds__(GT, OCC) void gemm_rows_kernel(RowsArgs a) {
 // Weight gradient C_e[I, N] = A_e^T B_e, reduced over the rows of expert e: both operands are row-major
 // [rows, .] (the reduction dim is the slow one), so both are staged N-major and read with the transpose read.
 __global__ __launch_bounds__(GT, OCC) void gemm_wgrad_kernel(WgradArgs a) {
-  // ring: A 32 rows x 128 columns (one N-major sub-tile), B 32 rows x 256 columns (two sub-tiles)
-  __shared__ __attribute__((aligned(1024))) bf16_t A0[BK * NS], A1[BK * NS], A2[BK * NS];
-  __shared__ __attribute__((aligned(1024))) bf16_t B0[BK * BN], B1[BK * BN], B2[BK * BN];
+  // ring: A 32 rows x 128 columns (one N-major sub-tile), B 32 rows x 256 columns (two sub-tiles); after the
+  // K loop the same memory stages the epilogue
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[3 * (NS + BN) * BK];
+  bf16_t* const A0 = smem;
+  bf16_t* const A1 = smem + BK * NS;
+  bf16_t* const A2 = smem + 2 * BK * NS;
+  bf16_t* const B0 = smem + 3 * BK * NS;
+  bf16_t* const B1 = B0 + BK * BN;
+  bf16_t* const B2 = B1 + BK * BN;
   const int64_t total = (int64_t)gridDim.x;
   int64_t logical = xcd_logical(blockIdx.x, total);
   const int64_t tiles_per_e = (int64_t)a.S * a.i_tiles * a.n_tiles;
@@ -524,25 +547,37 @@ __global__ __launch_bounds__(GT, OCC) void gemm_wgrad_kernel(WgradArgs a) {
   };
   k_loop(nk, issue, compute);
 
-  // epilogue (f32): acc[i][j][4q + t] = C[i0 + wm*64 + 32 i + lane%32][n0 + wn*128 + 32 j + 8 q + 4 (lane/32) + t]
+  // epilogue (f32), staged through LDS as in gemm_rows_kernel: acc[i][j][4q + t] is C row
+  // i0 + wm*64 + 32 i + lane%32, column n0 + wn*128 + 32 j + 8 q + 4 (lane/32) + t.  Read back with 16 lanes
+  // per row, each store instruction covers 4 rows x 512 contiguous bytes.
+  __syncthreads();  // all waves are done with the ring
+  float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * SP);
   const int lm = lane & 31, lh = lane >> 5;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int64_t row = i0 + wm * 64 + 32 * i + lm;
-    if (row >= I) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t col = n0 + wn * 128 + 32 * j + 8 * q + 4 * lh;
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4*>(stg + lm * SP + 32 * j + 8 * q + 4 * lh) =
+            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+#pragma unroll
+    for (int r8 = 0; r8 < 8; ++r8) {
+      const int r = 4 * r8 + (lane >> 4), c = 8 * (lane & 15);
+      const int64_t row = i0 + wm * 64 + 32 * i + r;
+      if (row >= I) continue;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t col = n0 + wn * 128 + c + 4 * h;
         if (col >= N) continue;
-        const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * SP + c + 4 * h);
         float* dst;
         if (a.S > 1) dst = a.part + (((int64_t)s * a.E + e) * I + row) * N + col;
         else if (a.C2 && col >= a.n_split) dst = a.C2 + (int64_t)e * a.c_estride + row * a.ldc + (col - a.n_split);
         else dst = a.C + (int64_t)e * a.c_estride + row * a.ldc + col;
         *reinterpret_cast<f32x4*>(dst) = v;
       }
+    }
   }
 }
 

@@ -12,9 +12,10 @@ Cases:
                    semantics of modal/test_moe_permute.py:23-26 (argsort(-logits)[:, :k], stable).
 * ragged_dot_te -- the known-answer shape of modal/te_run.py:72-79: gs = [5,0,9,3,7,1,6,4],
                    M = sum(gs) + 3, K = 64, N = 48; rows past sum(gs) are zero; forward and backward.
-* layer_small   -- whole MoE layer forward + backward with a shared expert (T=40, d=64, E=8, k=3, f=32).
+* layer_small   -- whole MoE layer forward + backward with a shared expert (T=40, d=64, E=8, k=3, f=64).
 * layer_zipf    -- whole layer with the Zipf router bias and empty experts, no shared expert
-                   (T=33, d=64, E=16, k=4, f=32).
+                   (T=24, d=64, E=8, k=2, f=64).
+Shapes follow the layer's limits: d, f, f_s multiples of 64, E a multiple of 8.
 
 bf16 tensors are stored as their uint16 bit patterns, float32 logits as uint32 bits.
 """
@@ -239,8 +240,8 @@ def make_layer(T, d, E, k, f, fs, seed, zipf):
 CASES = {
     "router_ties": make_router_ties,
     "ragged_dot_te": make_ragged_dot_te,
-    "layer_small": lambda: make_layer(40, 64, 8, 3, 32, 32, seed=7, zipf=False),
-    "layer_zipf": lambda: make_layer(33, 64, 16, 4, 32, 0, seed=8, zipf=True),
+    "layer_small": lambda: make_layer(40, 64, 8, 3, 64, 64, seed=7, zipf=False),
+    "layer_zipf": lambda: make_layer(24, 64, 8, 2, 64, 0, seed=8, zipf=True),
 }
 
 
