@@ -1,0 +1,646 @@
+// Grouped-GEMM kernels of the MoE layer on CDNA4 matrix cores: bf16 inputs, f32 accumulation,
+// v_mfma_f32_32x32x16_bf16.  The tile shape is a template parameter (GemmCfg): BM x BN workgroup tiles split
+// over WM x WN waves, K in BK-wide stages that the buffer unit copies straight into an ST-deep LDS ring
+// (buffer_load_dwordx4 ... lds).  gemm.hip instantiates the shapes the layer uses.
+//
+// Replaces the padded batched einsum of modal/padded_gmm.py:66-69 (cuBLAS on the reference's GPU path) and
+// its autodiff.  Two kernel families:
+//
+//  gemm_rows   row-tiled: C[tile rows, n-tile] = A[tile rows, :] @ B[expert(tile)].  A row tile is up to BM
+//              consecutive rows of one expert, looked up in a device tile table (128-row padded blocks, or
+//              256-row pairs of an expert's consecutive blocks).  Tiles past the device-side tile count exit at
+//              once, so padding tiles cost nothing; rows past a tile's valid count are loaded as zeros.
+//              B either K-major ([N, K], read with ds_read_b128) or N-major ([K, N], read with the gfx950
+//              LDS transpose read ds_read_b64_tr_b16).  Epilogues: plain store (bf16 or f32), SwiGLU forward
+//              (gate and up columns side by side in one accumulator set -> h = silu(g) * u, plus g and u
+//              for the backward), SwiGLU backward (dH -> dG, dU from the saved g, u).
+//  gemm_wgrad  per-expert weight gradient: C_e = A_e^T @ B_e with the reduction over the expert's rows
+//              (ragged K); both operands N-major in LDS, transpose-read.  Optional split of the rows into
+//              S slices with f32 partials summed afterwards in a fixed order (deterministic, no atomics).
+// The MFMA operands are passed weight-first, so each lane's accumulators hold four consecutive output
+// columns of one row.  Epilogues park the accumulators in the idle LDS ring and read them back
+// row-contiguous, so every global epilogue access is a 16-byte vector and a few lanes cover a whole row.
+//
+// Every output element is the same ascending sequence of 16-deep MFMA steps whatever the tile shape, so all
+// shapes give bitwise identical results.
+#pragma once
+#include "common.h"
+
+namespace lsgemm {
+
+enum { B_NK = 0, B_KN = 1 };                        // B operand storage
+enum { EPI_STORE = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
+
+constexpr int NS = 128;  // columns per N-major LDS sub-tile (256-byte rows)
+
+// Tile shape: BM x BN per workgroup, WM x WN waves (wave tile TM x TN = FM x FN fragments of 32 x 32), K in
+// BK-deep stages, an ST-stage LDS ring, OCC workgroups per CU.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int ST_, int OCC_>
+struct GemmCfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, ST = ST_, OCC = OCC_;
+  static constexpr int NW = WM * WN, GT = 64 * NW;
+  static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  static constexpr int A_EL = BM * BK, B_EL = BN * BK;                   // bf16 elements per stage
+  static constexpr int CPA = A_EL * 2 / 1024 / NW, CPB = B_EL * 2 / 1024 / NW, CP = CPA + CPB;  // copies per wave
+  static constexpr int RING_EL = ST * (A_EL + B_EL);
+  static constexpr int SP = TN + 4;                  // epilogue staging pitch (f32)
+  static constexpr int STG_EL = NW * 32 * SP * 2;    // epilogue staging, in bf16 element units
+  static constexpr int SMEM_EL = RING_EL > STG_EL ? RING_EL : STG_EL;
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(TM % 32 == 0 && TN % 64 == 0 && BN % NS == 0 && BM % NS == 0, "tile");
+  static_assert(CPA * NW * 1024 == A_EL * 2 && CPB * NW * 1024 == B_EL * 2, "copies must split evenly over waves");
+  static_assert((ST - 1) * CP < 64 && ST >= 2, "vmcnt field");
+  static_assert(SMEM_EL * 2 <= 160 * 1024 / OCC, "LDS");
+};
+
+struct RowsArgs {
+  const bf16_t* A;  // rows with K contiguous
+  int64_t lda;
+  const bf16_t* B;   // expert 0 of the first B matrix
+  const bf16_t* B2;  // second B (SwiGLU up weights / dgrad up weights), same strides
+  int64_t ldb;       // row pitch of B as stored
+  int64_t b_estride; // elements between experts
+  int64_t K, N;      // reduction dim, output columns (EPI_SWIGLU_FWD: N = f, a tile covers BN/2 outputs)
+  int64_t k_split;   // B_NK with B2: k < k_split from B, else B2 at k - k_split (0 = unused)
+  bf16_t* C;         // output [rows, ldc]
+  float* Cf;         // EPI_STORE: f32 output instead of C when set
+  int64_t ldc;
+  bf16_t* G;         // SwiGLU saved gate pre-activation [rows, ldg] (fwd: written, bwd: read)
+  bf16_t* U;         // SwiGLU saved up projection
+  int64_t ldg;
+  const int32_t* t_expert;   // tile table (nullptr: dense, expert 0, rows = min(BM, dense_rows - BM t))
+  const int32_t* t_rows;     // valid rows of tile t
+  const int32_t* t_row0;     // first row of tile t (nullptr: BM t)
+  const int32_t* num_tiles;  // device-side tile count
+  int64_t dense_rows;
+  int n_tiles;               // column tiles
+  int max_tiles;             // row tiles the grid covers
+};
+
+struct WgradArgs {
+  const bf16_t* A;   // [rows, lda], the reduction runs over rows; C's rows are A's columns
+  int64_t lda;
+  const bf16_t* B;   // [rows, ldb]
+  int64_t ldb;
+  int64_t I, N;      // output [I, N] per expert
+  float* C;          // expert e at C + e * c_estride, row pitch ldc
+  float* C2;         // columns n >= n_split go to C2 at column n - n_split (nullptr: unused)
+  int64_t n_split;
+  int64_t ldc, c_estride;
+  float* part;       // split partials [S][E][I][N] when S > 1
+  const int32_t* e_row0;  // first row of expert e, in units of row0_mult rows (nullptr: dense)
+  const int32_t* e_rows;  // rows of expert e
+  int row0_mult;
+  int64_t dense_rows;
+  int E, S, i_tiles, n_tiles;
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// D[32 x 32] += P[32 x 16] Q[16 x 32]; lane l supplies row l%32 of P and column l%32 of Q, k = 8(l/32)..+7.
+// The kernels call it with P = the weight fragment and Q = the activation fragment, so the accumulator holds
+// C^T: lane l owns activation row l%32 and output columns 8(r/4) + 4(l/32) + r%4 -- four consecutive columns
+// per register quad.
+__device__ __forceinline__ f32x16 mfma32(bf16x8 p, bf16x8 q, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------------------------- LDS tiles
+// K-major tile: rows of BK k (BK/8 chunks of 16 B; 64 B rows for BK = 32, 128 B rows for BK = 64), no padding.
+// Chunk c of row r sits at slot c ^ swz(r).  A fragment read takes one chunk of 32 consecutive rows; the 16
+// lanes of each read phase then hit 16 distinct 16-byte slots of a 256-byte bank window:
+//   BK = 32: granule 4 (r & 3) + (c ^ ((r >> 2) & 3))      BK = 64: granule 8 (r & 1) + (c ^ ((r >> 1) & 7))
+// and a copy instruction writes 1 KiB contiguously, so neither direction has bank conflicts.
+template <int BK>
+__device__ __forceinline__ int km_swz(int row) { return BK == 32 ? (row >> 2) & 3 : (row >> 1) & 7; }
+template <int BK>
+__device__ __forceinline__ int km_off(int row, int chunk) { return row * BK + ((chunk ^ km_swz<BK>(row)) << 3); }
+
+// N-major sub-tile: BK k-rows x 128 columns (16 chunks of 16 B, 256 B rows).  Chunk c of row k sits at slot
+// c ^ ((k & 3) << 2), which moves the 64-byte column group of 4 consecutive rows to 4 different 64-byte bank
+// groups: a transpose read (4 rows x 64 B per 32 lanes) is conflict-free.  One copy instruction fills 4 rows.
+__device__ __forceinline__ int nm_off(int k, int n) { return k * NS + ((((n >> 3) ^ ((k & 3) << 2))) << 3) + (n & 7); }
+
+// K-major fragment: 8 consecutive k (chunk kc) of one row -> one 16-byte LDS read
+template <int BK>
+__device__ __forceinline__ bf16x8 frag_k(const bf16_t* tile, int row, int kc) {
+  return as_bf16x8(*reinterpret_cast<const u32x4*>(tile + km_off<BK>(row, kc)));
+}
+
+// N-major fragment for the 32x32x16 operand layout: lane l needs rows (k) 8(l/32)+0..7 of column l%32.
+// ds_read_b64_tr_b16 in a 16-lane group g: lane i receives D[4j + i/4][i%4], j = 0..3, where D[s] are the four
+// 16-bit values at source lane s's address.  With source lane s pointing at (k = kb + s/4, n = nb + 4(s%4)),
+// lane i receives column nb + i, rows kb..kb+3.  Two reads give the 8 k values.
+__device__ __forceinline__ bf16x8 frag_n(const bf16_t* sub, int kbase, int nbase, int lane) {
+  const int g = lane >> 4, s = lane & 15;
+  const int n = nbase + 16 * (g & 1) + 4 * (s & 3);
+  const int k0 = kbase + 8 * (g >> 1) + (s >> 2);
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, sub + nm_off(k0, n)));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, sub + nm_off(k0 + 4, n)));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// ---------------------------------------------------------------------------------------------- global -> LDS
+// Operand tiles are copied by the buffer unit straight into LDS (buffer_load_dwordx4 ... lds): lane p of a copy
+// instruction writes its 16 bytes at (M0 + 16 p), so the LDS layouts above are produced by choosing which global
+// chunk each lane fetches.  One descriptor per operand covers exactly the bytes the tile may read (a tile's
+// valid rows, an expert's weight matrix), and a lane whose element lies outside (rows past the tile, K or N
+// tails) passes an offset past the end, for which the buffer unit writes zeros.  No VGPR staging, no LDS store
+// instructions.
+//
+// The copy is issued from inline asm so that the compiler does not see an LDS write: it would otherwise guard
+// LDS reads with waits for every copy in flight (it cannot tell the ring slots apart through the transpose
+// reads), draining the prefetch ring.  Completion is tracked by hand instead: stage_barrier<N> waits until at
+// most N copies of this wave are outstanding before the workgroup barrier.
+constexpr uint32_t OOB = 0x80000000u;  // every descriptor covers < 2^31 bytes (checked on the host)
+constexpr int KBIG = 1 << 30;          // per-lane k of a chunk outside the operand: never below K
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, int64_t bytes) {
+  const uint64_t b = (uint64_t)base;
+  // base (48 bits), stride 0, num_records = bytes, dword3 = 32-bit data format, no swizzle; all wave-uniform,
+  // readfirstlane keeps the descriptor in scalar registers for the copies
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b),
+               (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu),
+               (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)bytes), 0x00020000u};
+}
+// One 1 KiB copy: lane p's 16 bytes at byte_off of the buffer land at LDS byte address m0 + 16 p.  m0 is the
+// wave-uniform LDS address of the destination (the LDS base of the kernel's array plus a constant offset).
+__device__ __forceinline__ void copy16(u32x4 rsrc, uint32_t byte_off, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(rsrc), "s"(m0)
+               : "memory");
+}
+// LDS byte address of the kernel's shared array, as a scalar
+__device__ __forceinline__ uint32_t lds_addr(const bf16_t* p) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(size_t)LDS_PTR(const void, p));
+}
+
+// Wait until at most N copies of this wave are in flight and its LDS reads are done, then barrier: after it
+// every wave's copies of the stage in question have landed and nobody still reads the buffer about to be
+// refilled.  The barrier is an asm statement with a memory clobber so the compiler keeps LDS accesses on
+// their side of it without adding a wait for all copies (which would drain the prefetch ring).
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));  // vmcnt(N) lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// Software-pipelined K loop over an ST-deep ring; stage kt lives in slot kt % ST and a stage is KS = BK / 16
+// MFMA steps.  The fragments of step n + 1 are read from LDS (into the other half of a double buffer) before the
+// MFMAs of step n are issued, so the matrix pipe never waits for an LDS read.  The stage switch happens inside
+// the last step of a stage: wait until the next stage has landed (at most ST - 2 younger stages in flight),
+// barrier -- after which every wave has also finished reading the current slot -- refill the current slot with
+// stage kt + ST, read the next stage's first fragments, then issue the last step's MFMAs.  Stages past the end
+// copy zeros (out-of-range offsets), so every step has the same shape and the wait counts stay exact.
+//   issue(slot, kt)     enqueue the copies of stage kt into ring slot `slot`
+//   load(slot, s, F)    read the fragments of step s of the stage in `slot` into F
+//   mma(F)              the MFMAs of one step
+template <int ST, int CP, int KS, class Frags, class Issue, class Load, class Mma>
+__device__ __forceinline__ void k_loop(int nk, Issue&& issue, Load&& load, Mma&& mma) {
+  static_assert(KS % 2 == 0, "fragment double buffer parity");
+#pragma unroll
+  for (int s = 0; s < ST; ++s) issue(s, s);
+  stage_barrier<(ST - 1) * CP>();
+  Frags f0, f1;
+  load(0, 0, f0);
+  for (int kt0 = 0;; kt0 += ST) {
+    bool done = false;
+#pragma unroll
+    for (int j = 0; j < ST; ++j) {
+      if (!done) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          Frags& cur = (s & 1) ? f1 : f0;
+          Frags& nxt = (s & 1) ? f0 : f1;
+          if (s + 1 < KS) {
+            load(j, s + 1, nxt);
+          } else {
+            stage_barrier<(ST - 2) * CP>();
+            issue(j, kt0 + j + ST);
+            load((j + 1) % ST, 0, nxt);
+          }
+          // keep the reads of the next step ahead of this step's MFMAs (the scheduler would otherwise sink
+          // each read to just before its first use and the MFMAs would wait on LDS latency again)
+          __builtin_amdgcn_sched_barrier(0);
+          mma(cur);
+          __builtin_amdgcn_sched_barrier(0);  // and this step's MFMAs ahead of the next stage barrier
+        }
+        done = kt0 + j + 1 >= nk;
+      }
+    }
+    if (done) break;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the copies of the zero stages past the end land before the epilogue
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void st_bf16x8(bf16_t* p, const float* v) {
+  *reinterpret_cast<u32x4*>(p) =
+      u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+}
+
+// 1 / (1 + e^-g) with the hardware reciprocal (about 1 ulp): plenty for bf16 outputs, and it keeps the
+// epilogue short
+__device__ __forceinline__ float sigmoid_f(float g) { return __builtin_amdgcn_rcpf(1.f + __expf(-g)); }
+__device__ __forceinline__ float silu_f(float g) { return g * sigmoid_f(g); }
+
+// XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so consecutive logical
+// tiles (same expert tile, neighbouring N tiles and experts) are sent to the same XCD's L2.
+__device__ __forceinline__ int64_t xcd_logical(int64_t id, int64_t total) {
+  const int64_t per = total / 8;
+  return (id % 8) * per + id / 8;
+}
+
+// Park fragment row i of the accumulators (32 rows x TN f32 columns) in this wave's staging area.
+// acc[i][j][4q + t] is row lane%32, wave column 32 j + 8 q + 4 (lane/32) + t.
+template <class Cfg>
+__device__ __forceinline__ void park(float* stg, const f32x16 (&acc)[Cfg::FM][Cfg::FN], int i, int lane) {
+  const int lm = lane & 31, lh = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<f32x4*>(stg + lm * Cfg::SP + 32 * j + 8 * q + 4 * lh) =
+          f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+}
+
+template <int FM, int FN>
+struct FragSet {
+  bf16x8 x[FM], w[FN];
+};
+
+// =====================================================================================================
+template <class Cfg, int BMODE, int EPI>
+__global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW * Cfg::OCC / 4)))
+void gemm_rows_kernel(RowsArgs a) {
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, ST = Cfg::ST;
+  constexpr int TM = Cfg::TM, TN = Cfg::TN, FM = Cfg::FM, FN = Cfg::FN, SP = Cfg::SP;
+  constexpr int CPA = Cfg::CPA, CPB = Cfg::CPB;
+  constexpr int RPC = 1024 / (2 * BK), CPR = BK / 8;  // K-major copy: rows per copy, chunks per row
+  constexpr int NSUB = BN / NS;                      // N-major B: sub-tiles
+  constexpr int CPS = BK / 4;                        // N-major: copies per sub-tile
+  // LDS ring: ST stages of A (K-major BM x BK) and B (K-major BN x BK, or NSUB N-major BK x 128 sub-tiles).
+  // After the K loop the same memory stages the epilogue.
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[Cfg::SMEM_EL];
+  constexpr uint32_t A_SLOT = Cfg::A_EL * 2, B_SLOT = Cfg::B_EL * 2, B_RING = ST * A_SLOT;  // bytes
+
+  const int64_t total = (int64_t)gridDim.x;
+  const int64_t logical = xcd_logical(blockIdx.x, total);
+  const int nt = (int)(logical % a.n_tiles);
+  const int b = (int)(logical / a.n_tiles);
+  if (b >= a.max_tiles) return;
+  int expert, rows;
+  int64_t row0;
+  if (a.t_expert) {
+    if (b >= a.num_tiles[0]) return;
+    expert = a.t_expert[b];
+    rows = a.t_rows[b];
+    row0 = a.t_row0 ? (int64_t)a.t_row0[b] : (int64_t)b * BM;
+  } else {
+    expert = 0;
+    row0 = (int64_t)b * BM;
+    rows = (int)min((int64_t)BM, a.dense_rows - row0);
+    if (rows <= 0) return;
+  }
+  // the wave index is uniform: keeping it in a scalar register keeps the copy destinations (M0) and the choice
+  // of weight descriptor scalar as well
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  // column origin of this tile: weight columns for B, output columns for C (SwiGLU: gate and up halves)
+  const int64_t n0 = (int64_t)nt * (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN);
+  const bf16_t* Bbase = a.B + (int64_t)expert * a.b_estride;
+  const bf16_t* B2base = a.B2 ? a.B2 + (int64_t)expert * a.b_estride : Bbase;
+  const int K = (int)a.K, N = (int)a.N, lda = (int)a.lda, ldb = (int)a.ldb, ksplit = (int)a.k_split;
+  const int nk = (K + BK - 1) / BK;
+  const uint32_t lds0 = lds_addr(smem);
+
+  // descriptors: this tile's rows of A; the expert's B (and B2) matrix
+  const u32x4 rsA = make_rsrc(a.A + row0 * a.lda, (int64_t)rows * a.lda * 2);
+  const int64_t b_bytes = (int64_t)(BMODE == B_NK ? N : K) * a.ldb * 2;
+  const u32x4 rsB = make_rsrc(Bbase, b_bytes);
+  const u32x4 rsB2 = make_rsrc(B2base, b_bytes);
+
+  // ---- per-lane copy geometry, fixed over k: byte offset of this lane's chunk at k = 0 and the k of the chunk
+  // within a stage (KBIG when its row or column is outside the operand, so the k test alone rejects it).
+  // K-major: copy q covers rows RPC q .. RPC q + RPC - 1; lane -> row RPC q + lane / CPR, slot lane % CPR.
+  uint32_t a_off[CPA];
+  int a_k[CPA];
+#pragma unroll
+  for (int c = 0; c < CPA; ++c) {
+    const int r = RPC * (CPA * wave + c) + lane / CPR;
+    const int kc = (lane % CPR) ^ km_swz<BK>(r);
+    a_off[c] = (uint32_t)(r * lda + 8 * kc) * 2u;
+    a_k[c] = r < rows ? 8 * kc : KBIG;
+  }
+  // B K-major: as A over n.  B N-major: copy q fills k rows 4 (q % CPS) + lane / 16 of sub-tile q / CPS, slot
+  // lane % 16 (SwiGLU forward: sub-tiles [0, NSUB/2) gate, [NSUB/2, NSUB) up, same output columns).
+  uint32_t b_off[CPB];
+  int b_k[CPB];
+#pragma unroll
+  for (int c = 0; c < CPB; ++c) {
+    const int q = CPB * wave + c;
+    if (BMODE == B_NK) {
+      const int n = RPC * q + lane / CPR;
+      const int kc = (lane % CPR) ^ km_swz<BK>(n);
+      const int64_t gn = n0 + n;
+      b_off[c] = (uint32_t)(gn * ldb + 8 * kc) * 2u;
+      b_k[c] = gn < N ? 8 * kc : KBIG;
+    } else {
+      const int sub = q / CPS;
+      const int k = 4 * (q % CPS) + (lane >> 4);
+      const int ch = (lane & 15) ^ ((k & 3) << 2);
+      const int64_t gn = EPI == EPI_SWIGLU_FWD ? n0 + NS * (sub % (NSUB / 2)) + 8 * ch : n0 + NS * sub + 8 * ch;
+      b_off[c] = (uint32_t)(k * ldb + gn) * 2u;
+      b_k[c] = gn < N ? k : KBIG;
+    }
+  }
+
+  auto issue = [&](int slot, int kt) {
+    const int k0 = kt * BK;
+    const uint32_t at = lds0 + slot * A_SLOT, bt = lds0 + B_RING + slot * B_SLOT;
+#pragma unroll
+    for (int c = 0; c < CPA; ++c)
+      copy16(rsA, k0 + a_k[c] < K ? a_off[c] + 2u * k0 : OOB, at + 1024 * (CPA * wave + c));
+    if (BMODE == B_NK) {
+      const bool second = ksplit && k0 >= ksplit;  // k range of B2 (gate/up dgrad); uniform
+      const int kb = second ? k0 - ksplit : k0;
+      const u32x4 rs = second ? rsB2 : rsB;
+#pragma unroll
+      for (int c = 0; c < CPB; ++c)
+        copy16(rs, k0 + b_k[c] < K ? b_off[c] + 2u * kb : OOB, bt + 1024 * (CPB * wave + c));
+    } else {
+      const uint32_t kstep = 2u * (uint32_t)k0 * (uint32_t)ldb;
+#pragma unroll
+      for (int c = 0; c < CPB; ++c) {
+        const int q = CPB * wave + c, sub = q / CPS;  // wave-uniform
+        const u32x4 rs = (EPI == EPI_SWIGLU_FWD && sub >= NSUB / 2) ? rsB2 : rsB;
+        copy16(rs, k0 + b_k[c] < K ? b_off[c] + kstep : OOB,
+               bt + sub * (BK * NS * 2) + 1024 * (q % CPS));
+      }
+    }
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+
+  // tile column of this wave's weight fragment j (SwiGLU: the first FN/2 gate, the rest up, same outputs)
+  auto bcol = [&](int j) {
+    if (EPI == EPI_SWIGLU_FWD)
+      return (j < FN / 2 ? 0 : BN / 2) + wn * (TN / 2) + 32 * (j < FN / 2 ? j : j - FN / 2);
+    return wn * TN + 32 * j;
+  };
+  typedef FragSet<FM, FN> F;
+  auto load = [&](int slot, int s, F& f) {
+    const bf16_t* at = smem + slot * Cfg::A_EL;
+    const bf16_t* bt = smem + ST * Cfg::A_EL + slot * Cfg::B_EL;
+    const int kk = 16 * s;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) f.x[i] = frag_k<BK>(at, wm * TM + 32 * i + (lane & 31), kk / 8 + (lane >> 5));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = bcol(j);
+      if (BMODE == B_NK) f.w[j] = frag_k<BK>(bt, col + (lane & 31), kk / 8 + (lane >> 5));
+      else f.w[j] = frag_n(bt + (col / NS) * (BK * NS), kk, col % NS, lane);
+    }
+  };
+  auto mma = [&](const F& f) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
+  };
+
+  k_loop<ST, Cfg::CP, BK / 16, F>(nk, issue, load, mma);
+
+  // ---- epilogue, staged through LDS.  Written straight out, one store instruction would cover 16 bytes of 32
+  // different rows.  Instead each wave parks one 32-row slice of its accumulators in the (now idle) ring as f32
+  // rows, then reads them back row-contiguous: TN / 8 lanes x 8 columns cover a row, so every global load and
+  // store spans whole lines.
+  __syncthreads();  // all waves are done with the ring
+  float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * SP);
+  constexpr int LPR = TN / 8, RPP = 64 / LPR, PASSES = 32 / RPP;          // store mapping
+  constexpr int LPR2 = TN / 16, RPP2 = 64 / LPR2, PASSES2 = 32 / RPP2;    // SwiGLU forward: TN / 2 outputs
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int mbase = wm * TM + 32 * i;  // first tile row of this slice
+    // SwiGLU backward: fetch the saved g, u of this slice before parking the accumulators, so the loads'
+    // latency overlaps the LDS round trip.
+    u32x4 gq[PASSES], uq[PASSES];
+    if (EPI == EPI_SWIGLU_BWD) {
+#pragma unroll
+      for (int it = 0; it < PASSES; ++it) {
+        const int r = RPP * it + lane / LPR;
+        const int64_t col = n0 + wn * TN + 8 * (lane % LPR);
+        const bool ok = mbase + r < rows && col < N;
+        const int64_t off = ok ? (row0 + mbase + r) * a.ldg + col : row0 * a.ldg;
+        gq[it] = *reinterpret_cast<const u32x4*>(a.G + off);
+        uq[it] = *reinterpret_cast<const u32x4*>(a.U + off);
+      }
+    }
+    if (i > 0) __builtin_amdgcn_wave_barrier();
+    park<Cfg>(stg, acc, i, lane);
+    if (EPI == EPI_SWIGLU_FWD) {
+#pragma unroll
+      for (int it = 0; it < PASSES2; ++it) {
+        const int r = RPP2 * it + lane / LPR2, c = 8 * (lane % LPR2);
+        const int64_t col = n0 + wn * (TN / 2) + c;
+        if (mbase + r >= rows || col >= N) continue;
+        const float* src = stg + r * SP + c;
+        const f32x4 g0 = *reinterpret_cast<const f32x4*>(src), g1 = *reinterpret_cast<const f32x4*>(src + 4);
+        const f32x4 u0 = *reinterpret_cast<const f32x4*>(src + TN / 2);
+        const f32x4 u1 = *reinterpret_cast<const f32x4*>(src + TN / 2 + 4);
+        const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+        const float u[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+        float h[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) h[t] = silu_f(g[t]) * u[t];
+        const int64_t gr = row0 + mbase + r;
+        st_bf16x8(a.C + gr * a.ldc + col, h);
+        if (a.G) st_bf16x8(a.G + gr * a.ldg + col, g);
+        if (a.U) st_bf16x8(a.U + gr * a.ldg + col, u);
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < PASSES; ++it) {
+        const int r = RPP * it + lane / LPR, c = 8 * (lane % LPR);
+        const int64_t col = n0 + wn * TN + c;
+        if (mbase + r >= rows || col >= N) continue;
+        const float* src = stg + r * SP + c;
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(src), v1 = *reinterpret_cast<const f32x4*>(src + 4);
+        const int64_t gr = row0 + mbase + r;
+        if (EPI == EPI_STORE) {
+          if (a.Cf) {
+            *reinterpret_cast<f32x4*>(a.Cf + gr * a.ldc + col) = v0;
+            *reinterpret_cast<f32x4*>(a.Cf + gr * a.ldc + col + 4) = v1;
+          } else {
+            const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            st_bf16x8(a.C + gr * a.ldc + col, v);
+          }
+        } else {  // EPI_SWIGLU_BWD: v = dH; C row = [dG (N cols) | dU (N cols)]
+          const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          float dg[8], du[8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const uint32_t gw = gq[it][t >> 1], uw = uq[it][t >> 1];
+            const float g = __uint_as_float((t & 1) ? (gw & 0xffff0000u) : (gw << 16));
+            const float u = __uint_as_float((t & 1) ? (uw & 0xffff0000u) : (uw << 16));
+            const float sg = sigmoid_f(g);
+            dg[t] = v[t] * u * sg * (1.f + g * (1.f - sg));
+            du[t] = v[t] * g * sg;
+          }
+          st_bf16x8(a.C + gr * a.ldc + col, dg);
+          st_bf16x8(a.C + gr * a.ldc + N + col, du);
+        }
+      }
+    }
+  }
+}
+
+// =====================================================================================================
+// Weight gradient C_e[I, N] = A_e^T B_e, reduced over the rows of expert e: both operands are row-major
+// [rows, .] (the reduction dim is the slow one), so both are staged N-major and read with the transpose read.
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW * Cfg::OCC / 4)))
+void gemm_wgrad_kernel(WgradArgs a) {
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, ST = Cfg::ST;
+  constexpr int TM = Cfg::TM, TN = Cfg::TN, FM = Cfg::FM, FN = Cfg::FN, SP = Cfg::SP;
+  constexpr int CPA = Cfg::CPA, CPB = Cfg::CPB, CPS = BK / 4;
+  // ring: A BM/128 N-major sub-tiles (BK rows x 128 columns), B BN/128 sub-tiles; after the K loop the same
+  // memory stages the epilogue
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[Cfg::SMEM_EL];
+  constexpr uint32_t A_SLOT = Cfg::A_EL * 2, B_SLOT = Cfg::B_EL * 2, B_RING = ST * A_SLOT;  // bytes
+  const int64_t total = (int64_t)gridDim.x;
+  int64_t logical = xcd_logical(blockIdx.x, total);
+  const int64_t tiles_per_e = (int64_t)a.S * a.i_tiles * a.n_tiles;
+  const int e = (int)(logical / tiles_per_e);
+  if (e >= a.E) return;
+  int64_t rem = logical % tiles_per_e;
+  const int s = (int)(rem / ((int64_t)a.i_tiles * a.n_tiles));
+  rem %= (int64_t)a.i_tiles * a.n_tiles;
+  const int it = (int)(rem / a.n_tiles), nt = (int)(rem % a.n_tiles);
+  int64_t r0, nrows;
+  if (a.e_rows) {
+    r0 = (int64_t)a.e_row0[e] * a.row0_mult;
+    nrows = a.e_rows[e];
+  } else {
+    r0 = 0;
+    nrows = a.dense_rows;
+  }
+  // rows of split s
+  const int64_t chunk = ((nrows + a.S - 1) / a.S + BK - 1) / BK * BK;
+  const int64_t rs = (int64_t)s * chunk;
+  const int64_t re = min(nrows, rs + chunk);
+  const int64_t i0 = (int64_t)it * BM, n0 = (int64_t)nt * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  const int64_t I = a.I, N = a.N;
+  const int lda = (int)a.lda, ldb = (int)a.ldb;
+  const uint32_t lds0 = lds_addr(smem);
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+
+  const int nk = re > rs ? (int)((re - rs + BK - 1) / BK) : 0;
+  // descriptors over rows [rs, re) of this expert (empty when the split has no rows)
+  const int span = re > rs ? (int)(re - rs) : 0;
+  const u32x4 rsA = make_rsrc(a.A + (r0 + rs) * a.lda, (int64_t)span * a.lda * 2);
+  const u32x4 rsB = make_rsrc(a.B + (r0 + rs) * a.ldb, (int64_t)span * a.ldb * 2);
+  // copy q of an operand fills k rows 4 (q % CPS) + lane / 16 of sub-tile q / CPS, slot lane % 16: byte offset of
+  // this lane's chunk at row 0 of the span and its row in a stage (KBIG when its column is outside the operand)
+  uint32_t a_off[CPA], b_off[CPB];
+  int a_k[CPA], b_k[CPB];
+#pragma unroll
+  for (int c = 0; c < CPA; ++c) {
+    const int q = CPA * wave + c, sub = q / CPS;
+    const int k = 4 * (q % CPS) + (lane >> 4);
+    const int64_t ic = i0 + NS * sub + 8 * ((lane & 15) ^ ((k & 3) << 2));
+    a_off[c] = (uint32_t)(k * lda + ic) * 2u;
+    a_k[c] = ic < I ? k : KBIG;
+  }
+#pragma unroll
+  for (int c = 0; c < CPB; ++c) {
+    const int q = CPB * wave + c, sub = q / CPS;
+    const int k = 4 * (q % CPS) + (lane >> 4);
+    const int64_t nc = n0 + NS * sub + 8 * ((lane & 15) ^ ((k & 3) << 2));
+    b_off[c] = (uint32_t)(k * ldb + nc) * 2u;
+    b_k[c] = nc < N ? k : KBIG;
+  }
+  auto issue = [&](int slot, int kt) {
+    const int rb = kt * BK;
+    const uint32_t at = lds0 + slot * A_SLOT, bt = lds0 + B_RING + slot * B_SLOT;
+    const uint32_t astep = 2u * (uint32_t)rb * (uint32_t)lda, bstep = 2u * (uint32_t)rb * (uint32_t)ldb;
+#pragma unroll
+    for (int c = 0; c < CPA; ++c) {
+      const int q = CPA * wave + c;
+      copy16(rsA, rb + a_k[c] < span ? a_off[c] + astep : OOB,
+             at + (q / CPS) * (BK * NS * 2) + 1024 * (q % CPS));
+    }
+#pragma unroll
+    for (int c = 0; c < CPB; ++c) {
+      const int q = CPB * wave + c;
+      copy16(rsB, rb + b_k[c] < span ? b_off[c] + bstep : OOB,
+             bt + (q / CPS) * (BK * NS * 2) + 1024 * (q % CPS));
+    }
+  };
+  typedef FragSet<FM, FN> F;
+  auto load = [&](int slot, int st, F& f) {
+    const bf16_t* at = smem + slot * Cfg::A_EL;
+    const bf16_t* bt = smem + ST * Cfg::A_EL + slot * Cfg::B_EL;
+    const int kk = 16 * st;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int col = wm * TM + 32 * i;
+      f.x[i] = frag_n(at + (col / NS) * (BK * NS), kk, col % NS, lane);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = wn * TN + 32 * j;
+      f.w[j] = frag_n(bt + (col / NS) * (BK * NS), kk, col % NS, lane);
+    }
+  };
+  auto mma = [&](const F& f) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
+  };
+  if (nk > 0) k_loop<ST, Cfg::CP, BK / 16, F>(nk, issue, load, mma);
+
+  // epilogue (f32), staged through LDS as in gemm_rows_kernel: acc[i][j][4q + t] is C row
+  // i0 + wm*TM + 32 i + lane%32, column n0 + wn*TN + 32 j + 8 q + 4 (lane/32) + t.  Read back with TN/8 lanes
+  // per row, each lane storing 8 contiguous f32.
+  __syncthreads();  // all waves are done with the ring
+  float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * SP);
+  constexpr int LPR = TN / 8, RPP = 64 / LPR, PASSES = 32 / RPP;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    if (i > 0) __builtin_amdgcn_wave_barrier();
+    park<Cfg>(stg, acc, i, lane);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int r = RPP * p + lane / LPR, c = 8 * (lane % LPR);
+      const int64_t row = i0 + wm * TM + 32 * i + r;
+      if (row >= I) continue;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t col = n0 + wn * TN + c + 4 * h;
+        if (col >= N) continue;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * SP + c + 4 * h);
+        float* dst;
+        if (a.S > 1) dst = a.part + (((int64_t)s * a.E + e) * I + row) * N + col;
+        else if (a.C2 && col >= a.n_split) dst = a.C2 + (int64_t)e * a.c_estride + row * a.ldc + (col - a.n_split);
+        else dst = a.C + (int64_t)e * a.c_estride + row * a.ldc + col;
+        *reinterpret_cast<f32x4*>(dst) = v;
+      }
+    }
+  }
+}
+
+}  // namespace lsgemm

@@ -53,16 +53,52 @@ __global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__
                                                            int32_t* __restrict__ blk_expert,
                                                            int32_t* __restrict__ blk_rows,
                                                            int32_t* __restrict__ num_blocks, int max_blocks) {
-  __shared__ int32_t gs_s[LT_EMAX], off_s[LT_EMAX], boff_s[LT_EMAX + 1];
+  __shared__ int32_t gs_s[LT_EMAX], off_s[LT_EMAX], boff_s[LT_EMAX + 1], part_s[1024];
   const int tid = threadIdx.x;
+  // Per-expert exclusive scan over chunks, split over tpe threads per expert (thread (e, j) owns a contiguous
+  // range of chunks): a partial sum per range, an exclusive scan of the tpe partials, then each range rewritten
+  // with its running base.  Loads within a range are issued 8 at a time, so the walk is not a chain of
+  // dependent global round trips.
+  int tpe = 1;
+  while (tpe * 2 * E <= (int)blockDim.x && tpe < 64) tpe *= 2;
+  const int e_t = tid % E, j_t = tid / E;
+  const bool scan_lane = j_t < tpe;
+  const int cpt = (nchunk + tpe - 1) / tpe;
+  const int c0 = j_t * cpt, c1 = min(nchunk, c0 + cpt);
+  if (scan_lane) {
+    int sum = 0;
+    for (int c = c0; c < c1; c += 8) {
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum += v[u];
+    }
+    part_s[j_t * E + e_t] = sum;
+  }
+  __syncthreads();
   for (int e = tid; e < E; e += blockDim.x) {
     int run = 0;
-    for (int c = 0; c < nchunk; ++c) {
-      const int v = hist[(int64_t)c * E + e];
-      hist[(int64_t)c * E + e] = run;
+    for (int j = 0; j < tpe; ++j) {
+      const int v = part_s[j * E + e];
+      part_s[j * E + e] = run;
       run += v;
     }
     gs_s[e] = run;
+  }
+  __syncthreads();
+  if (scan_lane) {
+    int run = part_s[j_t * E + e_t];
+    for (int c = c0; c < c1; c += 8) {
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (c + u < c1) hist[(int64_t)(c + u) * E + e_t] = run;
+        run += v[u];
+      }
+    }
   }
   __syncthreads();
   if (tid == 0) {  // E <= 1024: a serial scan is a few microseconds at most
