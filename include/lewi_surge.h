@@ -205,7 +205,6 @@ typedef struct {
   int32_t* row_src;    /* [128*max_blocks] */
   int32_t* blk_expert, *blk_rows;             /* [max_blocks] */
   int32_t* num_blocks; /* [1] */
-  void* x_pad;         /* [128*max_blocks, d] bf16 dispatched rows */
   void* h_gate;        /* [128*max_blocks, f] bf16 x.W_gate */
   void* h_up;          /* [128*max_blocks, f] bf16 x.W_up */
   void* h;             /* [128*max_blocks, f] bf16 silu(gate)*up */

@@ -37,7 +37,7 @@ class MoeGrads(ctypes.Structure):
 
 class MoeSavedViews(ctypes.Structure):
     _fields_ = [(n, _p) for n in ("logits", "sel", "weights", "group_sizes", "offsets", "block_off", "order", "pos",
-                                  "slot", "row_src", "blk_expert", "blk_rows", "num_blocks", "x_pad", "h_gate", "h_up",
+                                  "slot", "row_src", "blk_expert", "blk_rows", "num_blocks", "h_gate", "h_up",
                                   "h", "y_pad")]
 
 

@@ -2,6 +2,7 @@
 // grid sizes, the split-K reduction of dense weight gradients, and the ragged_dot entry points that replace
 // modal/padded_gmm.py:45-69 (padded_ragged_dot and its gather-only VJP).
 #include "gemm_kernels.h"
+#include "launchers.h"
 
 namespace {
 using namespace lsgemm;
@@ -76,14 +77,6 @@ inline unsigned pad8(int64_t g) { return (unsigned)((g + 7) / 8 * 8); }
 // ------------------------------------------------------------------------------ internal launchers
 namespace lsurge {
 
-struct GemmBlocks {
-  const int32_t* blk_expert;
-  const int32_t* blk_rows;
-  const int32_t* blk_row0;
-  const int32_t* num_blocks;
-  int max_blocks;
-  int64_t dense_rows;  // used when blk_expert == nullptr
-};
 
 static int check_gemm_shape(int64_t K, int64_t N, const char* what) {
   LSURGE_REQUIRE(K > 0 && N > 0 && K % 8 == 0 && N % 8 == 0, "%s: K=%lld N=%lld must be positive multiples of 8", what,
@@ -121,13 +114,19 @@ int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
   return LSURGE_OK;
 }
 
-// h = silu(A @ Bg) * (A @ Bu); also stores g, u.  Bg, Bu: [K, N] per expert.
+// h = silu(A @ Bg) * (A @ Bu); also stores g, u.  Bg, Bu: [K, N] per expert.  With a gather (gather.rows set),
+// tile row r reads A[gather.rows[row0 + r] / gather.div] of an A with gather.nrows rows (negative: zero row).
 int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* Bg, const void* Bu,
                          int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* H, void* Gs, void* Us,
-                         int64_t ldh, hipStream_t s) {
+                         int64_t ldh, hipStream_t s, const RowGather& gather) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_swiglu_fwd")) return rc;
   if (int rc = check_desc(std::max<int64_t>(BM * lda, K * ldb) * 2, "gemm_rows_swiglu_fwd")) return rc;
+  if (gather.rows) {
+    LSURGE_REQUIRE(gather.div >= 1 && gather.nrows >= 1, "gemm_rows_swiglu_fwd: bad row gather");
+    if (int rc = check_desc(gather.nrows * lda * 2, "gemm_rows_swiglu_fwd gather")) return rc;
+  }
   RowsArgs a{};
+  a.a_rows = gather.rows; a.a_nrows = gather.nrows; a.a_div = gather.div;
   a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)Bg; a.B2 = (const bf16_t*)Bu; a.ldb = ldb;
   a.b_estride = b_estride; a.K = K; a.N = N; a.C = (bf16_t*)H; a.ldc = ldh; a.G = (bf16_t*)Gs; a.U = (bf16_t*)Us;
   a.ldg = ldh;
@@ -176,11 +175,16 @@ size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S) {
 int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
                int64_t max_rows, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N, float* C,
                float* C2, int64_t n_split, int64_t ldc, int64_t c_estride, int S, void* ws, size_t ws_bytes,
-               hipStream_t s) {
+               hipStream_t s, const RowGather& gather) {
   if (int rc = check_gemm_shape(I, N, "gemm_wgrad")) return rc;
   if (int rc = check_desc(max_rows * std::max(lda, ldb) * 2, "gemm_wgrad")) return rc;
   LSURGE_REQUIRE(S >= 1 && E >= 1, "gemm_wgrad: bad S/E");
+  if (gather.rows) {
+    LSURGE_REQUIRE(gather.div >= 1 && gather.nrows >= 1 && e_rows, "gemm_wgrad: bad row gather");
+    if (int rc = check_desc(gather.nrows * lda * 2, "gemm_wgrad gather")) return rc;
+  }
   WgradArgs a{};
+  a.a_rows = gather.rows; a.a_nrows = gather.nrows; a.a_div = gather.div;
   a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.I = I; a.N = N; a.C = C; a.C2 = C2;
   a.n_split = n_split; a.ldc = ldc; a.c_estride = c_estride; a.e_row0 = e_row0; a.e_rows = e_rows;
   a.row0_mult = row0_mult;
@@ -277,7 +281,7 @@ int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group
   }
   // drhs[e] = lhs_e^T @ g_e
   return lsurge::gemm_wgrad(KID_MISC, (int)e, e_row0, 1, e_rows, 0, m, lhs, kdim, g, n, kdim, n, drhs, nullptr, 0, n,
-                            kdim * n, 1, nullptr, 0, s);
+                            kdim * n, 1, nullptr, 0, s, lsurge::RowGather());
 }
 
 }  // extern "C"

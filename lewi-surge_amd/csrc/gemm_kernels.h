@@ -72,6 +72,9 @@ struct RowsArgs {
   const int32_t* t_rows;     // valid rows of tile t
   const int32_t* t_row0;     // first row of tile t (nullptr: BM t)
   const int32_t* num_tiles;  // device-side tile count
+  const int32_t* a_rows;     // row gather: A row r of the tile is A[a_rows[row0 + r] / a_div] (< 0: zero row),
+  int64_t a_nrows;           // A spans a_nrows rows; nullptr: the tile's rows are A[row0 .. row0 + rows)
+  int a_div;
   int64_t dense_rows;
   int n_tiles;               // column tiles
   int max_tiles;             // row tiles the grid covers
@@ -93,6 +96,9 @@ struct WgradArgs {
   int row0_mult;
   int64_t dense_rows;
   int E, S, i_tiles, n_tiles;
+  const int32_t* a_rows;  // row gather of A: reduction row r (an index into the expert's row range) reads
+  int64_t a_nrows;        // A[a_rows[r] / a_div] of an A with a_nrows rows; nullptr: A's rows are contiguous
+  int a_div;
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -167,9 +173,16 @@ __device__ __forceinline__ u32x4 make_rsrc(const void* base, int64_t bytes) {
 // One 1 KiB copy: lane p's 16 bytes at byte_off of the buffer land at LDS byte address m0 + 16 p.  m0 is the
 // wave-uniform LDS address of the destination (the LDS base of the kernel's array plus a constant offset).
 __device__ __forceinline__ void copy16(u32x4 rsrc, uint32_t byte_off, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(rsrc), "s"(m0)
+  // m0 is uniform by construction; readfirstlane states it for the compiler (free when already scalar)
+  const uint32_t m0s = (uint32_t)__builtin_amdgcn_readfirstlane(m0);
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(rsrc), "s"(m0s)
                : "memory");
 }
+// n / d for 0 <= n < 2^31 and 1 <= d <= 256 as one 64-bit multiply: with m = ceil(2^40 / d),
+// n m / 2^40 = n / d + n (m - 2^40 / d) / 2^40, and the error term stays below 1 / d for n < 2^40 / d.
+__device__ __forceinline__ uint64_t div_magic(int d) { return ((1ull << 40) + (uint64_t)d - 1) / (uint64_t)d; }
+__device__ __forceinline__ int div_by(int n, uint64_t magic) { return (int)(((uint64_t)(uint32_t)n * magic) >> 40); }
+
 // LDS byte address of the kernel's shared array, as a scalar
 __device__ __forceinline__ uint32_t lds_addr(const bf16_t* p) {
   return (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(size_t)LDS_PTR(const void, p));
@@ -316,7 +329,7 @@ void gemm_rows_kernel(RowsArgs a) {
   const uint32_t lds0 = lds_addr(smem);
 
   // descriptors: this tile's rows of A; the expert's B (and B2) matrix
-  const u32x4 rsA = make_rsrc(a.A + row0 * a.lda, (int64_t)rows * a.lda * 2);
+  const u32x4 rsA = a.a_rows ? make_rsrc(a.A, a.a_nrows * a.lda * 2) : make_rsrc(a.A + row0 * a.lda, (int64_t)rows * a.lda * 2);
   const int64_t b_bytes = (int64_t)(BMODE == B_NK ? N : K) * a.ldb * 2;
   const u32x4 rsB = make_rsrc(Bbase, b_bytes);
   const u32x4 rsB2 = make_rsrc(B2base, b_bytes);
@@ -330,8 +343,15 @@ void gemm_rows_kernel(RowsArgs a) {
   for (int c = 0; c < CPA; ++c) {
     const int r = RPC * (CPA * wave + c) + lane / CPR;
     const int kc = (lane % CPR) ^ km_swz<BK>(r);
-    a_off[c] = (uint32_t)(r * lda + 8 * kc) * 2u;
-    a_k[c] = r < rows ? 8 * kc : KBIG;
+    if (a.a_rows) {  // gathered rows: the source row of tile row r (padding rows and rows past the tile: zeros)
+      const int flat = r < rows ? a.a_rows[row0 + r] : -1;
+      const int src = flat >= 0 ? div_by(flat, div_magic(a.a_div)) : -1;
+      a_off[c] = (uint32_t)(max(src, 0) * lda + 8 * kc) * 2u;
+      a_k[c] = src >= 0 ? 8 * kc : KBIG;
+    } else {
+      a_off[c] = (uint32_t)(r * lda + 8 * kc) * 2u;
+      a_k[c] = r < rows ? 8 * kc : KBIG;
+    }
   }
   // B K-major: as A over n.  B N-major: copy q fills k rows 4 (q % CPS) + lane / 16 of sub-tile q / CPS, slot
   // lane % 16 (SwiGLU forward: sub-tiles [0, NSUB/2) gate, [NSUB/2, NSUB) up, same output columns).
@@ -548,10 +568,30 @@ void gemm_wgrad_kernel(WgradArgs a) {
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
 
   const int nk = re > rs ? (int)((re - rs + BK - 1) / BK) : 0;
-  // descriptors over rows [rs, re) of this expert (empty when the split has no rows)
+  // descriptors over rows [rs, re) of this expert (empty when the split has no rows); a gathered A spans the
+  // whole source matrix and its row indices come through an LDS window (below)
   const int span = re > rs ? (int)(re - rs) : 0;
-  const u32x4 rsA = make_rsrc(a.A + (r0 + rs) * a.lda, (int64_t)span * a.lda * 2);
+  const bool gath = a.a_rows != nullptr;
+  const u32x4 rsA = gath ? make_rsrc(a.A, a.a_nrows * a.lda * 2) : make_rsrc(a.A + (r0 + rs) * a.lda, (int64_t)span * a.lda * 2);
   const u32x4 rsB = make_rsrc(a.B + (r0 + rs) * a.ldb, (int64_t)span * a.ldb * 2);
+  // Gathered A: the row indices of the span pass through a double-buffered LDS window of 2 x 256 entries.  Wave 0
+  // copies window m (rows [256 m, 256 m + 256)) into buffer m % 2 when the first stage of window m - 1 is
+  // issued, i.e. SPW stages before its first use and after every wave is done with the buffer's previous
+  // window; the stage waits and barriers of the K loop then cover its completion like any other copy.
+  constexpr int SPW = 256 / BK;  // stages per window
+  __shared__ __attribute__((aligned(1024))) int32_t idxwin[512];
+  const uint32_t win0 = lds_addr(reinterpret_cast<const bf16_t*>(idxwin));
+  const u32x4 rsI = make_rsrc(gath ? a.a_rows + r0 + rs : nullptr, gath ? (int64_t)span * 4 : 0);
+  const uint64_t magic = div_magic(gath ? a.a_div : 1);
+  int nidx[Cfg::CPA];  // gathered A: row indices of the next stage to issue (this lane's rows)
+  if (gath) {
+    if (wave == 0) {
+      copy16(rsI, 16u * lane, win0);
+      copy16(rsI, 1024u + 16u * lane, win0 + 1024);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
   // copy q of an operand fills k rows 4 (q % CPS) + lane / 16 of sub-tile q / CPS, slot lane % 16: byte offset of
   // this lane's chunk at row 0 of the span and its row in a stage (KBIG when its column is outside the operand)
   uint32_t a_off[CPA], b_off[CPB];
@@ -561,7 +601,7 @@ void gemm_wgrad_kernel(WgradArgs a) {
     const int q = CPA * wave + c, sub = q / CPS;
     const int k = 4 * (q % CPS) + (lane >> 4);
     const int64_t ic = i0 + NS * sub + 8 * ((lane & 15) ^ ((k & 3) << 2));
-    a_off[c] = (uint32_t)(k * lda + ic) * 2u;
+    a_off[c] = gath ? (uint32_t)ic * 2u : (uint32_t)(k * lda + ic) * 2u;  // gathered: the row part comes later
     a_k[c] = ic < I ? k : KBIG;
   }
 #pragma unroll
@@ -572,15 +612,38 @@ void gemm_wgrad_kernel(WgradArgs a) {
     b_off[c] = (uint32_t)(k * ldb + nc) * 2u;
     b_k[c] = nc < N ? k : KBIG;
   }
+#pragma unroll
+  for (int c = 0; c < CPA; ++c) nidx[c] = gath ? idxwin[a_k[c] & 511] : 0;  // stage 0
   auto issue = [&](int slot, int kt) {
     const int rb = kt * BK;
     const uint32_t at = lds0 + slot * A_SLOT, bt = lds0 + B_RING + slot * B_SLOT;
     const uint32_t astep = 2u * (uint32_t)rb * (uint32_t)lda, bstep = 2u * (uint32_t)rb * (uint32_t)ldb;
+    if (gath) {
+      // the window holding stage kt's rows is resident; refill the other buffer with the window after it
+      if (kt % SPW == 0 && kt >= SPW && wave == 0) {
+        const int m = kt / SPW + 1;
+        copy16(rsI, 1024u * m + 16u * lane, win0 + 1024u * (m & 1));
+      }
 #pragma unroll
-    for (int c = 0; c < CPA; ++c) {
-      const int q = CPA * wave + c;
-      copy16(rsA, rb + a_k[c] < span ? a_off[c] + astep : OOB,
-             at + (q / CPS) * (BK * NS * 2) + 1024 * (q % CPS));
+      for (int c = 0; c < CPA; ++c) {
+        const int q = CPA * wave + c;
+        const int rr = rb + a_k[c];
+        const int idx = nidx[c];  // read one stage earlier
+        const bool ok = rr < span && idx >= 0;
+        copy16(rsA, ok ? (uint32_t)div_by(idx, magic) * (2u * (uint32_t)lda) + a_off[c] : OOB,
+               at + (q / CPS) * (BK * NS * 2) + 1024 * (q % CPS));
+      }
+      // indices of the next stage: its window is resident (copied at least SPW - 1 stages ago, and this step's
+      // barrier has passed), so the LDS reads overlap this stage instead of stalling the next copy issue
+#pragma unroll
+      for (int c = 0; c < CPA; ++c) nidx[c] = idxwin[(rb + BK + a_k[c]) & 511];
+    } else {
+#pragma unroll
+      for (int c = 0; c < CPA; ++c) {
+        const int q = CPA * wave + c;
+        copy16(rsA, rb + a_k[c] < span ? a_off[c] + astep : OOB,
+               at + (q / CPS) * (BK * NS * 2) + 1024 * (q % CPS));
+      }
     }
 #pragma unroll
     for (int c = 0; c < CPB; ++c) {

@@ -1,0 +1,56 @@
+// Internal launchers shared by the translation units of the library (not part of the C ABI): the layer
+// (moe_layer.hip) composes them; layout.hip, permute.hip and gemm.hip define them.
+#pragma once
+#include "common.h"
+
+namespace lsurge {
+
+// ---- routing layout (layout.hip)
+int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
+                      int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
+                      int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s);
+
+// ---- row movement (permute.hip)
+int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src, const int32_t* num_blocks,
+                        int64_t max_rows, void* xp, hipStream_t s);
+int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, const float* w, int64_t n,
+                       const void* add, void* out, int out_dtype, hipStream_t s);
+int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
+                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s);
+int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* slot, int64_t n, const float* dl,
+                            const int32_t* sel, const void* w_rT, const void* add, void* dx, hipStream_t s);
+int launch_transpose_bf16(const void* a, int R, int C, void* at, hipStream_t s);
+int launch_scatter_dlogits(const float* dl, const int32_t* sel, int64_t T, int E, int k, void* dlog, hipStream_t s);
+
+// ---- grouped GEMMs (gemm.hip)
+// Row tiles: the padded 128-row expert blocks (blk_expert set) or a dense matrix of dense_rows rows.
+struct GemmBlocks {
+  const int32_t* blk_expert;
+  const int32_t* blk_rows;
+  const int32_t* blk_row0;   // first row of block b (nullptr: 128 b)
+  const int32_t* num_blocks;
+  int max_blocks;
+  int64_t dense_rows;        // used when blk_expert == nullptr
+};
+// Optional row gather of the A operand: row r of the rows operand (a tile row of gemm_rows, a reduction row of an
+// expert in gemm_wgrad) reads A[rows[r] / div], indexed by padded row (negative index: zero row).
+struct RowGather {
+  const int32_t* rows = nullptr;
+  int div = 1;
+  int64_t nrows = 0;  // rows of the gathered-from matrix
+};
+int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, int64_t ldb,
+                 int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32 = false);
+int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* Bg, const void* Bu,
+                         int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* H, void* Gs, void* Us,
+                         int64_t ldh, hipStream_t s, const RowGather& gather = RowGather());
+int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
+                 int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
+                 bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false);
+size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S);
+int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
+               int64_t max_rows, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N,
+               float* C, float* C2, int64_t n_split, int64_t ldc, int64_t c_estride, int S, void* ws, size_t ws_bytes,
+               hipStream_t s, const RowGather& gather = RowGather());
+
+}  // namespace lsurge

@@ -11,7 +11,7 @@
 //   rank  one workgroup per chunk again; each wave walks its slots 64 at a time in ascending slot order:
 //         lanes with the same expert are found with 8 ballots over the expert-id bits, the rank inside
 //         the wave is popcount(peers below me), and a per-wave LDS counter advances by popcount(peers).
-#include "common.h"
+#include "launchers.h"
 
 namespace {
 

@@ -1,8 +1,8 @@
 // Whole MoE layer, forward and gather-only backward, as one stream-ordered sequence of the hot-path kernels.
 //
-// Forward:  router top-k -> routing layout -> dispatch into 128-row expert blocks -> gate/up grouped GEMM with
-//           the SiLU*mul epilogue -> down grouped GEMM -> weighted combine (+ shared expert, the dense E = 1 case
-//           of the same GEMMs).
+// Forward:  router top-k -> routing layout -> gate/up grouped GEMM over 128-row expert blocks whose rows are
+//           gathered from x (the dispatch, fused into the GEMM's operand load) with the SiLU*mul epilogue -> down
+//           grouped GEMM -> weighted combine (+ shared expert, the dense E = 1 case of the same GEMMs).
 // Backward: fused combine backward (dY rows, d(routing weights), d(router logits)) -> down dgrad with the
 //           SwiGLU backward epilogue -> down wgrad -> gate/up dgrad -> gate/up wgrad -> shared expert ->
 //           router wgrad -> dispatch backward (gather-reduce, plus the router and shared-expert dx terms).
@@ -13,44 +13,7 @@
 // moe_permute.moe_block (modal/moe_permute.py:348-353) with a SwiGLU expert_fn.
 #include <cstring>
 
-#include "common.h"
-
-namespace lsurge {
-int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
-                      int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
-                      int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s);
-int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src, const int32_t* num_blocks,
-                        int64_t max_rows, void* xp, hipStream_t s);
-int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, const float* w, int64_t n,
-                       const void* add, void* out, int out_dtype, hipStream_t s);
-int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
-                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s);
-int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* slot, int64_t n, const float* dl,
-                            const int32_t* sel, const void* w_rT, const void* add, void* dx, hipStream_t s);
-int launch_transpose_bf16(const void* a, int R, int C, void* at, hipStream_t s);
-int launch_scatter_dlogits(const float* dl, const int32_t* sel, int64_t T, int E, int k, void* dlog, hipStream_t s);
-
-struct GemmBlocks {
-  const int32_t* blk_expert;
-  const int32_t* blk_rows;
-  const int32_t* blk_row0;
-  const int32_t* num_blocks;
-  int max_blocks;
-  int64_t dense_rows;
-};
-int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, int64_t ldb,
-                 int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32 = false);
-int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* Bg, const void* Bu,
-                         int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* H, void* Gs, void* Us,
-                         int64_t ldh, hipStream_t s);
-int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
-                 int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
-                 bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false);
-size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S);
-int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
-               int64_t max_rows, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2,
-               int64_t n_split, int64_t ldc, int64_t c_estride, int S, void* ws, size_t ws_bytes, hipStream_t s);
-}  // namespace lsurge
+#include "launchers.h"
 
 namespace {
 
@@ -87,7 +50,7 @@ struct Saved {
   int32_t *sel;
   float* weights;
   int32_t *gs, *offsets, *block_off, *order, *pos, *slot, *row_src, *blk_expert, *blk_rows, *num_blocks;
-  bf16_t *x_pad, *g, *u, *h, *y_pad;
+  bf16_t *g, *u, *h, *y_pad;
   bf16_t *sg, *su, *sh, *sy;  // shared expert: gate, up, h, output
 };
 
@@ -106,7 +69,6 @@ size_t carve_saved(const Dims& q, void* base, Saved* sv) {
   sv->blk_expert = c.take<int32_t>(q.MB);
   sv->blk_rows = c.take<int32_t>(q.MB);
   sv->num_blocks = c.take<int32_t>(4);
-  sv->x_pad = c.take<bf16_t>(q.P * q.d);
   sv->g = c.take<bf16_t>(q.P * q.f);
   sv->u = c.take<bf16_t>(q.P * q.f);
   sv->h = c.take<bf16_t>(q.P * q.f);
@@ -203,7 +165,7 @@ int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_s
   carve_saved(dims_of(s), saved, &sv);
   v->logits = sv.logits; v->sel = sv.sel; v->weights = sv.weights; v->group_sizes = sv.gs; v->offsets = sv.offsets;
   v->block_off = sv.block_off; v->order = sv.order; v->pos = sv.pos; v->slot = sv.slot; v->row_src = sv.row_src;
-  v->blk_expert = sv.blk_expert; v->blk_rows = sv.blk_rows; v->num_blocks = sv.num_blocks; v->x_pad = sv.x_pad;
+  v->blk_expert = sv.blk_expert; v->blk_rows = sv.blk_rows; v->num_blocks = sv.num_blocks;
   v->h_gate = sv.g; v->h_up = sv.u; v->h = sv.h; v->y_pad = sv.y_pad;
   return LSURGE_OK;
 }
@@ -228,8 +190,12 @@ struct ForkGuard {
 
 extern "C" {
 
-// Forward.  Stream plan: the shared expert (dense, depends on x only) runs on a helper stream while the routed
-// chain (router -> layout -> dispatch -> gate/up -> down) runs on the caller's stream; the combine joins both.
+// Forward.  Stream plan:
+//   main: router -> layout -> gate/up GEMM -> down GEMM -> [join] -> combine
+//   s0:   shared expert (depends on x only)
+// The dispatch into padded expert blocks is fused into the gate/up GEMM: its A tiles are gathered straight from
+// the token rows x through row_src (padded row -> flat slot t*k + j), so the padded copy of x is never
+// materialised (the backward's gate/up weight gradient gathers the same way).
 int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* out, void* saved, size_t saved_bytes,
                    void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
   if (int rc = check_shape(s)) return rc;
@@ -245,8 +211,8 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   if (int rc = fg.acquire(st)) return rc;
   hipStream_t s0 = fg.f.side[0];
 
+  if (int rc = lsurge::stream_after(s0, st, fg.f.ev[0])) return rc;
   if (q.fs) {
-    if (int rc = lsurge::stream_after(s0, st, fg.f.ev[0])) return rc;
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
     if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
                                               q.fs, sv.sh, sv.sg, sv.su, q.fs, s0))
@@ -261,25 +227,29 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
                                          sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks, workspace,
                                          workspace_bytes, st))
     return rc;
-  if (int rc = lsurge::launch_dispatch_pad(p->x, q.d, (int)q.k, sv.row_src, sv.num_blocks, q.P, sv.x_pad, st)) return rc;
   const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
-  if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_GEMM_GU_FWD, blocks, sv.x_pad, q.d, p->w_gate, p->w_up, q.f, q.d * q.f,
-                                            q.d, q.f, sv.h, sv.g, sv.u, q.f, st))
+  lsurge::RowGather gather;
+  gather.rows = sv.row_src;
+  gather.div = (int)q.k;
+  gather.nrows = q.T;
+  if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_GEMM_GU_FWD, blocks, p->x, q.d, p->w_gate, p->w_up, q.f, q.d * q.f,
+                                            q.d, q.f, sv.h, sv.g, sv.u, q.f, st, gather))
     return rc;
   if (int rc = lsurge::gemm_rows_kn(KID_GEMM_DOWN_FWD, blocks, sv.h, q.f, p->w_down, q.d, q.f * q.d, q.f, q.d, sv.y_pad,
                                     q.d, st))
     return rc;
-  if (q.fs)
-    if (int rc = lsurge::stream_after(st, s0, fg.f.ev[1])) return rc;
+  if (int rc = lsurge::stream_after(st, s0, fg.f.ev[1])) return rc;
   return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sv.sy : nullptr, out,
                                     LSURGE_BF16, st);
 }
 
 // Backward.  Stream plan (caller's stream = critical path):
-//   main:  combine bwd -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd
+//   main:  combine bwd -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
 //   s0:    shared expert: down dgrad, down wgrad, gate/up dgrad, gate/up wgrad   (needs dy only)
 //   s1:    W_r transpose; after combine bwd: down wgrad, d(logits) scatter, router wgrad
-//   s2:    after down dgrad: gate/up wgrad
+// The helper chains overlap the first two kernels of the main chain; the two largest GEMMs run after them on
+// their own (every GEMM here is bound by the operand-copy path, so overlapping two of them gains little), and
+// the dispatch backward reads dX_pad right after the GEMM that wrote it, while it is still in cache.
 int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* dy, const void* saved,
                    const lsurge_moe_grads* g, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
   if (int rc = check_shape(s)) return rc;
@@ -299,7 +269,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
   ForkGuard fg;
   if (int rc = fg.acquire(st)) return rc;
-  hipStream_t s0 = fg.f.side[0], s1 = fg.f.side[1], s2 = fg.f.side[2];
+  hipStream_t s0 = fg.f.side[0], s1 = fg.f.side[1];
   hipEvent_t* ev = fg.f.ev;
 
   // fork: the helper streams start after everything the caller enqueued before this call
@@ -347,11 +317,6 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   if (int rc = lsurge::gemm_rows_nk(KID_GEMM_DOWN_DGRAD, blocks, w.dy_pad, q.d, p->w_down, nullptr, 0, q.d, q.f * q.d,
                                     q.d, q.f, w.dgu, 2 * q.f, true, sv.g, sv.u, q.f, st))
     return rc;
-  if (int rc = lsurge::stream_after(s2, st, ev[3])) return rc;
-  // s2: gate/up wgrad: [dW_gate | dW_up][e] = x_e^T [dG | dU]_e
-  if (int rc = lsurge::gemm_wgrad(KID_GEMM_GU_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, sv.x_pad, q.d, w.dgu,
-                                  2 * q.f, q.d, 2 * q.f, g->dw_gate, g->dw_up, q.f, q.f, q.d * q.f, 1, nullptr, 0, s2))
-    return rc;
   // main: gate/up dgrad: dX_pad = dG W_gate^T + dU W_up^T
   if (int rc = lsurge::gemm_rows_nk(KID_GEMM_GU_DGRAD, blocks, w.dgu, 2 * q.f, p->w_gate, p->w_up, q.f, q.f, q.d * q.f,
                                     2 * q.f, q.d, w.dx_pad, q.d, false, nullptr, nullptr, 0, st))
@@ -359,9 +324,21 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   // join all helpers, then dx = gather-reduce of dX_pad + router dx term + shared-expert dx, one rounding
   if (int rc = lsurge::stream_after(st, s0, ev[4])) return rc;
   if (int rc = lsurge::stream_after(st, s1, ev[5])) return rc;
-  if (int rc = lsurge::stream_after(st, s2, ev[6])) return rc;
-  return lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT,
-                                         q.fs ? w.sdx : nullptr, g->dx, st);
+  if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT,
+                                              q.fs ? w.sdx : nullptr, g->dx, st))
+    return rc;
+  // main: gate/up wgrad: [dW_gate | dW_up][e] = x_e^T [dG | dU]_e
+  {
+    lsurge::RowGather gather;  // x_e rows gathered from x through row_src, as in the forward
+    gather.rows = sv.row_src;
+    gather.div = (int)q.k;
+    gather.nrows = q.T;
+    if (int rc = lsurge::gemm_wgrad(KID_GEMM_GU_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, p->x, q.d, w.dgu,
+                                    2 * q.f, q.d, 2 * q.f, g->dw_gate, g->dw_up, q.f, q.f, q.d * q.f, 1, nullptr, 0, st,
+                                    gather))
+      return rc;
+  }
+  return LSURGE_OK;
 }
 
 }  // extern "C"

@@ -5,7 +5,7 @@
 // On CDNA a row is moved by one wave with 16-byte vector accesses (coalesced 1 KiB per instruction); there
 // is no need for the TPU's bf16 u32 packing (moe_permute.py:68-84).  All reductions run in f32 with the
 // choice index j ascending, the order of moe_permute.py:189-200.
-#include "common.h"
+#include "launchers.h"
 
 namespace {
 

@@ -147,7 +147,7 @@ class MoELayer:
             order=view("order", i32, (s.m,)), pos=view("pos", i32, (s.m,)), slot=view("slot", i32, (s.m,)),
             row_src=view("row_src", i32, (p_rows,)), blk_expert=view("blk_expert", i32, (mb,)),
             blk_rows=view("blk_rows", i32, (mb,)), num_blocks=view("num_blocks", i32, (1,)),
-            x_pad=view("x_pad", b16, (p_rows, s.d)), h_gate=view("h_gate", b16, (p_rows, s.f)),
+            h_gate=view("h_gate", b16, (p_rows, s.f)),
             h_up=view("h_up", b16, (p_rows, s.f)), h=view("h", b16, (p_rows, s.f)),
             y_pad=view("y_pad", b16, (p_rows, s.d)))
 
