@@ -72,6 +72,87 @@ __global__ void zero_rows_from_kernel(void* __restrict__ out, int64_t m, int64_t
 
 inline unsigned pad8(int64_t g) { return (unsigned)((g + 7) / 8 * 8); }
 
+// Chunk table of the routed weight gradients (one workgroup of 256 threads, thread e = expert e).  Expert e owns
+// padded rows [128 block_off[e], 128 block_off[e] + gs[e]); they are cut into ceil(gs[e] / R) chunks of R rows.
+// An empty expert keeps one empty chunk, which writes its zero gradient.  An expert with more than one chunk
+// gets consecutive partial slots (summed in chunk order by wgrad_chunk_reduce_kernel) and an entry in split_list
+// (ascending e).  The bounds max_chunks >= E + ceil(M / R) and max_parts >= 2 M / R hold for any group sizes that
+// sum to at most M; if the slots would not fit anyway (corrupt sizes), every expert is left as one unsplit chunk.
+__device__ __forceinline__ int block_excl_scan(int v, int* sh) {  // 256 threads; returns the exclusive prefix
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) sh[w] = x;
+  __syncthreads();
+  int base = 0;
+  for (int i = 0; i < w; ++i) base += sh[i];
+  const int total = sh[0] + sh[1] + sh[2] + sh[3];
+  __syncthreads();
+  if (tid == 0) sh[4] = total;
+  __syncthreads();
+  return base + x - v;
+}
+
+__global__ __launch_bounds__(256) void wgrad_chunks_kernel(
+    const int32_t* __restrict__ gs, const int32_t* __restrict__ block_off, int E, int R, int max_chunks,
+    int max_parts, int32_t* __restrict__ c_expert, int32_t* __restrict__ c_row0, int32_t* __restrict__ c_rows,
+    int32_t* __restrict__ c_part, int32_t* __restrict__ num_chunks, int32_t* __restrict__ e_pbase,
+    int32_t* __restrict__ e_nparts, int32_t* __restrict__ split_list, int32_t* __restrict__ num_split) {
+  __shared__ int sh[8];
+  const int e = threadIdx.x;
+  const int g = e < E ? max(gs[e], 0) : 0;
+  int n = e < E ? max(1, (g + R - 1) / R) : 0;
+  const int pbase = block_excl_scan(n > 1 ? n : 0, sh);
+  const bool fits = sh[4] <= max_parts;
+  if (!fits && n > 1) n = 1;
+  const int cbase = block_excl_scan(n, sh);
+  const int nchunks = sh[4];
+  const int sidx = block_excl_scan(n > 1 ? 1 : 0, sh);
+  if (e == 0) {
+    num_chunks[0] = min(nchunks, max_chunks);
+    num_split[0] = sh[4];
+  }
+  if (e >= E) return;
+  e_pbase[e] = pbase;
+  e_nparts[e] = n > 1 ? n : 0;
+  if (n > 1) split_list[sidx] = e;
+  for (int j = 0; j < n; ++j) {
+    const int c = cbase + j;
+    if (c >= max_chunks) break;
+    c_expert[c] = e;
+    c_row0[c] = block_off[e] * BM + j * R;
+    c_rows[c] = n > 1 ? min(R, g - j * R) : g;
+    c_part[c] = n > 1 ? pbase + j : -1;
+  }
+}
+
+// dW of each split expert = its chunk partials summed in chunk order (f32, deterministic), -> C (and C2 for
+// columns >= n_split).  Grid-stride over (split expert, 4-element group).
+__global__ void wgrad_chunk_reduce_kernel(const float* __restrict__ part, const int32_t* __restrict__ split_list,
+                                          const int32_t* __restrict__ num_split, const int32_t* __restrict__ e_pbase,
+                                          const int32_t* __restrict__ e_nparts, int64_t I, int64_t N,
+                                          float* __restrict__ C, float* __restrict__ C2, int64_t n_split, int64_t ldc,
+                                          int64_t c_estride) {
+  const int64_t IN = I * N, q4 = IN / 4;
+  const int64_t total = (int64_t)num_split[0] * q4;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < total; x += (int64_t)gridDim.x * blockDim.x) {
+    const int e = split_list[x / q4];
+    const int64_t o = (x % q4) * 4;
+    const float* p0 = part + (int64_t)e_pbase[e] * IN + o;
+    f32x4 v = *reinterpret_cast<const f32x4*>(p0);
+    const int np = e_nparts[e];
+    for (int q = 1; q < np; ++q) v += *reinterpret_cast<const f32x4*>(p0 + (int64_t)q * IN);
+    const int64_t row = o / N, col = o % N;
+    float* dst = (C2 && col >= n_split) ? C2 + e * c_estride + row * ldc + (col - n_split)
+                                        : C + e * c_estride + row * ldc + col;
+    *reinterpret_cast<f32x4*>(dst) = v;
+  }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------------ internal launchers
@@ -205,6 +286,87 @@ int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32
                   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(256), 0, s, (const float*)ws, S, E, I, N, C,
                                      C2, n_split, ldc, c_estride));
   }
+  return LSURGE_OK;
+}
+
+WgradChunkPlan wgrad_chunk_plan(int64_t M, int64_t E) {
+  WgradChunkPlan p;
+  // R: at least 4096 rows and at least twice the mean expert load (rounded to blocks), so balanced routings keep
+  // one chunk per expert; the M / 64 floor bounds the partial slots at 128
+  const int64_t mean2 = (2 * ((M + E - 1) / E) + BM - 1) / BM * BM;
+  const int64_t m64 = ((M + 63) / 64 + BM - 1) / BM * BM;
+  p.R = (int)std::max<int64_t>(4096, std::max(mean2, m64));
+  p.max_chunks = (int)(E + (M + p.R - 1) / p.R);
+  p.max_parts = (int)std::max<int64_t>(1, (2 * M + p.R - 1) / p.R);
+  return p;
+}
+
+size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E) {
+  return 4 * (size_t)p.max_chunks + 2 * (size_t)E + (size_t)p.max_parts + 2;
+}
+
+int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
+                       WgradChunks* ch, hipStream_t s) {
+  LSURGE_REQUIRE(E >= 1 && E <= 256, "wgrad chunks: E=%d must be in [1, 256]", E);
+  int32_t* t = table;
+  ch->c_expert = t; t += p.max_chunks;
+  ch->c_row0 = t; t += p.max_chunks;
+  ch->c_rows = t; t += p.max_chunks;
+  ch->c_part = t; t += p.max_chunks;
+  ch->e_pbase = t; t += E;
+  ch->e_nparts = t; t += E;
+  ch->split_list = t; t += p.max_parts;
+  ch->num_chunks = t;
+  ch->num_split = t + 1;
+  ch->max_chunks = p.max_chunks;
+  ch->max_parts = p.max_parts;
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(wgrad_chunks_kernel, dim3(1), dim3(256), 0, s, gs, block_off, E, p.R, p.max_chunks,
+                                   p.max_parts, (int32_t*)ch->c_expert, (int32_t*)ch->c_row0, (int32_t*)ch->c_rows,
+                                   (int32_t*)ch->c_part, (int32_t*)ch->num_chunks, (int32_t*)ch->e_pbase,
+                                   (int32_t*)ch->e_nparts, (int32_t*)ch->split_list, (int32_t*)ch->num_split));
+  return LSURGE_OK;
+}
+
+size_t wgrad_chunked_workspace_bytes(const WgradChunkPlan& p, int64_t I, int64_t N) {
+  return sizeof(float) * (size_t)p.max_parts * I * N;
+}
+
+// C_e[I, N] = A_e^T @ B_e over the chunks of a chunk table (see WgradArgs); split experts are summed from their
+// partials afterwards.  max_rows bounds the rows of any one chunk (the token count for routed rows: a chunk never
+// spans more rows than its expert, and a token picks an expert at most once).
+int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, const void* A, int64_t lda,
+                       const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
+                       int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s,
+                       const RowGather& gather) {
+  if (int rc = check_gemm_shape(I, N, "gemm_wgrad_chunked")) return rc;
+  if (int rc = check_desc(max_rows * std::max(lda, ldb) * 2, "gemm_wgrad_chunked")) return rc;
+  LSURGE_REQUIRE(E >= 1 && ch.max_chunks >= 1, "gemm_wgrad_chunked: bad E / chunk table");
+  LSURGE_REQUIRE(part && part_bytes >= sizeof(float) * (size_t)ch.max_parts * I * N,
+                 "gemm_wgrad_chunked: partial workspace %zu < %zu bytes", part_bytes,
+                 sizeof(float) * (size_t)ch.max_parts * I * N);
+  LSURGE_REQUIRE(!C2 || n_split % 4 == 0, "gemm_wgrad_chunked: n_split must be a multiple of 4");
+  if (gather.rows) {
+    LSURGE_REQUIRE(gather.div >= 1 && gather.nrows >= 1, "gemm_wgrad_chunked: bad row gather");
+    if (int rc = check_desc(gather.nrows * lda * 2, "gemm_wgrad_chunked gather")) return rc;
+  }
+  WgradArgs a{};
+  a.a_rows = gather.rows; a.a_nrows = gather.nrows; a.a_div = gather.div;
+  a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.I = I; a.N = N; a.C = C; a.C2 = C2;
+  a.n_split = n_split; a.ldc = ldc; a.c_estride = c_estride;
+  a.E = E; a.S = 1; a.part = (float*)part;
+  a.c_expert = ch.c_expert; a.c_row0 = ch.c_row0; a.c_rows = ch.c_rows; a.c_part = ch.c_part;
+  a.num_chunks = ch.num_chunks; a.max_chunks = ch.max_chunks;
+  a.i_tiles = (int)((I + BM - 1) / BM);
+  a.n_tiles = (int)((N + BN - 1) / BN);
+  const int64_t tiles = (int64_t)pad8(ch.max_chunks) * a.i_tiles * a.n_tiles;  // see the chunk tile order
+  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel<Cfg>, dim3((unsigned)tiles), dim3(GT), 0, s, a));
+  // grid-stride over the split experts' elements; small, since balanced routings split nothing
+  const unsigned grid = (unsigned)std::min<int64_t>((I * N / 4 + 255) / 256, 256);
+  LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
+                hipLaunchKernelGGL(wgrad_chunk_reduce_kernel, dim3(grid), dim3(256), 0, s, (const float*)part,
+                                   ch.split_list, ch.num_split, ch.e_pbase, ch.e_nparts, I, N, C, C2, n_split, ldc,
+                                   c_estride));
   return LSURGE_OK;
 }
 

@@ -99,6 +99,16 @@ struct WgradArgs {
   const int32_t* a_rows;  // row gather of A: reduction row r (an index into the expert's row range) reads
   int64_t a_nrows;        // A[a_rows[r] / a_div] of an A with a_nrows rows; nullptr: A's rows are contiguous
   int a_div;
+  // Chunk table (replaces e_row0 / e_rows / S when set): chunk c reduces rows [c_row0[c], c_row0[c] + c_rows[c])
+  // of expert c_expert[c] and writes C (c_part[c] < 0: the expert's only chunk) or the f32 partial slot
+  // part + c_part[c] * I * N, summed afterwards in chunk order.  Chunks of at most a few thousand rows keep
+  // one hot expert from serialising the whole launch behind its few tiles.
+  const int32_t* c_expert;
+  const int32_t* c_row0;
+  const int32_t* c_rows;
+  const int32_t* c_part;
+  const int32_t* num_chunks;  // device-side chunk count
+  int max_chunks;             // chunks the grid covers
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -298,15 +308,25 @@ void gemm_rows_kernel(RowsArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16_t smem[Cfg::SMEM_EL];
   constexpr uint32_t A_SLOT = Cfg::A_EL * 2, B_SLOT = Cfg::B_EL * 2, B_RING = ST * A_SLOT;  // bytes
 
-  const int64_t total = (int64_t)gridDim.x;
-  const int64_t logical = xcd_logical(blockIdx.x, total);
+  // XCD-aware tile order over the tiles that exist: with a tile table the grid covers the bound max_tiles, but only
+  // num_tiles row tiles are real, so the per-XCD ranges are cut from the device-side count (an XCD whose range
+  // would start past the real tiles would otherwise sit idle while the others take its share).
+  int64_t logical;
+  if (a.t_expert) {
+    const int64_t real = (int64_t)min(a.num_tiles[0], a.max_tiles) * a.n_tiles;
+    const int64_t per = (real + 7) / 8, l = blockIdx.x / 8;
+    if (l >= per) return;
+    logical = (blockIdx.x % 8) * per + l;
+    if (logical >= real) return;
+  } else {
+    logical = xcd_logical(blockIdx.x, (int64_t)gridDim.x);
+  }
   const int nt = (int)(logical % a.n_tiles);
   const int b = (int)(logical / a.n_tiles);
   if (b >= a.max_tiles) return;
   int expert, rows;
   int64_t row0;
   if (a.t_expert) {
-    if (b >= a.num_tiles[0]) return;
     expert = a.t_expert[b];
     rows = a.t_rows[b];
     row0 = a.t_row0 ? (int64_t)a.t_row0[b] : (int64_t)b * BM;
@@ -534,24 +554,46 @@ void gemm_wgrad_kernel(WgradArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16_t smem[Cfg::SMEM_EL];
   constexpr uint32_t A_SLOT = Cfg::A_EL * 2, B_SLOT = Cfg::B_EL * 2, B_RING = ST * A_SLOT;  // bytes
   const int64_t total = (int64_t)gridDim.x;
-  int64_t logical = xcd_logical(blockIdx.x, total);
-  const int64_t tiles_per_e = (int64_t)a.S * a.i_tiles * a.n_tiles;
-  const int e = (int)(logical / tiles_per_e);
-  if (e >= a.E) return;
+  const int64_t tiles_per_e = (int64_t)(a.c_expert ? 1 : a.S) * a.i_tiles * a.n_tiles;
+  // Tile order.  Expert slices: XCD-aware contiguous ranges (xcd_logical).  Chunk table (grid = 8 x ceil(chunks / 8)
+  // x tiles per chunk): chunk c runs on XCD c % 8 with its tiles consecutive there, so the chunks that exist
+  // (a device-side count below the grid's bound) are spread evenly over the XCDs, and a hot expert's chunks too.
+  int64_t logical;
+  if (a.c_expert) {
+    const int64_t l = blockIdx.x / 8;
+    logical = (8 * (l / tiles_per_e) + blockIdx.x % 8) * tiles_per_e + l % tiles_per_e;
+  } else {
+    logical = xcd_logical(blockIdx.x, total);
+  }
+  const int g = (int)(logical / tiles_per_e);  // expert, or chunk with a chunk table
   int64_t rem = logical % tiles_per_e;
   const int s = (int)(rem / ((int64_t)a.i_tiles * a.n_tiles));
   rem %= (int64_t)a.i_tiles * a.n_tiles;
   const int it = (int)(rem / a.n_tiles), nt = (int)(rem % a.n_tiles);
+  int e, S = a.S;
   int64_t r0, nrows;
-  if (a.e_rows) {
-    r0 = (int64_t)a.e_row0[e] * a.row0_mult;
-    nrows = a.e_rows[e];
+  float* part_out = nullptr;  // chunk partial slot ([I][N] f32), when the chunk writes one
+  if (a.c_expert) {
+    if (g >= a.max_chunks || g >= a.num_chunks[0]) return;
+    e = a.c_expert[g];
+    r0 = a.c_row0[g];
+    nrows = a.c_rows[g];
+    S = 1;
+    const int ps = a.c_part[g];
+    if (ps >= 0) part_out = a.part + (int64_t)ps * a.I * a.N;
   } else {
-    r0 = 0;
-    nrows = a.dense_rows;
+    e = g;
+    if (e >= a.E) return;
+    if (a.e_rows) {
+      r0 = (int64_t)a.e_row0[e] * a.row0_mult;
+      nrows = a.e_rows[e];
+    } else {
+      r0 = 0;
+      nrows = a.dense_rows;
+    }
   }
   // rows of split s
-  const int64_t chunk = ((nrows + a.S - 1) / a.S + BK - 1) / BK * BK;
+  const int64_t chunk = ((nrows + S - 1) / S + BK - 1) / BK * BK;
   const int64_t rs = (int64_t)s * chunk;
   const int64_t re = min(nrows, rs + chunk);
   const int64_t i0 = (int64_t)it * BM, n0 = (int64_t)nt * BN;
@@ -697,7 +739,8 @@ void gemm_wgrad_kernel(WgradArgs a) {
         if (col >= N) continue;
         const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * SP + c + 4 * h);
         float* dst;
-        if (a.S > 1) dst = a.part + (((int64_t)s * a.E + e) * I + row) * N + col;
+        if (part_out) dst = part_out + row * N + col;
+        else if (S > 1) dst = a.part + (((int64_t)s * a.E + e) * I + row) * N + col;
         else if (a.C2 && col >= a.n_split) dst = a.C2 + (int64_t)e * a.c_estride + row * a.ldc + (col - a.n_split);
         else dst = a.C + (int64_t)e * a.c_estride + row * a.ldc + col;
         *reinterpret_cast<f32x4*>(dst) = v;

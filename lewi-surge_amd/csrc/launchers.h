@@ -53,4 +53,26 @@ int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32
                float* C, float* C2, int64_t n_split, int64_t ldc, int64_t c_estride, int S, void* ws, size_t ws_bytes,
                hipStream_t s, const RowGather& gather = RowGather());
 
+// Chunked routed weight gradient: every expert's rows cut into chunks of at most R rows (see WgradArgs), so a
+// hot expert spreads over many workgroups; split experts are reduced from f32 partial slots in chunk order.
+struct WgradChunkPlan {
+  int R = 0;           // rows per chunk
+  int max_chunks = 0;  // bound on the chunk count
+  int max_parts = 0;   // bound on the partial slots
+};
+struct WgradChunks {
+  const int32_t *c_expert, *c_row0, *c_rows, *c_part, *num_chunks, *e_pbase, *e_nparts, *split_list, *num_split;
+  int max_chunks, max_parts;
+};
+WgradChunkPlan wgrad_chunk_plan(int64_t M, int64_t E);
+size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E);
+// builds the table (in `table`, wgrad_chunk_table_ints entries) from device group sizes and block offsets
+int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
+                       WgradChunks* ch, hipStream_t s);
+size_t wgrad_chunked_workspace_bytes(const WgradChunkPlan& p, int64_t I, int64_t N);
+int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, const void* A, int64_t lda,
+                       const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
+                       int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s,
+                       const RowGather& gather = RowGather());
+
 }  // namespace lsurge

@@ -97,6 +97,12 @@ struct BwdWs {
   size_t part_bytes;
   void* part_r;       // split-K partials of the router weight gradient (another stream)
   size_t part_r_bytes;
+  lsurge::WgradChunkPlan cplan;  // chunk table of the routed weight gradients and the partials of split experts
+  int32_t* chunk_tab;
+  void* part_dn;      // down-projection weight gradient (helper stream)
+  size_t part_dn_bytes;
+  void* part_gu;      // gate/up weight gradient (caller's stream)
+  size_t part_gu_bytes;
 };
 
 size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
@@ -119,6 +125,12 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   w->part = c.take<char>(part);
   w->part_r_bytes = lsurge::wgrad_workspace_bytes(1, q.d, q.E, dense_splits(q.T, q.d, q.E));
   w->part_r = c.take<char>(w->part_r_bytes);
+  w->cplan = lsurge::wgrad_chunk_plan(q.M, q.E);
+  w->chunk_tab = c.take<int32_t>(lsurge::wgrad_chunk_table_ints(w->cplan, q.E));
+  w->part_dn_bytes = lsurge::wgrad_chunked_workspace_bytes(w->cplan, q.f, q.d);
+  w->part_dn = c.take<char>(w->part_dn_bytes);
+  w->part_gu_bytes = lsurge::wgrad_chunked_workspace_bytes(w->cplan, q.d, 2 * q.f);
+  w->part_gu = c.take<char>(w->part_gu_bytes);
   return c.off + 256;
 }
 
@@ -297,14 +309,17 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   // s1: W_r^T for the router's dx term (independent of everything else)
   if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, s1)) return rc;
 
+  // main: chunk table of the routed weight gradients (read by both wgrads, after the s1 fork below)
+  lsurge::WgradChunks chunks;
+  if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, st)) return rc;
   // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel)
   if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, q.P, sv.slot, sv.weights, q.T, (int)q.k, q.d, dy, w.dy_pad,
                                               dweights, w.dl, st))
     return rc;
   if (int rc = lsurge::stream_after(s1, st, ev[2])) return rc;
   // s1: down wgrad dW_down[e] = h_e^T dY_e; router: dW_r = x^T dlogits (bf16 MFMA over the dense [T, E] dlogits)
-  if (int rc = lsurge::gemm_wgrad(KID_GEMM_DOWN_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, sv.h, q.f, w.dy_pad,
-                                  q.d, q.f, q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, 1, nullptr, 0, s1))
+  if (int rc = lsurge::gemm_wgrad_chunked(KID_GEMM_DOWN_WGRAD, chunks, (int)q.E, q.T, sv.h, q.f, w.dy_pad, q.d, q.f,
+                                          q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, w.part_dn, w.part_dn_bytes, s1))
     return rc;
   if (int rc = lsurge::launch_scatter_dlogits(w.dl, sv.sel, q.T, (int)q.E, (int)q.k, w.dlog, s1)) return rc;
   {
@@ -333,9 +348,9 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
     gather.rows = sv.row_src;
     gather.div = (int)q.k;
     gather.nrows = q.T;
-    if (int rc = lsurge::gemm_wgrad(KID_GEMM_GU_WGRAD, (int)q.E, sv.block_off, BLK, sv.gs, 0, q.T, p->x, q.d, w.dgu,
-                                    2 * q.f, q.d, 2 * q.f, g->dw_gate, g->dw_up, q.f, q.f, q.d * q.f, 1, nullptr, 0, st,
-                                    gather))
+    if (int rc = lsurge::gemm_wgrad_chunked(KID_GEMM_GU_WGRAD, chunks, (int)q.E, q.T, p->x, q.d, w.dgu, 2 * q.f, q.d,
+                                            2 * q.f, g->dw_gate, g->dw_up, q.f, q.f, q.d * q.f, w.part_gu,
+                                            w.part_gu_bytes, st, gather))
       return rc;
   }
   return LSURGE_OK;

@@ -288,6 +288,65 @@ __global__ __launch_bounds__(256) void router_select_kernel(const float* __restr
   if (lane < k) weights[(int64_t)t * k + lane] = mine / denom;
 }
 
+// one lane per token: the k largest logits (ties -> lower expert index) kept in a sorted register list while the
+// token's logits are scanned in ascending expert order, then the softmax over them in rank order.  A new logit
+// enters at the first slot whose logit it strictly exceeds (or the first empty slot); everything below shifts down,
+// so equal logits stay in ascending expert order.  K >= k is the list's compile-time size.
+template <int K>
+__global__ __launch_bounds__(256) void router_select_lane_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                                 int32_t* __restrict__ sel,
+                                                                 float* __restrict__ weights) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= T) return;
+  const float* l = logits + (int64_t)t * E;
+  float tv[K];
+  int ti[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    tv[j] = 0.f;
+    ti[j] = -1;
+  }
+  auto insert = [&](float v, int e) {
+    bool placed = false;
+    float cv = v;
+    int ci = e;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const bool g = placed || ti[j] < 0 || cv > tv[j];
+      const float ov = tv[j];
+      const int oi = ti[j];
+      tv[j] = g ? cv : ov;
+      ti[j] = g ? ci : oi;
+      cv = g ? ov : cv;
+      ci = g ? oi : ci;
+      placed = g;
+    }
+  };
+  if ((E & 3) == 0) {
+    for (int e = 0; e < E; e += 4) {
+      const f32x4 q = *reinterpret_cast<const f32x4*>(l + e);
+      insert(q[0], e);
+      insert(q[1], e + 1);
+      insert(q[2], e + 2);
+      insert(q[3], e + 3);
+    }
+  } else {
+    for (int e = 0; e < E; ++e) insert(l[e], e);
+  }
+  // softmax over the k best, denominator summed in rank order
+  float denom = 0.f;
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+    if (j < k) denom += __expf(tv[j] - tv[0]);
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    if (j < k) {
+      sel[(int64_t)t * k + j] = ti[j];
+      weights[(int64_t)t * k + j] = __expf(tv[j] - tv[0]) / denom;
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" int lsurge_router_topk(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d,
@@ -304,6 +363,18 @@ extern "C" int lsurge_router_topk(const void* x, const void* w_r, const float* b
     LSURGE_LAUNCH(KID_ROUTER, s,
                   hipLaunchKernelGGL(router_logits_kernel, lg, dim3(RL_THREADS), 0, s, (const bf16_t*)x,
                                      (const bf16_t*)w_r, bias, (int)t, (int)d, (int)e, logits));
+    if (k <= 16 && t >= 8192) {  // lane per token (enough tokens to fill the GPU); else one wave per token
+      const dim3 lg2((unsigned)((t + 255) / 256));
+      if (k <= 8)
+        LSURGE_LAUNCH(KID_ROUTER_SELECT, s,
+                      hipLaunchKernelGGL(router_select_lane_kernel<8>, lg2, dim3(256), 0, s, logits, (int)t, (int)e,
+                                         (int)k, sel, weights));
+      else
+        LSURGE_LAUNCH(KID_ROUTER_SELECT, s,
+                      hipLaunchKernelGGL(router_select_lane_kernel<16>, lg2, dim3(256), 0, s, logits, (int)t, (int)e,
+                                         (int)k, sel, weights));
+      return LSURGE_OK;
+    }
     const dim3 sg((unsigned)((t + 3) / 4));
 #define RS_CASE(EC)                                                                                        \
   LSURGE_LAUNCH(KID_ROUTER_SELECT, s,                                                                      \

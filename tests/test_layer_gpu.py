@@ -78,6 +78,21 @@ def test_small_layer_zipf_bias(dev):
     check_layer(p, MoEShape(2048, 256, 32, 4, 128, 128), dev)
 
 
+def test_hot_experts_chunked_wgrad(dev):
+    """Every token routes to experts 0 and 1 (a large bias), so each holds 5000 rows: the routed weight gradients
+    cut them into 4096 + 904-row chunks summed from partials, and the six empty experts get zero gradients."""
+    T, d, E, k, f = 5000, 128, 8, 2, 64
+    p = mo.make_inputs(T=T, d=d, E=E, k=k, f=f, fs=0, seed=5)
+    p["bias"] = np.array([20.0, 19.0] + [0.0] * (E - 2), dtype=np.float32)
+    shape = MoEShape(T, d, E, k, f, 0)
+    errs = check_layer(p, shape, dev)
+    _, views, grads = run_gpu(p, shape, dev)
+    assert list(views["group_sizes"]) == [T, T] + [0] * (E - 2)
+    for n in ("dw_gate", "dw_up", "dw_down"):
+        assert not grads[n][2:].any(), n
+    assert errs["dw_gate"] < TOL
+
+
 @pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4"])
 def test_baseline_configs(name, dev):
     c = mo.CONFIGS[name]

@@ -86,10 +86,12 @@ def test_router_and_layout_bit_exact(name, dev):
         print(f"\n{name} load min/mean/max {gs.min()}/{gs.mean():.0f}/{gs.max()} empty={int((gs == 0).sum())}")
 
 
-def test_router_ties_lower_index(dev):
-    """Planted ties: duplicated router columns give identical logits; the lower expert index must win."""
+@pytest.mark.parametrize("T", [512, 8192])
+def test_router_ties_lower_index(T, dev):
+    """Planted ties: duplicated router columns give identical logits; the lower expert index must win (both
+    selection kernels: one wave per token for small T, one lane per token from 8192 tokens)."""
     rng = np.random.default_rng(5)
-    T, d, E, k = 512, 256, 64, 6
+    d, E, k = 256, 64, 6
     x = mo.round_bf16(rng.standard_normal((T, d), dtype=np.float32))
     w_r = mo.round_bf16(rng.standard_normal((d, E), dtype=np.float32) * np.float32(0.02))
     w_r[:, 40:48] = w_r[:, 0:8]  # experts 40..47 tie with 0..7 on every token
@@ -99,6 +101,28 @@ def test_router_ties_lower_index(dev):
     want = co.topk(co.router_logits(x, w_r), k)
     assert np.array_equal(sel, want)
     assert np.array_equal(sel[:7], np.tile(np.arange(k), (7, 1)))
+
+
+@pytest.mark.parametrize("T,d,E,k,neg_inf", [(1, 8, 8, 1, 0), (65, 100, 20, 3, 0), (130, 64, 37, 16, 0),
+                                             (200, 96, 256, 8, 0), (64, 1024, 256, 16, 0), (3000, 256, 64, 6, 0),
+                                             (97, 40, 16, 12, 8), (70, 33, 9, 9, 3)])
+def test_router_ragged_shapes(T, d, E, k, neg_inf, dev):
+    """Router on shapes off every vector width: T not a multiple of 64, d not a multiple of 8 or 32, E not a
+    multiple of the expert group, k up to 16 and k = E; `neg_inf` experts carry a -inf bias, so ties at -inf
+    are resolved by the lower index and their weights are 0."""
+    rng = np.random.default_rng(T * 7 + E)
+    x = mo.round_bf16(rng.standard_normal((T, d), dtype=np.float32))
+    w_r = mo.round_bf16(rng.standard_normal((d, E), dtype=np.float32) * np.float32(0.05))
+    bias = None
+    if neg_inf:
+        bias = np.zeros(E, np.float32)
+        bias[rng.choice(E, neg_inf, replace=False)] = -np.inf
+    logits, sel, wts = gpu_router(x, w_r, k, bias, dev)
+    want_l = co.router_logits(x, w_r, bias)
+    assert np.array_equal(logits.view(np.uint32), want_l.view(np.uint32))
+    want_sel = co.topk(want_l, k)
+    assert np.array_equal(sel, want_sel)
+    assert mo.rel_l2(wts, mo.topk_softmax(want_l, want_sel)) < 1e-6
 
 
 @pytest.mark.parametrize("T,k,E", [(1, 1, 8), (3, 2, 8), (1000, 6, 16), (4096, 8, 256), (300, 12, 16)])
