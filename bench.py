@@ -42,6 +42,8 @@ def kernel_work(c):
     """Algorithmic work per launch of each kernel: ('mfma', flops) over useful rows, or ('hbm', bytes)."""
     T, d, E, k, f, fs = c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"]
     M = T * k
+    if fs and fs == f:  # the shared expert rides along the routed experts: T more rows in every grouped GEMM
+        M += T
     w = {
         "gemm_gu_fwd": ("mfma", 2 * M * d * 2 * f),
         "gemm_down_fwd": ("mfma", 2 * M * f * d),
@@ -59,7 +61,7 @@ def kernel_work(c):
         "layout_hist": ("hbm", 4 * M),
         "layout_rank": ("hbm", 4 * M + 16 * M),
     }
-    if fs:
+    if fs and fs != f:
         w.update({
             "shared_gu_fwd": ("mfma", 2 * T * d * 2 * fs),
             "shared_down_fwd": ("mfma", 2 * T * fs * d),

@@ -72,13 +72,17 @@ __global__ void zero_rows_from_kernel(void* __restrict__ out, int64_t m, int64_t
 
 inline unsigned pad8(int64_t g) { return (unsigned)((g + 7) / 8 * 8); }
 
-// Chunk table of the routed weight gradients (one workgroup of 256 threads, thread e = expert e).  Expert e owns
+// Chunk table of the routed weight gradients (one workgroup of 512 threads, thread e = expert e).  Expert e owns
 // padded rows [128 block_off[e], 128 block_off[e] + gs[e]); they are cut into ceil(gs[e] / R) chunks of R rows.
-// An empty expert keeps one empty chunk, which writes its zero gradient.  An expert with more than one chunk
-// gets consecutive partial slots (summed in chunk order by wgrad_chunk_reduce_kernel) and an entry in split_list
-// (ascending e).  The bounds max_chunks >= E + ceil(M / R) and max_parts >= 2 M / R hold for any group sizes that
-// sum to at most M; if the slots would not fit anyway (corrupt sizes), every expert is left as one unsplit chunk.
-__device__ __forceinline__ int block_excl_scan(int v, int* sh) {  // 256 threads; returns the exclusive prefix
+// An optional extra expert (id E: the shared expert) owns x_rows rows from padded row x_row0.  An empty expert
+// keeps one empty chunk, which writes its zero gradient.  An expert with more than one chunk gets consecutive
+// partial slots (summed in chunk order by wgrad_chunk_reduce_kernel) and an entry in split_list (ascending e).
+// The bounds max_chunks >= E' + ceil(M' / R) and max_parts >= 2 M' / R (E', M': experts and rows including the
+// extra one) hold for any group sizes that sum to at most M; if the slots would not fit anyway (corrupt sizes),
+// every expert is left as one unsplit chunk.
+constexpr int WC_THREADS = 512;
+__device__ __forceinline__ int block_excl_scan(int v, int* sh) {  // WC_THREADS threads; returns the exclusive prefix
+  constexpr int NWV = WC_THREADS / 64;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int x = v;
 #pragma unroll
@@ -88,35 +92,43 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh) {  // 256 threads
   }
   if (lane == 63) sh[w] = x;
   __syncthreads();
-  int base = 0;
-  for (int i = 0; i < w; ++i) base += sh[i];
-  const int total = sh[0] + sh[1] + sh[2] + sh[3];
+  int base = 0, total = 0;
+  for (int i = 0; i < NWV; ++i) {
+    if (i < w) base += sh[i];
+    total += sh[i];
+  }
   __syncthreads();
-  if (tid == 0) sh[4] = total;
+  if (tid == 0) sh[NWV] = total;
   __syncthreads();
   return base + x - v;
 }
 
-__global__ __launch_bounds__(256) void wgrad_chunks_kernel(
+__global__ __launch_bounds__(WC_THREADS) void wgrad_chunks_kernel(
     const int32_t* __restrict__ gs, const int32_t* __restrict__ block_off, int E, int R, int max_chunks,
-    int max_parts, int32_t* __restrict__ c_expert, int32_t* __restrict__ c_row0, int32_t* __restrict__ c_rows,
-    int32_t* __restrict__ c_part, int32_t* __restrict__ num_chunks, int32_t* __restrict__ e_pbase,
-    int32_t* __restrict__ e_nparts, int32_t* __restrict__ split_list, int32_t* __restrict__ num_split) {
-  __shared__ int sh[8];
-  const int e = threadIdx.x;
-  const int g = e < E ? max(gs[e], 0) : 0;
-  int n = e < E ? max(1, (g + R - 1) / R) : 0;
+    int max_parts, int x_rows, int x_row0, int32_t* __restrict__ c_expert, int32_t* __restrict__ c_row0,
+    int32_t* __restrict__ c_rows, int32_t* __restrict__ c_part, int32_t* __restrict__ num_chunks,
+    int32_t* __restrict__ e_pbase, int32_t* __restrict__ e_nparts, int32_t* __restrict__ split_list,
+    int32_t* __restrict__ num_split) {
+  __shared__ int sh[WC_THREADS / 64 + 1];
+  constexpr int TOT = WC_THREADS / 64;
+  // the extra expert (the largest: every token) takes the first chunks, so its long tiles start first
+  const bool has_x = x_rows >= 0;
+  const int e = has_x ? (threadIdx.x == 0 ? E : (int)threadIdx.x - 1) : (int)threadIdx.x;
+  const bool routed = e < E && !(has_x && threadIdx.x == 0), extra = has_x && threadIdx.x == 0;
+  const int g = routed ? max(gs[e], 0) : (extra ? x_rows : 0);
+  const int r0 = routed ? block_off[e] * BM : x_row0;
+  int n = (routed || extra) ? max(1, (g + R - 1) / R) : 0;
   const int pbase = block_excl_scan(n > 1 ? n : 0, sh);
-  const bool fits = sh[4] <= max_parts;
+  const bool fits = sh[TOT] <= max_parts;
   if (!fits && n > 1) n = 1;
   const int cbase = block_excl_scan(n, sh);
-  const int nchunks = sh[4];
+  const int nchunks = sh[TOT];
   const int sidx = block_excl_scan(n > 1 ? 1 : 0, sh);
   if (e == 0) {
     num_chunks[0] = min(nchunks, max_chunks);
-    num_split[0] = sh[4];
+    num_split[0] = sh[TOT];
   }
-  if (e >= E) return;
+  if (!routed && !extra) return;
   e_pbase[e] = pbase;
   e_nparts[e] = n > 1 ? n : 0;
   if (n > 1) split_list[sidx] = e;
@@ -124,7 +136,7 @@ __global__ __launch_bounds__(256) void wgrad_chunks_kernel(
     const int c = cbase + j;
     if (c >= max_chunks) break;
     c_expert[c] = e;
-    c_row0[c] = block_off[e] * BM + j * R;
+    c_row0[c] = r0 + j * R;
     c_rows[c] = n > 1 ? min(R, g - j * R) : g;
     c_part[c] = n > 1 ? pbase + j : -1;
   }
@@ -136,7 +148,8 @@ __global__ void wgrad_chunk_reduce_kernel(const float* __restrict__ part, const 
                                           const int32_t* __restrict__ num_split, const int32_t* __restrict__ e_pbase,
                                           const int32_t* __restrict__ e_nparts, int64_t I, int64_t N,
                                           float* __restrict__ C, float* __restrict__ C2, int64_t n_split, int64_t ldc,
-                                          int64_t c_estride) {
+                                          int64_t c_estride, int x_expert, float* __restrict__ Cx,
+                                          float* __restrict__ C2x) {
   const int64_t IN = I * N, q4 = IN / 4;
   const int64_t total = (int64_t)num_split[0] * q4;
   for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < total; x += (int64_t)gridDim.x * blockDim.x) {
@@ -145,10 +158,22 @@ __global__ void wgrad_chunk_reduce_kernel(const float* __restrict__ part, const 
     const float* p0 = part + (int64_t)e_pbase[e] * IN + o;
     f32x4 v = *reinterpret_cast<const f32x4*>(p0);
     const int np = e_nparts[e];
-    for (int q = 1; q < np; ++q) v += *reinterpret_cast<const f32x4*>(p0 + (int64_t)q * IN);
+    int q = 1;
+    for (; q + 4 <= np; q += 4) {  // four partials in flight, added in order
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(p0 + (int64_t)q * IN);
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(p0 + (int64_t)(q + 1) * IN);
+      const f32x4 a2 = *reinterpret_cast<const f32x4*>(p0 + (int64_t)(q + 2) * IN);
+      const f32x4 a3 = *reinterpret_cast<const f32x4*>(p0 + (int64_t)(q + 3) * IN);
+      v += a0;
+      v += a1;
+      v += a2;
+      v += a3;
+    }
+    for (; q < np; ++q) v += *reinterpret_cast<const f32x4*>(p0 + (int64_t)q * IN);
     const int64_t row = o / N, col = o % N;
-    float* dst = (C2 && col >= n_split) ? C2 + e * c_estride + row * ldc + (col - n_split)
-                                        : C + e * c_estride + row * ldc + col;
+    float* dst;
+    if (e == x_expert) dst = (C2x && col >= n_split) ? C2x + row * ldc + (col - n_split) : Cx + row * ldc + col;
+    else dst = (C2 && col >= n_split) ? C2 + e * c_estride + row * ldc + (col - n_split) : C + e * c_estride + row * ldc + col;
     *reinterpret_cast<f32x4*>(dst) = v;
   }
 }
@@ -178,7 +203,8 @@ static int max_blocks_of(const GemmBlocks& g) {
 
 // C[rows, N] = A[rows, K] @ B_e where B_e is [K, N] (n-major) -- forward projections
 int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, int64_t ldb,
-                 int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32) {
+                 int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32,
+                 const ExtraExpert& xe) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_kn")) return rc;
   if (int rc = check_desc(std::max<int64_t>(BM * lda, K * ldb) * 2, "gemm_rows_kn")) return rc;
   RowsArgs a{};
@@ -188,6 +214,8 @@ int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
   else a.C = (bf16_t*)C;
   a.t_expert = g.blk_expert; a.t_rows = g.blk_rows; a.t_row0 = g.blk_row0; a.num_tiles = g.num_blocks;
   a.dense_rows = g.dense_rows; a.max_tiles = max_blocks_of(g);
+  a.x_expert = xe.expert; a.Bx = (const bf16_t*)xe.B; a.B2x = (const bf16_t*)xe.B2;
+  LSURGE_REQUIRE(xe.expert < 0 || (xe.B && (xe.B2 || !a.B2)), "grouped GEMM: extra expert weights missing");
   a.n_tiles = (int)((N + BN - 1) / BN);
   if (a.max_tiles == 0) return LSURGE_OK;
   LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, B_KN, EPI_STORE>),
@@ -199,7 +227,7 @@ int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
 // tile row r reads A[gather.rows[row0 + r] / gather.div] of an A with gather.nrows rows (negative: zero row).
 int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* Bg, const void* Bu,
                          int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* H, void* Gs, void* Us,
-                         int64_t ldh, hipStream_t s, const RowGather& gather) {
+                         int64_t ldh, hipStream_t s, const RowGather& gather, const ExtraExpert& xe) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_swiglu_fwd")) return rc;
   if (int rc = check_desc(std::max<int64_t>(BM * lda, K * ldb) * 2, "gemm_rows_swiglu_fwd")) return rc;
   if (gather.rows) {
@@ -213,6 +241,8 @@ int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t ld
   a.ldg = ldh;
   a.t_expert = g.blk_expert; a.t_rows = g.blk_rows; a.t_row0 = g.blk_row0; a.num_tiles = g.num_blocks;
   a.dense_rows = g.dense_rows; a.max_tiles = max_blocks_of(g);
+  a.x_expert = xe.expert; a.Bx = (const bf16_t*)xe.B; a.B2x = (const bf16_t*)xe.B2;
+  LSURGE_REQUIRE(xe.expert < 0 || (xe.B && (xe.B2 || !a.B2)), "grouped GEMM: extra expert weights missing");
   a.n_tiles = (int)((N + BN / 2 - 1) / (BN / 2));
   if (a.max_tiles == 0) return LSURGE_OK;
   LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, B_KN, EPI_SWIGLU_FWD>),
@@ -225,7 +255,8 @@ int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t ld
 // swiglu_bwd: C = [dG | dU] from dH = A @ B^T and the saved G, U (ldg pitch).
 int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
                  int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
-                 bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32) {
+                 bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32,
+                 const ExtraExpert& xe) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_nk")) return rc;
   if (int rc = check_desc(std::max<int64_t>(BM * lda, N * ldb) * 2, "gemm_rows_nk")) return rc;
   LSURGE_REQUIRE(!B2 || (k_split > 0 && k_split % BK == 0), "gemm_rows_nk: k_split must be a multiple of %d", BK);
@@ -237,6 +268,8 @@ int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
   a.G = (bf16_t*)Gs; a.U = (bf16_t*)Us; a.ldg = ldg;
   a.t_expert = g.blk_expert; a.t_rows = g.blk_rows; a.t_row0 = g.blk_row0; a.num_tiles = g.num_blocks;
   a.dense_rows = g.dense_rows; a.max_tiles = max_blocks_of(g);
+  a.x_expert = xe.expert; a.Bx = (const bf16_t*)xe.B; a.B2x = (const bf16_t*)xe.B2;
+  LSURGE_REQUIRE(xe.expert < 0 || (xe.B && (xe.B2 || !a.B2)), "grouped GEMM: extra expert weights missing");
   a.n_tiles = (int)((N + BN - 1) / BN);
   if (a.max_tiles == 0) return LSURGE_OK;
   const dim3 grid(pad8((int64_t)a.n_tiles * a.max_tiles));
@@ -291,38 +324,41 @@ int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32
 
 WgradChunkPlan wgrad_chunk_plan(int64_t M, int64_t E) {
   WgradChunkPlan p;
-  // R: at least 4096 rows and at least twice the mean expert load (rounded to blocks), so balanced routings keep
-  // one chunk per expert; the M / 64 floor bounds the partial slots at 128
-  const int64_t mean2 = (2 * ((M + E - 1) / E) + BM - 1) / BM * BM;
-  const int64_t m64 = ((M + 63) / 64 + BM - 1) / BM * BM;
-  p.R = (int)std::max<int64_t>(4096, std::max(mean2, m64));
+  // R: at least 2048 rows, 1.5 x the mean expert load (so balanced routings keep one chunk per routed expert) and
+  // M / 32.  A chunk of M / 32 rows is about the work each of the 512 workgroup slots gets anyway (an expert's 16 or
+  // 32 tiles over all M rows), so a hot expert's chunks, placed first, do not extend the launch; and the partial
+  // slots stay at most 64.
+  const int64_t mean15 = ((3 * M + 2 * E - 1) / (2 * E) + BM - 1) / BM * BM;  // 1.5 x the mean load, in blocks
+  const int64_t m32 = ((M + 31) / 32 + BM - 1) / BM * BM;
+  p.R = (int)std::max<int64_t>(2048, std::max(mean15, m32));
   p.max_chunks = (int)(E + (M + p.R - 1) / p.R);
   p.max_parts = (int)std::max<int64_t>(1, (2 * M + p.R - 1) / p.R);
   return p;
 }
 
 size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E) {
-  return 4 * (size_t)p.max_chunks + 2 * (size_t)E + (size_t)p.max_parts + 2;
+  return 4 * (size_t)p.max_chunks + 2 * (size_t)(E + 1) + (size_t)p.max_parts + 2;
 }
 
 int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
-                       WgradChunks* ch, hipStream_t s) {
+                       WgradChunks* ch, hipStream_t s, int64_t x_rows, int64_t x_row0) {
   LSURGE_REQUIRE(E >= 1 && E <= 256, "wgrad chunks: E=%d must be in [1, 256]", E);
+  LSURGE_REQUIRE(x_rows < (1ll << 31) && x_row0 >= 0 && x_row0 < (1ll << 31), "wgrad chunks: extra expert rows");
   int32_t* t = table;
   ch->c_expert = t; t += p.max_chunks;
   ch->c_row0 = t; t += p.max_chunks;
   ch->c_rows = t; t += p.max_chunks;
   ch->c_part = t; t += p.max_chunks;
-  ch->e_pbase = t; t += E;
-  ch->e_nparts = t; t += E;
+  ch->e_pbase = t; t += E + 1;
+  ch->e_nparts = t; t += E + 1;
   ch->split_list = t; t += p.max_parts;
   ch->num_chunks = t;
   ch->num_split = t + 1;
   ch->max_chunks = p.max_chunks;
   ch->max_parts = p.max_parts;
   LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(wgrad_chunks_kernel, dim3(1), dim3(256), 0, s, gs, block_off, E, p.R, p.max_chunks,
-                                   p.max_parts, (int32_t*)ch->c_expert, (int32_t*)ch->c_row0, (int32_t*)ch->c_rows,
+                hipLaunchKernelGGL(wgrad_chunks_kernel, dim3(1), dim3(WC_THREADS), 0, s, gs, block_off, E, p.R,
+                                   p.max_chunks, p.max_parts, (int)x_rows, (int)x_row0, (int32_t*)ch->c_expert, (int32_t*)ch->c_row0, (int32_t*)ch->c_rows,
                                    (int32_t*)ch->c_part, (int32_t*)ch->num_chunks, (int32_t*)ch->e_pbase,
                                    (int32_t*)ch->e_nparts, (int32_t*)ch->split_list, (int32_t*)ch->num_split));
   return LSURGE_OK;
@@ -338,8 +374,9 @@ size_t wgrad_chunked_workspace_bytes(const WgradChunkPlan& p, int64_t I, int64_t
 int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, const void* A, int64_t lda,
                        const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
                        int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s,
-                       const RowGather& gather) {
+                       const RowGather& gather, const ExtraOut& xo) {
   if (int rc = check_gemm_shape(I, N, "gemm_wgrad_chunked")) return rc;
+  LSURGE_REQUIRE(xo.expert < 0 || (xo.C && (xo.C2 || !C2)), "gemm_wgrad_chunked: extra expert outputs missing");
   if (int rc = check_desc(max_rows * std::max(lda, ldb) * 2, "gemm_wgrad_chunked")) return rc;
   LSURGE_REQUIRE(E >= 1 && ch.max_chunks >= 1, "gemm_wgrad_chunked: bad E / chunk table");
   LSURGE_REQUIRE(part && part_bytes >= sizeof(float) * (size_t)ch.max_parts * I * N,
@@ -357,16 +394,17 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
   a.E = E; a.S = 1; a.part = (float*)part;
   a.c_expert = ch.c_expert; a.c_row0 = ch.c_row0; a.c_rows = ch.c_rows; a.c_part = ch.c_part;
   a.num_chunks = ch.num_chunks; a.max_chunks = ch.max_chunks;
+  a.x_expert = xo.expert; a.Cx = xo.C; a.C2x = xo.C2;
   a.i_tiles = (int)((I + BM - 1) / BM);
   a.n_tiles = (int)((N + BN - 1) / BN);
   const int64_t tiles = (int64_t)pad8(ch.max_chunks) * a.i_tiles * a.n_tiles;  // see the chunk tile order
   LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel<Cfg>, dim3((unsigned)tiles), dim3(GT), 0, s, a));
-  // grid-stride over the split experts' elements; small, since balanced routings split nothing
-  const unsigned grid = (unsigned)std::min<int64_t>((I * N / 4 + 255) / 256, 256);
+  // grid-stride over the split experts' elements: two experts' worth of threads per pass
+  const unsigned grid = (unsigned)std::min<int64_t>(2 * ((I * N / 4 + 255) / 256), 2048);
   LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
                 hipLaunchKernelGGL(wgrad_chunk_reduce_kernel, dim3(grid), dim3(256), 0, s, (const float*)part,
                                    ch.split_list, ch.num_split, ch.e_pbase, ch.e_nparts, I, N, C, C2, n_split, ldc,
-                                   c_estride));
+                                   c_estride, xo.expert, xo.C, xo.C2));
   return LSURGE_OK;
 }
 

@@ -78,6 +78,9 @@ struct RowsArgs {
   int64_t dense_rows;
   int n_tiles;               // column tiles
   int max_tiles;             // row tiles the grid covers
+  int x_expert = -1;         // tiles of this expert id read Bx / B2x instead of B / B2 (-1: none); the layer's
+  const bf16_t* Bx = nullptr;   // shared expert rides along the routed ones as expert E
+  const bf16_t* B2x = nullptr;
 };
 
 struct WgradArgs {
@@ -109,6 +112,9 @@ struct WgradArgs {
   const int32_t* c_part;
   const int32_t* num_chunks;  // device-side chunk count
   int max_chunks;             // chunks the grid covers
+  int x_expert = -1;          // this expert id writes Cx / C2x (row pitch ldc) instead of C / C2 (-1: none)
+  float* Cx = nullptr;
+  float* C2x = nullptr;
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -342,8 +348,9 @@ void gemm_rows_kernel(RowsArgs a) {
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   // column origin of this tile: weight columns for B, output columns for C (SwiGLU: gate and up halves)
   const int64_t n0 = (int64_t)nt * (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN);
-  const bf16_t* Bbase = a.B + (int64_t)expert * a.b_estride;
-  const bf16_t* B2base = a.B2 ? a.B2 + (int64_t)expert * a.b_estride : Bbase;
+  const bool xe = expert == a.x_expert;
+  const bf16_t* Bbase = xe ? a.Bx : a.B + (int64_t)expert * a.b_estride;
+  const bf16_t* B2base = xe ? (a.B2x ? a.B2x : Bbase) : (a.B2 ? a.B2 + (int64_t)expert * a.b_estride : Bbase);
   const int K = (int)a.K, N = (int)a.N, lda = (int)a.lda, ldb = (int)a.ldb, ksplit = (int)a.k_split;
   const int nk = (K + BK - 1) / BK;
   const uint32_t lds0 = lds_addr(smem);
@@ -741,6 +748,8 @@ void gemm_wgrad_kernel(WgradArgs a) {
         float* dst;
         if (part_out) dst = part_out + row * N + col;
         else if (S > 1) dst = a.part + (((int64_t)s * a.E + e) * I + row) * N + col;
+        else if (e == a.x_expert) dst = (a.C2x && col >= a.n_split) ? a.C2x + row * a.ldc + (col - a.n_split)
+                                                                    : a.Cx + row * a.ldc + col;
         else if (a.C2 && col >= a.n_split) dst = a.C2 + (int64_t)e * a.c_estride + row * a.ldc + (col - a.n_split);
         else dst = a.C + (int64_t)e * a.c_estride + row * a.ldc + col;
         *reinterpret_cast<f32x4*>(dst) = v;

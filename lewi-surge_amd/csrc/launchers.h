@@ -16,7 +16,8 @@ int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src,
 int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, const float* w, int64_t n,
                        const void* add, void* out, int out_dtype, hipStream_t s);
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
-                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s);
+                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s,
+                           void* gcopy = nullptr);
 int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* slot, int64_t n, const float* dl,
                             const int32_t* sel, const void* w_rT, const void* add, void* dx, hipStream_t s);
 int launch_transpose_bf16(const void* a, int R, int C, void* at, hipStream_t s);
@@ -39,14 +40,24 @@ struct RowGather {
   int div = 1;
   int64_t nrows = 0;  // rows of the gathered-from matrix
 };
+// One extra expert id whose weights live in matrices of their own (the layer's shared expert, carried along the
+// routed experts as expert E): its tiles read B / B2 here instead of the routed weight stack.
+struct ExtraExpert {
+  int expert = -1;
+  const void* B = nullptr;
+  const void* B2 = nullptr;
+};
 int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, int64_t ldb,
-                 int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32 = false);
+                 int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32 = false,
+                 const ExtraExpert& xe = ExtraExpert());
 int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* Bg, const void* Bu,
                          int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* H, void* Gs, void* Us,
-                         int64_t ldh, hipStream_t s, const RowGather& gather = RowGather());
+                         int64_t ldh, hipStream_t s, const RowGather& gather = RowGather(),
+                         const ExtraExpert& xe = ExtraExpert());
 int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
                  int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
-                 bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false);
+                 bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false,
+                 const ExtraExpert& xe = ExtraExpert());
 size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S);
 int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
                int64_t max_rows, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N,
@@ -67,12 +78,19 @@ struct WgradChunks {
 WgradChunkPlan wgrad_chunk_plan(int64_t M, int64_t E);
 size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E);
 // builds the table (in `table`, wgrad_chunk_table_ints entries) from device group sizes and block offsets
+// Extra expert of the chunk table (id E, after the routed ones): x_rows rows from padded row x_row0 (x_rows < 0:
+// none); its gradient goes to C / C2 of an ExtraOut.
 int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
-                       WgradChunks* ch, hipStream_t s);
+                       WgradChunks* ch, hipStream_t s, int64_t x_rows = -1, int64_t x_row0 = 0);
+struct ExtraOut {
+  int expert = -1;
+  float* C = nullptr;
+  float* C2 = nullptr;
+};
 size_t wgrad_chunked_workspace_bytes(const WgradChunkPlan& p, int64_t I, int64_t N);
 int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, const void* A, int64_t lda,
                        const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
                        int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s,
-                       const RowGather& gather = RowGather());
+                       const RowGather& gather = RowGather(), const ExtraOut& xo = ExtraOut());
 
 }  // namespace lsurge

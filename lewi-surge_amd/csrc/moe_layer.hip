@@ -2,7 +2,12 @@
 //
 // Forward:  router top-k -> routing layout -> gate/up grouped GEMM over 128-row expert blocks whose rows are
 //           gathered from x (the dispatch, fused into the GEMM's operand load) with the SiLU*mul epilogue -> down
-//           grouped GEMM -> weighted combine (+ shared expert, the dense E = 1 case of the same GEMMs).
+//           grouped GEMM -> weighted combine (+ shared expert).
+// Shared expert.  When its FFN width equals the routed one (fs == f) it rides along the routed experts as expert E:
+// its T rows (every token once) follow the routed block bound in the padded row space, so every grouped GEMM of
+// the layer covers routed and shared rows in one launch (tiles of expert E read the shared weights), and its
+// weight gradients join the routed chunk table.  Otherwise it runs as dense (E = 1) GEMMs of its own on a
+// helper stream.
 // Backward: fused combine backward (dY rows, d(routing weights), d(router logits)) -> down dgrad with the
 //           SwiGLU backward epilogue -> down wgrad -> gate/up dgrad -> gate/up wgrad -> shared expert ->
 //           router wgrad -> dispatch backward (gather-reduce, plus the router and shared-expert dx terms).
@@ -34,6 +39,9 @@ struct Carve {
 
 struct Dims {
   int64_t T, d, E, k, f, fs, M, MB, P;
+  bool merged;      // shared expert carried as expert E of the grouped GEMMs (fs == f)
+  int64_t SB;       // its blocks (ceil(T / 128)), after the routed block bound MB
+  int64_t MT, PT;   // tile bound and padded rows including them
 };
 
 Dims dims_of(const lsurge_moe_shape* s) {
@@ -42,6 +50,10 @@ Dims dims_of(const lsurge_moe_shape* s) {
   q.M = q.T * q.k;
   q.MB = lsurge_max_blocks(q.M, q.E);
   q.P = q.MB * BLK;
+  q.merged = q.fs > 0 && q.fs == q.f;
+  q.SB = q.merged ? (q.T + BLK - 1) / BLK : 0;
+  q.MT = q.MB + q.SB;
+  q.PT = q.MT * BLK;
   return q;
 }
 
@@ -50,8 +62,9 @@ struct Saved {
   int32_t *sel;
   float* weights;
   int32_t *gs, *offsets, *block_off, *order, *pos, *slot, *row_src, *blk_expert, *blk_rows, *num_blocks;
+  int32_t *t_expert, *t_rows, *t_row0, *num_tiles;  // tile table of routed + shared blocks (merged shared expert)
   bf16_t *g, *u, *h, *y_pad;
-  bf16_t *sg, *su, *sh, *sy;  // shared expert: gate, up, h, output
+  bf16_t *sg, *su, *sh, *sy;  // shared expert run on its own: gate, up, h, output
 };
 
 size_t carve_saved(const Dims& q, void* base, Saved* sv) {
@@ -65,18 +78,23 @@ size_t carve_saved(const Dims& q, void* base, Saved* sv) {
   sv->order = c.take<int32_t>(q.M);
   sv->pos = c.take<int32_t>(q.M);
   sv->slot = c.take<int32_t>(q.M);
-  sv->row_src = c.take<int32_t>(q.P);
+  sv->row_src = c.take<int32_t>(q.PT);
   sv->blk_expert = c.take<int32_t>(q.MB);
   sv->blk_rows = c.take<int32_t>(q.MB);
   sv->num_blocks = c.take<int32_t>(4);
-  sv->g = c.take<bf16_t>(q.P * q.f);
-  sv->u = c.take<bf16_t>(q.P * q.f);
-  sv->h = c.take<bf16_t>(q.P * q.f);
-  sv->y_pad = c.take<bf16_t>(q.P * q.d);
-  sv->sg = c.take<bf16_t>(q.T * q.fs);
-  sv->su = c.take<bf16_t>(q.T * q.fs);
-  sv->sh = c.take<bf16_t>(q.T * q.fs);
-  sv->sy = c.take<bf16_t>(q.fs ? q.T * q.d : 0);
+  sv->t_expert = c.take<int32_t>(q.merged ? q.MT : 0);
+  sv->t_rows = c.take<int32_t>(q.merged ? q.MT : 0);
+  sv->t_row0 = c.take<int32_t>(q.merged ? q.MT : 0);
+  sv->num_tiles = c.take<int32_t>(4);
+  sv->g = c.take<bf16_t>(q.PT * q.f);
+  sv->u = c.take<bf16_t>(q.PT * q.f);
+  sv->h = c.take<bf16_t>(q.PT * q.f);
+  sv->y_pad = c.take<bf16_t>(q.PT * q.d);
+  const int64_t own = (q.fs && !q.merged) ? q.T : 0;  // rows of the separately run shared expert
+  sv->sg = c.take<bf16_t>(own * q.fs);
+  sv->su = c.take<bf16_t>(own * q.fs);
+  sv->sh = c.take<bf16_t>(own * q.fs);
+  sv->sy = c.take<bf16_t>(own * q.d);
   return c.off + 256;
 }
 
@@ -107,17 +125,18 @@ struct BwdWs {
 
 size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   Carve c(base);
-  w->dy_pad = c.take<bf16_t>(q.P * q.d);
-  w->dgu = c.take<bf16_t>(q.P * 2 * q.f);
-  w->dx_pad = c.take<bf16_t>(q.P * q.d);
-  w->sdgu = c.take<bf16_t>(q.T * 2 * q.fs);
-  w->sdx = c.take<bf16_t>(q.fs ? q.T * q.d : 0);
+  w->dy_pad = c.take<bf16_t>(q.PT * q.d);
+  w->dgu = c.take<bf16_t>(q.PT * 2 * q.f);
+  w->dx_pad = c.take<bf16_t>(q.PT * q.d);
+  const int64_t own = (q.fs && !q.merged) ? q.T : 0;
+  w->sdgu = c.take<bf16_t>(own * 2 * q.fs);
+  w->sdx = c.take<bf16_t>(own * q.d);
   w->dlog = c.take<bf16_t>(q.T * q.E);
   w->w_rT = c.take<bf16_t>(q.E * q.d);
   w->dl = c.take<float>(q.M);
   w->dweights = c.take<float>(q.M);
   size_t part = 0;
-  if (q.fs) {
+  if (q.fs && !q.merged) {
     part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, 2 * q.fs, dense_splits(q.T, q.d, 2 * q.fs)));
     part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.fs, q.d, dense_splits(q.T, q.fs, q.d)));
   }
@@ -125,13 +144,45 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   w->part = c.take<char>(part);
   w->part_r_bytes = lsurge::wgrad_workspace_bytes(1, q.d, q.E, dense_splits(q.T, q.d, q.E));
   w->part_r = c.take<char>(w->part_r_bytes);
-  w->cplan = lsurge::wgrad_chunk_plan(q.M, q.E);
+  w->cplan = q.merged ? lsurge::wgrad_chunk_plan(q.M + q.T, q.E + 1) : lsurge::wgrad_chunk_plan(q.M, q.E);
   w->chunk_tab = c.take<int32_t>(lsurge::wgrad_chunk_table_ints(w->cplan, q.E));
   w->part_dn_bytes = lsurge::wgrad_chunked_workspace_bytes(w->cplan, q.f, q.d);
   w->part_dn = c.take<char>(w->part_dn_bytes);
   w->part_gu_bytes = lsurge::wgrad_chunked_workspace_bytes(w->cplan, q.d, 2 * q.f);
   w->part_gu = c.take<char>(w->part_gu_bytes);
   return c.off + 256;
+}
+
+// Tile table of the grouped GEMMs with the shared expert carried as expert E: routed blocks [0, nb) as the layout
+// wrote them, then the SB shared blocks (rows 128 MB + 128 j ..), then empty entries up to the bound MB + SB.
+// Also fills row_src of the shared rows (token t -> flat slot t k, so the row gather reads x[t]).
+__global__ void shared_tiles_kernel(const int32_t* __restrict__ blk_expert, const int32_t* __restrict__ blk_rows,
+                                    const int32_t* __restrict__ num_blocks, int MB, int E, int64_t T, int k,
+                                    int32_t* __restrict__ t_expert, int32_t* __restrict__ t_rows,
+                                    int32_t* __restrict__ t_row0, int32_t* __restrict__ num_tiles,
+                                    int32_t* __restrict__ row_src) {
+  const int nb = min(num_blocks[0], MB);
+  const int SB = (int)((T + BLK - 1) / BLK);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t i = i0; i < MB + SB; i += stride) {
+    if (i < nb) {
+      t_expert[i] = blk_expert[i];
+      t_rows[i] = blk_rows[i];
+      t_row0[i] = (int32_t)(i * BLK);
+    } else if (i < nb + SB) {
+      const int64_t j = i - nb;
+      t_expert[i] = E;
+      t_rows[i] = (int32_t)min((int64_t)BLK, T - j * BLK);
+      t_row0[i] = (int32_t)((MB + j) * BLK);
+    } else {
+      t_expert[i] = -1;
+      t_rows[i] = 0;
+      t_row0[i] = 0;
+    }
+  }
+  for (int64_t r = i0; r < T; r += stride) row_src[(int64_t)MB * BLK + r] = (int32_t)(r * k);
+  if (i0 == 0) num_tiles[0] = nb + SB;
 }
 
 int check_shape(const lsurge_moe_shape* s) {
@@ -144,7 +195,7 @@ int check_shape(const lsurge_moe_shape* s) {
   LSURGE_REQUIRE(s->d % 64 == 0 && s->f % 64 == 0 && s->fs % 64 == 0,
                  "moe: d, f and fs must be multiples of 64 (d=%lld f=%lld fs=%lld)", (long long)s->d, (long long)s->f,
                  (long long)s->fs);
-  LSURGE_REQUIRE(s->t * s->k < (1ll << 31) && lsurge_max_blocks(s->t * s->k, s->e) * BLK < (1ll << 31),
+  LSURGE_REQUIRE(s->t * s->k < (1ll << 31) && (lsurge_max_blocks(s->t * s->k, s->e) + s->t / BLK + 1) * BLK < (1ll << 31),
                  "moe: too many routed rows");
   return LSURGE_OK;
 }
@@ -224,7 +275,7 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   hipStream_t s0 = fg.f.side[0];
 
   if (int rc = lsurge::stream_after(s0, st, fg.f.ev[0])) return rc;
-  if (q.fs) {
+  if (q.fs && !q.merged) {  // shared expert of its own width: dense GEMMs on the helper stream
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
     if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
                                               q.fs, sv.sh, sv.sg, sv.su, q.fs, s0))
@@ -239,20 +290,34 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
                                          sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks, workspace,
                                          workspace_bytes, st))
     return rc;
-  const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+  lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+  lsurge::ExtraExpert xgu, xdn;  // the shared expert's weights when it rides along as expert E
+  const bf16_t* shared_y = q.fs ? sv.sy : nullptr;
+  if (q.merged) {
+    LSURGE_LAUNCH(KID_MISC, st,
+                  hipLaunchKernelGGL(shared_tiles_kernel, dim3(256), dim3(256), 0, st, sv.blk_expert, sv.blk_rows,
+                                     sv.num_blocks, (int)q.MB, (int)q.E, q.T, (int)q.k, sv.t_expert, sv.t_rows,
+                                     sv.t_row0, sv.num_tiles, sv.row_src));
+    blocks = lsurge::GemmBlocks{sv.t_expert, sv.t_rows, sv.t_row0, sv.num_tiles, (int)q.MT, 0};
+    xgu.expert = xdn.expert = (int)q.E;
+    xgu.B = p->ws_gate;
+    xgu.B2 = p->ws_up;
+    xdn.B = p->ws_down;
+    shared_y = sv.y_pad + q.P * q.d;  // rows 128 MB + t
+  }
   lsurge::RowGather gather;
   gather.rows = sv.row_src;
   gather.div = (int)q.k;
   gather.nrows = q.T;
   if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_GEMM_GU_FWD, blocks, p->x, q.d, p->w_gate, p->w_up, q.f, q.d * q.f,
-                                            q.d, q.f, sv.h, sv.g, sv.u, q.f, st, gather))
+                                            q.d, q.f, sv.h, sv.g, sv.u, q.f, st, gather, xgu))
     return rc;
   if (int rc = lsurge::gemm_rows_kn(KID_GEMM_DOWN_FWD, blocks, sv.h, q.f, p->w_down, q.d, q.f * q.d, q.f, q.d, sv.y_pad,
-                                    q.d, st))
+                                    q.d, st, false, xdn))
     return rc;
   if (int rc = lsurge::stream_after(st, s0, fg.f.ev[1])) return rc;
-  return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sv.sy : nullptr, out,
-                                    LSURGE_BF16, st);
+  return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, shared_y, out, LSURGE_BF16,
+                                    st);
 }
 
 // Backward.  Stream plan (caller's stream = critical path):
@@ -278,7 +343,19 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   carve_bwd(q, workspace, &w);
   hipStream_t st = (hipStream_t)stream;
   float* dweights = g->dweights ? g->dweights : w.dweights;
-  const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+  lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+  lsurge::ExtraExpert xgu, xdn;  // the shared expert carried as expert E: its weights and gradients
+  lsurge::ExtraOut ogu, odn;
+  if (q.merged) {
+    blocks = lsurge::GemmBlocks{sv.t_expert, sv.t_rows, sv.t_row0, sv.num_tiles, (int)q.MT, 0};
+    xgu.expert = xdn.expert = ogu.expert = odn.expert = (int)q.E;
+    xgu.B = p->ws_gate;
+    xgu.B2 = p->ws_up;
+    xdn.B = p->ws_down;
+    ogu.C = g->dws_gate;
+    ogu.C2 = g->dws_up;
+    odn.C = g->dws_down;
+  }
   ForkGuard fg;
   if (int rc = fg.acquire(st)) return rc;
   hipStream_t s0 = fg.f.side[0], s1 = fg.f.side[1];
@@ -288,8 +365,8 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   if (int rc = lsurge::stream_after(s0, st, ev[0])) return rc;
   if (int rc = lsurge::stream_after(s1, st, ev[1])) return rc;
 
-  // s0: shared expert backward
-  if (q.fs) {
+  // s0: backward of a shared expert of its own width
+  if (q.fs && !q.merged) {
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
     if (int rc = lsurge::gemm_rows_nk(KID_SHARED_DOWN_DGRAD, dense, dy, q.d, p->ws_down, nullptr, 0, q.d, 0, q.d, q.fs,
                                       w.sdgu, 2 * q.fs, true, sv.sg, sv.su, q.fs, s0))
@@ -311,15 +388,19 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
 
   // main: chunk table of the routed weight gradients (read by both wgrads, after the s1 fork below)
   lsurge::WgradChunks chunks;
-  if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, st)) return rc;
-  // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel)
+  if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, st,
+                                         q.merged ? q.T : -1, q.P))
+    return rc;
+  // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel); a merged
+  // shared expert's rows of dY_pad get dY itself
   if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, q.P, sv.slot, sv.weights, q.T, (int)q.k, q.d, dy, w.dy_pad,
-                                              dweights, w.dl, st))
+                                              dweights, w.dl, st, q.merged ? w.dy_pad + q.P * q.d : nullptr))
     return rc;
   if (int rc = lsurge::stream_after(s1, st, ev[2])) return rc;
   // s1: down wgrad dW_down[e] = h_e^T dY_e; router: dW_r = x^T dlogits (bf16 MFMA over the dense [T, E] dlogits)
   if (int rc = lsurge::gemm_wgrad_chunked(KID_GEMM_DOWN_WGRAD, chunks, (int)q.E, q.T, sv.h, q.f, w.dy_pad, q.d, q.f,
-                                          q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, w.part_dn, w.part_dn_bytes, s1))
+                                          q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, w.part_dn, w.part_dn_bytes, s1,
+                                          lsurge::RowGather(), odn))
     return rc;
   if (int rc = lsurge::launch_scatter_dlogits(w.dl, sv.sel, q.T, (int)q.E, (int)q.k, w.dlog, s1)) return rc;
   {
@@ -330,17 +411,18 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   }
   // main: down dgrad + SwiGLU backward: dH = dY W_down^T -> [dG | dU]
   if (int rc = lsurge::gemm_rows_nk(KID_GEMM_DOWN_DGRAD, blocks, w.dy_pad, q.d, p->w_down, nullptr, 0, q.d, q.f * q.d,
-                                    q.d, q.f, w.dgu, 2 * q.f, true, sv.g, sv.u, q.f, st))
+                                    q.d, q.f, w.dgu, 2 * q.f, true, sv.g, sv.u, q.f, st, false, xdn))
     return rc;
   // main: gate/up dgrad: dX_pad = dG W_gate^T + dU W_up^T
   if (int rc = lsurge::gemm_rows_nk(KID_GEMM_GU_DGRAD, blocks, w.dgu, 2 * q.f, p->w_gate, p->w_up, q.f, q.f, q.d * q.f,
-                                    2 * q.f, q.d, w.dx_pad, q.d, false, nullptr, nullptr, 0, st))
+                                    2 * q.f, q.d, w.dx_pad, q.d, false, nullptr, nullptr, 0, st, false, xgu))
     return rc;
   // join all helpers, then dx = gather-reduce of dX_pad + router dx term + shared-expert dx, one rounding
   if (int rc = lsurge::stream_after(st, s0, ev[4])) return rc;
   if (int rc = lsurge::stream_after(st, s1, ev[5])) return rc;
-  if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT,
-                                              q.fs ? w.sdx : nullptr, g->dx, st))
+  const bf16_t* shared_dx = q.merged ? w.dx_pad + q.P * q.d : (q.fs ? w.sdx : nullptr);
+  if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT, shared_dx,
+                                              g->dx, st))
     return rc;
   // main: gate/up wgrad: [dW_gate | dW_up][e] = x_e^T [dG | dU]_e
   {
@@ -350,7 +432,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
     gather.nrows = q.T;
     if (int rc = lsurge::gemm_wgrad_chunked(KID_GEMM_GU_WGRAD, chunks, (int)q.E, q.T, p->x, q.d, w.dgu, 2 * q.f, q.d,
                                             2 * q.f, g->dw_gate, g->dw_up, q.f, q.f, q.d * q.f, w.part_gu,
-                                            w.part_gu_bytes, st, gather))
+                                            w.part_gu_bytes, st, gather, ogu))
       return rc;
   }
   return LSURGE_OK;

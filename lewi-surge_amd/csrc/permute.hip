@@ -381,20 +381,27 @@ __global__ __launch_bounds__(PM_THREADS) void combine_pad_kernel(const bf16_t* _
 // Fused combine backward of the layer (bf16 rows): per token, g is read once; for every choice j the expert
 // row y_pad[slot] is read once, dy_pad[slot] = bf16(w_j g) written once and <g, y> reduced; then the router
 // term dl[t,j] = w_j (dw_j - sum_i w_i dw_i).  moe_permute.py:303-309 does this in two passes over g and y.
+// gcopy (optional): g row t is also copied to gcopy[t] (the shared expert's rows of the padded dY, when the shared
+// expert rides along the routed experts).
 template <int NC, int KK>
 __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_t* __restrict__ yp,
                                                                      const int32_t* __restrict__ slot,
                                                                      const float* __restrict__ w, int64_t n,
                                                                      int64_t d, const bf16_t* __restrict__ g,
                                                                      bf16_t* __restrict__ dyp, float* __restrict__ dw,
-                                                                     float* __restrict__ dl) {
+                                                                     float* __restrict__ dl,
+                                                                     bf16_t* __restrict__ gcopy) {
   static_assert(NC > 0 && KK > 0, "fixed-shape kernel");
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
   for (int64_t t = wave_id(); t < n; t += nwaves) {
     float gv[NC][8];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) V8<LSURGE_BF16>::ld(g + t * d + (c * 64 + lane) * 8, gv[c]);
+    for (int c = 0; c < NC; ++c) {
+      const int64_t o = t * d + (c * 64 + lane) * 8;
+      if (gcopy) *reinterpret_cast<u32x4*>(gcopy + o) = *reinterpret_cast<const u32x4*>(g + o);
+      V8<LSURGE_BF16>::ld(g + o, gv[c]);
+    }
     float dot[KK];
 #pragma unroll
     for (int j = 0; j < KK; ++j) {
@@ -590,7 +597,7 @@ int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, co
 }
 
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
-                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s) {
+                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s, void* gcopy) {
   const dim3 grid(grid_for_rows(n));
   const int nc = row_chunks(d);
   if (nc && (k == 6 || k == 8)) {
@@ -598,10 +605,14 @@ int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, co
       if (NC && KK)
         LSURGE_LAUNCH(KID_COMBINE_BWD, s,
                       hipLaunchKernelGGL((combine_bwd_pad_kernel<NC ? NC : 1, KK ? KK : 1>), grid, dim3(PM_THREADS), 0,
-                                         s, (const bf16_t*)yp, slot, w, n, d, (const bf16_t*)g, (bf16_t*)dyp, dw, dl));
+                                         s, (const bf16_t*)yp, slot, w, n, d, (const bf16_t*)g, (bf16_t*)dyp, dw, dl,
+                                         (bf16_t*)gcopy));
     }));
     return LSURGE_OK;
   }
+  if (gcopy)  // generic shapes: a plain copy of g into the shared expert's rows
+    if (hipMemcpyAsync(gcopy, g, (size_t)n * d * 2, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return lsurge::set_error(LSURGE_ERR_LAUNCH, "combine_bwd: copy of dY into the shared rows failed");
   LSURGE_LAUNCH(KID_COMBINE_BWD, s,
                 hipLaunchKernelGGL((combine_bwd_kernel<LSURGE_BF16, LSURGE_BF16, true>), grid, dim3(PM_THREADS), 0, s,
                                    yp, rows, slot, w, n, k, d, g, dyp, dw, dl));
