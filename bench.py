@@ -42,29 +42,32 @@ def kernel_work(c):
     """Algorithmic work per launch of each kernel: ('mfma', flops) over useful rows, or ('hbm', bytes)."""
     T, d, E, k, f, fs = c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"]
     M = T * k
-    if fs and fs == f:  # the shared expert rides along the routed experts: T more rows in every grouped GEMM
-        M += T
+    # the backward's grouped GEMMs carry the shared expert as one more expert (T rows) when fs == f
+    Mb = M + T if fs and fs == f else M
     w = {
         "gemm_gu_fwd": ("mfma", 2 * M * d * 2 * f),
         "gemm_down_fwd": ("mfma", 2 * M * f * d),
-        "gemm_down_dgrad": ("mfma", 2 * M * d * f),
-        "gemm_down_wgrad": ("mfma", 2 * M * f * d),
-        "gemm_gu_dgrad": ("mfma", 2 * M * 2 * f * d),
-        "gemm_gu_wgrad": ("mfma", 2 * M * d * 2 * f),
+        "gemm_down_dgrad": ("mfma", 2 * Mb * d * f),
+        "gemm_down_wgrad": ("mfma", 2 * Mb * f * d),
+        "gemm_gu_dgrad": ("mfma", 2 * Mb * 2 * f * d),
+        "gemm_gu_wgrad": ("mfma", 2 * Mb * d * 2 * f),
         "router_wgrad": ("mfma", 2 * T * d * E),
         "router_topk": ("hbm", T * d * 2 + d * E * 2 + T * E * 4),
         "router_select": ("hbm", T * E * 4 + 8 * T * k),
         "dispatch": ("hbm", 2 * M * d * 2 + 4 * M),
         "combine_fwd": ("hbm", M * d * 2 + T * d * 2 * (2 if fs else 1) + 8 * T * k),
-        "combine_bwd": ("hbm", 2 * M * d * 2 + T * d * 2 + 16 * T * k),
+        "combine_bwd": ("hbm", 2 * M * d * 2 + T * d * 2 * (2 if Mb > M else 1) + 16 * T * k),  # + dY copy
         "dispatch_bwd": ("hbm", M * d * 2 + T * d * 2 * (2 if fs else 1) + 12 * T * k),
         "layout_hist": ("hbm", 4 * M),
         "layout_rank": ("hbm", 4 * M + 16 * M),
     }
-    if fs and fs != f:
+    if fs:
         w.update({
             "shared_gu_fwd": ("mfma", 2 * T * d * 2 * fs),
             "shared_down_fwd": ("mfma", 2 * T * fs * d),
+        })
+    if fs and fs != f:
+        w.update({
             "shared_down_dgrad": ("mfma", 2 * T * d * fs),
             "shared_down_wgrad": ("mfma", 2 * T * fs * d),
             "shared_gu_dgrad": ("mfma", 2 * T * 2 * fs * d),

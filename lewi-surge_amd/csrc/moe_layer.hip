@@ -3,11 +3,12 @@
 // Forward:  router top-k -> routing layout -> gate/up grouped GEMM over 128-row expert blocks whose rows are
 //           gathered from x (the dispatch, fused into the GEMM's operand load) with the SiLU*mul epilogue -> down
 //           grouped GEMM -> weighted combine (+ shared expert).
-// Shared expert.  When its FFN width equals the routed one (fs == f) it rides along the routed experts as expert E:
-// its T rows (every token once) follow the routed block bound in the padded row space, so every grouped GEMM of
-// the layer covers routed and shared rows in one launch (tiles of expert E read the shared weights), and its
-// weight gradients join the routed chunk table.  Otherwise it runs as dense (E = 1) GEMMs of its own on a
-// helper stream.
+// Shared expert.  Its forward runs as dense (E = 1) GEMMs on a helper stream, where it overlaps the router and the
+// layout (it depends on x only).  When its FFN width equals the routed one (fs == f) its rows (every token once)
+// sit right after the routed block bound in the padded row space, and in the backward it rides along the routed
+// experts as expert E: every grouped GEMM covers routed and shared rows in one launch (tiles of expert E read the
+// shared weights) and its weight gradients join the routed chunk table.  Otherwise its backward is dense GEMMs
+// of its own on a helper stream.
 // Backward: fused combine backward (dY rows, d(routing weights), d(router logits)) -> down dgrad with the
 //           SwiGLU backward epilogue -> down wgrad -> gate/up dgrad -> gate/up wgrad -> shared expert ->
 //           router wgrad -> dispatch backward (gather-reduce, plus the router and shared-expert dx terms).
@@ -254,7 +255,7 @@ struct ForkGuard {
 extern "C" {
 
 // Forward.  Stream plan:
-//   main: router -> layout -> gate/up GEMM -> down GEMM -> [join] -> combine
+//   main: router -> layout (-> tile table of the backward) -> gate/up GEMM -> down GEMM -> [join] -> combine
 //   s0:   shared expert (depends on x only)
 // The dispatch into padded expert blocks is fused into the gate/up GEMM: its A tiles are gathered straight from
 // the token rows x through row_src (padded row -> flat slot t*k + j), so the padded copy of x is never
@@ -274,14 +275,23 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   if (int rc = fg.acquire(st)) return rc;
   hipStream_t s0 = fg.f.side[0];
 
+  // s0: the shared expert's forward, dense GEMMs over all T tokens (it depends on x only, so it overlaps the
+  // router and the layout).  A merged shared expert writes its g, u, h and output rows where the backward's tile
+  // table expects expert E (padded rows 128 MB + t).
+  bf16_t *sg = sv.sg, *su = sv.su, *sh = sv.sh, *sy = sv.sy;
+  if (q.merged) {
+    sg = sv.g + q.P * q.f;
+    su = sv.u + q.P * q.f;
+    sh = sv.h + q.P * q.f;
+    sy = sv.y_pad + q.P * q.d;
+  }
   if (int rc = lsurge::stream_after(s0, st, fg.f.ev[0])) return rc;
-  if (q.fs && !q.merged) {  // shared expert of its own width: dense GEMMs on the helper stream
+  if (q.fs) {
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
     if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
-                                              q.fs, sv.sh, sv.sg, sv.su, q.fs, s0))
+                                              q.fs, sh, sg, su, q.fs, s0))
       return rc;
-    if (int rc = lsurge::gemm_rows_kn(KID_SHARED_DOWN_FWD, dense, sv.sh, q.fs, p->ws_down, q.d, 0, q.fs, q.d, sv.sy, q.d,
-                                      s0))
+    if (int rc = lsurge::gemm_rows_kn(KID_SHARED_DOWN_FWD, dense, sh, q.fs, p->ws_down, q.d, 0, q.fs, q.d, sy, q.d, s0))
       return rc;
   }
   if (int rc = lsurge_router_topk(p->x, p->w_r, p->bias, q.T, q.d, q.E, q.k, sv.logits, sv.sel, sv.weights, stream))
@@ -290,43 +300,34 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
                                          sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks, workspace,
                                          workspace_bytes, st))
     return rc;
-  lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
-  lsurge::ExtraExpert xgu, xdn;  // the shared expert's weights when it rides along as expert E
-  const bf16_t* shared_y = q.fs ? sv.sy : nullptr;
-  if (q.merged) {
+  const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+  if (q.merged)  // the backward's tile table: routed blocks, then the shared expert's (and its row_src)
     LSURGE_LAUNCH(KID_MISC, st,
                   hipLaunchKernelGGL(shared_tiles_kernel, dim3(256), dim3(256), 0, st, sv.blk_expert, sv.blk_rows,
                                      sv.num_blocks, (int)q.MB, (int)q.E, q.T, (int)q.k, sv.t_expert, sv.t_rows,
                                      sv.t_row0, sv.num_tiles, sv.row_src));
-    blocks = lsurge::GemmBlocks{sv.t_expert, sv.t_rows, sv.t_row0, sv.num_tiles, (int)q.MT, 0};
-    xgu.expert = xdn.expert = (int)q.E;
-    xgu.B = p->ws_gate;
-    xgu.B2 = p->ws_up;
-    xdn.B = p->ws_down;
-    shared_y = sv.y_pad + q.P * q.d;  // rows 128 MB + t
-  }
   lsurge::RowGather gather;
   gather.rows = sv.row_src;
   gather.div = (int)q.k;
   gather.nrows = q.T;
   if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_GEMM_GU_FWD, blocks, p->x, q.d, p->w_gate, p->w_up, q.f, q.d * q.f,
-                                            q.d, q.f, sv.h, sv.g, sv.u, q.f, st, gather, xgu))
+                                            q.d, q.f, sv.h, sv.g, sv.u, q.f, st, gather))
     return rc;
   if (int rc = lsurge::gemm_rows_kn(KID_GEMM_DOWN_FWD, blocks, sv.h, q.f, p->w_down, q.d, q.f * q.d, q.f, q.d, sv.y_pad,
-                                    q.d, st, false, xdn))
+                                    q.d, st))
     return rc;
   if (int rc = lsurge::stream_after(st, s0, fg.f.ev[1])) return rc;
-  return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, shared_y, out, LSURGE_BF16,
-                                    st);
+  return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sy : nullptr, out,
+                                    LSURGE_BF16, st);
 }
 
 // Backward.  Stream plan (caller's stream = critical path):
-//   main:  combine bwd -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
-//   s0:    shared expert: down dgrad, down wgrad, gate/up dgrad, gate/up wgrad   (needs dy only)
+//   main:  chunk table -> combine bwd -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd ->
+//          gate/up wgrad
+//   s0:    a shared expert of its own width (fs != f): down dgrad, down wgrad, gate/up dgrad, gate/up wgrad
 //   s1:    W_r transpose; after combine bwd: down wgrad, d(logits) scatter, router wgrad
-// The helper chains overlap the first two kernels of the main chain; the two largest GEMMs run after them on
-// their own (every GEMM here is bound by the operand-copy path, so overlapping two of them gains little), and
-// the dispatch backward reads dX_pad right after the GEMM that wrote it, while it is still in cache.
+// The helper chains overlap the dgrads of the main chain; the gate/up weight gradient runs after the join on its
+// own, and the dispatch backward reads dX_pad right after the GEMM that wrote it, while it is still in cache.
 int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* dy, const void* saved,
                    const lsurge_moe_grads* g, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
   if (int rc = check_shape(s)) return rc;
