@@ -164,6 +164,136 @@ def cpu_baseline(c, target_s=15.0):
                        f"x {n} iterations ({el:.1f} s), BLAS threads={cores}, router in C (1 thread)")
 
 
+# ------------------------------------------------------------------------------------------ profile summary
+def short_kernel(name):
+    """rocprofv3 kernel name -> template name with its integer template arguments, e.g. gemm_rows_kernel<1,1>."""
+    import re
+    n = name.replace("void ", "")
+    n = re.sub(r"\([^()]*\)$", "", n)               # argument list
+    n = re.sub(r"lsgemm::GemmCfg<[^>]*>,? ?", "", n)  # the tile shape (one for every GEMM)
+    n = n.replace("lsgemm::", "").replace("(anonymous namespace)::", "")
+    n = n.replace(" ", "").replace("<>", "")
+    return n
+
+
+def launch_roles(c):
+    """Role of every hot-path launch of one layer call, per kernel template, in host submission order."""
+    fs, f = c["fs"], c["f"]
+    own = bool(fs) and fs != f  # shared expert of its own width: dense backward GEMMs on a helper stream
+    r = {
+        "router_logits_kernel": ["router_topk"], "router_select_lane_kernel<8>": ["router_select"],
+        "router_select_lane_kernel<16>": ["router_select"], "router_select_kernel<1>": ["router_select"],
+        "router_select_kernel<2>": ["router_select"], "router_select_kernel<4>": ["router_select"],
+        "layout_hist_kernel": ["layout_hist"], "layout_scan_kernel": ["layout_scan"],
+        "layout_rank_kernel": ["layout_rank"], "shared_tiles_kernel": ["misc"],
+        "gemm_rows_kernel<1,1>": (["shared_gu_fwd"] if fs else []) + ["gemm_gu_fwd"],
+        "gemm_rows_kernel<1,0>": (["shared_down_fwd"] if fs else []) + ["gemm_down_fwd"],
+        "combine_pad_kernel<2,6,1>": ["combine_fwd"], "combine_pad_kernel<2,8,1>": ["combine_fwd"],
+        "combine_pad_kernel<4,8,1>": ["combine_fwd"],
+    }
+    if c["bwd"]:
+        r.update({
+            "gemm_rows_kernel<0,2>": (["shared_down_dgrad"] if own else []) + ["gemm_down_dgrad"],
+            "gemm_rows_kernel<0,0>": (["shared_gu_dgrad"] if own else []) + ["gemm_gu_dgrad"],
+            "gemm_wgrad_kernel": (["shared_down_wgrad", "shared_gu_wgrad"] if own else [])
+                                 + ["gemm_down_wgrad", "router_wgrad", "gemm_gu_wgrad"],
+            "splitk_reduce_kernel": ["splitk_reduce"] * (3 if own else 1),
+            "wgrad_chunk_reduce_kernel": ["chunk_reduce", "chunk_reduce"],
+            "wgrad_chunks_kernel": ["misc"], "transpose_bf16_kernel": ["misc"], "scatter_dlogits_kernel": ["misc"],
+            "combine_bwd_pad_kernel<2,6>": ["combine_bwd"], "combine_bwd_pad_kernel<2,8>": ["combine_bwd"],
+            "combine_bwd_pad_kernel<4,8>": ["combine_bwd"],
+            "dispatch_bwd_pad_kernel<2,6>": ["dispatch_bwd"], "dispatch_bwd_pad_kernel<2,8>": ["dispatch_bwd"],
+            "dispatch_bwd_pad_kernel<4,8>": ["dispatch_bwd"],
+        })
+    return r
+
+
+def label_launches(rows, c):
+    """rows: dicts with Correlation_Id and Kernel_Name -> list of (role, short name, row) for the hot-path launches.
+    The forward's dense shared-expert GEMMs (launched before the router, on a helper stream) are told apart from the
+    routed ones by their workgroup count; otherwise a layer call starts at each router_logits_kernel and within it
+    the n-th launch of a template has the n-th role."""
+    roles = launch_roles(c)
+    T, d, fs = c["T"], c["d"], c["fs"]
+    pad8 = lambda n: (n + 7) // 8 * 8  # noqa: E731
+    tb = (T + 127) // 128
+    shared_wgs = {"gemm_rows_kernel<1,1>": pad8((fs + 127) // 128 * tb), "gemm_rows_kernel<1,0>": pad8((d + 255) // 256 * tb)}
+
+    def wgs(row):
+        g = row.get("Grid_Size_X", row.get("Grid_Size"))
+        w = row.get("Workgroup_Size_X", row.get("Workgroup_Size"))
+        return int(g) // max(1, int(w))
+
+    out, seen = [], {}
+    for row in sorted(rows, key=lambda x: int(x["Correlation_Id"])):
+        k = short_kernel(row["Kernel_Name"])
+        if k == "router_logits_kernel":
+            seen = {}
+        if k not in roles:
+            continue
+        if fs and k in shared_wgs:  # forward GEMM: shared (dense) or routed
+            shared = wgs(row) == shared_wgs[k]
+            out.append((roles[k][0 if shared else 1], k, row))
+            continue
+        i = seen.get(k, 0)
+        seen[k] = i + 1
+        out.append((roles[k][i] if i < len(roles[k]) else "other", k, row))
+    return out
+
+
+def profile_summary(a):
+    """Markdown summary of rocprofv3 outputs of bench.py runs (kernel trace; FETCH_SIZE / WRITE_SIZE counter runs of
+    the layer and of --copy-probe for calibration), with `bench-traffic <role> <bytes>` lines for the roofline."""
+    import csv
+    import glob
+
+    c = CONFIGS[a.config]
+
+    def rows_of(d, kind):
+        files = glob.glob(os.path.join(d, f"*{kind}.csv"))
+        if not files:
+            raise SystemExit(f"profile summary: no *{kind}.csv under {d}")
+        with open(files[0]) as fh:
+            return list(csv.DictReader(fh))
+
+    trace = label_launches(rows_of(a.profile_summary, "kernel_trace"), c)
+    dur = {}
+    for role, k, row in trace:
+        dur.setdefault((role, k), []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    counters = {}
+    fac = {}
+    for name, d, cd in (("FETCH_SIZE", a.pmc_fetch, a.copy_fetch), ("WRITE_SIZE", a.pmc_write, a.copy_write)):
+        if not d:
+            continue
+        probe = [r for r in rows_of(cd, "counter_collection") if "copyBuffer" in r["Kernel_Name"]] if cd else []
+        # the copy probe moves 1 GiB per launch: bytes = KiB counter x 1024 x factor
+        fac[name] = (a.copy_probe_mib << 20) / (sum(float(r["Counter_Value"]) for r in probe) / len(probe) * 1024) \
+            if probe else 1.0
+        for role, k, row in label_launches([r for r in rows_of(d, "counter_collection") if r["Counter_Name"] == name], c):
+            counters.setdefault((role, name), []).append(float(row["Counter_Value"]) * 1024 * fac[name])
+    total = sum(sum(v) for v in dur.values())
+    print("| role | kernel | launches | avg us | share of hot-path GPU time | HBM read MB / launch | "
+          "HBM write MB / launch |")
+    print("|---|---|---|---|---|---|---|")
+    traffic = {}
+    for (role, k), v in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+        rd = counters.get((role, "FETCH_SIZE"))
+        wr = counters.get((role, "WRITE_SIZE"))
+        rmb = sum(rd) / len(rd) if rd else None
+        wmb = sum(wr) / len(wr) if wr else None
+        if rmb is not None and wmb is not None:
+            traffic[role] = rmb + wmb
+        fmt = lambda x: "-" if x is None else f"{x / 1e6:.1f}"  # noqa: E731
+        print(f"| {role} | `{k}` | {len(v)} | {sum(v) / len(v):.1f} | {100 * sum(v) / total:.1f}% | {fmt(rmb)} | "
+              f"{fmt(wmb)} |")
+    print()
+    for n, f in fac.items():
+        print(f"calibration {n}: x{f:.3f} (bytes per KiB-count unit x 1024)")
+    print()
+    for role, b in sorted(traffic.items()):
+        print(f"bench-traffic {role} {b:.0f}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,6 +305,14 @@ def main():
     ap.add_argument("--concurrency", type=int, default=1,
                     help="timed region: 1 runs the layer's independent chains on helper streams "
                          "(lsurge_set_concurrency), 0 everything on one stream")
+    ap.add_argument("--profile-summary", metavar="DIR", help="print the markdown summary of a rocprofv3 "
+                    "--kernel-trace output directory of this bench (with --pmc-fetch/--pmc-write and "
+                    "--copy-fetch/--copy-write counter directories for traffic) and exit")
+    ap.add_argument("--pmc-fetch", metavar="DIR")
+    ap.add_argument("--pmc-write", metavar="DIR")
+    ap.add_argument("--copy-fetch", metavar="DIR")
+    ap.add_argument("--copy-write", metavar="DIR")
+    ap.add_argument("--copy-probe-mib", type=int, default=1024, help="size of the --copy-probe run being calibrated on")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against a known byte count) and exit")
@@ -183,6 +321,10 @@ def main():
         print("bench.py: this build measures one GPU only (the MoE layer at one GPU's share); "
               f"--gpus {a.gpus} is not supported", file=sys.stderr)
         sys.exit(2)
+
+    if a.profile_summary:
+        profile_summary(a)
+        return
 
     import torch
 
