@@ -138,7 +138,10 @@ int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_siz
 
 /* Backward of lsurge_ragged_dot for upstream g [m, n] bf16: dlhs [m, kdim] bf16 (rows past the groups
  * = 0) and drhs [e, kdim, n] f32.  Replaces the VJP of padded_gmm.padded_ragged_dot
- * (modal/padded_gmm.py:35-39 + XLA autodiff of the einsum at 67-68). */
+ * (modal/padded_gmm.py:35-39 + XLA autodiff of the einsum at 67-68).
+ * Workspace: lsurge_ragged_dot_bwd_workspace_bytes(m, kdim, n, e) lets drhs cut hot groups into row chunks
+ * (e <= 256); the forward's lsurge_ragged_dot_workspace_bytes(m, e) is also accepted (one slice per group). */
+size_t lsurge_ragged_dot_bwd_workspace_bytes(int64_t m, int64_t kdim, int64_t n, int64_t e);
 int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group_sizes, const void* g,
                           int64_t m, int64_t kdim, int64_t n, int64_t e, void* dlhs, float* drhs,
                           void* workspace, size_t workspace_bytes, lsurge_stream_t stream);

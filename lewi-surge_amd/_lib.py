@@ -61,6 +61,7 @@ _SIGS = {
     "lsurge_ragged_dot_workspace_bytes": (_sz, [_i64, _i64]),
     "lsurge_ragged_dot": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _int, _p, _sz, _p]),
     "lsurge_ragged_dot_bwd": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _sz, _p]),
+    "lsurge_ragged_dot_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "lsurge_moe_saved_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
     "lsurge_moe_fwd_workspace_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
     "lsurge_moe_bwd_workspace_bytes": (_sz, [ctypes.POINTER(MoeShape)]),

@@ -28,34 +28,94 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, int S, int 
   }
 }
 
-// block table of an unpadded ragged layout (rows of group e start at sum_{e'<e} gs[e']).  Group sizes are
-// clamped so that no group reaches past row m: negative sizes count as 0 and a sum above m is cut at m, so a
-// bad group_sizes array can never send the GEMMs outside lhs/out.
-__global__ void ragged_blocks_kernel(const int32_t* __restrict__ gs, int E, int64_t m, int max_blocks,
-                                     int32_t* __restrict__ blk_row0, int32_t* __restrict__ blk_rows,
-                                     int32_t* __restrict__ blk_expert, int32_t* __restrict__ num_blocks,
-                                     int32_t* __restrict__ total_rows, int32_t* __restrict__ e_row0,
-                                     int32_t* __restrict__ e_rows) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int b = 0, run = 0;
-  for (int e = 0; e < E; ++e) {
-    const int g = (int)min((int64_t)max(gs[e], 0), m - run);
-    e_rows[e] = g;
-    e_row0[e] = run;
-    for (int j = 0; j * BM < g; ++j, ++b) {
-      if (b < max_blocks) {
-        blk_row0[b] = run + j * BM;
-        blk_rows[b] = min(BM, g - j * BM);
-        blk_expert[b] = e;
-      }
+// Block table of an unpadded ragged layout (rows of group e start at sum_{e'<e} gs[e']), in two launches.  Group
+// sizes are clamped so that no group reaches past row m: negative sizes count as 0 and a sum above m is cut at m,
+// so a bad group_sizes array can never send the GEMMs outside lhs/out.
+// ragged_groups_kernel (one workgroup): clamped group starts and sizes and the exclusive scan of their 128-row
+// block counts, 1024 groups per pass with a running carry.
+__global__ __launch_bounds__(1024) void ragged_groups_kernel(const int32_t* __restrict__ gs, int E, int64_t m,
+                                                            int max_blocks, int32_t* __restrict__ e_row0,
+                                                            int32_t* __restrict__ e_rows, int32_t* __restrict__ e_boff,
+                                                            int32_t* __restrict__ num_blocks,
+                                                            int32_t* __restrict__ total_rows) {
+  __shared__ int64_t wsum[16];
+  __shared__ int wblk[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int64_t carry_rows = 0;
+  int carry_blk = 0;
+  for (int base = 0; base < E; base += 1024) {
+    const int e = base + tid;
+    const int64_t g = e < E ? (int64_t)max(gs[e], 0) : 0;
+    int64_t x = g;  // inclusive prefix of the raw sizes within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
     }
-    run += g;
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    int64_t wb = 0, tot = 0;
+    for (int i = 0; i < 16; ++i) {
+      if (i < w) wb += wsum[i];
+      tot += wsum[i];
+    }
+    const int64_t incl = carry_rows + wb + x;
+    const int64_t row0 = min(incl - g, m), rows = min(incl, m) - row0;
+    const int nb = (int)((rows + BM - 1) / BM);
+    int xb = nb;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(xb, o, 64);
+      if (lane >= o) xb += y;
+    }
+    __syncthreads();  // everyone has read wsum
+    if (lane == 63) wblk[w] = xb;
+    __syncthreads();
+    int bb = 0, btot = 0;
+    for (int i = 0; i < 16; ++i) {
+      if (i < w) bb += wblk[i];
+      btot += wblk[i];
+    }
+    if (e < E) {
+      e_row0[e] = (int32_t)row0;
+      e_rows[e] = (int32_t)rows;
+      e_boff[e] = carry_blk + bb + xb - nb;
+    }
+    carry_rows += tot;
+    carry_blk += btot;
+    __syncthreads();  // everyone has read wblk before the next pass overwrites it
   }
-  num_blocks[0] = min(b, max_blocks);
-  total_rows[0] = run;
-  for (int i = b; i < max_blocks; ++i) {
-    blk_rows[i] = 0;
-    blk_expert[i] = -1;
+  if (tid == 0) {
+    e_boff[E] = carry_blk;
+    num_blocks[0] = min(carry_blk, max_blocks);
+    total_rows[0] = (int32_t)min(carry_rows, m);
+  }
+}
+
+// ragged_blocks_kernel (grid over the block bound): block b belongs to the group e with e_boff[e] <= b <
+// e_boff[e + 1] (binary search; empty groups have e_boff[e] == e_boff[e + 1]); entries past the count are empty.
+__global__ void ragged_blocks_kernel(const int32_t* __restrict__ e_row0, const int32_t* __restrict__ e_rows,
+                                     const int32_t* __restrict__ e_boff, int E, int max_blocks,
+                                     int32_t* __restrict__ blk_row0, int32_t* __restrict__ blk_rows,
+                                     int32_t* __restrict__ blk_expert) {
+  const int nb = min(e_boff[E], max_blocks);
+  for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < max_blocks; b += gridDim.x * blockDim.x) {
+    if (b >= nb) {
+      blk_row0[b] = 0;
+      blk_rows[b] = 0;
+      blk_expert[b] = -1;
+      continue;
+    }
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (e_boff[mid] <= b) lo = mid;
+      else hi = mid - 1;
+    }
+    const int j = b - e_boff[lo];
+    blk_row0[b] = e_row0[lo] + j * BM;
+    blk_rows[b] = min(BM, e_rows[lo] - j * BM);
+    blk_expert[b] = lo;
   }
 }
 
@@ -73,7 +133,8 @@ __global__ void zero_rows_from_kernel(void* __restrict__ out, int64_t m, int64_t
 inline unsigned pad8(int64_t g) { return (unsigned)((g + 7) / 8 * 8); }
 
 // Chunk table of the routed weight gradients (one workgroup of 512 threads, thread e = expert e).  Expert e owns
-// padded rows [128 block_off[e], 128 block_off[e] + gs[e]); they are cut into ceil(gs[e] / R) chunks of R rows.
+// rows [row0_mult block_off[e], row0_mult block_off[e] + gs[e]) (row0_mult = 128 for the padded layout, 1 for a
+// ragged one); they are cut into ceil(gs[e] / R) chunks of R rows.
 // An optional extra expert (id E: the shared expert) owns x_rows rows from padded row x_row0.  An empty expert
 // keeps one empty chunk, which writes its zero gradient.  An expert with more than one chunk gets consecutive
 // partial slots (summed in chunk order by wgrad_chunk_reduce_kernel) and an entry in split_list (ascending e).
@@ -104,8 +165,8 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh) {  // WC_THREADS 
 }
 
 __global__ __launch_bounds__(WC_THREADS) void wgrad_chunks_kernel(
-    const int32_t* __restrict__ gs, const int32_t* __restrict__ block_off, int E, int R, int max_chunks,
-    int max_parts, int x_rows, int x_row0, int32_t* __restrict__ c_expert, int32_t* __restrict__ c_row0,
+    const int32_t* __restrict__ gs, const int32_t* __restrict__ block_off, int row0_mult, int E, int R,
+    int max_chunks, int max_parts, int x_rows, int x_row0, int32_t* __restrict__ c_expert, int32_t* __restrict__ c_row0,
     int32_t* __restrict__ c_rows, int32_t* __restrict__ c_part, int32_t* __restrict__ num_chunks,
     int32_t* __restrict__ e_pbase, int32_t* __restrict__ e_nparts, int32_t* __restrict__ split_list,
     int32_t* __restrict__ num_split) {
@@ -116,7 +177,7 @@ __global__ __launch_bounds__(WC_THREADS) void wgrad_chunks_kernel(
   const int e = has_x ? (threadIdx.x == 0 ? E : (int)threadIdx.x - 1) : (int)threadIdx.x;
   const bool routed = e < E && !(has_x && threadIdx.x == 0), extra = has_x && threadIdx.x == 0;
   const int g = routed ? max(gs[e], 0) : (extra ? x_rows : 0);
-  const int r0 = routed ? block_off[e] * BM : x_row0;
+  const int r0 = routed ? block_off[e] * row0_mult : x_row0;
   int n = (routed || extra) ? max(1, (g + R - 1) / R) : 0;
   const int pbase = block_excl_scan(n > 1 ? n : 0, sh);
   const bool fits = sh[TOT] <= max_parts;
@@ -341,7 +402,7 @@ size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E) {
 }
 
 int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
-                       WgradChunks* ch, hipStream_t s, int64_t x_rows, int64_t x_row0) {
+                       WgradChunks* ch, hipStream_t s, int64_t x_rows, int64_t x_row0, int row0_mult) {
   LSURGE_REQUIRE(E >= 1 && E <= 256, "wgrad chunks: E=%d must be in [1, 256]", E);
   LSURGE_REQUIRE(x_rows < (1ll << 31) && x_row0 >= 0 && x_row0 < (1ll << 31), "wgrad chunks: extra expert rows");
   int32_t* t = table;
@@ -357,7 +418,7 @@ int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const
   ch->max_chunks = p.max_chunks;
   ch->max_parts = p.max_parts;
   LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(wgrad_chunks_kernel, dim3(1), dim3(WC_THREADS), 0, s, gs, block_off, E, p.R,
+                hipLaunchKernelGGL(wgrad_chunks_kernel, dim3(1), dim3(WC_THREADS), 0, s, gs, block_off, row0_mult, E, p.R,
                                    p.max_chunks, p.max_parts, (int)x_rows, (int)x_row0, (int32_t*)ch->c_expert, (int32_t*)ch->c_row0, (int32_t*)ch->c_rows,
                                    (int32_t*)ch->c_part, (int32_t*)ch->num_chunks, (int32_t*)ch->e_pbase,
                                    (int32_t*)ch->e_nparts, (int32_t*)ch->split_list, (int32_t*)ch->num_split));
@@ -414,15 +475,30 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
 // workspace: blk_row0, blk_rows, blk_expert [max_blocks] | num_blocks, total_rows | e_row0 [e]
 extern "C" {
 
-size_t lsurge_ragged_dot_workspace_bytes(int64_t m, int64_t e) {
-  const int64_t mb = lsurge_max_blocks(m, e);
-  return sizeof(int32_t) * (size_t)(3 * mb + 4 + 2 * e);
+// workspace: blk_row0, blk_rows, blk_expert [max_blocks] | num_blocks, total_rows, 2 spare | e_row0, e_rows [e] |
+// e_boff [e + 1]; the backward's chunked weight gradient adds its chunk table and partial slots after that
+static size_t ragged_table_ints(int64_t m, int64_t e) { return (size_t)(3 * lsurge_max_blocks(m, e) + 4 + 3 * e + 1); }
+
+size_t lsurge_ragged_dot_workspace_bytes(int64_t m, int64_t e) { return sizeof(int32_t) * ragged_table_ints(m, e); }
+
+// the chunked weight gradient of the backward takes the table's rows as chunks of at most R (hot groups split)
+static bool ragged_chunked(int64_t e) { return e >= 1 && e <= 256; }
+
+size_t lsurge_ragged_dot_bwd_workspace_bytes(int64_t m, int64_t kdim, int64_t n, int64_t e) {
+  size_t b = lsurge_ragged_dot_workspace_bytes(m, e);
+  if (m > 0 && ragged_chunked(e)) {
+    const lsurge::WgradChunkPlan p = lsurge::wgrad_chunk_plan(m, e);
+    b = (b + 255) / 256 * 256 + sizeof(int32_t) * lsurge::wgrad_chunk_table_ints(p, e);
+    b = (b + 255) / 256 * 256 + lsurge::wgrad_chunked_workspace_bytes(p, kdim, n);
+  }
+  return b;
 }
 
 static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_t ws_bytes, hipStream_t s,
                         lsurge::GemmBlocks* g, int32_t** total_rows, int32_t** e_row0, int32_t** e_rows) {
   const size_t need = lsurge_ragged_dot_workspace_bytes(m, e);
   LSURGE_REQUIRE(ws && ws_bytes >= need, "ragged_dot: workspace %zu < %zu bytes", ws_bytes, need);
+  LSURGE_REQUIRE(e < (1 << 30), "ragged_dot: e too large");
   const int64_t mb = lsurge_max_blocks(m, e);
   int32_t* p = (int32_t*)ws;
   int32_t* blk_row0 = p;
@@ -432,9 +508,14 @@ static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_
   *total_rows = nb + 1;
   *e_row0 = nb + 4;
   *e_rows = nb + 4 + e;
+  int32_t* e_boff = nb + 4 + 2 * e;
   LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(ragged_blocks_kernel, dim3(1), dim3(64), 0, s, gs, (int)e, m, (int)mb, blk_row0,
-                                   blk_rows, blk_expert, nb, *total_rows, *e_row0, *e_rows));
+                hipLaunchKernelGGL(ragged_groups_kernel, dim3(1), dim3(1024), 0, s, gs, (int)e, m, (int)mb, *e_row0,
+                                   *e_rows, e_boff, nb, *total_rows));
+  const unsigned grid = (unsigned)std::min<int64_t>((mb + 255) / 256, 1024);
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(ragged_blocks_kernel, dim3(grid), dim3(256), 0, s, *e_row0, *e_rows, e_boff, (int)e,
+                                   (int)mb, blk_row0, blk_rows, blk_expert));
   g->blk_expert = blk_expert;
   g->blk_rows = blk_rows;
   g->blk_row0 = blk_row0;
@@ -479,7 +560,20 @@ int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group
     LSURGE_LAUNCH(KID_MISC, s,
                   hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, dlhs, m, kdim, 2, total));
   }
-  // drhs[e] = lhs_e^T @ g_e
+  // drhs[e] = lhs_e^T @ g_e.  With room for the chunk table and partials (lsurge_ragged_dot_bwd_workspace_bytes), a
+  // hot group's rows are cut into chunks that spread over the GPU; with only the forward's workspace, one slice
+  // per group.
+  if (m > 0 && ragged_chunked(e) && workspace_bytes >= lsurge_ragged_dot_bwd_workspace_bytes(m, kdim, n, e)) {
+    const lsurge::WgradChunkPlan p = lsurge::wgrad_chunk_plan(m, e);
+    char* base = (char*)workspace;
+    size_t off = (lsurge_ragged_dot_workspace_bytes(m, e) + 255) / 256 * 256;
+    int32_t* table = (int32_t*)(base + off);
+    off = (off + sizeof(int32_t) * lsurge::wgrad_chunk_table_ints(p, e) + 255) / 256 * 256;
+    lsurge::WgradChunks ch;
+    if (int rc = lsurge::build_wgrad_chunks(e_rows, e_row0, (int)e, p, table, &ch, s, -1, 0, 1)) return rc;
+    return lsurge::gemm_wgrad_chunked(KID_MISC, ch, (int)e, m, lhs, kdim, g, n, kdim, n, drhs, nullptr, 0, n, kdim * n,
+                                      base + off, lsurge::wgrad_chunked_workspace_bytes(p, kdim, n), s);
+  }
   return lsurge::gemm_wgrad(KID_MISC, (int)e, e_row0, 1, e_rows, 0, m, lhs, kdim, g, n, kdim, n, drhs, nullptr, 0, n,
                             kdim * n, 1, nullptr, 0, s, lsurge::RowGather());
 }

@@ -78,10 +78,12 @@ struct WgradChunks {
 WgradChunkPlan wgrad_chunk_plan(int64_t M, int64_t E);
 size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E);
 // builds the table (in `table`, wgrad_chunk_table_ints entries) from device group sizes and block offsets
-// Extra expert of the chunk table (id E, after the routed ones): x_rows rows from padded row x_row0 (x_rows < 0:
-// none); its gradient goes to C / C2 of an ExtraOut.
+// Expert e's rows start at row0_mult block_off[e] (128 for the padded layout, 1 for a ragged one).  Extra expert
+// of the chunk table (id E, after the routed ones): x_rows rows from row x_row0 (x_rows < 0: none); its gradient
+// goes to C / C2 of an ExtraOut.
 int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
-                       WgradChunks* ch, hipStream_t s, int64_t x_rows = -1, int64_t x_row0 = 0);
+                       WgradChunks* ch, hipStream_t s, int64_t x_rows = -1, int64_t x_row0 = 0,
+                       int row0_mult = LSURGE_BLOCK_ROWS);
 struct ExtraOut {
   int expert = -1;
   float* C = nullptr;

@@ -94,7 +94,7 @@ class _RaggedDot(torch.autograd.Function):
         g = L.contig(g.to(torch.bfloat16))
         dlhs = torch.empty_like(lhs)
         drhs = torch.empty((e, k, n), dtype=torch.float32, device=lhs.device)
-        ws = L.workspace(L.lib().lsurge_ragged_dot_workspace_bytes(m, e), lhs.device)
+        ws = L.workspace(L.lib().lsurge_ragged_dot_bwd_workspace_bytes(m, k, n, e), lhs.device)
         L.check(L.lib().lsurge_ragged_dot_bwd(L.ptr(lhs), L.ptr(rhs), L.ptr(gs), L.ptr(g), m, k, n, e, L.ptr(dlhs),
                                               L.ptr(drhs), L.ptr(ws), ws.numel(), L.stream(lhs.device)),
                 "ragged_dot_bwd")

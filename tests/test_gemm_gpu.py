@@ -87,3 +87,42 @@ def test_perm_gather_sentinel(dev):
     g = torch.randn(8, 16, device=dev).to(torch.bfloat16)
     y.backward(g)
     assert torch.equal(x.grad, g[inv.long()])
+
+
+def test_hot_group_chunked_weight_gradient(dev):
+    """A group far above the mean (8000 of 9000 rows): drhs cuts it into row chunks summed from partials."""
+    gs = [0, 8000, 0, 995]
+    run_case(gs, 9000, 128, 64, dev, seed=11)
+
+
+def test_many_groups_block_table(dev):
+    """1500 groups: the block-table scan takes two passes of 1024 groups; drhs takes one slice per group (E > 256)."""
+    rng = np.random.default_rng(7)
+    gs = rng.integers(0, 5, 1500).tolist()
+    run_case(gs, int(np.sum(gs)) + 7, 64, 64, dev, seed=12)
+
+
+def test_ragged_bwd_forward_sized_workspace(dev):
+    """lsurge_ragged_dot_bwd also accepts the forward's workspace size (one slice per group, no chunk partials)."""
+    import _lib as L
+    gs = [0, 8000, 0, 995]
+    M, K, N, E = 9000, 128, 64, 4
+    rng = np.random.default_rng(13)
+    a = mo.round_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    b = mo.round_bf16(rng.standard_normal((E, K, N)).astype(np.float32))
+    g = mo.round_bf16(rng.standard_normal((M, N)).astype(np.float32))
+    at, bt, gt = _bf(a, dev), _bf(b, dev), _bf(g, dev)
+    gst = torch.tensor(gs, dtype=torch.int32, device=dev)
+    lib = L.lib()
+    outs = []
+    for nbytes in (lib.lsurge_ragged_dot_workspace_bytes(M, E), lib.lsurge_ragged_dot_bwd_workspace_bytes(M, K, N, E)):
+        ws = L.workspace(nbytes, dev)
+        dl = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+        dr = torch.empty((E, K, N), dtype=torch.float32, device=dev)
+        L.check(lib.lsurge_ragged_dot_bwd(L.ptr(at), L.ptr(bt), L.ptr(gst), L.ptr(gt), M, K, N, E, L.ptr(dl), L.ptr(dr),
+                                          L.ptr(ws), ws.numel(), L.stream(dev)), "ragged_dot_bwd")
+        outs.append((dl.float().cpu().numpy(), dr.cpu().numpy()))
+    want_l, want_r = mo.ragged_dot_bwd(a, b, gs, g)
+    for dl, dr in outs:
+        assert mo.rel_l2(dl, want_l) < TOL and mo.rel_l2(dr, want_r) < TOL
+    assert np.array_equal(outs[0][0], outs[1][0])  # dlhs does not depend on the workspace
