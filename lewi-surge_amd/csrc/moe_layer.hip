@@ -322,10 +322,10 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
 }
 
 // Backward.  Stream plan (caller's stream = critical path):
-//   main:  chunk table -> combine bwd -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd ->
-//          gate/up wgrad
-//   s0:    a shared expert of its own width (fs != f): down dgrad, down wgrad, gate/up dgrad, gate/up wgrad
-//   s1:    W_r transpose; after combine bwd: down wgrad, d(logits) scatter, router wgrad
+//   main:  combine bwd -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
+//   s0:    after combine bwd: d(logits) scatter, router wgrad (merged shared expert); with fs != f instead the
+//          shared expert's own backward: down dgrad, down wgrad, gate/up dgrad, gate/up wgrad
+//   s1:    W_r transpose; after combine bwd: chunk table, down wgrad (then the router backward when fs != f)
 // The helper chains overlap the dgrads of the main chain; the gate/up weight gradient runs after the join on its
 // own, and the dispatch backward reads dX_pad right after the GEMM that wrote it, while it is still in cache.
 int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* dy, const void* saved,
@@ -387,27 +387,33 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   // s1: W_r^T for the router's dx term (independent of everything else)
   if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, s1)) return rc;
 
-  // main: chunk table of the routed weight gradients (read by both wgrads, after the s1 fork below)
-  lsurge::WgradChunks chunks;
-  if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, st,
-                                         q.merged ? q.T : -1, q.P))
-    return rc;
   // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel); a merged
   // shared expert's rows of dY_pad get dY itself
   if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, q.P, sv.slot, sv.weights, q.T, (int)q.k, q.d, dy, w.dy_pad,
                                               dweights, w.dl, st, q.merged ? w.dy_pad + q.P * q.d : nullptr))
     return rc;
   if (int rc = lsurge::stream_after(s1, st, ev[2])) return rc;
-  // s1: down wgrad dW_down[e] = h_e^T dY_e; router: dW_r = x^T dlogits (bf16 MFMA over the dense [T, E] dlogits)
+  // s1: the chunk table of the weight gradients (read by both), then down wgrad dW_down[e] = h_e^T dY_e
+  lsurge::WgradChunks chunks;
+  if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, s1,
+                                         q.merged ? q.T : -1, q.P))
+    return rc;
   if (int rc = lsurge::gemm_wgrad_chunked(KID_GEMM_DOWN_WGRAD, chunks, (int)q.E, q.T, sv.h, q.f, w.dy_pad, q.d, q.f,
                                           q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, w.part_dn, w.part_dn_bytes, s1,
                                           lsurge::RowGather(), odn))
     return rc;
-  if (int rc = lsurge::launch_scatter_dlogits(w.dl, sv.sel, q.T, (int)q.E, (int)q.k, w.dlog, s1)) return rc;
+  // router backward dW_r = x^T dlogits (bf16 MFMA over the dense [T, E] dlogits): on s0 beside the down wgrad when
+  // s0 is free (merged shared expert), else after the down wgrad on s1
+  hipStream_t sr = s1;
+  if (q.merged) {
+    sr = s0;
+    if (int rc = lsurge::stream_after(s0, st, ev[3])) return rc;
+  }
+  if (int rc = lsurge::launch_scatter_dlogits(w.dl, sv.sel, q.T, (int)q.E, (int)q.k, w.dlog, sr)) return rc;
   {
     const int S = dense_splits(q.T, q.d, q.E);
     if (int rc = lsurge::gemm_wgrad(KID_ROUTER_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.dlog, q.E, q.d,
-                                    q.E, g->dw_r, nullptr, 0, q.E, 0, S, w.part_r, w.part_r_bytes, s1))
+                                    q.E, g->dw_r, nullptr, 0, q.E, 0, S, w.part_r, w.part_r_bytes, sr))
       return rc;
   }
   // main: down dgrad + SwiGLU backward: dH = dY W_down^T -> [dG | dU]
