@@ -5,6 +5,10 @@
 
 namespace lsurge {
 
+// ---- router (router.hip): lsurge_router_topk with an optional event recorded right after the logits kernel
+int router_topk_impl(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d, int64_t e, int64_t k,
+                     float* logits, int32_t* sel, float* weights, hipStream_t s, hipEvent_t after_logits);
+
 // ---- routing layout (layout.hip)
 int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
                       int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,

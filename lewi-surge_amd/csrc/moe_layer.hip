@@ -255,8 +255,9 @@ struct ForkGuard {
 extern "C" {
 
 // Forward.  Stream plan:
-//   main: router -> layout (-> tile table of the backward) -> gate/up GEMM -> down GEMM -> [join] -> combine
-//   s0:   shared expert (depends on x only)
+//   main: router logits -> selection -> layout (-> tile table of the backward) -> gate/up GEMM -> down GEMM ->
+//         [join] -> combine
+//   s0:   after the logits: shared expert (depends on x only)
 // The dispatch into padded expert blocks is fused into the gate/up GEMM: its A tiles are gathered straight from
 // the token rows x through row_src (padded row -> flat slot t*k + j), so the padded copy of x is never
 // materialised (the backward's gate/up weight gradient gathers the same way).
@@ -275,9 +276,15 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   if (int rc = fg.acquire(st)) return rc;
   hipStream_t s0 = fg.f.side[0];
 
-  // s0: the shared expert's forward, dense GEMMs over all T tokens (it depends on x only, so it overlaps the
-  // router and the layout).  A merged shared expert writes its g, u, h and output rows where the backward's tile
-  // table expects expert E (padded rows 128 MB + t).
+  // main: router logits -> (s0 forks here) -> top-k selection
+  // (serial mode: the helpers are the caller's stream and have no events)
+  if (int rc = lsurge::router_topk_impl(p->x, p->w_r, p->bias, q.T, q.d, q.E, q.k, sv.logits, sv.sel, sv.weights, st,
+                                        s0 != st ? fg.f.ev[0] : nullptr))
+    return rc;
+  // s0: the shared expert's forward, dense GEMMs over all T tokens.  It depends on x only; it starts after the
+  // router's logits kernel (VALU-bound, it would share the CUs badly) and overlaps the selection and the layout,
+  // whose small grids leave most of the GPU idle.  A merged shared expert writes its g, u, h and output rows where
+  // the backward's tile table expects expert E (padded rows 128 MB + t).
   bf16_t *sg = sv.sg, *su = sv.su, *sh = sv.sh, *sy = sv.sy;
   if (q.merged) {
     sg = sv.g + q.P * q.f;
@@ -285,7 +292,8 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
     sh = sv.h + q.P * q.f;
     sy = sv.y_pad + q.P * q.d;
   }
-  if (int rc = lsurge::stream_after(s0, st, fg.f.ev[0])) return rc;
+  if (s0 != st && hipStreamWaitEvent(s0, fg.f.ev[0], 0) != hipSuccess)
+    return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipStreamWaitEvent failed");
   if (q.fs) {
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
     if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
@@ -294,8 +302,6 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
     if (int rc = lsurge::gemm_rows_kn(KID_SHARED_DOWN_FWD, dense, sh, q.fs, p->ws_down, q.d, 0, q.fs, q.d, sy, q.d, s0))
       return rc;
   }
-  if (int rc = lsurge_router_topk(p->x, p->w_r, p->bias, q.T, q.d, q.E, q.k, sv.logits, sv.sel, sv.weights, stream))
-    return rc;
   if (int rc = lsurge::build_layout_impl(sv.sel, q.M, q.E, sv.gs, sv.offsets, sv.block_off, sv.order, sv.pos, sv.slot,
                                          sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks, workspace,
                                          workspace_bytes, st))

@@ -349,9 +349,22 @@ __global__ __launch_bounds__(256) void router_select_lane_kernel(const float* __
 
 }  // namespace
 
+namespace lsurge {
+// after_logits (optional): a hipEvent recorded on the stream right after the logits kernel of the split path, so a
+// caller can start independent work beside the selection
+int router_topk_impl(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d, int64_t e, int64_t k,
+                     float* logits, int32_t* sel, float* weights, hipStream_t s, hipEvent_t after_logits);
+}  // namespace lsurge
+
 extern "C" int lsurge_router_topk(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d,
                                   int64_t e, int64_t k, float* logits, int32_t* sel, float* weights,
                                   lsurge_stream_t stream) {
+  return lsurge::router_topk_impl(x, w_r, bias, t, d, e, k, logits, sel, weights, (hipStream_t)stream, nullptr);
+}
+
+int lsurge::router_topk_impl(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d, int64_t e,
+                             int64_t k, float* logits, int32_t* sel, float* weights, hipStream_t stream,
+                             hipEvent_t after_logits) {
   LSURGE_REQUIRE(x && w_r && sel && weights, "router_topk: null pointer");
   LSURGE_REQUIRE(t >= 0 && d > 0 && e >= 1 && e <= RT_EMAX && k >= 1 && k <= e, "router_topk: bad shape t=%lld d=%lld e=%lld k=%lld",
                  (long long)t, (long long)d, (long long)e, (long long)k);
@@ -363,6 +376,8 @@ extern "C" int lsurge_router_topk(const void* x, const void* w_r, const float* b
     LSURGE_LAUNCH(KID_ROUTER, s,
                   hipLaunchKernelGGL(router_logits_kernel, lg, dim3(RL_THREADS), 0, s, (const bf16_t*)x,
                                      (const bf16_t*)w_r, bias, (int)t, (int)d, (int)e, logits));
+    if (after_logits && hipEventRecord(after_logits, s) != hipSuccess)
+      return lsurge::set_error(LSURGE_ERR_LAUNCH, "router_topk: hipEventRecord failed");
     if (k <= 16 && t >= 8192) {  // lane per token (enough tokens to fill the GPU); else one wave per token
       const dim3 lg2((unsigned)((t + 255) / 256));
       if (k <= 8)
@@ -386,6 +401,8 @@ extern "C" int lsurge_router_topk(const void* x, const void* w_r, const float* b
 #undef RS_CASE
     return LSURGE_OK;
   }
+  if (after_logits && hipEventRecord(after_logits, s) != hipSuccess)  // fused path: no separate logits kernel
+    return lsurge::set_error(LSURGE_ERR_LAUNCH, "router_topk: hipEventRecord failed");
   dim3 grid((unsigned)((t + RT_TOK - 1) / RT_TOK)), block(RT_THREADS);
   const bf16_t* xb = (const bf16_t*)x;
   const bf16_t* wb = (const bf16_t*)w_r;
