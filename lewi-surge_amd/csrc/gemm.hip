@@ -12,6 +12,10 @@ using namespace lsgemm;
 // epilogue overlap the other's MFMAs.
 using Cfg = GemmCfg<128, 256, 32, 2, 2, 3, 2>;
 constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, GT = Cfg::GT;
+// Row GEMMs over 256-row tiles (GemmBlocks::tile_rows = 256; the layer's dgrads and its dense shared-expert
+// forward): 256 x 256 tiles, 8 waves of 128 x 64 in two ping-pong groups, a 3-stage ring of 32-deep stages
+// (96 KiB), one workgroup per CU.  Same MFMA sequence per output element, so the results are bitwise those of Cfg.
+using CfgPP = GemmCfg<256, 256, 32, 2, 4, 3, 1, 1>;
 
 // sum of the S split partials in split order -> C (and C2 for n >= n_split)
 __global__ void splitk_reduce_kernel(const float* __restrict__ part, int S, int E, int64_t I, int64_t N,
@@ -259,7 +263,23 @@ static int check_desc(int64_t bytes, const char* what) {
 }
 
 static int max_blocks_of(const GemmBlocks& g) {
-  return g.blk_expert ? g.max_blocks : (int)((g.dense_rows + BM - 1) / BM);
+  return g.blk_expert ? g.max_blocks : (int)((g.dense_rows + g.tile_rows - 1) / g.tile_rows);
+}
+
+// launch gemm_rows_kernel with the tile config that matches the row tiles of g (column tiles: BN output columns, or
+// BN / 2 for the SwiGLU forward)
+template <int BMODE, int EPI>
+static int launch_rows(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t s) {
+  LSURGE_REQUIRE(g.tile_rows == 128 || g.tile_rows == 256, "grouped GEMM: tile_rows=%d must be 128 or 256", g.tile_rows);
+  a.max_tiles = max_blocks_of(g);
+  a.n_tiles = (int)((a.N + (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN) - 1) / (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN));
+  if (a.max_tiles == 0) return LSURGE_OK;
+  const dim3 grid(pad8((int64_t)a.n_tiles * a.max_tiles));
+  if (g.tile_rows == 256)
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<CfgPP, BMODE, EPI>), grid, dim3(CfgPP::GT), 0, s, a));
+  else
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, BMODE, EPI>), grid, dim3(Cfg::GT), 0, s, a));
+  return LSURGE_OK;
 }
 
 // C[rows, N] = A[rows, K] @ B_e where B_e is [K, N] (n-major) -- forward projections
@@ -267,21 +287,17 @@ int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
                  int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32,
                  const ExtraExpert& xe) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_kn")) return rc;
-  if (int rc = check_desc(std::max<int64_t>(BM * lda, K * ldb) * 2, "gemm_rows_kn")) return rc;
+  if (int rc = check_desc(std::max<int64_t>(g.tile_rows * lda, K * ldb) * 2, "gemm_rows_kn")) return rc;
   RowsArgs a{};
   a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.b_estride = b_estride;
   a.K = K; a.N = N; a.ldc = ldc;
   if (out_f32) a.Cf = (float*)C;
   else a.C = (bf16_t*)C;
   a.t_expert = g.blk_expert; a.t_rows = g.blk_rows; a.t_row0 = g.blk_row0; a.num_tiles = g.num_blocks;
-  a.dense_rows = g.dense_rows; a.max_tiles = max_blocks_of(g);
+  a.dense_rows = g.dense_rows;
   a.x_expert = xe.expert; a.Bx = (const bf16_t*)xe.B; a.B2x = (const bf16_t*)xe.B2;
   LSURGE_REQUIRE(xe.expert < 0 || (xe.B && (xe.B2 || !a.B2)), "grouped GEMM: extra expert weights missing");
-  a.n_tiles = (int)((N + BN - 1) / BN);
-  if (a.max_tiles == 0) return LSURGE_OK;
-  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, B_KN, EPI_STORE>),
-                                           dim3(pad8((int64_t)a.n_tiles * a.max_tiles)), dim3(GT), 0, s, a));
-  return LSURGE_OK;
+  return launch_rows<B_KN, EPI_STORE>(kid, g, a, s);
 }
 
 // h = silu(A @ Bg) * (A @ Bu); also stores g, u.  Bg, Bu: [K, N] per expert.  With a gather (gather.rows set),
@@ -290,7 +306,7 @@ int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t ld
                          int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* H, void* Gs, void* Us,
                          int64_t ldh, hipStream_t s, const RowGather& gather, const ExtraExpert& xe) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_swiglu_fwd")) return rc;
-  if (int rc = check_desc(std::max<int64_t>(BM * lda, K * ldb) * 2, "gemm_rows_swiglu_fwd")) return rc;
+  if (int rc = check_desc(std::max<int64_t>(g.tile_rows * lda, K * ldb) * 2, "gemm_rows_swiglu_fwd")) return rc;
   if (gather.rows) {
     LSURGE_REQUIRE(gather.div >= 1 && gather.nrows >= 1, "gemm_rows_swiglu_fwd: bad row gather");
     if (int rc = check_desc(gather.nrows * lda * 2, "gemm_rows_swiglu_fwd gather")) return rc;
@@ -301,14 +317,10 @@ int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t ld
   a.b_estride = b_estride; a.K = K; a.N = N; a.C = (bf16_t*)H; a.ldc = ldh; a.G = (bf16_t*)Gs; a.U = (bf16_t*)Us;
   a.ldg = ldh;
   a.t_expert = g.blk_expert; a.t_rows = g.blk_rows; a.t_row0 = g.blk_row0; a.num_tiles = g.num_blocks;
-  a.dense_rows = g.dense_rows; a.max_tiles = max_blocks_of(g);
+  a.dense_rows = g.dense_rows;
   a.x_expert = xe.expert; a.Bx = (const bf16_t*)xe.B; a.B2x = (const bf16_t*)xe.B2;
   LSURGE_REQUIRE(xe.expert < 0 || (xe.B && (xe.B2 || !a.B2)), "grouped GEMM: extra expert weights missing");
-  a.n_tiles = (int)((N + BN / 2 - 1) / (BN / 2));
-  if (a.max_tiles == 0) return LSURGE_OK;
-  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, B_KN, EPI_SWIGLU_FWD>),
-                                           dim3(pad8((int64_t)a.n_tiles * a.max_tiles)), dim3(GT), 0, s, a));
-  return LSURGE_OK;
+  return launch_rows<B_KN, EPI_SWIGLU_FWD>(kid, g, a, s);
 }
 
 // C[rows, N] = A[rows, K] @ B_e^T where B_e is stored [N, K] (k-major); with B2 and k_split the K range
@@ -319,7 +331,7 @@ int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
                  bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32,
                  const ExtraExpert& xe) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_nk")) return rc;
-  if (int rc = check_desc(std::max<int64_t>(BM * lda, N * ldb) * 2, "gemm_rows_nk")) return rc;
+  if (int rc = check_desc(std::max<int64_t>(g.tile_rows * lda, N * ldb) * 2, "gemm_rows_nk")) return rc;
   LSURGE_REQUIRE(!B2 || (k_split > 0 && k_split % BK == 0), "gemm_rows_nk: k_split must be a multiple of %d", BK);
   RowsArgs a{};
   a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.B2 = (const bf16_t*)B2; a.k_split = B2 ? k_split : 0;
@@ -328,17 +340,10 @@ int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
   else a.C = (bf16_t*)C;
   a.G = (bf16_t*)Gs; a.U = (bf16_t*)Us; a.ldg = ldg;
   a.t_expert = g.blk_expert; a.t_rows = g.blk_rows; a.t_row0 = g.blk_row0; a.num_tiles = g.num_blocks;
-  a.dense_rows = g.dense_rows; a.max_tiles = max_blocks_of(g);
+  a.dense_rows = g.dense_rows;
   a.x_expert = xe.expert; a.Bx = (const bf16_t*)xe.B; a.B2x = (const bf16_t*)xe.B2;
   LSURGE_REQUIRE(xe.expert < 0 || (xe.B && (xe.B2 || !a.B2)), "grouped GEMM: extra expert weights missing");
-  a.n_tiles = (int)((N + BN - 1) / BN);
-  if (a.max_tiles == 0) return LSURGE_OK;
-  const dim3 grid(pad8((int64_t)a.n_tiles * a.max_tiles));
-  if (swiglu_bwd)
-    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, B_NK, EPI_SWIGLU_BWD>), grid, dim3(GT), 0, s, a));
-  else
-    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, B_NK, EPI_STORE>), grid, dim3(GT), 0, s, a));
-  return LSURGE_OK;
+  return swiglu_bwd ? launch_rows<B_NK, EPI_SWIGLU_BWD>(kid, g, a, s) : launch_rows<B_NK, EPI_STORE>(kid, g, a, s);
 }
 
 size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S) {

@@ -34,10 +34,12 @@ enum { EPI_STORE = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
 constexpr int NS = 128;  // columns per N-major LDS sub-tile (256-byte rows)
 
 // Tile shape: BM x BN per workgroup, WM x WN waves (wave tile TM x TN = FM x FN fragments of 32 x 32), K in
-// BK-deep stages, an ST-stage LDS ring, OCC workgroups per CU.
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int ST_, int OCC_>
+// BK-deep stages, an ST-stage LDS ring, OCC workgroups per CU.  PP selects the ping-pong K loop (k_loop_pp): eight
+// waves in two groups of four, one wave of each group per SIMD, taking turns between the matrix pipe and the
+// memory pipes.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int ST_, int OCC_, int PP_ = 0>
 struct GemmCfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, ST = ST_, OCC = OCC_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, ST = ST_, OCC = OCC_, PP = PP_;
   static constexpr int NW = WM * WN, GT = 64 * NW;
   static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
   static constexpr int A_EL = BM * BK, B_EL = BN * BK;                   // bf16 elements per stage
@@ -51,6 +53,7 @@ struct GemmCfg {
   static_assert(CPA * NW * 1024 == A_EL * 2 && CPB * NW * 1024 == B_EL * 2, "copies must split evenly over waves");
   static_assert((ST - 1) * CP < 64 && ST >= 2, "vmcnt field");
   static_assert(SMEM_EL * 2 <= 160 * 1024 / OCC, "LDS");
+  static_assert(!PP || (NW == 8 && WM == 2 && OCC == 1 && ST >= 3), "ping-pong: 8 waves, groups = wave rows");
 };
 
 struct RowsArgs {
@@ -263,6 +266,69 @@ __device__ __forceinline__ void k_loop(int nk, Issue&& issue, Load&& load, Mma&&
   __builtin_amdgcn_s_waitcnt(0);  // the copies of the zero stages past the end land before the epilogue
 }
 
+// vmcnt(N) alone (expcnt and lgkmcnt at their maxima: no wait on them)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0) alone
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Ping-pong K loop.  The eight waves form two groups of four (group = wave / 4; waves w and w + 4 share SIMD w % 4)
+// that alternate between a memory phase -- read all fragments of stage i from LDS, enqueue the copies of stage
+// i + ST - 1 -- and a compute phase -- the MFMAs of stage i from registers -- with a workgroup barrier between
+// phases.  Group 1 runs one phase behind group 0, so on every SIMD one wave feeds the matrix pipe while the other
+// issues its LDS reads and copies.  Barrier b starts phase b; group 0 does memory(i) in phase 2i and compute(i) in
+// 2i + 1, group 1 memory(i) in 2i + 1 and compute(i) in 2i + 2.
+//  - Data ready: every wave waits until at most ST - 2 younger stages of its own copies are in flight before the
+//    barrier that starts phase 2i + 2 (group 0 after compute(i), group 1 after memory(i)), so stage i + 1 has
+//    landed everywhere before group 0 reads it in phase 2i + 2 (and group 1 in 2i + 3).
+//  - Slot reuse: stage i + ST - 1 overwrites the slot of stage i - 1, whose last reader is group 1's memory phase
+//    2i - 1; group 1 drains its LDS reads before the barrier that ends it, and group 0 enqueues the copies in
+//    phase 2i, group 1 in 2i + 1.
+// Both groups pass 2 nk + 2 barriers (group 1 one extra at the start, group 0 one at the end).  Stages past the
+// end copy zeros (out-of-range offsets), so the wait counts stay exact.
+template <int ST, int CP, int KS, class Frags, class Issue, class Load, class Mma>
+__device__ __forceinline__ void k_loop_pp(int nk, int grp, Issue&& issue, Load&& load, Mma&& mma) {
+  static_assert(ST >= 3, "ping-pong ring depth");
+#pragma unroll
+  for (int s = 0; s < ST - 1; ++s) issue(s, s);
+  wait_vmcnt<(ST - 2) * CP>();
+  wg_barrier();
+  if (grp == 1) wg_barrier();
+  Frags f[KS];
+  int slot = 0;
+  for (int i = 0; i < nk; ++i) {
+    // memory phase
+#pragma unroll
+    for (int s = 0; s < KS; ++s) load(slot, s, f[s]);
+    const int refill = slot == 0 ? ST - 1 : slot - 1;
+    issue(refill, i + ST - 1);
+    if (grp == 1) {
+      wait_vmcnt<(ST - 2) * CP>();
+      wait_lgkmcnt0();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wg_barrier();
+    // compute phase
+#pragma unroll
+    for (int s = 0; s < KS; ++s) mma(f[s]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (grp == 0) wait_vmcnt<(ST - 2) * CP>();
+    wg_barrier();
+    slot = slot == ST - 1 ? 0 : slot + 1;
+  }
+  if (grp == 0) wg_barrier();
+  __builtin_amdgcn_s_waitcnt(0);  // the copies of the zero stages past the end land before the epilogue
+}
+
+template <class Cfg, class Frags, class Issue, class Load, class Mma>
+__device__ __forceinline__ void run_k_loop(int nk, int wave, Issue&& issue, Load&& load, Mma&& mma) {
+  if constexpr (Cfg::PP) k_loop_pp<Cfg::ST, Cfg::CP, Cfg::BK / 16, Frags>(nk, wave >> 2, issue, load, mma);
+  else k_loop<Cfg::ST, Cfg::CP, Cfg::BK / 16, Frags>(nk, issue, load, mma);
+}
+
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void st_bf16x8(bf16_t* p, const float* v) {
   *reinterpret_cast<u32x4*>(p) =
@@ -454,14 +520,18 @@ void gemm_rows_kernel(RowsArgs a) {
       else f.w[j] = frag_n(bt + (col / NS) * (BK * NS), kk, col % NS, lane);
     }
   };
+  // a wave whose rows or output columns all lie outside the tile skips its MFMAs (a one-block tile of a 256-row
+  // table, the N tail); its accumulators stay zero and are never stored
+  const bool live = wm * TM < rows && n0 + wn * (EPI == EPI_SWIGLU_FWD ? TN / 2 : TN) < N;
   auto mma = [&](const F& f) {
+    if (!live) return;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
   };
 
-  k_loop<ST, Cfg::CP, BK / 16, F>(nk, issue, load, mma);
+  run_k_loop<Cfg, F>(nk, wave, issue, load, mma);
 
   // ---- epilogue, staged through LDS.  Written straight out, one store instruction would cover 16 bytes of 32
   // different rows.  Instead each wave parks one 32-row slice of its accumulators in the (now idle) ring as f32
@@ -717,13 +787,15 @@ void gemm_wgrad_kernel(WgradArgs a) {
       f.w[j] = frag_n(bt + (col / NS) * (BK * NS), kk, col % NS, lane);
     }
   };
+  const bool live = i0 + wm * TM < I && n0 + wn * TN < N;  // as in gemm_rows_kernel
   auto mma = [&](const F& f) {
+    if (!live) return;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
   };
-  if (nk > 0) k_loop<ST, Cfg::CP, BK / 16, F>(nk, issue, load, mma);
+  if (nk > 0) run_k_loop<Cfg, F>(nk, wave, issue, load, mma);
 
   // epilogue (f32), staged through LDS as in gemm_rows_kernel: acc[i][j][4q + t] is C row
   // i0 + wm*TM + 32 i + lane%32, column n0 + wn*TN + 32 j + 8 q + 4 (lane/32) + t.  Read back with TN/8 lanes

@@ -32,10 +32,12 @@ int launch_scatter_dlogits(const float* dl, const int32_t* sel, int64_t T, int E
 struct GemmBlocks {
   const int32_t* blk_expert;
   const int32_t* blk_rows;
-  const int32_t* blk_row0;   // first row of block b (nullptr: 128 b)
+  const int32_t* blk_row0;   // first row of block b (nullptr: tile_rows b)
   const int32_t* num_blocks;
   int max_blocks;
   int64_t dense_rows;        // used when blk_expert == nullptr
+  int tile_rows = 128;       // rows per tile: 128 (4-wave kernel) or 256 (8-wave ping-pong kernel; a table of
+                             // 256-row tiles, or dense rows)
 };
 // Optional row gather of the A operand: row r of the rows operand (a tile row of gemm_rows, a reduction row of an
 // expert in gemm_wgrad) reads A[rows[r] / div], indexed by padded row (negative index: zero row).

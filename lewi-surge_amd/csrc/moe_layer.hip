@@ -42,7 +42,8 @@ struct Dims {
   int64_t T, d, E, k, f, fs, M, MB, P;
   bool merged;      // shared expert carried as expert E of the grouped GEMMs (fs == f)
   int64_t SB;       // its blocks (ceil(T / 128)), after the routed block bound MB
-  int64_t MT, PT;   // tile bound and padded rows including them
+  int64_t PT;       // padded rows including them
+  int64_t TB, TS;   // 256-row tiles: bound on the routed ones, the shared expert's (merged only)
 };
 
 Dims dims_of(const lsurge_moe_shape* s) {
@@ -53,8 +54,10 @@ Dims dims_of(const lsurge_moe_shape* s) {
   q.P = q.MB * BLK;
   q.merged = q.fs > 0 && q.fs == q.f;
   q.SB = q.merged ? (q.T + BLK - 1) / BLK : 0;
-  q.MT = q.MB + q.SB;
-  q.PT = q.MT * BLK;
+  q.PT = (q.MB + q.SB) * BLK;
+  // expert e has ceil(gs[e] / 256) tiles, and sum_e ceil(gs[e] / 256) <= ceil(M / 256) + E
+  q.TB = (q.M + 2 * BLK - 1) / (2 * BLK) + q.E;
+  q.TS = q.merged ? (q.T + 2 * BLK - 1) / (2 * BLK) : 0;
   return q;
 }
 
@@ -63,7 +66,9 @@ struct Saved {
   int32_t *sel;
   float* weights;
   int32_t *gs, *offsets, *block_off, *order, *pos, *slot, *row_src, *blk_expert, *blk_rows, *num_blocks;
-  int32_t *t_expert, *t_rows, *t_row0, *num_tiles;  // tile table of routed + shared blocks (merged shared expert)
+  // 256-row tile table of the grouped GEMMs: routed tiles (two consecutive blocks of one expert), then those of a
+  // merged shared expert; num_tiles[0] counts the routed ones, num_tiles[1] all
+  int32_t *t_expert, *t_rows, *t_row0, *num_tiles;
   bf16_t *g, *u, *h, *y_pad;
   bf16_t *sg, *su, *sh, *sy;  // shared expert run on its own: gate, up, h, output
 };
@@ -83,9 +88,9 @@ size_t carve_saved(const Dims& q, void* base, Saved* sv) {
   sv->blk_expert = c.take<int32_t>(q.MB);
   sv->blk_rows = c.take<int32_t>(q.MB);
   sv->num_blocks = c.take<int32_t>(4);
-  sv->t_expert = c.take<int32_t>(q.merged ? q.MT : 0);
-  sv->t_rows = c.take<int32_t>(q.merged ? q.MT : 0);
-  sv->t_row0 = c.take<int32_t>(q.merged ? q.MT : 0);
+  sv->t_expert = c.take<int32_t>(q.TB + q.TS);
+  sv->t_rows = c.take<int32_t>(q.TB + q.TS);
+  sv->t_row0 = c.take<int32_t>(q.TB + q.TS);
   sv->num_tiles = c.take<int32_t>(4);
   sv->g = c.take<bf16_t>(q.PT * q.f);
   sv->u = c.take<bf16_t>(q.PT * q.f);
@@ -154,36 +159,52 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   return c.off + 256;
 }
 
-// Tile table of the grouped GEMMs with the shared expert carried as expert E: routed blocks [0, nb) as the layout
-// wrote them, then the SB shared blocks (rows 128 MB + 128 j ..), then empty entries up to the bound MB + SB.
-// Also fills row_src of the shared rows (token t -> flat slot t k, so the row gather reads x[t]).
-__global__ void shared_tiles_kernel(const int32_t* __restrict__ blk_expert, const int32_t* __restrict__ blk_rows,
-                                    const int32_t* __restrict__ num_blocks, int MB, int E, int64_t T, int k,
-                                    int32_t* __restrict__ t_expert, int32_t* __restrict__ t_rows,
-                                    int32_t* __restrict__ t_row0, int32_t* __restrict__ num_tiles,
-                                    int32_t* __restrict__ row_src) {
-  const int nb = min(num_blocks[0], MB);
-  const int SB = (int)((T + BLK - 1) / BLK);
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (int64_t i = i0; i < MB + SB; i += stride) {
-    if (i < nb) {
-      t_expert[i] = blk_expert[i];
-      t_rows[i] = blk_rows[i];
-      t_row0[i] = (int32_t)(i * BLK);
-    } else if (i < nb + SB) {
-      const int64_t j = i - nb;
-      t_expert[i] = E;
-      t_rows[i] = (int32_t)min((int64_t)BLK, T - j * BLK);
-      t_row0[i] = (int32_t)((MB + j) * BLK);
-    } else {
-      t_expert[i] = -1;
-      t_rows[i] = 0;
-      t_row0[i] = 0;
-    }
+// 256-row tile table of the grouped GEMMs (one workgroup; E <= 256).  Expert e owns padded rows
+// [128 block_off[e], 128 block_off[e] + gs[e]) and gets ceil(gs[e] / 256) tiles, each two consecutive 128-row blocks
+// of its own (the last one may hold a single block; its second half belongs to no tile and is never touched).  A
+// merged shared expert (SB2 > 0) follows as expert E with tiles over its rows P + 256 j, and row_src of those rows
+// gets token t -> flat slot t k, so the row gathers read x[t].  Entries past the tiles are empty.
+__global__ __launch_bounds__(256) void pair_tiles_kernel(const int32_t* __restrict__ gs,
+                                                         const int32_t* __restrict__ block_off, int E, int TB, int SB2,
+                                                         int64_t P, int64_t T, int k, int32_t* __restrict__ t_expert,
+                                                         int32_t* __restrict__ t_rows, int32_t* __restrict__ t_row0,
+                                                         int32_t* __restrict__ num_tiles, int32_t* __restrict__ row_src) {
+  __shared__ int wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = tid < E ? max(gs[tid], 0) : 0;
+  const int n = (g + 2 * BLK - 1) / (2 * BLK);
+  int x = n;  // inclusive scan of the tile counts
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
   }
-  for (int64_t r = i0; r < T; r += stride) row_src[(int64_t)MB * BLK + r] = (int32_t)(r * k);
-  if (i0 == 0) num_tiles[0] = nb + SB;
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  int base = x - n, total = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (i < w) base += wsum[i];
+    total += wsum[i];
+  }
+  total = min(total, TB);  // never for layout-made sizes (they sum to M)
+  for (int j = 0; j < n && base + j < TB; ++j) {
+    t_expert[base + j] = tid;
+    t_row0[base + j] = BLK * block_off[tid] + 2 * BLK * j;
+    t_rows[base + j] = min(2 * BLK, g - 2 * BLK * j);
+  }
+  for (int i = total + tid; i < TB + SB2; i += blockDim.x) {
+    const int j = i - total;
+    const bool sh = j < SB2;
+    t_expert[i] = sh ? E : -1;
+    t_row0[i] = sh ? (int32_t)(P + 2 * BLK * j) : 0;
+    t_rows[i] = sh ? (int32_t)min((int64_t)2 * BLK, T - 2 * BLK * j) : 0;
+  }
+  if (SB2 > 0)
+    for (int64_t r = tid; r < T; r += blockDim.x) row_src[P + r] = (int32_t)(r * k);
+  if (tid == 0) {
+    num_tiles[0] = total;
+    num_tiles[1] = total + SB2;
+  }
 }
 
 int check_shape(const lsurge_moe_shape* s) {
@@ -295,7 +316,7 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   if (s0 != st && hipStreamWaitEvent(s0, fg.f.ev[0], 0) != hipSuccess)
     return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipStreamWaitEvent failed");
   if (q.fs) {
-    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
+    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
     if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
                                               q.fs, sh, sg, su, q.fs, s0))
       return rc;
@@ -306,12 +327,13 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
                                          sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks, workspace,
                                          workspace_bytes, st))
     return rc;
+  // the backward's 256-row tile table: routed tiles, then the merged shared expert's (and its row_src)
+  LSURGE_LAUNCH(KID_MISC, st,
+                hipLaunchKernelGGL(pair_tiles_kernel, dim3(1), dim3(256), 0, st, sv.gs, sv.block_off, (int)q.E,
+                                   (int)q.TB, (int)q.TS, q.P, q.T, (int)q.k, sv.t_expert, sv.t_rows, sv.t_row0,
+                                   sv.num_tiles, sv.row_src));
+  // the routed forward GEMMs run 128-row blocks on the 4-wave kernel (the ping-pong kernel measured no faster here)
   const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
-  if (q.merged)  // the backward's tile table: routed blocks, then the shared expert's (and its row_src)
-    LSURGE_LAUNCH(KID_MISC, st,
-                  hipLaunchKernelGGL(shared_tiles_kernel, dim3(256), dim3(256), 0, st, sv.blk_expert, sv.blk_rows,
-                                     sv.num_blocks, (int)q.MB, (int)q.E, q.T, (int)q.k, sv.t_expert, sv.t_rows,
-                                     sv.t_row0, sv.num_tiles, sv.row_src));
   lsurge::RowGather gather;
   gather.rows = sv.row_src;
   gather.div = (int)q.k;
@@ -350,11 +372,12 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   carve_bwd(q, workspace, &w);
   hipStream_t st = (hipStream_t)stream;
   float* dweights = g->dweights ? g->dweights : w.dweights;
-  lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+  // the dgrads run 256-row tiles on the ping-pong kernel (routed tiles, then a merged shared expert's)
+  lsurge::GemmBlocks blocks{sv.t_expert, sv.t_rows, sv.t_row0, sv.num_tiles, (int)q.TB, 0, 256};
   lsurge::ExtraExpert xgu, xdn;  // the shared expert carried as expert E: its weights and gradients
   lsurge::ExtraOut ogu, odn;
   if (q.merged) {
-    blocks = lsurge::GemmBlocks{sv.t_expert, sv.t_rows, sv.t_row0, sv.num_tiles, (int)q.MT, 0};
+    blocks = lsurge::GemmBlocks{sv.t_expert, sv.t_rows, sv.t_row0, sv.num_tiles + 1, (int)(q.TB + q.TS), 0, 256};
     xgu.expert = xdn.expert = ogu.expert = odn.expert = (int)q.E;
     xgu.B = p->ws_gate;
     xgu.B2 = p->ws_up;
@@ -374,7 +397,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
 
   // s0: backward of a shared expert of its own width
   if (q.fs && !q.merged) {
-    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T};
+    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
     if (int rc = lsurge::gemm_rows_nk(KID_SHARED_DOWN_DGRAD, dense, dy, q.d, p->ws_down, nullptr, 0, q.d, 0, q.d, q.fs,
                                       w.sdgu, 2 * q.fs, true, sv.sg, sv.su, q.fs, s0))
       return rc;
