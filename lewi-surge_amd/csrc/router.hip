@@ -13,6 +13,8 @@
 // left in LDS.
 #include "common.h"
 
+#include <utility>
+
 namespace {
 
 constexpr int RT_TOK = 64;       // tokens per workgroup
@@ -158,75 +160,141 @@ __global__ __launch_bounds__(RT_THREADS) void router_topk_kernel(const bf16_t* _
 // Logits kernel: workgroup = 64 tokens x 32 experts (256 threads, 4 tokens x 2 experts each), grid over token
 // blocks x expert blocks, so there are enough waves to fill every SIMD; the d loop is the same sequential
 // f32 sum as above.  The top-k then runs as its own kernel, one wave per token, over the logits in HBM.
+//
+// Lane layout: the 16 lanes of a DPP row (lane / 16) share a token quad and hold 16 different expert pairs
+// (lane % 16).  In each block of 16 d steps, lane i of a row reads the row's four x values of step i from LDS once,
+// and step j takes them from lane j by a DPP row broadcast inside the FMA itself (v_fmac_f32 with row_newbcast:j).
+// So the x operand costs no LDS bandwidth per FMA: only the two weights of the lane's experts are read per step,
+// 144 bytes of LDS reads per 128 FMAs instead of 24 per 8.  v_fmac_f32 rounds like fmaf, so every logit is still
+// the sequential f32 sum over d.
 constexpr int RL_TOK = 64, RL_EXP = 32, RL_DC = 64, RL_THREADS = 256;
 
+// acc + (x of lane J of this lane's row of 16) * w, one rounding
+template <int J>
+__device__ __forceinline__ float fmac_row_bcast(float acc, float x, float w) {
+  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(x), "v"(w), "n"(J));
+  return acc;
+}
+template <int J>
+__device__ __forceinline__ void logits_step(float (&acc)[4][2], const f32x4& xv, const float (*ws)[RL_EXP],
+                                            int dd, int ep) {
+  const float w0 = ws[dd + J][2 * ep], w1 = ws[dd + J][2 * ep + 1];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    acc[a][0] = fmac_row_bcast<J>(acc[a][0], xv[a], w0);
+    acc[a][1] = fmac_row_bcast<J>(acc[a][1], xv[a], w1);
+  }
+}
+template <int... J>
+__device__ __forceinline__ void logits_block(float (&acc)[4][2], const f32x4& xv, const float (*ws)[RL_EXP], int dd,
+                                             int ep, std::integer_sequence<int, J...>) {
+  (logits_step<J>(acc, xv, ws, dd, ep), ...);
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const u32x4& u, float (&v)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(u[i] << 16);
+    v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+  }
+}
+
+// LDS: two buffers of (x chunk transposed to [d][token] f32, w chunk [d][expert] f32).  When d and E are multiples
+// of 8 the next chunk's global loads (raw bf16 in registers) are issued right after the barrier that publishes the
+// current chunk, so their latency hides behind the current chunk's FMAs; other shapes load each chunk in place.
+// Bank-conflict-free LDS traffic: a wave stages 64 consecutive tokens of one d row (lane = token), w goes in as
+// 16-byte stores of 4 consecutive experts, and the x rows are padded to RL_XP floats so the 16 lanes of a DPP row,
+// which read 16 consecutive d rows at the same tokens, hit 16 different groups of 4 banks.
+constexpr int RL_XP = RL_TOK + 4;
 __global__ __launch_bounds__(RL_THREADS) void router_logits_kernel(const bf16_t* __restrict__ x,
                                                                    const bf16_t* __restrict__ w,
                                                                    const float* __restrict__ bias, int T, int d,
                                                                    int E, float* __restrict__ logits) {
-  __shared__ __attribute__((aligned(16))) float xs[RL_DC][RL_TOK];
-  __shared__ __attribute__((aligned(16))) float ws[RL_DC][RL_EXP];
+  __shared__ __attribute__((aligned(16))) float xs[2][RL_DC][RL_XP];
+  __shared__ __attribute__((aligned(16))) float ws[2][RL_DC][RL_EXP];
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * RL_TOK, e0 = blockIdx.y * RL_EXP;
-  const int ep = tid & 15;   // experts e0 + 2 ep, e0 + 2 ep + 1
-  const int tq = tid >> 4;   // tokens t0 + 4 tq .. + 3
+  const int ep = tid & 15;   // experts e0 + 2 ep, e0 + 2 ep + 1 (position in the DPP row)
+  const int tq = tid >> 4;   // tokens t0 + 4 tq .. + 3 (one DPP row)
   float acc[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
   const bool vec = (d & 7) == 0 && (E & 7) == 0;
-  for (int d0 = 0; d0 < d; d0 += RL_DC) {
-    const int dc = min(RL_DC, d - d0);
-    // x: 64 tokens x 64 d as 16-byte chunks (2 per thread), stored transposed as f32
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int c = tid + RL_THREADS * r;
-      const int tt = c >> 3, dd0 = (c & 7) * 8;
-      const int t = t0 + tt;
-      float v[8];
-      if (vec && t < T && dd0 + 8 <= dc) {
-        const u32x4 u = *reinterpret_cast<const u32x4*>(x + (int64_t)t * d + d0 + dd0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[2 * i] = __uint_as_float(u[i] << 16);
-          v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          v[i] = (t < T && dd0 + i < dc) ? bf16_to_f32(x[(int64_t)t * d + d0 + dd0 + i]) : 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xs[dd0 + i][tt] = v[i];
+  // this thread's staging share: x token tid % 64 at d offsets 8 (tid / 64) and 8 (tid / 64 + 4) of the chunk; w d
+  // row tid / 4, experts 8 (tid % 4) ..
+  const int xtt = tid & 63, xc0 = tid >> 6;
+  const int wdd = tid >> 2, wec = (tid & 3) * 8;
+
+  auto compute = [&](int buf, int dc) {
+    const float(*wsb)[RL_EXP] = ws[buf];
+    // whole blocks of 16 d steps: the x values of step dd + i come from lane i of the row (rows past dc are
+    // zero-filled, but the sum must stop at d, so a partial block takes the plain loop)
+    int dd = 0;
+    for (; dd + 16 <= dc; dd += 16) {
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[buf][dd + ep][4 * tq]);
+      logits_block(acc, xv, wsb, dd, ep, std::make_integer_sequence<int, 16>());
     }
-    // w: 64 d x 32 experts as 16-byte chunks (8 experts, 1 per thread)
-    {
-      const int dd = tid >> 2, ec = (tid & 3) * 8;
-      float v[8];
-      if (vec && dd < dc && e0 + ec + 8 <= E) {
-        const u32x4 u = *reinterpret_cast<const u32x4*>(w + (int64_t)(d0 + dd) * E + e0 + ec);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[2 * i] = __uint_as_float(u[i] << 16);
-          v[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          v[i] = (dd < dc && e0 + ec + i < E) ? bf16_to_f32(w[(int64_t)(d0 + dd) * E + e0 + ec + i]) : 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ws[dd][ec + i] = v[i];
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int dd = 0; dd < dc; ++dd) {
-      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[dd][4 * tq]);
-      const float w0 = ws[dd][2 * ep], w1 = ws[dd][2 * ep + 1];
+    for (; dd < dc; ++dd) {
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[buf][dd][4 * tq]);
+      const float w0 = wsb[dd][2 * ep], w1 = wsb[dd][2 * ep + 1];
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         acc[a][0] = __builtin_fmaf(xv[a], w0, acc[a][0]);
         acc[a][1] = __builtin_fmaf(xv[a], w1, acc[a][1]);
       }
     }
-    __syncthreads();
+  };
+
+  if (vec) {
+    u32x4 xr[2], wr;  // raw bf16 of the chunk being loaded (zeros outside the matrices)
+    auto gload = [&](int d0) {
+      const int dc = min(RL_DC, d - d0), t = t0 + xtt;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int dd0 = 8 * (xc0 + 4 * r);
+        xr[r] = (t < T && dd0 < dc) ? *reinterpret_cast<const u32x4*>(x + (int64_t)t * d + d0 + dd0) : u32x4{0, 0, 0, 0};
+      }
+      wr = (wdd < dc && e0 + wec < E) ? *reinterpret_cast<const u32x4*>(w + (int64_t)(d0 + wdd) * E + e0 + wec)
+                                      : u32x4{0, 0, 0, 0};
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int dd0 = 8 * (xc0 + 4 * r);
+        float v[8];
+        unpack_bf16x8(xr[r], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xs[buf][dd0 + i][xtt] = v[i];
+      }
+      float v[8];
+      unpack_bf16x8(wr, v);
+      *reinterpret_cast<f32x4*>(&ws[buf][wdd][wec]) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(&ws[buf][wdd][wec + 4]) = f32x4{v[4], v[5], v[6], v[7]};
+    };
+    gload(0);
+    int buf = 0;
+    for (int d0 = 0; d0 < d; d0 += RL_DC, buf ^= 1) {
+      // buffer buf was last read two chunks ago, before the barrier of the previous chunk
+      sstore(buf);
+      __syncthreads();
+      if (d0 + RL_DC < d) gload(d0 + RL_DC);
+      compute(buf, min(RL_DC, d - d0));
+    }
+  } else {
+    for (int d0 = 0; d0 < d; d0 += RL_DC) {
+      const int dc = min(RL_DC, d - d0);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int dd0 = 8 * (xc0 + 4 * r), t = t0 + xtt;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          xs[0][dd0 + i][xtt] = (t < T && dd0 + i < dc) ? bf16_to_f32(x[(int64_t)t * d + d0 + dd0 + i]) : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        ws[0][wdd][wec + i] = (wdd < dc && e0 + wec + i < E) ? bf16_to_f32(w[(int64_t)(d0 + wdd) * E + e0 + wec + i]) : 0.f;
+      __syncthreads();
+      compute(0, dc);
+      __syncthreads();
+    }
   }
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
