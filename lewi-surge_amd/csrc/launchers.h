@@ -10,9 +10,23 @@ int router_topk_impl(const void* x, const void* w_r, const float* bias, int64_t 
                      float* logits, int32_t* sel, float* weights, hipStream_t s, hipEvent_t after_logits);
 
 // ---- routing layout (layout.hip)
+// Optional 256-row tile table of the layer's grouped GEMMs, written by the layout's scan kernel: expert e gets
+// ceil(gs[e] / 256) tiles, each two consecutive 128-row blocks of its own (the last may hold one block); TS tiles of
+// a shared expert carried as expert E follow (rows P + 256 j of its T rows; row_src of those rows = t k); entries up
+// to TB + TS past them are empty.  num_tiles[0] = routed tiles, num_tiles[1] = all.
+struct LayoutTiles {
+  int32_t* t_expert = nullptr;
+  int32_t* t_rows = nullptr;
+  int32_t* t_row0 = nullptr;
+  int32_t* num_tiles = nullptr;
+  int TB = 0, TS = 0;
+  int64_t P = 0, T = 0;
+  int k = 1;
+};
 int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
                       int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
-                      int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s);
+                      int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s,
+                      const LayoutTiles& tiles = LayoutTiles());
 
 // ---- row movement (permute.hip)
 int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src, const int32_t* num_blocks,

@@ -7,7 +7,8 @@
 // Three kernels:
 //   hist  one workgroup per chunk of LT_CHUNK slots; per-wave LDS histograms -> hist[chunk][E]
 //   scan  one workgroup: per expert, exclusive scan over chunks (chunk_base), group sizes, expert
-//         offsets, block offsets, block table and padding markers in row_src
+//         offsets, block offsets, block table and padding markers in row_src (and, for the layer, the
+//         256-row tile table of its grouped GEMMs)
 //   rank  one workgroup per chunk again; each wave walks its slots 64 at a time in ascending slot order:
 //         lanes with the same expert are found with 8 ballots over the expert-id bits, the rank inside
 //         the wave is popcount(peers below me), and a per-wave LDS counter advances by popcount(peers).
@@ -44,7 +45,36 @@ __global__ __launch_bounds__(LT_THREADS) void layout_hist_kernel(const int32_t* 
   }
 }
 
-// One workgroup.  hist [nchunk][E] is overwritten with the exclusive per-expert chunk base.
+// Exclusive scan of one int per thread over the workgroup (blockDim.x <= 1024): returns the prefix and the total,
+// through the 16-entry LDS scratch ws (reusable after the trailing barrier).
+__device__ __forceinline__ int block_scan_excl(int v, int* ws, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nw = (int)blockDim.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) ws[w] = x;
+  __syncthreads();
+  int base = 0, tot = 0;
+  for (int i = 0; i < nw; ++i) {
+    const int t = ws[i];
+    if (i < w) base += t;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return base + x - v;
+}
+
+// One workgroup of at least E threads (512 or 1024).  hist [nchunk][E] is overwritten with the exclusive per-expert
+// chunk base.
+// Thread (e, j) owns expert e's chunks [j cpt, (j + 1) cpt), kept in registers between the two passes (up to
+// LS_REG chunks; more are read again).  The expert-level scans are block-wide shuffle scans, and the padding
+// markers of row_src are spread over all threads.  With tiles.t_expert set it also writes the 256-row tile table of
+// the layer's grouped GEMMs (see LayoutTiles).
+constexpr int LS_REG = 16;
 __global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__ hist, int nchunk, int E,
                                                            int32_t* __restrict__ group_sizes,
                                                            int32_t* __restrict__ offsets,
@@ -52,27 +82,33 @@ __global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__
                                                            int32_t* __restrict__ row_src,
                                                            int32_t* __restrict__ blk_expert,
                                                            int32_t* __restrict__ blk_rows,
-                                                           int32_t* __restrict__ num_blocks, int max_blocks) {
-  __shared__ int32_t gs_s[LT_EMAX], off_s[LT_EMAX], boff_s[LT_EMAX + 1], part_s[1024];
+                                                           int32_t* __restrict__ num_blocks, int max_blocks,
+                                                           lsurge::LayoutTiles tiles) {
+  __shared__ int32_t gs_s[LT_EMAX], boff_s[LT_EMAX + 1], tb_s[LT_EMAX + 1], part_s[1024], ws[16];
   const int tid = threadIdx.x;
-  // Per-expert exclusive scan over chunks, split over tpe threads per expert (thread (e, j) owns a contiguous
-  // range of chunks): a partial sum per range, an exclusive scan of the tpe partials, then each range rewritten
-  // with its running base.  Loads within a range are issued 8 at a time, so the walk is not a chain of
-  // dependent global round trips.
   int tpe = 1;
   while (tpe * 2 * E <= (int)blockDim.x && tpe < 64) tpe *= 2;
   const int e_t = tid % E, j_t = tid / E;
   const bool scan_lane = j_t < tpe;
   const int cpt = (nchunk + tpe - 1) / tpe;
   const int c0 = j_t * cpt, c1 = min(nchunk, c0 + cpt);
+  const bool in_regs = cpt <= LS_REG;
+  int v[LS_REG];
   if (scan_lane) {
     int sum = 0;
-    for (int c = c0; c < c1; c += 8) {
-      int v[8];
+    if (in_regs) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
+      for (int u = 0; u < LS_REG; ++u) v[u] = c0 + u < c1 ? hist[(int64_t)(c0 + u) * E + e_t] : 0;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) sum += v[u];
+      for (int u = 0; u < LS_REG; ++u) sum += v[u];
+    } else {
+      for (int c = c0; c < c1; c += 8) {
+        int w8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w8[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sum += w8[u];
+      }
     }
     part_s[j_t * E + e_t] = sum;
   }
@@ -80,65 +116,114 @@ __global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__
   for (int e = tid; e < E; e += blockDim.x) {
     int run = 0;
     for (int j = 0; j < tpe; ++j) {
-      const int v = part_s[j * E + e];
+      const int x = part_s[j * E + e];
       part_s[j * E + e] = run;
-      run += v;
+      run += x;
     }
     gs_s[e] = run;
   }
   __syncthreads();
   if (scan_lane) {
     int run = part_s[j_t * E + e_t];
-    for (int c = c0; c < c1; c += 8) {
-      int v[8];
+    if (in_regs) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (c + u < c1) hist[(int64_t)(c + u) * E + e_t] = run;
+      for (int u = 0; u < LS_REG; ++u) {
+        if (c0 + u < c1) hist[(int64_t)(c0 + u) * E + e_t] = run;
         run += v[u];
+      }
+    } else {
+      for (int c = c0; c < c1; c += 8) {
+        int w8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w8[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (c + u < c1) hist[(int64_t)(c + u) * E + e_t] = run;
+          run += w8[u];
+        }
       }
     }
   }
-  __syncthreads();
-  if (tid == 0) {  // E <= 1024: a serial scan is a few microseconds at most
-    int run = 0, brun = 0;
-    for (int e = 0; e < E; ++e) {
-      off_s[e] = run;
-      boff_s[e] = brun;
-      run += gs_s[e];
-      brun += (gs_s[e] + BLK - 1) / BLK;
-    }
-    boff_s[E] = brun;
-    num_blocks[0] = brun;
+  // expert offsets and block offsets (E <= 1024 = one expert per thread), and the 256-row tile bases
+  const int g = tid < E ? gs_s[tid] : 0;
+  int tot;
+  const int off = block_scan_excl(g, ws, &tot);
+  const int nb = (g + BLK - 1) / BLK;
+  int nbt;
+  const int boff = block_scan_excl(nb, ws, &nbt);
+  const int nt = (g + 2 * BLK - 1) / (2 * BLK);
+  int ntt = 0;
+  const int tbase = tiles.t_expert ? block_scan_excl(nt, ws, &ntt) : 0;
+  if (tid < E) {
+    boff_s[tid] = boff;
+    tb_s[tid] = tbase;
+    if (group_sizes) group_sizes[tid] = g;
+    if (offsets) offsets[tid] = off;
+    if (block_off) block_off[tid] = boff;
+  }
+  if (tid == 0) {
+    boff_s[E] = nbt;
+    tb_s[E] = ntt;
+    if (num_blocks) num_blocks[0] = nbt;
   }
   __syncthreads();
-  for (int e = tid; e < E; e += blockDim.x) {
-    if (group_sizes) group_sizes[e] = gs_s[e];
-    if (offsets) offsets[e] = off_s[e];
-    if (block_off) block_off[e] = boff_s[e];
+  if (blk_expert) {
+    // block table: expert e with boff[e] <= b < boff[e + 1] (skips empty experts)
+    for (int b = tid; b < max_blocks; b += blockDim.x) {
+      if (b >= nbt) {
+        blk_expert[b] = -1;
+        blk_rows[b] = 0;
+        continue;
+      }
+      int lo = 0, hi = E - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (boff_s[mid] <= b) lo = mid;
+        else hi = mid - 1;
+      }
+      blk_expert[b] = lo;
+      blk_rows[b] = min(BLK, gs_s[lo] - (b - boff_s[lo]) * BLK);
+    }
+    // padding rows of each expert's last block: row_src = -1
+    for (int i = tid; i < E * BLK; i += blockDim.x) {
+      const int e = i / BLK, r = i % BLK;
+      const int ge = gs_s[e], pad = (ge + BLK - 1) / BLK * BLK - ge;
+      if (r < pad) row_src[(int64_t)BLK * boff_s[e] + ge + r] = -1;
+    }
   }
-  if (!blk_expert) return;
-  // block table; padding rows of the last block of each expert get row_src = -1
-  const int nb = boff_s[E];
-  for (int b = tid; b < max_blocks; b += blockDim.x) {
-    if (b >= nb) {
-      blk_expert[b] = -1;
-      blk_rows[b] = 0;
-      continue;
+  if (tiles.t_expert) {
+    // routed tiles (two consecutive blocks of one expert; the last may hold a single block), then the shared expert's
+    // (expert E, rows P + 256 j), then empty entries up to the bound TB + TS
+    const int total = min(ntt, tiles.TB);  // never clipped for layout-made sizes (they sum to M)
+    for (int t = tid; t < tiles.TB + tiles.TS; t += blockDim.x) {
+      int ex = -1, r0 = 0, rows = 0;
+      if (t < total) {
+        int lo = 0, hi = E - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (tb_s[mid] <= t) lo = mid;
+          else hi = mid - 1;
+        }
+        const int j = t - tb_s[lo];
+        ex = lo;
+        r0 = BLK * boff_s[lo] + 2 * BLK * j;
+        rows = min(2 * BLK, gs_s[lo] - 2 * BLK * j);
+      } else if (t < total + tiles.TS) {
+        const int j = t - total;
+        ex = E;
+        r0 = (int)(tiles.P + 2 * BLK * (int64_t)j);
+        rows = (int)min((int64_t)2 * BLK, tiles.T - 2 * BLK * (int64_t)j);
+      }
+      tiles.t_expert[t] = ex;
+      tiles.t_row0[t] = r0;
+      tiles.t_rows[t] = rows;
     }
-    int lo = 0, hi = E - 1;  // expert e with boff[e] <= b < boff[e+1] (skips empty experts)
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (boff_s[mid] <= b) lo = mid;
-      else hi = mid - 1;
+    if (tiles.TS > 0)
+      for (int64_t r = tid; r < tiles.T; r += blockDim.x) row_src[tiles.P + r] = (int32_t)(r * tiles.k);
+    if (tid == 0) {
+      tiles.num_tiles[0] = total;
+      tiles.num_tiles[1] = total + tiles.TS;
     }
-    const int e = lo;
-    const int j = b - boff_s[e];
-    const int rows = min(BLK, gs_s[e] - j * BLK);
-    blk_expert[b] = e;
-    blk_rows[b] = rows;
-    for (int r = rows; r < BLK; ++r) row_src[(int64_t)b * BLK + r] = -1;
   }
 }
 
@@ -220,7 +305,7 @@ __global__ void invert_perm_kernel(const int32_t* __restrict__ idx, int64_t m, i
 int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
                   int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
                   int32_t* blk_rows, int32_t* num_blocks, int64_t max_blocks, void* ws, size_t ws_bytes,
-                  hipStream_t s) {
+                  hipStream_t s, const lsurge::LayoutTiles& tiles = lsurge::LayoutTiles()) {
   const int64_t nchunk = (M + LT_CHUNK - 1) / LT_CHUNK;
   // workspace: hist [nchunk][E] | offsets [E] | block_off [E] | num_blocks (when caller gives none)
   const size_t need = sizeof(int32_t) * (size_t)(nchunk * E + 2 * E + 4);
@@ -234,10 +319,14 @@ int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_
   if (!num_blocks) num_blocks = nb_ws;
   int nbits = 1;
   while ((1ll << nbits) <= E) ++nbits;  // keys 0..E-1 valid, (1<<nbits)-1 >= E reserved for idle lanes
+  // the scan needs a thread per expert; 512 threads (two waves per SIMD) when that is enough, so that it fits on a CU
+  // beside a running 8-wave GEMM tile (the layer's shared expert runs beside the layout) instead of waiting for one
+  // to drain
+  const unsigned scan_threads = E <= 512 ? 512 : 1024;
   if (M == 0) {
     LSURGE_LAUNCH(KID_LAYOUT_SCAN, s,
-                  hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(1024), 0, s, hist, 0, (int)E, gs, offsets,
-                                     block_off, row_src, blk_expert, blk_rows, num_blocks, (int)max_blocks));
+                  hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(scan_threads), 0, s, hist, 0, (int)E, gs, offsets,
+                                     block_off, row_src, blk_expert, blk_rows, num_blocks, (int)max_blocks, tiles));
     return LSURGE_OK;
   }
   const size_t lds = sizeof(int32_t) * LT_WAVES * (size_t)E;
@@ -245,9 +334,9 @@ int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_
                 hipLaunchKernelGGL(layout_hist_kernel, dim3((unsigned)nchunk), dim3(LT_THREADS), lds, s, flat, M,
                                    (int)E, hist));
   LSURGE_LAUNCH(KID_LAYOUT_SCAN, s,
-                hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(1024), 0, s, hist, (int)nchunk, (int)E, gs,
+                hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(scan_threads), 0, s, hist, (int)nchunk, (int)E, gs,
                                    offsets, block_off, row_src, blk_expert, blk_rows, num_blocks,
-                                   (int)max_blocks));
+                                   (int)max_blocks, tiles));
   LSURGE_LAUNCH(KID_LAYOUT_RANK, s,
                 hipLaunchKernelGGL(layout_rank_kernel, dim3((unsigned)nchunk), dim3(LT_THREADS), lds, s, flat, M,
                                    (int)E, hist, offsets, block_off, nbits, order, pos, slot, row_src));
@@ -259,9 +348,12 @@ int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_
 namespace lsurge {
 int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
                       int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
-                      int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s) {
+                      int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s,
+                      const LayoutTiles& tiles) {
+  LSURGE_REQUIRE(!tiles.t_expert || (tiles.t_rows && tiles.t_row0 && tiles.num_tiles && row_src && E <= 1024),
+                 "layout: incomplete tile table outputs");
   return layout_common(flat, M, E, gs, offsets, block_off, order, pos, slot, row_src, blk_expert, blk_rows,
-                       num_blocks, lsurge_max_blocks(M, E), ws, ws_bytes, s);
+                       num_blocks, lsurge_max_blocks(M, E), ws, ws_bytes, s, tiles);
 }
 }  // namespace lsurge
 

@@ -159,54 +159,6 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   return c.off + 256;
 }
 
-// 256-row tile table of the grouped GEMMs (one workgroup; E <= 256).  Expert e owns padded rows
-// [128 block_off[e], 128 block_off[e] + gs[e]) and gets ceil(gs[e] / 256) tiles, each two consecutive 128-row blocks
-// of its own (the last one may hold a single block; its second half belongs to no tile and is never touched).  A
-// merged shared expert (SB2 > 0) follows as expert E with tiles over its rows P + 256 j, and row_src of those rows
-// gets token t -> flat slot t k, so the row gathers read x[t].  Entries past the tiles are empty.
-__global__ __launch_bounds__(256) void pair_tiles_kernel(const int32_t* __restrict__ gs,
-                                                         const int32_t* __restrict__ block_off, int E, int TB, int SB2,
-                                                         int64_t P, int64_t T, int k, int32_t* __restrict__ t_expert,
-                                                         int32_t* __restrict__ t_rows, int32_t* __restrict__ t_row0,
-                                                         int32_t* __restrict__ num_tiles, int32_t* __restrict__ row_src) {
-  __shared__ int wsum[4];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int g = tid < E ? max(gs[tid], 0) : 0;
-  const int n = (g + 2 * BLK - 1) / (2 * BLK);
-  int x = n;  // inclusive scan of the tile counts
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  if (lane == 63) wsum[w] = x;
-  __syncthreads();
-  int base = x - n, total = 0;
-  for (int i = 0; i < 4; ++i) {
-    if (i < w) base += wsum[i];
-    total += wsum[i];
-  }
-  total = min(total, TB);  // never for layout-made sizes (they sum to M)
-  for (int j = 0; j < n && base + j < TB; ++j) {
-    t_expert[base + j] = tid;
-    t_row0[base + j] = BLK * block_off[tid] + 2 * BLK * j;
-    t_rows[base + j] = min(2 * BLK, g - 2 * BLK * j);
-  }
-  for (int i = total + tid; i < TB + SB2; i += blockDim.x) {
-    const int j = i - total;
-    const bool sh = j < SB2;
-    t_expert[i] = sh ? E : -1;
-    t_row0[i] = sh ? (int32_t)(P + 2 * BLK * j) : 0;
-    t_rows[i] = sh ? (int32_t)min((int64_t)2 * BLK, T - 2 * BLK * j) : 0;
-  }
-  if (SB2 > 0)
-    for (int64_t r = tid; r < T; r += blockDim.x) row_src[P + r] = (int32_t)(r * k);
-  if (tid == 0) {
-    num_tiles[0] = total;
-    num_tiles[1] = total + SB2;
-  }
-}
-
 int check_shape(const lsurge_moe_shape* s) {
   LSURGE_REQUIRE(s, "moe: null shape");
   LSURGE_REQUIRE(s->t >= 1 && s->d >= 8 && s->e >= 1 && s->e <= 256 && s->k >= 1 && s->k <= s->e && s->k <= 16 &&
@@ -323,15 +275,22 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
     if (int rc = lsurge::gemm_rows_kn(KID_SHARED_DOWN_FWD, dense, sh, q.fs, p->ws_down, q.d, 0, q.fs, q.d, sy, q.d, s0))
       return rc;
   }
+  // the layout also writes the backward's 256-row tile table: routed tiles, then the merged shared expert's (and
+  // its row_src)
+  lsurge::LayoutTiles tiles;
+  tiles.t_expert = sv.t_expert;
+  tiles.t_rows = sv.t_rows;
+  tiles.t_row0 = sv.t_row0;
+  tiles.num_tiles = sv.num_tiles;
+  tiles.TB = (int)q.TB;
+  tiles.TS = (int)q.TS;
+  tiles.P = q.P;
+  tiles.T = q.T;
+  tiles.k = (int)q.k;
   if (int rc = lsurge::build_layout_impl(sv.sel, q.M, q.E, sv.gs, sv.offsets, sv.block_off, sv.order, sv.pos, sv.slot,
                                          sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks, workspace,
-                                         workspace_bytes, st))
+                                         workspace_bytes, st, tiles))
     return rc;
-  // the backward's 256-row tile table: routed tiles, then the merged shared expert's (and its row_src)
-  LSURGE_LAUNCH(KID_MISC, st,
-                hipLaunchKernelGGL(pair_tiles_kernel, dim3(1), dim3(256), 0, st, sv.gs, sv.block_off, (int)q.E,
-                                   (int)q.TB, (int)q.TS, q.P, q.T, (int)q.k, sv.t_expert, sv.t_rows, sv.t_row0,
-                                   sv.num_tiles, sv.row_src));
   // the routed forward GEMMs run 128-row blocks on the 4-wave kernel (the ping-pong kernel measured no faster here)
   const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
   lsurge::RowGather gather;
