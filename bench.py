@@ -38,6 +38,11 @@ CONFIGS = {  # BASELINE.json configs (T, d, E, k, f, fs, zipf bias, fwd+bwd)
 }
 
 
+def fused_router(c):
+    """Shapes whose router runs as one kernel (logits, top-k, softmax, the layout's per-64-token histograms)."""
+    return c["E"] in (32, 64, 128) and c["k"] <= 8 and c["d"] % 64 == 0
+
+
 def kernel_work(c):
     """Algorithmic work per launch of each kernel: ('mfma', flops) over useful rows, or ('hbm', bytes)."""
     T, d, E, k, f, fs = c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"]
@@ -52,7 +57,8 @@ def kernel_work(c):
         "gemm_gu_dgrad": ("mfma", 2 * Mb * 2 * f * d),
         "gemm_gu_wgrad": ("mfma", 2 * Mb * d * 2 * f),
         "router_wgrad": ("mfma", 2 * T * d * E),
-        "router_topk": ("hbm", T * d * 2 + d * E * 2 + T * E * 4),
+        "router_topk": ("hbm", T * d * 2 + d * E * 2 + T * E * 4
+                        + (8 * T * k + 4 * E * ((T + 63) // 64) if fused_router(c) else 0)),
         "router_select": ("hbm", T * E * 4 + 8 * T * k),
         "dispatch": ("hbm", 2 * M * d * 2 + 4 * M),
         "combine_fwd": ("hbm", M * d * 2 + T * d * 2 * (2 if fs else 1) + 8 * T * k),
@@ -181,11 +187,13 @@ def launch_roles(c):
     fs, f = c["fs"], c["f"]
     own = bool(fs) and fs != f  # shared expert of its own width: dense backward GEMMs on a helper stream
     r = {
-        "router_logits_kernel": ["router_topk"], "router_select_lane_kernel<8>": ["router_select"],
+        "router_logits_kernel": ["router_topk"], "router_fused_kernel<1>": ["router_topk"],
+        "router_fused_kernel<2>": ["router_topk"], "router_fused_kernel<4>": ["router_topk"],
+        "router_select_lane_kernel<8>": ["router_select"],
         "router_select_lane_kernel<16>": ["router_select"], "router_select_kernel<1>": ["router_select"],
         "router_select_kernel<2>": ["router_select"], "router_select_kernel<4>": ["router_select"],
         "layout_hist_kernel": ["layout_hist"], "layout_scan_kernel": ["layout_scan"],
-        "layout_rank_kernel": ["layout_rank"], "shared_tiles_kernel": ["misc"],
+        "layout_rank_kernel": ["layout_rank"],
         "gemm_rows_kernel<1,1>": (["shared_gu_fwd"] if fs else []) + ["gemm_gu_fwd"],
         "gemm_rows_kernel<1,0>": (["shared_down_fwd"] if fs else []) + ["gemm_down_fwd"],
         "combine_pad_kernel<2,6,1>": ["combine_fwd"], "combine_pad_kernel<2,8,1>": ["combine_fwd"],

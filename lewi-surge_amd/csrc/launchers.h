@@ -6,8 +6,15 @@
 namespace lsurge {
 
 // ---- router (router.hip): lsurge_router_topk with an optional event recorded right after the logits kernel
+// after_logits (optional): a hipEvent recorded on the stream right after the logits kernel of the split path (after
+// the fused kernel on the fused path), so a caller can start independent work beside the selection
 int router_topk_impl(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d, int64_t e, int64_t k,
-                     float* logits, int32_t* sel, float* weights, hipStream_t s, hipEvent_t after_logits);
+                     float* logits, int32_t* sel, float* weights, hipStream_t s, hipEvent_t after_logits,
+                     int32_t* hist = nullptr);
+// Shapes the workgroup-fused router takes (logits, top-k, softmax and the per-64-token expert histograms in one
+// kernel): e in {32, 64, 128}, k <= 8, d a multiple of 64.  router_topk_impl uses it when given hist
+// ([ceil(t / 64)][e] int32, the layout's chunk counts for chunks of 64 tokens).
+bool router_fused_ok(int64_t d, int64_t e, int64_t k);
 
 // ---- routing layout (layout.hip)
 // Optional 256-row tile table of the layer's grouped GEMMs, written by the layout's scan kernel: expert e gets
@@ -23,10 +30,16 @@ struct LayoutTiles {
   int64_t P = 0, T = 0;
   int k = 1;
 };
+// Optional per-chunk expert histograms made by the caller (the fused router): hist [nchunk][E] for chunks of
+// waves x 64 consecutive slots (overwritten with the per-expert chunk bases); the layout then skips its own.
+struct LayoutChunks {
+  int32_t* hist = nullptr;
+  int waves = 0;
+};
 int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
                       int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
                       int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s,
-                      const LayoutTiles& tiles = LayoutTiles());
+                      const LayoutTiles& tiles = LayoutTiles(), const LayoutChunks& pre = LayoutChunks());
 
 // ---- row movement (permute.hip)
 int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src, const int32_t* num_blocks,

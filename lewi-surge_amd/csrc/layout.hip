@@ -9,7 +9,8 @@
 //   scan  one workgroup: per expert, exclusive scan over chunks (chunk_base), group sizes, expert
 //         offsets, block offsets, block table and padding markers in row_src (and, for the layer, the
 //         256-row tile table of its grouped GEMMs)
-//   rank  one workgroup per chunk again; each wave walks its slots 64 at a time in ascending slot order:
+//   rank  one workgroup per chunk again (or per chunk of the fused router's histograms, which replace the hist
+//         kernel in the layer); each wave walks its slots 64 at a time in ascending slot order:
 //         lanes with the same expert are found with 8 ballots over the expert-id bits, the rank inside
 //         the wave is popcount(peers below me), and a per-wave LDS counter advances by popcount(peers).
 #include "launchers.h"
@@ -236,20 +237,22 @@ __device__ __forceinline__ uint64_t peers_of(int key, int nbits) {
   return m;
 }
 
-__global__ __launch_bounds__(LT_THREADS) void layout_rank_kernel(
+// One workgroup per chunk of (blockDim.x / 64) * per_wave slots (LT_CHUNK for the layout's own histograms, 64 k
+// when the fused router made them: one 64-slot pass per wave).
+__global__ __launch_bounds__(1024) void layout_rank_kernel(
     const int32_t* __restrict__ flat, int64_t M, int E, const int32_t* __restrict__ chunk_base,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ block_off, int nbits,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ block_off, int nbits, int per_wave,
     int32_t* __restrict__ order, int32_t* __restrict__ pos, int32_t* __restrict__ slot,
     int32_t* __restrict__ row_src) {
-  extern __shared__ int32_t sh[];  // cnt[LT_WAVES][E] (per-wave running rank base inside the expert)
+  extern __shared__ int32_t sh[];  // cnt[waves][E] (per-wave running rank base inside the expert)
   int32_t* cnt = sh;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int64_t cbase = (int64_t)blockIdx.x * LT_CHUNK;
-  for (int i = tid; i < LT_WAVES * E; i += LT_THREADS) cnt[i] = 0;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = (int)blockDim.x >> 6;
+  const int64_t cbase = (int64_t)blockIdx.x * nw * per_wave;
+  for (int i = tid; i < nw * E; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
   // per-wave histograms of this chunk
-  for (int r = 0; r < LT_PER_WAVE; r += 64) {
-    const int64_t i = cbase + (int64_t)wv * LT_PER_WAVE + r + lane;
+  for (int r = 0; r < per_wave; r += 64) {
+    const int64_t i = cbase + (int64_t)wv * per_wave + r + lane;
     if (i < M) {
       const int e = flat[i];
       if (e >= 0 && e < E) atomicAdd(&cnt[wv * E + e], 1);
@@ -257,9 +260,9 @@ __global__ __launch_bounds__(LT_THREADS) void layout_rank_kernel(
   }
   __syncthreads();
   // exclusive scan over waves, seeded with the chunk base (rank of the first slot of this chunk in e)
-  for (int e = tid; e < E; e += LT_THREADS) {
+  for (int e = tid; e < E; e += blockDim.x) {
     int run = chunk_base[(int64_t)blockIdx.x * E + e];
-    for (int w = 0; w < LT_WAVES; ++w) {
+    for (int w = 0; w < nw; ++w) {
       const int v = cnt[w * E + e];
       cnt[w * E + e] = run;
       run += v;
@@ -268,8 +271,8 @@ __global__ __launch_bounds__(LT_THREADS) void layout_rank_kernel(
   __syncthreads();
   int32_t* my = cnt + wv * E;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int r = 0; r < LT_PER_WAVE; r += 64) {
-    const int64_t i = cbase + (int64_t)wv * LT_PER_WAVE + r + lane;
+  for (int r = 0; r < per_wave; r += 64) {
+    const int64_t i = cbase + (int64_t)wv * per_wave + r + lane;
     const int fe = i < M ? flat[i] : -1;
     const bool valid = fe >= 0 && fe < E;  // ids outside [0, E) are skipped (documented as invalid input)
     const int e = valid ? fe : -1;
@@ -305,13 +308,17 @@ __global__ void invert_perm_kernel(const int32_t* __restrict__ idx, int64_t m, i
 int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
                   int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
                   int32_t* blk_rows, int32_t* num_blocks, int64_t max_blocks, void* ws, size_t ws_bytes,
-                  hipStream_t s, const lsurge::LayoutTiles& tiles = lsurge::LayoutTiles()) {
-  const int64_t nchunk = (M + LT_CHUNK - 1) / LT_CHUNK;
-  // workspace: hist [nchunk][E] | offsets [E] | block_off [E] | num_blocks (when caller gives none)
-  const size_t need = sizeof(int32_t) * (size_t)(nchunk * E + 2 * E + 4);
+                  hipStream_t s, const lsurge::LayoutTiles& tiles = lsurge::LayoutTiles(),
+                  const lsurge::LayoutChunks& pre = lsurge::LayoutChunks()) {
+  // chunks: LT_CHUNK slots with histograms made here, or the caller's (pre.hist, pre.waves x 64 slots each)
+  const int waves = pre.hist ? pre.waves : LT_WAVES, per_wave = pre.hist ? 64 : LT_PER_WAVE;
+  const int64_t chunk = (int64_t)waves * per_wave;
+  const int64_t nchunk = (M + chunk - 1) / chunk;
+  // workspace: hist [nchunk][E] (unless given) | offsets [E] | block_off [E] | num_blocks (when caller gives none)
+  const size_t need = sizeof(int32_t) * (size_t)((pre.hist ? 0 : nchunk * E) + 2 * E + 4);
   LSURGE_REQUIRE(ws && ws_bytes >= need, "layout: workspace %zu < %zu bytes", ws_bytes, need);
-  int32_t* hist = (int32_t*)ws;
-  int32_t* off_ws = hist + nchunk * E;
+  int32_t* hist = pre.hist ? pre.hist : (int32_t*)ws;
+  int32_t* off_ws = (int32_t*)ws + (pre.hist ? 0 : nchunk * E);
   int32_t* boff_ws = off_ws + E;
   int32_t* nb_ws = boff_ws + E;
   if (!offsets) offsets = off_ws;
@@ -329,17 +336,18 @@ int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_
                                      block_off, row_src, blk_expert, blk_rows, num_blocks, (int)max_blocks, tiles));
     return LSURGE_OK;
   }
-  const size_t lds = sizeof(int32_t) * LT_WAVES * (size_t)E;
-  LSURGE_LAUNCH(KID_LAYOUT_HIST, s,
-                hipLaunchKernelGGL(layout_hist_kernel, dim3((unsigned)nchunk), dim3(LT_THREADS), lds, s, flat, M,
-                                   (int)E, hist));
+  if (!pre.hist)
+    LSURGE_LAUNCH(KID_LAYOUT_HIST, s,
+                  hipLaunchKernelGGL(layout_hist_kernel, dim3((unsigned)nchunk), dim3(LT_THREADS),
+                                     sizeof(int32_t) * LT_WAVES * (size_t)E, s, flat, M, (int)E, hist));
   LSURGE_LAUNCH(KID_LAYOUT_SCAN, s,
                 hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(scan_threads), 0, s, hist, (int)nchunk, (int)E, gs,
                                    offsets, block_off, row_src, blk_expert, blk_rows, num_blocks,
                                    (int)max_blocks, tiles));
   LSURGE_LAUNCH(KID_LAYOUT_RANK, s,
-                hipLaunchKernelGGL(layout_rank_kernel, dim3((unsigned)nchunk), dim3(LT_THREADS), lds, s, flat, M,
-                                   (int)E, hist, offsets, block_off, nbits, order, pos, slot, row_src));
+                hipLaunchKernelGGL(layout_rank_kernel, dim3((unsigned)nchunk), dim3(64 * waves),
+                                   sizeof(int32_t) * waves * (size_t)E, s, flat, M, (int)E, hist, offsets, block_off,
+                                   nbits, per_wave, order, pos, slot, row_src));
   return LSURGE_OK;
 }
 
@@ -349,11 +357,12 @@ namespace lsurge {
 int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
                       int32_t* order, int32_t* pos, int32_t* slot, int32_t* row_src, int32_t* blk_expert,
                       int32_t* blk_rows, int32_t* num_blocks, void* ws, size_t ws_bytes, hipStream_t s,
-                      const LayoutTiles& tiles) {
+                      const LayoutTiles& tiles, const LayoutChunks& pre) {
   LSURGE_REQUIRE(!tiles.t_expert || (tiles.t_rows && tiles.t_row0 && tiles.num_tiles && row_src && E <= 1024),
                  "layout: incomplete tile table outputs");
+  LSURGE_REQUIRE(!pre.hist || (pre.waves >= 1 && pre.waves <= 16), "layout: chunk waves=%d not in [1, 16]", pre.waves);
   return layout_common(flat, M, E, gs, offsets, block_off, order, pos, slot, row_src, blk_expert, blk_rows,
-                       num_blocks, lsurge_max_blocks(M, E), ws, ws_bytes, s, tiles);
+                       num_blocks, lsurge_max_blocks(M, E), ws, ws_bytes, s, tiles, pre);
 }
 }  // namespace lsurge
 

@@ -159,6 +159,13 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   return c.off + 256;
 }
 
+// The fused router's per-64-token expert histograms (the layout's chunk counts), at the start of the forward
+// workspace; 0 when the shape takes the split router.
+size_t router_hist_bytes(const lsurge_moe_shape* s) {
+  if (!lsurge::router_fused_ok(s->d, s->e, s->k)) return 0;
+  return ((size_t)((s->t + 63) / 64) * (size_t)s->e * sizeof(int32_t) + 255) / 256 * 256;
+}
+
 int check_shape(const lsurge_moe_shape* s) {
   LSURGE_REQUIRE(s, "moe: null shape");
   LSURGE_REQUIRE(s->t >= 1 && s->d >= 8 && s->e >= 1 && s->e <= 256 && s->k >= 1 && s->k <= s->e && s->k <= 16 &&
@@ -186,7 +193,7 @@ size_t lsurge_moe_saved_bytes(const lsurge_moe_shape* s) {
 
 size_t lsurge_moe_fwd_workspace_bytes(const lsurge_moe_shape* s) {
   if (check_shape(s)) return 0;
-  return lsurge_layout_workspace_bytes(s->t * s->k, s->e) + 256;
+  return router_hist_bytes(s) + lsurge_layout_workspace_bytes(s->t * s->k, s->e) + 256;
 }
 
 size_t lsurge_moe_bwd_workspace_bytes(const lsurge_moe_shape* s) {
@@ -249,10 +256,14 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   if (int rc = fg.acquire(st)) return rc;
   hipStream_t s0 = fg.f.side[0];
 
-  // main: router logits -> (s0 forks here) -> top-k selection
+  // main: router logits -> (s0 forks here) -> top-k selection; where the fused router takes the shape, one kernel
+  // (logits, top-k, softmax and the layout's per-64-token histograms), after which s0 forks
   // (serial mode: the helpers are the caller's stream and have no events)
+  const size_t hist_bytes = router_hist_bytes(s);
+  LSURGE_REQUIRE(workspace && workspace_bytes >= hist_bytes, "moe_fwd: workspace %zu bytes too small", workspace_bytes);
+  int32_t* rhist = hist_bytes ? (int32_t*)workspace : nullptr;
   if (int rc = lsurge::router_topk_impl(p->x, p->w_r, p->bias, q.T, q.d, q.E, q.k, sv.logits, sv.sel, sv.weights, st,
-                                        s0 != st ? fg.f.ev[0] : nullptr))
+                                        s0 != st ? fg.f.ev[0] : nullptr, rhist))
     return rc;
   // s0: the shared expert's forward, dense GEMMs over all T tokens.  It depends on x only; it starts after the
   // router's logits kernel (VALU-bound, it would share the CUs badly) and overlaps the selection and the layout,
@@ -287,9 +298,13 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   tiles.P = q.P;
   tiles.T = q.T;
   tiles.k = (int)q.k;
+  lsurge::LayoutChunks chunks;  // the fused router's histograms: chunks of 64 tokens = k waves of 64 slots
+  chunks.hist = rhist;
+  chunks.waves = (int)q.k;
   if (int rc = lsurge::build_layout_impl(sv.sel, q.M, q.E, sv.gs, sv.offsets, sv.block_off, sv.order, sv.pos, sv.slot,
-                                         sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks, workspace,
-                                         workspace_bytes, st, tiles))
+                                         sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks,
+                                         (char*)workspace + hist_bytes, workspace_bytes - hist_bytes, st, tiles,
+                                         chunks))
     return rc;
   // the routed forward GEMMs run 128-row blocks on the 4-wave kernel (the ping-pong kernel measured no faster here)
   const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};

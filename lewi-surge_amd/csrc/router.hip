@@ -11,7 +11,7 @@
 // experts in registers; per d it reads one f32x4 of x (4 tokens) and EPT/4 f32x4 of w from LDS, so the loop is
 // FMA-bound (32 FMAs per 3 LDS reads at E = 64).  The selection then runs one wave per token over the logits
 // left in LDS.
-#include "common.h"
+#include "launchers.h"
 
 #include <utility>
 
@@ -175,8 +175,8 @@ __device__ __forceinline__ float fmac_row_bcast(float acc, float x, float w) {
   asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(x), "v"(w), "n"(J));
   return acc;
 }
-template <int J>
-__device__ __forceinline__ void logits_step(float (&acc)[4][2], const f32x4& xv, const float (*ws)[RL_EXP],
+template <int J, int WP = RL_EXP>
+__device__ __forceinline__ void logits_step(float (&acc)[4][2], const f32x4& xv, const float (*ws)[WP],
                                             int dd, int ep) {
   const float w0 = ws[dd + J][2 * ep], w1 = ws[dd + J][2 * ep + 1];
 #pragma unroll
@@ -185,10 +185,10 @@ __device__ __forceinline__ void logits_step(float (&acc)[4][2], const f32x4& xv,
     acc[a][1] = fmac_row_bcast<J>(acc[a][1], xv[a], w1);
   }
 }
-template <int... J>
-__device__ __forceinline__ void logits_block(float (&acc)[4][2], const f32x4& xv, const float (*ws)[RL_EXP], int dd,
+template <int WP = RL_EXP, int... J>
+__device__ __forceinline__ void logits_block(float (&acc)[4][2], const f32x4& xv, const float (*ws)[WP], int dd,
                                              int ep, std::integer_sequence<int, J...>) {
-  (logits_step<J>(acc, xv, ws, dd, ep), ...);
+  (logits_step<J, WP>(acc, xv, ws, dd, ep), ...);
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const u32x4& u, float (&v)[8]) {
@@ -308,6 +308,174 @@ __global__ __launch_bounds__(RL_THREADS) void router_logits_kernel(const bf16_t*
   }
 }
 
+// ---------------------------------------------------------------------------------------------- workgroup-fused path
+// Fused router of the layer (E = 32 NEG experts, k <= 8): one workgroup = 64 tokens x all E experts, 4 NEG waves.  Wave w covers
+// tokens 16 (w % 4) .. + 15 and experts 32 (w / 4) .. + 31 with the lane layout of router_logits_kernel (a DPP row =
+// one token quad x 16 expert pairs), the same prefetched, bank-conflict-free staging and the same sequential f32
+// sum over d, so the logits are bitwise those of the split path.  Then, in the same workgroup:
+//  - the logits go to HBM and to an LDS tile [64][E + 1];
+//  - top-k + softmax per token: L = 4 NEG lanes per token each keep a sorted list of their E / L = 8 experts (scanned
+//    in ascending expert order, a logit moves ahead only of strictly smaller ones), and k merge rounds take the best
+//    head of the L lists (larger logit, ties to the lower expert index) -- the order of a stable descending sort, as
+//    in router_select_lane_kernel, whose softmax (in rank order) this repeats;
+//  - the expert histogram of the workgroup's 64 k slots (LDS counters) -> hist[blockIdx.x][E], the layout's
+//    per-chunk counts (chunks of 64 tokens).
+// This replaces the selection kernel, the layout's histogram kernel and the logits round trip between them.
+constexpr int RF_TOK = 64, RF_DC = 64, RF_XP = RF_TOK + 4;
+
+template <int NEG>
+__global__ __launch_bounds__(256 * NEG) void router_fused_kernel(const bf16_t* __restrict__ x,
+                                                                 const bf16_t* __restrict__ w,
+                                                                 const float* __restrict__ bias, int T, int d, int k,
+                                                                 float* __restrict__ logits, int32_t* __restrict__ sel,
+                                                                 float* __restrict__ weights,
+                                                                 int32_t* __restrict__ hist) {
+  constexpr int E = 32 * NEG, NT = 256 * NEG, L = NT / RF_TOK, EPL = E / L;  // lanes per token, experts per lane
+  static_assert(EPL == 8, "eight experts per lane");
+  __shared__ __attribute__((aligned(16))) float xs[2][RF_DC][RF_XP];  // after the d loop: logits tile [64][E + 1]
+  __shared__ __attribute__((aligned(16))) float ws[2][RF_DC][E];
+  __shared__ int32_t cnt[E];
+  static_assert(RF_TOK * (E + 1) <= 2 * RF_DC * RF_XP, "logits tile fits the x buffers");
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int t0 = blockIdx.x * RF_TOK;
+  const int tq = 4 * (wv & 3) + (lane >> 4);  // token quad (tokens t0 + 4 tq ..)
+  const int ep = 16 * (wv >> 2) + (lane & 15);  // expert pair (experts 2 ep, 2 ep + 1)
+  float acc[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+  for (int e = tid; e < E; e += NT) cnt[e] = 0;
+  // staging: x chunks q = tid + NT r (q < 512): token q % 64, d offset 8 (q / 64); w chunk tid: d row tid / (E / 8),
+  // experts 8 (tid % (E / 8)) ..
+  constexpr int XQ = RF_TOK * (RF_DC / 8), XR = (XQ + NT - 1) / NT;  // x chunks, per thread
+  const int xtt = tid & 63;
+  const int wdd = tid / (E / 8), wec = 8 * (tid % (E / 8));
+  u32x4 xr[XR], wr;
+  auto gload = [&](int d0) {
+    const int t = t0 + xtt;
+#pragma unroll
+    for (int r = 0; r < XR; ++r) {
+      const int q = tid + NT * r;
+      if (q < XQ) xr[r] = t < T ? *reinterpret_cast<const u32x4*>(x + (int64_t)t * d + d0 + 8 * (q >> 6)) : u32x4{0, 0, 0, 0};
+    }
+    wr = *reinterpret_cast<const u32x4*>(w + (int64_t)(d0 + wdd) * E + wec);
+  };
+  auto sstore = [&](int buf) {
+    float v[8];
+#pragma unroll
+    for (int r = 0; r < XR; ++r) {
+      const int q = tid + NT * r;
+      if (q < XQ) {
+        unpack_bf16x8(xr[r], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xs[buf][8 * (q >> 6) + i][xtt] = v[i];
+      }
+    }
+    unpack_bf16x8(wr, v);
+    *reinterpret_cast<f32x4*>(&ws[buf][wdd][wec]) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(&ws[buf][wdd][wec + 4]) = f32x4{v[4], v[5], v[6], v[7]};
+  };
+  gload(0);
+  int buf = 0;
+  for (int d0 = 0; d0 < d; d0 += RF_DC, buf ^= 1) {  // d % 64 == 0 (checked on the host)
+    sstore(buf);
+    __syncthreads();
+    if (d0 + RF_DC < d) gload(d0 + RF_DC);
+    const float(*wsb)[E] = ws[buf];
+#pragma unroll
+    for (int dd = 0; dd < RF_DC; dd += 16) {
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[buf][dd + (lane & 15)][4 * tq]);
+      logits_block<E>(acc, xv, wsb, dd, ep, std::make_integer_sequence<int, 16>());
+    }
+  }
+  __syncthreads();  // every wave is done with the x buffers: they now hold the logits tile
+  float* lt = &xs[0][0][0];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int tt = 4 * tq + a, t = t0 + tt;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = 2 * ep + j;
+      const float v = bias ? acc[a][j] + bias[e] : acc[a][j];
+      lt[tt * (E + 1) + e] = v;
+      if (t < T) logits[(int64_t)t * E + e] = v;
+    }
+  }
+  __syncthreads();
+  // selection: token tid / L, lane part tid % L scans experts part, part + L, ... (ascending)
+  const int tt = tid / L, part = tid % L, t = t0 + tt;
+  float tv[EPL];
+  int ti[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    tv[j] = 0.f;
+    ti[j] = -1;
+  }
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) {
+    const int e = part + L * c;
+    const float v = lt[tt * (E + 1) + e];
+    bool placed = false;
+    float cv = v;
+    int ci = e;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const bool g = placed || ti[j] < 0 || cv > tv[j];
+      const float ov = tv[j];
+      const int oi = ti[j];
+      tv[j] = g ? cv : ov;
+      ti[j] = g ? ci : oi;
+      cv = g ? ov : cv;
+      ci = g ? oi : ci;
+      placed = g;
+    }
+  }
+  // k merge rounds over the L lanes of the token (an aligned group of L lanes of one wave)
+  float top0 = 0.f, denom = 0.f, zj[8];
+  int sj[8];
+  int head = 0;
+  for (int j = 0; j < k; ++j) {
+    float hv = 0.f;
+    int hi = -1;
+#pragma unroll
+    for (int q = 0; q < EPL; ++q)
+      if (q == head) {
+        hv = tv[q];
+        hi = ti[q];
+      }
+    float bv = hv;
+    int bi = hi;
+#pragma unroll
+    for (int o = 1; o < L; o <<= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (hi == bi && hi >= 0) ++head;  // the lane that held the winner advances
+    if (j == 0) top0 = bv;
+    const float z = __expf(bv - top0);
+    denom += z;
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (q == j) {
+        zj[q] = z;
+        sj[q] = bi;
+      }
+  }
+  if (part == 0 && t < T) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < k) {
+        sel[(int64_t)t * k + j] = sj[j];
+        weights[(int64_t)t * k + j] = zj[j] / denom;
+        atomicAdd(&cnt[sj[j]], 1);  // LDS counter: the count does not depend on the order
+      }
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += NT) hist[(int64_t)blockIdx.x * E + e] = cnt[e];
+}
+
 // one wave per token: top-k (larger logit first, ties to the lower expert index), softmax over the k
 template <int EC>  // logits per lane: E <= 64 EC
 __global__ __launch_bounds__(256) void router_select_kernel(const float* __restrict__ logits, int T, int E, int k,
@@ -417,12 +585,6 @@ __global__ __launch_bounds__(256) void router_select_lane_kernel(const float* __
 
 }  // namespace
 
-namespace lsurge {
-// after_logits (optional): a hipEvent recorded on the stream right after the logits kernel of the split path, so a
-// caller can start independent work beside the selection
-int router_topk_impl(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d, int64_t e, int64_t k,
-                     float* logits, int32_t* sel, float* weights, hipStream_t s, hipEvent_t after_logits);
-}  // namespace lsurge
 
 extern "C" int lsurge_router_topk(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d,
                                   int64_t e, int64_t k, float* logits, int32_t* sel, float* weights,
@@ -430,15 +592,35 @@ extern "C" int lsurge_router_topk(const void* x, const void* w_r, const float* b
   return lsurge::router_topk_impl(x, w_r, bias, t, d, e, k, logits, sel, weights, (hipStream_t)stream, nullptr);
 }
 
+bool lsurge::router_fused_ok(int64_t d, int64_t e, int64_t k) {
+  return (e == 32 || e == 64 || e == 128) && k >= 1 && k <= 8 && d >= 64 && d % 64 == 0;
+}
+
 int lsurge::router_topk_impl(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d, int64_t e,
                              int64_t k, float* logits, int32_t* sel, float* weights, hipStream_t stream,
-                             hipEvent_t after_logits) {
+                             hipEvent_t after_logits, int32_t* hist) {
   LSURGE_REQUIRE(x && w_r && sel && weights, "router_topk: null pointer");
   LSURGE_REQUIRE(t >= 0 && d > 0 && e >= 1 && e <= RT_EMAX && k >= 1 && k <= e, "router_topk: bad shape t=%lld d=%lld e=%lld k=%lld",
                  (long long)t, (long long)d, (long long)e, (long long)k);
   LSURGE_REQUIRE(t < (1ll << 31) && t * d < (1ll << 40), "router_topk: too large");
   if (t == 0) return LSURGE_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (hist) {  // workgroup-fused path: logits, top-k, softmax and the per-64-token histograms in one kernel
+    LSURGE_REQUIRE(logits && router_fused_ok(d, e, k), "router_topk: shape d=%lld e=%lld k=%lld has no fused kernel",
+                   (long long)d, (long long)e, (long long)k);
+    const dim3 grid((unsigned)((t + RF_TOK - 1) / RF_TOK));
+#define RF_CASE(NEG)                                                                                            \
+  LSURGE_LAUNCH(KID_ROUTER, s,                                                                                  \
+                hipLaunchKernelGGL(router_fused_kernel<NEG>, grid, dim3(256 * NEG), 0, s, (const bf16_t*)x,     \
+                                   (const bf16_t*)w_r, bias, (int)t, (int)d, (int)k, logits, sel, weights, hist))
+    if (e == 32) RF_CASE(1);
+    else if (e == 64) RF_CASE(2);
+    else RF_CASE(4);
+#undef RF_CASE
+    if (after_logits && hipEventRecord(after_logits, s) != hipSuccess)
+      return lsurge::set_error(LSURGE_ERR_LAUNCH, "router_topk: hipEventRecord failed");
+    return LSURGE_OK;
+  }
   if (logits && k <= 64) {  // split path: logits kernel over (token, expert) blocks, then one wave per token
     const dim3 lg((unsigned)((t + RL_TOK - 1) / RL_TOK), (unsigned)((e + RL_EXP - 1) / RL_EXP));
     LSURGE_LAUNCH(KID_ROUTER, s,
@@ -469,7 +651,7 @@ int lsurge::router_topk_impl(const void* x, const void* w_r, const float* bias, 
 #undef RS_CASE
     return LSURGE_OK;
   }
-  if (after_logits && hipEventRecord(after_logits, s) != hipSuccess)  // fused path: no separate logits kernel
+  if (after_logits && hipEventRecord(after_logits, s) != hipSuccess)  // one-kernel lane-per-token path
     return lsurge::set_error(LSURGE_ERR_LAUNCH, "router_topk: hipEventRecord failed");
   dim3 grid((unsigned)((t + RT_TOK - 1) / RT_TOK)), block(RT_THREADS);
   const bf16_t* xb = (const bf16_t*)x;

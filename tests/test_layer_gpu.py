@@ -78,6 +78,36 @@ def test_small_layer_zipf_bias(dev):
     check_layer(p, MoEShape(2048, 256, 32, 4, 128, 128), dev)
 
 
+@pytest.mark.parametrize("E,k", [(32, 4), (64, 6), (64, 8), (128, 8), (128, 1)])
+def test_fused_router_ties(E, k, dev):
+    """The layer's fused router (one workgroup per 64 tokens: logits, top-k split over several lanes per token and
+    merged, softmax, per-chunk histograms for the layout) on planted ties: duplicated router columns give identical
+    logits on every token, and all-zero tokens tie every expert.  Logits bitwise those of the C oracle, selection the
+    stable descending order (lower expert index first), weights bitwise those of the split router, layout exact."""
+    from test_router_layout_gpu import gpu_router
+    T, d, f = 8192, 256, 64
+    p = mo.make_inputs(T=T, d=d, E=E, k=k, f=f, fs=0, seed=E + k)
+    w_r = p["w_r"]
+    w_r[:, E // 2:E // 2 + 8] = w_r[:, 0:8]  # experts E/2 .. E/2 + 7 tie with 0..7
+    w_r[:, E - 1] = w_r[:, 3]
+    p["x"][:5] = 0.0
+    p["x"][100] = 0.0                            # a zero token inside the first workgroup and one further on
+    layer = MoELayer(MoEShape(T, d, E, k, f, 0), dev)
+    layer.forward(to_dev(p, dev))
+    v = {n: t.cpu().numpy() for n, t in layer.views().items() if t.dtype != torch.bfloat16}
+    logits = co.router_logits(p["x"], w_r)
+    sel = co.topk(logits, k)
+    assert np.array_equal(v["logits"], logits)
+    assert np.array_equal(v["sel"], sel)
+    assert np.array_equal(v["sel"][:5], np.tile(np.arange(k), (5, 1)))
+    _, sel_s, wts_s = gpu_router(p["x"], w_r, k, None, dev)
+    assert np.array_equal(sel_s, sel)
+    assert np.array_equal(v["weights"], wts_s)
+    lay = co.build_layout(sel, E)
+    for n in ("group_sizes", "offsets", "block_off", "order", "pos", "slot"):
+        assert np.array_equal(v[n], lay[n]), n
+
+
 def test_hot_experts_chunked_wgrad(dev):
     """Every token routes to experts 0 and 1 (a large bias), so each holds 5000 rows: the routed weight gradients
     cut them into 4096 + 904-row chunks summed from partials, and the six empty experts get zero gradients."""
