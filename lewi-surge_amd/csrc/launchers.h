@@ -46,9 +46,10 @@ int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src,
                         int64_t max_rows, void* xp, hipStream_t s);
 int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, const float* w, int64_t n,
                        const void* add, void* out, int out_dtype, hipStream_t s);
+// dlog (optional, needs sel and dl): also the dense bf16 d(logits) [n, E] of the router's weight gradient
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
                            int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s,
-                           void* gcopy = nullptr);
+                           void* gcopy = nullptr, const int32_t* sel = nullptr, void* dlog = nullptr, int E = 0);
 int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* slot, int64_t n, const float* dl,
                             const int32_t* sel, const void* w_rT, const void* add, void* dx, hipStream_t s);
 int launch_transpose_bf16(const void* a, int R, int C, void* at, hipStream_t s);

@@ -325,7 +325,7 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
 
 // Backward.  Stream plan (caller's stream = critical path):
 //   main:  combine bwd -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
-//   s0:    after combine bwd: d(logits) scatter, router wgrad (merged shared expert); with fs != f instead the
+//   s0:    after combine bwd: router wgrad (merged shared expert); with fs != f instead the
 //          shared expert's own backward: down dgrad, down wgrad, gate/up dgrad, gate/up wgrad
 //   s1:    W_r transpose; after combine bwd: chunk table, down wgrad (then the router backward when fs != f)
 // The helper chains overlap the dgrads of the main chain; the gate/up weight gradient runs after the join on its
@@ -390,10 +390,12 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   // s1: W_r^T for the router's dx term (independent of everything else)
   if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, s1)) return rc;
 
-  // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel); a merged
+  // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel) and their
+  // dense bf16 rows for the router's weight gradient; a merged
   // shared expert's rows of dY_pad get dY itself
   if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, q.P, sv.slot, sv.weights, q.T, (int)q.k, q.d, dy, w.dy_pad,
-                                              dweights, w.dl, st, q.merged ? w.dy_pad + q.P * q.d : nullptr))
+                                              dweights, w.dl, st, q.merged ? w.dy_pad + q.P * q.d : nullptr, sv.sel,
+                                              w.dlog, (int)q.E))
     return rc;
   if (int rc = lsurge::stream_after(s1, st, ev[2])) return rc;
   // s1: the chunk table of the weight gradients (read by both), then down wgrad dW_down[e] = h_e^T dY_e
@@ -412,7 +414,6 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
     sr = s0;
     if (int rc = lsurge::stream_after(s0, st, ev[3])) return rc;
   }
-  if (int rc = lsurge::launch_scatter_dlogits(w.dl, sv.sel, q.T, (int)q.E, (int)q.k, w.dlog, sr)) return rc;
   {
     const int S = dense_splits(q.T, q.d, q.E);
     if (int rc = lsurge::gemm_wgrad(KID_ROUTER_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.dlog, q.E, q.d,

@@ -382,7 +382,8 @@ __global__ __launch_bounds__(PM_THREADS) void combine_pad_kernel(const bf16_t* _
 // row y_pad[slot] is read once, dy_pad[slot] = bf16(w_j g) written once and <g, y> reduced; then the router
 // term dl[t,j] = w_j (dw_j - sum_i w_i dw_i).  moe_permute.py:303-309 does this in two passes over g and y.
 // gcopy (optional): g row t is also copied to gcopy[t] (the shared expert's rows of the padded dY, when the shared
-// expert rides along the routed experts).
+// expert rides along the routed experts).  dlog (optional, with sel): the dense bf16 row [E] of d(logits), dl[t,j] at
+// column sel[t,j] and 0 elsewhere -- the operand of the router's weight gradient.
 template <int NC, int KK>
 __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_t* __restrict__ yp,
                                                                      const int32_t* __restrict__ slot,
@@ -390,7 +391,9 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_
                                                                      int64_t d, const bf16_t* __restrict__ g,
                                                                      bf16_t* __restrict__ dyp, float* __restrict__ dw,
                                                                      float* __restrict__ dl,
-                                                                     bf16_t* __restrict__ gcopy) {
+                                                                     bf16_t* __restrict__ gcopy,
+                                                                     const int32_t* __restrict__ sel,
+                                                                     bf16_t* __restrict__ dlog, int E) {
   static_assert(NC > 0 && KK > 0, "fixed-shape kernel");
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
@@ -423,16 +426,28 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_
     }
 #pragma unroll
     for (int j = 0; j < KK; ++j) dot[j] = wave_sum(dot[j]);
+    // every lane holds the reduced dots; the router terms are computed wave-wide (the same operations in the same
+    // order on every lane)
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < KK; ++j) s += w[t * KK + j] * dot[j];
+    float dlj[KK];
+#pragma unroll
+    for (int j = 0; j < KK; ++j) dlj[j] = w[t * KK + j] * (dot[j] - s);
     if (lane == 0) {
-      float s = 0.f;
 #pragma unroll
       for (int j = 0; j < KK; ++j) {
         if (dw) dw[t * KK + j] = dot[j];
-        s += w[t * KK + j] * dot[j];
+        if (dl) dl[t * KK + j] = dlj[j];
       }
-      if (dl) {
+    }
+    if (dlog) {
+      for (int e = lane; e < E; e += 64) {
+        float v = 0.f;
 #pragma unroll
-        for (int j = 0; j < KK; ++j) dl[t * KK + j] = w[t * KK + j] * (dot[j] - s);
+        for (int j = 0; j < KK; ++j)
+          if (sel[t * KK + j] == e) v = dlj[j];
+        dlog[t * E + e] = f32_to_bf16(v);
       }
     }
   }
@@ -597,16 +612,18 @@ int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, co
 }
 
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
-                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s, void* gcopy) {
+                           int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s, void* gcopy,
+                           const int32_t* sel, void* dlog, int E) {
   const dim3 grid(grid_for_rows(n));
   const int nc = row_chunks(d);
+  LSURGE_REQUIRE(!dlog || (sel && dl && E >= 1), "combine_bwd: dense d(logits) needs sel, dl and E");
   if (nc && (k == 6 || k == 8)) {
     LS_NC_SWITCH(nc, NC, LS_KK_SWITCH(k, KK, {
       if (NC && KK)
         LSURGE_LAUNCH(KID_COMBINE_BWD, s,
                       hipLaunchKernelGGL((combine_bwd_pad_kernel<NC ? NC : 1, KK ? KK : 1>), grid, dim3(PM_THREADS), 0,
                                          s, (const bf16_t*)yp, slot, w, n, d, (const bf16_t*)g, (bf16_t*)dyp, dw, dl,
-                                         (bf16_t*)gcopy));
+                                         (bf16_t*)gcopy, sel, (bf16_t*)dlog, E));
     }));
     return LSURGE_OK;
   }
@@ -616,6 +633,7 @@ int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, co
   LSURGE_LAUNCH(KID_COMBINE_BWD, s,
                 hipLaunchKernelGGL((combine_bwd_kernel<LSURGE_BF16, LSURGE_BF16, true>), grid, dim3(PM_THREADS), 0, s,
                                    yp, rows, slot, w, n, k, d, g, dyp, dw, dl));
+  if (dlog) return launch_scatter_dlogits(dl, sel, n, E, k, dlog, s);
   return LSURGE_OK;
 }
 
