@@ -520,18 +520,19 @@ void gemm_rows_kernel(RowsArgs a) {
       else f.w[j] = frag_n(bt + (col / NS) * (BK * NS), kk, col % NS, lane);
     }
   };
-  // a wave whose rows or output columns all lie outside the tile skips its MFMAs (a one-block tile of a 256-row
-  // table, the N tail); its accumulators stay zero and are never stored
-  const bool live = wm * TM < rows && n0 + wn * (EPI == EPI_SWIGLU_FWD ? TN / 2 : TN) < N;
   auto mma = [&](const F& f) {
-    if (!live) return;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
   };
-
-  run_k_loop<Cfg, F>(nk, wave, issue, load, mma);
+  // a wave whose rows or output columns all lie outside the tile (a one-block tile of a 256-row table, the N tail)
+  // runs the loop for its copies and barriers only, without fragment reads or MFMAs; its accumulators stay zero and
+  // are never stored.  One branch per wave, so the live loop is the plain one.
+  if (wm * TM < rows && n0 + wn * (EPI == EPI_SWIGLU_FWD ? TN / 2 : TN) < N)
+    run_k_loop<Cfg, F>(nk, wave, issue, load, mma);
+  else
+    run_k_loop<Cfg, F>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
 
   // ---- epilogue, staged through LDS.  Written straight out, one store instruction would cover 16 bytes of 32
   // different rows.  Instead each wave parks one 32-row slice of its accumulators in the (now idle) ring as f32
@@ -787,15 +788,16 @@ void gemm_wgrad_kernel(WgradArgs a) {
       f.w[j] = frag_n(bt + (col / NS) * (BK * NS), kk, col % NS, lane);
     }
   };
-  const bool live = i0 + wm * TM < I && n0 + wn * TN < N;  // as in gemm_rows_kernel
   auto mma = [&](const F& f) {
-    if (!live) return;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
   };
-  if (nk > 0) run_k_loop<Cfg, F>(nk, wave, issue, load, mma);
+  if (nk > 0) {  // waves outside the tile: copies and barriers only, as in gemm_rows_kernel
+    if (i0 + wm * TM < I && n0 + wn * TN < N) run_k_loop<Cfg, F>(nk, wave, issue, load, mma);
+    else run_k_loop<Cfg, F>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
+  }
 
   // epilogue (f32), staged through LDS as in gemm_rows_kernel: acc[i][j][4q + t] is C row
   // i0 + wm*TM + 32 i + lane%32, column n0 + wn*TN + 32 j + 8 q + 4 (lane/32) + t.  Read back with TN/8 lanes
