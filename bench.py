@@ -218,13 +218,13 @@ def launch_roles(c):
 
 def label_launches(rows, c):
     """rows: dicts with Correlation_Id and Kernel_Name -> list of (role, short name, row) for the hot-path launches.
-    The forward's dense shared-expert GEMMs (launched before the router, on a helper stream) are told apart from the
-    routed ones by their workgroup count; otherwise a layer call starts at each router_logits_kernel and within it
-    the n-th launch of a template has the n-th role."""
+    The forward's dense shared-expert GEMMs (on a helper stream, 256-row tiles) are told apart from the routed ones
+    by their workgroup count; otherwise a layer call starts at each router kernel (fused, or the split path's logits
+    kernel) and within it the n-th launch of a template has the n-th role."""
     roles = launch_roles(c)
     T, d, fs = c["T"], c["d"], c["fs"]
     pad8 = lambda n: (n + 7) // 8 * 8  # noqa: E731
-    tb = (T + 127) // 128
+    tb = (T + 255) // 256
     shared_wgs = {"gemm_rows_kernel<1,1>": pad8((fs + 127) // 128 * tb), "gemm_rows_kernel<1,0>": pad8((d + 255) // 256 * tb)}
 
     def wgs(row):
@@ -235,7 +235,7 @@ def label_launches(rows, c):
     out, seen = [], {}
     for row in sorted(rows, key=lambda x: int(x["Correlation_Id"])):
         k = short_kernel(row["Kernel_Name"])
-        if k == "router_logits_kernel":
+        if k == "router_logits_kernel" or k.startswith("router_fused_kernel"):
             seen = {}
         if k not in roles:
             continue
@@ -247,6 +247,30 @@ def label_launches(rows, c):
         seen[k] = i + 1
         out.append((roles[k][i] if i < len(roles[k]) else "other", k, row))
     return out
+
+
+def stats_summary(d):
+    """Plain-text table of a rocprofv3 --stats kernel summary (*kernel_stats.csv under d): tile shapes named
+    C128 (4-wave, 128 x 256) and PP256 (ping-pong, 256 x 256), argument lists dropped."""
+    import csv
+    import glob
+    import re
+    files = glob.glob(os.path.join(d, "*kernel_stats.csv"))
+    if not files:
+        raise SystemExit(f"stats summary: no *kernel_stats.csv under {d}")
+    with open(files[0]) as fh:
+        rows = list(csv.DictReader(fh))
+    print(f"{'kernel':58s} {'calls':>6s} {'avg us':>9s} {'total ms':>9s} {'share':>7s}")
+    for r in rows:
+        n = r["Name"].replace("void ", "")
+        n = re.sub(r"\([^()]*\)$", "", n)
+        n = n.replace("lsgemm::GemmCfg<128, 256, 32, 2, 2, 3, 2, 0>", "C128")
+        n = n.replace("lsgemm::GemmCfg<256, 256, 32, 2, 4, 3, 1, 1>", "PP256")
+        n = n.replace("lsgemm::", "").replace("(anonymous namespace)::", "")
+        if "at::" in n:
+            n = "torch (synthetic inputs)"
+        print(f"{n[:58]:58s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.1f} "
+              f"{int(r['TotalDurationNs']) / 1e6:9.2f} {float(r['Percentage']):6.2f}%")
 
 
 def profile_summary(a):
@@ -316,6 +340,7 @@ def main():
     ap.add_argument("--profile-summary", metavar="DIR", help="print the markdown summary of a rocprofv3 "
                     "--kernel-trace output directory of this bench (with --pmc-fetch/--pmc-write and "
                     "--copy-fetch/--copy-write counter directories for traffic) and exit")
+    ap.add_argument("--stats-summary", metavar="DIR", help="print the kernel table of a rocprofv3 --stats run and exit")
     ap.add_argument("--pmc-fetch", metavar="DIR")
     ap.add_argument("--pmc-write", metavar="DIR")
     ap.add_argument("--copy-fetch", metavar="DIR")
@@ -330,6 +355,9 @@ def main():
               f"--gpus {a.gpus} is not supported", file=sys.stderr)
         sys.exit(2)
 
+    if a.stats_summary:
+        stats_summary(a.stats_summary)
+        return
     if a.profile_summary:
         profile_summary(a)
         return
