@@ -324,12 +324,15 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
 }
 
 // Backward.  Stream plan (caller's stream = critical path):
-//   main:  combine bwd -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
-//   s0:    after combine bwd: router wgrad (merged shared expert); with fs != f instead the
+//   main:  combine bwd -> [fork] -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up
+//          wgrad
+//   s0:    after the fork: router wgrad (merged shared expert); with fs != f instead, from the start of the call, the
 //          shared expert's own backward: down dgrad, down wgrad, gate/up dgrad, gate/up wgrad
-//   s1:    W_r transpose; after combine bwd: chunk table, down wgrad (then the router backward when fs != f)
+//   s1:    after the fork: W_r transpose, chunk table, down wgrad (then the router backward when fs != f)
 // The helper chains overlap the dgrads of the main chain; the gate/up weight gradient runs after the join on its
 // own, and the dispatch backward reads dX_pad right after the GEMM that wrote it, while it is still in cache.
+// Every event record or wait on a stream idles it for several microseconds between the kernels around it, so the
+// critical stream gets one record (the fork, shared by both helpers) and one wait (the join: s1 waits for s0 first).
 int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* dy, const void* saved,
                    const lsurge_moe_grads* g, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
   if (int rc = check_shape(s)) return rc;
@@ -365,12 +368,10 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   hipStream_t s0 = fg.f.side[0], s1 = fg.f.side[1];
   hipEvent_t* ev = fg.f.ev;
 
-  // fork: the helper streams start after everything the caller enqueued before this call
-  if (int rc = lsurge::stream_after(s0, st, ev[0])) return rc;
-  if (int rc = lsurge::stream_after(s1, st, ev[1])) return rc;
-
-  // s0: backward of a shared expert of its own width
+  // s0: backward of a shared expert of its own width, from the start of the call (after everything the caller
+  // enqueued before it)
   if (q.fs && !q.merged) {
+    if (int rc = lsurge::stream_after(s0, st, ev[0])) return rc;
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
     if (int rc = lsurge::gemm_rows_nk(KID_SHARED_DOWN_DGRAD, dense, dy, q.d, p->ws_down, nullptr, 0, q.d, 0, q.d, q.fs,
                                       w.sdgu, 2 * q.fs, true, sv.sg, sv.su, q.fs, s0))
@@ -387,9 +388,6 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                     q.d, 2 * q.fs, g->dws_gate, g->dws_up, q.fs, q.fs, 0, S, w.part, w.part_bytes, s0))
       return rc;
   }
-  // s1: W_r^T for the router's dx term (independent of everything else)
-  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, s1)) return rc;
-
   // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel) and their
   // dense bf16 rows for the router's weight gradient; a merged
   // shared expert's rows of dY_pad get dY itself
@@ -397,8 +395,16 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                               dweights, w.dl, st, q.merged ? w.dy_pad + q.P * q.d : nullptr, sv.sel,
                                               w.dlog, (int)q.E))
     return rc;
-  if (int rc = lsurge::stream_after(s1, st, ev[2])) return rc;
-  // s1: the chunk table of the weight gradients (read by both), then down wgrad dW_down[e] = h_e^T dY_e
+  // fork: the helpers start after the combine backward (and everything the caller enqueued before the call); one
+  // record on the critical stream serves both
+  if (s1 != st) {
+    if (hipEventRecord(ev[2], st) != hipSuccess || hipStreamWaitEvent(s1, ev[2], 0) != hipSuccess ||
+        (q.merged && hipStreamWaitEvent(s0, ev[2], 0) != hipSuccess))
+      return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_bwd: fork events failed");
+  }
+  // s1: W_r^T for the router's dx term, the chunk table of the weight gradients (read by both), then down wgrad
+  // dW_down[e] = h_e^T dY_e
+  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, s1)) return rc;
   lsurge::WgradChunks chunks;
   if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, s1,
                                          q.merged ? q.T : -1, q.P))
@@ -409,11 +415,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
     return rc;
   // router backward dW_r = x^T dlogits (bf16 MFMA over the dense [T, E] dlogits): on s0 beside the down wgrad when
   // s0 is free (merged shared expert), else after the down wgrad on s1
-  hipStream_t sr = s1;
-  if (q.merged) {
-    sr = s0;
-    if (int rc = lsurge::stream_after(s0, st, ev[3])) return rc;
-  }
+  hipStream_t sr = q.merged ? s0 : s1;
   {
     const int S = dense_splits(q.T, q.d, q.E);
     if (int rc = lsurge::gemm_wgrad(KID_ROUTER_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.dlog, q.E, q.d,
@@ -428,8 +430,9 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   if (int rc = lsurge::gemm_rows_nk(KID_GEMM_GU_DGRAD, blocks, w.dgu, 2 * q.f, p->w_gate, p->w_up, q.f, q.f, q.d * q.f,
                                     2 * q.f, q.d, w.dx_pad, q.d, false, nullptr, nullptr, 0, st, false, xgu))
     return rc;
-  // join all helpers, then dx = gather-reduce of dX_pad + router dx term + shared-expert dx, one rounding
-  if (int rc = lsurge::stream_after(st, s0, ev[4])) return rc;
+  // join all helpers (s1 after s0, the critical stream after s1), then dx = gather-reduce of dX_pad + router dx term
+  // + shared-expert dx, one rounding
+  if (int rc = lsurge::stream_after(s1, s0, ev[4])) return rc;
   if (int rc = lsurge::stream_after(st, s1, ev[5])) return rc;
   const bf16_t* shared_dx = q.merged ? w.dx_pad + q.P * q.d : (q.fs ? w.sdx : nullptr);
   if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT, shared_dx,
