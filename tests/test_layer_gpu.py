@@ -195,3 +195,49 @@ def test_autograd_function(dev):
     assert mo.rel_l2(out.detach().float().cpu().numpy(), want) < TOL
     assert mo.rel_l2(tp["w_gate"].grad.float().cpu().numpy(), g["dw_gate"]) < TOL
     assert mo.rel_l2(tp["x"].grad.float().cpu().numpy(), g["dx"]) < TOL
+
+
+def test_graph_capture_replays(dev):
+    """A layer step (forward + backward, helper-stream concurrency on) captured in a HIP graph: the library's
+    fork/join events join the helper streams into the capture and no memset is recorded.  Several replays, with eager
+    steps and synchronisations between them, each bitwise equal to the eager result."""
+    import _lib as L
+    c = dict(mo.CONFIGS["C2"], T=2048)
+    p = mo.make_inputs(**c)
+    shape = MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"])
+    tp = to_dev(p, dev)
+    dy = torch.from_numpy(p["dy"]).to(dev).to(torch.bfloat16)
+    lib = L.lib()
+    lib.lsurge_set_concurrency(1)
+    try:
+        layer = MoELayer(shape, dev)
+
+        def step():
+            layer.forward(tp)
+            layer.backward(tp, dy)
+
+        step()
+        torch.cuda.synchronize()
+        ref = [layer.out.clone()] + [v.clone() for v in layer.grads.values()]
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            step()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=s):
+                step()
+        torch.cuda.synchronize()
+        for _ in range(3):
+            layer.out.zero_()
+            for v in layer.grads.values():
+                v.zero_()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            got = [layer.out] + list(layer.grads.values())
+            assert all(torch.equal(a, b) for a, b in zip(got, ref))
+            step()  # eager work between replays
+            torch.cuda.synchronize()
+    finally:
+        lib.lsurge_set_concurrency(0)
