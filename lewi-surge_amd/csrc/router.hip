@@ -13,7 +13,6 @@
 // left in LDS.
 #include "launchers.h"
 
-#include <utility>
 
 namespace {
 
@@ -161,34 +160,22 @@ __global__ __launch_bounds__(RT_THREADS) void router_topk_kernel(const bf16_t* _
 // blocks x expert blocks, so there are enough waves to fill every SIMD; the d loop is the same sequential
 // f32 sum as above.  The top-k then runs as its own kernel, one wave per token, over the logits in HBM.
 //
-// Lane layout: the 16 lanes of a DPP row (lane / 16) share a token quad and hold 16 different expert pairs
-// (lane % 16).  In each block of 16 d steps, lane i of a row reads the row's four x values of step i from LDS once,
-// and step j takes them from lane j by a DPP row broadcast inside the FMA itself (v_fmac_f32 with row_newbcast:j).
-// So the x operand costs no LDS bandwidth per FMA: only the two weights of the lane's experts are read per step,
-// 144 bytes of LDS reads per 128 FMAs instead of 24 per 8.  v_fmac_f32 rounds like fmaf, so every logit is still
-// the sequential f32 sum over d.
+// Lane layout: the 16 lanes of a row (lane / 16) share a token quad and hold 16 different expert pairs (lane % 16),
+// so a row's x read is one LDS broadcast and its weight reads are 128 contiguous bytes.
 constexpr int RL_TOK = 64, RL_EXP = 32, RL_DC = 64, RL_THREADS = 256;
 
-// acc + (x of lane J of this lane's row of 16) * w, one rounding
-template <int J>
-__device__ __forceinline__ float fmac_row_bcast(float acc, float x, float w) {
-  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(x), "v"(w), "n"(J));
-  return acc;
-}
-template <int J, int WP = RL_EXP>
-__device__ __forceinline__ void logits_step(float (&acc)[4][2], const f32x4& xv, const float (*ws)[WP],
-                                            int dd, int ep) {
-  const float w0 = ws[dd + J][2 * ep], w1 = ws[dd + J][2 * ep + 1];
+// One d step of a thread's 4 tokens x 2 experts: x of the 4 tokens (one LDS read that the 16 lanes of the quad's row
+// share) and the two weights; fmaf rounds once, so each logit stays the sequential f32 sum over d.
+template <int WP>
+__device__ __forceinline__ void logits_step(float (&acc)[4][2], const float* xrow, const float (*ws)[WP], int dd,
+                                            int tq, int ep) {
+  const f32x4 xv = *reinterpret_cast<const f32x4*>(xrow + 4 * tq);
+  const float w0 = ws[dd][2 * ep], w1 = ws[dd][2 * ep + 1];
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
-    acc[a][0] = fmac_row_bcast<J>(acc[a][0], xv[a], w0);
-    acc[a][1] = fmac_row_bcast<J>(acc[a][1], xv[a], w1);
+    acc[a][0] = __builtin_fmaf(xv[a], w0, acc[a][0]);
+    acc[a][1] = __builtin_fmaf(xv[a], w1, acc[a][1]);
   }
-}
-template <int WP = RL_EXP, int... J>
-__device__ __forceinline__ void logits_block(float (&acc)[4][2], const f32x4& xv, const float (*ws)[WP], int dd,
-                                             int ep, std::integer_sequence<int, J...>) {
-  (logits_step<J, WP>(acc, xv, ws, dd, ep), ...);
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const u32x4& u, float (&v)[8]) {
@@ -202,9 +189,8 @@ __device__ __forceinline__ void unpack_bf16x8(const u32x4& u, float (&v)[8]) {
 // LDS: two buffers of (x chunk transposed to [d][token] f32, w chunk [d][expert] f32).  When d and E are multiples
 // of 8 the next chunk's global loads (raw bf16 in registers) are issued right after the barrier that publishes the
 // current chunk, so their latency hides behind the current chunk's FMAs; other shapes load each chunk in place.
-// Bank-conflict-free LDS traffic: a wave stages 64 consecutive tokens of one d row (lane = token), w goes in as
-// 16-byte stores of 4 consecutive experts, and the x rows are padded to RL_XP floats so the 16 lanes of a DPP row,
-// which read 16 consecutive d rows at the same tokens, hit 16 different groups of 4 banks.
+// Bank-conflict-free LDS traffic: a wave stages 64 consecutive tokens of one d row (lane = token) and w goes in as
+// 16-byte stores of 4 consecutive experts (the x rows keep a padded pitch of RL_XP floats).
 constexpr int RL_XP = RL_TOK + 4;
 __global__ __launch_bounds__(RL_THREADS) void router_logits_kernel(const bf16_t* __restrict__ x,
                                                                    const bf16_t* __restrict__ w,
@@ -214,8 +200,8 @@ __global__ __launch_bounds__(RL_THREADS) void router_logits_kernel(const bf16_t*
   __shared__ __attribute__((aligned(16))) float ws[2][RL_DC][RL_EXP];
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * RL_TOK, e0 = blockIdx.y * RL_EXP;
-  const int ep = tid & 15;   // experts e0 + 2 ep, e0 + 2 ep + 1 (position in the DPP row)
-  const int tq = tid >> 4;   // tokens t0 + 4 tq .. + 3 (one DPP row)
+  const int ep = tid & 15;   // experts e0 + 2 ep, e0 + 2 ep + 1 (position in the row of 16 lanes)
+  const int tq = tid >> 4;   // tokens t0 + 4 tq .. + 3 (one row of 16 lanes)
   float acc[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
   const bool vec = (d & 7) == 0 && (E & 7) == 0;
   // this thread's staging share: x token tid % 64 at d offsets 8 (tid / 64) and 8 (tid / 64 + 4) of the chunk; w d
@@ -225,21 +211,11 @@ __global__ __launch_bounds__(RL_THREADS) void router_logits_kernel(const bf16_t*
 
   auto compute = [&](int buf, int dc) {
     const float(*wsb)[RL_EXP] = ws[buf];
-    // whole blocks of 16 d steps: the x values of step dd + i come from lane i of the row (rows past dc are
-    // zero-filled, but the sum must stop at d, so a partial block takes the plain loop)
-    int dd = 0;
-    for (; dd + 16 <= dc; dd += 16) {
-      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[buf][dd + ep][4 * tq]);
-      logits_block(acc, xv, wsb, dd, ep, std::make_integer_sequence<int, 16>());
-    }
-    for (; dd < dc; ++dd) {
-      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[buf][dd][4 * tq]);
-      const float w0 = wsb[dd][2 * ep], w1 = wsb[dd][2 * ep + 1];
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        acc[a][0] = __builtin_fmaf(xv[a], w0, acc[a][0]);
-        acc[a][1] = __builtin_fmaf(xv[a], w1, acc[a][1]);
-      }
+    if (dc == RL_DC) {
+#pragma unroll 8
+      for (int dd = 0; dd < RL_DC; ++dd) logits_step<RL_EXP>(acc, xs[buf][dd], wsb, dd, tq, ep);
+    } else {
+      for (int dd = 0; dd < dc; ++dd) logits_step<RL_EXP>(acc, xs[buf][dd], wsb, dd, tq, ep);
     }
   };
 
@@ -310,9 +286,9 @@ __global__ __launch_bounds__(RL_THREADS) void router_logits_kernel(const bf16_t*
 
 // ---------------------------------------------------------------------------------------------- workgroup-fused path
 // Fused router of the layer (E = 32 NEG experts, k <= 8): one workgroup = 64 tokens x all E experts, 4 NEG waves.  Wave w covers
-// tokens 16 (w % 4) .. + 15 and experts 32 (w / 4) .. + 31 with the lane layout of router_logits_kernel (a DPP row =
-// one token quad x 16 expert pairs), the same prefetched, bank-conflict-free staging and the same sequential f32
-// sum over d, so the logits are bitwise those of the split path.  Then, in the same workgroup:
+// tokens 16 (w % 4) .. + 15 and experts 32 (w / 4) .. + 31 with the lane layout of router_logits_kernel (a row of 16
+// lanes = one token quad x 16 expert pairs), the same prefetched, bank-conflict-free staging and the same sequential
+// f32 sum over d, so the logits are bitwise those of the split path.  Then, in the same workgroup:
 //  - the logits go to HBM and to an LDS tile [64][E + 1];
 //  - top-k + softmax per token: L = 4 NEG lanes per token each keep a sorted list of their E / L = 8 experts (scanned
 //    in ascending expert order, a logit moves ahead only of strictly smaller ones), and k merge rounds take the best
@@ -338,7 +314,7 @@ __global__ __launch_bounds__(256 * NEG) void router_fused_kernel(const bf16_t* _
   static_assert(RF_TOK * (E + 1) <= 2 * RF_DC * RF_XP, "logits tile fits the x buffers");
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int t0 = blockIdx.x * RF_TOK;
-  const int tq = 4 * (wv & 3) + (lane >> 4);  // token quad (tokens t0 + 4 tq ..)
+  const int tq = 4 * (wv & 3) + (lane >> 4);    // token quad (tokens t0 + 4 tq ..)
   const int ep = 16 * (wv >> 2) + (lane & 15);  // expert pair (experts 2 ep, 2 ep + 1)
   float acc[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
   for (int e = tid; e < E; e += NT) cnt[e] = 0;
@@ -379,11 +355,8 @@ __global__ __launch_bounds__(256 * NEG) void router_fused_kernel(const bf16_t* _
     __syncthreads();
     if (d0 + RF_DC < d) gload(d0 + RF_DC);
     const float(*wsb)[E] = ws[buf];
-#pragma unroll
-    for (int dd = 0; dd < RF_DC; dd += 16) {
-      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[buf][dd + (lane & 15)][4 * tq]);
-      logits_block<E>(acc, xv, wsb, dd, ep, std::make_integer_sequence<int, 16>());
-    }
+#pragma unroll 8
+    for (int dd = 0; dd < RF_DC; ++dd) logits_step<E>(acc, xs[buf][dd], wsb, dd, tq, ep);
   }
   __syncthreads();  // every wave is done with the x buffers: they now hold the logits tile
   float* lt = &xs[0][0][0];
