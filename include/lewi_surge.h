@@ -216,6 +216,50 @@ typedef struct {
 int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_saved_views* v);
 
 /* ------------------------------------------------------------------------------------------------
+ * FP8 variant of the forward GEMMs (OCP E4M3 operands, f32 accumulation, v_mfma_f32_32x32x64_f8f6f4).
+ * Current scaling: every tensor, or every group of one (an expert's weight matrix), is quantised with its
+ * own scale = 448 / amax taken just before the cast (1 when amax = 0); values are rounded to nearest even
+ * and saturated at +-448; scale_inv = 1 / scale multiplies the GEMM's accumulator back.  This is the
+ * recipe of Transformer Engine's FP8 current scaling that the reference tries through MaxText's
+ * `quantization=te_fp8_currentscaling` (modal/te_run.py:99; TE and MaxText are third-party, and the
+ * reference's own MoE path has no FP8 entry point, so these functions replace none of its interfaces).
+ * ------------------------------------------------------------------------------------------------ */
+
+/* x: `groups` consecutive [rows, cols] bf16 matrices -> q: the same shape in E4M3 bytes, or [cols, rows]
+ * per group with transpose = 1 (rows, cols multiples of 16; untransposed: rows * cols a multiple of 16);
+ * scale_inv: [groups] f32.  x and q 16-byte aligned. */
+size_t lsurge_fp8_quantize_workspace_bytes(int64_t groups, int64_t rows, int64_t cols);
+int lsurge_fp8_quantize(const void* x, int64_t groups, int64_t rows, int64_t cols, int transpose, void* q,
+                        float* scale_inv, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
+/* lsurge_ragged_dot on FP8 operands: out[r] = (lhs_q[r] . rhs_q[e(r)]^T) * lhs_scale_inv[0] *
+ * rhs_scale_inv[e(r)] for r < sum(group_sizes), 0 after.  lhs_q: [m, kdim] E4M3; rhs_q: [e, n, kdim] E4M3
+ * (K contiguous, as lsurge_fp8_quantize with transpose = 1 makes it from [e, kdim, n]); scale_inv f32
+ * device arrays [1] and [e]; out [m, n] bf16 or f32.  kdim % 16 == 0, n % 8 == 0.  Workspace:
+ * lsurge_ragged_dot_workspace_bytes(m, e). */
+int lsurge_ragged_dot_fp8(const void* lhs_q, const float* lhs_scale_inv, const void* rhs_q,
+                          const float* rhs_scale_inv, const int32_t* group_sizes, int64_t m, int64_t kdim,
+                          int64_t n, int64_t e, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
+                          lsurge_stream_t stream);
+
+/* The layer's weights in E4M3, one buffer: gate, up [e, f, d], down [e, d, f] (K contiguous), shared gate,
+ * up [fs, d], down [d, fs], then the f32 scale_inv of gate, up, down per expert and of the three shared
+ * matrices.  Filled by lsurge_moe_fp8_quantize_weights from the bf16 weights of p (one scale per expert and
+ * matrix); a caller whose weights do not change (serving) fills it once. */
+size_t lsurge_moe_fp8_weights_bytes(const lsurge_moe_shape* s);
+size_t lsurge_moe_fp8_quantize_weights_workspace_bytes(const lsurge_moe_shape* s);
+int lsurge_moe_fp8_quantize_weights(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* wq,
+                                    size_t wq_bytes, void* workspace, size_t workspace_bytes,
+                                    lsurge_stream_t stream);
+/* lsurge_moe_fwd with every expert GEMM in FP8: x is quantised per tensor, h = silu(g) * u (bf16, kept in
+ * `saved`) per tensor (routed and shared separately) before the down projections.  Router, layout and
+ * combine are those of lsurge_moe_fwd.  `saved` has the same layout, so lsurge_moe_bwd (bf16) runs on it. */
+size_t lsurge_moe_fwd_fp8_workspace_bytes(const lsurge_moe_shape* s);
+int lsurge_moe_fwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* wq, size_t wq_bytes,
+                       void* out, void* saved, size_t saved_bytes, void* workspace, size_t workspace_bytes,
+                       lsurge_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Live per-kernel timing with HIP events on the launch stream (used by the benchmark).
  * ------------------------------------------------------------------------------------------------ */
 int lsurge_prof_enable(int on);            /* on=1: create events, start recording; 0: stop */

@@ -69,6 +69,16 @@ _SIGS = {
     "lsurge_moe_bwd": (_int, [ctypes.POINTER(MoeShape), ctypes.POINTER(MoeParams), _p, _p, ctypes.POINTER(MoeGrads),
                               _p, _sz, _p]),
     "lsurge_moe_saved_layout": (_int, [ctypes.POINTER(MoeShape), _p, ctypes.POINTER(MoeSavedViews)]),
+    "lsurge_fp8_quantize_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "lsurge_fp8_quantize": (_int, [_p, _i64, _i64, _i64, _int, _p, _p, _p, _sz, _p]),
+    "lsurge_ragged_dot_fp8": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _int, _p, _sz, _p]),
+    "lsurge_moe_fp8_weights_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
+    "lsurge_moe_fp8_quantize_weights_workspace_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
+    "lsurge_moe_fp8_quantize_weights": (_int, [ctypes.POINTER(MoeShape), ctypes.POINTER(MoeParams), _p, _sz, _p, _sz,
+                                               _p]),
+    "lsurge_moe_fwd_fp8_workspace_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
+    "lsurge_moe_fwd_fp8": (_int, [ctypes.POINTER(MoeShape), ctypes.POINTER(MoeParams), _p, _sz, _p, _p, _sz, _p, _sz,
+                                  _p]),
     "lsurge_prof_enable": (_int, [_int]),
     "lsurge_prof_collect": (_int, []),
     "lsurge_prof_kernel_count": (_int, []),

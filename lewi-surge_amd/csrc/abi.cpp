@@ -49,7 +49,8 @@ const char* g_names[KID_COUNT] = {
     "gemm_gu_fwd",      "gemm_down_fwd",     "combine_fwd",       "combine_bwd",      "gemm_down_dgrad",
     "gemm_down_wgrad",  "gemm_gu_dgrad",     "gemm_gu_wgrad",     "dispatch_bwd",     "router_wgrad",
     "shared_gu_fwd",    "shared_down_fwd",   "shared_down_dgrad", "shared_down_wgrad", "shared_gu_dgrad",
-    "shared_gu_wgrad",  "splitk_reduce",     "misc",             "router_select"};
+    "shared_gu_wgrad",  "splitk_reduce",     "misc",             "router_select",
+    "fp8_quantize"};
 constexpr size_t kPool = 8192;
 }  // namespace
 

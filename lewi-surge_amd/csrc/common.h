@@ -11,6 +11,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 #define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
 
@@ -110,6 +111,7 @@ enum {
   KID_SPLITK_REDUCE,
   KID_MISC,
   KID_ROUTER_SELECT,
+  KID_FP8_QUANT,
   KID_COUNT
 };
 

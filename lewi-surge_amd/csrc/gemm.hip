@@ -35,9 +35,9 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, int S, int 
 // Block table of an unpadded ragged layout (rows of group e start at sum_{e'<e} gs[e']), in two launches.  Group
 // sizes are clamped so that no group reaches past row m: negative sizes count as 0 and a sum above m is cut at m,
 // so a bad group_sizes array can never send the GEMMs outside lhs/out.
-// ragged_groups_kernel (one workgroup): clamped group starts and sizes and the exclusive scan of their 128-row
-// block counts, 1024 groups per pass with a running carry.
-__global__ __launch_bounds__(1024) void ragged_groups_kernel(const int32_t* __restrict__ gs, int E, int64_t m,
+// ragged_groups_kernel (one workgroup): clamped group starts and sizes and the exclusive scan of their tr-row
+// block counts (tr = 128, or 256 for the ping-pong kernel's tiles), 1024 groups per pass with a running carry.
+__global__ __launch_bounds__(1024) void ragged_groups_kernel(const int32_t* __restrict__ gs, int E, int64_t m, int tr,
                                                             int max_blocks, int32_t* __restrict__ e_row0,
                                                             int32_t* __restrict__ e_rows, int32_t* __restrict__ e_boff,
                                                             int32_t* __restrict__ num_blocks,
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(1024) void ragged_groups_kernel(const int32_t* __re
     }
     const int64_t incl = carry_rows + wb + x;
     const int64_t row0 = min(incl - g, m), rows = min(incl, m) - row0;
-    const int nb = (int)((rows + BM - 1) / BM);
+    const int nb = (int)((rows + tr - 1) / tr);
     int xb = nb;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(1024) void ragged_groups_kernel(const int32_t* __re
 // ragged_blocks_kernel (grid over the block bound): block b belongs to the group e with e_boff[e] <= b <
 // e_boff[e + 1] (binary search; empty groups have e_boff[e] == e_boff[e + 1]); entries past the count are empty.
 __global__ void ragged_blocks_kernel(const int32_t* __restrict__ e_row0, const int32_t* __restrict__ e_rows,
-                                     const int32_t* __restrict__ e_boff, int E, int max_blocks,
+                                     const int32_t* __restrict__ e_boff, int E, int tr, int max_blocks,
                                      int32_t* __restrict__ blk_row0, int32_t* __restrict__ blk_rows,
                                      int32_t* __restrict__ blk_expert) {
   const int nb = min(e_boff[E], max_blocks);
@@ -117,8 +117,8 @@ __global__ void ragged_blocks_kernel(const int32_t* __restrict__ e_row0, const i
       else hi = mid - 1;
     }
     const int j = b - e_boff[lo];
-    blk_row0[b] = e_row0[lo] + j * BM;
-    blk_rows[b] = min(BM, e_rows[lo] - j * BM);
+    blk_row0[b] = e_row0[lo] + j * tr;
+    blk_rows[b] = min(tr, e_rows[lo] - j * tr);
     blk_expert[b] = lo;
   }
 }
@@ -268,14 +268,19 @@ static int max_blocks_of(const GemmBlocks& g) {
 
 // launch gemm_rows_kernel with the tile config that matches the row tiles of g (column tiles: BN output columns, or
 // BN / 2 for the SwiGLU forward)
-template <int BMODE, int EPI>
+template <int BMODE, int EPI, bool F8 = false>
 static int launch_rows(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t s) {
   LSURGE_REQUIRE(g.tile_rows == 128 || g.tile_rows == 256, "grouped GEMM: tile_rows=%d must be 128 or 256", g.tile_rows);
   a.max_tiles = max_blocks_of(g);
   a.n_tiles = (int)((a.N + (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN) - 1) / (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN));
   if (a.max_tiles == 0) return LSURGE_OK;
   const dim3 grid(pad8((int64_t)a.n_tiles * a.max_tiles));
-  if (g.tile_rows == 256)
+  // FP8 runs on the ping-pong kernel only: the 4-wave kernel's double-buffered 32-byte fragments do not fit in the
+  // registers of two workgroups per CU
+  LSURGE_REQUIRE(!F8 || g.tile_rows == 256, "FP8 grouped GEMM: tile_rows=%d must be 256", g.tile_rows);
+  if constexpr (F8)
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<CfgPP, BMODE, EPI, F8>), grid, dim3(CfgPP::GT), 0, s, a));
+  else if (g.tile_rows == 256)
     LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<CfgPP, BMODE, EPI>), grid, dim3(CfgPP::GT), 0, s, a));
   else
     LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, BMODE, EPI>), grid, dim3(Cfg::GT), 0, s, a));
@@ -344,6 +349,39 @@ int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
   a.x_expert = xe.expert; a.Bx = (const bf16_t*)xe.B; a.B2x = (const bf16_t*)xe.B2;
   LSURGE_REQUIRE(xe.expert < 0 || (xe.B && (xe.B2 || !a.B2)), "grouped GEMM: extra expert weights missing");
   return swiglu_bwd ? launch_rows<B_NK, EPI_SWIGLU_BWD>(kid, g, a, s) : launch_rows<B_NK, EPI_STORE>(kid, g, a, s);
+}
+
+// FP8 row GEMM: C[rows, N] = (A[rows, K] @ B_e^T) * a_sinv[0] * b_sinv[e], A and B_e = [N, K] in E4M3 (K
+// contiguous, pitches lda / ldb and expert stride in bytes).  With swiglu, B2 holds the up rows (scaled by
+// b2_sinv[e]), C = h = silu(g) * u, Gs / Us (optional) receive g and u, and amax (optional) the max |h| as
+// bf16-rounded float bits (atomic max: the caller zeroes it first).  Otherwise C (bf16) or Cf (f32) is the product.
+int gemm_rows_f8(int kid, const GemmBlocks& g, const void* A, int64_t lda, const float* a_sinv, const void* B,
+                 const void* B2, int64_t ldb, int64_t b_estride, const float* b_sinv, const float* b2_sinv, int64_t K,
+                 int64_t N, void* C, int64_t ldc, bool out_f32, bool swiglu, void* Gs, void* Us, uint32_t* amax,
+                 hipStream_t s, const RowGather& gather) {
+  LSURGE_REQUIRE(K > 0 && N > 0 && K % 16 == 0 && N % 8 == 0 && lda % 16 == 0 && ldb % 16 == 0 && lda >= K && ldb >= K,
+                 "gemm_rows_f8: K=%lld (multiple of 16), N=%lld (multiple of 8), lda=%lld, ldb=%lld (multiples of 16, >= K)",
+                 (long long)K, (long long)N, (long long)lda, (long long)ldb);
+  LSURGE_REQUIRE(A && B && C && a_sinv && b_sinv && (!swiglu || (B2 && b2_sinv)), "gemm_rows_f8: null pointer");
+  LSURGE_REQUIRE(((uintptr_t)A | (uintptr_t)B | (uintptr_t)B2 | (uintptr_t)(b_estride)) % 16 == 0,
+                 "gemm_rows_f8: operands and the expert stride must be 16-byte aligned");
+  LSURGE_REQUIRE(!swiglu || !out_f32, "gemm_rows_f8: the SwiGLU epilogue writes bf16");
+  if (int rc = check_desc(std::max<int64_t>(g.tile_rows * lda, N * ldb), "gemm_rows_f8")) return rc;
+  if (gather.rows) {
+    LSURGE_REQUIRE(gather.div >= 1 && gather.nrows >= 1, "gemm_rows_f8: bad row gather");
+    if (int rc = check_desc(gather.nrows * lda, "gemm_rows_f8 gather")) return rc;
+  }
+  RowsArgs a{};
+  a.a_rows = gather.rows; a.a_nrows = gather.nrows; a.a_div = gather.div;
+  a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.B2 = (const bf16_t*)B2; a.ldb = ldb;
+  a.b_estride = b_estride; a.K = K; a.N = N; a.ldc = ldc;
+  if (out_f32) a.Cf = (float*)C;
+  else a.C = (bf16_t*)C;
+  a.G = (bf16_t*)Gs; a.U = (bf16_t*)Us; a.ldg = ldc;
+  a.t_expert = g.blk_expert; a.t_rows = g.blk_rows; a.t_row0 = g.blk_row0; a.num_tiles = g.num_blocks;
+  a.dense_rows = g.dense_rows;
+  a.a_sinv = a_sinv; a.b_sinv = b_sinv; a.b2_sinv = b2_sinv; a.amax = amax;
+  return swiglu ? launch_rows<B_NK, EPI_SWIGLU_FWD, true>(kid, g, a, s) : launch_rows<B_NK, EPI_STORE, true>(kid, g, a, s);
 }
 
 size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S) {
@@ -499,8 +537,10 @@ size_t lsurge_ragged_dot_bwd_workspace_bytes(int64_t m, int64_t kdim, int64_t n,
   return b;
 }
 
+// tile table of a ragged layout: tr = 128 (4-wave kernel) or 256 (ping-pong kernel); the bound
+// lsurge_max_blocks(m, e) on 128-row blocks covers both
 static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_t ws_bytes, hipStream_t s,
-                        lsurge::GemmBlocks* g, int32_t** total_rows, int32_t** e_row0, int32_t** e_rows) {
+                        lsurge::GemmBlocks* g, int32_t** total_rows, int32_t** e_row0, int32_t** e_rows, int tr = 128) {
   const size_t need = lsurge_ragged_dot_workspace_bytes(m, e);
   LSURGE_REQUIRE(ws && ws_bytes >= need, "ragged_dot: workspace %zu < %zu bytes", ws_bytes, need);
   LSURGE_REQUIRE(e < (1 << 30), "ragged_dot: e too large");
@@ -515,18 +555,19 @@ static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_
   *e_rows = nb + 4 + e;
   int32_t* e_boff = nb + 4 + 2 * e;
   LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(ragged_groups_kernel, dim3(1), dim3(1024), 0, s, gs, (int)e, m, (int)mb, *e_row0,
+                hipLaunchKernelGGL(ragged_groups_kernel, dim3(1), dim3(1024), 0, s, gs, (int)e, m, tr, (int)mb, *e_row0,
                                    *e_rows, e_boff, nb, *total_rows));
   const unsigned grid = (unsigned)std::min<int64_t>((mb + 255) / 256, 1024);
   LSURGE_LAUNCH(KID_MISC, s,
                 hipLaunchKernelGGL(ragged_blocks_kernel, dim3(grid), dim3(256), 0, s, *e_row0, *e_rows, e_boff, (int)e,
-                                   (int)mb, blk_row0, blk_rows, blk_expert));
+                                   tr, (int)mb, blk_row0, blk_rows, blk_expert));
   g->blk_expert = blk_expert;
   g->blk_rows = blk_rows;
   g->blk_row0 = blk_row0;
   g->num_blocks = nb;
   g->max_blocks = (int)mb;
   g->dense_rows = 0;
+  g->tile_rows = tr;
   return LSURGE_OK;
 }
 
@@ -543,6 +584,27 @@ int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_siz
   if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0, &e_rows)) return rc;
   const bool f32 = out_dtype == LSURGE_F32;
   if (int rc = lsurge::gemm_rows_kn(KID_MISC, g, lhs, kdim, rhs, n, kdim * n, kdim, n, out, n, s, f32)) return rc;
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, out, m, n, f32 ? 4 : 2, total));
+  return LSURGE_OK;
+}
+
+int lsurge_ragged_dot_fp8(const void* lhs_q, const float* lhs_scale_inv, const void* rhs_q, const float* rhs_scale_inv,
+                          const int32_t* group_sizes, int64_t m, int64_t kdim, int64_t n, int64_t e, void* out,
+                          int out_dtype, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(m >= 0 && e >= 1 && m < (1ll << 31), "ragged_dot_fp8: bad m/e");
+  LSURGE_REQUIRE(out_dtype == LSURGE_BF16 || out_dtype == LSURGE_F32, "ragged_dot_fp8: out_dtype must be bf16 or f32");
+  if (m == 0) return LSURGE_OK;
+  LSURGE_REQUIRE(lhs_q && lhs_scale_inv && rhs_q && rhs_scale_inv && group_sizes && out, "ragged_dot_fp8: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  lsurge::GemmBlocks g;
+  int32_t *total, *e_row0, *e_rows;
+  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0, &e_rows, 256))
+    return rc;
+  const bool f32 = out_dtype == LSURGE_F32;
+  if (int rc = lsurge::gemm_rows_f8(KID_MISC, g, lhs_q, kdim, lhs_scale_inv, rhs_q, nullptr, kdim, n * kdim,
+                                    rhs_scale_inv, nullptr, kdim, n, out, n, f32, false, nullptr, nullptr, nullptr, s))
+    return rc;
   LSURGE_LAUNCH(KID_MISC, s,
                 hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, out, m, n, f32 ? 4 : 2, total));
   return LSURGE_OK;

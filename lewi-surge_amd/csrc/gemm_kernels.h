@@ -23,7 +23,14 @@
 //
 // Every output element is the same ascending sequence of 16-deep MFMA steps whatever the tile shape, so all
 // shapes give bitwise identical results.
+//
+// FP8 variant of gemm_rows (template flag F8): A and B in OCP E4M3, both K-contiguous, v_mfma_f32_32x32x64_f8f6f4.
+// The operands move through the same copy and LDS machinery counted in 2-byte units, so a 32-unit stage holds 64
+// values of k, one MFMA step; the epilogue multiplies the accumulators by the dequantisation factors (per-tensor
+// for A, per expert for B and B2) before the usual epilogues.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace lsgemm {
@@ -84,6 +91,12 @@ struct RowsArgs {
   int x_expert = -1;         // tiles of this expert id read Bx / B2x instead of B / B2 (-1: none); the layer's
   const bf16_t* Bx = nullptr;   // shared expert rides along the routed ones as expert E
   const bf16_t* B2x = nullptr;
+  // FP8 (F8 kernels only; A, B and B2 point at E4M3 bytes and K, lda, ldb, b_estride count them): dequantisation
+  // factors of A (one value) and of B / B2 (one per expert)
+  const float* a_sinv = nullptr;
+  const float* b_sinv = nullptr;
+  const float* b2_sinv = nullptr;
+  uint32_t* amax = nullptr;  // SwiGLU forward: atomic max of |h| as bf16-rounded float bits (nullptr: none)
 };
 
 struct WgradArgs {
@@ -130,6 +143,14 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 p, bf16x8 q, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
 }
 
+// D[32 x 32] += P[32 x 64] Q[64 x 32] with E4M3 operands (formats 0 / 0); with zero scale operands the compiler
+// emits the unscaled v_mfma_f32_32x32x64_f8f6f4.  Lane l supplies row l%32 of P and column l%32 of Q as 32 bytes;
+// P and Q take their bytes from the same k positions, and D sums over all 64, so which k a byte slot stands for
+// never matters.  Same output layout as mfma32.
+__device__ __forceinline__ f32x16 mfma32_f8(i32x8 p, i32x8 q, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(p, q, c, 0, 0, 0, 0, 0, 0);
+}
+
 // ---------------------------------------------------------------------------------------------- LDS tiles
 // K-major tile: rows of BK k (BK/8 chunks of 16 B; 64 B rows for BK = 32, 128 B rows for BK = 64), no padding.
 // Chunk c of row r sits at slot c ^ swz(r).  A fragment read takes one chunk of 32 consecutive rows; the 16
@@ -140,6 +161,13 @@ template <int BK>
 __device__ __forceinline__ int km_swz(int row) { return BK == 32 ? (row >> 2) & 3 : (row >> 1) & 7; }
 template <int BK>
 __device__ __forceinline__ int km_off(int row, int chunk) { return row * BK + ((chunk ^ km_swz<BK>(row)) << 3); }
+
+// FP8 fragment of a 32-unit (64-byte) K-major row: lane half h takes chunks h and h + 2, 32 of the stage's 64 k
+__device__ __forceinline__ i32x8 frag_k8(const bf16_t* tile, int row, int h) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + km_off<32>(row, h));
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + km_off<32>(row, h + 2));
+  return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
 
 // N-major sub-tile: BK k-rows x 128 columns (16 chunks of 16 B, 256 B rows).  Chunk c of row k sits at slot
 // c ^ ((k & 3) << 2), which moves the 64-byte column group of 4 consecutive rows to 4 different 64-byte bank
@@ -228,28 +256,31 @@ __device__ __forceinline__ void stage_barrier() {
 //   issue(slot, kt)     enqueue the copies of stage kt into ring slot `slot`
 //   load(slot, s, F)    read the fragments of step s of the stage in `slot` into F
 //   mma(F)              the MFMAs of one step
+// One pass of the outer loop covers R = ST stages (2 ST when ST KS is odd), so that the fragment buffer a step
+// uses is fixed at compile time.
 template <int ST, int CP, int KS, class Frags, class Issue, class Load, class Mma>
 __device__ __forceinline__ void k_loop(int nk, Issue&& issue, Load&& load, Mma&& mma) {
-  static_assert(KS % 2 == 0, "fragment double buffer parity");
+  constexpr int R = (ST * KS) % 2 ? 2 * ST : ST;
 #pragma unroll
   for (int s = 0; s < ST; ++s) issue(s, s);
   stage_barrier<(ST - 1) * CP>();
   Frags f0, f1;
   load(0, 0, f0);
-  for (int kt0 = 0;; kt0 += ST) {
+  for (int kt0 = 0;; kt0 += R) {
     bool done = false;
 #pragma unroll
-    for (int j = 0; j < ST; ++j) {
+    for (int j = 0; j < R; ++j) {
       if (!done) {
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-          Frags& cur = (s & 1) ? f1 : f0;
-          Frags& nxt = (s & 1) ? f0 : f1;
+          const int step = j * KS + s;
+          Frags& cur = (step & 1) ? f1 : f0;
+          Frags& nxt = (step & 1) ? f0 : f1;
           if (s + 1 < KS) {
-            load(j, s + 1, nxt);
+            load(j % ST, s + 1, nxt);
           } else {
             stage_barrier<(ST - 2) * CP>();
-            issue(j, kt0 + j + ST);
+            issue(j % ST, kt0 + j + ST);
             load((j + 1) % ST, 0, nxt);
           }
           // keep the reads of the next step ahead of this step's MFMAs (the scheduler would otherwise sink
@@ -323,10 +354,11 @@ __device__ __forceinline__ void k_loop_pp(int nk, int grp, Issue&& issue, Load&&
   __builtin_amdgcn_s_waitcnt(0);  // the copies of the zero stages past the end land before the epilogue
 }
 
-template <class Cfg, class Frags, class Issue, class Load, class Mma>
+// KS: MFMA steps per stage (BK / 16 for bf16, 1 for an FP8 stage of 64 values)
+template <class Cfg, class Frags, int KS = Cfg::BK / 16, class Issue, class Load, class Mma>
 __device__ __forceinline__ void run_k_loop(int nk, int wave, Issue&& issue, Load&& load, Mma&& mma) {
-  if constexpr (Cfg::PP) k_loop_pp<Cfg::ST, Cfg::CP, Cfg::BK / 16, Frags>(nk, wave >> 2, issue, load, mma);
-  else k_loop<Cfg::ST, Cfg::CP, Cfg::BK / 16, Frags>(nk, issue, load, mma);
+  if constexpr (Cfg::PP) k_loop_pp<Cfg::ST, Cfg::CP, KS, Frags>(nk, wave >> 2, issue, load, mma);
+  else k_loop<Cfg::ST, Cfg::CP, KS, Frags>(nk, issue, load, mma);
 }
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -360,15 +392,17 @@ __device__ __forceinline__ void park(float* stg, const f32x16 (&acc)[Cfg::FM][Cf
           f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
 }
 
-template <int FM, int FN>
+template <int FM, int FN, class FT = bf16x8>
 struct FragSet {
-  bf16x8 x[FM], w[FN];
+  FT x[FM], w[FN];
 };
 
 // =====================================================================================================
-template <class Cfg, int BMODE, int EPI>
+template <class Cfg, int BMODE, int EPI, bool F8 = false>
 __global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW * Cfg::OCC / 4)))
 void gemm_rows_kernel(RowsArgs a) {
+  static_assert(!F8 || (BMODE == B_NK && Cfg::BK == 32), "FP8: both operands K-contiguous, 64-value stages");
+  constexpr int UE = F8 ? 2 : 1;  // operand elements per 2-byte copy unit
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, ST = Cfg::ST;
   constexpr int TM = Cfg::TM, TN = Cfg::TN, FM = Cfg::FM, FN = Cfg::FN, SP = Cfg::SP;
   constexpr int CPA = Cfg::CPA, CPB = Cfg::CPB;
@@ -415,15 +449,17 @@ void gemm_rows_kernel(RowsArgs a) {
   // column origin of this tile: weight columns for B, output columns for C (SwiGLU: gate and up halves)
   const int64_t n0 = (int64_t)nt * (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN);
   const bool xe = expert == a.x_expert;
-  const bf16_t* Bbase = xe ? a.Bx : a.B + (int64_t)expert * a.b_estride;
-  const bf16_t* B2base = xe ? (a.B2x ? a.B2x : Bbase) : (a.B2 ? a.B2 + (int64_t)expert * a.b_estride : Bbase);
-  const int K = (int)a.K, N = (int)a.N, lda = (int)a.lda, ldb = (int)a.ldb, ksplit = (int)a.k_split;
+  // K, pitches and expert stride in 2-byte units (FP8: pairs of values)
+  const int64_t lda64 = a.lda / UE, ldb64 = a.ldb / UE, bes = a.b_estride / UE;
+  const bf16_t* Bbase = xe ? a.Bx : a.B + (int64_t)expert * bes;
+  const bf16_t* B2base = xe ? (a.B2x ? a.B2x : Bbase) : (a.B2 ? a.B2 + (int64_t)expert * bes : Bbase);
+  const int K = (int)(a.K / UE), N = (int)a.N, lda = (int)lda64, ldb = (int)ldb64, ksplit = (int)(a.k_split / UE);
   const int nk = (K + BK - 1) / BK;
   const uint32_t lds0 = lds_addr(smem);
 
   // descriptors: this tile's rows of A; the expert's B (and B2) matrix
-  const u32x4 rsA = a.a_rows ? make_rsrc(a.A, a.a_nrows * a.lda * 2) : make_rsrc(a.A + row0 * a.lda, (int64_t)rows * a.lda * 2);
-  const int64_t b_bytes = (int64_t)(BMODE == B_NK ? N : K) * a.ldb * 2;
+  const u32x4 rsA = a.a_rows ? make_rsrc(a.A, a.a_nrows * lda64 * 2) : make_rsrc(a.A + row0 * lda64, (int64_t)rows * lda64 * 2);
+  const int64_t b_bytes = (int64_t)(BMODE == B_NK ? N : K) * ldb64 * 2;
   const u32x4 rsB = make_rsrc(Bbase, b_bytes);
   const u32x4 rsB2 = make_rsrc(B2base, b_bytes);
 
@@ -446,8 +482,9 @@ void gemm_rows_kernel(RowsArgs a) {
       a_k[c] = r < rows ? 8 * kc : KBIG;
     }
   }
-  // B K-major: as A over n.  B N-major: copy q fills k rows 4 (q % CPS) + lane / 16 of sub-tile q / CPS, slot
-  // lane % 16 (SwiGLU forward: sub-tiles [0, NSUB/2) gate, [NSUB/2, NSUB) up, same output columns).
+  // B K-major: as A over n (SwiGLU forward: tile columns [0, BN/2) gate rows, [BN/2, BN) up rows, same output
+  // columns).  B N-major: copy q fills k rows 4 (q % CPS) + lane / 16 of sub-tile q / CPS, slot lane % 16
+  // (SwiGLU forward: sub-tiles [0, NSUB/2) gate, [NSUB/2, NSUB) up).
   uint32_t b_off[CPB];
   int b_k[CPB];
 #pragma unroll
@@ -456,7 +493,7 @@ void gemm_rows_kernel(RowsArgs a) {
     if (BMODE == B_NK) {
       const int n = RPC * q + lane / CPR;
       const int kc = (lane % CPR) ^ km_swz<BK>(n);
-      const int64_t gn = n0 + n;
+      const int64_t gn = n0 + (EPI == EPI_SWIGLU_FWD ? n % (BN / 2) : n);
       b_off[c] = (uint32_t)(gn * ldb + 8 * kc) * 2u;
       b_k[c] = gn < N ? 8 * kc : KBIG;
     } else {
@@ -478,10 +515,12 @@ void gemm_rows_kernel(RowsArgs a) {
     if (BMODE == B_NK) {
       const bool second = ksplit && k0 >= ksplit;  // k range of B2 (gate/up dgrad); uniform
       const int kb = second ? k0 - ksplit : k0;
-      const u32x4 rs = second ? rsB2 : rsB;
 #pragma unroll
-      for (int c = 0; c < CPB; ++c)
+      for (int c = 0; c < CPB; ++c) {
+        // SwiGLU forward: the copy's rows are all gate or all up (RPC divides BN / 2); wave-uniform
+        const u32x4 rs = EPI == EPI_SWIGLU_FWD ? (RPC * (CPB * wave + c) >= BN / 2 ? rsB2 : rsB) : (second ? rsB2 : rsB);
         copy16(rs, k0 + b_k[c] < K ? b_off[c] + 2u * kb : OOB, bt + 1024 * (CPB * wave + c));
+      }
     } else {
       const uint32_t kstep = 2u * (uint32_t)k0 * (uint32_t)ldb;
 #pragma unroll
@@ -506,33 +545,53 @@ void gemm_rows_kernel(RowsArgs a) {
       return (j < FN / 2 ? 0 : BN / 2) + wn * (TN / 2) + 32 * (j < FN / 2 ? j : j - FN / 2);
     return wn * TN + 32 * j;
   };
-  typedef FragSet<FM, FN> F;
+  typedef FragSet<FM, FN, typename std::conditional<F8, i32x8, bf16x8>::type> F;
+  constexpr int KS = F8 ? 1 : BK / 16;
   auto load = [&](int slot, int s, F& f) {
     const bf16_t* at = smem + slot * Cfg::A_EL;
     const bf16_t* bt = smem + ST * Cfg::A_EL + slot * Cfg::B_EL;
-    const int kk = 16 * s;
+    if constexpr (F8) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) f.x[i] = frag_k<BK>(at, wm * TM + 32 * i + (lane & 31), kk / 8 + (lane >> 5));
+      for (int i = 0; i < FM; ++i) f.x[i] = frag_k8(at, wm * TM + 32 * i + (lane & 31), lane >> 5);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int col = bcol(j);
-      if (BMODE == B_NK) f.w[j] = frag_k<BK>(bt, col + (lane & 31), kk / 8 + (lane >> 5));
-      else f.w[j] = frag_n(bt + (col / NS) * (BK * NS), kk, col % NS, lane);
+      for (int j = 0; j < FN; ++j) f.w[j] = frag_k8(bt, bcol(j) + (lane & 31), lane >> 5);
+    } else {
+      const int kk = 16 * s;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) f.x[i] = frag_k<BK>(at, wm * TM + 32 * i + (lane & 31), kk / 8 + (lane >> 5));
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int col = bcol(j);
+        if (BMODE == B_NK) f.w[j] = frag_k<BK>(bt, col + (lane & 31), kk / 8 + (lane >> 5));
+        else f.w[j] = frag_n(bt + (col / NS) * (BK * NS), kk, col % NS, lane);
+      }
     }
   };
   auto mma = [&](const F& f) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (F8) acc[i][j] = mfma32_f8(f.w[j], f.x[i], acc[i][j]);
+        else acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
+      }
   };
   // a wave whose rows or output columns all lie outside the tile (a one-block tile of a 256-row table, the N tail)
   // runs the loop for its copies and barriers only, without fragment reads or MFMAs; its accumulators stay zero and
   // are never stored.  One branch per wave, so the live loop is the plain one.
   if (wm * TM < rows && n0 + wn * (EPI == EPI_SWIGLU_FWD ? TN / 2 : TN) < N)
-    run_k_loop<Cfg, F>(nk, wave, issue, load, mma);
+    run_k_loop<Cfg, F, KS>(nk, wave, issue, load, mma);
   else
-    run_k_loop<Cfg, F>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
+    run_k_loop<Cfg, F, KS>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
+  if constexpr (F8) {  // dequantise: gate (or plain) columns by a_sinv * b_sinv[e], up columns by a_sinv * b2_sinv[e]
+    const float sa = a.a_sinv[0];
+    const float s1 = sa * a.b_sinv[expert];
+    const float s2 = a.b2_sinv ? sa * a.b2_sinv[expert] : s1;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] *= (EPI == EPI_SWIGLU_FWD && j >= FN / 2) ? s2 : s1;
+  }
 
   // ---- epilogue, staged through LDS.  Written straight out, one store instruction would cover 16 bytes of 32
   // different rows.  Instead each wave parks one 32-row slice of its accumulators in the (now idle) ring as f32
@@ -542,6 +601,7 @@ void gemm_rows_kernel(RowsArgs a) {
   float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * SP);
   constexpr int LPR = TN / 8, RPP = 64 / LPR, PASSES = 32 / RPP;          // store mapping
   constexpr int LPR2 = TN / 16, RPP2 = 64 / LPR2, PASSES2 = 32 / RPP2;    // SwiGLU forward: TN / 2 outputs
+  [[maybe_unused]] float hmax = 0.f;  // SwiGLU forward with a.amax: max |h| over this lane's outputs
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int mbase = wm * TM + 32 * i;  // first tile row of this slice
@@ -575,7 +635,10 @@ void gemm_rows_kernel(RowsArgs a) {
         const float u[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
         float h[8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) h[t] = silu_f(g[t]) * u[t];
+        for (int t = 0; t < 8; ++t) {
+          h[t] = silu_f(g[t]) * u[t];
+          hmax = fmaxf(hmax, fabsf(h[t]));
+        }
         const int64_t gr = row0 + mbase + r;
         st_bf16x8(a.C + gr * a.ldc + col, h);
         if (a.G) st_bf16x8(a.G + gr * a.ldg + col, g);
@@ -615,6 +678,13 @@ void gemm_rows_kernel(RowsArgs a) {
         }
       }
     }
+  }
+  if (EPI == EPI_SWIGLU_FWD && a.amax) {
+    // max |bf16(h)| = bf16(max |h|) (rounding is monotonic); non-negative floats order like their bit patterns,
+    // so an unsigned max over the bits is the float max, whatever order the waves arrive in
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) hmax = fmaxf(hmax, __shfl_xor(hmax, o, 64));
+    if (lane == 0) atomicMax(a.amax, (uint32_t)f32_to_bf16(hmax) << 16);
   }
 }
 

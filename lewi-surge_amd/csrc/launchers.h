@@ -92,6 +92,11 @@ int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
                  int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
                  bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false,
                  const ExtraExpert& xe = ExtraExpert());
+// FP8 (E4M3) row GEMM, both operands K-contiguous (B_e stored [N, K]); byte pitches; see gemm.hip
+int gemm_rows_f8(int kid, const GemmBlocks& g, const void* A, int64_t lda, const float* a_sinv, const void* B,
+                 const void* B2, int64_t ldb, int64_t b_estride, const float* b_sinv, const float* b2_sinv, int64_t K,
+                 int64_t N, void* C, int64_t ldc, bool out_f32, bool swiglu, void* Gs, void* Us, uint32_t* amax,
+                 hipStream_t s, const RowGather& gather = RowGather());
 size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S);
 int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
                int64_t max_rows, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N,
@@ -128,5 +133,16 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
                        const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
                        int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s,
                        const RowGather& gather = RowGather(), const ExtraOut& xo = ExtraOut());
+
+// ---- FP8 quantisation (fp8.hip), current scaling to OCP E4M3
+size_t fp8_partial_bytes(int64_t groups);  // amax partials of fp8_quantize_impl
+// groups of [rows, cols] bf16 -> q (transpose: [cols, rows] per group), sinv[g] = 1 / scale; zero[0 .. nzero) is
+// cleared by the cast kernel (untransposed only), for slots a later kernel fills by atomic max
+int fp8_quantize_impl(const void* x, int64_t groups, int64_t rows, int64_t cols, bool transpose, void* q, float* sinv,
+                      float* partial, hipStream_t s, uint32_t* zero = nullptr, int nzero = 0);
+// cast of n bf16 values with the amax in *amax_bits (float bits); nrows (optional): only the first
+// nrows[0] * row_elems values
+int fp8_cast_with_amax(const void* x, int64_t n, const uint32_t* amax_bits, void* q, float* sinv,
+                       const int32_t* nrows, int64_t row_elems, hipStream_t s);
 
 }  // namespace lsurge

@@ -166,6 +166,46 @@ size_t router_hist_bytes(const lsurge_moe_shape* s) {
   return ((size_t)((s->t + 63) / 64) * (size_t)s->e * sizeof(int32_t) + 255) / 256 * 256;
 }
 
+// FP8 weights (one caller buffer): E4M3 gate, up [E, f, d], down [E, d, f], shared gate, up [fs, d], down [d, fs]
+// (all K-contiguous), then the scale_inv of gate, up, down [E] each and of the three shared matrices.
+struct Fp8W {
+  uint8_t *q_gate, *q_up, *q_down, *qs_gate, *qs_up, *qs_down;
+  float *s_gate, *s_up, *s_down, *s_shared;
+};
+size_t carve_fp8w(const Dims& q, void* base, Fp8W* w) {
+  Carve c(base);
+  w->q_gate = c.take<uint8_t>(q.E * q.f * q.d);
+  w->q_up = c.take<uint8_t>(q.E * q.f * q.d);
+  w->q_down = c.take<uint8_t>(q.E * q.d * q.f);
+  w->qs_gate = c.take<uint8_t>(q.fs * q.d);
+  w->qs_up = c.take<uint8_t>(q.fs * q.d);
+  w->qs_down = c.take<uint8_t>(q.d * q.fs);
+  w->s_gate = c.take<float>(q.E);
+  w->s_up = c.take<float>(q.E);
+  w->s_down = c.take<float>(q.E);
+  w->s_shared = c.take<float>(3);
+  return c.off + 256;
+}
+
+// FP8 forward scratch: x and the two h tensors in E4M3, x's amax partials, the atomic-max slots of the routed and
+// shared h, and the scale_inv of x, routed h and shared h
+struct Fp8Ws {
+  uint8_t *xq, *hq, *shq;
+  float* partial;
+  uint32_t* slots;
+  float* sinv;
+};
+size_t carve_fp8ws(const Dims& q, void* base, Fp8Ws* w) {
+  Carve c(base);
+  w->xq = c.take<uint8_t>(q.T * q.d);
+  w->hq = c.take<uint8_t>(q.P * q.f);
+  w->shq = c.take<uint8_t>(q.fs ? q.T * q.fs : 0);
+  w->partial = c.take<float>(lsurge::fp8_partial_bytes(1) / sizeof(float));
+  w->slots = c.take<uint32_t>(2);
+  w->sinv = c.take<float>(4);
+  return c.off;
+}
+
 int check_shape(const lsurge_moe_shape* s) {
   LSURGE_REQUIRE(s, "moe: null shape");
   LSURGE_REQUIRE(s->t >= 1 && s->d >= 8 && s->e >= 1 && s->e <= 256 && s->k >= 1 && s->k <= s->e && s->k <= 16 &&
@@ -194,6 +234,50 @@ size_t lsurge_moe_saved_bytes(const lsurge_moe_shape* s) {
 size_t lsurge_moe_fwd_workspace_bytes(const lsurge_moe_shape* s) {
   if (check_shape(s)) return 0;
   return router_hist_bytes(s) + lsurge_layout_workspace_bytes(s->t * s->k, s->e) + 256;
+}
+
+size_t lsurge_moe_fwd_fp8_workspace_bytes(const lsurge_moe_shape* s) {
+  if (check_shape(s)) return 0;
+  Fp8Ws w;
+  const size_t f8 = (carve_fp8ws(dims_of(s), nullptr, &w) + 255) / 256 * 256;
+  return router_hist_bytes(s) + f8 + lsurge_layout_workspace_bytes(s->t * s->k, s->e) + 256;
+}
+
+size_t lsurge_moe_fp8_weights_bytes(const lsurge_moe_shape* s) {
+  if (check_shape(s)) return 0;
+  Fp8W w;
+  return carve_fp8w(dims_of(s), nullptr, &w);
+}
+
+size_t lsurge_moe_fp8_quantize_weights_workspace_bytes(const lsurge_moe_shape* s) {
+  if (check_shape(s)) return 0;
+  return lsurge::fp8_partial_bytes(s->e);
+}
+
+// one scale per expert and matrix; each weight is transposed into the K-contiguous operand of the FP8 GEMM
+int lsurge_moe_fp8_quantize_weights(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* wq, size_t wq_bytes,
+                                    void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+  if (int rc = check_shape(s)) return rc;
+  LSURGE_REQUIRE(p && p->w_gate && p->w_up && p->w_down && wq && workspace, "moe_fp8_quantize_weights: null pointer");
+  LSURGE_REQUIRE(!s->fs || (p->ws_gate && p->ws_up && p->ws_down), "moe_fp8_quantize_weights: shared expert weights missing");
+  const Dims q = dims_of(s);
+  Fp8W w;
+  LSURGE_REQUIRE(wq_bytes >= carve_fp8w(q, nullptr, &w), "moe_fp8_quantize_weights: weight buffer %zu < %zu bytes",
+                 wq_bytes, carve_fp8w(q, nullptr, &w));
+  LSURGE_REQUIRE(workspace_bytes >= lsurge::fp8_partial_bytes(q.E), "moe_fp8_quantize_weights: workspace too small");
+  carve_fp8w(q, wq, &w);
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  if (int rc = lsurge::fp8_quantize_impl(p->w_gate, q.E, q.d, q.f, true, w.q_gate, w.s_gate, part, st)) return rc;
+  if (int rc = lsurge::fp8_quantize_impl(p->w_up, q.E, q.d, q.f, true, w.q_up, w.s_up, part, st)) return rc;
+  if (int rc = lsurge::fp8_quantize_impl(p->w_down, q.E, q.f, q.d, true, w.q_down, w.s_down, part, st)) return rc;
+  if (q.fs) {
+    if (int rc = lsurge::fp8_quantize_impl(p->ws_gate, 1, q.d, q.fs, true, w.qs_gate, w.s_shared, part, st)) return rc;
+    if (int rc = lsurge::fp8_quantize_impl(p->ws_up, 1, q.d, q.fs, true, w.qs_up, w.s_shared + 1, part, st)) return rc;
+    if (int rc = lsurge::fp8_quantize_impl(p->ws_down, 1, q.fs, q.d, true, w.qs_down, w.s_shared + 2, part, st))
+      return rc;
+  }
+  return LSURGE_OK;
 }
 
 size_t lsurge_moe_bwd_workspace_bytes(const lsurge_moe_shape* s) {
@@ -241,8 +325,11 @@ extern "C" {
 // The dispatch into padded expert blocks is fused into the gate/up GEMM: its A tiles are gathered straight from
 // the token rows x through row_src (padded row -> flat slot t*k + j), so the padded copy of x is never
 // materialised (the backward's gate/up weight gradient gathers the same way).
-int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* out, void* saved, size_t saved_bytes,
-                   void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+// FP8 (w8 set): x is quantised first (its cast kernel also clears the h amax slots); the expert GEMMs run on E4M3
+// operands on the ping-pong kernel over 256-row tiles, the gate/up epilogues take the amax of h, and h is cast
+// before each down projection.
+static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, const Fp8W* w8, void* out, void* saved,
+                        size_t saved_bytes, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
   if (int rc = check_shape(s)) return rc;
   LSURGE_REQUIRE(p && p->x && p->w_r && p->w_gate && p->w_up && p->w_down && out && saved, "moe_fwd: null pointer");
   LSURGE_REQUIRE(!s->fs || (p->ws_gate && p->ws_up && p->ws_down), "moe_fwd: shared expert weights missing");
@@ -260,8 +347,16 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   // (logits, top-k, softmax and the layout's per-64-token histograms), after which s0 forks
   // (serial mode: the helpers are the caller's stream and have no events)
   const size_t hist_bytes = router_hist_bytes(s);
-  LSURGE_REQUIRE(workspace && workspace_bytes >= hist_bytes, "moe_fwd: workspace %zu bytes too small", workspace_bytes);
+  Fp8Ws f8{};
+  const size_t f8_bytes = w8 ? (carve_fp8ws(q, nullptr, &f8) + 255) / 256 * 256 : 0;
+  LSURGE_REQUIRE(workspace && workspace_bytes >= hist_bytes + f8_bytes, "moe_fwd: workspace %zu bytes too small",
+                 workspace_bytes);
   int32_t* rhist = hist_bytes ? (int32_t*)workspace : nullptr;
+  if (w8) {
+    carve_fp8ws(q, (char*)workspace + hist_bytes, &f8);
+    if (int rc = lsurge::fp8_quantize_impl(p->x, 1, q.T, q.d, false, f8.xq, f8.sinv, f8.partial, st, f8.slots, 2))
+      return rc;
+  }
   if (int rc = lsurge::router_topk_impl(p->x, p->w_r, p->bias, q.T, q.d, q.E, q.k, sv.logits, sv.sel, sv.weights, st,
                                         s0 != st ? fg.f.ev[0] : nullptr, rhist))
     return rc;
@@ -278,7 +373,19 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   }
   if (s0 != st && hipStreamWaitEvent(s0, fg.f.ev[0], 0) != hipSuccess)
     return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipStreamWaitEvent failed");
-  if (q.fs) {
+  if (q.fs && w8) {
+    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
+    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_GU_FWD, dense, f8.xq, q.d, f8.sinv, w8->qs_gate, w8->qs_up, q.d, 0,
+                                      w8->s_shared, w8->s_shared + 1, q.d, q.fs, sh, q.fs, false, true, sg, su,
+                                      f8.slots + 1, s0))
+      return rc;
+    if (int rc = lsurge::fp8_cast_with_amax(sh, q.T * q.fs, f8.slots + 1, f8.shq, f8.sinv + 2, nullptr, 0, s0))
+      return rc;
+    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_DOWN_FWD, dense, f8.shq, q.fs, f8.sinv + 2, w8->qs_down, nullptr, q.fs,
+                                      0, w8->s_shared + 2, nullptr, q.fs, q.d, sy, q.d, false, false, nullptr, nullptr,
+                                      nullptr, s0))
+      return rc;
+  } else if (q.fs) {
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
     if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
                                               q.fs, sh, sg, su, q.fs, s0))
@@ -303,8 +410,8 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   chunks.waves = (int)q.k;
   if (int rc = lsurge::build_layout_impl(sv.sel, q.M, q.E, sv.gs, sv.offsets, sv.block_off, sv.order, sv.pos, sv.slot,
                                          sv.row_src, sv.blk_expert, sv.blk_rows, sv.num_blocks,
-                                         (char*)workspace + hist_bytes, workspace_bytes - hist_bytes, st, tiles,
-                                         chunks))
+                                         (char*)workspace + hist_bytes + f8_bytes,
+                                         workspace_bytes - hist_bytes - f8_bytes, st, tiles, chunks))
     return rc;
   // the routed forward GEMMs run 128-row blocks on the 4-wave kernel (the ping-pong kernel measured no faster here)
   const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
@@ -312,6 +419,23 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   gather.rows = sv.row_src;
   gather.div = (int)q.k;
   gather.nrows = q.T;
+  if (w8) {
+    // 256-row tiles of the layout's table (routed ones: num_tiles[0]); h is cast over the rows of real blocks
+    const lsurge::GemmBlocks tiles256{sv.t_expert, sv.t_rows, sv.t_row0, sv.num_tiles, (int)q.TB, 0, 256};
+    if (int rc = lsurge::gemm_rows_f8(KID_GEMM_GU_FWD, tiles256, f8.xq, q.d, f8.sinv, w8->q_gate, w8->q_up, q.d,
+                                      q.f * q.d, w8->s_gate, w8->s_up, q.d, q.f, sv.h, q.f, false, true, sv.g, sv.u,
+                                      f8.slots, st, gather))
+      return rc;
+    if (int rc = lsurge::fp8_cast_with_amax(sv.h, q.P * q.f, f8.slots, f8.hq, f8.sinv + 1, sv.num_blocks, BLK * q.f, st))
+      return rc;
+    if (int rc = lsurge::gemm_rows_f8(KID_GEMM_DOWN_FWD, tiles256, f8.hq, q.f, f8.sinv + 1, w8->q_down, nullptr, q.f,
+                                      q.d * q.f, w8->s_down, nullptr, q.f, q.d, sv.y_pad, q.d, false, false, nullptr,
+                                      nullptr, nullptr, st))
+      return rc;
+    if (int rc = lsurge::stream_after(st, s0, fg.f.ev[1])) return rc;
+    return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sy : nullptr, out,
+                                      LSURGE_BF16, st);
+  }
   if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_GEMM_GU_FWD, blocks, p->x, q.d, p->w_gate, p->w_up, q.f, q.d * q.f,
                                             q.d, q.f, sv.h, sv.g, sv.u, q.f, st, gather))
     return rc;
@@ -321,6 +445,24 @@ int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* 
   if (int rc = lsurge::stream_after(st, s0, fg.f.ev[1])) return rc;
   return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sy : nullptr, out,
                                     LSURGE_BF16, st);
+}
+
+int lsurge_moe_fwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* out, void* saved, size_t saved_bytes,
+                   void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+  return moe_fwd_impl(s, p, nullptr, out, saved, saved_bytes, workspace, workspace_bytes, stream);
+}
+
+int lsurge_moe_fwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* wq, size_t wq_bytes, void* out,
+                       void* saved, size_t saved_bytes, void* workspace, size_t workspace_bytes,
+                       lsurge_stream_t stream) {
+  if (int rc = check_shape(s)) return rc;
+  LSURGE_REQUIRE(wq, "moe_fwd_fp8: null weight buffer");
+  const Dims q = dims_of(s);
+  Fp8W w;
+  LSURGE_REQUIRE(wq_bytes >= carve_fp8w(q, nullptr, &w), "moe_fwd_fp8: weight buffer %zu < %zu bytes", wq_bytes,
+                 carve_fp8w(q, nullptr, &w));
+  carve_fp8w(q, (void*)wq, &w);
+  return moe_fwd_impl(s, p, &w, out, saved, saved_bytes, workspace, workspace_bytes, stream);
 }
 
 // Backward.  Stream plan (caller's stream = critical path):

@@ -94,6 +94,40 @@ class MoELayer:
                                        L.stream(self.device)), "moe_fwd")
         return out
 
+    # -- FP8 forward (E4M3 expert GEMMs, current scaling) ------------------------------------------------------
+    def quantize_weights_fp8(self, p: dict):
+        """Quantise the expert and shared weights of p into this layer's FP8 weight buffer (one scale per expert
+        and matrix).  Call again whenever the weights change."""
+        _check_params(self.shape, p)
+        lib = L.lib()
+        if getattr(self, "wq", None) is None:
+            self.wq = torch.empty(lib.lsurge_moe_fp8_weights_bytes(ctypes.byref(self._cs)), dtype=torch.uint8,
+                                  device=self.device)
+            self._wq_ws = L.workspace(lib.lsurge_moe_fp8_quantize_weights_workspace_bytes(ctypes.byref(self._cs)),
+                                      self.device)
+        ps = _params_struct(p)
+        L.check(lib.lsurge_moe_fp8_quantize_weights(ctypes.byref(self._cs), ctypes.byref(ps), L.ptr(self.wq),
+                                                    self.wq.numel(), L.ptr(self._wq_ws), self._wq_ws.numel(),
+                                                    L.stream(self.device)), "moe_fp8_quantize_weights")
+        return self.wq
+
+    def forward_fp8(self, p: dict, out=None):
+        """forward() with the expert GEMMs in FP8 on the weights of the last quantize_weights_fp8(); the saved
+        activations have the same layout, so backward() (bf16) runs after it."""
+        s = self.shape
+        _check_params(s, p)
+        if getattr(self, "wq", None) is None:
+            raise RuntimeError("moe_layer: call quantize_weights_fp8() before forward_fp8()")
+        lib = L.lib()
+        if getattr(self, "_fwd8_ws", None) is None:
+            self._fwd8_ws = L.workspace(lib.lsurge_moe_fwd_fp8_workspace_bytes(ctypes.byref(self._cs)), self.device)
+        out = self.out if out is None else out
+        ps = _params_struct(p)
+        L.check(lib.lsurge_moe_fwd_fp8(ctypes.byref(self._cs), ctypes.byref(ps), L.ptr(self.wq), self.wq.numel(),
+                                       L.ptr(out), L.ptr(self.saved), self.saved.numel(), L.ptr(self._fwd8_ws),
+                                       self._fwd8_ws.numel(), L.stream(self.device)), "moe_fwd_fp8")
+        return out
+
     def alloc_grads(self):
         s = self.shape
         z = lambda *shape: torch.empty(shape, dtype=torch.float32, device=self.device)  # noqa: E731

@@ -456,6 +456,158 @@ def moe_layer_bwd(p, cache, dy, dtype=np.float64):
     return out
 
 
+# --------------------------------------------------------------------------------------------- FP8 variant
+#
+# FP8 forward GEMMs with current (per-tensor, just-in-time) scaling, the scheme of Transformer Engine's
+# Float8CurrentScaling recipe that the reference tries through MaxText's `quantization=te_fp8_currentscaling`
+# (modal/te_run.py:99; TE and MaxText are third-party and not in the reference tree, so the recipe is restated
+# here from its published definition, and no reference test pins it):
+#   amax = max|x| over the tensor (of the bf16 values), scale = 448 / amax in float32 (1 when amax is 0, the
+#   largest float32 when the quotient overflows), q = e4m3(float32(x * scale)), scale_inv = 1 / scale (float32)
+#   multiplies the GEMM's f32 accumulator back.
+# e4m3 is the OCP FP8 E4M3 format ("fn": bias 7, 3 mantissa bits, no infinities, 0x7F / 0xFF NaN, largest 448),
+# rounded to nearest even and saturated at +-448.  Weights take one scale per expert and matrix; activations one
+# per tensor.
+
+E4M3_MAX = 448.0
+
+
+def _e4m3_table():
+    c = np.arange(128)
+    ex, mt = c >> 3, c & 7
+    v = np.where(ex == 0, mt * 2.0 ** -9, (1.0 + mt / 8.0) * np.exp2(ex - 7.0))
+    v[127] = np.nan
+    return v
+
+
+E4M3_VALUES = _e4m3_table()  # value of codes 0x00..0x7F (sign clear), ascending up to 0x7E
+
+
+def e4m3_decode(q):
+    """E4M3 bit patterns (uint8) -> float64 values."""
+    q = np.asarray(q, np.uint8)
+    mag = E4M3_VALUES[q & 0x7F]
+    return np.where(q & 0x80, -mag, mag)
+
+
+def e4m3_bits(a):
+    """float32 -> E4M3 bit pattern (uint8): round to nearest even, saturate at +-448, sign kept (-0 -> 0x80)."""
+    a = np.asarray(a, np.float32)
+    m = np.minimum(np.abs(a).astype(np.float64), E4M3_MAX)
+    _, ex = np.frexp(m)  # m in [2^(ex-1), 2^ex)
+    quantum = np.ldexp(1.0, np.maximum(ex - 4, -9))  # 3 mantissa bits; subnormal spacing 2^-9
+    r = np.rint(m / quantum) * quantum  # exact: power-of-two division, ties to even
+    code = np.searchsorted(E4M3_VALUES[:127], r).astype(np.uint8)
+    return code | np.where(np.signbit(a), np.uint8(0x80), np.uint8(0))
+
+
+def fp8_scale(amax):
+    """(scale, scale_inv) of current scaling for a float32 amax."""
+    amax = np.float32(amax)
+    if not amax > 0:
+        return np.float32(1.0), np.float32(1.0)
+    with np.errstate(over="ignore"):
+        scale = np.float32(E4M3_MAX) / amax
+    if not np.isfinite(scale):
+        scale = np.float32(np.finfo(np.float32).max)
+    return scale, np.float32(1.0) / scale
+
+
+def fp8_quantize(x, groups=1, transpose=False):
+    """Current-scaling quantisation of `groups` equal [R, C] groups of bf16 values.
+
+    Returns (q uint8 [groups, R, C], or [groups, C, R] with transpose; scale_inv float32 [groups]).
+    """
+    x = np.asarray(x, np.float32)
+    x = x.reshape(groups, -1, x.shape[-1])
+    q = np.empty(x.shape, np.uint8)
+    sinv = np.empty(groups, np.float32)
+    for g in range(groups):
+        scale, sinv[g] = fp8_scale(np.abs(x[g]).max() if x[g].size else 0.0)
+        q[g] = e4m3_bits(x[g] * scale)
+    if transpose:
+        q = np.ascontiguousarray(q.transpose(0, 2, 1))
+    return q, sinv
+
+
+def fp8_dequant(q, sinv):
+    """[G, ...] codes times their group's scale_inv, float64."""
+    q = np.asarray(q)
+    s = np.asarray(sinv, np.float64).reshape((-1,) + (1,) * (q.ndim - 1))
+    return e4m3_decode(q) * s
+
+
+def fp8_ragged_dot(lhs_q, lhs_sinv, rhs_q, rhs_sinv, group_sizes):
+    """ragged_dot of dequantised FP8 operands: lhs [m, K] (one scale), rhs [e, n, K] (K contiguous, one scale per
+    group), exact in float64; rows past sum(group_sizes) are 0."""
+    lhs = e4m3_decode(lhs_q) * float(np.asarray(lhs_sinv).reshape(-1)[0])
+    rhs = np.transpose(fp8_dequant(rhs_q, rhs_sinv), (0, 2, 1))
+    return ragged_dot(lhs, rhs, group_sizes)
+
+
+def moe_layer_fwd_fp8(p, route=None):
+    """`moe_layer_fwd` with every expert GEMM on FP8 operands (current scaling).
+
+    x, each expert's W_gate / W_up / W_down and the shared weights are quantised as above; h = silu(g) * u is
+    rounded to bf16 (the saved activation) and quantised over all routed rows (the shared expert's h on its own)
+    before the down projection.  Routing, combine and shared-expert sum are those of `moe_layer_fwd`, in float64.
+    Returns (out [T, d], cache) with cache["h"] the bf16 routed h in sorted-row order.
+    """
+    k = p["k"]
+    x = np.asarray(p["x"], np.float32)
+    if route is None:
+        logits, sel, _ = router(p["x"], p["w_r"], k, p.get("bias"))
+    else:
+        logits, sel = route
+    lw = x.astype(np.float64) @ np.asarray(p["w_r"], np.float64)
+    if p.get("bias") is not None:
+        lw = lw + np.asarray(p["bias"], np.float64)
+    w = topk_softmax(lw, sel)
+    E = p["w_gate"].shape[0]
+    T, d = x.shape
+    xq, sx = fp8_quantize(x)
+    xd = fp8_dequant(xq, sx)[0]
+
+    def deq(name, groups):
+        wt = np.asarray(p[name], np.float32)
+        q, s = fp8_quantize(wt, groups=groups)
+        return fp8_dequant(q, s)
+
+    wg, wu, wd = deq("w_gate", E), deq("w_up", E), deq("w_down", E)
+    lay = build_layout(sel, E)
+    gs = lay["group_sizes"]
+    xs = xd[lay["order"] // k]
+    f = wg.shape[2]
+    gg = np.zeros((xs.shape[0], f))
+    uu = np.zeros_like(gg)
+    start = 0
+    for e in range(E):
+        n = int(gs[e])
+        gg[start:start + n] = xs[start:start + n] @ wg[e]
+        uu[start:start + n] = xs[start:start + n] @ wu[e]
+        start += n
+    hb = round_bf16(silu(gg) * uu)
+    hq, shv = fp8_quantize(hb)
+    hd = fp8_dequant(hq, shv)[0]
+    ys = np.zeros((xs.shape[0], d))
+    start = 0
+    for e in range(E):
+        n = int(gs[e])
+        ys[start:start + n] = hd[start:start + n] @ wd[e]
+        start += n
+    out = (ys[lay["pos"]].reshape(T, k, d) * w[:, :, None]).sum(axis=1)
+    shared = None
+    if p.get("ws_gate") is not None:
+        sg_, su_, sd_ = (deq(n, 1)[0] for n in ("ws_gate", "ws_up", "ws_down"))
+        shb = round_bf16(silu(xd @ sg_) * (xd @ su_))
+        sq, ss = fp8_quantize(shb)
+        out = out + fp8_dequant(sq, ss)[0] @ sd_
+        shared = dict(h=shb)
+    cache = dict(logits=logits, sel=sel, w=w, lay=lay, g=gg, u=uu, h=hb, y=ys, shared=shared, x_sinv=sx[0],
+                 h_sinv=shv[0])
+    return out, cache
+
+
 # --------------------------------------------------------------------------------------------- metrics
 
 
