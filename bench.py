@@ -12,6 +12,10 @@ achieved = algorithmic flops (or bytes) per launch / its mean event-timed durati
 layer's independent chains on helper streams (--concurrency 1, the default; lsurge_set_concurrency).
 cpu_baseline: the numpy CPU oracle's float32 layer forward + backward on a bounded token sample of the same
 layer, timed on this host.
+
+--fp8: the layer forward with every expert GEMM on E4M3 operands (lsurge_moe_fwd_fp8, current scaling); a step is
+the weights' quantisation (once per optimizer step in training) plus the forward; `ms_per_step_cached_weights`
+times the forward alone (weights quantised once, as in serving).  GEMM rooflines are priced against the fp8 peak.
 """
 from __future__ import annotations
 
@@ -27,6 +31,7 @@ for _p in (ROOT, os.path.join(ROOT, "lewi-surge_amd")):
         sys.path.insert(0, _p)
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0   # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 CONFIGS = {  # BASELINE.json configs (T, d, E, k, f, fs, zipf bias, fwd+bwd)
@@ -333,6 +338,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--fp8", action="store_true", help="forward only, expert GEMMs in FP8 (E4M3, current scaling)")
+    ap.add_argument("--fwd-only", action="store_true", help="time the forward alone (bf16)")
     ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")
     ap.add_argument("--concurrency", type=int, default=1,
                     help="timed region: 1 runs the layer's independent chains on helper streams "
@@ -378,6 +385,8 @@ def main():
     from moe_layer import MoELayer, MoEShape
 
     c = CONFIGS[a.config]
+    if a.fp8 or a.fwd_only:
+        c = dict(c, bwd=False)
     dev = torch.device("cuda", 0)
     lib = _lib.lib()
     lib.lsurge_set_concurrency(0)
@@ -386,6 +395,10 @@ def main():
     grads = layer.alloc_grads() if c["bwd"] else None
 
     def step():
+        if a.fp8:
+            layer.quantize_weights_fp8(p)
+            layer.forward_fp8(p)
+            return
         layer.forward(p)
         if c["bwd"]:
             layer.backward(p, dy, grads)
@@ -428,13 +441,22 @@ def main():
     timed = prof_table(lib, a.steps)
     dom_ms = timed[dom][0]
     bound, amount = work[dom]
+    peak_mfma = PEAK_FP8_TFLOPS if a.fp8 else PEAK_BF16_TFLOPS
     if bound == "mfma":
-        achieved, peak, unit = amount / (dom_ms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+        achieved, peak, unit = amount / (dom_ms * 1e-3) / 1e12, peak_mfma, "TFLOP/s"
     else:
         achieved, peak, unit = amount / (dom_ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
 
     ms = el / a.steps * 1e3
     tokens_s = c["T"] * a.steps / el
+    cached_ms = None
+    if a.fp8:  # the forward alone, on weights quantised once
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            layer.forward_fp8(p)
+        torch.cuda.synchronize()
+        cached_ms = (time.perf_counter() - t0) / a.steps * 1e3
     serial_ms = sum(v[2] for v in table.values())
     kern = {n: dict(ms=round(v[0], 4), share=round(v[2] / serial_ms, 4)) for n, v in sorted(table.items(),
                                                                                           key=lambda kv: -kv[1][2])}
@@ -448,7 +470,8 @@ def main():
             print(f"  {n:20s} {v}", file=sys.stderr)
 
     res = {
-        "metric": "MoE-layer fwd+bwd tokens/sec @1 GPU; GEMM MFMA util %, permute HBM GB/s",
+        "metric": ("MoE-layer fwd tokens/sec @1 GPU, FP8 expert GEMMs" if a.fp8 else
+                   "MoE-layer fwd+bwd tokens/sec @1 GPU; GEMM MFMA util %, permute HBM GB/s"),
         "value": round(tokens_s, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -458,19 +481,21 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8-e4m3 expert GEMMs (bf16 router, combine, activations)" if a.fp8 else "bf16",
         "data": "synthetic (torch seeded normals: x~N(0,1), weights~N(0,0.02), dy~N(0,1), bf16), resident in HBM",
-        "config": {"workload": f"{a.config}: MoE layer {'fwd+bwd' if c['bwd'] else 'fwd'} T={c['T']} d={c['d']} "
+        "config": {"workload": f"{a.config}: MoE layer {'fwd+bwd' if c['bwd'] else 'fwd'}{' fp8' if a.fp8 else ''} T={c['T']} d={c['d']} "
                                f"E={c['E']}x{c['f']} top-{c['k']} shared={c['fs']}" + (" zipf-bias" if c["zipf"] else ""),
                    "T": c["T"], "d_model": c["d"], "experts": c["E"], "top_k": c["k"], "expert_ffn": c["f"],
                    "shared_ffn": c["fs"], "block_rows": 128, "parallelism": "single GPU",
                    "concurrent_streams": bool(a.concurrency)},
         "layer_tflops": round(layer_flops(c) / (ms * 1e-3) / 1e12, 1),
-        "mfu": round(layer_flops(c) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "mfu": round(layer_flops(c) / (ms * 1e-3) / 1e12 / peak_mfma, 4),
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4), "traffic": measured_traffic(a.config, dom),
                      "launch_ms": round(dom_ms, 4)},
         "kernels": kern,
+        **({"ms_per_step_cached_weights": round(cached_ms, 4),
+            "tokens_s_cached_weights": round(c["T"] / (cached_ms * 1e-3), 1)} if a.fp8 else {}),
         "kernels_note": "per-kernel ms from a profiled pass on one stream (share of that pass's kernel time); "
                         "the timed region runs with concurrent_streams",
     }

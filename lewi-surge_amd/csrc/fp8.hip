@@ -17,7 +17,8 @@
 namespace {
 
 constexpr int QT = 256;       // threads per workgroup
-constexpr int MAX_PARTS = 256; // amax partials per group
+constexpr int MAX_PARTS = 1024; // amax partials per group
+constexpr int AU = 4;           // independent 16-byte loads per thread and step of the amax kernel
 
 __device__ __forceinline__ float block_max(float v, float* sh) {
 #pragma unroll
@@ -55,18 +56,24 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// amax partials: grid (nb, G); block b of group g reads 8-element chunks b QT + tid, + nb QT, ... of the group's n
-// elements (n % 8 == 0) and writes partial[g nb + b]
+// amax partials: grid (nb, G); block b of group g reads the 8-element chunks b AU QT + u QT + tid (u < AU), then
+// + nb AU QT, ... of the group's n elements (n % 8 == 0), AU loads in flight per thread, and writes
+// partial[g nb + b]
 __global__ __launch_bounds__(QT) void fp8_amax_kernel(const bf16_t* __restrict__ x, int64_t n, int64_t gstride, int nb,
                                                       float* __restrict__ partial) {
   __shared__ float sh[QT / 64];
   const bf16_t* xg = x + (int64_t)blockIdx.y * gstride;
   const int64_t nc = n / 8;
   float m = 0.f;
-  for (int64_t c = (int64_t)blockIdx.x * QT + threadIdx.x; c < nc; c += (int64_t)nb * QT) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xg + 8 * c);
+  for (int64_t c = (int64_t)blockIdx.x * AU * QT + threadIdx.x; c < nc; c += (int64_t)nb * AU * QT) {
+    u32x4 v[AU];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bf_lo(v[i])), fabsf(bf_hi(v[i]))));
+    for (int u = 0; u < AU; ++u)
+      v[u] = c + u * QT < nc ? *reinterpret_cast<const u32x4*>(xg + 8 * (c + u * QT)) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < AU; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bf_lo(v[u][i])), fabsf(bf_hi(v[u][i]))));
   }
   m = block_max(m, sh);
   if (threadIdx.x == 0) partial[(int64_t)blockIdx.y * nb + blockIdx.x] = m;
@@ -139,7 +146,10 @@ __global__ __launch_bounds__(QT) void fp8_cast_t_kernel(const bf16_t* __restrict
   *reinterpret_cast<u32x4*>(q + (int64_t)g * R * C + (int64_t)(c0 + rr) * R + r0 + cq) = o;
 }
 
-int amax_parts(int64_t n) { return (int)std::min<int64_t>(MAX_PARTS, std::max<int64_t>(1, (n / 8 + 8 * QT - 1) / (8 * QT))); }
+// blocks per group: about two steps of AU chunks per thread
+int amax_parts(int64_t n) {
+  return (int)std::min<int64_t>(MAX_PARTS, std::max<int64_t>(1, (n / 8 + 2 * AU * QT - 1) / (2 * AU * QT)));
+}
 
 }  // namespace
 

@@ -251,10 +251,29 @@ size_t lsurge_moe_fp8_weights_bytes(const lsurge_moe_shape* s) {
 
 size_t lsurge_moe_fp8_quantize_weights_workspace_bytes(const lsurge_moe_shape* s) {
   if (check_shape(s)) return 0;
-  return lsurge::fp8_partial_bytes(s->e);
+  return lsurge::fp8_partial_bytes(s->e) + lsurge::fp8_partial_bytes(1);
 }
 
-// one scale per expert and matrix; each weight is transposed into the K-contiguous operand of the FP8 GEMM
+}  // extern "C"
+namespace {
+// holds a device's helper streams for the duration of one layer call
+struct ForkGuard {
+  lsurge::ForkSet f;
+  bool held = false;
+  int acquire(hipStream_t main) {
+    const int rc = lsurge::fork_acquire(&f, main);
+    held = rc == LSURGE_OK;
+    return rc;
+  }
+  ~ForkGuard() {
+    if (held) lsurge::fork_release(&f);
+  }
+};
+}  // namespace
+extern "C" {
+
+// one scale per expert and matrix; each weight is transposed into the K-contiguous operand of the FP8 GEMM.  The
+// small shared-expert matrices (latency-bound launches) go on a helper stream beside the routed ones.
 int lsurge_moe_fp8_quantize_weights(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* wq, size_t wq_bytes,
                                     void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
   if (int rc = check_shape(s)) return rc;
@@ -264,20 +283,26 @@ int lsurge_moe_fp8_quantize_weights(const lsurge_moe_shape* s, const lsurge_moe_
   Fp8W w;
   LSURGE_REQUIRE(wq_bytes >= carve_fp8w(q, nullptr, &w), "moe_fp8_quantize_weights: weight buffer %zu < %zu bytes",
                  wq_bytes, carve_fp8w(q, nullptr, &w));
-  LSURGE_REQUIRE(workspace_bytes >= lsurge::fp8_partial_bytes(q.E), "moe_fp8_quantize_weights: workspace too small");
+  LSURGE_REQUIRE(workspace_bytes >= lsurge_moe_fp8_quantize_weights_workspace_bytes(s),
+                 "moe_fp8_quantize_weights: workspace too small");
   carve_fp8w(q, wq, &w);
   hipStream_t st = (hipStream_t)stream;
   float* part = (float*)workspace;
+  float* part_s = part + lsurge::fp8_partial_bytes(q.E) / sizeof(float);
+  ForkGuard fg;
+  if (int rc = fg.acquire(st)) return rc;
+  hipStream_t s0 = fg.f.side[0];
+  if (q.fs) {
+    if (int rc = lsurge::stream_after(s0, st, fg.f.ev[0])) return rc;
+    if (int rc = lsurge::fp8_quantize_impl(p->ws_gate, 1, q.d, q.fs, true, w.qs_gate, w.s_shared, part_s, s0)) return rc;
+    if (int rc = lsurge::fp8_quantize_impl(p->ws_up, 1, q.d, q.fs, true, w.qs_up, w.s_shared + 1, part_s, s0)) return rc;
+    if (int rc = lsurge::fp8_quantize_impl(p->ws_down, 1, q.fs, q.d, true, w.qs_down, w.s_shared + 2, part_s, s0))
+      return rc;
+  }
   if (int rc = lsurge::fp8_quantize_impl(p->w_gate, q.E, q.d, q.f, true, w.q_gate, w.s_gate, part, st)) return rc;
   if (int rc = lsurge::fp8_quantize_impl(p->w_up, q.E, q.d, q.f, true, w.q_up, w.s_up, part, st)) return rc;
   if (int rc = lsurge::fp8_quantize_impl(p->w_down, q.E, q.f, q.d, true, w.q_down, w.s_down, part, st)) return rc;
-  if (q.fs) {
-    if (int rc = lsurge::fp8_quantize_impl(p->ws_gate, 1, q.d, q.fs, true, w.qs_gate, w.s_shared, part, st)) return rc;
-    if (int rc = lsurge::fp8_quantize_impl(p->ws_up, 1, q.d, q.fs, true, w.qs_up, w.s_shared + 1, part, st)) return rc;
-    if (int rc = lsurge::fp8_quantize_impl(p->ws_down, 1, q.fs, q.d, true, w.qs_down, w.s_shared + 2, part, st))
-      return rc;
-  }
-  return LSURGE_OK;
+  return q.fs ? lsurge::stream_after(st, s0, fg.f.ev[1]) : LSURGE_OK;
 }
 
 size_t lsurge_moe_bwd_workspace_bytes(const lsurge_moe_shape* s) {
@@ -298,25 +323,6 @@ int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_s
   return LSURGE_OK;
 }
 
-}  // extern "C"
-
-namespace {
-// holds a device's helper streams for the duration of one layer call
-struct ForkGuard {
-  lsurge::ForkSet f;
-  bool held = false;
-  int acquire(hipStream_t main) {
-    const int rc = lsurge::fork_acquire(&f, main);
-    held = rc == LSURGE_OK;
-    return rc;
-  }
-  ~ForkGuard() {
-    if (held) lsurge::fork_release(&f);
-  }
-};
-}  // namespace
-
-extern "C" {
 
 // Forward.  Stream plan:
 //   main: router logits -> selection -> layout (-> tile table of the backward) -> gate/up GEMM -> down GEMM ->
