@@ -545,13 +545,14 @@ def fp8_ragged_dot(lhs_q, lhs_sinv, rhs_q, rhs_sinv, group_sizes):
     return ragged_dot(lhs, rhs, group_sizes)
 
 
-def moe_layer_fwd_fp8(p, route=None):
+def moe_layer_fwd_fp8(p, route=None, dtype=np.float64):
     """`moe_layer_fwd` with every expert GEMM on FP8 operands (current scaling).
 
     x, each expert's W_gate / W_up / W_down and the shared weights are quantised as above; h = silu(g) * u is
     rounded to bf16 (the saved activation) and quantised over all routed rows (the shared expert's h on its own)
     before the down projection.  Routing, combine and shared-expert sum are those of `moe_layer_fwd`, in float64.
-    Returns (out [T, d], cache) with cache["h"] the bf16 routed h in sorted-row order.
+    Returns (out [T, d], cache) with cache["h"] the bf16 routed h in sorted-row order.  dtype: the arithmetic of the
+    GEMMs and the combine (float64; float32 for BASELINE-size checks, where float64 would take minutes).
     """
     k = p["k"]
     x = np.asarray(p["x"], np.float32)
@@ -566,19 +567,19 @@ def moe_layer_fwd_fp8(p, route=None):
     E = p["w_gate"].shape[0]
     T, d = x.shape
     xq, sx = fp8_quantize(x)
-    xd = fp8_dequant(xq, sx)[0]
+    xd = fp8_dequant(xq, sx)[0].astype(dtype)
 
     def deq(name, groups):
         wt = np.asarray(p[name], np.float32)
         q, s = fp8_quantize(wt, groups=groups)
-        return fp8_dequant(q, s)
+        return fp8_dequant(q, s).astype(dtype)
 
     wg, wu, wd = deq("w_gate", E), deq("w_up", E), deq("w_down", E)
     lay = build_layout(sel, E)
     gs = lay["group_sizes"]
     xs = xd[lay["order"] // k]
     f = wg.shape[2]
-    gg = np.zeros((xs.shape[0], f))
+    gg = np.zeros((xs.shape[0], f), dtype)
     uu = np.zeros_like(gg)
     start = 0
     for e in range(E):
@@ -588,20 +589,20 @@ def moe_layer_fwd_fp8(p, route=None):
         start += n
     hb = round_bf16(silu(gg) * uu)
     hq, shv = fp8_quantize(hb)
-    hd = fp8_dequant(hq, shv)[0]
-    ys = np.zeros((xs.shape[0], d))
+    hd = fp8_dequant(hq, shv)[0].astype(dtype)
+    ys = np.zeros((xs.shape[0], d), dtype)
     start = 0
     for e in range(E):
         n = int(gs[e])
         ys[start:start + n] = hd[start:start + n] @ wd[e]
         start += n
-    out = (ys[lay["pos"]].reshape(T, k, d) * w[:, :, None]).sum(axis=1)
+    out = (ys[lay["pos"]].reshape(T, k, d) * w.astype(dtype)[:, :, None]).sum(axis=1)
     shared = None
     if p.get("ws_gate") is not None:
         sg_, su_, sd_ = (deq(n, 1)[0] for n in ("ws_gate", "ws_up", "ws_down"))
         shb = round_bf16(silu(xd @ sg_) * (xd @ su_))
         sq, ss = fp8_quantize(shb)
-        out = out + fp8_dequant(sq, ss)[0] @ sd_
+        out = out + fp8_dequant(sq, ss)[0].astype(dtype) @ sd_
         shared = dict(h=shb)
     cache = dict(logits=logits, sel=sel, w=w, lay=lay, g=gg, u=uu, h=hb, y=ys, shared=shared, x_sinv=sx[0],
                  h_sinv=shv[0])

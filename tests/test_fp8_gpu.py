@@ -138,6 +138,23 @@ def test_layer_fwd_fp8(cfg, dev):
     assert 1e-3 < e16 < 0.1, e16  # FP8 is a few percent from the bf16 layer
 
 
+def test_layer_fwd_fp8_baseline_c1(dev):
+    """BASELINE config C1 at full size (T=4096, d=1024, 64 experts x 512, top-6, shared 512) against the float32
+    oracle (all tensors: the scales are global)."""
+    cfg = dict(T=4096, d=1024, E=64, k=6, f=512, fs=512)
+    p = mo.make_inputs(**cfg, seed=0)
+    s = MoEShape(cfg["T"], cfg["d"], cfg["E"], cfg["k"], cfg["f"], cfg["fs"])
+    tp = {n: _bf(p[n], dev) for n in ("x", "w_r", "w_gate", "w_up", "w_down", "ws_gate", "ws_up", "ws_down")}
+    layer = MoELayer(s, dev)
+    layer.quantize_weights_fp8(tp)
+    out = layer.forward_fp8(tp).float().cpu().numpy()
+    sel = layer.views()["sel"].cpu().numpy()
+    want, cache = mo.moe_layer_fwd_fp8(p, dtype=np.float32)
+    assert np.array_equal(sel, cache["sel"])
+    err = mo.rel_l2(out, want)
+    assert err < 2e-2, err
+
+
 def test_layer_fp8_forward_then_bf16_backward(dev):
     cfg = LAYER_CASES[0]
     p = mo.make_inputs(**cfg, seed=5)
