@@ -112,10 +112,10 @@ def make_params(c, dev, seed=0):
     return p, dy
 
 
-def measured_traffic(config, kernel):
+def measured_traffic(config, kernel, fp8=False):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (lines
-    `bench-traffic <kernel> <bytes>` in profiles/moe_layer_<config>_fwd_bwd.md), or None."""
-    path = os.path.join(ROOT, "profiles", f"moe_layer_{config.lower()}_fwd_bwd.md")
+    `bench-traffic <kernel> <bytes>` in profiles/moe_layer_<config>_fwd_bwd.md, or _fp8_fwd.md for --fp8), or None."""
+    path = os.path.join(ROOT, "profiles", f"moe_layer_{config.lower()}_{'fp8_fwd' if fp8 else 'fwd_bwd'}.md")
     try:
         with open(path) as fh:
             for line in fh:
@@ -491,7 +491,7 @@ def main():
         "layer_tflops": round(layer_flops(c) / (ms * 1e-3) / 1e12, 1),
         "mfu": round(layer_flops(c) / (ms * 1e-3) / 1e12 / peak_mfma, 4),
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(a.config, dom),
+                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(a.config, dom, a.fp8),
                      "launch_ms": round(dom_ms, 4)},
         "kernels": kern,
         **({"ms_per_step_cached_weights": round(cached_ms, 4),

@@ -275,13 +275,13 @@ static int launch_rows(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t s)
   a.n_tiles = (int)((a.N + (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN) - 1) / (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN));
   if (a.max_tiles == 0) return LSURGE_OK;
   const dim3 grid(pad8((int64_t)a.n_tiles * a.max_tiles));
-  // FP8 runs on the ping-pong kernel only.  The 4-wave 128 x 256 shape spills (double-buffered 32-byte fragments
-  // and accumulators of two workgroups per CU); a 4-wave 128 x 128 shape fits, but its column tiles gather the
-  // token rows twice as often: the layer's FP8 gate/up GEMM measured 0.32 ms on it against 0.20 ms here.
-  LSURGE_REQUIRE(!F8 || g.tile_rows == 256, "FP8 grouped GEMM: tile_rows=%d must be 256", g.tile_rows);
-  if constexpr (F8)
-    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<CfgPP, BMODE, EPI, F8>), grid, dim3(CfgPP::GT), 0, s, a));
-  else if (g.tile_rows == 256)
+  // FP8: 256-row tiles on the ping-pong kernel, 128-row tiles on the 4-wave kernel with the single-buffered K loop
+  if constexpr (F8) {
+    if (g.tile_rows == 256)
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<CfgPP, BMODE, EPI, F8>), grid, dim3(CfgPP::GT), 0, s, a));
+    else
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, BMODE, EPI, F8>), grid, dim3(Cfg::GT), 0, s, a));
+  } else if (g.tile_rows == 256)
     LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<CfgPP, BMODE, EPI>), grid, dim3(CfgPP::GT), 0, s, a));
   else
     LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, BMODE, EPI>), grid, dim3(Cfg::GT), 0, s, a));
@@ -600,8 +600,7 @@ int lsurge_ragged_dot_fp8(const void* lhs_q, const float* lhs_scale_inv, const v
   hipStream_t s = (hipStream_t)stream;
   lsurge::GemmBlocks g;
   int32_t *total, *e_row0, *e_rows;
-  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0, &e_rows, 256))
-    return rc;
+  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0, &e_rows)) return rc;
   const bool f32 = out_dtype == LSURGE_F32;
   if (int rc = lsurge::gemm_rows_f8(KID_MISC, g, lhs_q, kdim, lhs_scale_inv, rhs_q, nullptr, kdim, n * kdim,
                                     rhs_scale_inv, nullptr, kdim, n, out, n, f32, false, nullptr, nullptr, nullptr, s))

@@ -354,10 +354,32 @@ __device__ __forceinline__ void k_loop_pp(int nk, int grp, Issue&& issue, Load&&
   __builtin_amdgcn_s_waitcnt(0);  // the copies of the zero stages past the end land before the epilogue
 }
 
-// KS: MFMA steps per stage (BK / 16 for bf16, 1 for an FP8 stage of 64 values)
-template <class Cfg, class Frags, int KS = Cfg::BK / 16, class Issue, class Load, class Mma>
+// Single-buffered K loop for one MFMA step per stage: wait until stage kt has landed (at most ST - 2 younger stages
+// in flight) and barrier -- after which every wave is also done with the slot of stage kt - 1 --, refill that slot
+// with stage kt + ST - 1, then read stage kt's fragments and issue its MFMAs.  No fragment double buffer: the
+// registers it saves keep two workgroups on a CU, and the other workgroup's waves cover this one's LDS reads.
+template <int ST, int CP, class Frags, class Issue, class Load, class Mma>
+__device__ __forceinline__ void k_loop_sb(int nk, Issue&& issue, Load&& load, Mma&& mma) {
+#pragma unroll
+  for (int s = 0; s < ST - 1; ++s) issue(s, s);
+  int slot = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    stage_barrier<(ST - 2) * CP>();
+    issue(slot == 0 ? ST - 1 : slot - 1, kt + ST - 1);
+    Frags f;
+    load(slot, 0, f);
+    mma(f);
+    slot = slot == ST - 1 ? 0 : slot + 1;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the copies of the zero stages past the end land before the epilogue
+}
+
+// KS: MFMA steps per stage (BK / 16 for bf16, 1 for an FP8 stage of 64 values).  SB: the single-buffered loop
+// (4-wave FP8).
+template <class Cfg, class Frags, int KS = Cfg::BK / 16, bool SB = false, class Issue, class Load, class Mma>
 __device__ __forceinline__ void run_k_loop(int nk, int wave, Issue&& issue, Load&& load, Mma&& mma) {
   if constexpr (Cfg::PP) k_loop_pp<Cfg::ST, Cfg::CP, KS, Frags>(nk, wave >> 2, issue, load, mma);
+  else if constexpr (SB) k_loop_sb<Cfg::ST, Cfg::CP, Frags>(nk, issue, load, mma);
   else k_loop<Cfg::ST, Cfg::CP, KS, Frags>(nk, issue, load, mma);
 }
 
@@ -580,9 +602,9 @@ void gemm_rows_kernel(RowsArgs a) {
   // runs the loop for its copies and barriers only, without fragment reads or MFMAs; its accumulators stay zero and
   // are never stored.  One branch per wave, so the live loop is the plain one.
   if (wm * TM < rows && n0 + wn * (EPI == EPI_SWIGLU_FWD ? TN / 2 : TN) < N)
-    run_k_loop<Cfg, F, KS>(nk, wave, issue, load, mma);
+    run_k_loop<Cfg, F, KS, F8>(nk, wave, issue, load, mma);
   else
-    run_k_loop<Cfg, F, KS>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
+    run_k_loop<Cfg, F, KS, F8>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
   if constexpr (F8) {  // dequantise: gate (or plain) columns by a_sinv * b_sinv[e], up columns by a_sinv * b2_sinv[e]
     const float sa = a.a_sinv[0];
     const float s1 = sa * a.b_sinv[expert];
