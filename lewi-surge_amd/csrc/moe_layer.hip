@@ -358,10 +358,15 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   LSURGE_REQUIRE(workspace && workspace_bytes >= hist_bytes + f8_bytes, "moe_fwd: workspace %zu bytes too small",
                  workspace_bytes);
   int32_t* rhist = hist_bytes ? (int32_t*)workspace : nullptr;
+  // FP8: x's quantisation (memory-bound) runs on s0 beside the router (VALU-bound); the caller's stream waits for
+  // it (event ev[2]) only before the routed gate/up GEMM
   if (w8) {
     carve_fp8ws(q, (char*)workspace + hist_bytes, &f8);
-    if (int rc = lsurge::fp8_quantize_impl(p->x, 1, q.T, q.d, false, f8.xq, f8.sinv, f8.partial, st, f8.slots, 2))
+    if (int rc = lsurge::stream_after(s0, st, fg.f.ev[3])) return rc;
+    if (int rc = lsurge::fp8_quantize_impl(p->x, 1, q.T, q.d, false, f8.xq, f8.sinv, f8.partial, s0, f8.slots, 2))
       return rc;
+    if (s0 != st && hipEventRecord(fg.f.ev[2], s0) != hipSuccess)
+      return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipEventRecord failed");
   }
   if (int rc = lsurge::router_topk_impl(p->x, p->w_r, p->bias, q.T, q.d, q.E, q.k, sv.logits, sv.sel, sv.weights, st,
                                         s0 != st ? fg.f.ev[0] : nullptr, rhist))
@@ -430,6 +435,8 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
     // gate/up / down at C2 against 0.200 / 0.110 on the ping-pong kernel's 256-row tiles; h is cast over the rows of
     // real blocks
     const lsurge::GemmBlocks blocks8{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0, 128};
+    if (s0 != st && hipStreamWaitEvent(st, fg.f.ev[2], 0) != hipSuccess)
+      return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipStreamWaitEvent failed");
     if (int rc = lsurge::gemm_rows_f8(KID_GEMM_GU_FWD, blocks8, f8.xq, q.d, f8.sinv, w8->q_gate, w8->q_up, q.d,
                                       q.f * q.d, w8->s_gate, w8->s_up, q.d, q.f, sv.h, q.f, false, true, sv.g, sv.u,
                                       f8.slots, st, gather))
