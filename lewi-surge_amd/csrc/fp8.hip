@@ -159,7 +159,10 @@ size_t fp8_partial_bytes(int64_t groups) { return sizeof(float) * (size_t)groups
 
 int fp8_quantize_impl(const void* x, int64_t groups, int64_t rows, int64_t cols, bool transpose, void* q, float* sinv,
                       float* partial, hipStream_t s, uint32_t* zero, int nzero) {
-  LSURGE_REQUIRE(groups >= 1 && groups < 65536 && rows >= 1 && cols >= 1, "fp8_quantize: bad shape");
+  LSURGE_REQUIRE(groups >= 1 && groups < 65536 && rows >= 1 && cols >= 1 && rows < (1 << 30) && cols < (1 << 30) &&
+                     rows * cols < (1ll << 40),
+                 "fp8_quantize: bad shape groups=%lld rows=%lld cols=%lld", (long long)groups, (long long)rows,
+                 (long long)cols);
   LSURGE_REQUIRE(transpose ? (rows % 16 == 0 && cols % 16 == 0) : (rows * cols) % 16 == 0,
                  "fp8_quantize: rows and cols must be multiples of 16 (transposed), rows x cols of 16 (untransposed)");
   LSURGE_REQUIRE(((uintptr_t)x | (uintptr_t)q) % 16 == 0, "fp8_quantize: x and q must be 16-byte aligned");

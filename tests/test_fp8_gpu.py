@@ -112,15 +112,18 @@ def test_ragged_dot_fp8_ragged(K, N, dev):
 LAYER_CASES = [dict(T=1024, d=256, E=16, k=4, f=128, fs=128),  # shared expert merged into the grouped GEMMs
                dict(T=777, d=256, E=16, k=3, f=128, fs=256),   # shared expert of its own width; ragged T
                dict(T=512, d=128, E=8, k=2, f=64, fs=0),
-               dict(T=2048, d=512, E=64, k=6, f=256, fs=256)]
+               dict(T=2048, d=512, E=64, k=6, f=256, fs=256),
+               dict(T=2048, d=256, E=32, k=4, f=128, fs=128, zipf=True)]  # hot and empty experts
 
 
-@pytest.mark.parametrize("cfg", LAYER_CASES, ids=lambda c: "T{T}_d{d}_E{E}_k{k}_f{f}_fs{fs}".format(**c))
+@pytest.mark.parametrize("cfg", LAYER_CASES,
+                         ids=lambda c: "T{T}_d{d}_E{E}_k{k}_f{f}_fs{fs}".format(**c) + ("_zipf" if c.get("zipf") else ""))
 def test_layer_fwd_fp8(cfg, dev):
     p = mo.make_inputs(**cfg, seed=cfg["T"])
     s = MoEShape(cfg["T"], cfg["d"], cfg["E"], cfg["k"], cfg["f"], cfg["fs"])
     names = ("x", "w_r", "w_gate", "w_up", "w_down") + (("ws_gate", "ws_up", "ws_down") if cfg["fs"] else ())
     tp = {n: _bf(p[n], dev) for n in names}
+    tp["bias"] = torch.from_numpy(p["bias"]).to(dev) if p.get("bias") is not None else None
     layer = MoELayer(s, dev)
     out16 = layer.forward(tp).float().cpu().numpy()
     layer.quantize_weights_fp8(tp)
@@ -136,6 +139,35 @@ def test_layer_fwd_fp8(cfg, dev):
     assert mo.rel_l2(h, cache["h"]) < 1e-2
     e16 = mo.rel_l2(out, out16)
     assert 1e-3 < e16 < 0.1, e16  # FP8 is a few percent from the bf16 layer
+
+
+def test_layer_fwd_fp8_concurrent_bitwise(dev):
+    """The forward's helper-stream schedule (x quantised beside the router, the shared expert beside the layout)
+    gives the bits of the serial run."""
+    cfg = LAYER_CASES[0]
+    p = mo.make_inputs(**cfg, seed=11)
+    s = MoEShape(cfg["T"], cfg["d"], cfg["E"], cfg["k"], cfg["f"], cfg["fs"])
+    tp = {n: _bf(p[n], dev) for n in ("x", "w_r", "w_gate", "w_up", "w_down", "ws_gate", "ws_up", "ws_down")}
+    lib = L.lib()
+    prev = lib.lsurge_get_concurrency()
+    outs = []
+    try:
+        for conc in (0, 1, 0, 1):
+            lib.lsurge_set_concurrency(conc)
+            layer = MoELayer(s, dev)
+            # zeroed, so the buffer's alignment gaps (never written) compare equal too
+            layer.wq = torch.zeros(lib.lsurge_moe_fp8_weights_bytes(ctypes.byref(s.c())), dtype=torch.uint8,
+                                   device=dev)
+            layer._wq_ws = L.workspace(lib.lsurge_moe_fp8_quantize_weights_workspace_bytes(ctypes.byref(s.c())), dev)
+            layer.quantize_weights_fp8(tp)
+            out = layer.forward_fp8(tp, out=torch.empty_like(layer.out))
+            torch.cuda.synchronize()
+            v = layer.views()
+            outs.append((out.clone(), layer.wq.clone(), v["h"][v["slot"].long()].clone()))  # h of the valid rows
+    finally:
+        lib.lsurge_set_concurrency(prev)
+    for o, w, h in outs[1:]:
+        assert torch.equal(o, outs[0][0]) and torch.equal(w, outs[0][1]) and torch.equal(h, outs[0][2])
 
 
 def test_layer_fwd_fp8_baseline_c1(dev):
