@@ -331,6 +331,56 @@ def profile_summary(a):
         print(f"bench-traffic {role} {b:.0f}")
 
 
+def conv_bench(a):
+    """Causal depthwise Conv1D at configs/stage1.yml's GDN shape: per_device_batch_size 8, max_target_length 4096,
+    kernel 4 over 2 x 4 key heads x 128 + 8 value heads x 128 = 2048 channels.  HBM-bound: algorithmic bytes are
+    x read + y written (forward), x and dy read + dx written + the f32 partials of dw (backward)."""
+    import torch
+
+    import _lib as L
+
+    B, T, C, K = 8, 4096, 2048, 4
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((B, T, C), device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn((K, C), device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    dy = torch.randn((B, T, C), device=dev, generator=g).to(torch.bfloat16)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    dw = torch.empty((K, C), dtype=torch.float32, device=dev)
+    lib = L.lib()
+    ws = L.workspace(lib.lsurge_causal_conv1d_bwd_workspace_bytes(B, T, C, K), dev)
+    st = L.stream(dev)
+    fwd = lambda: L.check(lib.lsurge_causal_conv1d(L.ptr(x), L.ptr(w), B, T, C, K, L.ptr(y), st), "conv")  # noqa
+    bwd = lambda: L.check(lib.lsurge_causal_conv1d_bwd(L.ptr(x), L.ptr(w), L.ptr(dy), B, T, C, K, L.ptr(dx),  # noqa
+                                                       L.ptr(dw), L.ptr(ws), ws.numel(), st), "conv_bwd")
+    res = {}
+    parts = B * ((T + 63) // 64 + 3) // 4  # dw partial slots (written, then read by the reduction)
+    nbytes = {"fwd": 2 * B * T * C * 2 + K * C * 2, "bwd": 3 * B * T * C * 2 + K * C * 2 + 2 * parts * K * C * 4}
+    for name, fn in (("fwd", fwd), ("bwd", bwd)):
+        for _ in range(a.warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(a.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / a.steps
+        res[name] = (ms, nbytes[name] / (ms * 1e-3) / 1e9)
+    ms = res["fwd"][0] + res["bwd"][0]
+    gbs = (nbytes["fwd"] + nbytes["bwd"]) / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "causal depthwise Conv1D (GDN block) fwd+bwd GB/s @1 GPU", "value": round(gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 (f32 accumulation)", "data": "synthetic normals",
+        "config": {"workload": f"causal depthwise conv1d B={B} T={T} C={C} K={K} (configs/stage1.yml GDN shape)"},
+        "fwd": {"ms": round(res["fwd"][0], 4), "GB/s": round(res["fwd"][1], 1)},
+        "bwd": {"ms": round(res["bwd"][0], 4), "GB/s": round(res["bwd"][1], 1)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -340,6 +390,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fp8", action="store_true", help="forward only, expert GEMMs in FP8 (E4M3, current scaling)")
     ap.add_argument("--fwd-only", action="store_true", help="time the forward alone (bf16)")
+    ap.add_argument("--op", choices=["moe", "conv"], default="moe",
+                    help="conv: the Gated DeltaNet block's causal depthwise Conv1D (modal/fast_conv.py) at the "
+                         "reference config's shape, forward + backward GB/s")
     ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")
     ap.add_argument("--concurrency", type=int, default=1,
                     help="timed region: 1 runs the layer's independent chains on helper streams "
@@ -379,6 +432,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "launches": 3}), flush=True)
+        return
+
+    if a.op == "conv":
+        conv_bench(a)
         return
 
     import _lib

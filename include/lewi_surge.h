@@ -260,6 +260,23 @@ int lsurge_moe_fwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
                        lsurge_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * Causal depthwise Conv1D of the Gated DeltaNet block (memory-bound).
+ * ------------------------------------------------------------------------------------------------ */
+
+/* y[b,t,c] = sum_{j<k} w[j,c] * x[b, t-(k-1)+j, c] (zero before t = 0), f32 accumulation, one rounding.
+ * x, y: [b, t, c] bf16; w: [k, c] bf16 (the kernel [k, 1, c] of nnx.Conv).  c % 8 == 0, 1 <= k <= 8.
+ * Replaces fast_conv._fast_call (modal/fast_conv.py:14-31), the stand-in for
+ * nnx.Conv(padding="CAUSAL", feature_group_count=c). */
+int lsurge_causal_conv1d(const void* x, const void* w, int64_t b, int64_t t, int64_t c, int64_t k, void* y,
+                         lsurge_stream_t stream);
+/* Backward of lsurge_causal_conv1d for upstream dy [b, t, c] bf16:
+ *   dx[b,t,c] = sum_j w[j,c] * dy[b, t+(k-1)-j, c] (bf16),  dw[j,c] = sum_{b,t} dy[b,t,c] * x[b, t-(k-1)+j, c]
+ * (f32, summed in a fixed order).  Replaces the XLA autodiff of fast_conv._fast_call (modal/fast_conv.py:27-30). */
+size_t lsurge_causal_conv1d_bwd_workspace_bytes(int64_t b, int64_t t, int64_t c, int64_t k);
+int lsurge_causal_conv1d_bwd(const void* x, const void* w, const void* dy, int64_t b, int64_t t, int64_t c, int64_t k,
+                             void* dx, float* dw, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Live per-kernel timing with HIP events on the launch stream (used by the benchmark).
  * ------------------------------------------------------------------------------------------------ */
 int lsurge_prof_enable(int on);            /* on=1: create events, start recording; 0: stop */

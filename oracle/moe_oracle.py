@@ -609,6 +609,41 @@ def moe_layer_fwd_fp8(p, route=None, dtype=np.float64):
     return out, cache
 
 
+# --------------------------------------------------------------------------------------------- causal depthwise conv
+#
+# modal/fast_conv.py:14-31 (`_fast_call`, standing in for flax nnx.Conv(padding="CAUSAL",
+# feature_group_count=C) on [B, T, C] inputs with a [K, 1, C] kernel): y[b, t, c] = sum_{j<K} w[j, c] x[b, t-(K-1)+j, c],
+# zero before t = 0 (fast_conv.py:27-30 pads K-1 rows in front and adds the K shifted products, j ascending).
+
+
+def causal_conv1d(x, w):
+    """x [B, T, C], w [K, C] -> y [B, T, C] in float64."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    K, T = w.shape[0], x.shape[1]
+    xp = np.concatenate([np.zeros((x.shape[0], K - 1, x.shape[2])), x], axis=1)
+    y = xp[:, 0:T] * w[0]
+    for j in range(1, K):
+        y = y + xp[:, j:j + T] * w[j]
+    return y
+
+
+def causal_conv1d_bwd(x, w, dy):
+    """(dx [B, T, C], dw [K, C]) of causal_conv1d for upstream dy, float64:
+    dx[b, t, c] = sum_j w[j, c] dy[b, t+(K-1)-j, c] (zero past T); dw[j, c] = sum_{b,t} dy[b, t, c] x[b, t-(K-1)+j, c]."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    dy = np.asarray(dy, np.float64)
+    K, T = w.shape[0], x.shape[1]
+    dyp = np.concatenate([dy, np.zeros((dy.shape[0], K - 1, dy.shape[2]))], axis=1)
+    dx = np.zeros_like(x)
+    for j in range(K):
+        dx += w[j] * dyp[:, K - 1 - j:K - 1 - j + T]
+    xp = np.concatenate([np.zeros((x.shape[0], K - 1, x.shape[2])), x], axis=1)
+    dw = np.stack([(dy * xp[:, j:j + T]).sum(axis=(0, 1)) for j in range(K)])
+    return dx, dw
+
+
 # --------------------------------------------------------------------------------------------- metrics
 
 
