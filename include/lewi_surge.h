@@ -277,6 +277,22 @@ int lsurge_causal_conv1d_bwd(const void* x, const void* w, const void* dy, int64
                              void* dx, float* dw, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * Chunked gated delta rule of the Gated DeltaNet block (forward).
+ * ------------------------------------------------------------------------------------------------ */
+
+/* Per sequence and head, state S [dk, dv]: S_t = exp(g_t) (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T,
+ * o_t = S_t^T q_t / sqrt(dk), computed in 64-token chunks (WY form) with the reference's bf16 rounding points
+ * (q * scale, k beta, v beta, and the chunk-local u and w) and f32 arithmetic otherwise.
+ * q, k: [b, t, h, dk] bf16; v: [b, t, h, dv] bf16; g: [b, t, h] f32 (log decay); beta: [b, t, h] bf16;
+ * h0: [b, h, dk, dv] f32 initial state or NULL; o: [b, t, h, dv] bf16; h_out: [b, h, dk, dv] f32 or NULL.
+ * dk = dv = 128.  Replaces fast_chunk_gated_delta_rule (modal/gdn_fast.py:37-113) without qk-norm or context
+ * parallelism. */
+size_t lsurge_gdn_chunked_workspace_bytes(int64_t b, int64_t t, int64_t h, int64_t dk, int64_t dv);
+int lsurge_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float* g, const void* beta, int64_t b,
+                           int64_t t, int64_t h, int64_t dk, int64_t dv, const float* h0, void* o, float* h_out,
+                           void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Live per-kernel timing with HIP events on the launch stream (used by the benchmark).
  * ------------------------------------------------------------------------------------------------ */
 int lsurge_prof_enable(int on);            /* on=1: create events, start recording; 0: stop */

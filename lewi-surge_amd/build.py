@@ -25,7 +25,7 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(HERE, "..", "include"),
 ]
-SOURCES = ["abi.cpp", "router.hip", "layout.hip", "permute.hip", "gemm.hip", "fp8.hip", "conv.hip", "moe_layer.hip"]
+SOURCES = ["abi.cpp", "router.hip", "layout.hip", "permute.hip", "gemm.hip", "fp8.hip", "conv.hip", "gdn.hip", "moe_layer.hip"]
 
 
 def _compile(src):

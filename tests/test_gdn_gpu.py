@@ -1,0 +1,70 @@
+"""Chunked gated delta rule (modal/gdn_fast.py:37-113) on the GPU against the oracle with the reference's bf16
+rounding points (oracle/gdn_oracle.py, itself pinned against the token-by-token recurrence).
+
+Outputs and final states within 2e-2 relative L2 (f32 arithmetic against float64, and a few
+bf16 roundings that can fall either way).  Covers lengths below, at and across chunk boundaries, several heads and
+sequences, an initial state, and the reference config's shape (8 value heads x 128, T = 4096;
+configs/stage1.yml:49-53).
+"""
+import numpy as np
+import pytest
+import torch
+
+import _lib as L
+from oracle import gdn_oracle as go
+from oracle import moe_oracle as mo
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+def _inputs(B, T, H, seed):
+    rng = np.random.default_rng(seed)
+    q = mo.round_bf16(rng.standard_normal((B, T, H, D)).astype(np.float32))
+    k = rng.standard_normal((B, T, H, D))
+    k = mo.round_bf16((k / np.linalg.norm(k, axis=-1, keepdims=True)).astype(np.float32))  # l2-normalised keys
+    v = mo.round_bf16(rng.standard_normal((B, T, H, D)).astype(np.float32))
+    g = (-np.abs(rng.standard_normal((B, T, H))) * 0.05).astype(np.float32)
+    beta = mo.round_bf16((1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H))))).astype(np.float32))
+    return q, k, v, g, beta
+
+
+def gpu_gdn(q, k, v, g, beta, dev, h0=None):
+    B, T, H, _ = q.shape
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev).to(torch.bfloat16)  # noqa: E731
+    qt, kt, vt, bt = bf(q), bf(k), bf(v), bf(beta)
+    gt = torch.from_numpy(np.ascontiguousarray(g, np.float32)).to(dev)
+    h0t = None if h0 is None else torch.from_numpy(np.ascontiguousarray(h0, np.float32)).to(dev)
+    o = torch.empty_like(vt)
+    hout = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    lib = L.lib()
+    ws = L.workspace(lib.lsurge_gdn_chunked_workspace_bytes(B, T, H, D, D), dev)
+    L.check(lib.lsurge_gdn_chunked_fwd(L.ptr(qt), L.ptr(kt), L.ptr(vt), L.ptr(gt), L.ptr(bt), B, T, H, D, D,
+                                       L.ptr(h0t), L.ptr(o), L.ptr(hout), L.ptr(ws), ws.numel(), L.stream(dev)),
+            "gdn_chunked_fwd")
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), hout.cpu().numpy()
+
+
+@pytest.mark.parametrize("B,T,H", [(1, 1, 1), (1, 63, 2), (2, 64, 1), (2, 100, 3), (1, 333, 2)])
+def test_against_oracle(B, T, H, dev):
+    q, k, v, g, beta = _inputs(B, T, H, seed=T + H)
+    o, h = gpu_gdn(q, k, v, g, beta, dev)
+    wo, wh = go.gdn_chunked(q, k, v, g, beta, chunk=64, rounding="bf16")
+    eo, eh = mo.rel_l2(o, wo), mo.rel_l2(h, wh)
+    assert eo < 2e-2 and eh < 2e-2, (eo, eh)
+
+
+def test_initial_state(dev):
+    q, k, v, g, beta = _inputs(2, 150, 2, seed=7)
+    h0 = np.random.default_rng(8).standard_normal((2, 2, D, D)).astype(np.float32) * 0.1
+    o, h = gpu_gdn(q, k, v, g, beta, dev, h0=h0)
+    wo, wh = go.gdn_chunked(q, k, v, g, beta, chunk=64, h0=h0, rounding="bf16")
+    assert mo.rel_l2(o, wo) < 2e-2 and mo.rel_l2(h, wh) < 2e-2
+
+
+def test_reference_config_shape(dev):
+    q, k, v, g, beta = _inputs(1, 4096, 8, seed=1)
+    o, h = gpu_gdn(q, k, v, g, beta, dev)
+    wo, wh = go.gdn_chunked(q, k, v, g, beta, chunk=64, rounding="bf16")
+    assert mo.rel_l2(o, wo) < 2e-2 and mo.rel_l2(h, wh) < 2e-2
