@@ -381,6 +381,57 @@ def conv_bench(a):
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}), flush=True)
 
 
+def gdn_bench(a):
+    """Chunked gated delta rule forward at configs/stage1.yml's GDN shape: per_device_batch_size 8,
+    max_target_length 4096, 8 value heads x 128 (keys repeated to the value heads), chunks of 64.  Algorithmic flops
+    per chunk and head: 2 (2 C^2 Dk + 2 C^2 Dv) chunk-local (S, attn, u, w) + 2 (2 C Dk Dv + C^2 Dv + C Dk Dv) scan
+    (q S, w S, attn v_new, the state update), counted in full as the reference's dense products are."""
+    import torch
+
+    import _lib as L
+
+    B, T, H, D, C = 8, 4096, 8, 128, 64
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn((B, T, H, D), device=dev, generator=gen).to(torch.bfloat16)
+    k = torch.nn.functional.normalize(torch.randn((B, T, H, D), device=dev, generator=gen), dim=-1).to(torch.bfloat16)
+    v = torch.randn((B, T, H, D), device=dev, generator=gen).to(torch.bfloat16)
+    g = -torch.rand((B, T, H), device=dev, generator=gen) * 0.1
+    beta = torch.sigmoid(torch.randn((B, T, H), device=dev, generator=gen)).to(torch.bfloat16)
+    o = torch.empty_like(v)
+    lib = L.lib()
+    ws = L.workspace(lib.lsurge_gdn_chunked_workspace_bytes(B, T, H, D, D), dev)
+    st = L.stream(dev)
+
+    def fwd():
+        L.check(lib.lsurge_gdn_chunked_fwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D, None,
+                                           L.ptr(o), None, L.ptr(ws), ws.numel(), st), "gdn_chunked_fwd")
+
+    for _ in range(a.warmup):
+        fwd()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(a.steps):
+        fwd()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / a.steps
+    chunks = B * H * ((T + C - 1) // C)
+    flops = chunks * 2 * (2 * C * C * D + 2 * C * C * D + 2 * C * D * D + C * C * D + C * D * D)
+    tf = flops / (ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "Gated DeltaNet chunked scan forward tokens/sec @1 GPU", "value": round(B * T / (ms * 1e-3), 1),
+        "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16 in/out, f32 arithmetic",
+        "data": "synthetic normals (l2-normalised keys)",
+        "config": {"workload": f"chunked gated delta rule fwd B={B} T={T} H={H} Dk=Dv={D} chunk={C} "
+                               "(configs/stage1.yml GDN shape)"},
+        "roofline": {"bound": "valu", "achieved": round(tf, 2), "peak": 157.3, "unit": "TFLOP/s",
+                     "frac": round(tf / 157.3, 4), "traffic": None,
+                     "note": "f32 arithmetic on the VALU, priced against the MI355X fp32 matrix peak"}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -390,9 +441,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fp8", action="store_true", help="forward only, expert GEMMs in FP8 (E4M3, current scaling)")
     ap.add_argument("--fwd-only", action="store_true", help="time the forward alone (bf16)")
-    ap.add_argument("--op", choices=["moe", "conv"], default="moe",
+    ap.add_argument("--op", choices=["moe", "conv", "gdn"], default="moe",
                     help="conv: the Gated DeltaNet block's causal depthwise Conv1D (modal/fast_conv.py) at the "
-                         "reference config's shape, forward + backward GB/s")
+                         "reference config's shape, forward + backward GB/s; gdn: its chunked gated delta rule "
+                         "forward (modal/gdn_fast.py), tokens/s")
     ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")
     ap.add_argument("--concurrency", type=int, default=1,
                     help="timed region: 1 runs the layer's independent chains on helper streams "
@@ -436,6 +488,9 @@ def main():
 
     if a.op == "conv":
         conv_bench(a)
+        return
+    if a.op == "gdn":
+        gdn_bench(a)
         return
 
     import _lib

@@ -24,7 +24,7 @@ namespace {
 constexpr int GC = 64;   // chunk
 constexpr int GD = 128;  // head dim (keys and values)
 constexpr int GP = GD + 8;  // LDS row pitch of a bf16 [GC][GD] tile (272 bytes: rows start 16 bytes apart in banks)
-constexpr int GTH = 256;
+constexpr int GTH = 512;  // 8 waves: one workgroup fills a CU (its LDS tiles leave no room for a second)
 constexpr int SB = 32;   // value columns per scan workgroup
 
 __device__ __forceinline__ void unpack8g(u32x4 v, float* f) {
@@ -93,20 +93,21 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
     vbs[i][c] = f32_to_bf16(bf16_to_f32(vbs[i][c]) * bt[i]);
   }
   __syncthreads();
-  // S (strictly lower) and attn (lower incl. diagonal), 4 x 4 entries per thread, dot products over GD
+  // S (strictly lower) and attn (lower incl. diagonal), 2 x 4 entries per thread, dot products over GD
   {
-    const int i0 = 4 * (tid / 16), j0 = 4 * (tid % 16);
-    float sd[4][4] = {}, ad[4][4] = {};
+    const int i0 = 2 * (tid / 16), j0 = 4 * (tid % 16);
+    float sd[2][4] = {}, ad[2][4] = {};
     for (int d = 0; d < GD; d += 8) {
-      float kb8[4][8], q8[4][8], k8[4][8];
+      float kb8[2][8], q8[2][8], k8[4][8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < 2; ++r) {
         unpack8g(*reinterpret_cast<const u32x4*>(&kbs[i0 + r][d]), kb8[r]);
         unpack8g(*reinterpret_cast<const u32x4*>(&qs[i0 + r][d]), q8[r]);
-        unpack8g(*reinterpret_cast<const u32x4*>(&ks[j0 + r][d]), k8[r]);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < 4; ++r) unpack8g(*reinterpret_cast<const u32x4*>(&ks[j0 + r][d]), k8[r]);
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -117,7 +118,7 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
     }
     float* att = attn_out + chunk_id * GC * GC;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 2; ++r)
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int i = i0 + r, j = j0 + s;
@@ -127,30 +128,31 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
       }
   }
   __syncthreads();
-  // A = (I + S)^-1, row by row: A[i][c] = -sum_{c <= j < i} S[i][j] A[j][c] (c < i), A[i][i] = 1, 0 above.  Four
-  // threads per column split the sum (fixed order: the four partial sums are combined by an xor butterfly).
+  // A = (I + S)^-1, row by row: A[i][c] = -sum_{c <= j < i} S[i][j] A[j][c] (c < i), A[i][i] = 1, 0 above.  Eight
+  // threads per column split the sum (fixed order: the partial sums are combined by an xor butterfly).
   {
-    const int c = tid / 4, part = tid % 4;
+    const int c = tid / 8, part = tid % 8;
     for (int i = 0; i < GC; ++i) {
       float s = 0.f;
-      for (int j = c + part; j < i; j += 4) s = fmaf(Sm[i][j], Am[j][c], s);
+      for (int j = c + part; j < i; j += 8) s = fmaf(Sm[i][j], Am[j][c], s);
       s += __shfl_xor(s, 1, 64);
       s += __shfl_xor(s, 2, 64);
+      s += __shfl_xor(s, 4, 64);
       if (part == 0) Am[i][c] = c < i ? -s : (c == i ? 1.f : 0.f);
       __syncthreads();
     }
   }
-  // u = A vb, w = A (kb e^gcum): 4 rows x 8 columns of each per thread, rounded to bf16 (gdn_fast.py:88-90)
+  // u = A vb, w = A (kb e^gcum): 2 rows x 8 columns of each per thread, rounded to bf16 (gdn_fast.py:88-90)
   {
-    const int i0 = 4 * (tid / 16), c0 = 8 * (tid % 16);
-    float ua[4][8] = {}, wa[4][8] = {};
+    const int i0 = 2 * (tid / 16), c0 = 8 * (tid % 16);
+    float ua[2][8] = {}, wa[2][8] = {};
     for (int j = 0; j < GC; ++j) {
       float vb8[8], kb8[8];
       unpack8g(*reinterpret_cast<const u32x4*>(&vbs[j][c0]), vb8);
       unpack8g(*reinterpret_cast<const u32x4*>(&kbs[j][c0]), kb8);
       const float e = eg[j];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < 2; ++r) {
         const float a = Am[i0 + r][j];
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
@@ -162,7 +164,7 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
     bf16_t* ub = u_out + chunk_id * GC * GD;
     bf16_t* wb = w_out + chunk_id * GC * GD;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < 2; ++r) {
       *reinterpret_cast<u32x4*>(ub + (i0 + r) * GD + c0) =
           u32x4{pack_bf16x2(ua[r][0], ua[r][1]), pack_bf16x2(ua[r][2], ua[r][3]), pack_bf16x2(ua[r][4], ua[r][5]),
                 pack_bf16x2(ua[r][6], ua[r][7])};
@@ -191,10 +193,10 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
     const int d = e / SB, c = e % SB;
     hs[d][c] = h0 ? h0[(bh * GD + d) * GD + cb + c] : 0.f;
   }
-  // outputs of this thread: rows ri .. ri + 1, columns ci .. ci + 3 of the [GC][SB] chunk products; state entries
-  // rows hd .. hd + 1 (of GD), columns hc .. hc + 7
-  const int ri = 2 * (tid / 8), ci = 4 * (tid % 8);
-  const int hd = 2 * (tid / 4), hc = 8 * (tid % 4);
+  // outputs of this thread: row ri, columns ci .. ci + 3 of the [GC][SB] chunk products; state entries row hd (of
+  // GD), columns hc .. hc + 7
+  const int ri = tid / 8, ci = 4 * (tid % 8);
+  const int hd = tid / 4, hc = 8 * (tid % 4);
   for (int n = 0; n < N; ++n) {
     const int t0 = n * GC;
     const int64_t chunk_id = bh * N + n;
@@ -210,37 +212,28 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
     for (int e = tid; e < GC * GC; e += GTH) at[e / GC][e % GC] = asrc[e];
     if (tid < GC) gc[tid] = gcum_in[chunk_id * GC + tid];
     __syncthreads();
-    // v_new = u - w S and inter = (q e^gcum) S for this thread's 2 x 4 outputs
-    float vacc[2][4] = {}, iacc[2][4] = {};
+    // v_new = u - w S and inter = (q e^gcum) S for this thread's 1 x 4 outputs
+    float vacc[1][4] = {}, iacc[1][4] = {};
     for (int d = 0; d < GD; d += 8) {
-      float w8[2][8], q8[2][8];
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        unpack8g(*reinterpret_cast<const u32x4*>(&ws[ri + r][d]), w8[r]);
-        unpack8g(*reinterpret_cast<const u32x4*>(&qs[ri + r][d]), q8[r]);
-      }
+      float w8[1][8], q8[1][8];
+      unpack8g(*reinterpret_cast<const u32x4*>(&ws[ri][d]), w8[0]);
+      unpack8g(*reinterpret_cast<const u32x4*>(&qs[ri][d]), q8[0]);
 #pragma unroll
       for (int x = 0; x < 8; ++x)
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const float hv = hs[d + x][ci + s];
-#pragma unroll
-          for (int r = 0; r < 2; ++r) {
-            vacc[r][s] = fmaf(w8[r][x], hv, vacc[r][s]);
-            iacc[r][s] = fmaf(q8[r][x], hv, iacc[r][s]);
-          }
+          vacc[0][s] = fmaf(w8[0][x], hv, vacc[0][s]);
+          iacc[0][s] = fmaf(q8[0][x], hv, iacc[0][s]);
         }
     }
     const bf16_t* ub = u_in + chunk_id * GC * GD;
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) vn[ri + r][ci + s] = bf16_to_f32(ub[(ri + r) * GD + cb + ci + s]) - vacc[r][s];
+    for (int s = 0; s < 4; ++s) vn[ri][ci + s] = bf16_to_f32(ub[ri * GD + cb + ci + s]) - vacc[0][s];
     __syncthreads();
     // o = inter e^gcum + attn v_new (attn is zero above the diagonal)
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int i = ri + r;
+    {
+      const int r = 0, i = ri;
       float acc[4];
       const float e = __expf(gc[i]);
 #pragma unroll
@@ -258,26 +251,17 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
     // S = e^gcum_last S + (k e^(gcum_last - gcum))^T v_new; every read of the old state happened before the barrier
     // above
     const float gl = gc[GC - 1], el = __expf(gl);
-    float hn[2][8];
+    float hn[8];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int x = 0; x < 8; ++x) hn[r][x] = hs[hd + r][hc + x] * el;
+    for (int x = 0; x < 8; ++x) hn[x] = hs[hd][hc + x] * el;
     for (int i = 0; i < GC; ++i) {
-      const float e = __expf(gl - gc[i]);
-      const float k0 = bf16_to_f32(ks[i][hd]) * e, k1 = bf16_to_f32(ks[i][hd + 1]) * e;
+      const float k0 = bf16_to_f32(ks[i][hd]) * __expf(gl - gc[i]);
 #pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        const float vv = vn[i][hc + x];
-        hn[0][x] = fmaf(k0, vv, hn[0][x]);
-        hn[1][x] = fmaf(k1, vv, hn[1][x]);
-      }
+      for (int x = 0; x < 8; ++x) hn[x] = fmaf(k0, vn[i][hc + x], hn[x]);
     }
     __syncthreads();  // every thread has read the old state (o used only vn and at)
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int x = 0; x < 8; ++x) hs[hd + r][hc + x] = hn[r][x];
+    for (int x = 0; x < 8; ++x) hs[hd][hc + x] = hn[x];
   }
   __syncthreads();
   if (h_out)
