@@ -59,7 +59,9 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
                                                         const bf16_t* __restrict__ beta, int T, int H, float qscale,
                                                         bf16_t* __restrict__ u_out, bf16_t* __restrict__ w_out,
                                                         float* __restrict__ attn_out, float* __restrict__ gcum_out) {
-  __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], kbs[GC][GP], qs[GC][GP], vbs[GC][GP];
+  // k, and q (then v once the attention is done); k beta is formed from k where it is used.  68 KB of LDS: two
+  // workgroups per CU.
+  __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], qs[GC][GP];
   __shared__ float Sm[GC][GC + 1], Am[GC][GC + 1];
   __shared__ float gc[GC], eg[GC], bt[GC];
   const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z, N = gridDim.x;
@@ -73,7 +75,6 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
   }
   load_tile(ks, k, row0, T, t0, H, h, 1.f);
   load_tile(qs, q, row0, T, t0, H, h, qscale);  // q * scale in the compute dtype (gdn_fast.py:56-57)
-  load_tile(vbs, v, row0, T, t0, H, h, 1.f);
   __syncthreads();
   if (tid < GC) {  // inclusive cumulative sum of g over the chunk (wave 0)
     float x = gc[tid];
@@ -86,23 +87,23 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
     eg[tid] = __expf(x);
     gcum_out[chunk_id * GC + tid] = x;
   }
-  // k beta and v beta in the compute dtype (gdn_fast.py:78, 87)
-  for (int e = tid; e < GC * GD; e += GTH) {
-    const int i = e / GD, c = e % GD;
-    kbs[i][c] = f32_to_bf16(bf16_to_f32(ks[i][c]) * bt[i]);
-    vbs[i][c] = f32_to_bf16(bf16_to_f32(vbs[i][c]) * bt[i]);
-  }
   __syncthreads();
   // S (strictly lower) and attn (lower incl. diagonal), 2 x 4 entries per thread, dot products over GD
   {
     const int i0 = 2 * (tid / 16), j0 = 4 * (tid % 16);
     float sd[2][4] = {}, ad[2][4] = {};
+    const float b0 = bt[i0], b1 = bt[i0 + 1];
     for (int d = 0; d < GD; d += 8) {
       float kb8[2][8], q8[2][8], k8[4][8];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        unpack8g(*reinterpret_cast<const u32x4*>(&kbs[i0 + r][d]), kb8[r]);
+        unpack8g(*reinterpret_cast<const u32x4*>(&ks[i0 + r][d]), kb8[r]);
         unpack8g(*reinterpret_cast<const u32x4*>(&qs[i0 + r][d]), q8[r]);
+      }
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {  // k beta in the compute dtype (gdn_fast.py:78)
+        kb8[0][x] = bf16_to_f32(f32_to_bf16(kb8[0][x] * b0));
+        kb8[1][x] = bf16_to_f32(f32_to_bf16(kb8[1][x] * b1));
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) unpack8g(*reinterpret_cast<const u32x4*>(&ks[j0 + r][d]), k8[r]);
@@ -128,6 +129,7 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
       }
   }
   __syncthreads();
+  load_tile(qs, v, row0, T, t0, H, h, 1.f);  // v replaces q (every read of q is done)
   // A = (I + S)^-1, row by row: A[i][c] = -sum_{c <= j < i} S[i][j] A[j][c] (c < i), A[i][i] = 1, 0 above.  Eight
   // threads per column split the sum (fixed order: the partial sums are combined by an xor butterfly).
   {
@@ -148,8 +150,14 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
     float ua[2][8] = {}, wa[2][8] = {};
     for (int j = 0; j < GC; ++j) {
       float vb8[8], kb8[8];
-      unpack8g(*reinterpret_cast<const u32x4*>(&vbs[j][c0]), vb8);
-      unpack8g(*reinterpret_cast<const u32x4*>(&kbs[j][c0]), kb8);
+      unpack8g(*reinterpret_cast<const u32x4*>(&qs[j][c0]), vb8);
+      unpack8g(*reinterpret_cast<const u32x4*>(&ks[j][c0]), kb8);
+      const float bj = bt[j];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {  // v beta and k beta in the compute dtype (gdn_fast.py:78, 87)
+        vb8[x] = bf16_to_f32(f32_to_bf16(vb8[x] * bj));
+        kb8[x] = bf16_to_f32(f32_to_bf16(kb8[x] * bj));
+      }
       const float e = eg[j];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
@@ -183,8 +191,12 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
                                                        float qscale, const float* __restrict__ h0,
                                                        bf16_t* __restrict__ o, float* __restrict__ h_out) {
   __shared__ __attribute__((aligned(16))) bf16_t qs[GC][GP], ks[GC][GP], ws[GC][GP];
-  __shared__ float hs[GD][SB + 1], vn[GC][SB + 1], at[GC][GC + 1];
-  __shared__ float gc[GC];
+  // state slice and v_new with 16-byte aligned rows (pitch SB + 4): a thread reads 4 or 8 consecutive columns at once,
+  // and the 8 column groups of a row that a wave reads at one d are distinct 16-byte slots
+  constexpr int SP = SB + 4;
+  __shared__ __attribute__((aligned(16))) float hs[GD][SP], vn[GC][SP];
+  __shared__ float at[GC][GC + 1];
+  __shared__ float gc[GC], ek[GC];  // gcum, exp(gcum_last - gcum)
   const int cb = blockIdx.x * SB, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const int64_t row0 = (int64_t)b * T;
@@ -197,21 +209,58 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
   // GD), columns hc .. hc + 7
   const int ri = tid / 8, ci = 4 * (tid % 8);
   const int hd = tid / 4, hc = 8 * (tid % 4);
+  // The next chunk's tiles are fetched into registers while the current one computes: this thread's two 16-byte
+  // pieces of each of q, k and w (piece e = tid + GTH p: row e / 16, columns 8 (e % 16)), its eight attn values and
+  // (threads < GC) one gcum value.
+  constexpr int PP = GC * (GD / 8) / GTH;  // pieces per thread and tile
+  static_assert(PP * GTH == GC * (GD / 8) && GC * GC == 8 * GTH, "scan tile split");
+  u32x4 pq[PP], pk[PP], pw[PP];
+  f32x4 pa[2];
+  float pg = 0.f;
+  auto fetch = [&](int n) {
+    const int t0 = n * GC;
+    const int64_t chunk_id = bh * N + n;
+#pragma unroll
+    for (int p = 0; p < PP; ++p) {
+      const int e = tid + GTH * p, i = e / (GD / 8), c = 8 * (e % (GD / 8));
+      const bool in = t0 + i < T;
+      const int64_t off = ((row0 + t0 + i) * H + h) * GD + c;
+      pq[p] = in ? *reinterpret_cast<const u32x4*>(q + off) : u32x4{0u, 0u, 0u, 0u};
+      pk[p] = in ? *reinterpret_cast<const u32x4*>(k + off) : u32x4{0u, 0u, 0u, 0u};
+      pw[p] = *reinterpret_cast<const u32x4*>(w_in + chunk_id * GC * GD + i * GD + c);
+    }
+    const float* asrc = attn_in + chunk_id * GC * GC;
+    pa[0] = *reinterpret_cast<const f32x4*>(asrc + 4 * tid);
+    pa[1] = *reinterpret_cast<const f32x4*>(asrc + 4 * (tid + GTH));
+    if (tid < GC) pg = gcum_in[chunk_id * GC + tid];
+  };
+  fetch(0);
   for (int n = 0; n < N; ++n) {
     const int t0 = n * GC;
     const int64_t chunk_id = bh * N + n;
     __syncthreads();  // the previous chunk is done with the tiles
-    load_tile(qs, q, row0, T, t0, H, h, qscale);
-    load_tile(ks, k, row0, T, t0, H, h, 1.f);
-    const bf16_t* wsrc = w_in + chunk_id * GC * GD;
-    for (int e = tid; e < GC * (GD / 8); e += GTH) {
-      const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
-      *reinterpret_cast<u32x4*>(&ws[i][c]) = *reinterpret_cast<const u32x4*>(wsrc + i * GD + c);
+#pragma unroll
+    for (int p = 0; p < PP; ++p) {
+      const int e = tid + GTH * p, i = e / (GD / 8), c = 8 * (e % (GD / 8));
+      float f[8];
+      unpack8g(pq[p], f);  // q * scale in the compute dtype (gdn_fast.py:56-57)
+      *reinterpret_cast<u32x4*>(&qs[i][c]) =
+          u32x4{pack_bf16x2(f[0] * qscale, f[1] * qscale), pack_bf16x2(f[2] * qscale, f[3] * qscale),
+                pack_bf16x2(f[4] * qscale, f[5] * qscale), pack_bf16x2(f[6] * qscale, f[7] * qscale)};
+      *reinterpret_cast<u32x4*>(&ks[i][c]) = pk[p];
+      *reinterpret_cast<u32x4*>(&ws[i][c]) = pw[p];
     }
-    const float* asrc = attn_in + chunk_id * GC * GC;
-    for (int e = tid; e < GC * GC; e += GTH) at[e / GC][e % GC] = asrc[e];
-    if (tid < GC) gc[tid] = gcum_in[chunk_id * GC + tid];
+#pragma unroll
+    for (int hlf = 0; hlf < 2; ++hlf)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const int e = 4 * (tid + GTH * hlf) + x;
+        at[e / GC][e % GC] = pa[hlf][x];
+      }
+    if (tid < GC) gc[tid] = pg;
     __syncthreads();
+    if (tid < GC) ek[tid] = __expf(gc[GC - 1] - gc[tid]);  // read after the barrier that follows v_new
+    if (n + 1 < N) fetch(n + 1);
     // v_new = u - w S and inter = (q e^gcum) S for this thread's 1 x 4 outputs
     float vacc[1][4] = {}, iacc[1][4] = {};
     for (int d = 0; d < GD; d += 8) {
@@ -219,13 +268,14 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
       unpack8g(*reinterpret_cast<const u32x4*>(&ws[ri][d]), w8[0]);
       unpack8g(*reinterpret_cast<const u32x4*>(&qs[ri][d]), q8[0]);
 #pragma unroll
-      for (int x = 0; x < 8; ++x)
+      for (int x = 0; x < 8; ++x) {
+        const f32x4 hv = *reinterpret_cast<const f32x4*>(&hs[d + x][ci]);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const float hv = hs[d + x][ci + s];
-          vacc[0][s] = fmaf(w8[0][x], hv, vacc[0][s]);
-          iacc[0][s] = fmaf(q8[0][x], hv, iacc[0][s]);
+          vacc[0][s] = fmaf(w8[0][x], hv[s], vacc[0][s]);
+          iacc[0][s] = fmaf(q8[0][x], hv[s], iacc[0][s]);
         }
+      }
     }
     const bf16_t* ub = u_in + chunk_id * GC * GD;
 #pragma unroll
@@ -240,8 +290,9 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
       for (int s = 0; s < 4; ++s) acc[s] = iacc[r][s] * e;
       for (int j = 0; j <= i; ++j) {
         const float a = at[i][j];
+        const f32x4 vv = *reinterpret_cast<const f32x4*>(&vn[j][ci]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc[s] = fmaf(a, vn[j][ci + s], acc[s]);
+        for (int s = 0; s < 4; ++s) acc[s] = fmaf(a, vv[s], acc[s]);
       }
       if (t0 + i < T) {
         bf16_t* op = o + ((row0 + t0 + i) * H + h) * GD + cb + ci;
@@ -255,9 +306,13 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
 #pragma unroll
     for (int x = 0; x < 8; ++x) hn[x] = hs[hd][hc + x] * el;
     for (int i = 0; i < GC; ++i) {
-      const float k0 = bf16_to_f32(ks[i][hd]) * __expf(gl - gc[i]);
+      const float k0 = bf16_to_f32(ks[i][hd]) * ek[i];
+      const f32x4 v0 = *reinterpret_cast<const f32x4*>(&vn[i][hc]), v1 = *reinterpret_cast<const f32x4*>(&vn[i][hc + 4]);
 #pragma unroll
-      for (int x = 0; x < 8; ++x) hn[x] = fmaf(k0, vn[i][hc + x], hn[x]);
+      for (int x = 0; x < 4; ++x) {
+        hn[x] = fmaf(k0, v0[x], hn[x]);
+        hn[x + 4] = fmaf(k0, v1[x], hn[x + 4]);
+      }
     }
     __syncthreads();  // every thread has read the old state (o used only vn and at)
 #pragma unroll
