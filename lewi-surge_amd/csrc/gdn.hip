@@ -59,8 +59,8 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
                                                         const bf16_t* __restrict__ beta, int T, int H, float qscale,
                                                         bf16_t* __restrict__ u_out, bf16_t* __restrict__ w_out,
                                                         float* __restrict__ attn_out, float* __restrict__ gcum_out) {
-  // k, and q (then v once the attention is done); k beta is formed from k where it is used.  68 KB of LDS: two
-  // workgroups per CU.
+  // k (then k beta) and q (then v beta once the attention is done); in the S product k beta is formed from k where it
+  // is used.  68 KB of LDS: two workgroups per CU.
   __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], qs[GC][GP];
   __shared__ float Sm[GC][GC + 1], Am[GC][GC + 1];
   __shared__ float gc[GC], eg[GC], bt[GC];
@@ -129,7 +129,23 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
       }
   }
   __syncthreads();
-  load_tile(qs, v, row0, T, t0, H, h, 1.f);  // v replaces q (every read of q is done)
+  // every read of q and of raw k is done: v beta replaces q and k beta replaces k, in the compute dtype
+  // (gdn_fast.py:78, 87), formed once here for the u and w products below
+  for (int e = tid; e < GC * (GD / 8); e += GTH) {
+    const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (t0 + i < T) raw = *reinterpret_cast<const u32x4*>(v + ((row0 + t0 + i) * H + h) * GD + c);
+    float f[8], kf[8];
+    unpack8g(raw, f);
+    unpack8g(*reinterpret_cast<const u32x4*>(&ks[i][c]), kf);
+    const float bi = bt[i];
+    *reinterpret_cast<u32x4*>(&qs[i][c]) =
+        u32x4{pack_bf16x2(f[0] * bi, f[1] * bi), pack_bf16x2(f[2] * bi, f[3] * bi), pack_bf16x2(f[4] * bi, f[5] * bi),
+              pack_bf16x2(f[6] * bi, f[7] * bi)};
+    *reinterpret_cast<u32x4*>(&ks[i][c]) =
+        u32x4{pack_bf16x2(kf[0] * bi, kf[1] * bi), pack_bf16x2(kf[2] * bi, kf[3] * bi),
+              pack_bf16x2(kf[4] * bi, kf[5] * bi), pack_bf16x2(kf[6] * bi, kf[7] * bi)};
+  }
   // A = (I + S)^-1, row by row: A[i][c] = -sum_{c <= j < i} S[i][j] A[j][c] (c < i), A[i][i] = 1, 0 above.  Eight
   // threads per column split the sum (fixed order: the partial sums are combined by an xor butterfly).
   {
@@ -150,14 +166,8 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
     float ua[2][8] = {}, wa[2][8] = {};
     for (int j = 0; j < GC; ++j) {
       float vb8[8], kb8[8];
-      unpack8g(*reinterpret_cast<const u32x4*>(&qs[j][c0]), vb8);
-      unpack8g(*reinterpret_cast<const u32x4*>(&ks[j][c0]), kb8);
-      const float bj = bt[j];
-#pragma unroll
-      for (int x = 0; x < 8; ++x) {  // v beta and k beta in the compute dtype (gdn_fast.py:78, 87)
-        vb8[x] = bf16_to_f32(f32_to_bf16(vb8[x] * bj));
-        kb8[x] = bf16_to_f32(f32_to_bf16(kb8[x] * bj));
-      }
+      unpack8g(*reinterpret_cast<const u32x4*>(&qs[j][c0]), vb8);  // v beta
+      unpack8g(*reinterpret_cast<const u32x4*>(&ks[j][c0]), kb8);  // k beta
       const float e = eg[j];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
