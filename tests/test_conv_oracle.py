@@ -47,3 +47,15 @@ def test_conv_backward_adjoints():
     # dx is the same causal convolution run backwards in time: dx[t] = sum_j w[j] dy[t + K-1 - j]
     flip = mo.causal_conv1d(dy[:, ::-1], w)[:, ::-1]
     assert np.allclose(dx, flip)
+
+
+def test_applies_mirrors_reference_conditions():
+    # modal/fast_conv.py:17-22: 1-D kernel, depthwise (groups == in == out), CAUSAL padding, rank-3 input, no bias,
+    # dilation and stride 1; anything else goes to the original nnx.Conv
+    import fast_conv
+    ok = dict(kernel_size=(4,), feature_group_count=64, in_features=64, out_features=64, padding="CAUSAL", ndim=3)
+    assert fast_conv.applies(**ok)
+    assert fast_conv.applies(**dict(ok, kernel_size=4))
+    for bad in (dict(kernel_size=(3, 3)), dict(feature_group_count=1), dict(out_features=128), dict(padding="SAME"),
+                dict(ndim=4), dict(has_bias=True), dict(dilation=2), dict(strides=(2,))):
+        assert not fast_conv.applies(**dict(ok, **bad)), bad
