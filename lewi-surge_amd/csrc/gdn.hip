@@ -63,6 +63,7 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
   // is used.  68 KB of LDS: two workgroups per CU.
   __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], qs[GC][GP];
   __shared__ float Sm[GC][GC + 1], Am[GC][GC + 1];
+  __shared__ float Tb[GC / 16 - 1][16][17];  // the blocked inverse's partial products of one level
   __shared__ float gc[GC], eg[GC], bt[GC];
   const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z, N = gridDim.x;
   const int tid = threadIdx.x, t0 = n * GC;
@@ -146,17 +147,41 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
         u32x4{pack_bf16x2(kf[0] * bi, kf[1] * bi), pack_bf16x2(kf[2] * bi, kf[3] * bi),
               pack_bf16x2(kf[4] * bi, kf[5] * bi), pack_bf16x2(kf[6] * bi, kf[7] * bi)};
   }
-  // A = (I + S)^-1, row by row: A[i][c] = -sum_{c <= j < i} S[i][j] A[j][c] (c < i), A[i][i] = 1, 0 above.  Eight
-  // threads per column split the sum (fixed order: the partial sums are combined by an xor butterfly).
+  // A = (I + S)^-1 in 16 x 16 blocks (L = I + S is unit lower triangular; its off-diagonal blocks are those of S):
+  //  1. the four diagonal blocks A_II = L_II^-1 at once, row by row: A[i][c] = -sum_{c <= j < i} S[i][j] A[j][c]
+  //     (c < i), A[i][i] = 1, 0 above; eight threads per column split the sum (combined by an xor butterfly);
+  //  2. block row I = 1 .. 3: A_IJ = -A_II sum_{K=J}^{I-1} S_IK A_KJ for every J < I (from L A = I), blocks above the
+  //     diagonal 0.  22 workgroup barriers where the plain row-by-row substitution takes 64.
   {
-    const int c = tid / 8, part = tid % 8;
-    for (int i = 0; i < GC; ++i) {
+    for (int e = tid; e < GC * GC; e += GTH) {
+      const int r = e / GC, c = e % GC;
+      if (r / 16 != c / 16) Am[r][c] = 0.f;  // off-diagonal blocks: filled below (lower) or zero (upper)
+    }
+    const int blk = tid / 128, c = (tid % 128) / 8, part = tid % 8, o = 16 * blk;
+    for (int i = 0; i < 16; ++i) {
       float s = 0.f;
-      for (int j = c + part; j < i; j += 8) s = fmaf(Sm[i][j], Am[j][c], s);
+      for (int j = c + part; j < i; j += 8) s = fmaf(Sm[o + i][o + j], Am[o + j][o + c], s);
       s += __shfl_xor(s, 1, 64);
       s += __shfl_xor(s, 2, 64);
       s += __shfl_xor(s, 4, 64);
-      if (part == 0) Am[i][c] = c < i ? -s : (c == i ? 1.f : 0.f);
+      if (part == 0) Am[o + i][o + c] = c < i ? -s : (c == i ? 1.f : 0.f);
+      __syncthreads();
+    }
+    for (int I = 1; I < GC / 16; ++I) {
+      for (int e = tid; e < I * 256; e += GTH) {  // T_J = sum_{K=J}^{I-1} S_IK A_KJ
+        const int J = e / 256, r = (e % 256) / 16, cc = e % 16;
+        float t = 0.f;
+        for (int m = 16 * J; m < 16 * I; ++m) t = fmaf(Sm[16 * I + r][m], Am[m][16 * J + cc], t);
+        Tb[J][r][cc] = t;
+      }
+      __syncthreads();
+      for (int e = tid; e < I * 256; e += GTH) {  // A_IJ = -A_II T_J
+        const int J = e / 256, r = (e % 256) / 16, cc = e % 16;
+        float t = 0.f;
+#pragma unroll
+        for (int m = 0; m < 16; ++m) t = fmaf(Am[16 * I + r][16 * I + m], Tb[J][m][cc], t);
+        Am[16 * I + r][16 * J + cc] = -t;
+      }
       __syncthreads();
     }
   }
