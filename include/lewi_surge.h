@@ -38,7 +38,7 @@ enum {
   LSURGE_ERR_WORKSPACE = -4    /* workspace too small */
 };
 
-#define LSURGE_ABI_VERSION 1
+#define LSURGE_ABI_VERSION 2
 #define LSURGE_BLOCK_ROWS 128 /* rows per padded expert block */
 
 int lsurge_abi_version(void);
@@ -83,7 +83,9 @@ int lsurge_combine_bwd(const void* y, int y_dtype, const int32_t* pos, const flo
                        int64_t d, const void* g, int g_dtype, void* dy, float* dw, lsurge_stream_t stream);
 
 /* inv[idx[i]] = i for a permutation idx of [0, m).  Replaces jnp.argsort(idx) in
- * moe_permute._permute_rows_bwd (modal/moe_permute.py:325-326). */
+ * moe_permute._permute_rows_bwd (modal/moe_permute.py:325-326).  For an idx that is not a permutation: entries
+ * outside [0, m) are skipped, entries of inv that no idx hits are m (so a gather through inv gives zero rows
+ * there), and of duplicated entries one unspecified i is kept.  No write ever leaves inv. */
 int lsurge_invert_permutation(const int32_t* idx, int64_t m, int32_t* inv, lsurge_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------
@@ -127,23 +129,23 @@ int lsurge_build_layout(const int32_t* flat, int64_t m, int64_t num_experts, int
  * ------------------------------------------------------------------------------------------------ */
 
 /* Dropless ragged_dot: out[r] = lhs[r] @ rhs[e(r)] for r < sum(group_sizes), 0 for the rows after.
- * lhs: [m, kdim] bf16 rows sorted by group; rhs: [e, kdim, n] bf16; group_sizes: [e] int32 (device);
- * out: [m, n] of out_dtype (LSURGE_BF16, or LSURGE_F32 for preferred_element_type=float32).
- * kdim % 8 == 0, n % 8 == 0.
+ * lhs: [m, kdim] rows sorted by group and rhs: [e, kdim, n], both of in_dtype (LSURGE_BF16 or LSURGE_F16; f32
+ * operands return LSURGE_ERR_DTYPE); group_sizes: [e] int32 (device); out: [m, n] of out_dtype (in_dtype, or
+ * LSURGE_F32 for preferred_element_type=float32); f32 accumulation.  kdim % 8 == 0, n % 8 == 0.
  * Replaces padded_gmm.padded_ragged_dot (modal/padded_gmm.py:45-69) / jax.lax.ragged_dot. */
 size_t lsurge_ragged_dot_workspace_bytes(int64_t m, int64_t e);
 int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_sizes, int64_t m, int64_t kdim,
-                      int64_t n, int64_t e, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
-                      lsurge_stream_t stream);
+                      int64_t n, int64_t e, int in_dtype, void* out, int out_dtype, void* workspace,
+                      size_t workspace_bytes, lsurge_stream_t stream);
 
-/* Backward of lsurge_ragged_dot for upstream g [m, n] bf16: dlhs [m, kdim] bf16 (rows past the groups
+/* Backward of lsurge_ragged_dot for upstream g [m, n] of in_dtype: dlhs [m, kdim] in_dtype (rows past the groups
  * = 0) and drhs [e, kdim, n] f32.  Replaces the VJP of padded_gmm.padded_ragged_dot
  * (modal/padded_gmm.py:35-39 + XLA autodiff of the einsum at 67-68).
  * Workspace: lsurge_ragged_dot_bwd_workspace_bytes(m, kdim, n, e) lets drhs cut hot groups into row chunks
  * (e <= 256); the forward's lsurge_ragged_dot_workspace_bytes(m, e) is also accepted (one slice per group). */
 size_t lsurge_ragged_dot_bwd_workspace_bytes(int64_t m, int64_t kdim, int64_t n, int64_t e);
 int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group_sizes, const void* g,
-                          int64_t m, int64_t kdim, int64_t n, int64_t e, void* dlhs, float* drhs,
+                          int64_t m, int64_t kdim, int64_t n, int64_t e, int in_dtype, void* dlhs, float* drhs,
                           void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------
@@ -291,6 +293,16 @@ size_t lsurge_gdn_chunked_workspace_bytes(int64_t b, int64_t t, int64_t h, int64
 int lsurge_gdn_chunked_fwd(const void* q, const void* k, const void* v, const float* g, const void* beta, int64_t b,
                            int64_t t, int64_t h, int64_t dk, int64_t dv, const float* h0, void* o, float* h_out,
                            void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Test hooks (no reference counterpart): failure injection for the error paths.
+ * ------------------------------------------------------------------------------------------------ */
+/* Arm a host-side failure: the nth launch (counting from 1) of the kernel with profiler id kernel_id
+ * (lsurge_prof_kernel_name) returns LSURGE_ERR_LAUNCH without launching; nth = 0 disarms.  Process-wide. */
+int lsurge_test_fail_launch(int kernel_id, int nth);
+/* 1 when every helper stream of the current device has finished its work (hipStreamQuery), 0 when one is
+ * still busy, -1 when no helper stream exists yet. */
+int lsurge_test_helpers_idle(void);
 
 /* ------------------------------------------------------------------------------------------------
  * Live per-kernel timing with HIP events on the launch stream (used by the benchmark).

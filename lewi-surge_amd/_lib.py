@@ -44,6 +44,8 @@ class MoeSavedViews(ctypes.Structure):
 # name -> (restype, argtypes)
 _SIGS = {
     "lsurge_abi_version": (_int, []),
+    "lsurge_test_fail_launch": (_int, [_int, _int]),
+    "lsurge_test_helpers_idle": (_int, []),
     "lsurge_last_error": (ctypes.c_char_p, []),
     "lsurge_set_concurrency": (_int, [_int]),
     "lsurge_get_concurrency": (_int, []),
@@ -59,8 +61,8 @@ _SIGS = {
     "lsurge_layout_workspace_bytes": (_sz, [_i64, _i64]),
     "lsurge_build_layout": (_int, [_p, _i64, _i64] + [_p] * 10 + [_p, _sz, _p]),
     "lsurge_ragged_dot_workspace_bytes": (_sz, [_i64, _i64]),
-    "lsurge_ragged_dot": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _int, _p, _sz, _p]),
-    "lsurge_ragged_dot_bwd": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _sz, _p]),
+    "lsurge_ragged_dot": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _int, _p, _int, _p, _sz, _p]),
+    "lsurge_ragged_dot_bwd": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _int, _p, _p, _p, _sz, _p]),
     "lsurge_ragged_dot_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "lsurge_moe_saved_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
     "lsurge_moe_fwd_workspace_bytes": (_sz, [ctypes.POINTER(MoeShape)]),

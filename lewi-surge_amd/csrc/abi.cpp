@@ -129,6 +129,26 @@ void fork_release(ForkSet* f) {
   if (f->dev >= 0) g_fork[f->dev].mu.unlock();
 }
 
+// the last kForkStreams events of a set are reserved for this join (the layer's own joins use the first ones)
+void fork_join_all(ForkSet* f, hipStream_t main) {
+  for (int i = 0; i < kForkStreams; ++i) {
+    if (f->side[i] == main) continue;
+    hipEvent_t ev = f->ev[kForkEvents - kForkStreams + i];
+    if (hipEventRecord(ev, f->side[i]) == hipSuccess) (void)hipStreamWaitEvent(main, ev, 0);
+  }
+}
+
+// ------------------------------------------------------------------------------ test hooks
+static std::atomic<int> g_fail_kid{-1};
+static std::atomic<int> g_fail_left{0};
+
+bool test_fail_hit(int kid) {
+  if (g_fail_kid.load(std::memory_order_relaxed) != kid) return false;
+  if (g_fail_left.fetch_sub(1) != 1) return false;
+  g_fail_kid.store(-1);
+  return true;
+}
+
 int stream_after(hipStream_t waiter, hipStream_t producer, hipEvent_t ev) {
   if (waiter == producer) return LSURGE_OK;
   hipError_t e = hipEventRecord(ev, producer);
@@ -151,6 +171,24 @@ int lsurge_set_concurrency(int on) {
 }
 int lsurge_get_concurrency(void) { return g_concurrency.load(); }
 const char* lsurge_last_error(void) { return g_err; }
+
+int lsurge_test_fail_launch(int kernel_id, int nth) {
+  if (kernel_id < -1 || kernel_id >= KID_COUNT || nth < 0) return set_error(LSURGE_ERR_INVALID, "bad test hook arguments");
+  g_fail_left.store(nth);
+  g_fail_kid.store(nth > 0 ? kernel_id : -1);
+  return LSURGE_OK;
+}
+
+int lsurge_test_helpers_idle(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+  DeviceFork& d = g_fork[dev];
+  std::lock_guard<std::mutex> lk(d.mu);
+  if (!d.ready) return -1;
+  for (int i = 0; i < kForkStreams; ++i)
+    if (hipStreamQuery(d.side[i]) != hipSuccess) return 0;
+  return 1;
+}
 
 int lsurge_prof_kernel_count(void) { return KID_COUNT; }
 const char* lsurge_prof_kernel_name(int id) { return (id >= 0 && id < KID_COUNT) ? g_names[id] : ""; }

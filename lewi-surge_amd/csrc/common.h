@@ -74,6 +74,11 @@ struct ForkSet {
 };
 int fork_acquire(ForkSet* f, hipStream_t main);
 void fork_release(ForkSet* f);
+// make `main` wait for everything enqueued so far on every helper of f (the error path of a forked call)
+void fork_join_all(ForkSet* f, hipStream_t main);
+// test hook: true when this launch of kernel id `kid` is the one lsurge_test_fail_launch armed (it then fails
+// without launching)
+bool test_fail_hit(int kid);
 // enqueue on `waiter` a wait for everything enqueued so far on `producer`
 int stream_after(hipStream_t waiter, hipStream_t producer, hipEvent_t ev);
 hipError_t prof_mark_begin(int kernel_id, hipStream_t s);
@@ -118,6 +123,8 @@ enum {
 // RAII-free launch bracket used by the layer entry points.
 #define LSURGE_LAUNCH(kid, stream, ...)             \
   do {                                              \
+    if (lsurge::test_fail_hit(kid))                 \
+      return lsurge::set_error(LSURGE_ERR_LAUNCH, "%s: launch failure injected by lsurge_test_fail_launch", #kid); \
     (void)lsurge::prof_mark_begin((kid), (stream)); \
     __VA_ARGS__;                                    \
     (void)lsurge::prof_mark_end((kid), (stream));   \

@@ -269,13 +269,22 @@ static int max_blocks_of(const GemmBlocks& g) {
 // launch gemm_rows_kernel with the tile config that matches the row tiles of g (column tiles: BN output columns, or
 // BN / 2 for the SwiGLU forward)
 template <int BMODE, int EPI, bool F8 = false>
-static int launch_rows(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t s) {
+static int launch_rows(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t s, int et = LSURGE_BF16) {
   LSURGE_REQUIRE(g.tile_rows == 128 || g.tile_rows == 256, "grouped GEMM: tile_rows=%d must be 128 or 256", g.tile_rows);
   a.max_tiles = max_blocks_of(g);
   a.n_tiles = (int)((a.N + (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN) - 1) / (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN));
   if (a.max_tiles == 0) return LSURGE_OK;
   const dim3 grid(pad8((int64_t)a.n_tiles * a.max_tiles));
   // FP8: 256-row tiles on the ping-pong kernel, 128-row tiles on the 4-wave kernel with the single-buffered K loop
+  if constexpr (EPI == EPI_STORE && !F8) {
+    if (et == LSURGE_F16) {  // f16 operands (the ragged_dot entry points): 4-wave kernel
+      LSURGE_REQUIRE(g.tile_rows == 128, "grouped GEMM: f16 operands take 128-row tiles");
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<Cfg, BMODE, EPI, false, LSURGE_F16>), grid,
+                                               dim3(Cfg::GT), 0, s, a));
+      return LSURGE_OK;
+    }
+  }
+  LSURGE_REQUIRE(et == LSURGE_BF16 || (EPI == EPI_STORE && !F8), "grouped GEMM: f16 operands need the plain epilogue");
   if constexpr (F8) {
     if (g.tile_rows == 256)
       LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_rows_kernel<CfgPP, BMODE, EPI, F8>), grid, dim3(CfgPP::GT), 0, s, a));
@@ -291,7 +300,7 @@ static int launch_rows(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t s)
 // C[rows, N] = A[rows, K] @ B_e where B_e is [K, N] (n-major) -- forward projections
 int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, int64_t ldb,
                  int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32,
-                 const ExtraExpert& xe) {
+                 const ExtraExpert& xe, int et) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_kn")) return rc;
   if (int rc = check_desc(std::max<int64_t>(g.tile_rows * lda, K * ldb) * 2, "gemm_rows_kn")) return rc;
   RowsArgs a{};
@@ -303,7 +312,7 @@ int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
   a.dense_rows = g.dense_rows;
   a.x_expert = xe.expert; a.Bx = (const bf16_t*)xe.B; a.B2x = (const bf16_t*)xe.B2;
   LSURGE_REQUIRE(xe.expert < 0 || (xe.B && (xe.B2 || !a.B2)), "grouped GEMM: extra expert weights missing");
-  return launch_rows<B_KN, EPI_STORE>(kid, g, a, s);
+  return launch_rows<B_KN, EPI_STORE>(kid, g, a, s, et);
 }
 
 // h = silu(A @ Bg) * (A @ Bu); also stores g, u.  Bg, Bu: [K, N] per expert.  With a gather (gather.rows set),
@@ -335,7 +344,7 @@ int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t ld
 int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
                  int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
                  bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32,
-                 const ExtraExpert& xe) {
+                 const ExtraExpert& xe, int et) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_nk")) return rc;
   if (int rc = check_desc(std::max<int64_t>(g.tile_rows * lda, N * ldb) * 2, "gemm_rows_nk")) return rc;
   LSURGE_REQUIRE(!B2 || (k_split > 0 && k_split % BK == 0), "gemm_rows_nk: k_split must be a multiple of %d", BK);
@@ -349,7 +358,7 @@ int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
   a.dense_rows = g.dense_rows;
   a.x_expert = xe.expert; a.Bx = (const bf16_t*)xe.B; a.B2x = (const bf16_t*)xe.B2;
   LSURGE_REQUIRE(xe.expert < 0 || (xe.B && (xe.B2 || !a.B2)), "grouped GEMM: extra expert weights missing");
-  return swiglu_bwd ? launch_rows<B_NK, EPI_SWIGLU_BWD>(kid, g, a, s) : launch_rows<B_NK, EPI_STORE>(kid, g, a, s);
+  return swiglu_bwd ? launch_rows<B_NK, EPI_SWIGLU_BWD>(kid, g, a, s, et) : launch_rows<B_NK, EPI_STORE>(kid, g, a, s, et);
 }
 
 // FP8 row GEMM: C[rows, N] = (A[rows, K] @ B_e^T) * a_sinv[0] * b_sinv[e], A and B_e = [N, K] in E4M3 (K
@@ -394,7 +403,7 @@ size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S) {
 int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
                int64_t max_rows, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N, float* C,
                float* C2, int64_t n_split, int64_t ldc, int64_t c_estride, int S, void* ws, size_t ws_bytes,
-               hipStream_t s, const RowGather& gather) {
+               hipStream_t s, const RowGather& gather, int et) {
   if (int rc = check_gemm_shape(I, N, "gemm_wgrad")) return rc;
   if (int rc = check_desc(max_rows * std::max(lda, ldb) * 2, "gemm_wgrad")) return rc;
   LSURGE_REQUIRE(S >= 1 && E >= 1, "gemm_wgrad: bad S/E");
@@ -416,7 +425,10 @@ int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32
     a.part = (float*)ws;
   }
   const int64_t tiles = (int64_t)E * S * a.i_tiles * a.n_tiles;
-  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel<Cfg>, dim3(pad8(tiles)), dim3(GT), 0, s, a));
+  if (et == LSURGE_F16)
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_wgrad_kernel<Cfg, LSURGE_F16>), dim3(pad8(tiles)), dim3(GT), 0, s, a));
+  else
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel<Cfg>, dim3(pad8(tiles)), dim3(GT), 0, s, a));
   if (S > 1) {
     const int64_t total = (int64_t)E * I * N;
     const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
@@ -479,7 +491,7 @@ size_t wgrad_chunked_workspace_bytes(const WgradChunkPlan& p, int64_t I, int64_t
 int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, const void* A, int64_t lda,
                        const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
                        int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s,
-                       const RowGather& gather, const ExtraOut& xo) {
+                       const RowGather& gather, const ExtraOut& xo, int et) {
   if (int rc = check_gemm_shape(I, N, "gemm_wgrad_chunked")) return rc;
   LSURGE_REQUIRE(xo.expert < 0 || (xo.C && (xo.C2 || !C2)), "gemm_wgrad_chunked: extra expert outputs missing");
   if (int rc = check_desc(max_rows * std::max(lda, ldb) * 2, "gemm_wgrad_chunked")) return rc;
@@ -503,7 +515,10 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
   a.i_tiles = (int)((I + BM - 1) / BM);
   a.n_tiles = (int)((N + BN - 1) / BN);
   const int64_t tiles = (int64_t)pad8(ch.max_chunks) * a.i_tiles * a.n_tiles;  // see the chunk tile order
-  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel<Cfg>, dim3((unsigned)tiles), dim3(GT), 0, s, a));
+  if (et == LSURGE_F16)
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_wgrad_kernel<Cfg, LSURGE_F16>), dim3((unsigned)tiles), dim3(GT), 0, s, a));
+  else
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel<Cfg>, dim3((unsigned)tiles), dim3(GT), 0, s, a));
   // grid-stride over the split experts' elements: two experts' worth of threads per pass
   const unsigned grid = (unsigned)std::min<int64_t>(2 * ((I * N / 4 + 255) / 256), 2048);
   LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
@@ -573,10 +588,13 @@ static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_
 }
 
 int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_sizes, int64_t m, int64_t kdim, int64_t n,
-                      int64_t e, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
+                      int64_t e, int in_dtype, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
                       lsurge_stream_t stream) {
   LSURGE_REQUIRE(m >= 0 && e >= 1 && m < (1ll << 31), "ragged_dot: bad m/e");
-  LSURGE_REQUIRE(out_dtype == LSURGE_BF16 || out_dtype == LSURGE_F32, "ragged_dot: out_dtype must be bf16 or f32");
+  if (in_dtype != LSURGE_BF16 && in_dtype != LSURGE_F16)
+    return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot: operands must be bf16 or f16 (got dtype %d)", in_dtype);
+  if (out_dtype != in_dtype && out_dtype != LSURGE_F32)
+    return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot: out_dtype must be the operand dtype or f32");
   if (m == 0) return LSURGE_OK;
   LSURGE_REQUIRE(lhs && rhs && group_sizes && out, "ragged_dot: null pointer");
   hipStream_t s = (hipStream_t)stream;
@@ -584,7 +602,9 @@ int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_siz
   int32_t *total, *e_row0, *e_rows;
   if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0, &e_rows)) return rc;
   const bool f32 = out_dtype == LSURGE_F32;
-  if (int rc = lsurge::gemm_rows_kn(KID_MISC, g, lhs, kdim, rhs, n, kdim * n, kdim, n, out, n, s, f32)) return rc;
+  if (int rc = lsurge::gemm_rows_kn(KID_MISC, g, lhs, kdim, rhs, n, kdim * n, kdim, n, out, n, s, f32,
+                                    lsurge::ExtraExpert(), in_dtype))
+    return rc;
   LSURGE_LAUNCH(KID_MISC, s,
                 hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, out, m, n, f32 ? 4 : 2, total));
   return LSURGE_OK;
@@ -611,9 +631,11 @@ int lsurge_ragged_dot_fp8(const void* lhs_q, const float* lhs_scale_inv, const v
 }
 
 int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group_sizes, const void* g, int64_t m,
-                          int64_t kdim, int64_t n, int64_t e, void* dlhs, float* drhs, void* workspace,
+                          int64_t kdim, int64_t n, int64_t e, int in_dtype, void* dlhs, float* drhs, void* workspace,
                           size_t workspace_bytes, lsurge_stream_t stream) {
   LSURGE_REQUIRE(m >= 0 && e >= 1 && m < (1ll << 31), "ragged_dot_bwd: bad m/e");
+  if (in_dtype != LSURGE_BF16 && in_dtype != LSURGE_F16)
+    return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot_bwd: operands must be bf16 or f16 (got dtype %d)", in_dtype);
   LSURGE_REQUIRE(lhs && rhs && group_sizes && g && dlhs && drhs, "ragged_dot_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   lsurge::GemmBlocks gb;
@@ -622,7 +644,7 @@ int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group
   // dlhs[r] = g[r] @ rhs[e]^T : rhs[e] is [K, N] = k-major storage of the [N -> K] operand
   if (m > 0) {
     if (int rc = lsurge::gemm_rows_nk(KID_MISC, gb, g, n, rhs, nullptr, 0, n, kdim * n, n, kdim, dlhs, kdim, false,
-                                      nullptr, nullptr, 0, s, false))
+                                      nullptr, nullptr, 0, s, false, lsurge::ExtraExpert(), in_dtype))
       return rc;
     LSURGE_LAUNCH(KID_MISC, s,
                   hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, dlhs, m, kdim, 2, total));
@@ -639,10 +661,11 @@ int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group
     lsurge::WgradChunks ch;
     if (int rc = lsurge::build_wgrad_chunks(e_rows, e_row0, (int)e, p, table, &ch, s, -1, 0, 1)) return rc;
     return lsurge::gemm_wgrad_chunked(KID_MISC, ch, (int)e, m, lhs, kdim, g, n, kdim, n, drhs, nullptr, 0, n, kdim * n,
-                                      base + off, lsurge::wgrad_chunked_workspace_bytes(p, kdim, n), s);
+                                      base + off, lsurge::wgrad_chunked_workspace_bytes(p, kdim, n), s,
+                                      lsurge::RowGather(), lsurge::ExtraOut(), in_dtype);
   }
   return lsurge::gemm_wgrad(KID_MISC, (int)e, e_row0, 1, e_rows, 0, m, lhs, kdim, g, n, kdim, n, drhs, nullptr, 0, n,
-                            kdim * n, 1, nullptr, 0, s, lsurge::RowGather());
+                            kdim * n, 1, nullptr, 0, s, lsurge::RowGather(), in_dtype);
 }
 
 }  // extern "C"

@@ -139,8 +139,16 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 // The kernels call it with P = the weight fragment and Q = the activation fragment, so the accumulator holds
 // C^T: lane l owns activation row l%32 and output columns 8(r/4) + 4(l/32) + r%4 -- four consecutive columns
 // per register quad.
+// ET = LSURGE_F16: the same fragments hold IEEE half bit patterns (v_mfma_f32_32x32x16_f16, same operand layout).
+template <int ET = LSURGE_BF16>
 __device__ __forceinline__ f32x16 mfma32(bf16x8 p, bf16x8 q, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
+  if constexpr (ET == LSURGE_F16) {
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, p), __builtin_bit_cast(f16x8, q), c, 0, 0,
+                                                  0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
+  }
 }
 
 // D[32 x 32] += P[32 x 64] Q[64 x 32] with E4M3 operands (formats 0 / 0); with zero scale operands the compiler
@@ -388,6 +396,18 @@ __device__ __forceinline__ void st_bf16x8(bf16_t* p, const float* v) {
   *reinterpret_cast<u32x4*>(p) =
       u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
 }
+// 8 f32 -> 8 16-bit values of element type ET (round to nearest even), one 16-byte store
+template <int ET>
+__device__ __forceinline__ void st_x8(bf16_t* p, const float* v) {
+  if constexpr (ET == LSURGE_F16) {
+    uint32_t u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = (uint32_t)f32_to_f16(v[2 * i]) | ((uint32_t)f32_to_f16(v[2 * i + 1]) << 16);
+    *reinterpret_cast<u32x4*>(p) = u32x4{u[0], u[1], u[2], u[3]};
+  } else {
+    st_bf16x8(p, v);
+  }
+}
 
 // 1 / (1 + e^-g) with the hardware reciprocal (about 1 ulp): plenty for bf16 outputs, and it keeps the
 // epilogue short
@@ -420,10 +440,11 @@ struct FragSet {
 };
 
 // =====================================================================================================
-template <class Cfg, int BMODE, int EPI, bool F8 = false>
+template <class Cfg, int BMODE, int EPI, bool F8 = false, int ET = LSURGE_BF16>
 __global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW * Cfg::OCC / 4)))
 void gemm_rows_kernel(RowsArgs a) {
   static_assert(!F8 || (BMODE == B_NK && Cfg::BK == 32), "FP8: both operands K-contiguous, 64-value stages");
+  static_assert(ET == LSURGE_BF16 || (EPI == EPI_STORE && !F8), "f16 operands: plain store epilogue only");
   constexpr int UE = F8 ? 2 : 1;  // operand elements per 2-byte copy unit
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, ST = Cfg::ST;
   constexpr int TM = Cfg::TM, TN = Cfg::TN, FM = Cfg::FM, FN = Cfg::FN, SP = Cfg::SP;
@@ -595,7 +616,7 @@ void gemm_rows_kernel(RowsArgs a) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if constexpr (F8) acc[i][j] = mfma32_f8(f.w[j], f.x[i], acc[i][j]);
-        else acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
+        else acc[i][j] = mfma32<ET>(f.w[j], f.x[i], acc[i][j]);
       }
   };
   // a wave whose rows or output columns all lie outside the tile (a one-block tile of a 256-row table, the N tail)
@@ -681,7 +702,7 @@ void gemm_rows_kernel(RowsArgs a) {
             *reinterpret_cast<f32x4*>(a.Cf + gr * a.ldc + col + 4) = v1;
           } else {
             const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            st_bf16x8(a.C + gr * a.ldc + col, v);
+            st_x8<ET>(a.C + gr * a.ldc + col, v);
           }
         } else {  // EPI_SWIGLU_BWD: v = dH; C row = [dG (N cols) | dU (N cols)]
           const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
@@ -713,7 +734,7 @@ void gemm_rows_kernel(RowsArgs a) {
 // =====================================================================================================
 // Weight gradient C_e[I, N] = A_e^T B_e, reduced over the rows of expert e: both operands are row-major
 // [rows, .] (the reduction dim is the slow one), so both are staged N-major and read with the transpose read.
-template <class Cfg>
+template <class Cfg, int ET = LSURGE_BF16>
 __global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW * Cfg::OCC / 4)))
 void gemm_wgrad_kernel(WgradArgs a) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, ST = Cfg::ST;
@@ -884,7 +905,7 @@ void gemm_wgrad_kernel(WgradArgs a) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(f.w[j], f.x[i], acc[i][j]);
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma32<ET>(f.w[j], f.x[i], acc[i][j]);
   };
   if (nk > 0) {  // waves outside the tile: copies and barriers only, as in gemm_rows_kernel
     if (i0 + wm * TM < I && n0 + wn * TN < N) run_k_loop<Cfg, F>(nk, wave, issue, load, mma);

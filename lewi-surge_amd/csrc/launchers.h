@@ -55,7 +55,8 @@ int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* sl
 int launch_transpose_bf16(const void* a, int R, int C, void* at, hipStream_t s);
 int launch_scatter_dlogits(const float* dl, const int32_t* sel, int64_t T, int E, int k, void* dlog, hipStream_t s);
 
-// ---- grouped GEMMs (gemm.hip)
+// ---- grouped GEMMs (gemm.hip).  et: element type of the 16-bit operands (LSURGE_BF16, or LSURGE_F16 for the plain-store
+// row GEMMs and the weight gradients of the ragged_dot entry points).
 // Row tiles: the padded 128-row expert blocks (blk_expert set) or a dense matrix of dense_rows rows.
 struct GemmBlocks {
   const int32_t* blk_expert;
@@ -83,7 +84,7 @@ struct ExtraExpert {
 };
 int gemm_rows_kn(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, int64_t ldb,
                  int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc, hipStream_t s, bool out_f32 = false,
-                 const ExtraExpert& xe = ExtraExpert());
+                 const ExtraExpert& xe = ExtraExpert(), int et = LSURGE_BF16);
 int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* Bg, const void* Bu,
                          int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* H, void* Gs, void* Us,
                          int64_t ldh, hipStream_t s, const RowGather& gather = RowGather(),
@@ -91,7 +92,7 @@ int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t ld
 int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
                  int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
                  bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false,
-                 const ExtraExpert& xe = ExtraExpert());
+                 const ExtraExpert& xe = ExtraExpert(), int et = LSURGE_BF16);
 // FP8 (E4M3) row GEMM, both operands K-contiguous (B_e stored [N, K]); byte pitches; see gemm.hip
 int gemm_rows_f8(int kid, const GemmBlocks& g, const void* A, int64_t lda, const float* a_sinv, const void* B,
                  const void* B2, int64_t ldb, int64_t b_estride, const float* b_sinv, const float* b2_sinv, int64_t K,
@@ -101,7 +102,7 @@ size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S);
 int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
                int64_t max_rows, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N,
                float* C, float* C2, int64_t n_split, int64_t ldc, int64_t c_estride, int S, void* ws, size_t ws_bytes,
-               hipStream_t s, const RowGather& gather = RowGather());
+               hipStream_t s, const RowGather& gather = RowGather(), int et = LSURGE_BF16);
 
 // Chunked routed weight gradient: every expert's rows cut into chunks of at most R rows (see WgradArgs), so a
 // hot expert spreads over many workgroups; split experts are reduced from f32 partial slots in chunk order.
@@ -132,7 +133,7 @@ size_t wgrad_chunked_workspace_bytes(const WgradChunkPlan& p, int64_t I, int64_t
 int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, const void* A, int64_t lda,
                        const void* B, int64_t ldb, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
                        int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s,
-                       const RowGather& gather = RowGather(), const ExtraOut& xo = ExtraOut());
+                       const RowGather& gather = RowGather(), const ExtraOut& xo = ExtraOut(), int et = LSURGE_BF16);
 
 // ---- FP8 quantisation (fp8.hip), current scaling to OCP E4M3
 size_t fp8_partial_bytes(int64_t groups);  // amax partials of fp8_quantize_impl

@@ -300,9 +300,18 @@ __global__ __launch_bounds__(1024) void layout_rank_kernel(
   }
 }
 
+// inv[v] = m for every v (the entries that no index hits keep it; a gather through inv gives zero rows there)
+__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t m, int32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < m) p[i] = v;
+}
+// inv[idx[i]] = i; entries of idx outside [0, m) are skipped, so no index can write outside inv
 __global__ void invert_perm_kernel(const int32_t* __restrict__ idx, int64_t m, int32_t* __restrict__ inv) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < m) inv[idx[i]] = (int32_t)i;
+  if (i < m) {
+    const int32_t v = idx[i];
+    if ((uint32_t)v < (uint32_t)m) inv[v] = (int32_t)i;
+  }
 }
 
 int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_t* offsets, int32_t* block_off,
@@ -408,9 +417,9 @@ int lsurge_invert_permutation(const int32_t* idx, int64_t m, int32_t* inv, lsurg
   if (m == 0) return LSURGE_OK;
   LSURGE_REQUIRE(idx && inv, "invert_permutation: null pointer");
   hipStream_t s = (hipStream_t)stream;
-  LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(invert_perm_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, idx, m,
-                                   inv));
+  const dim3 grid((unsigned)((m + 255) / 256));
+  LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL(fill_i32_kernel, grid, dim3(256), 0, s, inv, m, (int32_t)m));
+  LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL(invert_perm_kernel, grid, dim3(256), 0, s, idx, m, inv));
   return LSURGE_OK;
 }
 

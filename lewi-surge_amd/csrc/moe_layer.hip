@@ -256,17 +256,28 @@ size_t lsurge_moe_fp8_quantize_weights_workspace_bytes(const lsurge_moe_shape* s
 
 }  // extern "C"
 namespace {
-// holds a device's helper streams for the duration of one layer call
+// Holds a device's helper streams for the duration of one layer call.  A call that returns early (an error after
+// the fork) leaves work on the helpers that the caller's stream has not joined yet: the destructor then makes the
+// caller's stream wait for every helper before the lock is released, so the call stays stream-ordered on every
+// path.  joined() marks the normal path, whose own joins already ordered everything.
 struct ForkGuard {
   lsurge::ForkSet f;
-  bool held = false;
-  int acquire(hipStream_t main) {
-    const int rc = lsurge::fork_acquire(&f, main);
+  hipStream_t main = nullptr;
+  bool held = false, done = false;
+  int acquire(hipStream_t m) {
+    main = m;
+    const int rc = lsurge::fork_acquire(&f, m);
     held = rc == LSURGE_OK;
     return rc;
   }
+  int joined(int rc = LSURGE_OK) {
+    done = rc == LSURGE_OK;
+    return rc;
+  }
   ~ForkGuard() {
-    if (held) lsurge::fork_release(&f);
+    if (!held) return;
+    if (!done) lsurge::fork_join_all(&f, main);
+    lsurge::fork_release(&f);
   }
 };
 }  // namespace
@@ -302,7 +313,7 @@ int lsurge_moe_fp8_quantize_weights(const lsurge_moe_shape* s, const lsurge_moe_
   if (int rc = lsurge::fp8_quantize_impl(p->w_gate, q.E, q.d, q.f, true, w.q_gate, w.s_gate, part, st)) return rc;
   if (int rc = lsurge::fp8_quantize_impl(p->w_up, q.E, q.d, q.f, true, w.q_up, w.s_up, part, st)) return rc;
   if (int rc = lsurge::fp8_quantize_impl(p->w_down, q.E, q.f, q.d, true, w.q_down, w.s_down, part, st)) return rc;
-  return q.fs ? lsurge::stream_after(st, s0, fg.f.ev[1]) : LSURGE_OK;
+  return fg.joined(q.fs ? lsurge::stream_after(st, s0, fg.f.ev[1]) : LSURGE_OK);
 }
 
 size_t lsurge_moe_bwd_workspace_bytes(const lsurge_moe_shape* s) {
@@ -447,7 +458,7 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
                                       q.d * q.f, w8->s_down, nullptr, q.f, q.d, sv.y_pad, q.d, false, false, nullptr,
                                       nullptr, nullptr, st))
       return rc;
-    if (int rc = lsurge::stream_after(st, s0, fg.f.ev[1])) return rc;
+    if (int rc = fg.joined(lsurge::stream_after(st, s0, fg.f.ev[1]))) return rc;
     return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sy : nullptr, out,
                                       LSURGE_BF16, st);
   }
@@ -457,7 +468,7 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   if (int rc = lsurge::gemm_rows_kn(KID_GEMM_DOWN_FWD, blocks, sv.h, q.f, p->w_down, q.d, q.f * q.d, q.f, q.d, sv.y_pad,
                                     q.d, st))
     return rc;
-  if (int rc = lsurge::stream_after(st, s0, fg.f.ev[1])) return rc;
+  if (int rc = fg.joined(lsurge::stream_after(st, s0, fg.f.ev[1]))) return rc;
   return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sy : nullptr, out,
                                     LSURGE_BF16, st);
 }
@@ -590,7 +601,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   // join all helpers (s1 after s0, the critical stream after s1), then dx = gather-reduce of dX_pad + router dx term
   // + shared-expert dx, one rounding
   if (int rc = lsurge::stream_after(s1, s0, ev[4])) return rc;
-  if (int rc = lsurge::stream_after(st, s1, ev[5])) return rc;
+  if (int rc = fg.joined(lsurge::stream_after(st, s1, ev[5]))) return rc;
   const bf16_t* shared_dx = q.merged ? w.dx_pad + q.P * q.d : (q.fs ? w.sdx : nullptr);
   if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT, shared_dx,
                                               g->dx, st))

@@ -258,10 +258,10 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_kernel(const void* __r
       if (j < 16) dwv[j] = acc;
       if (lane == 0 && dw) dw[t * k + j] = acc;
     }
-    if (dl && lane == 0) {
+    if (dl && lane == 0) {  // choices past the 16 kept in registers come back from dw (written by this lane)
       float s = 0.f;
-      for (int j = 0; j < k; ++j) s += w[t * k + j] * dwv[j];
-      for (int j = 0; j < k; ++j) dl[t * k + j] = w[t * k + j] * (dwv[j] - s);
+      for (int j = 0; j < k; ++j) s += w[t * k + j] * (j < 16 ? dwv[j] : dw[t * k + j]);
+      for (int j = 0; j < k; ++j) dl[t * k + j] = w[t * k + j] * ((j < 16 ? dwv[j] : dw[t * k + j]) - s);
     }
   }
 }
@@ -617,6 +617,7 @@ int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, co
   const dim3 grid(grid_for_rows(n));
   const int nc = row_chunks(d);
   LSURGE_REQUIRE(!dlog || (sel && dl && E >= 1), "combine_bwd: dense d(logits) needs sel, dl and E");
+  LSURGE_REQUIRE(!dl || dw, "combine_bwd: the router backward needs dw");
   if (nc && (k == 6 || k == 8)) {
     LS_NC_SWITCH(nc, NC, LS_KK_SWITCH(k, KK, {
       if (NC && KK)
@@ -731,7 +732,7 @@ int lsurge_gather_dot(const void* y, int64_t m, int64_t d, int y_dtype, const in
 
 int lsurge_combine_bwd(const void* y, int y_dtype, const int32_t* pos, const float* w, int64_t n, int64_t k, int64_t d,
                        const void* g, int g_dtype, void* dy, float* dw, lsurge_stream_t stream) {
-  LSURGE_REQUIRE(n >= 0 && k >= 0 && d >= 0 && k <= 16, "combine_bwd: bad shape (k <= 16)");
+  LSURGE_REQUIRE(n >= 0 && k >= 0 && d >= 0, "combine_bwd: negative shape");
   if (n == 0 || k == 0) return LSURGE_OK;
   LSURGE_REQUIRE(y && pos && w && g && dy && dw, "combine_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;

@@ -1,5 +1,5 @@
 """Grouped GEMM in place of jax.lax.ragged_dot -- the public surface of the reference's modal/padded_gmm.py,
-computed by hand-written gfx950 bf16 MFMA kernels (liblewi_surge.so).
+computed by hand-written gfx950 MFMA kernels (liblewi_surge.so) on bf16 or f16 operands.
 
 Input as for ragged_dot: lhs [M, K] sorted by group, rhs [E, K, N], group_sizes [E] -> [M, N].
 
@@ -81,8 +81,9 @@ class _RaggedDot(torch.autograd.Function):
         e, _, n = rhs.shape
         out = torch.empty((m, n), dtype=out_dtype, device=lhs.device)
         ws = L.workspace(L.lib().lsurge_ragged_dot_workspace_bytes(m, e), lhs.device)
-        L.check(L.lib().lsurge_ragged_dot(L.ptr(lhs), L.ptr(rhs), L.ptr(group_sizes), m, k, n, e, L.ptr(out),
-                                          L.dt(out), L.ptr(ws), ws.numel(), L.stream(lhs.device)), "ragged_dot")
+        L.check(L.lib().lsurge_ragged_dot(L.ptr(lhs), L.ptr(rhs), L.ptr(group_sizes), m, k, n, e, L.dt(lhs),
+                                          L.ptr(out), L.dt(out), L.ptr(ws), ws.numel(), L.stream(lhs.device)),
+                "ragged_dot")
         ctx.save_for_backward(lhs, rhs, group_sizes)
         return out
 
@@ -91,12 +92,12 @@ class _RaggedDot(torch.autograd.Function):
         lhs, rhs, gs = ctx.saved_tensors
         m, k = lhs.shape
         e, _, n = rhs.shape
-        g = L.contig(g.to(torch.bfloat16))
+        g = L.contig(g.to(lhs.dtype))
         dlhs = torch.empty_like(lhs)
         drhs = torch.empty((e, k, n), dtype=torch.float32, device=lhs.device)
         ws = L.workspace(L.lib().lsurge_ragged_dot_bwd_workspace_bytes(m, k, n, e), lhs.device)
-        L.check(L.lib().lsurge_ragged_dot_bwd(L.ptr(lhs), L.ptr(rhs), L.ptr(gs), L.ptr(g), m, k, n, e, L.ptr(dlhs),
-                                              L.ptr(drhs), L.ptr(ws), ws.numel(), L.stream(lhs.device)),
+        L.check(L.lib().lsurge_ragged_dot_bwd(L.ptr(lhs), L.ptr(rhs), L.ptr(gs), L.ptr(g), m, k, n, e, L.dt(lhs),
+                                              L.ptr(dlhs), L.ptr(drhs), L.ptr(ws), ws.numel(), L.stream(lhs.device)),
                 "ragged_dot_bwd")
         return dlhs, drhs.to(rhs.dtype), None, None
 
@@ -104,18 +105,20 @@ class _RaggedDot(torch.autograd.Function):
 def padded_ragged_dot(lhs, rhs, group_sizes, precision=None, preferred_element_type=None, **kw):
     """Dropless grouped GEMM with ragged_dot's signature.  modal/padded_gmm.py:45-69.
 
-    lhs [M, K] bf16 (rows sorted by group), rhs [E, K, N] (cast to lhs.dtype as in the reference, 67),
+    lhs [M, K] bf16 or f16 (rows sorted by group), rhs [E, K, N] (cast to lhs.dtype as in the reference, 67),
     group_sizes [E] int -> [M, N] in preferred_element_type (default lhs.dtype); rows past sum(gs) are 0.
+    float32 lhs is rejected with TypeError: the MFMA kernels take 16-bit operands (a deliberate limit; the
+    reference's XLA einsum would run it in f32).
     """
     if lhs.ndim != 2 or rhs.ndim != 3 or kw.get("group_offset") is not None:
         return _orig_ragged_dot(lhs, rhs, group_sizes, precision=precision,
                                 preferred_element_type=preferred_element_type, **kw)
     L.require_cuda(lhs, rhs, group_sizes)
-    if lhs.dtype != torch.bfloat16:
-        raise TypeError(f"padded_ragged_dot: the MFMA kernel takes bf16 operands, got lhs {lhs.dtype}")
+    if lhs.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"padded_ragged_dot: the MFMA kernels take bf16 or f16 operands, got lhs {lhs.dtype}")
     out_dtype = preferred_element_type or lhs.dtype
-    if out_dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError(f"padded_ragged_dot: preferred_element_type {out_dtype} not supported (bf16 or float32)")
+    if out_dtype not in (lhs.dtype, torch.float32):
+        raise TypeError(f"padded_ragged_dot: preferred_element_type {out_dtype} not supported ({lhs.dtype} or float32)")
     m, k = lhs.shape
     e, k2, n = rhs.shape
     if k2 != k or group_sizes.shape != (e,):

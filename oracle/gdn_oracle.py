@@ -66,11 +66,12 @@ def neumann_inverse(S):
     return A
 
 
-def gdn_chunked(q, k, v, g, beta, chunk=64, h0=None, rounding=None):
+def gdn_chunked(q, k, v, g, beta, chunk=64, h0=None, rounding=None, return_uw=False):
     """fast_chunk_gated_delta_rule (modal/gdn_fast.py:37-113) without qk-norm or context parallelism.
 
     rounding=None: float64 throughout; "bf16": bf16 roundings at the reference's compute-dtype points.
-    Returns (o [B, T, H, Dv], final state [B, H, Dk, Dv])."""
+    Returns (o [B, T, H, Dv], final state [B, H, Dk, Dv]), plus the chunk-local u [B, N, H, C, Dv] and
+    w [B, N, H, C, Dk] (gdn_fast.py:88-90) with return_uw."""
     def rd(a):  # a value the reference holds in its compute dtype
         if rounding == "bf16":
             return round_bf16(np.asarray(a, np.float32)).astype(np.float64)
@@ -119,4 +120,4 @@ def gdn_chunked(q, k, v, g, beta, chunk=64, h0=None, rounding=None):
         ki = kn * np.exp(gg[..., -1, None] - gg)[..., None]
         h = h * np.exp(gg[..., -1])[..., None, None] + ki.swapaxes(-1, -2) @ v_new
     o = o.transpose(0, 1, 3, 2, 4).reshape(B, N * chunk, H, Dv)[:, :T]
-    return o, h
+    return (o, h, u, w) if return_uw else (o, h)

@@ -243,6 +243,19 @@ def permute_rows_bwd(g, idx):
     return np.asarray(g)[inv]
 
 
+def invert_permutation(idx):
+    """inv[idx[i]] = i, the argsort of a permutation (modal/moe_permute.py:325-326 takes argsort(idx)).  For an idx that
+    is not a permutation this states the guarded kernel's contract: entries outside [0, m) are skipped and entries of
+    inv that no index hits hold m (a gather through inv then gives zero rows).  Duplicated in-range entries keep an
+    unspecified writer, so callers that test them must not have any."""
+    idx = np.asarray(idx, np.int64)
+    m = idx.shape[0]
+    inv = np.full(m, m, np.int32)
+    ok = (idx >= 0) & (idx < m)
+    inv[idx[ok]] = np.nonzero(ok)[0].astype(np.int32)
+    return inv
+
+
 def ref_dispatch(x, flat_experts):
     """modal/moe_permute.py:335-338."""
     k = flat_experts.shape[0] // x.shape[0]
@@ -454,6 +467,53 @@ def moe_layer_bwd(p, cache, dy, dtype=np.float64):
         dxs_, out["dws_gate"], out["dws_up"], out["dws_down"] = swiglu_bwd(x, *ws, cache["shared"], dy)
         out["dx"] = out["dx"] + dxs_
     return out
+
+
+def expert_grads(p, sel, e, dy, dtype=np.float32):
+    """(dw_gate[e], dw_up[e], dw_down[e]) of one routed expert, the per-expert slice of `moe_layer_bwd` computed
+    from that expert's tokens only (ascending t, as the stable sort orders them): their routing weights are the
+    softmax over the selected logits recomputed in `dtype`, dY rows = w[t,j] dy[t].  For configurations too large
+    for the whole-layer oracle."""
+    x = np.asarray(p["x"], dtype)
+    sel = np.asarray(sel)
+    toks, js = np.nonzero(sel == e)
+    if toks.size == 0:
+        d, f = p["w_gate"].shape[1:]
+        return np.zeros((d, f), dtype), np.zeros((d, f), dtype), np.zeros((f, d), dtype)
+    xs = x[toks]
+    lw = xs @ np.asarray(p["w_r"], dtype)
+    if p.get("bias") is not None:
+        lw = lw + np.asarray(p["bias"], dtype)
+    w = topk_softmax(lw, sel[toks])[np.arange(toks.size), js]
+    wg, wu, wd = (np.asarray(p[n][e], dtype) for n in ("w_gate", "w_up", "w_down"))
+    _, cache = swiglu(xs, wg, wu, wd)
+    dys = np.asarray(dy, dtype)[toks] * w[:, None]
+    _, dwg, dwu, dwd = swiglu_bwd(xs, wg, wu, wd, cache, dys)
+    return dwg, dwu, dwd
+
+
+def shared_grads(p, dy, dtype=np.float32):
+    """(dws_gate, dws_up, dws_down, dx_shared) of the shared expert over all tokens (its part of `moe_layer_bwd`)."""
+    x = np.asarray(p["x"], dtype)
+    ws = [np.asarray(p[n], dtype) for n in ("ws_gate", "ws_up", "ws_down")]
+    _, cache = swiglu(x, *ws)
+    dxs, dwg, dwu, dwd = swiglu_bwd(x, *ws, cache, np.asarray(dy, dtype))
+    return dwg, dwu, dwd, dxs
+
+
+def router_wgrad(p, sel, dweights, dtype=np.float32):
+    """dW_r = x^T dlogits, dlogits = the softmax-over-selected Jacobian applied to the routing weights' gradient
+    (the router part of `moe_layer_bwd`), for a given d(weights) [T, k]."""
+    x = np.asarray(p["x"], dtype)
+    lw = x @ np.asarray(p["w_r"], dtype)
+    if p.get("bias") is not None:
+        lw = lw + np.asarray(p["bias"], dtype)
+    w = topk_softmax(lw, sel).astype(dtype)
+    dw = np.asarray(dweights, dtype)
+    dl_sel = w * (dw - (w * dw).sum(axis=1, keepdims=True))
+    dlogits = np.zeros((x.shape[0], p["w_r"].shape[1]), dtype)
+    np.put_along_axis(dlogits, np.asarray(sel, np.int64), dl_sel, axis=1)
+    return x.T @ dlogits
 
 
 # --------------------------------------------------------------------------------------------- FP8 variant

@@ -20,7 +20,7 @@ def declared():
 
 def test_library_built_and_loads():
     assert os.path.exists(L.LIB_PATH), "run __graft_entry__.build() first"
-    assert L.lib().lsurge_abi_version() == 1
+    assert L.lib().lsurge_abi_version() == 2
 
 
 def test_every_declared_symbol_is_exported_and_bound():

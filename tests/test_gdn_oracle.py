@@ -71,3 +71,40 @@ def test_bf16_rounding_points_stay_close():
     o16, _ = go.gdn_chunked(q, k, v, g, beta, chunk=64, rounding="bf16")
     err = np.linalg.norm(o16 - o) / np.linalg.norm(o)
     assert 1e-4 < err < 2e-2, err
+
+
+def test_correlated_keys_separate_inverse_mistakes(monkeypatch):
+    """Keys sharing one direction (k = normalize(dir + 0.5 noise), the case the GPU tests add) make the chunk's
+    S = (k beta) k^T large, so the exact inverse matters: the chunked form still equals the recurrence, the bf16
+    rounding points stay within 1e-2 of it, and the approximation (I + S)^-1 ~ I - S -- what a blocked inverse that
+    drops its diagonal-block factor degenerates to -- is off by far more than the 2e-2 bar (with i.i.d. keys it is
+    not, which is why the correlated case is needed)."""
+    rng = np.random.default_rng(11)
+    B, T, H, D = 1, 128, 2, 128
+    q = rng.standard_normal((B, T, H, D))
+    v = rng.standard_normal((B, T, H, D))
+    g = -np.abs(rng.standard_normal((B, T, H))) * 0.05
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H))))
+
+    def keys(correlated):
+        k = rng.standard_normal((B, T, H, D))
+        if correlated:
+            k = rng.standard_normal((1, 1, H, D)) + 0.5 * k
+        return k / np.linalg.norm(k, axis=-1, keepdims=True)
+
+    def rel(a, b):
+        return np.linalg.norm(a - b) / np.linalg.norm(b)
+
+    errs = {}
+    for correlated in (False, True):
+        k = keys(correlated)
+        o_ref, _ = go.gated_delta_recurrence(q, k, v, g, beta)
+        o, _ = go.gdn_chunked(q, k, v, g, beta, chunk=64)
+        assert np.allclose(o, o_ref, rtol=1e-8, atol=1e-8)
+        o16, _ = go.gdn_chunked(q, k, v, g, beta, chunk=64, rounding="bf16")
+        assert rel(o16, o_ref) < 1e-2
+        with monkeypatch.context() as m:
+            m.setattr(go, "unit_lower_inverse", lambda S: np.eye(S.shape[-1]) - S)
+            bad, _ = go.gdn_chunked(q, k, v, g, beta, chunk=64)
+        errs[correlated] = rel(bad, o_ref)
+    assert errs[True] > 0.1 and errs[True] > 5 * errs[False], errs

@@ -19,17 +19,21 @@ def _bf(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev).to(torch.bfloat16)
 
 
-def run_case(gs, M, K, N, dev, seed=0, out_dtype=None):
+def run_case(gs, M, K, N, dev, seed=0, out_dtype=None, dt=torch.bfloat16):
+    """Forward and backward of padded_ragged_dot on operands of dtype dt (bf16 or f16) against the fp64 oracle."""
     rng = np.random.default_rng(seed)
     E = len(gs)
-    a = mo.round_bf16(rng.standard_normal((M, K)).astype(np.float32))
-    b = mo.round_bf16(rng.standard_normal((E, K, N)).astype(np.float32))
-    g = mo.round_bf16(rng.standard_normal((M, N)).astype(np.float32))
-    at = _bf(a, dev).requires_grad_(True)
-    bt = _bf(b, dev).requires_grad_(True)
+    rnd = mo.round_bf16 if dt == torch.bfloat16 else (lambda v: v.astype(np.float16).astype(np.float32))
+    a = rnd(rng.standard_normal((M, K)).astype(np.float32))
+    b = rnd(rng.standard_normal((E, K, N)).astype(np.float32))
+    g = rnd(rng.standard_normal((M, N)).astype(np.float32))
+    tdev = lambda v: torch.from_numpy(np.ascontiguousarray(v, np.float32)).to(dev).to(dt)  # noqa: E731
+    at = tdev(a).requires_grad_(True)
+    bt = tdev(b).requires_grad_(True)
     gst = torch.tensor(gs, dtype=torch.int32, device=dev)
     out = pg.padded_ragged_dot(at, bt, gst, preferred_element_type=out_dtype)
-    out.backward(_bf(g, dev).to(out.dtype))
+    assert out.dtype == (out_dtype or dt)
+    out.backward(tdev(g).to(out.dtype))
     want = mo.ragged_dot(a, b, gs)
     S = int(np.sum(gs))
     got = out.detach().float().cpu().numpy()
@@ -56,6 +60,24 @@ def test_te_known_answer_case(dev):
 def test_f32_output(dev):
     gs = [5, 0, 9, 3, 7, 1, 6, 4]
     run_case(gs, sum(gs) + 3, 64, 48, dev, out_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("gs,M,K,N,out_dtype", [([5, 0, 9, 3, 7, 1, 6, 4], 38, 64, 48, None),
+                                                ([5, 0, 9, 3, 7, 1, 6, 4], 38, 64, 48, torch.float32),
+                                                ([700, 0, 1300, 20, 5000], 7100, 512, 1024, None),
+                                                ([1536] * 16, 24576, 1024, 512, None)])
+def test_f16_operands(gs, M, K, N, out_dtype, dev):
+    """f16 lhs / rhs (the reference's einsum runs in lhs.dtype, modal/padded_gmm.py:67): v_mfma_f32_32x32x16_f16,
+    f16 or f32 output, dlhs in f16, drhs f32 -- including a group big enough for the chunked weight gradient."""
+    err = run_case(gs, M, K, N, dev, seed=3, out_dtype=out_dtype, dt=torch.float16)
+    assert err < 5e-3
+
+
+def test_f32_operands_rejected(dev):
+    a = torch.zeros((16, 64), dtype=torch.float32, device=dev)
+    b = torch.zeros((2, 64, 32), dtype=torch.float32, device=dev)
+    with pytest.raises(TypeError, match="bf16 or f16"):
+        pg.padded_ragged_dot(a, b, torch.tensor([8, 8], dtype=torch.int32, device=dev))
 
 
 @pytest.mark.parametrize("E,M,K,N", [(8, 1000, 256, 192), (4, 777, 128, 1024), (64, 6000, 1024, 512),
@@ -119,7 +141,7 @@ def test_ragged_bwd_forward_sized_workspace(dev):
         ws = L.workspace(nbytes, dev)
         dl = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
         dr = torch.empty((E, K, N), dtype=torch.float32, device=dev)
-        L.check(lib.lsurge_ragged_dot_bwd(L.ptr(at), L.ptr(bt), L.ptr(gst), L.ptr(gt), M, K, N, E, L.ptr(dl), L.ptr(dr),
+        L.check(lib.lsurge_ragged_dot_bwd(L.ptr(at), L.ptr(bt), L.ptr(gst), L.ptr(gt), M, K, N, E, L.BF16, L.ptr(dl), L.ptr(dr),
                                           L.ptr(ws), ws.numel(), L.stream(dev)), "ragged_dot_bwd")
         outs.append((dl.float().cpu().numpy(), dr.cpu().numpy()))
     want_l, want_r = mo.ragged_dot_bwd(a, b, gs, g)

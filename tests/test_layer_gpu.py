@@ -148,6 +148,23 @@ def test_c5_token_subset(dev):
     print(errs)
     assert all(v < TOL for v in errs.values()), errs
     assert all(np.isfinite(v).all() for v in grads.values())
+    # weight gradients on the full run: the hottest, the coldest and six more routed experts, the shared expert of
+    # its own width (fs != f: dense backward GEMMs with split-K partials on a helper stream) and the router
+    gs = views["group_sizes"]
+    pick = sorted({int(np.argmax(gs)), int(np.argmin(gs))} | set(np.random.default_rng(1).choice(c["E"], 6, replace=False).tolist()))
+    werr = {}
+    for e in pick:
+        dwg, dwu, dwd = mo.expert_grads(p, views["sel"], e, p["dy"])
+        werr[f"dw_gate[{e}]"] = mo.rel_l2(grads["dw_gate"][e], dwg)
+        werr[f"dw_up[{e}]"] = mo.rel_l2(grads["dw_up"][e], dwu)
+        werr[f"dw_down[{e}]"] = mo.rel_l2(grads["dw_down"][e], dwd)
+    dsg, dsu, dsd, _ = mo.shared_grads(p, p["dy"])
+    werr.update({"dws_gate": mo.rel_l2(grads["dws_gate"], dsg), "dws_up": mo.rel_l2(grads["dws_up"], dsu),
+                 "dws_down": mo.rel_l2(grads["dws_down"], dsd)})
+    # the router's weight gradient from the layer's own d(weights) (checked on the token subset above)
+    werr["dw_r"] = mo.rel_l2(grads["dw_r"], mo.router_wgrad(p, views["sel"], grads["dweights"]))
+    print(werr)
+    assert all(v < TOL for v in werr.values()), werr
 
 
 def test_deterministic_bitwise(dev):
@@ -180,6 +197,41 @@ def test_concurrent_streams_bitwise(dev):
     assert np.array_equal(a[0], b[0]) and np.array_equal(b[0], b2[0])
     for k in a[2]:
         assert np.array_equal(a[2][k], b[2][k]), k
+
+
+def test_error_after_fork_keeps_stream_order(dev):
+    """A launch that fails after the backward forked its helper streams (forced from the host with
+    lsurge_test_fail_launch at the down dgrad, the first launch on the caller's stream after the fork, while the
+    helper already holds the down weight gradient): the call returns the error, and the caller's stream still waits
+    for the helpers, so once it is idle every helper is idle too.  The next call is unaffected."""
+    import _lib as L
+    c = mo.CONFIGS["C2"]
+    p = mo.make_inputs(**c)
+    shape = MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"])
+    lib = L.lib()
+    names = [lib.lsurge_prof_kernel_name(i).decode() for i in range(lib.lsurge_prof_kernel_count())]
+    kid = names.index("gemm_down_dgrad")
+    layer = MoELayer(shape, dev)
+    tp = to_dev(p, dev)
+    dy = torch.from_numpy(np.ascontiguousarray(p["dy"])).to(dev).to(torch.bfloat16)
+    layer.forward(tp)
+    want = {k: v.clone() for k, v in layer.backward(tp, dy).items()}
+    lib.lsurge_set_concurrency(1)
+    try:
+        layer.backward(tp, dy)  # the helper streams exist
+        torch.cuda.synchronize()
+        assert lib.lsurge_test_fail_launch(kid, 1) == 0
+        with pytest.raises(RuntimeError, match="injected"):
+            layer.backward(tp, dy)
+        torch.cuda.current_stream(dev).synchronize()
+        assert lib.lsurge_test_helpers_idle() == 1
+        got = layer.backward(tp, dy)
+        torch.cuda.synchronize()
+    finally:
+        lib.lsurge_test_fail_launch(-1, 0)
+        lib.lsurge_set_concurrency(0)
+    for k in want:
+        assert torch.equal(got[k], want[k]), k
 
 
 def test_autograd_function(dev):

@@ -217,6 +217,23 @@ def test_combine_bwd_and_permute_rows_vjp():
     assert np.isclose((gg * mo.permute_rows(x, perm)).sum(), (mo.permute_rows_bwd(gg, perm) * x).sum())
 
 
+def test_invert_permutation_guarded_contract():
+    """The inverse of a permutation is its argsort; with out-of-range entries (an index that is not a permutation),
+    a scalar loop of the guarded scatter: skipped entries, and m where no index lands."""
+    rng = np.random.default_rng(21)
+    for m in (1, 2, 37, 1000):
+        perm = rng.permutation(m).astype(np.int32)
+        assert np.array_equal(mo.invert_permutation(perm), np.argsort(perm, kind="stable"))
+        bad = perm.copy()
+        hit = rng.choice(m, size=max(1, m // 5), replace=False)
+        bad[hit] = rng.choice([-1, -7, m, m + 3, 2**31 - 1], size=hit.size)
+        want = [m] * m
+        for i, v in enumerate(bad.tolist()):
+            if 0 <= v < m:
+                want[v] = i
+        assert np.array_equal(mo.invert_permutation(bad), np.array(want, np.int32))
+
+
 # ------------------------------------------------------------------------------------------------ grouped GEMM
 
 
@@ -312,6 +329,28 @@ def test_layer_backward_finite_differences():
             assert np.array_equal(mo.moe_layer_fwd(q)[1]["sel"], cache["sel"])
             fd = (lp - lm) / (2 * eps)
             assert abs(fd - g[gname][idx]) <= 1e-6 * max(1.0, abs(fd)), (name, idx, fd, g[gname][idx])
+
+
+def test_per_expert_and_shared_slices_match_layer_oracle():
+    """expert_grads / shared_grads / router_wgrad (the slices the full-size C5 test uses) equal the whole-layer
+    oracle's gradients, which the finite-difference test pins."""
+    p = mo.make_inputs(T=300, d=64, E=8, k=3, f=32, fs=48, seed=4)
+    out, cache = mo.moe_layer_fwd(p)
+    g = mo.moe_layer_bwd(p, cache, p["dy"])
+    sel = cache["sel"]
+    for e in range(8):
+        dwg, dwu, dwd = mo.expert_grads(p, sel, e, p["dy"], np.float64)
+        assert np.allclose(dwg, g["dw_gate"][e], rtol=1e-10, atol=1e-12)
+        assert np.allclose(dwu, g["dw_up"][e], rtol=1e-10, atol=1e-12)
+        assert np.allclose(dwd, g["dw_down"][e], rtol=1e-10, atol=1e-12)
+    dsg, dsu, dsd, _ = mo.shared_grads(p, p["dy"], np.float64)
+    for a, n in ((dsg, "dws_gate"), (dsu, "dws_up"), (dsd, "dws_down")):
+        assert np.allclose(a, g[n], rtol=1e-10, atol=1e-12), n
+    assert np.allclose(mo.router_wgrad(p, sel, g["dw"], np.float64), g["dw_r"], rtol=1e-10, atol=1e-12)
+    # an expert no token picks has zero gradients
+    p2 = dict(p, bias=np.array([9.0] * 3 + [0.0] * 5, np.float32))
+    _, c2 = mo.moe_layer_fwd(p2)
+    assert not any(a.any() for a in mo.expert_grads(p2, c2["sel"], 7, p2["dy"]))
 
 
 def test_oracle_catches_planted_mistake(monkeypatch):

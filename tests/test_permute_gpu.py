@@ -158,3 +158,53 @@ def test_full_size_dispatch_combine_round_trip(dev):
     order, pos = mp.sort_indices(flat, e)
     out = mp.combine(mp.dispatch(x, order, pos), order, pos, w)
     assert (out - x.float()).abs().max().item() < 1e-5 * x.float().abs().max().item() + 1e-6
+
+
+def test_invert_permutation_out_of_range_entries(dev):
+    """The inverse-permutation kernel behind permute_rows' backward skips indices outside [0, m) (no write leaves inv)
+    and leaves m where no index lands, so the gather through it gives zero rows there (oracle.invert_permutation)."""
+    import _lib as L
+    rng = np.random.default_rng(8)
+    for m in (1, 300, 70001):
+        idx_np = rng.permutation(m).astype(np.int32)
+        hit = rng.choice(m, size=max(1, m // 7), replace=False)
+        idx_np[hit] = rng.choice(np.array([-1, -5, m, m + 9, 2**31 - 1], np.int32), size=hit.size)
+        inv = torch.full((m,), -3, dtype=torch.int32, device=dev)
+        idx = _t(idx_np, torch.int32, dev)
+        L.check(L.lib().lsurge_invert_permutation(L.ptr(idx), m, L.ptr(inv), L.stream(dev)), "invert_permutation")
+        assert np.array_equal(inv.cpu().numpy(), mo.invert_permutation(idx_np))
+    # through permute_rows' backward: rows of g whose slot no index names come back as zeros
+    m, d = 50, 24
+    idx_np = rng.permutation(m).astype(np.int32)
+    idx_np[[3, 17]] = [m + 1, -2]
+    x = torch.randn((m, d), device=dev).to(torch.bfloat16).requires_grad_(True)
+    g = torch.randn((m, d), device=dev).to(torch.bfloat16)
+    mp.permute_rows(x, _t(idx_np, torch.int32, dev)).backward(g)
+    inv = mo.invert_permutation(idx_np)
+    g_np = g.float().cpu().numpy()
+    want = np.where((inv < m)[:, None], g_np[np.minimum(inv, m - 1)], 0.0)
+    assert np.array_equal(x.grad.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("k,dname", [(24, "bf16"), (17, "f32"), (40, "f16")])
+def test_combine_any_k(k, dname, dev):
+    """combine forward and its fused backward for k above 16 (the reference takes any k,
+    modal/moe_permute.py:292-312): dy rows, dw and the gather-reduce forward against the oracle."""
+    n, d, e = 96, 264, 64
+    dtype = TORCH_DT[dname]
+    tol = 1e-5 if dname == "f32" else 2e-2
+    rng = np.random.default_rng(k)
+    sel = rand_routing(rng, n, k, e)
+    flat = sel.reshape(-1)
+    order_np, pos_np = mo.sort_indices(flat, e)
+    w_np = rng.random((n, k)).astype(np.float32)
+    y_np = _cast_np(rng.standard_normal((n * k, d)), dname)
+    g_np = _cast_np(rng.standard_normal((n, d)), dname)
+    yg = _t(y_np, dtype, dev).requires_grad_(True)
+    wg = _t(w_np, torch.float32, dev).requires_grad_(True)
+    out = mp.combine(yg, _t(order_np, torch.int32, dev), _t(pos_np, torch.int32, dev), wg)
+    out.backward(_t(g_np, torch.float32, dev))
+    check(out.detach(), mo.combine(y_np, pos_np, w_np), tol)
+    dys, dw = mo.combine_bwd(y_np, order_np, pos_np, w_np, g_np, dname)
+    check(yg.grad, dys, tol)
+    check(wg.grad, dw, tol)
