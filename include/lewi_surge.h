@@ -138,6 +138,17 @@ int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_siz
                       int64_t n, int64_t e, int in_dtype, void* out, int out_dtype, void* workspace,
                       size_t workspace_bytes, lsurge_stream_t stream);
 
+/* lsurge_ragged_dot that allocates nothing and takes no workspace: its block table lives in a static device array
+ * of the library (221 KB per GPU, held until the process ends), so m <= lsurge_ragged_dot_noalloc_max_rows() (2^21)
+ * and e <= lsurge_ragged_dot_noalloc_max_groups() (1024); larger calls return LSURGE_ERR_INVALID.  Same results as
+ * lsurge_ragged_dot.  Calls that overlap on one GPU share the array and race: serialise them (one stream).
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). */
+size_t lsurge_ragged_dot_noalloc_max_rows(void);
+size_t lsurge_ragged_dot_noalloc_max_groups(void);
+int lsurge_ragged_dot_noalloc(const void* lhs, const void* rhs, const int32_t* group_sizes, int64_t m, int64_t kdim,
+                              int64_t n, int64_t e, int in_dtype, void* out, int out_dtype, lsurge_stream_t stream);
+
 /* Backward of lsurge_ragged_dot for upstream g [m, n] of in_dtype: dlhs [m, kdim] in_dtype (rows past the groups
  * = 0) and drhs [e, kdim, n] f32.  Replaces the VJP of padded_gmm.padded_ragged_dot
  * (modal/padded_gmm.py:35-39 + XLA autodiff of the einsum at 67-68).

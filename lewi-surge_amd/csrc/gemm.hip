@@ -1,6 +1,8 @@
 // Launchers and C ABI of the grouped GEMMs of the MoE layer (the kernels are in gemm_kernels.h): shape checks,
 // grid sizes, the split-K reduction of dense weight gradients, and the ragged_dot entry points that replace
 // modal/padded_gmm.py:45-69 (padded_ragged_dot and its gather-only VJP).
+#include <mutex>
+
 #include "gemm_kernels.h"
 #include "launchers.h"
 
@@ -608,6 +610,66 @@ int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_siz
   LSURGE_LAUNCH(KID_MISC, s,
                 hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, out, m, n, f32 ? 4 : 2, total));
   return LSURGE_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------ C ABI: ragged_dot without allocation
+// The block table of lsurge_ragged_dot_noalloc lives in this file-scope device array instead of a caller workspace.
+// Each GPU holds its own copy until the process ends; in host code `scratch` only names the symbol, so kernels get
+// the per-device address that hipGetSymbolAddress returns (looked up once per device, with that device current).
+// Every entry the table's kernels read is written earlier in the same call, so nothing needs clearing between calls;
+// calls that overlap on one GPU (different streams) share the array and race.
+namespace {
+constexpr int64_t kNoallocMaxRows = 1ll << 21;  // m <= 2^21 rows
+constexpr int64_t kNoallocMaxGroups = 1024;     // e <= 1024 groups
+constexpr size_t kScratchInts = 3 * (size_t)((kNoallocMaxRows + LSURGE_BLOCK_ROWS - 1) / LSURGE_BLOCK_ROWS +
+                                             kNoallocMaxGroups) + 4 + 3 * (size_t)kNoallocMaxGroups + 1;  // 221 KB
+__device__ __align__(256) int32_t scratch[kScratchInts];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// the current device's address of `scratch` (looked up on its first call), or nullptr with the error set
+int32_t* scratch_on_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    lsurge::set_error(LSURGE_ERR_LAUNCH, "ragged_dot_noalloc: no usable current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int32_t* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      lsurge::set_error(LSURGE_ERR_LAUNCH, "ragged_dot_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" {
+
+size_t lsurge_ragged_dot_noalloc_max_rows(void) { return (size_t)kNoallocMaxRows; }
+size_t lsurge_ragged_dot_noalloc_max_groups(void) { return (size_t)kNoallocMaxGroups; }
+
+int lsurge_ragged_dot_noalloc(const void* lhs, const void* rhs, const int32_t* group_sizes, int64_t m, int64_t kdim,
+                              int64_t n, int64_t e, int in_dtype, void* out, int out_dtype, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(m >= 0 && m <= kNoallocMaxRows && e >= 1 && e <= kNoallocMaxGroups,
+                 "ragged_dot_noalloc: m=%lld e=%lld outside the static scratch (m <= %lld, e <= %lld)", (long long)m,
+                 (long long)e, (long long)kNoallocMaxRows, (long long)kNoallocMaxGroups);
+  const size_t need = lsurge_ragged_dot_workspace_bytes(m, e);
+  LSURGE_REQUIRE(need <= sizeof(int32_t) * kScratchInts, "ragged_dot_noalloc: table of %zu bytes exceeds the scratch",
+                 need);
+  if (m == 0) return LSURGE_OK;
+  int32_t* ws = scratch_on_current_device();
+  if (!ws) return LSURGE_ERR_LAUNCH;
+  return lsurge_ragged_dot(lhs, rhs, group_sizes, m, kdim, n, e, in_dtype, out, out_dtype, ws,
+                           sizeof(int32_t) * kScratchInts, stream);
 }
 
 int lsurge_ragged_dot_fp8(const void* lhs_q, const float* lhs_scale_inv, const void* rhs_q, const float* rhs_scale_inv,
