@@ -184,6 +184,12 @@ def short_kernel(name):
     n = re.sub(r"lsgemm::GemmCfg<[^>]*>,? ?", "", n)  # the tile shape (one for every GEMM)
     n = n.replace("lsgemm::", "").replace("(anonymous namespace)::", "")
     n = n.replace(" ", "").replace("<>", "")
+    # the GEMM templates' element-type / FP8 flags (defaults) are not part of the role: B layout and epilogue only
+    m = re.match(r"(gemm_rows_kernel)<(\d+),(\d+)(,.*)?>$", n)
+    if m:
+        n = f"{m.group(1)}<{m.group(2)},{m.group(3)}>" + ("<f8>" if m.group(4) and "true" in m.group(4) else "")
+    if n.startswith("gemm_wgrad_kernel<"):
+        n = "gemm_wgrad_kernel"
     return n
 
 
@@ -324,11 +330,72 @@ def profile_summary(a):
         print(f"| {role} | `{k}` | {len(v)} | {sum(v) / len(v):.1f} | {100 * sum(v) / total:.1f}% | {fmt(rmb)} | "
               f"{fmt(wmb)} |")
     print()
+    if a.pmc_extra:
+        counter_table(a, c, rows_of)
+        print()
     for n, f in fac.items():
         print(f"calibration {n}: x{f:.3f} (bytes per KiB-count unit x 1024)")
     print()
     for role, b in sorted(traffic.items()):
         print(f"bench-traffic {role} {b:.0f}")
+
+
+def counter_table(a, c, rows_of):
+    """Per-role averages of the rocprofv3 --pmc runs in a.pmc_extra (one directory per pass), with derived rates.
+    Counter values are whole-GPU sums per dispatch: GRBM_GUI_ACTIVE adds the 8 XCDs' busy cycles, so the clock is
+    GRBM_GUI_ACTIVE / 8 / duration; MFMA util = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024 SIMDs) (the
+    counter adds 32 cycles per 32x32x16 MFMA, so this is achieved flops over the peak at the measured clock); TA / TD
+    busy = TA_TA_BUSY_sum / TD_TD_BUSY_sum over (GRBM_GUI_ACTIVE / 8 x 256 CUs); LDS issue wait = SQ_WAIT_INST_LDS /
+    SQ_WAVE_CYCLES (the share of wave time spent waiting to issue an LDS instruction)."""
+    import collections
+    per = collections.defaultdict(lambda: collections.defaultdict(list))
+    dur = collections.defaultdict(list)
+    for d in a.pmc_extra:
+        rows = rows_of(d, "counter_collection")
+        disp = {}
+        for r in rows:
+            e = disp.setdefault(r["Dispatch_Id"], dict(r, ctr={}))
+            e["ctr"][r["Counter_Name"]] = e["ctr"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        for role, k, row in label_launches(list(disp.values()), c):
+            dns = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+            for n, v in row["ctr"].items():
+                per[role][(d, n)].append((v, dns))
+            dur[role].append(dns)
+
+    def avg(role, name):
+        vals = [(v, t) for (d, n), lst in per[role].items() if n == name for v, t in lst]
+        return (sum(v for v, _ in vals) / len(vals), sum(t for _, t in vals) / len(vals)) if vals else (None, None)
+
+    def grbm(role, name):  # GRBM of the same pass as counter `name`
+        for (d, n), lst in per[role].items():
+            if n == name:
+                g = [v for (d2, n2), l2 in per[role].items() if d2 == d and n2 == "GRBM_GUI_ACTIVE" for v, _ in l2]
+                return sum(g) / len(g) / 8 if g else None
+        return None
+
+    print("| role | avg us | clock GHz | MFMA util | LDS instrs / launch | LDS bank conflicts | LDS issue wait | "
+          "TA busy | TD busy | TD waits on L1 (TCP_PENDING) |")
+    print("|---|---|---|---|---|---|---|---|---|---|")
+    for role in sorted(dur, key=lambda r: -sum(dur[r])):
+        g, t = avg(role, "GRBM_GUI_ACTIVE")
+        clk = g / 8 / t if g else None
+        mf, _ = avg(role, "SQ_VALU_MFMA_BUSY_CYCLES")
+        gm = grbm(role, "SQ_VALU_MFMA_BUSY_CYCLES")
+        lds, _ = avg(role, "SQ_INSTS_LDS")
+        bc, _ = avg(role, "SQ_LDS_BANK_CONFLICT")
+        wl, _ = avg(role, "SQ_WAIT_INST_LDS")
+        wc, _ = avg(role, "SQ_WAVE_CYCLES")
+        ta, _ = avg(role, "TA_TA_BUSY_sum")
+        gt = grbm(role, "TA_TA_BUSY_sum")
+        td, _ = avg(role, "TD_TD_BUSY_sum")
+        tp, _ = avg(role, "TCP_PENDING_STALL_CYCLES_sum")
+        f = lambda x, fmt: "-" if x is None else fmt.format(x)  # noqa: E731
+        print(f"| {role} | {sum(dur[role]) / len(dur[role]) / 1e3:.1f} | {f(clk, '{:.2f}')} | "
+              f"{f(mf / (gm * 1024) if mf is not None and gm else None, '{:.1%}')} | {f(lds, '{:.3g}')} | "
+              f"{f(bc, '{:.3g}')} | {f(wl / wc if wl is not None and wc else None, '{:.1%}')} | "
+              f"{f(ta / (gt * 256) if ta is not None and gt else None, '{:.0%}')} | "
+              f"{f(td / (gt * 256) if td is not None and gt else None, '{:.0%}')} | "
+              f"{f(tp / (gt * 256) if tp is not None and gt else None, '{:.0%}')} |")
 
 
 def conv_bench(a):
@@ -432,6 +499,160 @@ def gdn_bench(a):
                      "note": "f32 arithmetic on the VALU, priced against the MI355X fp32 matrix peak"}}), flush=True)
 
 
+
+def _time_ms(fn, steps, warmup):
+    """Mean ms per call of fn, HIP events on torch's current stream (where the kernels are launched)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def permute_bench(a):
+    """The drop-in permute kernels at the shapes of the reference's own microbench (colab/tpu_permute_bench.py:22-104:
+    N = 8 x 4096 tokens, D = 1024, E = 128, k in {6, 12}): gather_rows, gather_reduce, gather_dot, sort_indices
+    (argsort vs count, both the same counting-sort kernel here), and the dispatch -> identity expert -> combine block
+    forward + backward.  GB/s use the reference's byte model, read + write of the gathered rows (line 63), per kernel:
+    gather_rows 2 M D 2, gather_reduce M D 2 + N D 2 (bf16 out), gather_dot M D 2 + N D 2, and for the block the sum
+    over its kernels of the SURVEY byte model (dispatch 2 M D 2, combine M D 2 + N D 4, combine backward dy 2 M D 2 and
+    dw M D 2 + N D 2, dispatch backward M D 2 + N D 2; index bytes included)."""
+    import torch
+
+    import moe_permute as mp
+
+    dev = torch.device("cuda", 0)
+    E, N, D = 128, 8 * 4096, 1024
+    out = {}
+    for k in (6, 12):
+        M = N * k
+        gen = torch.Generator(device=dev).manual_seed(0)
+        x = torch.randn((N, D), device=dev, generator=gen).to(torch.bfloat16)
+        sel = torch.argsort(-torch.randn((N, E), device=dev, generator=gen), dim=1, stable=True)[:, :k].to(torch.int32)
+        flat = sel.reshape(-1).contiguous()
+        w = torch.softmax(torch.randn((N, k), device=dev, generator=gen), dim=1)
+        y = torch.randn((M, D), device=dev, generator=gen).to(torch.bfloat16)
+        g = torch.randn((N, D), device=dev, generator=gen).to(torch.bfloat16)
+        order, pos = mp.sort_indices(flat, E)
+        idx = torch.div(order, k, rounding_mode="floor").to(torch.int32)
+        pos2 = pos.reshape(N, k)
+        res = {}
+        t = _time_ms(lambda: mp.sort_indices(flat, E, "count"), a.steps, a.warmup)
+        res["sort_indices"] = dict(ms=round(t, 4), GBs=round((4 * M + 8 * M) / (t * 1e-3) / 1e9, 1))
+        for name, fn, nbytes in (
+                ("gather_rows", lambda: mp.gather_rows(x, idx), 2 * M * D * 2 + 4 * M),
+                ("gather_reduce", lambda: mp.gather_reduce(y, pos2, w), M * D * 2 + N * D * 2 + 8 * M),
+                ("gather_dot", lambda: mp.gather_dot(y, pos2, g), M * D * 2 + N * D * 2 + 8 * M)):
+            t = _time_ms(fn, a.steps, a.warmup)
+            res[name] = dict(ms=round(t, 4), GBs=round(nbytes / (t * 1e-3) / 1e9, 1))
+        mp.CFG["num_experts"] = E
+        try:
+            xg = x.clone().requires_grad_(True)
+            wg = w.clone().requires_grad_(True)
+            gf = g.float()
+
+            def block():
+                xg.grad = None
+                wg.grad = None
+                o = mp.moe_block(xg, flat, wg, lambda r: r, use_kernels=True)
+                (o * gf).sum().backward()
+
+            t = _time_ms(block, max(5, a.steps // 4), max(2, a.warmup // 4))
+        finally:
+            mp.CFG["num_experts"] = None
+        model = (2 * M * D * 2 + 4 * M) + (M * D * 2 + N * D * 4 + 8 * N * k) + (2 * M * D * 2 + 8 * M) \
+            + (M * D * 2 + N * D * 2 + 4 * N * k) + (M * D * 2 + N * D * 2 + 4 * N * k)
+        res["block_fwd_bwd"] = dict(ms=round(t, 4), GBs=round(model / (t * 1e-3) / 1e9, 1),
+                                    note="sort + dispatch + combine fwd, fused combine bwd + dispatch bwd, torch glue "
+                                         "(the loss reduction) included")
+        out[f"k={k}"] = res
+    k6 = out["k=6"]["gather_rows"]["GBs"]
+    print(json.dumps({
+        "metric": "MoE permute kernels GB/s @1 GPU (reference microbench shapes)", "value": k6, "unit": "GB/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": out["k=6"]["gather_rows"]["ms"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16 rows, f32 reductions",
+        "data": "synthetic normals, top-k of random logits",
+        "config": {"workload": f"colab/tpu_permute_bench.py shapes: N={N} D={D} E={E} k in (6, 12)"},
+        "kernels": out,
+        "roofline": {"kernel": "gather_rows (k=6)", "bound": "hbm", "achieved": k6, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(k6 / PEAK_HBM_GBS, 4), "traffic": None}}), flush=True)
+
+
+def ragged_bench(a):
+    """lsurge_ragged_dot (forward) and lsurge_ragged_dot_bwd (dlhs + drhs) at the MoE layer's per-weight shapes, the
+    pattern of the reference's GEMM ceiling bench (modal/gemm_bench.py:25-35: up, down and dW per weight): C2's
+    routing (M = 98304 rows in 64 groups from the layer's own top-6 of seeded logits), wi_0 / wi_1 [1024 -> 512] and
+    wo [512 -> 1024]; plus the reference's 8192^3 ceiling (one group) and torch.matmul (hipBLASLt) on the same dense
+    shapes for context.  TF/s count useful rows only."""
+    import torch
+
+    import _lib as L
+    from oracle import moe_oracle as mo
+
+    dev = torch.device("cuda", 0)
+    lib = L.lib()
+    st = L.stream(dev)
+    c = CONFIGS["C2"]
+    rng = __import__("numpy").random.default_rng(0)
+    sel = mo.topk_lower_index(rng.standard_normal((c["T"], c["E"])).astype("float32"), c["k"])
+    gs_np = __import__("numpy").bincount(sel.reshape(-1), minlength=c["E"]).astype("int32")
+    M, E = int(gs_np.sum()), c["E"]
+    gs = torch.from_numpy(gs_np).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    res = {}
+    for name, K, Nn in (("up (wi_0 / wi_1) 1024->512", 1024, 512), ("down (wo) 512->1024", 512, 1024)):
+        lhs = torch.randn((M, K), device=dev, generator=gen).to(torch.bfloat16)
+        rhs = (torch.randn((E, K, Nn), device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        g = torch.randn((M, Nn), device=dev, generator=gen).to(torch.bfloat16)
+        out = torch.empty((M, Nn), dtype=torch.bfloat16, device=dev)
+        dl = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+        dr = torch.empty((E, K, Nn), dtype=torch.float32, device=dev)
+        ws = L.workspace(lib.lsurge_ragged_dot_bwd_workspace_bytes(M, K, Nn, E), dev)
+        fl = 2 * M * K * Nn
+
+        def fwd():
+            L.check(lib.lsurge_ragged_dot(L.ptr(lhs), L.ptr(rhs), L.ptr(gs), M, K, Nn, E, L.BF16, L.ptr(out), L.BF16,
+                                          L.ptr(ws), ws.numel(), st), "ragged_dot")
+
+        def bwd():
+            L.check(lib.lsurge_ragged_dot_bwd(L.ptr(lhs), L.ptr(rhs), L.ptr(gs), L.ptr(g), M, K, Nn, E, L.BF16, L.ptr(dl),
+                                              L.ptr(dr), L.ptr(ws), ws.numel(), st), "ragged_dot_bwd")
+
+        tf, tb = _time_ms(fwd, a.steps, a.warmup), _time_ms(bwd, a.steps, a.warmup)
+        dense = torch.randn((M, K), device=dev, generator=gen).to(torch.bfloat16)
+        wd = rhs[0].contiguous()
+        th = _time_ms(lambda: torch.matmul(dense, wd), a.steps, a.warmup)
+        res[name] = dict(fwd_ms=round(tf, 4), fwd_TFs=round(fl / (tf * 1e-3) / 1e12, 1), bwd_ms=round(tb, 4),
+                         bwd_TFs=round(2 * fl / (tb * 1e-3) / 1e12, 1),
+                         hipblaslt_dense_same_shape_TFs=round(fl / (th * 1e-3) / 1e12, 1))
+    big = torch.randn((8192, 8192), device=dev, generator=gen).to(torch.bfloat16)
+    out = torch.empty_like(big)
+    one = torch.tensor([8192], dtype=torch.int32, device=dev)
+    ws = L.workspace(lib.lsurge_ragged_dot_workspace_bytes(8192, 1), dev)
+    bigt = big.t().contiguous()
+    t8 = _time_ms(lambda: L.check(lib.lsurge_ragged_dot(L.ptr(big), L.ptr(bigt), L.ptr(one), 8192, 8192, 8192, 1,
+                                                         L.BF16, L.ptr(out), L.BF16, L.ptr(ws), ws.numel(), st), "rd"),
+                  max(3, a.steps // 4), 2)
+    t8h = _time_ms(lambda: torch.matmul(big, big), max(3, a.steps // 4), 2)
+    res["reference 8192^3 (one group)"] = dict(ms=round(t8, 4), TFs=round(2 * 8192 ** 3 / (t8 * 1e-3) / 1e12, 1),
+                                               hipblaslt_TFs=round(2 * 8192 ** 3 / (t8h * 1e-3) / 1e12, 1))
+    up = res["up (wi_0 / wi_1) 1024->512"]["fwd_TFs"]
+    print(json.dumps({
+        "metric": "ragged_dot (padded_gmm drop-in) TFLOP/s @1 GPU, layer per-weight shapes", "value": up,
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": res["up (wi_0 / wi_1) 1024->512"]["fwd_ms"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 (f32 accumulation)", "data": "synthetic normals; C2 group sizes",
+        "config": {"workload": f"ragged_dot M={M} E={E} (C2 routing), per-weight shapes of modal/gemm_bench.py"},
+        "kernels": res,
+        "roofline": {"kernel": "ragged_dot up fwd", "bound": "mfma", "achieved": up, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(up / PEAK_BF16_TFLOPS, 4), "traffic": None}}), flush=True)
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -441,10 +662,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fp8", action="store_true", help="forward only, expert GEMMs in FP8 (E4M3, current scaling)")
     ap.add_argument("--fwd-only", action="store_true", help="time the forward alone (bf16)")
-    ap.add_argument("--op", choices=["moe", "conv", "gdn"], default="moe",
+    ap.add_argument("--op", choices=["moe", "conv", "gdn", "permute", "ragged_dot"], default="moe",
                     help="conv: the Gated DeltaNet block's causal depthwise Conv1D (modal/fast_conv.py) at the "
                          "reference config's shape, forward + backward GB/s; gdn: its chunked gated delta rule "
-                         "forward (modal/gdn_fast.py), tokens/s")
+                         "forward (modal/gdn_fast.py), tokens/s; permute: the moe_permute kernels at the shapes of "
+                         "colab/tpu_permute_bench.py; ragged_dot: the padded_gmm drop-in at the layer's per-weight "
+                         "shapes (modal/gemm_bench.py)")
     ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")
     ap.add_argument("--concurrency", type=int, default=1,
                     help="timed region: 1 runs the layer's independent chains on helper streams "
@@ -458,6 +681,9 @@ def main():
     ap.add_argument("--copy-fetch", metavar="DIR")
     ap.add_argument("--copy-write", metavar="DIR")
     ap.add_argument("--copy-probe-mib", type=int, default=1024, help="size of the --copy-probe run being calibrated on")
+    ap.add_argument("--pmc-extra", metavar="DIR", action="append", default=[],
+                    help="with --profile-summary: rocprofv3 --pmc output directories of further counter passes "
+                         "(clock, MFMA utilisation, LDS and TA/TD activity per role)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against a known byte count) and exit")
@@ -491,6 +717,12 @@ def main():
         return
     if a.op == "gdn":
         gdn_bench(a)
+        return
+    if a.op == "permute":
+        permute_bench(a)
+        return
+    if a.op == "ragged_dot":
+        ragged_bench(a)
         return
 
     import _lib

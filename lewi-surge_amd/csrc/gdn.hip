@@ -60,7 +60,7 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
                                                         bf16_t* __restrict__ u_out, bf16_t* __restrict__ w_out,
                                                         float* __restrict__ attn_out, float* __restrict__ gcum_out) {
   // k (then k beta) and q (then v beta once the attention is done); in the S product k beta is formed from k where it
-  // is used.  68 KB of LDS: two workgroups per CU.
+  // is used.  72,128 bytes (70.4 KiB) of LDS: two workgroups per CU.
   __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], qs[GC][GP];
   __shared__ float Sm[GC][GC + 1], Am[GC][GC + 1];
   __shared__ float Tb[GC / 16 - 1][16][17];  // the blocked inverse's partial products of one level
