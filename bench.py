@@ -10,8 +10,8 @@ roofline: the dominant kernel (largest share of the step, found with HIP events 
 profiled pass that runs every kernel on one stream) is bracketed by a pair of HIP events in every timed step;
 achieved = algorithmic flops (or bytes) per launch / its mean event-timed duration.  The timed region runs the
 layer's independent chains on helper streams (--concurrency 1, the default; lsurge_set_concurrency).
-cpu_baseline: the numpy CPU oracle's float32 layer forward + backward on a bounded token sample of the same
-layer, timed on this host.
+cpu_baseline: the numpy CPU oracle's float32 layer forward + backward at the config's full token count, timed on this
+host; at C2 also `cpu_baseline_c1_fwd`, the C1 forward (BASELINE.md's pair).
 
 --fp8: the layer forward with every expert GEMM on E4M3 operands (lsurge_moe_fwd_fp8, current scaling); a step is
 the weights' quantisation (once per optimizer step in training) plus the forward; `ms_per_step_cached_weights`
@@ -138,8 +138,10 @@ def prof_table(lib, steps):
     return out
 
 
-def cpu_baseline(c, target_s=15.0):
-    """Time the numpy oracle (float32) on a bounded token sample of the same layer; returns tokens/s."""
+def cpu_baseline(c, target_s=12.0, max_iters=50):
+    """Time the numpy oracle (float32) of the same layer at the config's full token count on this host's cores:
+    router (the bit-exact C restatement, one thread), forward, and the backward when the config has one.  One warm-up
+    call, then calls until target_s has passed (at least one).  Returns the cpu_baseline object of the JSON line."""
     import numpy as np
     from oracle import c_oracle as co
     from oracle import moe_oracle as mo
@@ -149,8 +151,8 @@ def cpu_baseline(c, target_s=15.0):
     except ImportError:  # pragma: no cover
         threadpool_limits = None
     cores = len(os.sched_getaffinity(0))
-    Ts = 1024
-    p = mo.make_inputs(T=Ts, d=c["d"], E=c["E"], k=c["k"], f=c["f"], fs=c["fs"], seed=0, zipf=c["zipf"])
+    T = c["T"]
+    p = mo.make_inputs(T=T, d=c["d"], E=c["E"], k=c["k"], f=c["f"], fs=c["fs"], seed=0, zipf=c["zipf"])
     ctx = threadpool_limits(limits=cores) if threadpool_limits else None
     try:
         def one():
@@ -165,14 +167,15 @@ def cpu_baseline(c, target_s=15.0):
             one()
             n += 1
             el = time.perf_counter() - t0
-            if el > target_s or n >= 50:
+            if el > target_s or n >= max_iters:
                 break
     finally:
         if ctx is not None:
             ctx.__exit__(None, None, None)
-    return dict(value=Ts * n / el, unit="tokens/s", cores=cores, kind="port",
-                sample=f"numpy float32 oracle ({'fwd+bwd' if c['bwd'] else 'fwd'}) of the same layer on {Ts} tokens "
-                       f"x {n} iterations ({el:.1f} s), BLAS threads={cores}, router in C (1 thread)")
+    return dict(value=T * n / el, unit="tokens/s", cores=cores, kind="port",
+                sample=f"numpy float32 oracle ({'fwd+bwd' if c['bwd'] else 'fwd'}) of the same layer at the full T={T} "
+                       f"(about {T * c['k'] // c['E']} rows per expert), {n} calls after one warm-up ({el:.1f} s), "
+                       f"BLAS threads={cores}, router in C (1 thread)")
 
 
 # ------------------------------------------------------------------------------------------ profile summary
@@ -845,6 +848,8 @@ def main():
     }
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(c)
+        if a.config == "C2" and c["bwd"]:  # BASELINE.md's pair: C1 forward beside C2 forward + backward
+            res["cpu_baseline_c1_fwd"] = cpu_baseline(CONFIGS["C1"], target_s=5.0)
     print(json.dumps(res), flush=True)
 
 
