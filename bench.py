@@ -452,10 +452,12 @@ def conv_bench(a):
 
 
 def gdn_bench(a):
-    """Chunked gated delta rule forward at configs/stage1.yml's GDN shape: per_device_batch_size 8,
-    max_target_length 4096, 8 value heads x 128 (keys repeated to the value heads), chunks of 64.  Algorithmic flops
-    per chunk and head: 2 (2 C^2 Dk + 2 C^2 Dv) chunk-local (S, attn, u, w) + 2 (2 C Dk Dv + C^2 Dv + C Dk Dv) scan
-    (q S, w S, attn v_new, the state update), counted in full as the reference's dense products are."""
+    """Chunked gated delta rule at configs/stage1.yml's GDN shape: per_device_batch_size 8, max_target_length 4096,
+    8 value heads x 128 (keys repeated to the value heads), chunks of 64: the forward, and forward + backward (the
+    backward recomputes the forward's chunk products and states, as a remat'd training step would).  Algorithmic flops
+    per chunk and head, forward: 2 (2 C^2 Dk + 2 C^2 Dv) chunk-local (S, attn, u, w) + 2 (2 C Dk Dv + C^2 Dv + C Dk Dv)
+    scan (q S, w S, attn v_new, the state update); the backward counts twice the forward's (the usual 2x for the
+    gradients of every product), so fwd + bwd = 3 x forward, counted in full as the reference's dense products are."""
     import torch
 
     import _lib as L
@@ -468,39 +470,49 @@ def gdn_bench(a):
     v = torch.randn((B, T, H, D), device=dev, generator=gen).to(torch.bfloat16)
     g = -torch.rand((B, T, H), device=dev, generator=gen) * 0.1
     beta = torch.sigmoid(torch.randn((B, T, H), device=dev, generator=gen)).to(torch.bfloat16)
+    do = torch.randn((B, T, H, D), device=dev, generator=gen).to(torch.bfloat16)
     o = torch.empty_like(v)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dg = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    db = torch.empty_like(dg)
     lib = L.lib()
     ws = L.workspace(lib.lsurge_gdn_chunked_workspace_bytes(B, T, H, D, D), dev)
+    wsb = L.workspace(lib.lsurge_gdn_chunked_bwd_workspace_bytes(B, T, H, D, D), dev)
     st = L.stream(dev)
 
     def fwd():
         L.check(lib.lsurge_gdn_chunked_fwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D, None,
                                            L.ptr(o), None, L.ptr(ws), ws.numel(), st), "gdn_chunked_fwd")
 
-    for _ in range(a.warmup):
+    def bwd():
+        L.check(lib.lsurge_gdn_chunked_bwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D, None,
+                                           L.ptr(do), None, L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg), L.ptr(db), None,
+                                           L.ptr(wsb), wsb.numel(), st), "gdn_chunked_bwd")
+
+    def step():
         fwd()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(a.steps):
-        fwd()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / a.steps
+        bwd()
+
+    ms_f = _time_ms(fwd, a.steps, a.warmup)
+    ms_b = _time_ms(bwd, a.steps, a.warmup)
+    ms = _time_ms(step, a.steps, a.warmup)
     chunks = B * H * ((T + C - 1) // C)
     flops = chunks * 2 * (2 * C * C * D + 2 * C * C * D + 2 * C * D * D + C * C * D + C * D * D)
-    tf = flops / (ms * 1e-3) / 1e12
+    tf = 3 * flops / (ms * 1e-3) / 1e12
     print(json.dumps({
-        "metric": "Gated DeltaNet chunked scan forward tokens/sec @1 GPU", "value": round(B * T / (ms * 1e-3), 1),
+        "metric": "Gated DeltaNet chunked scan fwd+bwd tokens/sec @1 GPU", "value": round(B * T / (ms * 1e-3), 1),
         "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16 in/out, f32 arithmetic",
         "data": "synthetic normals (l2-normalised keys)",
-        "config": {"workload": f"chunked gated delta rule fwd B={B} T={T} H={H} Dk=Dv={D} chunk={C} "
+        "config": {"workload": f"chunked gated delta rule fwd+bwd B={B} T={T} H={H} Dk=Dv={D} chunk={C} "
                                "(configs/stage1.yml GDN shape)"},
+        "fwd": {"ms": round(ms_f, 4), "tokens_s": round(B * T / (ms_f * 1e-3), 1),
+                "TFLOP/s": round(flops / (ms_f * 1e-3) / 1e12, 2)},
+        "bwd": {"ms": round(ms_b, 4), "TFLOP/s": round(2 * flops / (ms_b * 1e-3) / 1e12, 2),
+                "note": "includes the recompute of the forward's chunk products and states"},
         "roofline": {"bound": "valu", "achieved": round(tf, 2), "peak": 157.3, "unit": "TFLOP/s",
                      "frac": round(tf / 157.3, 4), "traffic": None,
                      "note": "f32 arithmetic on the VALU, priced against the MI355X fp32 matrix peak"}}), flush=True)
-
 
 
 def _time_ms(fn, steps, warmup):

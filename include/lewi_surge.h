@@ -305,6 +305,18 @@ int lsurge_gdn_chunked_fwd(const void* q, const void* k, const void* v, const fl
                            int64_t t, int64_t h, int64_t dk, int64_t dv, const float* h0, void* o, float* h_out,
                            void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
 
+/* Backward of lsurge_gdn_chunked_fwd for upstream do [b, t, h, dv] bf16 and dh_final [b, h, dk, dv] f32 (the final
+ * state's gradient, or NULL for 0): dq, dk, dv [b, t, h, 128] bf16, dg, dbeta [b, t, h] f32 and dh0 [b, h, dk, dv] f32
+ * (NULL: not written).  h0 is the forward's initial state (NULL = 0).  The forward is recomputed from the inputs.
+ * The gradients are those XLA's autodiff gives for the reference's chunked form (the bf16 rounding points taken with
+ * derivative 1, as for a dtype cast), computed in f32.  Replaces the training backward of fast_chunk_gated_delta_rule
+ * (modal/gdn_fast.py:37-113; installed for training at lightning/train_stage1.py:67-69). */
+size_t lsurge_gdn_chunked_bwd_workspace_bytes(int64_t b, int64_t t, int64_t h, int64_t dk, int64_t dv);
+int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const float* g, const void* beta, int64_t b,
+                           int64_t t, int64_t h, int64_t dk, int64_t dv, const float* h0, const void* dout,
+                           const float* dh_final, void* dq, void* dk_out, void* dv_out, float* dg, float* dbeta,
+                           float* dh0, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Test hooks (no reference counterpart): failure injection for the error paths.
  * ------------------------------------------------------------------------------------------------ */

@@ -89,6 +89,9 @@ _SIGS = {
     "lsurge_causal_conv1d_bwd": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _sz, _p]),
     "lsurge_gdn_chunked_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "lsurge_gdn_chunked_fwd": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _sz, _p]),
+    "lsurge_gdn_chunked_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "lsurge_gdn_chunked_bwd": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p,
+                                      _p, _p, _sz, _p]),
     "lsurge_prof_enable": (_int, [_int]),
     "lsurge_prof_collect": (_int, []),
     "lsurge_prof_kernel_count": (_int, []),

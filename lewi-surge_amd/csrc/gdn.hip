@@ -58,7 +58,9 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
                                                         const bf16_t* __restrict__ v, const float* __restrict__ g,
                                                         const bf16_t* __restrict__ beta, int T, int H, float qscale,
                                                         bf16_t* __restrict__ u_out, bf16_t* __restrict__ w_out,
-                                                        float* __restrict__ attn_out, float* __restrict__ gcum_out) {
+                                                        float* __restrict__ attn_out, float* __restrict__ gcum_out,
+                                                        float* __restrict__ s_out = nullptr,
+                                                        float* __restrict__ a_out = nullptr) {
   // k (then k beta) and q (then v beta once the attention is done); in the S product k beta is formed from k where it
   // is used.  72,128 bytes (70.4 KiB) of LDS: two workgroups per CU.
   __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], qs[GC][GP];
@@ -204,6 +206,11 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
         }
       }
     }
+    if (s_out)  // the backward reads the decayed S and A = (I + S)^-1 of every chunk
+      for (int e = tid; e < GC * GC; e += GTH) {
+        s_out[chunk_id * GC * GC + e] = Sm[e / GC][e % GC];
+        a_out[chunk_id * GC * GC + e] = Am[e / GC][e % GC];
+      }
     bf16_t* ub = u_out + chunk_id * GC * GD;
     bf16_t* wb = w_out + chunk_id * GC * GD;
 #pragma unroll
@@ -224,7 +231,8 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
                                                        const float* __restrict__ attn_in,
                                                        const float* __restrict__ gcum_in, int T, int H, int N,
                                                        float qscale, const float* __restrict__ h0,
-                                                       bf16_t* __restrict__ o, float* __restrict__ h_out) {
+                                                       bf16_t* __restrict__ o, float* __restrict__ h_out,
+                                                       float* __restrict__ h_chunks = nullptr) {
   __shared__ __attribute__((aligned(16))) bf16_t qs[GC][GP], ks[GC][GP], ws[GC][GP];
   // state slice and v_new with 16-byte aligned rows (pitch SB + 4): a thread reads 4 or 8 consecutive columns at once,
   // and the 8 column groups of a row that a wave reads at one d are distinct 16-byte slots
@@ -274,6 +282,11 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
     const int t0 = n * GC;
     const int64_t chunk_id = bh * N + n;
     __syncthreads();  // the previous chunk is done with the tiles
+    if (h_chunks)  // the state entering chunk n, for the backward
+      for (int e = tid; e < GD * SB; e += GTH) {
+        const int d = e / SB, c = e % SB;
+        h_chunks[(chunk_id * GD + d) * GD + cb + c] = hs[d][c];
+      }
 #pragma unroll
     for (int p = 0; p < PP; ++p) {
       const int e = tid + GTH * p, i = e / (GD / 8), c = 8 * (e % (GD / 8));
@@ -329,7 +342,7 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
 #pragma unroll
         for (int s = 0; s < 4; ++s) acc[s] = fmaf(a, vv[s], acc[s]);
       }
-      if (t0 + i < T) {
+      if (o && t0 + i < T) {  // the backward's recompute needs the states only
         bf16_t* op = o + ((row0 + t0 + i) * H + h) * GD + cb + ci;
         *reinterpret_cast<uint2*>(op) = uint2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
       }
@@ -359,6 +372,566 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
       const int d = e / SB, c = e % SB;
       h_out[(bh * GD + d) * GD + cb + c] = hs[d][c];
     }
+}
+
+
+// =====================================================================================================================
+// Backward.  XLA differentiates the reference's chunked form when the model trains through it (gdn_fast.py:37-113,
+// installed for training at lightning/train_stage1.py:67-69); these kernels compute the same gradients in reverse
+// order.  With the upstream gradient do of o and dH_T of the final state, per chunk (rows i, j of the chunk; the bf16
+// rounding points of the forward are taken with derivative 1, as autodiff takes a dtype cast):
+//   reverse scan   dH_n = the gradient of the state leaving chunk n (dH_T for the last chunk), and
+//                  dv_new = attn^T do + kd dH_n,  dH_{n-1} = e^gl dH_n + qg^T do - w^T dv_new
+//                  with kd = k e^(gl - gcum), qg = q e^gcum, gl = gcum of the last row;
+//   chunk grads    (all chunks at once, from the forward's saved states h_n and the reverse scan's dH_n)
+//                  v_new = u - w h_n, dqg = do h_n^T, dkd = v_new dH_n^T, dP = do v_new^T (lower), du = dv_new,
+//                  dw = -dv_new h_n^T, dgl = e^gl <dH_n, h_n>;
+//   chunk-local    dA = du vb^T + dw kbg^T, dS = -(A^T dA A^T) (strictly lower), dvb = A^T du, dkbg = A^T dw and from
+//                  there dq, dk, dv, dbeta and dg (the gradient of gcum, then a suffix sum over the chunk).
+
+// grid (GD / SB, H, B): the reverse scan for SB value columns of the state gradient.
+__global__ __launch_bounds__(GTH) void gdn_bscan_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                                        const bf16_t* __restrict__ w_in, const float* __restrict__ attn_in,
+                                                        const float* __restrict__ gcum_in, const bf16_t* __restrict__ dout,
+                                                        int T, int H, int N, float qscale,
+                                                        const float* __restrict__ dh_final,
+                                                        float* __restrict__ dh_chunks, float* __restrict__ dh0) {
+  __shared__ __attribute__((aligned(16))) bf16_t qs[GC][GP], ks[GC][GP], ws[GC][GP];
+  constexpr int SP = SB + 4;
+  __shared__ __attribute__((aligned(16))) float dh[GD][SP], dvn[GC][SP], dos[GC][SP];
+  __shared__ float at[GC][GC + 1];
+  __shared__ float gc[GC], ek[GC], eg[GC];
+  const int cb = blockIdx.x * SB, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int64_t row0 = (int64_t)b * T;
+  const int64_t bh = (int64_t)b * H + h;
+  for (int e = tid; e < GD * SB; e += GTH) {
+    const int d = e / SB, c = e % SB;
+    dh[d][c] = dh_final ? dh_final[(bh * GD + d) * GD + cb + c] : 0.f;
+  }
+  const int ri = tid / 8, ci = 4 * (tid % 8);   // dv_new outputs: row ri, columns ci .. ci + 3
+  const int hd = tid / 4, hc = 8 * (tid % 4);   // state-gradient outputs: row hd, columns hc .. hc + 7
+  for (int n = N - 1; n >= 0; --n) {
+    const int t0 = n * GC;
+    const int64_t chunk_id = bh * N + n;
+    __syncthreads();  // the previous chunk is done with the tiles and dh is final
+    load_tile(ks, k, row0, T, t0, H, h, 1.f);
+    load_tile(qs, q, row0, T, t0, H, h, qscale);
+    for (int e = tid; e < GC * (GD / 8); e += GTH) {
+      const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
+      *reinterpret_cast<u32x4*>(&ws[i][c]) = *reinterpret_cast<const u32x4*>(w_in + chunk_id * GC * GD + i * GD + c);
+    }
+    for (int e = tid; e < GC * GC; e += GTH) at[e / GC][e % GC] = attn_in[chunk_id * GC * GC + e];
+    for (int e = tid; e < GC * SB; e += GTH) {
+      const int i = e / SB, c = e % SB;
+      dos[i][c] = t0 + i < T ? bf16_to_f32(dout[((row0 + t0 + i) * H + h) * GD + cb + c]) : 0.f;
+    }
+    if (tid < GC) gc[tid] = gcum_in[chunk_id * GC + tid];
+    for (int e = tid; e < GD * SB; e += GTH) {  // the gradient of the state leaving this chunk
+      const int d = e / SB, c = e % SB;
+      dh_chunks[(chunk_id * GD + d) * GD + cb + c] = dh[d][c];
+    }
+    __syncthreads();
+    if (tid < GC) {
+      ek[tid] = __expf(gc[GC - 1] - gc[tid]);
+      eg[tid] = __expf(gc[tid]);
+    }
+    __syncthreads();
+    // dv_new = attn^T do + kd dH (attn is zero above the diagonal: rows j >= ri)
+    {
+      float acc[4] = {}, kacc[4] = {};
+      for (int j = ri; j < GC; ++j) {
+        const float a = at[j][ri];
+        const f32x4 dv = *reinterpret_cast<const f32x4*>(&dos[j][ci]);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) acc[s2] = fmaf(a, dv[s2], acc[s2]);
+      }
+      for (int d = 0; d < GD; d += 8) {
+        float k8[8];
+        unpack8g(*reinterpret_cast<const u32x4*>(&ks[ri][d]), k8);
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+          const f32x4 hv = *reinterpret_cast<const f32x4*>(&dh[d + x][ci]);
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2) kacc[s2] = fmaf(k8[x], hv[s2], kacc[s2]);
+        }
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) dvn[ri][ci + s2] = fmaf(ek[ri], kacc[s2], acc[s2]);
+    }
+    __syncthreads();
+    // dH <- e^gl dH + qg^T do - w^T dv_new
+    float nd[8];
+    {
+      const float el = __expf(gc[GC - 1]);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) nd[x] = dh[hd][hc + x] * el;
+      for (int i = 0; i < GC; ++i) {
+        const float qv = bf16_to_f32(qs[i][hd]) * eg[i], wv = bf16_to_f32(ws[i][hd]);
+        const f32x4 d0 = *reinterpret_cast<const f32x4*>(&dos[i][hc]), d1 = *reinterpret_cast<const f32x4*>(&dos[i][hc + 4]);
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(&dvn[i][hc]), v1 = *reinterpret_cast<const f32x4*>(&dvn[i][hc + 4]);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          nd[x] = fmaf(qv, d0[x], fmaf(-wv, v0[x], nd[x]));
+          nd[x + 4] = fmaf(qv, d1[x], fmaf(-wv, v1[x], nd[x + 4]));
+        }
+      }
+    }
+    __syncthreads();  // every thread has read the old dH
+#pragma unroll
+    for (int x = 0; x < 8; ++x) dh[hd][hc + x] = nd[x];
+  }
+  __syncthreads();
+  if (dh0)
+    for (int e = tid; e < GD * SB; e += GTH) {
+      const int d = e / SB, c = e % SB;
+      dh0[(bh * GD + d) * GD + cb + c] = dh[d][c];
+    }
+}
+
+// grid (N, H, B): per chunk, the products with the saved state h_n and the scan's dH_n, streamed over the value
+// columns in blocks of SB: v_new, dv_new (= du, written in bf16, the compute dtype of u), dqg, dkd, dw (bf16, the
+// compute dtype of w), dP (lower incl. diagonal) and dgl.
+__global__ __launch_bounds__(GTH) void gdn_bgrad_kernel(const bf16_t* __restrict__ k,
+                                                        const bf16_t* __restrict__ u_in, const bf16_t* __restrict__ w_in,
+                                                        const float* __restrict__ attn_in,
+                                                        const float* __restrict__ gcum_in, const bf16_t* __restrict__ dout,
+                                                        const float* __restrict__ h_chunks,
+                                                        const float* __restrict__ dh_chunks, int T, int H,
+                                                        float* __restrict__ dqg_out, float* __restrict__ dkd_out,
+                                                        bf16_t* __restrict__ du_out, bf16_t* __restrict__ dw_out,
+                                                        float* __restrict__ dp_out, float* __restrict__ dgl_out) {
+  __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], ws[GC][GP];
+  constexpr int SP = SB + 4;
+  __shared__ __attribute__((aligned(16))) float hb[GD][SP], db[GD][SP], dob[GC][SP], vnb[GC][SP], dvb[GC][SP];
+  // the block's h, dH and v_new transposed ([column][row]): in the accumulation below the 16 lanes of a row group read
+  // 16 consecutive 32-byte (16-byte) pieces of one row instead of one value from each of 16 rows 8 (4) rows apart,
+  // which put them on 2 (4) banks
+  constexpr int TP = GD + 4;
+  __shared__ __attribute__((aligned(16))) float hT[SB][TP], dT[SB][TP], vT[SB][GC + 4];
+  __shared__ float at[GC][GC + 1];
+  __shared__ float gc[GC], ek[GC], red[GTH / 64];
+  const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z, N = gridDim.x;
+  const int tid = threadIdx.x, t0 = n * GC;
+  const int64_t row0 = (int64_t)b * T;
+  const int64_t chunk_id = ((int64_t)b * H + h) * N + n;
+  load_tile(ks, k, row0, T, t0, H, h, 1.f);
+  for (int e = tid; e < GC * (GD / 8); e += GTH) {
+    const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
+    *reinterpret_cast<u32x4*>(&ws[i][c]) = *reinterpret_cast<const u32x4*>(w_in + chunk_id * GC * GD + i * GD + c);
+  }
+  for (int e = tid; e < GC * GC; e += GTH) at[e / GC][e % GC] = attn_in[chunk_id * GC * GC + e];
+  if (tid < GC) gc[tid] = gcum_in[chunk_id * GC + tid];
+  __syncthreads();
+  if (tid < GC) ek[tid] = __expf(gc[GC - 1] - gc[tid]);
+  const int ri = tid / 8, ci = 4 * (tid % 8);          // [GC][SB] block products: row ri, columns ci .. ci + 3
+  const int i0 = 2 * (tid / 16), c0 = 8 * (tid % 16);  // [GC][GD] accumulators: rows i0, i0 + 1, columns c0 .. c0 + 7
+  const int j0 = 4 * (tid % 16);                       // [GC][GC] accumulator: rows i0, i0 + 1, columns j0 .. j0 + 3
+  const int hd = tid / 4, hc = 8 * (tid % 4);          // [GD][SB] elementwise: row hd, columns hc .. hc + 7
+  float aq[2][8] = {}, ak[2][8] = {}, aw[2][8] = {}, ap[2][4] = {};
+  float gl_part = 0.f;
+  const float* hsrc = h_chunks + chunk_id * GD * GD;
+  const float* dsrc = dh_chunks + chunk_id * GD * GD;
+  for (int cb = 0; cb < GD; cb += SB) {
+    __syncthreads();  // the previous block's tiles are consumed (and the setup above is done)
+    for (int e = tid; e < GD * SB / 4; e += GTH) {
+      const int d = e / (SB / 4), c = 4 * (e % (SB / 4));
+      const f32x4 hv = *reinterpret_cast<const f32x4*>(hsrc + d * GD + cb + c);
+      const f32x4 dv = *reinterpret_cast<const f32x4*>(dsrc + d * GD + cb + c);
+      *reinterpret_cast<f32x4*>(&hb[d][c]) = hv;
+      *reinterpret_cast<f32x4*>(&db[d][c]) = dv;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        hT[c + x][d] = hv[x];
+        dT[c + x][d] = dv[x];
+      }
+    }
+    for (int e = tid; e < GC * SB; e += GTH) {
+      const int i = e / SB, c = e % SB;
+      dob[i][c] = t0 + i < T ? bf16_to_f32(dout[((row0 + t0 + i) * H + h) * GD + cb + c]) : 0.f;
+    }
+    __syncthreads();
+    {  // <dH, h> over this block
+#pragma unroll
+      for (int x = 0; x < 8; ++x) gl_part = fmaf(hb[hd][hc + x], db[hd][hc + x], gl_part);
+    }
+    {  // v_new = u - w h and dv_new = attn^T do + kd dH for row ri, columns ci .. ci + 3
+      float wv[4] = {}, kv[4] = {}, av[4] = {};
+      for (int d = 0; d < GD; d += 8) {
+        float w8[8], k8[8];
+        unpack8g(*reinterpret_cast<const u32x4*>(&ws[ri][d]), w8);
+        unpack8g(*reinterpret_cast<const u32x4*>(&ks[ri][d]), k8);
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+          const f32x4 hv = *reinterpret_cast<const f32x4*>(&hb[d + x][ci]);
+          const f32x4 dv = *reinterpret_cast<const f32x4*>(&db[d + x][ci]);
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2) {
+            wv[s2] = fmaf(w8[x], hv[s2], wv[s2]);
+            kv[s2] = fmaf(k8[x], dv[s2], kv[s2]);
+          }
+        }
+      }
+      for (int j = ri; j < GC; ++j) {
+        const float a = at[j][ri];
+        const f32x4 dv = *reinterpret_cast<const f32x4*>(&dob[j][ci]);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) av[s2] = fmaf(a, dv[s2], av[s2]);
+      }
+      const bf16_t* ub = u_in + chunk_id * GC * GD + ri * GD + cb + ci;
+      float dvv[4];
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        vnb[ri][ci + s2] = bf16_to_f32(ub[s2]) - wv[s2];
+        vT[ci + s2][ri] = vnb[ri][ci + s2];
+        dvv[s2] = fmaf(ek[ri], kv[s2], av[s2]);
+        dvb[ri][ci + s2] = dvv[s2];
+      }
+      *reinterpret_cast<uint2*>(du_out + chunk_id * GC * GD + ri * GD + cb + ci) =
+          uint2{pack_bf16x2(dvv[0], dvv[1]), pack_bf16x2(dvv[2], dvv[3])};
+    }
+    __syncthreads();
+    // dqg += do h^T, dkd += v_new dH^T, dw -= dv_new h^T ([GC][GD]); dP += do v_new^T ([GC][GC])
+    for (int c = 0; c < SB; ++c) {
+      float dq0 = dob[i0][c], dq1 = dob[i0 + 1][c];
+      float vn0 = vnb[i0][c], vn1 = vnb[i0 + 1][c];
+      float dv0 = dvb[i0][c], dv1 = dvb[i0 + 1][c];
+      const f32x4 h0v = *reinterpret_cast<const f32x4*>(&hT[c][c0]), h1v = *reinterpret_cast<const f32x4*>(&hT[c][c0 + 4]);
+      const f32x4 d0v = *reinterpret_cast<const f32x4*>(&dT[c][c0]), d1v = *reinterpret_cast<const f32x4*>(&dT[c][c0 + 4]);
+      const float hv8[8] = {h0v[0], h0v[1], h0v[2], h0v[3], h1v[0], h1v[1], h1v[2], h1v[3]};
+      const float dv8[8] = {d0v[0], d0v[1], d0v[2], d0v[3], d1v[0], d1v[1], d1v[2], d1v[3]};
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        aq[0][x] = fmaf(dq0, hv8[x], aq[0][x]);
+        aq[1][x] = fmaf(dq1, hv8[x], aq[1][x]);
+        ak[0][x] = fmaf(vn0, dv8[x], ak[0][x]);
+        ak[1][x] = fmaf(vn1, dv8[x], ak[1][x]);
+        aw[0][x] = fmaf(-dv0, hv8[x], aw[0][x]);
+        aw[1][x] = fmaf(-dv1, hv8[x], aw[1][x]);
+      }
+      const f32x4 vj = *reinterpret_cast<const f32x4*>(&vT[c][j0]);
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        ap[0][y] = fmaf(dq0, vj[y], ap[0][y]);
+        ap[1][y] = fmaf(dq1, vj[y], ap[1][y]);
+      }
+    }
+  }
+  const int64_t ob = chunk_id * GC * GD;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int i = i0 + r;
+    *reinterpret_cast<f32x4*>(dqg_out + ob + i * GD + c0) = f32x4{aq[r][0], aq[r][1], aq[r][2], aq[r][3]};
+    *reinterpret_cast<f32x4*>(dqg_out + ob + i * GD + c0 + 4) = f32x4{aq[r][4], aq[r][5], aq[r][6], aq[r][7]};
+    *reinterpret_cast<f32x4*>(dkd_out + ob + i * GD + c0) = f32x4{ak[r][0], ak[r][1], ak[r][2], ak[r][3]};
+    *reinterpret_cast<f32x4*>(dkd_out + ob + i * GD + c0 + 4) = f32x4{ak[r][4], ak[r][5], ak[r][6], ak[r][7]};
+    *reinterpret_cast<u32x4*>(dw_out + ob + i * GD + c0) =
+        u32x4{pack_bf16x2(aw[r][0], aw[r][1]), pack_bf16x2(aw[r][2], aw[r][3]), pack_bf16x2(aw[r][4], aw[r][5]),
+              pack_bf16x2(aw[r][6], aw[r][7])};
+    *reinterpret_cast<f32x4*>(dp_out + chunk_id * GC * GC + i * GC + j0) =
+        f32x4{j0 <= i ? ap[r][0] : 0.f, j0 + 1 <= i ? ap[r][1] : 0.f, j0 + 2 <= i ? ap[r][2] : 0.f,
+              j0 + 3 <= i ? ap[r][3] : 0.f};
+  }
+  // dgl = e^gl <dH, h>: wave sums, then the 8 waves in order
+  float v = gl_part;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.f;
+    for (int i = 0; i < GTH / 64; ++i) t += red[i];
+    dgl_out[chunk_id] = __expf(gc[GC - 1]) * t;
+  }
+}
+
+// grid (N, H, B): the chunk-local backward of one chunk and the assembly of its input gradients.
+__global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const bf16_t* __restrict__ beta, const float* __restrict__ attn_in, const float* __restrict__ gcum_in,
+    const float* __restrict__ s_in, const float* __restrict__ a_in, const float* __restrict__ dqg_in,
+    const float* __restrict__ dkd_in, const bf16_t* __restrict__ du_in, const bf16_t* __restrict__ dw_in,
+    const float* __restrict__ dp_in, const float* __restrict__ dgl_in, int T, int H, float qscale,
+    bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, float* __restrict__ dg,
+    float* __restrict__ dbeta) {
+  // T1 k, T2 q * scale, T3 k beta, T4 v beta, T5 du, T6 dw (bf16 tiles); M1 / M2 scratch [GC][GC], M3 A
+  __shared__ __attribute__((aligned(16))) bf16_t T1[GC][GP], T2[GC][GP], T3[GC][GP], T4[GC][GP], T5[GC][GP], T6[GC][GP];
+  __shared__ float M1[GC][GC + 1], M2[GC][GC + 1], M3[GC][GC + 1];
+  __shared__ float gc[GC], eg[GC], bt[GC], dgg[GC], rs[GC], cs[GC];
+  const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z, N = gridDim.x;
+  const int tid = threadIdx.x, t0 = n * GC;
+  const int64_t row0 = (int64_t)b * T;
+  const int64_t chunk_id = ((int64_t)b * H + h) * N + n;
+  const int64_t mo = chunk_id * GC * GC, to = chunk_id * GC * GD;
+  if (tid < GC) {
+    const int t = t0 + tid;
+    gc[tid] = gcum_in[chunk_id * GC + tid];
+    bt[tid] = t < T ? bf16_to_f32(beta[(row0 + t) * H + h]) : 0.f;
+    dgg[tid] = 0.f;
+  }
+  load_tile(T1, k, row0, T, t0, H, h, 1.f);
+  load_tile(T2, q, row0, T, t0, H, h, qscale);
+  for (int e = tid; e < GC * (GD / 8); e += GTH) {
+    const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
+    *reinterpret_cast<u32x4*>(&T5[i][c]) = *reinterpret_cast<const u32x4*>(du_in + to + i * GD + c);
+    *reinterpret_cast<u32x4*>(&T6[i][c]) = *reinterpret_cast<const u32x4*>(dw_in + to + i * GD + c);
+  }
+  for (int e = tid; e < GC * GC; e += GTH) {
+    const int i = e / GC, j = e % GC;
+    M2[i][j] = dp_in[mo + e];
+    M3[i][j] = a_in[mo + e];
+    M1[i][j] = dp_in[mo + e] * attn_in[mo + e];  // dP . P: its row sums less its column sums go to dgcum
+  }
+  __syncthreads();
+  if (tid < GC) eg[tid] = __expf(gc[tid]);
+  // k beta and v beta in the compute dtype (gdn_fast.py:78, 87)
+  for (int e = tid; e < GC * (GD / 8); e += GTH) {
+    const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (t0 + i < T) raw = *reinterpret_cast<const u32x4*>(v + ((row0 + t0 + i) * H + h) * GD + c);
+    float f[8], kf[8];
+    unpack8g(raw, f);
+    unpack8g(*reinterpret_cast<const u32x4*>(&T1[i][c]), kf);
+    const float bi = bt[i];
+    *reinterpret_cast<u32x4*>(&T4[i][c]) =
+        u32x4{pack_bf16x2(f[0] * bi, f[1] * bi), pack_bf16x2(f[2] * bi, f[3] * bi), pack_bf16x2(f[4] * bi, f[5] * bi),
+              pack_bf16x2(f[6] * bi, f[7] * bi)};
+    *reinterpret_cast<u32x4*>(&T3[i][c]) =
+        u32x4{pack_bf16x2(kf[0] * bi, kf[1] * bi), pack_bf16x2(kf[2] * bi, kf[3] * bi),
+              pack_bf16x2(kf[4] * bi, kf[5] * bi), pack_bf16x2(kf[6] * bi, kf[7] * bi)};
+  }
+  // row and column sums of M1 (fixed order) -> dgcum
+  auto rowcol = [&]() {
+    if (tid < GC) {
+      float r = 0.f, c = 0.f;
+      for (int j = 0; j < GC; ++j) {
+        r += M1[tid][j];
+        c += M1[j][tid];
+      }
+      dgg[tid] += r - c;
+    }
+  };
+  __syncthreads();
+  rowcol();
+  __syncthreads();
+  const int i0 = 2 * (tid / 16), c0 = 8 * (tid % 16), j0 = 4 * (tid % 16);
+  const float gl = gc[GC - 1];
+  // dP_r = dP . Gi (Gi = e^(gcum_i - gcum_j), lower incl. diagonal) in place
+  for (int e = tid; e < GC * GC; e += GTH) {
+    const int i = e / GC, j = e % GC;
+    M2[i][j] = j <= i ? M2[i][j] * __expf(gc[i] - gc[j]) : 0.f;
+  }
+  __syncthreads();
+  // dq = dP_r k + dqg e^gcum ; dk = dP_r^T q + dkd e^(gl - gcum) (+ the chunk-local terms below)
+  float aq[2][8] = {}, ak[2][8] = {}, akb[2][8] = {};
+  float dgr[2] = {0.f, 0.f}, dgl_rows = 0.f;
+  for (int j = 0; j < GC; ++j) {
+    float k8[8], q8[8];
+    unpack8g(*reinterpret_cast<const u32x4*>(&T1[j][c0]), k8);
+    unpack8g(*reinterpret_cast<const u32x4*>(&T2[j][c0]), q8);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float pij = M2[i0 + r][j], pji = M2[j][i0 + r];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        aq[r][x] = fmaf(pij, k8[x], aq[r][x]);
+        ak[r][x] = fmaf(pji, q8[x], ak[r][x]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int i = i0 + r;
+    const f32x4 g0 = *reinterpret_cast<const f32x4*>(dqg_in + to + i * GD + c0);
+    const f32x4 g1 = *reinterpret_cast<const f32x4*>(dqg_in + to + i * GD + c0 + 4);
+    const f32x4 d0 = *reinterpret_cast<const f32x4*>(dkd_in + to + i * GD + c0);
+    const f32x4 d1 = *reinterpret_cast<const f32x4*>(dkd_in + to + i * GD + c0 + 4);
+    const float gq[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+    const float gk[8] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3]};
+    float q8[8], k8[8];
+    unpack8g(*reinterpret_cast<const u32x4*>(&T2[i][c0]), q8);
+    unpack8g(*reinterpret_cast<const u32x4*>(&T1[i][c0]), k8);
+    const float e = eg[i], ed = __expf(gl - gc[i]);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      aq[r][x] = fmaf(gq[x], e, aq[r][x]);
+      ak[r][x] = fmaf(gk[x], ed, ak[r][x]);
+      dgr[r] = fmaf(gq[x], q8[x] * e, dgr[r]);        // + <dqg, qg>
+      const float s2 = gk[x] * k8[x] * ed;            // <dkd, kd>: - to row i, + to gl
+      dgr[r] -= s2;
+      dgl_rows += s2;
+    }
+  }
+  // dA = du vb^T + dw kbg^T  (kbg = kb e^gcum) -> M1
+  __syncthreads();  // M1's sums are read
+  {
+    float acc[2][4] = {};
+    for (int c = 0; c < GD; c += 8) {
+      float du8[2][8], dw8[2][8];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        unpack8g(*reinterpret_cast<const u32x4*>(&T5[i0 + r][c]), du8[r]);
+        unpack8g(*reinterpret_cast<const u32x4*>(&T6[i0 + r][c]), dw8[r]);
+      }
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        float vb8[8], kb8[8];
+        unpack8g(*reinterpret_cast<const u32x4*>(&T4[j0 + y][c]), vb8);
+        unpack8g(*reinterpret_cast<const u32x4*>(&T3[j0 + y][c]), kb8);
+        const float e = eg[j0 + y];
+#pragma unroll
+        for (int x = 0; x < 8; ++x)
+#pragma unroll
+          for (int r = 0; r < 2; ++r) acc[r][y] = fmaf(du8[r][x], vb8[x], fmaf(dw8[r][x], kb8[x] * e, acc[r][y]));
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) M1[i0 + r][j0 + y] = acc[r][y];
+  }
+  __syncthreads();
+  // X = A^T dA -> M2
+  {
+    float acc[2][4] = {};
+    for (int m = 0; m < GC; ++m) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const float a = M3[m][i0 + r];
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[r][y] = fmaf(a, M1[m][j0 + y], acc[r][y]);
+      }
+    }
+    __syncthreads();  // every read of M2 (dP_r) is done before it is overwritten
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) M2[i0 + r][j0 + y] = acc[r][y];
+  }
+  __syncthreads();
+  // dS = -(X A^T), strictly lower -> M1 (dA is no longer needed); t2 = dS . S for dgcum -> M2 after X is read
+  float dsv[2][4];
+  {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) dsv[r][y] = 0.f;
+    for (int m = 0; m < GC; ++m) {
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        const float a = M3[j0 + y][m];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) dsv[r][y] = fmaf(M2[i0 + r][m], a, dsv[r][y]);
+      }
+    }
+  }
+  __syncthreads();  // X (M2) is read
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+      const int i = i0 + r, j = j0 + y;
+      const float ds = j < i ? -dsv[r][y] : 0.f;
+      M2[i][j] = ds * s_in[mo + i * GC + j];                        // dS . S
+      M1[i][j] = j < i ? ds * __expf(gc[i] - gc[j]) : 0.f;          // dS0 = dS . Gs
+    }
+  __syncthreads();
+  if (tid < GC) {  // dgcum += row sums - column sums of dS . S
+    float r = 0.f, c = 0.f;
+    for (int j = 0; j < GC; ++j) {
+      r += M2[tid][j];
+      c += M2[j][tid];
+    }
+    rs[tid] = r - c;
+  }
+  // dvb = A^T du, dkbg = A^T dw; dkb = dkbg e^gcum + dS0 k; dk += dS0^T kb
+  float avb[2][8] = {}, akg[2][8] = {};
+  for (int m = 0; m < GC; ++m) {
+    float du8[8], dw8[8], k8[8], kb8[8];
+    unpack8g(*reinterpret_cast<const u32x4*>(&T5[m][c0]), du8);
+    unpack8g(*reinterpret_cast<const u32x4*>(&T6[m][c0]), dw8);
+    unpack8g(*reinterpret_cast<const u32x4*>(&T1[m][c0]), k8);
+    unpack8g(*reinterpret_cast<const u32x4*>(&T3[m][c0]), kb8);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float a = M3[m][i0 + r], s0 = M1[i0 + r][m], s0t = M1[m][i0 + r];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        avb[r][x] = fmaf(a, du8[x], avb[r][x]);
+        akg[r][x] = fmaf(a, dw8[x], akg[r][x]);
+        akb[r][x] = fmaf(s0, k8[x], akb[r][x]);
+        ak[r][x] = fmaf(s0t, kb8[x], ak[r][x]);
+      }
+    }
+  }
+  float dbr[2] = {0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int i = i0 + r;
+    float k8[8], kb8[8], v8[8];
+    unpack8g(*reinterpret_cast<const u32x4*>(&T1[i][c0]), k8);
+    unpack8g(*reinterpret_cast<const u32x4*>(&T3[i][c0]), kb8);
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (t0 + i < T) raw = *reinterpret_cast<const u32x4*>(v + ((row0 + t0 + i) * H + h) * GD + c0);
+    unpack8g(raw, v8);
+    const float e = eg[i], bi = bt[i];
+    float dvo[8], dko[8], dqo[8];
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      const float dkb = fmaf(akg[r][x], e, akb[r][x]);   // dkbg e^gcum + dS0 k
+      dgr[r] = fmaf(akg[r][x], kb8[x] * e, dgr[r]);      // + <dkbg, kbg>
+      dbr[r] = fmaf(avb[r][x], v8[x], fmaf(dkb, k8[x], dbr[r]));
+      dvo[x] = avb[r][x] * bi;
+      dko[x] = fmaf(dkb, bi, ak[r][x]);
+      dqo[x] = aq[r][x] * qscale;
+    }
+    if (t0 + i < T) {
+      const int64_t off = ((row0 + t0 + i) * H + h) * GD + c0;
+      *reinterpret_cast<u32x4*>(dq + off) = u32x4{pack_bf16x2(dqo[0], dqo[1]), pack_bf16x2(dqo[2], dqo[3]),
+                                                  pack_bf16x2(dqo[4], dqo[5]), pack_bf16x2(dqo[6], dqo[7])};
+      *reinterpret_cast<u32x4*>(dk + off) = u32x4{pack_bf16x2(dko[0], dko[1]), pack_bf16x2(dko[2], dko[3]),
+                                                  pack_bf16x2(dko[4], dko[5]), pack_bf16x2(dko[6], dko[7])};
+      *reinterpret_cast<u32x4*>(dv + off) = u32x4{pack_bf16x2(dvo[0], dvo[1]), pack_bf16x2(dvo[2], dvo[3]),
+                                                  pack_bf16x2(dvo[4], dvo[5]), pack_bf16x2(dvo[6], dvo[7])};
+    }
+  }
+  // per-row sums over the 16 threads of a row pair (consecutive lanes), then dgcum and dbeta in fixed order
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    dgr[0] += __shfl_xor(dgr[0], o, 64);
+    dgr[1] += __shfl_xor(dgr[1], o, 64);
+    dbr[0] += __shfl_xor(dbr[0], o, 64);
+    dbr[1] += __shfl_xor(dbr[1], o, 64);
+  }
+  __shared__ float dgrow[GC], dbrow[GC], glw[GTH / 64];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) dgl_rows += __shfl_xor(dgl_rows, o, 64);
+  if ((tid & 63) == 0) glw[tid >> 6] = dgl_rows;
+  if ((tid & 15) == 0) {
+    dgrow[i0] = dgr[0];
+    dgrow[i0 + 1] = dgr[1];
+    dbrow[i0] = dbr[0];
+    dbrow[i0 + 1] = dbr[1];
+  }
+  __syncthreads();
+  if (tid < GC) {  // dgcum of row tid, then dg = its suffix sum over the chunk (gcum = cumsum(g)), one wave
+    float x = dgg[tid] + rs[tid] + dgrow[tid];
+    if (tid == GC - 1) {
+      float t = dgl_in[chunk_id];
+      for (int w = 0; w < GTH / 64; ++w) t += glw[w];
+      x += t;
+    }
+#pragma unroll
+    for (int o = 1; o < GC; o <<= 1) {
+      const float y = __shfl_down(x, o, 64);
+      if (tid + o < GC) x += y;
+    }
+    const int t = t0 + tid;
+    if (t < T) {
+      dg[(row0 + t) * H + h] = x;
+      dbeta[(row0 + t) * H + h] = dbrow[tid];
+    }
+  }
 }
 
 int64_t gdn_chunks(int64_t t) { return (t + GC - 1) / GC; }
@@ -412,6 +985,94 @@ int lsurge_gdn_chunked_fwd(const void* q, const void* k, const void* v, const fl
                                    (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)u, (const bf16_t*)w,
                                    (const float*)attn, (const float*)gcum, (int)t, (int)h, (int)N, qscale, h0,
                                    (bf16_t*)o, h_out));
+  return LSURGE_OK;
+}
+
+// workspace of the backward: the forward's chunk products (u, w, attn, gcum) plus S, A and the state entering each
+// chunk, the reverse scan's state gradients, and the chunk gradients (dqg, dkd f32; du, dw bf16; dP, dgl)
+struct GdnBwdWs {
+  bf16_t *u, *w, *du, *dw;
+  float *attn, *gcum, *S, *A, *hs, *dhs, *dqg, *dkd, *dP, *dgl;
+};
+static size_t gdn_bwd_carve(int64_t chunks, void* base, GdnBwdWs* p) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* r = base ? (char*)base + off : nullptr;
+    off += (bytes + 255) / 256 * 256;
+    return r;
+  };
+  const size_t tile16 = (size_t)chunks * GC * GD * sizeof(bf16_t), tile32 = (size_t)chunks * GC * GD * sizeof(float);
+  const size_t mat = (size_t)chunks * GC * GC * sizeof(float), st = (size_t)chunks * GD * GD * sizeof(float);
+  p->u = (bf16_t*)take(tile16);
+  p->w = (bf16_t*)take(tile16);
+  p->du = (bf16_t*)take(tile16);
+  p->dw = (bf16_t*)take(tile16);
+  p->attn = (float*)take(mat);
+  p->gcum = (float*)take((size_t)chunks * GC * sizeof(float));
+  p->S = (float*)take(mat);
+  p->A = (float*)take(mat);
+  p->hs = (float*)take(st);
+  p->dhs = (float*)take(st);
+  p->dqg = (float*)take(tile32);
+  p->dkd = (float*)take(tile32);
+  p->dP = (float*)take(mat);
+  p->dgl = (float*)take((size_t)chunks * sizeof(float));
+  return off;
+}
+
+size_t lsurge_gdn_chunked_bwd_workspace_bytes(int64_t b, int64_t t, int64_t h, int64_t dk, int64_t dv) {
+  if (b < 1 || t < 1 || h < 1 || dk != GD || dv != GD) return 0;
+  GdnBwdWs p;
+  return gdn_bwd_carve(b * h * gdn_chunks(t), nullptr, &p);
+}
+
+int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const float* g, const void* beta, int64_t b,
+                           int64_t t, int64_t h, int64_t dk, int64_t dv, const float* h0, const void* dout,
+                           const float* dh_final, void* dq, void* dk_out, void* dv_out, float* dg, float* dbeta,
+                           float* dh0, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(q && k && v && g && beta && dout && dq && dk_out && dv_out && dg && dbeta && workspace,
+                 "gdn_chunked_bwd: null pointer");
+  LSURGE_REQUIRE(dk == GD && dv == GD, "gdn_chunked_bwd: head dims dk=%lld dv=%lld must be %d", (long long)dk,
+                 (long long)dv, GD);
+  LSURGE_REQUIRE(b >= 1 && b < 65536 && h >= 1 && h < 65536 && t >= 1 && b * t * h < (1ll << 31) / GD &&
+                     b * h * gdn_chunks(t) < (1ll << 31) / (GD * GD),
+                 "gdn_chunked_bwd: bad shape b=%lld t=%lld h=%lld", (long long)b, (long long)t, (long long)h);
+  LSURGE_REQUIRE(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout | (uintptr_t)dq | (uintptr_t)dk_out |
+                  (uintptr_t)dv_out | (uintptr_t)workspace) % 16 == 0,
+                 "gdn_chunked_bwd: q, k, v, do, dq, dk, dv and workspace must be 16-byte aligned");
+  const size_t need = lsurge_gdn_chunked_bwd_workspace_bytes(b, t, h, dk, dv);
+  LSURGE_REQUIRE(workspace_bytes >= need, "gdn_chunked_bwd: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t N = gdn_chunks(t);
+  GdnBwdWs p;
+  gdn_bwd_carve(b * h * N, workspace, &p);
+  const float qscale = round_bf16_host(1.f / sqrtf((float)GD));
+  const dim3 chunk_grid((unsigned)N, (unsigned)h, (unsigned)b), scan_grid(GD / SB, (unsigned)h, (unsigned)b);
+  // forward recompute: chunk products (with S and A) and the state entering every chunk
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(gdn_chunk_kernel, chunk_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
+                                   (const bf16_t*)v, g, (const bf16_t*)beta, (int)t, (int)h, qscale, p.u, p.w, p.attn,
+                                   p.gcum, p.S, p.A));
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(gdn_scan_kernel, scan_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
+                                   (const bf16_t*)p.u, (const bf16_t*)p.w, (const float*)p.attn, (const float*)p.gcum,
+                                   (int)t, (int)h, (int)N, qscale, h0, (bf16_t*)nullptr, (float*)nullptr, p.hs));
+  // reverse scan of the state gradient, then the chunk gradients and the chunk-local backward
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(gdn_bscan_kernel, scan_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
+                                   (const bf16_t*)p.w, (const float*)p.attn, (const float*)p.gcum, (const bf16_t*)dout,
+                                   (int)t, (int)h, (int)N, qscale, dh_final, p.dhs, dh0));
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(gdn_bgrad_kernel, chunk_grid, dim3(GTH), 0, s, (const bf16_t*)k,
+                                   (const bf16_t*)p.u, (const bf16_t*)p.w, (const float*)p.attn, (const float*)p.gcum,
+                                   (const bf16_t*)dout, (const float*)p.hs, (const float*)p.dhs, (int)t, (int)h, p.dqg,
+                                   p.dkd, p.du, p.dw, p.dP, p.dgl));
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(gdn_bchunk_kernel, chunk_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
+                                   (const bf16_t*)v, (const bf16_t*)beta, (const float*)p.attn, (const float*)p.gcum,
+                                   (const float*)p.S, (const float*)p.A, (const float*)p.dqg, (const float*)p.dkd,
+                                   (const bf16_t*)p.du, (const bf16_t*)p.dw, (const float*)p.dP, (const float*)p.dgl,
+                                   (int)t, (int)h, qscale, (bf16_t*)dq, (bf16_t*)dk_out, (bf16_t*)dv_out, dg, dbeta));
   return LSURGE_OK;
 }
 

@@ -1,0 +1,92 @@
+"""Chunked gated delta rule of the Gated DeltaNet block on the HIP library (mirrors modal/gdn_fast.py).
+
+The reference swaps MaxText's `jax_chunk_gated_delta_rule` for `fast_chunk_gated_delta_rule` (gdn_fast.py:37-113) and
+trains through it with XLA autodiff.  Here the forward is lsurge_gdn_chunked_fwd and the backward
+lsurge_gdn_chunked_bwd (which recomputes the forward's chunk products and states from the inputs).
+
+  fast_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None, ...)
+      differentiable op with the reference's signature: query, key [B, T, H, 128], value [B, T, H, 128], g [B, T, H]
+      (log decay, float32), beta [B, T, H]; returns (o [B, T, H, 128] in query's dtype, the final state in the compute
+      dtype when initial_state is given, else None)
+  install(prec, inv, unroll)   the reference's switches (gdn_fast.py:116-125): recorded, the kernels always compute in
+      f32 with the exact inverse
+"""
+from __future__ import annotations
+
+import torch
+
+import _lib as L
+
+PREC = "highest"
+INV = "solve"
+UNROLL = 1
+D = 128
+
+
+class _GdnFn(torch.autograd.Function):
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, h0, want_state):
+        B, T, H, _ = q.shape
+        o = torch.empty_like(v)
+        h_out = torch.empty((B, H, D, D), dtype=torch.float32, device=q.device) if want_state else None
+        lib = L.lib()
+        ws = L.workspace(lib.lsurge_gdn_chunked_workspace_bytes(B, T, H, D, D), q.device)
+        L.check(lib.lsurge_gdn_chunked_fwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D,
+                                           L.ptr(h0), L.ptr(o), L.ptr(h_out), L.ptr(ws), ws.numel(),
+                                           L.stream(q.device)), "gdn_chunked_fwd")
+        ctx.save_for_backward(q, k, v, g, beta, h0)
+        ctx.has_h0 = h0 is not None
+        return (o, h_out) if want_state else (o,)
+
+    @staticmethod
+    def backward(ctx, do, dh_final=None):
+        q, k, v, g, beta, h0 = ctx.saved_tensors
+        B, T, H, _ = q.shape
+        do = L.contig(do.to(torch.bfloat16))
+        dhf = None if dh_final is None else L.contig(dh_final.to(torch.float32))
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        dg = torch.empty((B, T, H), dtype=torch.float32, device=q.device)
+        db = torch.empty_like(dg)
+        dh0 = torch.empty((B, H, D, D), dtype=torch.float32, device=q.device) if ctx.has_h0 else None
+        lib = L.lib()
+        ws = L.workspace(lib.lsurge_gdn_chunked_bwd_workspace_bytes(B, T, H, D, D), q.device)
+        L.check(lib.lsurge_gdn_chunked_bwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D,
+                                           L.ptr(h0), L.ptr(do), L.ptr(dhf), L.ptr(dq), L.ptr(dk), L.ptr(dv),
+                                           L.ptr(dg), L.ptr(db), L.ptr(dh0), L.ptr(ws), ws.numel(),
+                                           L.stream(q.device)), "gdn_chunked_bwd")
+        return dq, dk, dv, dg, db, dh0, None
+
+
+def fast_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
+                                use_qk_norm_in_gdn=False, cp_axis=None, compute_dtype=torch.bfloat16):
+    """modal/gdn_fast.py:37-113.  The kernels take chunks of 64, head dims of 128 and the bf16 compute dtype; the
+    reference's qk-norm and context-parallel branches (43-46, 39-42) are not built and raise NotImplementedError."""
+    if cp_axis is not None:
+        raise NotImplementedError("fast_chunk_gated_delta_rule: context parallelism (cp_axis) is not built")
+    if use_qk_norm_in_gdn:
+        raise NotImplementedError("fast_chunk_gated_delta_rule: the qk-norm branch is not built")
+    if chunk_size != 64 or compute_dtype != torch.bfloat16:
+        raise ValueError("fast_chunk_gated_delta_rule: the kernels take chunk_size=64 and a bf16 compute dtype")
+    if query.shape[-1] != D or value.shape[-1] != D or key.shape != query.shape:
+        raise ValueError(f"fast_chunk_gated_delta_rule: head dims must be {D} (query {tuple(query.shape)}, "
+                         f"value {tuple(value.shape)})")
+    L.require_cuda(query, key, value, g, beta, initial_state)
+    out_dtype = query.dtype
+    q, k, v = (L.contig(t.to(torch.bfloat16)) for t in (query, key, value))
+    bt = L.contig(beta.to(torch.bfloat16))
+    gf = L.contig(g.to(torch.float32))
+    h0 = None if initial_state is None else L.contig(initial_state.to(torch.float32))
+    res = _GdnFn.apply(q, k, v, gf, bt, h0, initial_state is not None)
+    o = res[0].to(out_dtype)
+    return o, (res[1].to(compute_dtype) if initial_state is not None else None)
+
+
+def install(prec="high", inv="neumann", unroll=1):
+    """Record the reference's switches (gdn_fast.py:116-125).  The reference then rebinds MaxText's
+    qwen3.jax_chunk_gated_delta_rule; MaxText is a JAX package and absent here, so JAX callers bind the C ABI through
+    XLA FFI instead."""
+    global PREC, INV, UNROLL
+    PREC, INV, UNROLL = prec, inv, int(unroll)
+    print(f"[gdn_fast] chunked gated delta rule -> gfx950 kernels (precision={prec} and inverse={inv} recorded; "
+          "f32 arithmetic, exact inverse)", flush=True)

@@ -121,3 +121,130 @@ def gdn_chunked(q, k, v, g, beta, chunk=64, h0=None, rounding=None, return_uw=Fa
         h = h * np.exp(gg[..., -1])[..., None, None] + ki.swapaxes(-1, -2) @ v_new
     o = o.transpose(0, 1, 3, 2, 4).reshape(B, N * chunk, H, Dv)[:, :T]
     return (o, h, u, w) if return_uw else (o, h)
+
+
+def gdn_chunked_bwd(q, k, v, g, beta, do, chunk=64, h0=None, dh_final=None, rounding=None):
+    """Gradients of `gdn_chunked` for the upstream gradients do [B, T, H, Dv] of o and dh_final [B, H, Dk, Dv] of the
+    final state (None: 0): reverse-mode through the chunked algorithm of gdn_fast.py:63-111, which is what XLA's
+    autodiff of the reference computes when the layer trains through it (installed for training at
+    lightning/train_stage1.py:67-69).  The bf16 rounding points of `rounding="bf16"` round the forward values only;
+    their derivative is taken as 1, as autodiff takes it for a dtype cast.
+
+    Returns (dq, dk, dv, dg, dbeta, dh0) shaped like (q, k, v, g, beta, the initial state)."""
+    def rd(a):
+        if rounding == "bf16":
+            return round_bf16(np.asarray(a, np.float32)).astype(np.float64)
+        return np.asarray(a, np.float64)
+
+    B, T, H, Dk = np.shape(k)
+    Dv = np.shape(v)[-1]
+    scale = 1.0 / np.sqrt(Dk)
+    if rounding == "bf16":
+        scale = float(round_bf16(np.float32(scale)).reshape(-1)[0])
+    g = np.asarray(g, np.float64)
+    q = rd(rd(q) * scale)
+    k, v, beta = rd(k), rd(v), rd(beta)
+    do = np.asarray(do, np.float64)
+    C = chunk
+    pad = (C - T % C) % C
+    if pad:
+        padf = lambda a: np.concatenate([a, np.zeros((B, pad) + a.shape[2:])], axis=1)  # noqa: E731
+        q, k, v, g, beta, do = map(padf, (q, k, v, g, beta, do))
+    N = q.shape[1] // C
+
+    def to_chunk(a):
+        return a.reshape(B, N, C, H, -1).transpose(0, 1, 3, 2, 4)
+
+    qc, kc, vc, doc = to_chunk(q), to_chunk(k), to_chunk(v), to_chunk(do)
+    gc = g.reshape(B, N, C, H).transpose(0, 1, 3, 2)
+    bc = beta.reshape(B, N, C, H).transpose(0, 1, 3, 2)
+    gg = np.cumsum(gc, axis=-1)
+    strict = np.tril(np.ones((C, C), bool), k=-1)
+    incl = np.tril(np.ones((C, C), bool))
+    kb = rd(kc * bc[..., None])
+    Gs = np.where(strict, np.exp(np.where(strict, gg[..., :, None] - gg[..., None, :], 0.0)), 0.0)
+    S = (kb @ kc.swapaxes(-1, -2)) * Gs
+    A = unit_lower_inverse(S)
+    vb = rd(vc * bc[..., None])
+    u = rd(A @ vb)
+    kbg = kb * np.exp(gg)[..., None]
+    w = rd(A @ kbg)
+    Gi = np.where(incl, np.exp(np.where(incl, gg[..., :, None] - gg[..., None, :], 0.0)), 0.0)
+    P = (qc @ kc.swapaxes(-1, -2)) * Gi
+    # forward scan, keeping the state entering each chunk
+    hs = np.zeros((B, N, H, Dk, Dv))
+    h = np.zeros((B, H, Dk, Dv)) if h0 is None else np.array(h0, np.float64)
+    for n in range(N):
+        hs[:, n] = h
+        gl = gg[:, n][..., -1]
+        vn = u[:, n] - w[:, n] @ h
+        kd = kc[:, n] * np.exp(gl[..., None] - gg[:, n])[..., None]
+        h = h * np.exp(gl)[..., None, None] + kd.swapaxes(-1, -2) @ vn
+    # reverse scan
+    dq, dk, dv = np.zeros_like(qc), np.zeros_like(kc), np.zeros_like(vc)
+    dgg, dbc = np.zeros_like(gg), np.zeros_like(bc)
+    dh = np.zeros((B, H, Dk, Dv)) if dh_final is None else np.array(dh_final, np.float64)
+    for n in reversed(range(N)):
+        h, ggn, qn, kn = hs[:, n], gg[:, n], qc[:, n], kc[:, n]
+        gl = ggn[..., -1]
+        eg = np.exp(ggn)
+        vn = u[:, n] - w[:, n] @ h
+        kd = kn * np.exp(gl[..., None] - ggn)[..., None]
+        qg = qn * eg[..., None]
+        don = doc[:, n]
+        # o = qg h + P v_new
+        d_qg = don @ h.swapaxes(-1, -2)
+        dh_prev = qg.swapaxes(-1, -2) @ don
+        dP = (don @ vn.swapaxes(-1, -2)) * incl
+        dvn = P[:, n].swapaxes(-1, -2) @ don
+        # h_next = e^gl h + kd^T v_new
+        dvn = dvn + kd @ dh
+        d_kd = vn @ dh.swapaxes(-1, -2)
+        dgl = np.exp(gl) * (dh * h).sum(axis=(-1, -2))
+        dh_prev = dh_prev + np.exp(gl)[..., None, None] * dh
+        # v_new = u - w h
+        du, dw = dvn, -dvn @ h.swapaxes(-1, -2)
+        dh_prev = dh_prev - w[:, n].swapaxes(-1, -2) @ dvn
+        dggn = np.zeros_like(ggn)
+        # P = (q k^T) * Gi
+        dPr = dP * Gi[:, n]
+        dq[:, n] += dPr @ kn
+        dk[:, n] += dPr.swapaxes(-1, -2) @ qn
+        t = dP * P[:, n]
+        dggn += t.sum(axis=-1) - t.sum(axis=-2)
+        # qg = q e^gg
+        dq[:, n] += d_qg * eg[..., None]
+        dggn += (d_qg * qg).sum(axis=-1)
+        # kd = k e^(gl - gg)
+        dk[:, n] += d_kd * np.exp(gl[..., None] - ggn)[..., None]
+        s = (d_kd * kd).sum(axis=-1)
+        dgl = dgl + s.sum(axis=-1)
+        dggn -= s
+        dggn[..., -1] += dgl
+        # chunk-local: u = A vb, w = A kbg
+        An = A[:, n]
+        dA = du @ vb[:, n].swapaxes(-1, -2) + dw @ kbg[:, n].swapaxes(-1, -2)
+        dvb = An.swapaxes(-1, -2) @ du
+        dkbg = An.swapaxes(-1, -2) @ dw
+        dkb = dkbg * eg[..., None]
+        dggn += (dkbg * kbg[:, n]).sum(axis=-1)
+        dS = -(An.swapaxes(-1, -2) @ dA @ An.swapaxes(-1, -2)) * strict
+        dS0 = dS * Gs[:, n]
+        t2 = dS * S[:, n]
+        dggn += t2.sum(axis=-1) - t2.sum(axis=-2)
+        dkb = dkb + dS0 @ kn
+        dk[:, n] += dS0.swapaxes(-1, -2) @ kb[:, n]
+        dv[:, n] += dvb * bc[:, n][..., None]
+        dbc[:, n] += (dvb * vc[:, n]).sum(axis=-1) + (dkb * kn).sum(axis=-1)
+        dk[:, n] += dkb * bc[:, n][..., None]
+        dgg[:, n] = dggn
+        dh = dh_prev
+    dgc = np.flip(np.cumsum(np.flip(dgg, axis=-1), axis=-1), axis=-1)  # gg = cumsum(g) within the chunk
+
+    def from_chunk(a):
+        return a.transpose(0, 1, 3, 2, 4).reshape(B, N * C, H, -1)[:, :T]
+
+    def from_chunk_s(a):
+        return a.transpose(0, 1, 3, 2).reshape(B, N * C, H)[:, :T]
+
+    return (from_chunk(dq) * scale, from_chunk(dk), from_chunk(dv), from_chunk_s(dgc), from_chunk_s(dbc), dh)

@@ -99,3 +99,91 @@ def test_reference_config_shape(correlated, dev):
     eu, ew = check_uw(u, w, wu, ww, UW_TOL)
     print(dict(o=eo, h=eh, u=eu, w=ew))
     assert eo < OH_TOL and eh < OH_TOL, (eo, eh)
+
+
+def gpu_gdn_bwd(q, k, v, g, beta, do, dev, h0=None, dh_final=None):
+    B, T, H, _ = q.shape
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev).to(torch.bfloat16)  # noqa: E731
+    f32 = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)  # noqa: E731
+    qt, kt, vt, bt, dot = bf(q), bf(k), bf(v), bf(beta), bf(do)
+    gt, h0t, dht = f32(g), f32(h0), f32(dh_final)
+    dq, dk, dv = torch.empty_like(qt), torch.empty_like(kt), torch.empty_like(vt)
+    dg = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    db = torch.empty_like(dg)
+    dh0 = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    lib = L.lib()
+    ws = L.workspace(lib.lsurge_gdn_chunked_bwd_workspace_bytes(B, T, H, D, D), dev)
+    L.check(lib.lsurge_gdn_chunked_bwd(L.ptr(qt), L.ptr(kt), L.ptr(vt), L.ptr(gt), L.ptr(bt), B, T, H, D, D,
+                                       L.ptr(h0t), L.ptr(dot), L.ptr(dht), L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg),
+                                       L.ptr(db), L.ptr(dh0), L.ptr(ws), ws.numel(), L.stream(dev)), "gdn_chunked_bwd")
+    torch.cuda.synchronize()
+    return [a.float().cpu().numpy() for a in (dq, dk, dv, dg, db, dh0)]
+
+
+NAMES = ("dq", "dk", "dv", "dg", "dbeta", "dh0")
+
+
+def check_bwd(q, k, v, g, beta, dev, seed, h0=None, with_dhf=False, tol=2e-2):
+    rng = np.random.default_rng(seed)
+    B, T, H, _ = q.shape
+    do = mo.round_bf16(rng.standard_normal((B, T, H, D)).astype(np.float32))
+    dhf = (rng.standard_normal((B, H, D, D)) * 0.1).astype(np.float32) if with_dhf else None
+    got = gpu_gdn_bwd(q, k, v, g, beta, do, dev, h0=h0, dh_final=dhf)
+    want = go.gdn_chunked_bwd(q, k, v, g, beta, do, chunk=64, h0=h0, dh_final=dhf, rounding="bf16")
+    errs = {n: mo.rel_l2(a, b) for n, a, b in zip(NAMES, got, want)}
+    print(errs)
+    assert all(e < tol for e in errs.values()), errs
+    return errs
+
+
+@pytest.mark.parametrize("correlated", [False, True])
+@pytest.mark.parametrize("B,T,H", [(1, 1, 1), (1, 63, 2), (2, 64, 1), (2, 100, 3), (1, 333, 2)])
+def test_backward_against_oracle(B, T, H, correlated, dev):
+    """dq, dk, dv, dg, dbeta and dh0 of lsurge_gdn_chunked_bwd against the oracle's reverse-mode gradients (pinned by
+    finite differences of the token recurrence), within the north star's 2e-2."""
+    q, k, v, g, beta = _inputs(B, T, H, seed=3 * T + H, correlated=correlated)
+    check_bwd(q, k, v, g, beta, dev, seed=T)
+
+
+def test_backward_initial_and_final_state(dev):
+    q, k, v, g, beta = _inputs(2, 150, 2, seed=17)
+    h0 = np.random.default_rng(18).standard_normal((2, 2, D, D)).astype(np.float32) * 0.1
+    check_bwd(q, k, v, g, beta, dev, seed=19, h0=h0, with_dhf=True)
+
+
+@pytest.mark.parametrize("correlated", [False, True])
+def test_backward_reference_config_shape(correlated, dev):
+    q, k, v, g, beta = _inputs(1, 4096, 8, seed=2, correlated=correlated)
+    check_bwd(q, k, v, g, beta, dev, seed=5)
+
+
+def test_autograd_surface(dev):
+    """gdn_fast.fast_chunk_gated_delta_rule (the reference's signature) forward and backward through torch autograd,
+    with an initial state whose final state feeds the loss too."""
+    import gdn_fast
+    B, T, H = 2, 130, 2
+    q, k, v, g, beta = _inputs(B, T, H, seed=31)
+    h0 = (np.random.default_rng(32).standard_normal((B, H, D, D)) * 0.1).astype(np.float32)
+    rng = np.random.default_rng(33)
+    do = mo.round_bf16(rng.standard_normal((B, T, H, D)).astype(np.float32))
+    dhf = (rng.standard_normal((B, H, D, D)) * 0.1).astype(np.float32)
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev).to(torch.bfloat16)  # noqa: E731
+    ts = [bf(q).requires_grad_(True), bf(k).requires_grad_(True), bf(v).requires_grad_(True),
+          torch.from_numpy(g).to(dev).requires_grad_(True), bf(beta).requires_grad_(True),
+          torch.from_numpy(h0).to(dev).requires_grad_(True)]
+    o, hT = gdn_fast.fast_chunk_gated_delta_rule(*ts[:5], initial_state=ts[5])
+    assert o.dtype == torch.bfloat16 and hT.dtype == torch.bfloat16
+    (o.float() * torch.from_numpy(do).to(dev)).sum().backward(retain_graph=True)
+    # the final state's gradient enters through the second output
+    ts2 = [t.detach().clone().requires_grad_(True) for t in ts]
+    o2, hT2 = gdn_fast.fast_chunk_gated_delta_rule(*ts2[:5], initial_state=ts2[5])
+    ((o2.float() * torch.from_numpy(do).to(dev)).sum() + (hT2.float() * torch.from_numpy(dhf).to(dev)).sum()).backward()
+    wo, wh = go.gdn_chunked(q, k, v, g, beta, chunk=64, h0=h0, rounding="bf16")
+    assert mo.rel_l2(o.detach().float().cpu().numpy(), wo) < OH_TOL
+    for tset, dh in ((ts, None), (ts2, dhf)):
+        want = go.gdn_chunked_bwd(q, k, v, g, beta, do, chunk=64, h0=h0, dh_final=dh, rounding="bf16")
+        for t, w, n in zip(tset, want, NAMES):
+            err = mo.rel_l2(t.grad.float().cpu().numpy(), w)
+            assert err < 2e-2, (n, err)
+    with pytest.raises(NotImplementedError):
+        gdn_fast.fast_chunk_gated_delta_rule(*ts[:5], use_qk_norm_in_gdn=True)

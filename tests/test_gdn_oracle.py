@@ -108,3 +108,59 @@ def test_correlated_keys_separate_inverse_mistakes(monkeypatch):
             bad, _ = go.gdn_chunked(q, k, v, g, beta, chunk=64)
         errs[correlated] = rel(bad, o_ref)
     assert errs[True] > 0.1 and errs[True] > 5 * errs[False], errs
+
+
+@pytest.mark.parametrize("chunk,T,with_state", [(8, 20, False), (4, 13, True), (16, 16, True)])
+def test_backward_finite_differences(chunk, T, with_state):
+    """The chunked backward equals central finite differences of the token recurrence (float64) for
+    L = <do, o> + <dh_final, h_T>, on every input: q, k, v, g, beta and the initial state."""
+    B, H, Dk, Dv = 1, 2, 5, 6
+    q, k, v, g, beta = _inputs(B=B, T=T, H=H, Dk=Dk, Dv=Dv, seed=chunk + T)
+    rng = np.random.default_rng(99)
+    do = rng.standard_normal((B, T, H, Dv))
+    h0 = rng.standard_normal((B, H, Dk, Dv)) * 0.3 if with_state else None
+    dhf = rng.standard_normal((B, H, Dk, Dv)) if with_state else None
+    grads = go.gdn_chunked_bwd(q, k, v, g, beta, do, chunk=chunk, h0=h0, dh_final=dhf)
+
+    def loss(q_, k_, v_, g_, b_, h0_):
+        o, hT = go.gated_delta_recurrence(q_, k_, v_, g_, b_, h0=h0_)
+        return float((o * do).sum() + ((hT * dhf).sum() if dhf is not None else 0.0))
+
+    args = [q, k, v, g, beta, h0 if h0 is not None else np.zeros((B, H, Dk, Dv))]
+    eps = 1e-6
+    for ai, name in enumerate(("dq", "dk", "dv", "dg", "dbeta", "dh0")):
+        if name == "dh0" and not with_state:
+            continue
+        flat_idx = rng.choice(args[ai].size, size=min(6, args[ai].size), replace=False)
+        for fi in flat_idx:
+            idx = np.unravel_index(fi, args[ai].shape)
+            plus = [a.copy() for a in args]
+            minus = [a.copy() for a in args]
+            plus[ai][idx] += eps
+            minus[ai][idx] -= eps
+            num = (loss(*plus) - loss(*minus)) / (2 * eps)
+            got = grads[ai][idx]
+            assert abs(num - got) <= 1e-6 * max(1.0, abs(num)), (name, idx, num, got)
+
+
+def test_backward_planted_mistake_fails(monkeypatch):
+    """Dropping the decay's term in the state update's key gradient (a plausible slip) breaks the finite-difference
+    agreement the test above checks."""
+    q, k, v, g, beta = _inputs(B=1, T=12, H=1, Dk=4, Dv=3, seed=5)
+    do = np.random.default_rng(6).standard_normal((1, 12, 1, 3))
+    dq, dk, dv, dg, db, _ = go.gdn_chunked_bwd(q, k, v, g, beta, do, chunk=4)
+    eps = 1e-6
+    kp, km = k.copy(), k.copy()
+    kp[0, 2, 0, 1] += eps
+    km[0, 2, 0, 1] -= eps
+    L = lambda kk: float((go.gated_delta_recurrence(q, kk, v, g, beta)[0] * do).sum())  # noqa: E731
+    num = (L(kp) - L(km)) / (2 * eps)
+    assert abs(num - dk[0, 2, 0, 1]) < 1e-6
+    real_exp = np.exp
+
+    def no_decay_exp(x):  # e^0 = 1 for every decay factor: the gradient of a different function
+        return real_exp(np.zeros_like(x))
+    monkeypatch.setattr(go.np, "exp", no_decay_exp)
+    _, dk_bad, _, _, _, _ = go.gdn_chunked_bwd(q, k, v, g, beta, do, chunk=4)
+    monkeypatch.undo()
+    assert abs(num - dk_bad[0, 2, 0, 1]) > 1e-3
