@@ -13,9 +13,10 @@ layer's independent chains on helper streams (--concurrency 1, the default; lsur
 cpu_baseline: the numpy CPU oracle's float32 layer forward + backward at the config's full token count, timed on this
 host; at C2 also `cpu_baseline_c1_fwd`, the C1 forward (BASELINE.md's pair).
 
---fp8: the layer forward with every expert GEMM on E4M3 operands (lsurge_moe_fwd_fp8, current scaling); a step is
-the weights' quantisation (once per optimizer step in training) plus the forward; `ms_per_step_cached_weights`
-times the forward alone (weights quantised once, as in serving).  GEMM rooflines are priced against the fp8 peak.
+--fp8: every expert GEMM on FP8 operands with current scaling (E4M3 activations and weights, E5M2 gradients:
+lsurge_moe_fwd_fp8 + lsurge_moe_bwd_fp8); a step is the weights' quantisation (once per optimizer step in training)
+plus the forward and backward (--fwd-only: the forward alone); `ms_per_step_cached_weights` times the same without
+the weights' quantisation (as in serving, for --fwd-only).  GEMM rooflines are priced against the fp8 peak.
 """
 from __future__ import annotations
 
@@ -48,12 +49,14 @@ def fused_router(c):
     return c["E"] in (32, 64, 128) and c["k"] <= 8 and c["d"] % 64 == 0
 
 
-def kernel_work(c):
+def kernel_work(c, fp8=False):
     """Algorithmic work per launch of each kernel: ('mfma', flops) over useful rows, or ('hbm', bytes)."""
     T, d, E, k, f, fs = c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"]
     M = T * k
-    # the backward's grouped GEMMs carry the shared expert as one more expert (T rows) when fs == f
-    Mb = M + T if fs and fs == f else M
+    # the bf16 backward's grouped GEMMs carry the shared expert as one more expert (T rows) when fs == f; the FP8
+    # backward runs it as dense GEMMs of its own
+    merged = bool(fs) and fs == f and not fp8
+    Mb = M + T if merged else M
     w = {
         "gemm_gu_fwd": ("mfma", 2 * M * d * 2 * f),
         "gemm_down_fwd": ("mfma", 2 * M * f * d),
@@ -77,7 +80,7 @@ def kernel_work(c):
             "shared_gu_fwd": ("mfma", 2 * T * d * 2 * fs),
             "shared_down_fwd": ("mfma", 2 * T * fs * d),
         })
-    if fs and fs != f:
+    if fs and not merged:
         w.update({
             "shared_down_dgrad": ("mfma", 2 * T * d * fs),
             "shared_down_wgrad": ("mfma", 2 * T * fs * d),
@@ -112,10 +115,12 @@ def make_params(c, dev, seed=0):
     return p, dy
 
 
-def measured_traffic(config, kernel, fp8=False):
+def measured_traffic(config, kernel, fp8=False, bwd=True):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (lines
-    `bench-traffic <kernel> <bytes>` in profiles/moe_layer_<config>_fwd_bwd.md, or _fp8_fwd.md for --fp8), or None."""
-    path = os.path.join(ROOT, "profiles", f"moe_layer_{config.lower()}_{'fp8_fwd' if fp8 else 'fwd_bwd'}.md")
+    `bench-traffic <kernel> <bytes>` in profiles/moe_layer_<config>_fwd_bwd.md, or _fp8_fwd_bwd.md / _fp8_fwd.md for
+    --fp8), or None."""
+    name = ("fp8_fwd_bwd" if bwd else "fp8_fwd") if fp8 else "fwd_bwd"
+    path = os.path.join(ROOT, "profiles", f"moe_layer_{config.lower()}_{name}.md")
     try:
         with open(path) as fh:
             for line in fh:
@@ -675,8 +680,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--fp8", action="store_true", help="forward only, expert GEMMs in FP8 (E4M3, current scaling)")
-    ap.add_argument("--fwd-only", action="store_true", help="time the forward alone (bf16)")
+    ap.add_argument("--fp8", action="store_true", help="expert GEMMs in FP8 (current scaling: E4M3 forward, E5M2 "
+                    "gradients)")
+    ap.add_argument("--fwd-only", action="store_true", help="time the forward alone")
     ap.add_argument("--op", choices=["moe", "conv", "gdn", "permute", "ragged_dot"], default="moe",
                     help="conv: the Gated DeltaNet block's causal depthwise Conv1D (modal/fast_conv.py) at the "
                          "reference config's shape, forward + backward GB/s; gdn: its chunked gated delta rule "
@@ -744,7 +750,7 @@ def main():
     from moe_layer import MoELayer, MoEShape
 
     c = CONFIGS[a.config]
-    if a.fp8 or a.fwd_only:
+    if a.fwd_only:
         c = dict(c, bwd=False)
     dev = torch.device("cuda", 0)
     lib = _lib.lib()
@@ -757,6 +763,8 @@ def main():
         if a.fp8:
             layer.quantize_weights_fp8(p)
             layer.forward_fp8(p)
+            if c["bwd"]:
+                layer.backward_fp8(p, dy, grads)
             return
         layer.forward(p)
         if c["bwd"]:
@@ -777,7 +785,7 @@ def main():
     lib.lsurge_prof_collect()
     lib.lsurge_prof_enable(0)
     table = prof_table(lib, nprof)
-    work = kernel_work(c)
+    work = kernel_work(c, a.fp8)
     dom = max((n for n in table if n in work), key=lambda n: table[n][2])
     names = [lib.lsurge_prof_kernel_name(i).decode() for i in range(lib.lsurge_prof_kernel_count())]
 
@@ -809,11 +817,13 @@ def main():
     ms = el / a.steps * 1e3
     tokens_s = c["T"] * a.steps / el
     cached_ms = None
-    if a.fp8:  # the forward alone, on weights quantised once
+    if a.fp8:  # the same step on weights quantised once
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(a.steps):
             layer.forward_fp8(p)
+            if c["bwd"]:
+                layer.backward_fp8(p, dy, grads)
         torch.cuda.synchronize()
         cached_ms = (time.perf_counter() - t0) / a.steps * 1e3
     serial_ms = sum(v[2] for v in table.values())
@@ -829,7 +839,7 @@ def main():
             print(f"  {n:20s} {v}", file=sys.stderr)
 
     res = {
-        "metric": ("MoE-layer fwd tokens/sec @1 GPU, FP8 expert GEMMs" if a.fp8 else
+        "metric": (f"MoE-layer {'fwd+bwd' if c['bwd'] else 'fwd'} tokens/sec @1 GPU, FP8 expert GEMMs" if a.fp8 else
                    "MoE-layer fwd+bwd tokens/sec @1 GPU; GEMM MFMA util %, permute HBM GB/s"),
         "value": round(tokens_s, 1),
         "unit": "tokens/s",
@@ -840,7 +850,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8-e4m3 expert GEMMs (bf16 router, combine, activations)" if a.fp8 else "bf16",
+        "dtype": ("fp8 expert GEMMs: e4m3 activations and weights, e5m2 gradients (bf16 router, combine, saved "
+                  "activations)" if a.fp8 else "bf16"),
         "data": "synthetic (torch seeded normals: x~N(0,1), weights~N(0,0.02), dy~N(0,1), bf16), resident in HBM",
         "config": {"workload": f"{a.config}: MoE layer {'fwd+bwd' if c['bwd'] else 'fwd'}{' fp8' if a.fp8 else ''} T={c['T']} d={c['d']} "
                                f"E={c['E']}x{c['f']} top-{c['k']} shared={c['fs']}" + (" zipf-bias" if c["zipf"] else ""),
@@ -850,7 +861,7 @@ def main():
         "layer_tflops": round(layer_flops(c) / (ms * 1e-3) / 1e12, 1),
         "mfu": round(layer_flops(c) / (ms * 1e-3) / 1e12 / peak_mfma, 4),
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(a.config, dom, a.fp8),
+                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(a.config, dom, a.fp8, c["bwd"]),
                      "launch_ms": round(dom_ms, 4)},
         "kernels": kern,
         **({"ms_per_step_cached_weights": round(cached_ms, 4),

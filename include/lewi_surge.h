@@ -38,7 +38,7 @@ enum {
   LSURGE_ERR_WORKSPACE = -4    /* workspace too small */
 };
 
-#define LSURGE_ABI_VERSION 2
+#define LSURGE_ABI_VERSION 3
 #define LSURGE_BLOCK_ROWS 128 /* rows per padded expert block */
 
 int lsurge_abi_version(void);
@@ -229,14 +229,17 @@ typedef struct {
 int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_saved_views* v);
 
 /* ------------------------------------------------------------------------------------------------
- * FP8 variant of the forward GEMMs (OCP E4M3 operands, f32 accumulation, v_mfma_f32_32x32x64_f8f6f4).
+ * FP8 variant of the expert GEMMs (OCP FP8 operands, f32 accumulation, v_mfma_f32_32x32x64_f8f6f4).
  * Current scaling: every tensor, or every group of one (an expert's weight matrix), is quantised with its
- * own scale = 448 / amax taken just before the cast (1 when amax = 0); values are rounded to nearest even
- * and saturated at +-448; scale_inv = 1 / scale multiplies the GEMM's accumulator back.  This is the
- * recipe of Transformer Engine's FP8 current scaling that the reference tries through MaxText's
- * `quantization=te_fp8_currentscaling` (modal/te_run.py:99; TE and MaxText are third-party, and the
- * reference's own MoE path has no FP8 entry point, so these functions replace none of its interfaces).
+ * own scale = fmax / amax taken just before the cast (1 when amax = 0); values are rounded to nearest even
+ * and saturated at +-fmax; scale_inv = 1 / scale multiplies the GEMM's accumulator back.  Activations and
+ * weights are E4M3 (fmax 448), gradients E5M2 (fmax 57344): the hybrid recipe of Transformer Engine's FP8
+ * current scaling that the reference trains with through MaxText's `quantization=te_fp8_currentscaling`
+ * (modal/te_run.py:95-99; TE and MaxText are third-party, and the reference's own MoE path has no FP8 entry
+ * point, so these functions replace none of its interfaces).
  * ------------------------------------------------------------------------------------------------ */
+#define LSURGE_FP8_E4M3 0
+#define LSURGE_FP8_E5M2 1
 
 /* x: `groups` consecutive [rows, cols] bf16 matrices -> q: the same shape in E4M3 bytes, or [cols, rows]
  * per group with transpose = 1 (rows, cols multiples of 16; untransposed: rows * cols a multiple of 16);
@@ -244,6 +247,16 @@ int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_s
 size_t lsurge_fp8_quantize_workspace_bytes(int64_t groups, int64_t rows, int64_t cols);
 int lsurge_fp8_quantize(const void* x, int64_t groups, int64_t rows, int64_t cols, int transpose, void* q,
                         float* scale_inv, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
+/* One [rows, cols] bf16 tensor (cols % 16 == 0) -> format (LSURGE_FP8_E4M3 / _E5M2) with one scale, written
+ * row-wise to q [rows, cols] and / or transposed to qt [cols, ldqt] (ldqt >= rows rounded up to 64, a multiple
+ * of 16; columns past rows hold zeros up to the next multiple of 16) -- the cast + transpose a training step
+ * makes of an activation or gradient whose two GEMMs need it K-contiguous in both directions.  Either q or qt
+ * may be null; all pointers 16-byte aligned; scale_inv [1] f32. */
+size_t lsurge_fp8_cast_workspace_bytes(void);
+int lsurge_fp8_cast_transpose(const void* x, int64_t rows, int64_t cols, int format, void* q, void* qt,
+                              int64_t ldqt, float* scale_inv, void* workspace, size_t workspace_bytes,
+                              lsurge_stream_t stream);
 
 /* lsurge_ragged_dot on FP8 operands: out[r] = (lhs_q[r] . rhs_q[e(r)]^T) * lhs_scale_inv[0] *
  * rhs_scale_inv[e(r)] for r < sum(group_sizes), 0 after.  lhs_q: [m, kdim] E4M3; rhs_q: [e, n, kdim] E4M3
@@ -255,10 +268,12 @@ int lsurge_ragged_dot_fp8(const void* lhs_q, const float* lhs_scale_inv, const v
                           int64_t n, int64_t e, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
                           lsurge_stream_t stream);
 
-/* The layer's weights in E4M3, one buffer: gate, up [e, f, d], down [e, d, f] (K contiguous), shared gate,
- * up [fs, d], down [d, fs], then the f32 scale_inv of gate, up, down per expert and of the three shared
- * matrices.  Filled by lsurge_moe_fp8_quantize_weights from the bf16 weights of p (one scale per expert and
- * matrix); a caller whose weights do not change (serving) fills it once. */
+/* The layer's weights in E4M3, one buffer: gate, up [e, f, d], down [e, d, f] (K contiguous for the
+ * forward), shared gate, up [fs, d], down [d, fs], the same codes again in the weights' own layout (K
+ * contiguous for the backward's dgrads), then the f32 scale_inv of gate, up, down per expert and of the
+ * three shared matrices.  Filled by lsurge_moe_fp8_quantize_weights from the bf16 weights of p (one scale
+ * per expert and matrix); a caller whose weights do not change (serving) fills it once, a training step
+ * after every weight update. */
 size_t lsurge_moe_fp8_weights_bytes(const lsurge_moe_shape* s);
 size_t lsurge_moe_fp8_quantize_weights_workspace_bytes(const lsurge_moe_shape* s);
 int lsurge_moe_fp8_quantize_weights(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* wq,
@@ -271,6 +286,17 @@ size_t lsurge_moe_fwd_fp8_workspace_bytes(const lsurge_moe_shape* s);
 int lsurge_moe_fwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* wq, size_t wq_bytes,
                        void* out, void* saved, size_t saved_bytes, void* workspace, size_t workspace_bytes,
                        lsurge_stream_t stream);
+/* lsurge_moe_bwd with every expert GEMM in FP8, after lsurge_moe_fwd_fp8 on the same `saved` and weight
+ * buffer (it reads the scales the forward saved).  Gradients are cast to E5M2 per tensor: the routed dY rows
+ * and [dG | dU] over all routed rows, the shared expert's dY and [dG | dU] on their own.  dgrads: E5M2 x the
+ * weights' E4M3 codes (each weight at its own scale); wgrads: the forward's E4M3 codes of h and x (same
+ * scales) x the E5M2 gradients.  Combine, dispatch and router backward are those of lsurge_moe_bwd; the
+ * gradients come out in the same buffers and dtypes.  p needs x and w_r (the bf16 expert weights are not
+ * read). */
+size_t lsurge_moe_bwd_fp8_workspace_bytes(const lsurge_moe_shape* s);
+int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* wq, size_t wq_bytes,
+                       const void* dy, const void* saved, const lsurge_moe_grads* g, void* workspace,
+                       size_t workspace_bytes, lsurge_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------
  * Causal depthwise Conv1D of the Gated DeltaNet block (memory-bound).

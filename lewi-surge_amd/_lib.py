@@ -84,6 +84,11 @@ _SIGS = {
     "lsurge_moe_fwd_fp8_workspace_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
     "lsurge_moe_fwd_fp8": (_int, [ctypes.POINTER(MoeShape), ctypes.POINTER(MoeParams), _p, _sz, _p, _p, _sz, _p, _sz,
                                   _p]),
+    "lsurge_moe_bwd_fp8_workspace_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
+    "lsurge_moe_bwd_fp8": (_int, [ctypes.POINTER(MoeShape), ctypes.POINTER(MoeParams), _p, _sz, _p, _p,
+                                  ctypes.POINTER(MoeGrads), _p, _sz, _p]),
+    "lsurge_fp8_cast_workspace_bytes": (_sz, []),
+    "lsurge_fp8_cast_transpose": (_int, [_p, _i64, _i64, _int, _p, _p, _i64, _p, _p, _sz, _p]),
     "lsurge_causal_conv1d": (_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _p]),
     "lsurge_causal_conv1d_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "lsurge_causal_conv1d_bwd": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _sz, _p]),

@@ -657,7 +657,7 @@ __global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
   // T1 k, T2 q * scale, T3 k beta, T4 v beta, T5 du, T6 dw (bf16 tiles); M1 / M2 scratch [GC][GC], M3 A
   __shared__ __attribute__((aligned(16))) bf16_t T1[GC][GP], T2[GC][GP], T3[GC][GP], T4[GC][GP], T5[GC][GP], T6[GC][GP];
   __shared__ float M1[GC][GC + 1], M2[GC][GC + 1], M3[GC][GC + 1];
-  __shared__ float gc[GC], eg[GC], bt[GC], dgg[GC], rs[GC], cs[GC];
+  __shared__ float gc[GC], eg[GC], bt[GC], dgg[GC], rs[GC];
   const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z, N = gridDim.x;
   const int tid = threadIdx.x, t0 = n * GC;
   const int64_t row0 = (int64_t)b * T;

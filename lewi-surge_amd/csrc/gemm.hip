@@ -270,7 +270,7 @@ static int max_blocks_of(const GemmBlocks& g) {
 
 // launch gemm_rows_kernel with the tile config that matches the row tiles of g (column tiles: BN output columns, or
 // BN / 2 for the SwiGLU forward)
-template <int BMODE, int EPI, bool F8 = false>
+template <int BMODE, int EPI, int F8 = 0>
 static int launch_rows(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t s, int et = LSURGE_BF16) {
   LSURGE_REQUIRE(g.tile_rows == 128 || g.tile_rows == 256, "grouped GEMM: tile_rows=%d must be 128 or 256", g.tile_rows);
   a.max_tiles = max_blocks_of(g);
@@ -363,21 +363,34 @@ int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
   return swiglu_bwd ? launch_rows<B_NK, EPI_SWIGLU_BWD>(kid, g, a, s, et) : launch_rows<B_NK, EPI_STORE>(kid, g, a, s, et);
 }
 
-// FP8 row GEMM: C[rows, N] = (A[rows, K] @ B_e^T) * a_sinv[0] * b_sinv[e], A and B_e = [N, K] in E4M3 (K
-// contiguous, pitches lda / ldb and expert stride in bytes).  With swiglu, B2 holds the up rows (scaled by
-// b2_sinv[e]), C = h = silu(g) * u, Gs / Us (optional) receive g and u, and amax (optional) the max |h| as
-// bf16-rounded float bits (atomic max: the caller zeroes it first).  Otherwise C (bf16) or Cf (f32) is the product.
+// FP8 row GEMM: C[rows, N] = (A[rows, K] @ B_e^T) * a_sinv[0] * b_sinv[e], B_e = [N, K] in E4M3 and A in E4M3 (or
+// E5M2 with a_e5m2: a gradient), both K contiguous, pitches lda / ldb and expert stride in bytes.
+//   F8_SWIGLU_FWD: B2 holds the up rows (scaled by b2_sinv[e]), C = h = silu(g) * u, Gs / Us (optional) receive g and
+//                  u, and amax (optional) the max |h| as bf16-rounded float bits (atomic max: the caller zeroes it).
+//   F8_SWIGLU_BWD: the product is dH; C = [dG | dU] (pitch ldc >= 2N) from the saved Gs, Us (pitch N), and amax
+//                  (optional) receives max(|dG|, |dU|) as for the forward.
+//   F8_STORE:      C (bf16) or Cf (f32) is the product; with k_split, K columns [k_split, K) read B2 (at k - k_split)
+//                  with its own per-expert scale b2_sinv (the gate/up dgrad over [dG | dU]).
 int gemm_rows_f8(int kid, const GemmBlocks& g, const void* A, int64_t lda, const float* a_sinv, const void* B,
                  const void* B2, int64_t ldb, int64_t b_estride, const float* b_sinv, const float* b2_sinv, int64_t K,
-                 int64_t N, void* C, int64_t ldc, bool out_f32, bool swiglu, void* Gs, void* Us, uint32_t* amax,
-                 hipStream_t s, const RowGather& gather) {
-  LSURGE_REQUIRE(K > 0 && N > 0 && K % 16 == 0 && N % 8 == 0 && lda % 16 == 0 && ldb % 16 == 0 && lda >= K && ldb >= K,
+                 int64_t N, void* C, int64_t ldc, bool out_f32, int epi, void* Gs, void* Us, uint32_t* amax,
+                 hipStream_t s, const RowGather& gather, int64_t k_split, bool a_e5m2) {
+  const bool swiglu = epi == F8_SWIGLU_FWD, sbwd = epi == F8_SWIGLU_BWD;
+  LSURGE_REQUIRE(epi == F8_STORE || swiglu || sbwd, "gemm_rows_f8: bad epilogue %d", epi);
+  const int64_t kb = k_split ? k_split : K;  // K extent of one B matrix
+  LSURGE_REQUIRE(K > 0 && N > 0 && K % 16 == 0 && N % 8 == 0 && lda % 16 == 0 && ldb % 16 == 0 && lda >= K && ldb >= kb,
                  "gemm_rows_f8: K=%lld (multiple of 16), N=%lld (multiple of 8), lda=%lld, ldb=%lld (multiples of 16, >= K)",
                  (long long)K, (long long)N, (long long)lda, (long long)ldb);
-  LSURGE_REQUIRE(A && B && C && a_sinv && b_sinv && (!swiglu || (B2 && b2_sinv)), "gemm_rows_f8: null pointer");
+  LSURGE_REQUIRE(A && B && C && a_sinv && b_sinv && (!swiglu || (B2 && b2_sinv)) && (!sbwd || (Gs && Us)),
+                 "gemm_rows_f8: null pointer");
+  LSURGE_REQUIRE(!k_split || (epi == F8_STORE && B2 && b2_sinv && k_split % 64 == 0 && 2 * k_split == K),
+                 "gemm_rows_f8: k_split=%lld must be K / 2 and a multiple of 64, with B2 and its scales",
+                 (long long)k_split);
+  LSURGE_REQUIRE(!a_e5m2 || !swiglu, "gemm_rows_f8: the SwiGLU forward takes E4M3 activations");
   LSURGE_REQUIRE(((uintptr_t)A | (uintptr_t)B | (uintptr_t)B2 | (uintptr_t)(b_estride)) % 16 == 0,
                  "gemm_rows_f8: operands and the expert stride must be 16-byte aligned");
-  LSURGE_REQUIRE(!swiglu || !out_f32, "gemm_rows_f8: the SwiGLU epilogue writes bf16");
+  LSURGE_REQUIRE(!(swiglu || sbwd) || !out_f32, "gemm_rows_f8: the SwiGLU epilogues write bf16");
+  LSURGE_REQUIRE(!sbwd || ldc >= 2 * N, "gemm_rows_f8: the SwiGLU backward writes [dG | dU] rows of 2N");
   if (int rc = check_desc(std::max<int64_t>(g.tile_rows * lda, N * ldb), "gemm_rows_f8")) return rc;
   if (gather.rows) {
     LSURGE_REQUIRE(gather.div >= 1 && gather.nrows >= 1, "gemm_rows_f8: bad row gather");
@@ -389,11 +402,14 @@ int gemm_rows_f8(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
   a.b_estride = b_estride; a.K = K; a.N = N; a.ldc = ldc;
   if (out_f32) a.Cf = (float*)C;
   else a.C = (bf16_t*)C;
-  a.G = (bf16_t*)Gs; a.U = (bf16_t*)Us; a.ldg = ldc;
+  a.G = (bf16_t*)Gs; a.U = (bf16_t*)Us; a.ldg = sbwd ? N : ldc;
+  a.k_split = k_split;
   a.t_expert = g.blk_expert; a.t_rows = g.blk_rows; a.t_row0 = g.blk_row0; a.num_tiles = g.num_blocks;
   a.dense_rows = g.dense_rows;
   a.a_sinv = a_sinv; a.b_sinv = b_sinv; a.b2_sinv = b2_sinv; a.amax = amax;
-  return swiglu ? launch_rows<B_NK, EPI_SWIGLU_FWD, true>(kid, g, a, s) : launch_rows<B_NK, EPI_STORE, true>(kid, g, a, s);
+  if (swiglu) return launch_rows<B_NK, EPI_SWIGLU_FWD, 1>(kid, g, a, s);
+  if (sbwd) return a_e5m2 ? launch_rows<B_NK, EPI_SWIGLU_BWD, 2>(kid, g, a, s) : launch_rows<B_NK, EPI_SWIGLU_BWD, 1>(kid, g, a, s);
+  return a_e5m2 ? launch_rows<B_NK, EPI_STORE, 2>(kid, g, a, s) : launch_rows<B_NK, EPI_STORE, 1>(kid, g, a, s);
 }
 
 size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S) {
@@ -527,6 +543,74 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
                 hipLaunchKernelGGL(wgrad_chunk_reduce_kernel, dim3(grid), dim3(256), 0, s, (const float*)part,
                                    ch.split_list, ch.num_split, ch.e_pbase, ch.e_nparts, I, N, C, C2, n_split, ldc,
                                    c_estride, xo.expert, xo.C, xo.C2));
+  return LSURGE_OK;
+}
+
+static int check_wgrad_f8(const void* A, int64_t lda, const float* a_sinv, const void* B, int64_t ldb,
+                          const float* b_sinv, int64_t I, int64_t N, float* C, const char* what) {
+  LSURGE_REQUIRE(A && B && a_sinv && b_sinv && C, "%s: null pointer", what);
+  LSURGE_REQUIRE(I > 0 && N > 0 && I % 8 == 0 && N % 8 == 0 && lda % 16 == 0 && ldb % 16 == 0,
+                 "%s: I=%lld N=%lld (multiples of 8), lda=%lld ldb=%lld (multiples of 16)", what, (long long)I,
+                 (long long)N, (long long)lda, (long long)ldb);
+  LSURGE_REQUIRE(((uintptr_t)A | (uintptr_t)B) % 16 == 0, "%s: operands must be 16-byte aligned", what);
+  if (int rc = check_desc(I * lda, what)) return rc;
+  return check_desc(N * ldb, what);
+}
+
+int gemm_wgrad_f8_chunked(int kid, const WgradChunks& ch, int E, const void* A, int64_t lda, const float* a_sinv,
+                          const void* B, int64_t ldb, const float* b_sinv, int64_t I, int64_t N, float* C, float* C2,
+                          int64_t n_split, int64_t ldc, int64_t c_estride, void* part, size_t part_bytes,
+                          hipStream_t s) {
+  if (int rc = check_wgrad_f8(A, lda, a_sinv, B, ldb, b_sinv, I, N, C, "gemm_wgrad_f8_chunked")) return rc;
+  LSURGE_REQUIRE(E >= 1 && ch.max_chunks >= 1, "gemm_wgrad_f8_chunked: bad E / chunk table");
+  LSURGE_REQUIRE(part && part_bytes >= sizeof(float) * (size_t)ch.max_parts * I * N,
+                 "gemm_wgrad_f8_chunked: partial workspace %zu < %zu bytes", part_bytes,
+                 sizeof(float) * (size_t)ch.max_parts * I * N);
+  LSURGE_REQUIRE(!C2 || n_split % 4 == 0, "gemm_wgrad_f8_chunked: n_split must be a multiple of 4");
+  WgradArgs a{};
+  a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.I = I; a.N = N; a.C = C; a.C2 = C2;
+  a.n_split = n_split; a.ldc = ldc; a.c_estride = c_estride;
+  a.E = E; a.S = 1; a.part = (float*)part;
+  a.c_expert = ch.c_expert; a.c_row0 = ch.c_row0; a.c_rows = ch.c_rows; a.c_part = ch.c_part;
+  a.num_chunks = ch.num_chunks; a.max_chunks = ch.max_chunks;
+  a.a_sinv = a_sinv; a.b_sinv = b_sinv;
+  a.i_tiles = (int)((I + BM - 1) / BM);
+  a.n_tiles = (int)((N + BN - 1) / BN);
+  const int64_t tiles = (int64_t)pad8(ch.max_chunks) * a.i_tiles * a.n_tiles;
+  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_wgrad_f8_kernel<Cfg, 0, 1>), dim3((unsigned)tiles), dim3(GT), 0, s, a));
+  const unsigned grid = (unsigned)std::min<int64_t>(2 * ((I * N / 4 + 255) / 256), 2048);
+  LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
+                hipLaunchKernelGGL(wgrad_chunk_reduce_kernel, dim3(grid), dim3(256), 0, s, (const float*)part,
+                                   ch.split_list, ch.num_split, ch.e_pbase, ch.e_nparts, I, N, C, C2, n_split, ldc,
+                                   c_estride, -1, (float*)nullptr, (float*)nullptr));
+  return LSURGE_OK;
+}
+
+int gemm_wgrad_f8_dense(int kid, int64_t rows, const void* A, int64_t lda, const float* a_sinv, const void* B,
+                        int64_t ldb, const float* b_sinv, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
+                        int64_t ldc, int S, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (int rc = check_wgrad_f8(A, lda, a_sinv, B, ldb, b_sinv, I, N, C, "gemm_wgrad_f8_dense")) return rc;
+  LSURGE_REQUIRE(rows >= 1 && rows <= lda && rows <= ldb && S >= 1, "gemm_wgrad_f8_dense: rows=%lld, S=%d",
+                 (long long)rows, S);
+  WgradArgs a{};
+  a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.I = I; a.N = N; a.C = C; a.C2 = C2;
+  a.n_split = n_split; a.ldc = ldc; a.c_estride = 0; a.dense_rows = rows; a.E = 1; a.S = S;
+  a.a_sinv = a_sinv; a.b_sinv = b_sinv;
+  a.i_tiles = (int)((I + BM - 1) / BM);
+  a.n_tiles = (int)((N + BN - 1) / BN);
+  if (S > 1) {
+    const size_t need = wgrad_workspace_bytes(1, I, N, S);
+    LSURGE_REQUIRE(ws && ws_bytes >= need, "gemm_wgrad_f8_dense: workspace %zu < %zu", ws_bytes, need);
+    a.part = (float*)ws;
+  }
+  const int64_t tiles = (int64_t)S * a.i_tiles * a.n_tiles;
+  LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_wgrad_f8_kernel<Cfg, 0, 1>), dim3(pad8(tiles)), dim3(GT), 0, s, a));
+  if (S > 1) {
+    const unsigned grid = (unsigned)std::min<int64_t>((I * N + 255) / 256, 8192);
+    LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
+                  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(256), 0, s, (const float*)ws, S, 1, I, N, C,
+                                     C2, n_split, ldc, (int64_t)0));
+  }
   return LSURGE_OK;
 }
 
@@ -685,7 +769,7 @@ int lsurge_ragged_dot_fp8(const void* lhs_q, const float* lhs_scale_inv, const v
   if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0, &e_rows)) return rc;
   const bool f32 = out_dtype == LSURGE_F32;
   if (int rc = lsurge::gemm_rows_f8(KID_MISC, g, lhs_q, kdim, lhs_scale_inv, rhs_q, nullptr, kdim, n * kdim,
-                                    rhs_scale_inv, nullptr, kdim, n, out, n, f32, false, nullptr, nullptr, nullptr, s))
+                                    rhs_scale_inv, nullptr, kdim, n, out, n, f32, lsurge::F8_STORE, nullptr, nullptr, nullptr, s))
     return rc;
   LSURGE_LAUNCH(KID_MISC, s,
                 hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, out, m, n, f32 ? 4 : 2, total));

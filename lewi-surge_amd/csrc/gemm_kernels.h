@@ -24,10 +24,14 @@
 // Every output element is the same ascending sequence of 16-deep MFMA steps whatever the tile shape, so all
 // shapes give bitwise identical results.
 //
-// FP8 variant of gemm_rows (template flag F8): A and B in OCP E4M3, both K-contiguous, v_mfma_f32_32x32x64_f8f6f4.
-// The operands move through the same copy and LDS machinery counted in 2-byte units, so a 32-unit stage holds 64
-// values of k, one MFMA step; the epilogue multiplies the accumulators by the dequantisation factors (per-tensor
-// for A, per expert for B and B2) before the usual epilogues.
+// FP8 variant of gemm_rows (template flag F8): B in OCP E4M3, A in E4M3 (F8 = 1) or E5M2 (F8 = 2, a gradient), both
+// K-contiguous, v_mfma_f32_32x32x64_f8f6f4.  The operands move through the same copy and LDS machinery counted in
+// 2-byte units, so a 32-unit stage holds 64 values of k, one MFMA step; the epilogue multiplies the accumulators by
+// the dequantisation factors (per-tensor for A, per expert for B and B2) before the usual epilogues.  With a k split
+// (B up to k_split, B2 after it: the gate/up dgrad) the two weights keep scales of their own: at the first B2 stage
+// the accumulators are multiplied by b_sinv / b2_sinv, and the epilogue by a_sinv b2_sinv.
+// gemm_wgrad_f8 is the FP8 weight gradient: both operands are the transposed (K-contiguous over the padded rows)
+// copies that the backward's casts write, so it runs the FP8 row kernel's operand path over a chunk's K range.
 #pragma once
 #include <type_traits>
 
@@ -91,12 +95,14 @@ struct RowsArgs {
   int x_expert = -1;         // tiles of this expert id read Bx / B2x instead of B / B2 (-1: none); the layer's
   const bf16_t* Bx = nullptr;   // shared expert rides along the routed ones as expert E
   const bf16_t* B2x = nullptr;
-  // FP8 (F8 kernels only; A, B and B2 point at E4M3 bytes and K, lda, ldb, b_estride count them): dequantisation
+  // FP8 (F8 kernels only; A, B and B2 point at FP8 bytes and K, lda, ldb, b_estride count them): dequantisation
   // factors of A (one value) and of B / B2 (one per expert)
   const float* a_sinv = nullptr;
   const float* b_sinv = nullptr;
   const float* b2_sinv = nullptr;
-  uint32_t* amax = nullptr;  // SwiGLU forward: atomic max of |h| as bf16-rounded float bits (nullptr: none)
+  // SwiGLU forward: atomic max of |h|; FP8 SwiGLU backward: of |dG| and |dU|; as bf16-rounded float bits (nullptr:
+  // none)
+  uint32_t* amax = nullptr;
 };
 
 struct WgradArgs {
@@ -131,6 +137,10 @@ struct WgradArgs {
   int x_expert = -1;          // this expert id writes Cx / C2x (row pitch ldc) instead of C / C2 (-1: none)
   float* Cx = nullptr;
   float* C2x = nullptr;
+  // FP8 (gemm_wgrad_f8_kernel): A = [I, lda] and B = [N, ldb] bytes, K-contiguous over the rows; dequantisation
+  // factors of each (one value)
+  const float* a_sinv = nullptr;
+  const float* b_sinv = nullptr;
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -151,12 +161,13 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 p, bf16x8 q, f32x16 c) {
   }
 }
 
-// D[32 x 32] += P[32 x 64] Q[64 x 32] with E4M3 operands (formats 0 / 0); with zero scale operands the compiler
-// emits the unscaled v_mfma_f32_32x32x64_f8f6f4.  Lane l supplies row l%32 of P and column l%32 of Q as 32 bytes;
-// P and Q take their bytes from the same k positions, and D sums over all 64, so which k a byte slot stands for
-// never matters.  Same output layout as mfma32.
+// D[32 x 32] += P[32 x 64] Q[64 x 32] with FP8 operands of formats FP, FQ (0 = E4M3, 1 = E5M2); with zero scale
+// operands the compiler emits the unscaled v_mfma_f32_32x32x64_f8f6f4.  Lane l supplies row l%32 of P and column
+// l%32 of Q as 32 bytes; P and Q take their bytes from the same k positions, and D sums over all 64, so which k a
+// byte slot stands for never matters.  Same output layout as mfma32.
+template <int FP = 0, int FQ = 0>
 __device__ __forceinline__ f32x16 mfma32_f8(i32x8 p, i32x8 q, f32x16 c) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(p, q, c, 0, 0, 0, 0, 0, 0);
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(p, q, c, FP, FQ, 0, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------------------------- LDS tiles
@@ -440,7 +451,7 @@ struct FragSet {
 };
 
 // =====================================================================================================
-template <class Cfg, int BMODE, int EPI, bool F8 = false, int ET = LSURGE_BF16>
+template <class Cfg, int BMODE, int EPI, int F8 = 0, int ET = LSURGE_BF16>
 __global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW * Cfg::OCC / 4)))
 void gemm_rows_kernel(RowsArgs a) {
   static_assert(!F8 || (BMODE == B_NK && Cfg::BK == 32), "FP8: both operands K-contiguous, 64-value stages");
@@ -588,7 +599,7 @@ void gemm_rows_kernel(RowsArgs a) {
       return (j < FN / 2 ? 0 : BN / 2) + wn * (TN / 2) + 32 * (j < FN / 2 ? j : j - FN / 2);
     return wn * TN + 32 * j;
   };
-  typedef FragSet<FM, FN, typename std::conditional<F8, i32x8, bf16x8>::type> F;
+  typedef FragSet<FM, FN, typename std::conditional<F8 != 0, i32x8, bf16x8>::type> F;
   constexpr int KS = F8 ? 1 : BK / 16;
   auto load = [&](int slot, int s, F& f) {
     const bf16_t* at = smem + slot * Cfg::A_EL;
@@ -610,12 +621,26 @@ void gemm_rows_kernel(RowsArgs a) {
       }
     }
   };
+  // FP8 k split: stage index where B2 starts (-1: none) and the factor that carries the B part over to B2's scale
+  [[maybe_unused]] int kstage = 0;
+  [[maybe_unused]] const int ks_stage = (F8 && ksplit) ? ksplit / BK : -1;
+  [[maybe_unused]] float ks_ratio = 1.f;
+  if constexpr (F8 != 0 && EPI != EPI_SWIGLU_FWD)
+    if (ksplit) ks_ratio = a.b_sinv[expert] / a.b2_sinv[expert];
   auto mma = [&](const F& f) {
+    if constexpr (F8 != 0 && EPI != EPI_SWIGLU_FWD) {
+      if (kstage++ == ks_stage) {  // wave-uniform; once per tile
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[i][j] *= ks_ratio;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        if constexpr (F8) acc[i][j] = mfma32_f8(f.w[j], f.x[i], acc[i][j]);
+        if constexpr (F8 != 0) acc[i][j] = mfma32_f8<0, F8 == 2 ? 1 : 0>(f.w[j], f.x[i], acc[i][j]);
         else acc[i][j] = mfma32<ET>(f.w[j], f.x[i], acc[i][j]);
       }
   };
@@ -623,12 +648,13 @@ void gemm_rows_kernel(RowsArgs a) {
   // runs the loop for its copies and barriers only, without fragment reads or MFMAs; its accumulators stay zero and
   // are never stored.  One branch per wave, so the live loop is the plain one.
   if (wm * TM < rows && n0 + wn * (EPI == EPI_SWIGLU_FWD ? TN / 2 : TN) < N)
-    run_k_loop<Cfg, F, KS, F8>(nk, wave, issue, load, mma);
+    run_k_loop<Cfg, F, KS, F8 != 0>(nk, wave, issue, load, mma);
   else
-    run_k_loop<Cfg, F, KS, F8>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
-  if constexpr (F8) {  // dequantise: gate (or plain) columns by a_sinv * b_sinv[e], up columns by a_sinv * b2_sinv[e]
+    run_k_loop<Cfg, F, KS, F8 != 0>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
+  if constexpr (F8 != 0) {  // dequantise: gate (or plain) columns by a_sinv * b_sinv[e], up columns by a_sinv * b2_sinv[e]
+    // (k split: everything by a_sinv * b2_sinv[e], the B part having been carried over at the switch)
     const float sa = a.a_sinv[0];
-    const float s1 = sa * a.b_sinv[expert];
+    const float s1 = sa * ((EPI != EPI_SWIGLU_FWD && ksplit) ? a.b2_sinv[expert] : a.b_sinv[expert]);
     const float s2 = a.b2_sinv ? sa * a.b2_sinv[expert] : s1;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -644,7 +670,7 @@ void gemm_rows_kernel(RowsArgs a) {
   float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * SP);
   constexpr int LPR = TN / 8, RPP = 64 / LPR, PASSES = 32 / RPP;          // store mapping
   constexpr int LPR2 = TN / 16, RPP2 = 64 / LPR2, PASSES2 = 32 / RPP2;    // SwiGLU forward: TN / 2 outputs
-  [[maybe_unused]] float hmax = 0.f;  // SwiGLU forward with a.amax: max |h| over this lane's outputs
+  [[maybe_unused]] float hmax = 0.f;  // with a.amax: max |h| (|dG|, |dU| in the FP8 backward) over this lane's outputs
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int mbase = wm * TM + 32 * i;  // first tile row of this slice
@@ -715,6 +741,7 @@ void gemm_rows_kernel(RowsArgs a) {
             const float sg = sigmoid_f(g);
             dg[t] = v[t] * u * sg * (1.f + g * (1.f - sg));
             du[t] = v[t] * g * sg;
+            if constexpr (F8 != 0) hmax = fmaxf(hmax, fmaxf(fabsf(dg[t]), fabsf(du[t])));
           }
           st_bf16x8(a.C + gr * a.ldc + col, dg);
           st_bf16x8(a.C + gr * a.ldc + N + col, du);
@@ -722,12 +749,52 @@ void gemm_rows_kernel(RowsArgs a) {
       }
     }
   }
-  if (EPI == EPI_SWIGLU_FWD && a.amax) {
+  if ((EPI == EPI_SWIGLU_FWD || (F8 != 0 && EPI == EPI_SWIGLU_BWD)) && a.amax) {
     // max |bf16(h)| = bf16(max |h|) (rounding is monotonic); non-negative floats order like their bit patterns,
     // so an unsigned max over the bits is the float max, whatever order the waves arrive in
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) hmax = fmaxf(hmax, __shfl_xor(hmax, o, 64));
     if (lane == 0) atomicMax(a.amax, (uint32_t)f32_to_bf16(hmax) << 16);
+  }
+}
+
+// Weight-gradient epilogue (f32), staged through LDS as in gemm_rows_kernel: acc[i][j][4q + t] is C row
+// i0 + wm*TM + 32 i + lane%32, column n0 + wn*TN + 32 j + 8 q + 4 (lane/32) + t.  Read back with TN/8 lanes per row,
+// each lane storing 8 contiguous f32, to the chunk's partial slot, the split partials, or the gradient itself.
+template <class Cfg>
+__device__ __forceinline__ void wgrad_epilogue(const WgradArgs& a, const f32x16 (&acc)[Cfg::FM][Cfg::FN],
+                                               bf16_t* smem, int wave, int lane, int64_t i0, int64_t n0,
+                                               float* part_out, int S, int s, int e) {
+  constexpr int TM = Cfg::TM, TN = Cfg::TN, FM = Cfg::FM, SP = Cfg::SP;
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  const int64_t I = a.I, N = a.N;
+  __syncthreads();  // all waves are done with the ring
+  float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * SP);
+  constexpr int LPR = TN / 8, RPP = 64 / LPR, PASSES = 32 / RPP;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    if (i > 0) __builtin_amdgcn_wave_barrier();
+    park<Cfg>(stg, acc, i, lane);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int r = RPP * p + lane / LPR, c = 8 * (lane % LPR);
+      const int64_t row = i0 + wm * TM + 32 * i + r;
+      if (row >= I) continue;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t col = n0 + wn * TN + c + 4 * h;
+        if (col >= N) continue;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * SP + c + 4 * h);
+        float* dst;
+        if (part_out) dst = part_out + row * N + col;
+        else if (S > 1) dst = a.part + (((int64_t)s * a.E + e) * I + row) * N + col;
+        else if (e == a.x_expert) dst = (a.C2x && col >= a.n_split) ? a.C2x + row * a.ldc + (col - a.n_split)
+                                                                    : a.Cx + row * a.ldc + col;
+        else if (a.C2 && col >= a.n_split) dst = a.C2 + (int64_t)e * a.c_estride + row * a.ldc + (col - a.n_split);
+        else dst = a.C + (int64_t)e * a.c_estride + row * a.ldc + col;
+        *reinterpret_cast<f32x4*>(dst) = v;
+      }
+    }
   }
 }
 
@@ -738,7 +805,7 @@ template <class Cfg, int ET = LSURGE_BF16>
 __global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW * Cfg::OCC / 4)))
 void gemm_wgrad_kernel(WgradArgs a) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, ST = Cfg::ST;
-  constexpr int TM = Cfg::TM, TN = Cfg::TN, FM = Cfg::FM, FN = Cfg::FN, SP = Cfg::SP;
+  constexpr int TM = Cfg::TM, TN = Cfg::TN, FM = Cfg::FM, FN = Cfg::FN;
   constexpr int CPA = Cfg::CPA, CPB = Cfg::CPB, CPS = BK / 4;
   // ring: A BM/128 N-major sub-tiles (BK rows x 128 columns), B BN/128 sub-tiles; after the K loop the same
   // memory stages the epilogue
@@ -912,37 +979,127 @@ void gemm_wgrad_kernel(WgradArgs a) {
     else run_k_loop<Cfg, F>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
   }
 
-  // epilogue (f32), staged through LDS as in gemm_rows_kernel: acc[i][j][4q + t] is C row
-  // i0 + wm*TM + 32 i + lane%32, column n0 + wn*TN + 32 j + 8 q + 4 (lane/32) + t.  Read back with TN/8 lanes
-  // per row, each lane storing 8 contiguous f32.
-  __syncthreads();  // all waves are done with the ring
-  float* const stg = reinterpret_cast<float*>(smem) + wave * (32 * SP);
-  constexpr int LPR = TN / 8, RPP = 64 / LPR, PASSES = 32 / RPP;
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    if (i > 0) __builtin_amdgcn_wave_barrier();
-    park<Cfg>(stg, acc, i, lane);
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int r = RPP * p + lane / LPR, c = 8 * (lane % LPR);
-      const int64_t row = i0 + wm * TM + 32 * i + r;
-      if (row >= I) continue;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int64_t col = n0 + wn * TN + c + 4 * h;
-        if (col >= N) continue;
-        const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * SP + c + 4 * h);
-        float* dst;
-        if (part_out) dst = part_out + row * N + col;
-        else if (S > 1) dst = a.part + (((int64_t)s * a.E + e) * I + row) * N + col;
-        else if (e == a.x_expert) dst = (a.C2x && col >= a.n_split) ? a.C2x + row * a.ldc + (col - a.n_split)
-                                                                    : a.Cx + row * a.ldc + col;
-        else if (a.C2 && col >= a.n_split) dst = a.C2 + (int64_t)e * a.c_estride + row * a.ldc + (col - a.n_split);
-        else dst = a.C + (int64_t)e * a.c_estride + row * a.ldc + col;
-        *reinterpret_cast<f32x4*>(dst) = v;
-      }
-    }
+  wgrad_epilogue<Cfg>(a, acc, smem, wave, lane, i0, n0, part_out, S, s, e);
+}
+
+// =====================================================================================================
+// FP8 weight gradient C_e[I, N] = (A'_e B'_e^T) a_sinv b_sinv.  A' [I, lda] and B' [N, ldb] are the transposed copies
+// the backward's casts write (activations in format FA, gradients in FB), K-contiguous over the padded rows, so a
+// chunk's reduction over rows [c_row0, c_row0 + c_rows) is a K range of both, read with gemm_rows_kernel's FP8
+// operand path (K-major LDS tiles, one 64-value MFMA step per stage).  Chunk table, tile order, partial slots and
+// output routing as in gemm_wgrad_kernel; dense (no table): the dense_rows reduction split S ways on 64-value
+// boundaries.  Values past a chunk's end within its 16-byte copy granule are padding rows (zero in the casts), or
+// the next chunk of the same expert, whose boundaries are multiples of 64.
+template <class Cfg, int FA, int FB>
+__global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW * Cfg::OCC / 4)))
+void gemm_wgrad_f8_kernel(WgradArgs a) {
+  static_assert(Cfg::BK == 32 && !Cfg::PP, "FP8 weight gradient: 64-value stages, 4-wave single-buffered loop");
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, ST = Cfg::ST;
+  constexpr int TM = Cfg::TM, FM = Cfg::FM, FN = Cfg::FN;
+  constexpr int CPA = Cfg::CPA, CPB = Cfg::CPB;
+  constexpr int RPC = 1024 / (2 * BK), CPR = BK / 8;  // rows per copy, 16-byte chunks per row and stage
+  constexpr int SB = 2 * BK;                          // values (bytes) per stage
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[Cfg::SMEM_EL];
+  constexpr uint32_t A_SLOT = Cfg::A_EL * 2, B_SLOT = Cfg::B_EL * 2, B_RING = ST * A_SLOT;  // bytes
+  const int64_t tiles_per_e = (int64_t)(a.c_expert ? 1 : a.S) * a.i_tiles * a.n_tiles;
+  int64_t logical;
+  if (a.c_expert) {
+    const int64_t l = blockIdx.x / 8;
+    logical = (8 * (l / tiles_per_e) + blockIdx.x % 8) * tiles_per_e + l % tiles_per_e;
+  } else {
+    logical = xcd_logical(blockIdx.x, (int64_t)gridDim.x);
   }
+  const int g = (int)(logical / tiles_per_e);
+  int64_t rem = logical % tiles_per_e;
+  const int s = (int)(rem / ((int64_t)a.i_tiles * a.n_tiles));
+  rem %= (int64_t)a.i_tiles * a.n_tiles;
+  const int it = (int)(rem / a.n_tiles), nt = (int)(rem % a.n_tiles);
+  int e, S = a.S;
+  int64_t r0, nrows;
+  float* part_out = nullptr;
+  if (a.c_expert) {
+    if (g >= a.max_chunks || g >= a.num_chunks[0]) return;
+    e = a.c_expert[g];
+    r0 = a.c_row0[g];
+    nrows = a.c_rows[g];
+    S = 1;
+    const int ps = a.c_part[g];
+    if (ps >= 0) part_out = a.part + (int64_t)ps * a.I * a.N;
+  } else {
+    e = g;
+    if (e >= a.E) return;
+    r0 = 0;
+    nrows = a.dense_rows;
+  }
+  const int64_t chunk = ((nrows + S - 1) / S + SB - 1) / SB * SB;
+  const int64_t rs = (int64_t)s * chunk, re = min(nrows, rs + chunk);
+  const int K = re > rs ? (int)(re - rs) : 0;  // reduction length (values = bytes)
+  const int nk = (K + SB - 1) / SB;
+  const int64_t i0 = (int64_t)it * BM, n0 = (int64_t)nt * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  const uint32_t lds0 = lds_addr(smem);
+  const int64_t kb = r0 + rs;  // first reduction column of both operands
+  const u32x4 rsA = make_rsrc(reinterpret_cast<const uint8_t*>(a.A) + kb, a.I * a.lda - kb);
+  const u32x4 rsB = make_rsrc(reinterpret_cast<const uint8_t*>(a.B) + kb, a.N * a.ldb - kb);
+  // K-major copies as in gemm_rows_kernel: copy q covers tile rows RPC q .. RPC q + RPC - 1, lane -> row
+  // RPC q + lane / CPR, slot lane % CPR holding chunk slot ^ swz(row); byte offset at k = 0 and the chunk's k
+  uint32_t a_off[CPA], b_off[CPB];
+  int a_k[CPA], b_k[CPB];
+#pragma unroll
+  for (int c = 0; c < CPA; ++c) {
+    const int r = RPC * (CPA * wave + c) + lane / CPR;
+    const int kc = (lane % CPR) ^ km_swz<BK>(r);
+    a_off[c] = (uint32_t)((i0 + r) * a.lda + 16 * kc);
+    a_k[c] = i0 + r < a.I ? 16 * kc : KBIG;
+  }
+#pragma unroll
+  for (int c = 0; c < CPB; ++c) {
+    const int n = RPC * (CPB * wave + c) + lane / CPR;
+    const int kc = (lane % CPR) ^ km_swz<BK>(n);
+    b_off[c] = (uint32_t)((n0 + n) * a.ldb + 16 * kc);
+    b_k[c] = n0 + n < a.N ? 16 * kc : KBIG;
+  }
+  auto issue = [&](int slot, int kt) {
+    const int k0 = kt * SB;
+    const uint32_t at = lds0 + slot * A_SLOT, bt = lds0 + B_RING + slot * B_SLOT;
+#pragma unroll
+    for (int c = 0; c < CPA; ++c)
+      copy16(rsA, k0 + a_k[c] < K ? a_off[c] + (uint32_t)k0 : OOB, at + 1024 * (CPA * wave + c));
+#pragma unroll
+    for (int c = 0; c < CPB; ++c)
+      copy16(rsB, k0 + b_k[c] < K ? b_off[c] + (uint32_t)k0 : OOB, bt + 1024 * (CPB * wave + c));
+  };
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+  typedef FragSet<FM, FN, i32x8> F;
+  auto load = [&](int slot, int, F& f) {
+    const bf16_t* at = smem + slot * Cfg::A_EL;
+    const bf16_t* bt = smem + ST * Cfg::A_EL + slot * Cfg::B_EL;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) f.x[i] = frag_k8(at, wm * TM + 32 * i + (lane & 31), lane >> 5);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) f.w[j] = frag_k8(bt, wn * Cfg::TN + 32 * j + (lane & 31), lane >> 5);
+  };
+  auto mma = [&](const F& f) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma32_f8<FB, FA>(f.w[j], f.x[i], acc[i][j]);
+  };
+  if (nk > 0) {  // waves outside the tile: copies and barriers only
+    if (i0 + wm * TM < a.I && n0 + wn * Cfg::TN < a.N) run_k_loop<Cfg, F, 1, true>(nk, wave, issue, load, mma);
+    else run_k_loop<Cfg, F, 1, true>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
+  }
+  const float sab = a.a_sinv[0] * a.b_sinv[0];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] *= sab;
+  wgrad_epilogue<Cfg>(a, acc, smem, wave, lane, i0, n0, part_out, S, s, e);
 }
 
 }  // namespace lsgemm

@@ -93,11 +93,13 @@ int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const
                  int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
                  bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false,
                  const ExtraExpert& xe = ExtraExpert(), int et = LSURGE_BF16);
-// FP8 (E4M3) row GEMM, both operands K-contiguous (B_e stored [N, K]); byte pitches; see gemm.hip
+// FP8 row GEMM, both operands K-contiguous (B_e stored [N, K], E4M3; A E4M3, or E5M2 with a_e5m2); byte pitches;
+// epilogue F8_STORE, F8_SWIGLU_FWD or F8_SWIGLU_BWD; k_split: B2 for k >= k_split (multiple of 64); see gemm.hip
+enum F8Epi { F8_STORE = 0, F8_SWIGLU_FWD = 1, F8_SWIGLU_BWD = 2 };
 int gemm_rows_f8(int kid, const GemmBlocks& g, const void* A, int64_t lda, const float* a_sinv, const void* B,
                  const void* B2, int64_t ldb, int64_t b_estride, const float* b_sinv, const float* b2_sinv, int64_t K,
-                 int64_t N, void* C, int64_t ldc, bool out_f32, bool swiglu, void* Gs, void* Us, uint32_t* amax,
-                 hipStream_t s, const RowGather& gather = RowGather());
+                 int64_t N, void* C, int64_t ldc, bool out_f32, int epi, void* Gs, void* Us, uint32_t* amax,
+                 hipStream_t s, const RowGather& gather = RowGather(), int64_t k_split = 0, bool a_e5m2 = false);
 size_t wgrad_workspace_bytes(int E, int64_t I, int64_t N, int S);
 int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32_t* e_rows, int64_t dense_rows,
                int64_t max_rows, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t I, int64_t N,
@@ -135,15 +137,40 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
                        int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s,
                        const RowGather& gather = RowGather(), const ExtraOut& xo = ExtraOut(), int et = LSURGE_BF16);
 
-// ---- FP8 quantisation (fp8.hip), current scaling to OCP E4M3
+// FP8 weight gradients (E4M3 activations x E5M2 gradients): A [I, lda] and B [N, ldb] bytes, the transposed casts,
+// K-contiguous over the rows; dequantised by a_sinv[0] b_sinv[0].  Chunked: the routed experts over a chunk table;
+// dense: one matrix over `rows` rows split S ways (f32 partials in ws, wgrad_workspace_bytes(1, I, N, S)).
+int gemm_wgrad_f8_chunked(int kid, const WgradChunks& ch, int E, const void* A, int64_t lda, const float* a_sinv,
+                          const void* B, int64_t ldb, const float* b_sinv, int64_t I, int64_t N, float* C, float* C2,
+                          int64_t n_split, int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s);
+int gemm_wgrad_f8_dense(int kid, int64_t rows, const void* A, int64_t lda, const float* a_sinv, const void* B,
+                        int64_t ldb, const float* b_sinv, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
+                        int64_t ldc, int S, void* ws, size_t ws_bytes, hipStream_t s);
+
+// ---- FP8 quantisation (fp8.hip), current scaling to OCP E4M3 (and E5M2 for gradients)
 size_t fp8_partial_bytes(int64_t groups);  // amax partials of fp8_quantize_impl
 // groups of [rows, cols] bf16 -> q (transpose: [cols, rows] per group), sinv[g] = 1 / scale; zero[0 .. nzero) is
-// cleared by the cast kernel (untransposed only), for slots a later kernel fills by atomic max
+// cleared by the cast kernel (untransposed only), for slots a later kernel fills by atomic max.  q_nt (transposed
+// casts only): the same codes untransposed as well.  scale_out (untransposed only): the scale of each group.
 int fp8_quantize_impl(const void* x, int64_t groups, int64_t rows, int64_t cols, bool transpose, void* q, float* sinv,
-                      float* partial, hipStream_t s, uint32_t* zero = nullptr, int nzero = 0);
+                      float* partial, hipStream_t s, uint32_t* zero = nullptr, int nzero = 0, void* q_nt = nullptr,
+                      float* scale_out = nullptr);
 // cast of n bf16 values with the amax in *amax_bits (float bits); nrows (optional): only the first
-// nrows[0] * row_elems values
+// nrows[0] * row_elems values; scale_out (optional) receives the scale
 int fp8_cast_with_amax(const void* x, int64_t n, const uint32_t* amax_bits, void* q, float* sinv,
-                       const int32_t* nrows, int64_t row_elems, hipStream_t s);
+                       const int32_t* nrows, int64_t row_elems, hipStream_t s, float* scale_out = nullptr);
+// Row-layout casts of the backward.  Rows r < min(rows, nrows[0] nmul) (nrows optional: a block count and its rows
+// per block, or a row count and 1) with row_src[r] >= 0 (row_src optional) are data, read from x row r, or from x row row_src[r] / kdiv when gathered; the others are zeros.
+// fp8_amax_rows writes one amax partial per workgroup into partial (fp8_rows_partial_bytes) and returns their count
+// (negative: an error code); its first workgroup also clears zero[0 .. nzero).
+size_t fp8_rows_partial_bytes();
+int fp8_amax_rows(const void* x, int64_t rows, int64_t cols, const int32_t* nrows, int nmul, const int32_t* row_src,
+                  int kdiv, bool gather, float* partial, hipStream_t s, uint32_t* zero = nullptr, int nzero = 0);
+// cast to E4M3 or E5M2 (e5m2) into a row-wise copy qr [rows, cols] and / or a transposed copy qt [cols, ldq]; the
+// scale comes from nparts > 0 amax partials at src, from an amax slot (nparts == 0: float bits), or is src[0]
+// (nparts < 0).  sinv[0] receives 1 / scale and scale_out[0] (optional) the scale.
+int fp8_cast_rows(const void* x, int64_t rows, int64_t cols, const int32_t* nrows, int nmul, const int32_t* row_src,
+                  int kdiv, bool gather, const float* src, int nparts, bool e5m2, void* qr, void* qt, int64_t ldq,
+                  float* sinv, float* scale_out, hipStream_t s);
 
 }  // namespace lsurge

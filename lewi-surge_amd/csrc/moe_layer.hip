@@ -71,6 +71,7 @@ struct Saved {
   int32_t *t_expert, *t_rows, *t_row0, *num_tiles;
   bf16_t *g, *u, *h, *y_pad;
   bf16_t *sg, *su, *sh, *sy;  // shared expert run on its own: gate, up, h, output
+  float* f8_scale;  // FP8 forward: the scales of x, routed h and shared h (the backward casts them again)
 };
 
 size_t carve_saved(const Dims& q, void* base, Saved* sv) {
@@ -101,6 +102,7 @@ size_t carve_saved(const Dims& q, void* base, Saved* sv) {
   sv->su = c.take<bf16_t>(own * q.fs);
   sv->sh = c.take<bf16_t>(own * q.fs);
   sv->sy = c.take<bf16_t>(own * q.d);
+  sv->f8_scale = c.take<float>(4);
   return c.off + 256;
 }
 
@@ -167,9 +169,12 @@ size_t router_hist_bytes(const lsurge_moe_shape* s) {
 }
 
 // FP8 weights (one caller buffer): E4M3 gate, up [E, f, d], down [E, d, f], shared gate, up [fs, d], down [d, fs]
-// (all K-contiguous), then the scale_inv of gate, up, down [E] each and of the three shared matrices.
+// (all K-contiguous for the forward), the same codes in the weights' own layout for the backward's dgrads (gate, up
+// [E, d, f], down [E, f, d], shared gate, up [d, fs], down [fs, d]: K-contiguous there), then the scale_inv of gate,
+// up, down [E] each and of the three shared matrices (one scale per matrix, both copies).
 struct Fp8W {
   uint8_t *q_gate, *q_up, *q_down, *qs_gate, *qs_up, *qs_down;
+  uint8_t *qb_gate, *qb_up, *qb_down, *qbs_gate, *qbs_up, *qbs_down;
   float *s_gate, *s_up, *s_down, *s_shared;
 };
 size_t carve_fp8w(const Dims& q, void* base, Fp8W* w) {
@@ -180,6 +185,12 @@ size_t carve_fp8w(const Dims& q, void* base, Fp8W* w) {
   w->qs_gate = c.take<uint8_t>(q.fs * q.d);
   w->qs_up = c.take<uint8_t>(q.fs * q.d);
   w->qs_down = c.take<uint8_t>(q.d * q.fs);
+  w->qb_gate = c.take<uint8_t>(q.E * q.d * q.f);
+  w->qb_up = c.take<uint8_t>(q.E * q.d * q.f);
+  w->qb_down = c.take<uint8_t>(q.E * q.f * q.d);
+  w->qbs_gate = c.take<uint8_t>(q.d * q.fs);
+  w->qbs_up = c.take<uint8_t>(q.d * q.fs);
+  w->qbs_down = c.take<uint8_t>(q.fs * q.d);
   w->s_gate = c.take<float>(q.E);
   w->s_up = c.take<float>(q.E);
   w->s_down = c.take<float>(q.E);
@@ -204,6 +215,56 @@ size_t carve_fp8ws(const Dims& q, void* base, Fp8Ws* w) {
   w->slots = c.take<uint32_t>(2);
   w->sinv = c.take<float>(4);
   return c.off;
+}
+
+// FP8 backward scratch (after the bf16 backward's BwdWs in the same workspace).  Routed, over the padded rows (P):
+// dY and [dG | dU] in E5M2 row-wise (the dgrads' A operands) and transposed (the wgrads' B operands), h and the
+// gathered x rows transposed in E4M3 with the forward's scales (the wgrads' A operands).  Shared expert, over its T
+// rows: the same set for its own GEMMs, plus its [dG | dU] and dx in bf16.  Amax partials per stream, the atomic
+// max slots of the two [dG | dU] and the scale_inv of every cast:
+//   sinv: 0 dY, 1 dGU, 2 h^T, 3 x^T (gathered), 4 shared dY, 5 shared dGU, 6 shared h^T, 7 x^T (dense)
+struct Fp8Bws {
+  uint8_t *dyq, *dyqT, *dguq, *dguqT, *hqT, *xqT;
+  uint8_t *sdyq, *sdyqT, *sdguq, *sdguqT, *shqT, *sxqT;
+  bf16_t *sdgu, *sdx;
+  float *part_main, *part_side;
+  uint32_t* slots;
+  float* sinv;
+  void* part_s;  // split-K partials of the shared weight gradients
+  size_t part_s_bytes;
+  int64_t T64;   // pitch of the shared expert's transposed copies
+};
+size_t carve_fp8bws(const Dims& q, void* base, Fp8Bws* w) {
+  Carve c(base);
+  const int64_t P = q.P, T = q.fs ? q.T : 0;
+  w->T64 = (q.T + 63) / 64 * 64;
+  const int64_t T64 = q.fs ? w->T64 : 0;
+  w->dyq = c.take<uint8_t>(P * q.d);
+  w->dyqT = c.take<uint8_t>(q.d * P);
+  w->dguq = c.take<uint8_t>(P * 2 * q.f);
+  w->dguqT = c.take<uint8_t>(2 * q.f * P);
+  w->hqT = c.take<uint8_t>(q.f * P);
+  w->xqT = c.take<uint8_t>(q.d * P);
+  w->sdyq = c.take<uint8_t>(T * q.d);
+  w->sdyqT = c.take<uint8_t>(q.d * T64);
+  w->sdguq = c.take<uint8_t>(T * 2 * q.fs);
+  w->sdguqT = c.take<uint8_t>(2 * q.fs * T64);
+  w->shqT = c.take<uint8_t>(q.fs * T64);
+  w->sxqT = c.take<uint8_t>(q.d * T64);
+  w->sdgu = c.take<bf16_t>(T * 2 * q.fs);
+  w->sdx = c.take<bf16_t>(T * q.d);
+  w->part_main = c.take<float>(lsurge::fp8_rows_partial_bytes() / sizeof(float));
+  w->part_side = c.take<float>(lsurge::fp8_rows_partial_bytes() / sizeof(float));
+  w->slots = c.take<uint32_t>(2);
+  w->sinv = c.take<float>(8);
+  size_t part = 0;
+  if (q.fs) {
+    part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, 2 * q.fs, dense_splits(q.T, q.d, 2 * q.fs)));
+    part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.fs, q.d, dense_splits(q.T, q.fs, q.d)));
+  }
+  w->part_s_bytes = part;
+  w->part_s = c.take<char>(part);
+  return c.off + 256;
 }
 
 int check_shape(const lsurge_moe_shape* s) {
@@ -283,8 +344,9 @@ struct ForkGuard {
 }  // namespace
 extern "C" {
 
-// one scale per expert and matrix; each weight is transposed into the K-contiguous operand of the FP8 GEMM.  The
-// small shared-expert matrices (latency-bound launches) go on a helper stream beside the routed ones.
+// one scale per expert and matrix; each weight is transposed into the K-contiguous operand of the forward's FP8 GEMM
+// and also kept in its own layout, the K-contiguous operand of the backward's dgrad (same codes).  The small
+// shared-expert matrices (latency-bound launches) go on a helper stream beside the routed ones.
 int lsurge_moe_fp8_quantize_weights(const lsurge_moe_shape* s, const lsurge_moe_params* p, void* wq, size_t wq_bytes,
                                     void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
   if (int rc = check_shape(s)) return rc;
@@ -305,14 +367,24 @@ int lsurge_moe_fp8_quantize_weights(const lsurge_moe_shape* s, const lsurge_moe_
   hipStream_t s0 = fg.f.side[0];
   if (q.fs) {
     if (int rc = lsurge::stream_after(s0, st, fg.f.ev[0])) return rc;
-    if (int rc = lsurge::fp8_quantize_impl(p->ws_gate, 1, q.d, q.fs, true, w.qs_gate, w.s_shared, part_s, s0)) return rc;
-    if (int rc = lsurge::fp8_quantize_impl(p->ws_up, 1, q.d, q.fs, true, w.qs_up, w.s_shared + 1, part_s, s0)) return rc;
-    if (int rc = lsurge::fp8_quantize_impl(p->ws_down, 1, q.fs, q.d, true, w.qs_down, w.s_shared + 2, part_s, s0))
+    if (int rc = lsurge::fp8_quantize_impl(p->ws_gate, 1, q.d, q.fs, true, w.qs_gate, w.s_shared, part_s, s0, nullptr,
+                                           0, w.qbs_gate))
+      return rc;
+    if (int rc = lsurge::fp8_quantize_impl(p->ws_up, 1, q.d, q.fs, true, w.qs_up, w.s_shared + 1, part_s, s0, nullptr,
+                                           0, w.qbs_up))
+      return rc;
+    if (int rc = lsurge::fp8_quantize_impl(p->ws_down, 1, q.fs, q.d, true, w.qs_down, w.s_shared + 2, part_s, s0,
+                                           nullptr, 0, w.qbs_down))
       return rc;
   }
-  if (int rc = lsurge::fp8_quantize_impl(p->w_gate, q.E, q.d, q.f, true, w.q_gate, w.s_gate, part, st)) return rc;
-  if (int rc = lsurge::fp8_quantize_impl(p->w_up, q.E, q.d, q.f, true, w.q_up, w.s_up, part, st)) return rc;
-  if (int rc = lsurge::fp8_quantize_impl(p->w_down, q.E, q.f, q.d, true, w.q_down, w.s_down, part, st)) return rc;
+  if (int rc = lsurge::fp8_quantize_impl(p->w_gate, q.E, q.d, q.f, true, w.q_gate, w.s_gate, part, st, nullptr, 0,
+                                         w.qb_gate))
+    return rc;
+  if (int rc = lsurge::fp8_quantize_impl(p->w_up, q.E, q.d, q.f, true, w.q_up, w.s_up, part, st, nullptr, 0, w.qb_up))
+    return rc;
+  if (int rc = lsurge::fp8_quantize_impl(p->w_down, q.E, q.f, q.d, true, w.q_down, w.s_down, part, st, nullptr, 0,
+                                         w.qb_down))
+    return rc;
   return fg.joined(q.fs ? lsurge::stream_after(st, s0, fg.f.ev[1]) : LSURGE_OK);
 }
 
@@ -374,7 +446,8 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   if (w8) {
     carve_fp8ws(q, (char*)workspace + hist_bytes, &f8);
     if (int rc = lsurge::stream_after(s0, st, fg.f.ev[3])) return rc;
-    if (int rc = lsurge::fp8_quantize_impl(p->x, 1, q.T, q.d, false, f8.xq, f8.sinv, f8.partial, s0, f8.slots, 2))
+    if (int rc = lsurge::fp8_quantize_impl(p->x, 1, q.T, q.d, false, f8.xq, f8.sinv, f8.partial, s0, f8.slots, 2,
+                                           nullptr, sv.f8_scale))
       return rc;
     if (s0 != st && hipEventRecord(fg.f.ev[2], s0) != hipSuccess)
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipEventRecord failed");
@@ -398,14 +471,15 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   if (q.fs && w8) {
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
     if (int rc = lsurge::gemm_rows_f8(KID_SHARED_GU_FWD, dense, f8.xq, q.d, f8.sinv, w8->qs_gate, w8->qs_up, q.d, 0,
-                                      w8->s_shared, w8->s_shared + 1, q.d, q.fs, sh, q.fs, false, true, sg, su,
-                                      f8.slots + 1, s0))
+                                      w8->s_shared, w8->s_shared + 1, q.d, q.fs, sh, q.fs, false, lsurge::F8_SWIGLU_FWD,
+                                      sg, su, f8.slots + 1, s0))
       return rc;
-    if (int rc = lsurge::fp8_cast_with_amax(sh, q.T * q.fs, f8.slots + 1, f8.shq, f8.sinv + 2, nullptr, 0, s0))
+    if (int rc = lsurge::fp8_cast_with_amax(sh, q.T * q.fs, f8.slots + 1, f8.shq, f8.sinv + 2, nullptr, 0, s0,
+                                            sv.f8_scale + 2))
       return rc;
     if (int rc = lsurge::gemm_rows_f8(KID_SHARED_DOWN_FWD, dense, f8.shq, q.fs, f8.sinv + 2, w8->qs_down, nullptr, q.fs,
-                                      0, w8->s_shared + 2, nullptr, q.fs, q.d, sy, q.d, false, false, nullptr, nullptr,
-                                      nullptr, s0))
+                                      0, w8->s_shared + 2, nullptr, q.fs, q.d, sy, q.d, false, lsurge::F8_STORE,
+                                      nullptr, nullptr, nullptr, s0))
       return rc;
   } else if (q.fs) {
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
@@ -449,14 +523,15 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
     if (s0 != st && hipStreamWaitEvent(st, fg.f.ev[2], 0) != hipSuccess)
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipStreamWaitEvent failed");
     if (int rc = lsurge::gemm_rows_f8(KID_GEMM_GU_FWD, blocks8, f8.xq, q.d, f8.sinv, w8->q_gate, w8->q_up, q.d,
-                                      q.f * q.d, w8->s_gate, w8->s_up, q.d, q.f, sv.h, q.f, false, true, sv.g, sv.u,
-                                      f8.slots, st, gather))
+                                      q.f * q.d, w8->s_gate, w8->s_up, q.d, q.f, sv.h, q.f, false,
+                                      lsurge::F8_SWIGLU_FWD, sv.g, sv.u, f8.slots, st, gather))
       return rc;
-    if (int rc = lsurge::fp8_cast_with_amax(sv.h, q.P * q.f, f8.slots, f8.hq, f8.sinv + 1, sv.num_blocks, BLK * q.f, st))
+    if (int rc = lsurge::fp8_cast_with_amax(sv.h, q.P * q.f, f8.slots, f8.hq, f8.sinv + 1, sv.num_blocks, BLK * q.f, st,
+                                            sv.f8_scale + 1))
       return rc;
     if (int rc = lsurge::gemm_rows_f8(KID_GEMM_DOWN_FWD, blocks8, f8.hq, q.f, f8.sinv + 1, w8->q_down, nullptr, q.f,
-                                      q.d * q.f, w8->s_down, nullptr, q.f, q.d, sv.y_pad, q.d, false, false, nullptr,
-                                      nullptr, nullptr, st))
+                                      q.d * q.f, w8->s_down, nullptr, q.f, q.d, sv.y_pad, q.d, false, lsurge::F8_STORE,
+                                      nullptr, nullptr, nullptr, st))
       return rc;
     if (int rc = fg.joined(lsurge::stream_after(st, s0, fg.f.ev[1]))) return rc;
     return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sy : nullptr, out,
@@ -618,6 +693,161 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
       return rc;
   }
   return LSURGE_OK;
+}
+
+size_t lsurge_moe_bwd_fp8_workspace_bytes(const lsurge_moe_shape* s) {
+  if (check_shape(s)) return 0;
+  const Dims q = dims_of(s);
+  BwdWs w;
+  Fp8Bws f;
+  return (carve_bwd(q, nullptr, &w) + 255) / 256 * 256 + carve_fp8bws(q, nullptr, &f);
+}
+
+// FP8 backward (Transformer Engine's current-scaling training recipe, hybrid formats): gradients are cast to E5M2
+// with scales of their own (dY rows, [dG | dU], per tensor, just before use), the dgrads multiply them with the
+// weights' E4M3 codes of the forward (their untransposed copies, same scales), and the wgrads with the forward's
+// E4M3 codes of h and x (cast again, transposed, with the scales the forward saved).  Combine, dispatch and router
+// backward are those of the bf16 backward; the shared expert runs its FP8 backward as dense GEMMs of its own.
+// Stream plan (caller's stream = critical path):
+//   main: combine bwd -> dY amax -> dY cast -> [record] -> down dgrad (+SwiGLU bwd, amax of [dG | dU]) -> [dG | dU]
+//         cast -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
+//   s1:   from the start: W_r transpose, chunk table, h^T and gathered x^T casts; after the record: down wgrad
+//   s0:   from the start: the shared expert's backward; after the record: router wgrad
+int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* wq, size_t wq_bytes,
+                       const void* dy, const void* saved, const lsurge_moe_grads* g, void* workspace,
+                       size_t workspace_bytes, lsurge_stream_t stream) {
+  if (int rc = check_shape(s)) return rc;
+  LSURGE_REQUIRE(p && p->x && p->w_r && wq && dy && saved && g, "moe_bwd_fp8: null pointer");
+  LSURGE_REQUIRE(g->dx && g->dw_r && g->dw_gate && g->dw_up && g->dw_down, "moe_bwd_fp8: null gradient pointer");
+  LSURGE_REQUIRE(!s->fs || (g->dws_gate && g->dws_up && g->dws_down), "moe_bwd_fp8: shared expert gradients missing");
+  const Dims q = dims_of(s);
+  Fp8W w8;
+  LSURGE_REQUIRE(wq_bytes >= carve_fp8w(q, nullptr, &w8), "moe_bwd_fp8: weight buffer %zu < %zu bytes", wq_bytes,
+                 carve_fp8w(q, nullptr, &w8));
+  carve_fp8w(q, (void*)wq, &w8);
+  Saved sv;
+  carve_saved(q, (void*)saved, &sv);
+  BwdWs w;
+  Fp8Bws f8;
+  const size_t wb = (carve_bwd(q, nullptr, &w) + 255) / 256 * 256;
+  const size_t need = wb + carve_fp8bws(q, nullptr, &f8);
+  LSURGE_REQUIRE(workspace && workspace_bytes >= need, "moe_bwd_fp8: workspace %zu < %zu bytes", workspace_bytes, need);
+  carve_bwd(q, workspace, &w);
+  carve_fp8bws(q, (char*)workspace + wb, &f8);
+  hipStream_t st = (hipStream_t)stream;
+  float* dweights = g->dweights ? g->dweights : w.dweights;
+  const int64_t d = q.d, f = q.f, fs = q.fs, P = q.P, T = q.T;
+  // the routed dgrads run the forward's 128-row blocks on the 4-wave kernel
+  const lsurge::GemmBlocks blocks8{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0, 128};
+  ForkGuard fg;
+  if (int rc = fg.acquire(st)) return rc;
+  hipStream_t s0 = fg.f.side[0], s1 = fg.f.side[1];
+  hipEvent_t* ev = fg.f.ev;
+  if (int rc = lsurge::stream_after(s1, st, ev[0])) return rc;
+  if (s0 != st && hipStreamWaitEvent(s0, ev[0], 0) != hipSuccess)
+    return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_bwd_fp8: hipStreamWaitEvent failed");
+
+  // s1: W_r^T, the chunk table, and the wgrads' A operands: h (forward scale) and the gathered x rows
+  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)d, (int)q.E, w.w_rT, s1)) return rc;
+  lsurge::WgradChunks chunks;
+  if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, s1)) return rc;
+  if (int rc = lsurge::fp8_cast_rows(sv.h, P, f, sv.num_blocks, BLK, sv.row_src, 1, false, sv.f8_scale + 1, -1, false,
+                                     nullptr, f8.hqT, P, f8.sinv + 2, nullptr, s1))
+    return rc;
+  if (int rc = lsurge::fp8_cast_rows(p->x, P, d, sv.num_blocks, BLK, sv.row_src, (int)q.k, true, sv.f8_scale, -1, false,
+                                     nullptr, f8.xqT, P, f8.sinv + 3, nullptr, s1))
+    return rc;
+
+  // s0: the shared expert's backward over its T rows (its own dY cast; g, u, h where the forward left them)
+  if (fs) {
+    const bf16_t* sg = q.merged ? sv.g + P * f : sv.sg;
+    const bf16_t* su = q.merged ? sv.u + P * f : sv.su;
+    const bf16_t* sh = q.merged ? sv.h + P * f : sv.sh;
+    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, T, 256};
+    const int64_t T64 = f8.T64;
+    const int nb = lsurge::fp8_amax_rows(dy, T, d, nullptr, 1, nullptr, 1, false, f8.part_side, s0, f8.slots + 1, 1);
+    if (nb < 0) return nb;
+    if (int rc = lsurge::fp8_cast_rows(dy, T, d, nullptr, 1, nullptr, 1, false, f8.part_side, nb, true, f8.sdyq,
+                                       f8.sdyqT, T64, f8.sinv + 4, nullptr, s0))
+      return rc;
+    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_DOWN_DGRAD, dense, f8.sdyq, d, f8.sinv + 4, w8.qbs_down, nullptr, d, 0,
+                                      w8.s_shared + 2, nullptr, d, fs, f8.sdgu, 2 * fs, false, lsurge::F8_SWIGLU_BWD,
+                                      (void*)sg, (void*)su, f8.slots + 1, s0, lsurge::RowGather(), 0, true))
+      return rc;
+    if (int rc = lsurge::fp8_cast_rows(f8.sdgu, T, 2 * fs, nullptr, 1, nullptr, 1, false, (const float*)(f8.slots + 1),
+                                       0, true, f8.sdguq, f8.sdguqT, T64, f8.sinv + 5, nullptr, s0))
+      return rc;
+    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_GU_DGRAD, dense, f8.sdguq, 2 * fs, f8.sinv + 5, w8.qbs_gate, w8.qbs_up,
+                                      fs, 0, w8.s_shared, w8.s_shared + 1, 2 * fs, d, f8.sdx, d, false,
+                                      lsurge::F8_STORE, nullptr, nullptr, nullptr, s0, lsurge::RowGather(), fs, true))
+      return rc;
+    if (int rc = lsurge::fp8_cast_rows(sh, T, fs, nullptr, 1, nullptr, 1, false, sv.f8_scale + 2, -1, false, nullptr,
+                                       f8.shqT, T64, f8.sinv + 6, nullptr, s0))
+      return rc;
+    if (int rc = lsurge::gemm_wgrad_f8_dense(KID_SHARED_DOWN_WGRAD, T, f8.shqT, T64, f8.sinv + 6, f8.sdyqT, T64,
+                                             f8.sinv + 4, fs, d, g->dws_down, nullptr, 0, d, dense_splits(T, fs, d),
+                                             f8.part_s, f8.part_s_bytes, s0))
+      return rc;
+    if (int rc = lsurge::fp8_cast_rows(p->x, T, d, nullptr, 1, nullptr, 1, false, sv.f8_scale, -1, false, nullptr,
+                                       f8.sxqT, T64, f8.sinv + 7, nullptr, s0))
+      return rc;
+    if (int rc = lsurge::gemm_wgrad_f8_dense(KID_SHARED_GU_WGRAD, T, f8.sxqT, T64, f8.sinv + 7, f8.sdguqT, T64,
+                                             f8.sinv + 5, d, 2 * fs, g->dws_gate, g->dws_up, fs, fs,
+                                             dense_splits(T, d, 2 * fs), f8.part_s, f8.part_s_bytes, s0))
+      return rc;
+  }
+
+  // main: combine backward (dY rows scaled by the routing weight, d(weights), d(logits) and their dense rows)
+  if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, P, sv.slot, sv.weights, T, (int)q.k, d, dy, w.dy_pad, dweights,
+                                              w.dl, st, nullptr, sv.sel, w.dlog, (int)q.E))
+    return rc;
+  // main: dY -> E5M2 row-wise and transposed (the amax kernel also clears the [dG | dU] amax slot)
+  {
+    const int nb = lsurge::fp8_amax_rows(w.dy_pad, P, d, sv.num_blocks, BLK, sv.row_src, 1, false, f8.part_main, st,
+                                         f8.slots, 1);
+    if (nb < 0) return nb;
+    if (int rc = lsurge::fp8_cast_rows(w.dy_pad, P, d, sv.num_blocks, BLK, sv.row_src, 1, false, f8.part_main, nb, true,
+                                       f8.dyq, f8.dyqT, P, f8.sinv, nullptr, st))
+      return rc;
+  }
+  if (s1 != st) {
+    if (hipEventRecord(ev[2], st) != hipSuccess || hipStreamWaitEvent(s1, ev[2], 0) != hipSuccess ||
+        hipStreamWaitEvent(s0, ev[2], 0) != hipSuccess)
+      return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_bwd_fp8: fork events failed");
+  }
+  // s1: down wgrad dW_down[e] = h_e^T dY_e;  s0: router wgrad dW_r = x^T dlogits (bf16)
+  if (int rc = lsurge::gemm_wgrad_f8_chunked(KID_GEMM_DOWN_WGRAD, chunks, (int)q.E, f8.hqT, P, f8.sinv + 2, f8.dyqT, P,
+                                             f8.sinv, f, d, g->dw_down, nullptr, 0, d, f * d, w.part_dn, w.part_dn_bytes,
+                                             s1))
+    return rc;
+  {
+    const int S = dense_splits(T, d, q.E);
+    if (int rc = lsurge::gemm_wgrad(KID_ROUTER_WGRAD, 1, nullptr, 1, nullptr, T, T, p->x, d, w.dlog, q.E, d, q.E,
+                                    g->dw_r, nullptr, 0, q.E, 0, S, w.part_r, w.part_r_bytes, s0))
+      return rc;
+  }
+  // main: down dgrad + SwiGLU backward, dH = dY W_down^T -> [dG | dU] (bf16) and its amax
+  if (int rc = lsurge::gemm_rows_f8(KID_GEMM_DOWN_DGRAD, blocks8, f8.dyq, d, f8.sinv, w8.qb_down, nullptr, d, f * d,
+                                    w8.s_down, nullptr, d, f, w.dgu, 2 * f, false, lsurge::F8_SWIGLU_BWD, sv.g, sv.u,
+                                    f8.slots, st, lsurge::RowGather(), 0, true))
+    return rc;
+  if (int rc = lsurge::fp8_cast_rows(w.dgu, P, 2 * f, sv.num_blocks, BLK, sv.row_src, 1, false,
+                                     (const float*)f8.slots, 0, true, f8.dguq, f8.dguqT, P, f8.sinv + 1, nullptr, st))
+    return rc;
+  // main: gate/up dgrad dX_pad = dG W_gate^T + dU W_up^T (each weight at its own scale)
+  if (int rc = lsurge::gemm_rows_f8(KID_GEMM_GU_DGRAD, blocks8, f8.dguq, 2 * f, f8.sinv + 1, w8.qb_gate, w8.qb_up, f,
+                                    d * f, w8.s_gate, w8.s_up, 2 * f, d, w.dx_pad, d, false, lsurge::F8_STORE, nullptr,
+                                    nullptr, nullptr, st, lsurge::RowGather(), f, true))
+    return rc;
+  // join (s1 after s0, the caller's stream after s1), then the dispatch backward and the gate/up wgrad
+  if (int rc = lsurge::stream_after(s1, s0, ev[4])) return rc;
+  if (int rc = fg.joined(lsurge::stream_after(st, s1, ev[5]))) return rc;
+  if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, d, (int)q.k, sv.slot, T, w.dl, sv.sel, w.w_rT,
+                                              fs ? f8.sdx : nullptr, g->dx, st))
+    return rc;
+  return lsurge::gemm_wgrad_f8_chunked(KID_GEMM_GU_WGRAD, chunks, (int)q.E, f8.xqT, P, f8.sinv + 3, f8.dguqT, P,
+                                       f8.sinv + 1, d, 2 * f, g->dw_gate, g->dw_up, f, f, d * f, w.part_gu,
+                                       w.part_gu_bytes, st);
 }
 
 }  // extern "C"

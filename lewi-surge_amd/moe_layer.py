@@ -113,7 +113,7 @@ class MoELayer:
 
     def forward_fp8(self, p: dict, out=None):
         """forward() with the expert GEMMs in FP8 on the weights of the last quantize_weights_fp8(); the saved
-        activations have the same layout, so backward() (bf16) runs after it."""
+        activations have the same layout, so backward() (bf16) or backward_fp8() runs after it."""
         s = self.shape
         _check_params(s, p)
         if getattr(self, "wq", None) is None:
@@ -153,6 +153,29 @@ class MoELayer:
         L.check(L.lib().lsurge_moe_bwd(ctypes.byref(self._cs), ctypes.byref(ps), L.ptr(dy), L.ptr(self.saved),
                                        ctypes.byref(gs), L.ptr(self._bwd_ws), self._bwd_ws.numel(),
                                        L.stream(self.device)), "moe_bwd")
+        return grads
+
+    def backward_fp8(self, p: dict, dy, grads=None):
+        """backward() with the expert GEMMs in FP8 (E5M2 gradients x the E4M3 weights / activations of the forward),
+        after forward_fp8() on the same weights; same gradient buffers and dtypes as backward()."""
+        s = self.shape
+        _check_params(s, p)
+        if getattr(self, "wq", None) is None:
+            raise RuntimeError("moe_layer: call quantize_weights_fp8() and forward_fp8() before backward_fp8()")
+        if tuple(dy.shape) != (s.t, s.d) or dy.dtype != torch.bfloat16 or not dy.is_contiguous():
+            raise ValueError("moe_layer: dy must be a contiguous bf16 [t, d] tensor")
+        if grads is None:
+            if self.grads is None:
+                self.grads = self.alloc_grads()
+            grads = self.grads
+        lib = L.lib()
+        if getattr(self, "_bwd8_ws", None) is None:
+            self._bwd8_ws = L.workspace(lib.lsurge_moe_bwd_fp8_workspace_bytes(ctypes.byref(self._cs)), self.device)
+        gs = L.MoeGrads(*[None if grads.get(n) is None else grads[n].data_ptr() for n in GRAD_NAMES])
+        ps = _params_struct(p)
+        L.check(lib.lsurge_moe_bwd_fp8(ctypes.byref(self._cs), ctypes.byref(ps), L.ptr(self.wq), self.wq.numel(),
+                                       L.ptr(dy), L.ptr(self.saved), ctypes.byref(gs), L.ptr(self._bwd8_ws),
+                                       self._bwd8_ws.numel(), L.stream(self.device)), "moe_bwd_fp8")
         return grads
 
     # -- views of the saved routing data / activations (device tensors) ----------------------------------------

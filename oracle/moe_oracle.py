@@ -527,9 +527,12 @@ def router_wgrad(p, sel, dweights, dtype=np.float32):
 #   multiplies the GEMM's f32 accumulator back.
 # e4m3 is the OCP FP8 E4M3 format ("fn": bias 7, 3 mantissa bits, no infinities, 0x7F / 0xFF NaN, largest 448),
 # rounded to nearest even and saturated at +-448.  Weights take one scale per expert and matrix; activations one
-# per tensor.
+# per tensor.  The backward casts gradients to OCP E5M2 (bias 15, 2 mantissa bits, 0x7C infinity, largest 57344),
+# the same way with 57344 in place of 448 and the scale rounded down to a power of two (the recipe's hybrid format:
+# E4M3 forward, E5M2 backward; TE's power-of-two scale option).
 
 E4M3_MAX = 448.0
+E5M2_MAX = 57344.0
 
 
 def _e4m3_table():
@@ -561,20 +564,57 @@ def e4m3_bits(a):
     return code | np.where(np.signbit(a), np.uint8(0x80), np.uint8(0))
 
 
-def fp8_scale(amax):
-    """(scale, scale_inv) of current scaling for a float32 amax."""
+def _e5m2_table():
+    c = np.arange(128)
+    ex, mt = c >> 2, c & 3
+    v = np.where(ex == 0, mt * 2.0 ** -16, (1.0 + mt / 4.0) * np.exp2(ex - 15.0))
+    v[124] = np.inf
+    v[125:] = np.nan
+    return v
+
+
+E5M2_VALUES = _e5m2_table()  # value of codes 0x00..0x7F (sign clear), ascending up to 0x7C (infinity)
+
+
+def e5m2_decode(q):
+    """E5M2 bit patterns (uint8) -> float64 values."""
+    q = np.asarray(q, np.uint8)
+    mag = E5M2_VALUES[q & 0x7F]
+    return np.where(q & 0x80, -mag, mag)
+
+
+def e5m2_bits(a):
+    """float32 -> E5M2 bit pattern (uint8): round to nearest even, saturate at +-57344, sign kept (-0 -> 0x80)."""
+    a = np.asarray(a, np.float32)
+    m = np.minimum(np.abs(a).astype(np.float64), E5M2_MAX)
+    _, ex = np.frexp(m)  # m in [2^(ex-1), 2^ex)
+    quantum = np.ldexp(1.0, np.maximum(ex - 3, -16))  # 2 mantissa bits; subnormal spacing 2^-16
+    r = np.rint(m / quantum) * quantum  # exact: power-of-two division, ties to even
+    code = np.searchsorted(E5M2_VALUES[:124], r).astype(np.uint8)
+    return code | np.where(np.signbit(a), np.uint8(0x80), np.uint8(0))
+
+
+FP8_FORMATS = {"e4m3": (E4M3_MAX, e4m3_bits, e4m3_decode), "e5m2": (E5M2_MAX, e5m2_bits, e5m2_decode)}
+
+
+def fp8_scale(amax, fmt="e4m3"):
+    """(scale, scale_inv) of current scaling for a float32 amax; E5M2 (gradient) scales are rounded down to a power of
+    two (Transformer Engine's power-of-two option: a one-ulp change of a gradient's amax then moves the grid only
+    when it crosses a binade)."""
     amax = np.float32(amax)
     if not amax > 0:
         return np.float32(1.0), np.float32(1.0)
     with np.errstate(over="ignore"):
-        scale = np.float32(E4M3_MAX) / amax
+        scale = np.float32(FP8_FORMATS[fmt][0]) / amax
     if not np.isfinite(scale):
         scale = np.float32(np.finfo(np.float32).max)
+    if fmt == "e5m2":
+        scale = np.float32(np.ldexp(1.0, int(np.frexp(scale)[1]) - 1))
     return scale, np.float32(1.0) / scale
 
 
-def fp8_quantize(x, groups=1, transpose=False):
-    """Current-scaling quantisation of `groups` equal [R, C] groups of bf16 values.
+def fp8_quantize(x, groups=1, transpose=False, fmt="e4m3"):
+    """Current-scaling quantisation of `groups` equal [R, C] groups of bf16 values to fmt ("e4m3" / "e5m2").
 
     Returns (q uint8 [groups, R, C], or [groups, C, R] with transpose; scale_inv float32 [groups]).
     """
@@ -582,19 +622,20 @@ def fp8_quantize(x, groups=1, transpose=False):
     x = x.reshape(groups, -1, x.shape[-1])
     q = np.empty(x.shape, np.uint8)
     sinv = np.empty(groups, np.float32)
+    enc = FP8_FORMATS[fmt][1]
     for g in range(groups):
-        scale, sinv[g] = fp8_scale(np.abs(x[g]).max() if x[g].size else 0.0)
-        q[g] = e4m3_bits(x[g] * scale)
+        scale, sinv[g] = fp8_scale(np.abs(x[g]).max() if x[g].size else 0.0, fmt)
+        q[g] = enc(x[g] * scale)
     if transpose:
         q = np.ascontiguousarray(q.transpose(0, 2, 1))
     return q, sinv
 
 
-def fp8_dequant(q, sinv):
+def fp8_dequant(q, sinv, fmt="e4m3"):
     """[G, ...] codes times their group's scale_inv, float64."""
     q = np.asarray(q)
     s = np.asarray(sinv, np.float64).reshape((-1,) + (1,) * (q.ndim - 1))
-    return e4m3_decode(q) * s
+    return FP8_FORMATS[fmt][2](q) * s
 
 
 def fp8_ragged_dot(lhs_q, lhs_sinv, rhs_q, rhs_sinv, group_sizes):
@@ -660,13 +701,103 @@ def moe_layer_fwd_fp8(p, route=None, dtype=np.float64):
     shared = None
     if p.get("ws_gate") is not None:
         sg_, su_, sd_ = (deq(n, 1)[0] for n in ("ws_gate", "ws_up", "ws_down"))
-        shb = round_bf16(silu(xd @ sg_) * (xd @ su_))
+        sgv, suv = xd @ sg_, xd @ su_
+        shb = round_bf16(silu(sgv) * suv)
         sq, ss = fp8_quantize(shb)
         out = out + fp8_dequant(sq, ss)[0].astype(dtype) @ sd_
-        shared = dict(h=shb)
+        shared = dict(h=shb, g=sgv, u=suv, h_sinv=ss[0])
     cache = dict(logits=logits, sel=sel, w=w, lay=lay, g=gg, u=uu, h=hb, y=ys, shared=shared, x_sinv=sx[0],
                  h_sinv=shv[0])
     return out, cache
+
+
+def _swiglu_bwd_rows(dh, g, u):
+    """(dG, dU) of h = silu(g) * u for dH, each rounded to bf16 (the GPU's SwiGLU backward epilogue)."""
+    sg = 1.0 / (1.0 + np.exp(-g))
+    return round_bf16(dh * u * sg * (1.0 + g * (1.0 - sg))), round_bf16(dh * g * sg)
+
+
+def moe_layer_bwd_fp8(p, cache, dy, dtype=np.float64, quantize=True):
+    """Backward of `moe_layer_fwd_fp8` with every expert GEMM on FP8 operands: the training half of the recipe.
+
+    Gradients are quantised to E5M2 with current scaling just before their GEMMs: the routed dY rows (bf16
+    w[t,j] dy[t], all routed rows one tensor) and [dG | dU] (bf16, all routed rows), the shared expert's dY (= dy)
+    and [dG | dU] on their own.  dgrads multiply them with the weights' E4M3 values of the forward (one scale per
+    expert and matrix, gate and up each their own); wgrads multiply the E4M3 values of the forward's x and h (same
+    scales) with the E5M2 gradients.  g and u enter the SwiGLU backward as the bf16 values the forward saved, the
+    expert dX rows are rounded to bf16 before the gather-reduce.  Routing-weight, router and dispatch backward are
+    those of `moe_layer_bwd` (y rows in bf16).  Returns the dict of `moe_layer_bwd`.
+    quantize=False skips every FP8 cast (the operands stay bf16 / exact) and keeps the bf16 roundings: the same data
+    flow, for pinning it against `moe_layer_bwd`.
+    """
+    k = p["k"]
+    x = np.asarray(p["x"], np.float32)
+    T, d = x.shape
+    E = p["w_gate"].shape[0]
+    lay, w, sel = cache["lay"], cache["w"], cache["sel"]
+    order, pos, gs = lay["order"], lay["pos"], lay["group_sizes"]
+
+    def q4(a, groups=1):  # E4M3 and back, one scale per group
+        a = np.asarray(a, np.float32)
+        if not quantize:
+            return a.astype(dtype).reshape((groups,) + a.shape[-2:])
+        q, sc = fp8_quantize(a, groups=groups)
+        return fp8_dequant(q, sc).astype(dtype)
+
+    def q5(a):  # one tensor to E5M2 and back
+        if not quantize:
+            return np.asarray(a, dtype)
+        q, sc = fp8_quantize(a, fmt="e5m2")
+        return fp8_dequant(q, sc, fmt="e5m2")[0].astype(dtype)
+
+    def deq(name, groups):
+        return q4(p[name], groups)
+
+    xd = q4(x)[0]
+
+    wg, wu, wd = deq("w_gate", E), deq("w_up", E), deq("w_down", E)
+    f = wg.shape[2]
+    xs = xd[order // k]
+    gb, ub = round_bf16(cache["g"]), round_bf16(cache["u"])
+    hd = q4(cache["h"])[0]
+    wf = np.asarray(w, np.float32).reshape(-1)
+    dys = q5(round_bf16(np.asarray(dy, np.float32)[order // k] * wf[order][:, None]))
+    dh = np.zeros((xs.shape[0], f), dtype)
+    start = 0
+    for e in range(E):
+        n = int(gs[e])
+        dh[start:start + n] = dys[start:start + n] @ wd[e].T
+        start += n
+    dgu = q5(np.concatenate(_swiglu_bwd_rows(dh, gb, ub), axis=1))
+    dxs = np.zeros((xs.shape[0], d), dtype)
+    dwg, dwu, dwd = np.zeros_like(wg), np.zeros_like(wu), np.zeros_like(wd)
+    start = 0
+    for e in range(E):
+        n = int(gs[e])
+        sl = slice(start, start + n)
+        dxs[sl] = dgu[sl, :f] @ wg[e].T + dgu[sl, f:] @ wu[e].T
+        dwg[e], dwu[e], dwd[e] = xs[sl].T @ dgu[sl, :f], xs[sl].T @ dgu[sl, f:], hd[sl].T @ dys[sl]
+        start += n
+    dx = round_bf16(dxs)[pos].reshape(T, k, d).sum(axis=1)
+    dyf = np.asarray(dy, dtype)
+    dw = np.einsum("tkd,td->tk", round_bf16(cache["y"])[pos].reshape(T, k, d), dyf)
+    w64 = np.asarray(w, dtype)
+    dl_sel = w64 * (dw - (w64 * dw).sum(axis=1, keepdims=True))
+    dlogits = np.zeros((T, E), dtype)
+    np.put_along_axis(dlogits, sel.astype(np.int64), dl_sel, axis=1)
+    x64 = x.astype(dtype)
+    dx = dx + dlogits @ np.asarray(p["w_r"], dtype).T
+    out = dict(dx=dx, dw_r=x64.T @ dlogits, dw_gate=dwg, dw_up=dwu, dw_down=dwd, dw=dw, dlogits=dlogits)
+    if cache["shared"] is not None:
+        sh = cache["shared"]
+        sgw, suw, sdw = (deq(n, 1)[0] for n in ("ws_gate", "ws_up", "ws_down"))
+        fs = sgw.shape[1]
+        sdy = q5(np.asarray(dy, np.float32))
+        sdgu = q5(np.concatenate(_swiglu_bwd_rows(sdy @ sdw.T, round_bf16(sh["g"]), round_bf16(sh["u"])), axis=1))
+        shd = q4(sh["h"])[0]
+        out["dx"] = out["dx"] + round_bf16(sdgu[:, :fs] @ sgw.T + sdgu[:, fs:] @ suw.T)
+        out["dws_gate"], out["dws_up"], out["dws_down"] = xd.T @ sdgu[:, :fs], xd.T @ sdgu[:, fs:], shd.T @ sdy
+    return out
 
 
 # --------------------------------------------------------------------------------------------- causal depthwise conv

@@ -20,7 +20,7 @@ def declared():
 
 def test_library_built_and_loads():
     assert os.path.exists(L.LIB_PATH), "run __graft_entry__.build() first"
-    assert L.lib().lsurge_abi_version() == 2
+    assert L.lib().lsurge_abi_version() == 3
 
 
 def test_every_declared_symbol_is_exported_and_bound():
@@ -59,3 +59,25 @@ def test_sizes():
     assert lib.lsurge_moe_bwd_workspace_bytes(ctypes.byref(s)) > 0
     bad = L.MoeShape(16, 100, 64, 6, 512, 512)  # d not a multiple of 64
     assert lib.lsurge_moe_saved_bytes(ctypes.byref(bad)) == 0
+
+
+def test_fp8_backward_argument_errors_without_gpu():
+    lib = L.lib()
+    s = L.MoeShape(512, 128, 8, 2, 64, 0)
+    fake = ctypes.c_void_p(256)
+    p = L.MoeParams(x=fake, w_r=fake)
+    g = L.MoeGrads(dx=fake, dw_r=fake, dw_gate=fake, dw_up=fake, dw_down=fake)
+    need_w = lib.lsurge_moe_fp8_weights_bytes(ctypes.byref(s))
+    assert need_w >= 3 * 8 * 64 * 128 * 2  # forward and backward copies of every expert matrix
+    need_ws = lib.lsurge_moe_bwd_fp8_workspace_bytes(ctypes.byref(s))
+    assert need_ws > lib.lsurge_moe_bwd_workspace_bytes(ctypes.byref(s))
+    rc = lib.lsurge_moe_bwd_fp8(ctypes.byref(s), ctypes.byref(p), fake, need_w - 1, fake, fake, ctypes.byref(g), fake,
+                                need_ws, None)
+    assert rc != 0 and b"weight buffer" in lib.lsurge_last_error()
+    rc = lib.lsurge_moe_bwd_fp8(ctypes.byref(s), ctypes.byref(p), fake, need_w, fake, fake, ctypes.byref(g), fake,
+                                need_ws - 1, None)
+    assert rc != 0 and b"workspace" in lib.lsurge_last_error()
+    rc = lib.lsurge_fp8_cast_transpose(fake, 64, 24, 1, fake, None, 64, fake, fake, 1 << 20, None)
+    assert rc != 0 and b"multiple of 16" in lib.lsurge_last_error()
+    rc = lib.lsurge_fp8_cast_transpose(fake, 64, 32, 2, fake, None, 64, fake, fake, 1 << 20, None)
+    assert rc != 0 and b"format" in lib.lsurge_last_error()

@@ -118,3 +118,105 @@ def test_fp8_layer_equals_bf16_layer_on_representable_operands():
         _, c8 = mo.moe_layer_fwd_fp8(p)
         _, c16 = mo.moe_layer_fwd(p)
     assert np.array_equal(c8["g"], c16["g"]) and np.array_equal(c8["u"], c16["u"])
+
+
+# ------------------------------------------------------------------------------------------------ E5M2 (gradients)
+
+def test_e5m2_matches_torch_on_every_bf16_value():
+    f = mo.bf16_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    a = f[np.isfinite(f) & (np.abs(f) <= mo.E5M2_MAX)]
+    want = torch.from_numpy(a).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    assert np.array_equal(mo.e5m2_bits(a), want)
+
+
+def test_e5m2_matches_torch_on_random_f32():
+    r = np.random.default_rng(7).standard_normal(1 << 18).astype(np.float32)
+    for scale in (1e-5, 1.0, 300.0, 40000.0):
+        a = np.clip(r * np.float32(scale), -mo.E5M2_MAX, mo.E5M2_MAX).astype(np.float32)
+        want = torch.from_numpy(a).to(torch.float8_e5m2).view(torch.uint8).numpy()
+        assert np.array_equal(mo.e5m2_bits(a), want)
+
+
+def test_e5m2_decode_every_code():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e5m2).float().numpy()
+    got = mo.e5m2_decode(codes)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok], want[ok])
+
+
+def test_e5m2_closed_forms():
+    cases = [(57344.0, 0x7B), (-57344.0, 0xFB), (1e9, 0x7B), (61440.0, 0x7B), (1.0, 0x3C), (1.25, 0x3D),
+             (1.125, 0x3C), (1.375, 0x3E), (2.0 ** -14, 0x04), (2.0 ** -16, 0x01), (2.0 ** -17, 0x00),
+             (3 * 2.0 ** -17, 0x02), (0.0, 0x00), (-0.0, 0x80), (28.0, 0x4F), (24.0, 0x4E)]
+    for v, code in cases:
+        assert int(mo.e5m2_bits(np.float32(v))) == code, (v, hex(int(mo.e5m2_bits(np.float32(v)))), hex(code))
+    codes = np.array([c for c in range(256) if c & 0x7F < 0x7C], np.uint8)  # every finite code round-trips
+    assert np.array_equal(mo.e5m2_bits(mo.e5m2_decode(codes).astype(np.float32)), codes)
+
+
+def test_quantize_e5m2_scale():
+    rng = np.random.default_rng(8)
+    x = mo.round_bf16(rng.standard_normal((64, 96)).astype(np.float32) * 5.0)
+    q, sinv = mo.fp8_quantize(x, fmt="e5m2")
+    amax = np.abs(x).max()
+    # power-of-two scale: the largest one that keeps amax within 57344, so amax lands in (28672, 57344]
+    assert np.frexp(sinv[0])[0] == 0.5 and mo.E5M2_MAX / 2 < amax / sinv[0] <= mo.E5M2_MAX
+    assert mo.fp8_scale(57344.0, "e5m2") == (np.float32(1.0), np.float32(1.0))
+    assert mo.fp8_scale(57343.0, "e5m2")[0] == np.float32(1.0)
+    assert mo.fp8_scale(28672.0, "e5m2")[0] == np.float32(2.0)
+    assert mo.fp8_scale(1.0, "e5m2")[0] == np.float32(32768.0)  # 57344 = 1.75 * 2^15
+    d = mo.fp8_dequant(q, sinv, fmt="e5m2")[0]
+    assert np.all(np.abs(d - x) <= np.abs(x) * 2.0 ** -3 + 2.0 ** -16 * sinv[0])  # half a step of 2 mantissa bits
+
+
+# ------------------------------------------------------------------------------------------------ FP8 backward
+
+def _bwd_pair(seed=0, fs=64):
+    p = mo.make_inputs(T=256, d=128, E=8, k=2, f=64, fs=fs, seed=seed)
+    dy = p["dy"]
+    _, c16 = mo.moe_layer_fwd(p)
+    g16 = mo.moe_layer_bwd(p, c16, dy)
+    # the bf16 forward's cache in the FP8 backward's format (y and h as the bf16 values a GPU saves)
+    ca = dict(c16, y=c16["ys"], h=mo.round_bf16(c16["h"]))
+    if fs:
+        sg, su, sh = c16["shared"]
+        ca["shared"] = dict(g=sg, u=su, h=mo.round_bf16(sh))
+    return p, dy, g16, ca
+
+
+NAMES = ("dx", "dw_r", "dw_gate", "dw_up", "dw_down", "dw", "dws_gate", "dws_up", "dws_down")
+
+
+def test_fp8_backward_dataflow_is_the_bf16_backward():
+    """With every FP8 cast switched off the FP8 backward is the bf16 backward up to the bf16 roundings it keeps (g,
+    u, dY rows, dG, dU, expert dX rows, y): a mis-wired operand (a swapped gate/up, a missing transpose, a wrong
+    expert slice) would be off by O(1)."""
+    p, dy, g16, ca = _bwd_pair()
+    gn = mo.moe_layer_bwd_fp8(p, ca, dy, quantize=False)
+    for n in NAMES:
+        assert mo.rel_l2(gn[n], g16[n]) < 1e-2, (n, mo.rel_l2(gn[n], g16[n]))
+
+
+def test_fp8_backward_planted_mistake_is_caught(monkeypatch):
+    """The check above fails when the oracle's SwiGLU backward swaps dG and dU."""
+    p, dy, g16, ca = _bwd_pair(seed=1)
+    real = mo._swiglu_bwd_rows
+    monkeypatch.setattr(mo, "_swiglu_bwd_rows", lambda dh, g, u: real(dh, g, u)[::-1])
+    gn = mo.moe_layer_bwd_fp8(p, ca, dy, quantize=False)
+    assert mo.rel_l2(gn["dw_gate"], g16["dw_gate"]) > 0.3
+    assert mo.rel_l2(gn["dx"], g16["dx"]) > 0.1
+
+
+def test_fp8_backward_close_to_bf16_backward():
+    """Quantised (E5M2 gradients, E4M3 weights and activations): a few percent from the bf16 backward, never exact,
+    never far (a dropped or inverted scale is off by orders of magnitude)."""
+    p = mo.make_inputs(T=256, d=128, E=8, k=2, f=64, fs=64, seed=2)
+    _, c16 = mo.moe_layer_fwd(p)
+    g16 = mo.moe_layer_bwd(p, c16, p["dy"])
+    _, c8 = mo.moe_layer_fwd_fp8(p)
+    g8 = mo.moe_layer_bwd_fp8(p, c8, p["dy"])
+    for n in NAMES:
+        err = mo.rel_l2(g8[n], g16[n])
+        assert 1e-2 < err < 0.2, (n, err)
