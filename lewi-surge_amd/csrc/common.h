@@ -50,11 +50,40 @@ template <> struct Elem<LSURGE_F16> {
   static __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = f32_to_f16(v); }
 };
 
+// ------------------------------------------------------------------------------------ FP8 gradients (E5M2)
+// Gradients of the FP8 backward are OCP E5M2 with a power-of-two current scale: scale = the largest power of two
+// not above 57344 / amax (1 when amax is 0).  A gradient's amax is one element of a GEMM's output, and a one-ulp
+// change of it would otherwise move the whole tensor's quantisation grid; a power-of-two scale moves only when the
+// amax crosses a binade, and it dequantises exactly.
+__device__ __forceinline__ float e5m2_scale(float amax) {
+  if (!(amax > 0.f)) return 1.f;
+  float s = __fdiv_rn(57344.f, amax);
+  if (!(s <= 3.4028234663852886e38f)) s = 3.4028234663852886e38f;
+  int e;
+  (void)frexpf(s, &e);  // s = m 2^e, m in [0.5, 1)
+  return ldexpf(1.f, e - 1);
+}
+// four floats (already scaled) -> four E5M2 bytes (nearest even, saturated at +-57344), element 0 in the low byte
+__device__ __forceinline__ uint32_t e5m2x4(float a, float b, float c, float d) {
+  a = fminf(fmaxf(a, -57344.f), 57344.f);
+  b = fminf(fmaxf(b, -57344.f), 57344.f);
+  c = fminf(fmaxf(c, -57344.f), 57344.f);
+  d = fminf(fmaxf(d, -57344.f), 57344.f);
+  int w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
 // ------------------------------------------------------------------------------------ wave helpers
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
 

@@ -32,11 +32,13 @@ __device__ __forceinline__ float block_max(float v, float* sh) {
   return m;
 }
 
-// scale of a group from its amax partials (every thread gets it)
+// scale of a group from its amax partials (every thread gets it); E5: the power-of-two E5M2 scale of gradients
+template <bool E5 = false>
 __device__ __forceinline__ float group_scale(const float* partial, int nparts, float* sh) {
   float m = 0.f;
   for (int i = threadIdx.x; i < nparts; i += blockDim.x) m = fmaxf(m, partial[i]);
   const float amax = block_max(m, sh);
+  if constexpr (E5) return e5m2_scale(amax);
   if (!(amax > 0.f)) return 1.f;
   const float s = __fdiv_rn(448.f, amax);
   return s <= FLT_MAX ? s : FLT_MAX;
@@ -55,6 +57,13 @@ __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// four scaled floats -> E4M3, or E5M2 (gradients: common.h) with E5
+template <bool E5>
+__device__ __forceinline__ uint32_t f8x4(float a, float b, float c, float d) {
+  if constexpr (E5) return e5m2x4(a, b, c, d);
+  else return e4m3x4(a, b, c, d);
+}
 
 // amax partials: grid (nb, G); block b of group g reads the 8-element chunks b AU QT + u QT + tid (u < AU), then
 // + nb AU QT, ... of the group's n elements (n % 8 == 0), AU loads in flight per thread, and writes
@@ -82,7 +91,8 @@ __global__ __launch_bounds__(QT) void fp8_amax_kernel(const bf16_t* __restrict__
 // cast of group blockIdx.y: 16 elements per thread and step, grid-stride over the group's n elements (n % 16 == 0;
 // with nrows set, only the first nrows[0] * row_elems).  Block (0, g) writes sinv[g] (and scale_out[g] when set:
 // the backward casts the same tensor again with it); block (0, 0) zeroes zero[0 .. nzero) (slots a later kernel
-// fills by atomic max).
+// fills by atomic max).  E5: E5M2 codes with the power-of-two scale (gradients).
+template <bool E5 = false>
 __global__ __launch_bounds__(QT) void fp8_cast_kernel(const bf16_t* __restrict__ x, int64_t n, int64_t gstride,
                                                       const float* __restrict__ partial, int nparts,
                                                       uint8_t* __restrict__ q, float* __restrict__ sinv,
@@ -91,7 +101,7 @@ __global__ __launch_bounds__(QT) void fp8_cast_kernel(const bf16_t* __restrict__
                                                       float* __restrict__ scale_out) {
   __shared__ float sh[QT / 64];
   const int g = blockIdx.y;
-  const float scale = group_scale(partial + (int64_t)g * nparts, nparts, sh);
+  const float scale = group_scale<E5>(partial + (int64_t)g * nparts, nparts, sh);
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     sinv[g] = __fdiv_rn(1.f, scale);
     if (scale_out) scale_out[g] = scale;
@@ -106,10 +116,10 @@ __global__ __launch_bounds__(QT) void fp8_cast_kernel(const bf16_t* __restrict__
     u32x4 o;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      o[i] = e4m3x4(bf_lo(v0[2 * i]) * scale, bf_hi(v0[2 * i]) * scale, bf_lo(v0[2 * i + 1]) * scale,
-                    bf_hi(v0[2 * i + 1]) * scale);
-      o[i + 2] = e4m3x4(bf_lo(v1[2 * i]) * scale, bf_hi(v1[2 * i]) * scale, bf_lo(v1[2 * i + 1]) * scale,
-                        bf_hi(v1[2 * i + 1]) * scale);
+      o[i] = f8x4<E5>(bf_lo(v0[2 * i]) * scale, bf_hi(v0[2 * i]) * scale, bf_lo(v0[2 * i + 1]) * scale,
+                      bf_hi(v0[2 * i + 1]) * scale);
+      o[i + 2] = f8x4<E5>(bf_lo(v1[2 * i]) * scale, bf_hi(v1[2 * i]) * scale, bf_lo(v1[2 * i + 1]) * scale,
+                          bf_hi(v1[2 * i + 1]) * scale);
     }
     *reinterpret_cast<u32x4*>(qg + 16 * c) = o;
   }
@@ -169,20 +179,6 @@ __global__ __launch_bounds__(QT) void fp8_cast_t_kernel(const bf16_t* __restrict
 // Padding rows hold no data there, so these kernels read row r only when r < nrows[0] nmul (the real blocks) and
 // row_src[r] >= 0 (zeros otherwise), and they take the format as a template argument: E4M3 for activations (largest 448), E5M2 for
 // gradients (largest 57344), the hybrid format of Transformer Engine's FP8 training.
-template <bool E5>
-__device__ __forceinline__ uint32_t f8x4(float a, float b, float c, float d) {
-  if constexpr (E5) {
-    a = fminf(fmaxf(a, -57344.f), 57344.f);
-    b = fminf(fmaxf(b, -57344.f), 57344.f);
-    c = fminf(fmaxf(c, -57344.f), 57344.f);
-    d = fminf(fmaxf(d, -57344.f), 57344.f);
-    int w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
-    w = __builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true);
-    return (uint32_t)w;
-  } else {
-    return e4m3x4(a, b, c, d);
-  }
-}
 
 // amax partials of the valid rows of a [rows, cols] bf16 matrix (cols % 8 == 0): row r is read from x row
 // row_src[r] / kdiv when gathered, else row r itself; grid-strided 8-element chunks, one partial per block.  Block 0
@@ -227,15 +223,10 @@ __device__ __forceinline__ float cast_scale(const float* src, int nparts, float*
   } else {
     amax = src[0];
   }
+  if constexpr (E5) return e5m2_scale(amax);
   if (!(amax > 0.f)) return 1.f;
-  float s = __fdiv_rn(E5 ? 57344.f : 448.f, amax);
-  s = s <= FLT_MAX ? s : FLT_MAX;
-  if constexpr (E5) {
-    int e;
-    (void)frexpf(s, &e);  // s = m 2^e, m in [0.5, 1)
-    s = ldexpf(1.f, e - 1);
-  }
-  return s;
+  const float s = __fdiv_rn(448.f, amax);
+  return s <= FLT_MAX ? s : FLT_MAX;
 }
 
 // Cast of the valid rows of a [rows, cols] bf16 matrix (row r read from x row row_src[r] / kdiv when gathered) into
@@ -339,7 +330,7 @@ int fp8_quantize_impl(const void* x, int64_t groups, int64_t rows, int64_t cols,
   } else {
     const unsigned grid = (unsigned)std::min<int64_t>((n / 16 + QT - 1) / QT, 2048);
     LSURGE_LAUNCH(KID_FP8_QUANT, s,
-                  hipLaunchKernelGGL(fp8_cast_kernel, dim3(grid, (unsigned)groups), dim3(QT), 0, s, (const bf16_t*)x, n, n,
+                  hipLaunchKernelGGL(fp8_cast_kernel<false>, dim3(grid, (unsigned)groups), dim3(QT), 0, s, (const bf16_t*)x, n, n,
                                      (const float*)partial, nb, (uint8_t*)q, sinv, (const int32_t*)nullptr, (int64_t)0,
                                      zero, nzero, scale_out));
   }
@@ -352,7 +343,7 @@ int fp8_cast_with_amax(const void* x, int64_t n, const uint32_t* amax_bits, void
   LSURGE_REQUIRE(((uintptr_t)x | (uintptr_t)q) % 16 == 0, "fp8_cast: x and q must be 16-byte aligned");
   const unsigned grid = (unsigned)std::min<int64_t>((n / 16 + QT - 1) / QT, 2048);
   LSURGE_LAUNCH(KID_FP8_QUANT, s,
-                hipLaunchKernelGGL(fp8_cast_kernel, dim3(grid, 1), dim3(QT), 0, s, (const bf16_t*)x, n, n,
+                hipLaunchKernelGGL(fp8_cast_kernel<false>, dim3(grid, 1), dim3(QT), 0, s, (const bf16_t*)x, n, n,
                                    (const float*)amax_bits, 1, (uint8_t*)q, sinv, nrows, row_elems, (uint32_t*)nullptr, 0,
                                    scale_out));
   return LSURGE_OK;
@@ -393,6 +384,26 @@ int fp8_cast_rows(const void* x, int64_t rows, int64_t cols, const int32_t* nrow
 }
 
 size_t fp8_rows_partial_bytes() { return sizeof(float) * MAX_PARTS; }
+
+int fp8_amax(const void* x, int64_t n, float* partial, hipStream_t s) {
+  LSURGE_REQUIRE(n >= 8 && n % 8 == 0 && (uintptr_t)x % 16 == 0, "fp8_amax: n=%lld", (long long)n);
+  const int nb = amax_parts(n);
+  LSURGE_LAUNCH(KID_FP8_QUANT, s,
+                hipLaunchKernelGGL(fp8_amax_kernel, dim3(nb, 1), dim3(QT), 0, s, (const bf16_t*)x, n, n, nb, partial));
+  return nb;
+}
+
+int fp8_cast_e5m2(const void* x, int64_t n, const float* amax, int nparts, void* q, float* sinv, const int32_t* nrows,
+                  int64_t row_elems, hipStream_t s, uint32_t* zero, int nzero) {
+  LSURGE_REQUIRE(n >= 16 && n % 16 == 0 && nparts >= 1 && nzero >= 0 && nzero <= QT,
+                 "fp8_cast_e5m2: n=%lld must be a positive multiple of 16", (long long)n);
+  LSURGE_REQUIRE(((uintptr_t)x | (uintptr_t)q) % 16 == 0, "fp8_cast_e5m2: x and q must be 16-byte aligned");
+  const unsigned grid = (unsigned)std::min<int64_t>((n / 16 + QT - 1) / QT, 4096);
+  LSURGE_LAUNCH(KID_FP8_QUANT, s,
+                hipLaunchKernelGGL(fp8_cast_kernel<true>, dim3(grid, 1), dim3(QT), 0, s, (const bf16_t*)x, n, n, amax,
+                                   nparts, (uint8_t*)q, sinv, nrows, row_elems, zero, nzero, (float*)nullptr));
+  return LSURGE_OK;
+}
 
 }  // namespace lsurge
 

@@ -547,27 +547,32 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
 }
 
 static int check_wgrad_f8(const void* A, int64_t lda, const float* a_sinv, const void* B, int64_t ldb,
-                          const float* b_sinv, int64_t I, int64_t N, float* C, const char* what) {
+                          const float* b_sinv, int64_t I, int64_t N, float* C, int64_t max_rows, const char* what) {
   LSURGE_REQUIRE(A && B && a_sinv && b_sinv && C, "%s: null pointer", what);
-  LSURGE_REQUIRE(I > 0 && N > 0 && I % 8 == 0 && N % 8 == 0 && lda % 16 == 0 && ldb % 16 == 0,
-                 "%s: I=%lld N=%lld (multiples of 8), lda=%lld ldb=%lld (multiples of 16)", what, (long long)I,
-                 (long long)N, (long long)lda, (long long)ldb);
+  LSURGE_REQUIRE(I > 0 && N > 0 && I % 16 == 0 && N % 16 == 0 && lda % 16 == 0 && ldb % 16 == 0 && lda >= I &&
+                     ldb >= N,
+                 "%s: I=%lld N=%lld (multiples of 16), lda=%lld ldb=%lld (multiples of 16, >= I / N)", what,
+                 (long long)I, (long long)N, (long long)lda, (long long)ldb);
   LSURGE_REQUIRE(((uintptr_t)A | (uintptr_t)B) % 16 == 0, "%s: operands must be 16-byte aligned", what);
-  if (int rc = check_desc(I * lda, what)) return rc;
-  return check_desc(N * ldb, what);
+  return check_desc(max_rows * std::max(lda, ldb), what);
 }
 
-int gemm_wgrad_f8_chunked(int kid, const WgradChunks& ch, int E, const void* A, int64_t lda, const float* a_sinv,
-                          const void* B, int64_t ldb, const float* b_sinv, int64_t I, int64_t N, float* C, float* C2,
-                          int64_t n_split, int64_t ldc, int64_t c_estride, void* part, size_t part_bytes,
-                          hipStream_t s) {
-  if (int rc = check_wgrad_f8(A, lda, a_sinv, B, ldb, b_sinv, I, N, C, "gemm_wgrad_f8_chunked")) return rc;
+int gemm_wgrad_f8_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, const void* A, int64_t lda,
+                          const float* a_sinv, const void* B, int64_t ldb, const float* b_sinv, int64_t I, int64_t N,
+                          float* C, float* C2, int64_t n_split, int64_t ldc, int64_t c_estride, void* part,
+                          size_t part_bytes, hipStream_t s, const RowGather& gather) {
+  if (int rc = check_wgrad_f8(A, lda, a_sinv, B, ldb, b_sinv, I, N, C, max_rows, "gemm_wgrad_f8_chunked")) return rc;
   LSURGE_REQUIRE(E >= 1 && ch.max_chunks >= 1, "gemm_wgrad_f8_chunked: bad E / chunk table");
   LSURGE_REQUIRE(part && part_bytes >= sizeof(float) * (size_t)ch.max_parts * I * N,
                  "gemm_wgrad_f8_chunked: partial workspace %zu < %zu bytes", part_bytes,
                  sizeof(float) * (size_t)ch.max_parts * I * N);
   LSURGE_REQUIRE(!C2 || n_split % 4 == 0, "gemm_wgrad_f8_chunked: n_split must be a multiple of 4");
+  if (gather.rows) {
+    LSURGE_REQUIRE(gather.div >= 1 && gather.nrows >= 1, "gemm_wgrad_f8_chunked: bad row gather");
+    if (int rc = check_desc(gather.nrows * lda, "gemm_wgrad_f8_chunked gather")) return rc;
+  }
   WgradArgs a{};
+  a.a_rows = gather.rows; a.a_nrows = gather.nrows; a.a_div = gather.div;
   a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.I = I; a.N = N; a.C = C; a.C2 = C2;
   a.n_split = n_split; a.ldc = ldc; a.c_estride = c_estride;
   a.E = E; a.S = 1; a.part = (float*)part;
@@ -589,9 +594,8 @@ int gemm_wgrad_f8_chunked(int kid, const WgradChunks& ch, int E, const void* A, 
 int gemm_wgrad_f8_dense(int kid, int64_t rows, const void* A, int64_t lda, const float* a_sinv, const void* B,
                         int64_t ldb, const float* b_sinv, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
                         int64_t ldc, int S, void* ws, size_t ws_bytes, hipStream_t s) {
-  if (int rc = check_wgrad_f8(A, lda, a_sinv, B, ldb, b_sinv, I, N, C, "gemm_wgrad_f8_dense")) return rc;
-  LSURGE_REQUIRE(rows >= 1 && rows <= lda && rows <= ldb && S >= 1, "gemm_wgrad_f8_dense: rows=%lld, S=%d",
-                 (long long)rows, S);
+  if (int rc = check_wgrad_f8(A, lda, a_sinv, B, ldb, b_sinv, I, N, C, rows, "gemm_wgrad_f8_dense")) return rc;
+  LSURGE_REQUIRE(rows >= 1 && S >= 1, "gemm_wgrad_f8_dense: rows=%lld, S=%d", (long long)rows, S);
   WgradArgs a{};
   a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.I = I; a.N = N; a.C = C; a.C2 = C2;
   a.n_split = n_split; a.ldc = ldc; a.c_estride = 0; a.dense_rows = rows; a.E = 1; a.S = S;

@@ -30,8 +30,8 @@
 // the dequantisation factors (per-tensor for A, per expert for B and B2) before the usual epilogues.  With a k split
 // (B up to k_split, B2 after it: the gate/up dgrad) the two weights keep scales of their own: at the first B2 stage
 // the accumulators are multiplied by b_sinv / b2_sinv, and the epilogue by a_sinv b2_sinv.
-// gemm_wgrad_f8 is the FP8 weight gradient: both operands are the transposed (K-contiguous over the padded rows)
-// copies that the backward's casts write, so it runs the FP8 row kernel's operand path over a chunk's K range.
+// gemm_wgrad_f8_kernel is the FP8 weight gradient: it stages the row-major FP8 tensors N-major like the bf16 weight
+// gradient and reads K-contiguous fragments with the 8-bit LDS transpose read.
 #pragma once
 #include <type_traits>
 
@@ -983,22 +983,50 @@ void gemm_wgrad_kernel(WgradArgs a) {
 }
 
 // =====================================================================================================
-// FP8 weight gradient C_e[I, N] = (A'_e B'_e^T) a_sinv b_sinv.  A' [I, lda] and B' [N, ldb] are the transposed copies
-// the backward's casts write (activations in format FA, gradients in FB), K-contiguous over the padded rows, so a
-// chunk's reduction over rows [c_row0, c_row0 + c_rows) is a K range of both, read with gemm_rows_kernel's FP8
-// operand path (K-major LDS tiles, one 64-value MFMA step per stage).  Chunk table, tile order, partial slots and
-// output routing as in gemm_wgrad_kernel; dense (no table): the dense_rows reduction split S ways on 64-value
-// boundaries.  Values past a chunk's end within its 16-byte copy granule are padding rows (zero in the casts), or
-// the next chunk of the same expert, whose boundaries are multiples of 64.
+// FP8 weight gradient C_e[I, N] = (A_e^T B_e) a_sinv b_sinv over the rows of expert e, from the row-major FP8
+// tensors themselves (activations A in format FA: E4M3 x or h; gradients B in FB: E5M2 dY or [dG | dU]; one byte per
+// value, pitches in bytes).  As in gemm_wgrad_kernel both operands are staged N-major -- a stage is SK = 64 rows of
+// the reduction by 128-column sub-tiles -- and the MFMA fragments come out of LDS already K-contiguous through the
+// gfx950 8-bit transpose read, so no transposed copy of any operand is ever written.  Chunk table, row gather of A
+// (the token rows of x through row_src), split partials and output routing are those of gemm_wgrad_kernel.
+//
+// LDS sub-tile: 64 rows x 128 bytes; 16-byte chunk c of row k sits at slot c ^ (2 ((k >> 1) & 3)).  A copy fills 8
+// rows (lane p: row p / 8, slot p % 8).  A fragment read (below) takes, per 32-lane half of the wave, 8 rows x 2
+// adjacent chunks; the 4 even rows' chunks land on distinct slots of banks 0-31 and the odd rows' on 32-63, so the
+// 256 bytes of each pass hit all 64 banks once.
+constexpr int SK8 = 64;  // reduction rows per FP8 stage (one 32x32x64 MFMA step)
+__device__ __forceinline__ int nm8_off(int k, int n) {
+  return k * NS + ((((n >> 4) ^ (((k >> 1) & 3) << 1))) << 4) + (n & 15);
+}
+// ds_read_b64_tr_b8 in a 16-lane group: source lane s points at 8 bytes (row kb + s / 2, columns nb + 8 (s % 2) ..
+// + 7 of an N-major tile); lane i receives column nb + i, rows kb .. kb + 7, row j in byte j.  Fragment for the
+// 32x32x64 operand layout: lane l (column nbase + l % 32, half h = l / 32) gets rows 32 h .. 32 h + 31 of its column,
+// byte b = row 32 h + b, in four reads.
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ i32x8 frag_n8(const uint8_t* sub, int nbase, int lane) {
+  const int g = lane >> 4, s = lane & 15, h = lane >> 5;
+  const int n = nbase + 16 * (g & 1) + 8 * (s & 1);
+  i32x8 f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int k = 32 * h + 8 * q + (s >> 1);
+    const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(i32x2, sub + nm8_off(k, n)));
+    f[2 * q] = v[0];
+    f[2 * q + 1] = v[1];
+  }
+  return f;
+}
+
 template <class Cfg, int FA, int FB>
 __global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW * Cfg::OCC / 4)))
 void gemm_wgrad_f8_kernel(WgradArgs a) {
-  static_assert(Cfg::BK == 32 && !Cfg::PP, "FP8 weight gradient: 64-value stages, 4-wave single-buffered loop");
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, ST = Cfg::ST;
-  constexpr int TM = Cfg::TM, FM = Cfg::FM, FN = Cfg::FN;
+  static_assert(Cfg::BK == 32 && !Cfg::PP, "FP8 weight gradient: 64-row stages, 4-wave single-buffered loop");
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, ST = Cfg::ST;
+  constexpr int TM = Cfg::TM, TN = Cfg::TN, FM = Cfg::FM, FN = Cfg::FN;
   constexpr int CPA = Cfg::CPA, CPB = Cfg::CPB;
-  constexpr int RPC = 1024 / (2 * BK), CPR = BK / 8;  // rows per copy, 16-byte chunks per row and stage
-  constexpr int SB = 2 * BK;                          // values (bytes) per stage
+  constexpr int SUB = SK8 * NS;      // bytes per sub-tile (8 KiB)
+  constexpr int CPS = SUB / 1024;    // copies per sub-tile
+  static_assert(CPA * Cfg::NW * 1024 == (BM / NS) * SUB && CPB * Cfg::NW * 1024 == (BN / NS) * SUB, "stage bytes");
   __shared__ __attribute__((aligned(1024))) bf16_t smem[Cfg::SMEM_EL];
   constexpr uint32_t A_SLOT = Cfg::A_EL * 2, B_SLOT = Cfg::B_EL * 2, B_RING = ST * A_SLOT;  // bytes
   const int64_t tiles_per_e = (int64_t)(a.c_expert ? 1 : a.S) * a.i_tiles * a.n_tiles;
@@ -1031,44 +1059,88 @@ void gemm_wgrad_f8_kernel(WgradArgs a) {
     r0 = 0;
     nrows = a.dense_rows;
   }
-  const int64_t chunk = ((nrows + S - 1) / S + SB - 1) / SB * SB;
+  const int64_t chunk = ((nrows + S - 1) / S + SK8 - 1) / SK8 * SK8;
   const int64_t rs = (int64_t)s * chunk, re = min(nrows, rs + chunk);
-  const int K = re > rs ? (int)(re - rs) : 0;  // reduction length (values = bytes)
-  const int nk = (K + SB - 1) / SB;
+  const int span = re > rs ? (int)(re - rs) : 0;
+  const int nk = (span + SK8 - 1) / SK8;
   const int64_t i0 = (int64_t)it * BM, n0 = (int64_t)nt * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const uint32_t lds0 = lds_addr(smem);
-  const int64_t kb = r0 + rs;  // first reduction column of both operands
-  const u32x4 rsA = make_rsrc(reinterpret_cast<const uint8_t*>(a.A) + kb, a.I * a.lda - kb);
-  const u32x4 rsB = make_rsrc(reinterpret_cast<const uint8_t*>(a.B) + kb, a.N * a.ldb - kb);
-  // K-major copies as in gemm_rows_kernel: copy q covers tile rows RPC q .. RPC q + RPC - 1, lane -> row
-  // RPC q + lane / CPR, slot lane % CPR holding chunk slot ^ swz(row); byte offset at k = 0 and the chunk's k
+  const uint8_t* A8 = reinterpret_cast<const uint8_t*>(a.A);
+  const uint8_t* B8 = reinterpret_cast<const uint8_t*>(a.B);
+  const bool gath = a.a_rows != nullptr;
+  const u32x4 rsA = gath ? make_rsrc(A8, a.a_nrows * a.lda) : make_rsrc(A8 + (r0 + rs) * a.lda, (int64_t)span * a.lda);
+  const u32x4 rsB = make_rsrc(B8 + (r0 + rs) * a.ldb, (int64_t)span * a.ldb);
+  // gathered A: the row indices pass through a double-buffered LDS window of 2 x 256 entries, as in
+  // gemm_wgrad_kernel (SPW stages per window)
+  constexpr int SPW = 256 / SK8;
+  __shared__ __attribute__((aligned(1024))) int32_t idxwin[512];
+  const uint32_t win0 = lds_addr(reinterpret_cast<const bf16_t*>(idxwin));
+  const u32x4 rsI = make_rsrc(gath ? a.a_rows + r0 + rs : nullptr, gath ? (int64_t)span * 4 : 0);
+  const uint64_t magic = div_magic(gath ? a.a_div : 1);
+  int nidx[CPA];
+  if (gath) {
+    if (wave == 0) {
+      copy16(rsI, 16u * lane, win0);
+      copy16(rsI, 1024u + 16u * lane, win0 + 1024);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  // copy q of an operand fills rows 8 (q % CPS) + lane / 8 of sub-tile q / CPS, slot lane % 8: byte offset of this
+  // lane's chunk at row 0 of the span and its row in a stage (KBIG when its columns are outside the operand)
   uint32_t a_off[CPA], b_off[CPB];
   int a_k[CPA], b_k[CPB];
 #pragma unroll
   for (int c = 0; c < CPA; ++c) {
-    const int r = RPC * (CPA * wave + c) + lane / CPR;
-    const int kc = (lane % CPR) ^ km_swz<BK>(r);
-    a_off[c] = (uint32_t)((i0 + r) * a.lda + 16 * kc);
-    a_k[c] = i0 + r < a.I ? 16 * kc : KBIG;
+    const int q = CPA * wave + c, sub = q / CPS;
+    const int k = 8 * (q % CPS) + (lane >> 3);
+    const int64_t ic = i0 + NS * sub + 16 * ((lane & 7) ^ (((k >> 1) & 3) << 1));
+    a_off[c] = gath ? (uint32_t)ic : (uint32_t)(k * a.lda + ic);  // gathered: the row part comes later
+    a_k[c] = ic < a.I ? k : KBIG;
   }
 #pragma unroll
   for (int c = 0; c < CPB; ++c) {
-    const int n = RPC * (CPB * wave + c) + lane / CPR;
-    const int kc = (lane % CPR) ^ km_swz<BK>(n);
-    b_off[c] = (uint32_t)((n0 + n) * a.ldb + 16 * kc);
-    b_k[c] = n0 + n < a.N ? 16 * kc : KBIG;
+    const int q = CPB * wave + c, sub = q / CPS;
+    const int k = 8 * (q % CPS) + (lane >> 3);
+    const int64_t nc = n0 + NS * sub + 16 * ((lane & 7) ^ (((k >> 1) & 3) << 1));
+    b_off[c] = (uint32_t)(k * a.ldb + nc);
+    b_k[c] = nc < a.N ? k : KBIG;
   }
+#pragma unroll
+  for (int c = 0; c < CPA; ++c) nidx[c] = gath ? idxwin[a_k[c] & 511] : 0;  // stage 0
+  const uint32_t lda = (uint32_t)a.lda, ldb = (uint32_t)a.ldb;
   auto issue = [&](int slot, int kt) {
-    const int k0 = kt * SB;
+    const int rb = kt * SK8;
     const uint32_t at = lds0 + slot * A_SLOT, bt = lds0 + B_RING + slot * B_SLOT;
+    if (gath) {
+      if (kt % SPW == 0 && kt >= SPW && wave == 0) {
+        const int m = kt / SPW + 1;
+        copy16(rsI, 1024u * m + 16u * lane, win0 + 1024u * (m & 1));
+      }
 #pragma unroll
-    for (int c = 0; c < CPA; ++c)
-      copy16(rsA, k0 + a_k[c] < K ? a_off[c] + (uint32_t)k0 : OOB, at + 1024 * (CPA * wave + c));
+      for (int c = 0; c < CPA; ++c) {
+        const int q = CPA * wave + c;
+        const int idx = nidx[c];
+        const bool ok = rb + a_k[c] < span && idx >= 0;
+        copy16(rsA, ok ? (uint32_t)div_by(idx, magic) * lda + a_off[c] : OOB, at + (q / CPS) * SUB + 1024 * (q % CPS));
+      }
 #pragma unroll
-    for (int c = 0; c < CPB; ++c)
-      copy16(rsB, k0 + b_k[c] < K ? b_off[c] + (uint32_t)k0 : OOB, bt + 1024 * (CPB * wave + c));
+      for (int c = 0; c < CPA; ++c) nidx[c] = idxwin[(rb + SK8 + a_k[c]) & 511];
+    } else {
+#pragma unroll
+      for (int c = 0; c < CPA; ++c) {
+        const int q = CPA * wave + c;
+        copy16(rsA, rb + a_k[c] < span ? a_off[c] + (uint32_t)rb * lda : OOB,
+               at + (q / CPS) * SUB + 1024 * (q % CPS));
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CPB; ++c) {
+      const int q = CPB * wave + c;
+      copy16(rsB, rb + b_k[c] < span ? b_off[c] + (uint32_t)rb * ldb : OOB, bt + (q / CPS) * SUB + 1024 * (q % CPS));
+    }
   };
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -1077,12 +1149,18 @@ void gemm_wgrad_f8_kernel(WgradArgs a) {
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
   typedef FragSet<FM, FN, i32x8> F;
   auto load = [&](int slot, int, F& f) {
-    const bf16_t* at = smem + slot * Cfg::A_EL;
-    const bf16_t* bt = smem + ST * Cfg::A_EL + slot * Cfg::B_EL;
+    const uint8_t* at = reinterpret_cast<const uint8_t*>(smem) + slot * A_SLOT;
+    const uint8_t* bt = reinterpret_cast<const uint8_t*>(smem) + B_RING + slot * B_SLOT;
 #pragma unroll
-    for (int i = 0; i < FM; ++i) f.x[i] = frag_k8(at, wm * TM + 32 * i + (lane & 31), lane >> 5);
+    for (int i = 0; i < FM; ++i) {
+      const int col = wm * TM + 32 * i;
+      f.x[i] = frag_n8(at + (col / NS) * SUB, col % NS, lane);
+    }
 #pragma unroll
-    for (int j = 0; j < FN; ++j) f.w[j] = frag_k8(bt, wn * Cfg::TN + 32 * j + (lane & 31), lane >> 5);
+    for (int j = 0; j < FN; ++j) {
+      const int col = wn * TN + 32 * j;
+      f.w[j] = frag_n8(bt + (col / NS) * SUB, col % NS, lane);
+    }
   };
   auto mma = [&](const F& f) {
 #pragma unroll
@@ -1091,7 +1169,7 @@ void gemm_wgrad_f8_kernel(WgradArgs a) {
       for (int j = 0; j < FN; ++j) acc[i][j] = mfma32_f8<FB, FA>(f.w[j], f.x[i], acc[i][j]);
   };
   if (nk > 0) {  // waves outside the tile: copies and barriers only
-    if (i0 + wm * TM < a.I && n0 + wn * Cfg::TN < a.N) run_k_loop<Cfg, F, 1, true>(nk, wave, issue, load, mma);
+    if (i0 + wm * TM < a.I && n0 + wn * TN < a.N) run_k_loop<Cfg, F, 1, true>(nk, wave, issue, load, mma);
     else run_k_loop<Cfg, F, 1, true>(nk, wave, issue, [](int, int, F&) {}, [](const F&) {});
   }
   const float sab = a.a_sinv[0] * a.b_sinv[0];

@@ -46,10 +46,25 @@ int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src,
                         int64_t max_rows, void* xp, hipStream_t s);
 int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, const float* w, int64_t n,
                        const void* add, void* out, int out_dtype, hipStream_t s);
-// dlog (optional, needs sel and dl): also the dense bf16 d(logits) [n, E] of the router's weight gradient
+// dlog (optional, needs sel and dl): also the dense bf16 d(logits) [n, E] of the router's weight gradient.
+// FP8 backward (dyq set): the dY rows as E5M2 codes (power-of-two scale from the launch_dy_rows_amax partials,
+// scale_inv to sinv[0]) in dyq [rows, d]; the rows of real blocks (nblocks[0] of 128) are written, dyp is scratch.
+struct CombineFp8 {
+  void* dyq = nullptr;
+  const float* amax_part = nullptr;
+  int nparts = 0;
+  float* sinv = nullptr;
+  const int32_t* nblocks = nullptr;
+};
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
                            int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s,
-                           void* gcopy = nullptr, const int32_t* sel = nullptr, void* dlog = nullptr, int E = 0);
+                           void* gcopy = nullptr, const int32_t* sel = nullptr, void* dlog = nullptr, int E = 0,
+                           const CombineFp8& f8 = CombineFp8());
+// amax partials of the dY rows w[t, j] g[t] (bf16-rounded) from g [n, d] and w [n, k] alone; returns their count
+// (at most dy_rows_amax_parts(); negative: an error code).  Its first workgroup also clears zero[0 .. nzero).
+int dy_rows_amax_parts();
+int launch_dy_rows_amax(const void* g, const float* w, int64_t n, int64_t d, int k, float* partial, hipStream_t s,
+                        uint32_t* zero = nullptr, int nzero = 0);
 int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* slot, int64_t n, const float* dl,
                             const int32_t* sel, const void* w_rT, const void* add, void* dx, hipStream_t s);
 int launch_transpose_bf16(const void* a, int R, int C, void* at, hipStream_t s);
@@ -137,12 +152,14 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
                        int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s,
                        const RowGather& gather = RowGather(), const ExtraOut& xo = ExtraOut(), int et = LSURGE_BF16);
 
-// FP8 weight gradients (E4M3 activations x E5M2 gradients): A [I, lda] and B [N, ldb] bytes, the transposed casts,
-// K-contiguous over the rows; dequantised by a_sinv[0] b_sinv[0].  Chunked: the routed experts over a chunk table;
-// dense: one matrix over `rows` rows split S ways (f32 partials in ws, wgrad_workspace_bytes(1, I, N, S)).
-int gemm_wgrad_f8_chunked(int kid, const WgradChunks& ch, int E, const void* A, int64_t lda, const float* a_sinv,
-                          const void* B, int64_t ldb, const float* b_sinv, int64_t I, int64_t N, float* C, float* C2,
-                          int64_t n_split, int64_t ldc, int64_t c_estride, void* part, size_t part_bytes, hipStream_t s);
+// FP8 weight gradients (E4M3 activations x E5M2 gradients) from the row-major FP8 tensors: A [rows, lda] and B
+// [rows, ldb] bytes (A optionally gathered through row_src, as gemm_wgrad_chunked), C = A^T B a_sinv[0] b_sinv[0].
+// Chunked: the routed experts over a chunk table; dense: one matrix over `rows` rows split S ways (f32 partials in ws,
+// wgrad_workspace_bytes(1, I, N, S)).  I, N, lda, ldb multiples of 16.
+int gemm_wgrad_f8_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, const void* A, int64_t lda,
+                          const float* a_sinv, const void* B, int64_t ldb, const float* b_sinv, int64_t I, int64_t N,
+                          float* C, float* C2, int64_t n_split, int64_t ldc, int64_t c_estride, void* part,
+                          size_t part_bytes, hipStream_t s, const RowGather& gather = RowGather());
 int gemm_wgrad_f8_dense(int kid, int64_t rows, const void* A, int64_t lda, const float* a_sinv, const void* B,
                         int64_t ldb, const float* b_sinv, int64_t I, int64_t N, float* C, float* C2, int64_t n_split,
                         int64_t ldc, int S, void* ws, size_t ws_bytes, hipStream_t s);
@@ -164,6 +181,12 @@ int fp8_cast_with_amax(const void* x, int64_t n, const uint32_t* amax_bits, void
 // fp8_amax_rows writes one amax partial per workgroup into partial (fp8_rows_partial_bytes) and returns their count
 // (negative: an error code); its first workgroup also clears zero[0 .. nzero).
 size_t fp8_rows_partial_bytes();
+// amax partials of n bf16 values (n % 8 == 0, fp8_partial_bytes(1)); returns their count (negative: an error code)
+int fp8_amax(const void* x, int64_t n, float* partial, hipStream_t s);
+// E5M2 cast (power-of-two scale) of n bf16 values with the amax of nparts partials (or nparts = 1 and an amax slot);
+// nrows (optional): only the first nrows[0] * row_elems values
+int fp8_cast_e5m2(const void* x, int64_t n, const float* amax, int nparts, void* q, float* sinv, const int32_t* nrows,
+                  int64_t row_elems, hipStream_t s, uint32_t* zero = nullptr, int nzero = 0);
 int fp8_amax_rows(const void* x, int64_t rows, int64_t cols, const int32_t* nrows, int nmul, const int32_t* row_src,
                   int kdiv, bool gather, float* partial, hipStream_t s, uint32_t* zero = nullptr, int nzero = 0);
 // cast to E4M3 or E5M2 (e5m2) into a row-wise copy qr [rows, cols] and / or a transposed copy qt [cols, ldq]; the

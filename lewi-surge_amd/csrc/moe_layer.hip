@@ -71,7 +71,10 @@ struct Saved {
   int32_t *t_expert, *t_rows, *t_row0, *num_tiles;
   bf16_t *g, *u, *h, *y_pad;
   bf16_t *sg, *su, *sh, *sy;  // shared expert run on its own: gate, up, h, output
-  float* f8_scale;  // FP8 forward: the scales of x, routed h and shared h (the backward casts them again)
+  // FP8 forward: x [T, d], routed h [P, f] (padded rows) and shared h [T, fs] in E4M3, and their scale_inv, the
+  // operands the FP8 backward's weight gradients read again
+  uint8_t *xq, *hq, *shq;
+  float* f8_sinv;
 };
 
 size_t carve_saved(const Dims& q, void* base, Saved* sv) {
@@ -102,7 +105,10 @@ size_t carve_saved(const Dims& q, void* base, Saved* sv) {
   sv->su = c.take<bf16_t>(own * q.fs);
   sv->sh = c.take<bf16_t>(own * q.fs);
   sv->sy = c.take<bf16_t>(own * q.d);
-  sv->f8_scale = c.take<float>(4);
+  sv->xq = c.take<uint8_t>(q.T * q.d);
+  sv->hq = c.take<uint8_t>(q.P * q.f);
+  sv->shq = c.take<uint8_t>(q.T * q.fs);
+  sv->f8_sinv = c.take<float>(4);
   return c.off + 256;
 }
 
@@ -198,65 +204,45 @@ size_t carve_fp8w(const Dims& q, void* base, Fp8W* w) {
   return c.off + 256;
 }
 
-// FP8 forward scratch: x and the two h tensors in E4M3, x's amax partials, the atomic-max slots of the routed and
-// shared h, and the scale_inv of x, routed h and shared h
+// FP8 forward scratch: x's amax partials and the atomic-max slots of the routed and shared h (the E4M3 tensors and
+// their scale_inv go to the saved buffer)
 struct Fp8Ws {
-  uint8_t *xq, *hq, *shq;
   float* partial;
   uint32_t* slots;
-  float* sinv;
 };
-size_t carve_fp8ws(const Dims& q, void* base, Fp8Ws* w) {
+size_t carve_fp8ws(const Dims&, void* base, Fp8Ws* w) {
   Carve c(base);
-  w->xq = c.take<uint8_t>(q.T * q.d);
-  w->hq = c.take<uint8_t>(q.P * q.f);
-  w->shq = c.take<uint8_t>(q.fs ? q.T * q.fs : 0);
   w->partial = c.take<float>(lsurge::fp8_partial_bytes(1) / sizeof(float));
   w->slots = c.take<uint32_t>(2);
-  w->sinv = c.take<float>(4);
   return c.off;
 }
 
-// FP8 backward scratch (after the bf16 backward's BwdWs in the same workspace).  Routed, over the padded rows (P):
-// dY and [dG | dU] in E5M2 row-wise (the dgrads' A operands) and transposed (the wgrads' B operands), h and the
-// gathered x rows transposed in E4M3 with the forward's scales (the wgrads' A operands).  Shared expert, over its T
-// rows: the same set for its own GEMMs, plus its [dG | dU] and dx in bf16.  Amax partials per stream, the atomic
-// max slots of the two [dG | dU] and the scale_inv of every cast:
-//   sinv: 0 dY, 1 dGU, 2 h^T, 3 x^T (gathered), 4 shared dY, 5 shared dGU, 6 shared h^T, 7 x^T (dense)
+// FP8 backward scratch (after the bf16 backward's BwdWs in the same workspace): the E5M2 gradients, row-major --
+// routed dY and [dG | dU] over the padded rows, the shared expert's dY and [dG | dU] over its T rows -- the shared
+// expert's [dG | dU] and dx in bf16, amax partials per stream, the atomic-max slots of the two [dG | dU] and the
+// scale_inv of the four E5M2 tensors (0 dY, 1 dGU, 2 shared dY, 3 shared dGU).
 struct Fp8Bws {
-  uint8_t *dyq, *dyqT, *dguq, *dguqT, *hqT, *xqT;
-  uint8_t *sdyq, *sdyqT, *sdguq, *sdguqT, *shqT, *sxqT;
+  uint8_t *dyq, *dguq, *sdyq, *sdguq;
   bf16_t *sdgu, *sdx;
   float *part_main, *part_side;
   uint32_t* slots;
   float* sinv;
   void* part_s;  // split-K partials of the shared weight gradients
   size_t part_s_bytes;
-  int64_t T64;   // pitch of the shared expert's transposed copies
 };
 size_t carve_fp8bws(const Dims& q, void* base, Fp8Bws* w) {
   Carve c(base);
-  const int64_t P = q.P, T = q.fs ? q.T : 0;
-  w->T64 = (q.T + 63) / 64 * 64;
-  const int64_t T64 = q.fs ? w->T64 : 0;
-  w->dyq = c.take<uint8_t>(P * q.d);
-  w->dyqT = c.take<uint8_t>(q.d * P);
-  w->dguq = c.take<uint8_t>(P * 2 * q.f);
-  w->dguqT = c.take<uint8_t>(2 * q.f * P);
-  w->hqT = c.take<uint8_t>(q.f * P);
-  w->xqT = c.take<uint8_t>(q.d * P);
+  const int64_t T = q.fs ? q.T : 0;
+  w->dyq = c.take<uint8_t>(q.P * q.d);
+  w->dguq = c.take<uint8_t>(q.P * 2 * q.f);
   w->sdyq = c.take<uint8_t>(T * q.d);
-  w->sdyqT = c.take<uint8_t>(q.d * T64);
   w->sdguq = c.take<uint8_t>(T * 2 * q.fs);
-  w->sdguqT = c.take<uint8_t>(2 * q.fs * T64);
-  w->shqT = c.take<uint8_t>(q.fs * T64);
-  w->sxqT = c.take<uint8_t>(q.d * T64);
   w->sdgu = c.take<bf16_t>(T * 2 * q.fs);
   w->sdx = c.take<bf16_t>(T * q.d);
-  w->part_main = c.take<float>(lsurge::fp8_rows_partial_bytes() / sizeof(float));
-  w->part_side = c.take<float>(lsurge::fp8_rows_partial_bytes() / sizeof(float));
+  w->part_main = c.take<float>(lsurge::dy_rows_amax_parts());
+  w->part_side = c.take<float>(lsurge::fp8_partial_bytes(1) / sizeof(float));
   w->slots = c.take<uint32_t>(2);
-  w->sinv = c.take<float>(8);
+  w->sinv = c.take<float>(4);
   size_t part = 0;
   if (q.fs) {
     part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, 2 * q.fs, dense_splits(q.T, q.d, 2 * q.fs)));
@@ -446,8 +432,7 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   if (w8) {
     carve_fp8ws(q, (char*)workspace + hist_bytes, &f8);
     if (int rc = lsurge::stream_after(s0, st, fg.f.ev[3])) return rc;
-    if (int rc = lsurge::fp8_quantize_impl(p->x, 1, q.T, q.d, false, f8.xq, f8.sinv, f8.partial, s0, f8.slots, 2,
-                                           nullptr, sv.f8_scale))
+    if (int rc = lsurge::fp8_quantize_impl(p->x, 1, q.T, q.d, false, sv.xq, sv.f8_sinv, f8.partial, s0, f8.slots, 2))
       return rc;
     if (s0 != st && hipEventRecord(fg.f.ev[2], s0) != hipSuccess)
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipEventRecord failed");
@@ -470,14 +455,13 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
     return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipStreamWaitEvent failed");
   if (q.fs && w8) {
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
-    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_GU_FWD, dense, f8.xq, q.d, f8.sinv, w8->qs_gate, w8->qs_up, q.d, 0,
+    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_GU_FWD, dense, sv.xq, q.d, sv.f8_sinv, w8->qs_gate, w8->qs_up, q.d, 0,
                                       w8->s_shared, w8->s_shared + 1, q.d, q.fs, sh, q.fs, false, lsurge::F8_SWIGLU_FWD,
                                       sg, su, f8.slots + 1, s0))
       return rc;
-    if (int rc = lsurge::fp8_cast_with_amax(sh, q.T * q.fs, f8.slots + 1, f8.shq, f8.sinv + 2, nullptr, 0, s0,
-                                            sv.f8_scale + 2))
+    if (int rc = lsurge::fp8_cast_with_amax(sh, q.T * q.fs, f8.slots + 1, sv.shq, sv.f8_sinv + 2, nullptr, 0, s0))
       return rc;
-    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_DOWN_FWD, dense, f8.shq, q.fs, f8.sinv + 2, w8->qs_down, nullptr, q.fs,
+    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_DOWN_FWD, dense, sv.shq, q.fs, sv.f8_sinv + 2, w8->qs_down, nullptr, q.fs,
                                       0, w8->s_shared + 2, nullptr, q.fs, q.d, sy, q.d, false, lsurge::F8_STORE,
                                       nullptr, nullptr, nullptr, s0))
       return rc;
@@ -522,14 +506,14 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
     const lsurge::GemmBlocks blocks8{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0, 128};
     if (s0 != st && hipStreamWaitEvent(st, fg.f.ev[2], 0) != hipSuccess)
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipStreamWaitEvent failed");
-    if (int rc = lsurge::gemm_rows_f8(KID_GEMM_GU_FWD, blocks8, f8.xq, q.d, f8.sinv, w8->q_gate, w8->q_up, q.d,
+    if (int rc = lsurge::gemm_rows_f8(KID_GEMM_GU_FWD, blocks8, sv.xq, q.d, sv.f8_sinv, w8->q_gate, w8->q_up, q.d,
                                       q.f * q.d, w8->s_gate, w8->s_up, q.d, q.f, sv.h, q.f, false,
                                       lsurge::F8_SWIGLU_FWD, sv.g, sv.u, f8.slots, st, gather))
       return rc;
-    if (int rc = lsurge::fp8_cast_with_amax(sv.h, q.P * q.f, f8.slots, f8.hq, f8.sinv + 1, sv.num_blocks, BLK * q.f, st,
-                                            sv.f8_scale + 1))
+    if (int rc = lsurge::fp8_cast_with_amax(sv.h, q.P * q.f, f8.slots, sv.hq, sv.f8_sinv + 1, sv.num_blocks, BLK * q.f,
+                                            st))
       return rc;
-    if (int rc = lsurge::gemm_rows_f8(KID_GEMM_DOWN_FWD, blocks8, f8.hq, q.f, f8.sinv + 1, w8->q_down, nullptr, q.f,
+    if (int rc = lsurge::gemm_rows_f8(KID_GEMM_DOWN_FWD, blocks8, sv.hq, q.f, sv.f8_sinv + 1, w8->q_down, nullptr, q.f,
                                       q.d * q.f, w8->s_down, nullptr, q.f, q.d, sv.y_pad, q.d, false, lsurge::F8_STORE,
                                       nullptr, nullptr, nullptr, st))
       return rc;
@@ -704,14 +688,17 @@ size_t lsurge_moe_bwd_fp8_workspace_bytes(const lsurge_moe_shape* s) {
 }
 
 // FP8 backward (Transformer Engine's current-scaling training recipe, hybrid formats): gradients are cast to E5M2
-// with scales of their own (dY rows, [dG | dU], per tensor, just before use), the dgrads multiply them with the
-// weights' E4M3 codes of the forward (their untransposed copies, same scales), and the wgrads with the forward's
-// E4M3 codes of h and x (cast again, transposed, with the scales the forward saved).  Combine, dispatch and router
-// backward are those of the bf16 backward; the shared expert runs its FP8 backward as dense GEMMs of its own.
+// with power-of-two scales of their own (dY rows, [dG | dU], per tensor, just before use), the dgrads multiply them
+// with the weights' E4M3 codes of the forward (their untransposed copies, same scales), and the wgrads multiply the
+// forward's E4M3 x and h (kept in `saved`) with them.  Every FP8 operand is row-major: the weight gradients stage
+// both operands N-major and read K-contiguous fragments with the 8-bit LDS transpose read, so nothing is cast twice
+// or transposed.  The dY rows come out of the combine backward as E5M2 directly (their amax from dy and the routing
+// weights beforehand).  Combine, dispatch and router backward are those of the bf16 backward; the shared expert runs
+// its FP8 backward as dense GEMMs of its own.
 // Stream plan (caller's stream = critical path):
-//   main: combine bwd -> dY amax -> dY cast -> [record] -> down dgrad (+SwiGLU bwd, amax of [dG | dU]) -> [dG | dU]
-//         cast -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
-//   s1:   from the start: W_r transpose, chunk table, h^T and gathered x^T casts; after the record: down wgrad
+//   main: dY amax -> combine bwd (E5M2 dY rows) -> [record] -> down dgrad (+SwiGLU bwd, amax of [dG | dU]) ->
+//         [dG | dU] cast -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
+//   s1:   from the start: W_r transpose, chunk table; after the record: down wgrad
 //   s0:   from the start: the shared expert's backward; after the record: router wgrad
 int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* wq, size_t wq_bytes,
                        const void* dy, const void* saved, const lsurge_moe_grads* g, void* workspace,
@@ -747,67 +734,54 @@ int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
   if (s0 != st && hipStreamWaitEvent(s0, ev[0], 0) != hipSuccess)
     return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_bwd_fp8: hipStreamWaitEvent failed");
 
-  // s1: W_r^T, the chunk table, and the wgrads' A operands: h (forward scale) and the gathered x rows
+  // s1: W_r^T and the chunk table
   if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)d, (int)q.E, w.w_rT, s1)) return rc;
   lsurge::WgradChunks chunks;
   if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, s1)) return rc;
-  if (int rc = lsurge::fp8_cast_rows(sv.h, P, f, sv.num_blocks, BLK, sv.row_src, 1, false, sv.f8_scale + 1, -1, false,
-                                     nullptr, f8.hqT, P, f8.sinv + 2, nullptr, s1))
-    return rc;
-  if (int rc = lsurge::fp8_cast_rows(p->x, P, d, sv.num_blocks, BLK, sv.row_src, (int)q.k, true, sv.f8_scale, -1, false,
-                                     nullptr, f8.xqT, P, f8.sinv + 3, nullptr, s1))
-    return rc;
 
-  // s0: the shared expert's backward over its T rows (its own dY cast; g, u, h where the forward left them)
+  // s0: the shared expert's backward over its T rows (its own dY cast; g, u where the forward left them)
   if (fs) {
     const bf16_t* sg = q.merged ? sv.g + P * f : sv.sg;
     const bf16_t* su = q.merged ? sv.u + P * f : sv.su;
-    const bf16_t* sh = q.merged ? sv.h + P * f : sv.sh;
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, T, 256};
-    const int64_t T64 = f8.T64;
-    const int nb = lsurge::fp8_amax_rows(dy, T, d, nullptr, 1, nullptr, 1, false, f8.part_side, s0, f8.slots + 1, 1);
+    const int nb = lsurge::fp8_amax(dy, T * d, f8.part_side, s0);
     if (nb < 0) return nb;
-    if (int rc = lsurge::fp8_cast_rows(dy, T, d, nullptr, 1, nullptr, 1, false, f8.part_side, nb, true, f8.sdyq,
-                                       f8.sdyqT, T64, f8.sinv + 4, nullptr, s0))
+    if (int rc = lsurge::fp8_cast_e5m2(dy, T * d, f8.part_side, nb, f8.sdyq, f8.sinv + 2, nullptr, 0, s0, f8.slots + 1, 1))
       return rc;
-    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_DOWN_DGRAD, dense, f8.sdyq, d, f8.sinv + 4, w8.qbs_down, nullptr, d, 0,
+    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_DOWN_DGRAD, dense, f8.sdyq, d, f8.sinv + 2, w8.qbs_down, nullptr, d, 0,
                                       w8.s_shared + 2, nullptr, d, fs, f8.sdgu, 2 * fs, false, lsurge::F8_SWIGLU_BWD,
                                       (void*)sg, (void*)su, f8.slots + 1, s0, lsurge::RowGather(), 0, true))
       return rc;
-    if (int rc = lsurge::fp8_cast_rows(f8.sdgu, T, 2 * fs, nullptr, 1, nullptr, 1, false, (const float*)(f8.slots + 1),
-                                       0, true, f8.sdguq, f8.sdguqT, T64, f8.sinv + 5, nullptr, s0))
+    if (int rc = lsurge::fp8_cast_e5m2(f8.sdgu, T * 2 * fs, (const float*)(f8.slots + 1), 1, f8.sdguq, f8.sinv + 3,
+                                       nullptr, 0, s0))
       return rc;
-    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_GU_DGRAD, dense, f8.sdguq, 2 * fs, f8.sinv + 5, w8.qbs_gate, w8.qbs_up,
+    if (int rc = lsurge::gemm_rows_f8(KID_SHARED_GU_DGRAD, dense, f8.sdguq, 2 * fs, f8.sinv + 3, w8.qbs_gate, w8.qbs_up,
                                       fs, 0, w8.s_shared, w8.s_shared + 1, 2 * fs, d, f8.sdx, d, false,
                                       lsurge::F8_STORE, nullptr, nullptr, nullptr, s0, lsurge::RowGather(), fs, true))
       return rc;
-    if (int rc = lsurge::fp8_cast_rows(sh, T, fs, nullptr, 1, nullptr, 1, false, sv.f8_scale + 2, -1, false, nullptr,
-                                       f8.shqT, T64, f8.sinv + 6, nullptr, s0))
-      return rc;
-    if (int rc = lsurge::gemm_wgrad_f8_dense(KID_SHARED_DOWN_WGRAD, T, f8.shqT, T64, f8.sinv + 6, f8.sdyqT, T64,
-                                             f8.sinv + 4, fs, d, g->dws_down, nullptr, 0, d, dense_splits(T, fs, d),
+    if (int rc = lsurge::gemm_wgrad_f8_dense(KID_SHARED_DOWN_WGRAD, T, sv.shq, fs, sv.f8_sinv + 2, f8.sdyq, d,
+                                             f8.sinv + 2, fs, d, g->dws_down, nullptr, 0, d, dense_splits(T, fs, d),
                                              f8.part_s, f8.part_s_bytes, s0))
       return rc;
-    if (int rc = lsurge::fp8_cast_rows(p->x, T, d, nullptr, 1, nullptr, 1, false, sv.f8_scale, -1, false, nullptr,
-                                       f8.sxqT, T64, f8.sinv + 7, nullptr, s0))
-      return rc;
-    if (int rc = lsurge::gemm_wgrad_f8_dense(KID_SHARED_GU_WGRAD, T, f8.sxqT, T64, f8.sinv + 7, f8.sdguqT, T64,
-                                             f8.sinv + 5, d, 2 * fs, g->dws_gate, g->dws_up, fs, fs,
+    if (int rc = lsurge::gemm_wgrad_f8_dense(KID_SHARED_GU_WGRAD, T, sv.xq, d, sv.f8_sinv, f8.sdguq, 2 * fs,
+                                             f8.sinv + 3, d, 2 * fs, g->dws_gate, g->dws_up, fs, fs,
                                              dense_splits(T, d, 2 * fs), f8.part_s, f8.part_s_bytes, s0))
       return rc;
   }
 
-  // main: combine backward (dY rows scaled by the routing weight, d(weights), d(logits) and their dense rows)
-  if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, P, sv.slot, sv.weights, T, (int)q.k, d, dy, w.dy_pad, dweights,
-                                              w.dl, st, nullptr, sv.sel, w.dlog, (int)q.E))
-    return rc;
-  // main: dY -> E5M2 row-wise and transposed (the amax kernel also clears the [dG | dU] amax slot)
+  // main: amax of the dY rows (from dy and the routing weights; also clears the [dG | dU] amax slot), then the combine
+  // backward writing them as E5M2 (plus d(weights), d(logits) and their dense rows)
   {
-    const int nb = lsurge::fp8_amax_rows(w.dy_pad, P, d, sv.num_blocks, BLK, sv.row_src, 1, false, f8.part_main, st,
-                                         f8.slots, 1);
+    const int nb = lsurge::launch_dy_rows_amax(dy, sv.weights, T, d, (int)q.k, f8.part_main, st, f8.slots, 1);
     if (nb < 0) return nb;
-    if (int rc = lsurge::fp8_cast_rows(w.dy_pad, P, d, sv.num_blocks, BLK, sv.row_src, 1, false, f8.part_main, nb, true,
-                                       f8.dyq, f8.dyqT, P, f8.sinv, nullptr, st))
+    lsurge::CombineFp8 c8;
+    c8.dyq = f8.dyq;
+    c8.amax_part = f8.part_main;
+    c8.nparts = nb;
+    c8.sinv = f8.sinv;
+    c8.nblocks = sv.num_blocks;
+    if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, P, sv.slot, sv.weights, T, (int)q.k, d, dy, w.dy_pad,
+                                                dweights, w.dl, st, nullptr, sv.sel, w.dlog, (int)q.E, c8))
       return rc;
   }
   if (s1 != st) {
@@ -816,9 +790,9 @@ int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_bwd_fp8: fork events failed");
   }
   // s1: down wgrad dW_down[e] = h_e^T dY_e;  s0: router wgrad dW_r = x^T dlogits (bf16)
-  if (int rc = lsurge::gemm_wgrad_f8_chunked(KID_GEMM_DOWN_WGRAD, chunks, (int)q.E, f8.hqT, P, f8.sinv + 2, f8.dyqT, P,
-                                             f8.sinv, f, d, g->dw_down, nullptr, 0, d, f * d, w.part_dn, w.part_dn_bytes,
-                                             s1))
+  if (int rc = lsurge::gemm_wgrad_f8_chunked(KID_GEMM_DOWN_WGRAD, chunks, (int)q.E, T, sv.hq, f, sv.f8_sinv + 1,
+                                             f8.dyq, d, f8.sinv, f, d, g->dw_down, nullptr, 0, d, f * d, w.part_dn,
+                                             w.part_dn_bytes, s1))
     return rc;
   {
     const int S = dense_splits(T, d, q.E);
@@ -831,23 +805,28 @@ int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
                                     w8.s_down, nullptr, d, f, w.dgu, 2 * f, false, lsurge::F8_SWIGLU_BWD, sv.g, sv.u,
                                     f8.slots, st, lsurge::RowGather(), 0, true))
     return rc;
-  if (int rc = lsurge::fp8_cast_rows(w.dgu, P, 2 * f, sv.num_blocks, BLK, sv.row_src, 1, false,
-                                     (const float*)f8.slots, 0, true, f8.dguq, f8.dguqT, P, f8.sinv + 1, nullptr, st))
+  if (int rc = lsurge::fp8_cast_e5m2(w.dgu, P * 2 * f, (const float*)f8.slots, 1, f8.dguq, f8.sinv + 1, sv.num_blocks,
+                                     BLK * 2 * f, st))
     return rc;
   // main: gate/up dgrad dX_pad = dG W_gate^T + dU W_up^T (each weight at its own scale)
   if (int rc = lsurge::gemm_rows_f8(KID_GEMM_GU_DGRAD, blocks8, f8.dguq, 2 * f, f8.sinv + 1, w8.qb_gate, w8.qb_up, f,
                                     d * f, w8.s_gate, w8.s_up, 2 * f, d, w.dx_pad, d, false, lsurge::F8_STORE, nullptr,
                                     nullptr, nullptr, st, lsurge::RowGather(), f, true))
     return rc;
-  // join (s1 after s0, the caller's stream after s1), then the dispatch backward and the gate/up wgrad
+  // join (s1 after s0, the caller's stream after s1), then the dispatch backward and the gate/up wgrad over the
+  // E4M3 x rows gathered through row_src
   if (int rc = lsurge::stream_after(s1, s0, ev[4])) return rc;
   if (int rc = fg.joined(lsurge::stream_after(st, s1, ev[5]))) return rc;
   if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, d, (int)q.k, sv.slot, T, w.dl, sv.sel, w.w_rT,
                                               fs ? f8.sdx : nullptr, g->dx, st))
     return rc;
-  return lsurge::gemm_wgrad_f8_chunked(KID_GEMM_GU_WGRAD, chunks, (int)q.E, f8.xqT, P, f8.sinv + 3, f8.dguqT, P,
+  lsurge::RowGather gather;
+  gather.rows = sv.row_src;
+  gather.div = (int)q.k;
+  gather.nrows = T;
+  return lsurge::gemm_wgrad_f8_chunked(KID_GEMM_GU_WGRAD, chunks, (int)q.E, T, sv.xq, d, sv.f8_sinv, f8.dguq, 2 * f,
                                        f8.sinv + 1, d, 2 * f, g->dw_gate, g->dw_up, f, f, d * f, w.part_gu,
-                                       w.part_gu_bytes, st);
+                                       w.part_gu_bytes, st, gather);
 }
 
 }  // extern "C"

@@ -378,12 +378,48 @@ __global__ __launch_bounds__(PM_THREADS) void combine_pad_kernel(const bf16_t* _
   }
 }
 
+// amax of the FP8 backward's dY rows bf16(w[t,j] dy[t]) without forming them: f32 products and bf16 rounding are
+// monotonic, so max over (t, j, c) of |bf16(w[t,j] dy[t,c])| = max over t of bf16(max_j |w[t,j]| max_c |dy[t,c]|).  One
+// wave per token (grid-strided), one partial per workgroup.  d % 8 == 0.
+__global__ __launch_bounds__(PM_THREADS) void dy_rows_amax_kernel(const bf16_t* __restrict__ dy,
+                                                                  const float* __restrict__ w, int64_t n, int64_t d,
+                                                                  int k, float* __restrict__ partial,
+                                                                  uint32_t* __restrict__ zero, int nzero) {
+  __shared__ float sh[PM_WAVES];
+  const int lane = threadIdx.x & 63;
+  if (blockIdx.x == 0 && (int)threadIdx.x < nzero) zero[threadIdx.x] = 0u;  // slots a later kernel fills by atomic max
+  const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  float m = 0.f;
+  for (int64_t t = wave_id(); t < n; t += nwaves) {
+    float a = 0.f;
+    for (int64_t c = 8 * lane; c < d; c += 512) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(dy + t * d + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        a = fmaxf(a, fmaxf(fabsf(__uint_as_float(v[i] << 16)), fabsf(__uint_as_float(v[i] & 0xffff0000u))));
+    }
+    a = wave_max(a);
+    float wm = 0.f;
+    for (int j = 0; j < k; ++j) wm = fmaxf(wm, fabsf(w[t * k + j]));
+    m = fmaxf(m, bf16_to_f32(f32_to_bf16(wm * a)));
+  }
+  if (lane == 0) sh[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = sh[0];
+    for (int i = 1; i < PM_WAVES; ++i) b = fmaxf(b, sh[i]);
+    partial[blockIdx.x] = b;
+  }
+}
+
 // Fused combine backward of the layer (bf16 rows): per token, g is read once; for every choice j the expert
 // row y_pad[slot] is read once, dy_pad[slot] = bf16(w_j g) written once and <g, y> reduced; then the router
 // term dl[t,j] = w_j (dw_j - sum_i w_i dw_i).  moe_permute.py:303-309 does this in two passes over g and y.
 // gcopy (optional): g row t is also copied to gcopy[t] (the shared expert's rows of the padded dY, when the shared
 // expert rides along the routed experts).  dlog (optional, with sel): the dense bf16 row [E] of d(logits), dl[t,j] at
 // column sel[t,j] and 0 elsewhere -- the operand of the router's weight gradient.
+// FP8 backward (dyq set): the dY rows go out as E5M2 codes of bf16(w_j g) times the power-of-two scale of the amax
+// that dy_rows_amax_kernel left in nparts partials (dyp is not written); sinv[0] = 1 / scale.
 template <int NC, int KK>
 __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_t* __restrict__ yp,
                                                                      const int32_t* __restrict__ slot,
@@ -393,10 +429,20 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_
                                                                      float* __restrict__ dl,
                                                                      bf16_t* __restrict__ gcopy,
                                                                      const int32_t* __restrict__ sel,
-                                                                     bf16_t* __restrict__ dlog, int E) {
+                                                                     bf16_t* __restrict__ dlog, int E,
+                                                                     uint8_t* __restrict__ dyq,
+                                                                     const float* __restrict__ amax_part, int nparts,
+                                                                     float* __restrict__ sinv) {
   static_assert(NC > 0 && KK > 0, "fixed-shape kernel");
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
+  float scale = 1.f;
+  if (dyq) {  // wave-uniform
+    float m = 0.f;
+    for (int i = lane; i < nparts; i += 64) m = fmaxf(m, amax_part[i]);
+    scale = e5m2_scale(wave_max(m));
+    if (blockIdx.x == 0 && threadIdx.x == 0) sinv[0] = __fdiv_rn(1.f, scale);
+  }
   for (int64_t t = wave_id(); t < n; t += nwaves) {
     float gv[NC][8];
 #pragma unroll
@@ -420,7 +466,15 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_
           acc += v[e] * gv[c][e];
           o[e] = wj * gv[c][e];
         }
-        V8<LSURGE_BF16>::st(dyp + r * d + (c * 64 + lane) * 8, o);
+        if (dyq) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = bf16_to_f32(f32_to_bf16(o[e])) * scale;
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u32x2*>(dyq + r * d + (c * 64 + lane) * 8) =
+              u32x2{e5m2x4(o[0], o[1], o[2], o[3]), e5m2x4(o[4], o[5], o[6], o[7])};
+        } else {
+          V8<LSURGE_BF16>::st(dyp + r * d + (c * 64 + lane) * 8, o);
+        }
       }
       dot[j] = acc;
     }
@@ -611,20 +665,36 @@ int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, co
   return LSURGE_OK;
 }
 
+int dy_rows_amax_parts() { return 256; }
+
+int launch_dy_rows_amax(const void* g, const float* w, int64_t n, int64_t d, int k, float* partial, hipStream_t s,
+                        uint32_t* zero, int nzero) {
+  LSURGE_REQUIRE(n >= 1 && d >= 8 && d % 8 == 0 && k >= 1 && aligned16(g) && nzero >= 0 && nzero <= PM_THREADS,
+                 "dy_rows_amax: bad shape");
+  const int nb = (int)std::min<int64_t>(dy_rows_amax_parts(), (n + PM_WAVES - 1) / PM_WAVES);
+  LSURGE_LAUNCH(KID_COMBINE_BWD, s,
+                hipLaunchKernelGGL(dy_rows_amax_kernel, dim3(nb), dim3(PM_THREADS), 0, s, (const bf16_t*)g, w, n, d, k,
+                                   partial, zero, nzero));
+  return nb;
+}
+
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
                            int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s, void* gcopy,
-                           const int32_t* sel, void* dlog, int E) {
+                           const int32_t* sel, void* dlog, int E, const CombineFp8& f8) {
   const dim3 grid(grid_for_rows(n));
   const int nc = row_chunks(d);
   LSURGE_REQUIRE(!dlog || (sel && dl && E >= 1), "combine_bwd: dense d(logits) needs sel, dl and E");
   LSURGE_REQUIRE(!dl || dw, "combine_bwd: the router backward needs dw");
+  LSURGE_REQUIRE(!f8.dyq || (f8.amax_part && f8.nparts >= 1 && f8.sinv && f8.nblocks && !gcopy),
+                 "combine_bwd: the FP8 dY rows need the amax partials, scale_inv and block count");
   if (nc && (k == 6 || k == 8)) {
     LS_NC_SWITCH(nc, NC, LS_KK_SWITCH(k, KK, {
       if (NC && KK)
         LSURGE_LAUNCH(KID_COMBINE_BWD, s,
                       hipLaunchKernelGGL((combine_bwd_pad_kernel<NC ? NC : 1, KK ? KK : 1>), grid, dim3(PM_THREADS), 0,
                                          s, (const bf16_t*)yp, slot, w, n, d, (const bf16_t*)g, (bf16_t*)dyp, dw, dl,
-                                         (bf16_t*)gcopy, sel, (bf16_t*)dlog, E));
+                                         (bf16_t*)gcopy, sel, (bf16_t*)dlog, E, (uint8_t*)f8.dyq, f8.amax_part,
+                                         f8.nparts, f8.sinv));
     }));
     return LSURGE_OK;
   }
@@ -634,7 +704,13 @@ int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, co
   LSURGE_LAUNCH(KID_COMBINE_BWD, s,
                 hipLaunchKernelGGL((combine_bwd_kernel<LSURGE_BF16, LSURGE_BF16, true>), grid, dim3(PM_THREADS), 0, s,
                                    yp, rows, slot, w, n, k, d, g, dyp, dw, dl));
-  if (dlog) return launch_scatter_dlogits(dl, sel, n, E, k, dlog, s);
+  if (dlog)
+    if (int rc = launch_scatter_dlogits(dl, sel, n, E, k, dlog, s)) return rc;
+  // generic shapes, FP8: the bf16 rows are cast afterwards with the same scale (the rows of real blocks; padding rows
+  // are never read)
+  if (f8.dyq)
+    return fp8_cast_e5m2(dyp, rows * d, f8.amax_part, f8.nparts, f8.dyq, f8.sinv, f8.nblocks,
+                         (int64_t)LSURGE_BLOCK_ROWS * d, s);
   return LSURGE_OK;
 }
 
