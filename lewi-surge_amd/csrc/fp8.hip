@@ -35,6 +35,7 @@ __device__ __forceinline__ float block_max(float v, float* sh) {
 // scale of a group from its amax partials (every thread gets it); E5: the power-of-two E5M2 scale of gradients
 template <bool E5 = false>
 __device__ __forceinline__ float group_scale(const float* partial, int nparts, float* sh) {
+  if (nparts < 0) return partial[0];  // the scale itself
   float m = 0.f;
   for (int i = threadIdx.x; i < nparts; i += blockDim.x) m = fmaxf(m, partial[i]);
   const float amax = block_max(m, sh);
@@ -101,8 +102,8 @@ __global__ __launch_bounds__(QT) void fp8_cast_kernel(const bf16_t* __restrict__
                                                       float* __restrict__ scale_out) {
   __shared__ float sh[QT / 64];
   const int g = blockIdx.y;
-  const float scale = group_scale<E5>(partial + (int64_t)g * nparts, nparts, sh);
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
+  const float scale = group_scale<E5>(partial + (int64_t)g * max(nparts, 0), nparts, sh);
+  if (blockIdx.x == 0 && threadIdx.x == 0 && sinv) {
     sinv[g] = __fdiv_rn(1.f, scale);
     if (scale_out) scale_out[g] = scale;
   }
@@ -110,18 +111,31 @@ __global__ __launch_bounds__(QT) void fp8_cast_kernel(const bf16_t* __restrict__
   const int64_t ne = nrows ? min(n, (int64_t)max(nrows[0], 0) * row_elems) : n;
   const bf16_t* xg = x + (int64_t)g * gstride;
   uint8_t* qg = q + (int64_t)g * n;
-  for (int64_t c = (int64_t)blockIdx.x * QT + threadIdx.x; c < ne / 16; c += (int64_t)gridDim.x * QT) {
-    const u32x4 v0 = *reinterpret_cast<const u32x4*>(xg + 16 * c);
-    const u32x4 v1 = *reinterpret_cast<const u32x4*>(xg + 16 * c + 8);
-    u32x4 o;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      o[i] = f8x4<E5>(bf_lo(v0[2 * i]) * scale, bf_hi(v0[2 * i]) * scale, bf_lo(v0[2 * i + 1]) * scale,
-                      bf_hi(v0[2 * i + 1]) * scale);
-      o[i + 2] = f8x4<E5>(bf_lo(v1[2 * i]) * scale, bf_hi(v1[2 * i]) * scale, bf_lo(v1[2 * i + 1]) * scale,
-                          bf_hi(v1[2 * i + 1]) * scale);
+  // two 16-element chunks per thread and step (four 16-byte loads in flight)
+  const int64_t nc = ne / 16, stride = (int64_t)gridDim.x * QT;
+  for (int64_t c = (int64_t)blockIdx.x * QT + threadIdx.x; c < nc; c += 2 * stride) {
+    const bool two = c + stride < nc;
+    u32x4 v[4];
+    v[0] = *reinterpret_cast<const u32x4*>(xg + 16 * c);
+    v[1] = *reinterpret_cast<const u32x4*>(xg + 16 * c + 8);
+    if (two) {
+      v[2] = *reinterpret_cast<const u32x4*>(xg + 16 * (c + stride));
+      v[3] = *reinterpret_cast<const u32x4*>(xg + 16 * (c + stride) + 8);
     }
-    *reinterpret_cast<u32x4*>(qg + 16 * c) = o;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (h == 1 && !two) break;
+      const u32x4 v0 = v[2 * h], v1 = v[2 * h + 1];
+      u32x4 o;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        o[i] = f8x4<E5>(bf_lo(v0[2 * i]) * scale, bf_hi(v0[2 * i]) * scale, bf_lo(v0[2 * i + 1]) * scale,
+                        bf_hi(v0[2 * i + 1]) * scale);
+        o[i + 2] = f8x4<E5>(bf_lo(v1[2 * i]) * scale, bf_hi(v1[2 * i]) * scale, bf_lo(v1[2 * i + 1]) * scale,
+                            bf_hi(v1[2 * i + 1]) * scale);
+      }
+      *reinterpret_cast<u32x4*>(qg + 16 * (c + h * stride)) = o;
+    }
   }
 }
 
@@ -395,7 +409,7 @@ int fp8_amax(const void* x, int64_t n, float* partial, hipStream_t s) {
 
 int fp8_cast_e5m2(const void* x, int64_t n, const float* amax, int nparts, void* q, float* sinv, const int32_t* nrows,
                   int64_t row_elems, hipStream_t s, uint32_t* zero, int nzero) {
-  LSURGE_REQUIRE(n >= 16 && n % 16 == 0 && nparts >= 1 && nzero >= 0 && nzero <= QT,
+  LSURGE_REQUIRE(n >= 16 && n % 16 == 0 && nparts != 0 && nzero >= 0 && nzero <= QT,
                  "fp8_cast_e5m2: n=%lld must be a positive multiple of 16", (long long)n);
   LSURGE_REQUIRE(((uintptr_t)x | (uintptr_t)q) % 16 == 0, "fp8_cast_e5m2: x and q must be 16-byte aligned");
   const unsigned grid = (unsigned)std::min<int64_t>((n / 16 + QT - 1) / QT, 4096);

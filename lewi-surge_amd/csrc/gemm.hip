@@ -19,19 +19,54 @@ constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, GT = Cfg::GT;
 // (96 KiB), one workgroup per CU.  Same MFMA sequence per output element, so the results are bitwise those of Cfg.
 using CfgPP = GemmCfg<256, 256, 32, 2, 4, 3, 1, 1>;
 
-// sum of the S split partials in split order -> C (and C2 for n >= n_split)
+// sum of the S split partials in split order -> C (and C2 for n >= n_split).  V = 4: four consecutive columns per
+// thread with 16-byte loads and stores (N, n_split, ldc, c_estride multiples of 4, C and C2 16-byte aligned), and
+// the S loads of an element group issued before the adds; the same additions in the same order either way.
+template <int V>
 __global__ void splitk_reduce_kernel(const float* __restrict__ part, int S, int E, int64_t I, int64_t N,
                                      float* __restrict__ C, float* __restrict__ C2, int64_t n_split, int64_t ldc,
                                      int64_t c_estride) {
+  typedef float fv __attribute__((ext_vector_type(V)));
   const int64_t total = (int64_t)E * I * N;
-  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < total; x += (int64_t)gridDim.x * blockDim.x) {
-    float v = 0.f;
-    for (int s = 0; s < S; ++s) v += part[(int64_t)s * total + x];
+  for (int64_t x = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V; x < total;
+       x += (int64_t)gridDim.x * blockDim.x * V) {
+    fv v = *reinterpret_cast<const fv*>(part + x);
+    int s = 1;
+    for (; s + 4 <= S; s += 4) {
+      const fv a0 = *reinterpret_cast<const fv*>(part + (int64_t)s * total + x);
+      const fv a1 = *reinterpret_cast<const fv*>(part + (int64_t)(s + 1) * total + x);
+      const fv a2 = *reinterpret_cast<const fv*>(part + (int64_t)(s + 2) * total + x);
+      const fv a3 = *reinterpret_cast<const fv*>(part + (int64_t)(s + 3) * total + x);
+      v += a0;
+      v += a1;
+      v += a2;
+      v += a3;
+    }
+    for (; s < S; ++s) v += *reinterpret_cast<const fv*>(part + (int64_t)s * total + x);
     const int64_t e = x / (I * N), rem = x % (I * N);
     const int64_t row = rem / N, col = rem % N;
-    if (C2 && col >= n_split) C2[e * c_estride + row * ldc + (col - n_split)] = v;
-    else C[e * c_estride + row * ldc + col] = v;
+    float* dst = (C2 && col >= n_split) ? C2 + e * c_estride + row * ldc + (col - n_split)
+                                        : C + e * c_estride + row * ldc + col;
+    *reinterpret_cast<fv*>(dst) = v;
   }
+}
+
+static int launch_splitk_reduce(const float* part, int S, int E, int64_t I, int64_t N, float* C, float* C2,
+                                int64_t n_split, int64_t ldc, int64_t c_estride, hipStream_t s) {
+  const int64_t total = (int64_t)E * I * N;
+  const bool v4 = N % 4 == 0 && n_split % 4 == 0 && ldc % 4 == 0 && c_estride % 4 == 0 &&
+                  ((uintptr_t)C | (uintptr_t)C2 | (uintptr_t)part) % 16 == 0;
+  const int64_t items = v4 ? total / 4 : total;
+  const unsigned grid = (unsigned)std::min<int64_t>((items + 255) / 256, 8192);
+  if (v4)
+    LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
+                  hipLaunchKernelGGL(splitk_reduce_kernel<4>, dim3(grid), dim3(256), 0, s, part, S, E, I, N, C, C2,
+                                     n_split, ldc, c_estride));
+  else
+    LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
+                  hipLaunchKernelGGL(splitk_reduce_kernel<1>, dim3(grid), dim3(256), 0, s, part, S, E, I, N, C, C2,
+                                     n_split, ldc, c_estride));
+  return LSURGE_OK;
 }
 
 // Block table of an unpadded ragged layout (rows of group e start at sum_{e'<e} gs[e']), in two launches.  Group
@@ -447,13 +482,7 @@ int gemm_wgrad(int kid, int E, const int32_t* e_row0, int row0_mult, const int32
     LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_wgrad_kernel<Cfg, LSURGE_F16>), dim3(pad8(tiles)), dim3(GT), 0, s, a));
   else
     LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel<Cfg>, dim3(pad8(tiles)), dim3(GT), 0, s, a));
-  if (S > 1) {
-    const int64_t total = (int64_t)E * I * N;
-    const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-    LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
-                  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(256), 0, s, (const float*)ws, S, E, I, N, C,
-                                     C2, n_split, ldc, c_estride));
-  }
+  if (S > 1) return launch_splitk_reduce((const float*)ws, S, E, I, N, C, C2, n_split, ldc, c_estride, s);
   return LSURGE_OK;
 }
 
@@ -609,12 +638,7 @@ int gemm_wgrad_f8_dense(int kid, int64_t rows, const void* A, int64_t lda, const
   }
   const int64_t tiles = (int64_t)S * a.i_tiles * a.n_tiles;
   LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_wgrad_f8_kernel<Cfg, 0, 1>), dim3(pad8(tiles)), dim3(GT), 0, s, a));
-  if (S > 1) {
-    const unsigned grid = (unsigned)std::min<int64_t>((I * N + 255) / 256, 8192);
-    LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,
-                  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(256), 0, s, (const float*)ws, S, 1, I, N, C,
-                                     C2, n_split, ldc, (int64_t)0));
-  }
+  if (S > 1) return launch_splitk_reduce((const float*)ws, S, 1, I, N, C, C2, n_split, ldc, 0, s);
   return LSURGE_OK;
 }
 

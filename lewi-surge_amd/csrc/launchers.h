@@ -47,24 +47,23 @@ int launch_dispatch_pad(const void* x, int64_t d, int k, const int32_t* row_src,
 int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, const float* w, int64_t n,
                        const void* add, void* out, int out_dtype, hipStream_t s);
 // dlog (optional, needs sel and dl): also the dense bf16 d(logits) [n, E] of the router's weight gradient.
-// FP8 backward (dyq set): the dY rows as E5M2 codes (power-of-two scale from the launch_dy_rows_amax partials,
-// scale_inv to sinv[0]) in dyq [rows, d]; the rows of real blocks (nblocks[0] of 128) are written, dyp is scratch.
+// FP8 backward (dyq set): the dY rows as E5M2 codes with scale[0] (launch_dy_scale) in dyq [rows, d]; the rows of
+// real blocks (nblocks[0] of 128) are written, dyp is scratch.
 struct CombineFp8 {
   void* dyq = nullptr;
-  const float* amax_part = nullptr;
-  int nparts = 0;
-  float* sinv = nullptr;
+  const float* scale = nullptr;
   const int32_t* nblocks = nullptr;
 };
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
                            int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s,
                            void* gcopy = nullptr, const int32_t* sel = nullptr, void* dlog = nullptr, int E = 0,
                            const CombineFp8& f8 = CombineFp8());
-// amax partials of the dY rows w[t, j] g[t] (bf16-rounded) from g [n, d] and w [n, k] alone; returns their count
-// (at most dy_rows_amax_parts(); negative: an error code).  Its first workgroup also clears zero[0 .. nzero).
+// The E5M2 scale (power of two) of the dY rows w[t, j] g[t] (bf16-rounded) from g [n, d] and w [n, k] alone: amax
+// partials (dy_rows_amax_parts() floats at partial), then scale[0] and sinv[0] = 1 / scale; also clears
+// zero[0 .. nzero).
 int dy_rows_amax_parts();
-int launch_dy_rows_amax(const void* g, const float* w, int64_t n, int64_t d, int k, float* partial, hipStream_t s,
-                        uint32_t* zero = nullptr, int nzero = 0);
+int launch_dy_scale(const void* g, const float* w, int64_t n, int64_t d, int k, float* partial, float* scale,
+                    float* sinv, hipStream_t s, uint32_t* zero = nullptr, int nzero = 0);
 int launch_dispatch_bwd_pad(const void* dxp, int64_t d, int k, const int32_t* slot, int64_t n, const float* dl,
                             const int32_t* sel, const void* w_rT, const void* add, void* dx, hipStream_t s);
 int launch_transpose_bf16(const void* a, int R, int C, void* at, hipStream_t s);
@@ -183,8 +182,9 @@ int fp8_cast_with_amax(const void* x, int64_t n, const uint32_t* amax_bits, void
 size_t fp8_rows_partial_bytes();
 // amax partials of n bf16 values (n % 8 == 0, fp8_partial_bytes(1)); returns their count (negative: an error code)
 int fp8_amax(const void* x, int64_t n, float* partial, hipStream_t s);
-// E5M2 cast (power-of-two scale) of n bf16 values with the amax of nparts partials (or nparts = 1 and an amax slot);
-// nrows (optional): only the first nrows[0] * row_elems values
+// E5M2 cast (power-of-two scale) of n bf16 values with the amax of nparts partials (or nparts = 1 and an amax slot;
+// nparts < 0: amax[0] is the scale itself, and sinv may be null); nrows (optional): only the first
+// nrows[0] * row_elems values
 int fp8_cast_e5m2(const void* x, int64_t n, const float* amax, int nparts, void* q, float* sinv, const int32_t* nrows,
                   int64_t row_elems, hipStream_t s, uint32_t* zero = nullptr, int nzero = 0);
 int fp8_amax_rows(const void* x, int64_t rows, int64_t cols, const int32_t* nrows, int nmul, const int32_t* row_src,

@@ -227,6 +227,7 @@ struct Fp8Bws {
   float *part_main, *part_side;
   uint32_t* slots;
   float* sinv;
+  float* dy_scale;  // the scale of the routed dY rows
   void* part_s;  // split-K partials of the shared weight gradients
   size_t part_s_bytes;
 };
@@ -243,6 +244,7 @@ size_t carve_fp8bws(const Dims& q, void* base, Fp8Bws* w) {
   w->part_side = c.take<float>(lsurge::fp8_partial_bytes(1) / sizeof(float));
   w->slots = c.take<uint32_t>(2);
   w->sinv = c.take<float>(4);
+  w->dy_scale = c.take<float>(1);
   size_t part = 0;
   if (q.fs) {
     part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, 2 * q.fs, dense_splits(q.T, q.d, 2 * q.fs)));
@@ -696,7 +698,7 @@ size_t lsurge_moe_bwd_fp8_workspace_bytes(const lsurge_moe_shape* s) {
 // weights beforehand).  Combine, dispatch and router backward are those of the bf16 backward; the shared expert runs
 // its FP8 backward as dense GEMMs of its own.
 // Stream plan (caller's stream = critical path):
-//   main: dY amax -> combine bwd (E5M2 dY rows) -> [record] -> down dgrad (+SwiGLU bwd, amax of [dG | dU]) ->
+//   main: dY scale -> combine bwd (E5M2 dY rows) -> [record] -> down dgrad (+SwiGLU bwd, amax of [dG | dU]) ->
 //         [dG | dU] cast -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
 //   s1:   from the start: W_r transpose, chunk table; after the record: down wgrad
 //   s0:   from the start: the shared expert's backward; after the record: router wgrad
@@ -769,16 +771,15 @@ int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
       return rc;
   }
 
-  // main: amax of the dY rows (from dy and the routing weights; also clears the [dG | dU] amax slot), then the combine
-  // backward writing them as E5M2 (plus d(weights), d(logits) and their dense rows)
+  // main: the scale of the dY rows (from dy and the routing weights; also clears the [dG | dU] amax slot), then the
+  // combine backward writing them as E5M2 (plus d(weights), d(logits) and their dense rows)
   {
-    const int nb = lsurge::launch_dy_rows_amax(dy, sv.weights, T, d, (int)q.k, f8.part_main, st, f8.slots, 1);
-    if (nb < 0) return nb;
+    if (int rc = lsurge::launch_dy_scale(dy, sv.weights, T, d, (int)q.k, f8.part_main, f8.dy_scale, f8.sinv, st,
+                                         f8.slots, 1))
+      return rc;
     lsurge::CombineFp8 c8;
     c8.dyq = f8.dyq;
-    c8.amax_part = f8.part_main;
-    c8.nparts = nb;
-    c8.sinv = f8.sinv;
+    c8.scale = f8.dy_scale;
     c8.nblocks = sv.num_blocks;
     if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, P, sv.slot, sv.weights, T, (int)q.k, d, dy, w.dy_pad,
                                                 dweights, w.dl, st, nullptr, sv.sel, w.dlog, (int)q.E, c8))

@@ -383,11 +383,9 @@ __global__ __launch_bounds__(PM_THREADS) void combine_pad_kernel(const bf16_t* _
 // wave per token (grid-strided), one partial per workgroup.  d % 8 == 0.
 __global__ __launch_bounds__(PM_THREADS) void dy_rows_amax_kernel(const bf16_t* __restrict__ dy,
                                                                   const float* __restrict__ w, int64_t n, int64_t d,
-                                                                  int k, float* __restrict__ partial,
-                                                                  uint32_t* __restrict__ zero, int nzero) {
+                                                                  int k, float* __restrict__ partial) {
   __shared__ float sh[PM_WAVES];
   const int lane = threadIdx.x & 63;
-  if (blockIdx.x == 0 && (int)threadIdx.x < nzero) zero[threadIdx.x] = 0u;  // slots a later kernel fills by atomic max
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
   float m = 0.f;
   for (int64_t t = wave_id(); t < n; t += nwaves) {
@@ -412,14 +410,35 @@ __global__ __launch_bounds__(PM_THREADS) void dy_rows_amax_kernel(const bf16_t* 
   }
 }
 
+// The power-of-two E5M2 scale of the dY rows from the partials (one workgroup): scale[0], and sinv[0] = 1 / scale;
+// also clears zero[0 .. nzero) (slots a later kernel fills by atomic max)
+__global__ __launch_bounds__(PM_THREADS) void dy_scale_kernel(const float* __restrict__ partial, int nparts,
+                                                              float* __restrict__ scale, float* __restrict__ sinv,
+                                                              uint32_t* __restrict__ zero, int nzero) {
+  __shared__ float sh[PM_WAVES];
+  if ((int)threadIdx.x < nzero) zero[threadIdx.x] = 0u;
+  float m = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += PM_THREADS) m = fmaxf(m, partial[i]);
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < PM_WAVES; ++i) m = fmaxf(m, sh[i]);
+    m = fmaxf(m, sh[0]);
+    const float sc = e5m2_scale(m);
+    scale[0] = sc;
+    sinv[0] = __fdiv_rn(1.f, sc);
+  }
+}
+
 // Fused combine backward of the layer (bf16 rows): per token, g is read once; for every choice j the expert
 // row y_pad[slot] is read once, dy_pad[slot] = bf16(w_j g) written once and <g, y> reduced; then the router
 // term dl[t,j] = w_j (dw_j - sum_i w_i dw_i).  moe_permute.py:303-309 does this in two passes over g and y.
 // gcopy (optional): g row t is also copied to gcopy[t] (the shared expert's rows of the padded dY, when the shared
 // expert rides along the routed experts).  dlog (optional, with sel): the dense bf16 row [E] of d(logits), dl[t,j] at
 // column sel[t,j] and 0 elsewhere -- the operand of the router's weight gradient.
-// FP8 backward (dyq set): the dY rows go out as E5M2 codes of bf16(w_j g) times the power-of-two scale of the amax
-// that dy_rows_amax_kernel left in nparts partials (dyp is not written); sinv[0] = 1 / scale.
+// FP8 backward (dyq set): the dY rows go out as E5M2 codes of bf16(w_j g) times scale[0] (dy_scale_kernel; dyp is
+// not written).
 template <int NC, int KK>
 __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_t* __restrict__ yp,
                                                                      const int32_t* __restrict__ slot,
@@ -431,18 +450,11 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_
                                                                      const int32_t* __restrict__ sel,
                                                                      bf16_t* __restrict__ dlog, int E,
                                                                      uint8_t* __restrict__ dyq,
-                                                                     const float* __restrict__ amax_part, int nparts,
-                                                                     float* __restrict__ sinv) {
+                                                                     const float* __restrict__ dy_scale) {
   static_assert(NC > 0 && KK > 0, "fixed-shape kernel");
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
-  float scale = 1.f;
-  if (dyq) {  // wave-uniform
-    float m = 0.f;
-    for (int i = lane; i < nparts; i += 64) m = fmaxf(m, amax_part[i]);
-    scale = e5m2_scale(wave_max(m));
-    if (blockIdx.x == 0 && threadIdx.x == 0) sinv[0] = __fdiv_rn(1.f, scale);
-  }
+  const float scale = dyq ? dy_scale[0] : 1.f;
   for (int64_t t = wave_id(); t < n; t += nwaves) {
     float gv[NC][8];
 #pragma unroll
@@ -665,17 +677,20 @@ int launch_combine_pad(const void* yp, int64_t d, int k, const int32_t* slot, co
   return LSURGE_OK;
 }
 
-int dy_rows_amax_parts() { return 256; }
+int dy_rows_amax_parts() { return 1024; }
 
-int launch_dy_rows_amax(const void* g, const float* w, int64_t n, int64_t d, int k, float* partial, hipStream_t s,
-                        uint32_t* zero, int nzero) {
+int launch_dy_scale(const void* g, const float* w, int64_t n, int64_t d, int k, float* partial, float* scale,
+                    float* sinv, hipStream_t s, uint32_t* zero, int nzero) {
   LSURGE_REQUIRE(n >= 1 && d >= 8 && d % 8 == 0 && k >= 1 && aligned16(g) && nzero >= 0 && nzero <= PM_THREADS,
-                 "dy_rows_amax: bad shape");
+                 "dy_scale: bad shape");
   const int nb = (int)std::min<int64_t>(dy_rows_amax_parts(), (n + PM_WAVES - 1) / PM_WAVES);
-  LSURGE_LAUNCH(KID_COMBINE_BWD, s,
+  LSURGE_LAUNCH(KID_FP8_QUANT, s,
                 hipLaunchKernelGGL(dy_rows_amax_kernel, dim3(nb), dim3(PM_THREADS), 0, s, (const bf16_t*)g, w, n, d, k,
-                                   partial, zero, nzero));
-  return nb;
+                                   partial));
+  LSURGE_LAUNCH(KID_FP8_QUANT, s,
+                hipLaunchKernelGGL(dy_scale_kernel, dim3(1), dim3(PM_THREADS), 0, s, (const float*)partial, nb, scale,
+                                   sinv, zero, nzero));
+  return LSURGE_OK;
 }
 
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
@@ -685,16 +700,15 @@ int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, co
   const int nc = row_chunks(d);
   LSURGE_REQUIRE(!dlog || (sel && dl && E >= 1), "combine_bwd: dense d(logits) needs sel, dl and E");
   LSURGE_REQUIRE(!dl || dw, "combine_bwd: the router backward needs dw");
-  LSURGE_REQUIRE(!f8.dyq || (f8.amax_part && f8.nparts >= 1 && f8.sinv && f8.nblocks && !gcopy),
-                 "combine_bwd: the FP8 dY rows need the amax partials, scale_inv and block count");
+  LSURGE_REQUIRE(!f8.dyq || (f8.scale && f8.nblocks && !gcopy), "combine_bwd: the FP8 dY rows need their scale and "
+                 "the block count");
   if (nc && (k == 6 || k == 8)) {
     LS_NC_SWITCH(nc, NC, LS_KK_SWITCH(k, KK, {
       if (NC && KK)
         LSURGE_LAUNCH(KID_COMBINE_BWD, s,
                       hipLaunchKernelGGL((combine_bwd_pad_kernel<NC ? NC : 1, KK ? KK : 1>), grid, dim3(PM_THREADS), 0,
                                          s, (const bf16_t*)yp, slot, w, n, d, (const bf16_t*)g, (bf16_t*)dyp, dw, dl,
-                                         (bf16_t*)gcopy, sel, (bf16_t*)dlog, E, (uint8_t*)f8.dyq, f8.amax_part,
-                                         f8.nparts, f8.sinv));
+                                         (bf16_t*)gcopy, sel, (bf16_t*)dlog, E, (uint8_t*)f8.dyq, f8.scale));
     }));
     return LSURGE_OK;
   }
@@ -709,8 +723,7 @@ int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, co
   // generic shapes, FP8: the bf16 rows are cast afterwards with the same scale (the rows of real blocks; padding rows
   // are never read)
   if (f8.dyq)
-    return fp8_cast_e5m2(dyp, rows * d, f8.amax_part, f8.nparts, f8.dyq, f8.sinv, f8.nblocks,
-                         (int64_t)LSURGE_BLOCK_ROWS * d, s);
+    return fp8_cast_e5m2(dyp, rows * d, f8.scale, -1, f8.dyq, nullptr, f8.nblocks, (int64_t)LSURGE_BLOCK_ROWS * d, s);
   return LSURGE_OK;
 }
 
