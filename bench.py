@@ -195,7 +195,8 @@ def short_kernel(name):
     # the GEMM templates' element-type / FP8 flags (defaults) are not part of the role: B layout and epilogue only
     m = re.match(r"(gemm_rows_kernel)<(\d+),(\d+)(,.*)?>$", n)
     if m:
-        n = f"{m.group(1)}<{m.group(2)},{m.group(3)}>" + ("<f8>" if m.group(4) and "true" in m.group(4) else "")
+        f8 = m.group(4).strip(",").split(",")[0] if m.group(4) else "0"  # the FP8 flag: 0, or the A format + 1
+        n = f"{m.group(1)}<{m.group(2)},{m.group(3)}>" + ("<f8>" if f8 not in ("0", "false") else "")
     if n.startswith("gemm_wgrad_kernel<"):
         n = "gemm_wgrad_kernel"
     return n
