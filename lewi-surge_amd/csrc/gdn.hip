@@ -13,8 +13,10 @@
 //                     of the state evolve independently, so the state's 128 x 32 slice stays in LDS and the scan
 //                     runs on 4x as many workgroups as there are heads.  Per chunk (gdn_fast.py:99-109):
 //                       v_new = u - w S,  o = (q e^gcum) S + attn v_new,  S = e^gcum_last S + (k e^(gcum_last-gcum))^T v_new
-// Arithmetic is f32 on the VALU (the reference runs these products at HIGHEST precision); padding tokens past T are
-// zeros with g = 0, as the reference pads (gdn_fast.py:61-65).
+// The chunk kernels' arithmetic is f32 on the VALU (the reference runs these products at HIGHEST precision); the forward
+// scan runs its products on the bf16 matrix cores with every f32 operand split into two bf16 terms (16 significant
+// bits, products exact, f32 sums).  Padding tokens past T are zeros with g = 0, as the reference pads
+// (gdn_fast.py:61-65).
 #include <cstring>
 
 #include "launchers.h"
@@ -226,6 +228,54 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
 }
 
 // grid (GD / SB, H, B): the scan over the chunks of one sequence and head for SB value columns.
+// bf16 matrix-core helpers of the scan.  D[32 x 32] += P[32 x 16] Q[16 x 32] (v_mfma_f32_32x32x16_bf16): lane l
+// supplies row l % 32 of P and column l % 32 of Q at k = 8 (l / 32) .. + 7, and holds D[8 (r / 4) + 4 (l / 32) + r % 4]
+// [l % 32] in acc[r].  An f32 operand goes in as two bf16 terms, hi = bf16(x) and lo = bf16(x - hi): 16 significant
+// bits, the products exact and summed in f32.
+__device__ __forceinline__ f32x16 mma_bf16(bf16x8 p, bf16x8 q, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
+}
+// 8 consecutive bf16 at (row, k) of a row-major LDS array of pitch PITCH elements (16-byte aligned rows)
+template <int PITCH>
+__device__ __forceinline__ bf16x8 frag_row(const bf16_t* base, int row, int k) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(base + row * PITCH + k));
+}
+// the same fragment with P[m][k] = A[k][m] read from a row-major A (rows k, pitch PITCH) by two transpose reads
+// (ds_read_b64_tr_b16: in a 16-lane group, source lane s points at 4 values of row kb + s / 4, columns nb + 4 (s % 4);
+// lane i receives column nb + i, rows kb .. kb + 3)
+template <int PITCH>
+__device__ __forceinline__ bf16x8 frag_col(const bf16_t* base, int mbase, int kbase, int lane) {
+  const int g = lane >> 4, s = lane & 15;
+  const int m = mbase + 16 * (g & 1) + 4 * (s & 3);
+  const int k0 = kbase + 8 * (g >> 1) + (s >> 2);
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, base + k0 * PITCH + m));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, base + (k0 + 4) * PITCH + m));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ uint32_t bf16_hi_lo(float x, uint32_t* lo) {
+  const bf16_t h = f32_to_bf16(x);
+  *lo = f32_to_bf16(x - bf16_to_f32(h));
+  return h;
+}
+// four f32 -> hi and lo bf16 quads, 8-byte stores at two row-major places
+__device__ __forceinline__ void store_hi_lo4(bf16_t* hi, bf16_t* lo, const float* x) {
+  uint32_t l[4], h[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h[i] = bf16_hi_lo(x[i], &l[i]);
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<u32x2*>(hi) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  *reinterpret_cast<u32x2*>(lo) = u32x2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+}
+
+// Scan over the chunks of one (32 value columns, head, sequence), on the matrix cores.  Eight waves:
+//   waves 4-7 hold the state slice S [128 x 32] in their accumulators (rows 32 (wave - 4) .., one 32 x 32 tile each),
+//   waves 0-1 form w S (rows 32 wave ..) and v_new = u - w S, waves 2-3 form (q e^gcum) S and o = that + attn v_new.
+// Per chunk: stage q, w, k, attn (hi / lo) and the state (hi / lo, transposed, from waves 4-7) in LDS; products
+// w S and q S; v_new to LDS (hi / lo, and e^(gcum_last - gcum) v_new for the state update); then attn v_new and
+// S = e^gcum_last S + k^T (e^(gcum_last - gcum) v_new).  The next chunk's tiles load into registers meanwhile.
+constexpr int KP = GC + 8;  // pitch of the [.][GC] bf16 tiles (144 bytes)
 __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                                        const bf16_t* __restrict__ u_in, const bf16_t* __restrict__ w_in,
                                                        const float* __restrict__ attn_in,
@@ -233,33 +283,35 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
                                                        float qscale, const float* __restrict__ h0,
                                                        bf16_t* __restrict__ o, float* __restrict__ h_out,
                                                        float* __restrict__ h_chunks = nullptr) {
-  __shared__ __attribute__((aligned(16))) bf16_t qs[GC][GP], ks[GC][GP], ws[GC][GP];
-  // state slice and v_new with 16-byte aligned rows (pitch SB + 4): a thread reads 4 or 8 consecutive columns at once,
-  // and the 8 column groups of a row that a wave reads at one d are distinct 16-byte slots
-  constexpr int SP = SB + 4;
-  __shared__ __attribute__((aligned(16))) float hs[GD][SP], vn[GC][SP];
-  __shared__ float at[GC][GC + 1];
+  __shared__ __attribute__((aligned(16))) bf16_t qs[GC][GP], ws[GC][GP], ks[GC][GP];  // [t][d]
+  __shared__ __attribute__((aligned(16))) bf16_t ah[GC][KP], al[GC][KP];             // attn hi / lo [t][j]
+  __shared__ __attribute__((aligned(16))) bf16_t shh[SB][GP], shl[SB][GP];           // state hi / lo [c][d]
+  __shared__ __attribute__((aligned(16))) bf16_t vh[SB][KP], vl[SB][KP];             // v_new hi / lo [c][t]
+  __shared__ __attribute__((aligned(16))) bf16_t vkh[SB][KP], vkl[SB][KP];           // e^(gl - g) v_new [c][t]
   __shared__ float gc[GC], ek[GC];  // gcum, exp(gcum_last - gcum)
   const int cb = blockIdx.x * SB, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lc = lane & 31, lh = lane >> 5;  // this lane's column of a 32 x 32 tile, and its row quad offset (x 4)
   const int64_t row0 = (int64_t)b * T;
   const int64_t bh = (int64_t)b * H + h;
-  for (int e = tid; e < GD * SB; e += GTH) {
-    const int d = e / SB, c = e % SB;
-    hs[d][c] = h0 ? h0[(bh * GD + d) * GD + cb + c] : 0.f;
-  }
-  // outputs of this thread: row ri, columns ci .. ci + 3 of the [GC][SB] chunk products; state entries row hd (of
-  // GD), columns hc .. hc + 7
-  const int ri = tid / 8, ci = 4 * (tid % 8);
-  const int hd = tid / 4, hc = 8 * (tid % 4);
+  // tile rows of this lane's accumulators: row(r) = rb + 8 (r / 4) + 4 lh + r % 4 (tokens for waves 0-3, state rows
+  // for waves 4-7)
+  const int rb = wave < 4 ? 32 * (wave & 1) : 32 * (wave - 4);
+  f32x16 acc = {};  // waves 4-7: the state tile; waves 0-3: this chunk's product
+  if (wave >= 4)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = rb + 8 * (r / 4) + 4 * lh + r % 4;
+      acc[r] = h0 ? h0[(bh * GD + d) * GD + cb + lc] : 0.f;
+    }
   // The next chunk's tiles are fetched into registers while the current one computes: this thread's two 16-byte
-  // pieces of each of q, k and w (piece e = tid + GTH p: row e / 16, columns 8 (e % 16)), its eight attn values and
-  // (threads < GC) one gcum value.
+  // pieces of each of q, k and w (piece e = tid + GTH p: row e / 16, columns 8 (e % 16)), its eight attn values,
+  // (threads < GC) one gcum value, and (waves 0-1) the 16 u values of its v_new outputs.
   constexpr int PP = GC * (GD / 8) / GTH;  // pieces per thread and tile
   static_assert(PP * GTH == GC * (GD / 8) && GC * GC == 8 * GTH, "scan tile split");
   u32x4 pq[PP], pk[PP], pw[PP];
   f32x4 pa[2];
-  float pg = 0.f;
+  float pg = 0.f, pu[16];
   auto fetch = [&](int n) {
     const int t0 = n * GC;
     const int64_t chunk_id = bh * N + n;
@@ -276,17 +328,17 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
     pa[0] = *reinterpret_cast<const f32x4*>(asrc + 4 * tid);
     pa[1] = *reinterpret_cast<const f32x4*>(asrc + 4 * (tid + GTH));
     if (tid < GC) pg = gcum_in[chunk_id * GC + tid];
+    if (wave < 2) {
+      const bf16_t* ub = u_in + chunk_id * GC * GD + cb + lc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pu[r] = bf16_to_f32(ub[(rb + 8 * (r / 4) + 4 * lh + r % 4) * GD]);
+    }
   };
   fetch(0);
   for (int n = 0; n < N; ++n) {
     const int t0 = n * GC;
     const int64_t chunk_id = bh * N + n;
-    __syncthreads();  // the previous chunk is done with the tiles
-    if (h_chunks)  // the state entering chunk n, for the backward
-      for (int e = tid; e < GD * SB; e += GTH) {
-        const int d = e / SB, c = e % SB;
-        h_chunks[(chunk_id * GD + d) * GD + cb + c] = hs[d][c];
-      }
+    __syncthreads();  // the previous chunk is done with every LDS tile
 #pragma unroll
     for (int p = 0; p < PP; ++p) {
       const int e = tid + GTH * p, i = e / (GD / 8), c = 8 * (e % (GD / 8));
@@ -299,78 +351,94 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
       *reinterpret_cast<u32x4*>(&ws[i][c]) = pw[p];
     }
 #pragma unroll
-    for (int hlf = 0; hlf < 2; ++hlf)
+    for (int hlf = 0; hlf < 2; ++hlf) {
+      const int e = 4 * (tid + GTH * hlf);
+      const float av[4] = {pa[hlf][0], pa[hlf][1], pa[hlf][2], pa[hlf][3]};
+      store_hi_lo4(&ah[e / GC][e % GC], &al[e / GC][e % GC], av);
+    }
+    if (tid < GC) {  // wave 0: gcum and exp(gcum_last - gcum)
+      gc[tid] = pg;
+      ek[tid] = __expf(__shfl(pg, GC - 1, 64) - pg);
+    }
+    if (wave >= 4) {  // the state entering chunk n: hi / lo transposed for the products, and to the backward
 #pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        const int e = 4 * (tid + GTH * hlf) + x;
-        at[e / GC][e % GC] = pa[hlf][x];
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = rb + 8 * q4 + 4 * lh;
+        const float sv[4] = {acc[4 * q4], acc[4 * q4 + 1], acc[4 * q4 + 2], acc[4 * q4 + 3]};
+        store_hi_lo4(&shh[lc][d], &shl[lc][d], sv);
+        if (h_chunks)
+#pragma unroll
+          for (int x = 0; x < 4; ++x) h_chunks[(chunk_id * GD + d + x) * GD + cb + lc] = sv[x];
       }
-    if (tid < GC) gc[tid] = pg;
+    }
     __syncthreads();
-    if (tid < GC) ek[tid] = __expf(gc[GC - 1] - gc[tid]);  // read after the barrier that follows v_new
+    float ub[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ub[r] = pu[r];
     if (n + 1 < N) fetch(n + 1);
-    // v_new = u - w S and inter = (q e^gcum) S for this thread's 1 x 4 outputs
-    float vacc[1][4] = {}, iacc[1][4] = {};
-    for (int d = 0; d < GD; d += 8) {
-      float w8[1][8], q8[1][8];
-      unpack8g(*reinterpret_cast<const u32x4*>(&ws[ri][d]), w8[0]);
-      unpack8g(*reinterpret_cast<const u32x4*>(&qs[ri][d]), q8[0]);
+    if (wave < 4) {  // w S (waves 0-1) or (q scale) S (waves 2-3), K = 128
+      const bf16_t* P = wave < 2 ? &ws[0][0] : &qs[0][0];
+      acc = f32x16{};
 #pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        const f32x4 hv = *reinterpret_cast<const f32x4*>(&hs[d + x][ci]);
+      for (int k0 = 0; k0 < GD; k0 += 16) {
+        const int kk = k0 + 8 * lh;
+        const bf16x8 pf = frag_row<GP>(P, rb + lc, kk);
+        acc = mma_bf16(pf, frag_row<GP>(&shh[0][0], lc, kk), acc);
+        acc = mma_bf16(pf, frag_row<GP>(&shl[0][0], lc, kk), acc);
+      }
+      if (wave < 2) {  // v_new = u - w S, to LDS as hi / lo and, scaled by exp(gcum_last - gcum), for the update
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          vacc[0][s] = fmaf(w8[0][x], hv[s], vacc[0][s]);
-          iacc[0][s] = fmaf(q8[0][x], hv[s], iacc[0][s]);
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int t = rb + 8 * q4 + 4 * lh;
+          float vv[4], vk[4];
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            vv[x] = ub[4 * q4 + x] - acc[4 * q4 + x];
+            vk[x] = vv[x] * ek[t + x];
+          }
+          store_hi_lo4(&vh[lc][t], &vl[lc][t], vv);
+          store_hi_lo4(&vkh[lc][t], &vkl[lc][t], vk);
         }
+      } else {  // inter = (q S) e^gcum
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] *= __expf(gc[rb + 8 * (r / 4) + 4 * lh + r % 4]);
       }
     }
-    const bf16_t* ub = u_in + chunk_id * GC * GD;
+    __syncthreads();  // v_new is in LDS
+    if (wave == 2 || wave == 3) {  // o = inter + attn v_new (attn is zero above the diagonal), K = 64
 #pragma unroll
-    for (int s = 0; s < 4; ++s) vn[ri][ci + s] = bf16_to_f32(ub[ri * GD + cb + ci + s]) - vacc[0][s];
-    __syncthreads();
-    // o = inter e^gcum + attn v_new (attn is zero above the diagonal)
-    {
-      const int r = 0, i = ri;
-      float acc[4];
-      const float e = __expf(gc[i]);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) acc[s] = iacc[r][s] * e;
-      for (int j = 0; j <= i; ++j) {
-        const float a = at[i][j];
-        const f32x4 vv = *reinterpret_cast<const f32x4*>(&vn[j][ci]);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc[s] = fmaf(a, vv[s], acc[s]);
+      for (int k0 = 0; k0 < GC; k0 += 16) {
+        const int kk = k0 + 8 * lh;
+        const bf16x8 ph = frag_row<KP>(&ah[0][0], rb + lc, kk), pl = frag_row<KP>(&al[0][0], rb + lc, kk);
+        const bf16x8 qh = frag_row<KP>(&vh[0][0], lc, kk);
+        acc = mma_bf16(ph, qh, acc);
+        acc = mma_bf16(ph, frag_row<KP>(&vl[0][0], lc, kk), acc);
+        acc = mma_bf16(pl, qh, acc);
       }
-      if (o && t0 + i < T) {  // the backward's recompute needs the states only
-        bf16_t* op = o + ((row0 + t0 + i) * H + h) * GD + cb + ci;
-        *reinterpret_cast<uint2*>(op) = uint2{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
-      }
-    }
-    // S = e^gcum_last S + (k e^(gcum_last - gcum))^T v_new; every read of the old state happened before the barrier
-    // above
-    const float gl = gc[GC - 1], el = __expf(gl);
-    float hn[8];
+      if (o)  // the backward's recompute needs the states only
 #pragma unroll
-    for (int x = 0; x < 8; ++x) hn[x] = hs[hd][hc + x] * el;
-    for (int i = 0; i < GC; ++i) {
-      const float k0 = bf16_to_f32(ks[i][hd]) * ek[i];
-      const f32x4 v0 = *reinterpret_cast<const f32x4*>(&vn[i][hc]), v1 = *reinterpret_cast<const f32x4*>(&vn[i][hc + 4]);
+        for (int r = 0; r < 16; ++r) {
+          const int t = rb + 8 * (r / 4) + 4 * lh + r % 4;
+          if (t0 + t < T) o[((row0 + t0 + t) * H + h) * GD + cb + lc] = f32_to_bf16(acc[r]);
+        }
+    } else if (wave >= 4) {  // S = e^gcum_last S + k^T (e^(gcum_last - gcum) v_new), K = 64
+      const float el = __expf(gc[GC - 1]);
 #pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        hn[x] = fmaf(k0, v0[x], hn[x]);
-        hn[x + 4] = fmaf(k0, v1[x], hn[x + 4]);
+      for (int r = 0; r < 16; ++r) acc[r] *= el;
+#pragma unroll
+      for (int k0 = 0; k0 < GC; k0 += 16) {
+        const int kk = k0 + 8 * lh;
+        const bf16x8 pf = frag_col<GP>(&ks[0][0], rb, k0, lane);
+        acc = mma_bf16(pf, frag_row<KP>(&vkh[0][0], lc, kk), acc);
+        acc = mma_bf16(pf, frag_row<KP>(&vkl[0][0], lc, kk), acc);
       }
     }
-    __syncthreads();  // every thread has read the old state (o used only vn and at)
-#pragma unroll
-    for (int x = 0; x < 8; ++x) hs[hd][hc + x] = hn[x];
   }
-  __syncthreads();
-  if (h_out)
-    for (int e = tid; e < GD * SB; e += GTH) {
-      const int d = e / SB, c = e % SB;
-      h_out[(bh * GD + d) * GD + cb + c] = hs[d][c];
+  if (h_out && wave >= 4)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = rb + 8 * (r / 4) + 4 * lh + r % 4;
+      h_out[(bh * GD + d) * GD + cb + lc] = acc[r];
     }
 }
 
