@@ -464,96 +464,155 @@ __global__ __launch_bounds__(GTH) void gdn_bscan_kernel(const bf16_t* __restrict
                                                         int T, int H, int N, float qscale,
                                                         const float* __restrict__ dh_final,
                                                         float* __restrict__ dh_chunks, float* __restrict__ dh0) {
-  __shared__ __attribute__((aligned(16))) bf16_t qs[GC][GP], ks[GC][GP], ws[GC][GP];
-  constexpr int SP = SB + 4;
-  __shared__ __attribute__((aligned(16))) float dh[GD][SP], dvn[GC][SP], dos[GC][SP];
-  __shared__ float at[GC][GC + 1];
-  __shared__ float gc[GC], ek[GC], eg[GC];
+  // On the bf16 matrix cores, as the forward scan: waves 4-7 hold the state gradient dH [128 x 32] in their
+  // accumulators; waves 0-1 form dv_new for token rows 32 wave .. (attn^T do + e^(gl - g) k dH); waves 4-7 then update
+  // dH <- e^gl dH + q^T (e^g do) - w^T dv_new.  f32 operands enter as hi / lo bf16 pairs.
+  __shared__ __attribute__((aligned(16))) bf16_t qs[GC][GP], ks[GC][GP], ws[GC][GP];  // [t][d]
+  __shared__ __attribute__((aligned(16))) bf16_t ah[GC][KP], al[GC][KP];             // attn hi / lo [j][t]
+  __shared__ __attribute__((aligned(16))) bf16_t dhh[SB][GP], dhl[SB][GP];           // dH hi / lo [c][d]
+  __shared__ __attribute__((aligned(16))) bf16_t doT[SB][KP];                        // do [c][t]
+  __shared__ __attribute__((aligned(16))) bf16_t deh[SB][KP], del_[SB][KP];          // e^g do hi / lo [c][t]
+  __shared__ __attribute__((aligned(16))) bf16_t dvh[SB][KP], dvl[SB][KP];           // -dv_new hi / lo [c][t]
+  __shared__ float gc[GC], ek[GC];
   const int cb = blockIdx.x * SB, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lc = lane & 31, lh = lane >> 5;
   const int64_t row0 = (int64_t)b * T;
   const int64_t bh = (int64_t)b * H + h;
-  for (int e = tid; e < GD * SB; e += GTH) {
-    const int d = e / SB, c = e % SB;
-    dh[d][c] = dh_final ? dh_final[(bh * GD + d) * GD + cb + c] : 0.f;
-  }
-  const int ri = tid / 8, ci = 4 * (tid % 8);   // dv_new outputs: row ri, columns ci .. ci + 3
-  const int hd = tid / 4, hc = 8 * (tid % 4);   // state-gradient outputs: row hd, columns hc .. hc + 7
-  for (int n = N - 1; n >= 0; --n) {
+  const int rb = wave < 4 ? 32 * (wave & 1) : 32 * (wave - 4);
+  f32x16 acc = {};
+  if (wave >= 4)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = rb + 8 * (r / 4) + 4 * lh + r % 4;
+      acc[r] = dh_final ? dh_final[(bh * GD + d) * GD + cb + lc] : 0.f;
+    }
+  // next chunk's tiles in registers: q, k, w pieces as the forward scan, attn, and (threads < 256) one 8-column piece
+  // of do (row e / 4, columns 8 (e % 4) of this block) with its row's gcum; (threads < GC) gcum of row tid
+  constexpr int PP = GC * (GD / 8) / GTH;
+  u32x4 pq[PP], pk[PP], pw[PP], pd = {0u, 0u, 0u, 0u};
+  f32x4 pa[2];
+  float pg = 0.f, pgd = 0.f;
+  auto fetch = [&](int n) {
     const int t0 = n * GC;
     const int64_t chunk_id = bh * N + n;
-    __syncthreads();  // the previous chunk is done with the tiles and dh is final
-    load_tile(ks, k, row0, T, t0, H, h, 1.f);
-    load_tile(qs, q, row0, T, t0, H, h, qscale);
-    for (int e = tid; e < GC * (GD / 8); e += GTH) {
-      const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
-      *reinterpret_cast<u32x4*>(&ws[i][c]) = *reinterpret_cast<const u32x4*>(w_in + chunk_id * GC * GD + i * GD + c);
+#pragma unroll
+    for (int p = 0; p < PP; ++p) {
+      const int e = tid + GTH * p, i = e / (GD / 8), c = 8 * (e % (GD / 8));
+      const bool in = t0 + i < T;
+      const int64_t off = ((row0 + t0 + i) * H + h) * GD + c;
+      pq[p] = in ? *reinterpret_cast<const u32x4*>(q + off) : u32x4{0u, 0u, 0u, 0u};
+      pk[p] = in ? *reinterpret_cast<const u32x4*>(k + off) : u32x4{0u, 0u, 0u, 0u};
+      pw[p] = *reinterpret_cast<const u32x4*>(w_in + chunk_id * GC * GD + i * GD + c);
     }
-    for (int e = tid; e < GC * GC; e += GTH) at[e / GC][e % GC] = attn_in[chunk_id * GC * GC + e];
-    for (int e = tid; e < GC * SB; e += GTH) {
-      const int i = e / SB, c = e % SB;
-      dos[i][c] = t0 + i < T ? bf16_to_f32(dout[((row0 + t0 + i) * H + h) * GD + cb + c]) : 0.f;
+    const float* asrc = attn_in + chunk_id * GC * GC;
+    pa[0] = *reinterpret_cast<const f32x4*>(asrc + 4 * tid);
+    pa[1] = *reinterpret_cast<const f32x4*>(asrc + 4 * (tid + GTH));
+    if (tid < GC) pg = gcum_in[chunk_id * GC + tid];
+    if (tid < GC * SB / 8) {
+      const int i = tid / (SB / 8), c = 8 * (tid % (SB / 8));
+      pd = t0 + i < T ? *reinterpret_cast<const u32x4*>(dout + ((row0 + t0 + i) * H + h) * GD + cb + c)
+                      : u32x4{0u, 0u, 0u, 0u};
+      pgd = gcum_in[chunk_id * GC + i];
     }
-    if (tid < GC) gc[tid] = gcum_in[chunk_id * GC + tid];
-    for (int e = tid; e < GD * SB; e += GTH) {  // the gradient of the state leaving this chunk
-      const int d = e / SB, c = e % SB;
-      dh_chunks[(chunk_id * GD + d) * GD + cb + c] = dh[d][c];
+  };
+  fetch(N - 1);
+  for (int n = N - 1; n >= 0; --n) {
+    const int64_t chunk_id = bh * N + n;
+    __syncthreads();  // the previous chunk is done with every LDS tile
+#pragma unroll
+    for (int p = 0; p < PP; ++p) {
+      const int e = tid + GTH * p, i = e / (GD / 8), c = 8 * (e % (GD / 8));
+      float f[8];
+      unpack8g(pq[p], f);
+      *reinterpret_cast<u32x4*>(&qs[i][c]) =
+          u32x4{pack_bf16x2(f[0] * qscale, f[1] * qscale), pack_bf16x2(f[2] * qscale, f[3] * qscale),
+                pack_bf16x2(f[4] * qscale, f[5] * qscale), pack_bf16x2(f[6] * qscale, f[7] * qscale)};
+      *reinterpret_cast<u32x4*>(&ks[i][c]) = pk[p];
+      *reinterpret_cast<u32x4*>(&ws[i][c]) = pw[p];
     }
-    __syncthreads();
+#pragma unroll
+    for (int hlf = 0; hlf < 2; ++hlf) {
+      const int e = 4 * (tid + GTH * hlf);
+      const float av[4] = {pa[hlf][0], pa[hlf][1], pa[hlf][2], pa[hlf][3]};
+      store_hi_lo4(&ah[e / GC][e % GC], &al[e / GC][e % GC], av);
+    }
     if (tid < GC) {
-      ek[tid] = __expf(gc[GC - 1] - gc[tid]);
-      eg[tid] = __expf(gc[tid]);
+      gc[tid] = pg;
+      ek[tid] = __expf(__shfl(pg, GC - 1, 64) - pg);
+    }
+    if (tid < GC * SB / 8) {  // do and e^g do, transposed to [column][row]
+      const int i = tid / (SB / 8), c = 8 * (tid % (SB / 8));
+      float f[8];
+      unpack8g(pd, f);
+      const float eg = __expf(pgd);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        doT[c + x][i] = f32_to_bf16(f[x]);
+        uint32_t lo;
+        deh[c + x][i] = (bf16_t)bf16_hi_lo(f[x] * eg, &lo);
+        del_[c + x][i] = (bf16_t)lo;
+      }
+    }
+    if (wave >= 4) {  // the gradient of the state leaving this chunk: hi / lo for the products, and to the chunk grads
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = rb + 8 * q4 + 4 * lh;
+        const float sv[4] = {acc[4 * q4], acc[4 * q4 + 1], acc[4 * q4 + 2], acc[4 * q4 + 3]};
+        store_hi_lo4(&dhh[lc][d], &dhl[lc][d], sv);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) dh_chunks[(chunk_id * GD + d + x) * GD + cb + lc] = sv[x];
+      }
     }
     __syncthreads();
-    // dv_new = attn^T do + kd dH (attn is zero above the diagonal: rows j >= ri)
-    {
-      float acc[4] = {}, kacc[4] = {};
-      for (int j = ri; j < GC; ++j) {
-        const float a = at[j][ri];
-        const f32x4 dv = *reinterpret_cast<const f32x4*>(&dos[j][ci]);
+    if (n > 0) fetch(n - 1);
+    if (wave < 2) {  // dv_new = attn^T do + e^(gl - g) (k dH) for token rows rb ..
+      f32x16 a1 = {}, a2 = {};
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) acc[s2] = fmaf(a, dv[s2], acc[s2]);
-      }
-      for (int d = 0; d < GD; d += 8) {
-        float k8[8];
-        unpack8g(*reinterpret_cast<const u32x4*>(&ks[ri][d]), k8);
-#pragma unroll
-        for (int x = 0; x < 8; ++x) {
-          const f32x4 hv = *reinterpret_cast<const f32x4*>(&dh[d + x][ci]);
-#pragma unroll
-          for (int s2 = 0; s2 < 4; ++s2) kacc[s2] = fmaf(k8[x], hv[s2], kacc[s2]);
-        }
+      for (int k0 = 0; k0 < GC; k0 += 16) {
+        const int kk = k0 + 8 * lh;
+        const bf16x8 qf = frag_row<KP>(&doT[0][0], lc, kk);
+        a1 = mma_bf16(frag_col<KP>(&ah[0][0], rb, k0, lane), qf, a1);
+        a1 = mma_bf16(frag_col<KP>(&al[0][0], rb, k0, lane), qf, a1);
       }
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) dvn[ri][ci + s2] = fmaf(ek[ri], kacc[s2], acc[s2]);
+      for (int k0 = 0; k0 < GD; k0 += 16) {
+        const int kk = k0 + 8 * lh;
+        const bf16x8 pf = frag_row<GP>(&ks[0][0], rb + lc, kk);
+        a2 = mma_bf16(pf, frag_row<GP>(&dhh[0][0], lc, kk), a2);
+        a2 = mma_bf16(pf, frag_row<GP>(&dhl[0][0], lc, kk), a2);
+      }
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int t = rb + 8 * q4 + 4 * lh;
+        float nv[4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) nv[x] = -fmaf(ek[t + x], a2[4 * q4 + x], a1[4 * q4 + x]);
+        store_hi_lo4(&dvh[lc][t], &dvl[lc][t], nv);
+      }
     }
-    __syncthreads();
-    // dH <- e^gl dH + qg^T do - w^T dv_new
-    float nd[8];
-    {
+    __syncthreads();  // -dv_new is in LDS
+    if (wave >= 4) {  // dH <- e^gl dH + q^T (e^g do) - w^T dv_new, K = 64
       const float el = __expf(gc[GC - 1]);
 #pragma unroll
-      for (int x = 0; x < 8; ++x) nd[x] = dh[hd][hc + x] * el;
-      for (int i = 0; i < GC; ++i) {
-        const float qv = bf16_to_f32(qs[i][hd]) * eg[i], wv = bf16_to_f32(ws[i][hd]);
-        const f32x4 d0 = *reinterpret_cast<const f32x4*>(&dos[i][hc]), d1 = *reinterpret_cast<const f32x4*>(&dos[i][hc + 4]);
-        const f32x4 v0 = *reinterpret_cast<const f32x4*>(&dvn[i][hc]), v1 = *reinterpret_cast<const f32x4*>(&dvn[i][hc + 4]);
+      for (int r = 0; r < 16; ++r) acc[r] *= el;
 #pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          nd[x] = fmaf(qv, d0[x], fmaf(-wv, v0[x], nd[x]));
-          nd[x + 4] = fmaf(qv, d1[x], fmaf(-wv, v1[x], nd[x + 4]));
-        }
+      for (int k0 = 0; k0 < GC; k0 += 16) {
+        const int kk = k0 + 8 * lh;
+        const bf16x8 pq_ = frag_col<GP>(&qs[0][0], rb, k0, lane);
+        acc = mma_bf16(pq_, frag_row<KP>(&deh[0][0], lc, kk), acc);
+        acc = mma_bf16(pq_, frag_row<KP>(&del_[0][0], lc, kk), acc);
+        const bf16x8 pw_ = frag_col<GP>(&ws[0][0], rb, k0, lane);
+        acc = mma_bf16(pw_, frag_row<KP>(&dvh[0][0], lc, kk), acc);
+        acc = mma_bf16(pw_, frag_row<KP>(&dvl[0][0], lc, kk), acc);
       }
     }
-    __syncthreads();  // every thread has read the old dH
-#pragma unroll
-    for (int x = 0; x < 8; ++x) dh[hd][hc + x] = nd[x];
   }
-  __syncthreads();
-  if (dh0)
-    for (int e = tid; e < GD * SB; e += GTH) {
-      const int d = e / SB, c = e % SB;
-      dh0[(bh * GD + d) * GD + cb + c] = dh[d][c];
+  if (dh0 && wave >= 4)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = rb + 8 * (r / 4) + 4 * lh + r % 4;
+      dh0[(bh * GD + d) * GD + cb + lc] = acc[r];
     }
 }
 
