@@ -628,18 +628,22 @@ __global__ __launch_bounds__(GTH) void gdn_bgrad_kernel(const bf16_t* __restrict
                                                         float* __restrict__ dqg_out, float* __restrict__ dkd_out,
                                                         bf16_t* __restrict__ du_out, bf16_t* __restrict__ dw_out,
                                                         float* __restrict__ dp_out, float* __restrict__ dgl_out) {
-  __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], ws[GC][GP];
-  constexpr int SP = SB + 4;
-  __shared__ __attribute__((aligned(16))) float hb[GD][SP], db[GD][SP], dob[GC][SP], vnb[GC][SP], dvb[GC][SP];
-  // the block's h, dH and v_new transposed ([column][row]): in the accumulation below the 16 lanes of a row group read
-  // 16 consecutive 32-byte (16-byte) pieces of one row instead of one value from each of 16 rows 8 (4) rows apart,
-  // which put them on 2 (4) banks
-  constexpr int TP = GD + 4;
-  __shared__ __attribute__((aligned(16))) float hT[SB][TP], dT[SB][TP], vT[SB][GC + 4];
-  __shared__ float at[GC][GC + 1];
+  // On the bf16 matrix cores (f32 operands as hi / lo bf16 pairs).  Per value-column block (4 of 32): waves 0-1 form
+  // v_new = u - w h for token rows 32 wave .., waves 2-3 dv_new = e^(gl - g) (k dH) + attn^T do; then every wave adds
+  // the block's share (K = 32 columns) of one 32 x 32 tile each of dqg += do h^T, dkd += v_new dH^T, dw -= dv_new h^T
+  // (wave w: token rows 32 (w / 4), state rows 32 (w % 4)) and waves 0-3 of dP += do v_new^T.
+  constexpr int BP = SB + 8;  // pitch of the [.][SB] bf16 block tiles (80 bytes)
+  __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], ws[GC][GP];           // [t][d]
+  __shared__ __attribute__((aligned(16))) bf16_t ah[GC][KP], al[GC][KP];           // attn hi / lo [j][t]
+  __shared__ __attribute__((aligned(16))) bf16_t hh[GD][BP], hl[GD][BP];           // h block hi / lo [d][c]
+  __shared__ __attribute__((aligned(16))) bf16_t dhh[GD][BP], dhl[GD][BP];         // dH block hi / lo [d][c]
+  __shared__ __attribute__((aligned(16))) bf16_t dos[GC][BP];                      // do block [t][c]
+  __shared__ __attribute__((aligned(16))) bf16_t vh[GC][BP], vl[GC][BP];           // v_new hi / lo [t][c]
+  __shared__ __attribute__((aligned(16))) bf16_t dvh[GC][BP], dvl[GC][BP];         // dv_new hi / lo [t][c]
   __shared__ float gc[GC], ek[GC], red[GTH / 64];
   const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z, N = gridDim.x;
-  const int tid = threadIdx.x, t0 = n * GC;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t0 = n * GC;
+  const int lc = lane & 31, lh = lane >> 5;
   const int64_t row0 = (int64_t)b * T;
   const int64_t chunk_id = ((int64_t)b * H + h) * N + n;
   load_tile(ks, k, row0, T, t0, H, h, 1.f);
@@ -647,117 +651,133 @@ __global__ __launch_bounds__(GTH) void gdn_bgrad_kernel(const bf16_t* __restrict
     const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
     *reinterpret_cast<u32x4*>(&ws[i][c]) = *reinterpret_cast<const u32x4*>(w_in + chunk_id * GC * GD + i * GD + c);
   }
-  for (int e = tid; e < GC * GC; e += GTH) at[e / GC][e % GC] = attn_in[chunk_id * GC * GC + e];
-  if (tid < GC) gc[tid] = gcum_in[chunk_id * GC + tid];
-  __syncthreads();
-  if (tid < GC) ek[tid] = __expf(gc[GC - 1] - gc[tid]);
-  const int ri = tid / 8, ci = 4 * (tid % 8);          // [GC][SB] block products: row ri, columns ci .. ci + 3
-  const int i0 = 2 * (tid / 16), c0 = 8 * (tid % 16);  // [GC][GD] accumulators: rows i0, i0 + 1, columns c0 .. c0 + 7
-  const int j0 = 4 * (tid % 16);                       // [GC][GC] accumulator: rows i0, i0 + 1, columns j0 .. j0 + 3
-  const int hd = tid / 4, hc = 8 * (tid % 4);          // [GD][SB] elementwise: row hd, columns hc .. hc + 7
-  float aq[2][8] = {}, ak[2][8] = {}, aw[2][8] = {}, ap[2][4] = {};
+  for (int e = 4 * tid; e < GC * GC; e += 4 * GTH) {
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(attn_in + chunk_id * GC * GC + e);
+    const float av[4] = {a4[0], a4[1], a4[2], a4[3]};
+    store_hi_lo4(&ah[e / GC][e % GC], &al[e / GC][e % GC], av);
+  }
+  if (tid < GC) {
+    gc[tid] = gcum_in[chunk_id * GC + tid];
+    ek[tid] = __expf(gcum_in[chunk_id * GC + GC - 1] - gc[tid]);
+  }
+  const int tr = 32 * (wave / 4), dr = 32 * (wave % 4);  // this wave's tile of the [GC][GD] accumulators
+  const int rb = 32 * (wave & 1);                        // token rows of the block products (waves 0-3)
+  f32x16 aq = {}, ak = {}, aw = {}, ap = {};
   float gl_part = 0.f;
   const float* hsrc = h_chunks + chunk_id * GD * GD;
   const float* dsrc = dh_chunks + chunk_id * GD * GD;
   for (int cb = 0; cb < GD; cb += SB) {
     __syncthreads();  // the previous block's tiles are consumed (and the setup above is done)
-    for (int e = tid; e < GD * SB / 4; e += GTH) {
+    for (int e = tid; e < GD * SB / 4; e += GTH) {  // h and dH blocks: hi / lo, and <dH, h>
       const int d = e / (SB / 4), c = 4 * (e % (SB / 4));
       const f32x4 hv = *reinterpret_cast<const f32x4*>(hsrc + d * GD + cb + c);
       const f32x4 dv = *reinterpret_cast<const f32x4*>(dsrc + d * GD + cb + c);
-      *reinterpret_cast<f32x4*>(&hb[d][c]) = hv;
-      *reinterpret_cast<f32x4*>(&db[d][c]) = dv;
+      const float h4[4] = {hv[0], hv[1], hv[2], hv[3]}, d4[4] = {dv[0], dv[1], dv[2], dv[3]};
+      store_hi_lo4(&hh[d][c], &hl[d][c], h4);
+      store_hi_lo4(&dhh[d][c], &dhl[d][c], d4);
 #pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        hT[c + x][d] = hv[x];
-        dT[c + x][d] = dv[x];
-      }
+      for (int x = 0; x < 4; ++x) gl_part = fmaf(h4[x], d4[x], gl_part);
     }
-    for (int e = tid; e < GC * SB; e += GTH) {
-      const int i = e / SB, c = e % SB;
-      dob[i][c] = t0 + i < T ? bf16_to_f32(dout[((row0 + t0 + i) * H + h) * GD + cb + c]) : 0.f;
+    for (int e = tid; e < GC * SB / 8; e += GTH) {  // do block
+      const int i = e / (SB / 8), c = 8 * (e % (SB / 8));
+      *reinterpret_cast<u32x4*>(&dos[i][c]) =
+          t0 + i < T ? *reinterpret_cast<const u32x4*>(dout + ((row0 + t0 + i) * H + h) * GD + cb + c)
+                     : u32x4{0u, 0u, 0u, 0u};
     }
     __syncthreads();
-    {  // <dH, h> over this block
+    if (wave < 4) {
+      f32x16 acc = {};
+      if (wave < 2) {  // w h (K = 128)
 #pragma unroll
-      for (int x = 0; x < 8; ++x) gl_part = fmaf(hb[hd][hc + x], db[hd][hc + x], gl_part);
-    }
-    {  // v_new = u - w h and dv_new = attn^T do + kd dH for row ri, columns ci .. ci + 3
-      float wv[4] = {}, kv[4] = {}, av[4] = {};
-      for (int d = 0; d < GD; d += 8) {
-        float w8[8], k8[8];
-        unpack8g(*reinterpret_cast<const u32x4*>(&ws[ri][d]), w8);
-        unpack8g(*reinterpret_cast<const u32x4*>(&ks[ri][d]), k8);
+        for (int k0 = 0; k0 < GD; k0 += 16) {
+          const bf16x8 pf = frag_row<GP>(&ws[0][0], rb + lc, k0 + 8 * lh);
+          acc = mma_bf16(pf, frag_col<BP>(&hh[0][0], 0, k0, lane), acc);
+          acc = mma_bf16(pf, frag_col<BP>(&hl[0][0], 0, k0, lane), acc);
+        }
+        const bf16_t* ub = u_in + chunk_id * GC * GD + cb + lc;
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
-          const f32x4 hv = *reinterpret_cast<const f32x4*>(&hb[d + x][ci]);
-          const f32x4 dv = *reinterpret_cast<const f32x4*>(&db[d + x][ci]);
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int t = rb + 8 * q4 + 4 * lh;
+          float vv[4];
 #pragma unroll
-          for (int s2 = 0; s2 < 4; ++s2) {
-            wv[s2] = fmaf(w8[x], hv[s2], wv[s2]);
-            kv[s2] = fmaf(k8[x], dv[s2], kv[s2]);
+          for (int x = 0; x < 4; ++x) vv[x] = bf16_to_f32(ub[(t + x) * GD]) - acc[4 * q4 + x];
+          // rows t .. t + 3 of column lc: four scattered 2-byte stores each
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            uint32_t lo;
+            vh[t + x][lc] = (bf16_t)bf16_hi_lo(vv[x], &lo);
+            vl[t + x][lc] = (bf16_t)lo;
           }
         }
-      }
-      for (int j = ri; j < GC; ++j) {
-        const float a = at[j][ri];
-        const f32x4 dv = *reinterpret_cast<const f32x4*>(&dob[j][ci]);
+      } else {  // dv_new = e^(gl - g) (k dH) + attn^T do (K = 128, then 64)
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) av[s2] = fmaf(a, dv[s2], av[s2]);
-      }
-      const bf16_t* ub = u_in + chunk_id * GC * GD + ri * GD + cb + ci;
-      float dvv[4];
+        for (int k0 = 0; k0 < GD; k0 += 16) {
+          const bf16x8 pf = frag_row<GP>(&ks[0][0], rb + lc, k0 + 8 * lh);
+          acc = mma_bf16(pf, frag_col<BP>(&dhh[0][0], 0, k0, lane), acc);
+          acc = mma_bf16(pf, frag_col<BP>(&dhl[0][0], 0, k0, lane), acc);
+        }
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        vnb[ri][ci + s2] = bf16_to_f32(ub[s2]) - wv[s2];
-        vT[ci + s2][ri] = vnb[ri][ci + s2];
-        dvv[s2] = fmaf(ek[ri], kv[s2], av[s2]);
-        dvb[ri][ci + s2] = dvv[s2];
+        for (int r = 0; r < 16; ++r) acc[r] *= ek[rb + 8 * (r / 4) + 4 * lh + r % 4];
+#pragma unroll
+        for (int k0 = 0; k0 < GC; k0 += 16) {
+          const bf16x8 qf = frag_col<BP>(&dos[0][0], 0, k0, lane);
+          acc = mma_bf16(frag_col<KP>(&ah[0][0], rb, k0, lane), qf, acc);
+          acc = mma_bf16(frag_col<KP>(&al[0][0], rb, k0, lane), qf, acc);
+        }
+        bf16_t* dub = du_out + chunk_id * GC * GD + cb + lc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int t = rb + 8 * (r / 4) + 4 * lh + r % 4;
+          uint32_t lo;
+          const bf16_t hi = (bf16_t)bf16_hi_lo(acc[r], &lo);
+          dvh[t][lc] = hi;
+          dvl[t][lc] = (bf16_t)lo;
+          dub[t * GD] = f32_to_bf16(acc[r]);
+        }
       }
-      *reinterpret_cast<uint2*>(du_out + chunk_id * GC * GD + ri * GD + cb + ci) =
-          uint2{pack_bf16x2(dvv[0], dvv[1]), pack_bf16x2(dvv[2], dvv[3])};
     }
-    __syncthreads();
-    // dqg += do h^T, dkd += v_new dH^T, dw -= dv_new h^T ([GC][GD]); dP += do v_new^T ([GC][GC])
-    for (int c = 0; c < SB; ++c) {
-      float dq0 = dob[i0][c], dq1 = dob[i0 + 1][c];
-      float vn0 = vnb[i0][c], vn1 = vnb[i0 + 1][c];
-      float dv0 = dvb[i0][c], dv1 = dvb[i0 + 1][c];
-      const f32x4 h0v = *reinterpret_cast<const f32x4*>(&hT[c][c0]), h1v = *reinterpret_cast<const f32x4*>(&hT[c][c0 + 4]);
-      const f32x4 d0v = *reinterpret_cast<const f32x4*>(&dT[c][c0]), d1v = *reinterpret_cast<const f32x4*>(&dT[c][c0 + 4]);
-      const float hv8[8] = {h0v[0], h0v[1], h0v[2], h0v[3], h1v[0], h1v[1], h1v[2], h1v[3]};
-      const float dv8[8] = {d0v[0], d0v[1], d0v[2], d0v[3], d1v[0], d1v[1], d1v[2], d1v[3]};
+    __syncthreads();  // v_new and dv_new of the block are in LDS
+    // this block's K = 32 share of the tile products
 #pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        aq[0][x] = fmaf(dq0, hv8[x], aq[0][x]);
-        aq[1][x] = fmaf(dq1, hv8[x], aq[1][x]);
-        ak[0][x] = fmaf(vn0, dv8[x], ak[0][x]);
-        ak[1][x] = fmaf(vn1, dv8[x], ak[1][x]);
-        aw[0][x] = fmaf(-dv0, hv8[x], aw[0][x]);
-        aw[1][x] = fmaf(-dv1, hv8[x], aw[1][x]);
-      }
-      const f32x4 vj = *reinterpret_cast<const f32x4*>(&vT[c][j0]);
-#pragma unroll
-      for (int y = 0; y < 4; ++y) {
-        ap[0][y] = fmaf(dq0, vj[y], ap[0][y]);
-        ap[1][y] = fmaf(dq1, vj[y], ap[1][y]);
+    for (int k0 = 0; k0 < SB; k0 += 16) {
+      const int kk = k0 + 8 * lh;
+      const bf16x8 dof = frag_row<BP>(&dos[0][0], tr + lc, kk);
+      const bf16x8 qhh = frag_row<BP>(&hh[0][0], dr + lc, kk), qhl = frag_row<BP>(&hl[0][0], dr + lc, kk);
+      aq = mma_bf16(dof, qhh, aq);
+      aq = mma_bf16(dof, qhl, aq);
+      const bf16x8 pvh = frag_row<BP>(&vh[0][0], tr + lc, kk), pvl = frag_row<BP>(&vl[0][0], tr + lc, kk);
+      const bf16x8 qdh = frag_row<BP>(&dhh[0][0], dr + lc, kk);
+      ak = mma_bf16(pvh, qdh, ak);
+      ak = mma_bf16(pvh, frag_row<BP>(&dhl[0][0], dr + lc, kk), ak);
+      ak = mma_bf16(pvl, qdh, ak);
+      const bf16x8 pdh = frag_row<BP>(&dvh[0][0], tr + lc, kk), pdl = frag_row<BP>(&dvl[0][0], tr + lc, kk);
+      aw = mma_bf16(pdh, qhh, aw);
+      aw = mma_bf16(pdh, qhl, aw);
+      aw = mma_bf16(pdl, qhh, aw);
+      if (wave < 4) {  // dP tile: token rows 32 (wave / 2), columns 32 (wave % 2)
+        const int pr = 32 * (wave / 2), pc = 32 * (wave % 2);
+        const bf16x8 pdo = frag_row<BP>(&dos[0][0], pr + lc, kk);
+        ap = mma_bf16(pdo, frag_row<BP>(&vh[0][0], pc + lc, kk), ap);
+        ap = mma_bf16(pdo, frag_row<BP>(&vl[0][0], pc + lc, kk), ap);
       }
     }
   }
+  // the tiles: lane holds rows tr + 8 (r / 4) + 4 lh + r % 4, column dr + lc
   const int64_t ob = chunk_id * GC * GD;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int i = i0 + r;
-    *reinterpret_cast<f32x4*>(dqg_out + ob + i * GD + c0) = f32x4{aq[r][0], aq[r][1], aq[r][2], aq[r][3]};
-    *reinterpret_cast<f32x4*>(dqg_out + ob + i * GD + c0 + 4) = f32x4{aq[r][4], aq[r][5], aq[r][6], aq[r][7]};
-    *reinterpret_cast<f32x4*>(dkd_out + ob + i * GD + c0) = f32x4{ak[r][0], ak[r][1], ak[r][2], ak[r][3]};
-    *reinterpret_cast<f32x4*>(dkd_out + ob + i * GD + c0 + 4) = f32x4{ak[r][4], ak[r][5], ak[r][6], ak[r][7]};
-    *reinterpret_cast<u32x4*>(dw_out + ob + i * GD + c0) =
-        u32x4{pack_bf16x2(aw[r][0], aw[r][1]), pack_bf16x2(aw[r][2], aw[r][3]), pack_bf16x2(aw[r][4], aw[r][5]),
-              pack_bf16x2(aw[r][6], aw[r][7])};
-    *reinterpret_cast<f32x4*>(dp_out + chunk_id * GC * GC + i * GC + j0) =
-        f32x4{j0 <= i ? ap[r][0] : 0.f, j0 + 1 <= i ? ap[r][1] : 0.f, j0 + 2 <= i ? ap[r][2] : 0.f,
-              j0 + 3 <= i ? ap[r][3] : 0.f};
+  for (int r = 0; r < 16; ++r) {
+    const int i = tr + 8 * (r / 4) + 4 * lh + r % 4;
+    dqg_out[ob + i * GD + dr + lc] = aq[r];
+    dkd_out[ob + i * GD + dr + lc] = ak[r];
+    dw_out[ob + i * GD + dr + lc] = f32_to_bf16(-aw[r]);
+  }
+  if (wave < 4) {
+    const int pr = 32 * (wave / 2), pc = 32 * (wave % 2);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = pr + 8 * (r / 4) + 4 * lh + r % 4, j = pc + lc;
+      dp_out[chunk_id * GC * GC + i * GC + j] = j <= i ? ap[r] : 0.f;
+    }
   }
   // dgl = e^gl <dH, h>: wave sums, then the 8 waves in order
   float v = gl_part;
