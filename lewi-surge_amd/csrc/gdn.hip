@@ -55,6 +55,64 @@ __device__ __forceinline__ void load_tile(bf16_t (*dst)[GP], const bf16_t* src, 
   }
 }
 
+// bf16 matrix-core helpers.  D[32 x 32] += P[32 x 16] Q[16 x 32] (v_mfma_f32_32x32x16_bf16): lane l
+// supplies row l % 32 of P and column l % 32 of Q at k = 8 (l / 32) .. + 7, and holds D[8 (r / 4) + 4 (l / 32) + r % 4]
+// [l % 32] in acc[r].  An f32 operand goes in as two bf16 terms, hi = bf16(x) and lo = bf16(x - hi): 16 significant
+// bits, the products exact and summed in f32.
+__device__ __forceinline__ f32x16 mma_bf16(bf16x8 p, bf16x8 q, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
+}
+// 8 consecutive bf16 at (row, k) of a row-major LDS array of pitch PITCH elements (16-byte aligned rows)
+template <int PITCH>
+__device__ __forceinline__ bf16x8 frag_row(const bf16_t* base, int row, int k) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(base + row * PITCH + k));
+}
+// the same fragment with P[m][k] = A[k][m] read from a row-major A (rows k, pitch PITCH) by two transpose reads
+// (ds_read_b64_tr_b16: in a 16-lane group, source lane s points at 4 values of row kb + s / 4, columns nb + 4 (s % 4);
+// lane i receives column nb + i, rows kb .. kb + 3)
+template <int PITCH>
+__device__ __forceinline__ bf16x8 frag_col(const bf16_t* base, int mbase, int kbase, int lane) {
+  const int g = lane >> 4, s = lane & 15;
+  const int m = mbase + 16 * (g & 1) + 4 * (s & 3);
+  const int k0 = kbase + 8 * (g >> 1) + (s >> 2);
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, base + k0 * PITCH + m));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, base + (k0 + 4) * PITCH + m));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ uint32_t bf16_hi_lo(float x, uint32_t* lo) {
+  const bf16_t h = f32_to_bf16(x);
+  *lo = f32_to_bf16(x - bf16_to_f32(h));
+  return h;
+}
+// four f32 -> hi and lo bf16 quads, 8-byte stores at two row-major places
+__device__ __forceinline__ void store_hi_lo4(bf16_t* hi, bf16_t* lo, const float* x) {
+  uint32_t l[4], h[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h[i] = bf16_hi_lo(x[i], &l[i]);
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<u32x2*>(hi) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  *reinterpret_cast<u32x2*>(lo) = u32x2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+}
+
+// eight f32 -> bf16 fragment, and its hi / lo split
+__device__ __forceinline__ bf16x8 pack8(const float* f) {
+  return __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                                          pack_bf16x2(f[6], f[7])});
+}
+__device__ __forceinline__ void split8(const float* f, bf16x8& hi, bf16x8& lo) {
+  float r[8];
+  hi = pack8(f);
+  const u32x4 hw = __builtin_bit_cast(u32x4, hi);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[2 * i] = f[2 * i] - __uint_as_float(hw[i] << 16);
+    r[2 * i + 1] = f[2 * i + 1] - __uint_as_float(hw[i] & 0xffff0000u);
+  }
+  lo = pack8(r);
+}
+
 // grid (N, H, B).  Outputs per (b, h, n): u, w [GC][GD] bf16, attn [GC][GC] f32 (zero above the diagonal), gcum [GC].
 __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                                         const bf16_t* __restrict__ v, const float* __restrict__ g,
@@ -93,45 +151,37 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
     gcum_out[chunk_id * GC + tid] = x;
   }
   __syncthreads();
-  // S (strictly lower) and attn (lower incl. diagonal), 2 x 4 entries per thread, dot products over GD
+  // S = (k beta) k^T (strictly lower) and attn = (q scale) k^T (lower incl. diagonal), decayed: one 32 x 32 tile per
+  // wave (waves 0-3 S, 4-7 attn), K = 128 on the bf16 matrix cores (both operands bf16: the products are exact)
   {
-    const int i0 = 2 * (tid / 16), j0 = 4 * (tid % 16);
-    float sd[2][4] = {}, ad[2][4] = {};
-    const float b0 = bt[i0], b1 = bt[i0 + 1];
-    for (int d = 0; d < GD; d += 8) {
-      float kb8[2][8], q8[2][8], k8[4][8];
+    const int wave = tid >> 6, lane = tid & 63, lc = lane & 31, lh = lane >> 5;
+    const int ti = 32 * ((wave & 3) >> 1), tj = 32 * (wave & 1);
+    const bool is_s = wave < 4;
+    const float bi = bt[ti + lc];  // beta of this lane's row
+    f32x16 acc = {};
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        unpack8g(*reinterpret_cast<const u32x4*>(&ks[i0 + r][d]), kb8[r]);
-        unpack8g(*reinterpret_cast<const u32x4*>(&qs[i0 + r][d]), q8[r]);
+    for (int k0 = 0; k0 < GD; k0 += 16) {
+      const int kk = k0 + 8 * lh;
+      bf16x8 pf;
+      if (is_s) {  // k beta in the compute dtype (gdn_fast.py:78)
+        float f[8];
+        unpack8g(*reinterpret_cast<const u32x4*>(&ks[ti + lc][kk]), f);
+#pragma unroll
+        for (int x = 0; x < 8; ++x) f[x] *= bi;
+        pf = pack8(f);
+      } else {
+        pf = frag_row<GP>(&qs[0][0], ti + lc, kk);
       }
-#pragma unroll
-      for (int x = 0; x < 8; ++x) {  // k beta in the compute dtype (gdn_fast.py:78)
-        kb8[0][x] = bf16_to_f32(f32_to_bf16(kb8[0][x] * b0));
-        kb8[1][x] = bf16_to_f32(f32_to_bf16(kb8[1][x] * b1));
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) unpack8g(*reinterpret_cast<const u32x4*>(&ks[j0 + r][d]), k8[r]);
-#pragma unroll
-      for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            sd[r][s] = fmaf(kb8[r][x], k8[s][x], sd[r][s]);
-            ad[r][s] = fmaf(q8[r][x], k8[s][x], ad[r][s]);
-          }
+      acc = mma_bf16(pf, frag_row<GP>(&ks[0][0], tj + lc, kk), acc);
     }
     float* att = attn_out + chunk_id * GC * GC;
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int i = i0 + r, j = j0 + s;
-        const float dec = j <= i ? __expf(gc[i] - gc[j]) : 0.f;
-        Sm[i][j] = j < i ? sd[r][s] * dec : 0.f;
-        att[i * GC + j] = ad[r][s] * dec;
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int i = ti + 8 * (r / 4) + 4 * lh + r % 4, j = tj + lc;
+      const float dec = j <= i ? __expf(gc[i] - gc[j]) : 0.f;
+      if (is_s) Sm[i][j] = j < i ? acc[r] * dec : 0.f;
+      else att[i * GC + j] = acc[r] * dec;
+    }
   }
   __syncthreads();
   // every read of q and of raw k is done: v beta replaces q and k beta replaces k, in the compute dtype
@@ -189,24 +239,31 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
       __syncthreads();
     }
   }
-  // u = A vb, w = A (kb e^gcum): 2 rows x 8 columns of each per thread, rounded to bf16 (gdn_fast.py:88-90)
+  // u = A vb, w = (A e^gcum) kb (= A (kb e^gcum)): one 32 x 32 tile of each per wave (token rows 32 (wave / 4),
+  // columns 32 (wave % 4)), K = 64 on the bf16 matrix cores with A as hi / lo pairs; rounded to bf16
+  // (gdn_fast.py:88-90)
   {
-    const int i0 = 2 * (tid / 16), c0 = 8 * (tid % 16);
-    float ua[2][8] = {}, wa[2][8] = {};
-    for (int j = 0; j < GC; ++j) {
-      float vb8[8], kb8[8];
-      unpack8g(*reinterpret_cast<const u32x4*>(&qs[j][c0]), vb8);  // v beta
-      unpack8g(*reinterpret_cast<const u32x4*>(&ks[j][c0]), kb8);  // k beta
-      const float e = eg[j];
+    const int wave = tid >> 6, lane = tid & 63, lc = lane & 31, lh = lane >> 5;
+    const int ti = 32 * (wave >> 2), cd = 32 * (wave & 3);
+    f32x16 ua = {}, wa = {};
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const float a = Am[i0 + r][j];
+    for (int k0 = 0; k0 < GC; k0 += 16) {
+      const int kk = k0 + 8 * lh;
+      float a8[8], e8[8];
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
-          ua[r][x] = fmaf(a, vb8[x], ua[r][x]);
-          wa[r][x] = fmaf(a, kb8[x] * e, wa[r][x]);
-        }
+      for (int x = 0; x < 8; ++x) {
+        a8[x] = Am[ti + lc][kk + x];
+        e8[x] = a8[x] * eg[kk + x];
       }
+      bf16x8 ah, al, eh, el;
+      split8(a8, ah, al);
+      split8(e8, eh, el);
+      const bf16x8 qv = frag_col<GP>(&qs[0][0], cd, k0, lane);  // v beta
+      const bf16x8 qk = frag_col<GP>(&ks[0][0], cd, k0, lane);  // k beta
+      ua = mma_bf16(ah, qv, ua);
+      ua = mma_bf16(al, qv, ua);
+      wa = mma_bf16(eh, qk, wa);
+      wa = mma_bf16(el, qk, wa);
     }
     if (s_out)  // the backward reads the decayed S and A = (I + S)^-1 of every chunk
       for (int e = tid; e < GC * GC; e += GTH) {
@@ -216,57 +273,12 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
     bf16_t* ub = u_out + chunk_id * GC * GD;
     bf16_t* wb = w_out + chunk_id * GC * GD;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      *reinterpret_cast<u32x4*>(ub + (i0 + r) * GD + c0) =
-          u32x4{pack_bf16x2(ua[r][0], ua[r][1]), pack_bf16x2(ua[r][2], ua[r][3]), pack_bf16x2(ua[r][4], ua[r][5]),
-                pack_bf16x2(ua[r][6], ua[r][7])};
-      *reinterpret_cast<u32x4*>(wb + (i0 + r) * GD + c0) =
-          u32x4{pack_bf16x2(wa[r][0], wa[r][1]), pack_bf16x2(wa[r][2], wa[r][3]), pack_bf16x2(wa[r][4], wa[r][5]),
-                pack_bf16x2(wa[r][6], wa[r][7])};
+    for (int r = 0; r < 16; ++r) {
+      const int i = ti + 8 * (r / 4) + 4 * lh + r % 4;
+      ub[i * GD + cd + lc] = f32_to_bf16(ua[r]);
+      wb[i * GD + cd + lc] = f32_to_bf16(wa[r]);
     }
   }
-}
-
-// grid (GD / SB, H, B): the scan over the chunks of one sequence and head for SB value columns.
-// bf16 matrix-core helpers of the scan.  D[32 x 32] += P[32 x 16] Q[16 x 32] (v_mfma_f32_32x32x16_bf16): lane l
-// supplies row l % 32 of P and column l % 32 of Q at k = 8 (l / 32) .. + 7, and holds D[8 (r / 4) + 4 (l / 32) + r % 4]
-// [l % 32] in acc[r].  An f32 operand goes in as two bf16 terms, hi = bf16(x) and lo = bf16(x - hi): 16 significant
-// bits, the products exact and summed in f32.
-__device__ __forceinline__ f32x16 mma_bf16(bf16x8 p, bf16x8 q, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
-}
-// 8 consecutive bf16 at (row, k) of a row-major LDS array of pitch PITCH elements (16-byte aligned rows)
-template <int PITCH>
-__device__ __forceinline__ bf16x8 frag_row(const bf16_t* base, int row, int k) {
-  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(base + row * PITCH + k));
-}
-// the same fragment with P[m][k] = A[k][m] read from a row-major A (rows k, pitch PITCH) by two transpose reads
-// (ds_read_b64_tr_b16: in a 16-lane group, source lane s points at 4 values of row kb + s / 4, columns nb + 4 (s % 4);
-// lane i receives column nb + i, rows kb .. kb + 3)
-template <int PITCH>
-__device__ __forceinline__ bf16x8 frag_col(const bf16_t* base, int mbase, int kbase, int lane) {
-  const int g = lane >> 4, s = lane & 15;
-  const int m = mbase + 16 * (g & 1) + 4 * (s & 3);
-  const int k0 = kbase + 8 * (g >> 1) + (s >> 2);
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, base + k0 * PITCH + m));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, base + (k0 + 4) * PITCH + m));
-  typedef short s16x8 __attribute__((ext_vector_type(8)));
-  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8, v);
-}
-__device__ __forceinline__ uint32_t bf16_hi_lo(float x, uint32_t* lo) {
-  const bf16_t h = f32_to_bf16(x);
-  *lo = f32_to_bf16(x - bf16_to_f32(h));
-  return h;
-}
-// four f32 -> hi and lo bf16 quads, 8-byte stores at two row-major places
-__device__ __forceinline__ void store_hi_lo4(bf16_t* hi, bf16_t* lo, const float* x) {
-  uint32_t l[4], h[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) h[i] = bf16_hi_lo(x[i], &l[i]);
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  *reinterpret_cast<u32x2*>(hi) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-  *reinterpret_cast<u32x2*>(lo) = u32x2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
 }
 
 // Scan over the chunks of one (32 value columns, head, sequence), on the matrix cores.  Eight waves:
