@@ -804,7 +804,26 @@ __global__ __launch_bounds__(GTH) void gdn_bgrad_kernel(const bf16_t* __restrict
   }
 }
 
-// grid (N, H, B): the chunk-local backward of one chunk and the assembly of its input gradients.
+// MFMA fragments of an f32 [GC][GC + 1] LDS matrix M as hi / lo bf16 pairs: of row r (M[r][k .. k + 7]) or of column
+// c (M[k .. k + 7][c])
+__device__ __forceinline__ void frag_rowf(const float (*M)[GC + 1], int r, int k, bf16x8& hi, bf16x8& lo) {
+  float f[8];
+#pragma unroll
+  for (int x = 0; x < 8; ++x) f[x] = M[r][k + x];
+  split8(f, hi, lo);
+}
+__device__ __forceinline__ void frag_colf(const float (*M)[GC + 1], int c, int k, bf16x8& hi, bf16x8& lo) {
+  float f[8];
+#pragma unroll
+  for (int x = 0; x < 8; ++x) f[x] = M[k + x][c];
+  split8(f, hi, lo);
+}
+
+// grid (N, H, B): the chunk-local backward of one chunk and the assembly of its input gradients, on the bf16 matrix
+// cores (f32 operands as hi / lo bf16 pairs).  The [GC][GD] products (dq, dk, dvb, dkbg, dkb terms) take one 32 x 32
+// tile per wave (token rows 32 (wave / 4), columns 32 (wave % 4)); the [GC][GC] ones (dA, X, dS) one tile per wave
+// 0-3 (rows 32 (wave / 2), columns 32 (wave % 2)).  Every global load of a phase is issued before its first use, and
+// the row and column sums for dgcum come from registers (lane shuffles, then per-wave partials in a fixed order).
 __global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const bf16_t* __restrict__ beta, const float* __restrict__ attn_in, const float* __restrict__ gcum_in,
@@ -816,265 +835,282 @@ __global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
   // T1 k, T2 q * scale, T3 k beta, T4 v beta, T5 du, T6 dw (bf16 tiles); M1 / M2 scratch [GC][GC], M3 A
   __shared__ __attribute__((aligned(16))) bf16_t T1[GC][GP], T2[GC][GP], T3[GC][GP], T4[GC][GP], T5[GC][GP], T6[GC][GP];
   __shared__ float M1[GC][GC + 1], M2[GC][GC + 1], M3[GC][GC + 1];
-  __shared__ float gc[GC], eg[GC], bt[GC], dgg[GC], rs[GC];
+  __shared__ float gc[GC], eg[GC], bt[GC];
+  __shared__ float rs1[GC], cs1[GTH / 64][GC];     // dP . P: row sums; column sums of each wave's rows
+  __shared__ float rs2[2][GC], cs2[2][GC];         // dS . S: row sums of the two column tiles, column sums of the two row tiles
+  __shared__ float rowp[2][GD / 32][GC];           // dgcum and dbeta terms: row sums of the four [GC][GD] column tiles
+  __shared__ float glw[GTH / 64];
+  constexpr int TI = GC * (GD / 8) / GTH;          // u32x4 of a bf16 [GC][GD] tile per thread
+  static_assert(TI == 2 && GC * GC / 4 / GTH == TI && GD == 128 && GTH == 512, "thread mapping of the prologue");
   const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z, N = gridDim.x;
   const int tid = threadIdx.x, t0 = n * GC;
+  const int lane = tid & 63, wave = tid >> 6, lc = lane & 31, lh = lane >> 5;
   const int64_t row0 = (int64_t)b * T;
   const int64_t chunk_id = ((int64_t)b * H + h) * N + n;
   const int64_t mo = chunk_id * GC * GC, to = chunk_id * GC * GD;
+  const int ti = 32 * (wave >> 2), cd = 32 * (wave & 3);        // [GC][GD] tile of this wave
+  const int pi = 32 * ((wave & 3) >> 1), pj = 32 * (wave & 1);  // [GC][GC] tile (waves 0-3)
+  // prologue loads: rows tid / 16 + 32 x, bf16 columns 8 (tid % 16), f32 columns 4 (tid % 16)
+  const int cq = 8 * (tid & 15), cm = 4 * (tid & 15);
+  u32x4 kr[TI], qr[TI], vr[TI], ur[TI], wr[TI];
+  f32x4 dpr[TI], pr[TI], ar[TI];
+  float bir[TI];
+#pragma unroll
+  for (int x = 0; x < TI; ++x) {
+    const int i = (tid >> 4) + 32 * x;
+    const bool in = t0 + i < T;
+    const int64_t go = ((row0 + t0 + i) * H + h) * GD + cq;
+    kr[x] = qr[x] = vr[x] = u32x4{0u, 0u, 0u, 0u};
+    bir[x] = 0.f;
+    if (in) {
+      kr[x] = *reinterpret_cast<const u32x4*>(k + go);
+      qr[x] = *reinterpret_cast<const u32x4*>(q + go);
+      vr[x] = *reinterpret_cast<const u32x4*>(v + go);
+      bir[x] = bf16_to_f32(beta[(row0 + t0 + i) * H + h]);
+    }
+    ur[x] = *reinterpret_cast<const u32x4*>(du_in + to + i * GD + cq);
+    wr[x] = *reinterpret_cast<const u32x4*>(dw_in + to + i * GD + cq);
+    dpr[x] = *reinterpret_cast<const f32x4*>(dp_in + mo + i * GC + cm);
+    pr[x] = *reinterpret_cast<const f32x4*>(attn_in + mo + i * GC + cm);
+    ar[x] = *reinterpret_cast<const f32x4*>(a_in + mo + i * GC + cm);
+  }
+  float gcl = 0.f, btl = 0.f;
   if (tid < GC) {
-    const int t = t0 + tid;
-    gc[tid] = gcum_in[chunk_id * GC + tid];
-    bt[tid] = t < T ? bf16_to_f32(beta[(row0 + t) * H + h]) : 0.f;
-    dgg[tid] = 0.f;
+    gcl = gcum_in[chunk_id * GC + tid];
+    if (t0 + tid < T) btl = bf16_to_f32(beta[(row0 + t0 + tid) * H + h]);
   }
-  load_tile(T1, k, row0, T, t0, H, h, 1.f);
-  load_tile(T2, q, row0, T, t0, H, h, qscale);
-  for (int e = tid; e < GC * (GD / 8); e += GTH) {
-    const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
-    *reinterpret_cast<u32x4*>(&T5[i][c]) = *reinterpret_cast<const u32x4*>(du_in + to + i * GD + c);
-    *reinterpret_cast<u32x4*>(&T6[i][c]) = *reinterpret_cast<const u32x4*>(dw_in + to + i * GD + c);
+  float sv[16];  // S in the [GC][GC] tile layout (waves 0-3), for dS . S
+  if (wave < 4)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sv[r] = s_in[mo + (pi + 8 * (r / 4) + 4 * lh + r % 4) * GC + pj + lc];
+  if (tid < GC) {
+    gc[tid] = gcl;
+    eg[tid] = __expf(gcl);
+    bt[tid] = btl;
   }
-  for (int e = tid; e < GC * GC; e += GTH) {
-    const int i = e / GC, j = e % GC;
-    M2[i][j] = dp_in[mo + e];
-    M3[i][j] = a_in[mo + e];
-    M1[i][j] = dp_in[mo + e] * attn_in[mo + e];  // dP . P: its row sums less its column sums go to dgcum
-  }
-  __syncthreads();
-  if (tid < GC) eg[tid] = __expf(gc[tid]);
-  // k beta and v beta in the compute dtype (gdn_fast.py:78, 87)
-  for (int e = tid; e < GC * (GD / 8); e += GTH) {
-    const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
-    u32x4 raw = {0u, 0u, 0u, 0u};
-    if (t0 + i < T) raw = *reinterpret_cast<const u32x4*>(v + ((row0 + t0 + i) * H + h) * GD + c);
-    float f[8], kf[8];
-    unpack8g(raw, f);
-    unpack8g(*reinterpret_cast<const u32x4*>(&T1[i][c]), kf);
-    const float bi = bt[i];
-    *reinterpret_cast<u32x4*>(&T4[i][c]) =
-        u32x4{pack_bf16x2(f[0] * bi, f[1] * bi), pack_bf16x2(f[2] * bi, f[3] * bi), pack_bf16x2(f[4] * bi, f[5] * bi),
-              pack_bf16x2(f[6] * bi, f[7] * bi)};
-    *reinterpret_cast<u32x4*>(&T3[i][c]) =
-        u32x4{pack_bf16x2(kf[0] * bi, kf[1] * bi), pack_bf16x2(kf[2] * bi, kf[3] * bi),
-              pack_bf16x2(kf[4] * bi, kf[5] * bi), pack_bf16x2(kf[6] * bi, kf[7] * bi)};
-  }
-  // row and column sums of M1 (fixed order) -> dgcum
-  auto rowcol = [&]() {
-    if (tid < GC) {
-      float r = 0.f, c = 0.f;
-      for (int j = 0; j < GC; ++j) {
-        r += M1[tid][j];
-        c += M1[j][tid];
-      }
-      dgg[tid] += r - c;
+  // k, q * scale (gdn_fast.py:56-57), k beta and v beta in the compute dtype (gdn_fast.py:78, 87), du, dw, A
+#pragma unroll
+  for (int x = 0; x < TI; ++x) {
+    const int i = (tid >> 4) + 32 * x;
+    float kf[8], qf[8], vf[8];
+    unpack8g(kr[x], kf);
+    unpack8g(qr[x], qf);
+    unpack8g(vr[x], vf);
+    const float bi = bir[x];
+#pragma unroll
+    for (int y = 0; y < 8; ++y) {
+      qf[y] *= qscale;
+      vf[y] *= bi;
+      kf[y] *= bi;
     }
-  };
-  __syncthreads();
-  rowcol();
-  __syncthreads();
-  const int i0 = 2 * (tid / 16), c0 = 8 * (tid % 16), j0 = 4 * (tid % 16);
-  const float gl = gc[GC - 1];
-  // dP_r = dP . Gi (Gi = e^(gcum_i - gcum_j), lower incl. diagonal) in place
-  for (int e = tid; e < GC * GC; e += GTH) {
-    const int i = e / GC, j = e % GC;
-    M2[i][j] = j <= i ? M2[i][j] * __expf(gc[i] - gc[j]) : 0.f;
+    *reinterpret_cast<u32x4*>(&T1[i][cq]) = kr[x];
+    *reinterpret_cast<u32x4*>(&T2[i][cq]) = __builtin_bit_cast(u32x4, pack8(qf));
+    *reinterpret_cast<u32x4*>(&T3[i][cq]) = __builtin_bit_cast(u32x4, pack8(kf));
+    *reinterpret_cast<u32x4*>(&T4[i][cq]) = __builtin_bit_cast(u32x4, pack8(vf));
+    *reinterpret_cast<u32x4*>(&T5[i][cq]) = ur[x];
+    *reinterpret_cast<u32x4*>(&T6[i][cq]) = wr[x];
+#pragma unroll
+    for (int y = 0; y < 4; ++y) M3[i][cm + y] = ar[x][y];
   }
-  __syncthreads();
-  // dq = dP_r k + dqg e^gcum ; dk = dP_r^T q + dkd e^(gl - gcum) (+ the chunk-local terms below)
-  float aq[2][8] = {}, ak[2][8] = {}, akb[2][8] = {};
-  float dgr[2] = {0.f, 0.f}, dgl_rows = 0.f;
-  for (int j = 0; j < GC; ++j) {
-    float k8[8], q8[8];
-    unpack8g(*reinterpret_cast<const u32x4*>(&T1[j][c0]), k8);
-    unpack8g(*reinterpret_cast<const u32x4*>(&T2[j][c0]), q8);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const float pij = M2[i0 + r][j], pji = M2[j][i0 + r];
-#pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        aq[r][x] = fmaf(pij, k8[x], aq[r][x]);
-        ak[r][x] = fmaf(pji, q8[x], ak[r][x]);
-      }
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int i = i0 + r;
-    const f32x4 g0 = *reinterpret_cast<const f32x4*>(dqg_in + to + i * GD + c0);
-    const f32x4 g1 = *reinterpret_cast<const f32x4*>(dqg_in + to + i * GD + c0 + 4);
-    const f32x4 d0 = *reinterpret_cast<const f32x4*>(dkd_in + to + i * GD + c0);
-    const f32x4 d1 = *reinterpret_cast<const f32x4*>(dkd_in + to + i * GD + c0 + 4);
-    const float gq[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
-    const float gk[8] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3]};
-    float q8[8], k8[8];
-    unpack8g(*reinterpret_cast<const u32x4*>(&T2[i][c0]), q8);
-    unpack8g(*reinterpret_cast<const u32x4*>(&T1[i][c0]), k8);
-    const float e = eg[i], ed = __expf(gl - gc[i]);
-#pragma unroll
-    for (int x = 0; x < 8; ++x) {
-      aq[r][x] = fmaf(gq[x], e, aq[r][x]);
-      ak[r][x] = fmaf(gk[x], ed, ak[r][x]);
-      dgr[r] = fmaf(gq[x], q8[x] * e, dgr[r]);        // + <dqg, qg>
-      const float s2 = gk[x] * k8[x] * ed;            // <dkd, kd>: - to row i, + to gl
-      dgr[r] -= s2;
-      dgl_rows += s2;
-    }
-  }
-  // dA = du vb^T + dw kbg^T  (kbg = kb e^gcum) -> M1
-  __syncthreads();  // M1's sums are read
+  // dP . P: its row sums less its column sums go to dgcum
   {
-    float acc[2][4] = {};
-    for (int c = 0; c < GD; c += 8) {
-      float du8[2][8], dw8[2][8];
+    float cs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        unpack8g(*reinterpret_cast<const u32x4*>(&T5[i0 + r][c]), du8[r]);
-        unpack8g(*reinterpret_cast<const u32x4*>(&T6[i0 + r][c]), dw8[r]);
-      }
+    for (int x = 0; x < TI; ++x) {
+      float r = 0.f;
 #pragma unroll
       for (int y = 0; y < 4; ++y) {
-        float vb8[8], kb8[8];
-        unpack8g(*reinterpret_cast<const u32x4*>(&T4[j0 + y][c]), vb8);
-        unpack8g(*reinterpret_cast<const u32x4*>(&T3[j0 + y][c]), kb8);
-        const float e = eg[j0 + y];
-#pragma unroll
-        for (int x = 0; x < 8; ++x)
-#pragma unroll
-          for (int r = 0; r < 2; ++r) acc[r][y] = fmaf(du8[r][x], vb8[x], fmaf(dw8[r][x], kb8[x] * e, acc[r][y]));
+        const float m = dpr[x][y] * pr[x][y];
+        r += m;
+        cs[y] += m;
       }
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) r += __shfl_xor(r, o, 64);
+      if ((tid & 15) == 0) rs1[(tid >> 4) + 32 * x] = r;
     }
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int y = 0; y < 4; ++y) M1[i0 + r][j0 + y] = acc[r][y];
-  }
-  __syncthreads();
-  // X = A^T dA -> M2
-  {
-    float acc[2][4] = {};
-    for (int m = 0; m < GC; ++m) {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const float a = M3[m][i0 + r];
-#pragma unroll
-        for (int y = 0; y < 4; ++y) acc[r][y] = fmaf(a, M1[m][j0 + y], acc[r][y]);
-      }
-    }
-    __syncthreads();  // every read of M2 (dP_r) is done before it is overwritten
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int y = 0; y < 4; ++y) M2[i0 + r][j0 + y] = acc[r][y];
-  }
-  __syncthreads();
-  // dS = -(X A^T), strictly lower -> M1 (dA is no longer needed); t2 = dS . S for dgcum -> M2 after X is read
-  float dsv[2][4];
-  {
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int y = 0; y < 4; ++y) dsv[r][y] = 0.f;
-    for (int m = 0; m < GC; ++m) {
-#pragma unroll
-      for (int y = 0; y < 4; ++y) {
-        const float a = M3[j0 + y][m];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) dsv[r][y] = fmaf(M2[i0 + r][m], a, dsv[r][y]);
-      }
-    }
-  }
-  __syncthreads();  // X (M2) is read
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int y = 0; y < 4; ++y) {
-      const int i = i0 + r, j = j0 + y;
-      const float ds = j < i ? -dsv[r][y] : 0.f;
-      M2[i][j] = ds * s_in[mo + i * GC + j];                        // dS . S
-      M1[i][j] = j < i ? ds * __expf(gc[i] - gc[j]) : 0.f;          // dS0 = dS . Gs
+      cs[y] += __shfl_xor(cs[y], 16, 64);
+      cs[y] += __shfl_xor(cs[y], 32, 64);
     }
+    if (lane < 16)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) cs1[wave][cm + y] = cs[y];
+  }
   __syncthreads();
-  if (tid < GC) {  // dgcum += row sums - column sums of dS . S
-    float r = 0.f, c = 0.f;
-    for (int j = 0; j < GC; ++j) {
-      r += M2[tid][j];
-      c += M2[j][tid];
-    }
-    rs[tid] = r - c;
-  }
-  // dvb = A^T du, dkbg = A^T dw; dkb = dkbg e^gcum + dS0 k; dk += dS0^T kb
-  float avb[2][8] = {}, akg[2][8] = {};
-  for (int m = 0; m < GC; ++m) {
-    float du8[8], dw8[8], k8[8], kb8[8];
-    unpack8g(*reinterpret_cast<const u32x4*>(&T5[m][c0]), du8);
-    unpack8g(*reinterpret_cast<const u32x4*>(&T6[m][c0]), dw8);
-    unpack8g(*reinterpret_cast<const u32x4*>(&T1[m][c0]), k8);
-    unpack8g(*reinterpret_cast<const u32x4*>(&T3[m][c0]), kb8);
+  // dP_r = dP . Gi (Gi = e^(gcum_i - gcum_j), lower incl. diagonal)
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const float a = M3[m][i0 + r], s0 = M1[i0 + r][m], s0t = M1[m][i0 + r];
+  for (int x = 0; x < TI; ++x) {
+    const int i = (tid >> 4) + 32 * x;
+    const float gi = gc[i];
 #pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        avb[r][x] = fmaf(a, du8[x], avb[r][x]);
-        akg[r][x] = fmaf(a, dw8[x], akg[r][x]);
-        akb[r][x] = fmaf(s0, k8[x], akb[r][x]);
-        ak[r][x] = fmaf(s0t, kb8[x], ak[r][x]);
-      }
+    for (int y = 0; y < 4; ++y) {
+      const int j = cm + y;
+      const float e = __expf(gi - gc[j]);
+      M2[i][j] = j <= i ? dpr[x][y] * e : 0.f;
     }
   }
-  float dbr[2] = {0.f, 0.f};
+  // dA = du vb^T + dw kbg^T (kbg = kb e^gcum), K = 128
+  f32x16 da1 = {}, da2 = {};
+  if (wave < 4) {
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int i = i0 + r;
-    float k8[8], kb8[8], v8[8];
-    unpack8g(*reinterpret_cast<const u32x4*>(&T1[i][c0]), k8);
-    unpack8g(*reinterpret_cast<const u32x4*>(&T3[i][c0]), kb8);
-    u32x4 raw = {0u, 0u, 0u, 0u};
-    if (t0 + i < T) raw = *reinterpret_cast<const u32x4*>(v + ((row0 + t0 + i) * H + h) * GD + c0);
-    unpack8g(raw, v8);
-    const float e = eg[i], bi = bt[i];
-    float dvo[8], dko[8], dqo[8];
-#pragma unroll
-    for (int x = 0; x < 8; ++x) {
-      const float dkb = fmaf(akg[r][x], e, akb[r][x]);   // dkbg e^gcum + dS0 k
-      dgr[r] = fmaf(akg[r][x], kb8[x] * e, dgr[r]);      // + <dkbg, kbg>
-      dbr[r] = fmaf(avb[r][x], v8[x], fmaf(dkb, k8[x], dbr[r]));
-      dvo[x] = avb[r][x] * bi;
-      dko[x] = fmaf(dkb, bi, ak[r][x]);
-      dqo[x] = aq[r][x] * qscale;
+    for (int k0 = 0; k0 < GD; k0 += 16) {
+      const int kk = k0 + 8 * lh;
+      da1 = mma_bf16(frag_row<GP>(&T5[0][0], pi + lc, kk), frag_row<GP>(&T4[0][0], pj + lc, kk), da1);
+      da2 = mma_bf16(frag_row<GP>(&T6[0][0], pi + lc, kk), frag_row<GP>(&T3[0][0], pj + lc, kk), da2);
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) M1[pi + 8 * (r / 4) + 4 * lh + r % 4][pj + lc] = fmaf(eg[pj + lc], da2[r], da1[r]);
+  }
+  __syncthreads();
+  const float gl = gc[GC - 1];
+  // dq = dP_r k (+ dqg e^gcum in the epilogue); dk = dP_r^T q (+ dkd e^(gl - gcum) and the chunk-local terms), K = 64
+  f32x16 aq = {}, ak = {};
+#pragma unroll
+  for (int k0 = 0; k0 < GC; k0 += 16) {
+    const int kk = k0 + 8 * lh;
+    bf16x8 ph, pl;
+    frag_rowf(M2, ti + lc, kk, ph, pl);
+    const bf16x8 qk = frag_col<GP>(&T1[0][0], cd, k0, lane);
+    aq = mma_bf16(ph, qk, aq);
+    aq = mma_bf16(pl, qk, aq);
+    frag_colf(M2, ti + lc, kk, ph, pl);
+    const bf16x8 qq = frag_col<GP>(&T2[0][0], cd, k0, lane);
+    ak = mma_bf16(ph, qq, ak);
+    ak = mma_bf16(pl, qq, ak);
+  }
+  // X = A^T dA, K = 64
+  f32x16 xa = {};
+  if (wave < 4)
+#pragma unroll
+    for (int k0 = 0; k0 < GC; k0 += 16) {
+      const int kk = k0 + 8 * lh;
+      bf16x8 ph, pl, qh, ql;
+      frag_colf(M3, pi + lc, kk, ph, pl);
+      frag_colf(M1, pj + lc, kk, qh, ql);
+      xa = mma_bf16(ph, qh, xa);
+      xa = mma_bf16(ph, ql, xa);
+      xa = mma_bf16(pl, qh, xa);
+    }
+  __syncthreads();  // dP_r (M2) and dA (M1) are read
+  if (wave < 4)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) M2[pi + 8 * (r / 4) + 4 * lh + r % 4][pj + lc] = xa[r];
+  __syncthreads();
+  // dS = -(X A^T), strictly lower, K = 64; dS0 = dS . Gs -> M1; row and column sums of dS . S for dgcum
+  if (wave < 4) {
+    xa = f32x16{};
+#pragma unroll
+    for (int k0 = 0; k0 < GC; k0 += 16) {
+      const int kk = k0 + 8 * lh;
+      bf16x8 ph, pl, qh, ql;
+      frag_rowf(M2, pi + lc, kk, ph, pl);
+      frag_rowf(M3, pj + lc, kk, qh, ql);
+      xa = mma_bf16(ph, qh, xa);
+      xa = mma_bf16(ph, ql, xa);
+      xa = mma_bf16(pl, qh, xa);
+    }
+    const int j = pj + lc;
+    const float gj = gc[j];
+    float cs = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = pi + 8 * (r / 4) + 4 * lh + r % 4;
+      const float ds = j < i ? -xa[r] : 0.f;
+      const float e = __expf(gc[i] - gj);
+      M1[i][j] = j < i ? ds * e : 0.f;
+      float t = ds * sv[r];
+      cs += t;
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) t += __shfl_xor(t, o, 64);
+      if (lc == 0) rs2[wave & 1][i] = t;
+    }
+    cs += __shfl_xor(cs, 32, 64);
+    if (lh == 0) cs2[wave >> 1][j] = cs;
+  }
+  // epilogue loads, in flight during the products below
+  float gqv[16], gkv[16], v1v[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int i = ti + 8 * (r / 4) + 4 * lh + r % 4, c = cd + lc;
+    gqv[r] = dqg_in[to + i * GD + c];
+    gkv[r] = dkd_in[to + i * GD + c];
+    v1v[r] = t0 + i < T ? bf16_to_f32(v[((row0 + t0 + i) * H + h) * GD + c]) : 0.f;
+  }
+  __syncthreads();
+  // dvb = A^T du, dkbg = A^T dw; dkb = dkbg e^gcum + dS0 k; dk += dS0^T kb, K = 64
+  f32x16 avb = {}, akg = {}, akb = {};
+#pragma unroll
+  for (int k0 = 0; k0 < GC; k0 += 16) {
+    const int kk = k0 + 8 * lh;
+    bf16x8 ph, pl;
+    frag_colf(M3, ti + lc, kk, ph, pl);  // A^T
+    const bf16x8 qu = frag_col<GP>(&T5[0][0], cd, k0, lane), qw = frag_col<GP>(&T6[0][0], cd, k0, lane);
+    avb = mma_bf16(ph, qu, avb);
+    avb = mma_bf16(pl, qu, avb);
+    akg = mma_bf16(ph, qw, akg);
+    akg = mma_bf16(pl, qw, akg);
+    frag_rowf(M1, ti + lc, kk, ph, pl);  // dS0
+    const bf16x8 qk = frag_col<GP>(&T1[0][0], cd, k0, lane);
+    akb = mma_bf16(ph, qk, akb);
+    akb = mma_bf16(pl, qk, akb);
+    frag_colf(M1, ti + lc, kk, ph, pl);  // dS0^T
+    const bf16x8 qb = frag_col<GP>(&T3[0][0], cd, k0, lane);
+    ak = mma_bf16(ph, qb, ak);
+    ak = mma_bf16(pl, qb, ak);
+  }
+  float dgr[16], dbr[16], dgl_rows = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int i = ti + 8 * (r / 4) + 4 * lh + r % 4, c = cd + lc;
+    const float gq = gqv[r], gk = gkv[r];
+    const float k1 = bf16_to_f32(T1[i][c]), kb1 = bf16_to_f32(T3[i][c]);
+    const float e = eg[i], ed = __expf(gl - gc[i]), bi = bt[i];
+    aq[r] = fmaf(gq, e, aq[r]);
+    ak[r] = fmaf(gk, ed, ak[r]);
+    const float s2 = gk * k1 * ed;              // <dkd, kd>: - to row i, + to gl
+    dgl_rows += s2;
+    const float dkb = fmaf(akg[r], e, akb[r]);  // dkbg e^gcum + dS0 k
+    dgr[r] = fmaf(akg[r], kb1 * e, fmaf(gq, bf16_to_f32(T2[i][c]) * e, -s2));  // <dkbg, kbg> + <dqg, qg> - s2
+    dbr[r] = fmaf(avb[r], v1v[r], dkb * k1);
     if (t0 + i < T) {
-      const int64_t off = ((row0 + t0 + i) * H + h) * GD + c0;
-      *reinterpret_cast<u32x4*>(dq + off) = u32x4{pack_bf16x2(dqo[0], dqo[1]), pack_bf16x2(dqo[2], dqo[3]),
-                                                  pack_bf16x2(dqo[4], dqo[5]), pack_bf16x2(dqo[6], dqo[7])};
-      *reinterpret_cast<u32x4*>(dk + off) = u32x4{pack_bf16x2(dko[0], dko[1]), pack_bf16x2(dko[2], dko[3]),
-                                                  pack_bf16x2(dko[4], dko[5]), pack_bf16x2(dko[6], dko[7])};
-      *reinterpret_cast<u32x4*>(dv + off) = u32x4{pack_bf16x2(dvo[0], dvo[1]), pack_bf16x2(dvo[2], dvo[3]),
-                                                  pack_bf16x2(dvo[4], dvo[5]), pack_bf16x2(dvo[6], dvo[7])};
+      const int64_t off = ((row0 + t0 + i) * H + h) * GD + c;
+      dq[off] = f32_to_bf16(aq[r] * qscale);
+      dk[off] = f32_to_bf16(fmaf(dkb, bi, ak[r]));
+      dv[off] = f32_to_bf16(avb[r] * bi);
     }
   }
-  // per-row sums over the 16 threads of a row pair (consecutive lanes), then dgcum and dbeta in fixed order
+  // per-row sums: over the 32 columns of this lane group (xor butterfly), then the four column tiles in order
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1) {
-    dgr[0] += __shfl_xor(dgr[0], o, 64);
-    dgr[1] += __shfl_xor(dgr[1], o, 64);
-    dbr[0] += __shfl_xor(dbr[0], o, 64);
-    dbr[1] += __shfl_xor(dbr[1], o, 64);
+  for (int r = 0; r < 16; ++r) {
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      dgr[r] += __shfl_xor(dgr[r], o, 64);
+      dbr[r] += __shfl_xor(dbr[r], o, 64);
+    }
   }
-  __shared__ float dgrow[GC], dbrow[GC], glw[GTH / 64];
+  if (lc == 0)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = ti + 8 * (r / 4) + 4 * lh + r % 4;
+      rowp[0][wave & 3][i] = dgr[r];
+      rowp[1][wave & 3][i] = dbr[r];
+    }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) dgl_rows += __shfl_xor(dgl_rows, o, 64);
-  if ((tid & 63) == 0) glw[tid >> 6] = dgl_rows;
-  if ((tid & 15) == 0) {
-    dgrow[i0] = dgr[0];
-    dgrow[i0 + 1] = dgr[1];
-    dbrow[i0] = dbr[0];
-    dbrow[i0 + 1] = dbr[1];
-  }
+  if (lane == 0) glw[wave] = dgl_rows;
   __syncthreads();
   if (tid < GC) {  // dgcum of row tid, then dg = its suffix sum over the chunk (gcum = cumsum(g)), one wave
-    float x = dgg[tid] + rs[tid] + dgrow[tid];
+    float x = rs1[tid] + (rs2[0][tid] + rs2[1][tid]) - (cs2[0][tid] + cs2[1][tid]);
+    float c1 = 0.f, dbrow = 0.f;
+#pragma unroll
+    for (int w = 0; w < GTH / 64; ++w) c1 += cs1[w][tid];
+    x -= c1;
+#pragma unroll
+    for (int w = 0; w < GD / 32; ++w) {
+      x += rowp[0][w][tid];
+      dbrow += rowp[1][w][tid];
+    }
     if (tid == GC - 1) {
       float t = dgl_in[chunk_id];
       for (int w = 0; w < GTH / 64; ++w) t += glw[w];
@@ -1088,7 +1124,7 @@ __global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
     const int t = t0 + tid;
     if (t < T) {
       dg[(row0 + t) * H + h] = x;
-      dbeta[(row0 + t) * H + h] = dbrow[tid];
+      dbeta[(row0 + t) * H + h] = dbrow;
     }
   }
 }
