@@ -516,9 +516,11 @@ def gdn_bench(a):
                 "TFLOP/s": round(flops / (ms_f * 1e-3) / 1e12, 2)},
         "bwd": {"ms": round(ms_b, 4), "TFLOP/s": round(2 * flops / (ms_b * 1e-3) / 1e12, 2),
                 "note": "includes the recompute of the forward's chunk products and states"},
-        "roofline": {"bound": "valu", "achieved": round(tf, 2), "peak": 157.3, "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 157.3, "unit": "TFLOP/s",
                      "frac": round(tf / 157.3, 4), "traffic": None,
-                     "note": "f32 arithmetic on the VALU, priced against the MI355X fp32 matrix peak"}}), flush=True)
+                     "note": "f32-accurate products on the bf16 matrix cores (f32 operands split into hi/lo bf16 "
+                             "terms, 2-3 MFMAs per product); achieved counts the algorithmic flops once and is "
+                             "priced against the MI355X fp32 matrix peak, the f32 work it stands for"}}), flush=True)
 
 
 def _time_ms(fn, steps, warmup):
@@ -687,7 +689,7 @@ def main():
     ap.add_argument("--op", choices=["moe", "conv", "gdn", "permute", "ragged_dot"], default="moe",
                     help="conv: the Gated DeltaNet block's causal depthwise Conv1D (modal/fast_conv.py) at the "
                          "reference config's shape, forward + backward GB/s; gdn: its chunked gated delta rule "
-                         "forward (modal/gdn_fast.py), tokens/s; permute: the moe_permute kernels at the shapes of "
+                         "(modal/gdn_fast.py), forward + backward tokens/s; permute: the moe_permute kernels at the shapes of "
                          "colab/tpu_permute_bench.py; ragged_dot: the padded_gmm drop-in at the layer's per-weight "
                          "shapes (modal/gemm_bench.py)")
     ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")

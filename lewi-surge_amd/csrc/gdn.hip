@@ -113,6 +113,20 @@ __device__ __forceinline__ void split8(const float* f, bf16x8& hi, bf16x8& lo) {
   lo = pack8(r);
 }
 
+// Workgroup -> (value-column slice, head, sequence) of a scan grid (GD / SB, H, B).  The hardware deals workgroups to
+// the 8 XCDs round-robin by linear id; renumbering id -> (id % 8) (count / 8) + id / 8 puts the GD / SB slices of one
+// (sequence, head), which read the same q, k, w and attention tiles at the same time, on one XCD, whose L2 then
+// fetches those tiles once instead of once per slice.
+__device__ __forceinline__ void scan_ids(int& cb, int& h, int& b) {
+  const int nx = gridDim.x, total = nx * gridDim.y * gridDim.z;
+  int id = blockIdx.x + nx * (blockIdx.y + gridDim.y * blockIdx.z);
+  if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+  cb = SB * (id % nx);
+  const int bh = id / nx;
+  h = bh % gridDim.y;
+  b = bh / gridDim.y;
+}
+
 // grid (N, H, B).  Outputs per (b, h, n): u, w [GC][GD] bf16, attn [GC][GC] f32 (zero above the diagonal), gcum [GC].
 __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                                         const bf16_t* __restrict__ v, const float* __restrict__ g,
@@ -301,7 +315,8 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
   __shared__ __attribute__((aligned(16))) bf16_t vh[SB][KP], vl[SB][KP];             // v_new hi / lo [c][t]
   __shared__ __attribute__((aligned(16))) bf16_t vkh[SB][KP], vkl[SB][KP];           // e^(gl - g) v_new [c][t]
   __shared__ float gc[GC], ek[GC];  // gcum, exp(gcum_last - gcum)
-  const int cb = blockIdx.x * SB, h = blockIdx.y, b = blockIdx.z;
+  int cb, h, b;
+  scan_ids(cb, h, b);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lc = lane & 31, lh = lane >> 5;  // this lane's column of a 32 x 32 tile, and its row quad offset (x 4)
   const int64_t row0 = (int64_t)b * T;
@@ -323,7 +338,8 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
   static_assert(PP * GTH == GC * (GD / 8) && GC * GC == 8 * GTH, "scan tile split");
   u32x4 pq[PP], pk[PP], pw[PP];
   f32x4 pa[2];
-  float pg = 0.f, pu[16];
+  float pg = 0.f;
+  bf16_t pu[16];  // raw: converted after the next barrier, so the loads stay in flight behind this chunk's products
   auto fetch = [&](int n) {
     const int t0 = n * GC;
     const int64_t chunk_id = bh * N + n;
@@ -343,7 +359,7 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
     if (wave < 2) {
       const bf16_t* ub = u_in + chunk_id * GC * GD + cb + lc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pu[r] = bf16_to_f32(ub[(rb + 8 * (r / 4) + 4 * lh + r % 4) * GD]);
+      for (int r = 0; r < 16; ++r) pu[r] = ub[(rb + 8 * (r / 4) + 4 * lh + r % 4) * GD];
     }
   };
   fetch(0);
@@ -386,7 +402,7 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
     __syncthreads();
     float ub[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) ub[r] = pu[r];
+    for (int r = 0; r < 16; ++r) ub[r] = bf16_to_f32(pu[r]);
     if (n + 1 < N) fetch(n + 1);
     if (wave < 4) {  // w S (waves 0-1) or (q scale) S (waves 2-3), K = 128
       const bf16_t* P = wave < 2 ? &ws[0][0] : &qs[0][0];
@@ -486,7 +502,8 @@ __global__ __launch_bounds__(GTH) void gdn_bscan_kernel(const bf16_t* __restrict
   __shared__ __attribute__((aligned(16))) bf16_t deh[SB][KP], del_[SB][KP];          // e^g do hi / lo [c][t]
   __shared__ __attribute__((aligned(16))) bf16_t dvh[SB][KP], dvl[SB][KP];           // -dv_new hi / lo [c][t]
   __shared__ float gc[GC], ek[GC];
-  const int cb = blockIdx.x * SB, h = blockIdx.y, b = blockIdx.z;
+  int cb, h, b;
+  scan_ids(cb, h, b);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lc = lane & 31, lh = lane >> 5;
   const int64_t row0 = (int64_t)b * T;
