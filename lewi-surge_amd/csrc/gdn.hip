@@ -298,10 +298,16 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
 // Scan over the chunks of one (32 value columns, head, sequence), on the matrix cores.  Eight waves:
 //   waves 4-7 hold the state slice S [128 x 32] in their accumulators (rows 32 (wave - 4) .., one 32 x 32 tile each),
 //   waves 0-1 form w S (rows 32 wave ..) and v_new = u - w S, waves 2-3 form (q e^gcum) S and o = that + attn v_new.
-// Per chunk: stage q, w, k, attn (hi / lo) and the state (hi / lo, transposed, from waves 4-7) in LDS; products
-// w S and q S; v_new to LDS (hi / lo, and e^(gcum_last - gcum) v_new for the state update); then attn v_new and
-// S = e^gcum_last S + k^T (e^(gcum_last - gcum) v_new).  The next chunk's tiles load into registers meanwhile.
+// Per chunk, three phases between barriers:
+//   A  every thread stages its prefetched share of q (scaled), k, w, attn (hi / lo) and u in LDS;
+//   B  waves 0-3: w S or q S (K = 128); v_new to LDS as hi / lo, and e^(gcum_last - gcum) v_new for the update;
+//   C  waves 2-3: o = (q S) e^gcum + attn v_new; waves 4-7: S = e^gcum_last S + k^T (e^(gcum_last - gcum) v_new),
+//      then the new state to LDS (hi / lo, transposed) for the next chunk's phase B.
+// The next chunk's tiles load into registers while a wave is otherwise idle: waves 4-7 during phase B, waves 2-3
+// after their phase-B products, waves 0-1 during phase C.  LDS fragments of the next 16-deep step are read before
+// the MFMAs of the current one.
 constexpr int KP = GC + 8;  // pitch of the [.][GC] bf16 tiles (144 bytes)
+constexpr int UP = SB + 8;  // pitch of the u tile [GC][SB] (80 bytes)
 __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                                        const bf16_t* __restrict__ u_in, const bf16_t* __restrict__ w_in,
                                                        const float* __restrict__ attn_in,
@@ -314,6 +320,7 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
   __shared__ __attribute__((aligned(16))) bf16_t shh[SB][GP], shl[SB][GP];           // state hi / lo [c][d]
   __shared__ __attribute__((aligned(16))) bf16_t vh[SB][KP], vl[SB][KP];             // v_new hi / lo [c][t]
   __shared__ __attribute__((aligned(16))) bf16_t vkh[SB][KP], vkl[SB][KP];           // e^(gl - g) v_new [c][t]
+  __shared__ __attribute__((aligned(16))) bf16_t us[GC][UP];                          // u [t][c]
   __shared__ float gc[GC], ek[GC];  // gcum, exp(gcum_last - gcum)
   int cb, h, b;
   scan_ids(cb, h, b);
@@ -325,21 +332,31 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
   // for waves 4-7)
   const int rb = wave < 4 ? 32 * (wave & 1) : 32 * (wave - 4);
   f32x16 acc = {};  // waves 4-7: the state tile; waves 0-3: this chunk's product
-  if (wave >= 4)
+  // waves 4-7: the state entering the next chunk to LDS (hi / lo, transposed)
+  auto put_state = [&]() {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = rb + 8 * q4 + 4 * lh;
+      const float sv[4] = {acc[4 * q4], acc[4 * q4 + 1], acc[4 * q4 + 2], acc[4 * q4 + 3]};
+      store_hi_lo4(&shh[lc][d], &shl[lc][d], sv);
+    }
+  };
+  if (wave >= 4) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int d = rb + 8 * (r / 4) + 4 * lh + r % 4;
       acc[r] = h0 ? h0[(bh * GD + d) * GD + cb + lc] : 0.f;
     }
-  // The next chunk's tiles are fetched into registers while the current one computes: this thread's two 16-byte
-  // pieces of each of q, k and w (piece e = tid + GTH p: row e / 16, columns 8 (e % 16)), its eight attn values,
-  // (threads < GC) one gcum value, and (waves 0-1) the 16 u values of its v_new outputs.
+    put_state();
+  }
+  // This thread's share of the next chunk's tiles: two 16-byte pieces of each of q, k and w (piece e = tid + GTH p:
+  // row e / 16, columns 8 (e % 16)), eight attn values, (threads < GC) one gcum value and (waves 4-7) 8 u values
+  // (row (tid - 256) / 4, columns 8 ((tid - 256) % 4)).
   constexpr int PP = GC * (GD / 8) / GTH;  // pieces per thread and tile
-  static_assert(PP * GTH == GC * (GD / 8) && GC * GC == 8 * GTH, "scan tile split");
-  u32x4 pq[PP], pk[PP], pw[PP];
+  static_assert(PP * GTH == GC * (GD / 8) && GC * GC == 8 * GTH && GC * SB / 8 == GTH / 2, "scan tile split");
+  u32x4 pq[PP], pk[PP], pw[PP], pu = {0u, 0u, 0u, 0u};
   f32x4 pa[2];
   float pg = 0.f;
-  bf16_t pu[16];  // raw: converted after the next barrier, so the loads stay in flight behind this chunk's products
   auto fetch = [&](int n) {
     const int t0 = n * GC;
     const int64_t chunk_id = bh * N + n;
@@ -356,16 +373,14 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
     pa[0] = *reinterpret_cast<const f32x4*>(asrc + 4 * tid);
     pa[1] = *reinterpret_cast<const f32x4*>(asrc + 4 * (tid + GTH));
     if (tid < GC) pg = gcum_in[chunk_id * GC + tid];
-    if (wave < 2) {
-      const bf16_t* ub = u_in + chunk_id * GC * GD + cb + lc;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) pu[r] = ub[(rb + 8 * (r / 4) + 4 * lh + r % 4) * GD];
+    if (wave >= 4) {
+      const int e = tid - GTH / 2;
+      pu = *reinterpret_cast<const u32x4*>(u_in + chunk_id * GC * GD + (e / (SB / 8)) * GD + cb + 8 * (e % (SB / 8)));
     }
   };
   fetch(0);
   for (int n = 0; n < N; ++n) {
     const int t0 = n * GC;
-    const int64_t chunk_id = bh * N + n;
     __syncthreads();  // the previous chunk is done with every LDS tile
 #pragma unroll
     for (int p = 0; p < PP; ++p) {
@@ -388,31 +403,35 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
       gc[tid] = pg;
       ek[tid] = __expf(__shfl(pg, GC - 1, 64) - pg);
     }
-    if (wave >= 4) {  // the state entering chunk n: hi / lo transposed for the products, and to the backward
+    if (wave >= 4) {
+      const int e = tid - GTH / 2;
+      *reinterpret_cast<u32x4*>(&us[e / (SB / 8)][8 * (e % (SB / 8))]) = pu;
+      if (h_chunks)  // the state entering chunk n, for the backward (issued here, after this phase's load wait)
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = rb + 8 * q4 + 4 * lh;
-        const float sv[4] = {acc[4 * q4], acc[4 * q4 + 1], acc[4 * q4 + 2], acc[4 * q4 + 3]};
-        store_hi_lo4(&shh[lc][d], &shl[lc][d], sv);
-        if (h_chunks)
-#pragma unroll
-          for (int x = 0; x < 4; ++x) h_chunks[(chunk_id * GD + d + x) * GD + cb + lc] = sv[x];
-      }
+        for (int r = 0; r < 16; ++r)
+          h_chunks[((bh * N + n) * GD + rb + 8 * (r / 4) + 4 * lh + r % 4) * GD + cb + lc] = acc[r];
     }
     __syncthreads();
-    float ub[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) ub[r] = bf16_to_f32(pu[r]);
-    if (n + 1 < N) fetch(n + 1);
+    const bool more = n + 1 < N;
+    if (wave >= 4 && more) fetch(n + 1);
     if (wave < 4) {  // w S (waves 0-1) or (q scale) S (waves 2-3), K = 128
       const bf16_t* P = wave < 2 ? &ws[0][0] : &qs[0][0];
       acc = f32x16{};
-#pragma unroll
-      for (int k0 = 0; k0 < GD; k0 += 16) {
+      bf16x8 pf[2], fh[2], fl[2];
+      auto frags = [&](int s, int k0) {
         const int kk = k0 + 8 * lh;
-        const bf16x8 pf = frag_row<GP>(P, rb + lc, kk);
-        acc = mma_bf16(pf, frag_row<GP>(&shh[0][0], lc, kk), acc);
-        acc = mma_bf16(pf, frag_row<GP>(&shl[0][0], lc, kk), acc);
+        pf[s] = frag_row<GP>(P, rb + lc, kk);
+        fh[s] = frag_row<GP>(&shh[0][0], lc, kk);
+        fl[s] = frag_row<GP>(&shl[0][0], lc, kk);
+      };
+      frags(0, 0);
+#pragma unroll
+      for (int j = 0; j < GD / 16; ++j) {
+        if (j + 1 < GD / 16) frags((j + 1) & 1, 16 * (j + 1));
+        __builtin_amdgcn_sched_barrier(0);
+        acc = mma_bf16(pf[j & 1], fh[j & 1], acc);
+        acc = mma_bf16(pf[j & 1], fl[j & 1], acc);
+        __builtin_amdgcn_sched_barrier(0);
       }
       if (wave < 2) {  // v_new = u - w S, to LDS as hi / lo and, scaled by exp(gcum_last - gcum), for the update
 #pragma unroll
@@ -421,7 +440,7 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
           float vv[4], vk[4];
 #pragma unroll
           for (int x = 0; x < 4; ++x) {
-            vv[x] = ub[4 * q4 + x] - acc[4 * q4 + x];
+            vv[x] = bf16_to_f32(us[t + x][lc]) - acc[4 * q4 + x];
             vk[x] = vv[x] * ek[t + x];
           }
           store_hi_lo4(&vh[lc][t], &vl[lc][t], vv);
@@ -430,18 +449,30 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
       } else {  // inter = (q S) e^gcum
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] *= __expf(gc[rb + 8 * (r / 4) + 4 * lh + r % 4]);
+        if (more) fetch(n + 1);
       }
     }
     __syncthreads();  // v_new is in LDS
-    if (wave == 2 || wave == 3) {  // o = inter + attn v_new (attn is zero above the diagonal), K = 64
-#pragma unroll
-      for (int k0 = 0; k0 < GC; k0 += 16) {
+    if (wave < 2) {
+      if (more) fetch(n + 1);
+    } else if (wave < 4) {  // o = inter + attn v_new (attn is zero above the diagonal), K = 64
+      bf16x8 ph[2], pl[2], qh[2], ql[2];
+      auto frags = [&](int s, int k0) {
         const int kk = k0 + 8 * lh;
-        const bf16x8 ph = frag_row<KP>(&ah[0][0], rb + lc, kk), pl = frag_row<KP>(&al[0][0], rb + lc, kk);
-        const bf16x8 qh = frag_row<KP>(&vh[0][0], lc, kk);
-        acc = mma_bf16(ph, qh, acc);
-        acc = mma_bf16(ph, frag_row<KP>(&vl[0][0], lc, kk), acc);
-        acc = mma_bf16(pl, qh, acc);
+        ph[s] = frag_row<KP>(&ah[0][0], rb + lc, kk);
+        pl[s] = frag_row<KP>(&al[0][0], rb + lc, kk);
+        qh[s] = frag_row<KP>(&vh[0][0], lc, kk);
+        ql[s] = frag_row<KP>(&vl[0][0], lc, kk);
+      };
+      frags(0, 0);
+#pragma unroll
+      for (int j = 0; j < GC / 16; ++j) {
+        if (j + 1 < GC / 16) frags((j + 1) & 1, 16 * (j + 1));
+        __builtin_amdgcn_sched_barrier(0);
+        acc = mma_bf16(ph[j & 1], qh[j & 1], acc);
+        acc = mma_bf16(ph[j & 1], ql[j & 1], acc);
+        acc = mma_bf16(pl[j & 1], qh[j & 1], acc);
+        __builtin_amdgcn_sched_barrier(0);
       }
       if (o)  // the backward's recompute needs the states only
 #pragma unroll
@@ -449,17 +480,27 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
           const int t = rb + 8 * (r / 4) + 4 * lh + r % 4;
           if (t0 + t < T) o[((row0 + t0 + t) * H + h) * GD + cb + lc] = f32_to_bf16(acc[r]);
         }
-    } else if (wave >= 4) {  // S = e^gcum_last S + k^T (e^(gcum_last - gcum) v_new), K = 64
+    } else {  // S = e^gcum_last S + k^T (e^(gcum_last - gcum) v_new), K = 64
       const float el = __expf(gc[GC - 1]);
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] *= el;
-#pragma unroll
-      for (int k0 = 0; k0 < GC; k0 += 16) {
+      bf16x8 pf[2], fh[2], fl[2];
+      auto frags = [&](int s, int k0) {
         const int kk = k0 + 8 * lh;
-        const bf16x8 pf = frag_col<GP>(&ks[0][0], rb, k0, lane);
-        acc = mma_bf16(pf, frag_row<KP>(&vkh[0][0], lc, kk), acc);
-        acc = mma_bf16(pf, frag_row<KP>(&vkl[0][0], lc, kk), acc);
+        pf[s] = frag_col<GP>(&ks[0][0], rb, k0, lane);
+        fh[s] = frag_row<KP>(&vkh[0][0], lc, kk);
+        fl[s] = frag_row<KP>(&vkl[0][0], lc, kk);
+      };
+      frags(0, 0);
+#pragma unroll
+      for (int j = 0; j < GC / 16; ++j) {
+        if (j + 1 < GC / 16) frags((j + 1) & 1, 16 * (j + 1));
+        __builtin_amdgcn_sched_barrier(0);
+        acc = mma_bf16(pf[j & 1], fh[j & 1], acc);
+        acc = mma_bf16(pf[j & 1], fl[j & 1], acc);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      if (more) put_state();  // phase B of this chunk, the last reader of shh / shl, is past the barrier
     }
   }
   if (h_out && wave >= 4)
