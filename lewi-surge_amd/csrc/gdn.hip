@@ -910,32 +910,31 @@ __global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
   const int pi = 32 * ((wave & 3) >> 1), pj = 32 * (wave & 1);  // [GC][GC] tile (waves 0-3)
   // prologue loads: rows tid / 16 + 32 x, bf16 columns 8 (tid % 16), f32 columns 4 (tid % 16)
   const int cq = 8 * (tid & 15), cm = 4 * (tid & 15);
+  // Rows past T (the last chunk's tail) read row T - 1 and are zeroed where the values are used, so every load is
+  // unconditional and none waits for another.
   u32x4 kr[TI], qr[TI], vr[TI], ur[TI], wr[TI];
   f32x4 dpr[TI], pr[TI], ar[TI];
-  float bir[TI];
+  bf16_t bir[TI];
 #pragma unroll
   for (int x = 0; x < TI; ++x) {
     const int i = (tid >> 4) + 32 * x;
-    const bool in = t0 + i < T;
-    const int64_t go = ((row0 + t0 + i) * H + h) * GD + cq;
-    kr[x] = qr[x] = vr[x] = u32x4{0u, 0u, 0u, 0u};
-    bir[x] = 0.f;
-    if (in) {
-      kr[x] = *reinterpret_cast<const u32x4*>(k + go);
-      qr[x] = *reinterpret_cast<const u32x4*>(q + go);
-      vr[x] = *reinterpret_cast<const u32x4*>(v + go);
-      bir[x] = bf16_to_f32(beta[(row0 + t0 + i) * H + h]);
-    }
+    const int64_t tr = row0 + min(t0 + i, T - 1);
+    const int64_t go = (tr * H + h) * GD + cq;
+    kr[x] = *reinterpret_cast<const u32x4*>(k + go);
+    qr[x] = *reinterpret_cast<const u32x4*>(q + go);
+    vr[x] = *reinterpret_cast<const u32x4*>(v + go);
+    bir[x] = beta[tr * H + h];
     ur[x] = *reinterpret_cast<const u32x4*>(du_in + to + i * GD + cq);
     wr[x] = *reinterpret_cast<const u32x4*>(dw_in + to + i * GD + cq);
     dpr[x] = *reinterpret_cast<const f32x4*>(dp_in + mo + i * GC + cm);
     pr[x] = *reinterpret_cast<const f32x4*>(attn_in + mo + i * GC + cm);
     ar[x] = *reinterpret_cast<const f32x4*>(a_in + mo + i * GC + cm);
   }
-  float gcl = 0.f, btl = 0.f;
+  float gcl = 0.f;
+  bf16_t btr = 0;
   if (tid < GC) {
     gcl = gcum_in[chunk_id * GC + tid];
-    if (t0 + tid < T) btl = bf16_to_f32(beta[(row0 + t0 + tid) * H + h]);
+    btr = beta[(row0 + min(t0 + tid, T - 1)) * H + h];
   }
   float sv[16];  // S in the [GC][GC] tile layout (waves 0-3), for dS . S
   if (wave < 4)
@@ -944,17 +943,18 @@ __global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
   if (tid < GC) {
     gc[tid] = gcl;
     eg[tid] = __expf(gcl);
-    bt[tid] = btl;
+    bt[tid] = t0 + tid < T ? bf16_to_f32(btr) : 0.f;
   }
   // k, q * scale (gdn_fast.py:56-57), k beta and v beta in the compute dtype (gdn_fast.py:78, 87), du, dw, A
 #pragma unroll
   for (int x = 0; x < TI; ++x) {
     const int i = (tid >> 4) + 32 * x;
+    if (t0 + i >= T) kr[x] = qr[x] = vr[x] = u32x4{0u, 0u, 0u, 0u};
     float kf[8], qf[8], vf[8];
     unpack8g(kr[x], kf);
     unpack8g(qr[x], qf);
     unpack8g(vr[x], vf);
-    const float bi = bir[x];
+    const float bi = t0 + i < T ? bf16_to_f32(bir[x]) : 0.f;
 #pragma unroll
     for (int y = 0; y < 8; ++y) {
       qf[y] *= qscale;
@@ -1087,13 +1087,14 @@ __global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
     if (lh == 0) cs2[wave >> 1][j] = cs;
   }
   // epilogue loads, in flight during the products below
-  float gqv[16], gkv[16], v1v[16];
+  float gqv[16], gkv[16];
+  bf16_t v1v[16];  // raw, converted (and zeroed past T) where used
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int i = ti + 8 * (r / 4) + 4 * lh + r % 4, c = cd + lc;
     gqv[r] = dqg_in[to + i * GD + c];
     gkv[r] = dkd_in[to + i * GD + c];
-    v1v[r] = t0 + i < T ? bf16_to_f32(v[((row0 + t0 + i) * H + h) * GD + c]) : 0.f;
+    v1v[r] = v[((row0 + min(t0 + i, T - 1)) * H + h) * GD + c];
   }
   __syncthreads();
   // dvb = A^T du, dkbg = A^T dw; dkb = dkbg e^gcum + dS0 k; dk += dS0^T kb, K = 64
@@ -1130,7 +1131,7 @@ __global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
     dgl_rows += s2;
     const float dkb = fmaf(akg[r], e, akb[r]);  // dkbg e^gcum + dS0 k
     dgr[r] = fmaf(akg[r], kb1 * e, fmaf(gq, bf16_to_f32(T2[i][c]) * e, -s2));  // <dkbg, kbg> + <dqg, qg> - s2
-    dbr[r] = fmaf(avb[r], v1v[r], dkb * k1);
+    dbr[r] = fmaf(avb[r], t0 + i < T ? bf16_to_f32(v1v[r]) : 0.f, dkb * k1);
     if (t0 + i < T) {
       const int64_t off = ((row0 + t0 + i) * H + h) * GD + c;
       dq[off] = f32_to_bf16(aq[r] * qscale);
