@@ -716,44 +716,72 @@ __global__ __launch_bounds__(GTH) void gdn_bgrad_kernel(const bf16_t* __restrict
   const int lc = lane & 31, lh = lane >> 5;
   const int64_t row0 = (int64_t)b * T;
   const int64_t chunk_id = ((int64_t)b * H + h) * N + n;
-  load_tile(ks, k, row0, T, t0, H, h, 1.f);
-  for (int e = tid; e < GC * (GD / 8); e += GTH) {
-    const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
-    *reinterpret_cast<u32x4*>(&ws[i][c]) = *reinterpret_cast<const u32x4*>(w_in + chunk_id * GC * GD + i * GD + c);
-  }
-  for (int e = 4 * tid; e < GC * GC; e += 4 * GTH) {
-    const f32x4 a4 = *reinterpret_cast<const f32x4*>(attn_in + chunk_id * GC * GC + e);
-    const float av[4] = {a4[0], a4[1], a4[2], a4[3]};
-    store_hi_lo4(&ah[e / GC][e % GC], &al[e / GC][e % GC], av);
-  }
-  if (tid < GC) {
-    gc[tid] = gcum_in[chunk_id * GC + tid];
-    ek[tid] = __expf(gcum_in[chunk_id * GC + GC - 1] - gc[tid]);
+  // The setup's loads all issue before any is used (rows past T read row T - 1 and are zeroed here); the h, dH and
+  // do pieces of block cb + SB load into registers while block cb computes.
+  constexpr int TI = GC * (GD / 8) / GTH, HI = GD * SB / 4 / GTH;
+  static_assert(TI == 2 && GC * GC / 4 / GTH == TI && HI == 2 && GC * SB / 8 <= GTH, "bgrad thread mapping");
+  const float* hsrc = h_chunks + chunk_id * GD * GD;
+  const float* dsrc = dh_chunks + chunk_id * GD * GD;
+  f32x4 hv[HI], dv[HI];
+  u32x4 dov = {0u, 0u, 0u, 0u};
+  auto fetch_block = [&](int cb) {
+#pragma unroll
+    for (int x = 0; x < HI; ++x) {
+      const int e = tid + GTH * x, d = e / (SB / 4), c = 4 * (e % (SB / 4));
+      hv[x] = *reinterpret_cast<const f32x4*>(hsrc + d * GD + cb + c);
+      dv[x] = *reinterpret_cast<const f32x4*>(dsrc + d * GD + cb + c);
+    }
+    if (tid < GC * SB / 8) {
+      const int i = tid / (SB / 8), c = 8 * (tid % (SB / 8));
+      dov = *reinterpret_cast<const u32x4*>(dout + ((row0 + min(t0 + i, T - 1)) * H + h) * GD + cb + c);
+    }
+  };
+  {
+    u32x4 kr[TI], wr[TI];
+    f32x4 ar[TI];
+#pragma unroll
+    for (int x = 0; x < TI; ++x) {
+      const int e = tid + GTH * x, i = e / (GD / 8), c = 8 * (e % (GD / 8));
+      kr[x] = *reinterpret_cast<const u32x4*>(k + ((row0 + min(t0 + i, T - 1)) * H + h) * GD + c);
+      wr[x] = *reinterpret_cast<const u32x4*>(w_in + chunk_id * GC * GD + i * GD + c);
+      ar[x] = *reinterpret_cast<const f32x4*>(attn_in + chunk_id * GC * GC + 4 * e);
+    }
+    const float gcl = tid < GC ? gcum_in[chunk_id * GC + tid] : 0.f;
+    const float gll = gcum_in[chunk_id * GC + GC - 1];
+    fetch_block(0);
+#pragma unroll
+    for (int x = 0; x < TI; ++x) {
+      const int e = tid + GTH * x, i = e / (GD / 8), c = 8 * (e % (GD / 8));
+      *reinterpret_cast<u32x4*>(&ks[i][c]) = t0 + i < T ? kr[x] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(&ws[i][c]) = wr[x];
+      const float av[4] = {ar[x][0], ar[x][1], ar[x][2], ar[x][3]};
+      store_hi_lo4(&ah[(4 * e) / GC][(4 * e) % GC], &al[(4 * e) / GC][(4 * e) % GC], av);
+    }
+    if (tid < GC) {
+      gc[tid] = gcl;
+      ek[tid] = __expf(gll - gcl);
+    }
   }
   const int tr = 32 * (wave / 4), dr = 32 * (wave % 4);  // this wave's tile of the [GC][GD] accumulators
   const int rb = 32 * (wave & 1);                        // token rows of the block products (waves 0-3)
   f32x16 aq = {}, ak = {}, aw = {}, ap = {};
   float gl_part = 0.f;
-  const float* hsrc = h_chunks + chunk_id * GD * GD;
-  const float* dsrc = dh_chunks + chunk_id * GD * GD;
   for (int cb = 0; cb < GD; cb += SB) {
     __syncthreads();  // the previous block's tiles are consumed (and the setup above is done)
-    for (int e = tid; e < GD * SB / 4; e += GTH) {  // h and dH blocks: hi / lo, and <dH, h>
-      const int d = e / (SB / 4), c = 4 * (e % (SB / 4));
-      const f32x4 hv = *reinterpret_cast<const f32x4*>(hsrc + d * GD + cb + c);
-      const f32x4 dv = *reinterpret_cast<const f32x4*>(dsrc + d * GD + cb + c);
-      const float h4[4] = {hv[0], hv[1], hv[2], hv[3]}, d4[4] = {dv[0], dv[1], dv[2], dv[3]};
+#pragma unroll
+    for (int x = 0; x < HI; ++x) {  // h and dH blocks: hi / lo, and <dH, h>
+      const int e = tid + GTH * x, d = e / (SB / 4), c = 4 * (e % (SB / 4));
+      const float h4[4] = {hv[x][0], hv[x][1], hv[x][2], hv[x][3]}, d4[4] = {dv[x][0], dv[x][1], dv[x][2], dv[x][3]};
       store_hi_lo4(&hh[d][c], &hl[d][c], h4);
       store_hi_lo4(&dhh[d][c], &dhl[d][c], d4);
 #pragma unroll
-      for (int x = 0; x < 4; ++x) gl_part = fmaf(h4[x], d4[x], gl_part);
+      for (int y = 0; y < 4; ++y) gl_part = fmaf(h4[y], d4[y], gl_part);
     }
-    for (int e = tid; e < GC * SB / 8; e += GTH) {  // do block
-      const int i = e / (SB / 8), c = 8 * (e % (SB / 8));
-      *reinterpret_cast<u32x4*>(&dos[i][c]) =
-          t0 + i < T ? *reinterpret_cast<const u32x4*>(dout + ((row0 + t0 + i) * H + h) * GD + cb + c)
-                     : u32x4{0u, 0u, 0u, 0u};
+    if (tid < GC * SB / 8) {  // do block
+      const int i = tid / (SB / 8), c = 8 * (tid % (SB / 8));
+      *reinterpret_cast<u32x4*>(&dos[i][c]) = t0 + i < T ? dov : u32x4{0u, 0u, 0u, 0u};
     }
+    if (cb + SB < GD) fetch_block(cb + SB);
     __syncthreads();
     if (wave < 4) {
       f32x16 acc = {};
