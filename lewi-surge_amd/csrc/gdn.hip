@@ -37,24 +37,6 @@ __device__ __forceinline__ void unpack8g(u32x4 v, float* f) {
   }
 }
 
-// rows [t0, t0 + 64) of head h of a [B, T, H, GD] bf16 tensor (row0 = b T) into an LDS tile (zeros past T), each
-// element optionally scaled and rounded back to bf16 (scale != 1)
-__device__ __forceinline__ void load_tile(bf16_t (*dst)[GP], const bf16_t* src, int64_t row0, int T, int t0, int H,
-                                          int h, float scale) {
-  for (int e = threadIdx.x; e < GC * (GD / 8); e += GTH) {
-    const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (t0 + i < T) v = *reinterpret_cast<const u32x4*>(src + ((row0 + t0 + i) * H + h) * GD + c);
-    if (scale != 1.f) {
-      float f[8];
-      unpack8g(v, f);
-      v = u32x4{pack_bf16x2(f[0] * scale, f[1] * scale), pack_bf16x2(f[2] * scale, f[3] * scale),
-                pack_bf16x2(f[4] * scale, f[5] * scale), pack_bf16x2(f[6] * scale, f[7] * scale)};
-    }
-    *reinterpret_cast<u32x4*>(&dst[i][c]) = v;
-  }
-}
-
 // bf16 matrix-core helpers.  D[32 x 32] += P[32 x 16] Q[16 x 32] (v_mfma_f32_32x32x16_bf16): lane l
 // supplies row l % 32 of P and column l % 32 of Q at k = 8 (l / 32) .. + 7, and holds D[8 (r / 4) + 4 (l / 32) + r % 4]
 // [l % 32] in acc[r].  An f32 operand goes in as two bf16 terms, hi = bf16(x) and lo = bf16(x - hi): 16 significant
@@ -145,13 +127,41 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
   const int tid = threadIdx.x, t0 = n * GC;
   const int64_t row0 = (int64_t)b * T;
   const int64_t chunk_id = ((int64_t)b * H + h) * N + n;
-  if (tid < GC) {
-    const int t = t0 + tid;
-    gc[tid] = t < T ? g[(row0 + t) * H + h] : 0.f;
-    bt[tid] = t < T ? bf16_to_f32(beta[(row0 + t) * H + h]) : 0.f;
+  {  // every load first (rows past T read row T - 1 and are zeroed when stored), then the LDS stores
+    constexpr int TI = GC * (GD / 8) / GTH;
+    u32x4 kr[TI], qr[TI];
+#pragma unroll
+    for (int x = 0; x < TI; ++x) {
+      const int e = tid + GTH * x, i = e / (GD / 8), c = 8 * (e % (GD / 8));
+      const int64_t off = ((row0 + min(t0 + i, T - 1)) * H + h) * GD + c;
+      kr[x] = *reinterpret_cast<const u32x4*>(k + off);
+      qr[x] = *reinterpret_cast<const u32x4*>(q + off);
+    }
+    float gl = 0.f;
+    bf16_t br = 0;
+    if (tid < GC) {
+      const int64_t tr = row0 + min(t0 + tid, T - 1);
+      gl = g[tr * H + h];
+      br = beta[tr * H + h];
+    }
+#pragma unroll
+    for (int x = 0; x < TI; ++x) {
+      const int e = tid + GTH * x, i = e / (GD / 8), c = 8 * (e % (GD / 8));
+      const bool in = t0 + i < T;
+      float f[8];
+      unpack8g(qr[x], f);  // q * scale in the compute dtype (gdn_fast.py:56-57)
+      *reinterpret_cast<u32x4*>(&ks[i][c]) = in ? kr[x] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(&qs[i][c]) =
+          in ? u32x4{pack_bf16x2(f[0] * qscale, f[1] * qscale), pack_bf16x2(f[2] * qscale, f[3] * qscale),
+                     pack_bf16x2(f[4] * qscale, f[5] * qscale), pack_bf16x2(f[6] * qscale, f[7] * qscale)}
+             : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (tid < GC) {
+      const bool in = t0 + tid < T;
+      gc[tid] = in ? gl : 0.f;
+      bt[tid] = in ? bf16_to_f32(br) : 0.f;
+    }
   }
-  load_tile(ks, k, row0, T, t0, H, h, 1.f);
-  load_tile(qs, q, row0, T, t0, H, h, qscale);  // q * scale in the compute dtype (gdn_fast.py:56-57)
   __syncthreads();
   if (tid < GC) {  // inclusive cumulative sum of g over the chunk (wave 0)
     float x = gc[tid];
