@@ -46,7 +46,7 @@ CONFIGS = {  # BASELINE.json configs (T, d, E, k, f, fs, zipf bias, fwd+bwd)
 
 def fused_router(c):
     """Shapes whose router runs as one kernel (logits, top-k, softmax, the layout's per-64-token histograms)."""
-    return c["E"] in (32, 64, 128) and c["k"] <= 8 and c["d"] % 64 == 0
+    return c["E"] in (32, 64, 128, 256) and c["k"] <= 8 and c["d"] % 64 == 0
 
 
 def kernel_work(c, fp8=False):
@@ -207,8 +207,8 @@ def launch_roles(c):
     fs, f = c["fs"], c["f"]
     own = bool(fs) and fs != f  # shared expert of its own width: dense backward GEMMs on a helper stream
     r = {
-        "router_logits_kernel": ["router_topk"], "router_fused_kernel<1>": ["router_topk"],
-        "router_fused_kernel<2>": ["router_topk"], "router_fused_kernel<4>": ["router_topk"],
+        "router_logits_kernel": ["router_topk"], "router_fused_kernel<64,2>": ["router_topk"],
+        "router_fused_kernel<128,4>": ["router_topk"], "router_fused_kernel<256,4>": ["router_topk"],
         "router_select_lane_kernel<8>": ["router_select"],
         "router_select_lane_kernel<16>": ["router_select"], "router_select_kernel<1>": ["router_select"],
         "router_select_kernel<2>": ["router_select"], "router_select_kernel<4>": ["router_select"],

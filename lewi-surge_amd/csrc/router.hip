@@ -285,45 +285,57 @@ __global__ __launch_bounds__(RL_THREADS) void router_logits_kernel(const bf16_t*
 }
 
 // ---------------------------------------------------------------------------------------------- workgroup-fused path
-// Fused router of the layer (E = 32 NEG experts, k <= 8): one workgroup = 64 tokens x all E experts, 4 NEG waves.  Wave w covers
-// tokens 16 (w % 4) .. + 15 and experts 32 (w / 4) .. + 31 with the lane layout of router_logits_kernel (a row of 16
-// lanes = one token quad x 16 expert pairs), the same prefetched, bank-conflict-free staging and the same sequential
-// f32 sum over d, so the logits are bitwise those of the split path.  Then, in the same workgroup:
-//  - the logits go to HBM and to an LDS tile [64][E + 1];
-//  - top-k + softmax per token: L = 4 NEG lanes per token each keep a sorted list of their E / L = 8 experts (scanned
-//    in ascending expert order, a logit moves ahead only of strictly smaller ones), and k merge rounds take the best
-//    head of the L lists (larger logit, ties to the lower expert index) -- the order of a stable descending sort, as
-//    in router_select_lane_kernel, whose softmax (in rank order) this repeats;
+// Fused router of the layer (E = 32, 64, 128 or 256 experts, k <= 8): one workgroup = 64 tokens x all EP experts (EP =
+// E rounded up to a multiple of 64; the padding experts get zero weights and are never selected).  Each thread
+// accumulates 4 tokens x EL experts (EL = 2 or 4): per d step one f32x4 LDS read of x (its 4 tokens, the same address
+// for the 16 lanes of its row) and one EL-wide read of w, then 4 EL FMAs.  Wave w covers the token quads 4 (w % 4) ..
+// + 3 (one per row of 16 lanes) and the experts 16 EL (w / 4) ..  The sum over d is the sequential f32 fmaf chain of
+// the split path, so the logits are bitwise those of router_logits_kernel.  Then, in the same workgroup:
+//  - the logits go to HBM and to an LDS tile [64][EP + 1];
+//  - top-k + softmax per token: L = EP / (4 EL) lanes per token each keep a sorted list of their EPL = 4 EL experts
+//    (scanned in ascending expert order, a logit moves ahead only of strictly smaller ones), and k merge rounds take
+//    the best head of the L lists (larger logit, ties to the lower expert index) -- the order of a stable descending
+//    sort, as in router_select_lane_kernel, whose softmax (in rank order) this repeats;
 //  - the expert histogram of the workgroup's 64 k slots (LDS counters) -> hist[blockIdx.x][E], the layout's
 //    per-chunk counts (chunks of 64 tokens).
 // This replaces the selection kernel, the layout's histogram kernel and the logits round trip between them.
-constexpr int RF_TOK = 64, RF_DC = 64, RF_XP = RF_TOK + 4;
+// LDS: double-buffered x [DC][64] and w [DC][EP] f32 chunks (DC = 32 at EP = 256, else 64); after the d loop the
+// same bytes hold the logits tile.
+constexpr int RF_TOK = 64, RF_XP = RF_TOK + 4;
 
-template <int NEG>
-__global__ __launch_bounds__(256 * NEG) void router_fused_kernel(const bf16_t* __restrict__ x,
-                                                                 const bf16_t* __restrict__ w,
-                                                                 const float* __restrict__ bias, int T, int d, int k,
-                                                                 float* __restrict__ logits, int32_t* __restrict__ sel,
-                                                                 float* __restrict__ weights,
-                                                                 int32_t* __restrict__ hist) {
-  constexpr int E = 32 * NEG, NT = 256 * NEG, L = NT / RF_TOK, EPL = E / L;  // lanes per token, experts per lane
-  static_assert(EPL == 8, "eight experts per lane");
-  __shared__ __attribute__((aligned(16))) float xs[2][RF_DC][RF_XP];  // after the d loop: logits tile [64][E + 1]
-  __shared__ __attribute__((aligned(16))) float ws[2][RF_DC][E];
-  __shared__ int32_t cnt[E];
-  static_assert(RF_TOK * (E + 1) <= 2 * RF_DC * RF_XP, "logits tile fits the x buffers");
+template <int EP, int EL>
+__global__ __launch_bounds__(16 * EP / EL) void router_fused_kernel(const bf16_t* __restrict__ x,
+                                                                    const bf16_t* __restrict__ w,
+                                                                    const float* __restrict__ bias, int T, int d,
+                                                                    int E, int k, float* __restrict__ logits,
+                                                                    int32_t* __restrict__ sel,
+                                                                    float* __restrict__ weights,
+                                                                    int32_t* __restrict__ hist) {
+  constexpr int NT = 16 * EP / EL, L = NT / RF_TOK, EPL = EP / L;  // threads, lanes per token, experts per lane
+  constexpr int DC = EP >= 256 ? 32 : 64;
+  static_assert(EP % 64 == 0 && (EL == 2 || EL == 4) && EPL == 4 * EL && 64 % L == 0, "fused router shape");
+  constexpr int XS_EL = 2 * DC * RF_XP, WS_EL = 2 * DC * EP, TILE_EL = RF_TOK * (EP + 1);
+  constexpr int SM_EL = XS_EL + WS_EL > TILE_EL ? XS_EL + WS_EL : TILE_EL;
+  __shared__ __attribute__((aligned(16))) float sm[SM_EL];
+  __shared__ int32_t cnt[EP];
+  float(*xs)[DC][RF_XP] = reinterpret_cast<float(*)[DC][RF_XP]>(sm);
+  float(*ws)[DC][EP] = reinterpret_cast<float(*)[DC][EP]>(sm + XS_EL);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int t0 = blockIdx.x * RF_TOK;
   const int tq = 4 * (wv & 3) + (lane >> 4);    // token quad (tokens t0 + 4 tq ..)
-  const int ep = 16 * (wv >> 2) + (lane & 15);  // expert pair (experts 2 ep, 2 ep + 1)
-  float acc[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
-  for (int e = tid; e < E; e += NT) cnt[e] = 0;
-  // staging: x chunks q = tid + NT r (q < 512): token q % 64, d offset 8 (q / 64); w chunk tid: d row tid / (E / 8),
-  // experts 8 (tid % (E / 8)) ..
-  constexpr int XQ = RF_TOK * (RF_DC / 8), XR = (XQ + NT - 1) / NT;  // x chunks, per thread
+  const int eq = 16 * (wv >> 2) + (lane & 15);  // experts EL eq .. EL eq + EL - 1
+  float acc[4][EL];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int j = 0; j < EL; ++j) acc[a][j] = 0.f;
+  for (int e = tid; e < EP; e += NT) cnt[e] = 0;
+  // staging: x pieces q = tid + NT r (q < XQ): token q % 64, d offset 8 (q / 64); w pieces p = tid + NT r: d row
+  // p / (EP / 8), experts 8 (p % (EP / 8)) .. (zeros past E)
+  constexpr int XQ = RF_TOK * (DC / 8), XR = (XQ + NT - 1) / NT, WQ = DC * EP / 8, WR = WQ / NT;
+  static_assert(WR * NT == WQ, "w pieces split evenly over the threads");
   const int xtt = tid & 63;
-  const int wdd = tid / (E / 8), wec = 8 * (tid % (E / 8));
-  u32x4 xr[XR], wr;
+  u32x4 xr[XR], wr[WR];
   auto gload = [&](int d0) {
     const int t = t0 + xtt;
 #pragma unroll
@@ -331,7 +343,11 @@ __global__ __launch_bounds__(256 * NEG) void router_fused_kernel(const bf16_t* _
       const int q = tid + NT * r;
       if (q < XQ) xr[r] = t < T ? *reinterpret_cast<const u32x4*>(x + (int64_t)t * d + d0 + 8 * (q >> 6)) : u32x4{0, 0, 0, 0};
     }
-    wr = *reinterpret_cast<const u32x4*>(w + (int64_t)(d0 + wdd) * E + wec);
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      const int p = tid + NT * r, row = p / (EP / 8), e8 = 8 * (p % (EP / 8));
+      wr[r] = e8 < E ? *reinterpret_cast<const u32x4*>(w + (int64_t)(d0 + row) * E + e8) : u32x4{0, 0, 0, 0};
+    }
   };
   auto sstore = [&](int buf) {
     float v[8];
@@ -344,35 +360,55 @@ __global__ __launch_bounds__(256 * NEG) void router_fused_kernel(const bf16_t* _
         for (int i = 0; i < 8; ++i) xs[buf][8 * (q >> 6) + i][xtt] = v[i];
       }
     }
-    unpack_bf16x8(wr, v);
-    *reinterpret_cast<f32x4*>(&ws[buf][wdd][wec]) = f32x4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4*>(&ws[buf][wdd][wec + 4]) = f32x4{v[4], v[5], v[6], v[7]};
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      const int p = tid + NT * r, row = p / (EP / 8), e8 = 8 * (p % (EP / 8));
+      unpack_bf16x8(wr[r], v);
+      *reinterpret_cast<f32x4*>(&ws[buf][row][e8]) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4*>(&ws[buf][row][e8 + 4]) = f32x4{v[4], v[5], v[6], v[7]};
+    }
   };
   gload(0);
   int buf = 0;
-  for (int d0 = 0; d0 < d; d0 += RF_DC, buf ^= 1) {  // d % 64 == 0 (checked on the host)
+  for (int d0 = 0; d0 < d; d0 += DC, buf ^= 1) {  // d % 64 == 0 (checked on the host)
     sstore(buf);
     __syncthreads();
-    if (d0 + RF_DC < d) gload(d0 + RF_DC);
-    const float(*wsb)[E] = ws[buf];
+    if (d0 + DC < d) gload(d0 + DC);
 #pragma unroll 8
-    for (int dd = 0; dd < RF_DC; ++dd) logits_step<E>(acc, xs[buf][dd], wsb, dd, tq, ep);
+    for (int dd = 0; dd < DC; ++dd) {
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[buf][dd][4 * tq]);
+      float wv[EL];
+      if constexpr (EL == 4) {
+        const f32x4 w4 = *reinterpret_cast<const f32x4*>(&ws[buf][dd][4 * eq]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wv[j] = w4[j];
+      } else {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const f32x2 w2 = *reinterpret_cast<const f32x2*>(&ws[buf][dd][2 * eq]);
+        wv[0] = w2[0];
+        wv[1] = w2[1];
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int j = 0; j < EL; ++j) acc[a][j] = __builtin_fmaf(xv[a], wv[j], acc[a][j]);
+    }
   }
-  __syncthreads();  // every wave is done with the x buffers: they now hold the logits tile
-  float* lt = &xs[0][0][0];
+  __syncthreads();  // every wave is done with the staging buffers: they now hold the logits tile
+  float* lt = sm;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const int tt = 4 * tq + a, t = t0 + tt;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int e = 2 * ep + j;
-      const float v = bias ? acc[a][j] + bias[e] : acc[a][j];
-      lt[tt * (E + 1) + e] = v;
-      if (t < T) logits[(int64_t)t * E + e] = v;
+    for (int j = 0; j < EL; ++j) {
+      const int e = EL * eq + j;
+      const float v = bias && e < E ? acc[a][j] + bias[e] : acc[a][j];
+      lt[tt * (EP + 1) + e] = v;
+      if (t < T && e < E) logits[(int64_t)t * E + e] = v;
     }
   }
   __syncthreads();
-  // selection: token tid / L, lane part tid % L scans experts part, part + L, ... (ascending)
+  // selection: token tid / L, lane part tid % L scans experts part, part + L, ... (ascending, below E)
   const int tt = tid / L, part = tid % L, t = t0 + tt;
   float tv[EPL];
   int ti[EPL];
@@ -384,7 +420,8 @@ __global__ __launch_bounds__(256 * NEG) void router_fused_kernel(const bf16_t* _
 #pragma unroll
   for (int c = 0; c < EPL; ++c) {
     const int e = part + L * c;
-    const float v = lt[tt * (E + 1) + e];
+    if (e >= E) continue;
+    const float v = lt[tt * (EP + 1) + e];
     bool placed = false;
     float cv = v;
     int ci = e;
@@ -566,7 +603,7 @@ extern "C" int lsurge_router_topk(const void* x, const void* w_r, const float* b
 }
 
 bool lsurge::router_fused_ok(int64_t d, int64_t e, int64_t k) {
-  return (e == 32 || e == 64 || e == 128) && k >= 1 && k <= 8 && d >= 64 && d % 64 == 0;
+  return (e == 32 || e == 64 || e == 128 || e == 256) && k >= 1 && k <= 8 && d >= 64 && d % 64 == 0;
 }
 
 int lsurge::router_topk_impl(const void* x, const void* w_r, const float* bias, int64_t t, int64_t d, int64_t e,
@@ -582,13 +619,14 @@ int lsurge::router_topk_impl(const void* x, const void* w_r, const float* bias, 
     LSURGE_REQUIRE(logits && router_fused_ok(d, e, k), "router_topk: shape d=%lld e=%lld k=%lld has no fused kernel",
                    (long long)d, (long long)e, (long long)k);
     const dim3 grid((unsigned)((t + RF_TOK - 1) / RF_TOK));
-#define RF_CASE(NEG)                                                                                            \
-  LSURGE_LAUNCH(KID_ROUTER, s,                                                                                  \
-                hipLaunchKernelGGL(router_fused_kernel<NEG>, grid, dim3(256 * NEG), 0, s, (const bf16_t*)x,     \
-                                   (const bf16_t*)w_r, bias, (int)t, (int)d, (int)k, logits, sel, weights, hist))
-    if (e == 32) RF_CASE(1);
-    else if (e == 64) RF_CASE(2);
-    else RF_CASE(4);
+#define RF_CASE(EP, EL)                                                                                          \
+  LSURGE_LAUNCH(KID_ROUTER, s,                                                                                   \
+                hipLaunchKernelGGL((router_fused_kernel<EP, EL>), grid, dim3(16 * EP / EL), 0, s, (const bf16_t*)x, \
+                                   (const bf16_t*)w_r, bias, (int)t, (int)d, (int)e, (int)k, logits, sel, weights, \
+                                   hist))
+    if (e <= 64) RF_CASE(64, 2);
+    else if (e == 128) RF_CASE(128, 4);
+    else RF_CASE(256, 4);
 #undef RF_CASE
     if (after_logits && hipEventRecord(after_logits, s) != hipSuccess)
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "router_topk: hipEventRecord failed");
