@@ -109,7 +109,25 @@ __device__ __forceinline__ void scan_ids(int& cb, int& h, int& b) {
   b = bh / gridDim.y;
 }
 
+// MFMA fragments of an f32 [GC][GC + 1] LDS matrix M as hi / lo bf16 pairs: of row r (M[r][k .. k + 7]) or of column
+// c (M[k .. k + 7][c])
+__device__ __forceinline__ void frag_rowf(const float (*M)[GC + 1], int r, int k, bf16x8& hi, bf16x8& lo) {
+  float f[8];
+#pragma unroll
+  for (int x = 0; x < 8; ++x) f[x] = M[r][k + x];
+  split8(f, hi, lo);
+}
+__device__ __forceinline__ void frag_colf(const float (*M)[GC + 1], int c, int k, bf16x8& hi, bf16x8& lo) {
+  float f[8];
+#pragma unroll
+  for (int x = 0; x < 8; ++x) f[x] = M[k + x][c];
+  split8(f, hi, lo);
+}
+
 // grid (N, H, B).  Outputs per (b, h, n): u, w [GC][GD] bf16, attn [GC][GC] f32 (zero above the diagonal), gcum [GC].
+// A = (I + S)^-1 by blocked forward substitution, as the reference's default (gdn_fast.py:21-27, inv="solve").  The
+// reference's other mode, the Neumann product (I - S)(I + S^2)..(I + S^32), is exact in exact arithmetic but loses
+// all accuracy in f32 once keys correlate (|S| up to 0.7 makes the partial products grow like binomials).
 __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                                         const bf16_t* __restrict__ v, const float* __restrict__ g,
                                                         const bf16_t* __restrict__ beta, int T, int H, float qscale,
@@ -118,17 +136,18 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
                                                         float* __restrict__ s_out = nullptr,
                                                         float* __restrict__ a_out = nullptr) {
   // k (then k beta) and q (then v beta once the attention is done); in the S product k beta is formed from k where it
-  // is used.  72,128 bytes (70.4 KiB) of LDS: two workgroups per CU.
+  // is used.  68,864 bytes of LDS: two workgroups per CU.
   __shared__ __attribute__((aligned(16))) bf16_t ks[GC][GP], qs[GC][GP];
-  __shared__ float Sm[GC][GC + 1], Am[GC][GC + 1];
-  __shared__ float Tb[GC / 16 - 1][16][17];  // the blocked inverse's partial products of one level
+  __shared__ float Sm[GC][GC + 1], Am[GC][GC + 1];  // S (its upper triangle: scratch of the inverse); A
   __shared__ float gc[GC], eg[GC], bt[GC];
   const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z, N = gridDim.x;
   const int tid = threadIdx.x, t0 = n * GC;
+  const int wave = tid >> 6, lane = tid & 63, lc = lane & 31, lh = lane >> 5;
   const int64_t row0 = (int64_t)b * T;
   const int64_t chunk_id = ((int64_t)b * H + h) * N + n;
-  {  // every load first (rows past T read row T - 1 and are zeroed when stored), then the LDS stores
-    constexpr int TI = GC * (GD / 8) / GTH;
+  constexpr int TI = GC * (GD / 8) / GTH;
+  u32x4 vr[TI];  // v, loaded with k and q, used after the attention
+  {  // every load first (rows past T read row T - 1 and are zeroed when used), then the LDS stores
     u32x4 kr[TI], qr[TI];
 #pragma unroll
     for (int x = 0; x < TI; ++x) {
@@ -136,6 +155,7 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
       const int64_t off = ((row0 + min(t0 + i, T - 1)) * H + h) * GD + c;
       kr[x] = *reinterpret_cast<const u32x4*>(k + off);
       qr[x] = *reinterpret_cast<const u32x4*>(q + off);
+      vr[x] = *reinterpret_cast<const u32x4*>(v + off);
     }
     float gl = 0.f;
     bf16_t br = 0;
@@ -178,7 +198,6 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
   // S = (k beta) k^T (strictly lower) and attn = (q scale) k^T (lower incl. diagonal), decayed: one 32 x 32 tile per
   // wave (waves 0-3 S, 4-7 attn), K = 128 on the bf16 matrix cores (both operands bf16: the products are exact)
   {
-    const int wave = tid >> 6, lane = tid & 63, lc = lane & 31, lh = lane >> 5;
     const int ti = 32 * ((wave & 3) >> 1), tj = 32 * (wave & 1);
     const bool is_s = wave < 4;
     const float bi = bt[ti + lc];  // beta of this lane's row
@@ -203,19 +222,23 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
     for (int r = 0; r < 16; ++r) {
       const int i = ti + 8 * (r / 4) + 4 * lh + r % 4, j = tj + lc;
       const float dec = j <= i ? __expf(gc[i] - gc[j]) : 0.f;
-      if (is_s) Sm[i][j] = j < i ? acc[r] * dec : 0.f;
-      else att[i * GC + j] = acc[r] * dec;
+      if (is_s) {
+        const float sv = j < i ? acc[r] * dec : 0.f;
+        Sm[i][j] = sv;
+        if (s_out) s_out[chunk_id * GC * GC + i * GC + j] = sv;  // the backward reads the decayed S of every chunk
+      } else {
+        att[i * GC + j] = acc[r] * dec;
+      }
     }
   }
   __syncthreads();
   // every read of q and of raw k is done: v beta replaces q and k beta replaces k, in the compute dtype
   // (gdn_fast.py:78, 87), formed once here for the u and w products below
-  for (int e = tid; e < GC * (GD / 8); e += GTH) {
-    const int i = e / (GD / 8), c = 8 * (e % (GD / 8));
-    u32x4 raw = {0u, 0u, 0u, 0u};
-    if (t0 + i < T) raw = *reinterpret_cast<const u32x4*>(v + ((row0 + t0 + i) * H + h) * GD + c);
+#pragma unroll
+  for (int x = 0; x < TI; ++x) {
+    const int e = tid + GTH * x, i = e / (GD / 8), c = 8 * (e % (GD / 8));
     float f[8], kf[8];
-    unpack8g(raw, f);
+    unpack8g(t0 + i < T ? vr[x] : u32x4{0u, 0u, 0u, 0u}, f);
     unpack8g(*reinterpret_cast<const u32x4*>(&ks[i][c]), kf);
     const float bi = bt[i];
     *reinterpret_cast<u32x4*>(&qs[i][c]) =
@@ -225,49 +248,92 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
         u32x4{pack_bf16x2(kf[0] * bi, kf[1] * bi), pack_bf16x2(kf[2] * bi, kf[3] * bi),
               pack_bf16x2(kf[4] * bi, kf[5] * bi), pack_bf16x2(kf[6] * bi, kf[7] * bi)};
   }
-  // A = (I + S)^-1 in 16 x 16 blocks (L = I + S is unit lower triangular; its off-diagonal blocks are those of S):
-  //  1. the four diagonal blocks A_II = L_II^-1 at once, row by row: A[i][c] = -sum_{c <= j < i} S[i][j] A[j][c]
-  //     (c < i), A[i][i] = 1, 0 above; eight threads per column split the sum (combined by an xor butterfly);
-  //  2. block row I = 1 .. 3: A_IJ = -A_II sum_{K=J}^{I-1} S_IK A_KJ for every J < I (from L A = I), blocks above the
-  //     diagonal 0.  22 workgroup barriers where the plain row-by-row substitution takes 64.
-  {
-    for (int e = tid; e < GC * GC; e += GTH) {
-      const int r = e / GC, c = e % GC;
-      if (r / 16 != c / 16) Am[r][c] = 0.f;  // off-diagonal blocks: filled below (lower) or zero (upper)
-    }
-    const int blk = tid / 128, c = (tid % 128) / 8, part = tid % 8, o = 16 * blk;
-    for (int i = 0; i < 16; ++i) {
-      float s = 0.f;
-      for (int j = c + part; j < i; j += 8) s = fmaf(Sm[o + i][o + j], Am[o + j][o + c], s);
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
-      s += __shfl_xor(s, 4, 64);
-      if (part == 0) Am[o + i][o + c] = c < i ? -s : (c == i ? 1.f : 0.f);
-      __syncthreads();
-    }
-    for (int I = 1; I < GC / 16; ++I) {
-      for (int e = tid; e < I * 256; e += GTH) {  // T_J = sum_{K=J}^{I-1} S_IK A_KJ
-        const int J = e / 256, r = (e % 256) / 16, cc = e % 16;
-        float t = 0.f;
-        for (int m = 16 * J; m < 16 * I; ++m) t = fmaf(Sm[16 * I + r][m], Am[m][16 * J + cc], t);
-        Tb[J][r][cc] = t;
-      }
-      __syncthreads();
-      for (int e = tid; e < I * 256; e += GTH) {  // A_IJ = -A_II T_J
-        const int J = e / 256, r = (e % 256) / 16, cc = e % 16;
-        float t = 0.f;
+  // A = (I + S)^-1 (L = I + S unit lower triangular), in three steps with a workgroup barrier after each:
+  //  1. wave 0: the four diagonal 16 x 16 blocks B_b = L_bb^-1 by forward substitution: lane (b = l / 16,
+  //     c = l % 16) keeps column c of B_b in registers, row i = -sum_{j < i} S_bb[i][j] B_b[j][c] (column entries
+  //     above c are zero); the other waves zero the blocks above the diagonal;
+  //  2. waves 0-1: the 32 x 32 inverses A_pp = [[B_2p, 0], [-B_2p+1 (S_2p+1,2p B_2p), B_2p+1]], wave-local (the
+  //     partial product goes through the unused upper block of S);
+  //  3. wave 0: A_10 = -A_11 (S_10 A_00), 32 x 32 tiles on the matrix cores with operands split hi / lo.
+  // Three barriers where the row-by-row substitution takes 64.
+  if (wave == 0) {  // S is in LDS since the barrier above
+    const int o = 16 * (lane >> 4), c = lane & 15;
+    float col[16];
 #pragma unroll
-        for (int m = 0; m < 16; ++m) t = fmaf(Am[16 * I + r][16 * I + m], Tb[J][m][cc], t);
-        Am[16 * I + r][16 * J + cc] = -t;
-      }
-      __syncthreads();
+    for (int i = 0; i < 16; ++i) {
+      float sacc = 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) sacc = fmaf(Sm[o + i][o + j], col[j], sacc);
+      col[i] = c < i ? -sacc : (c == i ? 1.f : 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) Am[o + i][o + c] = col[i];
+  } else {
+    for (int e = tid - 64; e < 2 * 256 + 32 * 32; e += GTH - 64) {  // above the diagonal: two 16 blocks, one 32
+      const int r = e < 256 ? e / 16 : e < 512 ? 32 + (e - 256) / 16 : (e - 512) / 32;
+      const int c = e < 256 ? 16 + e % 16 : e < 512 ? 48 + e % 16 : 32 + (e - 512) % 32;
+      Am[r][c] = 0.f;
     }
   }
+  __syncthreads();
+  if (wave < 2) {
+    const int p = wave, ob = 32 * p, od = ob + 16;  // block 2p at ob, block 2p + 1 at od
+    const int r = lane >> 2, cq = 4 * (lane & 3);
+    float t4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const float sv = Sm[od + r][ob + m];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) t4[x] = fmaf(sv, Am[ob + m][ob + cq + x], t4[x]);
+    }
+#pragma unroll
+    for (int x = 0; x < 4; ++x) Sm[16 * p + r][32 + cq + x] = t4[x];  // S above the diagonal is no longer needed
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's partial product is in LDS
+    float x4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const float av = Am[od + r][od + m];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) x4[x] = fmaf(av, Sm[16 * p + m][32 + cq + x], x4[x]);
+    }
+#pragma unroll
+    for (int x = 0; x < 4; ++x) Am[od + r][ob + cq + x] = -x4[x];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    f32x16 y = {};
+#pragma unroll
+    for (int k0 = 0; k0 < 32; k0 += 16) {  // Y = S_10 A_00 (K = 32)
+      const int kk = k0 + 8 * lh;
+      bf16x8 ph_, pl_, qh_, ql_;
+      frag_rowf(Sm, 32 + lc, kk, ph_, pl_);
+      frag_colf(Am, lc, kk, qh_, ql_);
+      y = mma_bf16(ph_, qh_, y);
+      y = mma_bf16(ph_, ql_, y);
+      y = mma_bf16(pl_, qh_, y);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Sm[8 * (r / 4) + 4 * lh + r % 4][32 + lc] = y[r];  // into S's upper block
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    f32x16 z = {};
+#pragma unroll
+    for (int k0 = 0; k0 < 32; k0 += 16) {  // A_10 = -A_11 Y (K = 32)
+      const int kk = k0 + 8 * lh;
+      bf16x8 ph_, pl_, qh_, ql_;
+      frag_rowf(Am, 32 + lc, 32 + kk, ph_, pl_);
+      frag_colf(Sm, 32 + lc, kk, qh_, ql_);
+      z = mma_bf16(ph_, qh_, z);
+      z = mma_bf16(ph_, ql_, z);
+      z = mma_bf16(pl_, qh_, z);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Am[32 + 8 * (r / 4) + 4 * lh + r % 4][lc] = -z[r];
+  }
+  __syncthreads();
   // u = A vb, w = (A e^gcum) kb (= A (kb e^gcum)): one 32 x 32 tile of each per wave (token rows 32 (wave / 4),
   // columns 32 (wave % 4)), K = 64 on the bf16 matrix cores with A as hi / lo pairs; rounded to bf16
   // (gdn_fast.py:88-90)
   {
-    const int wave = tid >> 6, lane = tid & 63, lc = lane & 31, lh = lane >> 5;
     const int ti = 32 * (wave >> 2), cd = 32 * (wave & 3);
     f32x16 ua = {}, wa = {};
 #pragma unroll
@@ -289,11 +355,8 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
       wa = mma_bf16(eh, qk, wa);
       wa = mma_bf16(el, qk, wa);
     }
-    if (s_out)  // the backward reads the decayed S and A = (I + S)^-1 of every chunk
-      for (int e = tid; e < GC * GC; e += GTH) {
-        s_out[chunk_id * GC * GC + e] = Sm[e / GC][e % GC];
-        a_out[chunk_id * GC * GC + e] = Am[e / GC][e % GC];
-      }
+    if (a_out)  // the backward reads A = (I + S)^-1 of every chunk
+      for (int e = tid; e < GC * GC; e += GTH) a_out[chunk_id * GC * GC + e] = Am[e / GC][e % GC];
     bf16_t* ub = u_out + chunk_id * GC * GD;
     bf16_t* wb = w_out + chunk_id * GC * GD;
 #pragma unroll
@@ -898,21 +961,6 @@ __global__ __launch_bounds__(GTH) void gdn_bgrad_kernel(const bf16_t* __restrict
     for (int i = 0; i < GTH / 64; ++i) t += red[i];
     dgl_out[chunk_id] = __expf(gc[GC - 1]) * t;
   }
-}
-
-// MFMA fragments of an f32 [GC][GC + 1] LDS matrix M as hi / lo bf16 pairs: of row r (M[r][k .. k + 7]) or of column
-// c (M[k .. k + 7][c])
-__device__ __forceinline__ void frag_rowf(const float (*M)[GC + 1], int r, int k, bf16x8& hi, bf16x8& lo) {
-  float f[8];
-#pragma unroll
-  for (int x = 0; x < 8; ++x) f[x] = M[r][k + x];
-  split8(f, hi, lo);
-}
-__device__ __forceinline__ void frag_colf(const float (*M)[GC + 1], int c, int k, bf16x8& hi, bf16x8& lo) {
-  float f[8];
-#pragma unroll
-  for (int x = 0; x < 8; ++x) f[x] = M[k + x][c];
-  split8(f, hi, lo);
 }
 
 // grid (N, H, B): the chunk-local backward of one chunk and the assembly of its input gradients, on the bf16 matrix
