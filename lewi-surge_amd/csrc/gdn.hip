@@ -196,39 +196,49 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
   }
   __syncthreads();
   // S = (k beta) k^T (strictly lower) and attn = (q scale) k^T (lower incl. diagonal), decayed: one 32 x 32 tile per
-  // wave (waves 0-3 S, 4-7 attn), K = 128 on the bf16 matrix cores (both operands bf16: the products are exact)
+  // wave (waves 0-3 S, 4-7 attn), K = 128 on the bf16 matrix cores (both operands bf16: the products are exact).
+  // The wave index goes through readfirstlane so that both branches are scalar and straight-line.
   {
-    const int ti = 32 * ((wave & 3) >> 1), tj = 32 * (wave & 1);
-    const bool is_s = wave < 4;
-    const float bi = bt[ti + lc];  // beta of this lane's row
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int ti = 32 * ((wv & 3) >> 1), tj = 32 * (wv & 1), j = tj + lc;
     f32x16 acc = {};
+    if (wv < 4) {
+      const float bi = bt[ti + lc];  // beta of this lane's row
 #pragma unroll
-    for (int k0 = 0; k0 < GD; k0 += 16) {
-      const int kk = k0 + 8 * lh;
-      bf16x8 pf;
-      if (is_s) {  // k beta in the compute dtype (gdn_fast.py:78)
-        float f[8];
+      for (int k0 = 0; k0 < GD; k0 += 16) {
+        const int kk = k0 + 8 * lh;
+        float f[8];  // k beta in the compute dtype (gdn_fast.py:78)
         unpack8g(*reinterpret_cast<const u32x4*>(&ks[ti + lc][kk]), f);
 #pragma unroll
         for (int x = 0; x < 8; ++x) f[x] *= bi;
-        pf = pack8(f);
-      } else {
-        pf = frag_row<GP>(&qs[0][0], ti + lc, kk);
+        acc = mma_bf16(pack8(f), frag_row<GP>(&ks[0][0], j, kk), acc);
       }
-      acc = mma_bf16(pf, frag_row<GP>(&ks[0][0], tj + lc, kk), acc);
+    } else {
+#pragma unroll
+      for (int k0 = 0; k0 < GD; k0 += 16) {
+        const int kk = k0 + 8 * lh;
+        acc = mma_bf16(frag_row<GP>(&qs[0][0], ti + lc, kk), frag_row<GP>(&ks[0][0], j, kk), acc);
+      }
     }
-    float* att = attn_out + chunk_id * GC * GC;
+    // decay e^(gcum_i - gcum_j) for j <= i, zero above (selected, so an overflow above the diagonal never propagates)
+    const float gj = gc[j];
+    float dec[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int i = ti + 8 * (r / 4) + 4 * lh + r % 4, j = tj + lc;
-      const float dec = j <= i ? __expf(gc[i] - gc[j]) : 0.f;
-      if (is_s) {
-        const float sv = j < i ? acc[r] * dec : 0.f;
-        Sm[i][j] = sv;
-        if (s_out) s_out[chunk_id * GC * GC + i * GC + j] = sv;  // the backward reads the decayed S of every chunk
-      } else {
-        att[i * GC + j] = acc[r] * dec;
-      }
+      const int i = ti + 8 * (r / 4) + 4 * lh + r % 4;
+      const float e = __expf(gc[i] - gj);
+      dec[r] = (wv < 4 ? j < i : j <= i) ? acc[r] * e : 0.f;
+    }
+    if (wv < 4) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) Sm[ti + 8 * (r / 4) + 4 * lh + r % 4][j] = dec[r];
+      if (s_out)  // the backward reads the decayed S of every chunk
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s_out[chunk_id * GC * GC + (ti + 8 * (r / 4) + 4 * lh + r % 4) * GC + j] = dec[r];
+    } else {
+      float* att = attn_out + chunk_id * GC * GC;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) att[(ti + 8 * (r / 4) + 4 * lh + r % 4) * GC + j] = dec[r];
     }
   }
   __syncthreads();
