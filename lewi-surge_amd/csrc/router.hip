@@ -292,10 +292,10 @@ __global__ __launch_bounds__(RL_THREADS) void router_logits_kernel(const bf16_t*
 // + 3 (one per row of 16 lanes) and the experts 16 EL (w / 4) ..  The sum over d is the sequential f32 fmaf chain of
 // the split path, so the logits are bitwise those of router_logits_kernel.  Then, in the same workgroup:
 //  - the logits go to HBM and to an LDS tile [64][EP + 1];
-//  - top-k + softmax per token: L = EP / (4 EL) lanes per token each keep a sorted list of their EPL = 4 EL experts
-//    (scanned in ascending expert order, a logit moves ahead only of strictly smaller ones), and k merge rounds take
-//    the best head of the L lists (larger logit, ties to the lower expert index) -- the order of a stable descending
-//    sort, as in router_select_lane_kernel, whose softmax (in rank order) this repeats;
+//  - top-k + softmax per token: L = EP / (4 EL) lanes per token each keep a sorted list of the best 8 of their
+//    EPL = 4 EL experts (scanned in ascending expert order, a logit moves ahead only of strictly smaller ones), and
+//    k merge rounds take the best head of the L lists (larger logit, ties to the lower expert index) -- the order of
+//    a stable descending sort, as in router_select_lane_kernel, whose softmax (in rank order) this repeats;
 //  - the expert histogram of the workgroup's 64 k slots (LDS counters) -> hist[blockIdx.x][E], the layout's
 //    per-chunk counts (chunks of 64 tokens).
 // This replaces the selection kernel, the layout's histogram kernel and the logits round trip between them.
@@ -408,26 +408,27 @@ __global__ __launch_bounds__(16 * EP / EL) void router_fused_kernel(const bf16_t
     }
   }
   __syncthreads();
-  // selection: token tid / L, lane part tid % L scans experts part, part + L, ... (ascending, below E)
+  // selection: token tid / L, lane part tid % L scans experts part, part + L, ... (ascending, below E) into a sorted
+  // list of its best KL = 8 (k <= 8, so a lane's share of the top k is always in it; the rest never matter)
+  constexpr int KL = 8;
   const int tt = tid / L, part = tid % L, t = t0 + tt;
-  float tv[EPL];
-  int ti[EPL];
+  float tv[KL];
+  int ti[KL];
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) {
+  for (int j = 0; j < KL; ++j) {
     tv[j] = 0.f;
     ti[j] = -1;
   }
-#pragma unroll
+#pragma unroll 1
   for (int c = 0; c < EPL; ++c) {
     const int e = part + L * c;
-    if (e >= E) continue;
-    const float v = lt[tt * (EP + 1) + e];
-    bool placed = false;
-    float cv = v;
+    const bool valid = e < E;  // padding experts are never inserted
+    float cv = lt[tt * (EP + 1) + e];
     int ci = e;
+    bool placed = false;
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const bool g = placed || ti[j] < 0 || cv > tv[j];
+    for (int j = 0; j < KL; ++j) {
+      const bool g = valid && (placed || ti[j] < 0 || cv > tv[j]);
       const float ov = tv[j];
       const int oi = ti[j];
       tv[j] = g ? cv : ov;
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(16 * EP / EL) void router_fused_kernel(const bf16_t
     float hv = 0.f;
     int hi = -1;
 #pragma unroll
-    for (int q = 0; q < EPL; ++q)
+    for (int q = 0; q < KL; ++q)
       if (q == head) {
         hv = tv[q];
         hi = ti[q];
