@@ -343,6 +343,16 @@ int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const fl
                            const float* dh_final, void* dq, void* dk_out, void* dv_out, float* dg, float* dbeta,
                            float* dh0, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
 
+/* Row-wise l2 normalisation of the GDN block's query and key heads, the use_qk_norm_in_gdn branch of
+ * fast_chunk_gated_delta_rule (modal/gdn_fast.py:43-46, MaxText's l2norm(x, dim=-1, eps=1e-6)):
+ * y = x * rsqrt(sum(x^2) + eps) per row of dim elements, x and y bf16 [rows, dim], f32 arithmetic; rnorm [rows] f32
+ * receives rsqrt(sum(x^2) + eps) for the backward (NULL: not written).  dim a multiple of 8 in [8, 512]. */
+int lsurge_l2norm_rows(const void* x, int64_t rows, int64_t dim, float eps, void* y, float* rnorm,
+                       lsurge_stream_t stream);
+/* Its backward: dx = r dy - r^3 x (x . dy) per row (r = rnorm of the forward), x, dy and dx bf16 [rows, dim]. */
+int lsurge_l2norm_rows_bwd(const void* x, const void* dy, const float* rnorm, int64_t rows, int64_t dim, void* dx,
+                           lsurge_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Test hooks (no reference counterpart): failure injection for the error paths.
  * ------------------------------------------------------------------------------------------------ */

@@ -95,6 +95,8 @@ _SIGS = {
     "lsurge_gdn_chunked_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "lsurge_gdn_chunked_fwd": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _sz, _p]),
     "lsurge_gdn_chunked_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "lsurge_l2norm_rows": (_int, [_p, _i64, _i64, ctypes.c_float, _p, _p, _p]),
+    "lsurge_l2norm_rows_bwd": (_int, [_p, _p, _p, _i64, _i64, _p, _p]),
     "lsurge_gdn_chunked_bwd": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p,
                                       _p, _p, _sz, _p]),
     "lsurge_prof_enable": (_int, [_int]),

@@ -1284,6 +1284,58 @@ __global__ __launch_bounds__(GTH) void gdn_bchunk_kernel(
   }
 }
 
+// Row-wise l2 normalisation of the GDN block's query and key heads (use_qk_norm_in_gdn, gdn_fast.py:43-46, MaxText's
+// l2norm): y = x rsqrt(sum x^2 + eps), bf16 in and out, f32 arithmetic.  LPR = dim / 8 lanes per row (rounded up to
+// a power of two), each holding 8 consecutive elements; the row sum is a butterfly over those lanes.  rnorm keeps
+// rsqrt(sum x^2 + eps) per row for the backward: dx = r dy - r^3 x (x . dy).
+template <int LPR>
+__global__ __launch_bounds__(256) void l2norm_rows_kernel(const bf16_t* __restrict__ x, int64_t rows, int dim,
+                                                          float eps, bf16_t* __restrict__ y, float* __restrict__ rnorm) {
+  const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+  const int part = threadIdx.x % LPR, c = 8 * part;
+  const bool ok = row < rows && c < dim;
+  float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (ok) unpack8g(*reinterpret_cast<const u32x4*>(x + row * dim + c), f);
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sq = fmaf(f[i], f[i], sq);
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) sq += __shfl_xor(sq, o, 64);
+  const float r = 1.f / sqrtf(sq + eps);
+  if (ok) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] *= r;
+    *reinterpret_cast<u32x4*>(y + row * dim + c) = __builtin_bit_cast(u32x4, pack8(f));
+    if (part == 0 && rnorm) rnorm[row] = r;
+  }
+}
+template <int LPR>
+__global__ __launch_bounds__(256) void l2norm_rows_bwd_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ dy,
+                                                              const float* __restrict__ rnorm, int64_t rows, int dim,
+                                                              bf16_t* __restrict__ dx) {
+  const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+  const int part = threadIdx.x % LPR, c = 8 * part;
+  const bool ok = row < rows && c < dim;
+  float xf[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, gf[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float r = 0.f;
+  if (ok) {
+    unpack8g(*reinterpret_cast<const u32x4*>(x + row * dim + c), xf);
+    unpack8g(*reinterpret_cast<const u32x4*>(dy + row * dim + c), gf);
+    r = rnorm[row];
+  }
+  float dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dot = fmaf(xf[i], gf[i], dot);
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) dot += __shfl_xor(dot, o, 64);
+  if (ok) {
+    const float r3d = r * r * r * dot;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xf[i] = fmaf(r, gf[i], -r3d * xf[i]);
+    *reinterpret_cast<u32x4*>(dx + row * dim + c) = __builtin_bit_cast(u32x4, pack8(xf));
+  }
+}
+
 int64_t gdn_chunks(int64_t t) { return (t + GC - 1) / GC; }
 
 // f32 -> bf16 -> f32 on the host, round to nearest even (finite inputs)
@@ -1423,6 +1475,53 @@ int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const fl
                                    (const float*)p.S, (const float*)p.A, (const float*)p.dqg, (const float*)p.dkd,
                                    (const bf16_t*)p.du, (const bf16_t*)p.dw, (const float*)p.dP, (const float*)p.dgl,
                                    (int)t, (int)h, qscale, (bf16_t*)dq, (bf16_t*)dk_out, (bf16_t*)dv_out, dg, dbeta));
+  return LSURGE_OK;
+}
+
+int lsurge_l2norm_rows(const void* x, int64_t rows, int64_t dim, float eps, void* y, float* rnorm,
+                       lsurge_stream_t stream) {
+  LSURGE_REQUIRE(x && y, "l2norm_rows: null pointer");
+  LSURGE_REQUIRE(rows >= 0 && rows < (1ll << 40) && dim >= 8 && dim <= 512 && dim % 8 == 0 && eps >= 0.f,
+                 "l2norm_rows: rows=%lld dim=%lld eps=%g (dim a multiple of 8 in [8, 512], eps >= 0)", (long long)rows,
+                 (long long)dim, (double)eps);
+  LSURGE_REQUIRE(((uintptr_t)x | (uintptr_t)y) % 16 == 0, "l2norm_rows: x and y must be 16-byte aligned");
+  if (rows == 0) return LSURGE_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int lpr = dim <= 64 ? 8 : dim <= 128 ? 16 : dim <= 256 ? 32 : 64;
+  const dim3 grid((unsigned)((rows + 256 / lpr - 1) / (256 / lpr)));
+#define L2_CASE(LPR)                                                                                             \
+  LSURGE_LAUNCH(KID_MISC, s,                                                                                     \
+                hipLaunchKernelGGL(l2norm_rows_kernel<LPR>, grid, dim3(256), 0, s, (const bf16_t*)x, rows, (int)dim, \
+                                   eps, (bf16_t*)y, rnorm))
+  if (lpr == 8) L2_CASE(8);
+  else if (lpr == 16) L2_CASE(16);
+  else if (lpr == 32) L2_CASE(32);
+  else L2_CASE(64);
+#undef L2_CASE
+  return LSURGE_OK;
+}
+
+int lsurge_l2norm_rows_bwd(const void* x, const void* dy, const float* rnorm, int64_t rows, int64_t dim, void* dx,
+                           lsurge_stream_t stream) {
+  LSURGE_REQUIRE(x && dy && rnorm && dx, "l2norm_rows_bwd: null pointer");
+  LSURGE_REQUIRE(rows >= 0 && rows < (1ll << 40) && dim >= 8 && dim <= 512 && dim % 8 == 0,
+                 "l2norm_rows_bwd: rows=%lld dim=%lld (dim a multiple of 8 in [8, 512])", (long long)rows,
+                 (long long)dim);
+  LSURGE_REQUIRE(((uintptr_t)x | (uintptr_t)dy | (uintptr_t)dx) % 16 == 0,
+                 "l2norm_rows_bwd: x, dy and dx must be 16-byte aligned");
+  if (rows == 0) return LSURGE_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int lpr = dim <= 64 ? 8 : dim <= 128 ? 16 : dim <= 256 ? 32 : 64;
+  const dim3 grid((unsigned)((rows + 256 / lpr - 1) / (256 / lpr)));
+#define L2B_CASE(LPR)                                                                                               \
+  LSURGE_LAUNCH(KID_MISC, s,                                                                                        \
+                hipLaunchKernelGGL(l2norm_rows_bwd_kernel<LPR>, grid, dim3(256), 0, s, (const bf16_t*)x,           \
+                                   (const bf16_t*)dy, rnorm, rows, (int)dim, (bf16_t*)dx))
+  if (lpr == 8) L2B_CASE(8);
+  else if (lpr == 16) L2B_CASE(16);
+  else if (lpr == 32) L2B_CASE(32);
+  else L2B_CASE(64);
+#undef L2B_CASE
   return LSURGE_OK;
 }
 

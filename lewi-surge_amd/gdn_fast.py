@@ -10,6 +10,8 @@ lsurge_gdn_chunked_bwd (which recomputes the forward's chunk products and states
       dtype when initial_state is given, else None)
   install(prec, inv, unroll)   the reference's switches (gdn_fast.py:116-125): recorded, the kernels always compute in
       f32 with the exact inverse
+With use_qk_norm_in_gdn the query and key heads are l2-normalised first (gdn_fast.py:43-46) by lsurge_l2norm_rows,
+whose backward is lsurge_l2norm_rows_bwd.
 """
 from __future__ import annotations
 
@@ -58,14 +60,37 @@ class _GdnFn(torch.autograd.Function):
         return dq, dk, dv, dg, db, dh0, None
 
 
+class _L2NormFn(torch.autograd.Function):
+    """Row-wise l2 normalisation over the last axis (MaxText l2norm, eps as given), bf16 in and out."""
+
+    @staticmethod
+    def forward(ctx, x, eps):
+        rows = x.numel() // x.shape[-1]
+        y = torch.empty_like(x)
+        r = torch.empty(rows, dtype=torch.float32, device=x.device)
+        L.check(L.lib().lsurge_l2norm_rows(L.ptr(x), rows, x.shape[-1], float(eps), L.ptr(y), L.ptr(r),
+                                           L.stream(x.device)), "l2norm_rows")
+        ctx.save_for_backward(x, r)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, r = ctx.saved_tensors
+        dy = L.contig(dy.to(torch.bfloat16))
+        dx = torch.empty_like(x)
+        L.check(L.lib().lsurge_l2norm_rows_bwd(L.ptr(x), L.ptr(dy), L.ptr(r), r.numel(), x.shape[-1], L.ptr(dx),
+                                               L.stream(x.device)), "l2norm_rows_bwd")
+        return dx, None
+
+
 def fast_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
                                 use_qk_norm_in_gdn=False, cp_axis=None, compute_dtype=torch.bfloat16):
-    """modal/gdn_fast.py:37-113.  The kernels take chunks of 64, head dims of 128 and the bf16 compute dtype; the
-    reference's qk-norm and context-parallel branches (43-46, 39-42) are not built and raise NotImplementedError."""
+    """modal/gdn_fast.py:37-113.  The kernels take chunks of 64, head dims of 128 and the bf16 compute dtype.  With
+    use_qk_norm_in_gdn, query and key are l2-normalised over the head dim first (43-46; here after the cast to bf16,
+    where the reference normalises in the input dtype, the same thing for bf16 inputs).  The context-parallel branch
+    (39-42) is not built and raises NotImplementedError."""
     if cp_axis is not None:
         raise NotImplementedError("fast_chunk_gated_delta_rule: context parallelism (cp_axis) is not built")
-    if use_qk_norm_in_gdn:
-        raise NotImplementedError("fast_chunk_gated_delta_rule: the qk-norm branch is not built")
     if chunk_size != 64 or compute_dtype != torch.bfloat16:
         raise ValueError("fast_chunk_gated_delta_rule: the kernels take chunk_size=64 and a bf16 compute dtype")
     if query.shape[-1] != D or value.shape[-1] != D or key.shape != query.shape:
@@ -74,6 +99,8 @@ def fast_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initi
     L.require_cuda(query, key, value, g, beta, initial_state)
     out_dtype = query.dtype
     q, k, v = (L.contig(t.to(torch.bfloat16)) for t in (query, key, value))
+    if use_qk_norm_in_gdn:
+        q, k = _L2NormFn.apply(q, 1e-6), _L2NormFn.apply(k, 1e-6)
     bt = L.contig(beta.to(torch.bfloat16))
     gf = L.contig(g.to(torch.float32))
     h0 = None if initial_state is None else L.contig(initial_state.to(torch.float32))

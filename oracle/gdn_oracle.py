@@ -15,6 +15,10 @@ intra-chunk u and w; everything else is float64 here (the reference: float32).
 Pinned by tests/test_gdn_oracle.py: the chunked form equals the recurrence (float64, no rounding) for several
 chunk sizes, ragged lengths (padding) and an initial state; the unit-lower-triangular inverse equals numpy's
 solve and the reference's Neumann product (gdn_fast.py:21-34).
+
+`l2norm_rows` / `l2norm_rows_bwd` restate the qk-norm branch (gdn_fast.py:43-46: MaxText's l2norm, a third-party
+function absent here, y = x * rsqrt(sum(x^2) + eps) over the last axis, eps = 1e-6 as the call passes it), pinned
+by the closed-form norm of its rows, scale invariance, the zero row and central finite differences of the forward.
 """
 from __future__ import annotations
 
@@ -248,3 +252,20 @@ def gdn_chunked_bwd(q, k, v, g, beta, do, chunk=64, h0=None, dh_final=None, roun
         return a.transpose(0, 1, 3, 2).reshape(B, N * C, H)[:, :T]
 
     return (from_chunk(dq) * scale, from_chunk(dk), from_chunk(dv), from_chunk_s(dgc), from_chunk_s(dbc), dh)
+
+
+def l2norm_rows(x, eps=1e-6):
+    """y = x * rsqrt(sum(x^2) + eps) over the last axis (gdn_fast.py:43-46, MaxText l2norm), float64; returns (y, r)
+    with r = rsqrt(sum(x^2) + eps) per row."""
+    x = np.asarray(x, np.float64)
+    r = 1.0 / np.sqrt((x * x).sum(-1, keepdims=True) + eps)
+    return x * r, r[..., 0]
+
+
+def l2norm_rows_bwd(x, dy, eps=1e-6):
+    """Gradient of l2norm_rows: dx = r dy - r^3 x (x . dy) per row (d/dx of x_i r with dr/dx_j = -x_j r^3)."""
+    x = np.asarray(x, np.float64)
+    dy = np.asarray(dy, np.float64)
+    r = 1.0 / np.sqrt((x * x).sum(-1, keepdims=True) + eps)
+    return r * dy - r ** 3 * x * (x * dy).sum(-1, keepdims=True)
+

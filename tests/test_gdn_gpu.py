@@ -186,4 +186,57 @@ def test_autograd_surface(dev):
             err = mo.rel_l2(t.grad.float().cpu().numpy(), w)
             assert err < 2e-2, (n, err)
     with pytest.raises(NotImplementedError):
-        gdn_fast.fast_chunk_gated_delta_rule(*ts[:5], use_qk_norm_in_gdn=True)
+        gdn_fast.fast_chunk_gated_delta_rule(*ts[:5], cp_axis="context")
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 128), (1000, 128), (77, 64), (300, 96), (33, 512), (5, 8)])
+def test_l2norm_rows(rows, dim, dev):
+    """lsurge_l2norm_rows / _bwd against the oracle (f64): y within bf16 rounding, r to f32 accuracy, dx within the
+    bf16 rounding of its inputs and output; a zero row gives y = 0 and dx = dy / sqrt(eps)."""
+    rng = np.random.default_rng(rows + dim)
+    x = mo.round_bf16((rng.standard_normal((rows, dim)) * rng.uniform(0.1, 10, (rows, 1))).astype(np.float32))
+    x[0] = 0.0
+    dy = mo.round_bf16(rng.standard_normal((rows, dim)).astype(np.float32))
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev).to(torch.bfloat16)  # noqa: E731
+    xt, dyt = bf(x), bf(dy)
+    y = torch.empty_like(xt)
+    r = torch.empty(rows, dtype=torch.float32, device=dev)
+    dx = torch.empty_like(xt)
+    lib = L.lib()
+    L.check(lib.lsurge_l2norm_rows(L.ptr(xt), rows, dim, 1e-6, L.ptr(y), L.ptr(r), L.stream(dev)), "l2norm")
+    L.check(lib.lsurge_l2norm_rows_bwd(L.ptr(xt), L.ptr(dyt), L.ptr(r), rows, dim, L.ptr(dx), L.stream(dev)), "bwd")
+    torch.cuda.synchronize()
+    wy, wr = go.l2norm_rows(x, 1e-6)
+    wdx = go.l2norm_rows_bwd(x, dy, 1e-6)
+    gy, gr, gdx = y.float().cpu().numpy(), r.cpu().numpy(), dx.float().cpu().numpy()
+    assert np.abs(gy - wy).max() <= 2.0 ** -8 * np.abs(wy).max() + 1e-7
+    assert np.allclose(gr, wr, rtol=2e-6)
+    assert not gy[0].any() and np.allclose(gdx[0], mo.round_bf16(dy[0] * wr[0]), rtol=1e-2)
+    assert mo.rel_l2(gdx[1:], wdx[1:]) < 1e-2
+
+
+def test_qk_norm_branch(dev):
+    """use_qk_norm_in_gdn (gdn_fast.py:43-46): the forward equals the oracle on l2-normalised query and key, and the
+    query / key gradients are the oracle's chunked gradients pulled back through the l2norm."""
+    import gdn_fast
+    B, T, H = 2, 100, 2
+    rng = np.random.default_rng(41)
+    q = mo.round_bf16(rng.standard_normal((B, T, H, D)).astype(np.float32))
+    k = mo.round_bf16(rng.standard_normal((B, T, H, D)).astype(np.float32))  # not normalised: the branch does it
+    _, _, v, g, beta = _inputs(B, T, H, seed=42)
+    do = mo.round_bf16(rng.standard_normal((B, T, H, D)).astype(np.float32))
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev).to(torch.bfloat16)  # noqa: E731
+    ts = [bf(q).requires_grad_(True), bf(k).requires_grad_(True), bf(v).requires_grad_(True),
+          torch.from_numpy(g).to(dev).requires_grad_(True), bf(beta).requires_grad_(True)]
+    o, _ = gdn_fast.fast_chunk_gated_delta_rule(*ts, use_qk_norm_in_gdn=True)
+    (o.float() * torch.from_numpy(do).to(dev)).sum().backward()
+    qn = mo.round_bf16(go.l2norm_rows(q)[0].astype(np.float32))
+    kn = mo.round_bf16(go.l2norm_rows(k)[0].astype(np.float32))
+    wo, _ = go.gdn_chunked(qn, kn, v, g, beta, chunk=64, rounding="bf16")
+    assert mo.rel_l2(o.detach().float().cpu().numpy(), wo) < OH_TOL
+    want = go.gdn_chunked_bwd(qn, kn, v, g, beta, do, chunk=64, rounding="bf16")
+    dq = go.l2norm_rows_bwd(q, want[0])
+    dk = go.l2norm_rows_bwd(k, want[1])
+    for t, w, n in zip(ts, [dq, dk] + list(want[2:5]), NAMES):
+        err = mo.rel_l2(t.grad.float().cpu().numpy(), w)
+        assert err < 2e-2, (n, err)

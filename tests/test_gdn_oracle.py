@@ -164,3 +164,33 @@ def test_backward_planted_mistake_fails(monkeypatch):
     _, dk_bad, _, _, _, _ = go.gdn_chunked_bwd(q, k, v, g, beta, do, chunk=4)
     monkeypatch.undo()
     assert abs(num - dk_bad[0, 2, 0, 1]) > 1e-3
+
+
+def test_l2norm_oracle_pins():
+    """l2norm_rows against what the formula fixes: each row's norm is sqrt(s / (s + eps)) for s = |x|^2 (so 1 as
+    eps -> 0), the result is invariant to scaling a row, a zero row stays zero; l2norm_rows_bwd against central
+    finite differences of l2norm_rows (float64), and a planted sign error in the r^3 term fails that check."""
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((6, 16)) * rng.uniform(0.01, 100, (6, 1))
+    x[2] = 0.0
+    y, r = go.l2norm_rows(x, 1e-6)
+    s = (x * x).sum(-1)
+    assert np.allclose(np.linalg.norm(y, axis=-1), np.sqrt(s / (s + 1e-6)), rtol=1e-12)
+    y0, _ = go.l2norm_rows(x, 0.0 + 1e-300)
+    assert np.allclose(go.l2norm_rows(3.5 * x, 1e-300)[0][[0, 1, 3, 4, 5]], y0[[0, 1, 3, 4, 5]], rtol=1e-12)
+    assert not y[2].any() and np.isclose(r[2], 1e3)
+    dy = rng.standard_normal(x.shape)
+    dx = go.l2norm_rows_bwd(x, dy, 1e-6)
+    num = np.zeros_like(x)
+    for i in range(x.shape[0]):
+        for j in range(x.shape[1]):
+            h = 1e-6 * max(1.0, abs(x[i, j]))
+            xp, xm = x.copy(), x.copy()
+            xp[i, j] += h
+            xm[i, j] -= h
+            num[i, j] = ((go.l2norm_rows(xp, 1e-6)[0] - go.l2norm_rows(xm, 1e-6)[0]) * dy).sum() / (2 * h)
+    assert np.allclose(dx, num, rtol=1e-5, atol=1e-7 * np.abs(num).max())
+    xx = np.asarray(x, np.float64)
+    rr = 1.0 / np.sqrt((xx * xx).sum(-1, keepdims=True) + 1e-6)
+    planted = rr * dy + rr ** 3 * xx * (xx * dy).sum(-1, keepdims=True)
+    assert not np.allclose(planted, num, rtol=1e-3)
