@@ -388,7 +388,7 @@ __global__ __launch_bounds__(GTH) void gdn_chunk_kernel(const bf16_t* __restrict
 //      then the new state to LDS (hi / lo, transposed) for the next chunk's phase B.
 // The next chunk's tiles load into registers while a wave is otherwise idle: waves 4-7 during phase B, waves 2-3
 // after their phase-B products, waves 0-1 during phase C.  LDS fragments of the next 16-deep step are read before
-// the MFMAs of the current one.
+// the MFMAs of the current one, and the hi and lo products of a phase accumulate in two independent chains.
 constexpr int KP = GC + 8;  // pitch of the [.][GC] bf16 tiles (144 bytes)
 constexpr int UP = SB + 8;  // pitch of the u tile [GC][SB] (80 bytes)
 __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
@@ -500,6 +500,7 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
     if (wave < 4) {  // w S (waves 0-1) or (q scale) S (waves 2-3), K = 128
       const bf16_t* P = wave < 2 ? &ws[0][0] : &qs[0][0];
       acc = f32x16{};
+      f32x16 acc2 = {};
       bf16x8 pf[2], fh[2], fl[2];
       auto frags = [&](int s, int k0) {
         const int kk = k0 + 8 * lh;
@@ -513,9 +514,11 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
         if (j + 1 < GD / 16) frags((j + 1) & 1, 16 * (j + 1));
         __builtin_amdgcn_sched_barrier(0);
         acc = mma_bf16(pf[j & 1], fh[j & 1], acc);
-        acc = mma_bf16(pf[j & 1], fl[j & 1], acc);
+        acc2 = mma_bf16(pf[j & 1], fl[j & 1], acc2);
         __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += acc2[r];
       if (wave < 2) {  // v_new = u - w S, to LDS as hi / lo and, scaled by exp(gcum_last - gcum), for the update
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
@@ -548,15 +551,18 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
         ql[s] = frag_row<KP>(&vl[0][0], lc, kk);
       };
       frags(0, 0);
+      f32x16 acc2 = {};
 #pragma unroll
       for (int j = 0; j < GC / 16; ++j) {
         if (j + 1 < GC / 16) frags((j + 1) & 1, 16 * (j + 1));
         __builtin_amdgcn_sched_barrier(0);
         acc = mma_bf16(ph[j & 1], qh[j & 1], acc);
-        acc = mma_bf16(ph[j & 1], ql[j & 1], acc);
-        acc = mma_bf16(pl[j & 1], qh[j & 1], acc);
+        acc2 = mma_bf16(ph[j & 1], ql[j & 1], acc2);
+        acc2 = mma_bf16(pl[j & 1], qh[j & 1], acc2);
         __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += acc2[r];
       if (o)  // the backward's recompute needs the states only
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -575,14 +581,17 @@ __global__ __launch_bounds__(GTH) void gdn_scan_kernel(const bf16_t* __restrict_
         fl[s] = frag_row<KP>(&vkl[0][0], lc, kk);
       };
       frags(0, 0);
+      f32x16 acc2 = {};
 #pragma unroll
       for (int j = 0; j < GC / 16; ++j) {
         if (j + 1 < GC / 16) frags((j + 1) & 1, 16 * (j + 1));
         __builtin_amdgcn_sched_barrier(0);
         acc = mma_bf16(pf[j & 1], fh[j & 1], acc);
-        acc = mma_bf16(pf[j & 1], fl[j & 1], acc);
+        acc2 = mma_bf16(pf[j & 1], fl[j & 1], acc2);
         __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += acc2[r];
       if (more) put_state();  // phase B of this chunk, the last reader of shh / shl, is past the barrier
     }
   }
@@ -749,16 +758,19 @@ __global__ __launch_bounds__(GTH) void gdn_bscan_kernel(const bf16_t* __restrict
       const float el = __expf(gc[GC - 1]);
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] *= el;
+      f32x16 acc2 = {};  // a second, independent MFMA chain
 #pragma unroll
       for (int k0 = 0; k0 < GC; k0 += 16) {
         const int kk = k0 + 8 * lh;
         const bf16x8 pq_ = frag_col<GP>(&qs[0][0], rb, k0, lane);
         acc = mma_bf16(pq_, frag_row<KP>(&deh[0][0], lc, kk), acc);
-        acc = mma_bf16(pq_, frag_row<KP>(&del_[0][0], lc, kk), acc);
+        acc2 = mma_bf16(pq_, frag_row<KP>(&del_[0][0], lc, kk), acc2);
         const bf16x8 pw_ = frag_col<GP>(&ws[0][0], rb, k0, lane);
         acc = mma_bf16(pw_, frag_row<KP>(&dvh[0][0], lc, kk), acc);
-        acc = mma_bf16(pw_, frag_row<KP>(&dvl[0][0], lc, kk), acc);
+        acc2 = mma_bf16(pw_, frag_row<KP>(&dvl[0][0], lc, kk), acc2);
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += acc2[r];
     }
   }
   if (dh0 && wave >= 4)
