@@ -75,7 +75,7 @@ __device__ __forceinline__ int block_scan_excl(int v, int* ws, int* total) {
 // LS_REG chunks; more are read again).  The expert-level scans are block-wide shuffle scans, and the padding
 // markers of row_src are spread over all threads.  With tiles.t_expert set it also writes the 256-row tile table of
 // the layer's grouped GEMMs (see LayoutTiles).
-constexpr int LS_REG = 16;
+constexpr int LS_REG = 16, LS_BATCH = 32;
 __global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__ hist, int nchunk, int E,
                                                            int32_t* __restrict__ group_sizes,
                                                            int32_t* __restrict__ offsets,
@@ -102,13 +102,13 @@ __global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__
       for (int u = 0; u < LS_REG; ++u) v[u] = c0 + u < c1 ? hist[(int64_t)(c0 + u) * E + e_t] : 0;
 #pragma unroll
       for (int u = 0; u < LS_REG; ++u) sum += v[u];
-    } else {
-      for (int c = c0; c < c1; c += 8) {
-        int w8[8];
+    } else {  // LS_BATCH loads in flight per step: the scan is one round trip per batch, not per 8 chunks
+      for (int c = c0; c < c1; c += LS_BATCH) {
+        int wb[LS_BATCH];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) w8[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
+        for (int u = 0; u < LS_BATCH; ++u) wb[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) sum += w8[u];
+        for (int u = 0; u < LS_BATCH; ++u) sum += wb[u];
       }
     }
     part_s[j_t * E + e_t] = sum;
@@ -133,14 +133,14 @@ __global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__
         run += v[u];
       }
     } else {
-      for (int c = c0; c < c1; c += 8) {
-        int w8[8];
+      for (int c = c0; c < c1; c += LS_BATCH) {
+        int wb[LS_BATCH];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) w8[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
+        for (int u = 0; u < LS_BATCH; ++u) wb[u] = c + u < c1 ? hist[(int64_t)(c + u) * E + e_t] : 0;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < LS_BATCH; ++u) {
           if (c + u < c1) hist[(int64_t)(c + u) * E + e_t] = run;
-          run += w8[u];
+          run += wb[u];
         }
       }
     }
