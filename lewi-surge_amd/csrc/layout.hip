@@ -69,7 +69,7 @@ __device__ __forceinline__ int block_scan_excl(int v, int* ws, int* total) {
   return base + x - v;
 }
 
-// One workgroup of at least E threads (512 or 1024).  hist [nchunk][E] is overwritten with the exclusive per-expert
+// One workgroup of 1024 threads (at least E).  hist [nchunk][E] is overwritten with the exclusive per-expert
 // chunk base.
 // Thread (e, j) owns expert e's chunks [j cpt, (j + 1) cpt), kept in registers between the two passes (up to
 // LS_REG chunks; more are read again).  The expert-level scans are block-wide shuffle scans, and the padding
@@ -338,7 +338,7 @@ int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_
   // the scan needs a thread per expert; 512 threads (two waves per SIMD) when that is enough, so that it fits on a CU
   // beside a running 8-wave GEMM tile (the layer's shared expert runs beside the layout) instead of waiting for one
   // to drain
-  const unsigned scan_threads = E <= 512 ? 512 : 1024;
+  const unsigned scan_threads = 1024;
   if (M == 0) {
     LSURGE_LAUNCH(KID_LAYOUT_SCAN, s,
                   hipLaunchKernelGGL(layout_scan_kernel, dim3(1), dim3(scan_threads), 0, s, hist, 0, (int)E, gs, offsets,
