@@ -346,7 +346,8 @@ int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const fl
 /* Row-wise l2 normalisation of the GDN block's query and key heads, the use_qk_norm_in_gdn branch of
  * fast_chunk_gated_delta_rule (modal/gdn_fast.py:43-46, MaxText's l2norm(x, dim=-1, eps=1e-6)):
  * y = x * rsqrt(sum(x^2) + eps) per row of dim elements, x and y bf16 [rows, dim], f32 arithmetic; rnorm [rows] f32
- * receives rsqrt(sum(x^2) + eps) for the backward (NULL: not written).  dim a multiple of 8 in [8, 512]. */
+ * receives rsqrt(sum(x^2) + eps) for the backward (NULL: not written).  rows < 2^31, dim a multiple of 8 in
+ * [8, 512], x and y 16-byte aligned. */
 int lsurge_l2norm_rows(const void* x, int64_t rows, int64_t dim, float eps, void* y, float* rnorm,
                        lsurge_stream_t stream);
 /* Its backward: dx = r dy - r^3 x (x . dy) per row (r = rnorm of the forward), x, dy and dx bf16 [rows, dim]. */

@@ -1493,8 +1493,8 @@ int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const fl
 int lsurge_l2norm_rows(const void* x, int64_t rows, int64_t dim, float eps, void* y, float* rnorm,
                        lsurge_stream_t stream) {
   LSURGE_REQUIRE(x && y, "l2norm_rows: null pointer");
-  LSURGE_REQUIRE(rows >= 0 && rows < (1ll << 40) && dim >= 8 && dim <= 512 && dim % 8 == 0 && eps >= 0.f,
-                 "l2norm_rows: rows=%lld dim=%lld eps=%g (dim a multiple of 8 in [8, 512], eps >= 0)", (long long)rows,
+  LSURGE_REQUIRE(rows >= 0 && rows < (1ll << 31) && dim >= 8 && dim <= 512 && dim % 8 == 0 && eps >= 0.f,
+                 "l2norm_rows: rows=%lld dim=%lld eps=%g (rows < 2^31, dim a multiple of 8 in [8, 512], eps >= 0)", (long long)rows,
                  (long long)dim, (double)eps);
   LSURGE_REQUIRE(((uintptr_t)x | (uintptr_t)y) % 16 == 0, "l2norm_rows: x and y must be 16-byte aligned");
   if (rows == 0) return LSURGE_OK;
@@ -1516,8 +1516,8 @@ int lsurge_l2norm_rows(const void* x, int64_t rows, int64_t dim, float eps, void
 int lsurge_l2norm_rows_bwd(const void* x, const void* dy, const float* rnorm, int64_t rows, int64_t dim, void* dx,
                            lsurge_stream_t stream) {
   LSURGE_REQUIRE(x && dy && rnorm && dx, "l2norm_rows_bwd: null pointer");
-  LSURGE_REQUIRE(rows >= 0 && rows < (1ll << 40) && dim >= 8 && dim <= 512 && dim % 8 == 0,
-                 "l2norm_rows_bwd: rows=%lld dim=%lld (dim a multiple of 8 in [8, 512])", (long long)rows,
+  LSURGE_REQUIRE(rows >= 0 && rows < (1ll << 31) && dim >= 8 && dim <= 512 && dim % 8 == 0,
+                 "l2norm_rows_bwd: rows=%lld dim=%lld (rows < 2^31, dim a multiple of 8 in [8, 512])", (long long)rows,
                  (long long)dim);
   LSURGE_REQUIRE(((uintptr_t)x | (uintptr_t)dy | (uintptr_t)dx) % 16 == 0,
                  "l2norm_rows_bwd: x, dy and dx must be 16-byte aligned");

@@ -81,3 +81,21 @@ def test_fp8_backward_argument_errors_without_gpu():
     assert rc != 0 and b"multiple of 16" in lib.lsurge_last_error()
     rc = lib.lsurge_fp8_cast_transpose(fake, 64, 32, 2, fake, None, 64, fake, fake, 1 << 20, None)
     assert rc != 0 and b"format" in lib.lsurge_last_error()
+
+
+def test_l2norm_argument_errors_without_gpu():
+    """lsurge_l2norm_rows / _bwd reject bad shapes and alignment before touching the device."""
+    lib = L.lib()
+    fake = ctypes.c_void_p(256)
+    for rows, dim, eps, msg in ((10, 12, 1e-6, b"multiple of 8"), (10, 520, 1e-6, b"multiple of 8"),
+                                (1 << 31, 128, 1e-6, b"rows < 2^31"), (10, 128, -1.0, b"eps >= 0"),
+                                (10, 128, float("nan"), b"eps >= 0")):
+        assert lib.lsurge_l2norm_rows(fake, rows, dim, eps, fake, None, None) != 0
+        assert msg in lib.lsurge_last_error(), lib.lsurge_last_error()
+    assert lib.lsurge_l2norm_rows(ctypes.c_void_p(264), 10, 128, 1e-6, fake, None, None) != 0
+    assert b"16-byte aligned" in lib.lsurge_last_error()
+    assert lib.lsurge_l2norm_rows_bwd(fake, fake, fake, 1 << 31, 128, fake, None) != 0
+    assert b"rows < 2^31" in lib.lsurge_last_error()
+    assert lib.lsurge_l2norm_rows_bwd(fake, fake, None, 10, 128, fake, None) != 0
+    assert b"null pointer" in lib.lsurge_last_error()
+    assert lib.lsurge_l2norm_rows(fake, 0, 128, 1e-6, fake, None, None) == 0  # empty: nothing launched
