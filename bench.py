@@ -459,8 +459,9 @@ def conv_bench(a):
 
 def gdn_bench(a):
     """Chunked gated delta rule at configs/stage1.yml's GDN shape: per_device_batch_size 8, max_target_length 4096,
-    8 value heads x 128 (keys repeated to the value heads), chunks of 64: the forward, and forward + backward (the
-    backward recomputes the forward's chunk products and states, as a remat'd training step would).  Algorithmic flops
+    8 value heads x 128 (keys repeated to the value heads), chunks of 64: the forward, and the training step forward +
+    backward (the forward keeps its chunk products and states for the backward, as XLA's autodiff keeps residuals; the
+    backward that recomputes them instead, as a remat'd step would, is timed beside it).  Algorithmic flops
     per chunk and head, forward: 2 (2 C^2 Dk + 2 C^2 Dv) chunk-local (S, attn, u, w) + 2 (2 C Dk Dv + C^2 Dv + C Dk Dv)
     scan (q S, w S, attn v_new, the state update); the backward counts twice the forward's (the usual 2x for the
     gradients of every product), so fwd + bwd = 3 x forward, counted in full as the reference's dense products are."""
@@ -484,23 +485,43 @@ def gdn_bench(a):
     lib = L.lib()
     ws = L.workspace(lib.lsurge_gdn_chunked_workspace_bytes(B, T, H, D, D), dev)
     wsb = L.workspace(lib.lsurge_gdn_chunked_bwd_workspace_bytes(B, T, H, D, D), dev)
+    saved = L.workspace(lib.lsurge_gdn_chunked_saved_bytes(B, T, H, D, D), dev)
+    wss = L.workspace(lib.lsurge_gdn_chunked_bwd_saved_workspace_bytes(B, T, H, D, D), dev)
     st = L.stream(dev)
 
     def fwd():
         L.check(lib.lsurge_gdn_chunked_fwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D, None,
                                            L.ptr(o), None, L.ptr(ws), ws.numel(), st), "gdn_chunked_fwd")
 
-    def bwd():
+    def bwd_recompute():
         L.check(lib.lsurge_gdn_chunked_bwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D, None,
                                            L.ptr(do), None, L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg), L.ptr(db), None,
                                            L.ptr(wsb), wsb.numel(), st), "gdn_chunked_bwd")
 
+    def fwd_save():
+        L.check(lib.lsurge_gdn_chunked_fwd_save(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D,
+                                                None, L.ptr(o), None, L.ptr(saved), saved.numel(), st),
+                "gdn_chunked_fwd_save")
+
+    def bwd():
+        L.check(lib.lsurge_gdn_chunked_bwd_saved(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(beta), B, T, H, D, D, L.ptr(do),
+                                                 None, L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg), L.ptr(db), None,
+                                                 L.ptr(saved), saved.numel(), L.ptr(wss), wss.numel(), st),
+                "gdn_chunked_bwd_saved")
+
     def step():
-        fwd()
+        fwd_save()
         bwd()
 
+    def step_recompute():
+        fwd()
+        bwd_recompute()
+
     ms_f = _time_ms(fwd, a.steps, a.warmup)
+    ms_fs = _time_ms(fwd_save, a.steps, a.warmup)
     ms_b = _time_ms(bwd, a.steps, a.warmup)
+    ms_br = _time_ms(bwd_recompute, a.steps, a.warmup)
+    ms_r = _time_ms(step_recompute, a.steps, a.warmup)
     ms = _time_ms(step, a.steps, a.warmup)
     chunks = B * H * ((T + C - 1) // C)
     flops = chunks * 2 * (2 * C * C * D + 2 * C * C * D + 2 * C * D * D + C * C * D + C * D * D)
@@ -513,9 +534,13 @@ def gdn_bench(a):
         "config": {"workload": f"chunked gated delta rule fwd+bwd B={B} T={T} H={H} Dk=Dv={D} chunk={C} "
                                "(configs/stage1.yml GDN shape)"},
         "fwd": {"ms": round(ms_f, 4), "tokens_s": round(B * T / (ms_f * 1e-3), 1),
-                "TFLOP/s": round(flops / (ms_f * 1e-3) / 1e12, 2)},
+                "TFLOP/s": round(flops / (ms_f * 1e-3) / 1e12, 2), "note": "inference forward (no residuals kept)"},
+        "fwd_save": {"ms": round(ms_fs, 4), "saved_MB": round(saved.numel() / 1e6, 1),
+                     "note": "training forward: also keeps the chunk products and the state entering every chunk"},
         "bwd": {"ms": round(ms_b, 4), "TFLOP/s": round(2 * flops / (ms_b * 1e-3) / 1e12, 2),
-                "note": "includes the recompute of the forward's chunk products and states"},
+                "note": "from the kept residuals"},
+        "recompute": {"bwd_ms": round(ms_br, 4), "fwd_bwd_ms": round(ms_r, 4),
+                      "note": "backward recomputing the forward's chunk products and states (nothing kept)"},
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 157.3, "unit": "TFLOP/s",
                      "frac": round(tf / 157.3, 4), "traffic": None,
                      "note": "f32-accurate products on the bf16 matrix cores (f32 operands split into hi/lo bf16 "

@@ -343,6 +343,23 @@ int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const fl
                            const float* dh_final, void* dq, void* dk_out, void* dv_out, float* dg, float* dbeta,
                            float* dh0, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
 
+/* The same forward and backward split at the residuals, as jax.vjp splits fast_chunk_gated_delta_rule when XLA's
+ * autodiff trains through it (modal/gdn_fast.py:37-113; lightning/train_stage1.py:67-69).  The training forward also
+ * keeps the chunk products and the state entering every chunk in `saved` (lsurge_gdn_chunked_saved_bytes: about
+ * 2.25 KiB per token and head at dk = dv = 128), and the backward starts from them instead of recomputing the forward,
+ * with its own scratch `workspace` (lsurge_gdn_chunked_bwd_saved_workspace_bytes).  o, h_out and every gradient are
+ * bitwise those of lsurge_gdn_chunked_fwd / lsurge_gdn_chunked_bwd.  The backward only reads `saved`.  Arguments
+ * otherwise as above (the backward needs neither g nor h0). */
+size_t lsurge_gdn_chunked_saved_bytes(int64_t b, int64_t t, int64_t h, int64_t dk, int64_t dv);
+int lsurge_gdn_chunked_fwd_save(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                                int64_t b, int64_t t, int64_t h, int64_t dk, int64_t dv, const float* h0, void* o,
+                                float* h_out, void* saved, size_t saved_bytes, lsurge_stream_t stream);
+size_t lsurge_gdn_chunked_bwd_saved_workspace_bytes(int64_t b, int64_t t, int64_t h, int64_t dk, int64_t dv);
+int lsurge_gdn_chunked_bwd_saved(const void* q, const void* k, const void* v, const void* beta, int64_t b, int64_t t,
+                                 int64_t h, int64_t dk, int64_t dv, const void* dout, const float* dh_final, void* dq,
+                                 void* dk_out, void* dv_out, float* dg, float* dbeta, float* dh0, const void* saved,
+                                 size_t saved_bytes, void* workspace, size_t workspace_bytes, lsurge_stream_t stream);
+
 /* Row-wise l2 normalisation of the GDN block's query and key heads, the use_qk_norm_in_gdn branch of
  * fast_chunk_gated_delta_rule (modal/gdn_fast.py:43-46, MaxText's l2norm(x, dim=-1, eps=1e-6)):
  * y = x * rsqrt(sum(x^2) + eps) per row of dim elements, x and y bf16 [rows, dim], f32 arithmetic; rnorm [rows] f32

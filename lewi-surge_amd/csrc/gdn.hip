@@ -1402,36 +1402,51 @@ int lsurge_gdn_chunked_fwd(const void* q, const void* k, const void* v, const fl
   return LSURGE_OK;
 }
 
-// workspace of the backward: the forward's chunk products (u, w, attn, gcum) plus S, A and the state entering each
-// chunk, the reverse scan's state gradients, and the chunk gradients (dqg, dkd f32; du, dw bf16; dP, dgl)
+// workspace of the backward: the forward's residuals -- its chunk products (u, w, attn, gcum) plus S, A and the state
+// entering each chunk -- then the backward's scratch: the reverse scan's state gradients and the chunk gradients (dqg,
+// dkd f32; du, dw bf16; dP, dgl).  The two parts can live in separate buffers (lsurge_gdn_chunked_fwd_save keeps the
+// first between the passes).
 struct GdnBwdWs {
   bf16_t *u, *w, *du, *dw;
   float *attn, *gcum, *S, *A, *hs, *dhs, *dqg, *dkd, *dP, *dgl;
 };
-static size_t gdn_bwd_carve(int64_t chunks, void* base, GdnBwdWs* p) {
+struct Carver {
+  char* base;
   size_t off = 0;
-  auto take = [&](size_t bytes) {
-    char* r = base ? (char*)base + off : nullptr;
+  char* take(size_t bytes) {
+    char* r = base ? base + off : nullptr;
     off += (bytes + 255) / 256 * 256;
     return r;
-  };
+  }
+};
+static size_t gdn_carve_saved(int64_t chunks, void* base, GdnBwdWs* p) {
+  Carver c{(char*)base};
+  const size_t tile16 = (size_t)chunks * GC * GD * sizeof(bf16_t), mat = (size_t)chunks * GC * GC * sizeof(float);
+  p->u = (bf16_t*)c.take(tile16);
+  p->w = (bf16_t*)c.take(tile16);
+  p->attn = (float*)c.take(mat);
+  p->gcum = (float*)c.take((size_t)chunks * GC * sizeof(float));
+  p->S = (float*)c.take(mat);
+  p->A = (float*)c.take(mat);
+  p->hs = (float*)c.take((size_t)chunks * GD * GD * sizeof(float));
+  return c.off;
+}
+static size_t gdn_carve_scratch(int64_t chunks, void* base, GdnBwdWs* p) {
+  Carver c{(char*)base};
   const size_t tile16 = (size_t)chunks * GC * GD * sizeof(bf16_t), tile32 = (size_t)chunks * GC * GD * sizeof(float);
-  const size_t mat = (size_t)chunks * GC * GC * sizeof(float), st = (size_t)chunks * GD * GD * sizeof(float);
-  p->u = (bf16_t*)take(tile16);
-  p->w = (bf16_t*)take(tile16);
-  p->du = (bf16_t*)take(tile16);
-  p->dw = (bf16_t*)take(tile16);
-  p->attn = (float*)take(mat);
-  p->gcum = (float*)take((size_t)chunks * GC * sizeof(float));
-  p->S = (float*)take(mat);
-  p->A = (float*)take(mat);
-  p->hs = (float*)take(st);
-  p->dhs = (float*)take(st);
-  p->dqg = (float*)take(tile32);
-  p->dkd = (float*)take(tile32);
-  p->dP = (float*)take(mat);
-  p->dgl = (float*)take((size_t)chunks * sizeof(float));
-  return off;
+  p->du = (bf16_t*)c.take(tile16);
+  p->dw = (bf16_t*)c.take(tile16);
+  p->dhs = (float*)c.take((size_t)chunks * GD * GD * sizeof(float));
+  p->dqg = (float*)c.take(tile32);
+  p->dkd = (float*)c.take(tile32);
+  p->dP = (float*)c.take((size_t)chunks * GC * GC * sizeof(float));
+  p->dgl = (float*)c.take((size_t)chunks * sizeof(float));
+  return c.off;
+}
+// both parts in one buffer (the recomputing backward)
+static size_t gdn_bwd_carve(int64_t chunks, void* base, GdnBwdWs* p) {
+  const size_t a = gdn_carve_saved(chunks, base, p);
+  return a + gdn_carve_scratch(chunks, base ? (char*)base + a : nullptr, p);
 }
 
 size_t lsurge_gdn_chunked_bwd_workspace_bytes(int64_t b, int64_t t, int64_t h, int64_t dk, int64_t dv) {
@@ -1439,39 +1454,25 @@ size_t lsurge_gdn_chunked_bwd_workspace_bytes(int64_t b, int64_t t, int64_t h, i
   GdnBwdWs p;
   return gdn_bwd_carve(b * h * gdn_chunks(t), nullptr, &p);
 }
-
-int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const float* g, const void* beta, int64_t b,
-                           int64_t t, int64_t h, int64_t dk, int64_t dv, const float* h0, const void* dout,
-                           const float* dh_final, void* dq, void* dk_out, void* dv_out, float* dg, float* dbeta,
-                           float* dh0, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
-  LSURGE_REQUIRE(q && k && v && g && beta && dout && dq && dk_out && dv_out && dg && dbeta && workspace,
-                 "gdn_chunked_bwd: null pointer");
-  LSURGE_REQUIRE(dk == GD && dv == GD, "gdn_chunked_bwd: head dims dk=%lld dv=%lld must be %d", (long long)dk,
-                 (long long)dv, GD);
-  LSURGE_REQUIRE(b >= 1 && b < 65536 && h >= 1 && h < 65536 && t >= 1 && b * t * h < (1ll << 31) / GD &&
-                     b * h * gdn_chunks(t) < (1ll << 31) / (GD * GD),
-                 "gdn_chunked_bwd: bad shape b=%lld t=%lld h=%lld", (long long)b, (long long)t, (long long)h);
-  LSURGE_REQUIRE(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout | (uintptr_t)dq | (uintptr_t)dk_out |
-                  (uintptr_t)dv_out | (uintptr_t)workspace) % 16 == 0,
-                 "gdn_chunked_bwd: q, k, v, do, dq, dk, dv and workspace must be 16-byte aligned");
-  const size_t need = lsurge_gdn_chunked_bwd_workspace_bytes(b, t, h, dk, dv);
-  LSURGE_REQUIRE(workspace_bytes >= need, "gdn_chunked_bwd: workspace %zu < %zu bytes", workspace_bytes, need);
-  hipStream_t s = (hipStream_t)stream;
-  const int64_t N = gdn_chunks(t);
+size_t lsurge_gdn_chunked_saved_bytes(int64_t b, int64_t t, int64_t h, int64_t dk, int64_t dv) {
+  if (b < 1 || t < 1 || h < 1 || dk != GD || dv != GD) return 0;
   GdnBwdWs p;
-  gdn_bwd_carve(b * h * N, workspace, &p);
+  return gdn_carve_saved(b * h * gdn_chunks(t), nullptr, &p);
+}
+size_t lsurge_gdn_chunked_bwd_saved_workspace_bytes(int64_t b, int64_t t, int64_t h, int64_t dk, int64_t dv) {
+  if (b < 1 || t < 1 || h < 1 || dk != GD || dv != GD) return 0;
+  GdnBwdWs p;
+  return gdn_carve_scratch(b * h * gdn_chunks(t), nullptr, &p);
+}
+
+// The backward's launches after the forward's chunk products and states are in the workspace: the reverse scan of
+// the state gradient, then the chunk gradients and the chunk-local backward.
+static int gdn_bwd_from_ws(const void* q, const void* k, const void* v, const void* beta, int64_t b, int64_t t,
+                           int64_t h, const void* dout, const float* dh_final, void* dq, void* dk_out, void* dv_out,
+                           float* dg, float* dbeta, float* dh0, const GdnBwdWs& p, hipStream_t s) {
+  const int64_t N = gdn_chunks(t);
   const float qscale = round_bf16_host(1.f / sqrtf((float)GD));
   const dim3 chunk_grid((unsigned)N, (unsigned)h, (unsigned)b), scan_grid(GD / SB, (unsigned)h, (unsigned)b);
-  // forward recompute: chunk products (with S and A) and the state entering every chunk
-  LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(gdn_chunk_kernel, chunk_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
-                                   (const bf16_t*)v, g, (const bf16_t*)beta, (int)t, (int)h, qscale, p.u, p.w, p.attn,
-                                   p.gcum, p.S, p.A));
-  LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(gdn_scan_kernel, scan_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
-                                   (const bf16_t*)p.u, (const bf16_t*)p.w, (const float*)p.attn, (const float*)p.gcum,
-                                   (int)t, (int)h, (int)N, qscale, h0, (bf16_t*)nullptr, (float*)nullptr, p.hs));
-  // reverse scan of the state gradient, then the chunk gradients and the chunk-local backward
   LSURGE_LAUNCH(KID_MISC, s,
                 hipLaunchKernelGGL(gdn_bscan_kernel, scan_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
                                    (const bf16_t*)p.w, (const float*)p.attn, (const float*)p.gcum, (const bf16_t*)dout,
@@ -1489,6 +1490,90 @@ int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const fl
                                    (int)t, (int)h, qscale, (bf16_t*)dq, (bf16_t*)dk_out, (bf16_t*)dv_out, dg, dbeta));
   return LSURGE_OK;
 }
+
+// The forward's chunk products (with S and A) and, with o, its output as well, into the backward's workspace; the
+// scan stores the state entering every chunk.
+static int gdn_fwd_to_ws(const void* q, const void* k, const void* v, const float* g, const void* beta, int64_t b,
+                         int64_t t, int64_t h, const float* h0, void* o, float* h_out, const GdnBwdWs& p, hipStream_t s) {
+  const int64_t N = gdn_chunks(t);
+  const float qscale = round_bf16_host(1.f / sqrtf((float)GD));
+  const dim3 chunk_grid((unsigned)N, (unsigned)h, (unsigned)b), scan_grid(GD / SB, (unsigned)h, (unsigned)b);
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(gdn_chunk_kernel, chunk_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
+                                   (const bf16_t*)v, g, (const bf16_t*)beta, (int)t, (int)h, qscale, p.u, p.w, p.attn,
+                                   p.gcum, p.S, p.A));
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(gdn_scan_kernel, scan_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
+                                   (const bf16_t*)p.u, (const bf16_t*)p.w, (const float*)p.attn, (const float*)p.gcum,
+                                   (int)t, (int)h, (int)N, qscale, h0, (bf16_t*)o, h_out, p.hs));
+  return LSURGE_OK;
+}
+
+#define GDN_BWD_SHAPE_CHECKS(NAME)                                                                                     \
+  LSURGE_REQUIRE(dk == GD && dv == GD, NAME ": head dims dk=%lld dv=%lld must be %d", (long long)dk, (long long)dv,   \
+                 GD);                                                                                                  \
+  LSURGE_REQUIRE(b >= 1 && b < 65536 && h >= 1 && h < 65536 && t >= 1 && b * t * h < (1ll << 31) / GD &&              \
+                     b * h * gdn_chunks(t) < (1ll << 31) / (GD * GD),                                                  \
+                 NAME ": bad shape b=%lld t=%lld h=%lld", (long long)b, (long long)t, (long long)h)
+
+int lsurge_gdn_chunked_bwd(const void* q, const void* k, const void* v, const float* g, const void* beta, int64_t b,
+                           int64_t t, int64_t h, int64_t dk, int64_t dv, const float* h0, const void* dout,
+                           const float* dh_final, void* dq, void* dk_out, void* dv_out, float* dg, float* dbeta,
+                           float* dh0, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(q && k && v && g && beta && dout && dq && dk_out && dv_out && dg && dbeta && workspace,
+                 "gdn_chunked_bwd: null pointer");
+  GDN_BWD_SHAPE_CHECKS("gdn_chunked_bwd");
+  LSURGE_REQUIRE(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout | (uintptr_t)dq | (uintptr_t)dk_out |
+                  (uintptr_t)dv_out | (uintptr_t)workspace) % 16 == 0,
+                 "gdn_chunked_bwd: q, k, v, do, dq, dk, dv and workspace must be 16-byte aligned");
+  const size_t need = lsurge_gdn_chunked_bwd_workspace_bytes(b, t, h, dk, dv);
+  LSURGE_REQUIRE(workspace_bytes >= need, "gdn_chunked_bwd: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = (hipStream_t)stream;
+  GdnBwdWs p;
+  gdn_bwd_carve(b * h * gdn_chunks(t), workspace, &p);
+  // forward recompute: chunk products (with S and A) and the state entering every chunk (no output)
+  const int rc = gdn_fwd_to_ws(q, k, v, g, beta, b, t, h, h0, nullptr, nullptr, p, s);
+  if (rc != LSURGE_OK) return rc;
+  return gdn_bwd_from_ws(q, k, v, beta, b, t, h, dout, dh_final, dq, dk_out, dv_out, dg, dbeta, dh0, p, s);
+}
+
+int lsurge_gdn_chunked_fwd_save(const void* q, const void* k, const void* v, const float* g, const void* beta, int64_t b,
+                                int64_t t, int64_t h, int64_t dk, int64_t dv, const float* h0, void* o, float* h_out,
+                                void* saved, size_t saved_bytes, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(q && k && v && g && beta && o && saved, "gdn_chunked_fwd_save: null pointer");
+  GDN_BWD_SHAPE_CHECKS("gdn_chunked_fwd_save");
+  LSURGE_REQUIRE(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o | (uintptr_t)saved) % 16 == 0,
+                 "gdn_chunked_fwd_save: q, k, v, o and saved must be 16-byte aligned");
+  const size_t need = lsurge_gdn_chunked_saved_bytes(b, t, h, dk, dv);
+  LSURGE_REQUIRE(saved_bytes >= need, "gdn_chunked_fwd_save: saved buffer %zu < %zu bytes", saved_bytes, need);
+  GdnBwdWs p;
+  gdn_carve_saved(b * h * gdn_chunks(t), saved, &p);
+  return gdn_fwd_to_ws(q, k, v, g, beta, b, t, h, h0, o, h_out, p, (hipStream_t)stream);
+}
+
+int lsurge_gdn_chunked_bwd_saved(const void* q, const void* k, const void* v, const void* beta, int64_t b, int64_t t,
+                                 int64_t h, int64_t dk, int64_t dv, const void* dout, const float* dh_final, void* dq,
+                                 void* dk_out, void* dv_out, float* dg, float* dbeta, float* dh0, const void* saved,
+                                 size_t saved_bytes, void* workspace, size_t workspace_bytes, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(q && k && v && beta && dout && dq && dk_out && dv_out && dg && dbeta && saved && workspace,
+                 "gdn_chunked_bwd_saved: null pointer");
+  GDN_BWD_SHAPE_CHECKS("gdn_chunked_bwd_saved");
+  LSURGE_REQUIRE(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)dout | (uintptr_t)dq | (uintptr_t)dk_out |
+                  (uintptr_t)dv_out | (uintptr_t)saved | (uintptr_t)workspace) % 16 == 0,
+                 "gdn_chunked_bwd_saved: q, k, v, do, dq, dk, dv, saved and workspace must be 16-byte aligned");
+  const size_t need = lsurge_gdn_chunked_saved_bytes(b, t, h, dk, dv);
+  LSURGE_REQUIRE(saved_bytes >= need, "gdn_chunked_bwd_saved: saved buffer %zu < %zu bytes", saved_bytes, need);
+  const size_t need_ws = lsurge_gdn_chunked_bwd_saved_workspace_bytes(b, t, h, dk, dv);
+  LSURGE_REQUIRE(workspace_bytes >= need_ws, "gdn_chunked_bwd_saved: workspace %zu < %zu bytes", workspace_bytes,
+                 need_ws);
+  GdnBwdWs p;
+  const int64_t chunks = b * h * gdn_chunks(t);
+  gdn_carve_saved(chunks, const_cast<void*>(saved), &p);  // read only here
+  gdn_carve_scratch(chunks, workspace, &p);
+  return gdn_bwd_from_ws(q, k, v, beta, b, t, h, dout, dh_final, dq, dk_out, dv_out, dg, dbeta, dh0, p,
+                         (hipStream_t)stream);
+}
+#undef GDN_BWD_SHAPE_CHECKS
 
 int lsurge_l2norm_rows(const void* x, int64_t rows, int64_t dim, float eps, void* y, float* rnorm,
                        lsurge_stream_t stream) {

@@ -1,8 +1,11 @@
 """Chunked gated delta rule of the Gated DeltaNet block on the HIP library (mirrors modal/gdn_fast.py).
 
 The reference swaps MaxText's `jax_chunk_gated_delta_rule` for `fast_chunk_gated_delta_rule` (gdn_fast.py:37-113) and
-trains through it with XLA autodiff.  Here the forward is lsurge_gdn_chunked_fwd and the backward
-lsurge_gdn_chunked_bwd (which recomputes the forward's chunk products and states from the inputs).
+trains through it with XLA autodiff, which keeps the forward's residuals for the backward.  Here, when a gradient is
+needed, the forward is lsurge_gdn_chunked_fwd_save (the chunk products and the state entering every chunk kept, about
+2.25 KiB per token and head) and the backward lsurge_gdn_chunked_bwd_saved.  With SAVE_RESIDUALS = False the forward
+keeps only its inputs and the backward lsurge_gdn_chunked_bwd recomputes the rest (less memory, one more forward's
+work); the results are bitwise the same.  Without gradients the forward is lsurge_gdn_chunked_fwd.
 
   fast_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None, ...)
       differentiable op with the reference's signature: query, key [B, T, H, 128], value [B, T, H, 128], g [B, T, H]
@@ -19,6 +22,7 @@ import torch
 
 import _lib as L
 
+SAVE_RESIDUALS = True
 PREC = "highest"
 INV = "solve"
 UNROLL = 1
@@ -33,10 +37,17 @@ class _GdnFn(torch.autograd.Function):
         o = torch.empty_like(v)
         h_out = torch.empty((B, H, D, D), dtype=torch.float32, device=q.device) if want_state else None
         lib = L.lib()
-        ws = L.workspace(lib.lsurge_gdn_chunked_workspace_bytes(B, T, H, D, D), q.device)
-        L.check(lib.lsurge_gdn_chunked_fwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D,
-                                           L.ptr(h0), L.ptr(o), L.ptr(h_out), L.ptr(ws), ws.numel(),
-                                           L.stream(q.device)), "gdn_chunked_fwd")
+        ctx.saved = None
+        if SAVE_RESIDUALS and any(ctx.needs_input_grad[:6]):
+            ctx.saved = L.workspace(lib.lsurge_gdn_chunked_saved_bytes(B, T, H, D, D), q.device)
+            L.check(lib.lsurge_gdn_chunked_fwd_save(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D,
+                                                    D, L.ptr(h0), L.ptr(o), L.ptr(h_out), L.ptr(ctx.saved),
+                                                    ctx.saved.numel(), L.stream(q.device)), "gdn_chunked_fwd_save")
+        else:
+            ws = L.workspace(lib.lsurge_gdn_chunked_workspace_bytes(B, T, H, D, D), q.device)
+            L.check(lib.lsurge_gdn_chunked_fwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D,
+                                               L.ptr(h0), L.ptr(o), L.ptr(h_out), L.ptr(ws), ws.numel(),
+                                               L.stream(q.device)), "gdn_chunked_fwd")
         ctx.save_for_backward(q, k, v, g, beta, h0)
         ctx.has_h0 = h0 is not None
         return (o, h_out) if want_state else (o,)
@@ -52,11 +63,19 @@ class _GdnFn(torch.autograd.Function):
         db = torch.empty_like(dg)
         dh0 = torch.empty((B, H, D, D), dtype=torch.float32, device=q.device) if ctx.has_h0 else None
         lib = L.lib()
-        ws = L.workspace(lib.lsurge_gdn_chunked_bwd_workspace_bytes(B, T, H, D, D), q.device)
-        L.check(lib.lsurge_gdn_chunked_bwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D,
-                                           L.ptr(h0), L.ptr(do), L.ptr(dhf), L.ptr(dq), L.ptr(dk), L.ptr(dv),
-                                           L.ptr(dg), L.ptr(db), L.ptr(dh0), L.ptr(ws), ws.numel(),
-                                           L.stream(q.device)), "gdn_chunked_bwd")
+        if ctx.saved is not None:
+            ws = L.workspace(lib.lsurge_gdn_chunked_bwd_saved_workspace_bytes(B, T, H, D, D), q.device)
+            L.check(lib.lsurge_gdn_chunked_bwd_saved(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(beta), B, T, H, D, D,
+                                                     L.ptr(do), L.ptr(dhf), L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg),
+                                                     L.ptr(db), L.ptr(dh0), L.ptr(ctx.saved), ctx.saved.numel(),
+                                                     L.ptr(ws), ws.numel(), L.stream(q.device)), "gdn_chunked_bwd_saved")
+            ctx.saved = None
+        else:
+            ws = L.workspace(lib.lsurge_gdn_chunked_bwd_workspace_bytes(B, T, H, D, D), q.device)
+            L.check(lib.lsurge_gdn_chunked_bwd(L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(g), L.ptr(beta), B, T, H, D, D,
+                                               L.ptr(h0), L.ptr(do), L.ptr(dhf), L.ptr(dq), L.ptr(dk), L.ptr(dv),
+                                               L.ptr(dg), L.ptr(db), L.ptr(dh0), L.ptr(ws), ws.numel(),
+                                               L.stream(q.device)), "gdn_chunked_bwd")
         return dq, dk, dv, dg, db, dh0, None
 
 

@@ -189,6 +189,79 @@ def test_autograd_surface(dev):
         gdn_fast.fast_chunk_gated_delta_rule(*ts[:5], cp_axis="context")
 
 
+@pytest.mark.parametrize("B,T,H,states", [(1, 1, 1, False), (2, 100, 3, True), (1, 4096, 8, False)])
+def test_saved_residuals_bitwise(B, T, H, states, dev):
+    """lsurge_gdn_chunked_fwd_save + lsurge_gdn_chunked_bwd_saved (the training split: residuals kept, no recompute)
+    give the bits of lsurge_gdn_chunked_fwd + lsurge_gdn_chunked_bwd; the backward leaves `saved` as it was (a second
+    backward from it gives the same bits), and reads nothing of its scratch workspace before writing it (the
+    workspace is filled with 0xFF, NaN as floats, first)."""
+    q, k, v, g, beta = _inputs(B, T, H, seed=B * T + H, correlated=True)
+    rng = np.random.default_rng(T)
+    do = mo.round_bf16(rng.standard_normal((B, T, H, D)).astype(np.float32))
+    h0 = (rng.standard_normal((B, H, D, D)) * 0.1).astype(np.float32) if states else None
+    dhf = (rng.standard_normal((B, H, D, D)) * 0.1).astype(np.float32) if states else None
+    o_ref, h_ref, _, _ = gpu_gdn(q, k, v, g, beta, dev, h0=h0)
+    grads_ref = gpu_gdn_bwd(q, k, v, g, beta, do, dev, h0=h0, dh_final=dhf)
+
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev).to(torch.bfloat16)  # noqa: E731
+    f32 = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)  # noqa: E731
+    qt, kt, vt, bt, dot = bf(q), bf(k), bf(v), bf(beta), bf(do)
+    gt, h0t, dht = f32(g), f32(h0), f32(dhf)
+    lib = L.lib()
+    o = torch.empty_like(vt)
+    hout = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+    saved = L.workspace(lib.lsurge_gdn_chunked_saved_bytes(B, T, H, D, D), dev)
+    assert 0 < saved.numel() < lib.lsurge_gdn_chunked_bwd_workspace_bytes(B, T, H, D, D)
+    L.check(lib.lsurge_gdn_chunked_fwd_save(L.ptr(qt), L.ptr(kt), L.ptr(vt), L.ptr(gt), L.ptr(bt), B, T, H, D, D,
+                                            L.ptr(h0t), L.ptr(o), L.ptr(hout), L.ptr(saved), saved.numel(),
+                                            L.stream(dev)), "gdn_chunked_fwd_save")
+    torch.cuda.synchronize()
+    assert np.array_equal(o.float().cpu().numpy(), o_ref) and np.array_equal(hout.cpu().numpy(), h_ref)
+    snap = saved.clone()
+    ws = torch.full((lib.lsurge_gdn_chunked_bwd_saved_workspace_bytes(B, T, H, D, D),), 0xFF, dtype=torch.uint8,
+                    device=dev)
+    for rep in range(2):
+        dq, dk, dv = torch.empty_like(qt), torch.empty_like(kt), torch.empty_like(vt)
+        dg = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+        db = torch.empty_like(dg)
+        dh0 = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+        L.check(lib.lsurge_gdn_chunked_bwd_saved(L.ptr(qt), L.ptr(kt), L.ptr(vt), L.ptr(bt), B, T, H, D, D, L.ptr(dot),
+                                                 L.ptr(dht), L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(dg), L.ptr(db),
+                                                 L.ptr(dh0), L.ptr(saved), saved.numel(), L.ptr(ws), ws.numel(),
+                                                 L.stream(dev)), "gdn_chunked_bwd_saved")
+        torch.cuda.synchronize()
+        got = [a.float().cpu().numpy() for a in (dq, dk, dv, dg, db, dh0)]
+        for n, a, b in zip(NAMES, got, grads_ref):
+            assert np.array_equal(a, b), (rep, n)
+        assert torch.equal(saved, snap), rep
+
+
+def test_autograd_saved_vs_recompute_bitwise(dev):
+    """gdn_fast with SAVE_RESIDUALS (the default: forward keeps its residuals) and without (the backward recomputes
+    them) gives the same output and gradients bit for bit."""
+    import gdn_fast
+    B, T, H = 2, 200, 2
+    q, k, v, g, beta = _inputs(B, T, H, seed=51, correlated=True)
+    h0 = (np.random.default_rng(52).standard_normal((B, H, D, D)) * 0.1).astype(np.float32)
+    do = torch.from_numpy(mo.round_bf16(np.random.default_rng(53).standard_normal((B, T, H, D)).astype(np.float32)))
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev).to(torch.bfloat16)  # noqa: E731
+    outs = []
+    prev = gdn_fast.SAVE_RESIDUALS
+    try:
+        for save in (True, False):
+            gdn_fast.SAVE_RESIDUALS = save
+            ts = [bf(q).requires_grad_(True), bf(k).requires_grad_(True), bf(v).requires_grad_(True),
+                  torch.from_numpy(g).to(dev).requires_grad_(True), bf(beta).requires_grad_(True),
+                  torch.from_numpy(h0).to(dev).requires_grad_(True)]
+            o, hT = gdn_fast.fast_chunk_gated_delta_rule(*ts[:5], initial_state=ts[5])
+            ((o.float() * do.to(dev)).sum() + hT.float().sum()).backward()
+            outs.append([o.detach().float().cpu()] + [t.grad.float().cpu() for t in ts])
+    finally:
+        gdn_fast.SAVE_RESIDUALS = prev
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("rows,dim", [(1, 128), (1000, 128), (77, 64), (300, 96), (33, 512), (5, 8)])
 def test_l2norm_rows(rows, dim, dev):
     """lsurge_l2norm_rows / _bwd against the oracle (f64): y within bf16 rounding, r to f32 accuracy, dx within the
