@@ -456,6 +456,8 @@ __global__ __launch_bounds__(Cfg::GT) __attribute__((amdgpu_waves_per_eu(Cfg::NW
 void gemm_rows_kernel(RowsArgs a) {
   static_assert(!F8 || (BMODE == B_NK && Cfg::BK == 32), "FP8: both operands K-contiguous, 64-value stages");
   static_assert(ET == LSURGE_BF16 || (EPI == EPI_STORE && !F8), "f16 operands: plain store epilogue only");
+  static_assert(EPI != EPI_SWIGLU_FWD || (Cfg::BN / NS) % 2 == 0,
+                "SwiGLU forward: the gate and up halves need whole N-major sub-tiles each (BN a multiple of 256)");
   constexpr int UE = F8 ? 2 : 1;  // operand elements per 2-byte copy unit
   constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, ST = Cfg::ST;
   constexpr int TM = Cfg::TM, TN = Cfg::TN, FM = Cfg::FM, FN = Cfg::FN, SP = Cfg::SP;
