@@ -1,22 +1,28 @@
-// Chunked gated delta rule of the Gated DeltaNet block, forward (head dims 128, chunks of 64 tokens).
+// Chunked gated delta rule of the Gated DeltaNet block, forward and backward (head dims 128, chunks of 64 tokens),
+// and the row l2 normalisation of its qk-norm branch.
 //
-// Replaces fast_chunk_gated_delta_rule (modal/gdn_fast.py:37-113; compute dtype bf16, no qk-norm, no context
-// parallelism).  Per sequence b and head h, with state S [Dk, Dv]:
+// Replaces fast_chunk_gated_delta_rule (modal/gdn_fast.py:37-113; compute dtype bf16, no context parallelism) and its
+// XLA autodiff.  Per sequence b and head h, with state S [Dk, Dv]:
 //   S_t = exp(g_t) (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T,   o_t = S_t^T q_t / sqrt(Dk)
-// computed in the reference's chunked WY form.  Two kernels:
+// computed in the reference's chunked WY form.  Forward, two kernels:
 //   gdn_chunk_kernel  one workgroup per (chunk, head, sequence), all chunks at once: the decayed strictly-lower
-//                     S = (k beta) k^T, A = (I + S)^-1 by forward substitution, u = A (v beta), w = A (k beta e^gcum)
-//                     (both rounded to bf16, as the reference's compute dtype: gdn_fast.py:88-90), and the decayed
-//                     intra-chunk attention q k^T (the scan body's attn_i, gdn_fast.py:103-105, which does not
-//                     depend on the state).
+//                     S = (k beta) k^T, A = (I + S)^-1 by blocked forward substitution, u = A (v beta),
+//                     w = A (k beta e^gcum) (both rounded to bf16, as the reference's compute dtype:
+//                     gdn_fast.py:88-90), and the decayed intra-chunk attention q k^T (the scan body's attn_i,
+//                     gdn_fast.py:103-105, which does not depend on the state); optionally S and A for the backward.
 //   gdn_scan_kernel   one workgroup per (32 value columns, head, sequence), the chunks in order: the value columns
-//                     of the state evolve independently, so the state's 128 x 32 slice stays in LDS and the scan
-//                     runs on 4x as many workgroups as there are heads.  Per chunk (gdn_fast.py:99-109):
+//                     of the state evolve independently, so the state's 128 x 32 slice stays in the accumulators of
+//                     four waves and the scan runs on 4x as many workgroups as there are heads.  Per chunk
+//                     (gdn_fast.py:99-109):
 //                       v_new = u - w S,  o = (q e^gcum) S + attn v_new,  S = e^gcum_last S + (k e^(gcum_last-gcum))^T v_new
-// The chunk kernels' arithmetic is f32 on the VALU (the reference runs these products at HIGHEST precision); the forward
-// scan runs its products on the bf16 matrix cores with every f32 operand split into two bf16 terms (16 significant
-// bits, products exact, f32 sums).  Padding tokens past T are zeros with g = 0, as the reference pads
-// (gdn_fast.py:61-65).
+//                     optionally storing the state entering every chunk for the backward.
+// Backward, three more: gdn_bscan_kernel (reverse scan of the state gradient), gdn_bgrad_kernel (per chunk, the
+// products with the stored state and its gradient) and gdn_bchunk_kernel (the chunk-local backward through A, S and
+// the attention).  The training forward keeps the chunk products and the per-chunk states for them
+// (lsurge_gdn_chunked_fwd_save); lsurge_gdn_chunked_bwd recomputes them instead.
+// Every product runs on the bf16 matrix cores with each f32 operand split into two bf16 terms (16 significant bits,
+// products exact, f32 sums), as the reference runs them at HIGHEST precision.  Padding tokens past T are zeros with
+// g = 0, as the reference pads (gdn_fast.py:61-65).
 #include <cstring>
 
 #include "launchers.h"
