@@ -5,12 +5,11 @@
 // + bias[e].  bf16 x bf16 products are exact in f32, so fused multiply-add and the CPU's separate multiply and
 // add give the same bits: the result is reproducible bit for bit on the CPU whatever the thread mapping.
 //
-// Two paths.  With a logits buffer: a logits kernel over (token block, expert block) tiles and a selection
-// kernel with one wave per token (below).  Without one, the fused kernel: one workgroup of 128 threads owns 64
-// tokens and all experts.  Thread (tq, eq) accumulates 4 tokens x EPT
-// experts in registers; per d it reads one f32x4 of x (4 tokens) and EPT/4 f32x4 of w from LDS, so the loop is
-// FMA-bound (32 FMAs per 3 LDS reads at E = 64).  The selection then runs one wave per token over the logits
-// left in LDS.
+// Two paths.  The split path (the ABI's lsurge_router_topk, and shapes the fused kernel does not take): a logits
+// kernel over (token block, expert block) tiles, then a selection kernel (one lane per token from 8192 tokens, else
+// one wave per token).  The layer's fused path (E = 32, 64, 128 or 256, k <= 8): router_fused_kernel, one workgroup
+// of 64 tokens x all experts computing the same logits, then top-k, softmax and the layout's per-64-token expert
+// histograms in the same workgroup (described at the kernel).
 #include "launchers.h"
 
 
