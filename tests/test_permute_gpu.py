@@ -123,6 +123,35 @@ def test_ragged_widths_and_sentinels(dev):
         check(mp.gather_reduce(x, _t(pos, torch.int32, dev), None, torch.float32), mo.gather_reduce(x_np, pos), 1e-6)
 
 
+@pytest.mark.parametrize("dname,k,d", [("bf16", 3, 256), ("bf16", 9, 1024), ("f32", 17, 264), ("f16", 12, 104),
+                                        ("bf16", 8, 7), ("f32", 1, 8)])
+def test_gather_reduce_dot_out_of_range_positions(dname, k, d, dev):
+    """gather_reduce and gather_dot with a quarter of the positions outside [0, m) (negative or past the end): such
+    a position contributes nothing to the reduction and gives the dot product 0.  k below, at and above the
+    kernels' batch of 8 choices, and widths on the 16-byte and on the scalar path."""
+    rng = np.random.default_rng(k * 100 + d)
+    m, n = 50, 40
+    dtype = TORCH_DT[dname]
+    tol = 1e-5 if dname == "f32" else 2e-2
+    y_np = _cast_np(rng.standard_normal((m, d)), dname)
+    pos = rng.integers(0, m, (n, k)).astype(np.int32)
+    bad = rng.random((n, k)) < 0.25
+    pos[bad] = rng.choice(np.array([-1, -7, m, m + 3, 2**31 - 1], np.int32), size=int(bad.sum()))
+    w_np = rng.random((n, k)).astype(np.float32)
+    g_np = rng.standard_normal((n, d)).astype(np.float32)
+    valid = (pos >= 0) & (pos < m)
+    rows = np.where(valid[..., None], y_np.astype(np.float64)[np.clip(pos, 0, m - 1)], 0.0)  # (n, k, d)
+    want_sum = rows.sum(1)
+    want_red = (rows * w_np[..., None]).sum(1)
+    want_dot = (rows * g_np[:, None, :]).sum(-1)
+    y, pos_t = _t(y_np, dtype, dev), _t(pos, torch.int32, dev)
+    check(mp.gather_reduce(y, pos_t, None, torch.float32), want_sum, tol)
+    check(mp.gather_reduce(y, pos_t, _t(w_np, torch.float32, dev), torch.float32), want_red, tol)
+    got_dot = mp.gather_dot(y, pos_t, _t(g_np, torch.float32, dev))
+    check(got_dot, want_dot, tol)
+    assert not got_dot.cpu().numpy()[~valid].any()  # exactly 0 where the position is out of range
+
+
 def test_empty_inputs(dev):
     x = torch.zeros((0, 64), dtype=torch.bfloat16, device=dev)
     idx = torch.zeros((0,), dtype=torch.int32, device=dev)
