@@ -309,36 +309,66 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_kernel(const void* __r
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
   for (int64_t t = wave; t < n; t += nwaves) {
     float dwv[16];
-    for (int j = 0; j < k; ++j) {
-      const int64_t r = pos[t * k + j];
-      const float wj = w[t * k + j];
-      float acc = 0.f;
-      if (r < 0 || r >= m) {
-        // out-of-range position: nothing written, dw = 0
-      } else if (VEC) {
-        for (int64_t c = lane * 8; c < d; c += 64 * 8) {
-          float v[8], gv[8], o[8];
-          V8<DT>::ld((const char*)y + (r * d + c) * ES, v);
-          V8<GT>::ld((const char*)g + (t * d + c) * GS, gv);
+    for (int j0 = 0; j0 < k; j0 += GK) {
+      // a batch of GK choices, as in gather_dot: positions and weights first, then g and the expert rows of every
+      // choice per column chunk.  An out-of-range position writes nothing and gives dw = 0.
+      int64_t src[GK];
+      bool ok[GK];
+      float wj[GK], acc[GK];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            if (GT != DT) gv[e] = round_to<DT>(gv[e]);  // g.astype(y.dtype) first (moe_permute.py:307)
-            acc += v[e] * gv[e];
-            o[e] = wj * gv[e];
+      for (int q = 0; q < GK; ++q) {
+        const int j = j0 + q;
+        const int64_t r = j < k ? pos[t * k + j] : -1;
+        ok[q] = r >= 0 && r < m;
+        src[q] = ok[q] ? r : 0;
+        wj[q] = j < k ? w[t * k + j] : 0.f;
+        acc[q] = 0.f;
+      }
+      if (VEC) {
+        for (int64_t c = lane * 8; c < d; c += 64 * 8) {
+          const typename V8<GT>::Raw graw = V8<GT>::ldraw((const char*)g + (t * d + c) * GS);
+          typename V8<DT>::Raw raw[GK];
+#pragma unroll
+          for (int q = 0; q < GK; ++q)
+            if (m > 0 && j0 + q < k) raw[q] = V8<DT>::ldraw((const char*)y + (src[q] * d + c) * ES);
+          float gv[8];
+          V8<GT>::cvt(graw, gv);
+          if (GT != DT)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) gv[e] = round_to<DT>(gv[e]);  // g.astype(y.dtype) first (moe_permute.py:307)
+#pragma unroll
+          for (int q = 0; q < GK; ++q) {
+            if (!ok[q]) continue;
+            float v[8], o[8];
+            V8<DT>::cvt(raw[q], v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              acc[q] += v[e] * gv[e];
+              o[e] = wj[q] * gv[e];
+            }
+            V8<DT>::st((char*)dy + (src[q] * d + c) * ES, o);
           }
-          V8<DT>::st((char*)dy + (r * d + c) * ES, o);
         }
       } else {
-        for (int64_t c = lane; c < d; c += 64) {
-          float gv = Elem<GT>::ld((const G*)g, t * d + c);
-          if (GT != DT) gv = round_to<DT>(gv);
-          acc += Elem<DT>::ld((const T*)y, r * d + c) * gv;
-          Elem<DT>::st((T*)dy, r * d + c, wj * gv);
+#pragma unroll
+        for (int q = 0; q < GK; ++q) {
+          if (!ok[q]) continue;
+          for (int64_t c = lane; c < d; c += 64) {
+            float gv = Elem<GT>::ld((const G*)g, t * d + c);
+            if (GT != DT) gv = round_to<DT>(gv);
+            acc[q] += Elem<DT>::ld((const T*)y, src[q] * d + c) * gv;
+            Elem<DT>::st((T*)dy, src[q] * d + c, wj[q] * gv);
+          }
         }
       }
-      acc = wave_sum(acc);
-      if (j < 16) dwv[j] = acc;
-      if (lane == 0 && dw) dw[t * k + j] = acc;
+#pragma unroll
+      for (int q = 0; q < GK; ++q) {
+        const int j = j0 + q;
+        if (j >= k) break;
+        const float sum = wave_sum(acc[q]);
+        if (j < 16) dwv[j] = sum;
+        if (lane == 0 && dw) dw[t * k + j] = sum;
+      }
     }
     if (dl && lane == 0) {  // choices past the 16 kept in registers come back from dw (written by this lane)
       float s = 0.f;
