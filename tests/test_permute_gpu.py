@@ -152,6 +152,42 @@ def test_gather_reduce_dot_out_of_range_positions(dname, k, d, dev):
     assert not got_dot.cpu().numpy()[~valid].any()  # exactly 0 where the position is out of range
 
 
+@pytest.mark.parametrize("dname,k,d", [("bf16", 6, 1024), ("f32", 11, 264), ("bf16", 3, 7)])
+def test_combine_bwd_out_of_range_positions(dname, k, d, dev):
+    """lsurge_combine_bwd with a quarter of the positions outside [0, m): dy rows are written only at the valid
+    positions (w_j g[t], rounded to y's dtype), the others keep what they held, and dw is exactly 0 for the invalid
+    choices and <g[t], y[pos]> for the valid ones."""
+    import _lib as L
+    rng = np.random.default_rng(k + d)
+    n = 30
+    m = n * k
+    dtype = TORCH_DT[dname]
+    tol = 1e-5 if dname == "f32" else 2e-2
+    y_np = _cast_np(rng.standard_normal((m, d)), dname)
+    pos = rng.permutation(m)[: n * k].reshape(n, k).astype(np.int32)
+    bad = rng.random((n, k)) < 0.25
+    pos[bad] = rng.choice(np.array([-1, -9, m, m + 5], np.int32), size=int(bad.sum()))
+    valid = (pos >= 0) & (pos < m)
+    w_np = rng.random((n, k)).astype(np.float32)
+    g_np = _cast_np(rng.standard_normal((n, d)), dname)
+    y, g = _t(y_np, dtype, dev), _t(g_np, dtype, dev)
+    pos_t, w = _t(pos, torch.int32, dev), _t(w_np, torch.float32, dev)
+    dy = torch.full((m, d), 7.0, dtype=dtype, device=dev)
+    dw = torch.empty((n, k), dtype=torch.float32, device=dev)
+    L.check(L.lib().lsurge_combine_bwd(L.ptr(y), L.dt(y), L.ptr(pos_t), L.ptr(w), n, k, d, L.ptr(g), L.dt(g),
+                                       L.ptr(dy), L.ptr(dw), L.stream(dev)), "combine_bwd")
+    got_dy, got_dw = dy.float().cpu().numpy(), dw.cpu().numpy()
+    want_dw = np.where(valid, np.einsum("tkd,td->tk", y_np.astype(np.float64)[np.clip(pos, 0, m - 1)],
+                                        g_np.astype(np.float64)), 0.0)
+    check(got_dw, want_dw, tol)
+    assert not got_dw[~valid].any()
+    hit = np.zeros(m, bool)
+    hit[pos[valid]] = True
+    assert np.all(got_dy[~hit] == 7.0)  # rows no valid position names are untouched
+    want_rows = w_np[valid][:, None].astype(np.float64) * g_np[np.nonzero(valid)[0]].astype(np.float64)
+    check(got_dy[pos[valid]], _cast_np(want_rows, dname), tol)
+
+
 def test_empty_inputs(dev):
     x = torch.zeros((0, 64), dtype=torch.bfloat16, device=dev)
     idx = torch.zeros((0,), dtype=torch.int32, device=dev)
