@@ -73,12 +73,17 @@ static int launch_splitk_reduce(const float* part, int S, int E, int64_t I, int6
 // sizes are clamped so that no group reaches past row m: negative sizes count as 0 and a sum above m is cut at m,
 // so a bad group_sizes array can never send the GEMMs outside lhs/out.
 // ragged_groups_kernel (one workgroup): clamped group starts and sizes and the exclusive scan of their tr-row
-// block counts (tr = 128, or 256 for the ping-pong kernel's tiles), 1024 groups per pass with a running carry.
+// block counts (tr = 128, or 256 for the ping-pong kernel's tiles), 1024 groups per pass with a running carry; then
+// the block table itself: block b belongs to the group e with e_boff[e] <= b < e_boff[e + 1] (binary search; empty
+// groups have e_boff[e] == e_boff[e + 1]), and entries past the count are empty.
 __global__ __launch_bounds__(1024) void ragged_groups_kernel(const int32_t* __restrict__ gs, int E, int64_t m, int tr,
                                                             int max_blocks, int32_t* __restrict__ e_row0,
                                                             int32_t* __restrict__ e_rows, int32_t* __restrict__ e_boff,
                                                             int32_t* __restrict__ num_blocks,
-                                                            int32_t* __restrict__ total_rows) {
+                                                            int32_t* __restrict__ total_rows,
+                                                            int32_t* __restrict__ blk_row0,
+                                                            int32_t* __restrict__ blk_rows,
+                                                            int32_t* __restrict__ blk_expert) {
   __shared__ int64_t wsum[16];
   __shared__ int wblk[16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -131,16 +136,9 @@ __global__ __launch_bounds__(1024) void ragged_groups_kernel(const int32_t* __re
     num_blocks[0] = min(carry_blk, max_blocks);
     total_rows[0] = (int32_t)min(carry_rows, m);
   }
-}
-
-// ragged_blocks_kernel (grid over the block bound): block b belongs to the group e with e_boff[e] <= b <
-// e_boff[e + 1] (binary search; empty groups have e_boff[e] == e_boff[e + 1]); entries past the count are empty.
-__global__ void ragged_blocks_kernel(const int32_t* __restrict__ e_row0, const int32_t* __restrict__ e_rows,
-                                     const int32_t* __restrict__ e_boff, int E, int tr, int max_blocks,
-                                     int32_t* __restrict__ blk_row0, int32_t* __restrict__ blk_rows,
-                                     int32_t* __restrict__ blk_expert) {
-  const int nb = min(e_boff[E], max_blocks);
-  for (int b = blockIdx.x * blockDim.x + threadIdx.x; b < max_blocks; b += gridDim.x * blockDim.x) {
+  __syncthreads();  // the workgroup's e_row0, e_rows and e_boff writes are visible to all its threads
+  const int nb = min(carry_blk, max_blocks);
+  for (int b = tid; b < max_blocks; b += 1024) {
     if (b >= nb) {
       blk_row0[b] = 0;
       blk_rows[b] = 0;
@@ -686,11 +684,7 @@ static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_
   int32_t* e_boff = nb + 4 + 2 * e;
   LSURGE_LAUNCH(KID_MISC, s,
                 hipLaunchKernelGGL(ragged_groups_kernel, dim3(1), dim3(1024), 0, s, gs, (int)e, m, tr, (int)mb, *e_row0,
-                                   *e_rows, e_boff, nb, *total_rows));
-  const unsigned grid = (unsigned)std::min<int64_t>((mb + 255) / 256, 1024);
-  LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(ragged_blocks_kernel, dim3(grid), dim3(256), 0, s, *e_row0, *e_rows, e_boff, (int)e,
-                                   tr, (int)mb, blk_row0, blk_rows, blk_expert));
+                                   *e_rows, e_boff, nb, *total_rows, blk_row0, blk_rows, blk_expert));
   g->blk_expert = blk_expert;
   g->blk_rows = blk_rows;
   g->blk_row0 = blk_row0;
