@@ -99,3 +99,32 @@ def test_l2norm_argument_errors_without_gpu():
     assert lib.lsurge_l2norm_rows_bwd(fake, fake, None, 10, 128, fake, None) != 0
     assert b"null pointer" in lib.lsurge_last_error()
     assert lib.lsurge_l2norm_rows(fake, 0, 128, 1e-6, fake, None, None) == 0  # empty: nothing launched
+
+
+def test_gdn_saved_split_argument_errors_without_gpu():
+    """lsurge_gdn_chunked_fwd_save / lsurge_gdn_chunked_bwd_saved check their buffers and shapes before touching the
+    device; the saved buffer is smaller than the recomputing backward's workspace, and the two parts add up to it."""
+    lib = L.lib()
+    fake = ctypes.c_void_p(256)
+    B, T, H, D = 2, 200, 3, 128
+    saved = lib.lsurge_gdn_chunked_saved_bytes(B, T, H, D, D)
+    scratch = lib.lsurge_gdn_chunked_bwd_saved_workspace_bytes(B, T, H, D, D)
+    full = lib.lsurge_gdn_chunked_bwd_workspace_bytes(B, T, H, D, D)
+    assert 0 < saved < full and saved + scratch == full
+    assert lib.lsurge_gdn_chunked_saved_bytes(B, T, H, 64, D) == 0
+    rc = lib.lsurge_gdn_chunked_fwd_save(fake, fake, fake, fake, fake, B, T, H, D, D, None, fake, None, fake, saved - 1,
+                                         None)
+    assert rc != 0 and b"saved buffer" in lib.lsurge_last_error()
+    rc = lib.lsurge_gdn_chunked_fwd_save(fake, fake, fake, fake, fake, B, T, H, D, D, None, None, None, fake, saved,
+                                         None)
+    assert rc != 0 and b"null pointer" in lib.lsurge_last_error()
+    rc = lib.lsurge_gdn_chunked_fwd_save(fake, fake, fake, fake, fake, B, T, H, 64, D, None, fake, None, fake, saved,
+                                         None)
+    assert rc != 0 and b"head dims" in lib.lsurge_last_error()
+    args = [fake] * 4 + [B, T, H, D, D, fake, None, fake, fake, fake, fake, fake, None]
+    rc = lib.lsurge_gdn_chunked_bwd_saved(*args, fake, saved, fake, scratch - 1, None)
+    assert rc != 0 and b"workspace" in lib.lsurge_last_error()
+    rc = lib.lsurge_gdn_chunked_bwd_saved(*args, fake, saved - 1, fake, scratch, None)
+    assert rc != 0 and b"saved buffer" in lib.lsurge_last_error()
+    rc = lib.lsurge_gdn_chunked_bwd_saved(*args, ctypes.c_void_p(264), saved, fake, scratch, None)
+    assert rc != 0 and b"16-byte aligned" in lib.lsurge_last_error()
