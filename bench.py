@@ -718,6 +718,9 @@ def main():
                          "colab/tpu_permute_bench.py; ragged_dot: the padded_gmm drop-in at the layer's per-weight "
                          "shapes (modal/gemm_bench.py)")
     ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")
+    ap.add_argument("--gemm-variant", type=int, default=1, choices=[0, 1],
+                    help="grouped-GEMM kernels: 1 the persistent 256 x 256 kernel (default), 0 the classic 128 x 256 "
+                         "and ping-pong kernels (lsurge_set_gemm_variant; bitwise identical results)")
     ap.add_argument("--concurrency", type=int, default=1,
                     help="timed region: 1 runs the layer's independent chains on helper streams "
                          "(lsurge_set_concurrency), 0 everything on one stream")
@@ -750,6 +753,10 @@ def main():
         return
 
     import torch
+
+    if not a.copy_probe:
+        import _lib as _vlib
+        _vlib.check(_vlib.lib().lsurge_set_gemm_variant(a.gemm_variant), "set_gemm_variant")
 
     if a.copy_probe:
         n = a.copy_probe << 20
@@ -885,7 +892,7 @@ def main():
                                f"E={c['E']}x{c['f']} top-{c['k']} shared={c['fs']}" + (" zipf-bias" if c["zipf"] else ""),
                    "T": c["T"], "d_model": c["d"], "experts": c["E"], "top_k": c["k"], "expert_ffn": c["f"],
                    "shared_ffn": c["fs"], "block_rows": 128, "parallelism": "single GPU",
-                   "concurrent_streams": bool(a.concurrency)},
+                   "concurrent_streams": bool(a.concurrency), "gemm_variant": a.gemm_variant},
         "layer_tflops": round(layer_flops(c) / (ms * 1e-3) / 1e12, 1),
         "mfu": round(layer_flops(c) / (ms * 1e-3) / 1e12 / peak_mfma, 4),
         "roofline": {"kernel": dom, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,

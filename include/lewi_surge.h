@@ -52,6 +52,17 @@ const char* lsurge_last_error(void);
 int lsurge_set_concurrency(int on);
 int lsurge_get_concurrency(void);
 
+/* Kernel family of the bf16 / f16 grouped GEMMs (the layer's row GEMMs and ragged_dot): LSURGE_GEMM_CLASSIC
+ * (128 x 256 tiles over 128-row blocks, and the 8-wave ping-pong kernel over 256-row tiles) or LSURGE_GEMM_G256 (the
+ * default: persistent 256 x 256 x 64 tiles, one workgroup per CU).  Both compute every output element with the same
+ * sequence of MFMA steps, so the results are bitwise identical; the switch exists for same-process A/B timing and for
+ * the tests that check that identity.  Process-wide setting.  No reference counterpart (XLA picks the reference's
+ * GEMM kernels). */
+#define LSURGE_GEMM_CLASSIC 0
+#define LSURGE_GEMM_G256 1
+int lsurge_set_gemm_variant(int variant);
+int lsurge_get_gemm_variant(void);
+
 /* ------------------------------------------------------------------------------------------------
  * Row movement (memory-bound).
  * ------------------------------------------------------------------------------------------------ */

@@ -49,6 +49,8 @@ _SIGS = {
     "lsurge_last_error": (ctypes.c_char_p, []),
     "lsurge_set_concurrency": (_int, [_int]),
     "lsurge_get_concurrency": (_int, []),
+    "lsurge_set_gemm_variant": (_int, [_int]),
+    "lsurge_get_gemm_variant": (_int, []),
     "lsurge_gather_rows": (_int, [_p, _i64, _i64, _int, _p, _i64, _p, _p, _p]),
     "lsurge_gather_reduce": (_int, [_p, _i64, _i64, _int, _p, _i64, _i64, _p, _p, _int, _p]),
     "lsurge_gather_dot": (_int, [_p, _i64, _i64, _int, _p, _i64, _i64, _p, _int, _p, _p]),

@@ -89,6 +89,9 @@ DeviceFork g_fork[kMaxDevices];
 }  // namespace
 
 static std::atomic<int> g_concurrency{0};
+static std::atomic<int> g_gemm_variant{LSURGE_GEMM_G256};
+
+int gemm_variant() { return g_gemm_variant.load(std::memory_order_relaxed); }
 
 int fork_acquire(ForkSet* f, hipStream_t main) {
   if (!g_concurrency.load(std::memory_order_relaxed)) {  // serial: every chain on the caller's stream
@@ -170,6 +173,14 @@ int lsurge_set_concurrency(int on) {
   return LSURGE_OK;
 }
 int lsurge_get_concurrency(void) { return g_concurrency.load(); }
+int lsurge_set_gemm_variant(int variant) {
+  if (variant != LSURGE_GEMM_CLASSIC && variant != LSURGE_GEMM_G256)
+    return set_error(LSURGE_ERR_INVALID, "gemm variant %d: expected LSURGE_GEMM_CLASSIC (0) or LSURGE_GEMM_G256 (1)",
+                     variant);
+  g_gemm_variant.store(variant);
+  return LSURGE_OK;
+}
+int lsurge_get_gemm_variant(void) { return g_gemm_variant.load(); }
 const char* lsurge_last_error(void) { return g_err; }
 
 int lsurge_test_fail_launch(int kernel_id, int nth) {

@@ -102,6 +102,8 @@ struct ForkSet {
   int dev;
 };
 int fork_acquire(ForkSet* f, hipStream_t main);
+// the grouped-GEMM kernel family (lsurge_set_gemm_variant)
+int gemm_variant();
 void fork_release(ForkSet* f);
 // make `main` wait for everything enqueued so far on every helper of f (the error path of a forked call)
 void fork_join_all(ForkSet* f, hipStream_t main);

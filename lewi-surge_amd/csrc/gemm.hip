@@ -3,6 +3,7 @@
 // modal/padded_gmm.py:45-69 (padded_ragged_dot and its gather-only VJP).
 #include <mutex>
 
+#include "gemm256.h"
 #include "gemm_kernels.h"
 #include "launchers.h"
 
@@ -301,10 +302,43 @@ static int max_blocks_of(const GemmBlocks& g) {
   return g.blk_expert ? g.max_blocks : (int)((g.dense_rows + g.tile_rows - 1) / g.tile_rows);
 }
 
+// launch g256::rows_kernel (the persistent 256 x 256 kernel) over 256-row tiles or dense rows: one workgroup per CU
+template <int BMODE, int EPI>
+static int launch_rows256(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t s, int et) {
+  constexpr int nout = EPI == EPI_SWIGLU_FWD ? g256::BN / 2 : g256::BN;
+  a.max_tiles = max_blocks_of(g);
+  a.n_tiles = (int)((a.N + nout - 1) / nout);
+  if (a.max_tiles == 0) return LSURGE_OK;
+  const dim3 grid(g256::NWG), block(256);
+  const bool f16 = et == LSURGE_F16, f32out = a.Cf != nullptr;
+  if constexpr (EPI == EPI_SWIGLU_FWD) {
+    if (a.a_rows) LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, true>), grid, block, 0, s, a));
+    else LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false>), grid, block, 0, s, a));
+  } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+    LSURGE_REQUIRE(!a.a_rows, "grouped GEMM: no row gather with the SwiGLU backward");
+    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false>), grid, block, 0, s, a));
+  } else {
+    LSURGE_REQUIRE(!a.a_rows, "grouped GEMM: no row gather with the plain store");
+    if (f16 && f32out)
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false, LSURGE_F16, true>), grid, block, 0, s, a));
+    else if (f16)
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false, LSURGE_F16, false>), grid, block, 0, s, a));
+    else if (f32out)
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false, LSURGE_BF16, true>), grid, block, 0, s, a));
+    else
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false, LSURGE_BF16, false>), grid, block, 0, s, a));
+  }
+  return LSURGE_OK;
+}
+
 // launch gemm_rows_kernel with the tile config that matches the row tiles of g (column tiles: BN output columns, or
-// BN / 2 for the SwiGLU forward)
+// BN / 2 for the SwiGLU forward); 256-row tiles of bf16 / f16 operands go to the persistent kernel when it is selected
 template <int BMODE, int EPI, int F8 = 0>
 static int launch_rows(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t s, int et = LSURGE_BF16) {
+  if constexpr (!F8) {
+    if (gemm_variant() == LSURGE_GEMM_G256 && g.tile_rows == 256 && !a.amax && a.k_split % g256::BK == 0)
+      return launch_rows256<BMODE, EPI>(kid, g, a, s, et);
+  }
   LSURGE_REQUIRE(g.tile_rows == 128 || g.tile_rows == 256, "grouped GEMM: tile_rows=%d must be 128 or 256", g.tile_rows);
   a.max_tiles = max_blocks_of(g);
   a.n_tiles = (int)((a.N + (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN) - 1) / (EPI == EPI_SWIGLU_FWD ? BN / 2 : BN));
@@ -695,6 +729,9 @@ static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_
   return LSURGE_OK;
 }
 
+// row tiles of the bf16 / f16 ragged_dot GEMMs: 256 rows for the persistent kernel, else 128
+static int ragged_tile_rows() { return lsurge::gemm_variant() == LSURGE_GEMM_G256 ? 256 : 128; }
+
 int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_sizes, int64_t m, int64_t kdim, int64_t n,
                       int64_t e, int in_dtype, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
                       lsurge_stream_t stream) {
@@ -708,7 +745,9 @@ int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_siz
   hipStream_t s = (hipStream_t)stream;
   lsurge::GemmBlocks g;
   int32_t *total, *e_row0, *e_rows;
-  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0, &e_rows)) return rc;
+  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &g, &total, &e_row0, &e_rows,
+                            ragged_tile_rows()))
+    return rc;
   const bool f32 = out_dtype == LSURGE_F32;
   if (int rc = lsurge::gemm_rows_kn(KID_MISC, g, lhs, kdim, rhs, n, kdim * n, kdim, n, out, n, s, f32,
                                     lsurge::ExtraExpert(), in_dtype))
@@ -808,7 +847,9 @@ int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group
   hipStream_t s = (hipStream_t)stream;
   lsurge::GemmBlocks gb;
   int32_t *total, *e_row0, *e_rows;
-  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &gb, &total, &e_row0, &e_rows)) return rc;
+  if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &gb, &total, &e_row0, &e_rows,
+                            ragged_tile_rows()))
+    return rc;
   // dlhs[r] = g[r] @ rhs[e]^T : rhs[e] is [K, N] = k-major storage of the [N -> K] operand
   if (m > 0) {
     if (int rc = lsurge::gemm_rows_nk(KID_MISC, gb, g, n, rhs, nullptr, 0, n, kdim * n, n, kdim, dlhs, kdim, false,

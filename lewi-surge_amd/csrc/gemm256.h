@@ -1,0 +1,432 @@
+// Persistent 256 x 256 grouped GEMM of the MoE layer on CDNA4 matrix cores (bf16 or f16 inputs, f32 accumulation,
+// v_mfma_f32_32x32x16_bf16 / _f16).  One workgroup of 4 waves per CU; wave (wm, wn) owns a 128 x 128 block of the
+// 256 x 256 output tile: 256 accumulator registers, the whole AccVGPR file of a wave that is alone on its SIMD.
+//
+// Replaces the padded batched einsum of modal/padded_gmm.py:66-69 (and its autodiff) for the layer's row GEMMs, like
+// gemm_rows_kernel in gemm_kernels.h, whose operand layouts, tile tables and epilogues it keeps.  What differs is how
+// a tile's K loop is fed:
+//  - Global -> VGPR -> LDS.  K moves in 64-deep stages.  Every lane holds one stage of its copies in registers
+//    (16 x 16 bytes) and writes it to the other half of an LDS double buffer (2 x 64 KiB) while the MFMAs run on the
+//    current half; the registers are then refilled with the stage after.  One workgroup barrier per stage.  The
+//    VGPR path moves about twice the bytes per clock of buffer_load ... lds on this chip, which is what the 4-wave
+//    128 x 256 x 32 kernel's copy stream was limited by.
+//  - Explicit issue order.  A stage is four 16-deep MFMA steps of 16 MFMAs each.  During a step the wave issues the
+//    next step's 8 fragment reads, then a third of the stage's register -> LDS writes and global loads, each pinned
+//    between two MFMAs with sched_group_barrier, so the matrix pipe never waits on a burst of memory instructions.
+//    The last step starts with the stage barrier and reads the next stage's first fragments.
+//  - Persistent tiles.  The grid is one workgroup per CU (256); workgroup l of XCD x walks the tiles
+//    xbeg + l, xbeg + l + nper, ... of that XCD's contiguous share of the tiles (so neighbouring tiles of one expert
+//    share an XCD's L2).  The load stream runs across tile boundaries: the next tile's first stages are loaded while
+//    the current tile's last stages compute, and its first stage is already in LDS when the epilogue runs.
+//  - Epilogue through a wave-private 8 KiB LDS area beside the ring (32 rows of the wave's block at a time), so every
+//    global store (and the SwiGLU backward's loads of g and u) covers whole 128- or 256-byte row segments; the copy
+//    ring is untouched, and the next tile's loads stay in flight.
+//
+// Every output element is the same ascending sequence of 16-deep MFMA steps as in gemm_rows_kernel, so the results
+// are bitwise those of the other tile shapes.  Stages past K load zeros.
+#pragma once
+#include "gemm_kernels.h"
+
+namespace lsgemm {
+namespace g256 {
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int OP_BYTES = 256 * BK * 2;        // one operand of one stage: 32 KiB
+constexpr int STAGE_BYTES = 2 * OP_BYTES;     // A then B
+constexpr int RING_BYTES = 2 * STAGE_BYTES;   // double buffer, 128 KiB
+constexpr int STG_BYTES = 8192;               // per-wave epilogue staging
+constexpr int SMEM_BYTES = RING_BYTES + 4 * STG_BYTES;  // 160 KiB: the whole LDS of a CU
+constexpr int NWG = 256;                      // persistent grid: one workgroup per CU (a multiple of 8 XCDs)
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// raw buffer over [p, p + bytes): loads past the end return zeros (every span is below 2^31 bytes, host-checked)
+__device__ __forceinline__ rsrc_t rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 ld16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+enum { SG_MFMA = 0x8, SG_VMEM_R = 0x20, SG_DS_R = 0x100, SG_DS_W = 0x200 };
+
+// Row tile of the 256-row table, or of a dense matrix.  The table is read after the kernel's own stores, so the
+// compiler cannot tell the values are uniform; readfirstlane keeps them (and the descriptors made from them) in
+// scalar registers, where a divergent descriptor would wrap every buffer load in a waterfall loop.
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+struct Tile {
+  int expert, rows;
+  int64_t row0;
+};
+__device__ __forceinline__ Tile row_tile(const RowsArgs& a, int b) {
+  Tile t;
+  if (a.t_expert) {
+    t.expert = uni(a.t_expert[b]);
+    t.rows = uni(a.t_rows[b]);
+    t.row0 = a.t_row0 ? (int64_t)uni(a.t_row0[b]) : (int64_t)b * BM;
+  } else {
+    t.expert = 0;
+    t.row0 = (int64_t)b * BM;
+    t.rows = (int)min((int64_t)BM, a.dense_rows - t.row0);
+  }
+  return t;
+}
+
+// Row GEMM C[tile rows, n tile] = A[tile rows, :] @ B[expert(tile)] over the row tiles of a.t_expert / t_rows /
+// t_row0 (num_tiles[0] real ones) or of a dense matrix, n tiles of BN columns (SwiGLU forward: BN / 2 outputs, the
+// gate and up columns side by side).  Operands, epilogues and arguments as gemm_rows_kernel (RowsArgs); amax is not
+// supported here.  GATHER: A rows through a.a_rows; OUTF32: the plain store writes a.Cf.
+template <int BMODE, int EPI, bool GATHER, int ET = LSURGE_BF16, bool OUTF32 = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void rows_kernel(RowsArgs a) {
+  static_assert(ET == LSURGE_BF16 || EPI == EPI_STORE, "f16 operands: plain store epilogue only");
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
+  constexpr int NOUT = EPI == EPI_SWIGLU_FWD ? BN / 2 : BN;  // output columns of an n tile
+
+  // ---- this workgroup's tiles: XCD x = blockIdx % 8 takes tiles [x T / 8, (x + 1) T / 8) of the T that exist
+  const int ntr = a.t_expert ? min(uni(a.num_tiles[0]), a.max_tiles) : (int)((a.dense_rows + BM - 1) / BM);
+  const int total = ntr * a.n_tiles;
+  const int xcd = blockIdx.x % 8, nper = gridDim.x / 8;
+  const int xbeg = (int)((int64_t)xcd * total / 8), xend = (int)((int64_t)(xcd + 1) * total / 8);
+  int t_cur = xbeg + blockIdx.x / 8;
+  if (t_cur >= xend) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int K = (int)a.K, N = (int)a.N, ksplit = (int)a.k_split;
+  const int nk = ((K + 2 * BK - 1) / (2 * BK)) * 2;  // stages per tile, even (trailing zero stage for odd counts)
+  const uint32_t lda2 = (uint32_t)a.lda * 2u, ldb2 = (uint32_t)a.ldb * 2u;
+
+  // ---- copy geometry.  K-major operand (A, and B_NK): copy i of a lane takes row 32 i + tid / 8, 16-byte chunk
+  // tid % 8 of the stage's 64 k; LDS row r of 128 B holds chunk c at slot c ^ ((r >> 1) & 7).
+  const int kr = tid >> 3, kc = tid & 7;
+  const uint32_t km_w = (uint32_t)(kr * 128 + ((kc ^ ((kr >> 1) & 7)) << 4));
+  // N-major B (B_KN): copy i takes k row 16 (i % 4) + tid / 16 of sub-tile i / 4 (128 columns; SwiGLU: 0 gate, 1 up),
+  // chunk tid % 16; LDS: sub-tiles of 64 k rows x 256 B, chunk c of row k at slot c ^ ((k & 3) << 2) (nm_off).
+  const int nr = tid >> 4, nc = tid & 15;
+  const uint32_t nm_w = (uint32_t)(nr * 256 + ((nc ^ ((nr & 3) << 2)) << 4));
+
+  // ---- load cursor: tile lt (the stage to load comes with each call); its descriptors and per-lane offsets
+  int lt = t_cur;
+  rsrc_t la, lb, lb2;
+  const int a_kc = 8 * kc;  // k of this lane's K-major chunk within a stage
+  // K-major copies (contiguous A rows, B_NK): row 32 i + kr of the operand at a byte offset of km_base + 32 i ld
+  const uint32_t ka_base = (uint32_t)kr * lda2 + 16u * kc, kb_base = (uint32_t)kr * ldb2 + 16u * kc;
+  // B_KN copies: k row 16 (i % 4) + nr, column n0 + 8 nc (+ 128 for sub-tile 1 of the plain store); whether the
+  // column exists, per sub-tile
+  const uint32_t nb_base = (uint32_t)nr * ldb2 + 16u * nc;
+  bool ncol_ok[2] = {true, true};
+  // gathered A: byte offsets of this lane's 8 source rows in the cursor's tile, and the raw row indices of the tile
+  // after it (read one tile ahead, so their latency hides behind a whole tile)
+  uint32_t a_off[8];
+  const uint64_t magic = div_magic(GATHER ? a.a_div : 1);
+  int pf_t = -1;
+  int pf_idx[8];
+  auto fetch_idx = [&](int t) {
+    const Tile rt = row_tile(a, t / a.n_tiles);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 32 * i + kr;
+      const int v = a.a_rows[rt.row0 + min(r, rt.rows - 1)];  // rows past the tile: not read, marked -1
+      pf_idx[i] = r < rt.rows ? v : -1;
+    }
+    pf_t = t;
+  };
+  auto set_ld = [&]() {
+    const int b = lt / a.n_tiles, nt = lt % a.n_tiles;
+    const Tile rt = row_tile(a, b);
+    const bool xe = rt.expert == a.x_expert;
+    const bf16_t* Bb = xe ? a.Bx : a.B + (int64_t)rt.expert * a.b_estride;
+    const bf16_t* B2b = xe ? (a.B2x ? a.B2x : Bb) : (a.B2 ? a.B2 + (int64_t)rt.expert * a.b_estride : Bb);
+    if (GATHER) {
+      if (pf_t != lt) fetch_idx(lt);
+      la = rsrc(a.A, a.a_nrows * (int64_t)a.lda * 2);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int src = pf_idx[i] >= 0 ? div_by(pf_idx[i], magic) : -1;
+        a_off[i] = src >= 0 ? (uint32_t)src * lda2 + 16u * kc : OOB;
+      }
+      if (lt + nper < xend) fetch_idx(lt + nper);
+    } else {
+      la = rsrc(a.A + rt.row0 * a.lda, (int64_t)rt.rows * a.lda * 2);  // rows past the tile: zeros
+    }
+    if (BMODE == B_NK) {
+      const int64_t n0 = (int64_t)nt * BN;
+      const int64_t nb = max((int64_t)0, (int64_t)N - n0);  // columns of this tile that exist
+      lb = rsrc(Bb + n0 * a.ldb, nb * a.ldb * 2);
+      lb2 = rsrc(B2b + n0 * a.ldb, nb * a.ldb * 2);
+    } else {
+      const int64_t n0 = (int64_t)nt * NOUT;
+      lb = rsrc(Bb + n0, ((int64_t)K * a.ldb - n0) * 2);  // rows past K: zeros
+      lb2 = rsrc(B2b + n0, ((int64_t)K * a.ldb - n0) * 2);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) ncol_ok[h] = n0 + (EPI == EPI_SWIGLU_FWD ? 0 : NOUT / 2 * h) + 8 * nc < N;
+    }
+  };
+  set_ld();
+
+  u32x4 R[16];  // one stage of this lane's copies: A chunks 0..7, B chunks 8..15
+  // copy c of stage lk of the cursor's tile (nothing past the last tile: zeros)
+  auto gload = [&](int c, int lk) {
+    const bool live = lt < xend;
+    const int k0 = lk * BK;
+    if (c < 8) {
+      const bool ok = live && k0 + a_kc < K;
+      const uint32_t off = GATHER ? a_off[c] : ka_base + (uint32_t)(32 * c) * lda2;
+      R[c] = ld16(la, ok ? off + 2u * (uint32_t)k0 : OOB);
+    } else {
+      const int i = c - 8;
+      if (BMODE == B_NK) {
+        const bool second = ksplit && k0 >= ksplit;  // uniform
+        const int kb = second ? k0 - ksplit : k0;
+        const bool ok = live && k0 + a_kc < K;
+        R[c] = ld16(second ? lb2 : lb, ok ? kb_base + (uint32_t)(32 * i) * ldb2 + 2u * (uint32_t)kb : OOB);
+      } else {
+        const bool up = EPI == EPI_SWIGLU_FWD && i >= 4;
+        const uint32_t off = nb_base + (uint32_t)(16 * (i & 3) + k0) * ldb2 + (EPI == EPI_SWIGLU_FWD ? 0u : 256u * (i >> 2));
+        R[c] = ld16(up ? lb2 : lb, live && ncol_ok[i >> 2] ? off : OOB);
+      }
+    }
+  };
+  auto swrite = [&](int c, int buf) {
+    char* p = smem + buf * STAGE_BYTES;
+    if (c < 8) p += 4096 * c + km_w;
+    else if (BMODE == B_NK) p += OP_BYTES + 4096 * (c - 8) + km_w;
+    else p += OP_BYTES + ((c - 8) >> 2) * (BK * 256) + 16 * 256 * ((c - 8) & 3) + nm_w;
+    *reinterpret_cast<u32x4*>(p) = R[c];
+  };
+
+  // ---- fragments: A rows wm 128 + 32 i + lane % 32, chunk 2 s + lane / 32 (same swizzle for every i)
+  uint32_t rofs[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) rofs[s] = (uint32_t)(fr * 128 + (((2 * s + fh) ^ ((fr >> 1) & 7)) << 4));
+  // B column of fragment j within the tile (SwiGLU forward: j < 2 gate, j >= 2 up, same output columns)
+  auto bcol = [&](int j) {
+    if (EPI == EPI_SWIGLU_FWD) return (j >> 1) * 128 + wn * 64 + 32 * (j & 1);
+    return wn * 128 + 32 * j;
+  };
+  typedef FragSet<4, 4> F;
+  auto fread = [&](F& f, int buf, int s) {
+    const char* st = smem + buf * STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      f.x[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(st + rofs[s] + wm * 128 * 128 + 4096 * i));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (BMODE == B_NK) {
+        f.w[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(st + OP_BYTES + rofs[s] + wn * 128 * 128 + 4096 * j));
+      } else {
+        const int col = bcol(j);
+        f.w[j] = frag_n(reinterpret_cast<const bf16_t*>(st + OP_BYTES) + (col >> 7) * (BK * 128), 16 * s, col & 127,
+                        lane);
+      }
+    }
+  };
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  auto mma = [&](const F& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32<ET>(f.w[j], f.x[i], acc[i][j]);
+  };
+
+  // ---- prologue: stage 0 -> LDS half 0, stage 1 -> registers
+#pragma unroll
+  for (int c = 0; c < 16; ++c) gload(c, 0);
+#pragma unroll
+  for (int c = 0; c < 16; ++c) swrite(c, 0);
+#pragma unroll
+  for (int c = 0; c < 16; ++c) gload(c, 1);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  F f0, f1;
+  fread(f0, 0, 0);
+
+  // One stage on LDS half `cur`: step s reads step s + 1's fragments (step 3: after the barrier that publishes
+  // the next stage, its step 0 from the other half) and, in steps 0..2, moves copies [16 s / 3, 16 (s + 1) / 3)
+  // from registers to the other half, each followed by the load of the same chunk of the stage after.
+  auto stage = [&](int cur, int lk) {
+    const int nxt = cur ^ 1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      F& fc = (s & 1) ? f1 : f0;
+      F& fn = (s & 1) ? f0 : f1;
+      if (s == 3) {
+        // every wave's copies of the next stage have landed, and nobody reads this half's predecessor any more
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        fread(fn, nxt, 0);
+      } else {
+        fread(fn, cur, s + 1);
+      }
+      const int lo = s < 3 ? 16 * s / 3 : 0, hi = s < 3 ? 16 * (s + 1) / 3 : 0;
+#pragma unroll
+      for (int c = lo; c < hi; ++c) {
+        swrite(c, nxt);
+        gload(c, lk);
+      }
+      mma(fc);
+      const int nops = 8 + 2 * (hi - lo);
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        const int o0 = m * nops / 16, o1 = (m + 1) * nops / 16;
+#pragma unroll
+        for (int o = o0; o < o1; ++o) {
+          if (o < 8) __builtin_amdgcn_sched_group_barrier(SG_DS_R, 1, 0);
+          else if ((o - 8) % 2 == 0) __builtin_amdgcn_sched_group_barrier(SG_DS_W, 1, 0);
+          else __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, 1, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // ---- epilogue of tile t_cur from the accumulators, through this wave's staging area; clears the accumulators
+  char* const stg = smem + RING_BYTES + wave * STG_BYTES;
+  bf16_t* const pC = a.C;
+  bf16_t* const pG = a.G;
+  bf16_t* const pU = a.U;
+  float* const pCf = a.Cf;
+  const int64_t ldc = a.ldc, ldg = a.ldg;
+  auto epilogue = [&]() {
+    const int b = t_cur / a.n_tiles, nt = t_cur % a.n_tiles;
+    const Tile rt = row_tile(a, b);
+    const int64_t n0 = (int64_t)nt * NOUT;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rbase = wm * 128 + 32 * i;  // first tile row of this slice
+      if (EPI == EPI_SWIGLU_FWD) {
+        // 32 rows x 64 outputs in two passes of 32 columns: the f32 gate fragment j and up fragment j + 2 side by side
+        // (chunks 0-7 and 8-15 of a 256-byte staging row), read back 4 columns per lane -> h = silu(g) u, g, u
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int ch = 2 * q + fh;
+            *reinterpret_cast<f32x4*>(stg + fr * 256 + ((ch ^ (fr & 15)) << 4)) =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            *reinterpret_cast<f32x4*>(stg + fr * 256 + (((8 + ch) ^ (fr & 15)) << 4)) =
+                f32x4{acc[i][j + 2][4 * q], acc[i][j + 2][4 * q + 1], acc[i][j + 2][4 * q + 2], acc[i][j + 2][4 * q + 3]};
+          }
+#pragma unroll
+          for (int it = 0; it < 4; ++it) {
+            const int r = 8 * it + (lane >> 3), c = lane & 7;
+            const f32x4 g = *reinterpret_cast<const f32x4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
+            const f32x4 u = *reinterpret_cast<const f32x4*>(stg + r * 256 + (((8 + c) ^ (r & 15)) << 4));
+            float h[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) h[t] = silu_f(g[t]) * u[t];
+            const int64_t col = n0 + wn * 64 + 32 * j + 4 * c;
+            if (rbase + r >= rt.rows || col >= N) continue;
+            const int64_t gr = rt.row0 + rbase + r;
+            *reinterpret_cast<u32x2*>(pC + gr * ldc + col) = u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+            if (pG) *reinterpret_cast<u32x2*>(pG + gr * ldg + col) = u32x2{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3])};
+            if (pU) *reinterpret_cast<u32x2*>(pU + gr * ldg + col) = u32x2{pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3])};
+          }
+        }
+      } else if (EPI == EPI_STORE && !OUTF32) {
+        // 32 rows x 128 columns of 16-bit outputs
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            uint32_t w0, w1;
+            if constexpr (ET == LSURGE_F16) {
+              typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+              w0 = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){acc[i][j][4 * q], acc[i][j][4 * q + 1]}, h2));
+              w1 = __builtin_bit_cast(uint32_t,
+                                      __builtin_convertvector((f32x2_t){acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]}, h2));
+            } else {
+              w0 = pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+              w1 = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+            }
+            *reinterpret_cast<u32x2*>(stg + fr * 256 + (((4 * j + q) ^ (fr & 15)) << 4) + 8 * fh) = u32x2{w0, w1};
+          }
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+          const int r = 4 * it + (lane >> 4), c = lane & 15;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
+          const int64_t col = n0 + wn * 128 + 8 * c;
+          if (rbase + r < rt.rows && col < N) *reinterpret_cast<u32x4*>(pC + (rt.row0 + rbase + r) * ldc + col) = v;
+        }
+      } else {
+        // f32 slices of 32 rows x 64 columns (fragments j = 2 jp, 2 jp + 1): the plain f32 store, or dH of the
+        // SwiGLU backward -> [dG | dU] from the saved g, u
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp) {
+          u32x2 gq[8], uq[8];
+          if (EPI == EPI_SWIGLU_BWD) {  // fetch g, u first, so their latency overlaps the LDS round trip
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+              const int r = 4 * it + (lane >> 4);
+              const int64_t col = n0 + wn * 128 + 64 * jp + 4 * (lane & 15);
+              const bool ok = rbase + r < rt.rows && col < N;
+              const int64_t off = ok ? (rt.row0 + rbase + r) * ldg + col : rt.row0 * ldg;
+              gq[it] = *reinterpret_cast<const u32x2*>(pG + off);
+              uq[it] = *reinterpret_cast<const u32x2*>(pU + off);
+            }
+          }
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int ch = 8 * jj + 2 * q + fh;  // 16-byte chunk of 4 f32 columns
+              *reinterpret_cast<f32x4*>(stg + fr * 256 + ((ch ^ (fr & 15)) << 4)) =
+                  f32x4{acc[i][2 * jp + jj][4 * q], acc[i][2 * jp + jj][4 * q + 1], acc[i][2 * jp + jj][4 * q + 2],
+                        acc[i][2 * jp + jj][4 * q + 3]};
+            }
+#pragma unroll
+          for (int it = 0; it < 8; ++it) {
+            const int r = 4 * it + (lane >> 4), c = lane & 15;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
+            const int64_t col = n0 + wn * 128 + 64 * jp + 4 * c;
+            if (rbase + r >= rt.rows || col >= N) continue;
+            const int64_t gr = rt.row0 + rbase + r;
+            if (EPI == EPI_STORE) {
+              *reinterpret_cast<f32x4*>(pCf + gr * ldc + col) = v;
+            } else {
+              float dg[4], du[4];
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                const uint32_t gw = gq[it][t >> 1], uw = uq[it][t >> 1];
+                const float g = __uint_as_float((t & 1) ? (gw & 0xffff0000u) : (gw << 16));
+                const float u = __uint_as_float((t & 1) ? (uw & 0xffff0000u) : (uw << 16));
+                const float sg = sigmoid_f(g);
+                dg[t] = v[t] * u * sg * (1.f + g * (1.f - sg));
+                du[t] = v[t] * g * sg;
+              }
+              *reinterpret_cast<u32x2*>(pC + gr * ldc + col) = u32x2{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
+              *reinterpret_cast<u32x2*>(pC + gr * ldc + N + col) =
+                  u32x2{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    }
+  };
+
+  // stage kt loads stage kt + 2: within a tile's last pair of stages, the first two of the next tile
+  while (true) {
+    for (int kt = 0; kt < nk; kt += 2) {
+      if (kt + 2 == nk) {  // the last pair loads the next tile's first two stages
+        lt += nper;
+        if (lt < xend) set_ld();
+      }
+      const int lk = kt + 2 == nk ? 0 : kt + 2;
+      stage(0, lk);
+      stage(1, lk + 1);
+    }
+    epilogue();
+    t_cur += nper;
+    if (t_cur >= xend) break;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the zero loads past the last tile land before the wave ends
+}
+
+}  // namespace g256
+}  // namespace lsgemm

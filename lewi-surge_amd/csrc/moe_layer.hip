@@ -495,8 +495,11 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
                                          (char*)workspace + hist_bytes + f8_bytes,
                                          workspace_bytes - hist_bytes - f8_bytes, st, tiles, chunks))
     return rc;
-  // the routed forward GEMMs run 128-row blocks on the 4-wave kernel (the ping-pong kernel measured no faster here)
-  const lsurge::GemmBlocks blocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
+  // the routed forward GEMMs: the 256-row tiles (routed ones) on the persistent kernel, or, with the classic kernels,
+  // 128-row blocks on the 4-wave kernel (the ping-pong kernel measured no faster there)
+  const lsurge::GemmBlocks blocks = lsurge::gemm_variant() == LSURGE_GEMM_G256
+                                        ? lsurge::GemmBlocks{sv.t_expert, sv.t_rows, sv.t_row0, sv.num_tiles, (int)q.TB, 0, 256}
+                                        : lsurge::GemmBlocks{sv.blk_expert, sv.blk_rows, nullptr, sv.num_blocks, (int)q.MB, 0};
   lsurge::RowGather gather;
   gather.rows = sv.row_src;
   gather.div = (int)q.k;
