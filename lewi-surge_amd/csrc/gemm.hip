@@ -311,6 +311,9 @@ static int launch_rows256(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t
   if (a.max_tiles == 0) return LSURGE_OK;
   const dim3 grid(g256::NWG), block(256);
   const bool f16 = et == LSURGE_F16, f32out = a.Cf != nullptr;
+  // the epilogue's buffer descriptors span one tile's rows of each output
+  if (int rc = check_desc((int64_t)g256::BM * a.ldc * (f32out ? 4 : 2), "grouped GEMM output")) return rc;
+  if (int rc = check_desc((int64_t)g256::BM * a.ldg * 2, "grouped GEMM g / u")) return rc;
   if constexpr (EPI == EPI_SWIGLU_FWD) {
     if (a.a_rows) LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, true>), grid, block, 0, s, a));
     else LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false>), grid, block, 0, s, a));

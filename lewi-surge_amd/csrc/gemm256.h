@@ -284,23 +284,31 @@ void rows_kernel(RowsArgs a) {
     }
   };
 
-  // ---- epilogue of tile t_cur from the accumulators, through this wave's staging area; clears the accumulators
+  // ---- epilogue of tile t_cur from the accumulators, through this wave's staging area; clears the accumulators.
+  // No divergent control flow: every lane takes part in every LDS pass (passes split the wave's block by columns),
+  // and the global accesses are raw buffer accesses over the tile's rows, so rows past the tile fall outside the
+  // descriptor and a column past N takes the out-of-range offset -- the hardware drops such stores and returns zeros
+  // for such loads.  (An exec-masked staging pass was miscompiled: reads of a later pass were sunk into the masked
+  // write block of another.)
   char* const stg = smem + RING_BYTES + wave * STG_BYTES;
-  bf16_t* const pC = a.C;
-  bf16_t* const pG = a.G;
-  bf16_t* const pU = a.U;
-  float* const pCf = a.Cf;
-  const int64_t ldc = a.ldc, ldg = a.ldg;
+  auto st16 = [&](rsrc_t r, uint32_t off, u32x4 v) { __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0); };
   auto epilogue = [&]() {
     const int b = t_cur / a.n_tiles, nt = t_cur % a.n_tiles;
     const Tile rt = row_tile(a, b);
     const int64_t n0 = (int64_t)nt * NOUT;
+    // the tile's rows of each output (pitches in elements; an absent output gets an empty descriptor)
+    const int osz = (EPI == EPI_STORE && OUTF32) ? 4 : 2;
+    const rsrc_t rC = rsrc(reinterpret_cast<const char*>(OUTF32 ? (const void*)a.Cf : (const void*)a.C) + rt.row0 * a.ldc * osz,
+                           (int64_t)rt.rows * a.ldc * osz);
+    const rsrc_t rG = rsrc(a.G ? a.G + rt.row0 * a.ldg : nullptr, a.G ? (int64_t)rt.rows * a.ldg * 2 : 0);
+    const rsrc_t rU = rsrc(a.U ? a.U + rt.row0 * a.ldg : nullptr, a.U ? (int64_t)rt.rows * a.ldg * 2 : 0);
+    const uint32_t ldc_b = (uint32_t)a.ldc * osz, ldg_b = (uint32_t)a.ldg * 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int rbase = wm * 128 + 32 * i;  // first tile row of this slice
       if (EPI == EPI_SWIGLU_FWD) {
-        // 32 rows x 64 outputs in two passes of 32 columns: the f32 gate fragment j and up fragment j + 2 side by side
-        // (chunks 0-7 and 8-15 of a 256-byte staging row), read back 4 columns per lane -> h = silu(g) u, g, u
+        // 32 rows x 64 outputs in two passes of 32 columns: the f32 gate fragment j (chunks 0-7 of a 256-byte staging
+        // row) and up fragment j + 2 (chunks 8-15, same columns); read back 8 columns per lane -> h = silu(g) u, g, u
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -312,23 +320,86 @@ void rows_kernel(RowsArgs a) {
                 f32x4{acc[i][j + 2][4 * q], acc[i][j + 2][4 * q + 1], acc[i][j + 2][4 * q + 2], acc[i][j + 2][4 * q + 3]};
           }
 #pragma unroll
-          for (int it = 0; it < 4; ++it) {
-            const int r = 8 * it + (lane >> 3), c = lane & 7;
-            const f32x4 g = *reinterpret_cast<const f32x4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
-            const f32x4 u = *reinterpret_cast<const f32x4*>(stg + r * 256 + (((8 + c) ^ (r & 15)) << 4));
-            float h[4];
+          for (int it = 0; it < 2; ++it) {
+            const int r = 16 * it + (lane >> 2), c8 = lane & 3;
+            float g[8], u[8], h[8];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) h[t] = silu_f(g[t]) * u[t];
-            const int64_t col = n0 + wn * 64 + 32 * j + 4 * c;
-            if (rbase + r >= rt.rows || col >= N) continue;
-            const int64_t gr = rt.row0 + rbase + r;
-            *reinterpret_cast<u32x2*>(pC + gr * ldc + col) = u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
-            if (pG) *reinterpret_cast<u32x2*>(pG + gr * ldg + col) = u32x2{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3])};
-            if (pU) *reinterpret_cast<u32x2*>(pU + gr * ldg + col) = u32x2{pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3])};
+            for (int e = 0; e < 2; ++e) {
+              const f32x4 gv = *reinterpret_cast<const f32x4*>(stg + r * 256 + (((2 * c8 + e) ^ (r & 15)) << 4));
+              const f32x4 uv = *reinterpret_cast<const f32x4*>(stg + r * 256 + (((8 + 2 * c8 + e) ^ (r & 15)) << 4));
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                g[4 * e + t] = gv[t];
+                u[4 * e + t] = uv[t];
+              }
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) h[t] = silu_f(g[t]) * u[t];
+            const int64_t col = n0 + wn * 64 + 32 * j + 8 * c8;
+            const bool cok = col < N;
+            const uint32_t oc = cok ? (uint32_t)(rbase + r) * ldc_b + (uint32_t)col * 2u : OOB;
+            const uint32_t og = cok ? (uint32_t)(rbase + r) * ldg_b + (uint32_t)col * 2u : OOB;
+            st16(rC, oc, u32x4{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]), pack_bf16x2(h[4], h[5]),
+                               pack_bf16x2(h[6], h[7])});
+            st16(rG, og, u32x4{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]), pack_bf16x2(g[4], g[5]),
+                               pack_bf16x2(g[6], g[7])});
+            st16(rU, og, u32x4{pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]), pack_bf16x2(u[4], u[5]),
+                               pack_bf16x2(u[6], u[7])});
+          }
+        }
+      } else if (EPI == EPI_SWIGLU_BWD) {
+        // dH of 32 rows x 64 columns per pass (fragments 2 jp, 2 jp + 1, f32), read back 8 columns per lane beside
+        // the saved g and u -> [dG | dU]
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp) {
+          u32x4 gq[4], uq[4];  // fetched first, so their latency overlaps the LDS round trip
+          uint32_t oo[4];
+#pragma unroll
+          for (int it = 0; it < 4; ++it) {
+            const int r = 8 * it + (lane >> 3);
+            const int64_t col = n0 + wn * 128 + 64 * jp + 8 * (lane & 7);
+            const uint32_t og = col < N ? (uint32_t)(rbase + r) * ldg_b + (uint32_t)col * 2u : OOB;
+            oo[it] = col < N ? (uint32_t)(rbase + r) * ldc_b + (uint32_t)col * 2u : OOB;
+            gq[it] = ld16(rG, og);
+            uq[it] = ld16(rU, og);
+          }
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int ch = 8 * jj + 2 * q + fh;
+              *reinterpret_cast<f32x4*>(stg + fr * 256 + ((ch ^ (fr & 15)) << 4)) =
+                  f32x4{acc[i][2 * jp + jj][4 * q], acc[i][2 * jp + jj][4 * q + 1], acc[i][2 * jp + jj][4 * q + 2],
+                        acc[i][2 * jp + jj][4 * q + 3]};
+            }
+#pragma unroll
+          for (int it = 0; it < 4; ++it) {
+            const int r = 8 * it + (lane >> 3), c8 = lane & 7;
+            float v[8], dg[8], du[8];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const f32x4 x = *reinterpret_cast<const f32x4*>(stg + r * 256 + (((2 * c8 + e) ^ (r & 15)) << 4));
+#pragma unroll
+              for (int t = 0; t < 4; ++t) v[4 * e + t] = x[t];
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const uint32_t gw = gq[it][t >> 1], uw = uq[it][t >> 1];
+              const float g = __uint_as_float((t & 1) ? (gw & 0xffff0000u) : (gw << 16));
+              const float u = __uint_as_float((t & 1) ? (uw & 0xffff0000u) : (uw << 16));
+              const float sg = sigmoid_f(g);
+              dg[t] = v[t] * u * sg * (1.f + g * (1.f - sg));
+              du[t] = v[t] * g * sg;
+            }
+            st16(rC, oo[it], u32x4{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]), pack_bf16x2(dg[4], dg[5]),
+                                   pack_bf16x2(dg[6], dg[7])});
+            st16(rC, oo[it] == OOB ? OOB : oo[it] + (uint32_t)N * 2u,
+                 u32x4{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3]), pack_bf16x2(du[4], du[5]),
+                       pack_bf16x2(du[6], du[7])});
           }
         }
       } else if (EPI == EPI_STORE && !OUTF32) {
-        // 32 rows x 128 columns of 16-bit outputs
+        // 32 rows x 128 columns of 16-bit outputs; read back 8 columns per lane, 16 lanes per 256-byte row
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -350,25 +421,12 @@ void rows_kernel(RowsArgs a) {
           const int r = 4 * it + (lane >> 4), c = lane & 15;
           const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
           const int64_t col = n0 + wn * 128 + 8 * c;
-          if (rbase + r < rt.rows && col < N) *reinterpret_cast<u32x4*>(pC + (rt.row0 + rbase + r) * ldc + col) = v;
+          st16(rC, col < N ? (uint32_t)(rbase + r) * ldc_b + (uint32_t)col * 2u : OOB, v);
         }
       } else {
-        // f32 slices of 32 rows x 64 columns (fragments j = 2 jp, 2 jp + 1): the plain f32 store, or dH of the
-        // SwiGLU backward -> [dG | dU] from the saved g, u
+        // plain f32 store: 32 rows x 64 columns per pass (fragments 2 jp, 2 jp + 1), 16 lanes per 256-byte row
 #pragma unroll
         for (int jp = 0; jp < 2; ++jp) {
-          u32x2 gq[8], uq[8];
-          if (EPI == EPI_SWIGLU_BWD) {  // fetch g, u first, so their latency overlaps the LDS round trip
-#pragma unroll
-            for (int it = 0; it < 8; ++it) {
-              const int r = 4 * it + (lane >> 4);
-              const int64_t col = n0 + wn * 128 + 64 * jp + 4 * (lane & 15);
-              const bool ok = rbase + r < rt.rows && col < N;
-              const int64_t off = ok ? (rt.row0 + rbase + r) * ldg + col : rt.row0 * ldg;
-              gq[it] = *reinterpret_cast<const u32x2*>(pG + off);
-              uq[it] = *reinterpret_cast<const u32x2*>(pU + off);
-            }
-          }
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
@@ -381,27 +439,9 @@ void rows_kernel(RowsArgs a) {
 #pragma unroll
           for (int it = 0; it < 8; ++it) {
             const int r = 4 * it + (lane >> 4), c = lane & 15;
-            const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
+            const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
             const int64_t col = n0 + wn * 128 + 64 * jp + 4 * c;
-            if (rbase + r >= rt.rows || col >= N) continue;
-            const int64_t gr = rt.row0 + rbase + r;
-            if (EPI == EPI_STORE) {
-              *reinterpret_cast<f32x4*>(pCf + gr * ldc + col) = v;
-            } else {
-              float dg[4], du[4];
-#pragma unroll
-              for (int t = 0; t < 4; ++t) {
-                const uint32_t gw = gq[it][t >> 1], uw = uq[it][t >> 1];
-                const float g = __uint_as_float((t & 1) ? (gw & 0xffff0000u) : (gw << 16));
-                const float u = __uint_as_float((t & 1) ? (uw & 0xffff0000u) : (uw << 16));
-                const float sg = sigmoid_f(g);
-                dg[t] = v[t] * u * sg * (1.f + g * (1.f - sg));
-                du[t] = v[t] * g * sg;
-              }
-              *reinterpret_cast<u32x2*>(pC + gr * ldc + col) = u32x2{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
-              *reinterpret_cast<u32x2*>(pC + gr * ldc + N + col) =
-                  u32x2{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
-            }
+            st16(rC, col < N ? (uint32_t)(rbase + r) * ldc_b + (uint32_t)col * 4u : OOB, v);
           }
         }
       }
