@@ -594,13 +594,29 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
   a.c_expert = ch.c_expert; a.c_row0 = ch.c_row0; a.c_rows = ch.c_rows; a.c_part = ch.c_part;
   a.num_chunks = ch.num_chunks; a.max_chunks = ch.max_chunks;
   a.x_expert = xo.expert; a.Cx = xo.C; a.C2x = xo.C2;
-  a.i_tiles = (int)((I + BM - 1) / BM);
-  a.n_tiles = (int)((N + BN - 1) / BN);
-  const int64_t tiles = (int64_t)pad8(ch.max_chunks) * a.i_tiles * a.n_tiles;  // see the chunk tile order
-  if (et == LSURGE_F16)
-    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_wgrad_kernel<Cfg, LSURGE_F16>), dim3((unsigned)tiles), dim3(GT), 0, s, a));
-  else
-    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel<Cfg>, dim3((unsigned)tiles), dim3(GT), 0, s, a));
+  if (gemm_variant() == LSURGE_GEMM_G256) {
+    // persistent 256 x 256 tiles, one workgroup per CU; the epilogue's descriptors span one tile's rows of an output
+    if (int rc = check_desc((int64_t)g256::BM * std::max(N, ldc) * 4, "gemm_wgrad_chunked output")) return rc;
+    a.i_tiles = (int)((I + g256::BM - 1) / g256::BM);
+    a.n_tiles = (int)((N + g256::BN - 1) / g256::BN);
+    const dim3 grid(g256::NWG), block(256);
+    if (et == LSURGE_F16) {
+      LSURGE_REQUIRE(!a.a_rows, "gemm_wgrad_chunked: no row gather with f16 operands");
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::wgrad_kernel<false, LSURGE_F16>), grid, block, 0, s, a));
+    } else if (a.a_rows) {
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::wgrad_kernel<true>), grid, block, 0, s, a));
+    } else {
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::wgrad_kernel<false>), grid, block, 0, s, a));
+    }
+  } else {
+    a.i_tiles = (int)((I + BM - 1) / BM);
+    a.n_tiles = (int)((N + BN - 1) / BN);
+    const int64_t tiles = (int64_t)pad8(ch.max_chunks) * a.i_tiles * a.n_tiles;  // see the chunk tile order
+    if (et == LSURGE_F16)
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((gemm_wgrad_kernel<Cfg, LSURGE_F16>), dim3((unsigned)tiles), dim3(GT), 0, s, a));
+    else
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL(gemm_wgrad_kernel<Cfg>, dim3((unsigned)tiles), dim3(GT), 0, s, a));
+  }
   // grid-stride over the split experts' elements: two experts' worth of threads per pass
   const unsigned grid = (unsigned)std::min<int64_t>(2 * ((I * N / 4 + 255) / 256), 2048);
   LSURGE_LAUNCH(KID_SPLITK_REDUCE, s,

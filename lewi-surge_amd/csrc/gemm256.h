@@ -71,6 +71,50 @@ __device__ __forceinline__ Tile row_tile(const RowsArgs& a, int b) {
   return t;
 }
 
+// One stage on LDS half `cur` (four 16-deep MFMA steps over fragment buffers f0 / f1).  Step s reads step s + 1's
+// fragments (step 3: after the barrier that publishes the next stage, its step 0 from the other half) and, in steps
+// 0..2, moves copies [16 s / 3, 16 (s + 1) / 3) of stage lk from registers to the other half, each followed by the
+// load of the same chunk of the stage after.  The issue order is pinned: the NR fragment reads first, then the
+// write / load pairs, spread evenly over the step's 16 MFMAs.
+//   fread(F&, buf, step)   swrite(c, buf)   gload(c, lk)   mma(const F&)
+template <int NR, class F, class Fread, class Swrite, class Gload, class Mma>
+__device__ __forceinline__ void run_stage(F& f0, F& f1, int cur, int lk, Fread&& fread, Swrite&& swrite, Gload&& gload,
+                                          Mma&& mma) {
+  const int nxt = cur ^ 1;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    F& fc = (s & 1) ? f1 : f0;
+    F& fn = (s & 1) ? f0 : f1;
+    if (s == 3) {
+      // every wave's copies of the next stage have landed, and nobody reads this half's predecessor any more
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      fread(fn, nxt, 0);
+    } else {
+      fread(fn, cur, s + 1);
+    }
+    const int lo = s < 3 ? 16 * s / 3 : 0, hi = s < 3 ? 16 * (s + 1) / 3 : 0;
+#pragma unroll
+    for (int c = lo; c < hi; ++c) {
+      swrite(c, nxt);
+      gload(c, lk);
+    }
+    mma(fc);
+    const int nops = NR + 2 * (hi - lo);
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      const int o0 = m * nops / 16, o1 = (m + 1) * nops / 16;
+#pragma unroll
+      for (int o = o0; o < o1; ++o) {
+        if (o < NR) __builtin_amdgcn_sched_group_barrier(SG_DS_R, 1, 0);
+        else if ((o - NR) % 2 == 0) __builtin_amdgcn_sched_group_barrier(SG_DS_W, 1, 0);
+        else __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, 1, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Row GEMM C[tile rows, n tile] = A[tile rows, :] @ B[expert(tile)] over the row tiles of a.t_expert / t_rows /
 // t_row0 (num_tiles[0] real ones) or of a dense matrix, n tiles of BN columns (SwiGLU forward: BN / 2 outputs, the
 // gate and up columns side by side).  Operands, epilogues and arguments as gemm_rows_kernel (RowsArgs); amax is not
@@ -244,45 +288,6 @@ void rows_kernel(RowsArgs a) {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   F f0, f1;
   fread(f0, 0, 0);
-
-  // One stage on LDS half `cur`: step s reads step s + 1's fragments (step 3: after the barrier that publishes
-  // the next stage, its step 0 from the other half) and, in steps 0..2, moves copies [16 s / 3, 16 (s + 1) / 3)
-  // from registers to the other half, each followed by the load of the same chunk of the stage after.
-  auto stage = [&](int cur, int lk) {
-    const int nxt = cur ^ 1;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      F& fc = (s & 1) ? f1 : f0;
-      F& fn = (s & 1) ? f0 : f1;
-      if (s == 3) {
-        // every wave's copies of the next stage have landed, and nobody reads this half's predecessor any more
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        fread(fn, nxt, 0);
-      } else {
-        fread(fn, cur, s + 1);
-      }
-      const int lo = s < 3 ? 16 * s / 3 : 0, hi = s < 3 ? 16 * (s + 1) / 3 : 0;
-#pragma unroll
-      for (int c = lo; c < hi; ++c) {
-        swrite(c, nxt);
-        gload(c, lk);
-      }
-      mma(fc);
-      const int nops = 8 + 2 * (hi - lo);
-#pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-        const int o0 = m * nops / 16, o1 = (m + 1) * nops / 16;
-#pragma unroll
-        for (int o = o0; o < o1; ++o) {
-          if (o < 8) __builtin_amdgcn_sched_group_barrier(SG_DS_R, 1, 0);
-          else if ((o - 8) % 2 == 0) __builtin_amdgcn_sched_group_barrier(SG_DS_W, 1, 0);
-          else __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, 1, 0);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
 
   // ---- epilogue of tile t_cur from the accumulators, through this wave's staging area; clears the accumulators.
   // No divergent control flow: every lane takes part in every LDS pass (passes split the wave's block by columns),
@@ -458,14 +463,255 @@ void rows_kernel(RowsArgs a) {
         if (lt < xend) set_ld();
       }
       const int lk = kt + 2 == nk ? 0 : kt + 2;
-      stage(0, lk);
-      stage(1, lk + 1);
+      constexpr int NR = BMODE == B_NK ? 8 : 12;  // LDS reads per MFMA step (transpose reads take two per fragment)
+      run_stage<NR>(f0, f1, 0, lk, fread, swrite, gload, mma);
+      run_stage<NR>(f0, f1, 1, lk + 1, fread, swrite, gload, mma);
     }
     epilogue();
     t_cur += nper;
     if (t_cur >= xend) break;
   }
   __builtin_amdgcn_s_waitcnt(0);  // the zero loads past the last tile land before the wave ends
+}
+
+// Weight gradient C_e[I, N] = A_e^T B_e over the chunk table of gemm_wgrad_kernel (a.c_expert / c_row0 / c_rows /
+// c_part, num_chunks[0] real chunks): chunk c reduces rows [c_row0, c_row0 + c_rows) of expert c_expert and writes its
+// partial slot (c_part >= 0, summed afterwards in chunk order) or the gradient itself (C / C2 split at n_split, Cx / C2x
+// for the extra expert).  Tiles are 256 I-rows x 256 N-columns of one chunk (16 per chunk at the gate/up shape).
+// Both operands are row-major [rows, ld] with the reduction over the rows, so both are staged N-major (64 reduction
+// rows x 2 sub-tiles of 128 columns, the layout of the row GEMM's B_KN operand) and read with the transpose read.
+// GATHER: reduction row r of A is A[a_rows[r] / a_div] (the layer's x rows through row_src).  An index cursor runs one
+// stage ahead of the copies: each stage's row indices are read before the previous stage's data loads are issued,
+// so the wait for them never waits for data.
+template <bool GATHER, int ET = LSURGE_BF16>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void wgrad_kernel(WgradArgs a) {
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
+  const int nch = min(uni(a.num_chunks[0]), a.max_chunks);
+  const int tpc = a.i_tiles * a.n_tiles;
+  // Tile order: chunk c runs on XCD c % 8 (the table puts the hot and shared experts' chunks first, so they spread over
+  // the XCDs), its tiles on consecutive workgroups of that XCD, which share its rows in L2.  Persistent grid (one
+  // workgroup per CU): workgroup l of an XCD takes the XCD's tiles l, l + 32, ... and, of a last partial round, tile
+  // 31 - l, so that round lands on the workgroups that did not start with a heavy chunk.  Otherwise one tile per
+  // workgroup, dealt the same way over the grid.
+  const int xcd = blockIdx.x % 8, wl = blockIdx.x / 8;
+  const int xchunks = nch > xcd ? (nch - xcd + 7) / 8 : 0;  // chunks xcd, xcd + 8, ...
+  const int xlen = xchunks * tpc;
+  const int npx = gridDim.x / 8;  // workgroups per XCD
+  const bool pers = gridDim.x == NWG;
+  const int full = pers ? xlen / npx : 0, part_n = pers ? xlen % npx : 0;
+  const int ntiles_wg = pers ? full + ((npx - 1 - wl) < part_n ? 1 : 0) : (wl < xlen ? 1 : 0);
+  // k-th tile of this workgroup as (chunk, tile in chunk) packed into c * tpc + r
+  auto tile_of = [&](int k) {
+    const int idx = !pers ? wl : (k < full ? npx * k + wl : npx * full + (npx - 1 - wl));
+    return (xcd + 8 * (idx / tpc)) * tpc + idx % tpc;
+  };
+  if (ntiles_wg == 0) return;
+  int k_cur = 0, t_cur = tile_of(0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int I = (int)a.I, N = (int)a.N;
+  const uint32_t lda2 = (uint32_t)a.lda * 2u, ldb2 = (uint32_t)a.ldb * 2u;
+  // copy geometry (both operands N-major): copy i takes reduction row 16 (i % 4) + nr of sub-tile i / 4, chunk nc
+  const int nr = tid >> 4, nc = tid & 15;
+  const uint32_t nm_w = (uint32_t)(nr * 256 + ((nc ^ ((nr & 3) << 2)) << 4));
+  auto stages_of = [](int rows) { return max(2, (rows + 2 * BK - 1) / (2 * BK) * 2); };  // even, at least one pair
+
+  // ---- copy cursor: the workgroup's tile number lk_t (tile lt); its chunk's rows, descriptors and column offsets
+  int lk_t = 0, lt = t_cur;
+  rsrc_t la, lb;
+  uint32_t acol[2], bcol[2];  // byte offsets of this lane's A / B column in each sub-tile (OOB: past I / N)
+  auto set_ld = [&]() {
+    const int c = lt / tpc, rem = lt % tpc, it = rem / a.n_tiles, nt = rem % a.n_tiles;
+    const int64_t row0 = uni(a.c_row0[c]);
+    const int rows = uni(a.c_rows[c]);
+    if (GATHER) la = rsrc(a.A, a.a_nrows * (int64_t)a.lda * 2);
+    else la = rsrc(a.A + row0 * a.lda, (int64_t)rows * a.lda * 2);  // rows past the chunk: zeros
+    lb = rsrc(a.B + row0 * a.ldb, (int64_t)rows * a.ldb * 2);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t ca = (int64_t)it * BM + 128 * h + 8 * nc, cb = (int64_t)nt * BN + 128 * h + 8 * nc;
+      acol[h] = ca < I ? (uint32_t)ca * 2u : OOB;
+      bcol[h] = cb < N ? (uint32_t)cb * 2u : OOB;
+    }
+  };
+  set_ld();
+
+  // ---- gathered A: index cursor (tile xt, stage xk), one stage ahead of the copies; raw indices in flight (pend)
+  // and the source-row byte offsets of the stage being copied (g_off)
+  const uint64_t magic = div_magic(GATHER ? a.a_div : 1);
+  int xk_t = 0, xt = t_cur, xk = 0, x_rows = 0, x_nk = 2;
+  int64_t x_row0 = 0;
+  int pend[4];
+  uint32_t g_off[4];
+  auto x_set = [&]() {
+    if (xk_t < ntiles_wg) {
+      const int c = xt / tpc;
+      x_row0 = uni(a.c_row0[c]);
+      x_rows = uni(a.c_rows[c]);
+      x_nk = stages_of(x_rows);
+    }
+  };
+  auto x_issue = [&]() {  // read the indices at the index cursor into pend, then advance the cursor
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = xk * BK + 16 * q + nr;
+      const bool ok = xk_t < ntiles_wg && r < x_rows;
+      const int v = a.a_rows[x_row0 + (ok ? r : 0)];
+      pend[q] = ok ? v : -1;
+    }
+    if (++xk == x_nk) {
+      xk = 0;
+      if (++xk_t < ntiles_wg) xt = tile_of(xk_t);
+      x_set();
+    }
+  };
+  auto x_take = [&]() {  // the pending indices become the copy cursor's stage
+#pragma unroll
+    for (int q = 0; q < 4; ++q) g_off[q] = pend[q] >= 0 ? (uint32_t)div_by(pend[q], magic) * lda2 : OOB;
+  };
+  if (GATHER) x_set();
+
+  u32x4 R[16];
+  auto gload = [&](int c, int lk) {
+    const bool live = lk_t < ntiles_wg;
+    const int i = c & 7, h = i >> 2, q = i & 3;
+    const uint32_t krow = (uint32_t)(lk * BK + 16 * q + nr);
+    if (c < 8) {
+      const uint32_t ro = GATHER ? g_off[q] : krow * lda2;
+      R[c] = ld16(la, live && acol[h] != OOB && ro != OOB ? ro + acol[h] : OOB);
+    } else {
+      R[c] = ld16(lb, live && bcol[h] != OOB ? krow * ldb2 + bcol[h] : OOB);
+    }
+  };
+  auto swrite = [&](int c, int buf) {
+    const int i = c & 7;
+    char* p = smem + buf * STAGE_BYTES + (c < 8 ? 0 : OP_BYTES) + (i >> 2) * (BK * 256) + 16 * 256 * (i & 3) + nm_w;
+    *reinterpret_cast<u32x4*>(p) = R[c];
+  };
+  typedef FragSet<4, 4> F;
+  auto fread = [&](F& f, int buf, int s) {
+    const bf16_t* st = reinterpret_cast<const bf16_t*>(smem + buf * STAGE_BYTES);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.x[i] = frag_n(st + wm * (BK * 128), 16 * s, 32 * i, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.w[j] = frag_n(st + OP_BYTES / 2 + wn * (BK * 128), 16 * s, 32 * j, lane);
+  };
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  auto mma = [&](const F& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32<ET>(f.w[j], f.x[i], acc[i][j]);
+  };
+
+  // ---- prologue: stage 0 -> LDS half 0, stage 1 -> registers; the index cursor then points at stage 2
+  if (GATHER) {
+    x_issue();
+    x_take();
+  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c) gload(c, 0);
+#pragma unroll
+  for (int c = 0; c < 16; ++c) swrite(c, 0);
+  if (GATHER) {
+    x_issue();
+    x_take();
+  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c) gload(c, 1);
+  if (GATHER) x_issue();
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  F f0, f1;
+  fread(f0, 0, 0);
+
+  // ---- epilogue of tile t_cur (f32): the chunk's partial slot, or the gradient split at n_split -- two uniform
+  // destinations, lanes whose columns belong to the other one pass the out-of-range offset
+  char* const stg = smem + RING_BYTES + wave * STG_BYTES;
+  auto epilogue = [&]() {
+    const int c = t_cur / tpc, rem = t_cur % tpc, it = rem / a.n_tiles, nt = rem % a.n_tiles;
+    const int expert = uni(a.c_expert[c]), part = uni(a.c_part[c]);
+    const int64_t i0 = (int64_t)it * BM, n0 = (int64_t)nt * BN;
+    const int64_t irows = min((int64_t)BM, (int64_t)I - i0);
+    const float* d1;
+    const float* d2 = nullptr;
+    int64_t pitch, split;
+    if (part >= 0) {
+      d1 = a.part + (int64_t)part * I * N;
+      pitch = N;
+      split = N;
+    } else {
+      const bool xe = expert == a.x_expert;
+      d1 = xe ? a.Cx : a.C + (int64_t)expert * a.c_estride;
+      d2 = xe ? a.C2x : (a.C2 ? a.C2 + (int64_t)expert * a.c_estride : nullptr);
+      pitch = a.ldc;
+      split = d2 ? a.n_split : N;
+    }
+    const rsrc_t r1 = rsrc(d1 + i0 * pitch, irows * pitch * 4);
+    const rsrc_t r2 = rsrc(d2 ? d2 + i0 * pitch : nullptr, d2 ? irows * pitch * 4 : 0);
+    const uint32_t pb = (uint32_t)pitch * 4u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rbase = wm * 128 + 32 * i;
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int ch4 = 8 * jj + 2 * q + fh;
+            *reinterpret_cast<f32x4*>(stg + fr * 256 + ((ch4 ^ (fr & 15)) << 4)) =
+                f32x4{acc[i][2 * jp + jj][4 * q], acc[i][2 * jp + jj][4 * q + 1], acc[i][2 * jp + jj][4 * q + 2],
+                      acc[i][2 * jp + jj][4 * q + 3]};
+          }
+#pragma unroll
+        for (int it2 = 0; it2 < 8; ++it2) {
+          const int r = 4 * it2 + (lane >> 4), cc = lane & 15;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((cc ^ (r & 15)) << 4));
+          const int64_t col = n0 + wn * 128 + 64 * jp + 4 * cc;
+          const uint32_t rb = (uint32_t)(rbase + r) * pb;
+          __builtin_amdgcn_raw_buffer_store_b128(v, r1, col < split ? rb + (uint32_t)col * 4u : OOB, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(v, r2, col >= split && col < N ? rb + (uint32_t)(col - split) * 4u : OOB,
+                                                 0, 0);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    }
+  };
+
+  // stage kt loads stage kt + 2; the last pair loads the next tile's first two stages
+  while (true) {
+    const int nk = stages_of(uni(a.c_rows[t_cur / tpc]));
+    for (int kt = 0; kt < nk; kt += 2) {
+      if (kt + 2 == nk) {
+        if (++lk_t < ntiles_wg) {
+          lt = tile_of(lk_t);
+          set_ld();
+        }
+      }
+      const int lk = kt + 2 == nk ? 0 : kt + 2;
+      if (GATHER) {
+        x_take();
+        x_issue();
+      }
+      run_stage<16>(f0, f1, 0, lk, fread, swrite, gload, mma);
+      if (GATHER) {
+        x_take();
+        x_issue();
+      }
+      run_stage<16>(f0, f1, 1, lk + 1, fread, swrite, gload, mma);
+    }
+    epilogue();
+    if (++k_cur >= ntiles_wg) break;
+    t_cur = tile_of(k_cur);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 }  // namespace g256
