@@ -199,6 +199,13 @@ def short_kernel(name):
         n = f"{m.group(1)}<{m.group(2)},{m.group(3)}>" + ("<f8>" if f8 not in ("0", "false") else "")
     if n.startswith("gemm_wgrad_kernel<"):
         n = "gemm_wgrad_kernel"
+    # the persistent 256 x 256 kernels: B layout, epilogue and row gather (rows), row gather (weight gradient)
+    m = re.match(r"g256::rows_kernel<(\d+),(\d+),(true|false)", n)
+    if m:
+        n = f"g256_rows<{m.group(1)},{m.group(2)},{int(m.group(3) == 'true')}>"
+    m = re.match(r"g256::wgrad_kernel<(true|false)", n)
+    if m:
+        n = f"g256_wgrad<{int(m.group(1) == 'true')}>"
     return n
 
 
@@ -219,12 +226,21 @@ def launch_roles(c):
         "combine_pad_kernel<2,6,1>": ["combine_fwd"], "combine_pad_kernel<2,8,1>": ["combine_fwd"],
         "combine_pad_kernel<4,8,1>": ["combine_fwd"],
     }
+    # persistent kernels (gemm_variant 1): the shared expert's dense forward is the non-gathered SwiGLU launch
+    r.update({"g256_rows<1,1,0>": ["shared_gu_fwd"], "g256_rows<1,1,1>": ["gemm_gu_fwd"],
+              "g256_rows<1,0,0>": (["shared_down_fwd"] if fs else []) + ["gemm_down_fwd"]})
+    g256 = c.get("gemm_variant", 1) == 1
     if c["bwd"]:
+        r.update({
+            "g256_rows<0,2,0>": (["shared_down_dgrad"] if own else []) + ["gemm_down_dgrad"],
+            "g256_rows<0,0,0>": (["shared_gu_dgrad"] if own else []) + ["gemm_gu_dgrad"],
+            "g256_wgrad<0>": ["gemm_down_wgrad"], "g256_wgrad<1>": ["gemm_gu_wgrad"],
+        })
         r.update({
             "gemm_rows_kernel<0,2>": (["shared_down_dgrad"] if own else []) + ["gemm_down_dgrad"],
             "gemm_rows_kernel<0,0>": (["shared_gu_dgrad"] if own else []) + ["gemm_gu_dgrad"],
             "gemm_wgrad_kernel": (["shared_down_wgrad", "shared_gu_wgrad"] if own else [])
-                                 + ["gemm_down_wgrad", "router_wgrad", "gemm_gu_wgrad"],
+                                 + (["router_wgrad"] if g256 else ["gemm_down_wgrad", "router_wgrad", "gemm_gu_wgrad"]),
             "splitk_reduce_kernel": ["splitk_reduce"] * (3 if own else 1),
             "wgrad_chunk_reduce_kernel": ["chunk_reduce", "chunk_reduce"],
             "wgrad_chunks_kernel": ["misc"], "transpose_bf16_kernel": ["misc"], "scatter_dlogits_kernel": ["misc"],
@@ -299,7 +315,7 @@ def profile_summary(a):
     import csv
     import glob
 
-    c = CONFIGS[a.config]
+    c = dict(CONFIGS[a.config], gemm_variant=a.gemm_variant)
 
     def rows_of(d, kind):
         files = glob.glob(os.path.join(d, f"*{kind}.csv"))
@@ -640,16 +656,18 @@ def ragged_bench(a):
     shapes for context.  TF/s count useful rows only."""
     import torch
 
+    import numpy as np
+
     import _lib as L
-    from oracle import moe_oracle as mo
 
     dev = torch.device("cuda", 0)
     lib = L.lib()
     st = L.stream(dev)
     c = CONFIGS["C2"]
-    rng = __import__("numpy").random.default_rng(0)
-    sel = mo.topk_lower_index(rng.standard_normal((c["T"], c["E"])).astype("float32"), c["k"])
-    gs_np = __import__("numpy").bincount(sel.reshape(-1), minlength=c["E"]).astype("int32")
+    rng = np.random.default_rng(0)
+    # the top-k of seeded logits, ties to the lower expert index (a stable sort of the negated logits)
+    sel = np.argsort(-rng.standard_normal((c["T"], c["E"])).astype("float32"), axis=1, kind="stable")[:, :c["k"]]
+    gs_np = np.bincount(sel.reshape(-1), minlength=c["E"]).astype("int32")
     M, E = int(gs_np.sum()), c["E"]
     gs = torch.from_numpy(gs_np).to(dev)
     gen = torch.Generator(device=dev).manual_seed(0)
@@ -701,6 +719,104 @@ def ragged_bench(a):
         "roofline": {"kernel": "ragged_dot up fwd", "bound": "mfma", "achieved": up, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(up / PEAK_BF16_TFLOPS, 4), "traffic": None}}), flush=True)
 
+def layer_measure(a, c, steps, warmup):
+    """Time `steps` fwd(+bwd) layer steps of config c after `warmup` (helper streams per a.concurrency), with a
+    profiled one-stream pass first that finds the dominant kernel; that kernel is bracketed by HIP events on its
+    launch stream during the timed steps.  Returns the step time, tokens/s, the per-kernel table and the roofline
+    figures of the dominant kernel."""
+    import torch
+
+    import _lib
+    from moe_layer import MoELayer, MoEShape
+
+    dev = torch.device("cuda", 0)
+    lib = _lib.lib()
+    lib.lsurge_set_concurrency(0)
+    p, dy = make_params(c, dev)
+    layer = MoELayer(MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"]), dev)
+    grads = layer.alloc_grads() if c["bwd"] else None
+
+    def step():
+        if a.fp8:
+            layer.quantize_weights_fp8(p)
+            layer.forward_fp8(p)
+            if c["bwd"]:
+                layer.backward_fp8(p, dy, grads)
+            return
+        layer.forward(p)
+        if c["bwd"]:
+            layer.backward(p, dy, grads)
+
+    for _ in range(2):  # first-call work (code objects, helper events) before the profiled pass
+        step()
+    torch.cuda.synchronize()
+
+    # profiled pass (one stream, so every kernel's time is its own): every kernel bracketed, to find the
+    # dominant one and fill the per-kernel table
+    lib.lsurge_prof_reset()
+    lib.lsurge_prof_enable(-1)
+    nprof = 3
+    for _ in range(nprof):
+        step()
+    torch.cuda.synchronize()
+    lib.lsurge_prof_collect()
+    lib.lsurge_prof_enable(0)
+    table = prof_table(lib, nprof)
+    work = kernel_work(c, a.fp8)
+    dom = max((n for n in table if n in work), key=lambda n: table[n][2])
+    names = [lib.lsurge_prof_kernel_name(i).decode() for i in range(lib.lsurge_prof_kernel_count())]
+
+    # timed region: K steps, only the dominant kernel bracketed by events on its launch stream
+    # the W warm-up steps run in the timed region's mode (helper streams): the step time settles only after ~20
+    # back-to-back steps (measured: 2 steps leave the timed mean 3% high)
+    lib.lsurge_set_concurrency(a.concurrency)
+    for _ in range(warmup):
+        step()
+    lib.lsurge_prof_reset()
+    lib.lsurge_prof_enable(1 << names.index(dom))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    lib.lsurge_prof_collect()
+    lib.lsurge_prof_enable(0)
+    timed = prof_table(lib, steps)
+    dom_ms = timed[dom][0]
+    bound, amount = work[dom]
+    peak_mfma = PEAK_FP8_TFLOPS if a.fp8 else PEAK_BF16_TFLOPS
+    if bound == "mfma":
+        achieved, peak, unit = amount / (dom_ms * 1e-3) / 1e12, peak_mfma, "TFLOP/s"
+    else:
+        achieved, peak, unit = amount / (dom_ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+    ms = el / steps * 1e3
+    cached_ms = None
+    if a.fp8:  # the same step on weights quantised once
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            layer.forward_fp8(p)
+            if c["bwd"]:
+                layer.backward_fp8(p, dy, grads)
+        torch.cuda.synchronize()
+        cached_ms = (time.perf_counter() - t0) / steps * 1e3
+    serial_ms = sum(v[2] for v in table.values())
+    kern = {n: dict(ms=round(v[0], 4), share=round(v[2] / serial_ms, 4)) for n, v in sorted(table.items(),
+                                                                                          key=lambda kv: -kv[1][2])}
+    for n, v in kern.items():
+        if n in work:
+            b, amt = work[n]
+            v["achieved"] = round(amt / (v["ms"] * 1e-3) / (1e12 if b == "mfma" else 1e9), 1)
+            v["unit"] = "TFLOP/s" if b == "mfma" else "GB/s"
+    lib.lsurge_set_concurrency(0)
+    del layer, p, dy, grads
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return dict(ms=ms, tokens_s=c["T"] * steps / el, dom=dom, bound=bound, achieved=achieved, peak=peak, unit=unit,
+                dom_ms=dom_ms, kern=kern, cached_ms=cached_ms, peak_mfma=peak_mfma)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -708,6 +824,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="C2 run: skip the C1, C3, C4, C5 lines appended to the JSON (configs key)")
+    ap.add_argument("--other-steps", type=int, default=10, help="timed (and warm-up) steps of each other config")
     ap.add_argument("--fp8", action="store_true", help="expert GEMMs in FP8 (current scaling: E4M3 forward, E5M2 "
                     "gradients)")
     ap.add_argument("--fwd-only", action="store_true", help="time the forward alone")
@@ -781,94 +900,13 @@ def main():
         ragged_bench(a)
         return
 
-    import _lib
-    from moe_layer import MoELayer, MoEShape
-
     c = CONFIGS[a.config]
     if a.fwd_only:
         c = dict(c, bwd=False)
-    dev = torch.device("cuda", 0)
-    lib = _lib.lib()
-    lib.lsurge_set_concurrency(0)
-    p, dy = make_params(c, dev)
-    layer = MoELayer(MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"]), dev)
-    grads = layer.alloc_grads() if c["bwd"] else None
-
-    def step():
-        if a.fp8:
-            layer.quantize_weights_fp8(p)
-            layer.forward_fp8(p)
-            if c["bwd"]:
-                layer.backward_fp8(p, dy, grads)
-            return
-        layer.forward(p)
-        if c["bwd"]:
-            layer.backward(p, dy, grads)
-
-    for _ in range(2):  # first-call work (code objects, helper events) before the profiled pass
-        step()
-    torch.cuda.synchronize()
-
-    # profiled pass (one stream, so every kernel's time is its own): every kernel bracketed, to find the
-    # dominant one and fill the per-kernel table
-    lib.lsurge_prof_reset()
-    lib.lsurge_prof_enable(-1)
-    nprof = 3
-    for _ in range(nprof):
-        step()
-    torch.cuda.synchronize()
-    lib.lsurge_prof_collect()
-    lib.lsurge_prof_enable(0)
-    table = prof_table(lib, nprof)
-    work = kernel_work(c, a.fp8)
-    dom = max((n for n in table if n in work), key=lambda n: table[n][2])
-    names = [lib.lsurge_prof_kernel_name(i).decode() for i in range(lib.lsurge_prof_kernel_count())]
-
-    # timed region: K steps, only the dominant kernel bracketed by events on its launch stream
-    # the W warm-up steps run in the timed region's mode (helper streams): the step time settles only after ~20
-    # back-to-back steps (measured: 2 steps leave the timed mean 3% high)
-    lib.lsurge_set_concurrency(a.concurrency)
-    for _ in range(a.warmup):
-        step()
-    lib.lsurge_prof_reset()
-    lib.lsurge_prof_enable(1 << names.index(dom))
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        step()
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    lib.lsurge_prof_collect()
-    lib.lsurge_prof_enable(0)
-    timed = prof_table(lib, a.steps)
-    dom_ms = timed[dom][0]
-    bound, amount = work[dom]
-    peak_mfma = PEAK_FP8_TFLOPS if a.fp8 else PEAK_BF16_TFLOPS
-    if bound == "mfma":
-        achieved, peak, unit = amount / (dom_ms * 1e-3) / 1e12, peak_mfma, "TFLOP/s"
-    else:
-        achieved, peak, unit = amount / (dom_ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
-
-    ms = el / a.steps * 1e3
-    tokens_s = c["T"] * a.steps / el
-    cached_ms = None
-    if a.fp8:  # the same step on weights quantised once
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(a.steps):
-            layer.forward_fp8(p)
-            if c["bwd"]:
-                layer.backward_fp8(p, dy, grads)
-        torch.cuda.synchronize()
-        cached_ms = (time.perf_counter() - t0) / a.steps * 1e3
-    serial_ms = sum(v[2] for v in table.values())
-    kern = {n: dict(ms=round(v[0], 4), share=round(v[2] / serial_ms, 4)) for n, v in sorted(table.items(),
-                                                                                          key=lambda kv: -kv[1][2])}
-    for n, v in kern.items():
-        if n in work:
-            b, amt = work[n]
-            v["achieved"] = round(amt / (v["ms"] * 1e-3) / (1e12 if b == "mfma" else 1e9), 1)
-            v["unit"] = "TFLOP/s" if b == "mfma" else "GB/s"
+    m = layer_measure(a, c, a.steps, a.warmup)
+    ms, tokens_s, dom, bound, achieved, peak, unit, dom_ms, kern, cached_ms, peak_mfma = (
+        m["ms"], m["tokens_s"], m["dom"], m["bound"], m["achieved"], m["peak"], m["unit"], m["dom_ms"], m["kern"],
+        m["cached_ms"], m["peak_mfma"])
     if a.kernels:
         for n, v in kern.items():
             print(f"  {n:20s} {v}", file=sys.stderr)
@@ -904,6 +942,25 @@ def main():
         "kernels_note": "per-kernel ms from a profiled pass on one stream (share of that pass's kernel time); "
                         "the timed region runs with concurrent_streams",
     }
+    if a.config == "C2" and c["bwd"] and not a.fp8 and not a.no_other_configs:
+        # every other BASELINE config on the same line: a few timed steps each, with its dominant kernel's roofline
+        # (no CPU baseline for these)
+        res["configs"] = {}
+        for name in ("C1", "C3", "C4", "C5"):
+            cc = CONFIGS[name]
+            mm = layer_measure(a, cc, a.other_steps, a.other_steps)
+            res["configs"][name] = {
+                "workload": f"{name}: MoE layer {'fwd+bwd' if cc['bwd'] else 'fwd'} T={cc['T']} d={cc['d']} "
+                            f"E={cc['E']}x{cc['f']} top-{cc['k']} shared={cc['fs']}" + (" zipf-bias" if cc["zipf"] else ""),
+                "steps": a.other_steps, "warmup": a.other_steps, "ms_per_step": round(mm["ms"], 4),
+                "tokens_s": round(mm["tokens_s"], 1),
+                "layer_tflops": round(layer_flops(cc) / (mm["ms"] * 1e-3) / 1e12, 1),
+                "mfu": round(layer_flops(cc) / (mm["ms"] * 1e-3) / 1e12 / mm["peak_mfma"], 4),
+                "roofline": {"kernel": mm["dom"], "bound": mm["bound"], "achieved": round(mm["achieved"], 1),
+                             "peak": mm["peak"], "unit": mm["unit"], "frac": round(mm["achieved"] / mm["peak"], 4),
+                             "launch_ms": round(mm["dom_ms"], 4)},
+                "kernels": {n: v for n, v in list(mm["kern"].items())[:8]},
+            }
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(c)
         if a.config == "C2" and c["bwd"]:  # BASELINE.md's pair: C1 forward beside C2 forward + backward

@@ -242,9 +242,12 @@ int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_s
 /* ------------------------------------------------------------------------------------------------
  * FP8 variant of the expert GEMMs (OCP FP8 operands, f32 accumulation, v_mfma_f32_32x32x64_f8f6f4).
  * Current scaling: every tensor, or every group of one (an expert's weight matrix), is quantised with its
- * own scale = fmax / amax taken just before the cast (1 when amax = 0); values are rounded to nearest even
- * and saturated at +-fmax; scale_inv = 1 / scale multiplies the GEMM's accumulator back.  Activations and
- * weights are E4M3 (fmax 448), gradients E5M2 (fmax 57344): the hybrid recipe of Transformer Engine's FP8
+ * own scale taken just before the cast (1 when amax = 0); values are rounded to nearest even and saturated at
+ * +-fmax; scale_inv = 1 / scale multiplies the GEMM's accumulator back.  Activations and weights are E4M3
+ * (fmax 448) with scale = 448 / amax; gradients are E5M2 (fmax 57344) with scale = the largest power of two not
+ * above 57344 / amax (Transformer Engine's force_pow_2_scales variant, so that a one-ulp change of a gradient's
+ * amax moves the quantisation grid only at a binade; TE is not importable here, so parity with its recipe is
+ * not checked).  This is the hybrid recipe of Transformer Engine's FP8
  * current scaling that the reference trains with through MaxText's `quantization=te_fp8_currentscaling`
  * (modal/te_run.py:95-99; TE and MaxText are third-party, and the reference's own MoE path has no FP8 entry
  * point, so these functions replace none of its interfaces).
@@ -263,7 +266,8 @@ int lsurge_fp8_quantize(const void* x, int64_t groups, int64_t rows, int64_t col
  * row-wise to q [rows, cols] and / or transposed to qt [cols, ldqt] (ldqt >= rows rounded up to 64, a multiple
  * of 16; columns past rows hold zeros up to the next multiple of 16) -- the cast + transpose a training step
  * makes of an activation or gradient whose two GEMMs need it K-contiguous in both directions.  Either q or qt
- * may be null; all pointers 16-byte aligned; scale_inv [1] f32. */
+ * may be null; all pointers 16-byte aligned; scale_inv [1] f32.  The scale follows the format's rule above:
+ * 448 / amax for E4M3, the largest power of two not above 57344 / amax for E5M2. */
 size_t lsurge_fp8_cast_workspace_bytes(void);
 int lsurge_fp8_cast_transpose(const void* x, int64_t rows, int64_t cols, int format, void* q, void* qt,
                               int64_t ldqt, float* scale_inv, void* workspace, size_t workspace_bytes,

@@ -105,11 +105,16 @@ class _L2NormFn(torch.autograd.Function):
 def fast_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
                                 use_qk_norm_in_gdn=False, cp_axis=None, compute_dtype=torch.bfloat16):
     """modal/gdn_fast.py:37-113.  The kernels take chunks of 64, head dims of 128 and the bf16 compute dtype.  With
-    use_qk_norm_in_gdn, query and key are l2-normalised over the head dim first (43-46; here after the cast to bf16,
-    where the reference normalises in the input dtype, the same thing for bf16 inputs).  The context-parallel branch
-    (39-42) is not built and raises NotImplementedError."""
+    use_qk_norm_in_gdn, query and key are l2-normalised over the head dim first (43-46).  The reference normalises in
+    the input dtype and casts afterwards; the l2-norm kernel takes bf16, so qk-norm requires bf16 query and key (for
+    them the two orders agree) and other dtypes raise ValueError rather than round twice.  The context-parallel
+    branch (39-42) is not built and raises NotImplementedError."""
     if cp_axis is not None:
         raise NotImplementedError("fast_chunk_gated_delta_rule: context parallelism (cp_axis) is not built")
+    if use_qk_norm_in_gdn and (query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16):
+        raise ValueError("fast_chunk_gated_delta_rule: use_qk_norm_in_gdn takes bf16 query and key (got "
+                         f"{query.dtype}, {key.dtype}); the reference normalises before its cast, which the bf16 "
+                         "l2-norm kernel reproduces only for bf16 inputs")
     if chunk_size != 64 or compute_dtype != torch.bfloat16:
         raise ValueError("fast_chunk_gated_delta_rule: the kernels take chunk_size=64 and a bf16 compute dtype")
     if query.shape[-1] != D or value.shape[-1] != D or key.shape != query.shape:

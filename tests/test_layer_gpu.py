@@ -137,6 +137,12 @@ def test_c5_token_subset(dev):
     p = mo.make_inputs(**c)
     shape = MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"])
     out, views, grads = run_gpu(p, shape, dev, bwd=True)
+    # the full layout of all 65536 tokens (524288 routed rows over 256 experts) against the C oracle's, from the
+    # layer's own selection (itself checked below on a token subset, and in full on an 8192-token slice)
+    lay = co.build_layout(views["sel"], c["E"])
+    for n in ("group_sizes", "offsets", "block_off", "order", "pos", "slot"):
+        assert np.array_equal(views[n], lay[n]), n
+    assert int(views["num_blocks"][0]) == lay["num_blocks"]
     toks = np.random.default_rng(0).choice(c["T"], 192, replace=False)
     sub = dict(p)
     sub["x"], sub["dy"] = p["x"][toks], p["dy"][toks]
@@ -166,6 +172,40 @@ def test_c5_token_subset(dev):
     werr["dw_r"] = mo.rel_l2(grads["dw_r"], mo.router_wgrad(p, views["sel"], grads["dweights"]))
     print(werr)
     assert all(v < TOL for v in werr.values()), werr
+
+
+def test_c5_shape_slice_full(dev):
+    """C5's layer shape (d = 2048, 256 experts, top-8, shared expert of width 2048) on an 8192-token slice of its input
+    stream, where the fused router runs: logits bitwise equal to the C oracle's, the selection and the whole layout
+    exact, the softmax weights within 1e-6, and the output and every gradient within 2e-2 of the float32 oracle."""
+    c = dict(mo.CONFIGS["C5"], T=8192)
+    p = mo.make_inputs(**c)
+    shape = MoEShape(c["T"], c["d"], c["E"], c["k"], c["f"], c["fs"])
+    layer = MoELayer(shape, dev)
+    tp = to_dev(p, dev)
+    out = layer.forward(tp).float().cpu().numpy()
+    v = {n: t.cpu().numpy() for n, t in layer.views().items()
+         if n in ("logits", "sel", "weights", "group_sizes", "offsets", "block_off", "order", "pos", "slot", "num_blocks")}
+    dy = torch.from_numpy(np.ascontiguousarray(p["dy"])).to(dev).to(torch.bfloat16)
+    grads = {n: t.float().cpu().numpy() for n, t in layer.backward(tp, dy).items()}
+    logits = co.router_logits(p["x"], p["w_r"])
+    assert np.array_equal(v["logits"].view(np.uint32), logits.view(np.uint32))
+    sel = co.topk(logits, c["k"])
+    assert np.array_equal(v["sel"], sel)
+    assert mo.rel_l2(v["weights"], mo.topk_softmax(logits, sel)) < 1e-6
+    lay = co.build_layout(sel, c["E"])
+    for n in ("group_sizes", "offsets", "block_off", "order", "pos", "slot"):
+        assert np.array_equal(v[n], lay[n]), n
+    assert int(v["num_blocks"][0]) == lay["num_blocks"]
+    want, cache = mo.moe_layer_fwd(p, np.float32, route=(logits, sel))
+    g = mo.moe_layer_bwd(p, cache, p["dy"], np.float32)
+    errs = {"out": mo.rel_l2(out, want)}
+    for gn, on in [("dx", "dx"), ("dw_r", "dw_r"), ("dw_gate", "dw_gate"), ("dw_up", "dw_up"), ("dw_down", "dw_down"),
+                   ("dweights", "dw"), ("dws_gate", "dws_gate"), ("dws_up", "dws_up"), ("dws_down", "dws_down")]:
+        errs[gn] = mo.rel_l2(grads[gn], g[on])
+    print({k: f"{e:.2e}" for k, e in errs.items()})
+    bad = {k: e for k, e in errs.items() if not e < TOL}
+    assert not bad, bad
 
 
 def test_deterministic_bitwise(dev):

@@ -129,3 +129,17 @@ def test_tpu_helpers_keep_reference_values():
     finally:
         mp.CFG["even_low"] = old
     assert mp._interpret() is None
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_gdn_qk_norm_rejects_non_bf16(dt):
+    """use_qk_norm_in_gdn with f32 / f16 query and key: the reference normalises in the input dtype before its cast
+    (modal/gdn_fast.py:43-49); the bf16 l2-norm kernel cannot reproduce that, so the call raises before any device
+    work instead of rounding twice."""
+    import gdn_fast
+    q = torch.zeros((1, 64, 1, 128), dtype=dt)
+    v = torch.zeros((1, 64, 1, 128), dtype=dt)
+    g = torch.zeros((1, 64, 1), dtype=torch.float32)
+    beta = torch.zeros((1, 64, 1), dtype=dt)
+    with pytest.raises(ValueError, match="bf16 query and key"):
+        gdn_fast.fast_chunk_gated_delta_rule(q, q, v, g, beta, use_qk_norm_in_gdn=True)
