@@ -234,13 +234,14 @@ def launch_roles(c):
         r.update({
             "g256_rows<0,2,0>": (["shared_down_dgrad"] if own else []) + ["gemm_down_dgrad"],
             "g256_rows<0,0,0>": (["shared_gu_dgrad"] if own else []) + ["gemm_gu_dgrad"],
-            "g256_wgrad<0>": ["gemm_down_wgrad"], "g256_wgrad<1>": ["gemm_gu_wgrad"],
+            "g256_wgrad<1>": ["gemm_gu_wgrad"],
         })
         r.update({
             "gemm_rows_kernel<0,2>": (["shared_down_dgrad"] if own else []) + ["gemm_down_dgrad"],
             "gemm_rows_kernel<0,0>": (["shared_gu_dgrad"] if own else []) + ["gemm_gu_dgrad"],
             "gemm_wgrad_kernel": (["shared_down_wgrad", "shared_gu_wgrad"] if own else [])
-                                 + (["router_wgrad"] if g256 else ["gemm_down_wgrad", "router_wgrad", "gemm_gu_wgrad"]),
+                                 + (["gemm_down_wgrad", "router_wgrad"] if g256
+                                    else ["gemm_down_wgrad", "router_wgrad", "gemm_gu_wgrad"]),
             "splitk_reduce_kernel": ["splitk_reduce"] * (3 if own else 1),
             "wgrad_chunk_reduce_kernel": ["chunk_reduce", "chunk_reduce"],
             "wgrad_chunks_kernel": ["misc"], "transpose_bf16_kernel": ["misc"], "scatter_dlogits_kernel": ["misc"],

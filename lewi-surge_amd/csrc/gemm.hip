@@ -594,7 +594,13 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
   a.c_expert = ch.c_expert; a.c_row0 = ch.c_row0; a.c_rows = ch.c_rows; a.c_part = ch.c_part;
   a.num_chunks = ch.num_chunks; a.max_chunks = ch.max_chunks;
   a.x_expert = xo.expert; a.Cx = xo.C; a.C2x = xo.C2;
-  if (gemm_variant() == LSURGE_GEMM_G256) {
+  // The persistent 256 x 256 kernel when a chunk has at least 16 tiles (the gate/up weight gradient: 16 per chunk at
+  // d = 1024, 2f = 1024).  With fewer (the down weight gradient: 8 per chunk at f = 512, d = 1024) the persistent
+  // grid gets about two tiles per workgroup and the last round leaves most CUs idle; the 4-wave 128 x 256 kernel,
+  // whose non-persistent grid the dispatcher balances, measured faster there (176 against 203 us at C2).  Both give
+  // the same bits.
+  const bool g256_tiles = (int64_t)((I + g256::BM - 1) / g256::BM) * ((N + g256::BN - 1) / g256::BN) >= 16;
+  if (gemm_variant() == LSURGE_GEMM_G256 && g256_tiles) {
     // persistent 256 x 256 tiles, one workgroup per CU; the epilogue's descriptors span one tile's rows of an output
     if (int rc = check_desc((int64_t)g256::BM * std::max(N, ldc) * 4, "gemm_wgrad_chunked output")) return rc;
     a.i_tiles = (int)((I + g256::BM - 1) / g256::BM);
