@@ -34,6 +34,7 @@ for _p in (ROOT, os.path.join(ROOT, "lewi-surge_amd")):
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_FP8_TFLOPS = 5000.0   # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 matrix
 
 CONFIGS = {  # BASELINE.json configs (T, d, E, k, f, fs, zipf bias, fwd+bwd)
     "C1": dict(T=4096, d=1024, E=64, k=6, f=512, fs=512, zipf=False, bwd=False),
@@ -558,8 +559,8 @@ def gdn_bench(a):
                 "note": "from the kept residuals"},
         "recompute": {"bwd_ms": round(ms_br, 4), "fwd_bwd_ms": round(ms_r, 4),
                       "note": "backward recomputing the forward's chunk products and states (nothing kept)"},
-        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": 157.3, "unit": "TFLOP/s",
-                     "frac": round(tf / 157.3, 4), "traffic": None,
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_FP32_TFLOPS, 4), "traffic": None,
                      "note": "f32-accurate products on the bf16 matrix cores (f32 operands split into hi/lo bf16 "
                              "terms, 2-3 MFMAs per product); achieved counts the algorithmic flops once and is "
                              "priced against the MI355X fp32 matrix peak, the f32 work it stands for"}}), flush=True)
@@ -698,6 +699,28 @@ def ragged_bench(a):
         res[name] = dict(fwd_ms=round(tf, 4), fwd_TFs=round(fl / (tf * 1e-3) / 1e12, 1), bwd_ms=round(tb, 4),
                          bwd_TFs=round(2 * fl / (tb * 1e-3) / 1e12, 1),
                          hipblaslt_dense_same_shape_TFs=round(fl / (th * 1e-3) / 1e12, 1))
+    # f32 operands at the up shape: three bf16 terms per value, six term products (a GEMM six times as deep) plus the
+    # split kernels; TF/s count the f32 product's 2 M K N, against the fp32 matrix peak
+    K, Nn = 1024, 512
+    lhs = torch.randn((M, K), device=dev, generator=gen)
+    rhs = torch.randn((E, K, Nn), device=dev, generator=gen) * 0.02
+    g = torch.randn((M, Nn), device=dev, generator=gen)
+    out = torch.empty((M, Nn), dtype=torch.float32, device=dev)
+    dl = torch.empty((M, K), dtype=torch.float32, device=dev)
+    dr = torch.empty((E, K, Nn), dtype=torch.float32, device=dev)
+    ws = L.workspace(max(lib.lsurge_ragged_dot_f32_workspace_bytes(M, K, Nn, E),
+                         lib.lsurge_ragged_dot_bwd_f32_workspace_bytes(M, K, Nn, E)), dev)
+    fl = 2 * M * K * Nn
+    tf = _time_ms(lambda: L.check(lib.lsurge_ragged_dot(L.ptr(lhs), L.ptr(rhs), L.ptr(gs), M, K, Nn, E, L.F32,
+                                                        L.ptr(out), L.F32, L.ptr(ws), ws.numel(), st), "rd f32"),
+                  a.steps, a.warmup)
+    tb = _time_ms(lambda: L.check(lib.lsurge_ragged_dot_bwd(L.ptr(lhs), L.ptr(rhs), L.ptr(gs), L.ptr(g), M, K, Nn, E,
+                                                            L.F32, L.ptr(dl), L.ptr(dr), L.ptr(ws), ws.numel(), st),
+                                  "rd f32 bwd"), a.steps, a.warmup)
+    res["up 1024->512, f32 operands (3 bf16 terms, 6 products)"] = dict(
+        fwd_ms=round(tf, 4), fwd_TFs=round(fl / (tf * 1e-3) / 1e12, 1), bwd_ms=round(tb, 4),
+        bwd_TFs=round(2 * fl / (tb * 1e-3) / 1e12, 1), fp32_matrix_peak_TFs=PEAK_FP32_TFLOPS)
+    del lhs, rhs, g, out, dl, dr, ws
     big = torch.randn((8192, 8192), device=dev, generator=gen).to(torch.bfloat16)
     out = torch.empty_like(big)
     one = torch.tensor([8192], dtype=torch.int32, device=dev)

@@ -140,19 +140,25 @@ int lsurge_build_layout(const int32_t* flat, int64_t m, int64_t num_experts, int
  * ------------------------------------------------------------------------------------------------ */
 
 /* Dropless ragged_dot: out[r] = lhs[r] @ rhs[e(r)] for r < sum(group_sizes), 0 for the rows after.
- * lhs: [m, kdim] rows sorted by group and rhs: [e, kdim, n], both of in_dtype (LSURGE_BF16 or LSURGE_F16; f32
- * operands return LSURGE_ERR_DTYPE); group_sizes: [e] int32 (device); out: [m, n] of out_dtype (in_dtype, or
- * LSURGE_F32 for preferred_element_type=float32); f32 accumulation.  kdim % 8 == 0, n % 8 == 0.
+ * lhs: [m, kdim] rows sorted by group and rhs: [e, kdim, n], both of in_dtype (LSURGE_BF16, LSURGE_F16 or
+ * LSURGE_F32); group_sizes: [e] int32 (device); out: [m, n] of out_dtype (in_dtype, or LSURGE_F32 for
+ * preferred_element_type=float32; f32 operands: LSURGE_F32 or LSURGE_BF16); f32 accumulation.  kdim % 8 == 0,
+ * n % 8 == 0.  Workspace: lsurge_ragged_dot_workspace_bytes(m, e) for 16-bit operands,
+ * lsurge_ragged_dot_f32_workspace_bytes(m, kdim, n, e) for f32 ones.
+ * f32 operands run on the bf16 matrix cores: each value is split into three bf16 terms (24 significant bits) and the
+ * six term products of order <= 2 are summed in f32, a GEMM six times as deep (about 2^-24 relative error per
+ * product, the einsum's f32 result at precision=HIGHEST); lhs and rhs 16-byte aligned.
  * Replaces padded_gmm.padded_ragged_dot (modal/padded_gmm.py:45-69) / jax.lax.ragged_dot. */
 size_t lsurge_ragged_dot_workspace_bytes(int64_t m, int64_t e);
+size_t lsurge_ragged_dot_f32_workspace_bytes(int64_t m, int64_t kdim, int64_t n, int64_t e);
 int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_sizes, int64_t m, int64_t kdim,
                       int64_t n, int64_t e, int in_dtype, void* out, int out_dtype, void* workspace,
                       size_t workspace_bytes, lsurge_stream_t stream);
 
 /* lsurge_ragged_dot that allocates nothing and takes no workspace: its block table lives in a static device array
  * of the library (221 KB per GPU, held until the process ends), so m <= lsurge_ragged_dot_noalloc_max_rows() (2^21)
- * and e <= lsurge_ragged_dot_noalloc_max_groups() (1024); larger calls return LSURGE_ERR_INVALID.  Same results as
- * lsurge_ragged_dot.  Calls that overlap on one GPU share the array and race: serialise them (one stream).
+ * and e <= lsurge_ragged_dot_noalloc_max_groups() (1024); larger calls return LSURGE_ERR_INVALID.  16-bit operands
+ * only (f32 ones return LSURGE_ERR_DTYPE: their split terms need a workspace).  Same results as lsurge_ragged_dot.  Calls that overlap on one GPU share the array and race: serialise them (one stream).
  * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). */
 size_t lsurge_ragged_dot_noalloc_max_rows(void);
@@ -164,8 +170,11 @@ int lsurge_ragged_dot_noalloc(const void* lhs, const void* rhs, const int32_t* g
  * = 0) and drhs [e, kdim, n] f32.  Replaces the VJP of padded_gmm.padded_ragged_dot
  * (modal/padded_gmm.py:35-39 + XLA autodiff of the einsum at 67-68).
  * Workspace: lsurge_ragged_dot_bwd_workspace_bytes(m, kdim, n, e) lets drhs cut hot groups into row chunks
- * (e <= 256); the forward's lsurge_ragged_dot_workspace_bytes(m, e) is also accepted (one slice per group). */
+ * (e <= 256); the forward's lsurge_ragged_dot_workspace_bytes(m, e) is also accepted (one slice per group).
+ * f32 operands (split into bf16 terms as in the forward; 6 m < 2^31) need
+ * lsurge_ragged_dot_bwd_f32_workspace_bytes(m, kdim, n, e). */
 size_t lsurge_ragged_dot_bwd_workspace_bytes(int64_t m, int64_t kdim, int64_t n, int64_t e);
+size_t lsurge_ragged_dot_bwd_f32_workspace_bytes(int64_t m, int64_t kdim, int64_t n, int64_t e);
 int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group_sizes, const void* g,
                           int64_t m, int64_t kdim, int64_t n, int64_t e, int in_dtype, void* dlhs, float* drhs,
                           void* workspace, size_t workspace_bytes, lsurge_stream_t stream);

@@ -63,6 +63,8 @@ _SIGS = {
     "lsurge_layout_workspace_bytes": (_sz, [_i64, _i64]),
     "lsurge_build_layout": (_int, [_p, _i64, _i64] + [_p] * 10 + [_p, _sz, _p]),
     "lsurge_ragged_dot_workspace_bytes": (_sz, [_i64, _i64]),
+    "lsurge_ragged_dot_f32_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "lsurge_ragged_dot_bwd_f32_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "lsurge_ragged_dot": (_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _int, _p, _int, _p, _sz, _p]),
     "lsurge_ragged_dot_noalloc_max_rows": (_sz, []),
     "lsurge_ragged_dot_noalloc_max_groups": (_sz, []),

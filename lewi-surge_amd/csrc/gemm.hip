@@ -170,6 +170,50 @@ __global__ void zero_rows_from_kernel(void* __restrict__ out, int64_t m, int64_t
   }
 }
 
+// f32 operands on the bf16 matrix cores.  An f32 value x is the sum of three bf16 terms x0 = bf16(x),
+// x1 = bf16(x - x0), x2 = bf16(x - x0 - x1) (round to nearest even; each difference is exact in f32): 24 significant
+// bits.  The product x y is the sum of the six term products of order <= 2 (x0 y0, x1 y0, x2 y0, x0 y1, x1 y1,
+// x0 y2); the three left out and the remainder of each split are below 2^-24 |x y|, and every term product is exact
+// in the MFMA's f32 accumulation.  Laid side by side along a GEMM's reduction dimension, the six products are one
+// bf16 GEMM of six times the depth.  Term j of a split row is term ((pattern >> 2j) & 3) of the f32 row; the two
+// patterns below pair up as (t_j, s_j) = (0,0) (1,0) (2,0) (0,1) (1,1) (0,2).
+constexpr uint32_t kSplitT = 0u | 1u << 2 | 2u << 4 | 0u << 6 | 1u << 8 | 0u << 10;  // terms 0 1 2 0 1 0
+constexpr uint32_t kSplitS = 0u | 0u << 2 | 0u << 4 | 1u << 6 | 1u << 8 | 2u << 10;  // terms 0 0 0 1 1 2
+
+// x [rows, cols] f32 -> out [rows, 6 cols] bf16: out[r, j cols + c] = term ((PAT >> 2j) & 3) of x[r, c].  cols % 4 == 0
+// and x 16-byte aligned; one float4 per lane and step, six 8-byte stores (HBM-bound: 4 bytes in, 12 out per value).
+template <uint32_t PAT>
+__global__ __launch_bounds__(256) void split3_bf16_kernel(const float* __restrict__ x, int64_t rows, int64_t cols,
+                                                          bf16_t* __restrict__ out) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const int64_t c4n = cols / 4;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const float4* __restrict__ xr = reinterpret_cast<const float4*>(x + r * cols);
+    bf16_t* __restrict__ orow = out + r * 6 * cols;
+    for (int64_t c4 = (int64_t)blockIdx.x * 256 + threadIdx.x; c4 < c4n; c4 += (int64_t)gridDim.x * 256) {
+      const float4 v = xr[c4];
+      float rem[4] = {v.x, v.y, v.z, v.w};
+      u32x2 t[3];
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        t[q] = u32x2{pack_bf16x2(rem[0], rem[1]), pack_bf16x2(rem[2], rem[3])};
+        rem[0] -= __uint_as_float(t[q][0] << 16);
+        rem[1] -= __uint_as_float(t[q][0] & 0xffff0000u);
+        rem[2] -= __uint_as_float(t[q][1] << 16);
+        rem[3] -= __uint_as_float(t[q][1] & 0xffff0000u);
+      }
+#pragma unroll
+      for (int j = 0; j < 6; ++j)
+        *reinterpret_cast<u32x2*>(orow + j * cols + 4 * c4) = t[(PAT >> (2 * j)) & 3];
+    }
+  }
+}
+
+// group sizes times f (the row counts of the split weight gradient)
+__global__ void scale_counts_kernel(const int32_t* __restrict__ gs, int e, int f, int32_t* __restrict__ out) {
+  for (int i = threadIdx.x; i < e; i += blockDim.x) out[i] = gs[i] * f;
+}
+
 inline unsigned pad8(int64_t g) { return (unsigned)((g + 7) / 8 * 8); }
 
 // Chunk table of the routed weight gradients (one workgroup of 512 threads, thread e = expert e).  Expert e owns
@@ -757,12 +801,135 @@ static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_
 // row tiles of the bf16 / f16 ragged_dot GEMMs: 256 rows for the persistent kernel, else 128
 static int ragged_tile_rows() { return lsurge::gemm_variant() == LSURGE_GEMM_G256 ? 256 : 128; }
 
+// ---- f32 operands: three bf16 terms per value, six term products along a reduction six times as deep (the pairing
+// is described at split3_bf16_kernel).
+//   forward  out = A' B'      A' [m, 6k] = lhs terms t, B'_e [6k, n] = rhs terms s stacked along k
+//   dlhs     dl = G' R''^T    G' [m, 6n] = g terms s,   R''_e [k, 6n] = rhs terms t side by side along n
+//   drhs     dr_e = A'_e^T G'_e over 6 gs_e rows: A' and G' read as [6m, k] and [6m, n], whose row 6i + j holds term
+//            t_j of lhs row i and term s_j of g row i, so group e owns rows [6 start_e, 6 (start_e + gs_e))
+static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
+static size_t split_bytes(int64_t rows, int64_t cols) { return al256(12 * (size_t)std::max<int64_t>(0, rows) * cols); }
+
+size_t lsurge_ragged_dot_f32_workspace_bytes(int64_t m, int64_t kdim, int64_t n, int64_t e) {
+  return al256(lsurge_ragged_dot_workspace_bytes(m, e)) + split_bytes(m, kdim) + split_bytes(e * kdim, n);
+}
+
+// the f32 backward's chunked weight gradient (e <= 256) runs over 6 m rows
+static bool f32_bwd_chunked(int64_t m, int64_t e) { return m > 0 && ragged_chunked(e); }
+
+size_t lsurge_ragged_dot_bwd_f32_workspace_bytes(int64_t m, int64_t kdim, int64_t n, int64_t e) {
+  size_t b = al256(lsurge_ragged_dot_workspace_bytes(m, e)) + al256(lsurge_ragged_dot_workspace_bytes(6 * m, e)) +
+             al256(sizeof(int32_t) * (size_t)std::max<int64_t>(e, 0)) + split_bytes(m, kdim) + split_bytes(m, n) +
+             split_bytes(e * kdim, n);
+  if (f32_bwd_chunked(m, e)) {
+    const lsurge::WgradChunkPlan p = lsurge::wgrad_chunk_plan(6 * m, e);
+    b += al256(sizeof(int32_t) * lsurge::wgrad_chunk_table_ints(p, e)) + lsurge::wgrad_chunked_workspace_bytes(p, kdim, n);
+  }
+  return b;
+}
+
+// x [rows, cols] f32 -> [rows, 6 cols] bf16 terms in the order of pattern kSplitT (t) or kSplitS (s)
+static int split3(const float* x, int64_t rows, int64_t cols, bool t_terms, bf16_t* out, hipStream_t s) {
+  LSURGE_REQUIRE(cols % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0,
+                 "ragged_dot f32: operands must be 16-byte aligned with rows of a multiple of 4 values");
+  if (rows == 0) return LSURGE_OK;
+  const int64_t c4 = cols / 4;
+  const unsigned gx = (unsigned)std::min<int64_t>((c4 + 255) / 256, 1024);
+  const unsigned gy = (unsigned)std::min<int64_t>(rows, std::max<int64_t>(1, 8192 / gx));
+  if (t_terms)
+    LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL(split3_bf16_kernel<kSplitT>, dim3(gx, gy), dim3(256), 0, s, x, rows,
+                                                  cols, out));
+  else
+    LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL(split3_bf16_kernel<kSplitS>, dim3(gx, gy), dim3(256), 0, s, x, rows,
+                                                  cols, out));
+  return LSURGE_OK;
+}
+
+static int ragged_dot_f32(const float* lhs, const float* rhs, const int32_t* gs, int64_t m, int64_t kdim, int64_t n,
+                          int64_t e, void* out, int out_dtype, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (out_dtype != LSURGE_F32 && out_dtype != LSURGE_BF16)
+    return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot: out_dtype of f32 operands must be f32 or bf16");
+  if (int rc = lsurge::check_gemm_shape(kdim, n, "ragged_dot f32")) return rc;
+  const size_t need = lsurge_ragged_dot_f32_workspace_bytes(m, kdim, n, e);
+  LSURGE_REQUIRE(ws && ws_bytes >= need, "ragged_dot f32: workspace %zu < %zu bytes", ws_bytes, need);
+  char* base = (char*)ws;
+  size_t off = al256(lsurge_ragged_dot_workspace_bytes(m, e));
+  bf16_t* a2 = (bf16_t*)(base + off);
+  off += split_bytes(m, kdim);
+  bf16_t* b2 = (bf16_t*)(base + off);
+  lsurge::GemmBlocks g;
+  int32_t *total, *e_row0, *e_rows;
+  if (int rc = ragged_setup(gs, m, e, ws, ws_bytes, s, &g, &total, &e_row0, &e_rows, ragged_tile_rows())) return rc;
+  if (int rc = split3(lhs, m, kdim, true, a2, s)) return rc;
+  if (int rc = split3(rhs, e, kdim * n, false, b2, s)) return rc;
+  const bool f32 = out_dtype == LSURGE_F32;
+  if (int rc = lsurge::gemm_rows_kn(KID_MISC, g, a2, 6 * kdim, b2, n, 6 * kdim * n, 6 * kdim, n, out, n, s, f32,
+                                    lsurge::ExtraExpert(), LSURGE_BF16))
+    return rc;
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, out, m, n, f32 ? 4 : 2, total));
+  return LSURGE_OK;
+}
+
+static int ragged_dot_bwd_f32(const float* lhs, const float* rhs, const int32_t* gs, const float* g, int64_t m,
+                              int64_t kdim, int64_t n, int64_t e, float* dlhs, float* drhs, void* ws, size_t ws_bytes,
+                              hipStream_t s) {
+  if (int rc = lsurge::check_gemm_shape(kdim, n, "ragged_dot_bwd f32")) return rc;
+  LSURGE_REQUIRE(6 * m < (1ll << 31), "ragged_dot_bwd f32: m=%lld too large (6 m rows)", (long long)m);
+  const size_t need = lsurge_ragged_dot_bwd_f32_workspace_bytes(m, kdim, n, e);
+  LSURGE_REQUIRE(ws && ws_bytes >= need, "ragged_dot_bwd f32: workspace %zu < %zu bytes", ws_bytes, need);
+  char* base = (char*)ws;
+  const size_t t1 = al256(lsurge_ragged_dot_workspace_bytes(m, e));
+  const size_t t6 = al256(lsurge_ragged_dot_workspace_bytes(6 * m, e));
+  int32_t* gs6 = (int32_t*)(base + t1 + t6);
+  size_t off = t1 + t6 + al256(sizeof(int32_t) * e);
+  bf16_t* a2 = (bf16_t*)(base + off);
+  off += split_bytes(m, kdim);
+  bf16_t* g2 = (bf16_t*)(base + off);
+  off += split_bytes(m, n);
+  bf16_t* r2 = (bf16_t*)(base + off);
+  off += split_bytes(e * kdim, n);
+  lsurge::GemmBlocks gb, gb6;
+  int32_t *total, *e_row0, *e_rows, *total6, *e_row0_6, *e_rows_6;
+  if (int rc = ragged_setup(gs, m, e, base, t1, s, &gb, &total, &e_row0, &e_rows, ragged_tile_rows())) return rc;
+  LSURGE_LAUNCH(KID_MISC, s, hipLaunchKernelGGL(scale_counts_kernel, dim3(1), dim3(256), 0, s, gs, (int)e, 6, gs6));
+  if (int rc = ragged_setup(gs6, 6 * m, e, base + t1, t6, s, &gb6, &total6, &e_row0_6, &e_rows_6)) return rc;
+  if (int rc = split3(lhs, m, kdim, true, a2, s)) return rc;
+  if (int rc = split3(g, m, n, false, g2, s)) return rc;
+  if (int rc = split3(rhs, e * kdim, n, true, r2, s)) return rc;
+  if (m > 0) {
+    if (int rc = lsurge::gemm_rows_nk(KID_MISC, gb, g2, 6 * n, r2, nullptr, 0, 6 * n, 6 * kdim * n, 6 * n, kdim, dlhs,
+                                      kdim, false, nullptr, nullptr, 0, s, true, lsurge::ExtraExpert(), LSURGE_BF16))
+      return rc;
+    LSURGE_LAUNCH(KID_MISC, s,
+                  hipLaunchKernelGGL(zero_rows_from_kernel, dim3(1024), dim3(256), 0, s, dlhs, m, kdim, 4, total));
+  }
+  if (f32_bwd_chunked(m, e)) {
+    const lsurge::WgradChunkPlan p = lsurge::wgrad_chunk_plan(6 * m, e);
+    int32_t* table = (int32_t*)(base + off);
+    off += al256(sizeof(int32_t) * lsurge::wgrad_chunk_table_ints(p, e));
+    lsurge::WgradChunks ch;
+    if (int rc = lsurge::build_wgrad_chunks(e_rows_6, e_row0_6, (int)e, p, table, &ch, s, -1, 0, 1)) return rc;
+    return lsurge::gemm_wgrad_chunked(KID_MISC, ch, (int)e, 6 * m, a2, kdim, g2, n, kdim, n, drhs, nullptr, 0, n,
+                                      kdim * n, base + off, lsurge::wgrad_chunked_workspace_bytes(p, kdim, n), s,
+                                      lsurge::RowGather(), lsurge::ExtraOut(), LSURGE_BF16);
+  }
+  return lsurge::gemm_wgrad(KID_MISC, (int)e, e_row0_6, 1, e_rows_6, 0, 6 * m, a2, kdim, g2, n, kdim, n, drhs, nullptr,
+                            0, n, kdim * n, 1, nullptr, 0, s, lsurge::RowGather(), LSURGE_BF16);
+}
+
 int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_sizes, int64_t m, int64_t kdim, int64_t n,
                       int64_t e, int in_dtype, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
                       lsurge_stream_t stream) {
   LSURGE_REQUIRE(m >= 0 && e >= 1 && m < (1ll << 31), "ragged_dot: bad m/e");
+  if (in_dtype == LSURGE_F32) {
+    if (m == 0) return LSURGE_OK;
+    LSURGE_REQUIRE(lhs && rhs && group_sizes && out, "ragged_dot: null pointer");
+    return ragged_dot_f32((const float*)lhs, (const float*)rhs, group_sizes, m, kdim, n, e, out, out_dtype, workspace,
+                          workspace_bytes, (hipStream_t)stream);
+  }
   if (in_dtype != LSURGE_BF16 && in_dtype != LSURGE_F16)
-    return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot: operands must be bf16 or f16 (got dtype %d)", in_dtype);
+    return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot: operands must be f32, bf16 or f16 (got dtype %d)", in_dtype);
   if (out_dtype != in_dtype && out_dtype != LSURGE_F32)
     return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot: out_dtype must be the operand dtype or f32");
   if (m == 0) return LSURGE_OK;
@@ -835,6 +1002,9 @@ int lsurge_ragged_dot_noalloc(const void* lhs, const void* rhs, const int32_t* g
   const size_t need = lsurge_ragged_dot_workspace_bytes(m, e);
   LSURGE_REQUIRE(need <= sizeof(int32_t) * kScratchInts, "ragged_dot_noalloc: table of %zu bytes exceeds the scratch",
                  need);
+  if (in_dtype == LSURGE_F32)
+    return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot_noalloc: f32 operands need the split-term workspace of "
+                             "lsurge_ragged_dot");
   if (m == 0) return LSURGE_OK;
   int32_t* ws = scratch_on_current_device();
   if (!ws) return LSURGE_ERR_LAUNCH;
@@ -866,10 +1036,14 @@ int lsurge_ragged_dot_bwd(const void* lhs, const void* rhs, const int32_t* group
                           int64_t kdim, int64_t n, int64_t e, int in_dtype, void* dlhs, float* drhs, void* workspace,
                           size_t workspace_bytes, lsurge_stream_t stream) {
   LSURGE_REQUIRE(m >= 0 && e >= 1 && m < (1ll << 31), "ragged_dot_bwd: bad m/e");
-  if (in_dtype != LSURGE_BF16 && in_dtype != LSURGE_F16)
-    return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot_bwd: operands must be bf16 or f16 (got dtype %d)", in_dtype);
+  if (in_dtype != LSURGE_F32 && in_dtype != LSURGE_BF16 && in_dtype != LSURGE_F16)
+    return lsurge::set_error(LSURGE_ERR_DTYPE, "ragged_dot_bwd: operands must be f32, bf16 or f16 (got dtype %d)",
+                             in_dtype);
   LSURGE_REQUIRE(lhs && rhs && group_sizes && g && dlhs && drhs, "ragged_dot_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
+  if (in_dtype == LSURGE_F32)
+    return ragged_dot_bwd_f32((const float*)lhs, (const float*)rhs, group_sizes, (const float*)g, m, kdim, n, e,
+                              (float*)dlhs, drhs, workspace, workspace_bytes, s);
   lsurge::GemmBlocks gb;
   int32_t *total, *e_row0, *e_rows;
   if (int rc = ragged_setup(group_sizes, m, e, workspace, workspace_bytes, s, &gb, &total, &e_row0, &e_rows,

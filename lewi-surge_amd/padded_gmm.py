@@ -1,7 +1,8 @@
 """Grouped GEMM in place of jax.lax.ragged_dot -- the public surface of the reference's modal/padded_gmm.py,
-computed by hand-written gfx950 MFMA kernels (liblewi_surge.so) on bf16 or f16 operands.
+computed by hand-written gfx950 MFMA kernels (liblewi_surge.so) on bf16, f16 or f32 operands.
 
-Input as for ragged_dot: lhs [M, K] sorted by group, rhs [E, K, N], group_sizes [E] -> [M, N].
+Input as for ragged_dot: lhs [M, K] sorted by group, rhs [E, K, N], group_sizes [E] -> [M, N].  float32 operands
+run on the same bf16 kernels, each value split into three bf16 terms (see padded_ragged_dot).
 
 Layout.  The reference copies the rows into a capacity buffer [E, C, K] (C = roundup8(ceil(M/E * FACTOR))), runs
 one batched einsum and gathers back, silently dropping rows past C (modal/padded_gmm.py:8, 51-69).  Here the
@@ -73,6 +74,11 @@ def _perm_gather(x, idx, inv_idx):
     return _PermGather.apply(x, idx, inv_idx)
 
 
+def _aligned(t):
+    """t, or a copy of it when its data does not start on a 16-byte boundary (the f32 split kernels' float4 loads)."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 class _RaggedDot(torch.autograd.Function):
 
     @staticmethod
@@ -80,7 +86,12 @@ class _RaggedDot(torch.autograd.Function):
         m, k = lhs.shape
         e, _, n = rhs.shape
         out = torch.empty((m, n), dtype=out_dtype, device=lhs.device)
-        ws = L.workspace(L.lib().lsurge_ragged_dot_workspace_bytes(m, e), lhs.device)
+        if lhs.dtype == torch.float32:
+            lhs, rhs = _aligned(lhs), _aligned(rhs)
+            wsb = L.lib().lsurge_ragged_dot_f32_workspace_bytes(m, k, n, e)
+        else:
+            wsb = L.lib().lsurge_ragged_dot_workspace_bytes(m, e)
+        ws = L.workspace(wsb, lhs.device)
         L.check(L.lib().lsurge_ragged_dot(L.ptr(lhs), L.ptr(rhs), L.ptr(group_sizes), m, k, n, e, L.dt(lhs),
                                           L.ptr(out), L.dt(out), L.ptr(ws), ws.numel(), L.stream(lhs.device)),
                 "ragged_dot")
@@ -95,7 +106,12 @@ class _RaggedDot(torch.autograd.Function):
         g = L.contig(g.to(lhs.dtype))
         dlhs = torch.empty_like(lhs)
         drhs = torch.empty((e, k, n), dtype=torch.float32, device=lhs.device)
-        ws = L.workspace(L.lib().lsurge_ragged_dot_bwd_workspace_bytes(m, k, n, e), lhs.device)
+        if lhs.dtype == torch.float32:
+            g = _aligned(g)
+            wsb = L.lib().lsurge_ragged_dot_bwd_f32_workspace_bytes(m, k, n, e)
+        else:
+            wsb = L.lib().lsurge_ragged_dot_bwd_workspace_bytes(m, k, n, e)
+        ws = L.workspace(wsb, lhs.device)
         L.check(L.lib().lsurge_ragged_dot_bwd(L.ptr(lhs), L.ptr(rhs), L.ptr(gs), L.ptr(g), m, k, n, e, L.dt(lhs),
                                               L.ptr(dlhs), L.ptr(drhs), L.ptr(ws), ws.numel(), L.stream(lhs.device)),
                 "ragged_dot_bwd")
@@ -105,20 +121,23 @@ class _RaggedDot(torch.autograd.Function):
 def padded_ragged_dot(lhs, rhs, group_sizes, precision=None, preferred_element_type=None, **kw):
     """Dropless grouped GEMM with ragged_dot's signature.  modal/padded_gmm.py:45-69.
 
-    lhs [M, K] bf16 or f16 (rows sorted by group), rhs [E, K, N] (cast to lhs.dtype as in the reference, 67),
-    group_sizes [E] int -> [M, N] in preferred_element_type (default lhs.dtype); rows past sum(gs) are 0.
-    float32 lhs is rejected with TypeError: the MFMA kernels take 16-bit operands (a deliberate limit; the
-    reference's XLA einsum would run it in f32).
+    lhs [M, K] bf16, f16 or float32 (rows sorted by group), rhs [E, K, N] (cast to lhs.dtype as in the reference,
+    67), group_sizes [E] int -> [M, N] in preferred_element_type (default lhs.dtype); rows past sum(gs) are 0.
+    float32 operands run on the bf16 matrix cores as three bf16 terms per value, summing the six term products of
+    order <= 2 in f32 (about 2^-24 relative error per product: the einsum's f32 result at its highest precision,
+    whatever `precision` asks); their output is float32 or bfloat16.
     """
     if lhs.ndim != 2 or rhs.ndim != 3 or kw.get("group_offset") is not None:
         return _orig_ragged_dot(lhs, rhs, group_sizes, precision=precision,
                                 preferred_element_type=preferred_element_type, **kw)
     L.require_cuda(lhs, rhs, group_sizes)
-    if lhs.dtype not in (torch.bfloat16, torch.float16):
-        raise TypeError(f"padded_ragged_dot: the MFMA kernels take bf16 or f16 operands, got lhs {lhs.dtype}")
+    if lhs.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"padded_ragged_dot: lhs must be bfloat16, float16 or float32, got {lhs.dtype}")
     out_dtype = preferred_element_type or lhs.dtype
-    if out_dtype not in (lhs.dtype, torch.float32):
-        raise TypeError(f"padded_ragged_dot: preferred_element_type {out_dtype} not supported ({lhs.dtype} or float32)")
+    allowed = (torch.float32, torch.bfloat16) if lhs.dtype == torch.float32 else (lhs.dtype, torch.float32)
+    if out_dtype not in allowed:
+        raise TypeError(f"padded_ragged_dot: preferred_element_type {out_dtype} not supported for {lhs.dtype} "
+                        f"operands ({' or '.join(str(a) for a in allowed)})")
     m, k = lhs.shape
     e, k2, n = rhs.shape
     if k2 != k or group_sizes.shape != (e,):

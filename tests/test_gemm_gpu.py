@@ -73,11 +73,88 @@ def test_f16_operands(gs, M, K, N, out_dtype, dev):
     assert err < 5e-3
 
 
-def test_f32_operands_rejected(dev):
+F32_TOL = 1e-5  # the reference's f32 tolerance, max-normalised (modal/test_moe_permute.py:27-31, 44)
+
+
+def max_err(got, want):
+    """max |got - want| / (max |want| + 1e-6), the reference's check (modal/test_moe_permute.py:27-31)."""
+    return float(np.abs(got - want).max() / (np.abs(want).max() + 1e-6)) if want.size else 0.0
+
+
+def run_case_f32(gs, M, K, N, dev, seed=0, out_dtype=None, offset=0):
+    """float32 operands (split into bf16 terms on the device) against the fp64 oracle, forward and backward.
+    offset > 0 starts lhs and rhs `offset` floats into their storage (not 16-byte aligned)."""
+    rng = np.random.default_rng(seed)
+    E = len(gs)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal((E, K, N)).astype(np.float32)
+    g = rng.standard_normal((M, N)).astype(np.float32)
+
+    def tdev(v):
+        flat = torch.zeros(v.size + offset, dtype=torch.float32, device=dev)
+        t = flat[offset:].view(v.shape)
+        t.copy_(torch.from_numpy(v))
+        return t
+
+    at = tdev(a).requires_grad_(True)
+    bt = tdev(b).requires_grad_(True)
+    gst = torch.tensor(gs, dtype=torch.int32, device=dev)
+    out = pg.padded_ragged_dot(at, bt, gst, preferred_element_type=out_dtype)
+    assert out.dtype == (out_dtype or torch.float32)
+    out.backward(tdev(g).to(out.dtype))
+    S = int(np.sum(gs))
+    got = out.detach().float().cpu().numpy()
+    gl = at.grad.cpu().numpy()
+    gr = bt.grad.cpu().numpy()
+    assert at.grad.dtype == torch.float32 and bt.grad.dtype == torch.float32
+    assert np.all(got[S:] == 0) and np.all(gl[S:] == 0)
+    for e in range(E):
+        if gs[e] == 0:
+            assert np.all(gr[e] == 0)
+    want = mo.ragged_dot(a, b, gs)
+    gw = mo.round_bf16(g) if out_dtype == torch.bfloat16 else g
+    dl, dr = mo.ragged_dot_bwd(a, b, gs, gw)
+    return max_err(got, want), max_err(gl, dl), max_err(gr, dr)
+
+
+@pytest.mark.parametrize("gs,M,K,N", [
+    ([5, 0, 9, 3, 7, 1, 6, 4], 38, 64, 48),              # modal/te_run.py:72-79's case list, f32
+    ([300, 0, 517, 1, 255, 256, 257], 1700, 192, 200),   # K of 3 stages (x6 = 18), N tail inside a tile
+    ([1536] * 16, 24576, 1024, 512),                     # the dense shape of modal/gemm_bench.py:25-41
+    ([0, 8000, 0, 995], 9000, 128, 64),                  # hot group: the chunked weight gradient over 6 m rows
+    ([0, 0], 3, 64, 32),                                 # no rows in any group
+])
+def test_f32_operands(gs, M, K, N, dev):
+    """f32 lhs / rhs (the reference's einsum runs in lhs.dtype, modal/padded_gmm.py:67-68) against the fp64 oracle
+    at the reference's f32 tolerance, forward, dlhs and drhs."""
+    errs = run_case_f32(gs, M, K, N, dev, seed=M + K)
+    assert max(errs) <= F32_TOL, errs
+
+
+def test_f32_operands_many_groups(dev):
+    """E > 256: the f32 weight gradient without the chunk table (one slice per group)."""
+    rng = np.random.default_rng(5)
+    gs = rng.integers(0, 20, 300).tolist()
+    errs = run_case_f32(gs, int(np.sum(gs)) + 7, 64, 32, dev, seed=9)
+    assert max(errs) <= F32_TOL, errs
+
+
+def test_f32_operands_unaligned_and_bf16_out(dev):
+    """lhs / rhs starting 4 bytes into their storage (copied to aligned memory first), and bf16 output of f32
+    operands (the output rounding bounds the forward; the gradients stay f32)."""
+    gs = [100, 0, 57, 230]
+    errs = run_case_f32(gs, 400, 128, 96, dev, seed=2, offset=1)
+    assert max(errs) <= F32_TOL, errs
+    errs = run_case_f32(gs, 400, 128, 96, dev, seed=2, out_dtype=torch.bfloat16)
+    assert errs[0] <= 8e-3 and max(errs[1:]) <= F32_TOL, errs
+
+
+def test_f32_operands_reject_f16_output(dev):
     a = torch.zeros((16, 64), dtype=torch.float32, device=dev)
     b = torch.zeros((2, 64, 32), dtype=torch.float32, device=dev)
-    with pytest.raises(TypeError, match="bf16 or f16"):
-        pg.padded_ragged_dot(a, b, torch.tensor([8, 8], dtype=torch.int32, device=dev))
+    with pytest.raises(TypeError, match="preferred_element_type"):
+        pg.padded_ragged_dot(a, b, torch.tensor([8, 8], dtype=torch.int32, device=dev),
+                             preferred_element_type=torch.float16)
 
 
 @pytest.mark.parametrize("E,M,K,N", [(8, 1000, 256, 192), (4, 777, 128, 1024), (64, 6000, 1024, 512),
