@@ -121,7 +121,11 @@ def measured_traffic(config, kernel, fp8=False, bwd=True):
     `bench-traffic <kernel> <bytes>` in profiles/moe_layer_<config>_fwd_bwd.md, or _fp8_fwd_bwd.md / _fp8_fwd.md for
     --fp8), or None."""
     name = ("fp8_fwd_bwd" if bwd else "fp8_fwd") if fp8 else "fwd_bwd"
-    path = os.path.join(ROOT, "profiles", f"moe_layer_{config.lower()}_{name}.md")
+    return traffic_from(os.path.join(ROOT, "profiles", f"moe_layer_{config.lower()}_{name}.md"), kernel)
+
+
+def traffic_from(path, kernel):
+    """The `bench-traffic <kernel> <bytes>` line of a committed profile summary, or None."""
     try:
         with open(path) as fh:
             for line in fh:
@@ -285,6 +289,47 @@ def label_launches(rows, c):
         seen[k] = i + 1
         out.append((roles[k][i] if i < len(roles[k]) else "other", k, row))
     return out
+
+
+def kernel_traffic(a):
+    """Per-kernel HBM bytes per dispatch from rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs of any bench.py mode
+    (a.pmc_fetch, a.pmc_write), calibrated on --copy-probe runs (a.copy_fetch, a.copy_write) as in profile_summary;
+    kernels keyed by short name (gdn_bchunk_kernel -> gdn_bchunk).  Prints a markdown table and one
+    `bench-traffic <kernel> <bytes>` line per kernel (read + write bytes per launch)."""
+    import csv
+    import glob
+
+    def rows_of(d, kind):
+        files = glob.glob(os.path.join(d, f"*{kind}.csv"))
+        if not files:
+            raise SystemExit(f"kernel traffic: no *{kind}.csv under {d}")
+        with open(files[0]) as fh:
+            return list(csv.DictReader(fh))
+
+    per = {}
+    for name, d, cd in (("FETCH_SIZE", a.pmc_fetch, a.copy_fetch), ("WRITE_SIZE", a.pmc_write, a.copy_write)):
+        probe = [r for r in rows_of(cd, "counter_collection") if "copyBuffer" in r["Kernel_Name"]]
+        fac = (a.copy_probe_mib << 20) / (sum(float(r["Counter_Value"]) for r in probe) / len(probe) * 1024)
+        print(f"calibration {name}: x{fac:.3f} (bytes per KiB-count unit x 1024)")
+        for r in rows_of(d, "counter_collection"):
+            if r["Counter_Name"] != name:
+                continue
+            k = short_kernel(r["Kernel_Name"])
+            if "at::" in k or "copyBuffer" in k:
+                continue
+            k = k[:-len("_kernel")] if k.endswith("_kernel") else k
+            per.setdefault(k, {}).setdefault(name, []).append(float(r["Counter_Value"]) * 1024 * fac)
+    print()
+    print("| kernel | dispatches | HBM read MB / launch | HBM write MB / launch |")
+    print("|---|---|---|---|")
+    for k, v in sorted(per.items()):
+        rd, wr = v.get("FETCH_SIZE", []), v.get("WRITE_SIZE", [])
+        print(f"| {k} | {len(rd)} | {sum(rd) / max(1, len(rd)) / 1e6:.1f} | {sum(wr) / max(1, len(wr)) / 1e6:.1f} |")
+    print()
+    for k, v in sorted(per.items()):
+        if v.get("FETCH_SIZE") and v.get("WRITE_SIZE"):
+            print(f"bench-traffic {k} "
+                  f"{sum(v['FETCH_SIZE']) / len(v['FETCH_SIZE']) + sum(v['WRITE_SIZE']) / len(v['WRITE_SIZE']):.0f}")
 
 
 def stats_summary(d):
@@ -535,15 +580,55 @@ def gdn_bench(a):
         fwd()
         bwd_recompute()
 
+    # per-kernel averages over a few training steps (forward keeping its residuals + backward from them), each
+    # launch bracketed by the library's profiler
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    lib.lsurge_prof_reset()
+    lib.lsurge_prof_enable(-1)
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    lib.lsurge_prof_collect()
+    lib.lsurge_prof_enable(0)
+    table = prof_table(lib, 3)
+    chunks = B * H * ((T + C - 1) // C)
+    kbytes = gdn_kernel_bytes(C, D)
+    prof_md = os.path.join(ROOT, "profiles", "gdn_chunked_fwd_bwd.md")
+    kern = {}
+    for n, (rd, wr) in kbytes.items():
+        if n not in table:
+            continue
+        ms_k = table[n][0]
+        kern[n] = {"ms": round(ms_k, 4), "algorithmic_MB": round(chunks * (rd + wr) / 1e6, 1),
+                   "GB/s": round(chunks * (rd + wr) / (ms_k * 1e-3) / 1e9, 1),
+                   "hbm_frac": round(chunks * (rd + wr) / (ms_k * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                   "traffic": traffic_from(prof_md, n)}
+    dom = max(kern, key=lambda n: kern[n]["ms"])
+    # the dominant kernel alone bracketed (its launch stream is torch's current one) over a.steps training steps
+    names = [lib.lsurge_prof_kernel_name(i).decode() for i in range(lib.lsurge_prof_kernel_count())]
+    lib.lsurge_prof_reset()
+    lib.lsurge_prof_enable(1 << names.index(dom))
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    lib.lsurge_prof_collect()
+    lib.lsurge_prof_enable(0)
+    ms_k = prof_table(lib, a.steps)[dom][0]
+    rd, wr = kbytes[dom]
+    kern[dom].update({"ms": round(ms_k, 4), "GB/s": round(chunks * (rd + wr) / (ms_k * 1e-3) / 1e9, 1),
+                      "hbm_frac": round(chunks * (rd + wr) / (ms_k * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+
     ms_f = _time_ms(fwd, a.steps, a.warmup)
     ms_fs = _time_ms(fwd_save, a.steps, a.warmup)
     ms_b = _time_ms(bwd, a.steps, a.warmup)
     ms_br = _time_ms(bwd_recompute, a.steps, a.warmup)
     ms_r = _time_ms(step_recompute, a.steps, a.warmup)
     ms = _time_ms(step, a.steps, a.warmup)
-    chunks = B * H * ((T + C - 1) // C)
     flops = chunks * 2 * (2 * C * C * D + 2 * C * C * D + 2 * C * D * D + C * C * D + C * D * D)
     tf = 3 * flops / (ms * 1e-3) / 1e12
+    dk = kern[dom]
     print(json.dumps({
         "metric": "Gated DeltaNet chunked scan fwd+bwd tokens/sec @1 GPU", "value": round(B * T / (ms * 1e-3), 1),
         "unit": "tokens/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
@@ -559,11 +644,35 @@ def gdn_bench(a):
                 "note": "from the kept residuals"},
         "recompute": {"bwd_ms": round(ms_br, 4), "fwd_bwd_ms": round(ms_r, 4),
                       "note": "backward recomputing the forward's chunk products and states (nothing kept)"},
-        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tf / PEAK_FP32_TFLOPS, 4), "traffic": None,
-                     "note": "f32-accurate products on the bf16 matrix cores (f32 operands split into hi/lo bf16 "
-                             "terms, 2-3 MFMAs per product); achieved counts the algorithmic flops once and is "
-                             "priced against the MI355X fp32 matrix peak, the f32 work it stands for"}}), flush=True)
+        "kernels": kern,
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": dk["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": dk["hbm_frac"], "traffic": dk["traffic"], "launch_ms": dk["ms"],
+                     "note": "the step's longest kernel against HBM: achieved = its algorithmic bytes (tiles read and "
+                             "written once per chunk) / its average launch time; traffic = rocprofv3 FETCH_SIZE + "
+                             "WRITE_SIZE bytes per launch (profiles/gdn_chunked_fwd_bwd.md)"},
+        "matrix_view": {"achieved": round(tf, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tf / PEAK_FP32_TFLOPS, 4),
+                        "note": "the whole step's algorithmic f32 flops (counted once; the products run on the bf16 "
+                                "matrix cores as hi/lo terms) over the fp32 matrix peak"}}), flush=True)
+
+
+def gdn_kernel_bytes(C, D):
+    """Algorithmic HBM bytes per (chunk, head, sequence) of each chunked gated delta rule kernel of the training step
+    (read, written): every tile read or written once.  bf16 [C, D] tiles are 2 C D bytes, f32 [C, C] 4 C C, the f32
+    state [D, D] 4 D D; per-token scalars (g, beta, gcum, dg, dbeta) 4 C or 2 C.
+      gdn_chunk   reads q, k, v, g, beta; writes u, w, attn, gcum and the backward's S, A
+      gdn_scan    reads q, k, w, u, attn, gcum; writes o and the state entering the chunk
+      gdn_bscan   reads q, k, w, attn, gcum, do; writes dH entering the chunk
+      gdn_bgrad   reads k, u, w, attn, gcum, do, h, dH; writes dqg, dkd (f32), du, dw (bf16), dP (f32), dgl
+      gdn_bchunk  reads q, k, v, beta, attn, gcum, S, A, dqg, dkd, du, dw, dP, dgl; writes dq, dk, dv, dg, dbeta"""
+    t16, m32, st, sc = 2 * C * D, 4 * C * C, 4 * D * D, 4 * C
+    return {
+        "gdn_chunk": (3 * t16 + sc + 2 * C, 2 * t16 + 3 * m32 + sc),
+        "gdn_scan": (4 * t16 + m32 + sc, t16 + st),
+        "gdn_bscan": (4 * t16 + m32 + sc, st),
+        "gdn_bgrad": (4 * t16 + m32 + sc + 2 * st, 2 * 2 * t16 + 2 * t16 + m32 + 4),
+        "gdn_bchunk": (3 * t16 + 2 * C + 3 * m32 + sc + 2 * 2 * t16 + 2 * t16 + m32 + 4, 3 * t16 + 2 * sc),
+    }
 
 
 def _time_ms(fn, steps, warmup):
@@ -587,8 +696,10 @@ def permute_bench(a):
     (argsort vs count, both the same counting-sort kernel here), and the dispatch -> identity expert -> combine block
     forward + backward.  GB/s use the reference's byte model, read + write of the gathered rows (line 63), per kernel:
     gather_rows 2 M D 2, gather_reduce M D 2 + N D 2 (bf16 out), gather_dot M D 2 + N D 2, and for the block the sum
-    over its kernels of the SURVEY byte model (dispatch 2 M D 2, combine M D 2 + N D 4, combine backward dy 2 M D 2 and
-    dw M D 2 + N D 2, dispatch backward M D 2 + N D 2; index bytes included)."""
+    over its kernels of their byte models (dispatch 2 M D 2, combine M D 2 + N D 4, combine backward dy 2 M D 2 and
+    dw M D 2 + N D 2, dispatch backward M D 2 + N D 2; index bytes included).  Beside every kernel, the reference
+    column: the same call through the plain torch path (CFG["enabled"] = False) and the block with
+    use_kernels=False, as the reference times its XLA path (colab/tpu_permute_bench.py:72-77, 96-104)."""
     import torch
 
     import moe_permute as mp
@@ -609,34 +720,53 @@ def permute_bench(a):
         idx = torch.div(order, k, rounding_mode="floor").to(torch.int32)
         pos2 = pos.reshape(N, k)
         res = {}
-        t = _time_ms(lambda: mp.sort_indices(flat, E, "count"), a.steps, a.warmup)
-        res["sort_indices"] = dict(ms=round(t, 4), GBs=round((4 * M + 8 * M) / (t * 1e-3) / 1e9, 1))
+
+        def both(fn, steps, warmup):
+            """(kernel ms, reference ms): the reference column is the same call with CFG["enabled"] = False, the
+            plain torch path (the reference times its XLA path the same way, colab/tpu_permute_bench.py:72-77)."""
+            tk = _time_ms(fn, steps, warmup)
+            mp.CFG["enabled"] = False
+            try:
+                tr = _time_ms(fn, steps, warmup)
+            finally:
+                mp.CFG["enabled"] = True
+            return tk, tr
+
+        t, tr = both(lambda: mp.sort_indices(flat, E, "count"), a.steps, a.warmup)
+        res["sort_indices"] = dict(ms=round(t, 4), GBs=round((4 * M + 8 * M) / (t * 1e-3) / 1e9, 1),
+                                   ref_ms=round(tr, 4), ref_note="torch.argsort(flat) and argsort(argsort(flat))")
         for name, fn, nbytes in (
                 ("gather_rows", lambda: mp.gather_rows(x, idx), 2 * M * D * 2 + 4 * M),
                 ("gather_reduce", lambda: mp.gather_reduce(y, pos2, w), M * D * 2 + N * D * 2 + 8 * M),
                 ("gather_dot", lambda: mp.gather_dot(y, pos2, g), M * D * 2 + N * D * 2 + 8 * M)):
-            t = _time_ms(fn, a.steps, a.warmup)
-            res[name] = dict(ms=round(t, 4), GBs=round(nbytes / (t * 1e-3) / 1e9, 1))
+            t, tr = both(fn, a.steps, a.warmup)
+            res[name] = dict(ms=round(t, 4), GBs=round(nbytes / (t * 1e-3) / 1e9, 1), ref_ms=round(tr, 4),
+                             ref_GBs=round(nbytes / (tr * 1e-3) / 1e9, 1), speedup=round(tr / t, 2))
         mp.CFG["num_experts"] = E
         try:
             xg = x.clone().requires_grad_(True)
             wg = w.clone().requires_grad_(True)
             gf = g.float()
 
-            def block():
+            def block(use):
                 xg.grad = None
                 wg.grad = None
-                o = mp.moe_block(xg, flat, wg, lambda r: r, use_kernels=True)
+                o = mp.moe_block(xg, flat, wg, lambda r: r, use_kernels=use)
                 (o * gf).sum().backward()
 
-            t = _time_ms(block, max(5, a.steps // 4), max(2, a.warmup // 4))
+            bs, bw = max(5, a.steps // 4), max(2, a.warmup // 4)
+            t = _time_ms(lambda: block(True), bs, bw)
+            tr = _time_ms(lambda: block(False), bs, bw)
         finally:
             mp.CFG["num_experts"] = None
         model = (2 * M * D * 2 + 4 * M) + (M * D * 2 + N * D * 4 + 8 * N * k) + (2 * M * D * 2 + 8 * M) \
             + (M * D * 2 + N * D * 2 + 4 * N * k) + (M * D * 2 + N * D * 2 + 4 * N * k)
-        res["block_fwd_bwd"] = dict(ms=round(t, 4), GBs=round(model / (t * 1e-3) / 1e9, 1),
+        res["block_fwd_bwd"] = dict(ms=round(t, 4), GBs=round(model / (t * 1e-3) / 1e9, 1), ref_ms=round(tr, 4),
+                                    speedup=round(tr / t, 2),
                                     note="sort + dispatch + combine fwd, fused combine bwd + dispatch bwd, torch glue "
-                                         "(the loss reduction) included")
+                                         "(the loss reduction) included; the reference column is "
+                                         "moe_block(use_kernels=False): ref_dispatch / ref_combine under torch autograd "
+                                         "(colab/tpu_permute_bench.py:96-104)")
         out[f"k={k}"] = res
     k6 = out["k=6"]["gather_rows"]["GBs"]
     print(json.dumps({
@@ -871,6 +1001,8 @@ def main():
                     "--kernel-trace output directory of this bench (with --pmc-fetch/--pmc-write and "
                     "--copy-fetch/--copy-write counter directories for traffic) and exit")
     ap.add_argument("--stats-summary", metavar="DIR", help="print the kernel table of a rocprofv3 --stats run and exit")
+    ap.add_argument("--kernel-traffic", action="store_true", help="print per-kernel HBM bytes per launch from the "
+                    "--pmc-fetch / --pmc-write counter runs (calibrated by --copy-fetch / --copy-write) and exit")
     ap.add_argument("--pmc-fetch", metavar="DIR")
     ap.add_argument("--pmc-write", metavar="DIR")
     ap.add_argument("--copy-fetch", metavar="DIR")
@@ -890,6 +1022,9 @@ def main():
 
     if a.stats_summary:
         stats_summary(a.stats_summary)
+        return
+    if a.kernel_traffic:
+        kernel_traffic(a)
         return
     if a.profile_summary:
         profile_summary(a)

@@ -218,8 +218,10 @@ typedef struct {
   float* dweights; /* [t, k] f32 gradient of the routing weights (may be NULL) */
 } lsurge_moe_grads;
 
-/* Bytes of the `saved` buffer the forward fills and the backward reads (activations + layout). */
+/* Bytes of the `saved` buffer the forward fills and the backward reads (activations + layout).  The FP8 forward
+ * also keeps its E4M3 x and h there and needs lsurge_moe_saved_bytes_fp8 (the bf16 layout is a prefix of it). */
 size_t lsurge_moe_saved_bytes(const lsurge_moe_shape* s);
+size_t lsurge_moe_saved_bytes_fp8(const lsurge_moe_shape* s);
 /* Scratch bytes for forward and backward (not kept between calls). */
 size_t lsurge_moe_fwd_workspace_bytes(const lsurge_moe_shape* s);
 size_t lsurge_moe_bwd_workspace_bytes(const lsurge_moe_shape* s);
@@ -305,7 +307,8 @@ int lsurge_moe_fp8_quantize_weights(const lsurge_moe_shape* s, const lsurge_moe_
                                     lsurge_stream_t stream);
 /* lsurge_moe_fwd with every expert GEMM in FP8: x is quantised per tensor, h = silu(g) * u (bf16, kept in
  * `saved`) per tensor (routed and shared separately) before the down projections.  Router, layout and
- * combine are those of lsurge_moe_fwd.  `saved` has the same layout, so lsurge_moe_bwd (bf16) runs on it. */
+ * combine are those of lsurge_moe_fwd.  `saved` (lsurge_moe_saved_bytes_fp8 bytes) starts with the bf16
+ * layout, so lsurge_moe_bwd (bf16) runs on it too. */
 size_t lsurge_moe_fwd_fp8_workspace_bytes(const lsurge_moe_shape* s);
 int lsurge_moe_fwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* wq, size_t wq_bytes,
                        void* out, void* saved, size_t saved_bytes, void* workspace, size_t workspace_bytes,

@@ -72,6 +72,7 @@ _SIGS = {
     "lsurge_ragged_dot_bwd": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _int, _p, _p, _p, _sz, _p]),
     "lsurge_ragged_dot_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "lsurge_moe_saved_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
+    "lsurge_moe_saved_bytes_fp8": (_sz, [ctypes.POINTER(MoeShape)]),
     "lsurge_moe_fwd_workspace_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
     "lsurge_moe_bwd_workspace_bytes": (_sz, [ctypes.POINTER(MoeShape)]),
     "lsurge_moe_fwd": (_int, [ctypes.POINTER(MoeShape), ctypes.POINTER(MoeParams), _p, _p, _sz, _p, _sz, _p]),

@@ -50,7 +50,9 @@ const char* g_names[KID_COUNT] = {
     "gemm_down_wgrad",  "gemm_gu_dgrad",     "gemm_gu_wgrad",     "dispatch_bwd",     "router_wgrad",
     "shared_gu_fwd",    "shared_down_fwd",   "shared_down_dgrad", "shared_down_wgrad", "shared_gu_dgrad",
     "shared_gu_wgrad",  "splitk_reduce",     "misc",             "router_select",
-    "fp8_quantize"};
+    "fp8_quantize",     "gdn_chunk",         "gdn_scan",          "gdn_bscan",        "gdn_bgrad",
+    "gdn_bchunk"};
+static_assert(KID_COUNT <= 31, "lsurge_prof_enable takes the kernel ids as bits of an int");
 constexpr size_t kPool = 8192;
 }  // namespace
 

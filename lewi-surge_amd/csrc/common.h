@@ -148,6 +148,11 @@ enum {
   KID_MISC,
   KID_ROUTER_SELECT,
   KID_FP8_QUANT,
+  KID_GDN_CHUNK,
+  KID_GDN_SCAN,
+  KID_GDN_BSCAN,
+  KID_GDN_BGRAD,
+  KID_GDN_BCHUNK,
   KID_COUNT
 };
 

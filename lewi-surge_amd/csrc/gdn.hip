@@ -1396,11 +1396,11 @@ int lsurge_gdn_chunked_fwd(const void* q, const void* k, const void* v, const fl
   float* attn = (float*)(w + chunks * GC * GD);
   float* gcum = attn + chunks * GC * GC;
   const float qscale = round_bf16_host(1.f / sqrtf((float)GD));  // the scale in the compute dtype (gdn_fast.py:56)
-  LSURGE_LAUNCH(KID_MISC, s,
+  LSURGE_LAUNCH(KID_GDN_CHUNK, s,
                 hipLaunchKernelGGL(gdn_chunk_kernel, dim3((unsigned)N, (unsigned)h, (unsigned)b), dim3(GTH), 0, s,
                                    (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)v, g, (const bf16_t*)beta, (int)t,
                                    (int)h, qscale, u, w, attn, gcum));
-  LSURGE_LAUNCH(KID_MISC, s,
+  LSURGE_LAUNCH(KID_GDN_SCAN, s,
                 hipLaunchKernelGGL(gdn_scan_kernel, dim3(GD / SB, (unsigned)h, (unsigned)b), dim3(GTH), 0, s,
                                    (const bf16_t*)q, (const bf16_t*)k, (const bf16_t*)u, (const bf16_t*)w,
                                    (const float*)attn, (const float*)gcum, (int)t, (int)h, (int)N, qscale, h0,
@@ -1479,16 +1479,16 @@ static int gdn_bwd_from_ws(const void* q, const void* k, const void* v, const vo
   const int64_t N = gdn_chunks(t);
   const float qscale = round_bf16_host(1.f / sqrtf((float)GD));
   const dim3 chunk_grid((unsigned)N, (unsigned)h, (unsigned)b), scan_grid(GD / SB, (unsigned)h, (unsigned)b);
-  LSURGE_LAUNCH(KID_MISC, s,
+  LSURGE_LAUNCH(KID_GDN_BSCAN, s,
                 hipLaunchKernelGGL(gdn_bscan_kernel, scan_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
                                    (const bf16_t*)p.w, (const float*)p.attn, (const float*)p.gcum, (const bf16_t*)dout,
                                    (int)t, (int)h, (int)N, qscale, dh_final, p.dhs, dh0));
-  LSURGE_LAUNCH(KID_MISC, s,
+  LSURGE_LAUNCH(KID_GDN_BGRAD, s,
                 hipLaunchKernelGGL(gdn_bgrad_kernel, chunk_grid, dim3(GTH), 0, s, (const bf16_t*)k,
                                    (const bf16_t*)p.u, (const bf16_t*)p.w, (const float*)p.attn, (const float*)p.gcum,
                                    (const bf16_t*)dout, (const float*)p.hs, (const float*)p.dhs, (int)t, (int)h, p.dqg,
                                    p.dkd, p.du, p.dw, p.dP, p.dgl));
-  LSURGE_LAUNCH(KID_MISC, s,
+  LSURGE_LAUNCH(KID_GDN_BCHUNK, s,
                 hipLaunchKernelGGL(gdn_bchunk_kernel, chunk_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
                                    (const bf16_t*)v, (const bf16_t*)beta, (const float*)p.attn, (const float*)p.gcum,
                                    (const float*)p.S, (const float*)p.A, (const float*)p.dqg, (const float*)p.dkd,
@@ -1504,11 +1504,11 @@ static int gdn_fwd_to_ws(const void* q, const void* k, const void* v, const floa
   const int64_t N = gdn_chunks(t);
   const float qscale = round_bf16_host(1.f / sqrtf((float)GD));
   const dim3 chunk_grid((unsigned)N, (unsigned)h, (unsigned)b), scan_grid(GD / SB, (unsigned)h, (unsigned)b);
-  LSURGE_LAUNCH(KID_MISC, s,
+  LSURGE_LAUNCH(KID_GDN_CHUNK, s,
                 hipLaunchKernelGGL(gdn_chunk_kernel, chunk_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
                                    (const bf16_t*)v, g, (const bf16_t*)beta, (int)t, (int)h, qscale, p.u, p.w, p.attn,
                                    p.gcum, p.S, p.A));
-  LSURGE_LAUNCH(KID_MISC, s,
+  LSURGE_LAUNCH(KID_GDN_SCAN, s,
                 hipLaunchKernelGGL(gdn_scan_kernel, scan_grid, dim3(GTH), 0, s, (const bf16_t*)q, (const bf16_t*)k,
                                    (const bf16_t*)p.u, (const bf16_t*)p.w, (const float*)p.attn, (const float*)p.gcum,
                                    (int)t, (int)h, (int)N, qscale, h0, (bf16_t*)o, h_out, p.hs));

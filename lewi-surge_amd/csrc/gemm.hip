@@ -75,10 +75,49 @@ static int launch_splitk_reduce(const float* part, int S, int E, int64_t I, int6
 // so a bad group_sizes array can never send the GEMMs outside lhs/out.
 // ragged_groups_kernel (one workgroup): clamped group starts and sizes and the exclusive scan of their tr-row
 // block counts (tr = 128, or 256 for the ping-pong kernel's tiles), 1024 groups per pass with a running carry; then
-// the block table itself: block b belongs to the group e with e_boff[e] <= b < e_boff[e + 1] (binary search; empty
-// groups have e_boff[e] == e_boff[e + 1]), and entries past the count are empty.
+// (fill != 0) the block table itself, see fill_block.  Past kRaggedOneLaunchBlocks table entries the table is filled
+// by ragged_blocks_fill_kernel's grid instead, so that no thread walks more than 32 entries of it.
+constexpr int kRaggedOneLaunchBlocks = 32768;
+
+// block b belongs to the group e with e_boff[e] <= b < e_boff[e + 1] (binary search; empty groups have
+// e_boff[e] == e_boff[e + 1]), and entries past the count nb are empty
+__device__ __forceinline__ void fill_block(int b, int nb, int E, int tr, const int32_t* __restrict__ e_row0,
+                                           const int32_t* __restrict__ e_rows, const int32_t* __restrict__ e_boff,
+                                           int32_t* __restrict__ blk_row0, int32_t* __restrict__ blk_rows,
+                                           int32_t* __restrict__ blk_expert) {
+  if (b >= nb) {
+    blk_row0[b] = 0;
+    blk_rows[b] = 0;
+    blk_expert[b] = -1;
+    return;
+  }
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (e_boff[mid] <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  const int j = b - e_boff[lo];
+  blk_row0[b] = e_row0[lo] + j * tr;
+  blk_rows[b] = min(tr, e_rows[lo] - j * tr);
+  blk_expert[b] = lo;
+}
+
+__global__ __launch_bounds__(256) void ragged_blocks_fill_kernel(int E, int tr, int max_blocks,
+                                                                 const int32_t* __restrict__ e_row0,
+                                                                 const int32_t* __restrict__ e_rows,
+                                                                 const int32_t* __restrict__ e_boff,
+                                                                 const int32_t* __restrict__ num_blocks,
+                                                                 int32_t* __restrict__ blk_row0,
+                                                                 int32_t* __restrict__ blk_rows,
+                                                                 int32_t* __restrict__ blk_expert) {
+  const int nb = num_blocks[0];
+  for (int b = blockIdx.x * 256 + threadIdx.x; b < max_blocks; b += gridDim.x * 256)
+    fill_block(b, nb, E, tr, e_row0, e_rows, e_boff, blk_row0, blk_rows, blk_expert);
+}
+
 __global__ __launch_bounds__(1024) void ragged_groups_kernel(const int32_t* __restrict__ gs, int E, int64_t m, int tr,
-                                                            int max_blocks, int32_t* __restrict__ e_row0,
+                                                            int fill, int max_blocks, int32_t* __restrict__ e_row0,
                                                             int32_t* __restrict__ e_rows, int32_t* __restrict__ e_boff,
                                                             int32_t* __restrict__ num_blocks,
                                                             int32_t* __restrict__ total_rows,
@@ -137,26 +176,11 @@ __global__ __launch_bounds__(1024) void ragged_groups_kernel(const int32_t* __re
     num_blocks[0] = min(carry_blk, max_blocks);
     total_rows[0] = (int32_t)min(carry_rows, m);
   }
+  if (!fill) return;
   __syncthreads();  // the workgroup's e_row0, e_rows and e_boff writes are visible to all its threads
   const int nb = min(carry_blk, max_blocks);
-  for (int b = tid; b < max_blocks; b += 1024) {
-    if (b >= nb) {
-      blk_row0[b] = 0;
-      blk_rows[b] = 0;
-      blk_expert[b] = -1;
-      continue;
-    }
-    int lo = 0, hi = E - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (e_boff[mid] <= b) lo = mid;
-      else hi = mid - 1;
-    }
-    const int j = b - e_boff[lo];
-    blk_row0[b] = e_row0[lo] + j * tr;
-    blk_rows[b] = min(tr, e_rows[lo] - j * tr);
-    blk_expert[b] = lo;
-  }
+  for (int b = tid; b < max_blocks; b += 1024)
+    fill_block(b, nb, E, tr, e_row0, e_rows, e_boff, blk_row0, blk_rows, blk_expert);
 }
 
 // zero the rows [from[0], m) of an [m, n] matrix with esize-byte elements (rows past the groups)
@@ -785,9 +809,15 @@ static int ragged_setup(const int32_t* gs, int64_t m, int64_t e, void* ws, size_
   *e_row0 = nb + 4;
   *e_rows = nb + 4 + e;
   int32_t* e_boff = nb + 4 + 2 * e;
+  const bool one = mb <= kRaggedOneLaunchBlocks;
   LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(ragged_groups_kernel, dim3(1), dim3(1024), 0, s, gs, (int)e, m, tr, (int)mb, *e_row0,
-                                   *e_rows, e_boff, nb, *total_rows, blk_row0, blk_rows, blk_expert));
+                hipLaunchKernelGGL(ragged_groups_kernel, dim3(1), dim3(1024), 0, s, gs, (int)e, m, tr, (int)one,
+                                   (int)mb, *e_row0, *e_rows, e_boff, nb, *total_rows, blk_row0, blk_rows, blk_expert));
+  if (!one)
+    LSURGE_LAUNCH(KID_MISC, s,
+                  hipLaunchKernelGGL(ragged_blocks_fill_kernel, dim3((unsigned)std::min<int64_t>((mb + 255) / 256, 4096)),
+                                     dim3(256), 0, s, (int)e, tr, (int)mb, *e_row0, *e_rows, e_boff, nb, blk_row0,
+                                     blk_rows, blk_expert));
   g->blk_expert = blk_expert;
   g->blk_rows = blk_rows;
   g->blk_row0 = blk_row0;

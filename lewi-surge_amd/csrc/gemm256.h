@@ -17,7 +17,8 @@
 //  - Persistent tiles.  The grid is one workgroup per CU (256); workgroup l of XCD x walks the tiles
 //    xbeg + l, xbeg + l + nper, ... of that XCD's contiguous share of the tiles (so neighbouring tiles of one expert
 //    share an XCD's L2).  The load stream runs across tile boundaries: the next tile's first stages are loaded while
-//    the current tile's last stages compute, and its first stage is already in LDS when the epilogue runs.
+//    the current tile's last stages compute; its first two stages are in LDS and its third in registers before the
+//    epilogue's stores are issued.
 //  - Epilogue through a wave-private 8 KiB LDS area beside the ring (32 rows of the wave's block at a time), so every
 //    global store (and the SwiGLU backward's loads of g and u) covers whole 128- or 256-byte row segments; the copy
 //    ring is untouched, and the next tile's loads stay in flight.
@@ -76,8 +77,9 @@ __device__ __forceinline__ Tile row_tile(const RowsArgs& a, int b) {
 // 0..2, moves copies [16 s / 3, 16 (s + 1) / 3) of stage lk from registers to the other half, each followed by the
 // load of the same chunk of the stage after.  The issue order is pinned: the NR fragment reads first, then the
 // write / load pairs, spread evenly over the step's 16 MFMAs.
+// COPY = false: no copies in this stage (the fragment reads and MFMAs only).
 //   fread(F&, buf, step)   swrite(c, buf)   gload(c, lk)   mma(const F&)
-template <int NR, class F, class Fread, class Swrite, class Gload, class Mma>
+template <int NR, bool COPY = true, class F, class Fread, class Swrite, class Gload, class Mma>
 __device__ __forceinline__ void run_stage(F& f0, F& f1, int cur, int lk, Fread&& fread, Swrite&& swrite, Gload&& gload,
                                           Mma&& mma) {
   const int nxt = cur ^ 1;
@@ -92,7 +94,7 @@ __device__ __forceinline__ void run_stage(F& f0, F& f1, int cur, int lk, Fread&&
     } else {
       fread(fn, cur, s + 1);
     }
-    const int lo = s < 3 ? 16 * s / 3 : 0, hi = s < 3 ? 16 * (s + 1) / 3 : 0;
+    const int lo = COPY && s < 3 ? 16 * s / 3 : 0, hi = COPY && s < 3 ? 16 * (s + 1) / 3 : 0;
 #pragma unroll
     for (int c = lo; c < hi; ++c) {
       swrite(c, nxt);
@@ -150,8 +152,8 @@ void rows_kernel(RowsArgs a) {
   const int nr = tid >> 4, nc = tid & 15;
   const uint32_t nm_w = (uint32_t)(nr * 256 + ((nc ^ ((nr & 3) << 2)) << 4));
 
-  // ---- load cursor: tile lt (the stage to load comes with each call); its descriptors and per-lane offsets
-  int lt = t_cur;
+  // ---- load cursor: stage lk of tile lt; its descriptors and per-lane offsets
+  int lt = t_cur, lk = 0;
   rsrc_t la, lb, lb2;
   const int a_kc = 8 * kc;  // k of this lane's K-major chunk within a stage
   // K-major copies (contiguous A rows, B_NK): row 32 i + kr of the operand at a byte offset of km_base + 32 i ld
@@ -278,13 +280,35 @@ void rows_kernel(RowsArgs a) {
       for (int j = 0; j < 4; ++j) acc[i][j] = mfma32<ET>(f.w[j], f.x[i], acc[i][j]);
   };
 
-  // ---- prologue: stage 0 -> LDS half 0, stage 1 -> registers
+  // the cursor's next stage (past the last of a tile: the next tile's first)
+  auto adv = [&]() {
+    if (++lk == nk) {
+      lk = 0;
+      lt += nper;
+      if (lt < xend) set_ld();
+    }
+  };
+
+  // The SwiGLU forward (three outputs per tile) moves the next tile's stage 1 into LDS before its epilogue (EARLY,
+  // see the tile loop); the other epilogues keep stage 1 in registers, which leaves them more registers.
+  constexpr bool EARLY = EPI == EPI_SWIGLU_FWD;
+
+  // ---- prologue: stage 0 -> LDS half 0, stage 1 -> registers (EARLY: -> half 1, and stage 2 -> registers)
 #pragma unroll
-  for (int c = 0; c < 16; ++c) gload(c, 0);
+  for (int c = 0; c < 16; ++c) gload(c, lk);
+  adv();
 #pragma unroll
   for (int c = 0; c < 16; ++c) swrite(c, 0);
 #pragma unroll
-  for (int c = 0; c < 16; ++c) gload(c, 1);
+  for (int c = 0; c < 16; ++c) gload(c, lk);
+  adv();
+  if constexpr (EARLY) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) swrite(c, 1);
+#pragma unroll
+    for (int c = 0; c < 16; ++c) gload(c, lk);
+    adv();
+  }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   F f0, f1;
   fread(f0, 0, 0);
@@ -298,6 +322,11 @@ void rows_kernel(RowsArgs a) {
   char* const stg = smem + RING_BYTES + wave * STG_BYTES;
   auto st16 = [&](rsrc_t r, uint32_t off, u32x4 v) { __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0); };
   auto epilogue = [&]() {
+    // the lane index, opaque to the compiler here: the per-lane row offsets below are then formed inside each
+    // epilogue, instead of being hoisted out of the tile loop and held (or spilled) across every K loop
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    const int efr = el & 31, efh = el >> 5;
     const int b = t_cur / a.n_tiles, nt = t_cur % a.n_tiles;
     const Tile rt = row_tile(a, b);
     const int64_t n0 = (int64_t)nt * NOUT;
@@ -318,15 +347,15 @@ void rows_kernel(RowsArgs a) {
         for (int j = 0; j < 2; ++j) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int ch = 2 * q + fh;
-            *reinterpret_cast<f32x4*>(stg + fr * 256 + ((ch ^ (fr & 15)) << 4)) =
+            const int ch = 2 * q + efh;
+            *reinterpret_cast<f32x4*>(stg + efr * 256 + ((ch ^ (efr & 15)) << 4)) =
                 f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-            *reinterpret_cast<f32x4*>(stg + fr * 256 + (((8 + ch) ^ (fr & 15)) << 4)) =
+            *reinterpret_cast<f32x4*>(stg + efr * 256 + (((8 + ch) ^ (efr & 15)) << 4)) =
                 f32x4{acc[i][j + 2][4 * q], acc[i][j + 2][4 * q + 1], acc[i][j + 2][4 * q + 2], acc[i][j + 2][4 * q + 3]};
           }
 #pragma unroll
           for (int it = 0; it < 2; ++it) {
-            const int r = 16 * it + (lane >> 2), c8 = lane & 3;
+            const int r = 16 * it + (el >> 2), c8 = el & 3;
             float g[8], u[8], h[8];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
@@ -361,8 +390,8 @@ void rows_kernel(RowsArgs a) {
           uint32_t oo[4];
 #pragma unroll
           for (int it = 0; it < 4; ++it) {
-            const int r = 8 * it + (lane >> 3);
-            const int64_t col = n0 + wn * 128 + 64 * jp + 8 * (lane & 7);
+            const int r = 8 * it + (el >> 3);
+            const int64_t col = n0 + wn * 128 + 64 * jp + 8 * (el & 7);
             const uint32_t og = col < N ? (uint32_t)(rbase + r) * ldg_b + (uint32_t)col * 2u : OOB;
             oo[it] = col < N ? (uint32_t)(rbase + r) * ldc_b + (uint32_t)col * 2u : OOB;
             gq[it] = ld16(rG, og);
@@ -372,14 +401,14 @@ void rows_kernel(RowsArgs a) {
           for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              const int ch = 8 * jj + 2 * q + fh;
-              *reinterpret_cast<f32x4*>(stg + fr * 256 + ((ch ^ (fr & 15)) << 4)) =
+              const int ch = 8 * jj + 2 * q + efh;
+              *reinterpret_cast<f32x4*>(stg + efr * 256 + ((ch ^ (efr & 15)) << 4)) =
                   f32x4{acc[i][2 * jp + jj][4 * q], acc[i][2 * jp + jj][4 * q + 1], acc[i][2 * jp + jj][4 * q + 2],
                         acc[i][2 * jp + jj][4 * q + 3]};
             }
 #pragma unroll
           for (int it = 0; it < 4; ++it) {
-            const int r = 8 * it + (lane >> 3), c8 = lane & 7;
+            const int r = 8 * it + (el >> 3), c8 = el & 7;
             float v[8], dg[8], du[8];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
@@ -419,11 +448,11 @@ void rows_kernel(RowsArgs a) {
               w0 = pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
               w1 = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
             }
-            *reinterpret_cast<u32x2*>(stg + fr * 256 + (((4 * j + q) ^ (fr & 15)) << 4) + 8 * fh) = u32x2{w0, w1};
+            *reinterpret_cast<u32x2*>(stg + efr * 256 + (((4 * j + q) ^ (efr & 15)) << 4) + 8 * efh) = u32x2{w0, w1};
           }
 #pragma unroll
         for (int it = 0; it < 8; ++it) {
-          const int r = 4 * it + (lane >> 4), c = lane & 15;
+          const int r = 4 * it + (el >> 4), c = el & 15;
           const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
           const int64_t col = n0 + wn * 128 + 8 * c;
           st16(rC, col < N ? (uint32_t)(rbase + r) * ldc_b + (uint32_t)col * 2u : OOB, v);
@@ -436,14 +465,14 @@ void rows_kernel(RowsArgs a) {
           for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              const int ch = 8 * jj + 2 * q + fh;  // 16-byte chunk of 4 f32 columns
-              *reinterpret_cast<f32x4*>(stg + fr * 256 + ((ch ^ (fr & 15)) << 4)) =
+              const int ch = 8 * jj + 2 * q + efh;  // 16-byte chunk of 4 f32 columns
+              *reinterpret_cast<f32x4*>(stg + efr * 256 + ((ch ^ (efr & 15)) << 4)) =
                   f32x4{acc[i][2 * jp + jj][4 * q], acc[i][2 * jp + jj][4 * q + 1], acc[i][2 * jp + jj][4 * q + 2],
                         acc[i][2 * jp + jj][4 * q + 3]};
             }
 #pragma unroll
           for (int it = 0; it < 8; ++it) {
-            const int r = 4 * it + (lane >> 4), c = lane & 15;
+            const int r = 4 * it + (el >> 4), c = el & 15;
             const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((c ^ (r & 15)) << 4));
             const int64_t col = n0 + wn * 128 + 64 * jp + 4 * c;
             st16(rC, col < N ? (uint32_t)(rbase + r) * ldc_b + (uint32_t)col * 4u : OOB, v);
@@ -455,17 +484,40 @@ void rows_kernel(RowsArgs a) {
     }
   };
 
-  // stage kt loads stage kt + 2: within a tile's last pair of stages, the first two of the next tile
+  // Stage k writes stage k + 1 from the registers to LDS and loads stage k + 2 (past the tile's end: the next tile's
+  // stages 0 and 1).
+  // EARLY: a tile starts with stage 0 in LDS half 0, stage 1 in half 1 and stage 2 in registers, and its stage 0
+  // copies nothing.  Between the last stage and the epilogue the next tile's stage 1 goes to LDS (the half the last
+  // stage has just released) and its stage 2 is loaded, so every load the next tile's first two stages wait for was
+  // issued before the epilogue's stores.  The tile's output write (all workgroups finish their tiles at about the
+  // same time, so it is an HBM-bound burst) then drains while the next tile computes, instead of holding its LDS
+  // writes, which wait for the vector memory count in issue order.  Measured on the gate/up forward (three outputs
+  // per tile): 5% faster; on the plain-store and SwiGLU-backward epilogues no gain, and the plain store then spills.
+  constexpr int NR = BMODE == B_NK ? 8 : 12;  // LDS reads per MFMA step (transpose reads take two per fragment)
   while (true) {
-    for (int kt = 0; kt < nk; kt += 2) {
-      if (kt + 2 == nk) {  // the last pair loads the next tile's first two stages
-        lt += nper;
-        if (lt < xend) set_ld();
+    if constexpr (EARLY) {
+      run_stage<NR, false>(f0, f1, 0, lk, fread, swrite, gload, mma);
+      run_stage<NR>(f0, f1, 1, lk, fread, swrite, gload, mma);
+      adv();
+      for (int kt = 2; kt < nk; kt += 2) {
+        run_stage<NR>(f0, f1, 0, lk, fread, swrite, gload, mma);
+        adv();
+        run_stage<NR>(f0, f1, 1, lk, fread, swrite, gload, mma);
+        adv();
       }
-      const int lk = kt + 2 == nk ? 0 : kt + 2;
-      constexpr int NR = BMODE == B_NK ? 8 : 12;  // LDS reads per MFMA step (transpose reads take two per fragment)
-      run_stage<NR>(f0, f1, 0, lk, fread, swrite, gload, mma);
-      run_stage<NR>(f0, f1, 1, lk + 1, fread, swrite, gload, mma);
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        swrite(c, 1);
+        gload(c, lk);
+      }
+      adv();
+    } else {
+      for (int kt = 0; kt < nk; kt += 2) {
+        run_stage<NR>(f0, f1, 0, lk, fread, swrite, gload, mma);
+        adv();
+        run_stage<NR>(f0, f1, 1, lk, fread, swrite, gload, mma);
+        adv();
+      }
     }
     epilogue();
     t_cur += nper;

@@ -72,12 +72,13 @@ struct Saved {
   bf16_t *g, *u, *h, *y_pad;
   bf16_t *sg, *su, *sh, *sy;  // shared expert run on its own: gate, up, h, output
   // FP8 forward: x [T, d], routed h [P, f] (padded rows) and shared h [T, fs] in E4M3, and their scale_inv, the
-  // operands the FP8 backward's weight gradients read again
+  // operands the FP8 backward's weight gradients read again.  Carved after the bf16 layout and only for the FP8
+  // path (null otherwise), so a bf16 buffer is a prefix of an FP8 one.
   uint8_t *xq, *hq, *shq;
   float* f8_sinv;
 };
 
-size_t carve_saved(const Dims& q, void* base, Saved* sv) {
+size_t carve_saved(const Dims& q, void* base, Saved* sv, bool fp8) {
   Carve c(base);
   sv->logits = c.take<float>(q.T * q.E);
   sv->sel = c.take<int32_t>(q.M);
@@ -105,10 +106,15 @@ size_t carve_saved(const Dims& q, void* base, Saved* sv) {
   sv->su = c.take<bf16_t>(own * q.fs);
   sv->sh = c.take<bf16_t>(own * q.fs);
   sv->sy = c.take<bf16_t>(own * q.d);
-  sv->xq = c.take<uint8_t>(q.T * q.d);
-  sv->hq = c.take<uint8_t>(q.P * q.f);
-  sv->shq = c.take<uint8_t>(q.T * q.fs);
-  sv->f8_sinv = c.take<float>(4);
+  if (fp8) {
+    sv->xq = c.take<uint8_t>(q.T * q.d);
+    sv->hq = c.take<uint8_t>(q.P * q.f);
+    sv->shq = c.take<uint8_t>(q.T * q.fs);
+    sv->f8_sinv = c.take<float>(4);
+  } else {
+    sv->xq = sv->hq = sv->shq = nullptr;
+    sv->f8_sinv = nullptr;
+  }
   return c.off + 256;
 }
 
@@ -277,7 +283,13 @@ extern "C" {
 size_t lsurge_moe_saved_bytes(const lsurge_moe_shape* s) {
   if (check_shape(s)) return 0;
   Saved sv;
-  return carve_saved(dims_of(s), nullptr, &sv);
+  return carve_saved(dims_of(s), nullptr, &sv, false);
+}
+
+size_t lsurge_moe_saved_bytes_fp8(const lsurge_moe_shape* s) {
+  if (check_shape(s)) return 0;
+  Saved sv;
+  return carve_saved(dims_of(s), nullptr, &sv, true);
 }
 
 size_t lsurge_moe_fwd_workspace_bytes(const lsurge_moe_shape* s) {
@@ -386,7 +398,7 @@ int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_s
   if (int rc = check_shape(s)) return rc;
   LSURGE_REQUIRE(saved && v, "moe_saved_layout: null pointer");
   Saved sv;
-  carve_saved(dims_of(s), saved, &sv);
+  carve_saved(dims_of(s), saved, &sv, false);
   v->logits = sv.logits; v->sel = sv.sel; v->weights = sv.weights; v->group_sizes = sv.gs; v->offsets = sv.offsets;
   v->block_off = sv.block_off; v->order = sv.order; v->pos = sv.pos; v->slot = sv.slot; v->row_src = sv.row_src;
   v->blk_expert = sv.blk_expert; v->blk_rows = sv.blk_rows; v->num_blocks = sv.num_blocks;
@@ -412,9 +424,10 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   LSURGE_REQUIRE(!s->fs || (p->ws_gate && p->ws_up && p->ws_down), "moe_fwd: shared expert weights missing");
   const Dims q = dims_of(s);
   Saved sv;
-  const size_t need = carve_saved(q, nullptr, &sv);
-  LSURGE_REQUIRE(saved_bytes >= need, "moe_fwd: saved buffer %zu < %zu bytes", saved_bytes, need);
-  carve_saved(q, saved, &sv);
+  const size_t need = carve_saved(q, nullptr, &sv, w8 != nullptr);
+  LSURGE_REQUIRE(saved_bytes >= need, "moe_fwd: saved buffer %zu < %zu bytes%s", saved_bytes, need,
+                 w8 ? " (lsurge_moe_saved_bytes_fp8)" : "");
+  carve_saved(q, saved, &sv, w8 != nullptr);
   hipStream_t st = (hipStream_t)stream;
   ForkGuard fg;
   if (int rc = fg.acquire(st)) return rc;
@@ -574,7 +587,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                  "moe_bwd: shared expert pointers missing");
   const Dims q = dims_of(s);
   Saved sv;
-  carve_saved(q, (void*)saved, &sv);
+  carve_saved(q, (void*)saved, &sv, false);
   BwdWs w;
   const size_t need = carve_bwd(q, nullptr, &w);
   LSURGE_REQUIRE(workspace && workspace_bytes >= need, "moe_bwd: workspace %zu < %zu bytes", workspace_bytes, need);
@@ -620,6 +633,14 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                     q.d, 2 * q.fs, g->dws_gate, g->dws_up, q.fs, q.fs, 0, S, w.part, w.part_bytes, s0))
       return rc;
   }
+  // main, before any GEMM: W_r^T for the router's dx term and the chunk table of the weight gradients (read by both
+  // routed weight gradients).  Both are one-workgroup-class kernels: issued on a helper stream beside the persistent
+  // GEMMs (one workgroup per CU, the whole LDS and register file) they wait for a whole GEMM to drain first.
+  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, st)) return rc;
+  lsurge::WgradChunks chunks;
+  if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, st,
+                                         q.merged ? q.T : -1, q.P))
+    return rc;
   // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel) and their
   // dense bf16 rows for the router's weight gradient; a merged
   // shared expert's rows of dY_pad get dY itself
@@ -634,13 +655,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
         (q.merged && hipStreamWaitEvent(s0, ev[2], 0) != hipSuccess))
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_bwd: fork events failed");
   }
-  // s1: W_r^T for the router's dx term, the chunk table of the weight gradients (read by both), then down wgrad
-  // dW_down[e] = h_e^T dY_e
-  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, s1)) return rc;
-  lsurge::WgradChunks chunks;
-  if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, s1,
-                                         q.merged ? q.T : -1, q.P))
-    return rc;
+  // s1: down wgrad dW_down[e] = h_e^T dY_e
   if (int rc = lsurge::gemm_wgrad_chunked(KID_GEMM_DOWN_WGRAD, chunks, (int)q.E, q.T, sv.h, q.f, w.dy_pad, q.d, q.f,
                                           q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, w.part_dn, w.part_dn_bytes, s1,
                                           lsurge::RowGather(), odn))
@@ -718,7 +733,7 @@ int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
                  carve_fp8w(q, nullptr, &w8));
   carve_fp8w(q, (void*)wq, &w8);
   Saved sv;
-  carve_saved(q, (void*)saved, &sv);
+  carve_saved(q, (void*)saved, &sv, true);
   BwdWs w;
   Fp8Bws f8;
   const size_t wb = (carve_bwd(q, nullptr, &w) + 255) / 256 * 256;

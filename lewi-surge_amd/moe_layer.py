@@ -113,7 +113,7 @@ class MoELayer:
 
     def forward_fp8(self, p: dict, out=None):
         """forward() with the expert GEMMs in FP8 on the weights of the last quantize_weights_fp8(); the saved
-        activations have the same layout, so backward() (bf16) or backward_fp8() runs after it."""
+        activations start with the bf16 layout, so backward() (bf16) or backward_fp8() runs after it."""
         s = self.shape
         _check_params(s, p)
         if getattr(self, "wq", None) is None:
@@ -121,6 +121,10 @@ class MoELayer:
         lib = L.lib()
         if getattr(self, "_fwd8_ws", None) is None:
             self._fwd8_ws = L.workspace(lib.lsurge_moe_fwd_fp8_workspace_bytes(ctypes.byref(self._cs)), self.device)
+            # the FP8 forward also keeps its E4M3 x and h in `saved`, after the bf16 layout
+            n8 = lib.lsurge_moe_saved_bytes_fp8(ctypes.byref(self._cs))
+            if n8 > self.saved.numel():
+                self.saved = torch.empty(n8, dtype=torch.uint8, device=self.device)
         out = self.out if out is None else out
         ps = _params_struct(p)
         L.check(lib.lsurge_moe_fwd_fp8(ctypes.byref(self._cs), ctypes.byref(ps), L.ptr(self.wq), self.wq.numel(),

@@ -57,8 +57,14 @@ def test_sizes():
     assert saved >= p_rows * (1024 + 3 * 512) * 2
     assert saved < p_rows * (2 * 1024 + 3 * 512) * 2
     assert lib.lsurge_moe_bwd_workspace_bytes(ctypes.byref(s)) > 0
+    # the FP8 forward adds its E4M3 x [T, d], routed h [P, f] and shared h [T, fs] (and 4 scales) after the bf16
+    # layout; the bf16 size does not pay for them
+    saved8 = lib.lsurge_moe_saved_bytes_fp8(ctypes.byref(s))
+    fp8_tail = 16384 * 1024 + p_rows * 512 + 16384 * 512 + 16  # xq, hq over the routed padded rows, shq, scales
+    assert fp8_tail <= saved8 - saved < fp8_tail + 4 * 256
     bad = L.MoeShape(16, 100, 64, 6, 512, 512)  # d not a multiple of 64
     assert lib.lsurge_moe_saved_bytes(ctypes.byref(bad)) == 0
+    assert lib.lsurge_moe_saved_bytes_fp8(ctypes.byref(bad)) == 0
 
 
 def test_fp8_backward_argument_errors_without_gpu():

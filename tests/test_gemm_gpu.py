@@ -225,3 +225,20 @@ def test_ragged_bwd_forward_sized_workspace(dev):
     for dl, dr in outs:
         assert mo.rel_l2(dl, want_l) < TOL and mo.rel_l2(dr, want_r) < TOL
     assert np.array_equal(outs[0][0], outs[1][0])  # dlhs does not depend on the workspace
+
+
+def test_large_table_grid_fill(dev):
+    """m past 2^22 rows: the block table (over 32768 entries) is filled by the grid kernel instead of the group
+    workgroup; forward against the fp64 oracle on every row, and the rows past the groups are zero."""
+    gs = [3 << 20, 7, 0, (1 << 21) + 999, 12345]
+    M, K, N = int(np.sum(gs)) + 300, 16, 8
+    rng = np.random.default_rng(21)
+    a = mo.round_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    b = mo.round_bf16(rng.standard_normal((len(gs), K, N)).astype(np.float32))
+    out = pg.padded_ragged_dot(_bf(a, dev), _bf(b, dev), torch.tensor(gs, dtype=torch.int32, device=dev),
+                               preferred_element_type=torch.float32)
+    got = out.cpu().numpy()
+    S = int(np.sum(gs))
+    assert np.all(got[S:] == 0)
+    want = mo.ragged_dot(a, b, gs)
+    assert mo.rel_l2(got, want) < 5e-3
