@@ -873,6 +873,32 @@ def ragged_bench(a):
         "roofline": {"kernel": "ragged_dot up fwd", "bound": "mfma", "achieved": up, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(up / PEAK_BF16_TFLOPS, 4), "traffic": None}}), flush=True)
 
+def mfma_sustained(iters=2000, reps=3):
+    """The matrix cores' sustained bf16 rate on register-resident operands (lsurge_mfma_rate_probe, no memory traffic):
+    pseudo-random values and zeros, TFLOP/s from HIP events on the probe's stream, best of `reps` after a warm-up
+    launch.  Random operands draw more power than zeros, and the chip's power limit holds them below the datasheet
+    peak: the rate a GEMM on real data can approach."""
+    import torch
+    import _lib as L
+    dev = torch.device("cuda", torch.cuda.current_device())
+    out = torch.empty(L.lib().lsurge_mfma_rate_probe_out_floats(), dtype=torch.float32, device=dev)
+    flops = iters * float(2 ** 33)
+    rates = {}
+    for zero in (0, 1):
+        L.check(L.lib().lsurge_mfma_rate_probe(zero, iters, L.ptr(out), L.stream(dev)), "mfma_rate_probe")
+        best = 0.0
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            L.check(L.lib().lsurge_mfma_rate_probe(zero, iters, L.ptr(out), L.stream(dev)), "mfma_rate_probe")
+            e1.record()
+            e1.synchronize()
+            best = max(best, flops / (e0.elapsed_time(e1) * 1e-3) / 1e12)
+        rates[zero] = best
+    return {"random_bf16": round(rates[0], 1), "zero_operands": round(rates[1], 1), "unit": "TFLOP/s",
+            "kernel": "mfma_rate_kernel (v_mfma_f32_32x32x16_bf16, operands in registers)"}
+
+
 def layer_measure(a, c, steps, warmup):
     """Time `steps` fwd(+bwd) layer steps of config c after `warmup` (helper streams per a.concurrency), with a
     profiled one-stream pass first that finds the dominant kernel; that kernel is bracketed by HIP events on its
@@ -1069,6 +1095,9 @@ def main():
     if a.kernels:
         for n, v in kern.items():
             print(f"  {n:20s} {v}", file=sys.stderr)
+    sus = mfma_sustained()
+    if bound == "mfma":
+        sus["roofline_frac_of_sustained"] = round(achieved / sus["random_bf16"], 4)
 
     res = {
         "metric": (f"MoE-layer {'fwd+bwd' if c['bwd'] else 'fwd'} tokens/sec @1 GPU, FP8 expert GEMMs" if a.fp8 else
@@ -1096,6 +1125,7 @@ def main():
                      "frac": round(achieved / peak, 4), "traffic": measured_traffic(a.config, dom, a.fp8, c["bwd"]),
                      "launch_ms": round(dom_ms, 4)},
         "kernels": kern,
+        "mfma_sustained": sus,
         **({"ms_per_step_cached_weights": round(cached_ms, 4),
             "tokens_s_cached_weights": round(c["T"] / (cached_ms * 1e-3), 1)} if a.fp8 else {}),
         "kernels_note": "per-kernel ms from a profiled pass on one stream (share of that pass's kernel time); "

@@ -418,6 +418,15 @@ const char* lsurge_prof_kernel_name(int id);
 int lsurge_prof_read(int id, double* total_ms, int64_t* launches);
 void lsurge_prof_reset(void);
 
+/* Calibration (no reference counterpart; used by the benchmark): the matrix cores' sustained bf16 rate.  1024
+ * workgroups of 4 waves each issue iters x 64 v_mfma_f32_32x32x16_bf16 (32768 flops each) on register-resident
+ * operands -- pseudo-random bf16 values, or zeros with zero_operands = 1 -- and write one float per lane to out
+ * (lsurge_mfma_rate_probe_out_floats() floats).  Time it with events on the stream: iters x 2^33 flops divided by the
+ * time is the rate the chip sustains on such data (its power limit holds random operands below the
+ * datasheet peak).  iters in [1, 2^20]. */
+size_t lsurge_mfma_rate_probe_out_floats(void);
+int lsurge_mfma_rate_probe(int zero_operands, int iters, float* out, lsurge_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -109,6 +109,8 @@ _SIGS = {
     "lsurge_gdn_chunked_bwd_saved_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "lsurge_gdn_chunked_bwd_saved": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p,
                                             _p, _sz, _p, _sz, _p]),
+    "lsurge_mfma_rate_probe_out_floats": (_sz, []),
+    "lsurge_mfma_rate_probe": (_int, [_int, _int, _p, _p]),
     "lsurge_prof_enable": (_int, [_int]),
     "lsurge_prof_collect": (_int, []),
     "lsurge_prof_kernel_count": (_int, []),

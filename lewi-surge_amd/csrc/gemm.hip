@@ -981,6 +981,77 @@ int lsurge_ragged_dot(const void* lhs, const void* rhs, const int32_t* group_siz
 
 }  // extern "C"
 
+// ------------------------------------------------------------------------ sustained matrix-core rate (calibration)
+// Each wave keeps 8 operand fragments and 16 accumulator blocks (256 registers) resident and issues 64
+// v_mfma_f32_32x32x16_bf16 per iteration, the fragments rotating after every 16 so that consecutive MFMAs see other
+// data.  Nothing touches memory inside the loop, so the rate is what the matrix cores sustain on such operands; the
+// chip's power limit holds it below the datasheet peak for random values.  Operands: pseudo-random bf16 (random sign
+// and 7-bit mantissa, exponents 2^-4 .. 2^3, a lowbias32 hash of the element index) or zeros.  out: one f32 per lane
+// (the accumulators' sum, so the MFMAs are live).
+namespace {
+constexpr int kMfmaRateWG = 1024;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void mfma_rate_kernel(int zero, int iters, float* __restrict__ out) {
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  bf16x8 f[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    u32x4 w;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t h = gid * 32u + (uint32_t)(4 * i + q);
+      h ^= h >> 16; h *= 0x7feb352du; h ^= h >> 15; h *= 0x846ca68bu; h ^= h >> 16;
+      const uint32_t lo = (h & 0x807fu) | ((123u + ((h >> 7) & 7u)) << 7);
+      const uint32_t hi = ((h >> 16) & 0x807fu) | ((123u + ((h >> 23) & 7u)) << 7);
+      w[q] = zero ? 0u : (lo | (hi << 16));
+    }
+    f[i] = lsgemm::as_bf16x8(w);
+  }
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = lsgemm::mfma32(f[4 + j], f[i], acc[i][j]);
+      const bf16x8 t = f[0];
+#pragma unroll
+      for (int i = 0; i < 7; ++i) f[i] = f[i + 1];
+      f[7] = t;
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sum += acc[i][j][e];
+  out[gid] = sum;
+}
+}  // namespace
+
+extern "C" {
+
+size_t lsurge_mfma_rate_probe_out_floats(void) { return (size_t)kMfmaRateWG * 256; }
+
+int lsurge_mfma_rate_probe(int zero_operands, int iters, float* out, lsurge_stream_t stream) {
+  LSURGE_REQUIRE(out && iters >= 1 && iters <= (1 << 20), "mfma_rate_probe: null output or iters=%d not in [1, 2^20]",
+                 iters);
+  hipStream_t s = (hipStream_t)stream;
+  LSURGE_LAUNCH(KID_MISC, s,
+                hipLaunchKernelGGL(mfma_rate_kernel, dim3(kMfmaRateWG), dim3(256), 0, s, zero_operands ? 1 : 0, iters,
+                                   out));
+  return LSURGE_OK;
+}
+
+}  // extern "C"
+
 // ------------------------------------------------------------------------------ C ABI: ragged_dot without allocation
 // The block table of lsurge_ragged_dot_noalloc lives in this file-scope device array instead of a caller workspace.
 // Each GPU holds its own copy until the process ends; in host code `scratch` only names the symbol, so kernels get

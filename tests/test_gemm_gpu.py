@@ -242,3 +242,21 @@ def test_large_table_grid_fill(dev):
     assert np.all(got[S:] == 0)
     want = mo.ragged_dot(a, b, gs)
     assert mo.rel_l2(got, want) < 5e-3
+
+
+def test_mfma_rate_probe(dev):
+    """The calibration kernel of the bench: zero operands leave every accumulator 0; pseudo-random ones give finite,
+    nonzero per-lane sums that do not depend on the run (the operands are a hash of the element index)."""
+    import _lib as L
+    out = torch.empty(L.lib().lsurge_mfma_rate_probe_out_floats(), dtype=torch.float32, device=dev)
+    L.check(L.lib().lsurge_mfma_rate_probe(1, 3, L.ptr(out), L.stream(dev)), "mfma_rate_probe")
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out).item() == 0
+    runs = []
+    for _ in range(2):
+        L.check(L.lib().lsurge_mfma_rate_probe(0, 3, L.ptr(out), L.stream(dev)), "mfma_rate_probe")
+        torch.cuda.synchronize()
+        runs.append(out.clone())
+    assert torch.isfinite(runs[0]).all() and torch.count_nonzero(runs[0]).item() == out.numel()
+    assert torch.equal(runs[0], runs[1])
+    assert L.lib().lsurge_mfma_rate_probe(0, 0, L.ptr(out), L.stream(dev)) == -1  # iters out of range
