@@ -386,8 +386,8 @@ static int launch_rows256(int kid, const GemmBlocks& g, RowsArgs& a, hipStream_t
     if (a.a_rows) LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, true>), grid, block, 0, s, a));
     else LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false>), grid, block, 0, s, a));
   } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-    LSURGE_REQUIRE(!a.a_rows, "grouped GEMM: no row gather with the SwiGLU backward");
-    LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false>), grid, block, 0, s, a));
+    if (a.a_rows) LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, true>), grid, block, 0, s, a));
+    else LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::rows_kernel<BMODE, EPI, false>), grid, block, 0, s, a));
   } else {
     LSURGE_REQUIRE(!a.a_rows, "grouped GEMM: no row gather with the plain store");
     if (f16 && f32out)
@@ -480,15 +480,25 @@ int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t ld
 
 // C[rows, N] = A[rows, K] @ B_e^T where B_e is stored [N, K] (k-major); with B2 and k_split the K range
 // [k_split, K) reads B2 (gate/up dgrad: A = [dG | dU], B = W_gate, B2 = W_up, k_split = f).
-// swiglu_bwd: C = [dG | dU] from dH = A @ B^T and the saved G, U (ldg pitch).
+// swiglu_bwd: C = [dG | dU] from dH = A @ B^T and the saved G, U (ldg pitch); with row_scale, dH row r is first
+// multiplied by row_scale[r] (padded row; tiles of xe.expert: 1).  A row gather (gather.rows set) as in
+// gemm_rows_swiglu_fwd.
 int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
                  int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
                  bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32,
-                 const ExtraExpert& xe, int et) {
+                 const ExtraExpert& xe, int et, const RowGather& gather, const float* row_scale) {
   if (int rc = check_gemm_shape(K, N, "gemm_rows_nk")) return rc;
   if (int rc = check_desc(std::max<int64_t>(g.tile_rows * lda, N * ldb) * 2, "gemm_rows_nk")) return rc;
   LSURGE_REQUIRE(!B2 || (k_split > 0 && k_split % BK == 0), "gemm_rows_nk: k_split must be a multiple of %d", BK);
+  LSURGE_REQUIRE(!row_scale || swiglu_bwd, "gemm_rows_nk: row_scale is for the SwiGLU backward");
+  LSURGE_REQUIRE(!gather.rows || et == LSURGE_BF16, "gemm_rows_nk: the row gather takes bf16 operands");
+  if (gather.rows) {
+    LSURGE_REQUIRE(gather.div >= 1 && gather.nrows >= 1, "gemm_rows_nk: bad row gather");
+    if (int rc = check_desc(gather.nrows * lda * 2, "gemm_rows_nk gather")) return rc;
+  }
   RowsArgs a{};
+  a.a_rows = gather.rows; a.a_nrows = gather.nrows; a.a_div = gather.div;
+  a.row_scale = row_scale;
   a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.B2 = (const bf16_t*)B2; a.k_split = B2 ? k_split : 0;
   a.ldb = ldb; a.b_estride = b_estride; a.K = K; a.N = N; a.ldc = ldc;
   if (out_f32 && !swiglu_bwd) a.Cf = (float*)C;
@@ -652,10 +662,14 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
   LSURGE_REQUIRE(!C2 || n_split % 4 == 0, "gemm_wgrad_chunked: n_split must be a multiple of 4");
   if (gather.rows) {
     LSURGE_REQUIRE(gather.div >= 1 && gather.nrows >= 1, "gemm_wgrad_chunked: bad row gather");
-    if (int rc = check_desc(gather.nrows * lda * 2, "gemm_wgrad_chunked gather")) return rc;
+    if (int rc = check_desc(gather.nrows * (gather.on_b ? ldb : lda) * 2, "gemm_wgrad_chunked gather")) return rc;
   }
+  LSURGE_REQUIRE(!gather.on_b || (gather.rows && gather.scale && et == LSURGE_BF16 && gemm_variant() == LSURGE_GEMM_G256),
+                 "gemm_wgrad_chunked: the scaled B gather needs bf16 operands, row indices, weights and the persistent "
+                 "kernels");
   WgradArgs a{};
-  a.a_rows = gather.rows; a.a_nrows = gather.nrows; a.a_div = gather.div;
+  a.a_rows = gather.rows; a.a_nrows = gather.on_b ? 0 : gather.nrows; a.a_div = gather.div;
+  a.gather_b = gather.on_b; a.b_nrows = gather.on_b ? gather.nrows : 0; a.b_scale = gather.scale;
   a.A = (const bf16_t*)A; a.lda = lda; a.B = (const bf16_t*)B; a.ldb = ldb; a.I = I; a.N = N; a.C = C; a.C2 = C2;
   a.n_split = n_split; a.ldc = ldc; a.c_estride = c_estride;
   a.E = E; a.S = 1; a.part = (float*)part;
@@ -668,7 +682,7 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
   // whose non-persistent grid the dispatcher balances, measured faster there (176 against 203 us at C2).  Both give
   // the same bits.
   const bool g256_tiles = (int64_t)((I + g256::BM - 1) / g256::BM) * ((N + g256::BN - 1) / g256::BN) >= 16;
-  if (gemm_variant() == LSURGE_GEMM_G256 && g256_tiles) {
+  if (gemm_variant() == LSURGE_GEMM_G256 && (g256_tiles || gather.on_b)) {
     // persistent 256 x 256 tiles, one workgroup per CU; the epilogue's descriptors span one tile's rows of an output
     if (int rc = check_desc((int64_t)g256::BM * std::max(N, ldc) * 4, "gemm_wgrad_chunked output")) return rc;
     a.i_tiles = (int)((I + g256::BM - 1) / g256::BM);
@@ -677,6 +691,8 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
     if (et == LSURGE_F16) {
       LSURGE_REQUIRE(!a.a_rows, "gemm_wgrad_chunked: no row gather with f16 operands");
       LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::wgrad_kernel<false, LSURGE_F16>), grid, block, 0, s, a));
+    } else if (a.gather_b) {
+      LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::wgrad_kernel<true, LSURGE_BF16, true>), grid, block, 0, s, a));
     } else if (a.a_rows) {
       LSURGE_LAUNCH(kid, s, hipLaunchKernelGGL((g256::wgrad_kernel<true>), grid, block, 0, s, a));
     } else {

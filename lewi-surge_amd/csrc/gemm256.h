@@ -47,6 +47,9 @@ __device__ __forceinline__ rsrc_t rsrc(const void* p, int64_t bytes) {
 __device__ __forceinline__ u32x4 ld16(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
+__device__ __forceinline__ float ldf(rsrc_t r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
 
 enum { SG_MFMA = 0x8, SG_VMEM_R = 0x20, SG_DS_R = 0x100, SG_DS_W = 0x200 };
 
@@ -336,6 +339,9 @@ void rows_kernel(RowsArgs a) {
                            (int64_t)rt.rows * a.ldc * osz);
     const rsrc_t rG = rsrc(a.G ? a.G + rt.row0 * a.ldg : nullptr, a.G ? (int64_t)rt.rows * a.ldg * 2 : 0);
     const rsrc_t rU = rsrc(a.U ? a.U + rt.row0 * a.ldg : nullptr, a.U ? (int64_t)rt.rows * a.ldg * 2 : 0);
+    // SwiGLU backward: the routing weight of each row (tiles of the extra expert: 1)
+    const bool scl = EPI == EPI_SWIGLU_BWD && a.row_scale && rt.expert != a.x_expert;
+    const rsrc_t rW = rsrc(scl ? a.row_scale + rt.row0 : nullptr, scl ? (int64_t)rt.rows * 4 : 0);
     const uint32_t ldc_b = (uint32_t)a.ldc * osz, ldg_b = (uint32_t)a.ldg * 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -383,7 +389,10 @@ void rows_kernel(RowsArgs a) {
         }
       } else if (EPI == EPI_SWIGLU_BWD) {
         // dH of 32 rows x 64 columns per pass (fragments 2 jp, 2 jp + 1, f32), read back 8 columns per lane beside
-        // the saved g and u -> [dG | dU]
+        // the saved g and u -> [dG | dU]; dH rows scaled by their routing weight first (row_scale)
+        float ws[4];
+#pragma unroll
+        for (int it = 0; it < 4; ++it) ws[it] = scl ? ldf(rW, (uint32_t)(rbase + 8 * it + (el >> 3)) * 4u) : 1.f;
 #pragma unroll
         for (int jp = 0; jp < 2; ++jp) {
           u32x4 gq[4], uq[4];  // fetched first, so their latency overlaps the LDS round trip
@@ -422,8 +431,9 @@ void rows_kernel(RowsArgs a) {
               const float g = __uint_as_float((t & 1) ? (gw & 0xffff0000u) : (gw << 16));
               const float u = __uint_as_float((t & 1) ? (uw & 0xffff0000u) : (uw << 16));
               const float sg = sigmoid_f(g);
-              dg[t] = v[t] * u * sg * (1.f + g * (1.f - sg));
-              du[t] = v[t] * g * sg;
+              const float dh = v[t] * ws[it];
+              dg[t] = dh * u * sg * (1.f + g * (1.f - sg));
+              du[t] = dh * g * sg;
             }
             st16(rC, oo[it], u32x4{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]), pack_bf16x2(dg[4], dg[5]),
                                    pack_bf16x2(dg[6], dg[7])});
@@ -535,7 +545,10 @@ void rows_kernel(RowsArgs a) {
 // GATHER: reduction row r of A is A[a_rows[r] / a_div] (the layer's x rows through row_src).  An index cursor runs one
 // stage ahead of the copies: each stage's row indices are read before the previous stage's data loads are issued,
 // so the wait for them never waits for data.
-template <bool GATHER, int ET = LSURGE_BF16>
+// ONB (with GATHER): the gather applies to B instead, and each gathered B row is multiplied by b_scale[r] (chunks of
+// x_expert: 1) and rounded to bf16 as it is staged into LDS (the layer's dY rows times their routing weight, the
+// operand the combine backward would otherwise write out); the weights ride along the row indices.
+template <bool GATHER, int ET = LSURGE_BF16, bool ONB = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void wgrad_kernel(WgradArgs a) {
   __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
@@ -578,9 +591,10 @@ void wgrad_kernel(WgradArgs a) {
     const int c = lt / tpc, rem = lt % tpc, it = rem / a.n_tiles, nt = rem % a.n_tiles;
     const int64_t row0 = uni(a.c_row0[c]);
     const int rows = uni(a.c_rows[c]);
-    if (GATHER) la = rsrc(a.A, a.a_nrows * (int64_t)a.lda * 2);
+    if (GATHER && !ONB) la = rsrc(a.A, a.a_nrows * (int64_t)a.lda * 2);
     else la = rsrc(a.A + row0 * a.lda, (int64_t)rows * a.lda * 2);  // rows past the chunk: zeros
-    lb = rsrc(a.B + row0 * a.ldb, (int64_t)rows * a.ldb * 2);
+    if (ONB) lb = rsrc(a.B, a.b_nrows * (int64_t)a.ldb * 2);
+    else lb = rsrc(a.B + row0 * a.ldb, (int64_t)rows * a.ldb * 2);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int64_t ca = (int64_t)it * BM + 128 * h + 8 * nc, cb = (int64_t)nt * BN + 128 * h + 8 * nc;
@@ -595,7 +609,11 @@ void wgrad_kernel(WgradArgs a) {
   const uint64_t magic = div_magic(GATHER ? a.a_div : 1);
   int xk_t = 0, xt = t_cur, xk = 0, x_rows = 0, x_nk = 2;
   int64_t x_row0 = 0;
+  bool x_one = false;  // ONB: the cursor's chunk belongs to x_expert (weights 1)
   int pend[4];
+  // ONB: weights of the pending rows, of the copy stage, and of the B chunks in the staging registers (chunks i and
+  // i + 4 share row i: the later one's load, the row's last in a stage, moves the weight along)
+  float pend_w[4], w_cur[4], w_dat[4];
   uint32_t g_off[4];
   auto x_set = [&]() {
     if (xk_t < ntiles_wg) {
@@ -603,6 +621,7 @@ void wgrad_kernel(WgradArgs a) {
       x_row0 = uni(a.c_row0[c]);
       x_rows = uni(a.c_rows[c]);
       x_nk = stages_of(x_rows);
+      if (ONB) x_one = uni(a.c_expert[c]) == a.x_expert;
     }
   };
   auto x_issue = [&]() {  // read the indices at the index cursor into pend, then advance the cursor
@@ -612,6 +631,10 @@ void wgrad_kernel(WgradArgs a) {
       const bool ok = xk_t < ntiles_wg && r < x_rows;
       const int v = a.a_rows[x_row0 + (ok ? r : 0)];
       pend[q] = ok ? v : -1;
+      if (ONB) {
+        const float w = a.b_scale[x_row0 + (ok ? r : 0)];
+        pend_w[q] = x_one ? 1.f : w;
+      }
     }
     if (++xk == x_nk) {
       xk = 0;
@@ -621,7 +644,10 @@ void wgrad_kernel(WgradArgs a) {
   };
   auto x_take = [&]() {  // the pending indices become the copy cursor's stage
 #pragma unroll
-    for (int q = 0; q < 4; ++q) g_off[q] = pend[q] >= 0 ? (uint32_t)div_by(pend[q], magic) * lda2 : OOB;
+    for (int q = 0; q < 4; ++q) {
+      g_off[q] = pend[q] >= 0 ? (uint32_t)div_by(pend[q], magic) * (ONB ? ldb2 : lda2) : OOB;
+      if (ONB) w_cur[q] = pend_w[q];
+    }
   };
   if (GATHER) x_set();
 
@@ -631,16 +657,25 @@ void wgrad_kernel(WgradArgs a) {
     const int i = c & 7, h = i >> 2, q = i & 3;
     const uint32_t krow = (uint32_t)(lk * BK + 16 * q + nr);
     if (c < 8) {
-      const uint32_t ro = GATHER ? g_off[q] : krow * lda2;
+      const uint32_t ro = GATHER && !ONB ? g_off[q] : krow * lda2;
       R[c] = ld16(la, live && acol[h] != OOB && ro != OOB ? ro + acol[h] : OOB);
     } else {
-      R[c] = ld16(lb, live && bcol[h] != OOB ? krow * ldb2 + bcol[h] : OOB);
+      const uint32_t ro = ONB ? g_off[q] : krow * ldb2;
+      R[c] = ld16(lb, live && bcol[h] != OOB && ro != OOB ? ro + bcol[h] : OOB);
+      if (ONB && h == 1) w_dat[q] = w_cur[q];
     }
   };
   auto swrite = [&](int c, int buf) {
     const int i = c & 7;
     char* p = smem + buf * STAGE_BYTES + (c < 8 ? 0 : OP_BYTES) + (i >> 2) * (BK * 256) + 16 * 256 * (i & 3) + nm_w;
-    *reinterpret_cast<u32x4*>(p) = R[c];
+    u32x4 v = R[c];
+    if (ONB && c >= 8) {  // bf16(w * b), the rounding of the materialised operand
+      const float w = w_dat[i & 3];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = pack_bf16x2(__uint_as_float(v[e] << 16) * w, __uint_as_float(v[e] & 0xffff0000u) * w);
+    }
+    *reinterpret_cast<u32x4*>(p) = v;
   };
   typedef FragSet<4, 4> F;
   auto fread = [&](F& f, int buf, int s) {
@@ -686,6 +721,12 @@ void wgrad_kernel(WgradArgs a) {
   // destinations, lanes whose columns belong to the other one pass the out-of-range offset
   char* const stg = smem + RING_BYTES + wave * STG_BYTES;
   auto epilogue = [&]() {
+    // the lane index, opaque to the compiler here (as in the row kernel's epilogue): the per-lane offsets below are
+    // formed inside each epilogue instead of being held across the K loop, which the gathered-B variant's extra
+    // registers would otherwise spill
+    int el = lane;
+    if (ONB) asm volatile("" : "+v"(el));
+    const int efr = el & 31, efh = el >> 5;
     const int c = t_cur / tpc, rem = t_cur % tpc, it = rem / a.n_tiles, nt = rem % a.n_tiles;
     const int expert = uni(a.c_expert[c]), part = uni(a.c_part[c]);
     const int64_t i0 = (int64_t)it * BM, n0 = (int64_t)nt * BN;
@@ -716,14 +757,14 @@ void wgrad_kernel(WgradArgs a) {
         for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int ch4 = 8 * jj + 2 * q + fh;
-            *reinterpret_cast<f32x4*>(stg + fr * 256 + ((ch4 ^ (fr & 15)) << 4)) =
+            const int ch4 = 8 * jj + 2 * q + efh;
+            *reinterpret_cast<f32x4*>(stg + efr * 256 + ((ch4 ^ (efr & 15)) << 4)) =
                 f32x4{acc[i][2 * jp + jj][4 * q], acc[i][2 * jp + jj][4 * q + 1], acc[i][2 * jp + jj][4 * q + 2],
                       acc[i][2 * jp + jj][4 * q + 3]};
           }
 #pragma unroll
         for (int it2 = 0; it2 < 8; ++it2) {
-          const int r = 4 * it2 + (lane >> 4), cc = lane & 15;
+          const int r = 4 * it2 + (el >> 4), cc = el & 15;
           const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((cc ^ (r & 15)) << 4));
           const int64_t col = n0 + wn * 128 + 64 * jp + 4 * cc;
           const uint32_t rb = (uint32_t)(rbase + r) * pb;

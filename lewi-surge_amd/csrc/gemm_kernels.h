@@ -103,6 +103,10 @@ struct RowsArgs {
   // SwiGLU forward: atomic max of |h|; FP8 SwiGLU backward: of |dG| and |dU|; as bf16-rounded float bits (nullptr:
   // none)
   uint32_t* amax = nullptr;
+  // SwiGLU backward (bf16): dH row r of a tile is multiplied by row_scale[row0 + r] (indexed by padded row) before
+  // the SwiGLU backward, except in tiles of x_expert (scale 1); nullptr: no scaling.  The layer's routing weights,
+  // applied to dY @ W_down^T instead of to the dY rows.
+  const float* row_scale = nullptr;
 };
 
 struct WgradArgs {
@@ -137,6 +141,13 @@ struct WgradArgs {
   int x_expert = -1;          // this expert id writes Cx / C2x (row pitch ldc) instead of C / C2 (-1: none)
   float* Cx = nullptr;
   float* C2x = nullptr;
+  // Row gather of B instead of A (persistent kernel only): reduction row r reads B[a_rows[r] / a_div] of a B with
+  // b_nrows rows, times b_scale[r] (indexed by padded row like a_rows; chunks of x_expert: times 1), rounded to bf16
+  // as the staged operand -- the layer's dY rows scaled by their routing weight, as the combine backward would have
+  // written them.
+  bool gather_b = false;
+  int64_t b_nrows = 0;
+  const float* b_scale = nullptr;
   // FP8 (gemm_wgrad_f8_kernel): A = [I, lda] and B = [N, ldb] bytes, K-contiguous over the rows; dequantisation
   // factors of each (one value)
   const float* a_sinv = nullptr;
@@ -679,7 +690,9 @@ void gemm_rows_kernel(RowsArgs a) {
     // SwiGLU backward: fetch the saved g, u of this slice before parking the accumulators, so the loads'
     // latency overlaps the LDS round trip.
     u32x4 gq[PASSES], uq[PASSES];
+    float wsc[PASSES];  // routing weights of the rows (row_scale; 1 without, and in tiles of the extra expert)
     if (EPI == EPI_SWIGLU_BWD) {
+      const bool scl = !F8 && a.row_scale && expert != a.x_expert;
 #pragma unroll
       for (int it = 0; it < PASSES; ++it) {
         const int r = RPP * it + lane / LPR;
@@ -688,6 +701,7 @@ void gemm_rows_kernel(RowsArgs a) {
         const int64_t off = ok ? (row0 + mbase + r) * a.ldg + col : row0 * a.ldg;
         gq[it] = *reinterpret_cast<const u32x4*>(a.G + off);
         uq[it] = *reinterpret_cast<const u32x4*>(a.U + off);
+        wsc[it] = scl && mbase + r < rows ? a.row_scale[row0 + mbase + r] : 1.f;
       }
     }
     if (i > 0) __builtin_amdgcn_wave_barrier();
@@ -741,8 +755,9 @@ void gemm_rows_kernel(RowsArgs a) {
             const float g = __uint_as_float((t & 1) ? (gw & 0xffff0000u) : (gw << 16));
             const float u = __uint_as_float((t & 1) ? (uw & 0xffff0000u) : (uw << 16));
             const float sg = sigmoid_f(g);
-            dg[t] = v[t] * u * sg * (1.f + g * (1.f - sg));
-            du[t] = v[t] * g * sg;
+            const float dh = v[t] * wsc[it];
+            dg[t] = dh * u * sg * (1.f + g * (1.f - sg));
+            du[t] = dh * g * sg;
             if constexpr (F8 != 0) hmax = fmaxf(hmax, fmaxf(fabsf(dg[t]), fabsf(du[t])));
           }
           st_bf16x8(a.C + gr * a.ldc + col, dg);

@@ -57,7 +57,7 @@ struct CombineFp8 {
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
                            int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s,
                            void* gcopy = nullptr, const int32_t* sel = nullptr, void* dlog = nullptr, int E = 0,
-                           const CombineFp8& f8 = CombineFp8());
+                           const CombineFp8& f8 = CombineFp8(), float* wpad = nullptr);
 // The E5M2 scale (power of two) of the dY rows w[t, j] g[t] (bf16-rounded) from g [n, d] and w [n, k] alone: amax
 // partials (dy_rows_amax_parts() floats at partial), then scale[0] and sinv[0] = 1 / scale; also clears
 // zero[0 .. nzero).
@@ -88,6 +88,10 @@ struct RowGather {
   const int32_t* rows = nullptr;
   int div = 1;
   int64_t nrows = 0;  // rows of the gathered-from matrix
+  // gemm_wgrad_chunked only: gather B instead of A, each row times scale[r] (padded row; the extra expert's rows: 1)
+  // rounded to bf16 -- the persistent kernel only
+  bool on_b = false;
+  const float* scale = nullptr;
 };
 // One extra expert id whose weights live in matrices of their own (the layer's shared expert, carried along the
 // routed experts as expert E): its tiles read B / B2 here instead of the routed weight stack.
@@ -106,7 +110,8 @@ int gemm_rows_swiglu_fwd(int kid, const GemmBlocks& g, const void* A, int64_t ld
 int gemm_rows_nk(int kid, const GemmBlocks& g, const void* A, int64_t lda, const void* B, const void* B2,
                  int64_t k_split, int64_t ldb, int64_t b_estride, int64_t K, int64_t N, void* C, int64_t ldc,
                  bool swiglu_bwd, const void* Gs, const void* Us, int64_t ldg, hipStream_t s, bool out_f32 = false,
-                 const ExtraExpert& xe = ExtraExpert(), int et = LSURGE_BF16);
+                 const ExtraExpert& xe = ExtraExpert(), int et = LSURGE_BF16, const RowGather& gather = RowGather(),
+                 const float* row_scale = nullptr);
 // FP8 row GEMM, both operands K-contiguous (B_e stored [N, K], E4M3; A E4M3, or E5M2 with a_e5m2); byte pitches;
 // epilogue F8_STORE, F8_SWIGLU_FWD or F8_SWIGLU_BWD; k_split: B2 for k >= k_split (multiple of 64); see gemm.hip
 enum F8Epi { F8_STORE = 0, F8_SWIGLU_FWD = 1, F8_SWIGLU_BWD = 2 };

@@ -131,6 +131,7 @@ struct BwdWs {
   bf16_t *dy_pad, *dgu, *dx_pad, *sdgu, *sdx, *dlog, *w_rT;
   float* dl;
   float* dweights;
+  float* wpad;        // routing weight of each padded row (the down GEMMs scale by it instead of reading dY_pad)
   void* part;         // split-K partials of the shared-expert weight gradients (their own stream)
   size_t part_bytes;
   void* part_r;       // split-K partials of the router weight gradient (another stream)
@@ -155,6 +156,7 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   w->w_rT = c.take<bf16_t>(q.E * q.d);
   w->dl = c.take<float>(q.M);
   w->dweights = c.take<float>(q.M);
+  w->wpad = c.take<float>(q.PT);
   size_t part = 0;
   if (q.fs && !q.merged) {
     part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, 2 * q.fs, dense_splits(q.T, q.d, 2 * q.fs)));
@@ -645,13 +647,28 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, st,
                                          q.merged ? q.T : -1, q.P))
     return rc;
-  // main: combine backward: dY rows (scaled by the routing weight), d(weights), d(router logits at sel) and their
-  // dense bf16 rows for the router's weight gradient; a merged
-  // shared expert's rows of dY_pad get dY itself
-  if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, q.P, sv.slot, sv.weights, q.T, (int)q.k, q.d, dy, w.dy_pad,
-                                              dweights, w.dl, st, q.merged ? w.dy_pad + q.P * q.d : nullptr, sv.sel,
-                                              w.dlog, (int)q.E))
+  // main: combine backward: d(weights), d(router logits at sel) and their dense bf16 rows for the router's weight
+  // gradient, and the padded dY rows bf16(w dY) of the down projection's GEMMs (a merged shared expert's rows get dY
+  // itself).
+  // Where the down weight gradient runs on the persistent kernel anyway (at least 16 tiles of 256 x 256 per chunk:
+  // f d >= 16 * 65536, as at C5) the dY rows are not written out: the combine backward writes the routing weight of
+  // every padded row (wpad) instead, the down dgrad gathers dY rows and scales dH = dY W_down^T by wpad in its
+  // epilogue, and the weight gradient gathers and scales them as it stages them, to the bits of bf16(w dY).  C5:
+  // 18.20 -> 18.00 ms per step (the combine backward 0.91 -> 0.48 ms, the two down GEMMs +0.31 ms).  With fewer tiles
+  // per chunk the scaled gather costs the weight gradient more than the rows save (C2: 1.640 against 1.641 ms).
+  // The classic kernels' weight gradient copies its operands straight to LDS, so it reads the written rows; its dgrad
+  // takes the gathered path too, so both kernel families give the same bits.
+  const bool dy_gather = ((q.f + 255) / 256) * ((q.d + 255) / 256) >= 16;
+  const bool dy_rows = !dy_gather || lsurge::gemm_variant() != LSURGE_GEMM_G256;
+  if (int rc = lsurge::launch_combine_bwd_pad(sv.y_pad, q.P, sv.slot, sv.weights, q.T, (int)q.k, q.d, dy,
+                                              dy_rows ? w.dy_pad : nullptr, dweights, w.dl, st,
+                                              dy_rows && q.merged ? w.dy_pad + q.P * q.d : nullptr, sv.sel, w.dlog,
+                                              (int)q.E, lsurge::CombineFp8(), dy_gather ? w.wpad : nullptr))
     return rc;
+  lsurge::RowGather dyg;  // dY rows through row_src (padded row -> flat slot t k + j, the shared rows -> t k)
+  dyg.rows = sv.row_src;
+  dyg.div = (int)q.k;
+  dyg.nrows = q.T;
   // fork: the helpers start after the combine backward (and everything the caller enqueued before the call); one
   // record on the critical stream serves both
   if (s1 != st) {
@@ -659,11 +676,17 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
         (q.merged && hipStreamWaitEvent(s0, ev[2], 0) != hipSuccess))
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_bwd: fork events failed");
   }
-  // s1: down wgrad dW_down[e] = h_e^T dY_e
-  if (int rc = lsurge::gemm_wgrad_chunked(KID_GEMM_DOWN_WGRAD, chunks, (int)q.E, q.T, sv.h, q.f, w.dy_pad, q.d, q.f,
-                                          q.d, g->dw_down, nullptr, 0, q.d, q.f * q.d, w.part_dn, w.part_dn_bytes, s1,
-                                          lsurge::RowGather(), odn))
-    return rc;
+  // s1: down wgrad dW_down[e] = h_e^T dY_e (without written dY rows: gathered and scaled by wpad)
+  {
+    lsurge::RowGather bg = dyg;
+    bg.on_b = true;
+    bg.scale = w.wpad;
+    if (int rc = lsurge::gemm_wgrad_chunked(KID_GEMM_DOWN_WGRAD, chunks, (int)q.E, q.T, sv.h, q.f,
+                                            dy_rows ? (const void*)w.dy_pad : dy, q.d, q.f, q.d, g->dw_down, nullptr, 0,
+                                            q.d, q.f * q.d, w.part_dn, w.part_dn_bytes, s1,
+                                            dy_rows ? lsurge::RowGather() : bg, odn))
+      return rc;
+  }
   // router backward dW_r = x^T dlogits (bf16 MFMA over the dense [T, E] dlogits): on s0 beside the down wgrad when
   // s0 is free (merged shared expert), else after the down wgrad on s1
   hipStream_t sr = q.merged ? s0 : s1;
@@ -673,9 +696,11 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                     q.E, g->dw_r, nullptr, 0, q.E, 0, S, w.part_r, w.part_r_bytes, sr))
       return rc;
   }
-  // main: down dgrad + SwiGLU backward: dH = dY W_down^T -> [dG | dU]
-  if (int rc = lsurge::gemm_rows_nk(KID_GEMM_DOWN_DGRAD, blocks, w.dy_pad, q.d, p->w_down, nullptr, 0, q.d, q.f * q.d,
-                                    q.d, q.f, w.dgu, 2 * q.f, true, sv.g, sv.u, q.f, st, false, xdn))
+  // main: down dgrad + SwiGLU backward: dH = dY_pad W_down^T, or w (dY W_down^T) from gathered dY rows -> [dG | dU]
+  if (int rc = lsurge::gemm_rows_nk(KID_GEMM_DOWN_DGRAD, blocks, dy_gather ? dy : (const void*)w.dy_pad, q.d, p->w_down,
+                                    nullptr, 0, q.d, q.f * q.d, q.d, q.f, w.dgu, 2 * q.f, true, sv.g, sv.u, q.f, st,
+                                    false, xdn, LSURGE_BF16, dy_gather ? dyg : lsurge::RowGather(),
+                                    dy_gather ? w.wpad : nullptr))
     return rc;
   // main: gate/up dgrad: dX_pad = dG W_gate^T + dU W_up^T
   if (int rc = lsurge::gemm_rows_nk(KID_GEMM_GU_DGRAD, blocks, w.dgu, 2 * q.f, p->w_gate, p->w_up, q.f, q.f, q.d * q.f,

@@ -292,8 +292,8 @@ __global__ __launch_bounds__(PM_THREADS) void gather_dot_kernel(const void* __re
 }
 
 // ------------------------------------------------------------------------------ fused combine backward
-// One wave per token: g[t] is read once; for every j the expert row y[pos] is read, dy[pos] written and
-// the dot <g, y[pos]> reduced.  Optionally also the router backward dl[t,j] = w_j (dw_j - sum_i w_i dw_i).
+// One wave per token: g[t] is read once; for every j the expert row y[pos] is read, dy[pos] written (dy optional)
+// and the dot <g, y[pos]> reduced.  Optionally also the router backward dl[t,j] = w_j (dw_j - sum_i w_i dw_i).
 template <int DT, int GT, bool VEC>
 __global__ __launch_bounds__(PM_THREADS) void combine_bwd_kernel(const void* __restrict__ y, int64_t m,
                                                                  const int32_t* __restrict__ pos,
@@ -346,7 +346,7 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_kernel(const void* __r
               acc[q] += v[e] * gv[e];
               o[e] = wj[q] * gv[e];
             }
-            V8<DT>::st((char*)dy + (src[q] * d + c) * ES, o);
+            if (dy) V8<DT>::st((char*)dy + (src[q] * d + c) * ES, o);
           }
         }
       } else {
@@ -357,7 +357,7 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_kernel(const void* __r
             float gv = Elem<GT>::ld((const G*)g, t * d + c);
             if (GT != DT) gv = round_to<DT>(gv);
             acc[q] += Elem<DT>::ld((const T*)y, src[q] * d + c) * gv;
-            Elem<DT>::st((T*)dy, src[q] * d + c, wj[q] * gv);
+            if (dy) Elem<DT>::st((T*)dy, src[q] * d + c, wj[q] * gv);
           }
         }
       }
@@ -543,6 +543,16 @@ __global__ __launch_bounds__(PM_THREADS) void dy_scale_kernel(const float* __res
   }
 }
 
+// wpad[slot[i]] = w[i] for the n k flat slots (positions outside [0, rows) skipped): the routing weight of each
+// padded row, for the generic-shape path of launch_combine_bwd_pad.
+__global__ void scatter_weights_kernel(const int32_t* __restrict__ slot, const float* __restrict__ w, int64_t m,
+                                       int64_t rows, float* __restrict__ wpad) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < m; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = slot[i];
+    if (r >= 0 && r < rows) wpad[r] = w[i];
+  }
+}
+
 // Fused combine backward of the layer (bf16 rows): per token, g is read once; for every choice j the expert
 // row y_pad[slot] is read once, dy_pad[slot] = bf16(w_j g) written once and <g, y> reduced; then the router
 // term dl[t,j] = w_j (dw_j - sum_i w_i dw_i).  moe_permute.py:303-309 does this in two passes over g and y.
@@ -550,7 +560,8 @@ __global__ __launch_bounds__(PM_THREADS) void dy_scale_kernel(const float* __res
 // expert rides along the routed experts).  dlog (optional, with sel): the dense bf16 row [E] of d(logits), dl[t,j] at
 // column sel[t,j] and 0 elsewhere -- the operand of the router's weight gradient.
 // FP8 backward (dyq set): the dY rows go out as E5M2 codes of bf16(w_j g) times scale[0] (dy_scale_kernel; dyp is
-// not written).
+// not written).  dyp may be null (no dY rows: the persistent GEMMs gather g and apply w_j themselves); wpad (optional)
+// receives w_j at padded row slot[t, j], the weight those GEMMs apply.
 template <int NC, int KK>
 __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_t* __restrict__ yp,
                                                                      const int32_t* __restrict__ slot,
@@ -562,7 +573,8 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_
                                                                      const int32_t* __restrict__ sel,
                                                                      bf16_t* __restrict__ dlog, int E,
                                                                      uint8_t* __restrict__ dyq,
-                                                                     const float* __restrict__ dy_scale) {
+                                                                     const float* __restrict__ dy_scale,
+                                                                     float* __restrict__ wpad) {
   static_assert(NC > 0 && KK > 0, "fixed-shape kernel");
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * PM_WAVES;
@@ -596,10 +608,11 @@ __global__ __launch_bounds__(PM_THREADS) void combine_bwd_pad_kernel(const bf16_
           typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
           *reinterpret_cast<u32x2*>(dyq + r * d + (c * 64 + lane) * 8) =
               u32x2{e5m2x4(o[0], o[1], o[2], o[3]), e5m2x4(o[4], o[5], o[6], o[7])};
-        } else {
+        } else if (dyp) {
           V8<LSURGE_BF16>::st(dyp + r * d + (c * 64 + lane) * 8, o);
         }
       }
+      if (wpad && lane == 0) wpad[r] = wj;
       dot[j] = acc;
     }
 #pragma unroll
@@ -807,23 +820,28 @@ int launch_dy_scale(const void* g, const float* w, int64_t n, int64_t d, int k, 
 
 int launch_combine_bwd_pad(const void* yp, int64_t rows, const int32_t* slot, const float* w, int64_t n, int k,
                            int64_t d, const void* g, void* dyp, float* dw, float* dl, hipStream_t s, void* gcopy,
-                           const int32_t* sel, void* dlog, int E, const CombineFp8& f8) {
+                           const int32_t* sel, void* dlog, int E, const CombineFp8& f8, float* wpad) {
   const dim3 grid(grid_for_rows(n));
   const int nc = row_chunks(d);
   LSURGE_REQUIRE(!dlog || (sel && dl && E >= 1), "combine_bwd: dense d(logits) needs sel, dl and E");
   LSURGE_REQUIRE(!dl || dw, "combine_bwd: the router backward needs dw");
   LSURGE_REQUIRE(!f8.dyq || (f8.scale && f8.nblocks && !gcopy), "combine_bwd: the FP8 dY rows need their scale and "
                  "the block count");
+  LSURGE_REQUIRE(dyp || (!f8.dyq && !gcopy), "combine_bwd: the FP8 rows and the shared copy need the dY rows");
   if (nc && (k == 6 || k == 8)) {
     LS_NC_SWITCH(nc, NC, LS_KK_SWITCH(k, KK, {
       if (NC && KK)
         LSURGE_LAUNCH(KID_COMBINE_BWD, s,
                       hipLaunchKernelGGL((combine_bwd_pad_kernel<NC ? NC : 1, KK ? KK : 1>), grid, dim3(PM_THREADS), 0,
                                          s, (const bf16_t*)yp, slot, w, n, d, (const bf16_t*)g, (bf16_t*)dyp, dw, dl,
-                                         (bf16_t*)gcopy, sel, (bf16_t*)dlog, E, (uint8_t*)f8.dyq, f8.scale));
+                                         (bf16_t*)gcopy, sel, (bf16_t*)dlog, E, (uint8_t*)f8.dyq, f8.scale, wpad));
     }));
     return LSURGE_OK;
   }
+  if (wpad)
+    LSURGE_LAUNCH(KID_COMBINE_BWD, s,
+                  hipLaunchKernelGGL(scatter_weights_kernel, dim3((unsigned)std::min<int64_t>((n * k + 255) / 256, 4096)),
+                                     dim3(256), 0, s, slot, w, n * k, rows, wpad));
   if (gcopy)  // generic shapes: a plain copy of g into the shared expert's rows
     if (hipMemcpyAsync(gcopy, g, (size_t)n * d * 2, hipMemcpyDeviceToDevice, s) != hipSuccess)
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "combine_bwd: copy of dY into the shared rows failed");

@@ -96,6 +96,7 @@ def _layer(p, shape, dev):
     (4096, 1024, 64, 6, 512, 512, False),  # C1's shape, forward and backward
     (4096, 1024, 128, 6, 512, 512, True),  # Zipf loads: empty experts, one hot expert
     (2048, 2048, 256, 8, 512, 2048, False),  # C5's d, E, k and shared width on a token slice
+    (1500, 1024, 32, 4, 1024, 1024, False),  # gathered dY rows in the down GEMMs, merged shared expert
 ])
 def test_layer_bitwise(T, d, E, k, f, fs, zipf, dev):
     p = mo.make_inputs(T=T, d=d, E=E, k=k, f=f, fs=fs, seed=T + E, zipf=zipf)

@@ -73,6 +73,15 @@ def test_small_layers_fp64(T, d, E, k, f, fs, dev):
     check_layer(p, MoEShape(T, d, E, k, f, fs), dev)
 
 
+@pytest.mark.parametrize("T,d,E,k,f,fs", [(600, 1024, 16, 4, 1024, 1024), (400, 2048, 16, 6, 512, 0)])
+def test_gathered_dy_backward(T, d, E, k, f, fs, dev):
+    """Shapes whose down weight gradient has 16+ tiles per chunk: the backward gathers dY rows and applies the
+    routing weights inside the down GEMMs instead of writing the padded dY rows (with a merged shared expert, whose
+    rows take weight 1, and without one)."""
+    p = mo.make_inputs(T=T, d=d, E=E, k=k, f=f, fs=fs, seed=T + 3)
+    check_layer(p, MoEShape(T, d, E, k, f, fs), dev)
+
+
 def test_small_layer_zipf_bias(dev):
     p = mo.make_inputs(T=2048, d=256, E=32, k=4, f=128, fs=128, seed=2, zipf=True)
     check_layer(p, MoEShape(2048, 256, 32, 4, 128, 128), dev)
