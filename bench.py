@@ -235,6 +235,31 @@ def launch_roles(c):
     r.update({"g256_rows<1,1,0>": ["shared_gu_fwd"], "g256_rows<1,1,1>": ["gemm_gu_fwd"],
               "g256_rows<1,0,0>": (["shared_down_fwd"] if fs else []) + ["gemm_down_fwd"]})
     g256 = c.get("gemm_variant", 1) == 1
+    if c.get("fp8"):
+        # FP8 expert GEMMs (classic kernels): the shared expert runs dense GEMMs of its own in both directions, each
+        # template's shared launch submitted before the routed one (the FP8 GEMM templates are tagged <f8>)
+        sh = bool(fs)
+        r.update({
+            "gemm_rows_kernel<0,1><f8>": (["shared_gu_fwd"] if sh else []) + ["gemm_gu_fwd"],
+            "gemm_rows_kernel<0,0><f8>": (["shared_down_fwd"] if sh else []) + ["gemm_down_fwd"]
+                                          + ((["shared_gu_dgrad"] if sh else []) + ["gemm_gu_dgrad"] if c["bwd"] else []),
+            "fp8_cast_kernel<false>": ["fp8_cast"] * 8, "fp8_cast_kernel<true>": ["fp8_cast"] * 8,
+            "fp8_amax_kernel": ["fp8_amax"] * 16, "fp8_cast_t_kernel": ["fp8_quantize_weights"] * 16,
+        })
+        if c["bwd"]:
+            r.update({
+                "gemm_rows_kernel<0,2><f8>": (["shared_down_dgrad"] if sh else []) + ["gemm_down_dgrad"],
+                "gemm_wgrad_f8_kernel<0,1>": (["shared_down_wgrad", "shared_gu_wgrad"] if sh else [])
+                                             + ["gemm_down_wgrad", "gemm_gu_wgrad"],
+                "gemm_wgrad_kernel": ["router_wgrad"],
+                "dy_rows_amax_kernel": ["fp8_amax"], "dy_scale_kernel": ["misc"],
+                "splitk_reduce_kernel<4>": ["splitk_reduce"] * 3,
+                "wgrad_chunk_reduce_kernel": ["chunk_reduce", "chunk_reduce"],
+                "wgrad_chunks_kernel": ["misc"], "transpose_bf16_kernel": ["misc"],
+                "combine_bwd_pad_kernel<2,6>": ["combine_bwd"], "combine_bwd_pad_kernel<2,8>": ["combine_bwd"],
+                "dispatch_bwd_pad_kernel<2,6>": ["dispatch_bwd"], "dispatch_bwd_pad_kernel<2,8>": ["dispatch_bwd"],
+            })
+        return r
     if c["bwd"]:
         r.update({
             "g256_rows<0,2,0>": (["shared_down_dgrad"] if own else []) + ["gemm_down_dgrad"],
@@ -343,6 +368,9 @@ def stats_summary(d):
         raise SystemExit(f"stats summary: no *kernel_stats.csv under {d}")
     with open(files[0]) as fh:
         rows = list(csv.DictReader(fh))
+    # the bench's own calibration kernel (lsurge_mfma_rate_probe) is not part of the path: left out, shares rescaled
+    rows = [r for r in rows if "mfma_rate_kernel" not in r["Name"]]
+    tot = sum(int(r["TotalDurationNs"]) for r in rows) or 1
     print(f"{'kernel':58s} {'calls':>6s} {'avg us':>9s} {'total ms':>9s} {'share':>7s}")
     for r in rows:
         n = r["Name"].replace("void ", "")
@@ -353,7 +381,7 @@ def stats_summary(d):
         if "at::" in n:
             n = "torch (synthetic inputs)"
         print(f"{n[:58]:58s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.1f} "
-              f"{int(r['TotalDurationNs']) / 1e6:9.2f} {float(r['Percentage']):6.2f}%")
+              f"{int(r['TotalDurationNs']) / 1e6:9.2f} {100 * int(r['TotalDurationNs']) / tot:6.2f}%")
 
 
 def profile_summary(a):
@@ -362,7 +390,9 @@ def profile_summary(a):
     import csv
     import glob
 
-    c = dict(CONFIGS[a.config], gemm_variant=a.gemm_variant)
+    c = dict(CONFIGS[a.config], gemm_variant=a.gemm_variant, fp8=a.fp8)
+    if a.fwd_only:
+        c["bwd"] = False
 
     def rows_of(d, kind):
         files = glob.glob(os.path.join(d, f"*{kind}.csv"))
