@@ -412,7 +412,8 @@ int lsurge_moe_saved_layout(const lsurge_moe_shape* s, void* saved, lsurge_moe_s
 // Forward.  Stream plan:
 //   main: router logits -> selection -> layout (-> tile table of the backward) -> gate/up GEMM -> down GEMM ->
 //         [join] -> combine
-//   s0:   after the logits: shared expert (depends on x only)
+//   s0:   shared expert (depends on x only): bf16 from the start, on the classic kernels beside the router; FP8
+//         after the router's kernel
 // The dispatch into padded expert blocks is fused into the gate/up GEMM: its A tiles are gathered straight from
 // the token rows x through row_src (padded row -> flat slot t*k + j), so the padded copy of x is never
 // materialised (the backward's gate/up weight gradient gathers the same way).
@@ -447,6 +448,14 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   LSURGE_REQUIRE(workspace && workspace_bytes >= hist_bytes + f8_bytes, "moe_fwd: workspace %zu bytes too small",
                  workspace_bytes);
   int32_t* rhist = hist_bytes ? (int32_t*)workspace : nullptr;
+  // bf16: the shared expert's dense GEMMs fork at the start of the call and run on the classic kernels, whose
+  // workgroups (72 KiB of LDS, 4 waves) share a CU with the fused router's (66 KiB, 8 waves): MFMA-bound beside
+  // VALU-bound.  The persistent kernels take a CU's whole LDS, so beside them the router would wait for whole GEMMs.
+  // C2: 1.547 -> 1.537 ms per step, forward 0.537 -> 0.528 ms (same-box A/B against forking after the router with
+  // the persistent kernels).
+  const bool early = !w8 && q.fs && s0 != st;
+  if (early)
+    if (int rc = lsurge::stream_after(s0, st, fg.f.ev[3])) return rc;
   // FP8: x's quantisation (memory-bound) runs on s0 beside the router (VALU-bound); the caller's stream waits for
   // it (event ev[2]) only before the routed gate/up GEMM
   if (w8) {
@@ -458,12 +467,12 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
       return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipEventRecord failed");
   }
   if (int rc = lsurge::router_topk_impl(p->x, p->w_r, p->bias, q.T, q.d, q.E, q.k, sv.logits, sv.sel, sv.weights, st,
-                                        s0 != st ? fg.f.ev[0] : nullptr, rhist))
+                                        s0 != st && !early ? fg.f.ev[0] : nullptr, rhist))
     return rc;
-  // s0: the shared expert's forward, dense GEMMs over all T tokens.  It depends on x only; it starts after the
-  // router's logits kernel (VALU-bound, it would share the CUs badly) and overlaps the selection and the layout,
-  // whose small grids leave most of the GPU idle.  A merged shared expert writes its g, u, h and output rows where
-  // the backward's tile table expects expert E (padded rows 128 MB + t).
+  // s0: the shared expert's forward, dense GEMMs over all T tokens.  It depends on x only: in bf16 it runs beside the
+  // router (above); FP8 starts it after the router's kernel, beside the selection and the layout, whose small grids
+  // leave most of the GPU idle.  A merged shared expert writes its g, u, h and output rows where the backward's tile
+  // table expects expert E (padded rows 128 MB + t).
   bf16_t *sg = sv.sg, *su = sv.su, *sh = sv.sh, *sy = sv.sy;
   if (q.merged) {
     sg = sv.g + q.P * q.f;
@@ -471,7 +480,7 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
     sh = sv.h + q.P * q.f;
     sy = sv.y_pad + q.P * q.d;
   }
-  if (s0 != st && hipStreamWaitEvent(s0, fg.f.ev[0], 0) != hipSuccess)
+  if (s0 != st && !early && hipStreamWaitEvent(s0, fg.f.ev[0], 0) != hipSuccess)
     return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_fwd: hipStreamWaitEvent failed");
   if (q.fs && w8) {
     const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
@@ -486,7 +495,7 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
                                       nullptr, nullptr, nullptr, s0))
       return rc;
   } else if (q.fs) {
-    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, 256};
+    const lsurge::GemmBlocks dense{nullptr, nullptr, nullptr, nullptr, 0, q.T, early ? 128 : 256};
     if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
                                               q.fs, sh, sg, su, q.fs, s0))
       return rc;
