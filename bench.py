@@ -299,11 +299,19 @@ def label_launches(rows, c):
         w = row.get("Workgroup_Size_X", row.get("Workgroup_Size"))
         return int(g) // max(1, int(w))
 
+    g256 = c.get("gemm_variant", 1) == 1 and not c.get("fp8")
     out, seen = [], {}
     for row in sorted(rows, key=lambda x: int(x["Correlation_Id"])):
         k = short_kernel(row["Kernel_Name"])
         if k == "router_logits_kernel" or k.startswith("router_fused_kernel"):
             seen = {}
+        if g256 and fs and k in ("gemm_rows_kernel<1,1>", "gemm_rows_kernel<1,0>"):
+            # with helper streams the shared expert's dense forward runs on the classic kernels beside the router,
+            # submitted before the routed GEMMs; its down projection then takes the first persistent <1,0,0> role
+            if k == "gemm_rows_kernel<1,0>":
+                seen["g256_rows<1,0,0>"] = max(seen.get("g256_rows<1,0,0>", 0), 1)
+            out.append(("shared_gu_fwd" if k == "gemm_rows_kernel<1,1>" else "shared_down_fwd", k, row))
+            continue
         if k not in roles:
             continue
         if fs and k in shared_wgs:  # forward GEMM: shared (dense) or routed
