@@ -555,13 +555,16 @@ void wgrad_kernel(WgradArgs a) {
   const int nch = min(uni(a.num_chunks[0]), a.max_chunks);
   const int tpc = a.i_tiles * a.n_tiles;
   // Tile order: chunk c runs on XCD c % 8 (the table puts the hot and shared experts' chunks first, so they spread over
-  // the XCDs), its tiles on consecutive workgroups of that XCD, which share its rows in L2.  Persistent grid (one
-  // workgroup per CU): workgroup l of an XCD takes the XCD's tiles l, l + 32, ... and, of a last partial round, tile
-  // 31 - l, so that round lands on the workgroups that did not start with a heavy chunk.  Otherwise one tile per
-  // workgroup, dealt the same way over the grid.
+  // the XCDs), its tiles on consecutive workgroups of that XCD, which share its rows in L2.  With fewer chunks than
+  // XCDs that would leave XCDs idle (one chunk: 1/8 of the chip), so there every XCD takes an equal contiguous share
+  // of all nch * tpc tiles instead.  Persistent grid (one workgroup per CU): workgroup l of an XCD takes the XCD's
+  // tiles l, l + 32, ... and, of a last partial round, tile 31 - l, so that round lands on the workgroups that did
+  // not start with a heavy chunk.  Otherwise one tile per workgroup, dealt the same way over the grid.
   const int xcd = blockIdx.x % 8, wl = blockIdx.x / 8;
+  const bool flat = nch < 8;
+  const int xbase = flat ? xcd * nch * tpc / 8 : 0;
   const int xchunks = nch > xcd ? (nch - xcd + 7) / 8 : 0;  // chunks xcd, xcd + 8, ...
-  const int xlen = xchunks * tpc;
+  const int xlen = flat ? (xcd + 1) * nch * tpc / 8 - xbase : xchunks * tpc;
   const int npx = gridDim.x / 8;  // workgroups per XCD
   const bool pers = gridDim.x == NWG;
   const int full = pers ? xlen / npx : 0, part_n = pers ? xlen % npx : 0;
@@ -569,7 +572,7 @@ void wgrad_kernel(WgradArgs a) {
   // k-th tile of this workgroup as (chunk, tile in chunk) packed into c * tpc + r
   auto tile_of = [&](int k) {
     const int idx = !pers ? wl : (k < full ? npx * k + wl : npx * full + (npx - 1 - wl));
-    return (xcd + 8 * (idx / tpc)) * tpc + idx % tpc;
+    return flat ? xbase + idx : (xcd + 8 * (idx / tpc)) * tpc + idx % tpc;
   };
   if (ntiles_wg == 0) return;
   int k_cur = 0, t_cur = tile_of(0);

@@ -443,6 +443,17 @@ __device__ __forceinline__ int64_t xcd_logical(int64_t id, int64_t total) {
   return (id % 8) * per + id / 8;
 }
 
+// Tile of a chunk-table launch (grid = 8 x ceil(max_chunks / 8) x tpc tiles per chunk, nch chunks real): chunk c runs
+// on XCD c % 8 with its tiles consecutive there, so the chunks that exist are spread evenly over the XCDs, and a hot
+// expert's chunks too.  With fewer chunks than XCDs that would leave XCDs idle (one chunk: 1/8 of the chip), so there
+// every XCD takes an equal contiguous share of all nch * tpc tiles instead.  -1: no tile for this workgroup.
+__device__ __forceinline__ int64_t chunk_logical(int64_t tpc, int nch) {
+  const int64_t l = blockIdx.x / 8, x = blockIdx.x % 8;
+  if (nch >= 8) return (8 * (l / tpc) + x) * tpc + l % tpc;
+  const int64_t all = (int64_t)nch * tpc, b = x * all / 8;
+  return l < (x + 1) * all / 8 - b ? b + l : -1;
+}
+
 // Park fragment row i of the accumulators (32 rows x TN f32 columns) in this wave's staging area.
 // acc[i][j][4q + t] is row lane%32, wave column 32 j + 8 q + 4 (lane/32) + t.
 template <class Cfg>
@@ -830,13 +841,11 @@ void gemm_wgrad_kernel(WgradArgs a) {
   constexpr uint32_t A_SLOT = Cfg::A_EL * 2, B_SLOT = Cfg::B_EL * 2, B_RING = ST * A_SLOT;  // bytes
   const int64_t total = (int64_t)gridDim.x;
   const int64_t tiles_per_e = (int64_t)(a.c_expert ? 1 : a.S) * a.i_tiles * a.n_tiles;
-  // Tile order.  Expert slices: XCD-aware contiguous ranges (xcd_logical).  Chunk table (grid = 8 x ceil(chunks / 8)
-  // x tiles per chunk): chunk c runs on XCD c % 8 with its tiles consecutive there, so the chunks that exist
-  // (a device-side count below the grid's bound) are spread evenly over the XCDs, and a hot expert's chunks too.
+  // Tile order.  Expert slices: XCD-aware contiguous ranges (xcd_logical).  Chunk table: chunk_logical.
   int64_t logical;
   if (a.c_expert) {
-    const int64_t l = blockIdx.x / 8;
-    logical = (8 * (l / tiles_per_e) + blockIdx.x % 8) * tiles_per_e + l % tiles_per_e;
+    logical = chunk_logical(tiles_per_e, min(a.num_chunks[0], a.max_chunks));
+    if (logical < 0) return;
   } else {
     logical = xcd_logical(blockIdx.x, total);
   }
@@ -1049,8 +1058,8 @@ void gemm_wgrad_f8_kernel(WgradArgs a) {
   const int64_t tiles_per_e = (int64_t)(a.c_expert ? 1 : a.S) * a.i_tiles * a.n_tiles;
   int64_t logical;
   if (a.c_expert) {
-    const int64_t l = blockIdx.x / 8;
-    logical = (8 * (l / tiles_per_e) + blockIdx.x % 8) * tiles_per_e + l % tiles_per_e;
+    logical = chunk_logical(tiles_per_e, min(a.num_chunks[0], a.max_chunks));
+    if (logical < 0) return;
   } else {
     logical = xcd_logical(blockIdx.x, (int64_t)gridDim.x);
   }

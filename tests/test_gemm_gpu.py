@@ -158,7 +158,10 @@ def test_f32_operands_reject_f16_output(dev):
 
 
 @pytest.mark.parametrize("E,M,K,N", [(8, 1000, 256, 192), (4, 777, 128, 1024), (64, 6000, 1024, 512),
-                                     (3, 129, 520, 136)])
+                                     (3, 129, 520, 136),
+                                     # fewer weight-gradient chunks than XCDs: the tiles of one chunk are dealt over
+                                     # every XCD, the shares cut inside a row of tiles
+                                     (1, 3000, 768, 1024), (2, 2500, 1280, 768)])
 def test_random_groups(E, M, K, N, dev):
     rng = np.random.default_rng(M)
     cuts = np.sort(rng.integers(0, M - 5, E - 1))
