@@ -57,6 +57,12 @@ enum { SG_MFMA = 0x8, SG_VMEM_R = 0x20, SG_DS_R = 0x100, SG_DS_W = 0x200 };
 // compiler cannot tell the values are uniform; readfirstlane keeps them (and the descriptors made from them) in
 // scalar registers, where a divergent descriptor would wrap every buffer load in a waterfall loop.
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// Entry i (uniform) of a tile or chunk table through the scalar unit.  The tables are written by earlier launches
+// and only read here, so a constant-address-space load is valid; it lands in a scalar register and is counted by
+// lgkmcnt.  A vector load would be counted by the in-order vector memory count instead, and the wait for it would
+// drain every copy load issued before it.
+typedef const __attribute__((address_space(4))) int32_t cint32_t;
+__device__ __forceinline__ int ctab(const int32_t* p, int i) { return ((cint32_t*)p)[i]; }
 struct Tile {
   int expert, rows;
   int64_t row0;
@@ -552,7 +558,7 @@ template <bool GATHER, int ET = LSURGE_BF16, bool ONB = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void wgrad_kernel(WgradArgs a) {
   __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
-  const int nch = min(uni(a.num_chunks[0]), a.max_chunks);
+  const int nch = min(ctab(a.num_chunks, 0), a.max_chunks);
   const int tpc = a.i_tiles * a.n_tiles;
   // Tile order: chunk c runs on XCD c % 8 (the table puts the hot and shared experts' chunks first, so they spread over
   // the XCDs), its tiles on consecutive workgroups of that XCD, which share its rows in L2.  With fewer chunks than
@@ -592,8 +598,8 @@ void wgrad_kernel(WgradArgs a) {
   uint32_t acol[2], bcol[2];  // byte offsets of this lane's A / B column in each sub-tile (OOB: past I / N)
   auto set_ld = [&]() {
     const int c = lt / tpc, rem = lt % tpc, it = rem / a.n_tiles, nt = rem % a.n_tiles;
-    const int64_t row0 = uni(a.c_row0[c]);
-    const int rows = uni(a.c_rows[c]);
+    const int64_t row0 = ctab(a.c_row0, c);
+    const int rows = ctab(a.c_rows, c);
     if (GATHER && !ONB) la = rsrc(a.A, a.a_nrows * (int64_t)a.lda * 2);
     else la = rsrc(a.A + row0 * a.lda, (int64_t)rows * a.lda * 2);  // rows past the chunk: zeros
     if (ONB) lb = rsrc(a.B, a.b_nrows * (int64_t)a.ldb * 2);
@@ -613,32 +619,36 @@ void wgrad_kernel(WgradArgs a) {
   int xk_t = 0, xt = t_cur, xk = 0, x_rows = 0, x_nk = 2;
   int64_t x_row0 = 0;
   bool x_one = false;  // ONB: the cursor's chunk belongs to x_expert (weights 1)
+  // Raw indices in flight, and which of them are rows of the chunk (bit q; known at issue).  Nothing reads a loaded
+  // index before x_take, a stage later: a select on it at issue would wait for it there, and with the in-order
+  // vector memory count that wait drains every copy load in flight.
   int pend[4];
+  uint32_t pend_ok = 0;
+  bool pend_one = false;  // ONB: x_one of the pending rows
   // ONB: weights of the pending rows, of the copy stage, and of the B chunks in the staging registers (chunks i and
   // i + 4 share row i: the later one's load, the row's last in a stage, moves the weight along)
   float pend_w[4], w_cur[4], w_dat[4];
   uint32_t g_off[4];
-  auto x_set = [&]() {
-    if (xk_t < ntiles_wg) {
-      const int c = xt / tpc;
-      x_row0 = uni(a.c_row0[c]);
-      x_rows = uni(a.c_rows[c]);
-      x_nk = stages_of(x_rows);
-      if (ONB) x_one = uni(a.c_expert[c]) == a.x_expert;
-    }
+  auto x_set = [&]() {  // unconditional stores (past the last tile: chunk 0's entries, no rows)
+    const bool live = xk_t < ntiles_wg;
+    const int c = live ? xt / tpc : 0;
+    const int rows = ctab(a.c_rows, c);
+    x_row0 = ctab(a.c_row0, c);
+    x_rows = live ? rows : 0;
+    x_nk = stages_of(rows);
+    if (ONB) x_one = ctab(a.c_expert, c) == a.x_expert;
   };
   auto x_issue = [&]() {  // read the indices at the index cursor into pend, then advance the cursor
+    pend_ok = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = xk * BK + 16 * q + nr;
-      const bool ok = xk_t < ntiles_wg && r < x_rows;
-      const int v = a.a_rows[x_row0 + (ok ? r : 0)];
-      pend[q] = ok ? v : -1;
-      if (ONB) {
-        const float w = a.b_scale[x_row0 + (ok ? r : 0)];
-        pend_w[q] = x_one ? 1.f : w;
-      }
+      const bool ok = r < x_rows;
+      pend[q] = a.a_rows[x_row0 + (ok ? r : 0)];
+      pend_ok |= ok ? 1u << q : 0u;
+      if (ONB) pend_w[q] = a.b_scale[x_row0 + (ok ? r : 0)];
     }
+    if (ONB) pend_one = x_one;
     if (++xk == x_nk) {
       xk = 0;
       if (++xk_t < ntiles_wg) xt = tile_of(xk_t);
@@ -648,23 +658,25 @@ void wgrad_kernel(WgradArgs a) {
   auto x_take = [&]() {  // the pending indices become the copy cursor's stage
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      g_off[q] = pend[q] >= 0 ? (uint32_t)div_by(pend[q], magic) * (ONB ? ldb2 : lda2) : OOB;
-      if (ONB) w_cur[q] = pend_w[q];
+      g_off[q] = ((pend_ok >> q) & 1u) && pend[q] >= 0 ? (uint32_t)div_by(pend[q], magic) * (ONB ? ldb2 : lda2) : OOB;
+      if (ONB) w_cur[q] = pend_one ? 1.f : pend_w[q];
     }
   };
   if (GATHER) x_set();
 
   u32x4 R[16];
+  // Copy c of stage lk.  Branch-free: the out-of-range tests are per-lane selects (a row offset or a column past the
+  // operand is OOB; every in-range offset is below 2^31).  Past the last tile the cursor keeps that tile's descriptors
+  // and re-reads its first stages, which nothing consumes.
   auto gload = [&](int c, int lk) {
-    const bool live = lk_t < ntiles_wg;
     const int i = c & 7, h = i >> 2, q = i & 3;
     const uint32_t krow = (uint32_t)(lk * BK + 16 * q + nr);
     if (c < 8) {
       const uint32_t ro = GATHER && !ONB ? g_off[q] : krow * lda2;
-      R[c] = ld16(la, live && acol[h] != OOB && ro != OOB ? ro + acol[h] : OOB);
+      R[c] = ld16(la, ((acol[h] | ro) & OOB) ? OOB : ro + acol[h]);
     } else {
       const uint32_t ro = ONB ? g_off[q] : krow * ldb2;
-      R[c] = ld16(lb, live && bcol[h] != OOB && ro != OOB ? ro + bcol[h] : OOB);
+      R[c] = ld16(lb, ((bcol[h] | ro) & OOB) ? OOB : ro + bcol[h]);
       if (ONB && h == 1) w_dat[q] = w_cur[q];
     }
   };
@@ -700,7 +712,9 @@ void wgrad_kernel(WgradArgs a) {
       for (int j = 0; j < 4; ++j) acc[i][j] = mfma32<ET>(f.w[j], f.x[i], acc[i][j]);
   };
 
-  // ---- prologue: stage 0 -> LDS half 0, stage 1 -> registers; the index cursor then points at stage 2
+  // ---- prologue: stage 0 -> LDS half 0, stage 1 -> registers; the index cursor then points at stage 2.  Stage 2's
+  // indices are read before stage 1's copies, as in the loop, so that at the loop head they are 16 loads deep on
+  // either path (the wait there is then for them alone, not for the copies behind them).
   if (GATHER) {
     x_issue();
     x_take();
@@ -712,10 +726,10 @@ void wgrad_kernel(WgradArgs a) {
   if (GATHER) {
     x_issue();
     x_take();
+    x_issue();
   }
 #pragma unroll
   for (int c = 0; c < 16; ++c) gload(c, 1);
-  if (GATHER) x_issue();
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   F f0, f1;
   fread(f0, 0, 0);
@@ -731,7 +745,7 @@ void wgrad_kernel(WgradArgs a) {
     if (ONB) asm volatile("" : "+v"(el));
     const int efr = el & 31, efh = el >> 5;
     const int c = t_cur / tpc, rem = t_cur % tpc, it = rem / a.n_tiles, nt = rem % a.n_tiles;
-    const int expert = uni(a.c_expert[c]), part = uni(a.c_part[c]);
+    const int expert = ctab(a.c_expert, c), part = ctab(a.c_part, c);
     const int64_t i0 = (int64_t)it * BM, n0 = (int64_t)nt * BN;
     const int64_t irows = min((int64_t)BM, (int64_t)I - i0);
     const float* d1;
@@ -783,7 +797,7 @@ void wgrad_kernel(WgradArgs a) {
 
   // stage kt loads stage kt + 2; the last pair loads the next tile's first two stages
   while (true) {
-    const int nk = stages_of(uni(a.c_rows[t_cur / tpc]));
+    const int nk = stages_of(ctab(a.c_rows, t_cur / tpc));
     for (int kt = 0; kt < nk; kt += 2) {
       if (kt + 2 == nk) {
         if (++lk_t < ntiles_wg) {
