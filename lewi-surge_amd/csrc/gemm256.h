@@ -70,9 +70,9 @@ struct Tile {
 __device__ __forceinline__ Tile row_tile(const RowsArgs& a, int b) {
   Tile t;
   if (a.t_expert) {
-    t.expert = uni(a.t_expert[b]);
-    t.rows = uni(a.t_rows[b]);
-    t.row0 = a.t_row0 ? (int64_t)uni(a.t_row0[b]) : (int64_t)b * BM;
+    t.expert = ctab(a.t_expert, b);
+    t.rows = ctab(a.t_rows, b);
+    t.row0 = a.t_row0 ? (int64_t)ctab(a.t_row0, b) : (int64_t)b * BM;
   } else {
     t.expert = 0;
     t.row0 = (int64_t)b * BM;
@@ -138,7 +138,7 @@ void rows_kernel(RowsArgs a) {
   constexpr int NOUT = EPI == EPI_SWIGLU_FWD ? BN / 2 : BN;  // output columns of an n tile
 
   // ---- this workgroup's tiles: XCD x = blockIdx % 8 takes tiles [x T / 8, (x + 1) T / 8) of the T that exist
-  const int ntr = a.t_expert ? min(uni(a.num_tiles[0]), a.max_tiles) : (int)((a.dense_rows + BM - 1) / BM);
+  const int ntr = a.t_expert ? min(ctab(a.num_tiles, 0), a.max_tiles) : (int)((a.dense_rows + BM - 1) / BM);
   const int total = ntr * a.n_tiles;
   const int xcd = blockIdx.x % 8, nper = gridDim.x / 8;
   const int xbeg = (int)((int64_t)xcd * total / 8), xend = (int)((int64_t)(xcd + 1) * total / 8);
@@ -172,20 +172,18 @@ void rows_kernel(RowsArgs a) {
   const uint32_t nb_base = (uint32_t)nr * ldb2 + 16u * nc;
   bool ncol_ok[2] = {true, true};
   // gathered A: byte offsets of this lane's 8 source rows in the cursor's tile, and the raw row indices of the tile
-  // after it (read one tile ahead, so their latency hides behind a whole tile)
+  // after it (read one tile ahead, so their latency hides behind a whole tile) with that tile's row count.  Nothing
+  // reads a loaded index before set_ld uses it: a select on it here would wait for it at once, and with the in-order
+  // vector memory count that wait drains every copy load in flight.
   uint32_t a_off[8];
   const uint64_t magic = div_magic(GATHER ? a.a_div : 1);
-  int pf_t = -1;
+  int pf_rows = 0;
   int pf_idx[8];
   auto fetch_idx = [&](int t) {
     const Tile rt = row_tile(a, t / a.n_tiles);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 32 * i + kr;
-      const int v = a.a_rows[rt.row0 + min(r, rt.rows - 1)];  // rows past the tile: not read, marked -1
-      pf_idx[i] = r < rt.rows ? v : -1;
-    }
-    pf_t = t;
+    for (int i = 0; i < 8; ++i) pf_idx[i] = a.a_rows[rt.row0 + min(32 * i + kr, rt.rows - 1)];
+    pf_rows = rt.rows;
   };
   auto set_ld = [&]() {
     const int b = lt / a.n_tiles, nt = lt % a.n_tiles;
@@ -194,11 +192,10 @@ void rows_kernel(RowsArgs a) {
     const bf16_t* Bb = xe ? a.Bx : a.B + (int64_t)rt.expert * a.b_estride;
     const bf16_t* B2b = xe ? (a.B2x ? a.B2x : Bb) : (a.B2 ? a.B2 + (int64_t)rt.expert * a.b_estride : Bb);
     if (GATHER) {
-      if (pf_t != lt) fetch_idx(lt);
-      la = rsrc(a.A, a.a_nrows * (int64_t)a.lda * 2);
+      la = rsrc(a.A, a.a_nrows * (int64_t)a.lda * 2);  // pf_idx: tile lt's indices
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int src = pf_idx[i] >= 0 ? div_by(pf_idx[i], magic) : -1;
+        const int src = 32 * i + kr < pf_rows && pf_idx[i] >= 0 ? div_by(pf_idx[i], magic) : -1;  // rows past the tile: -1
         a_off[i] = src >= 0 ? (uint32_t)src * lda2 + 16u * kc : OOB;
       }
       if (lt + nper < xend) fetch_idx(lt + nper);
@@ -218,6 +215,7 @@ void rows_kernel(RowsArgs a) {
       for (int h = 0; h < 2; ++h) ncol_ok[h] = n0 + (EPI == EPI_SWIGLU_FWD ? 0 : NOUT / 2 * h) + 8 * nc < N;
     }
   };
+  if (GATHER) fetch_idx(lt);  // the first tile's indices; set_ld then reads each next tile's one tile ahead
   set_ld();
 
   u32x4 R[16];  // one stage of this lane's copies: A chunks 0..7, B chunks 8..15
@@ -584,7 +582,6 @@ void wgrad_kernel(WgradArgs a) {
   int k_cur = 0, t_cur = tile_of(0);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int fr = lane & 31, fh = lane >> 5;
   const int I = (int)a.I, N = (int)a.N;
   const uint32_t lda2 = (uint32_t)a.lda * 2u, ldb2 = (uint32_t)a.ldb * 2u;
   // copy geometry (both operands N-major): copy i takes reduction row 16 (i % 4) + nr of sub-tile i / 4, chunk nc
