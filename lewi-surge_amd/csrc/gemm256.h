@@ -776,15 +776,20 @@ void wgrad_kernel(WgradArgs a) {
                 f32x4{acc[i][2 * jp + jj][4 * q], acc[i][2 * jp + jj][4 * q + 1], acc[i][2 * jp + jj][4 * q + 2],
                       acc[i][2 * jp + jj][4 * q + 3]};
           }
+        // the pass's 64 columns: all before the split (one store to the first destination), all after it (one to
+        // the second), or across it (both, each lane's column on one side)
+        const int64_t seg = n0 + wn * 128 + 64 * jp;
+        const int side = seg + 64 <= split ? 0 : seg >= split ? 1 : 2;
 #pragma unroll
         for (int it2 = 0; it2 < 8; ++it2) {
           const int r = 4 * it2 + (el >> 4), cc = el & 15;
           const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((cc ^ (r & 15)) << 4));
-          const int64_t col = n0 + wn * 128 + 64 * jp + 4 * cc;
+          const int64_t col = seg + 4 * cc;
           const uint32_t rb = (uint32_t)(rbase + r) * pb;
-          __builtin_amdgcn_raw_buffer_store_b128(v, r1, col < split ? rb + (uint32_t)col * 4u : OOB, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(v, r2, col >= split && col < N ? rb + (uint32_t)(col - split) * 4u : OOB,
-                                                 0, 0);
+          const uint32_t o1 = col < split ? rb + (uint32_t)col * 4u : OOB;
+          const uint32_t o2 = col >= split && col < N ? rb + (uint32_t)(col - split) * 4u : OOB;
+          if (side != 1) __builtin_amdgcn_raw_buffer_store_b128(v, r1, o1, 0, 0);
+          if (side != 0) __builtin_amdgcn_raw_buffer_store_b128(v, r2, o2, 0, 0);
         }
       }
 #pragma unroll
