@@ -583,13 +583,13 @@ int lsurge_moe_fwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
 }
 
 // Backward.  Stream plan (caller's stream = critical path):
-//   main:  combine bwd -> [fork] -> down dgrad (+SwiGLU bwd) -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up
-//          wgrad
-//   s0:    after the fork: router wgrad (merged shared expert); with fs != f instead, from the start of the call, the
-//          shared expert's own backward: down dgrad, down wgrad, gate/up dgrad, gate/up wgrad
-//   s1:    after the fork: W_r transpose, chunk table, down wgrad (then the router backward when fs != f)
-// The helper chains overlap the dgrads of the main chain; the gate/up weight gradient runs after the join on its
-// own, and the dispatch backward reads dX_pad right after the GEMM that wrote it, while it is still in cache.
+//   main:  [fs != f: the shared expert's own backward: down dgrad, down wgrad, gate/up dgrad, gate/up wgrad] ->
+//          W_r transpose, chunk table -> combine bwd -> [fork] -> down dgrad (+SwiGLU bwd) -> gate/up dgrad ->
+//          dispatch bwd -> gate/up wgrad -> [join]
+//   s0:    after the fork, with a merged shared expert: router wgrad
+//   s1:    after the fork: down wgrad (then the router wgrad when the shared expert is not merged)
+// The helper chains overlap the dgrads of the main chain; nothing on the main chain reads their outputs, so the join
+// closes the call.  The dispatch backward reads dX_pad right after the GEMM that wrote it, while it is still in cache.
 // Every event record or wait on a stream idles it for several microseconds between the kernels around it, so the
 // critical stream gets one record (the fork, shared by both helpers) and one wait (the join: s1 waits for s0 first).
 int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* dy, const void* saved,
@@ -715,10 +715,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
   if (int rc = lsurge::gemm_rows_nk(KID_GEMM_GU_DGRAD, blocks, w.dgu, 2 * q.f, p->w_gate, p->w_up, q.f, q.f, q.d * q.f,
                                     2 * q.f, q.d, w.dx_pad, q.d, false, nullptr, nullptr, 0, st, false, xgu))
     return rc;
-  // join all helpers (s1 after s0, the critical stream after s1), then dx = gather-reduce of dX_pad + router dx term
-  // + shared-expert dx, one rounding
-  if (int rc = lsurge::stream_after(s1, s0, ev[4])) return rc;
-  if (int rc = fg.joined(lsurge::stream_after(st, s1, ev[5]))) return rc;
+  // main: dx = gather-reduce of dX_pad + router dx term + shared-expert dx, one rounding (all made on this stream)
   const bf16_t* shared_dx = q.merged ? w.dx_pad + q.P * q.d : (q.fs ? w.sdx : nullptr);
   if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT, shared_dx,
                                               g->dx, st))
@@ -734,7 +731,11 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                             w.part_gu_bytes, st, gather, ogu))
       return rc;
   }
-  return LSURGE_OK;
+  // join all helpers (s1 after s0, the critical stream after s1) at the end: nothing on the critical stream reads
+  // their outputs, and the wait lands next to the caller's following stream operation (the next forward's fork
+  // record), whose idle gap it then shares
+  if (int rc = lsurge::stream_after(s1, s0, ev[4])) return rc;
+  return fg.joined(lsurge::stream_after(st, s1, ev[5]));
 }
 
 size_t lsurge_moe_bwd_fp8_workspace_bytes(const lsurge_moe_shape* s) {
