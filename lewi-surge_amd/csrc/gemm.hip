@@ -293,7 +293,7 @@ __global__ __launch_bounds__(WC_THREADS) void wgrad_chunks_kernel(
   const int cbase = block_excl_scan(n, sh);
   const int nchunks = sh[TOT];
   const int sidx = block_excl_scan(n > 1 ? 1 : 0, sh);
-  if (e == 0) {
+  if (threadIdx.x == 0) {
     num_chunks[0] = min(nchunks, max_chunks);
     num_split[0] = sh[TOT];
   }
@@ -612,13 +612,25 @@ WgradChunkPlan wgrad_chunk_plan(int64_t M, int64_t E) {
   return p;
 }
 
+WgradChunkPlan wgrad_chunk_plan_dense(int64_t M, int64_t I, int64_t N) {
+  WgradChunkPlan p;
+  const int64_t tiles = ((I + g256::BM - 1) / g256::BM) * ((N + g256::BN - 1) / g256::BN);
+  const int64_t n = std::max<int64_t>(1, std::min<int64_t>({(g256::NWG + tiles - 1) / tiles, 16, M / 1024}));
+  p.R = (int)std::max<int64_t>(BM, ((M + n - 1) / n + BM - 1) / BM * BM);
+  p.max_chunks = (int)std::max<int64_t>(1, (M + p.R - 1) / p.R);
+  p.max_parts = p.max_chunks;
+  return p;
+}
+
 size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E) {
   return 4 * (size_t)p.max_chunks + 2 * (size_t)(E + 1) + (size_t)p.max_parts + 2;
 }
 
 int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
                        WgradChunks* ch, hipStream_t s, int64_t x_rows, int64_t x_row0, int row0_mult) {
-  LSURGE_REQUIRE(E >= 1 && E <= 256, "wgrad chunks: E=%d must be in [1, 256]", E);
+  LSURGE_REQUIRE((E >= 1 && E <= 256) || (E == 0 && x_rows >= 0), "wgrad chunks: E=%d must be in [1, 256] (0 with "
+                 "an extra expert)", E);
+  LSURGE_REQUIRE(E == 0 || (gs && block_off), "wgrad chunks: null group sizes");
   LSURGE_REQUIRE(x_rows < (1ll << 31) && x_row0 >= 0 && x_row0 < (1ll << 31), "wgrad chunks: extra expert rows");
   int32_t* t = table;
   ch->c_expert = t; t += p.max_chunks;
@@ -654,7 +666,7 @@ int gemm_wgrad_chunked(int kid, const WgradChunks& ch, int E, int64_t max_rows, 
   if (int rc = check_gemm_shape(I, N, "gemm_wgrad_chunked")) return rc;
   LSURGE_REQUIRE(xo.expert < 0 || (xo.C && (xo.C2 || !C2)), "gemm_wgrad_chunked: extra expert outputs missing");
   if (int rc = check_desc(max_rows * std::max(lda, ldb) * 2, "gemm_wgrad_chunked")) return rc;
-  LSURGE_REQUIRE(E >= 1 && ch.max_chunks >= 1, "gemm_wgrad_chunked: bad E / chunk table");
+  LSURGE_REQUIRE((E >= 1 || (E == 0 && xo.expert == 0)) && ch.max_chunks >= 1, "gemm_wgrad_chunked: bad E / chunk table");
   LSURGE_REQUIRE(part && part_bytes >= sizeof(float) * (size_t)ch.max_parts * I * N,
                  "gemm_wgrad_chunked: partial workspace %zu < %zu bytes", part_bytes,
                  sizeof(float) * (size_t)ch.max_parts * I * N);

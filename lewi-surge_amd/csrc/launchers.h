@@ -137,11 +137,14 @@ struct WgradChunks {
   int max_chunks, max_parts;
 };
 WgradChunkPlan wgrad_chunk_plan(int64_t M, int64_t E);
+// A dense weight gradient C[I, N] = A^T B over M rows as the chunk table's only (extra) expert: ceil(256 / tiles of
+// 256 x 256) chunks of equal rows (at most 16, at least 1024 rows each), so the chunks' tiles fill the GPU once.
+WgradChunkPlan wgrad_chunk_plan_dense(int64_t M, int64_t I, int64_t N);
 size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E);
 // builds the table (in `table`, wgrad_chunk_table_ints entries) from device group sizes and block offsets
 // Expert e's rows start at row0_mult block_off[e] (128 for the padded layout, 1 for a ragged one).  Extra expert
 // of the chunk table (id E, after the routed ones): x_rows rows from row x_row0 (x_rows < 0: none); its gradient
-// goes to C / C2 of an ExtraOut.
+// goes to C / C2 of an ExtraOut.  E = 0 with an extra expert is a dense weight gradient (gs, block_off unused).
 int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
                        WgradChunks* ch, hipStream_t s, int64_t x_rows = -1, int64_t x_row0 = 0,
                        int row0_mult = LSURGE_BLOCK_ROWS);

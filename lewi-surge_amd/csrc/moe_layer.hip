@@ -132,8 +132,9 @@ struct BwdWs {
   float* dl;
   float* dweights;
   float* wpad;        // routing weight of each padded row (the down GEMMs scale by it instead of reading dY_pad)
-  void* part;         // split-K partials of the shared-expert weight gradients (their own stream)
+  void* part;         // chunk partials of a shared expert's own dense weight gradients
   size_t part_bytes;
+  int32_t* dense_tab;  // their chunk table (the shared expert as the only, extra expert of a dense table)
   void* part_r;       // split-K partials of the router weight gradient (another stream)
   size_t part_r_bytes;
   lsurge::WgradChunkPlan cplan;  // chunk table of the routed weight gradients and the partials of split experts
@@ -157,13 +158,17 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   w->dl = c.take<float>(q.M);
   w->dweights = c.take<float>(q.M);
   w->wpad = c.take<float>(q.PT);
-  size_t part = 0;
+  size_t part = 0, tab = 0;
   if (q.fs && !q.merged) {
-    part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.d, 2 * q.fs, dense_splits(q.T, q.d, 2 * q.fs)));
-    part = std::max(part, lsurge::wgrad_workspace_bytes(1, q.fs, q.d, dense_splits(q.T, q.fs, q.d)));
+    const lsurge::WgradChunkPlan pg = lsurge::wgrad_chunk_plan_dense(q.T, q.d, 2 * q.fs);
+    const lsurge::WgradChunkPlan pd = lsurge::wgrad_chunk_plan_dense(q.T, q.fs, q.d);
+    part = std::max(lsurge::wgrad_chunked_workspace_bytes(pg, q.d, 2 * q.fs),
+                    lsurge::wgrad_chunked_workspace_bytes(pd, q.fs, q.d));
+    tab = std::max(lsurge::wgrad_chunk_table_ints(pg, 0), lsurge::wgrad_chunk_table_ints(pd, 0));
   }
   w->part_bytes = part;
   w->part = c.take<char>(part);
+  w->dense_tab = c.take<int32_t>(tab);
   w->part_r_bytes = lsurge::wgrad_workspace_bytes(1, q.d, q.E, dense_splits(q.T, q.d, q.E));
   w->part_r = c.take<char>(w->part_r_bytes);
   w->cplan = q.merged ? lsurge::wgrad_chunk_plan(q.M + q.T, q.E + 1) : lsurge::wgrad_chunk_plan(q.M, q.E);
@@ -636,16 +641,30 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
     if (int rc = lsurge::gemm_rows_nk(KID_SHARED_DOWN_DGRAD, dense, dy, q.d, p->ws_down, nullptr, 0, q.d, 0, q.d, q.fs,
                                       w.sdgu, 2 * q.fs, true, sv.sg, sv.su, q.fs, s0))
       return rc;
-    int S = dense_splits(q.T, q.fs, q.d);
-    if (int rc = lsurge::gemm_wgrad(KID_SHARED_DOWN_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, sv.sh, q.fs, dy, q.d, q.fs,
-                                    q.d, g->dws_down, nullptr, 0, q.d, 0, S, w.part, w.part_bytes, s0))
+    // the dense weight gradients as chunk tables of one (extra) expert: equal row chunks whose tiles fill the GPU
+    // once, reduced from f32 partials in chunk order (the persistent kernel, or the classic one, on the same table)
+    lsurge::WgradChunks dch;
+    lsurge::ExtraOut dxo;
+    dxo.expert = 0;
+    dxo.C = g->dws_down;
+    if (int rc = lsurge::build_wgrad_chunks(nullptr, nullptr, 0, lsurge::wgrad_chunk_plan_dense(q.T, q.fs, q.d),
+                                           w.dense_tab, &dch, s0, q.T, 0, 1))
+      return rc;
+    if (int rc = lsurge::gemm_wgrad_chunked(KID_SHARED_DOWN_WGRAD, dch, 0, q.T, sv.sh, q.fs, dy, q.d, q.fs, q.d,
+                                            nullptr, nullptr, 0, q.d, 0, w.part, w.part_bytes, s0,
+                                            lsurge::RowGather(), dxo))
       return rc;
     if (int rc = lsurge::gemm_rows_nk(KID_SHARED_GU_DGRAD, dense, w.sdgu, 2 * q.fs, p->ws_gate, p->ws_up, q.fs, q.fs, 0,
                                       2 * q.fs, q.d, w.sdx, q.d, false, nullptr, nullptr, 0, s0))
       return rc;
-    S = dense_splits(q.T, q.d, 2 * q.fs);
-    if (int rc = lsurge::gemm_wgrad(KID_SHARED_GU_WGRAD, 1, nullptr, 1, nullptr, q.T, q.T, p->x, q.d, w.sdgu, 2 * q.fs,
-                                    q.d, 2 * q.fs, g->dws_gate, g->dws_up, q.fs, q.fs, 0, S, w.part, w.part_bytes, s0))
+    dxo.C = g->dws_gate;
+    dxo.C2 = g->dws_up;
+    if (int rc = lsurge::build_wgrad_chunks(nullptr, nullptr, 0, lsurge::wgrad_chunk_plan_dense(q.T, q.d, 2 * q.fs),
+                                           w.dense_tab, &dch, s0, q.T, 0, 1))
+      return rc;
+    if (int rc = lsurge::gemm_wgrad_chunked(KID_SHARED_GU_WGRAD, dch, 0, q.T, p->x, q.d, w.sdgu, 2 * q.fs, q.d,
+                                            2 * q.fs, nullptr, nullptr, q.fs, q.fs, 0, w.part, w.part_bytes, s0,
+                                            lsurge::RowGather(), dxo))
       return rc;
   }
   // main, before any GEMM: W_r^T for the router's dx term and the chunk table of the weight gradients (read by both
