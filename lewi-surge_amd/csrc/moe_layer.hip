@@ -71,6 +71,8 @@ struct Saved {
   int32_t *t_expert, *t_rows, *t_row0, *num_tiles;
   bf16_t *g, *u, *h, *y_pad;
   bf16_t *sg, *su, *sh, *sy;  // shared expert run on its own: gate, up, h, output
+  bf16_t* w_rT;               // W_r^T [E, d]: the dispatch backward's router dx term, made by the forward off the
+                              // critical stream
   // FP8 forward: x [T, d], routed h [P, f] (padded rows) and shared h [T, fs] in E4M3, and their scale_inv, the
   // operands the FP8 backward's weight gradients read again.  Carved after the bf16 layout and only for the FP8
   // path (null otherwise), so a bf16 buffer is a prefix of an FP8 one.
@@ -106,6 +108,7 @@ size_t carve_saved(const Dims& q, void* base, Saved* sv, bool fp8) {
   sv->su = c.take<bf16_t>(own * q.fs);
   sv->sh = c.take<bf16_t>(own * q.fs);
   sv->sy = c.take<bf16_t>(own * q.d);
+  sv->w_rT = c.take<bf16_t>(q.E * q.d);
   if (fp8) {
     sv->xq = c.take<uint8_t>(q.T * q.d);
     sv->hq = c.take<uint8_t>(q.P * q.f);
@@ -128,7 +131,7 @@ int dense_splits(int64_t rows, int64_t I, int64_t N) {
 }
 
 struct BwdWs {
-  bf16_t *dy_pad, *dgu, *dx_pad, *sdgu, *sdx, *dlog, *w_rT;
+  bf16_t *dy_pad, *dgu, *dx_pad, *sdgu, *sdx, *dlog;
   float* dl;
   float* dweights;
   float* wpad;        // routing weight of each padded row (the down GEMMs scale by it instead of reading dY_pad)
@@ -154,7 +157,6 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   w->sdgu = c.take<bf16_t>(own * 2 * q.fs);
   w->sdx = c.take<bf16_t>(own * q.d);
   w->dlog = c.take<bf16_t>(q.T * q.E);
-  w->w_rT = c.take<bf16_t>(q.E * q.d);
   w->dl = c.take<float>(q.M);
   w->dweights = c.take<float>(q.M);
   w->wpad = c.take<float>(q.PT);
@@ -461,11 +463,16 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   const bool early = !w8 && q.fs && s0 != st;
   if (early)
     if (int rc = lsurge::stream_after(s0, st, fg.f.ev[3])) return rc;
+  // W_r^T for the backward's router dx term (saved): on the helper stream when it forks here (off the critical path),
+  // else first on the caller's stream
+  if (!w8)
+    if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, sv.w_rT, early ? s0 : st)) return rc;
   // FP8: x's quantisation (memory-bound) runs on s0 beside the router (VALU-bound); the caller's stream waits for
   // it (event ev[2]) only before the routed gate/up GEMM
   if (w8) {
     carve_fp8ws(q, (char*)workspace + hist_bytes, &f8);
     if (int rc = lsurge::stream_after(s0, st, fg.f.ev[3])) return rc;
+    if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, sv.w_rT, s0)) return rc;
     if (int rc = lsurge::fp8_quantize_impl(p->x, 1, q.T, q.d, false, sv.xq, sv.f8_sinv, f8.partial, s0, f8.slots, 2))
       return rc;
     if (s0 != st && hipEventRecord(fg.f.ev[2], s0) != hipSuccess)
@@ -667,10 +674,10 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                             lsurge::RowGather(), dxo))
       return rc;
   }
-  // main, before any GEMM: W_r^T for the router's dx term and the chunk table of the weight gradients (read by both
-  // routed weight gradients).  Both are one-workgroup-class kernels: issued on a helper stream beside the persistent
-  // GEMMs (one workgroup per CU, the whole LDS and register file) they wait for a whole GEMM to drain first.
-  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)q.d, (int)q.E, w.w_rT, st)) return rc;
+  // main, before any GEMM: the chunk table of the weight gradients (read by both routed weight gradients), a
+  // one-workgroup kernel: issued on a helper stream beside the persistent GEMMs (one workgroup per CU, the whole LDS
+  // and register file) it would wait for a whole GEMM to drain first.  (W_r^T, the router's dx term, was made by the
+  // forward.)
   lsurge::WgradChunks chunks;
   if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, st,
                                          q.merged ? q.T : -1, q.P))
@@ -736,7 +743,7 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
     return rc;
   // main: dx = gather-reduce of dX_pad + router dx term + shared-expert dx, one rounding (all made on this stream)
   const bf16_t* shared_dx = q.merged ? w.dx_pad + q.P * q.d : (q.fs ? w.sdx : nullptr);
-  if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, w.w_rT, shared_dx,
+  if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, q.d, (int)q.k, sv.slot, q.T, w.dl, sv.sel, sv.w_rT, shared_dx,
                                               g->dx, st))
     return rc;
   // main: gate/up wgrad: [dW_gate | dW_up][e] = x_e^T [dG | dU]_e
@@ -812,8 +819,7 @@ int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
   if (s0 != st && hipStreamWaitEvent(s0, ev[0], 0) != hipSuccess)
     return lsurge::set_error(LSURGE_ERR_LAUNCH, "moe_bwd_fp8: hipStreamWaitEvent failed");
 
-  // s1: W_r^T and the chunk table
-  if (int rc = lsurge::launch_transpose_bf16(p->w_r, (int)d, (int)q.E, w.w_rT, s1)) return rc;
+  // s1: the chunk table (W_r^T was made by the forward)
   lsurge::WgradChunks chunks;
   if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, s1)) return rc;
 
@@ -894,7 +900,7 @@ int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
   // E4M3 x rows gathered through row_src
   if (int rc = lsurge::stream_after(s1, s0, ev[4])) return rc;
   if (int rc = fg.joined(lsurge::stream_after(st, s1, ev[5]))) return rc;
-  if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, d, (int)q.k, sv.slot, T, w.dl, sv.sel, w.w_rT,
+  if (int rc = lsurge::launch_dispatch_bwd_pad(w.dx_pad, d, (int)q.k, sv.slot, T, w.dl, sv.sel, sv.w_rT,
                                               fs ? f8.sdx : nullptr, g->dx, st))
     return rc;
   lsurge::RowGather gather;
