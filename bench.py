@@ -225,7 +225,7 @@ def launch_roles(c):
         "router_select_lane_kernel<16>": ["router_select"], "router_select_kernel<1>": ["router_select"],
         "router_select_kernel<2>": ["router_select"], "router_select_kernel<4>": ["router_select"],
         "layout_hist_kernel": ["layout_hist"], "layout_scan_kernel": ["layout_scan"],
-        "layout_rank_kernel": ["layout_rank"],
+        "layout_rank_kernel": ["layout_rank"], "layout_fused_kernel": ["layout_rank"],
         "gemm_rows_kernel<1,1>": (["shared_gu_fwd"] if fs else []) + ["gemm_gu_fwd"],
         "gemm_rows_kernel<1,0>": (["shared_down_fwd"] if fs else []) + ["gemm_down_fwd"],
         "combine_pad_kernel<2,6,1>": ["combine_fwd"], "combine_pad_kernel<2,8,1>": ["combine_fwd"],

@@ -218,9 +218,9 @@ typedef struct {
   float* dweights; /* [t, k] f32 gradient of the routing weights (may be NULL) */
 } lsurge_moe_grads;
 
-/* Bytes of the `saved` buffer the forward fills and the backward reads (activations, layout and W_r^T).  The FP8
- * forward also keeps its E4M3 x and h there and needs lsurge_moe_saved_bytes_fp8 (the bf16 layout is a prefix of
- * it). */
+/* Bytes of the `saved` buffer the forward fills and the backward reads (activations, layout, the weight gradients'
+ * chunk table and W_r^T).  The FP8 forward also keeps its E4M3 x and h there and needs lsurge_moe_saved_bytes_fp8
+ * (the bf16 layout is a prefix of it). */
 size_t lsurge_moe_saved_bytes(const lsurge_moe_shape* s);
 size_t lsurge_moe_saved_bytes_fp8(const lsurge_moe_shape* s);
 /* Scratch bytes for forward and backward (not kept between calls). */

@@ -3,6 +3,7 @@
 // modal/padded_gmm.py:45-69 (padded_ragged_dot and its gather-only VJP).
 #include <mutex>
 
+#include "chunk_table.h"
 #include "gemm256.h"
 #include "gemm_kernels.h"
 #include "launchers.h"
@@ -272,43 +273,18 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sh) {  // WC_THREADS 
   return base + x - v;
 }
 
-__global__ __launch_bounds__(WC_THREADS) void wgrad_chunks_kernel(
-    const int32_t* __restrict__ gs, const int32_t* __restrict__ block_off, int row0_mult, int E, int R,
-    int max_chunks, int max_parts, int x_rows, int x_row0, int32_t* __restrict__ c_expert, int32_t* __restrict__ c_row0,
-    int32_t* __restrict__ c_rows, int32_t* __restrict__ c_part, int32_t* __restrict__ num_chunks,
-    int32_t* __restrict__ e_pbase, int32_t* __restrict__ e_nparts, int32_t* __restrict__ split_list,
-    int32_t* __restrict__ num_split) {
+__global__ __launch_bounds__(WC_THREADS) void wgrad_chunks_kernel(const int32_t* __restrict__ gs,
+                                                                   const int32_t* __restrict__ block_off,
+                                                                   int row0_mult, int E, lsurge::ChunkTableOut o) {
   __shared__ int sh[WC_THREADS / 64 + 1];
   constexpr int TOT = WC_THREADS / 64;
-  // the extra expert (the largest: every token) takes the first chunks, so its long tiles start first
-  const bool has_x = x_rows >= 0;
-  const int e = has_x ? (threadIdx.x == 0 ? E : (int)threadIdx.x - 1) : (int)threadIdx.x;
-  const bool routed = e < E && !(has_x && threadIdx.x == 0), extra = has_x && threadIdx.x == 0;
-  const int g = routed ? max(gs[e], 0) : (extra ? x_rows : 0);
-  const int r0 = routed ? block_off[e] * row0_mult : x_row0;
-  int n = (routed || extra) ? max(1, (g + R - 1) / R) : 0;
-  const int pbase = block_excl_scan(n > 1 ? n : 0, sh);
-  const bool fits = sh[TOT] <= max_parts;
-  if (!fits && n > 1) n = 1;
-  const int cbase = block_excl_scan(n, sh);
-  const int nchunks = sh[TOT];
-  const int sidx = block_excl_scan(n > 1 ? 1 : 0, sh);
-  if (threadIdx.x == 0) {
-    num_chunks[0] = min(nchunks, max_chunks);
-    num_split[0] = sh[TOT];
-  }
-  if (!routed && !extra) return;
-  e_pbase[e] = pbase;
-  e_nparts[e] = n > 1 ? n : 0;
-  if (n > 1) split_list[sidx] = e;
-  for (int j = 0; j < n; ++j) {
-    const int c = cbase + j;
-    if (c >= max_chunks) break;
-    c_expert[c] = e;
-    c_row0[c] = r0 + j * R;
-    c_rows[c] = n > 1 ? min(R, g - j * R) : g;
-    c_part[c] = n > 1 ? pbase + j : -1;
-  }
+  lsurge::write_chunk_table(
+      o, E, [&](int e) { return gs[e]; }, [&](int e) { return block_off[e] * row0_mult; },
+      [&](int v, int* total) {
+        const int base = block_excl_scan(v, sh);
+        *total = sh[TOT];
+        return base;
+      });
 }
 
 // dW of each split expert = its chunk partials summed in chunk order (f32, deterministic), -> C (and C2 for
@@ -626,29 +602,52 @@ size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E) {
   return 4 * (size_t)p.max_chunks + 2 * (size_t)(E + 1) + (size_t)p.max_parts + 2;
 }
 
+ChunkTableOut chunk_table_out(int32_t* table, int E, const WgradChunkPlan& p, int64_t x_rows, int64_t x_row0) {
+  ChunkTableOut o;
+  int32_t* t = table;
+  o.c_expert = t; t += p.max_chunks;
+  o.c_row0 = t; t += p.max_chunks;
+  o.c_rows = t; t += p.max_chunks;
+  o.c_part = t; t += p.max_chunks;
+  o.e_pbase = t; t += E + 1;
+  o.e_nparts = t; t += E + 1;
+  o.split_list = t; t += p.max_parts;
+  o.num_chunks = t;
+  o.num_split = t + 1;
+  o.R = p.R;
+  o.max_chunks = p.max_chunks;
+  o.max_parts = p.max_parts;
+  o.x_rows = (int)x_rows;
+  o.x_row0 = (int)x_row0;
+  return o;
+}
+
+WgradChunks chunk_table_view(const ChunkTableOut& o) {
+  WgradChunks ch;
+  ch.c_expert = o.c_expert;
+  ch.c_row0 = o.c_row0;
+  ch.c_rows = o.c_rows;
+  ch.c_part = o.c_part;
+  ch.num_chunks = o.num_chunks;
+  ch.e_pbase = o.e_pbase;
+  ch.e_nparts = o.e_nparts;
+  ch.split_list = o.split_list;
+  ch.num_split = o.num_split;
+  ch.max_chunks = o.max_chunks;
+  ch.max_parts = o.max_parts;
+  return ch;
+}
+
 int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
                        WgradChunks* ch, hipStream_t s, int64_t x_rows, int64_t x_row0, int row0_mult) {
   LSURGE_REQUIRE((E >= 1 && E <= 256) || (E == 0 && x_rows >= 0), "wgrad chunks: E=%d must be in [1, 256] (0 with "
                  "an extra expert)", E);
   LSURGE_REQUIRE(E == 0 || (gs && block_off), "wgrad chunks: null group sizes");
   LSURGE_REQUIRE(x_rows < (1ll << 31) && x_row0 >= 0 && x_row0 < (1ll << 31), "wgrad chunks: extra expert rows");
-  int32_t* t = table;
-  ch->c_expert = t; t += p.max_chunks;
-  ch->c_row0 = t; t += p.max_chunks;
-  ch->c_rows = t; t += p.max_chunks;
-  ch->c_part = t; t += p.max_chunks;
-  ch->e_pbase = t; t += E + 1;
-  ch->e_nparts = t; t += E + 1;
-  ch->split_list = t; t += p.max_parts;
-  ch->num_chunks = t;
-  ch->num_split = t + 1;
-  ch->max_chunks = p.max_chunks;
-  ch->max_parts = p.max_parts;
+  const ChunkTableOut o = chunk_table_out(table, E, p, x_rows, x_row0);
+  *ch = chunk_table_view(o);
   LSURGE_LAUNCH(KID_MISC, s,
-                hipLaunchKernelGGL(wgrad_chunks_kernel, dim3(1), dim3(WC_THREADS), 0, s, gs, block_off, row0_mult, E, p.R,
-                                   p.max_chunks, p.max_parts, (int)x_rows, (int)x_row0, (int32_t*)ch->c_expert, (int32_t*)ch->c_row0, (int32_t*)ch->c_rows,
-                                   (int32_t*)ch->c_part, (int32_t*)ch->num_chunks, (int32_t*)ch->e_pbase,
-                                   (int32_t*)ch->e_nparts, (int32_t*)ch->split_list, (int32_t*)ch->num_split));
+                hipLaunchKernelGGL(wgrad_chunks_kernel, dim3(1), dim3(WC_THREADS), 0, s, gs, block_off, row0_mult, E, o));
   return LSURGE_OK;
 }
 

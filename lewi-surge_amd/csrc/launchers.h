@@ -17,6 +17,14 @@ int router_topk_impl(const void* x, const void* w_r, const float* bias, int64_t 
 bool router_fused_ok(int64_t d, int64_t e, int64_t k);
 
 // ---- routing layout (layout.hip)
+// Device-side outputs of a weight-gradient chunk table (the entries of wgrad_chunk_table_ints; see WgradChunks) and
+// the plan values it is written with: R rows per chunk, the bounds, and the extra expert's rows (x_rows < 0: none)
+// from row x_row0.  c_expert == nullptr: no table.
+struct ChunkTableOut {
+  int32_t *c_expert = nullptr, *c_row0 = nullptr, *c_rows = nullptr, *c_part = nullptr, *e_pbase = nullptr,
+          *e_nparts = nullptr, *split_list = nullptr, *num_chunks = nullptr, *num_split = nullptr;
+  int R = 0, max_chunks = 0, max_parts = 0, x_rows = -1, x_row0 = 0;
+};
 // Optional 256-row tile table of the layer's grouped GEMMs, written by the layout's scan kernel: expert e gets
 // ceil(gs[e] / 256) tiles, each two consecutive 128-row blocks of its own (the last may hold one block); TS tiles of
 // a shared expert carried as expert E follow (rows P + 256 j of its T rows; row_src of those rows = t k); entries up
@@ -29,6 +37,9 @@ struct LayoutTiles {
   int TB = 0, TS = 0;
   int64_t P = 0, T = 0;
   int k = 1;
+  // optional: the weight gradients' chunk table over the padded layout (expert e's rows from 128 block_off[e]),
+  // written by the layout too, so the backward launches no kernel for it; needs E + 1 <= 1024
+  ChunkTableOut chunks;
 };
 // Optional per-chunk expert histograms made by the caller (the fused router): hist [nchunk][E] for chunks of
 // waves x 64 consecutive slots (overwritten with the per-expert chunk bases); the layout then skips its own.
@@ -148,6 +159,11 @@ size_t wgrad_chunk_table_ints(const WgradChunkPlan& p, int64_t E);
 int build_wgrad_chunks(const int32_t* gs, const int32_t* block_off, int E, const WgradChunkPlan& p, int32_t* table,
                        WgradChunks* ch, hipStream_t s, int64_t x_rows = -1, int64_t x_row0 = 0,
                        int row0_mult = LSURGE_BLOCK_ROWS);
+// The table's entries inside `table` for a plan and an extra expert, and the view the GEMMs read, without a launch
+// (for a table another kernel writes, such as the layout's)
+ChunkTableOut chunk_table_out(int32_t* table, int E, const WgradChunkPlan& p, int64_t x_rows = -1,
+                              int64_t x_row0 = 0);
+WgradChunks chunk_table_view(const ChunkTableOut& o);
 struct ExtraOut {
   int expert = -1;
   float* C = nullptr;

@@ -13,6 +13,9 @@
 //         kernel in the layer); each wave walks its slots 64 at a time in ascending slot order:
 //         lanes with the same expert are found with 8 ballots over the expert-id bits, the rank inside
 //         the wave is popcount(peers below me), and a per-wave LDS counter advances by popcount(peers).
+// In the layer, when the fused router's histograms are small, one kernel does it all (layout_fused_kernel): each
+// rank workgroup sums the histograms itself, so the scan's launch between the router and the ranks goes away.
+#include "chunk_table.h"
 #include "launchers.h"
 
 namespace {
@@ -69,12 +72,82 @@ __device__ __forceinline__ int block_scan_excl(int v, int* ws, int* total) {
   return base + x - v;
 }
 
+// The scan's tables from the expert-level results in LDS (gs_s [E], boff_s and tb_s [E + 1]: block and 256-row tile
+// bases, totals last): the block table, the padding markers of row_src, the tile table and the shared expert's
+// row_src, each over its entries i0, i0 + stride, ... (one workgroup's threads, or those of every workgroup).
+__device__ __forceinline__ void write_layout_tables(int E, const int32_t* gs_s, const int32_t* boff_s,
+                                                    const int32_t* tb_s, int32_t* __restrict__ row_src,
+                                                    int32_t* __restrict__ blk_expert, int32_t* __restrict__ blk_rows,
+                                                    int32_t* __restrict__ num_blocks, int max_blocks,
+                                                    const lsurge::LayoutTiles& tiles, int i0, int stride) {
+  const int nbt = boff_s[E], ntt = tb_s[E];
+  if (i0 == 0 && num_blocks) num_blocks[0] = nbt;
+  if (blk_expert) {
+    // block table: expert e with boff[e] <= b < boff[e + 1] (skips empty experts)
+    for (int b = i0; b < max_blocks; b += stride) {
+      if (b >= nbt) {
+        blk_expert[b] = -1;
+        blk_rows[b] = 0;
+        continue;
+      }
+      int lo = 0, hi = E - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (boff_s[mid] <= b) lo = mid;
+        else hi = mid - 1;
+      }
+      blk_expert[b] = lo;
+      blk_rows[b] = min(BLK, gs_s[lo] - (b - boff_s[lo]) * BLK);
+    }
+    // padding rows of each expert's last block: row_src = -1
+    for (int i = i0; i < E * BLK; i += stride) {
+      const int e = i / BLK, r = i % BLK;
+      const int ge = gs_s[e], pad = (ge + BLK - 1) / BLK * BLK - ge;
+      if (r < pad) row_src[(int64_t)BLK * boff_s[e] + ge + r] = -1;
+    }
+  }
+  if (tiles.t_expert) {
+    // routed tiles (two consecutive blocks of one expert; the last may hold a single block), then the shared expert's
+    // (expert E, rows P + 256 j), then empty entries up to the bound TB + TS
+    const int total = min(ntt, tiles.TB);  // never clipped for layout-made sizes (they sum to M)
+    for (int t = i0; t < tiles.TB + tiles.TS; t += stride) {
+      int ex = -1, r0 = 0, rows = 0;
+      if (t < total) {
+        int lo = 0, hi = E - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (tb_s[mid] <= t) lo = mid;
+          else hi = mid - 1;
+        }
+        const int j = t - tb_s[lo];
+        ex = lo;
+        r0 = BLK * boff_s[lo] + 2 * BLK * j;
+        rows = min(2 * BLK, gs_s[lo] - 2 * BLK * j);
+      } else if (t < total + tiles.TS) {
+        const int j = t - total;
+        ex = E;
+        r0 = (int)(tiles.P + 2 * BLK * (int64_t)j);
+        rows = (int)min((int64_t)2 * BLK, tiles.T - 2 * BLK * (int64_t)j);
+      }
+      tiles.t_expert[t] = ex;
+      tiles.t_row0[t] = r0;
+      tiles.t_rows[t] = rows;
+    }
+    if (tiles.TS > 0)
+      for (int64_t r = i0; r < tiles.T; r += stride) row_src[tiles.P + r] = (int32_t)(r * tiles.k);
+    if (i0 == 0) {
+      tiles.num_tiles[0] = total;
+      tiles.num_tiles[1] = total + tiles.TS;
+    }
+  }
+}
+
 // One workgroup of 1024 threads (at least E).  hist [nchunk][E] is overwritten with the exclusive per-expert
 // chunk base.
 // Thread (e, j) owns expert e's chunks [j cpt, (j + 1) cpt), kept in registers between the two passes (up to
 // LS_REG chunks; more are read again).  The expert-level scans are block-wide shuffle scans, and the padding
 // markers of row_src are spread over all threads.  With tiles.t_expert set it also writes the 256-row tile table of
-// the layer's grouped GEMMs (see LayoutTiles).
+// the layer's grouped GEMMs (see LayoutTiles), and with tiles.chunks.c_expert the weight gradients' chunk table.
 constexpr int LS_REG = 16, LS_BATCH = 32;
 __global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__ hist, int nchunk, int E,
                                                            int32_t* __restrict__ group_sizes,
@@ -165,67 +238,14 @@ __global__ __launch_bounds__(1024) void layout_scan_kernel(int32_t* __restrict__
   if (tid == 0) {
     boff_s[E] = nbt;
     tb_s[E] = ntt;
-    if (num_blocks) num_blocks[0] = nbt;
   }
   __syncthreads();
-  if (blk_expert) {
-    // block table: expert e with boff[e] <= b < boff[e + 1] (skips empty experts)
-    for (int b = tid; b < max_blocks; b += blockDim.x) {
-      if (b >= nbt) {
-        blk_expert[b] = -1;
-        blk_rows[b] = 0;
-        continue;
-      }
-      int lo = 0, hi = E - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (boff_s[mid] <= b) lo = mid;
-        else hi = mid - 1;
-      }
-      blk_expert[b] = lo;
-      blk_rows[b] = min(BLK, gs_s[lo] - (b - boff_s[lo]) * BLK);
-    }
-    // padding rows of each expert's last block: row_src = -1
-    for (int i = tid; i < E * BLK; i += blockDim.x) {
-      const int e = i / BLK, r = i % BLK;
-      const int ge = gs_s[e], pad = (ge + BLK - 1) / BLK * BLK - ge;
-      if (r < pad) row_src[(int64_t)BLK * boff_s[e] + ge + r] = -1;
-    }
-  }
-  if (tiles.t_expert) {
-    // routed tiles (two consecutive blocks of one expert; the last may hold a single block), then the shared expert's
-    // (expert E, rows P + 256 j), then empty entries up to the bound TB + TS
-    const int total = min(ntt, tiles.TB);  // never clipped for layout-made sizes (they sum to M)
-    for (int t = tid; t < tiles.TB + tiles.TS; t += blockDim.x) {
-      int ex = -1, r0 = 0, rows = 0;
-      if (t < total) {
-        int lo = 0, hi = E - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (tb_s[mid] <= t) lo = mid;
-          else hi = mid - 1;
-        }
-        const int j = t - tb_s[lo];
-        ex = lo;
-        r0 = BLK * boff_s[lo] + 2 * BLK * j;
-        rows = min(2 * BLK, gs_s[lo] - 2 * BLK * j);
-      } else if (t < total + tiles.TS) {
-        const int j = t - total;
-        ex = E;
-        r0 = (int)(tiles.P + 2 * BLK * (int64_t)j);
-        rows = (int)min((int64_t)2 * BLK, tiles.T - 2 * BLK * (int64_t)j);
-      }
-      tiles.t_expert[t] = ex;
-      tiles.t_row0[t] = r0;
-      tiles.t_rows[t] = rows;
-    }
-    if (tiles.TS > 0)
-      for (int64_t r = tid; r < tiles.T; r += blockDim.x) row_src[tiles.P + r] = (int32_t)(r * tiles.k);
-    if (tid == 0) {
-      tiles.num_tiles[0] = total;
-      tiles.num_tiles[1] = total + tiles.TS;
-    }
-  }
+  write_layout_tables(E, gs_s, boff_s, tb_s, row_src, blk_expert, blk_rows, num_blocks, max_blocks, tiles, tid,
+                      (int)blockDim.x);
+  if (tiles.chunks.c_expert)
+    lsurge::write_chunk_table(
+        tiles.chunks, E, [&](int e) { return gs_s[e]; }, [&](int e) { return BLK * boff_s[e]; },
+        [&](int v, int* total) { return block_scan_excl(v, ws, total); });
 }
 
 __device__ __forceinline__ uint64_t peers_of(int key, int nbits) {
@@ -237,19 +257,17 @@ __device__ __forceinline__ uint64_t peers_of(int key, int nbits) {
   return m;
 }
 
-// One workgroup per chunk of (blockDim.x / 64) * per_wave slots (LT_CHUNK for the layout's own histograms, 64 k
-// when the fused router made them: one 64-slot pass per wave).
-__global__ __launch_bounds__(1024) void layout_rank_kernel(
-    const int32_t* __restrict__ flat, int64_t M, int E, const int32_t* __restrict__ chunk_base,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ block_off, int nbits, int per_wave,
-    int32_t* __restrict__ order, int32_t* __restrict__ pos, int32_t* __restrict__ slot,
-    int32_t* __restrict__ row_src) {
-  extern __shared__ int32_t sh[];  // cnt[waves][E] (per-wave running rank base inside the expert)
-  int32_t* cnt = sh;
+// Ranks of one chunk's slots: chunk blockIdx.x of (blockDim.x / 64) * per_wave slots, each wave walking its own
+// per_wave slots 64 at a time in ascending order.  cnt [waves][E] in LDS must be zero (and the zeroing made visible
+// with a barrier); base(e) is the rank in expert e of the chunk's first slot, off(e) and boff(e) the expert's offset
+// and block offset.
+template <class Base, class Off, class Boff>
+__device__ __forceinline__ void rank_chunk(const int32_t* __restrict__ flat, int64_t M, int E, int32_t* cnt, Base base,
+                                           Off off, Boff boff, int nbits, int per_wave, int32_t* __restrict__ order,
+                                           int32_t* __restrict__ pos, int32_t* __restrict__ slot,
+                                           int32_t* __restrict__ row_src) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = (int)blockDim.x >> 6;
   const int64_t cbase = (int64_t)blockIdx.x * nw * per_wave;
-  for (int i = tid; i < nw * E; i += blockDim.x) cnt[i] = 0;
-  __syncthreads();
   // per-wave histograms of this chunk
   for (int r = 0; r < per_wave; r += 64) {
     const int64_t i = cbase + (int64_t)wv * per_wave + r + lane;
@@ -261,7 +279,7 @@ __global__ __launch_bounds__(1024) void layout_rank_kernel(
   __syncthreads();
   // exclusive scan over waves, seeded with the chunk base (rank of the first slot of this chunk in e)
   for (int e = tid; e < E; e += blockDim.x) {
-    int run = chunk_base[(int64_t)blockIdx.x * E + e];
+    int run = base(e);
     for (int w = 0; w < nw; ++w) {
       const int v = cnt[w * E + e];
       cnt[w * E + e] = run;
@@ -288,16 +306,120 @@ __global__ __launch_bounds__(1024) void layout_rank_kernel(
     if (valid && (peers >> lane) == 1ull) my[e] = rank + 1;
     __builtin_amdgcn_wave_barrier();
     if (valid) {
-      const int p = offsets[e] + rank;
+      const int p = off(e) + rank;
       if (pos) pos[i] = p;
       if (order) order[p] = (int32_t)i;
       if (slot) {
-        const int sl = BLK * block_off[e] + rank;
+        const int sl = BLK * boff(e) + rank;
         slot[i] = sl;
         if (row_src) row_src[sl] = (int32_t)i;
       }
     }
   }
+}
+
+// One workgroup per chunk of (blockDim.x / 64) * per_wave slots (LT_CHUNK for the layout's own histograms, 64 k
+// when the fused router made them: one 64-slot pass per wave).
+__global__ __launch_bounds__(1024) void layout_rank_kernel(
+    const int32_t* __restrict__ flat, int64_t M, int E, const int32_t* __restrict__ chunk_base,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ block_off, int nbits, int per_wave,
+    int32_t* __restrict__ order, int32_t* __restrict__ pos, int32_t* __restrict__ slot,
+    int32_t* __restrict__ row_src) {
+  extern __shared__ int32_t sh[];  // cnt[waves][E] (per-wave running rank base inside the expert)
+  const int nw = (int)blockDim.x >> 6;
+  for (int i = threadIdx.x; i < nw * E; i += blockDim.x) sh[i] = 0;
+  __syncthreads();
+  rank_chunk(
+      flat, M, E, sh, [&](int e) { return chunk_base[(int64_t)blockIdx.x * E + e]; },
+      [&](int e) { return offsets[e]; }, [&](int e) { return block_off[e]; }, nbits, per_wave, order, pos, slot,
+      row_src);
+}
+
+// The whole layout in one launch, for the layer when the fused router made the chunk histograms and they are small
+// (nchunk E <= LF_HIST_MAX): every workgroup sums the histograms itself (the chunks before its own give its
+// per-expert rank bases, all of them the expert totals), so no scan kernel runs between the router and the ranks.
+// The scan's tables are spread over all workgroups, and the last one writes the weight gradients' chunk table.
+// Needs E + 1 <= blockDim.x: a thread per expert in the expert-level scans, and one more for the chunk table's
+// extra expert.  Each workgroup reads nchunk E ints of histograms (64 KB at T = 16384 tokens, 64 experts), from L2.
+constexpr int LF_HIST_MAX = 32768, LF_LOADS = 16;
+__global__ __launch_bounds__(1024) void layout_fused_kernel(
+    const int32_t* __restrict__ flat, int64_t M, int E, const int32_t* __restrict__ hist, int nchunk, int nbits,
+    int per_wave, int32_t* __restrict__ order, int32_t* __restrict__ pos, int32_t* __restrict__ slot,
+    int32_t* __restrict__ row_src, int32_t* __restrict__ group_sizes, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ block_off, int32_t* __restrict__ blk_expert, int32_t* __restrict__ blk_rows,
+    int32_t* __restrict__ num_blocks, int max_blocks, lsurge::LayoutTiles tiles) {
+  extern __shared__ int32_t sh[];
+  const int tid = threadIdx.x, nt = (int)blockDim.x, nw = nt >> 6, me = (int)blockIdx.x;
+  const int tpe = nt / E;               // threads per expert in the histogram sums
+  int32_t* cnt = sh;                    // [nw][E]
+  int32_t* part = cnt + nw * E;         // [2][tpe][E]: partial sums below this chunk, and over all chunks
+  int32_t* below_s = part + 2 * tpe * E;
+  int32_t* gs_s = below_s + E;
+  int32_t* off_s = gs_s + E;
+  int32_t* boff_s = off_s + E;          // [E + 1]
+  int32_t* tb_s = boff_s + E + 1;       // [E + 1]
+  int32_t* ws = tb_s + E + 1;           // [16]
+  for (int i = tid; i < nw * E; i += nt) cnt[i] = 0;
+  const int e_t = tid % E, j_t = tid / E;
+  if (j_t < tpe) {
+    int below = 0, all = 0;
+    for (int c0 = j_t; c0 < nchunk; c0 += LF_LOADS * tpe) {
+      int v[LF_LOADS];
+#pragma unroll
+      for (int u = 0; u < LF_LOADS; ++u) {
+        const int c = c0 + u * tpe;
+        v[u] = c < nchunk ? hist[(int64_t)c * E + e_t] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < LF_LOADS; ++u) {
+        all += v[u];
+        below += c0 + u * tpe < me ? v[u] : 0;
+      }
+    }
+    part[j_t * E + e_t] = below;
+    part[(tpe + j_t) * E + e_t] = all;
+  }
+  __syncthreads();
+  if (tid < E) {
+    int below = 0, all = 0;
+    for (int j = 0; j < tpe; ++j) {
+      below += part[j * E + tid];
+      all += part[(tpe + j) * E + tid];
+    }
+    below_s[tid] = below;
+    gs_s[tid] = all;
+  }
+  __syncthreads();
+  // expert offsets, block offsets and tile bases: the same scans as the scan kernel's
+  const int g = tid < E ? gs_s[tid] : 0;
+  int tot, nbt, ntt = 0;
+  const int off = block_scan_excl(g, ws, &tot);
+  const int boff = block_scan_excl((g + BLK - 1) / BLK, ws, &nbt);
+  const int tbase = tiles.t_expert ? block_scan_excl((g + 2 * BLK - 1) / (2 * BLK), ws, &ntt) : 0;
+  if (tid < E) {
+    off_s[tid] = off;
+    boff_s[tid] = boff;
+    tb_s[tid] = tbase;
+    if (me == 0) {
+      if (group_sizes) group_sizes[tid] = g;
+      if (offsets) offsets[tid] = off;
+      if (block_off) block_off[tid] = boff;
+    }
+  }
+  if (tid == 0) {
+    boff_s[E] = nbt;
+    tb_s[E] = ntt;
+  }
+  __syncthreads();
+  rank_chunk(
+      flat, M, E, cnt, [&](int e) { return below_s[e]; }, [&](int e) { return off_s[e]; },
+      [&](int e) { return boff_s[e]; }, nbits, per_wave, order, pos, slot, row_src);
+  write_layout_tables(E, gs_s, boff_s, tb_s, row_src, blk_expert, blk_rows, num_blocks, max_blocks, tiles,
+                      me * nt + tid, (int)gridDim.x * nt);
+  if (tiles.chunks.c_expert && me == (int)gridDim.x - 1)
+    lsurge::write_chunk_table(
+        tiles.chunks, E, [&](int e) { return gs_s[e]; }, [&](int e) { return BLK * boff_s[e]; },
+        [&](int v, int* total) { return block_scan_excl(v, ws, total); });
 }
 
 // inv[v] = m for every v (the entries that no index hits keep it; a gather through inv gives zero rows there)
@@ -345,6 +467,16 @@ int layout_common(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, int32_
                                      block_off, row_src, blk_expert, blk_rows, num_blocks, (int)max_blocks, tiles));
     return LSURGE_OK;
   }
+  // the fused router's histograms, when small: the whole layout in one launch (layout_fused_kernel)
+  if (pre.hist && 64 * waves >= E + 1 && nchunk * E <= LF_HIST_MAX) {
+    const int nt = 64 * waves, tpe = nt / (int)E;
+    const size_t lds = sizeof(int32_t) * ((size_t)waves * E + 2 * (size_t)tpe * E + 5 * (size_t)E + 2 + 16);
+    LSURGE_LAUNCH(KID_LAYOUT_RANK, s,
+                  hipLaunchKernelGGL(layout_fused_kernel, dim3((unsigned)nchunk), dim3(nt), lds, s, flat, M, (int)E,
+                                     hist, (int)nchunk, nbits, per_wave, order, pos, slot, row_src, gs, offsets,
+                                     block_off, blk_expert, blk_rows, num_blocks, (int)max_blocks, tiles));
+    return LSURGE_OK;
+  }
   if (!pre.hist)
     LSURGE_LAUNCH(KID_LAYOUT_HIST, s,
                   hipLaunchKernelGGL(layout_hist_kernel, dim3((unsigned)nchunk), dim3(LT_THREADS),
@@ -370,6 +502,8 @@ int build_layout_impl(const int32_t* flat, int64_t M, int64_t E, int32_t* gs, in
   LSURGE_REQUIRE(!tiles.t_expert || (tiles.t_rows && tiles.t_row0 && tiles.num_tiles && row_src && E <= 1024),
                  "layout: incomplete tile table outputs");
   LSURGE_REQUIRE(!pre.hist || (pre.waves >= 1 && pre.waves <= 16), "layout: chunk waves=%d not in [1, 16]", pre.waves);
+  LSURGE_REQUIRE(!tiles.chunks.c_expert || (tiles.t_expert && E + 1 <= 1024 && tiles.chunks.R >= 1),
+                 "layout: chunk table needs the tile table, E + 1 <= 1024 and R >= 1");
   return layout_common(flat, M, E, gs, offsets, block_off, order, pos, slot, row_src, blk_expert, blk_rows,
                        num_blocks, lsurge_max_blocks(M, E), ws, ws_bytes, s, tiles, pre);
 }

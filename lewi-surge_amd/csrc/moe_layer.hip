@@ -73,12 +73,19 @@ struct Saved {
   bf16_t *sg, *su, *sh, *sy;  // shared expert run on its own: gate, up, h, output
   bf16_t* w_rT;               // W_r^T [E, d]: the dispatch backward's router dx term, made by the forward off the
                               // critical stream
+  int32_t* chunk_tab;         // the routed weight gradients' chunk table (routed_chunk_plan), written by the bf16
+                              // forward's layout
   // FP8 forward: x [T, d], routed h [P, f] (padded rows) and shared h [T, fs] in E4M3, and their scale_inv, the
   // operands the FP8 backward's weight gradients read again.  Carved after the bf16 layout and only for the FP8
   // path (null otherwise), so a bf16 buffer is a prefix of an FP8 one.
   uint8_t *xq, *hq, *shq;
   float* f8_sinv;
 };
+
+// chunk table of the routed weight gradients (a merged shared expert as the extra expert E) and its partial slots
+lsurge::WgradChunkPlan routed_chunk_plan(const Dims& q) {
+  return q.merged ? lsurge::wgrad_chunk_plan(q.M + q.T, q.E + 1) : lsurge::wgrad_chunk_plan(q.M, q.E);
+}
 
 size_t carve_saved(const Dims& q, void* base, Saved* sv, bool fp8) {
   Carve c(base);
@@ -109,6 +116,7 @@ size_t carve_saved(const Dims& q, void* base, Saved* sv, bool fp8) {
   sv->sh = c.take<bf16_t>(own * q.fs);
   sv->sy = c.take<bf16_t>(own * q.d);
   sv->w_rT = c.take<bf16_t>(q.E * q.d);
+  sv->chunk_tab = c.take<int32_t>(lsurge::wgrad_chunk_table_ints(routed_chunk_plan(q), q.E));
   if (fp8) {
     sv->xq = c.take<uint8_t>(q.T * q.d);
     sv->hq = c.take<uint8_t>(q.P * q.f);
@@ -141,7 +149,7 @@ struct BwdWs {
   void* part_r;       // split-K partials of the router weight gradient (another stream)
   size_t part_r_bytes;
   lsurge::WgradChunkPlan cplan;  // chunk table of the routed weight gradients and the partials of split experts
-  int32_t* chunk_tab;
+  int32_t* chunk_tab;            // the FP8 backward's chunk table (bf16: the forward's, in the saved buffer)
   void* part_dn;      // down-projection weight gradient (helper stream)
   size_t part_dn_bytes;
   void* part_gu;      // gate/up weight gradient (caller's stream)
@@ -173,7 +181,7 @@ size_t carve_bwd(const Dims& q, void* base, BwdWs* w) {
   w->dense_tab = c.take<int32_t>(tab);
   w->part_r_bytes = lsurge::wgrad_workspace_bytes(1, q.d, q.E, dense_splits(q.T, q.d, q.E));
   w->part_r = c.take<char>(w->part_r_bytes);
-  w->cplan = q.merged ? lsurge::wgrad_chunk_plan(q.M + q.T, q.E + 1) : lsurge::wgrad_chunk_plan(q.M, q.E);
+  w->cplan = routed_chunk_plan(q);
   w->chunk_tab = c.take<int32_t>(lsurge::wgrad_chunk_table_ints(w->cplan, q.E));
   w->part_dn_bytes = lsurge::wgrad_chunked_workspace_bytes(w->cplan, q.f, q.d);
   w->part_dn = c.take<char>(w->part_dn_bytes);
@@ -461,6 +469,9 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   // C2: 1.547 -> 1.537 ms per step, forward 0.537 -> 0.528 ms (same-box A/B against forking after the router with
   // the persistent kernels).
   const bool early = !w8 && q.fs && s0 != st;
+  // a merged shared expert forked early: its down projection rides along the routed down GEMM as expert E (its
+  // tiles follow the routed ones in the tile table), so the helper's classic-kernel GEMMs end with the layout
+  const bool ride = early && q.merged && lsurge::gemm_variant() == LSURGE_GEMM_G256;
   if (early)
     if (int rc = lsurge::stream_after(s0, st, fg.f.ev[3])) return rc;
   // W_r^T for the backward's router dx term (saved): on the helper stream when it forks here (off the critical path),
@@ -511,8 +522,10 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
     if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_SHARED_GU_FWD, dense, p->x, q.d, p->ws_gate, p->ws_up, q.fs, 0, q.d,
                                               q.fs, sh, sg, su, q.fs, s0))
       return rc;
-    if (int rc = lsurge::gemm_rows_kn(KID_SHARED_DOWN_FWD, dense, sh, q.fs, p->ws_down, q.d, 0, q.fs, q.d, sy, q.d, s0))
-      return rc;
+    if (!ride)
+      if (int rc = lsurge::gemm_rows_kn(KID_SHARED_DOWN_FWD, dense, sh, q.fs, p->ws_down, q.d, 0, q.fs, q.d, sy, q.d,
+                                        s0))
+        return rc;
   }
   // the layout also writes the backward's 256-row tile table: routed tiles, then the merged shared expert's (and
   // its row_src)
@@ -526,6 +539,9 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   tiles.P = q.P;
   tiles.T = q.T;
   tiles.k = (int)q.k;
+  // bf16: the layout also writes the backward's chunk table of the routed weight gradients
+  if (!w8)
+    tiles.chunks = lsurge::chunk_table_out(sv.chunk_tab, (int)q.E, routed_chunk_plan(q), q.merged ? q.T : -1, q.P);
   lsurge::LayoutChunks chunks;  // the fused router's histograms: chunks of 64 tokens = k waves of 64 slots
   chunks.hist = rhist;
   chunks.waves = (int)q.k;
@@ -568,10 +584,19 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   if (int rc = lsurge::gemm_rows_swiglu_fwd(KID_GEMM_GU_FWD, blocks, p->x, q.d, p->w_gate, p->w_up, q.f, q.d * q.f,
                                             q.d, q.f, sv.h, sv.g, sv.u, q.f, st, gather))
     return rc;
-  if (int rc = lsurge::gemm_rows_kn(KID_GEMM_DOWN_FWD, blocks, sv.h, q.f, p->w_down, q.d, q.f * q.d, q.f, q.d, sv.y_pad,
-                                    q.d, st))
+  lsurge::GemmBlocks dblocks = blocks;
+  lsurge::ExtraExpert xdn;
+  if (ride) {  // the shared expert's h rows come from the helper: join before the down GEMM
+    if (int rc = fg.joined(lsurge::stream_after(st, s0, fg.f.ev[1]))) return rc;
+    dblocks = lsurge::GemmBlocks{sv.t_expert, sv.t_rows, sv.t_row0, sv.num_tiles + 1, (int)(q.TB + q.TS), 0, 256};
+    xdn.expert = (int)q.E;
+    xdn.B = p->ws_down;
+  }
+  if (int rc = lsurge::gemm_rows_kn(KID_GEMM_DOWN_FWD, dblocks, sv.h, q.f, p->w_down, q.d, q.f * q.d, q.f, q.d,
+                                    sv.y_pad, q.d, st, false, xdn))
     return rc;
-  if (int rc = fg.joined(lsurge::stream_after(st, s0, fg.f.ev[1]))) return rc;
+  if (!ride)
+    if (int rc = fg.joined(lsurge::stream_after(st, s0, fg.f.ev[1]))) return rc;
   return lsurge::launch_combine_pad(sv.y_pad, q.d, (int)q.k, sv.slot, sv.weights, q.T, q.fs ? sy : nullptr, out,
                                     LSURGE_BF16, st);
 }
@@ -596,7 +621,7 @@ int lsurge_moe_fwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, co
 
 // Backward.  Stream plan (caller's stream = critical path):
 //   main:  [fs != f: the shared expert's own backward: down dgrad, down wgrad, gate/up dgrad, gate/up wgrad] ->
-//          W_r transpose, chunk table -> combine bwd -> [fork] -> down dgrad (+SwiGLU bwd) -> gate/up dgrad ->
+//          combine bwd -> [fork] -> down dgrad (+SwiGLU bwd) -> gate/up dgrad ->
 //          dispatch bwd -> gate/up wgrad -> [join]
 //   s0:    after the fork, with a merged shared expert: router wgrad
 //   s1:    after the fork: down wgrad (then the router wgrad when the shared expert is not merged)
@@ -674,14 +699,9 @@ int lsurge_moe_bwd(const lsurge_moe_shape* s, const lsurge_moe_params* p, const 
                                             lsurge::RowGather(), dxo))
       return rc;
   }
-  // main, before any GEMM: the chunk table of the weight gradients (read by both routed weight gradients), a
-  // one-workgroup kernel: issued on a helper stream beside the persistent GEMMs (one workgroup per CU, the whole LDS
-  // and register file) it would wait for a whole GEMM to drain first.  (W_r^T, the router's dx term, was made by the
-  // forward.)
-  lsurge::WgradChunks chunks;
-  if (int rc = lsurge::build_wgrad_chunks(sv.gs, sv.block_off, (int)q.E, w.cplan, w.chunk_tab, &chunks, st,
-                                         q.merged ? q.T : -1, q.P))
-    return rc;
+  // the chunk table of the routed weight gradients and W_r^T (the router's dx term) were made by the forward
+  const lsurge::WgradChunks chunks =
+      lsurge::chunk_table_view(lsurge::chunk_table_out(sv.chunk_tab, (int)q.E, w.cplan, q.merged ? q.T : -1, q.P));
   // main: combine backward: d(weights), d(router logits at sel) and their dense bf16 rows for the router's weight
   // gradient, and the padded dY rows bf16(w dY) of the down projection's GEMMs (a merged shared expert's rows get dY
   // itself).
@@ -783,7 +803,7 @@ size_t lsurge_moe_bwd_fp8_workspace_bytes(const lsurge_moe_shape* s) {
 // Stream plan (caller's stream = critical path):
 //   main: dY scale -> combine bwd (E5M2 dY rows) -> [record] -> down dgrad (+SwiGLU bwd, amax of [dG | dU]) ->
 //         [dG | dU] cast -> gate/up dgrad -> [join] -> dispatch bwd -> gate/up wgrad
-//   s1:   from the start: W_r transpose, chunk table; after the record: down wgrad
+//   s1:   from the start: the chunk table; after the record: down wgrad
 //   s0:   from the start: the shared expert's backward; after the record: router wgrad
 int lsurge_moe_bwd_fp8(const lsurge_moe_shape* s, const lsurge_moe_params* p, const void* wq, size_t wq_bytes,
                        const void* dy, const void* saved, const lsurge_moe_grads* g, void* workspace,
