@@ -73,8 +73,8 @@ struct Saved {
   bf16_t *sg, *su, *sh, *sy;  // shared expert run on its own: gate, up, h, output
   bf16_t* w_rT;               // W_r^T [E, d]: the dispatch backward's router dx term, made by the forward off the
                               // critical stream
-  int32_t* chunk_tab;         // the routed weight gradients' chunk table (routed_chunk_plan), written by the bf16
-                              // forward's layout
+  int32_t* chunk_tab;         // the bf16 backward's chunk table of the routed weight gradients (routed_chunk_plan),
+                              // written by the layout of either forward
   // FP8 forward: x [T, d], routed h [P, f] (padded rows) and shared h [T, fs] in E4M3, and their scale_inv, the
   // operands the FP8 backward's weight gradients read again.  Carved after the bf16 layout and only for the FP8
   // path (null otherwise), so a bf16 buffer is a prefix of an FP8 one.
@@ -539,9 +539,9 @@ static int moe_fwd_impl(const lsurge_moe_shape* s, const lsurge_moe_params* p, c
   tiles.P = q.P;
   tiles.T = q.T;
   tiles.k = (int)q.k;
-  // bf16: the layout also writes the backward's chunk table of the routed weight gradients
-  if (!w8)
-    tiles.chunks = lsurge::chunk_table_out(sv.chunk_tab, (int)q.E, routed_chunk_plan(q), q.merged ? q.T : -1, q.P);
+  // the layout also writes the bf16 backward's chunk table of the routed weight gradients (that backward also runs
+  // after the FP8 forward, on its saved buffer)
+  tiles.chunks = lsurge::chunk_table_out(sv.chunk_tab, (int)q.E, routed_chunk_plan(q), q.merged ? q.T : -1, q.P);
   lsurge::LayoutChunks chunks;  // the fused router's histograms: chunks of 64 tokens = k waves of 64 slots
   chunks.hist = rhist;
   chunks.waves = (int)q.k;
