@@ -308,7 +308,8 @@ def label_launches(rows, c):
         if g256 and fs and k in ("gemm_rows_kernel<1,1>", "gemm_rows_kernel<1,0>"):
             # with helper streams the shared expert's dense forward runs on the classic kernels beside the router,
             # submitted before the routed GEMMs; its down projection then takes the first persistent <1,0,0> role
-            if k == "gemm_rows_kernel<1,0>":
+            # (a merged shared expert's down projection rides along the routed one: that launch is gemm_down_fwd)
+            if k == "gemm_rows_kernel<1,0>" or fs == c["f"]:
                 seen["g256_rows<1,0,0>"] = max(seen.get("g256_rows<1,0,0>", 0), 1)
             out.append(("shared_gu_fwd" if k == "gemm_rows_kernel<1,1>" else "shared_down_fwd", k, row))
             continue
